@@ -1,0 +1,99 @@
+/* C ABI of the LogKV HIP library (liblogkv_hip.so, gfx950).
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * enqueues its kernels on the given HIP stream (NULL = the default stream),
+ * never allocates and never synchronises the host. Scratch memory is passed in
+ * by the caller; `*_workspace_bytes` reports how much. Return value: LOGKV_OK,
+ * LOGKV_EINVAL for a shape / layout mismatch (the reference raises ValueError),
+ * LOGKV_ERUNTIME for a HIP launch failure (RuntimeError); `logkv_last_error()`
+ * gives the message of the calling thread's last failure.
+ *
+ * Storage follows the reference cache's buffers (litgpt/log_kv_cache.py:881-1121):
+ * ladder fields are [lanes, K, L, B'] (+ feature axis), lanes = batch * groups;
+ * several layer caches may share one allocation by folding layers into batch.
+ * bf16 tensors are passed as uint16_t*, bool tensors as uint8_t*.
+ */
+#ifndef LOGKV_HIP_H
+#define LOGKV_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { LOGKV_OK = 0, LOGKV_EINVAL = 1, LOGKV_ERUNTIME = 2 };
+
+/* Persistent ladder and cluster state (all device pointers). */
+typedef struct logkv_ladder_view {
+  uint16_t* level_k;      /* bf16 [lanes, K, L, B', dk] */
+  uint16_t* level_v;      /* bf16 [lanes, K, L, B', dv] */
+  float* level_w;         /* [lanes, K, L, B'] */
+  int64_t* level_p_lo;
+  int64_t* level_p_hi;
+  int64_t* level_sum_wp;
+  int64_t* level_order;
+  uint8_t* pad_mask;
+  int16_t* level_count;   /* [lanes, K, L] */
+  float* centroid;        /* [lanes, K, dk] */
+  float* n_eff;           /* [lanes, K] */
+  int32_t* n_total;
+  int64_t* p_hi_c;
+  int32_t* level0_phase;
+  uint8_t* alive;
+  const float* s_h;       /* [lanes] */
+  int32_t n_batch, n_groups, k_max, levels, slots, dk, dv;
+} logkv_ladder_view;
+
+/* The rows of one flush: k_raw / v [n_batch, G, T, d] bf16 with element strides
+ * (last axis contiguous), positions [n_batch, T] int64, optional ragged counts. */
+typedef struct logkv_rows_view {
+  const uint16_t* k;
+  int64_t k_sb, k_sg, k_st;
+  const uint16_t* v;
+  int64_t v_sb, v_sg, v_st;
+  const int64_t* pos;
+  int64_t pos_sb;
+  const int32_t* counts;  /* [n_batch] device, rows at or past counts[b] are padding; NULL = T */
+  int32_t tokens;
+} logkv_rows_view;
+
+typedef struct logkv_route_params {
+  float eta;            /* temporal cost weight (seg_eta) */
+  float g0;             /* temporal cost scale (seg_g0) */
+  float lam;            /* radius multiplier (cluster_lambda_rel) */
+  int32_t late_joins;   /* 1 with Alpha: re-sort clusters whose p_hi passes a new row */
+  int32_t beta_merge;   /* 1: Beta 4->2 merges at non-top carry levels */
+} logkv_route_params;
+
+const char* logkv_last_error(void);
+
+/* Bytes of scratch needed by logkv_attach_assign / logkv_route_commit. */
+int64_t logkv_route_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins);
+
+/* Final attach cluster of every valid row, in position order: assign[lane, t]
+ * (int8, -1 past the row's count); order[b, t] (int32) lists row offsets by
+ * position. Frozen joins + farthest-point seeds + orphan joins.
+ * Replaces attach_assign (litgpt/log_kv_route_triton.py:894-917) and the seeding
+ * planner _semantic_attach_plan_torch (litgpt/log_kv_cache.py:4636-4680). */
+int logkv_attach_assign(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                        const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                        int8_t* assign, int32_t* order, void* stream);
+
+/* One attach-routed flush committed into the ladders: decisions as above, new
+ * clusters, ordinary and (with late_joins) delayed joins, Fenwick appends with
+ * pair or Beta carries and the top-level fold, ordered centroid updates and the
+ * cluster scalars. `assign` / `order` may be NULL.
+ * Replaces the device work of _semantic_attach_commit / _alpha_commit_joins /
+ * _semantic_apply_join_plan (litgpt/log_kv_cache.py:4682-4707, :3690-3788,
+ * :4225-4361) and the kernels fill, merge_scatter, centroid_parallel
+ * (litgpt/log_kv_updates_triton.py:79-87, :176-219, :268-282). */
+int logkv_route_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                       const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                       int8_t* assign, int32_t* order, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOGKV_HIP_H */

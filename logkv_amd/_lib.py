@@ -1,0 +1,93 @@
+"""ctypes binding of liblogkv_hip.so (the C ABI in include/logkv_hip.h).
+
+The library is the only compute path: if it is missing or a call fails, this
+module raises; nothing falls back to a CPU or PyTorch implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblogkv_hip.so"
+
+LOGKV_OK, LOGKV_EINVAL, LOGKV_ERUNTIME = 0, 1, 2
+
+_p = C.c_void_p
+_i64 = C.c_int64
+_i32 = C.c_int32
+
+
+class LadderView(C.Structure):
+    _fields_ = [
+        ("level_k", _p), ("level_v", _p), ("level_w", _p), ("level_p_lo", _p), ("level_p_hi", _p),
+        ("level_sum_wp", _p), ("level_order", _p), ("pad_mask", _p), ("level_count", _p),
+        ("centroid", _p), ("n_eff", _p), ("n_total", _p), ("p_hi_c", _p), ("level0_phase", _p),
+        ("alive", _p), ("s_h", _p),
+        ("n_batch", _i32), ("n_groups", _i32), ("k_max", _i32), ("levels", _i32), ("slots", _i32),
+        ("dk", _i32), ("dv", _i32),
+    ]
+
+
+class RowsView(C.Structure):
+    _fields_ = [
+        ("k", _p), ("k_sb", _i64), ("k_sg", _i64), ("k_st", _i64),
+        ("v", _p), ("v_sb", _i64), ("v_sg", _i64), ("v_st", _i64),
+        ("pos", _p), ("pos_sb", _i64), ("counts", _p), ("tokens", _i32),
+    ]
+
+
+class RouteParams(C.Structure):
+    _fields_ = [("eta", C.c_float), ("g0", C.c_float), ("lam", C.c_float),
+                ("late_joins", _i32), ("beta_merge", _i32)]
+
+
+# Exported symbol -> (restype, argtypes); the tests check this table against the header.
+SIGNATURES = {
+    "logkv_last_error": (C.c_char_p, []),
+    "logkv_route_workspace_bytes": (_i64, [C.POINTER(LadderView), _i32, _i32]),
+    "logkv_attach_assign": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
+                                   _p, _i64, _p, _p, _p]),
+    "logkv_route_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
+                                  _p, _i64, _p, _p, _p]),
+}
+
+
+class LogKVError(RuntimeError):
+    pass
+
+
+@lru_cache(maxsize=1)
+def lib() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise LogKVError(f"{LIB_PATH} is not built; run `python __graft_entry__.py` or logkv_amd/build.py")
+    handle = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype, fn.argtypes = res, args
+    return handle
+
+
+def check(rc: int, what: str) -> None:
+    if rc == LOGKV_OK:
+        return
+    msg = lib().logkv_last_error().decode(errors="replace")
+    if rc == LOGKV_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise LogKVError(f"{what}: {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{what} must live on a ROCm device (got {t.device}); the LogKV HIP library has no CPU path")

@@ -1,0 +1,148 @@
+// extern "C" entry points: argument validation, workspace carving, launches.
+#include <cstdio>
+#include <cstdarg>
+#include <cstring>
+
+#include "route.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, args);
+  va_end(args);
+  return code;
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+int check_ladder(const logkv_ladder_view* c) {
+  if (!c) return fail(LOGKV_EINVAL, "ladder view is NULL");
+  if (c->n_batch < 1 || c->n_groups < 1) return fail(LOGKV_EINVAL, "batch and groups must be >= 1");
+  if (c->k_max < 1 || c->k_max > logkv::kMaxClusters)
+    return fail(LOGKV_EINVAL, "cluster count %d outside [1, %d]", c->k_max, logkv::kMaxClusters);
+  if (c->slots < 2) return fail(LOGKV_EINVAL, "slots per level must be >= 2, got %d", c->slots);
+  if (c->levels < 1 || c->levels > 64) return fail(LOGKV_EINVAL, "levels %d outside [1, 64]", c->levels);
+  if (c->dk < 4 || c->dv < 4 || c->dk % 4 || c->dv % 4 || c->dk > logkv::kMaxDim || c->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "key/value widths must be multiples of 4 in [4, %d], got %d/%d", logkv::kMaxDim,
+                c->dk, c->dv);
+  if (!c->level_k || !c->level_v || !c->level_w || !c->level_p_lo || !c->level_p_hi || !c->level_sum_wp ||
+      !c->level_order || !c->pad_mask || !c->level_count || !c->centroid || !c->n_eff || !c->n_total ||
+      !c->p_hi_c || !c->level0_phase || !c->alive || !c->s_h)
+    return fail(LOGKV_EINVAL, "ladder view has a NULL buffer");
+  return LOGKV_OK;
+}
+
+int check_rows(const logkv_ladder_view* c, const logkv_rows_view* r) {
+  if (!r) return fail(LOGKV_EINVAL, "rows view is NULL");
+  if (r->tokens < 0 || r->tokens > logkv::kMaxOrderRows)
+    return fail(LOGKV_EINVAL, "rows per flush %d outside [0, %d]", r->tokens, logkv::kMaxOrderRows);
+  if (r->tokens && (!r->k || !r->v || !r->pos)) return fail(LOGKV_EINVAL, "rows view has a NULL buffer");
+  if (reinterpret_cast<uintptr_t>(r->k) % 8 || reinterpret_cast<uintptr_t>(r->v) % 8 || r->k_st % 4 ||
+      r->v_st % 4 || r->k_sb % 4 || r->k_sg % 4 || r->v_sb % 4 || r->v_sg % 4)
+    return fail(LOGKV_EINVAL, "row tensors need 8-byte aligned rows (strides multiple of 4 elements)");
+  (void)c;
+  return LOGKV_OK;
+}
+
+struct Plan {
+  int64_t order, assign, s_win, dist, ladder, total;
+  int64_t stride, s0, ca, cb;
+  int32_t sort_width;
+};
+
+Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
+  Plan p{};
+  const int64_t lanes = int64_t(c->n_batch) * c->n_groups;
+  const int64_t ladders = lanes * c->k_max;
+  const int64_t existing = late ? int64_t(c->levels) * c->slots : 0;
+  const int64_t m0 = tokens + existing;
+  logkv::ladder_scratch_rows(m0, c->slots, p.s0, p.ca, p.cb, existing);
+  p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.ca, p.cb));
+  int64_t off = 0;
+  p.order = off;
+  off += align256(int64_t(c->n_batch) * tokens * 4);
+  p.assign = off;
+  off += align256(lanes * tokens);
+  p.s_win = off;
+  off += align256(lanes * tokens * 4);
+  p.dist = off;
+  off += align256(lanes * tokens * 4);
+  p.ladder = off;
+  off += ladders * p.stride;
+  p.total = off;
+  int w = 1;
+  while (late && w < m0) w <<= 1;
+  p.sort_width = late ? w : 0;
+  return p;
+}
+
+int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_route_params* prm, void* workspace,
+          int64_t bytes, int8_t* assign, int32_t* order, logkv::Workspace& ws) {
+  int rc = check_ladder(c);
+  if (rc) return rc;
+  if ((rc = check_rows(c, r))) return rc;
+  if (!prm) return fail(LOGKV_EINVAL, "route params are NULL");
+  const int late = prm->late_joins ? 1 : 0;
+  if (late && int64_t(c->levels) * c->slots + r->tokens > logkv::kMaxOrderRows)
+    return fail(LOGKV_EINVAL, "delayed archive sort needs L*B' + T <= %d", logkv::kMaxOrderRows);
+  const Plan p = plan_for(c, r->tokens, late);
+  if (!workspace || bytes < p.total)
+    return fail(LOGKV_EINVAL, "workspace of %lld bytes is smaller than the %lld required", (long long)bytes,
+                (long long)p.total);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  ws.order = order ? order : reinterpret_cast<int32_t*>(base + p.order);
+  ws.assign = assign ? assign : reinterpret_cast<int8_t*>(base + p.assign);
+  ws.s_win = reinterpret_cast<float*>(base + p.s_win);
+  ws.dist = reinterpret_cast<float*>(base + p.dist);
+  ws.ladder = base + p.ladder;
+  ws.ladder_stride = p.stride;
+  ws.s0_rows = p.s0;
+  ws.carry_a_rows = p.ca;
+  ws.carry_b_rows = p.cb;
+  ws.sort_width = p.sort_width;
+  return LOGKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* logkv_last_error(void) { return g_error; }
+
+int64_t logkv_route_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins) {
+  if (check_ladder(cache) || tokens < 0) return -1;
+  return plan_for(cache, tokens, late_joins ? 1 : 0).total;
+}
+
+int logkv_attach_assign(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                        const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                        int8_t* assign, int32_t* order, void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, assign, order, ws);
+  if (rc) return rc;
+  if (!rows->tokens) return LOGKV_OK;
+  rc = logkv::launch_route(*cache, *rows, *params, ws, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "attach launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_route_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                       const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                       int8_t* assign, int32_t* order, void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, assign, order, ws);
+  if (rc) return rc;
+  if (!rows->tokens) return LOGKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = logkv::launch_route(*cache, *rows, *params, ws, s);
+  if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
+  if (rc) return fail(rc, "route/commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,349 @@
+// Attach routing on the device: position order, frozen-center decisions, farthest-point seeds.
+//
+// Follows litgpt/log_kv_route_triton.py:841-917 (fused attach decisions) and
+// litgpt/log_kv_cache.py:4597-4680 (position order, seeding planner), redesigned
+// for wave64: one wave evaluates one row against every cluster, holding features
+// l, l+64, ... of the row in lane l; distances are folded with the canonical
+// butterfly (common.hpp), so every lane holds the same decision inputs.
+#include "route.hpp"
+
+namespace logkv {
+
+// ---------------------------------------------------------------------------
+// Position order per batch row: stable argsort of positions, padding last.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void order_kernel(const int64_t* __restrict__ pos, int64_t pos_sb,
+                                                     const int32_t* __restrict__ counts, int32_t tokens,
+                                                     int32_t* __restrict__ order) {
+  __shared__ uint64_t keys[kMaxOrderRows];
+  const int b = blockIdx.x;
+  int n = counts ? counts[b] : tokens;
+  n = n < 0 ? 0 : (n > tokens ? tokens : n);
+  const int64_t* p = pos + b * pos_sb;
+  int32_t* out = order + static_cast<int64_t>(b) * tokens;
+  // Already non-decreasing (the common case: a contiguous recent window) ->
+  // the stable order is the identity.
+  int unsorted = 0;
+  for (int t = threadIdx.x; t + 1 < n; t += blockDim.x) unsorted |= p[t] > p[t + 1];
+  if (!__syncthreads_or(unsorted)) {
+    for (int t = threadIdx.x; t < tokens; t += blockDim.x) out[t] = t;
+    return;
+  }
+  int width = 1;
+  while (width < tokens) width <<= 1;
+  for (int t = threadIdx.x; t < width; t += blockDim.x) {
+    uint64_t key;
+    if (t < n) key = (static_cast<uint64_t>(p[t]) << kOrderIndexBits) | static_cast<uint64_t>(t);
+    else key = (~0ull << kOrderIndexBits) | static_cast<uint64_t>(t < tokens ? t : kOrderIndexMask);
+    keys[t] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= width; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < width; t += blockDim.x) {
+        const int partner = t ^ stride;
+        if (partner > t) {
+          const bool up = (t & size) == 0;
+          const uint64_t a = keys[t], c = keys[partner];
+          if ((a > c) == up) {
+            keys[t] = c;
+            keys[partner] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int t = threadIdx.x; t < tokens; t += blockDim.x) out[t] = static_cast<int32_t>(keys[t] & kOrderIndexMask);
+}
+
+// ---------------------------------------------------------------------------
+// Frozen-center decisions: one wave per row, tiles of kAttachTile rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+                                                     const int32_t* __restrict__ order,
+                                                     int8_t* __restrict__ assign, float* __restrict__ s_win) {
+  __shared__ float mu_s[kMaxClusters * kMaxDim];
+  __shared__ float mm_s[kMaxClusters];
+  const int lane_ix = blockIdx.y;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const int K = c.k_max, D = c.dk;
+  const int n = valid_rows(r, b);
+  const int tile0 = blockIdx.x * kAttachTile;
+  const float* mu = c.centroid + static_cast<int64_t>(lane_ix) * K * D;
+  for (int i = threadIdx.x; i < K * D; i += blockDim.x) mu_s[i] = mu[i];
+  __syncthreads();
+  const int l = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
+  const int J = (D + kWave - 1) / kWave;
+  for (int cc = w; cc < K; cc += nw) {
+    float s = 0.f;
+    for (int j = 0; j < J; ++j) {
+      const int d = l + j * kWave;
+      const float m = d < D ? mu_s[cc * D + d] : 0.f;
+      s = j == 0 ? m * m : s + m * m;
+    }
+    s = wave_tree(s);
+    if (l == 0) mm_s[cc] = s;
+  }
+  __syncthreads();
+  uint32_t alive_bits = 0;
+  for (int cc = 0; cc < K; ++cc) alive_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
+  const bool any_alive = alive_bits != 0;
+  const bool any_free = alive_bits != ((K >= 32) ? 0xffffffffu : ((1u << K) - 1u));
+  const float radius = prm.lam * c.s_h[lane_ix];
+  const int64_t* phi = c.p_hi_c + static_cast<int64_t>(lane_ix) * K;
+  const uint16_t* kbase = r.k + b * r.k_sb + g * r.k_sg;
+  for (int s = tile0 + w; s < tile0 + kAttachTile && s < n; s += nw) {
+    const int t = order[static_cast<int64_t>(b) * r.tokens + s];
+    const int64_t pos = r.pos[b * r.pos_sb + t];
+    const uint16_t* row = kbase + static_cast<int64_t>(t) * r.k_st;
+    float x[kMaxDim / kWave];
+    float xx = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxDim / kWave; ++j) {
+      const int d = l + j * kWave;
+      x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+      if (j < J) xx = j == 0 ? x[j] * x[j] : xx + x[j] * x[j];
+    }
+    xx = wave_tree(xx);
+    float best = __builtin_inff(), s_winner = 0.f, best_e = __builtin_inff();
+    int winner = 0, nearest = 0;
+    for (int cc = 0; cc < K; ++cc) {
+      float dot = 0.f, ex = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxDim / kWave; ++j) {
+        if (j < J) {
+          const int d = l + j * kWave;
+          const float m = d < D ? mu_s[cc * D + d] : 0.f;
+          const float diff = x[j] - m;
+          dot = j == 0 ? x[j] * m : dot + x[j] * m;
+          ex = j == 0 ? diff * diff : ex + diff * diff;
+        }
+      }
+      dot = wave_tree(dot);
+      ex = wave_tree(ex);
+      const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot, 0.0f);
+      const bool live = (alive_bits >> cc) & 1u;
+      if (cc == 0) s_winner = semantic;
+      if (live) {
+        const int64_t gi = pos - phi[cc];
+        const float gap = static_cast<float>(gi > 0 ? gi : 0);
+        const float cost = semantic + prm.eta * (gap / (gap + prm.g0));
+        if (cost < best) {
+          best = cost;
+          winner = cc;
+          s_winner = semantic;
+        }
+        if (ex < best_e) {
+          best_e = ex;
+          nearest = cc;
+        }
+      }
+    }
+    const bool direct = any_alive && (s_winner <= radius);
+    int out;
+    if (!any_free) out = direct ? winner : nearest;
+    else out = direct ? winner : -1;
+    if (l == 0) {
+      assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = static_cast<int8_t>(out);
+      if (any_free) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
+    }
+  }
+  // Padding rows of the lane keep -1.
+  for (int s = tile0 + threadIdx.x; s < tile0 + kAttachTile && s < r.tokens; s += blockDim.x)
+    if (s >= n) assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = -1;
+}
+
+// Canonical squared distance between a row (held in x[]) and another bf16 row.
+__device__ __forceinline__ float row_d2_bf16(const float* x, const uint16_t* other, int D, int J) {
+  const int l = lane_id();
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxDim / kWave; ++j) {
+    if (j < J) {
+      const int d = l + j * kWave;
+      const float diff = d < D ? x[j] - bf16_to_f32(other[d]) : 0.f;
+      s = j == 0 ? diff * diff : s + diff * diff;
+    }
+  }
+  return wave_tree(s);
+}
+
+// Block-wide argmax (first index on ties) of (value, index) pairs.
+__device__ __forceinline__ void block_argmax(float& v, int& i, float* sv, int* si) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(i, off, kWave);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  const int w = wave_id(), nw = blockDim.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) {
+    sv[w] = v;
+    si[w] = i;
+  }
+  __syncthreads();
+  v = sv[0];
+  i = si[0];
+  for (int k = 1; k < nw; ++k)
+    if (sv[k] > v || (sv[k] == v && si[k] < i)) {
+      v = sv[k];
+      i = si[k];
+    }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Seeds for lanes with free cluster slots (one block per lane).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, const int32_t* __restrict__ order,
+                                                    int8_t* __restrict__ assign, const float* __restrict__ s_win,
+                                                    float* __restrict__ dist) {
+  __shared__ float cand_s[kMaxClusters * kMaxDim];
+  __shared__ float red_v[16];
+  __shared__ int red_i[16];
+  __shared__ int picks_s[kMaxClusters];
+  __shared__ int free_s[kMaxClusters];
+  __shared__ int n_orphan_s;
+  const int lane_ix = blockIdx.x;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const int K = c.k_max, D = c.dk, J = (D + kWave - 1) / kWave;
+  const int n = valid_rows(r, b);
+  int n_free = 0;
+  for (int cc = 0; cc < K; ++cc)
+    if (!c.alive[lane_ix * K + cc]) {
+      if (threadIdx.x == 0) free_s[n_free] = cc;
+      ++n_free;
+    }
+  if (n_free == 0 || n == 0) return;
+  int8_t* as = assign + static_cast<int64_t>(lane_ix) * r.tokens;
+  const float* sw = s_win + static_cast<int64_t>(lane_ix) * r.tokens;
+  float* ds = dist + static_cast<int64_t>(lane_ix) * r.tokens;
+  const int32_t* ord = order + static_cast<int64_t>(b) * r.tokens;
+  const uint16_t* kbase = r.k + b * r.k_sb + g * r.k_sg;
+  if (threadIdx.x == 0) n_orphan_s = 0;
+  __syncthreads();
+  int mine = 0;
+  float v = -__builtin_inff();
+  int vi = 0x7fffffff;
+  for (int s = threadIdx.x; s < n; s += blockDim.x) {
+    if (as[s] < 0) {
+      ++mine;
+      const float val = sw[s];
+      if (val > v || (val == v && s < vi)) {
+        v = val;
+        vi = s;
+      }
+    }
+  }
+  atomicAdd(&n_orphan_s, mine);
+  __syncthreads();
+  const int n_orphan = n_orphan_s;
+  if (n_orphan == 0) return;
+  int n_use = n_free < n_orphan ? n_free : n_orphan;
+  block_argmax(v, vi, red_v, red_i);
+  int pick = vi;
+  // Every pick is an unpicked orphan with a finite score while n_use <= orphans;
+  // a non-finite score (NaN keys) could leave no valid index: seed fewer then.
+  if (pick < 0 || pick >= n) return;
+  if (threadIdx.x == 0) picks_s[0] = pick;
+  const int l = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
+  for (int step = 0; step + 1 < n_use; ++step) {
+    // dist = min(dist, d2(., pick)), with the pick itself masked; argmax -> next pick.
+    const uint16_t* prow = kbase + static_cast<int64_t>(ord[pick]) * r.k_st;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int s = w; s < n; s += nw) {
+      float x[kMaxDim / kWave];
+      const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
+#pragma unroll
+      for (int j = 0; j < kMaxDim / kWave; ++j) {
+        const int d = l + j * kWave;
+        x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+      }
+      const float d2 = row_d2_bf16(x, prow, D, J);
+      float val;
+      if (step == 0) val = as[s] < 0 ? d2 : -__builtin_inff();
+      else val = fminf(ds[s], d2);
+      if (s == pick) val = -__builtin_inff();
+      if (l == 0) ds[s] = val;
+      if (val > bv || (val == bv && s < bi)) {
+        bv = val;
+        bi = s;
+      }
+    }
+    block_argmax(bv, bi, red_v, red_i);
+    if (bi < 0 || bi >= n) {
+      n_use = step + 1;
+      break;
+    }
+    pick = bi;
+    if (threadIdx.x == 0) picks_s[step + 1] = pick;
+    __syncthreads();
+  }
+  __syncthreads();
+  // Candidate centers: live centroids, seed rows at the free slots.
+  const float* mu = c.centroid + static_cast<int64_t>(lane_ix) * K * D;
+  for (int i = threadIdx.x; i < K * D; i += blockDim.x) cand_s[i] = mu[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_use * D; i += blockDim.x) {
+    const int k = i / D, d = i % D;
+    const uint16_t* row = kbase + static_cast<int64_t>(ord[picks_s[k]]) * r.k_st;
+    cand_s[free_s[k] * D + d] = bf16_to_f32(row[d]);
+  }
+  __syncthreads();
+  uint32_t cand_bits = 0;
+  for (int cc = 0; cc < K; ++cc) cand_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
+  for (int k = 0; k < n_use; ++k) cand_bits |= 1u << free_s[k];
+  for (int s = w; s < n; s += nw) {
+    if (as[s] >= 0) continue;
+    float x[kMaxDim / kWave];
+    const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
+#pragma unroll
+    for (int j = 0; j < kMaxDim / kWave; ++j) {
+      const int d = l + j * kWave;
+      x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+    }
+    float best = __builtin_inff();
+    int arg = 0;
+    for (int cc = 0; cc < K; ++cc) {
+      float e = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxDim / kWave; ++j) {
+        if (j < J) {
+          const int d = l + j * kWave;
+          const float diff = d < D ? x[j] - cand_s[cc * D + d] : 0.f;
+          e = j == 0 ? diff * diff : e + diff * diff;
+        }
+      }
+      e = wave_tree(e);
+      if (((cand_bits >> cc) & 1u) && e < best) {
+        best = e;
+        arg = cc;
+      }
+    }
+    if (l == 0) as[s] = static_cast<int8_t>(arg);
+  }
+  __syncthreads();
+  if (threadIdx.x < n_use) as[picks_s[threadIdx.x]] = static_cast<int8_t>(free_s[threadIdx.x]);
+}
+
+int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
+                 hipStream_t stream) {
+  const int lanes = c.n_batch * c.n_groups;
+  hipLaunchKernelGGL(order_kernel, dim3(c.n_batch), dim3(1024), 0, stream, r.pos, r.pos_sb, r.counts, r.tokens,
+                     ws.order);
+  const int tiles = (r.tokens + kAttachTile - 1) / kAttachTile;
+  if (tiles > 0) {
+    hipLaunchKernelGGL(attach_kernel, dim3(tiles, lanes), dim3(256), 0, stream, c, r, p, ws.order, ws.assign,
+                       ws.s_win);
+    hipLaunchKernelGGL(seed_kernel, dim3(lanes), dim3(1024), 0, stream, c, r, ws.order, ws.assign, ws.s_win,
+                       ws.dist);
+  }
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+}  // namespace logkv

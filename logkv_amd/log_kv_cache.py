@@ -1,0 +1,463 @@
+"""LogStructuredKVCache for MI355X: the SemanticLogKV flush path on HIP kernels.
+
+Drop-in for the reference class (litgpt/log_kv_cache.py:640) on the path the
+current configurations use: semantic clusters (K > 1), attach routing, mid
+anchors, first-order entries, optional Alpha exact spans and Beta. The
+constructor keeps the reference signature (litgpt/log_kv_cache.py:681-720);
+options outside that path raise NotImplementedError instead of silently
+changing behaviour.
+
+Design: the cache state lives on the device in the reference's buffer layout,
+and a flush is a fixed sequence of kernels (position order, attach decisions,
+seeds, per-ladder commit) with no host planning and no device-to-host
+readback. The reference's host mirrors (``_semantic_counts`` ...) are
+read-only properties that copy from the device when asked.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from ._lib import LadderView, RouteParams, RowsView, check, lib, ptr, require_device, stream_of
+
+
+def ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, K, exact_tokens, element):
+    """(B', L, budget bytes) of the Alpha-adjusted ladder (litgpt/log_kv_cache.py:857, :879-898)."""
+    def levels(b):
+        return max(2, math.ceil(math.log2(max_seq_length / max(K * b, 1) + 1.0)) + 2)
+
+    L = levels(B)
+    if not exact_tokens:
+        return B, L, None
+    packed = ((max(k_dim + 1, v_dim) + 7) // 8) * 8
+    entry = (k_dim + v_dim + 2 * packed) * element + 41
+    exact = exact_tokens * (n_groups * (k_dim + v_dim + 2 * packed) * element + 9)
+    baseline = n_groups * K * L * (B * entry + 2)
+    for cand in range(B - 1, 1, -1):
+        lv = levels(cand)
+        need = n_groups * K * lv * (cand * entry + 2) + exact
+        if need <= baseline:
+            return cand, lv, (batch_size * baseline, batch_size * need)
+    raise ValueError("compressed ladder budget is too small for alpha_exact_tokens; increase B or reduce exact capacity")
+
+
+class LogStructuredKVCache(nn.Module):
+    """Semantic LogKV cache whose flush runs as HIP kernels on one MI355X.
+
+    Buffers keep the reference names and shapes (litgpt/log_kv_cache.py:881-1121):
+    ``level_{k,v}`` ``[Bt, G, K, L, B', D]`` bf16, ``level_w`` / ``level_imp`` f32,
+    ``level_{p_lo,p_hi,sum_wp,order}`` i64, ``pad_mask`` bool, ``level_count`` i16
+    ``[Bt, G, K, L]``, ``centroid`` f32 ``[Bt, G, K, D]``, ``n_eff`` f32,
+    ``n_total`` i32, ``p_hi_c`` i64, ``level0_phase`` i32, ``alive`` bool
+    ``[Bt, G, K]``, the recent window ``[Bt, G, 2*recent, D]`` and the exact pool.
+    """
+
+    def __init__(
+        self,
+        k_shape,
+        v_shape,
+        B: int = 512,
+        recent_size: int = 0,
+        device=None,
+        dtype=None,
+        importance_pooling: bool = False,
+        importance_pooling_lambda: float = 1.0,
+        importance_pooling_temperature: float = 1.0,
+        semantic_clusters: bool = False,
+        cluster_k_max: int = 1,
+        cluster_lambda_rel: float = 1.0,
+        seg_eta: float = 1.0,
+        seg_g0: float = 2048.0,
+        seg_gap_max: float | None = None,
+        seg_block_level: int = 0,
+        seg_forget: float = 0.5,
+        semantic_s_h=None,
+        semantic_flush_granularity: int = 2,
+        semantic_cluster_chunk_size: int = 0,
+        semantic_capacity_beta: float = 0.0,
+        semantic_capacity_hard_cap_mult: float = 0.0,
+        semantic_legacy_route: bool = False,
+        semantic_unified_route: bool = False,
+        semantic_merge_passes: int = 1,
+        semantic_anchor_mode: str = "multi",
+        semantic_pack_backend: str = "auto",
+        semantic_centroid_backend: str = "sequential",
+        semantic_replay_updates: bool = False,
+        cos_cache: torch.Tensor | None = None,
+        sin_cache: torch.Tensor | None = None,
+        rope_n_elem: int | None = None,
+        allocate_second_order: bool = True,
+        alpha_exact_tokens: int = 0,
+        alpha_span_max_tokens: int = 64,
+        beta_novelty: bool = False,
+        beta_adaptive_merge: bool = False,
+    ) -> None:
+        super().__init__()
+        batch_size, n_groups, max_seq_length, k_dim = k_shape
+        v_dim = v_shape[-1]
+        device = torch.device(device) if device is not None else torch.device("cuda")
+        dtype = dtype or torch.bfloat16
+        self.batch_size, self.n_groups, self.max_seq_length = batch_size, n_groups, max_seq_length
+        self.k_dim, self.v_dim = k_dim, v_dim
+        self.B = B
+        self.semantic_clusters = bool(semantic_clusters)
+        self.alpha_exact_tokens = int(alpha_exact_tokens)
+        self.alpha_span_max_tokens = int(alpha_span_max_tokens)
+        self.beta_novelty = bool(beta_novelty)
+        self.beta_adaptive_merge = bool(beta_adaptive_merge)
+        self.allocate_second_order = bool(allocate_second_order)
+        # Validation with the reference's messages (litgpt/log_kv_cache.py:739-898).
+        if (self.beta_novelty or self.beta_adaptive_merge) and not self.alpha_exact_tokens:
+            raise ValueError("BetaLogKV requires the Alpha exact-span cache (alpha_exact_tokens > 0)")
+        if self.alpha_exact_tokens < 0:
+            raise ValueError("alpha_exact_tokens must be >= 0")
+        if self.alpha_exact_tokens:
+            if not (semantic_clusters and semantic_anchor_mode == "mid" and not allocate_second_order
+                    and cluster_k_max > 1):
+                raise ValueError("AlphaLogKV requires semantic clusters, K > 1, mid anchors and no second-order allocation")
+            if semantic_legacy_route or semantic_cluster_chunk_size:
+                raise ValueError("AlphaLogKV archives through the attach or unified route; legacy/chunk-tree routing is not supported")
+            if (seg_gap_max is not None and math.isfinite(seg_gap_max)) or seg_block_level:
+                raise ValueError("AlphaLogKV requires disabled segment gaps/padding for delayed archival")
+            if not 1 <= self.alpha_span_max_tokens <= self.alpha_exact_tokens:
+                raise ValueError("alpha_span_max_tokens must be in [1, alpha_exact_tokens]")
+        if semantic_anchor_mode not in ("mid", "multi"):
+            raise ValueError("semantic_anchor_mode must be 'mid' or 'multi'")
+        if semantic_pack_backend not in ("auto", "torch", "triton", "hip"):
+            raise ValueError("semantic_pack_backend must be 'auto', 'torch', 'triton' or 'hip'")
+        if semantic_centroid_backend not in ("sequential", "parallel"):
+            raise ValueError("semantic_centroid_backend must be sequential or parallel")
+        if semantic_merge_passes < 1:
+            raise ValueError("semantic_merge_passes must be >= 1")
+        recent = recent_size if recent_size > 0 else 2
+        if recent < 2:
+            raise ValueError(f"recent_size ({recent}) must be >= 2")
+        if not 1 <= semantic_flush_granularity <= recent:
+            raise ValueError(
+                "semantic_flush_granularity must be in [1, recent_size], got "
+                f"{semantic_flush_granularity} for recent_size={recent}")
+        if not (math.isfinite(cluster_lambda_rel) and cluster_lambda_rel > 0.0):
+            raise ValueError(f"cluster_lambda_rel must be finite and > 0, got {cluster_lambda_rel}")
+        if not (math.isfinite(seg_g0) and seg_g0 > 0.0):
+            raise ValueError(f"seg_g0 must be finite and > 0, got {seg_g0}")
+        if cos_cache is None or sin_cache is None or rope_n_elem is None:
+            raise ValueError("semantic LogKV requires cos_cache, sin_cache, and rope_n_elem")
+        # The path this library implements; everything else is a different algorithm.
+        unsupported = []
+        if not semantic_clusters or cluster_k_max <= 1:
+            unsupported.append("semantic_clusters with cluster_k_max > 1")
+        if semantic_unified_route:
+            unsupported.append("semantic_unified_route=False (the unified Ward route is not built)")
+        if semantic_legacy_route or semantic_cluster_chunk_size:
+            unsupported.append("attach routing (no legacy / chunk-tree route)")
+        if semantic_capacity_beta or semantic_capacity_hard_cap_mult:
+            unsupported.append("no capacity penalty or hard cap")
+        if (seg_gap_max is not None and math.isfinite(seg_gap_max)) or seg_block_level:
+            unsupported.append("no segment gaps or padding")
+        if semantic_anchor_mode != "mid":
+            unsupported.append("semantic_anchor_mode='mid'")
+        if allocate_second_order:
+            unsupported.append("allocate_second_order=False")
+        if importance_pooling:
+            unsupported.append("importance_pooling=False")
+        if dtype != torch.bfloat16:
+            unsupported.append("bfloat16 storage")
+        if cluster_k_max > 32:
+            unsupported.append("cluster_k_max <= 32")
+        if unsupported:
+            raise NotImplementedError("logkv_amd implements the attach/mid/first-order flush path only; requires "
+                                      + "; ".join(unsupported))
+        if device.type != "cuda":
+            raise ValueError(f"logkv_amd caches live on a ROCm device, got {device}")
+
+        self.K_max = int(cluster_k_max)
+        self.cluster_lambda_rel = float(cluster_lambda_rel)
+        self.seg_eta, self.seg_g0 = float(seg_eta), float(seg_g0)
+        self.seg_gap_max, self.seg_block_level, self.seg_forget = math.inf, 0, float(seg_forget)
+        self.recent_size = recent
+        self.semantic_flush_granularity = int(semantic_flush_granularity)
+        self.semantic_anchor_mode = semantic_anchor_mode
+        self.semantic_pack_backend = semantic_pack_backend
+        self.semantic_centroid_backend = semantic_centroid_backend
+        self.semantic_replay_updates = bool(semantic_replay_updates)
+        self.semantic_unified_route = False
+        self.semantic_legacy_route = False
+        self.rope_n_elem = int(rope_n_elem)
+        self.register_buffer("cos_cache", cos_cache.to(device=device), persistent=False)
+        self.register_buffer("sin_cache", sin_cache.to(device=device), persistent=False)
+        self.slot_k_dim = int(cos_cache.size(1)) + k_dim - self.rope_n_elem
+        element = torch.empty((), dtype=dtype).element_size()
+        B_eff, L, budget = ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, self.K_max,
+                                         self.alpha_exact_tokens, element)
+        if budget is not None:
+            self.alpha_baseline_B = B
+            self.alpha_budget_bytes = budget
+        self.B = self.B_prime = B_eff
+        self.max_levels = self.L_alloc = L
+        self.recent_capacity = 2 * recent
+        self.token_count = 0
+        self.recent_count = 0
+        self._mid_decode_state = None
+        self._second_order = False
+
+        def buf(name, value):
+            self.register_buffer(name, value, persistent=False)
+
+        cap = self.recent_capacity
+        buf("recent_k", torch.zeros(batch_size, n_groups, cap, self.slot_k_dim, device=device, dtype=dtype))
+        buf("recent_v", torch.zeros(batch_size, n_groups, cap, v_dim, device=device, dtype=dtype))
+        buf("recent_k_raw", torch.zeros(batch_size, n_groups, cap, k_dim, device=device, dtype=dtype))
+        buf("recent_pos", torch.zeros(batch_size, cap, device=device, dtype=torch.int64))
+        self._recent_pos_host = [[0] * cap for _ in range(batch_size)]
+        self.alpha_count = 0
+        if self.alpha_exact_tokens:
+            P = self.alpha_exact_tokens
+            buf("alpha_k_raw", torch.zeros(batch_size, n_groups, P, k_dim, device=device, dtype=dtype))
+            buf("alpha_v", torch.zeros(batch_size, n_groups, P, v_dim, device=device, dtype=dtype))
+            buf("alpha_pos", torch.zeros(batch_size, P, device=device, dtype=torch.int64))
+            buf("alpha_valid", torch.zeros(batch_size, P, device=device, dtype=torch.bool))
+            self._alpha_spans = [[] for _ in range(batch_size)]
+            self._alpha_positions = [[] for _ in range(batch_size)]
+            self._recent_span_ends = [[False] * cap for _ in range(batch_size)]
+        shp = (batch_size, n_groups, self.K_max, L, B_eff)
+        i64max = torch.iinfo(torch.int64).max
+        buf("level_k", torch.zeros(*shp, k_dim, device=device, dtype=dtype))
+        buf("level_v", torch.zeros(*shp, v_dim, device=device, dtype=dtype))
+        buf("level_w", torch.zeros(shp, device=device, dtype=torch.float32))
+        buf("level_imp", torch.zeros(shp, device=device, dtype=torch.float32))
+        buf("level_count", torch.zeros(shp[:-1], device=device, dtype=torch.int16))
+        buf("pad_mask", torch.zeros(shp, device=device, dtype=torch.bool))
+        buf("level_p_lo", torch.full(shp, i64max, device=device, dtype=torch.int64))
+        buf("level_p_hi", torch.full(shp, -1, device=device, dtype=torch.int64))
+        buf("level_sum_wp", torch.zeros(shp, device=device, dtype=torch.int64))
+        buf("level_order", torch.zeros(shp, device=device, dtype=torch.int64))
+        lanes = (batch_size, n_groups, self.K_max)
+        buf("centroid", torch.zeros(*lanes, k_dim, device=device, dtype=torch.float32))
+        buf("n_eff", torch.zeros(lanes, device=device, dtype=torch.float32))
+        buf("n_total", torch.zeros(lanes, device=device, dtype=torch.int32))
+        buf("p_hi_c", torch.full(lanes, -1, device=device, dtype=torch.int64))
+        buf("current_segment", torch.zeros(lanes, device=device, dtype=torch.int32))
+        buf("level0_phase", torch.zeros(lanes, device=device, dtype=torch.int32))
+        buf("alive", torch.zeros(lanes, device=device, dtype=torch.bool))
+        if semantic_s_h is None:
+            s_h = torch.ones(batch_size, n_groups, device=device, dtype=torch.float32)
+        elif isinstance(semantic_s_h, torch.Tensor):
+            s_h = semantic_s_h.to(device=device, dtype=torch.float32)
+            if s_h.shape == (n_groups,):
+                s_h = s_h.unsqueeze(0).expand(batch_size, -1).contiguous()
+            elif s_h.shape != (batch_size, n_groups):
+                raise ValueError(f"semantic_s_h must have shape ({n_groups},) or ({batch_size},{n_groups}), got {tuple(s_h.shape)}")
+        else:
+            s_h = torch.full((batch_size, n_groups), float(semantic_s_h), device=device, dtype=torch.float32)
+        if not bool(torch.isfinite(s_h).all().item()) or not bool((s_h > 0).all().item()):
+            raise ValueError("semantic_s_h must be finite and > 0")
+        buf("s_h", s_h.contiguous())
+        self._workspace = None
+        self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
+                                   1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0)
+
+    # ------------------------------------------------------------------
+    # C-ABI views
+    # ------------------------------------------------------------------
+    def _ladder_view(self) -> LadderView:
+        return LadderView(
+            ptr(self.level_k), ptr(self.level_v), ptr(self.level_w), ptr(self.level_p_lo), ptr(self.level_p_hi),
+            ptr(self.level_sum_wp), ptr(self.level_order), ptr(self.pad_mask), ptr(self.level_count),
+            ptr(self.centroid), ptr(self.n_eff), ptr(self.n_total), ptr(self.p_hi_c), ptr(self.level0_phase),
+            ptr(self.alive), ptr(self.s_h),
+            self.batch_size, self.n_groups, self.K_max, self.L_alloc, self.B_prime, self.k_dim, self.v_dim,
+        )
+
+    def _workspace_for(self, view: LadderView, tokens: int) -> torch.Tensor:
+        need = lib().logkv_route_workspace_bytes(C.byref(view), tokens, self._params.late_joins)
+        if need < 0:
+            raise ValueError("invalid cache layout for the HIP route")
+        if self._workspace is None or self._workspace.numel() < need:
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.level_k.device)
+        return self._workspace
+
+    @staticmethod
+    def _rows_view(k_raw, v, positions, counts=None) -> RowsView:
+        for name, t in (("k_raw", k_raw), ("v", v)):
+            if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+                raise ValueError(f"{name} must be bf16 with a contiguous last axis")
+        if positions.dtype != torch.int64 or positions.stride(-1) != 1:
+            raise ValueError("positions must be int64 with a contiguous last axis")
+        return RowsView(
+            ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            ptr(positions), positions.stride(0), ptr(counts), k_raw.size(2),
+        )
+
+    # ------------------------------------------------------------------
+    # Flush
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def route_and_flush_batch(self, k_raw, v, positions, *, positions_host=None, record_op_log=False,
+                              replay_op_log=None, replay_op_log_len=None, replay_op_log_host=None,
+                              replay_plans=None, span_ends=None, counts=None, assign_out=None, order_out=None):
+        """Route one flush of rows ``[Bt, G, T, D]`` and commit them (litgpt/log_kv_cache.py:4946-5128)."""
+        if record_op_log or replay_op_log is not None or replay_plans is not None:
+            raise NotImplementedError("op-log record/replay is not part of the logkv_amd flush path")
+        if positions.dim() == 1:
+            positions = positions.unsqueeze(0).expand(k_raw.size(0), -1)
+        for t, what in ((k_raw, "k_raw"), (v, "v"), (positions, "positions")):
+            require_device(t, what)
+        if k_raw.shape[:2] != (self.batch_size, self.n_groups) or v.shape[:3] != k_raw.shape[:3]:
+            raise ValueError("flush rows must be [batch, groups, T, dim] matching the cache")
+        self._mid_decode_state = None
+        if self.alpha_exact_tokens:
+            return self._alpha_route_flush(k_raw, v, positions, positions_host, span_ends)
+        self._route_commit(k_raw, v, positions, counts, assign_out, order_out)
+
+    def _route_commit(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None):
+        view = self._ladder_view()
+        rows = self._rows_view(k_raw, v, positions, counts)
+        ws = self._workspace_for(view, rows.tokens)
+        rc = lib().logkv_route_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                      ptr(assign_out), ptr(order_out), stream_of(k_raw.device))
+        check(rc, "logkv_route_commit")
+
+    def _alpha_route_flush(self, k_raw, v, positions, positions_host, span_ends):
+        from .alpha_log_kv import alpha_flush
+        return alpha_flush(self, k_raw, v, positions, positions_host, span_ends)
+
+    def _semantic_flush_tokens(self, flush_len: int, span_ends=None) -> None:
+        pending = int(flush_len)
+        while pending > 0:
+            take = min(self.semantic_flush_granularity, pending)
+            if take > self.recent_count:
+                raise RuntimeError(f"semantic LogKV cannot flush {take} tokens from recent_count={self.recent_count}")
+            self.route_and_flush_batch(
+                self.recent_k_raw[:, :, :take], self.recent_v[:, :, :take], self.recent_pos[:, :take],
+                positions_host=[row[:take] for row in self._recent_pos_host],
+                span_ends=[row[:take] for row in self._recent_span_ends] if self.alpha_exact_tokens else None,
+            )
+            remaining = self.recent_count - take
+            if remaining > 0:
+                stage = (lambda x: x) if remaining <= take else torch.Tensor.clone
+                for name in ("recent_k", "recent_k_raw", "recent_v"):
+                    t = getattr(self, name)
+                    t[:, :, :remaining].copy_(stage(t[:, :, take:self.recent_count]))
+                self.recent_pos[:, :remaining].copy_(stage(self.recent_pos[:, take:self.recent_count]))
+                for b in range(self.batch_size):
+                    self._recent_pos_host[b][:remaining] = self._recent_pos_host[b][take:self.recent_count]
+                    if self.alpha_exact_tokens:
+                        self._recent_span_ends[b][:remaining] = self._recent_span_ends[b][take:self.recent_count]
+            self.recent_count = remaining
+            pending -= take
+
+    def _input_positions(self, n, input_pos):
+        dev = self.recent_k.device
+        if input_pos is None:
+            host = list(range(self.token_count, self.token_count + n))
+            return (torch.arange(self.token_count, self.token_count + n, device=dev).unsqueeze(0)
+                    .expand(self.batch_size, -1), [host[:] for _ in range(self.batch_size)])
+        if input_pos.dim() == 1:
+            values = [int(x) for x in input_pos.detach().cpu().tolist()] if self.alpha_exact_tokens else None
+            dev_pos = input_pos.to(dev, torch.int64).unsqueeze(0).expand(self.batch_size, -1)
+            return dev_pos, None if values is None else [values[:] for _ in range(self.batch_size)]
+        if input_pos.dim() == 2:
+            host = ([[int(x) for x in row] for row in input_pos.detach().cpu().tolist()]
+                    if self.alpha_exact_tokens else None)
+            return input_pos.to(dev, torch.int64), host
+        raise ValueError(f"input_pos must be 1-D or 2-D, got shape {tuple(input_pos.shape)}")
+
+    @torch.no_grad()
+    def add_recent(self, k, v, *, k_raw=None, input_pos=None, record_op_log=False, replay_op_log=None,
+                   replay_op_log_len=None, replay_op_log_host=None, replay_plans=None, span_ends=None):
+        """Append a block to the recent window; flush whole granules on overflow
+        (litgpt/log_kv_cache.py:5668-5718, :5847)."""
+        if k_raw is None:
+            raise ValueError("semantic LogKV add_recent requires pre-RoPE k_raw")
+        if record_op_log or replay_op_log is not None or replay_plans is not None:
+            raise NotImplementedError("op-log record/replay is not part of the logkv_amd flush path")
+        n = k.size(2)
+        if n > self.recent_size:
+            raise ValueError(f"chunk size {n} exceeds recent_size {self.recent_size}")
+        if k_raw.shape[:3] != k.shape[:3] or k_raw.size(-1) != self.k_dim:
+            raise ValueError(f"k_raw shape {tuple(k_raw.shape)} does not match semantic cache shape")
+        positions, positions_host = self._input_positions(n, input_pos)
+        if self.alpha_exact_tokens:
+            if span_ends is None or len(span_ends) != self.batch_size or any(len(row) != n for row in span_ends):
+                raise ValueError("AlphaLogKV span boundaries must match the input batch and token count")
+            for b in range(self.batch_size):
+                self._recent_span_ends[b][self.recent_count:self.recent_count + n] = list(span_ends[b])
+        if self.token_count + n > self.max_seq_length:
+            raise RuntimeError(
+                f"LogStructuredKVCache: token overflow! token_count={self.token_count}, n={n}, "
+                f"max_seq_length={self.max_seq_length}.")
+        self.token_count += n
+        if self.recent_count + n > self.recent_capacity:
+            raise RuntimeError(f"semantic LogKV recent buffer overflow: recent_count={self.recent_count}, n={n}, "
+                               f"capacity={self.recent_capacity}")
+        dst = slice(self.recent_count, self.recent_count + n)
+        self.recent_k[:, :, dst] = k
+        self.recent_k_raw[:, :, dst] = k_raw
+        self.recent_v[:, :, dst] = v
+        self.recent_pos[:, dst] = positions
+        if positions_host is not None:
+            for b in range(self.batch_size):
+                self._recent_pos_host[b][self.recent_count:self.recent_count + n] = positions_host[b]
+        self.recent_count += n
+        overflow = self.recent_count - self.recent_size
+        if overflow > 0:
+            F = self.semantic_flush_granularity
+            self._semantic_flush_tokens(F * ((overflow + F - 1) // F))
+
+    def reset_parameters(self) -> None:
+        """Empty cache (litgpt/log_kv_cache.py:6270)."""
+        i64max = torch.iinfo(torch.int64).max
+        for name in ("recent_k", "recent_v", "recent_k_raw", "recent_pos", "level_k", "level_v", "level_w",
+                     "level_imp", "level_count", "pad_mask", "level_sum_wp", "level_order", "centroid", "n_eff",
+                     "n_total", "current_segment", "level0_phase", "alive"):
+            getattr(self, name).zero_()
+        self.level_p_lo.fill_(i64max)
+        self.level_p_hi.fill_(-1)
+        self.p_hi_c.fill_(-1)
+        self.token_count = self.recent_count = self.alpha_count = 0
+        self._mid_decode_state = None
+        self._recent_pos_host = [[0] * self.recent_capacity for _ in range(self.batch_size)]
+        if self.alpha_exact_tokens:
+            for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid"):
+                getattr(self, name).zero_()
+            self._alpha_spans = [[] for _ in range(self.batch_size)]
+            self._alpha_positions = [[] for _ in range(self.batch_size)]
+            self._recent_span_ends = [[False] * self.recent_capacity for _ in range(self.batch_size)]
+
+    # ------------------------------------------------------------------
+    # Host mirrors of the reference, read from the device on demand
+    # ------------------------------------------------------------------
+    @property
+    def _semantic_counts(self):
+        return self.level_count.long().cpu().tolist()
+
+    @property
+    def _semantic_alive(self):
+        return self.alive.cpu().tolist()
+
+    @property
+    def _semantic_p_hi_c(self):
+        return self.p_hi_c.cpu().tolist()
+
+    @property
+    def _semantic_n_total(self):
+        return self.n_total.long().cpu().tolist()
+
+    @property
+    def _semantic_level0_phase(self):
+        return self.level0_phase.long().cpu().tolist()
+
+    @property
+    def second_order(self) -> bool:
+        return False
+
+    @second_order.setter
+    def second_order(self, value: bool) -> None:
+        if value:
+            raise RuntimeError("Second-order storage is disabled; rebuild the cache with allocate_second_order=True")

@@ -1,0 +1,94 @@
+"""Device flush (route + commit) against the oracle, bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+from harness import compare_state, feed, make_pair, to_np
+from logkv_amd.workloads import Mixture
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    # name: (batch, groups, dim, K, B, recent, flush, max_seq, s_h, blocks)
+    "small": (2, 2, 64, 4, 8, 32, 32, 1024, 16.0, 6),
+    "mixture": (1, 4, 128, 12, 16, 128, 128, 4096, 64.0, 6),
+    "qwen_layer": (1, 8, 128, 12, 128, 2048, 2048, 32768, 64.0, 3),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_flush_matches_oracle(name):
+    batch, groups, dim, K, B, recent, flush, max_seq, s_h, blocks = CASES[name]
+    print(f"case {name}", flush=True)
+    gpu, ora = make_pair(batch, groups, dim, K, B, recent, flush, max_seq, s_h)
+    mix = Mixture(batch, groups, dim, clusters=K, seed=7)
+    for blk in range(blocks):
+        feed(gpu, ora, mix, blk * recent, recent)
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"block {blk}: " + "; ".join(bad)
+    assert int(to_np(gpu.alive).sum()) > 0
+
+
+def test_top_level_fold_and_skewed_cluster():
+    """One hot cluster saturates every level, so the top level folds."""
+    batch, groups, dim, K, B = 1, 2, 64, 4, 4
+    gpu, ora = make_pair(batch, groups, dim, K, B, recent=64, flush=64, max_seq=64, s_h=1e9)
+    assert gpu.L_alloc == ora.L
+    mix = Mixture(batch, groups, dim, clusters=1, seed=3, outlier=0.0)
+    dev = gpu.level_k.device
+    start = 0
+    for n in (1, 40, 64, 64, 64, 64):
+        k, v = mix.rows(n), mix.rows(n)
+        pos = torch.arange(start, start + n).unsqueeze(0).expand(batch, -1).contiguous()
+        gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev))
+        ora.flush_rows(k.float().numpy(), v.float().numpy(), pos.numpy())
+        start += n
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"after {start} rows: " + "; ".join(bad)
+    counts = to_np(gpu.level_count)
+    assert (counts[..., -1] == B).any(), "top level never saturated"
+
+
+def test_attach_decisions_with_seeds_and_ragged_rows():
+    import ctypes as C
+
+    from logkv_amd._lib import check, lib, ptr, stream_of
+    from oracle import route
+
+    batch, groups, dim, K = 2, 3, 128, 8
+    gpu, ora = make_pair(batch, groups, dim, K, 16, recent=64, flush=64, max_seq=4096, s_h=40.0)
+    mix = Mixture(batch, groups, dim, clusters=K, seed=11)
+    dev = gpu.level_k.device
+    # Warm up: one flush opens clusters; then kill some so seeds are needed again.
+    k, v = mix.rows(64), mix.rows(64)
+    pos = torch.arange(0, 64).unsqueeze(0).expand(batch, -1).contiguous()
+    gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev))
+    ora.flush_rows(k.float().numpy(), v.float().numpy(), pos.numpy())
+    gpu.alive[0, 1, 2:5] = False
+    ora.alive[0, 1, 2:5] = False
+    T = 50
+    k = mix.rows(T)
+    perm = torch.stack([torch.randperm(T, generator=torch.Generator().manual_seed(b)) for b in range(batch)])
+    pos = (100 + perm).contiguous()
+    counts = torch.tensor([T, 37], dtype=torch.int32)
+    view = gpu._ladder_view()
+    # The view holds raw pointers: keep the device tensors alive until the kernels ran.
+    k_dev, pos_dev, counts_dev = k.to(dev), pos.to(dev), counts.to(dev)
+    rows = gpu._rows_view(k_dev, k_dev, pos_dev, counts_dev)
+    ws = gpu._workspace_for(view, T)
+    assign = torch.empty(batch, groups, T, dtype=torch.int8, device=dev)
+    order = torch.empty(batch, T, dtype=torch.int32, device=dev)
+    rc = lib().logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(gpu._params), ptr(ws), ws.numel(),
+                                   ptr(assign), ptr(order), stream_of(dev))
+    check(rc, "attach")
+    torch.cuda.synchronize()
+    want, want_order = route.attach_assign(k.float().numpy(), pos.numpy(), counts.numpy(), ora.centroid, ora.alive,
+                                           ora.p_hi_c, ora.s_h, ora.eta, ora.g0, ora.lam)
+    for b in range(batch):
+        n = int(counts[b])
+        np.testing.assert_array_equal(to_np(order)[b, :n], want_order[b, :n])
+        np.testing.assert_array_equal(to_np(assign)[b, :, :n], want[b, :, :n])
+        assert (to_np(assign)[b, :, n:] == -1).all()
