@@ -92,6 +92,14 @@ int logkv_route_commit(const logkv_ladder_view* cache, const logkv_rows_view* ro
                        const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
                        int8_t* assign, int32_t* order, void* stream);
 
+/* The commit half of logkv_route_commit for decisions already in `assign` /
+ * `order` (from logkv_attach_assign on the same rows and cache state, or NULL
+ * for the copies left in the same workspace). Lets a caller time or overlap
+ * the two halves; same replaced reference interfaces as logkv_route_commit. */
+int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                      const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                      const int8_t* assign, const int32_t* order, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,8 @@ SIGNATURES = {
                                    _p, _i64, _p, _p, _p]),
     "logkv_route_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
                                   _p, _i64, _p, _p, _p]),
+    "logkv_commit_only": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
+                                 _p, _i64, _p, _p, _p]),
 }
 
 

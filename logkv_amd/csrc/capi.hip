@@ -145,4 +145,17 @@ int logkv_route_commit(const logkv_ladder_view* cache, const logkv_rows_view* ro
   return LOGKV_OK;
 }
 
+int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
+                      void* workspace, int64_t workspace_bytes, const int8_t* assign, const int32_t* order,
+                      void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, const_cast<int8_t*>(assign),
+                 const_cast<int32_t*>(order), ws);
+  if (rc) return rc;
+  if (!rows->tokens) return LOGKV_OK;
+  rc = logkv::launch_commit(*cache, *rows, *params, ws, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"
