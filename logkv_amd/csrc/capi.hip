@@ -50,7 +50,7 @@ int check_rows(const logkv_ladder_view* c, const logkv_rows_view* r) {
 }
 
 struct Plan {
-  int64_t order, assign, s_win, dist, ladder, total;
+  int64_t order, assign, s_win, dist, snap, ladder, total;
   int64_t stride, s0, ca, cb;
   int32_t sort_width;
 };
@@ -61,7 +61,7 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   const int64_t ladders = lanes * c->k_max;
   const int64_t existing = late ? int64_t(c->levels) * c->slots : 0;
   const int64_t m0 = tokens + existing;
-  logkv::ladder_scratch_rows(m0, c->slots, p.s0, p.ca, p.cb, existing);
+  logkv::ladder_scratch_rows(m0, c->slots, p.s0, p.ca, p.cb, late ? m0 : 0);
   p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.ca, p.cb));
   int64_t off = 0;
   p.order = off;
@@ -72,6 +72,8 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   off += align256(lanes * tokens * 4);
   p.dist = off;
   off += align256(lanes * tokens * 4);
+  p.snap = off;
+  off += align256(ladders);
   p.ladder = off;
   off += ladders * p.stride;
   p.total = off;
@@ -99,6 +101,7 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   ws.assign = assign ? assign : reinterpret_cast<int8_t*>(base + p.assign);
   ws.s_win = reinterpret_cast<float*>(base + p.s_win);
   ws.dist = reinterpret_cast<float*>(base + p.dist);
+  ws.snap_alive = base + p.snap;
   ws.ladder = base + p.ladder;
   ws.ladder_stride = p.stride;
   ws.s0_rows = p.s0;

@@ -18,6 +18,26 @@
 
 namespace logkv {
 
+// Address-space-qualified pointers: loads and stores through them compile to
+// global_* / ds_* instructions instead of flat_* ones, which the compiler must
+// fence against both memory counters (a generic pointer might be LDS).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define LOGKV_G __attribute__((address_space(1)))
+#define LOGKV_S __attribute__((address_space(3)))
+#else
+#define LOGKV_G
+#define LOGKV_S
+#endif
+
+template <typename T>
+__device__ __forceinline__ LOGKV_G T* gp(T* p) {
+  return (LOGKV_G T*)p;
+}
+template <typename T>
+__device__ __forceinline__ const LOGKV_G T* gp(const T* p) {
+  return (const LOGKV_G T*)p;
+}
+
 constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

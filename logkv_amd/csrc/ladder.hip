@@ -18,18 +18,20 @@ namespace logkv {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kChunkRows = 64;   // survivor rows moved per barrier
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMoveUnits = 8;    // 8-byte units per thread staged in registers per move chunk
+constexpr int kCenterRows = 128;  // key rows staged in LDS per center-update chunk
 
 struct Soa {
-  uint16_t* k;
-  uint16_t* v;
-  float* w;
-  int64_t* lo;
-  int64_t* hi;
-  int64_t* swp;
-  int64_t* ord;
-  uint8_t* pad;
+  LOGKV_G uint16_t* k;
+  LOGKV_G uint16_t* v;
+  LOGKV_G float* w;
+  LOGKV_G int64_t* lo;
+  LOGKV_G int64_t* hi;
+  LOGKV_G int64_t* swp;
+  LOGKV_G int64_t* ord;
+  LOGKV_G uint8_t* pad;
 };
 
 __host__ __device__ inline int64_t align16(int64_t x) { return (x + 15) & ~int64_t(15); }
@@ -40,21 +42,21 @@ __host__ __device__ inline int64_t soa_bytes(int64_t cap, int dk, int dv) {
 
 __device__ inline Soa soa_at(uint8_t* base, int64_t cap, int dk, int dv) {
   Soa s;
-  s.k = reinterpret_cast<uint16_t*>(base);
+  s.k = gp(reinterpret_cast<uint16_t*>(base));
   base += align16(cap * dk * 2);
-  s.v = reinterpret_cast<uint16_t*>(base);
+  s.v = gp(reinterpret_cast<uint16_t*>(base));
   base += align16(cap * dv * 2);
-  s.w = reinterpret_cast<float*>(base);
+  s.w = gp(reinterpret_cast<float*>(base));
   base += align16(cap * 4);
-  s.lo = reinterpret_cast<int64_t*>(base);
+  s.lo = gp(reinterpret_cast<int64_t*>(base));
   base += align16(cap * 8);
-  s.hi = reinterpret_cast<int64_t*>(base);
+  s.hi = gp(reinterpret_cast<int64_t*>(base));
   base += align16(cap * 8);
-  s.swp = reinterpret_cast<int64_t*>(base);
+  s.swp = gp(reinterpret_cast<int64_t*>(base));
   base += align16(cap * 8);
-  s.ord = reinterpret_cast<int64_t*>(base);
+  s.ord = gp(reinterpret_cast<int64_t*>(base));
   base += align16(cap * 8);
-  s.pad = base;
+  s.pad = gp(base);
   return s;
 }
 
@@ -67,73 +69,31 @@ struct Meta {
 // Where the staged rows of the current level come from.
 //  kind 0: flush rows tok[r] of the lane (w=1, anchors = position, order = base + r)
 //  kind 1: a scratch SoA buffer
-//  kind 2: delayed archive, row r = perm[r] over [existing entries in S0 | flush rows tok[]]
 struct Src {
   int kind;
-  const uint16_t* tok;
+  const LOGKV_S uint16_t* tok;
   int64_t order_base;
-  const uint16_t* kb;
-  const uint16_t* vb;
+  const LOGKV_G uint16_t* kb;
+  const LOGKV_G uint16_t* vb;
   int64_t k_st, v_st;
-  const int64_t* posb;
+  const LOGKV_G int64_t* posb;
   Soa buf;
-  const uint16_t* perm;
-  int n_exist;
 };
 
 struct Ladder {
-  uint16_t* k;
-  uint16_t* v;
-  float* w;
-  int64_t* lo;
-  int64_t* hi;
-  int64_t* swp;
-  int64_t* ord;
-  uint8_t* pad;
+  LOGKV_G uint16_t* k;
+  LOGKV_G uint16_t* v;
+  LOGKV_G float* w;
+  LOGKV_G int64_t* lo;
+  LOGKV_G int64_t* hi;
+  LOGKV_G int64_t* swp;
+  LOGKV_G int64_t* ord;
+  LOGKV_G uint8_t* pad;
   int dk, dv, B;
 };
 
-__device__ __forceinline__ const uint16_t* src_k(const Src& s, int r, int dk) {
-  if (s.kind == 1) return s.buf.k + static_cast<int64_t>(r) * dk;
-  if (s.kind == 2) {
-    const int q = s.perm[r];
-    if (q < s.n_exist) return s.buf.k + static_cast<int64_t>(q) * dk;
-    return s.kb + static_cast<int64_t>(s.tok[q - s.n_exist]) * s.k_st;
-  }
-  return s.kb + static_cast<int64_t>(s.tok[r]) * s.k_st;
-}
-
-__device__ __forceinline__ const uint16_t* src_v(const Src& s, int r, int dv) {
-  if (s.kind == 1) return s.buf.v + static_cast<int64_t>(r) * dv;
-  if (s.kind == 2) {
-    const int q = s.perm[r];
-    if (q < s.n_exist) return s.buf.v + static_cast<int64_t>(q) * dv;
-    return s.vb + static_cast<int64_t>(s.tok[q - s.n_exist]) * s.v_st;
-  }
-  return s.vb + static_cast<int64_t>(s.tok[r]) * s.v_st;
-}
-
 __device__ __forceinline__ Meta soa_meta(const Soa& b, int64_t i) {
   return Meta{b.w[i], b.lo[i], b.hi[i], b.swp[i], b.ord[i], b.pad[i]};
-}
-
-__device__ __forceinline__ Meta src_meta(const Src& s, int r) {
-  if (s.kind == 1) return soa_meta(s.buf, r);
-  int t;
-  if (s.kind == 2) {
-    const int q = s.perm[r];
-    if (q < s.n_exist) {
-      Meta m = soa_meta(s.buf, q);
-      m.ord = r;
-      return m;
-    }
-    t = s.tok[q - s.n_exist];
-    const int64_t p = s.posb[t];
-    return Meta{1.0f, p, p, p, static_cast<int64_t>(r), 0};
-  }
-  t = s.tok[r];
-  const int64_t p = s.posb[t];
-  return Meta{1.0f, p, p, p, s.order_base + r, 0};
 }
 
 __device__ __forceinline__ Meta slot_meta(const Ladder& L, int64_t i) {
@@ -171,32 +131,73 @@ __device__ __forceinline__ Meta merge_meta(const Meta& a, const Meta& b) {
   return m;
 }
 
-// Pool row p of a level: storage slot p (p < B) or staged row take + p - B.
-struct Pool {
-  const Ladder* L;
-  int64_t level_base;  // row index of slot 0 of this level
-  const Src* src;
-  int take;
-  __device__ __forceinline__ bool stored(int p) const { return p < L->B; }
-  __device__ __forceinline__ const uint16_t* k(int p) const {
-    return stored(p) ? L->k + (level_base + p) * L->dk : src_k(*src, take + p - L->B, L->dk);
+// Virtual pool of one level: [stored slots 0..cnt | staged rows 0..m]. Filling
+// the free slots and then pairing the oldest rows of [stored | rest of staged]
+// (litgpt/log_kv_cache.py:1815-1853) only ever reads this sequence, so a level
+// step is a function of it and needs no barrier between fill and pairing.
+// KIND is the staged source (0 flush rows, 1 scratch rows); row addresses are
+// resolved with selects so the copy loops stay branch-free.
+template <int KIND>
+struct PoolT {
+  Ladder L;
+  int64_t base;  // row index of slot 0 of this level
+  int cnt;       // rows stored before this step
+  Src src;
+  __device__ __forceinline__ int64_t staged_row(int q) const {
+    return KIND == 1 ? static_cast<int64_t>(q) : static_cast<int64_t>(src.tok[q]);
   }
-  __device__ __forceinline__ const uint16_t* v(int p) const {
-    return stored(p) ? L->v + (level_base + p) * L->dv : src_v(*src, take + p - L->B, L->dv);
+  __device__ __forceinline__ const LOGKV_G uint16_t* k(int p) const {
+    const bool st = p < cnt;
+    const int q = st ? 0 : p - cnt;
+    const LOGKV_G uint16_t* staged =
+        KIND == 1 ? src.buf.k + staged_row(q) * L.dk : src.kb + staged_row(q) * src.k_st;
+    return st ? L.k + (base + p) * L.dk : staged;
+  }
+  __device__ __forceinline__ const LOGKV_G uint16_t* v(int p) const {
+    const bool st = p < cnt;
+    const int q = st ? 0 : p - cnt;
+    const LOGKV_G uint16_t* staged =
+        KIND == 1 ? src.buf.v + staged_row(q) * L.dv : src.vb + staged_row(q) * src.v_st;
+    return st ? L.v + (base + p) * L.dv : staged;
+  }
+  __device__ __forceinline__ float w(int p) const {
+    if (KIND == 0) return p < cnt ? L.w[base + p] : 1.0f;
+    const bool st = p < cnt;
+    const LOGKV_G float* wp = st ? L.w + base + p : src.buf.w + (p - cnt);
+    return *wp;
   }
   __device__ __forceinline__ Meta meta(int p) const {
-    return stored(p) ? slot_meta(*L, level_base + p) : src_meta(*src, take + p - L->B);
+    if (p < cnt) return slot_meta(L, base + p);
+    if (KIND == 1) return soa_meta(src.buf, p - cnt);
+    const int q = p - cnt;
+    const int64_t pos = src.posb[src.tok[q]];
+    return Meta{1.0f, pos, pos, pos, src.order_base + q, 0};
+  }
+};
+
+// Thread -> (row, unit) decomposition of a row-major K|V copy: thread t owns
+// unit t % units of rows t / units, t / units + rows_per_pass, ...
+struct RowUnits {
+  int ku, units, u, r0, step;
+  __device__ __forceinline__ RowUnits(int dk, int dv) {
+    ku = dk / 4;
+    units = (dk + dv) / 4;
+    u = static_cast<int>(threadIdx.x) % units;
+    r0 = static_cast<int>(threadIdx.x) / units;
+    step = kThreads / units;
+    if (r0 >= step) r0 = 1 << 30;  // threads past the last full pass stay idle
   }
 };
 
 // Copy 4 bf16 (8 bytes) units of a K|V row; unit u < dk/4 is K, the rest V.
-__device__ __forceinline__ uint2 load_unit(const uint16_t* k, const uint16_t* v, int u, int ku) {
-  return u < ku ? *reinterpret_cast<const uint2*>(k + 4 * u) : *reinterpret_cast<const uint2*>(v + 4 * (u - ku));
+__device__ __forceinline__ uint2 load_unit(const LOGKV_G uint16_t* k, const LOGKV_G uint16_t* v, int u, int ku) {
+  const LOGKV_G uint16_t* p = u < ku ? k + 4 * u : v + 4 * (u - ku);
+  return *(const LOGKV_G uint2*)p;
 }
 
-__device__ __forceinline__ void store_unit(uint16_t* k, uint16_t* v, int u, int ku, uint2 x) {
-  if (u < ku) *reinterpret_cast<uint2*>(k + 4 * u) = x;
-  else *reinterpret_cast<uint2*>(v + 4 * (u - ku)) = x;
+__device__ __forceinline__ void store_unit(LOGKV_G uint16_t* k, LOGKV_G uint16_t* v, int u, int ku, uint2 x) {
+  LOGKV_G uint16_t* p = u < ku ? k + 4 * u : v + 4 * (u - ku);
+  *(LOGKV_G uint2*)p = x;
 }
 
 __device__ __forceinline__ float lo_half(uint32_t x) { return __uint_as_float(x << 16); }
@@ -214,104 +215,132 @@ __device__ __forceinline__ uint2 blend_unit(uint2 a, uint2 b, float alpha) {
   return o;
 }
 
-// Rows [0, n) of `src` to storage slots [dst0, dst0 + n) (no overlap with the source).
-__device__ void copy_src_to_slots(const Ladder& L, int64_t level_base, const Src& src, int src0, int dst0, int n) {
-  const int ku = L.dk / 4, units = (L.dk + L.dv) / 4;
-  for (int i = threadIdx.x; i < n * units; i += kThreads) {
-    const int r = i / units, u = i % units;
-    const int64_t slot = level_base + dst0 + r;
-    store_unit(L.k + slot * L.dk, L.v + slot * L.dv, u, ku, load_unit(src_k(src, src0 + r, L.dk), src_v(src, src0 + r, L.dv), u, ku));
-  }
-  for (int r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, level_base + dst0 + r, src_meta(src, src0 + r));
-}
-
-// Storage slots [from, from + n) -> [to, to + n) with to <= from, overlap allowed.
-// Each chunk is loaded whole before any of it is stored; later chunks never
-// read what earlier chunks wrote because the destination trails the source.
-__device__ void shift_slots_down(const Ladder& L, int64_t level_base, int from, int to, int n) {
-  if (n <= 0 || from == to) return;
-  const int ku = L.dk / 4, units = (L.dk + L.dv) / 4;
-  constexpr int kMaxUnitsPerThread = kChunkRows * (2 * kMaxDim / 4) / kThreads;
-  for (int c0 = 0; c0 < n; c0 += kChunkRows) {
-    const int rows = min(kChunkRows, n - c0);
-    uint2 buf[kMaxUnitsPerThread];
-    Meta m{};
-    const int total = rows * units;
+// Pool rows [p0, p0 + n) -> slots [d0, d0 + n) of the level, d0 <= p0. Each chunk
+// is loaded whole into registers, then a barrier, then stored: a chunk's
+// stores never reach a later chunk's sources because the destination trails
+// the source, and every earlier load of the step precedes the first barrier.
+template <int KIND>
+__device__ __forceinline__ void move_rows(const PoolT<KIND>& pool, int p0, int d0, int n) {
+  const Ladder& L = pool.L;
+  const RowUnits ru(L.dk, L.dv);
+  const int per_chunk = kMoveUnits * ru.step;
+  for (int c0 = 0; c0 < n; c0 += per_chunk) {
+    const int rows = min(per_chunk, n - c0);
+    uint2 buf[kMoveUnits];
 #pragma unroll
-    for (int q = 0; q < kMaxUnitsPerThread; ++q) {
-      const int i = threadIdx.x + q * kThreads;
-      if (i < total) {
-        const int r = i / units, u = i % units;
-        const int64_t s = level_base + from + c0 + r;
-        buf[q] = load_unit(L.k + s * L.dk, L.v + s * L.dv, u, ku);
-      }
+    for (int q = 0; q < kMoveUnits; ++q) {
+      const int r = ru.r0 + q * ru.step;
+      if (r < rows) buf[q] = load_unit(pool.k(p0 + c0 + r), pool.v(p0 + c0 + r), ru.u, ru.ku);
     }
-    if (threadIdx.x < rows) m = slot_meta(L, level_base + from + c0 + threadIdx.x);
+    Meta m{};
+    if (static_cast<int>(threadIdx.x) < rows) m = pool.meta(p0 + c0 + threadIdx.x);
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < kMaxUnitsPerThread; ++q) {
-      const int i = threadIdx.x + q * kThreads;
-      if (i < total) {
-        const int r = i / units, u = i % units;
-        const int64_t d = level_base + to + c0 + r;
-        store_unit(L.k + d * L.dk, L.v + d * L.dv, u, ku, buf[q]);
+    for (int q = 0; q < kMoveUnits; ++q) {
+      const int r = ru.r0 + q * ru.step;
+      if (r < rows) {
+        const int64_t d = pool.base + d0 + c0 + r;
+        store_unit(L.k + d * L.dk, L.v + d * L.dv, ru.u, ru.ku, buf[q]);
       }
     }
-    if (threadIdx.x < rows) put_slot_meta(L, level_base + to + c0 + threadIdx.x, m);
+    if (static_cast<int>(threadIdx.x) < rows) put_slot_meta(L, pool.base + d0 + c0 + threadIdx.x, m);
   }
 }
 
-__device__ void clear_slots(const Ladder& L, int64_t first, int64_t n) {
-  const int ku = L.dk / 4, units = (L.dk + L.dv) / 4;
+constexpr int kBatch = 4;   // rows per thread whose loads are issued before any of their stores
+
+// Staged rows [s0, s0 + n) -> slots [d0, d0 + n); the staged rows never alias the level.
+template <int KIND>
+__device__ __forceinline__ void copy_staged(const Ladder& L, int64_t base, const Src& src, int s0, int d0, int n) {
+  const RowUnits ru(L.dk, L.dv);
+  const PoolT<KIND> pool{L, base, 0, src};
+  for (int r0 = ru.r0; r0 < n; r0 += kBatch * ru.step) {
+    uint2 x[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int r = r0 + q * ru.step;
+      if (r < n) x[q] = load_unit(pool.k(s0 + r), pool.v(s0 + r), ru.u, ru.ku);
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int r = r0 + q * ru.step;
+      if (r < n) {
+        const int64_t slot = base + d0 + r;
+        store_unit(L.k + slot * L.dk, L.v + slot * L.dv, ru.u, ru.ku, x[q]);
+      }
+    }
+  }
+  for (int r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, base + d0 + r, pool.meta(s0 + r));
+}
+
+__device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int64_t n) {
+  const RowUnits ru(L.dk, L.dv);
   const uint2 z = make_uint2(0u, 0u);
-  for (int64_t i = threadIdx.x; i < n * units; i += kThreads) {
-    const int64_t s = first + i / units;
-    store_unit(L.k + s * L.dk, L.v + s * L.dv, static_cast<int>(i % units), ku, z);
+  for (int64_t r = ru.r0; r < n; r += ru.step) {
+    const int64_t s = first + r;
+    store_unit(L.k + s * L.dk, L.v + s * L.dv, ru.u, ru.ku, z);
   }
   for (int64_t r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, first + r, Meta{0.f, 0, 0, 0, 0, 0});
 }
 
-// Carries j in [0, n_carry): pool rows (2j, 2j+1), one wave per carry.
-__device__ void pair_carries(const Pool& pool, const Soa& out, int n_carry, int dk, int dv) {
-  const int ku = dk / 4, units = (dk + dv) / 4;
-  const int l = lane_id(), w = wave_id(), nw = kThreads / kWave;
-  for (int j = w; j < n_carry; j += nw) {
-    const Meta a = pool.meta(2 * j), b = pool.meta(2 * j + 1);
-    const float alpha = a.w / fmaxf(a.w + b.w, 1e-8f);
-    const uint16_t *ak = pool.k(2 * j), *av = pool.v(2 * j), *bk = pool.k(2 * j + 1), *bv = pool.v(2 * j + 1);
-    for (int u = l; u < units; u += kWave)
-      store_unit(out.k + static_cast<int64_t>(j) * dk, out.v + static_cast<int64_t>(j) * dv, u, ku,
-                 blend_unit(load_unit(ak, av, u, ku), load_unit(bk, bv, u, ku), alpha));
-    if (l == 0) put_soa_meta(out, j, merge_meta(a, b));
+// Carries j in [0, n_carry) from pool rows (2j, 2j+1); loads of kBatch carries
+// per thread are issued before their stores.
+template <int KIND>
+__device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa& out, int n_carry, int dk, int dv) {
+  const RowUnits ru(dk, dv);
+  for (int j0 = ru.r0; j0 < n_carry; j0 += kBatch * ru.step) {
+    uint2 a[kBatch], b[kBatch];
+    float wa[kBatch], wb[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int j = j0 + q * ru.step;
+      if (j < n_carry) {
+        wa[q] = pool.w(2 * j);
+        wb[q] = pool.w(2 * j + 1);
+        a[q] = load_unit(pool.k(2 * j), pool.v(2 * j), ru.u, ru.ku);
+        b[q] = load_unit(pool.k(2 * j + 1), pool.v(2 * j + 1), ru.u, ru.ku);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int j = j0 + q * ru.step;
+      if (j < n_carry) {
+        const float alpha = wa[q] / fmaxf(wa[q] + wb[q], 1e-8f);
+        store_unit(out.k + static_cast<int64_t>(j) * dk, out.v + static_cast<int64_t>(j) * dv, ru.u, ru.ku,
+                   blend_unit(a[q], b[q], alpha));
+      }
+    }
   }
+  for (int j = threadIdx.x; j < n_carry; j += kThreads) put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
 }
 
 // ---- Beta 4->2 -------------------------------------------------------------
-constexpr int kJ = kMaxDim / kWave;
 
-// Canonical sum over the features held as x[j] (feature l + 64 j) in every lane.
-__device__ __forceinline__ float feat_sum(const float* t, int J) {
+// Canonical sum over the features held as t[j] (feature l + 64 j) in every lane.
+template <int NJ>
+__device__ __forceinline__ float feat_sum(const float* t) {
   float s = t[0];
 #pragma unroll
-  for (int j = 1; j < kJ; ++j)
-    if (j < J) s = s + t[j];
+  for (int j = 1; j < NJ; ++j) s = s + t[j];
   return wave_tree(s);
 }
 
-// Loss sum_i w_i |x_i - mean|^2 of one side; rows outside the side contribute +0.
-__device__ float side_loss(const float (*x)[kJ], const float* wt, const float* mean, int J, int D, unsigned member) {
+// sum_i w_i |x_i - mean|^2 over rows of one side; rows outside the side add +0.
+template <int NJ>
+__device__ __forceinline__ float side_loss(const float (&x)[4][NJ], const float* wt, const float* mean, int D, unsigned member) {
   float loss = 0.f;
   const int l = lane_id();
+#pragma unroll
   for (int i = 0; i < 4; ++i) {
     float per = 0.f;
     if ((member >> i) & 1u) {
-      float t[kJ];
+      float t[NJ];
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const float d = (l + j * kWave < D) ? x[i][j] - mean[j] : 0.f;
         t[j] = d * d;
       }
-      per = feat_sum(t, J);
+      per = feat_sum<NJ>(t);
     }
     const float term = per * wt[i];
     loss = i == 0 ? term : loss + term;
@@ -319,70 +348,78 @@ __device__ float side_loss(const float (*x)[kJ], const float* wt, const float* m
   return loss;
 }
 
-__device__ __forceinline__ void side_mean(const float (*x)[kJ], const float* wt, float* mean, float& mass, int J) {
+template <int NJ>
+__device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* wt, float* mean, float& mass) {
   mass = ((wt[0] + wt[1]) + wt[2]) + wt[3];
   const float den = fmaxf(mass, 1e-12f);
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
-    if (j < J) {
-      float acc = x[0][j] * wt[0];
-      acc = acc + x[1][j] * wt[1];
-      acc = acc + x[2][j] * wt[2];
-      acc = acc + x[3][j] * wt[3];
-      mean[j] = acc / den;
+  for (int j = 0; j < NJ; ++j) {
+    float acc = x[0][j] * wt[0];
+    acc = acc + x[1][j] * wt[1];
+    acc = acc + x[2][j] * wt[2];
+    acc = acc + x[3][j] * wt[3];
+    mean[j] = acc / den;
+  }
+}
+
+// Adds this component's normalised distortion of the cuts (2, 1, 3) to costs
+// in the Torch reference's order: left then right side, per option.
+template <int NJ>
+__device__ __forceinline__ void beta_component_cost(const float (&x)[4][NJ], const float* wr, float total, int D, float* costs) {
+  float e = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float t[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) t[j] = x[i][j] * x[i][j];
+    const float term = feat_sum<NJ>(t) * wr[i];
+    e = i == 0 ? term : e + term;
+  }
+  const float energy = fmaxf(e / total, 1e-12f);
+#pragma unroll
+  for (int opt = 0; opt < 3; ++opt) {
+    const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const unsigned member = side == 0 ? ((1u << c) - 1u) : (0xfu & ~((1u << c) - 1u));
+      float wt[4], mean[NJ], mass;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
+      side_mean<NJ>(x, wt, mean, mass);
+      costs[opt] = costs[opt] + side_loss<NJ>(x, wt, mean, D, member) / energy;
     }
   }
 }
 
-__device__ void beta_carries(const Pool& pool, const Soa& out, int n_pair, int dk, int dv) {
-  const int l = lane_id(), w = wave_id(), nw = kThreads / kWave;
-  const int Jk = (dk + kWave - 1) / kWave, Jv = (dv + kWave - 1) / kWave;
+// One wave per group of four carry inputs (litgpt/beta_log_kv.py:29-105).
+// Features l + 64 j (j < NJ) of every row live in lane l.
+template <int NJ, int KIND>
+__device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa& out, int n_pair, int dk, int dv) {
+  const int l = lane_id(), w = wave_id();
   const int n_groups = (n_pair + 3) / 4;
-  for (int gi = w; gi < n_groups; gi += nw) {
+  for (int gi = w; gi < n_groups; gi += kWaves) {
     const int start = 4 * gi;
     const int width = min(4, n_pair - start);
-    float xk[4][kJ], xv[4][kJ], wr[4];
-    Meta m[4];
+    float xk[4][NJ], xv[4][NJ], wr[4];
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool valid = i < width;
-      m[i] = valid ? pool.meta(start + i) : Meta{0.f, 0, 0, 0, 0, 0};
-      wr[i] = valid ? m[i].w : 0.f;
-      const uint16_t* kr = valid ? pool.k(start + i) : nullptr;
-      const uint16_t* vr = valid ? pool.v(start + i) : nullptr;
+      wr[i] = valid ? pool.w(start + i) : 0.f;
+      const LOGKV_G uint16_t* kr = pool.k(valid ? start + i : start);
+      const LOGKV_G uint16_t* vr = pool.v(valid ? start + i : start);
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int d = l + j * kWave;
-        xk[i][j] = (valid && j < Jk && d < dk) ? bf16_to_f32(kr[d]) : 0.f;
-        xv[i][j] = (valid && j < Jv && d < dv) ? bf16_to_f32(vr[d]) : 0.f;
+        xk[i][j] = (valid && d < dk) ? bf16_to_f32(kr[d]) : 0.f;
+        xv[i][j] = (valid && d < dv) ? bf16_to_f32(vr[d]) : 0.f;
       }
     }
     int cut = 1;
     if (width == 4) {
       const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
       float costs[3] = {0.f, 0.f, 0.f};
-      for (int comp = 0; comp < 2; ++comp) {
-        const float(*x)[kJ] = comp == 0 ? xk : xv;
-        const int J = comp == 0 ? Jk : Jv, D = comp == 0 ? dk : dv;
-        float e = 0.f;
-        for (int i = 0; i < 4; ++i) {
-          float t[kJ];
-#pragma unroll
-          for (int j = 0; j < kJ; ++j) t[j] = x[i][j] * x[i][j];
-          const float term = feat_sum(t, J) * wr[i];
-          e = i == 0 ? term : e + term;
-        }
-        const float energy = fmaxf(e / total, 1e-12f);
-        for (int opt = 0; opt < 3; ++opt) {
-          const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
-          for (int side = 0; side < 2; ++side) {
-            const unsigned member = side == 0 ? ((1u << c) - 1u) : (0xfu & ~((1u << c) - 1u));
-            float wt[4], mean[kJ], mass;
-            for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-            side_mean(x, wt, mean, mass, J);
-            costs[opt] = costs[opt] + side_loss(x, wt, mean, J, D, member) / energy;
-          }
-        }
-      }
+      beta_component_cost<NJ>(xk, wr, total, dk, costs);
+      beta_component_cost<NJ>(xv, wr, total, dv, costs);
       int best = 0;
       if (costs[1] < costs[best]) best = 1;
       if (costs[2] < costs[best]) best = 2;
@@ -393,31 +430,33 @@ __device__ void beta_carries(const Pool& pool, const Soa& out, int n_pair, int d
       unsigned member;
       if (width == 2) member = 0x3u;
       else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
-      float wt[4], mk[kJ], mv[kJ], mass;
+      float wt[4], mk[NJ], mv[NJ], mass;
+#pragma unroll
       for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-      side_mean(xk, wt, mk, mass, Jk);
-      side_mean(xv, wt, mv, mass, Jv);
+      side_mean<NJ>(xk, wt, mk, mass);
+      side_mean<NJ>(xv, wt, mv, mass);
       const int64_t o = dest + side;
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int d = l + j * kWave;
-        if (j < Jk && d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
-        if (j < Jv && d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
+        if (d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
+        if (d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
       }
       if (l == 0) {
         Meta r;
         r.w = mass;
         int64_t lo = INT64_MAX, hi = INT64_MIN, swp = 0, ord = INT64_MAX;
         uint8_t pad = 1;
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < width; ++i) {
           if (!((member >> i) & 1u)) continue;
-          if (m[i].w > 0.f) {
-            lo = imin64(lo, m[i].lo);
-            hi = imax64(hi, m[i].hi);
+          const Meta mi = pool.meta(start + i);
+          if (mi.w > 0.f) {
+            lo = imin64(lo, mi.lo);
+            hi = imax64(hi, mi.hi);
           }
-          swp += m[i].swp;
-          ord = imin64(ord, m[i].ord);
-          pad &= m[i].pad;
+          swp += mi.swp;
+          ord = imin64(ord, mi.ord);
+          pad &= mi.pad;
         }
         r.lo = mass > 0.f ? lo : 0;
         r.hi = mass > 0.f ? hi : 0;
@@ -430,14 +469,15 @@ __device__ void beta_carries(const Pool& pool, const Soa& out, int n_pair, int d
   }
 }
 
-// ---- top-level fold --------------------------------------------------------
-// Slot 0 <- left fold of pool[0..mr] (rounded to bf16 after each merge),
-// slots 1..B-1 <- pool[mr+1 .. mr+B-1].
-__device__ void fold_top(const Ladder& L, int64_t level_base, const Src& src, int take, int mr) {
-  const int B = L.B;
-  const int ku = L.dk / 4, units = (L.dk + L.dv) / 4;
-  Pool pool{&L, level_base, &src, take};
+// Saturated top level: slot 0 <- left fold of P[0..mr] (bf16 after every
+// merge), slots 1..B'-1 <- P[mr+1..]. Rare (a whole ladder must be full), so
+// it stays out of line with one wave doing the sequential fold.
+template <int KIND>
+__device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
+  const Ladder& L = pool.L;
   constexpr int kMaxUnitsPerLane = (2 * kMaxDim / 4) / kWave;
+  const int B = L.B, ku = L.dk / 4, units = (L.dk + L.dv) / 4;
+  const int64_t base = pool.base;
   uint2 acc[kMaxUnitsPerLane];
   Meta am{};
   if (wave_id() == 0) {
@@ -451,7 +491,7 @@ __device__ void fold_top(const Ladder& L, int64_t level_base, const Src& src, in
     for (int t = 1; t <= mr; ++t) {
       const Meta b = pool.meta(t);
       const float alpha = am.w / fmaxf(am.w + b.w, 1e-8f);
-      const uint16_t *bk = pool.k(t), *bv = pool.v(t);
+      const LOGKV_G uint16_t *bk = pool.k(t), *bv = pool.v(t);
 #pragma unroll
       for (int q = 0; q < kMaxUnitsPerLane; ++q) {
         const int u = l + q * kWave;
@@ -460,75 +500,74 @@ __device__ void fold_top(const Ladder& L, int64_t level_base, const Src& src, in
       am = merge_meta(am, b);
     }
   }
-  __syncthreads();
-  // Stored part of the tail shifts down by mr; staged part follows.
-  const int stored_from = mr + 1;
-  const int n_stored = stored_from < B ? B - stored_from : 0;
-  shift_slots_down(L, level_base, stored_from, 1, n_stored);
-  __syncthreads();
-  const int first_staged = stored_from > B ? stored_from : B;   // pool index
-  const int n_staged = (mr + B - 1) - first_staged + 1;
-  if (n_staged > 0) copy_src_to_slots(L, level_base, src, take + first_staged - B, first_staged - mr, n_staged);
+  move_rows(pool, mr + 1, 1, B - 1);
   if (wave_id() == 0) {
     const int l = lane_id();
 #pragma unroll
     for (int q = 0; q < kMaxUnitsPerLane; ++q) {
       const int u = l + q * kWave;
-      if (u < units) store_unit(L.k + level_base * L.dk, L.v + level_base * L.dv, u, ku, acc[q]);
+      if (u < units) store_unit(L.k + base * L.dk, L.v + base * L.dv, u, ku, acc[q]);
     }
-    if (l == 0) put_slot_meta(L, level_base, am);
+    if (l == 0) put_slot_meta(L, base, am);
   }
-  __syncthreads();
 }
 
-// Fenwick append of m0 staged rows from `src0` into one ladder.
-__device__ void fenwick_append(const Ladder& L, int16_t* counts_s, int levels, Src src0, int m0, Soa bufA, Soa bufB,
-                               bool beta) {
+// One level of a Fenwick append. With the virtual pool P = [stored 0..cnt |
+// staged 0..m] of n_pool = cnt + m rows:
+//  * n_pool <= B': the staged rows fill slots [cnt, n_pool);
+//  * otherwise, below the top: the oldest n_pair = 2*ceil((n_pool-B')/2) rows
+//    pair into carries, P[n_pair..) moves to slots [0, n_surv), the rest clears;
+//  * at the top: slot 0 = left fold of P[0..mr] (bf16 after every merge) and
+//    slots 1..B'-1 = P[mr+1..n_pool), mr = n_pool - B'.
+// Returns the number of carries written to `out` (0 ends the append).
+template <int KIND>
+__device__ __forceinline__ int level_step(const Ladder& L, int16_t* counts_s, int ell, bool top, const Src& cur, int m,
+                                          const Soa& out, bool beta) {
+  // Barriers: move_rows' load/store barrier is the only one a level needs. It
+  // orders this level's carry stores before the next level reads them, and
+  // every read of this level's staged source before the next level overwrites
+  // that buffer with its own carries. counts_s[ell] is written by thread 0 and
+  // read again only after the final barrier of the append.
   const int B = L.B;
-  Src cur = src0;
-  int m = m0;
-  for (int ell = 0; ell < levels && m > 0; ++ell) {
-    const int64_t level_base = static_cast<int64_t>(ell) * B;
-    const bool top = ell == levels - 1;
-    const int cnt = counts_s[ell];
-    const int take = min(B - cnt, m);
-    if (take > 0) copy_src_to_slots(L, level_base, cur, 0, cnt, take);
-    __syncthreads();
-    const int mr = m - take;
-    if (mr == 0) {
-      if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(cnt + take);
-      __syncthreads();
-      break;
-    }
-    if (top) {
-      fold_top(L, level_base, cur, take, mr);
-      if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(B);
-      __syncthreads();
-      break;
-    }
-    const int n_carry = (mr + 1) / 2, n_pair = 2 * n_carry;
-    const Soa out = (ell & 1) ? bufB : bufA;
-    Pool pool{&L, level_base, &cur, take};
-    if (beta) beta_carries(pool, out, n_pair, L.dk, L.dv);
-    else pair_carries(pool, out, n_carry, L.dk, L.dv);
-    __syncthreads();
-    const int n_surv = B + mr - n_pair;
-    if (n_pair < B) {
-      shift_slots_down(L, level_base, n_pair, 0, B - n_pair);
-      __syncthreads();
-      copy_src_to_slots(L, level_base, cur, take, B - n_pair, mr);
-    } else {
-      copy_src_to_slots(L, level_base, cur, take + n_pair - B, 0, n_surv);
-    }
-    clear_slots(L, level_base + n_surv, B - n_surv);
-    __syncthreads();
-    if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(n_surv);
-    __syncthreads();
-    Src next{};
-    next.kind = 1;
-    next.buf = out;
-    cur = next;
-    m = n_carry;
+  const int64_t base = static_cast<int64_t>(ell) * B;
+  const int cnt = counts_s[ell];
+  const int n_pool = cnt + m;
+  const PoolT<KIND> pool{L, base, cnt, cur};
+  if (n_pool <= B) {
+    copy_staged<KIND>(L, base, cur, 0, cnt, m);
+    if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(n_pool);
+    return 0;
+  }
+  const int mr = n_pool - B;
+  if (top) {
+    fold_top<KIND>(pool, mr);
+    if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(B);
+    return 0;
+  }
+  const int n_carry = (mr + 1) / 2, n_pair = 2 * n_carry;
+  const int n_surv = n_pool - n_pair;   // >= B' - 1 >= 1, so move_rows always runs its barrier
+  if (beta) {
+    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv);
+    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv);
+  } else {
+    pair_carries<KIND>(pool, out, n_carry, L.dk, L.dv);
+  }
+  move_rows<KIND>(pool, n_pair, 0, n_surv);
+  clear_slots(L, base + n_surv, B - n_surv);
+  if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(n_surv);
+  return n_carry;
+}
+
+// Fenwick append of m0 staged rows from `src0` into one ladder, level by level.
+__device__ __forceinline__ void fenwick_append(const Ladder& L, int16_t* counts_s, int levels, Src src0, int m0, Soa bufA, Soa bufB,
+                               bool beta) {
+  int m = src0.kind == 1 ? level_step<1>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta)
+                         : level_step<0>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta);
+  Src cur{};
+  cur.kind = 1;
+  for (int ell = 1; ell < levels && m > 0; ++ell) {
+    cur.buf = (ell & 1) ? bufA : bufB;   // carries written by the previous level
+    m = level_step<1>(L, counts_s, ell, ell == levels - 1, cur, m, (ell & 1) ? bufB : bufA, beta);
   }
 }
 
@@ -552,6 +591,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   extern __shared__ __align__(16) uint8_t dyn[];
   __shared__ int wave_sum[kThreads / kWave];
   __shared__ int16_t counts_s[64];
+  __shared__ int level_start_s[64];
   __shared__ int m_s;
   const int K = c.k_max, L = c.levels, B = c.slots, dk = c.dk, dv = c.dv;
   const int ladder = blockIdx.x;
@@ -559,8 +599,10 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   const int n = valid_rows(r, b);
   uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
-  const int8_t* as = ws.assign + static_cast<int64_t>(lane_ix) * r.tokens;
-  const int32_t* ord = ws.order + static_cast<int64_t>(b) * r.tokens;
+  const int c_stage_off = (2 * r.tokens + 15) & ~15;
+  const int keys_off = c_stage_off + kCenterRows * dk * 2;
+  const LOGKV_G int8_t* as = gp(ws.assign + static_cast<int64_t>(lane_ix) * r.tokens);
+  const LOGKV_G int32_t* ord = gp(ws.order + static_cast<int64_t>(b) * r.tokens);
 
   // 1. This cluster's rows in position order (stable compaction).
   if (threadIdx.x == 0) m_s = 0;
@@ -589,12 +631,14 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
 
   const int64_t cl = static_cast<int64_t>(lane_ix) * K + cc;
   const int64_t row0 = cl * L * B;
-  Ladder lad{c.level_k + row0 * dk, c.level_v + row0 * dv, c.level_w + row0, c.level_p_lo + row0,
-             c.level_p_hi + row0, c.level_sum_wp + row0, c.level_order + row0, c.pad_mask + row0, dk, dv, B};
-  const uint16_t* kb = r.k + b * r.k_sb + g * r.k_sg;
-  const uint16_t* vb = r.v + b * r.v_sb + g * r.v_sg;
-  const int64_t* posb = r.pos + b * r.pos_sb;
-  float* mu = c.centroid + cl * dk;
+  Ladder lad{gp(c.level_k + row0 * dk), gp(c.level_v + row0 * dv), gp(c.level_w + row0), gp(c.level_p_lo + row0),
+             gp(c.level_p_hi + row0), gp(c.level_sum_wp + row0), gp(c.level_order + row0), gp(c.pad_mask + row0),
+             dk, dv, B};
+  const LOGKV_G uint16_t* kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  const LOGKV_G uint16_t* vb = gp(r.v + b * r.v_sb + g * r.v_sg);
+  const LOGKV_G int64_t* posb = gp(r.pos + b * r.pos_sb);
+  LOGKV_G float* mu = gp(c.centroid + cl * dk);
+  const LOGKV_S uint16_t* tok_s = (const LOGKV_S uint16_t*)tok;
   uint8_t* scratch = ws.ladder + ladder * ws.ladder_stride;
   const Soa S0 = soa_at(scratch, ws.s0_rows, dk, dv);
   scratch += soa_bytes(ws.s0_rows, dk, dv);
@@ -602,55 +646,94 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   scratch += soa_bytes(ws.carry_a_rows, dk, dv);
   const Soa bufB = soa_at(scratch, ws.carry_b_rows, dk, dv);
 
+  const bool was_alive = ws.snap_alive[cl] != 0;
+  const int first = was_alive ? 0 : 1;   // a dead cluster opens with its earliest row
+  const int nn = m - first;
+
+  if (blockIdx.y == 1) {
+    // Center role: mu <- (pre*mu + sum k) / (pre + n), pre = n_eff, the new
+    // rows' keys summed in position order (litgpt/log_kv_cache.py:4344-4359);
+    // a new cluster starts from its first row's key with n_eff = 1
+    // (litgpt/log_kv_cache.py:2276-2278). Key rows are staged in LDS by all
+    // threads; one thread per feature adds them in order.
+    float n_eff = was_alive ? c.n_eff[cl] : 1.0f;
+    const int d = threadIdx.x;
+    float mu_d = 0.f;
+    if (d < dk) mu_d = was_alive ? mu[d] : bf16_to_f32(kb[static_cast<int64_t>(tok[0]) * r.k_st + d]);
+    if (nn > 0) {
+      uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + c_stage_off);
+      const int ku = dk / 4;
+      float acc = 0.f;
+      for (int c0 = first; c0 < m; c0 += kCenterRows) {
+        const int rows = min(kCenterRows, m - c0);
+        for (int i = threadIdx.x; i < rows * ku; i += kThreads) {
+          const int rr = i / ku, u = i - rr * ku;
+          *reinterpret_cast<uint2*>(stage + rr * dk + 4 * u) =
+              *(const LOGKV_G uint2*)(kb + static_cast<int64_t>(tok[c0 + rr]) * r.k_st + 4 * u);
+        }
+        __syncthreads();
+        if (d < dk) {
+          int rr = 0;
+          if (c0 == first) {
+            acc = bf16_to_f32(stage[d]);
+            rr = 1;
+          }
+          for (; rr + 8 <= rows; rr += 8) {
+            float x[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = bf16_to_f32(stage[(rr + q) * dk + d]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc = acc + x[q];
+          }
+          for (; rr < rows; ++rr) acc = acc + bf16_to_f32(stage[rr * dk + d]);
+        }
+        __syncthreads();
+      }
+      const float pre = n_eff;
+      const float den = pre + static_cast<float>(nn);
+      if (d < dk) mu_d = pre > 0.f ? (pre * mu_d + acc) / den : acc / static_cast<float>(nn);
+      n_eff = den;
+    }
+    if (d < dk) mu[d] = mu_d;
+    if (threadIdx.x == 0) c.n_eff[cl] = n_eff;
+    return;
+  }
+
+  // Ladder role.
   for (int e = threadIdx.x; e < L; e += kThreads) counts_s[e] = c.level_count[cl * L + e];
-  bool alive = c.alive[cl] != 0;
-  float n_eff = c.n_eff[cl];
   int32_t n_total = c.n_total[cl];
   int64_t p_hi = c.p_hi_c[cl];
   int32_t phase = c.level0_phase[cl];
   __syncthreads();
 
-  int first = 0;
-  if (!alive) {
-    // 2. A dead cluster opens with its earliest row (clears every slot first).
+  if (!was_alive) {
+    // 2. A dead cluster: clear every slot, its earliest row takes level 0 slot 0.
     clear_slots(lad, 0, static_cast<int64_t>(L) * B);
     for (int e = threadIdx.x; e < L; e += kThreads) counts_s[e] = 0;
     const int t0 = tok[0];
-    for (int d = threadIdx.x; d < dk; d += kThreads) mu[d] = bf16_to_f32(kb[static_cast<int64_t>(t0) * r.k_st + d]);
-    __syncthreads();
     Src one{};
     one.kind = 0;
-    one.tok = tok;
+    one.tok = tok_s;
     one.order_base = 0;
     one.kb = kb;
     one.vb = vb;
     one.k_st = r.k_st;
     one.v_st = r.v_st;
     one.posb = posb;
-    fenwick_append(lad, counts_s, L, one, 1, bufA, bufB, prm.beta_merge != 0);
-    alive = true;
-    n_eff = 1.0f;
+    __syncthreads();
+    copy_staged<0>(lad, 0, one, 0, 0, 1);
+    if (threadIdx.x == 0) counts_s[0] = 1;
+    __syncthreads();
     n_total = 1;
     p_hi = posb[t0];
     phase = 1;
-    first = 1;
   }
-  const int nn = m - first;
   if (nn > 0) {
     const int64_t first_pos = posb[tok[first]];
     const bool late = prm.late_joins && first_pos < p_hi;
-    // 3. Center update over the new rows, summed in position order
-    //    (mu = (pre*mu + sum)/(pre + n), pre = n_eff).
-    int64_t last_pos = posb[tok[m - 1]];
-    for (int d = threadIdx.x; d < dk; d += kThreads) {
-      float acc = bf16_to_f32(kb[static_cast<int64_t>(tok[first]) * r.k_st + d]);
-      for (int i = first + 1; i < m; ++i) acc = acc + bf16_to_f32(kb[static_cast<int64_t>(tok[i]) * r.k_st + d]);
-      const float pre = n_eff;
-      const float den = pre + static_cast<float>(nn);
-      mu[d] = pre > 0.f ? (pre * mu[d] + acc) / den : acc / static_cast<float>(nn);
-    }
+    const int64_t last_pos = posb[tok[m - 1]];
     Src src{};
-    src.tok = tok + first;
+    src.tok = tok_s + first;
     src.kb = kb;
     src.vb = vb;
     src.k_st = r.k_st;
@@ -664,35 +747,36 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       p_hi = last_pos;
     } else {
       // 4. Delayed archive: existing entries (level by level, slots in order)
-      //    and the new rows, stably sorted by p_lo, re-appended from level 0.
+      //    and the new rows, stably sorted by p_lo (key = p_lo << 13 | index),
+      //    gathered into S0 in that order with order = rank, re-appended from
+      //    level 0 of the cleared ladder.
       int n_exist = 0;
+      int* level_start = level_start_s;
       for (int e = 0; e < L; ++e) n_exist += counts_s[e];
-      uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + ((2 * r.tokens + 15) & ~15));
-      uint16_t* perm = reinterpret_cast<uint16_t*>(keys + ws.sort_width);
-      int base = 0;
-      for (int e = 0; e < L; ++e) {
-        const int ce = counts_s[e];
-        const int ku = dk / 4, units = (dk + dv) / 4;
-        for (int i = threadIdx.x; i < ce * units; i += kThreads) {
-          const int rr = i / units, u = i % units;
-          const int64_t slot = static_cast<int64_t>(e) * B + rr;
-          store_unit(S0.k + static_cast<int64_t>(base + rr) * dk, S0.v + static_cast<int64_t>(base + rr) * dv, u, ku,
-                     load_unit(lad.k + slot * dk, lad.v + slot * dv, u, ku));
+      if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int e = 0; e < L; ++e) {
+          level_start[e] = acc;
+          acc += counts_s[e];
         }
-        for (int rr = threadIdx.x; rr < ce; rr += kThreads) {
-          const Meta mt = slot_meta(lad, static_cast<int64_t>(e) * B + rr);
-          put_soa_meta(S0, base + rr, mt);
-          keys[base + rr] = (static_cast<uint64_t>(mt.lo) << kOrderIndexBits) | static_cast<uint64_t>(base + rr);
-        }
-        base += ce;
       }
+      __syncthreads();
+      uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + keys_off);
       const int total = n_exist + nn;
-      for (int i = threadIdx.x; i < nn; i += kThreads)
-        keys[n_exist + i] = (static_cast<uint64_t>(posb[tok[first + i]]) << kOrderIndexBits) |
-                            static_cast<uint64_t>(n_exist + i);
       int width = 1;
       while (width < total) width <<= 1;
-      for (int i = total + threadIdx.x; i < width; i += kThreads) keys[i] = ~0ull;
+      for (int i = threadIdx.x; i < width; i += kThreads) {
+        uint64_t key = ~0ull;
+        if (i < n_exist) {
+          int e = 0;
+          while (e + 1 < L && level_start[e + 1] <= i) ++e;
+          const int64_t slot = static_cast<int64_t>(e) * B + (i - level_start[e]);
+          key = (static_cast<uint64_t>(lad.lo[slot]) << kOrderIndexBits) | static_cast<uint64_t>(i);
+        } else if (i < total) {
+          key = (static_cast<uint64_t>(posb[tok[first + i - n_exist]]) << kOrderIndexBits) | static_cast<uint64_t>(i);
+        }
+        keys[i] = key;
+      }
       __syncthreads();
       for (int size = 2; size <= width; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -710,7 +794,40 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
           __syncthreads();
         }
       }
-      for (int i = threadIdx.x; i < total; i += kThreads) perm[i] = static_cast<uint16_t>(keys[i] & kOrderIndexMask);
+      // Gather row rank -> S0[rank].
+      const int ku = dk / 4, units = (dk + dv) / 4;
+      for (int i = threadIdx.x; i < total * units; i += kThreads) {
+        const int rank = i / units, u = i - (i / units) * units;
+        const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
+        const LOGKV_G uint16_t *ks, *vs;
+        if (q < n_exist) {
+          int e = 0;
+          while (e + 1 < L && level_start[e + 1] <= q) ++e;
+          const int64_t slot = static_cast<int64_t>(e) * B + (q - level_start[e]);
+          ks = lad.k + slot * dk;
+          vs = lad.v + slot * dv;
+        } else {
+          const int t = tok[first + q - n_exist];
+          ks = kb + static_cast<int64_t>(t) * r.k_st;
+          vs = vb + static_cast<int64_t>(t) * r.v_st;
+        }
+        store_unit(S0.k + static_cast<int64_t>(rank) * dk, S0.v + static_cast<int64_t>(rank) * dv, u, ku,
+                   load_unit(ks, vs, u, ku));
+      }
+      for (int rank = threadIdx.x; rank < total; rank += kThreads) {
+        const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
+        Meta mt;
+        if (q < n_exist) {
+          int e = 0;
+          while (e + 1 < L && level_start[e + 1] <= q) ++e;
+          mt = slot_meta(lad, static_cast<int64_t>(e) * B + (q - level_start[e]));
+        } else {
+          const int64_t p = posb[tok[first + q - n_exist]];
+          mt = Meta{1.0f, p, p, p, 0, 0};
+        }
+        mt.ord = rank;
+        put_soa_meta(S0, rank, mt);
+      }
       int64_t hi = p_hi;
       for (int i = first; i < m; ++i) hi = imax64(hi, posb[tok[i]]);
       p_hi = hi;
@@ -719,13 +836,10 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       clear_slots(lad, 0, static_cast<int64_t>(L) * B);
       for (int e = threadIdx.x; e < L; e += kThreads) counts_s[e] = 0;
       __syncthreads();
-      src.kind = 2;
+      src.kind = 1;
       src.buf = S0;
-      src.perm = perm;
-      src.n_exist = n_exist;
       m0 = total;
     }
-    n_eff = n_eff + static_cast<float>(nn);
     n_total += nn;
     __syncthreads();
     fenwick_append(lad, counts_s, L, src, m0, bufA, bufB, prm.beta_merge != 0);
@@ -734,7 +848,6 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   for (int e = threadIdx.x; e < L; e += kThreads) c.level_count[cl * L + e] = counts_s[e];
   if (threadIdx.x == 0) {
     c.alive[cl] = 1;
-    c.n_eff[cl] = n_eff;
     c.n_total[cl] = n_total;
     c.p_hi_c[cl] = p_hi;
     c.level0_phase[cl] = phase;
@@ -744,13 +857,14 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
-  size_t shmem = ((2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15));
-  if (p.late_joins) shmem += static_cast<size_t>(ws.sort_width) * 8 + static_cast<size_t>(ws.sort_width) * 2;
+  size_t shmem = ((2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15)) + static_cast<size_t>(kCenterRows) * c.dk * 2;
+  if (p.late_joins) shmem += static_cast<size_t>(ws.sort_width) * 8;
   if (shmem > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(&commit_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           static_cast<int>(shmem)) != hipSuccess)
     return LOGKV_ERUNTIME;
-  hipLaunchKernelGGL(commit_kernel, dim3(ladders), dim3(kThreads), shmem, stream, c, r, p, ws);
+  // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
+  hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

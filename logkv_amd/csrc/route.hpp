@@ -29,6 +29,7 @@ struct Workspace {
   int8_t* assign;      // [lanes, T]
   float* s_win;        // [lanes, T]
   float* dist;         // [lanes, T]
+  uint8_t* snap_alive; // [lanes, K] alive flags at the start of the flush
   uint8_t* ladder;     // per-ladder carry / staging rows
   int64_t ladder_stride;  // bytes per ladder
   int64_t s0_rows, carry_a_rows, carry_b_rows;
