@@ -100,6 +100,71 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
                       const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
                       const int8_t* assign, const int32_t* order, void* stream);
 
+/* Candidate span table over the virtual rows [old exact pool (old_width rows) |
+ * flush]: pool_* / flush_* are [n_batch, G, rows, d] bf16 with element strides;
+ * span i covers tokens[span_offsets[i] .. span_offsets[i+1]) of batch row
+ * span_rows[i]. With beta_novelty, centroids [n_batch, G, k_max, dk] f32 and
+ * centroid_valid [n_batch, G, k_max] are the centers before the flush. */
+typedef struct logkv_span_args {
+  const uint16_t* pool_k;
+  int64_t pk_sb, pk_sg, pk_st;
+  const uint16_t* pool_v;
+  int64_t pv_sb, pv_sg, pv_st;
+  const uint16_t* flush_k;
+  int64_t fk_sb, fk_sg, fk_st;
+  const uint16_t* flush_v;
+  int64_t fv_sb, fv_sg, fv_st;
+  int32_t old_width;
+  const int32_t* tokens;
+  const int32_t* span_offsets;
+  const int32_t* span_rows;
+  int32_t n_spans;
+  int32_t n_groups, dk, dv;
+  const float* centroids;
+  const uint8_t* centroid_valid;
+  int32_t k_max;
+  int32_t beta_novelty;
+} logkv_span_args;
+
+/* Score of every candidate span (f32 [n_spans]): Alpha's normalised K/V
+ * variance, or with beta_novelty the top-2 group mean of variance + novelty.
+ * Replaces score_spans (litgpt/alpha_log_kv.py:125-174). */
+int logkv_score_spans(const logkv_span_args* args, float* scores, void* stream);
+
+/* Exact-pool rewrite and archive gather over the same virtual rows: keep
+ * [n_batch, P] and archive [n_batch, A] list source rows (-1 = zero row).
+ * Outputs are contiguous: out_pool_k/v [n_batch, G, P, d], out_pool_pos /
+ * out_pool_valid [n_batch, P], arch_k/v [n_batch, G, A, d], arch_pos
+ * [n_batch, A]. The outputs must not alias the pool sources.
+ * Replaces alpha_partition (litgpt/log_kv_updates_triton.py:285-328). */
+typedef struct logkv_partition_args {
+  const uint16_t* pool_k;
+  int64_t pk_sb, pk_sg, pk_st;
+  const uint16_t* pool_v;
+  int64_t pv_sb, pv_sg, pv_st;
+  const int64_t* pool_pos;
+  int64_t pp_sb;
+  const uint16_t* flush_k;
+  int64_t fk_sb, fk_sg, fk_st;
+  const uint16_t* flush_v;
+  int64_t fv_sb, fv_sg, fv_st;
+  const int64_t* flush_pos;
+  int64_t fp_sb;
+  int32_t old_width;
+  const int32_t* keep;
+  const int32_t* archive;
+  int32_t P, A, n_batch, n_groups, dk, dv;
+  uint16_t* out_pool_k;
+  uint16_t* out_pool_v;
+  int64_t* out_pool_pos;
+  uint8_t* out_pool_valid;
+  uint16_t* arch_k;
+  uint16_t* arch_v;
+  int64_t* arch_pos;
+} logkv_partition_args;
+
+int logkv_alpha_partition(const logkv_partition_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,33 @@ class RouteParams(C.Structure):
                 ("late_joins", _i32), ("beta_merge", _i32)]
 
 
+class SpanArgs(C.Structure):
+    _fields_ = [
+        ("pool_k", _p), ("pk_sb", _i64), ("pk_sg", _i64), ("pk_st", _i64),
+        ("pool_v", _p), ("pv_sb", _i64), ("pv_sg", _i64), ("pv_st", _i64),
+        ("flush_k", _p), ("fk_sb", _i64), ("fk_sg", _i64), ("fk_st", _i64),
+        ("flush_v", _p), ("fv_sb", _i64), ("fv_sg", _i64), ("fv_st", _i64),
+        ("old_width", _i32), ("tokens", _p), ("span_offsets", _p), ("span_rows", _p), ("n_spans", _i32),
+        ("n_groups", _i32), ("dk", _i32), ("dv", _i32),
+        ("centroids", _p), ("centroid_valid", _p), ("k_max", _i32), ("beta_novelty", _i32),
+    ]
+
+
+class PartitionArgs(C.Structure):
+    _fields_ = [
+        ("pool_k", _p), ("pk_sb", _i64), ("pk_sg", _i64), ("pk_st", _i64),
+        ("pool_v", _p), ("pv_sb", _i64), ("pv_sg", _i64), ("pv_st", _i64),
+        ("pool_pos", _p), ("pp_sb", _i64),
+        ("flush_k", _p), ("fk_sb", _i64), ("fk_sg", _i64), ("fk_st", _i64),
+        ("flush_v", _p), ("fv_sb", _i64), ("fv_sg", _i64), ("fv_st", _i64),
+        ("flush_pos", _p), ("fp_sb", _i64),
+        ("old_width", _i32), ("keep", _p), ("archive", _p),
+        ("P", _i32), ("A", _i32), ("n_batch", _i32), ("n_groups", _i32), ("dk", _i32), ("dv", _i32),
+        ("out_pool_k", _p), ("out_pool_v", _p), ("out_pool_pos", _p), ("out_pool_valid", _p),
+        ("arch_k", _p), ("arch_v", _p), ("arch_pos", _p),
+    ]
+
+
 # Exported symbol -> (restype, argtypes); the tests check this table against the header.
 SIGNATURES = {
     "logkv_last_error": (C.c_char_p, []),
@@ -55,6 +82,8 @@ SIGNATURES = {
                                   _p, _i64, _p, _p, _p]),
     "logkv_commit_only": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
                                  _p, _i64, _p, _p, _p]),
+    "logkv_score_spans": (_i32, [C.POINTER(SpanArgs), _p, _p]),
+    "logkv_alpha_partition": (_i32, [C.POINTER(PartitionArgs), _p]),
 }
 
 

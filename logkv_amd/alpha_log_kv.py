@@ -1,0 +1,313 @@
+"""Alpha exact spans: whole-span candidates, device scoring, bounded greedy choice.
+
+Call surface of the reference module (litgpt/alpha_log_kv.py): ``SpanSelection``,
+``SpanCut``, ``cut_spans``, ``score_spans``, ``choose_spans``, ``select_spans``.
+Span cutting and the greedy choice are host logic over host position /
+boundary lists, as in the reference; scoring runs in the HIP library
+(``logkv_score_spans``) and the exact-pool / archive split in
+``logkv_alpha_partition``.
+
+Indices refer to the virtual row sequence ``[old exact pool (old_width rows) |
+current flush]`` shared by the KV groups of a batch row.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+@dataclass
+class SpanSelection:
+    keep: list[list[int]]
+    archive: list[list[int]]
+    spans: list[list[tuple[int, bool]]]
+    positions: list[list[int]]
+
+
+@dataclass
+class SpanCut:
+    """Candidate whole spans of one flush; host data only.
+
+    ``candidates[b]`` = (list of (token ranges, old, closed), positions of the
+    row's ``[pool | flush]`` rows); ``token_rows[b]`` flat token indices in span
+    order; ``length_rows[b]`` span lengths.
+    """
+    candidates: list
+    token_rows: list
+    length_rows: list
+
+
+_EMPTY = np.empty(0, dtype=np.int64)
+
+
+def _ranges(spans) -> np.ndarray:
+    """Concatenated half-open ``[start, stop)`` ranges as one int64 array."""
+    if not spans:
+        return _EMPTY
+    b = np.asarray(spans, dtype=np.int64).reshape(-1, 2)
+    n = np.maximum(b[:, 1] - b[:, 0], 0)
+    total = int(n.sum())
+    if not total:
+        return _EMPTY
+    return np.repeat(b[:, 0] - (np.cumsum(n) - n), n) + np.arange(total, dtype=np.int64)
+
+
+def _new_runs(new_pos, ends, pending, pending_pos, max_span):
+    """Runs of new tokens: (pending_closed, starts, stops, closed) (litgpt/alpha_log_kv.py:16-53).
+
+    A run closes after a boundary token or when it reaches ``max_span`` tokens
+    (an unfinished old span counts toward the first run), and is closed by a
+    position jump before the next token. A jump right after the old unfinished
+    span closes that span instead.
+    """
+    pos = np.asarray(new_pos, dtype=np.int64)
+    end = np.asarray(ends, dtype=bool)
+    n = len(pos)
+    if n == 0:
+        return False, _EMPTY, _EMPTY, np.empty(0, dtype=bool)
+    pending_closed = bool(pending) and int(pos[0]) != pending_pos + 1
+    carry = 0 if pending_closed else int(pending)
+    jump_before = np.zeros(n, dtype=bool)
+    jump_before[1:] = pos[1:] != pos[:-1] + 1
+    # Hard segments start at the first token, after a boundary and at a jump.
+    seg_start = np.ones(n, dtype=bool)
+    seg_start[1:] = jump_before[1:] | end[:-1]
+    seg = np.cumsum(seg_start) - 1
+    starts_of_seg = np.flatnonzero(seg_start)
+    depth = np.arange(n) - starts_of_seg[seg] + 1 + np.where(seg == 0, carry, 0)
+    at_cap = depth % max_span == 0
+    if carry >= max_span:
+        at_cap &= seg != 0      # an over-long carried span only closes at a boundary or jump
+    close = end | at_cap
+    last = close.copy()
+    last[:-1] |= jump_before[1:]
+    last[-1] = True
+    stops = np.flatnonzero(last) + 1
+    starts = np.concatenate(([0], stops[:-1]))
+    closed = close[stops - 1].copy()
+    closed[:-1] |= jump_before[stops[:-1]]
+    return pending_closed, starts.astype(np.int64), stops.astype(np.int64), closed
+
+
+def cut_spans(old_spans, old_positions, new_positions, ends, old_width, max_span):
+    """Whole candidate spans per row (host only); None when no row has one
+    (litgpt/alpha_log_kv.py:84-122)."""
+    candidates, token_rows, length_rows = [], [], []
+    for spans, old_pos, new_pos, boundaries in zip(old_spans, old_positions, new_positions, ends):
+        row, offset, pending = [], 0, None
+        for length, closed in spans:
+            if closed:
+                row.append(([(offset, offset + length)], True, True))
+            else:
+                pending = (offset, offset + length)
+            offset += length
+        all_pos = np.zeros(old_width + len(new_pos), dtype=np.int64)
+        all_pos[:len(old_pos)] = old_pos
+        all_pos[old_width:] = new_pos
+        pending_len = 0 if pending is None else pending[1] - pending[0]
+        pending_pos = int(all_pos[pending[1] - 1]) if pending_len else 0
+        pending_closed, starts, stops, closed = _new_runs(new_pos, boundaries, pending_len, pending_pos, max_span)
+        if pending_closed:
+            row.append(([pending], False, True))
+        for i, (a, z, done) in enumerate(zip((starts + old_width).tolist(), (stops + old_width).tolist(),
+                                              closed.tolist())):
+            ranges = [(a, z)]
+            if i == 0 and pending_len and not pending_closed:
+                ranges.insert(0, pending)
+            row.append((ranges, False, done))
+        if pending_len and not pending_closed and not len(starts):
+            row.append(([pending], False, False))
+        token_rows.append(_ranges([r for rs, _, _ in row for r in rs]))
+        length_rows.append([sum(z - a for a, z in rs) for rs, _, _ in row])
+        candidates.append((row, all_pos))
+    if not any(length_rows):
+        return None
+    return SpanCut(candidates, token_rows, length_rows)
+
+
+def _span_tables(cut: SpanCut, device):
+    """Device tables of the candidates: tokens int32, span offsets int32, span row int32."""
+    tokens = np.concatenate(cut.token_rows).astype(np.int32)
+    lengths = np.concatenate([np.asarray(x, dtype=np.int64) for x in cut.length_rows])
+    offsets = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    rows = np.repeat(np.arange(len(cut.length_rows)), [len(x) for x in cut.length_rows]).astype(np.int32)
+    packed = np.concatenate((tokens, offsets, rows)).astype(np.int32)
+    dev = torch.from_numpy(packed).pin_memory().to(device, non_blocking=True) if device.type == "cuda" else \
+        torch.from_numpy(packed).to(device)
+    n_tok, n_span = len(tokens), len(lengths)
+    return dev, dev[:n_tok], dev[n_tok:n_tok + n_span + 1], dev[n_tok + n_span + 1:], n_span
+
+
+def score_spans_split(pool_k, pool_v, flush_k, flush_v, old_width, cut: SpanCut, *, beta_novelty=False,
+                      centroids=None, centroid_valid=None):
+    """Scores of the candidates over ``[pool[:, :, :old_width] | flush]`` without materialising the cat."""
+    if beta_novelty and (centroids is None or centroid_valid is None):
+        raise ValueError("Beta span scoring requires centroids and centroid_valid from before the flush")
+    dev = flush_k.device
+    _lib.require_device(flush_k, "span scoring keys")
+    keep, tokens, offsets, rows, n_span = _span_tables(cut, dev)
+    out = torch.empty(n_span, dtype=torch.float32, device=dev)
+    if pool_k is None:
+        pool_k, pool_v = flush_k, flush_v
+    args = _lib.SpanArgs(
+        _lib.ptr(pool_k), pool_k.stride(0), pool_k.stride(1), pool_k.stride(2),
+        _lib.ptr(pool_v), pool_v.stride(0), pool_v.stride(1), pool_v.stride(2),
+        _lib.ptr(flush_k), flush_k.stride(0), flush_k.stride(1), flush_k.stride(2),
+        _lib.ptr(flush_v), flush_v.stride(0), flush_v.stride(1), flush_v.stride(2),
+        int(old_width), _lib.ptr(tokens), _lib.ptr(offsets), _lib.ptr(rows), n_span,
+        flush_k.size(1), flush_k.size(-1), flush_v.size(-1),
+        _lib.ptr(centroids) if beta_novelty else None, _lib.ptr(centroid_valid) if beta_novelty else None,
+        centroids.size(2) if beta_novelty else 0, 1 if beta_novelty else 0)
+    rc = _lib.lib().logkv_score_spans(C.byref(args), _lib.ptr(out), _lib.stream_of(dev))
+    _lib.check(rc, "logkv_score_spans")
+    out._logkv_keepalive = (keep, pool_k, pool_v, flush_k, flush_v, centroids, centroid_valid)
+    return out
+
+
+def score_spans(k, v, cut, *, beta_novelty=False, centroids=None, centroid_valid=None):
+    """Device tensor of span scores in candidate order (litgpt/alpha_log_kv.py:125-174)."""
+    for t in (k, v):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError("span scoring needs bf16 K/V with a contiguous last axis")
+    if beta_novelty:
+        centroids = centroids.float().contiguous()
+        centroid_valid = centroid_valid.contiguous()
+    return score_spans_split(None, None, k, v, 0, cut, beta_novelty=beta_novelty, centroids=centroids,
+                             centroid_valid=centroid_valid)
+
+
+def choose_spans(cut: SpanCut, host_scores, budget) -> SpanSelection:
+    """Bounded whole-span greedy from host scores in candidate order (litgpt/alpha_log_kv.py:177-226).
+
+    Unfinished spans are mandatory; old closed spans are kept first (density x1.1)
+    and evicted lowest density first (ties: later span first) to make room; a new
+    span replaces whole victims only if its density * length strictly exceeds
+    their summed density * length.
+    """
+    keep, archive, out_spans, out_pos = [], [], [], []
+    offset = 0
+    for (row, positions), tokens, size in zip(cut.candidates, cut.token_rows, cut.length_rows):
+        n = len(row)
+        old = [c[1] for c in row]
+        open_ = [not c[2] for c in row]
+        density = [float(host_scores[offset + i]) * (1.1 if old[i] else 1.0) for i in range(n)]
+        offset += n
+        chosen = [open_[i] or old[i] for i in range(n)]
+        room = budget - sum(size[i] for i in range(n) if chosen[i])
+
+        def evictable():
+            return sorted((i for i in range(n) if chosen[i] and not open_[i]), key=lambda i: (density[i], -i))
+
+        for i in evictable():
+            if room >= 0:
+                break
+            chosen[i] = False
+            room += size[i]
+        victims = None
+        for i in sorted((i for i in range(n) if not chosen[i]), key=lambda i: (-density[i], i)):
+            need = size[i]
+            free, lost, taken = room, 0.0, []
+            if free < need:
+                if victims is None:
+                    victims = evictable()
+                for j in victims:
+                    taken.append(j)
+                    free += size[j]
+                    lost += density[j] * size[j]
+                    if free >= need:
+                        break
+            if free >= need and (not taken or density[i] * need > lost):
+                for j in taken:
+                    chosen[j] = False
+                chosen[i] = True
+                room = free - need
+                victims = None
+        sel = np.repeat(np.asarray(chosen, dtype=bool), size) if n else np.zeros(0, dtype=bool)
+        keep.append(tokens[sel].tolist())
+        archive.append(tokens[~sel].tolist())
+        out_spans.append([(size[i], row[i][2]) for i in range(n) if chosen[i]])
+        out_pos.append(positions[tokens[sel]].tolist())
+    return SpanSelection(keep, archive, out_spans, out_pos)
+
+
+def select_spans(k, v, old_spans, old_positions, new_positions, ends, old_width, budget, max_span, *,
+                 beta_novelty=False, centroids=None, centroid_valid=None):
+    """Cut, score on the device (one score readback) and choose (litgpt/alpha_log_kv.py:69-81)."""
+    cut = cut_spans(old_spans, old_positions, new_positions, ends, old_width, max_span)
+    if cut is None:
+        rows = len(ends)
+        return SpanSelection([[] for _ in range(rows)], [[] for _ in range(rows)],
+                             [[] for _ in range(rows)], [[] for _ in range(rows)])
+    scores = score_spans(k, v, cut, beta_novelty=beta_novelty, centroids=centroids, centroid_valid=centroid_valid)
+    return choose_spans(cut, scores.cpu().tolist(), budget)
+
+
+def _table(rows, width, device):
+    t = np.full((len(rows), max(width, 1)), -1, dtype=np.int32)
+    for b, r in enumerate(rows):
+        t[b, :len(r)] = r
+    return torch.from_numpy(t).pin_memory().to(device, non_blocking=True)
+
+
+@torch.no_grad()
+def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
+    """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003).
+
+    Scores the whole candidate spans of ``[exact pool | flush]`` on the device,
+    reads the scores back once, chooses spans on the host, rewrites the exact
+    pool (into the cache's second pool buffer set, then swapped in) and archives
+    the rest, which is attach-routed with delayed joins.
+    """
+    if span_ends is None:
+        raise ValueError("AlphaLogKV requires natural span boundaries")
+    dev = k_raw.device
+    n_batch, G = cache.batch_size, cache.n_groups
+    P = cache.alpha_exact_tokens
+    old_width = cache.alpha_count
+    if positions_host is None:
+        positions_host = positions.cpu().tolist()
+    cut = cut_spans(cache._alpha_spans, cache._alpha_positions, positions_host, span_ends, old_width,
+                    cache.alpha_span_max_tokens)
+    if cut is None:
+        sel = SpanSelection([[] for _ in range(n_batch)], [[] for _ in range(n_batch)],
+                            [[] for _ in range(n_batch)], [[] for _ in range(n_batch)])
+    else:
+        scores = score_spans_split(cache.alpha_k_raw, cache.alpha_v, k_raw, v, old_width, cut,
+                                   beta_novelty=cache.beta_novelty, centroids=cache.centroid,
+                                   centroid_valid=cache.alive)
+        sel = choose_spans(cut, scores.cpu().tolist(), P)
+    cache._last_selection = sel
+    counts = [len(a) for a in sel.archive]
+    A = max(counts, default=0)
+    keep_t = _table(sel.keep, P, dev)
+    arch_t = _table(sel.archive, A, dev)
+    nk, nv, npos, nvalid = cache._alpha_spare
+    ak = torch.empty(n_batch, G, max(A, 1), cache.k_dim, dtype=k_raw.dtype, device=dev)
+    av = torch.empty(n_batch, G, max(A, 1), cache.v_dim, dtype=v.dtype, device=dev)
+    ap = torch.empty(n_batch, max(A, 1), dtype=torch.int64, device=dev)
+    pk, pv, ppos = cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos
+    args = _lib.PartitionArgs(
+        _lib.ptr(pk), pk.stride(0), pk.stride(1), pk.stride(2),
+        _lib.ptr(pv), pv.stride(0), pv.stride(1), pv.stride(2),
+        _lib.ptr(ppos), ppos.stride(0),
+        _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _lib.ptr(positions), positions.stride(0),
+        int(old_width), _lib.ptr(keep_t), _lib.ptr(arch_t), P, A, n_batch, G, cache.k_dim, cache.v_dim,
+        _lib.ptr(nk), _lib.ptr(nv), _lib.ptr(npos), _lib.ptr(nvalid),
+        _lib.ptr(ak), _lib.ptr(av), _lib.ptr(ap))
+    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(args), _lib.stream_of(dev)), "logkv_alpha_partition")
+    cache._alpha_spare = (pk, pv, ppos, cache.alpha_valid)
+    cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid = nk, nv, npos, nvalid
+    cache.alpha_count = max(map(len, sel.keep), default=0)
+    cache._alpha_spans, cache._alpha_positions = sel.spans, sel.positions
+    if A:
+        counts_t = torch.tensor(counts, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
+        cache._route_commit(ak, av, ap, counts_t)
+    return sel

@@ -161,4 +161,34 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
   return LOGKV_OK;
 }
 
+int logkv_score_spans(const logkv_span_args* a, float* scores, void* stream) {
+  if (!a || !scores) return fail(LOGKV_EINVAL, "span args or output are NULL");
+  if (a->n_spans < 0) return fail(LOGKV_EINVAL, "negative span count");
+  if (a->n_groups < 1 || a->n_groups > 16)
+    return fail(LOGKV_EINVAL, "span scoring supports 1..16 KV groups, got %d", a->n_groups);
+  if (a->dk < 1 || a->dv < 1 || a->dk > logkv::kMaxDim || a->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "span scoring widths must be in [1, %d]", logkv::kMaxDim);
+  if (a->n_spans && (!a->tokens || !a->span_offsets || !a->span_rows || !a->flush_k || !a->flush_v))
+    return fail(LOGKV_EINVAL, "span tables or rows are NULL");
+  if (a->old_width > 0 && (!a->pool_k || !a->pool_v)) return fail(LOGKV_EINVAL, "pool rows are NULL");
+  if (a->beta_novelty && (!a->centroids || !a->centroid_valid || a->k_max < 1))
+    return fail(LOGKV_EINVAL, "Beta novelty needs centroids and their valid flags");
+  const int rc = logkv::launch_score(*a, scores, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "score launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_alpha_partition(const logkv_partition_args* a, void* stream) {
+  if (!a) return fail(LOGKV_EINVAL, "partition args are NULL");
+  if (a->P < 0 || a->A < 0 || a->n_batch < 1 || a->n_groups < 1) return fail(LOGKV_EINVAL, "bad partition sizes");
+  if (a->dk % 4 || a->dv % 4 || a->dk < 4 || a->dv < 4)
+    return fail(LOGKV_EINVAL, "partition widths must be multiples of 4");
+  if ((a->P && (!a->out_pool_k || !a->out_pool_v || !a->out_pool_pos || !a->out_pool_valid || !a->keep)) ||
+      (a->A && (!a->arch_k || !a->arch_v || !a->arch_pos || !a->archive)))
+    return fail(LOGKV_EINVAL, "partition outputs or index tables are NULL");
+  const int rc = logkv::launch_partition(*a, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "partition launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"

@@ -41,6 +41,8 @@ int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t ca, int64_
 int64_t row_bytes(int dk, int dv);
 int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                  hipStream_t stream);
+int launch_score(const logkv_span_args& a, float* out, hipStream_t stream);
+int launch_partition(const logkv_partition_args& a, hipStream_t stream);
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
 

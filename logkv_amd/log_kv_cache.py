@@ -221,6 +221,11 @@ class LogStructuredKVCache(nn.Module):
             buf("alpha_v", torch.zeros(batch_size, n_groups, P, v_dim, device=device, dtype=dtype))
             buf("alpha_pos", torch.zeros(batch_size, P, device=device, dtype=torch.int64))
             buf("alpha_valid", torch.zeros(batch_size, P, device=device, dtype=torch.bool))
+            # The pool is rewritten from [old pool | flush] rows into this second
+            # buffer set, then the two sets swap, so no partition reads a row it
+            # has already overwritten.
+            self._alpha_spare = (torch.zeros_like(self.alpha_k_raw), torch.zeros_like(self.alpha_v),
+                                 torch.zeros_like(self.alpha_pos), torch.zeros_like(self.alpha_valid))
             self._alpha_spans = [[] for _ in range(batch_size)]
             self._alpha_positions = [[] for _ in range(batch_size)]
             self._recent_span_ends = [[False] * cap for _ in range(batch_size)]
@@ -426,6 +431,8 @@ class LogStructuredKVCache(nn.Module):
         if self.alpha_exact_tokens:
             for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid"):
                 getattr(self, name).zero_()
+            for t in self._alpha_spare:
+                t.zero_()
             self._alpha_spans = [[] for _ in range(self.batch_size)]
             self._alpha_positions = [[] for _ in range(self.batch_size)]
             self._recent_span_ends = [[False] * self.recent_capacity for _ in range(self.batch_size)]

@@ -101,6 +101,7 @@ class OracleCache:
         self.alpha_spans = [[] for _ in range(batch)]
         self.alpha_positions = [[] for _ in range(batch)]
         self.beta_cuts = []
+        self.late_joins = 0       # delayed-archive re-sorts performed (test coverage evidence)
 
     # ---- ladder access -------------------------------------------------
     def ladder(self, b, g, c) -> lad.Ladder:
@@ -146,6 +147,7 @@ class OracleCache:
 
     def join_late(self, b, g, c, keys, values, pos):
         """Delayed archive: re-sort the cluster's entries and the new rows by position."""
+        self.late_joins += 1
         ladder = self.ladder(b, g, c)
         old = ladder.entries()
         new = self._token_rows(keys, values, pos, 0)
