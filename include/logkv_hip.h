@@ -165,6 +165,87 @@ typedef struct logkv_partition_args {
 
 int logkv_alpha_partition(const logkv_partition_args* args, void* stream);
 
+/* Read-only view of one cache for the attention readout. Ladder fields as in
+ * logkv_ladder_view; exact pool alpha_* [n_batch, G, alpha_cap, d] with
+ * positions / valid flags [n_batch, alpha_cap]; recent window (post-RoPE keys)
+ * [n_batch, G, recent_cap, d]; RoPE tables cos / sin [positions, rope_n] f32 or
+ * bf16 (table_bf16 = 1) with element strides. */
+typedef struct logkv_readout_view {
+  const uint16_t* level_k;
+  const uint16_t* level_v;
+  const float* level_w;
+  const int64_t* level_sum_wp;
+  const int16_t* level_count;
+  int32_t n_batch, n_groups, k_max, levels, slots, dk, dv;
+  const uint16_t* alpha_k;
+  const uint16_t* alpha_v;
+  const int64_t* alpha_pos;
+  const uint8_t* alpha_valid;
+  int32_t alpha_cap, alpha_count;
+  const uint16_t* recent_k;
+  const uint16_t* recent_v;
+  int32_t recent_cap, recent_count;
+  const void* cos;
+  const void* sin;
+  int64_t cos_s0, cos_s1, sin_s0, sin_s1;
+  int32_t rope_n, table_bf16;
+  int64_t rope_rows;  /* positions in the tables; anchors beyond clamp to the last row */
+} logkv_readout_view;
+
+/* Ints of the plan table: per lane K*L + 1 pooled-row offsets (clusters in
+ * order, levels top first), then the pooled width (largest lane count). */
+int64_t logkv_plan_table_ints(const logkv_readout_view* cache);
+
+/* Mid-anchor slot plan of the occupied entries, kept on the device.
+ * Replaces _semantic_mid_attention_plan (litgpt/log_kv_cache.py:5979-6007). */
+int logkv_mid_plan(const logkv_readout_view* cache, int32_t* table, void* stream);
+
+/* Packed rows [pooled (width) | exact | recent | current] into out_k / out_v
+ * [n_batch, G, out_cap, dim] bf16. With skip_pooled, only rows from tail_start
+ * of the [exact | recent | current] tail are written (a decode step re-packs
+ * only its new rows). Current K/V [n_batch, G, cur_len, d] strided.
+ * Replaces pack / pack_mid_kv (litgpt/log_kv_pack_triton.py:95-125,
+ * litgpt/log_kv_pack.py:105-133). */
+typedef struct logkv_pack_args {
+  const uint16_t* cur_k;
+  int64_t ck_sb, ck_sg, ck_st;
+  const uint16_t* cur_v;
+  int64_t cv_sb, cv_sg, cv_st;
+  int32_t cur_len;
+  uint16_t* out_k;
+  uint16_t* out_v;
+  int32_t out_cap, dim;
+  int32_t skip_pooled, tail_start;
+} logkv_pack_args;
+
+int logkv_pack(const logkv_readout_view* cache, const logkv_pack_args* args, const int32_t* table, void* stream);
+
+/* Attention of queries q [n_batch, n_heads, tq, dk] (post-RoPE, bf16, strided)
+ * over the packed rows k / v [n_batch, G, cap, dim]: pooled width (read from
+ * the plan table) + `tail` rows, the last causal_tail rows causal; out
+ * [n_batch, n_heads, tq, dv] bf16 strided. inv_scale_bf16 is 1/scale rounded
+ * to bf16 (the packed query's bias coordinate).
+ * Replaces the Flash SDPA call on the packed workspace
+ * (litgpt/log_kv_cache.py:6751-6758) and log_kv_slot_attention's first-order
+ * math (litgpt/log_kv_cache.py:6501-6630). */
+typedef struct logkv_attention_args {
+  const uint16_t* q;
+  int64_t q_sb, q_sh, q_st;
+  int32_t n_batch, n_heads, n_groups, tq, dk, dv, dim;
+  const uint16_t* k;
+  const uint16_t* v;
+  int32_t cap;
+  int32_t tail;
+  int32_t causal_tail;
+  float scale, inv_scale_bf16;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_st;
+} logkv_attention_args;
+
+int64_t logkv_attention_workspace_bytes(const logkv_attention_args* args);
+int logkv_decode_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,38 @@ class PartitionArgs(C.Structure):
     ]
 
 
+class ReadoutView(C.Structure):
+    _fields_ = [
+        ("level_k", _p), ("level_v", _p), ("level_w", _p), ("level_sum_wp", _p), ("level_count", _p),
+        ("n_batch", _i32), ("n_groups", _i32), ("k_max", _i32), ("levels", _i32), ("slots", _i32),
+        ("dk", _i32), ("dv", _i32),
+        ("alpha_k", _p), ("alpha_v", _p), ("alpha_pos", _p), ("alpha_valid", _p),
+        ("alpha_cap", _i32), ("alpha_count", _i32),
+        ("recent_k", _p), ("recent_v", _p), ("recent_cap", _i32), ("recent_count", _i32),
+        ("cos", _p), ("sin", _p), ("cos_s0", _i64), ("cos_s1", _i64), ("sin_s0", _i64), ("sin_s1", _i64),
+        ("rope_n", _i32), ("table_bf16", _i32), ("rope_rows", _i64),
+    ]
+
+
+class PackArgs(C.Structure):
+    _fields_ = [
+        ("cur_k", _p), ("ck_sb", _i64), ("ck_sg", _i64), ("ck_st", _i64),
+        ("cur_v", _p), ("cv_sb", _i64), ("cv_sg", _i64), ("cv_st", _i64),
+        ("cur_len", _i32), ("out_k", _p), ("out_v", _p), ("out_cap", _i32), ("dim", _i32),
+        ("skip_pooled", _i32), ("tail_start", _i32),
+    ]
+
+
+class AttentionArgs(C.Structure):
+    _fields_ = [
+        ("q", _p), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64),
+        ("n_batch", _i32), ("n_heads", _i32), ("n_groups", _i32), ("tq", _i32), ("dk", _i32), ("dv", _i32),
+        ("dim", _i32), ("k", _p), ("v", _p), ("cap", _i32), ("tail", _i32), ("causal_tail", _i32),
+        ("scale", C.c_float), ("inv_scale_bf16", C.c_float),
+        ("out", _p), ("o_sb", _i64), ("o_sh", _i64), ("o_st", _i64),
+    ]
+
+
 # Exported symbol -> (restype, argtypes); the tests check this table against the header.
 SIGNATURES = {
     "logkv_last_error": (C.c_char_p, []),
@@ -84,6 +116,11 @@ SIGNATURES = {
                                  _p, _i64, _p, _p, _p]),
     "logkv_score_spans": (_i32, [C.POINTER(SpanArgs), _p, _p]),
     "logkv_alpha_partition": (_i32, [C.POINTER(PartitionArgs), _p]),
+    "logkv_plan_table_ints": (_i64, [C.POINTER(ReadoutView)]),
+    "logkv_mid_plan": (_i32, [C.POINTER(ReadoutView), _p, _p]),
+    "logkv_pack": (_i32, [C.POINTER(ReadoutView), C.POINTER(PackArgs), _p, _p]),
+    "logkv_attention_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
+    "logkv_decode_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
 }
 
 

@@ -191,4 +191,73 @@ int logkv_alpha_partition(const logkv_partition_args* a, void* stream) {
   return LOGKV_OK;
 }
 
+int64_t logkv_plan_table_ints(const logkv_readout_view* c) {
+  if (!c) return -1;
+  return int64_t(c->n_batch) * c->n_groups * (int64_t(c->k_max) * c->levels + 1) + 1;
+}
+
+static int check_readout(const logkv_readout_view* c) {
+  if (!c) return fail(LOGKV_EINVAL, "readout view is NULL");
+  if (c->n_batch < 1 || c->n_groups < 1 || c->k_max < 1 || c->levels < 1 || c->slots < 1)
+    return fail(LOGKV_EINVAL, "bad readout sizes");
+  if (c->dk < 1 || c->dv < 1 || c->dk > logkv::kMaxDim || c->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "readout widths must be in [1, %d]", logkv::kMaxDim);
+  if (!c->level_k || !c->level_v || !c->level_w || !c->level_sum_wp || !c->level_count)
+    return fail(LOGKV_EINVAL, "readout ladder buffer is NULL");
+  if (c->alpha_count < 0 || c->alpha_count > c->alpha_cap || (c->alpha_count && (!c->alpha_k || !c->alpha_v ||
+      !c->alpha_pos || !c->alpha_valid)))
+    return fail(LOGKV_EINVAL, "bad exact pool view");
+  if (c->recent_count < 0 || c->recent_count > c->recent_cap || (c->recent_count && (!c->recent_k || !c->recent_v)))
+    return fail(LOGKV_EINVAL, "bad recent window view");
+  if (!c->cos || !c->sin || c->rope_n < 0 || c->rope_n > c->dk || c->rope_n % 2 || c->rope_rows < 1)
+    return fail(LOGKV_EINVAL, "bad RoPE tables");
+  return LOGKV_OK;
+}
+
+int logkv_mid_plan(const logkv_readout_view* c, int32_t* table, void* stream) {
+  int rc = check_readout(c);
+  if (rc) return rc;
+  if (!table) return fail(LOGKV_EINVAL, "plan table is NULL");
+  rc = logkv::launch_plan(*c, table, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "plan launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_pack(const logkv_readout_view* c, const logkv_pack_args* p, const int32_t* table, void* stream) {
+  int rc = check_readout(c);
+  if (rc) return rc;
+  if (!p || !table || !p->out_k || !p->out_v) return fail(LOGKV_EINVAL, "pack outputs or plan table are NULL");
+  if (p->dim <= c->dk || p->dim < c->dv || p->dim % 8 || p->dim > 264)
+    return fail(LOGKV_EINVAL, "packed width %d must exceed dk, hold dv, be a multiple of 8 and <= 264", p->dim);
+  if (p->cur_len < 0 || (p->cur_len && (!p->cur_k || !p->cur_v)) || p->tail_start < 0 || p->out_cap < 0)
+    return fail(LOGKV_EINVAL, "bad current rows or output capacity");
+  rc = logkv::launch_pack(*c, *p, table, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "pack launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int64_t logkv_attention_workspace_bytes(const logkv_attention_args* a) {
+  if (!a || a->n_groups < 1) return -1;
+  return logkv::attention_workspace_floats(*a) * 4;
+}
+
+int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, int64_t table_ints, void* ws,
+                           int64_t ws_bytes, void* stream) {
+  if (!a || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention args or plan table are NULL");
+  if (a->n_groups < 1 || a->n_heads % a->n_groups) return fail(LOGKV_EINVAL, "heads must be a multiple of groups");
+  const int nq = (a->n_heads / a->n_groups) * a->tq;
+  if (a->tq < 1 || nq > 16) return fail(LOGKV_EINVAL, "queries per KV group (%d) must be in [1, 16]", nq);
+  if (a->dim % 8 || a->dim > 264 || a->dim <= a->dk || a->dim < a->dv || a->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "bad packed width %d", a->dim);
+  if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
+    return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
+  if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
+  if (!ws || ws_bytes < logkv::attention_workspace_floats(*a) * 4)
+    return fail(LOGKV_EINVAL, "attention workspace too small");
+  const int rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(ws),
+                                         static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"

@@ -43,6 +43,10 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
                  hipStream_t stream);
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream);
 int launch_partition(const logkv_partition_args& a, hipStream_t stream);
+int launch_plan(const logkv_readout_view& c, int32_t* table, hipStream_t stream);
+int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int32_t* table, hipStream_t stream);
+int64_t attention_workspace_floats(const logkv_attention_args& a);
+int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream);
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
 

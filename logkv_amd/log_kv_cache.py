@@ -437,6 +437,25 @@ class LogStructuredKVCache(nn.Module):
             self._alpha_positions = [[] for _ in range(self.batch_size)]
             self._recent_span_ends = [[False] * self.recent_capacity for _ in range(self.batch_size)]
 
+    def _apply(self, fn, recurse=True):
+        # Moving or casting buffers invalidates raw pointers held in workspaces
+        # (litgpt/log_kv_cache.py:6226-6232).
+        self._mid_decode_state = None
+        self._workspace = None
+        return super()._apply(fn, recurse)
+
+    # ------------------------------------------------------------------
+    # Readout plan
+    # ------------------------------------------------------------------
+    def _semantic_mid_attention_plan(self):
+        """Plan of the occupied slots, built on the device (litgpt/log_kv_cache.py:5979-6007)."""
+        from .log_kv_pack import semantic_mid_attention_plan
+        return semantic_mid_attention_plan(self)
+
+    def _semantic_attention_plan(self):
+        """Mid-anchor plan (litgpt/log_kv_cache.py:5955-5958); the only anchor mode built."""
+        return self._semantic_mid_attention_plan()
+
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand
     # ------------------------------------------------------------------

@@ -1,0 +1,237 @@
+"""Attention readout of a LogKV cache on the device: slot plan, packed K/V, decode attention.
+
+Mirrors the reference's first-order mid-anchor readout:
+
+* ``semantic_mid_attention_plan`` -> ``LogStructuredKVCache._semantic_mid_attention_plan``
+  (litgpt/log_kv_cache.py:5979-6007), here a device table of per-lane pooled-row
+  offsets plus the pooled width, so building it never waits for the host;
+* ``pack_mid_kv`` -> litgpt/log_kv_pack.py:105-133 (same arguments, checks and
+  return value);
+* ``log_kv_chunk_attention`` -> litgpt/log_kv_cache.py:6802-6836 for
+  ``second_order_scale == 0`` with mid anchors (the path that reaches
+  ``_mid_chunk_attention``, litgpt/log_kv_cache.py:6772-6799), including the
+  decode-prefix reuse of ``reuse_prefix=True``.
+
+Packed rows are ``[pooled (plan width) | exact pool | recent | current]`` of
+width ``dim = 8*ceil(max(Dk + 1, Dv) / 8)``; the key's column ``Dk`` carries
+``log(max(w, 1))`` for pooled slots, 0 for exact / recent / current rows and
+-10000 for empty rows, and the query carries ``1/scale`` there, so the logit of
+a slot is ``scale * q.k + log w`` (litgpt/log_kv_cache.py:6428-6464).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from ._lib import AttentionArgs, PackArgs, ReadoutView, check, lib, ptr, stream_of
+
+_BACKENDS = ("auto", "triton", "hip")
+
+
+def packed_dim(k_dim: int, v_dim: int) -> int:
+    return ((max(k_dim + 1, v_dim) + 7) // 8) * 8
+
+
+class MidAttentionPlan:
+    """Device plan of the occupied slots: ``table`` int32 ``[lanes * (K*L + 1) + 1]``.
+
+    Per lane, ``K*L`` offsets of the (cluster, level top-down) blocks in the
+    pooled rows and the lane's slot count; the last entry is the pooled width
+    (the largest lane count). ``width`` reads that entry back once.
+    """
+
+    __slots__ = ("table", "lanes", "blocks", "_width")
+
+    def __init__(self, table: torch.Tensor, lanes: int, blocks: int):
+        self.table, self.lanes, self.blocks = table, lanes, blocks
+        self._width = None
+
+    @property
+    def width(self) -> int:
+        if self._width is None:
+            self._width = int(self.table[-1].item())
+        return self._width
+
+    def lane_counts(self) -> torch.Tensor:
+        return self.table[:-1].view(self.lanes, self.blocks + 1)[:, -1]
+
+
+def readout_view(cache) -> ReadoutView:
+    table_bf16 = cache.cos_cache.dtype == torch.bfloat16
+    if cache.cos_cache.dtype not in (torch.float32, torch.bfloat16) or cache.sin_cache.dtype != cache.cos_cache.dtype:
+        raise ValueError("RoPE tables must both be float32 or both bfloat16")
+    if cache.cos_cache.size(1) != cache.rope_n_elem or cache.slot_k_dim != cache.k_dim:
+        raise NotImplementedError("packed readout requires RoPE tables of width rope_n_elem")
+    view = ReadoutView(
+        ptr(cache.level_k), ptr(cache.level_v), ptr(cache.level_w), ptr(cache.level_sum_wp), ptr(cache.level_count),
+        cache.batch_size, cache.n_groups, cache.K_max, cache.L_alloc, cache.B_prime, cache.k_dim, cache.v_dim)
+    if cache.alpha_exact_tokens:
+        view.alpha_k, view.alpha_v = ptr(cache.alpha_k_raw), ptr(cache.alpha_v)
+        view.alpha_pos, view.alpha_valid = ptr(cache.alpha_pos), ptr(cache.alpha_valid)
+        view.alpha_cap, view.alpha_count = cache.alpha_exact_tokens, cache.alpha_count
+    view.recent_k, view.recent_v = ptr(cache.recent_k), ptr(cache.recent_v)
+    view.recent_cap, view.recent_count = cache.recent_capacity, cache.recent_count
+    view.cos, view.sin = ptr(cache.cos_cache), ptr(cache.sin_cache)
+    view.cos_s0, view.cos_s1 = cache.cos_cache.stride()
+    view.sin_s0, view.sin_s1 = cache.sin_cache.stride()
+    view.rope_n, view.table_bf16 = cache.rope_n_elem, 1 if table_bf16 else 0
+    view.rope_rows = min(cache.cos_cache.size(0), cache.sin_cache.size(0))
+    return view
+
+
+def semantic_mid_attention_plan(cache, view: ReadoutView | None = None) -> MidAttentionPlan:
+    """Plan of the occupied slots (litgpt/log_kv_cache.py:5979-6007), built on the device."""
+    view = readout_view(cache) if view is None else view
+    n = int(lib().logkv_plan_table_ints(C.byref(view)))
+    table = torch.empty(n, dtype=torch.int32, device=cache.level_k.device)
+    check(lib().logkv_mid_plan(C.byref(view), ptr(table), stream_of(table.device)), "logkv_mid_plan")
+    return MidAttentionPlan(table, cache.batch_size * cache.n_groups, cache.K_max * cache.L_alloc)
+
+
+def _check_backend(backend):
+    if backend == "torch":
+        raise NotImplementedError("logkv_amd has no PyTorch packer; the HIP pack kernel is the only path")
+    if backend not in _BACKENDS:
+        raise ValueError("packing backend must be 'auto', 'torch' or 'triton'")
+
+
+def _check_kv(cache, k, v):
+    if (k.ndim != 4 or v.ndim != 4 or k.shape[:3] != v.shape[:3]
+            or k.shape[:2] != (cache.batch_size, cache.n_groups)
+            or k.size(-1) != cache.k_dim or v.size(-1) != cache.v_dim
+            or k.device != cache.level_k.device or v.device != k.device
+            or k.dtype != cache.level_k.dtype or v.dtype != k.dtype):
+        raise ValueError("K/V shape, device and dtype must match the cache")
+
+
+def _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, tail_start):
+    args = PackArgs(ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], k.size(2), ptr(ka), ptr(va), ka.size(2), dim,
+                    1 if skip_pooled else 0, tail_start)
+    if k.stride(3) != 1 or v.stride(3) != 1:
+        raise ValueError("current K/V rows must be contiguous in the feature dimension")
+    check(lib().logkv_pack(C.byref(view), C.byref(args), ptr(plan.table), stream_of(k.device)), "logkv_pack")
+
+
+def pack_mid_kv(cache, plan, k, v, dim, *, backend=None, buffers=None, skip_pooled=False, recent_start=0):
+    """Return final padded K/V ``[Bt, G, length, dim]``; K's extra coordinate stores log mass / masking.
+
+    Same contract as litgpt/log_kv_pack.py:105-133; ``length`` is the plan's
+    pooled width plus the exact, recent and current rows (reading the width
+    back once per plan).
+    """
+    backend = cache.semantic_pack_backend if backend is None else backend
+    _check_backend(backend)
+    if cache.semantic_anchor_mode != "mid":
+        raise ValueError("mid packer requires semantic_anchor_mode='mid'")
+    _check_kv(cache, k, v)
+    if not isinstance(plan, MidAttentionPlan) or plan.lanes != cache.batch_size * cache.n_groups \
+            or plan.table.device != k.device:
+        raise ValueError("mid attention plan must match K/V lanes and device")
+    if dim <= k.size(-1) or dim < v.size(-1):
+        raise ValueError("packed dimension must hold K, its bias coordinate, and V")
+    if ((skip_pooled and buffers is None) or (recent_start and not skip_pooled)
+            or not 0 <= recent_start <= cache.recent_count):
+        raise ValueError("prefix reuse requires a workspace and a valid recent offset")
+    if k.requires_grad or v.requires_grad:
+        raise NotImplementedError("logkv_amd packs for inference; K/V must not require grad")
+    length = plan.width + cache.alpha_count + cache.recent_count + k.size(2)
+    if buffers is not None:
+        if len(buffers) != 2 or any(buf.ndim != 4 or buf.shape[:2] != k.shape[:2] or buf.size(2) < length
+                                    or buf.size(3) != dim or not buf.is_contiguous() or buf.dtype != k.dtype
+                                    or buf.device != k.device for buf in buffers):
+            raise ValueError("decode workspace does not match the packed layout")
+        ka, va = buffers
+    else:
+        ka = k.new_empty((*k.shape[:2], length, dim))
+        va = v.new_empty((*v.shape[:2], length, dim))
+    view = readout_view(cache)
+    _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, cache.alpha_count + recent_start)
+    return ka[:, :, :length], va[:, :, :length]
+
+
+def _inv_scale_bf16(scale: float) -> float:
+    return torch.tensor(1.0 / scale, dtype=torch.float32).to(torch.bfloat16).item()
+
+
+def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups, workspace=None):
+    """Attention of ``q [Bt, Hq, Tq, Dk]`` over packed rows ``[plan width + tail]`` of ``ka / va``.
+
+    The pooled width is read on the device, so ``ka / va`` may be longer than
+    the packed rows (a reusable decode workspace)."""
+    bt, hq, tq, dk = q.shape
+    if q.dtype != torch.bfloat16 or q.stride(3) != 1:
+        raise ValueError("queries must be bfloat16 with contiguous features")
+    if not ka.is_contiguous() or not va.is_contiguous() or ka.shape != va.shape:
+        raise ValueError("packed K/V must be contiguous and of one shape")
+    out = q.new_empty(bt, hq, tq, v_dim)
+    args = AttentionArgs(ptr(q), *q.stride()[:3], bt, hq, n_groups, tq, dk, v_dim, ka.size(3), ptr(ka), ptr(va),
+                         ka.size(2), tail, causal_tail, float(scale), _inv_scale_bf16(scale), ptr(out),
+                         *out.stride()[:3])
+    need = int(lib().logkv_attention_workspace_bytes(C.byref(args)))
+    if need < 0:
+        raise ValueError("bad attention shape")
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    check(lib().logkv_decode_attention(C.byref(args), ptr(plan.table), plan.table.numel(), ptr(workspace),
+                                       workspace.numel(), stream_of(q.device)), "logkv_decode_attention")
+    return out, workspace
+
+
+def _decode_capacity(cache, t: int) -> int:
+    return cache.K_max * cache.L_alloc * cache.B_prime + cache.alpha_exact_tokens + cache.recent_capacity + max(2, t)
+
+
+def log_kv_chunk_attention(cache, q_b, k_b, v_b, scale, second_order_scale=1.0, attention_plan=None, *,
+                           causal_tail=None, reuse_prefix=False):
+    """One streaming attention step over ``[cache state | current chunk (causal)]``, without committing the chunk.
+
+    Restates litgpt/log_kv_cache.py:6802-6836 for the first-order mid-anchor
+    path (``second_order_scale == 0``); the packed workspace and the softmax
+    run in the HIP library. With ``reuse_prefix`` (inference, at most two query
+    rows) the packed prefix is kept on the cache and later steps re-pack only
+    their new rows, as in litgpt/log_kv_cache.py:6772-6799.
+    """
+    causal_tail = q_b.size(2) if causal_tail is None else causal_tail
+    if causal_tail and causal_tail != q_b.size(2):
+        raise ValueError("causal_tail must equal query length or be zero")
+    if second_order_scale != 0.0 or not cache.semantic_clusters or cache.semantic_anchor_mode != "mid":
+        raise NotImplementedError("logkv_amd reads out the first-order mid-anchor path (second_order_scale=0)")
+    _check_backend(cache.semantic_pack_backend)
+    _check_kv(cache, k_b, v_b)
+    if not 1e-3 <= scale <= 1.0:
+        raise NotImplementedError("attention scale must lie in [1e-3, 1]")
+    if q_b.ndim != 4 or q_b.size(0) != cache.batch_size or q_b.size(1) % cache.n_groups \
+            or q_b.size(-1) != cache.k_dim or q_b.device != k_b.device:
+        raise ValueError("queries must be [B, n_heads, t, k_dim] on the cache's device with n_heads % n_groups == 0")
+    dim = packed_dim(k_b.size(-1), v_b.size(-1))
+    view = readout_view(cache)
+    reuse = (reuse_prefix and not torch.is_grad_enabled() and q_b.size(2) <= 2
+             and not k_b.requires_grad and not v_b.requires_grad)
+    key = (k_b.device, k_b.dtype, dim, id(cache.cos_cache), id(cache.sin_cache))
+    buffers, skip_pooled, recent_start = None, False, 0
+    if reuse:
+        saved = cache._mid_decode_state
+        if saved is not None and saved[0] == key:
+            _, plan, buffers, recent_start, workspace = saved
+            skip_pooled = True
+        else:
+            plan = semantic_mid_attention_plan(cache, view) if attention_plan is None else attention_plan
+            workspace = None
+        if buffers is None:
+            cap = _decode_capacity(cache, k_b.size(2))
+            buffers = (k_b.new_empty(*k_b.shape[:2], cap, dim), v_b.new_empty(*v_b.shape[:2], cap, dim))
+    else:
+        plan = semantic_mid_attention_plan(cache, view) if attention_plan is None else attention_plan
+        workspace = None
+        cap = _decode_capacity(cache, k_b.size(2))
+        buffers = (k_b.new_empty(*k_b.shape[:2], cap, dim), v_b.new_empty(*v_b.shape[:2], cap, dim))
+    ka, va = buffers
+    _launch_pack(cache, view, plan, k_b, v_b, dim, ka, va, skip_pooled, cache.alpha_count + recent_start)
+    tail = cache.alpha_count + cache.recent_count + k_b.size(2)
+    out, workspace = packed_attention(q_b, ka, va, plan, tail, scale, causal_tail, v_b.size(-1), cache.n_groups,
+                                      workspace)
+    if reuse:
+        cache._mid_decode_state = (key, plan, buffers, cache.recent_count, workspace)
+    return out

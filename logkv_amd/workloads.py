@@ -40,3 +40,38 @@ def rope_tables(n_positions, n_elem, base=10000.0, dtype=torch.float32):
     idx = torch.outer(torch.arange(n_positions, dtype=torch.float32), theta)
     idx = torch.cat((idx, idx), dim=-1)
     return torch.cos(idx).to(dtype), torch.sin(idx).to(dtype)
+
+
+@torch.no_grad()
+def fill_readout_state(cache, seed=0, fill=0.75, recent=None, exact=None, mass=(1.0, 64.0)):
+    """Synthetic compressed-cache state for readout: random slot counts (about ``fill`` of
+    each ladder level), random bf16 keys / values, masses ~ U(mass), position sums
+    inside the cache's span; a full recent window and exact pool unless given."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    Bt, G, K, L, S = cache.level_w.shape
+    dk, dv = cache.k_dim, cache.v_dim
+    counts = torch.binomial(torch.full((Bt, G, K, L), float(S)), torch.full((Bt, G, K, L), fill), generator=g)
+    counts = counts.to(torch.int16)
+    occupied = torch.arange(S).view(1, 1, 1, 1, S) < counts.unsqueeze(-1)
+    w = torch.empty(Bt, G, K, L, S).uniform_(*mass, generator=g).floor() * occupied
+    horizon = max(cache.max_seq_length - cache.recent_capacity, 1)
+    anchor = torch.randint(0, horizon, (Bt, G, K, L, S), generator=g)
+    cache.level_count.copy_(counts)
+    cache.level_w.copy_(w)
+    cache.level_sum_wp.copy_((w.long() * anchor) * occupied)
+    cache.level_k.copy_((torch.randn(cache.level_k.shape, generator=g) * occupied.unsqueeze(-1)).to(torch.bfloat16))
+    cache.level_v.copy_((torch.randn(cache.level_v.shape, generator=g) * occupied.unsqueeze(-1)).to(torch.bfloat16))
+    n_recent = cache.recent_size if recent is None else recent
+    cache.recent_k[:, :, :n_recent].copy_(torch.randn(Bt, G, n_recent, cache.recent_k.size(-1), generator=g))
+    cache.recent_v[:, :, :n_recent].copy_(torch.randn(Bt, G, n_recent, dv, generator=g))
+    cache.recent_count = n_recent
+    if cache.alpha_exact_tokens:
+        P = cache.alpha_exact_tokens
+        n_exact = P if exact is None else exact
+        cache.alpha_k_raw[:, :, :n_exact].copy_(torch.randn(Bt, G, n_exact, dk, generator=g))
+        cache.alpha_v[:, :, :n_exact].copy_(torch.randn(Bt, G, n_exact, dv, generator=g))
+        cache.alpha_pos[:, :n_exact].copy_(torch.randint(0, horizon, (Bt, n_exact), generator=g))
+        cache.alpha_valid[:, :n_exact].copy_(torch.rand(Bt, n_exact, generator=g) < 0.95)
+        cache.alpha_count = n_exact
+    cache.token_count = horizon + n_recent
+    cache._mid_decode_state = None

@@ -128,7 +128,7 @@ def attention(q, ka, va, scale, causal_tail, dv):
     n_groups, total, dim = ka.shape[1], ka.shape[2], ka.shape[3]
     qa = np.zeros((n_batch, hq, tq, dim), np.float64)
     qa[..., :dk] = q
-    qa[..., dk] = float(bf16_round(np.float32(1.0 / scale)))
+    qa[..., dk] = float(np.asarray(bf16_round(np.float32(1.0 / scale))).reshape(-1)[0])
     rep = hq // n_groups
     kk = np.repeat(ka.astype(np.float64), rep, axis=1)
     vv = np.repeat(va.astype(np.float64), rep, axis=1)

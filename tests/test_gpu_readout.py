@@ -1,0 +1,199 @@
+"""Readout parity on the device: slot plan, packed K/V and mass-biased attention vs the oracle.
+
+Packed rows are compared value-for-value (bf16), except the log-mass column,
+which may differ by one bf16 ulp (device ``logf`` vs numpy ``log`` before
+rounding). Attention is compared with the oracle's float64 evaluation on the
+same bf16 operands: ``|out - ref| <= 2e-3 * max(1, |ref|) + ulp(ref) / 2``,
+the last term being the rounding of the output to bf16 (up to 2^-8 relative,
+so it is stated separately from the 2e-3 budget for the computation).
+"""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from harness import feed, make_pair, to_np
+from logkv_amd import LogStructuredKVCache, log_kv_chunk_attention, pack_mid_kv, packed_dim
+from logkv_amd.workloads import Mixture, fill_readout_state, rope_tables
+from oracle import readout as ro
+from oracle.numerics import bf16_round
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def state_of(cache):
+    """Oracle-side view of a device cache's readout fields."""
+    Bt, G = cache.batch_size, cache.n_groups
+    ns = SimpleNamespace(
+        level_k=to_np(cache.level_k), level_v=to_np(cache.level_v), level_w=to_np(cache.level_w),
+        level_sum_wp=to_np(cache.level_sum_wp), level_count=to_np(cache.level_count).astype(np.int64),
+        recent_k=to_np(cache.recent_k), recent_v=to_np(cache.recent_v), recent_count=cache.recent_count,
+        alpha_count=cache.alpha_count)
+    if cache.alpha_exact_tokens:
+        ns.alpha_k_raw, ns.alpha_v = to_np(cache.alpha_k_raw), to_np(cache.alpha_v)
+        ns.alpha_pos, ns.alpha_valid = to_np(cache.alpha_pos), to_np(cache.alpha_valid).astype(bool)
+    else:
+        ns.alpha_k_raw = np.zeros((Bt, G, 0, cache.k_dim), np.float32)
+        ns.alpha_v = np.zeros((Bt, G, 0, cache.v_dim), np.float32)
+        ns.alpha_pos, ns.alpha_valid = np.zeros((Bt, 0), np.int64), np.zeros((Bt, 0), bool)
+    return ns
+
+
+def assert_pack_equal(ka, va, ka_ref, va_ref, dk):
+    ka, va = to_np(ka), to_np(va)
+    assert ka.shape == ka_ref.shape and va.shape == va_ref.shape
+    np.testing.assert_array_equal(va, va_ref)
+    np.testing.assert_array_equal(np.delete(ka, dk, axis=-1), np.delete(ka_ref, dk, axis=-1))
+    bias, bias_ref = ka[..., dk], ka_ref[..., dk]
+    mag = np.abs(bias_ref.astype(np.float64))
+    ulp = np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 7), 0.0)
+    assert (np.abs(bias - bias_ref) <= ulp).all(), "log-mass column off by more than 1 bf16 ulp"
+
+
+def half_ulp_bf16(x):
+    mag = np.abs(x)
+    return np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 8), 0.0)
+
+
+def assert_attention_close(out, ref):
+    out = to_np(out).astype(np.float64)
+    err = (np.abs(out - ref) - half_ulp_bf16(ref)) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= ATOL, f"attention error beyond output rounding {err.max():.3e} > {ATOL}"
+
+
+def rand_bf16(g, *shape):
+    return torch.randn(*shape, generator=g).to(torch.bfloat16)
+
+
+def check_step(cache, cos, sin, q, k, v, scale, reuse=False, table_bf16=False):
+    state = state_of(cache)
+    ka_ref, va_ref = ro.pack(state, to_np(k), to_np(v), to_np(cos), to_np(sin), table_bf16=table_bf16)
+    dev = cache.level_k.device
+    with torch.no_grad():
+        out = log_kv_chunk_attention(cache, q.to(dev), k.to(dev), v.to(dev), scale, second_order_scale=0.0,
+                                     reuse_prefix=reuse)
+    ref = ro.attention(to_np(q), ka_ref, va_ref, scale, q.size(2), cache.v_dim)
+    assert_attention_close(out, ref)
+    return ka_ref, va_ref
+
+
+def test_plan_and_pack_after_flushes():
+    gpu, ora = make_pair(batch=2, groups=2, recent=64, flush=64, max_seq=2048)
+    mix = Mixture(2, 2, 128, 12, seed=5)
+    start = 0
+    for n in (64, 64, 64, 64, 64):
+        feed(gpu, ora, mix, start, n)
+        start += n
+    torch.cuda.synchronize()
+    plan = gpu._semantic_attention_plan()
+    idx, anchors, valid = ro.mid_plan(ora.level_count, ora.level_w, ora.level_sum_wp)
+    assert plan.width == idx.shape[-1]
+    ref_counts = ora.level_count.reshape(4, -1).sum(1)
+    assert to_np(plan.lane_counts()).tolist() == ref_counts.tolist()
+    g = torch.Generator().manual_seed(1)
+    k, v = rand_bf16(g, 2, 2, 3, 128), rand_bf16(g, 2, 2, 3, 128)
+    dim = packed_dim(128, 128)
+    ka, va = pack_mid_kv(gpu, plan, k.cuda(), v.cuda(), dim)
+    ka_ref, va_ref = ro.pack(ora, to_np(k), to_np(v), ora.cos, ora.sin)
+    assert_pack_equal(ka, va, ka_ref, va_ref, 128)
+
+
+def test_chunk_attention_after_flushes_alpha_beta():
+    gpu, ora = make_pair(batch=1, groups=2, recent=64, flush=64, max_seq=2048, exact=64, span=16,
+                         beta_novelty=True, beta_adaptive=True)
+    mix = Mixture(1, 2, 128, 12, seed=9)
+    start = 0
+    for n in (64,) * 6:
+        feed(gpu, ora, mix, start, n, with_ends=True)
+        start += n
+    assert ora.alpha_count > 0
+    g = torch.Generator().manual_seed(2)
+    q = rand_bf16(g, 1, 4, 2, 128)
+    k, v = rand_bf16(g, 1, 2, 2, 128), rand_bf16(g, 1, 2, 2, 128)
+    ka_ref, va_ref = ro.pack(ora, to_np(k), to_np(v), ora.cos, ora.sin)
+    with torch.no_grad():
+        out = log_kv_chunk_attention(gpu, q.cuda(), k.cuda(), v.cuda(), 128 ** -0.5, second_order_scale=0.0)
+    assert_attention_close(out, ro.attention(to_np(q), ka_ref, va_ref, 128 ** -0.5, 2, 128))
+    ka, va = pack_mid_kv(gpu, gpu._semantic_attention_plan(), k.cuda(), v.cuda(), packed_dim(128, 128))
+    assert_pack_equal(ka, va, ka_ref, va_ref, 128)
+
+
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16])
+def test_decode_reuse_synthetic_state(table_dtype):
+    """Decode steps with prefix reuse over a synthetic state (masses ~ U(1, 64)); each step
+    commits its token to the recent window, so the next one re-packs only new rows."""
+    dk = 128
+    cos, sin = rope_tables(4096, dk, dtype=table_dtype)
+    cache = LogStructuredKVCache(
+        (2, 4, 4096, dk), (2, 4, 4096, dk), B=32, recent_size=96, device="cuda", dtype=torch.bfloat16,
+        semantic_clusters=True, cluster_k_max=6, semantic_flush_granularity=32, semantic_anchor_mode="mid",
+        allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk, alpha_exact_tokens=32,
+        alpha_span_max_tokens=8)
+    fill_readout_state(cache, seed=3, recent=80)
+    g = torch.Generator().manual_seed(4)
+    scale = dk ** -0.5
+    for step in range(4):
+        q = rand_bf16(g, 2, 8, 1, dk)
+        k, v = rand_bf16(g, 2, 4, 1, dk), rand_bf16(g, 2, 4, 1, dk)
+        check_step(cache, cos, sin, q, k, v, scale, reuse=True, table_bf16=table_dtype == torch.bfloat16)
+        if step < 3:
+            pos = torch.full((2, 1), cache.token_count, dtype=torch.int64)
+            cache.add_recent(k.cuda(), v.cuda(), k_raw=k.cuda(), input_pos=pos.cuda(),
+                             span_ends=[[False], [False]])
+    assert cache._mid_decode_state is not None
+
+
+def test_decode_across_flush():
+    """Reuse is dropped when a flush rewrites the ladders."""
+    gpu, ora = make_pair(batch=1, groups=2, recent=32, flush=32, max_seq=1024)
+    mix = Mixture(1, 2, 128, 12, seed=11)
+    feed(gpu, ora, mix, 0, 32)
+    feed(gpu, ora, mix, 32, 31)
+    g = torch.Generator().manual_seed(5)
+    start = 63
+    for step in range(4):
+        q = rand_bf16(g, 1, 4, 1, 128)
+        k, v = rand_bf16(g, 1, 2, 1, 128), rand_bf16(g, 1, 2, 1, 128)
+        ka_ref, va_ref = ro.pack(ora, to_np(k), to_np(v), ora.cos, ora.sin)
+        with torch.no_grad():
+            out = log_kv_chunk_attention(gpu, q.cuda(), k.cuda(), v.cuda(), 0.1, second_order_scale=0.0,
+                                         reuse_prefix=True)
+        assert_attention_close(out, ro.attention(to_np(q), ka_ref, va_ref, 0.1, 1, 128))
+        feed(gpu, ora, mix, start, 1)
+        start += 1
+
+
+def test_decode_qwen_shape():
+    """Qwen3-1.7B GQA readout (16 query / 8 KV heads x 128) over a 32K-token cache layout:
+    recent 2048, exact pool 256, K=12 ladders; batch 2 to keep the oracle quick."""
+    dk = 128
+    cos, sin = rope_tables(32768, dk)
+    cache = LogStructuredKVCache(
+        (2, 8, 32768, dk), (2, 8, 32768, dk), B=128, recent_size=2048, device="cuda", dtype=torch.bfloat16,
+        semantic_clusters=True, cluster_k_max=12, semantic_flush_granularity=2048, semantic_anchor_mode="mid",
+        allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk, alpha_exact_tokens=256,
+        alpha_span_max_tokens=64)
+    fill_readout_state(cache, seed=7, fill=0.6)
+    g = torch.Generator().manual_seed(6)
+    q = rand_bf16(g, 2, 16, 1, dk)
+    k, v = rand_bf16(g, 2, 8, 1, dk), rand_bf16(g, 2, 8, 1, dk)
+    check_step(cache, cos, sin, q, k, v, dk ** -0.5, reuse=True)
+
+
+def test_causal_chunk():
+    """A multi-row chunk: row i sees the prefix and current rows 0..i only."""
+    dk = 64
+    cos, sin = rope_tables(1024, dk)
+    cache = LogStructuredKVCache(
+        (1, 2, 1024, dk), (1, 2, 1024, dk), B=16, recent_size=64, device="cuda", dtype=torch.bfloat16,
+        semantic_clusters=True, cluster_k_max=4, semantic_flush_granularity=16, semantic_anchor_mode="mid",
+        allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk)
+    fill_readout_state(cache, seed=8, recent=40)
+    g = torch.Generator().manual_seed(7)
+    q = rand_bf16(g, 1, 4, 8, dk)
+    k, v = rand_bf16(g, 1, 2, 8, dk), rand_bf16(g, 1, 2, 8, dk)
+    check_step(cache, cos, sin, q, k, v, dk ** -0.5)
