@@ -1,14 +1,26 @@
-"""Benchmark of the SemanticLogKV flush path on one MI355X.
+"""Benchmark of the SemanticLogKV flush path and its decode readout on one MI355X.
 
-A step is one flush of 2048 rows into every layer cache of a 28-layer
-Qwen3-1.7B-shaped KV stack (8 KV groups x 128, bf16, batch 1, K=12, B=128):
-attach route + per-ladder commit (merges, carries, centers). Rows are seeded
-synthetic Gaussian-mixture keys/values already resident in HBM. The caches are
-first warmed with two flushes; steps then continue the same 32K-token stream.
+Flush (the headline): a step is one flush of 2048 rows into every layer cache
+of a 28-layer Qwen3-1.7B-shaped KV stack (8 KV groups x 128, bf16, batch 1,
+K=12, B=128 with a 256-token Alpha exact pool and 64-token span cap, so
+B'=125 and L=7; Beta novelty scoring and the 4->2 split on): Alpha span
+scoring and choice, exact-pool partition, attach route of the archived rows,
+per-ladder commit (merges, carries, centers), then the mid-anchor plan and the
+pack of the new packed prefix that the next attention reads. Rows are seeded
+synthetic Gaussian-mixture keys/values already resident in HBM; span ends are
+seeded natural boundaries. The caches first take two untimed flushes; the
+steps continue the same 32K-token stream.
+
+Decode: one attention layer over a compressed 32K-token cache, batch 8,
+Qwen3-1.7B GQA (16 query / 8 KV heads x 128): recent window 2048, exact pool
+256, 12 clusters per lane with the ladder occupancy of 30,464 archived tokens,
+masses ~ U(1, 64). A step attends one new token per sequence with the packed
+prefix reused, as in the reference's decode loop.
 
 Prints one JSON line: flushed tokens/s over the timed steps, the roofline of
-the dominant kernel (the per-ladder commit) from HIP events on its stream, and
-the oracle's CPU throughput on a bounded sample of the same workload.
+the dominant kernel (the per-ladder commit) from HIP events on its stream over
+the timed region, decode ms/token with its own roofline, and the oracle's CPU
+throughput on a bounded sample of the flush workload.
 """
 
 from __future__ import annotations
@@ -16,7 +28,6 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -25,6 +36,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
+EXACT, SPAN = 256, 64
 
 
 def ladder_rows(counts, m, B, L):
@@ -85,7 +98,10 @@ def ladder_rows(counts, m, B, L):
 
 
 def commit_bytes(before_counts, before_alive, m_rows, B, L, dk, dv):
-    """Algorithmic HBM bytes of one commit launch, from the state before it and rows per ladder."""
+    """Algorithmic HBM bytes of one commit launch, from the state before it and rows per ladder.
+
+    Entry = K and V bf16 + w f32 + p_lo, p_hi, sum_wp, order i64 + pad flag;
+    token row = K and V bf16 + position i64; plus the center read and write."""
     import numpy as np
 
     entry = 2 * (dk + dv) + 4 + 4 * 8 + 1
@@ -98,75 +114,109 @@ def commit_bytes(before_counts, before_alive, m_rows, B, L, dk, dv):
             total += L * B * entry            # clear of the newly opened cluster
             counts = [0] * L
         rd, wr, tok = ladder_rows(counts, m, B, L)
-        total += (rd + wr) * entry + tok * token + 2 * dk * 4   # + center read and write
+        total += (rd + wr) * entry + tok * token + 2 * dk * 4
     return total
 
 
+def progress(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def span_ends_for(flush, rate=1 / 24, seed=99):
+    """Seeded natural span boundaries of the stream's flush ``flush`` (same for every layer)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed + flush)
+    return [(rng.random(F) < rate).tolist()]
+
+
 def cpu_baseline(seconds: float):
-    """Oracle (numpy restatement) flushes of one layer of the same workload on the host."""
+    """Oracle (numpy restatement) of the same flush for one layer on the host: Alpha/Beta, route,
+    commit and the pack of the new prefix."""
     import numpy as np
     import torch
 
-    from logkv_amd.workloads import Mixture
+    from logkv_amd.workloads import Mixture, rope_tables
     from oracle import OracleCache
 
     torch.set_num_threads(1)
-    mix = Mixture(1, 8, 128, clusters=12, seed=1)
-    rows = lambda: mix.rows(2048).float().numpy()  # noqa: E731
+    cos, sin = (t.numpy() for t in rope_tables(N, D))
+    mix = Mixture(1, G, D, clusters=K, seed=1)
+    rows = lambda: mix.rows(F).float().numpy()  # noqa: E731
     n, t, streams = 0, 0.0, 0
     while t < seconds:
         # One 32K-token stream per cache: two untimed warm-up flushes, then flushes 3..16.
-        ora = OracleCache(1, 8, 32768, 128, 128, B=128, recent_size=2048, K=12, s_h=64.0, flush=2048)
+        ora = OracleCache(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, exact_tokens=EXACT,
+                          span_max=SPAN, beta_novelty=True, beta_adaptive=True, cos=cos, sin=sin)
         streams += 1
         for j in range(16):
             k, v = rows(), rows()
-            pos = np.arange(j * 2048, (j + 1) * 2048)[None]
+            pos = np.arange(j * F, (j + 1) * F)[None]
             t0 = time.perf_counter()
-            ora.flush_rows(k, v, pos)
+            ora.flush_rows(k, v, pos, span_ends_for(j))
+            ora.pack(None, None)
             if j >= 2:
                 t += time.perf_counter() - t0
                 n += 1
             if t >= seconds:
                 break
-    return {"value": 2048 * n / t, "unit": "flushed tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle (numpy) route+commit of {n} flushes (flushes 3..16 of {streams} 32K-token streams) "
-                      f"of one layer, batch 1, 8 groups x 128, K=12, B=128, 2048 rows each, {t:.1f} s, 1 thread"}
+    return {"value": F * n / t, "unit": "flushed tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle (numpy) Alpha/Beta + route + commit + pack of {n} flushes (flushes 3..16 of "
+                      f"{streams} 32K-token streams) of one layer, batch 1, 8 groups x 128, K=12, B=128, "
+                      f"exact pool 256, {F} rows each, {t:.1f} s, 1 thread"}
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--layers", type=int, default=28)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box here has one MI355X, --gpus {args.gpus} is not run",
-              file=sys.stderr)
-        sys.exit(2)
-    if 2 + args.warmup + args.steps > 16:
-        print("warmup + steps must fit the 32K-token stream: at most 14 flushes after the two warm-up flushes",
-              file=sys.stderr)
-        sys.exit(2)
+class CommitMeter:
+    """Wraps a cache's route+commit so the commit launch is bracketed by HIP events on its
+    stream, with the ladder counts it starts from copied aside on the device (no host sync);
+    algorithmic bytes are computed from those copies after the timed region."""
 
-    import numpy as np
-    import torch
+    def __init__(self, cache, torch):
+        self.cache, self.torch = cache, torch
+        self.records = []
 
+    def __call__(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None):
+        from logkv_amd._lib import check, lib, ptr, stream_of
+
+        cache, torch = self.cache, self.torch
+        snap = (cache.level_count.clone(), cache.alive.clone(), cache.n_total.clone())
+        view = cache._ladder_view()
+        rows = cache._rows_view(k_raw, v, positions, counts)
+        ws = cache._workspace_for(view, rows.tokens)
+        sp = stream_of(k_raw.device)
+        stream = torch.cuda.current_stream(k_raw.device)
+        check(lib().logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
+                                        ptr(assign_out), ptr(order_out), sp), "attach")
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(stream)
+        check(lib().logkv_commit_only(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
+                                      ptr(assign_out), ptr(order_out), sp), "commit")
+        ev[1].record(stream)
+        self.records.append((snap, cache.n_total.clone(), ev))
+
+    def results(self, B_, L_):
+        out = []
+        for (counts, alive, n0), n1, ev in self.records:
+            m = (n1.long() - n0.long()).cpu().numpy()
+            out.append((commit_bytes(counts.long().cpu().numpy(), alive.cpu().numpy(), m, B_, L_, D, D),
+                        ev[0].elapsed_time(ev[1])))
+        return out
+
+
+def flush_workload(args, torch, np):
     from logkv_amd import LogStructuredKVCache
-    from logkv_amd._lib import check, lib, ptr, stream_of
+    from logkv_amd.log_kv_pack import _decode_capacity, _launch_pack, packed_dim, readout_view
     from logkv_amd.workloads import rope_tables
 
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
     layers = args.layers
     cos, sin = rope_tables(N, D)
     caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev,
                                    dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
                                    semantic_flush_granularity=F, semantic_anchor_mode="mid",
-                                   allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D)
+                                   allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                   alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                   beta_adaptive_merge=True)
               for _ in range(layers)]
     n_flush = 2 + args.warmup + args.steps
     gen = torch.Generator(device=dev).manual_seed(1234)
@@ -181,103 +231,185 @@ def main():
 
     data = [[(mixture(li), mixture(li)) for li in range(layers)] for _ in range(n_flush)]
     positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).contiguous() for j in range(n_flush)]
+    positions_host = [[list(range(j * F, (j + 1) * F))] for j in range(n_flush)]
+    ends = [span_ends_for(j) for j in range(n_flush)]
+    dim = packed_dim(D, D)
+    empty = torch.empty(1, G, 0, D, dtype=torch.bfloat16, device=dev)
+    workspaces = [(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev),
+                   torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev)) for c in caches]
     torch.cuda.synchronize()
 
-    # Per-layer C views and workspaces, built once (the timed loop only launches).
-    prepared = []
-    for j in range(n_flush):
-        row = []
+    def flush(j):
         for li, cache in enumerate(caches):
             k, v = data[j][li]
-            view = cache._ladder_view()
-            rows = cache._rows_view(k, v, positions[j])
-            ws = cache._workspace_for(view, F)
-            row.append((view, rows, ws))
-        prepared.append(row)
-    L_ = lib()
-    stream = torch.cuda.current_stream(dev)
-    sp = stream_of(dev)
+            cache.route_and_flush_batch(k, v, positions[j], positions_host=positions_host[j], span_ends=ends[j])
+            # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
+            view = readout_view(cache)
+            plan = cache._semantic_attention_plan()
+            _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
 
-    def flush(j, events=None):
-        for li, cache in enumerate(caches):
-            view, rows, ws = prepared[j][li]
-            if events is None:
-                check(L_.logkv_route_commit(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws),
-                                            ws.numel(), None, None, sp), "route_commit")
-            else:
-                check(L_.logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws),
-                                             ws.numel(), None, None, sp), "attach")
-                events[li][0].record(stream)
-                check(L_.logkv_commit_only(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws),
-                                           ws.numel(), None, None, sp), "commit")
-                events[li][1].record(stream)
-
-    for j in range(2):
+    for j in range(2 + args.warmup):
         flush(j)
     torch.cuda.synchronize()
+    progress(f"flush: {2 + args.warmup} untimed flushes done")
 
-    # Warm-up flushes double as the roofline accounting: per layer, the commit
-    # launch is bracketed by HIP events on its stream and its algorithmic bytes
-    # come from the count model over the state just before it.
-    acc_bytes, acc_ms = [], []
-    for j in range(2, 2 + args.warmup):
-        for li, cache in enumerate(caches):
-            before = (cache.level_count.long().cpu().numpy(), cache.alive.cpu().numpy(),
-                      cache.n_total.long().cpu().numpy())
-            view, rows, ws = prepared[j][li]
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            check(L_.logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws),
-                                         ws.numel(), None, None, sp), "attach")
-            ev[0].record(stream)
-            check(L_.logkv_commit_only(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws),
-                                       ws.numel(), None, None, sp), "commit")
-            ev[1].record(stream)
-            torch.cuda.synchronize()
-            m = cache.n_total.long().cpu().numpy() - before[2]
-            acc_bytes.append(commit_bytes(before[0], before[1], m, B, cache.L_alloc, D, D))
-            acc_ms.append(ev[0].elapsed_time(ev[1]))
-    torch.cuda.synchronize()
-
-    events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in caches] for _ in range(args.steps)]
+    meters = [CommitMeter(c, torch) for c in caches]
+    for c, m in zip(caches, meters):
+        c._route_commit = m
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        flush(2 + args.warmup + s, events[s])
+        flush(2 + args.warmup + s)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    timed_commit_ms = float(np.mean([events[s][li][0].elapsed_time(events[s][li][1])
-                                     for s in range(args.steps) for li in range(layers)]))
-    avg_bytes = float(np.mean(acc_bytes)) if acc_bytes else 0.0
-    avg_ms = float(np.mean(acc_ms)) if acc_ms else float("nan")
-    achieved = float(np.mean([b / (t * 1e-3) / 1e9 for b, t in zip(acc_bytes, acc_ms)])) if acc_bytes else 0.0
-
+    for c in caches:
+        del c._route_commit
+    progress(f"flush: {args.steps} timed flushes in {elapsed:.3f} s")
+    rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
+    launch_bytes = float(np.mean([b for b, _ in rec]))
+    launch_ms = float(np.mean([t for _, t in rec]))
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     tokens = F * layers * args.steps
+    widths = [int(c._semantic_attention_plan().width) for c in caches[:1]]
+    return {
+        "value": tokens / elapsed,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "config": {"workload": f"{layers}-layer flush, Qwen3-1.7B KV shape (8x128 bf16), batch 1, flush {F}, "
+                               f"K=12, B=128, Alpha exact pool {EXACT} / span cap {SPAN}, Beta novelty + 4->2 "
+                               "split, attach route, mid-anchor plan + pack",
+                   "layers": layers, "flush": F, "batch": 1, "kv_groups": G, "head_dim": D, "clusters": K,
+                   "slots_per_level": caches[0].B_prime, "levels": caches[0].L_alloc, "exact_tokens": EXACT,
+                   "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
+                   "pooled_width_after_last_flush": widths[0]},
+        "roofline": {"kernel": "commit_kernel", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
+                     "launches": len(rec)},
+    }
+
+
+def decode_workload(args, torch, np):
+    from logkv_amd import LogStructuredKVCache
+    from logkv_amd.log_kv_pack import _launch_pack, packed_attention, packed_dim, readout_view
+    from logkv_amd.workloads import fill_readout_state, rope_tables
+
+    dev = torch.device("cuda", 0)
+    Bt, HQ = 8, 16
+    cos, sin = rope_tables(N, D)
+    cache = LogStructuredKVCache((Bt, G, N, D), (Bt, G, N, D), B=B, recent_size=F, device=dev,
+                                 dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
+                                 semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                 allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                 alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                 beta_adaptive_merge=True)
+    archived = N - F - EXACT
+    fill_readout_state(cache, seed=21, recent=F, archived=archived)
+    steps, warm = args.decode_steps, 8
+    gen = torch.Generator(device=dev).manual_seed(77)
+    qs = torch.randn(steps + warm, Bt, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    ks = torch.randn(steps + warm, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    vs = torch.randn(steps + warm, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    dim = packed_dim(D, D)
+    scale = D ** -0.5
+    view = readout_view(cache)
+    plan = cache._semantic_attention_plan()
+    cap = cache.K_max * cache.L_alloc * cache.B_prime + EXACT + cache.recent_capacity + 2
+    ka = torch.empty(Bt, G, cap, dim, dtype=torch.bfloat16, device=dev)
+    va = torch.empty_like(ka)
+    # Packed prefix once (the first decode step after a flush), then one new row per step.
+    _launch_pack(cache, view, plan, ks[0], vs[0], dim, ka, va, False, 0)
+    tail = cache.alpha_count + cache.recent_count + 1
+    stream = torch.cuda.current_stream(dev)
+    workspace = None
+    events = []
+
+    def step(i, timed):
+        nonlocal workspace
+        _launch_pack(cache, view, plan, ks[i], vs[i], dim, ka, va, True, cache.alpha_count + cache.recent_count)
+        if timed:
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record(stream)
+        _, workspace = packed_attention(qs[i], ka, va, plan, tail, scale, 1, D, G, workspace)
+        if timed:
+            ev[1].record(stream)
+            events.append(ev)
+
+    for i in range(warm):
+        step(i, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(warm + i, True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    progress(f"decode: {steps} steps in {elapsed:.3f} s")
+    attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
+    width = plan.width
+    rows = width + tail
+    lanes = Bt * G
+    # Algorithmic bytes: every packed K and V row of every lane once, queries and outputs.
+    attn_bytes = lanes * rows * dim * 2 * 2 + Bt * HQ * D * 2 * 2
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    ms = elapsed / steps * 1e3
+    return {
+        "workload": "decode attention, one layer, batch 8, Qwen3-1.7B GQA (16 q / 8 KV heads x 128, bf16), "
+                    f"32K-token cache: recent {F}, exact pool {EXACT}, 12 clusters holding {archived} archived "
+                    "tokens per lane, masses ~ U(1,64); packed prefix reused, one new row per step",
+        "ms_per_token": ms, "ms_per_token_28_layers": 28 * ms, "steps": steps,
+        "packed_rows_per_lane": rows, "pooled_width": width,
+        "roofline": {"kernel": "decode_kernel + combine_kernel", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": attn_ms},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box here has one MI355X, --gpus {args.gpus} is not run",
+              file=sys.stderr)
+        sys.exit(2)
+    if 2 + args.warmup + args.steps > 16:
+        print("warmup + steps must fit the 32K-token stream: at most 14 flushes after the two warm-up flushes",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    torch.cuda.set_device(0)
+    fl = flush_workload(args, torch, np)
     result = {
         "metric": "flushed tokens/s (route+merge+pack) & decode ms/token at 32K ctx, 1 GPU",
-        "value": tokens / elapsed,
+        "value": fl["value"],
         "unit": "flushed tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": elapsed / args.steps * 1e3,
+        "ms_per_step": fl["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 storage, f32 math",
-        "data": "synthetic seeded Gaussian mixture (12 centers N(0,1)*4, noise 0.5, 10% outliers N(0,1)*12)",
-        "config": {"workload": f"{layers}-layer flush, Qwen3-1.7B KV shape (8x128 bf16), batch 1, flush 2048, "
-                               f"K=12, B=128, attach route; Alpha/Beta off",
-                   "layers": layers, "flush": F, "batch": 1, "kv_groups": G, "head_dim": D, "clusters": K,
-                   "slots_per_level": caches[0].B_prime, "levels": caches[0].L_alloc,
-                   "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}"},
-        "roofline": {"kernel": "commit_kernel", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes_per_launch": avg_bytes, "avg_launch_ms": avg_ms,
-                     "accounting": f"{len(acc_ms)} commit launches of the warm-up flushes",
-                     "timed_avg_launch_ms": timed_commit_ms},
-        "decode_ms_per_token": None,
+        "data": "synthetic seeded Gaussian mixture (12 centers N(0,1)*4, noise 0.5, 10% outliers N(0,1)*12), "
+                "seeded span ends (rate 1/24)",
+        "config": fl["config"],
+        "roofline": fl["roofline"],
     }
+    if not args.no_decode:
+        result["decode"] = decode_workload(args, torch, np)
+        result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
     if not args.no_cpu_baseline:
+        progress("cpu baseline: oracle flushes on the host")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

@@ -58,7 +58,7 @@ __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, 
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
       const int d = l + j * kWave;
-      x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+      x[j] = feat_or_zero(row, d, D);
       sq[j] = x[j] * x[j];
       acc[j] = i == 0 ? x[j] : acc[j] + x[j];
     }
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_ar
 #pragma unroll
         for (int j = 0; j < kJ; ++j) {
           const int d = l + j * kWave;
-          const float m = (j < J && d < a.dk) ? mu[c * a.dk + d] : 0.f;
+          const float m = feat_or_zero(mu + c * a.dk, d, a.dk);
           dt[j] = mean_k[j] * m;
           cc[j] = m * m;
         }

@@ -60,6 +60,34 @@ __device__ __forceinline__ float wave_tree(float s) {
   return s;
 }
 
+// Element d of a row as float, 0 for d >= D (D >= 1). The load is issued
+// unconditionally with the index clamped into the row, so it needs no branch
+// that would wait on it.
+__device__ __forceinline__ float feat_or_zero(const LOGKV_G uint16_t* row, int d, int D) {
+  const float x = bf16_to_f32(row[d < D ? d : D - 1]);
+  return d < D ? x : 0.f;
+}
+
+__device__ __forceinline__ float feat_or_zero(const LOGKV_G float* row, int d, int D) {
+  const float x = row[d < D ? d : D - 1];
+  return d < D ? x : 0.f;
+}
+
+// The same sum as wave_tree (offsets 32, 16, 8, 4, 2, 1; lane l adds lane
+// l + offset, which is what lane 0 of the xor butterfly adds), formed toward
+// lane 0 with the gfx950 permlane swaps (lanes 0-31 read 32-63, rows 0/2 read
+// rows 1/3) and DPP row shifts (lane l reads l + n within its 16-lane row),
+// then read from lane 0. Every lane of the wave must be active.
+__device__ __forceinline__ float wave_sum0(float s) {
+  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x108, 0xf, 0xf, false));  // row_shl:8
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x104, 0xf, 0xf, false));  // row_shl:4
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, false));  // row_shl:2
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x101, 0xf, 0xf, false));  // row_shl:1
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 

@@ -12,6 +12,8 @@
 // (top fold), :5217-5312 + litgpt/log_kv_position.py:13-30 (pair merge),
 // litgpt/beta_log_kv.py:29-105 (Beta), :2268-2298 (new cluster),
 // :4116-4175 + :4326-4359 (joins and centers), :3690-3788 (delayed archive).
+#include <algorithm>
+
 #include "route.hpp"
 
 namespace logkv {
@@ -160,18 +162,30 @@ struct PoolT {
         KIND == 1 ? src.buf.v + staged_row(q) * L.dv : src.vb + staged_row(q) * src.v_st;
     return st ? L.v + (base + p) * L.dv : staged;
   }
+  // Branch-free: every load is issued (a stored slot index clamps to slot 0,
+  // a staged index to row 0) and the value is selected afterwards.
   __device__ __forceinline__ float w(int p) const {
-    if (KIND == 0) return p < cnt ? L.w[base + p] : 1.0f;
     const bool st = p < cnt;
+    if (KIND == 0) {
+      const float stored = L.w[base + (st ? p : 0)];
+      return st ? stored : 1.0f;
+    }
     const LOGKV_G float* wp = st ? L.w + base + p : src.buf.w + (p - cnt);
     return *wp;
   }
   __device__ __forceinline__ Meta meta(int p) const {
-    if (p < cnt) return slot_meta(L, base + p);
-    if (KIND == 1) return soa_meta(src.buf, p - cnt);
-    const int q = p - cnt;
+    const bool st = p < cnt;
+    const int64_t i = st ? base + p : 0;
+    if (KIND == 1) {
+      const int64_t j = st ? 0 : p - cnt;
+      return Meta{*(st ? L.w + i : src.buf.w + j), *(st ? L.lo + i : src.buf.lo + j),
+                  *(st ? L.hi + i : src.buf.hi + j), *(st ? L.swp + i : src.buf.swp + j),
+                  *(st ? L.ord + i : src.buf.ord + j), *(st ? L.pad + i : src.buf.pad + j)};
+    }
+    const int q = st ? 0 : p - cnt;
     const int64_t pos = src.posb[src.tok[q]];
-    return Meta{1.0f, pos, pos, pos, src.order_base + q, 0};
+    const Meta stored = slot_meta(L, st ? i : base);
+    return st ? stored : Meta{1.0f, pos, pos, pos, src.order_base + q, 0};
   }
 };
 
@@ -316,13 +330,14 @@ __device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa&
 
 // ---- Beta 4->2 -------------------------------------------------------------
 
-// Canonical sum over the features held as t[j] (feature l + 64 j) in every lane.
+// Canonical sum over the features held as t[j] (feature l + 64 j) in every
+// lane; called with the whole wave active.
 template <int NJ>
 __device__ __forceinline__ float feat_sum(const float* t) {
   float s = t[0];
 #pragma unroll
   for (int j = 1; j < NJ; ++j) s = s + t[j];
-  return wave_tree(s);
+  return wave_sum0(s);
 }
 
 // sum_i w_i |x_i - mean|^2 over rows of one side; rows outside the side add +0.
@@ -391,79 +406,157 @@ __device__ __forceinline__ void beta_component_cost(const float (&x)[4][NJ], con
   }
 }
 
+// Quad (4-lane) butterfly exchanges: lane i reads lane i ^ 1 / i ^ 2 of its quad.
+constexpr int kQuadXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+
+template <int CTRL>
+__device__ __forceinline__ int64_t quad_xor64(int64_t x) {
+  const int lo = __builtin_amdgcn_mov_dpp(static_cast<int>(x & 0xffffffff), CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_mov_dpp(static_cast<int>(x >> 32), CTRL, 0xf, 0xf, false);
+  return (static_cast<int64_t>(hi) << 32) | static_cast<int64_t>(static_cast<uint32_t>(lo));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int quad_xor32(int x) {
+  return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
+}
+
+// Metadata of a merged side from lanes 0..3 of the wave, lane i holding row i
+// of the group (litgpt/beta_log_kv.py:86-105, litgpt/log_kv_position.py:13-30):
+// p_lo / p_hi over rows with w > 0, sums of w*p, smallest order, all-padding.
+// Integer reductions, so the lane order does not matter. Valid in lane 0.
+__device__ __forceinline__ Meta side_meta(const Meta& mine, bool member, float mass) {
+  const bool live = member && mine.w > 0.f;
+  int64_t lo = live ? mine.lo : INT64_MAX;
+  int64_t hi = live ? mine.hi : INT64_MIN;
+  int64_t swp = member ? mine.swp : 0;
+  int64_t ord = member ? mine.ord : INT64_MAX;
+  int pad = member ? mine.pad : 1;
+  lo = imin64(lo, quad_xor64<kQuadXor1>(lo));
+  hi = imax64(hi, quad_xor64<kQuadXor1>(hi));
+  swp = swp + quad_xor64<kQuadXor1>(swp);
+  ord = imin64(ord, quad_xor64<kQuadXor1>(ord));
+  pad = pad & quad_xor32<kQuadXor1>(pad);
+  lo = imin64(lo, quad_xor64<kQuadXor2>(lo));
+  hi = imax64(hi, quad_xor64<kQuadXor2>(hi));
+  swp = swp + quad_xor64<kQuadXor2>(swp);
+  ord = imin64(ord, quad_xor64<kQuadXor2>(ord));
+  pad = pad & quad_xor32<kQuadXor2>(pad);
+  Meta r;
+  r.w = mass;
+  r.lo = mass > 0.f ? lo : 0;
+  r.hi = mass > 0.f ? hi : 0;
+  r.swp = swp;
+  r.ord = ord;
+  r.pad = static_cast<uint8_t>(pad);
+  return r;
+}
+
+// Beta groups are staged in LDS a chunk at a time: the K|V rows and metadata
+// of up to beta_chunk_groups() groups of four, loaded by the whole block with
+// many rows in flight, then one wave per group computes from LDS.
+constexpr int kBetaStageBytes = 64 * 1024;
+
+__host__ __device__ inline int beta_chunk_groups(int dk, int dv) {
+  const int g = kBetaStageBytes / (4 * (dk + dv) * 2);
+  return g < kWaves ? kWaves : (g > 64 ? 64 : g);
+}
+
+__host__ __device__ inline int64_t beta_stage_bytes(int dk, int dv) {
+  const int64_t rows = 4 * static_cast<int64_t>(beta_chunk_groups(dk, dv));
+  return align16(rows * (dk + dv) * 2) + rows * static_cast<int64_t>(sizeof(Meta));
+}
+
 // One wave per group of four carry inputs (litgpt/beta_log_kv.py:29-105).
-// Features l + 64 j (j < NJ) of every row live in lane l.
+// Features l + 64 j (j < NJ) of every row live in lane l; lane i < 4 also
+// holds row i's metadata. `stage` is LDS of beta_stage_bytes(dk, dv).
 template <int NJ, int KIND>
-__device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa& out, int n_pair, int dk, int dv) {
+__device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa& out, int n_pair, int dk, int dv,
+                                             uint8_t* stage) {
   const int l = lane_id(), w = wave_id();
   const int n_groups = (n_pair + 3) / 4;
-  for (int gi = w; gi < n_groups; gi += kWaves) {
-    const int start = 4 * gi;
-    const int width = min(4, n_pair - start);
-    float xk[4][NJ], xv[4][NJ], wr[4];
+  const int cg = beta_chunk_groups(dk, dv);
+  LOGKV_S uint16_t* sk = (LOGKV_S uint16_t*)stage;
+  LOGKV_S uint16_t* sv = sk + 4 * cg * dk;
+  LOGKV_S Meta* sm = (LOGKV_S Meta*)(stage + align16(4 * static_cast<int64_t>(cg) * (dk + dv) * 2));
+  const RowUnits ru(dk, dv);
+  for (int g0 = 0; g0 < n_groups; g0 += cg) {
+    const int ng = min(cg, n_groups - g0);
+    const int p0 = 4 * g0;
+    const int rows = min(4 * ng, n_pair - p0);
+    __syncthreads();   // the previous chunk is done with the stage
+    for (int r0 = ru.r0; r0 < rows; r0 += kBatch * ru.step) {
+      uint2 x[kBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool valid = i < width;
-      wr[i] = valid ? pool.w(start + i) : 0.f;
-      const LOGKV_G uint16_t* kr = pool.k(valid ? start + i : start);
-      const LOGKV_G uint16_t* vr = pool.v(valid ? start + i : start);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = l + j * kWave;
-        xk[i][j] = (valid && d < dk) ? bf16_to_f32(kr[d]) : 0.f;
-        xv[i][j] = (valid && d < dv) ? bf16_to_f32(vr[d]) : 0.f;
+      for (int q = 0; q < kBatch; ++q) {
+        const int r = r0 + q * ru.step;
+        if (r < rows) x[q] = load_unit(pool.k(p0 + r), pool.v(p0 + r), ru.u, ru.ku);
       }
-    }
-    int cut = 1;
-    if (width == 4) {
-      const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
-      float costs[3] = {0.f, 0.f, 0.f};
-      beta_component_cost<NJ>(xk, wr, total, dk, costs);
-      beta_component_cost<NJ>(xv, wr, total, dv, costs);
-      int best = 0;
-      if (costs[1] < costs[best]) best = 1;
-      if (costs[2] < costs[best]) best = 2;
-      cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
-    }
-    const int dest = start / 2;
-    for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
-      unsigned member;
-      if (width == 2) member = 0x3u;
-      else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
-      float wt[4], mk[NJ], mv[NJ], mass;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-      side_mean<NJ>(xk, wt, mk, mass);
-      side_mean<NJ>(xv, wt, mv, mass);
-      const int64_t o = dest + side;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = l + j * kWave;
-        if (d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
-        if (d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
-      }
-      if (l == 0) {
-        Meta r;
-        r.w = mass;
-        int64_t lo = INT64_MAX, hi = INT64_MIN, swp = 0, ord = INT64_MAX;
-        uint8_t pad = 1;
-        for (int i = 0; i < width; ++i) {
-          if (!((member >> i) & 1u)) continue;
-          const Meta mi = pool.meta(start + i);
-          if (mi.w > 0.f) {
-            lo = imin64(lo, mi.lo);
-            hi = imax64(hi, mi.hi);
-          }
-          swp += mi.swp;
-          ord = imin64(ord, mi.ord);
-          pad &= mi.pad;
+      for (int q = 0; q < kBatch; ++q) {
+        const int r = r0 + q * ru.step;
+        if (r < rows) {
+          LOGKV_S uint16_t* dst = ru.u < ru.ku ? sk + r * dk + 4 * ru.u : sv + r * dv + 4 * (ru.u - ru.ku);
+          *(LOGKV_S uint2*)dst = x[q];
         }
-        r.lo = mass > 0.f ? lo : 0;
-        r.hi = mass > 0.f ? hi : 0;
-        r.swp = swp;
-        r.ord = ord;
-        r.pad = pad;
-        put_soa_meta(out, o, r);
+      }
+    }
+    for (int r = threadIdx.x; r < rows; r += kThreads) sm[r] = pool.meta(p0 + r);
+    __syncthreads();
+    for (int gl = w; gl < ng; gl += kWaves) {
+      const int start = p0 + 4 * gl;
+      const int width = min(4, n_pair - start);
+      const int rl = 4 * gl;
+      float xk[4][NJ], xv[4][NJ], wr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = i < width;
+        const int row = rl + (valid ? i : 0);
+        const float wi = sm[row].w;
+        wr[i] = valid ? wi : 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = l + j * kWave;
+          const float a = bf16_to_f32(sk[row * dk + (d < dk ? d : dk - 1)]);
+          const float b = bf16_to_f32(sv[row * dv + (d < dv ? d : dv - 1)]);
+          xk[i][j] = (valid && d < dk) ? a : 0.f;
+          xv[i][j] = (valid && d < dv) ? b : 0.f;
+        }
+      }
+      const Meta ml = sm[rl + (l & 3)];
+      const Meta mine = l < width ? ml : Meta{};
+      int cut = 1;
+      if (width == 4) {
+        const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
+        float costs[3] = {0.f, 0.f, 0.f};
+        beta_component_cost<NJ>(xk, wr, total, dk, costs);
+        beta_component_cost<NJ>(xv, wr, total, dv, costs);
+        int best = 0;
+        if (costs[1] < costs[best]) best = 1;
+        if (costs[2] < costs[best]) best = 2;
+        cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
+      }
+      const int dest = start / 2;
+      for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
+        unsigned member;
+        if (width == 2) member = 0x3u;
+        else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
+        float wt[4], mk[NJ], mv[NJ], mass;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
+        side_mean<NJ>(xk, wt, mk, mass);
+        side_mean<NJ>(xv, wt, mv, mass);
+        const int64_t o = dest + side;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = l + j * kWave;
+          if (d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
+          if (d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
+        }
+        const bool in_side = l < width && ((member >> (l & 3)) & 1u);
+        const Meta r = side_meta(mine, in_side, mass);
+        if (l == 0) put_soa_meta(out, o, r);
       }
     }
   }
@@ -522,7 +615,7 @@ __device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
 // Returns the number of carries written to `out` (0 ends the append).
 template <int KIND>
 __device__ __forceinline__ int level_step(const Ladder& L, int16_t* counts_s, int ell, bool top, const Src& cur, int m,
-                                          const Soa& out, bool beta) {
+                                          const Soa& out, bool beta, uint8_t* stage) {
   // Barriers: move_rows' load/store barrier is the only one a level needs. It
   // orders this level's carry stores before the next level reads them, and
   // every read of this level's staged source before the next level overwrites
@@ -547,8 +640,8 @@ __device__ __forceinline__ int level_step(const Ladder& L, int16_t* counts_s, in
   const int n_carry = (mr + 1) / 2, n_pair = 2 * n_carry;
   const int n_surv = n_pool - n_pair;   // >= B' - 1 >= 1, so move_rows always runs its barrier
   if (beta) {
-    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv);
-    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv);
+    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv, stage);
+    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv, stage);
   } else {
     pair_carries<KIND>(pool, out, n_carry, L.dk, L.dv);
   }
@@ -560,14 +653,14 @@ __device__ __forceinline__ int level_step(const Ladder& L, int16_t* counts_s, in
 
 // Fenwick append of m0 staged rows from `src0` into one ladder, level by level.
 __device__ __forceinline__ void fenwick_append(const Ladder& L, int16_t* counts_s, int levels, Src src0, int m0, Soa bufA, Soa bufB,
-                               bool beta) {
-  int m = src0.kind == 1 ? level_step<1>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta)
-                         : level_step<0>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta);
+                               bool beta, uint8_t* stage) {
+  int m = src0.kind == 1 ? level_step<1>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta, stage)
+                         : level_step<0>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta, stage);
   Src cur{};
   cur.kind = 1;
   for (int ell = 1; ell < levels && m > 0; ++ell) {
     cur.buf = (ell & 1) ? bufA : bufB;   // carries written by the previous level
-    m = level_step<1>(L, counts_s, ell, ell == levels - 1, cur, m, (ell & 1) ? bufB : bufA, beta);
+    m = level_step<1>(L, counts_s, ell, ell == levels - 1, cur, m, (ell & 1) ? bufB : bufA, beta, stage);
   }
 }
 
@@ -794,25 +887,39 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
           __syncthreads();
         }
       }
-      // Gather row rank -> S0[rank].
-      const int ku = dk / 4, units = (dk + dv) / 4;
-      for (int i = threadIdx.x; i < total * units; i += kThreads) {
-        const int rank = i / units, u = i - (i / units) * units;
-        const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
-        const LOGKV_G uint16_t *ks, *vs;
-        if (q < n_exist) {
-          int e = 0;
-          while (e + 1 < L && level_start[e + 1] <= q) ++e;
-          const int64_t slot = static_cast<int64_t>(e) * B + (q - level_start[e]);
-          ks = lad.k + slot * dk;
-          vs = lad.v + slot * dv;
-        } else {
-          const int t = tok[first + q - n_exist];
-          ks = kb + static_cast<int64_t>(t) * r.k_st;
-          vs = vb + static_cast<int64_t>(t) * r.v_st;
+      // Gather row rank -> S0[rank], kBatch rows per thread loaded before any store.
+      {
+        const RowUnits ru(dk, dv);
+        for (int r0 = ru.r0; r0 < total; r0 += kBatch * ru.step) {
+          uint2 x[kBatch];
+#pragma unroll
+          for (int qb = 0; qb < kBatch; ++qb) {
+            const int rank = r0 + qb * ru.step;
+            if (rank < total) {
+              const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
+              const LOGKV_G uint16_t *ks, *vs;
+              if (q < n_exist) {
+                int e = 0;
+                while (e + 1 < L && level_start[e + 1] <= q) ++e;
+                const int64_t slot = static_cast<int64_t>(e) * B + (q - level_start[e]);
+                ks = lad.k + slot * dk;
+                vs = lad.v + slot * dv;
+              } else {
+                const int t = tok[first + q - n_exist];
+                ks = kb + static_cast<int64_t>(t) * r.k_st;
+                vs = vb + static_cast<int64_t>(t) * r.v_st;
+              }
+              x[qb] = load_unit(ks, vs, ru.u, ru.ku);
+            }
+          }
+#pragma unroll
+          for (int qb = 0; qb < kBatch; ++qb) {
+            const int rank = r0 + qb * ru.step;
+            if (rank < total)
+              store_unit(S0.k + static_cast<int64_t>(rank) * dk, S0.v + static_cast<int64_t>(rank) * dv, ru.u, ru.ku,
+                         x[qb]);
+          }
         }
-        store_unit(S0.k + static_cast<int64_t>(rank) * dk, S0.v + static_cast<int64_t>(rank) * dv, u, ku,
-                   load_unit(ks, vs, u, ku));
       }
       for (int rank = threadIdx.x; rank < total; rank += kThreads) {
         const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
@@ -828,9 +935,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
         mt.ord = rank;
         put_soa_meta(S0, rank, mt);
       }
-      int64_t hi = p_hi;
-      for (int i = first; i < m; ++i) hi = imax64(hi, posb[tok[i]]);
-      p_hi = hi;
+      p_hi = imax64(p_hi, last_pos);   // rows are in position order
       phase = total;
       __syncthreads();
       clear_slots(lad, 0, static_cast<int64_t>(L) * B);
@@ -842,7 +947,9 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     }
     n_total += nn;
     __syncthreads();
-    fenwick_append(lad, counts_s, L, src, m0, bufA, bufB, prm.beta_merge != 0);
+    // The Beta stage reuses the LDS after the compacted rows (center staging
+    // belongs to the sibling block; the sort keys are dead by now).
+    fenwick_append(lad, counts_s, L, src, m0, bufA, bufB, prm.beta_merge != 0, dyn + c_stage_off);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < L; e += kThreads) c.level_count[cl * L + e] = counts_s[e];
@@ -857,8 +964,10 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
-  size_t shmem = ((2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15)) + static_cast<size_t>(kCenterRows) * c.dk * 2;
-  if (p.late_joins) shmem += static_cast<size_t>(ws.sort_width) * 8;
+  size_t region = static_cast<size_t>(kCenterRows) * c.dk * 2;
+  if (p.late_joins) region += static_cast<size_t>(ws.sort_width) * 8;
+  if (p.beta_merge) region = std::max(region, static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)));
+  const size_t shmem = ((2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15)) + region;
   if (shmem > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(&commit_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           static_cast<int>(shmem)) != hipSuccess)

@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
 #pragma unroll
     for (int j = 0; j < kMaxDim / kWave; ++j) {
       const int d = l + j * kWave;
-      x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+      x[j] = feat_or_zero(gp(row), d, D);
       if (j < J) xx = j == 0 ? x[j] * x[j] : xx + x[j] * x[j];
     }
     xx = wave_tree(xx);
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
 #pragma unroll
       for (int j = 0; j < kMaxDim / kWave; ++j) {
         const int d = l + j * kWave;
-        x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+        x[j] = feat_or_zero(gp(row), d, D);
       }
       const float d2 = row_d2_bf16(x, prow, D, J);
       float val;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
 #pragma unroll
     for (int j = 0; j < kMaxDim / kWave; ++j) {
       const int d = l + j * kWave;
-      x[j] = (j < J && d < D) ? bf16_to_f32(row[d]) : 0.f;
+      x[j] = feat_or_zero(gp(row), d, D);
     }
     float best = __builtin_inff();
     int arg = 0;

@@ -42,15 +42,50 @@ def rope_tables(n_positions, n_elem, base=10000.0, dtype=torch.float32):
     return torch.cos(idx).to(dtype), torch.sin(idx).to(dtype)
 
 
+def fenwick_counts(tokens, chunk, B, L):
+    """Per-level slot counts of one ladder after appending ``tokens`` rows in
+    ``chunk``-row batches: fill free slots, pair-merge the overflow into carries
+    for the next level, keep the survivors; a saturated top level stays full
+    (the count rule of litgpt/log_kv_cache.py:1815-1929)."""
+    counts = [0] * L
+    left = int(tokens)
+    while left > 0:
+        m = min(chunk, left)
+        left -= m
+        for ell in range(L):
+            take = min(B - counts[ell], m)
+            mr = m - take
+            if mr == 0:
+                counts[ell] += take
+                break
+            if ell == L - 1:
+                counts[ell] = B
+                break
+            n_carry = (mr + 1) // 2
+            counts[ell] = B + mr - 2 * n_carry
+            m = n_carry
+    return counts
+
+
 @torch.no_grad()
-def fill_readout_state(cache, seed=0, fill=0.75, recent=None, exact=None, mass=(1.0, 64.0)):
-    """Synthetic compressed-cache state for readout: random slot counts (about ``fill`` of
-    each ladder level), random bf16 keys / values, masses ~ U(mass), position sums
-    inside the cache's span; a full recent window and exact pool unless given."""
+def fill_readout_state(cache, seed=0, fill=0.75, recent=None, exact=None, mass=(1.0, 64.0), archived=None,
+                       flushes=15):
+    """Synthetic compressed-cache state for readout: random bf16 keys / values, masses ~ U(mass),
+    position sums inside the cache's span, a full recent window and exact pool unless given.
+
+    Slot counts: with ``archived`` tokens per lane, each cluster holds the ladder
+    occupancy of its share (a random split over the clusters) appended over
+    ``flushes`` flushes; otherwise about ``fill`` of each level, at random."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     Bt, G, K, L, S = cache.level_w.shape
     dk, dv = cache.k_dim, cache.v_dim
-    counts = torch.binomial(torch.full((Bt, G, K, L), float(S)), torch.full((Bt, G, K, L), fill), generator=g)
+    if archived is None:
+        counts = torch.binomial(torch.full((Bt, G, K, L), float(S)), torch.full((Bt, G, K, L), fill), generator=g)
+    else:
+        share = torch.rand(Bt, G, K, generator=g) + 0.5
+        share = (share / share.sum(-1, keepdim=True) * archived).long()
+        counts = torch.tensor([[[fenwick_counts(int(t), max(1, int(t) // flushes), S, L) for t in lane]
+                                for lane in row] for row in share.tolist()])
     counts = counts.to(torch.int16)
     occupied = torch.arange(S).view(1, 1, 1, 1, S) < counts.unsqueeze(-1)
     w = torch.empty(Bt, G, K, L, S).uniform_(*mass, generator=g).floor() * occupied
