@@ -40,11 +40,14 @@ __device__ __forceinline__ float canon_sum(const float* t, int J) {
 #pragma unroll
   for (int j = 1; j < kJ; ++j)
     if (j < J) s = s + t[j];
-  return wave_tree(s);
+  return wave_sum0(s);
 }
 
+constexpr int kTokBatch = 8;   // span rows whose loads are issued together
+
 // Token statistics of one component over a span: means (per lane features),
-// energy E and mean square of the means; returns R = residual / energy.
+// energy E and mean square of the means; returns R = residual / energy. Rows
+// are loaded kTokBatch at a time and then added in span order.
 __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, const LOGKV_G int32_t* tok, int n,
                                                 int D, float* mean, float& energy, float& msq) {
   const int l = lane_id(), J = (D + kWave - 1) / kWave;
@@ -52,18 +55,28 @@ __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, 
 #pragma unroll
   for (int j = 0; j < kJ; ++j) acc[j] = 0.f;
   const float d_f = static_cast<float>(D);
-  for (int i = 0; i < n; ++i) {
-    const LOGKV_G uint16_t* row = src.row(b, g, tok[i]);
-    float x[kJ], sq[kJ];
+  for (int i0 = 0; i0 < n; i0 += kTokBatch) {
+    float xb[kTokBatch][kJ];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int d = l + j * kWave;
-      x[j] = feat_or_zero(row, d, D);
-      sq[j] = x[j] * x[j];
-      acc[j] = i == 0 ? x[j] : acc[j] + x[j];
+    for (int t = 0; t < kTokBatch; ++t) {
+      const int i = i0 + t < n ? i0 + t : n - 1;
+      const LOGKV_G uint16_t* row = src.row(b, g, tok[i]);
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) xb[t][j] = j < J ? feat_or_zero(row, l + j * kWave, D) : 0.f;
     }
-    const float ms = canon_sum(sq, J) / d_f;
-    e = i == 0 ? ms : e + ms;
+#pragma unroll
+    for (int t = 0; t < kTokBatch; ++t) {
+      const int i = i0 + t;
+      if (i >= n) break;
+      float sq[kJ];
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        sq[j] = xb[t][j] * xb[t][j];
+        acc[j] = i == 0 ? xb[t][j] : acc[j] + xb[t][j];
+      }
+      const float ms = canon_sum(sq, J) / d_f;
+      e = i == 0 ? ms : e + ms;
+    }
   }
   const float cnt = static_cast<float>(n);
   float m2[kJ];

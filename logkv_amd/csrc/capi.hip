@@ -26,7 +26,8 @@ int check_ladder(const logkv_ladder_view* c) {
   if (c->k_max < 1 || c->k_max > logkv::kMaxClusters)
     return fail(LOGKV_EINVAL, "cluster count %d outside [1, %d]", c->k_max, logkv::kMaxClusters);
   if (c->slots < 2) return fail(LOGKV_EINVAL, "slots per level must be >= 2, got %d", c->slots);
-  if (c->levels < 1 || c->levels > 64) return fail(LOGKV_EINVAL, "levels %d outside [1, 64]", c->levels);
+  if (c->levels < 1 || c->levels > logkv::kMaxLevels)
+    return fail(LOGKV_EINVAL, "levels %d outside [1, %d]", c->levels, logkv::kMaxLevels);
   if (c->dk < 4 || c->dv < 4 || c->dk % 4 || c->dv % 4 || c->dk > logkv::kMaxDim || c->dv > logkv::kMaxDim)
     return fail(LOGKV_EINVAL, "key/value widths must be multiples of 4 in [4, %d], got %d/%d", logkv::kMaxDim,
                 c->dk, c->dv);
@@ -50,8 +51,8 @@ int check_rows(const logkv_ladder_view* c, const logkv_rows_view* r) {
 }
 
 struct Plan {
-  int64_t order, assign, s_win, dist, snap, ladder, total;
-  int64_t stride, s0, ca, cb;
+  int64_t order, assign, s_win, dist, snap, plans, tok, ladder, total;
+  int64_t stride, s0, carry[3];
   int32_t sort_width;
 };
 
@@ -61,8 +62,8 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   const int64_t ladders = lanes * c->k_max;
   const int64_t existing = late ? int64_t(c->levels) * c->slots : 0;
   const int64_t m0 = tokens + existing;
-  logkv::ladder_scratch_rows(m0, c->slots, p.s0, p.ca, p.cb, late ? m0 : 0);
-  p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.ca, p.cb));
+  logkv::ladder_scratch_rows(m0, p.s0, p.carry, late ? m0 : 0);
+  p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.carry));
   int64_t off = 0;
   p.order = off;
   off += align256(int64_t(c->n_batch) * tokens * 4);
@@ -74,6 +75,10 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   off += align256(lanes * tokens * 4);
   p.snap = off;
   off += align256(ladders);
+  p.plans = off;
+  off += align256(ladders * int64_t(sizeof(logkv::LadderPlan)));
+  p.tok = off;
+  off += align256(ladders * tokens * 2);
   p.ladder = off;
   off += ladders * p.stride;
   p.total = off;
@@ -105,8 +110,9 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   ws.ladder = base + p.ladder;
   ws.ladder_stride = p.stride;
   ws.s0_rows = p.s0;
-  ws.carry_a_rows = p.ca;
-  ws.carry_b_rows = p.cb;
+  for (int i = 0; i < 3; ++i) ws.carry_rows[i] = p.carry[i];
+  ws.plans = reinterpret_cast<logkv::LadderPlan*>(base + p.plans);
+  ws.tok = reinterpret_cast<uint16_t*>(base + p.tok);
   ws.sort_width = p.sort_width;
   return LOGKV_OK;
 }

@@ -297,12 +297,13 @@ __device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int6
   for (int64_t r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, first + r, Meta{0.f, 0, 0, 0, 0, 0});
 }
 
-// Carries j in [0, n_carry) from pool rows (2j, 2j+1); loads of kBatch carries
-// per thread are issued before their stores.
+// Carries j in [j_begin, j_end) from pool rows (2j, 2j+1); loads of kBatch
+// carries per thread are issued before their stores.
 template <int KIND>
-__device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa& out, int n_carry, int dk, int dv) {
+__device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa& out, int j_begin, int n_carry, int dk,
+                                             int dv) {
   const RowUnits ru(dk, dv);
-  for (int j0 = ru.r0; j0 < n_carry; j0 += kBatch * ru.step) {
+  for (int j0 = j_begin + ru.r0; j0 < n_carry; j0 += kBatch * ru.step) {
     uint2 a[kBatch], b[kBatch];
     float wa[kBatch], wb[kBatch];
 #pragma unroll
@@ -325,7 +326,8 @@ __device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa&
       }
     }
   }
-  for (int j = threadIdx.x; j < n_carry; j += kThreads) put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
+  for (int j = j_begin + threadIdx.x; j < n_carry; j += kThreads)
+    put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
 }
 
 // ---- Beta 4->2 -------------------------------------------------------------
@@ -473,15 +475,15 @@ __host__ __device__ inline int64_t beta_stage_bytes(int dk, int dv) {
 // holds row i's metadata. `stage` is LDS of beta_stage_bytes(dk, dv).
 template <int NJ, int KIND>
 __device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa& out, int n_pair, int dk, int dv,
-                                             uint8_t* stage) {
+                                             uint8_t* stage, int g_begin, int g_end) {
   const int l = lane_id(), w = wave_id();
-  const int n_groups = (n_pair + 3) / 4;
+  const int n_groups = min(g_end, (n_pair + 3) / 4);
   const int cg = beta_chunk_groups(dk, dv);
   LOGKV_S uint16_t* sk = (LOGKV_S uint16_t*)stage;
   LOGKV_S uint16_t* sv = sk + 4 * cg * dk;
   LOGKV_S Meta* sm = (LOGKV_S Meta*)(stage + align16(4 * static_cast<int64_t>(cg) * (dk + dv) * 2));
   const RowUnits ru(dk, dv);
-  for (int g0 = 0; g0 < n_groups; g0 += cg) {
+  for (int g0 = g_begin; g0 < n_groups; g0 += cg) {
     const int ng = min(cg, n_groups - g0);
     const int p0 = 4 * g0;
     const int rows = min(4 * ng, n_pair - p0);
@@ -612,73 +614,96 @@ __device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
 //    pair into carries, P[n_pair..) moves to slots [0, n_surv), the rest clears;
 //  * at the top: slot 0 = left fold of P[0..mr] (bf16 after every merge) and
 //    slots 1..B'-1 = P[mr+1..n_pool), mr = n_pool - B'.
-// Returns the number of carries written to `out` (0 ends the append).
+// The carries are computed by every block of a level launch (a slice each);
+// the slot writes (fill, move, clear, fold) by one block in the next launch,
+// after every carry of the level has read the stored slots.
+__host__ __device__ inline int carries_of(int cnt, int m, int B, bool top) {
+  const int n_pool = cnt + m;
+  if (m == 0 || n_pool <= B || top) return 0;
+  return (n_pool - B + 1) / 2;
+}
+
 template <int KIND>
-__device__ __forceinline__ int level_step(const Ladder& L, int16_t* counts_s, int ell, bool top, const Src& cur, int m,
-                                          const Soa& out, bool beta, uint8_t* stage) {
-  // Barriers: move_rows' load/store barrier is the only one a level needs. It
-  // orders this level's carry stores before the next level reads them, and
-  // every read of this level's staged source before the next level overwrites
-  // that buffer with its own carries. counts_s[ell] is written by thread 0 and
-  // read again only after the final barrier of the append.
+__device__ __forceinline__ void level_carries(const Ladder& L, int ell, int cnt, const Src& cur, int m, const Soa& out,
+                                              bool beta, uint8_t* stage, int part, int parts) {
+  const int n_carry = carries_of(cnt, m, L.B, false);
+  const PoolT<KIND> pool{L, static_cast<int64_t>(ell) * L.B, cnt, cur};
+  if (beta) {
+    const int n_pair = 2 * n_carry, n_groups = (n_pair + 3) / 4;
+    const int g0 = static_cast<int>(static_cast<int64_t>(part) * n_groups / parts);
+    const int g1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_groups / parts);
+    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
+    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
+  } else {
+    const int j0 = static_cast<int>(static_cast<int64_t>(part) * n_carry / parts);
+    const int j1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_carry / parts);
+    pair_carries<KIND>(pool, out, j0, j1, L.dk, L.dv);
+  }
+}
+
+// Slot writes of one level step; returns the level's new count.
+template <int KIND>
+__device__ __forceinline__ int level_finish(const Ladder& L, int ell, int cnt, const Src& cur, int m, bool top) {
   const int B = L.B;
   const int64_t base = static_cast<int64_t>(ell) * B;
-  const int cnt = counts_s[ell];
   const int n_pool = cnt + m;
   const PoolT<KIND> pool{L, base, cnt, cur};
   if (n_pool <= B) {
     copy_staged<KIND>(L, base, cur, 0, cnt, m);
-    if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(n_pool);
-    return 0;
+    return n_pool;
   }
   const int mr = n_pool - B;
   if (top) {
     fold_top<KIND>(pool, mr);
-    if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(B);
-    return 0;
+    return B;
   }
-  const int n_carry = (mr + 1) / 2, n_pair = 2 * n_carry;
+  const int n_pair = 2 * ((mr + 1) / 2);
   const int n_surv = n_pool - n_pair;   // >= B' - 1 >= 1, so move_rows always runs its barrier
-  if (beta) {
-    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv, stage);
-    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv, stage);
-  } else {
-    pair_carries<KIND>(pool, out, n_carry, L.dk, L.dv);
-  }
   move_rows<KIND>(pool, n_pair, 0, n_surv);
   clear_slots(L, base + n_surv, B - n_surv);
-  if (threadIdx.x == 0) counts_s[ell] = static_cast<int16_t>(n_surv);
-  return n_carry;
-}
-
-// Fenwick append of m0 staged rows from `src0` into one ladder, level by level.
-__device__ __forceinline__ void fenwick_append(const Ladder& L, int16_t* counts_s, int levels, Src src0, int m0, Soa bufA, Soa bufB,
-                               bool beta, uint8_t* stage) {
-  int m = src0.kind == 1 ? level_step<1>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta, stage)
-                         : level_step<0>(L, counts_s, 0, levels == 1, src0, m0, bufA, beta, stage);
-  Src cur{};
-  cur.kind = 1;
-  for (int ell = 1; ell < levels && m > 0; ++ell) {
-    cur.buf = (ell & 1) ? bufA : bufB;   // carries written by the previous level
-    m = level_step<1>(L, counts_s, ell, ell == levels - 1, cur, m, (ell & 1) ? bufB : bufA, beta, stage);
-  }
+  return n_surv;
 }
 
 }  // namespace
 
 int64_t row_bytes(int dk, int dv) { return 2 * (dk + dv) + 4 + 32 + 1; }
 
-int64_t ladder_scratch_rows(int64_t m0, int64_t slots, int64_t& s0, int64_t& ca, int64_t& cb, int64_t existing) {
-  (void)slots;
+// Level l's carries go to buffer l % 3: level l stages at most ceil(m0 / 2^l)
+// rows and emits at most ceil(m0 / 2^(l+1)) carries, and a level launch reads
+// the carries of level l - 1 (its own staged rows) and of level l - 2 (the
+// staged rows of the level it finishes) while it writes those of level l.
+int64_t ladder_scratch_rows(int64_t m0, int64_t& s0, int64_t* carry, int64_t existing) {
   s0 = existing;
-  ca = (m0 + 1) / 2 + 1;
-  cb = (m0 + 3) / 4 + 2;
-  return s0 + ca + cb;
+  carry[0] = (m0 + 1) / 2 + 1;
+  carry[1] = (m0 + 3) / 4 + 2;
+  carry[2] = (m0 + 7) / 8 + 3;
+  return s0 + carry[0] + carry[1] + carry[2];
 }
 
-int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t ca, int64_t cb) {
-  return soa_bytes(s0, c.dk, c.dv) + soa_bytes(ca, c.dk, c.dv) + soa_bytes(cb, c.dk, c.dv);
+int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, const int64_t* carry) {
+  return soa_bytes(s0, c.dk, c.dv) + soa_bytes(carry[0], c.dk, c.dv) + soa_bytes(carry[1], c.dk, c.dv) +
+         soa_bytes(carry[2], c.dk, c.dv);
 }
+
+namespace {
+
+struct Scratch {
+  Soa s0, carry[3];
+};
+
+__device__ inline Scratch scratch_of(const Workspace& ws, int ladder, int dk, int dv) {
+  uint8_t* p = ws.ladder + ladder * ws.ladder_stride;
+  Scratch sc;
+  sc.s0 = soa_at(p, ws.s0_rows, dk, dv);
+  p += soa_bytes(ws.s0_rows, dk, dv);
+  for (int i = 0; i < 3; ++i) {
+    sc.carry[i] = soa_at(p, ws.carry_rows[i], dk, dv);
+    p += soa_bytes(ws.carry_rows[i], dk, dv);
+  }
+  return sc;
+}
+
+}  // namespace
 
 __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws) {
   extern __shared__ __align__(16) uint8_t dyn[];
@@ -720,7 +745,10 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     __syncthreads();
   }
   const int m = m_s;
-  if (m == 0) return;
+  if (m == 0) {
+    if (blockIdx.y == 0 && threadIdx.x == 0) ws.plans[ladder].active = 0;
+    return;
+  }
 
   const int64_t cl = static_cast<int64_t>(lane_ix) * K + cc;
   const int64_t row0 = cl * L * B;
@@ -732,12 +760,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_G int64_t* posb = gp(r.pos + b * r.pos_sb);
   LOGKV_G float* mu = gp(c.centroid + cl * dk);
   const LOGKV_S uint16_t* tok_s = (const LOGKV_S uint16_t*)tok;
-  uint8_t* scratch = ws.ladder + ladder * ws.ladder_stride;
-  const Soa S0 = soa_at(scratch, ws.s0_rows, dk, dv);
-  scratch += soa_bytes(ws.s0_rows, dk, dv);
-  const Soa bufA = soa_at(scratch, ws.carry_a_rows, dk, dv);
-  scratch += soa_bytes(ws.carry_a_rows, dk, dv);
-  const Soa bufB = soa_at(scratch, ws.carry_b_rows, dk, dv);
+  const Soa S0 = scratch_of(ws, ladder, dk, dv).s0;
 
   const bool was_alive = ws.snap_alive[cl] != 0;
   const int first = was_alive ? 0 : 1;   // a dead cluster opens with its earliest row
@@ -821,21 +844,15 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     p_hi = posb[t0];
     phase = 1;
   }
+  int kind0 = 0, m0 = 0;
+  int64_t order_base = 0;
   if (nn > 0) {
     const int64_t first_pos = posb[tok[first]];
     const bool late = prm.late_joins && first_pos < p_hi;
     const int64_t last_pos = posb[tok[m - 1]];
-    Src src{};
-    src.tok = tok_s + first;
-    src.kb = kb;
-    src.vb = vb;
-    src.k_st = r.k_st;
-    src.v_st = r.v_st;
-    src.posb = posb;
-    int m0 = nn;
+    m0 = nn;
     if (!late) {
-      src.kind = 0;
-      src.order_base = phase;
+      order_base = phase;
       phase += nn;
       p_hi = last_pos;
     } else {
@@ -941,19 +958,32 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       clear_slots(lad, 0, static_cast<int64_t>(L) * B);
       for (int e = threadIdx.x; e < L; e += kThreads) counts_s[e] = 0;
       __syncthreads();
-      src.kind = 1;
-      src.buf = S0;
+      kind0 = 1;
       m0 = total;
     }
     n_total += nn;
-    __syncthreads();
-    // The Beta stage reuses the LDS after the compacted rows (center staging
-    // belongs to the sibling block; the sort keys are dead by now).
-    fenwick_append(lad, counts_s, L, src, m0, bufA, bufB, prm.beta_merge != 0, dyn + c_stage_off);
   }
+  // Hand-off to the level launches: this ladder's rows in position order, the
+  // counts before the append (the level launches rewrite the levels they
+  // touch) and the per-level plan of the cascade.
+  for (int i = threadIdx.x; i < m; i += kThreads) ws.tok[static_cast<int64_t>(ladder) * r.tokens + i] = tok[i];
   __syncthreads();
   for (int e = threadIdx.x; e < L; e += kThreads) c.level_count[cl * L + e] = counts_s[e];
   if (threadIdx.x == 0) {
+    LadderPlan pl;
+    pl.active = nn > 0 ? 1 : 0;
+    pl.kind0 = kind0;
+    pl.m_tok = m;
+    pl.first = first;
+    pl.order_base = order_base;
+    int mm = m0;
+    for (int e = 0; e < kMaxLevels; ++e) {
+      const bool used = e < L;
+      pl.cnt[e] = used ? counts_s[e] : 0;
+      pl.m[e] = used ? mm : 0;
+      mm = used ? carries_of(counts_s[e], mm, B, e == L - 1) : 0;
+    }
+    ws.plans[ladder] = pl;
     c.alive[cl] = 1;
     c.n_total[cl] = n_total;
     c.p_hi_c[cl] = p_hi;
@@ -961,19 +991,92 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   }
 }
 
+// Level launch `ell`: block (ladder, 0) finishes level ell - 1 (fill, move and
+// clear, or top fold) and every block (ladder, part) computes its slice of
+// level ell's carries. Launches ell = 0..L run in stream order.
+__global__ __launch_bounds__(kThreads) void level_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws,
+                                                         int ell) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  const int K = c.k_max, L = c.levels, B = c.slots, dk = c.dk, dv = c.dv;
+  const int ladder = blockIdx.x, part = blockIdx.y, parts = gridDim.y;
+  const LadderPlan* pl = ws.plans + ladder;
+  if (!pl->active) return;
+  const bool fin = part == 0 && ell > 0 && pl->m[ell - 1] > 0;
+  const bool carry = ell < L && carries_of(pl->cnt[ell], pl->m[ell], B, ell == L - 1) > 0;
+  if (!fin && !carry) return;
+  const int lane_ix = ladder / K;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const int64_t row0 = static_cast<int64_t>(ladder) * L * B;
+  const Ladder lad{gp(c.level_k + row0 * dk), gp(c.level_v + row0 * dv), gp(c.level_w + row0),
+                   gp(c.level_p_lo + row0), gp(c.level_p_hi + row0), gp(c.level_sum_wp + row0),
+                   gp(c.level_order + row0), gp(c.pad_mask + row0), dk, dv, B};
+  const Scratch sc = scratch_of(ws, ladder, dk, dv);
+  const int kind0 = pl->kind0;
+  uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
+  const int tok_bytes = (2 * r.tokens + 15) & ~15;
+  if (kind0 == 0 && ((carry && ell == 0) || (fin && ell == 1))) {
+    const int mt = pl->m_tok;
+    const LOGKV_G uint16_t* src = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
+    for (int i = threadIdx.x; i < mt; i += kThreads) tok[i] = src[i];
+    __syncthreads();
+  }
+  Src flush_rows{};
+  flush_rows.kind = 0;
+  flush_rows.tok = (const LOGKV_S uint16_t*)tok + pl->first;
+  flush_rows.order_base = pl->order_base;
+  flush_rows.kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  flush_rows.vb = gp(r.v + b * r.v_sb + g * r.v_sg);
+  flush_rows.k_st = r.k_st;
+  flush_rows.v_st = r.v_st;
+  flush_rows.posb = gp(r.pos + b * r.pos_sb);
+  auto staged = [&](int e) {
+    Src s{};
+    s.kind = 1;
+    s.buf = e == 0 ? sc.s0 : sc.carry[(e - 1) % 3];
+    return s;
+  };
+  if (fin) {
+    const int e = ell - 1;
+    const int cnt = pl->cnt[e], m = pl->m[e];
+    const int n = (e == 0 && kind0 == 0) ? level_finish<0>(lad, e, cnt, flush_rows, m, e == L - 1)
+                                         : level_finish<1>(lad, e, cnt, staged(e), m, e == L - 1);
+    if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * L + e] = static_cast<int16_t>(n);
+  }
+  if (carry) {
+    const int cnt = pl->cnt[ell], m = pl->m[ell];
+    uint8_t* stage = dyn + tok_bytes;
+    const bool beta = prm.beta_merge != 0;
+    if (ell == 0 && kind0 == 0)
+      level_carries<0>(lad, ell, cnt, flush_rows, m, sc.carry[0], beta, stage, part, parts);
+    else
+      level_carries<1>(lad, ell, cnt, staged(ell), m, sc.carry[ell % 3], beta, stage, part, parts);
+  }
+}
+
+constexpr int kParts = 16;   // blocks per ladder for level 0's carries (halved per level)
+
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
+  const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
   size_t region = static_cast<size_t>(kCenterRows) * c.dk * 2;
   if (p.late_joins) region += static_cast<size_t>(ws.sort_width) * 8;
-  if (p.beta_merge) region = std::max(region, static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)));
-  const size_t shmem = ((2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15)) + region;
+  const size_t shmem = tok_bytes + region;
   if (shmem > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(&commit_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           static_cast<int>(shmem)) != hipSuccess)
     return LOGKV_ERUNTIME;
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
+  const size_t level_shmem = tok_bytes + (p.beta_merge ? static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)) : 0);
+  if (level_shmem > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&level_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(level_shmem)) != hipSuccess)
+    return LOGKV_ERUNTIME;
+  for (int ell = 0; ell <= c.levels; ++ell) {
+    const int parts = ell < c.levels ? std::max(1, kParts >> ell) : 1;
+    hipLaunchKernelGGL(level_kernel, dim3(ladders, parts), dim3(kThreads), level_shmem, stream, c, r, p, ws, ell);
+  }
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

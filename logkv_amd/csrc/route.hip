@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
       const float m = d < D ? mu_s[cc * D + d] : 0.f;
       s = j == 0 ? m * m : s + m * m;
     }
-    s = wave_tree(s);
+    s = wave_sum0(s);
     if (l == 0) mm_s[cc] = s;
   }
   __syncthreads();
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
       x[j] = feat_or_zero(gp(row), d, D);
       if (j < J) xx = j == 0 ? x[j] * x[j] : xx + x[j] * x[j];
     }
-    xx = wave_tree(xx);
+    xx = wave_sum0(xx);
     float best = __builtin_inff(), s_winner = 0.f, best_e = __builtin_inff();
     int winner = 0, nearest = 0;
     for (int cc = 0; cc < K; ++cc) {
@@ -120,8 +120,8 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
           ex = j == 0 ? diff * diff : ex + diff * diff;
         }
       }
-      dot = wave_tree(dot);
-      ex = wave_tree(ex);
+      dot = wave_sum0(dot);
+      ex = wave_sum0(ex);
       const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot, 0.0f);
       const bool live = (alive_bits >> cc) & 1u;
       if (cc == 0) s_winner = semantic;
@@ -166,7 +166,7 @@ __device__ __forceinline__ float row_d2_bf16(const float* x, const uint16_t* oth
       s = j == 0 ? diff * diff : s + diff * diff;
     }
   }
-  return wave_tree(s);
+  return wave_sum0(s);
 }
 
 // Block-wide argmax (first index on ties) of (value, index) pairs.
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
           e = j == 0 ? diff * diff : e + diff * diff;
         }
       }
-      e = wave_tree(e);
+      e = wave_sum0(e);
       if (((cand_bits >> cc) & 1u) && e < best) {
         best = e;
         arg = cc;

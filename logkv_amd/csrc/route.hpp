@@ -12,7 +12,7 @@ using RouteParams = logkv_route_params;
 constexpr int kMaxOrderRows = 8192;   // rows per flush (position-order sort in LDS)
 constexpr int kOrderIndexBits = 13;
 constexpr uint64_t kOrderIndexMask = (1ull << kOrderIndexBits) - 1;
-constexpr int kAttachTile = 64;       // rows per attach block
+constexpr int kAttachTile = 16;       // rows per attach block
 constexpr int kMaxClusters = 32;      // K (alive bits are a 32-bit mask)
 constexpr int kMaxDim = 256;          // dk, dv
 
@@ -23,6 +23,20 @@ __device__ __forceinline__ int valid_rows(const logkv_rows_view& r, int b) {
   return n < 0 ? 0 : (n > r.tokens ? r.tokens : n);
 }
 
+constexpr int kMaxLevels = 32;        // ladder levels L
+
+// Per-ladder plan of one commit, written by the prepare launch and read by the
+// level launches: counts before each level step and the rows staged into it.
+struct LadderPlan {
+  int32_t active;       // rows to append after the prepare step
+  int32_t kind0;        // level-0 staged source: 0 flush rows (tok list), 1 S0 rows
+  int32_t m_tok;        // entries of the tok list
+  int32_t first;        // tok list offset of the first appended row
+  int64_t order_base;   // order of staged flush row 0 (kind 0)
+  int16_t cnt[kMaxLevels];
+  int32_t m[kMaxLevels];
+};
+
 // Device scratch of one route/commit call, carved from the caller's workspace.
 struct Workspace {
   int32_t* order;      // [n_batch, T]
@@ -32,12 +46,14 @@ struct Workspace {
   uint8_t* snap_alive; // [lanes, K] alive flags at the start of the flush
   uint8_t* ladder;     // per-ladder carry / staging rows
   int64_t ladder_stride;  // bytes per ladder
-  int64_t s0_rows, carry_a_rows, carry_b_rows;
+  int64_t s0_rows, carry_rows[3];
   int32_t sort_width;     // keys per block for the delayed-archive sort (0 without it)
+  LadderPlan* plans;      // [ladders]
+  uint16_t* tok;          // [ladders, T] each ladder's flush rows in position order
 };
 
-int64_t ladder_scratch_rows(int64_t m0, int64_t slots, int64_t& s0, int64_t& ca, int64_t& cb, int64_t existing);
-int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t ca, int64_t cb);
+int64_t ladder_scratch_rows(int64_t m0, int64_t& s0, int64_t* carry, int64_t existing);
+int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, const int64_t* carry);
 int64_t row_bytes(int dk, int dv);
 int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                  hipStream_t stream);
