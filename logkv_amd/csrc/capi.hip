@@ -52,7 +52,7 @@ int check_rows(const logkv_ladder_view* c, const logkv_rows_view* r) {
 
 struct Plan {
   int64_t order, assign, s_win, dist, snap, plans, tok, ladder, total;
-  int64_t stride, s0, carry[3];
+  int64_t stride, s0, m0;
   int32_t sort_width;
 };
 
@@ -62,8 +62,9 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   const int64_t ladders = lanes * c->k_max;
   const int64_t existing = late ? int64_t(c->levels) * c->slots : 0;
   const int64_t m0 = tokens + existing;
-  logkv::ladder_scratch_rows(m0, p.s0, p.carry, late ? m0 : 0);
-  p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.carry));
+  p.s0 = late ? m0 : 0;
+  p.m0 = m0;
+  p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.m0));
   int64_t off = 0;
   p.order = off;
   off += align256(int64_t(c->n_batch) * tokens * 4);
@@ -110,7 +111,7 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   ws.ladder = base + p.ladder;
   ws.ladder_stride = p.stride;
   ws.s0_rows = p.s0;
-  for (int i = 0; i < 3; ++i) ws.carry_rows[i] = p.carry[i];
+  ws.m0_cap = p.m0;
   ws.plans = reinterpret_cast<logkv::LadderPlan*>(base + p.plans);
   ws.tok = reinterpret_cast<uint16_t*>(base + p.tok);
   ws.sort_width = p.sort_width;

@@ -198,7 +198,7 @@ struct RowUnits {
     units = (dk + dv) / 4;
     u = static_cast<int>(threadIdx.x) % units;
     r0 = static_cast<int>(threadIdx.x) / units;
-    step = kThreads / units;
+    step = static_cast<int>(blockDim.x) / units;
     if (r0 >= step) r0 = 1 << 30;  // threads past the last full pass stay idle
   }
 };
@@ -284,7 +284,7 @@ __device__ __forceinline__ void copy_staged(const Ladder& L, int64_t base, const
       }
     }
   }
-  for (int r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, base + d0 + r, pool.meta(s0 + r));
+  for (int r = threadIdx.x; r < n; r += blockDim.x) put_slot_meta(L, base + d0 + r, pool.meta(s0 + r));
 }
 
 __device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int64_t n) {
@@ -294,7 +294,7 @@ __device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int6
     const int64_t s = first + r;
     store_unit(L.k + s * L.dk, L.v + s * L.dv, ru.u, ru.ku, z);
   }
-  for (int64_t r = threadIdx.x; r < n; r += kThreads) put_slot_meta(L, first + r, Meta{0.f, 0, 0, 0, 0, 0});
+  for (int64_t r = threadIdx.x; r < n; r += blockDim.x) put_slot_meta(L, first + r, Meta{0.f, 0, 0, 0, 0, 0});
 }
 
 // Carries j in [j_begin, j_end) from pool rows (2j, 2j+1); loads of kBatch
@@ -326,7 +326,7 @@ __device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa&
       }
     }
   }
-  for (int j = j_begin + threadIdx.x; j < n_carry; j += kThreads)
+  for (int j = j_begin + static_cast<int>(threadIdx.x); j < n_carry; j += blockDim.x)
     put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
 }
 
@@ -458,11 +458,13 @@ __device__ __forceinline__ Meta side_meta(const Meta& mine, bool member, float m
 // Beta groups are staged in LDS a chunk at a time: the K|V rows and metadata
 // of up to beta_chunk_groups() groups of four, loaded by the whole block with
 // many rows in flight, then one wave per group computes from LDS.
-constexpr int kBetaStageBytes = 64 * 1024;
+constexpr int kBetaStageBytes = 32 * 1024;
+constexpr int kCarryThreads = 256;   // block size of the carries launches
 
 __host__ __device__ inline int beta_chunk_groups(int dk, int dv) {
   const int g = kBetaStageBytes / (4 * (dk + dv) * 2);
-  return g < kWaves ? kWaves : (g > 64 ? 64 : g);
+  constexpr int waves = kCarryThreads / kWave;
+  return g < waves ? waves : (g > 64 ? 64 : g);
 }
 
 __host__ __device__ inline int64_t beta_stage_bytes(int dk, int dv) {
@@ -504,9 +506,9 @@ __device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa&
         }
       }
     }
-    for (int r = threadIdx.x; r < rows; r += kThreads) sm[r] = pool.meta(p0 + r);
+    for (int r = threadIdx.x; r < rows; r += blockDim.x) sm[r] = pool.meta(p0 + r);
     __syncthreads();
-    for (int gl = w; gl < ng; gl += kWaves) {
+    for (int gl = w; gl < ng; gl += static_cast<int>(blockDim.x) / kWave) {
       const int start = p0 + 4 * gl;
       const int width = min(4, n_pair - start);
       const int rl = 4 * gl;
@@ -623,7 +625,7 @@ __host__ __device__ inline int carries_of(int cnt, int m, int B, bool top) {
   return (n_pool - B + 1) / 2;
 }
 
-template <int KIND>
+template <int KIND, int NJ>
 __device__ __forceinline__ void level_carries(const Ladder& L, int ell, int cnt, const Src& cur, int m, const Soa& out,
                                               bool beta, uint8_t* stage, int part, int parts) {
   const int n_carry = carries_of(cnt, m, L.B, false);
@@ -632,8 +634,7 @@ __device__ __forceinline__ void level_carries(const Ladder& L, int ell, int cnt,
     const int n_pair = 2 * n_carry, n_groups = (n_pair + 3) / 4;
     const int g0 = static_cast<int>(static_cast<int64_t>(part) * n_groups / parts);
     const int g1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_groups / parts);
-    if (L.dk <= 2 * kWave && L.dv <= 2 * kWave) beta_carries<2, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
-    else beta_carries<4, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
+    beta_carries<NJ, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
   } else {
     const int j0 = static_cast<int>(static_cast<int64_t>(part) * n_carry / parts);
     const int j1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_carry / parts);
@@ -666,41 +667,65 @@ __device__ __forceinline__ int level_finish(const Ladder& L, int ell, int cnt, c
 
 }  // namespace
 
-int64_t row_bytes(int dk, int dv) { return 2 * (dk + dv) + 4 + 32 + 1; }
 
-// Level l's carries go to buffer l % 3: level l stages at most ceil(m0 / 2^l)
-// rows and emits at most ceil(m0 / 2^(l+1)) carries, and a level launch reads
-// the carries of level l - 1 (its own staged rows) and of level l - 2 (the
-// staged rows of the level it finishes) while it writes those of level l.
-int64_t ladder_scratch_rows(int64_t m0, int64_t& s0, int64_t* carry, int64_t existing) {
-  s0 = existing;
-  carry[0] = (m0 + 1) / 2 + 1;
-  carry[1] = (m0 + 3) / 4 + 2;
-  carry[2] = (m0 + 7) / 8 + 3;
-  return s0 + carry[0] + carry[1] + carry[2];
+// Carries of level l (at most ceil(m0 / 2^(l+1)): level l stages at most
+// ceil(m0 / 2^l) rows) get a buffer of their own, so every level's slot
+// writes can run after all carries, in one launch.
+__host__ __device__ inline int64_t carry_cap(int64_t m0, int ell) {
+  return ((m0 + (int64_t(1) << (ell + 1)) - 1) >> (ell + 1)) + 1;
 }
 
-int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, const int64_t* carry) {
-  return soa_bytes(s0, c.dk, c.dv) + soa_bytes(carry[0], c.dk, c.dv) + soa_bytes(carry[1], c.dk, c.dv) +
-         soa_bytes(carry[2], c.dk, c.dv);
+int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t m0) {
+  int64_t bytes = soa_bytes(s0, c.dk, c.dv);
+  for (int ell = 0; ell + 1 < c.levels; ++ell) bytes += soa_bytes(carry_cap(m0, ell), c.dk, c.dv);
+  return bytes;
 }
 
 namespace {
 
-struct Scratch {
-  Soa s0, carry[3];
-};
+__device__ inline Soa s0_of(const Workspace& ws, int ladder, int dk, int dv) {
+  return soa_at(ws.ladder + ladder * ws.ladder_stride, ws.s0_rows, dk, dv);
+}
 
-__device__ inline Scratch scratch_of(const Workspace& ws, int ladder, int dk, int dv) {
-  uint8_t* p = ws.ladder + ladder * ws.ladder_stride;
-  Scratch sc;
-  sc.s0 = soa_at(p, ws.s0_rows, dk, dv);
-  p += soa_bytes(ws.s0_rows, dk, dv);
-  for (int i = 0; i < 3; ++i) {
-    sc.carry[i] = soa_at(p, ws.carry_rows[i], dk, dv);
-    p += soa_bytes(ws.carry_rows[i], dk, dv);
-  }
-  return sc;
+__device__ inline Soa carry_of(const Workspace& ws, int ladder, int ell, int dk, int dv) {
+  int64_t off = soa_bytes(ws.s0_rows, dk, dv);
+  for (int e = 0; e < ell; ++e) off += soa_bytes(carry_cap(ws.m0_cap, e), dk, dv);
+  return soa_at(ws.ladder + ladder * ws.ladder_stride + off, carry_cap(ws.m0_cap, ell), dk, dv);
+}
+
+// Staged rows of level ell: S0 (delayed archive) at level 0, else level ell - 1's carries.
+__device__ inline Src staged_of(const Workspace& ws, int ladder, int ell, int dk, int dv) {
+  Src s{};
+  s.kind = 1;
+  s.buf = ell == 0 ? s0_of(ws, ladder, dk, dv) : carry_of(ws, ladder, ell - 1, dk, dv);
+  return s;
+}
+
+// The ladder's flush rows as a level-0 source; the tok list is copied to LDS.
+__device__ inline Src flush_rows_of(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const LadderPlan* pl,
+                                    int ladder, uint16_t* tok) {
+  const int lane_ix = ladder / c.k_max;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const LOGKV_G uint16_t* src = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
+  for (int i = threadIdx.x; i < pl->m_tok; i += blockDim.x) tok[i] = src[i];
+  __syncthreads();
+  Src s{};
+  s.kind = 0;
+  s.tok = (const LOGKV_S uint16_t*)tok + pl->first;
+  s.order_base = pl->order_base;
+  s.kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  s.vb = gp(r.v + b * r.v_sb + g * r.v_sg);
+  s.k_st = r.k_st;
+  s.v_st = r.v_st;
+  s.posb = gp(r.pos + b * r.pos_sb);
+  return s;
+}
+
+__device__ inline Ladder ladder_of(const LadderArgs& c, int ladder) {
+  const int64_t row0 = static_cast<int64_t>(ladder) * c.levels * c.slots;
+  return Ladder{gp(c.level_k + row0 * c.dk), gp(c.level_v + row0 * c.dv), gp(c.level_w + row0),
+                gp(c.level_p_lo + row0), gp(c.level_p_hi + row0), gp(c.level_sum_wp + row0),
+                gp(c.level_order + row0), gp(c.pad_mask + row0), c.dk, c.dv, c.slots};
 }
 
 }  // namespace
@@ -760,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_G int64_t* posb = gp(r.pos + b * r.pos_sb);
   LOGKV_G float* mu = gp(c.centroid + cl * dk);
   const LOGKV_S uint16_t* tok_s = (const LOGKV_S uint16_t*)tok;
-  const Soa S0 = scratch_of(ws, ladder, dk, dv).s0;
+  const Soa S0 = s0_of(ws, ladder, dk, dv);
 
   const bool was_alive = ws.snap_alive[cl] != 0;
   const int first = was_alive ? 0 : 1;   // a dead cluster opens with its earliest row
@@ -991,69 +1016,50 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   }
 }
 
-// Level launch `ell`: block (ladder, 0) finishes level ell - 1 (fill, move and
-// clear, or top fold) and every block (ladder, part) computes its slice of
-// level ell's carries. Launches ell = 0..L run in stream order.
-__global__ __launch_bounds__(kThreads) void level_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws,
-                                                         int ell) {
+// Carries launch `ell`: block (ladder, part) computes its slice of level
+// ell's carries. Launches ell = 0..L-2 run in stream order (level ell stages
+// level ell - 1's carries); slots are not written here.
+template <int NJ>
+__global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+                                                                Workspace ws, int ell) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  const int K = c.k_max, L = c.levels, B = c.slots, dk = c.dk, dv = c.dv;
   const int ladder = blockIdx.x, part = blockIdx.y, parts = gridDim.y;
   const LadderPlan* pl = ws.plans + ladder;
   if (!pl->active) return;
-  const bool fin = part == 0 && ell > 0 && pl->m[ell - 1] > 0;
-  const bool carry = ell < L && carries_of(pl->cnt[ell], pl->m[ell], B, ell == L - 1) > 0;
-  if (!fin && !carry) return;
-  const int lane_ix = ladder / K;
-  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
-  const int64_t row0 = static_cast<int64_t>(ladder) * L * B;
-  const Ladder lad{gp(c.level_k + row0 * dk), gp(c.level_v + row0 * dv), gp(c.level_w + row0),
-                   gp(c.level_p_lo + row0), gp(c.level_p_hi + row0), gp(c.level_sum_wp + row0),
-                   gp(c.level_order + row0), gp(c.pad_mask + row0), dk, dv, B};
-  const Scratch sc = scratch_of(ws, ladder, dk, dv);
-  const int kind0 = pl->kind0;
+  const int cnt = pl->cnt[ell], m = pl->m[ell];
+  if (carries_of(cnt, m, c.slots, ell == c.levels - 1) == 0) return;
+  const Ladder lad = ladder_of(c, ladder);
   uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
-  const int tok_bytes = (2 * r.tokens + 15) & ~15;
-  if (kind0 == 0 && ((carry && ell == 0) || (fin && ell == 1))) {
-    const int mt = pl->m_tok;
-    const LOGKV_G uint16_t* src = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
-    for (int i = threadIdx.x; i < mt; i += kThreads) tok[i] = src[i];
-    __syncthreads();
-  }
-  Src flush_rows{};
-  flush_rows.kind = 0;
-  flush_rows.tok = (const LOGKV_S uint16_t*)tok + pl->first;
-  flush_rows.order_base = pl->order_base;
-  flush_rows.kb = gp(r.k + b * r.k_sb + g * r.k_sg);
-  flush_rows.vb = gp(r.v + b * r.v_sb + g * r.v_sg);
-  flush_rows.k_st = r.k_st;
-  flush_rows.v_st = r.v_st;
-  flush_rows.posb = gp(r.pos + b * r.pos_sb);
-  auto staged = [&](int e) {
-    Src s{};
-    s.kind = 1;
-    s.buf = e == 0 ? sc.s0 : sc.carry[(e - 1) % 3];
-    return s;
-  };
-  if (fin) {
-    const int e = ell - 1;
-    const int cnt = pl->cnt[e], m = pl->m[e];
-    const int n = (e == 0 && kind0 == 0) ? level_finish<0>(lad, e, cnt, flush_rows, m, e == L - 1)
-                                         : level_finish<1>(lad, e, cnt, staged(e), m, e == L - 1);
-    if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * L + e] = static_cast<int16_t>(n);
-  }
-  if (carry) {
-    const int cnt = pl->cnt[ell], m = pl->m[ell];
-    uint8_t* stage = dyn + tok_bytes;
-    const bool beta = prm.beta_merge != 0;
-    if (ell == 0 && kind0 == 0)
-      level_carries<0>(lad, ell, cnt, flush_rows, m, sc.carry[0], beta, stage, part, parts);
-    else
-      level_carries<1>(lad, ell, cnt, staged(ell), m, sc.carry[ell % 3], beta, stage, part, parts);
-  }
+  uint8_t* stage = dyn + ((2 * r.tokens + 15) & ~15);
+  const bool beta = prm.beta_merge != 0;
+  const Soa out = carry_of(ws, ladder, ell, c.dk, c.dv);
+  if (ell == 0 && pl->kind0 == 0)
+    level_carries<0, NJ>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, tok), m, out, beta, stage, part, parts);
+  else
+    level_carries<1, NJ>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m, out, beta, stage, part, parts);
 }
 
-constexpr int kParts = 16;   // blocks per ladder for level 0's carries (halved per level)
+// Slot writes of every level (block (ladder, level)): fill, move and clear, or
+// top fold. A level's writes read only its own stored slots and its staged
+// rows (the previous level's carries), so the levels run side by side.
+__global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs r, Workspace ws) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  const int ladder = blockIdx.x, ell = blockIdx.y;
+  const LadderPlan* pl = ws.plans + ladder;
+  if (!pl->active) return;
+  const int cnt = pl->cnt[ell], m = pl->m[ell];
+  if (m == 0) return;
+  const Ladder lad = ladder_of(c, ladder);
+  const bool top = ell == c.levels - 1;
+  int n;
+  if (ell == 0 && pl->kind0 == 0)
+    n = level_finish<0>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m, top);
+  else
+    n = level_finish<1>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m, top);
+  if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * c.levels + ell] = static_cast<int16_t>(n);
+}
+
+constexpr int kParts = 32;   // blocks per ladder for level 0's carries (halved per level)
 
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
@@ -1068,15 +1074,22 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
     return LOGKV_ERUNTIME;
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
-  const size_t level_shmem = tok_bytes + (p.beta_merge ? static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)) : 0);
-  if (level_shmem > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&level_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(level_shmem)) != hipSuccess)
+  const size_t carry_shmem = tok_bytes + (p.beta_merge ? static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)) : 0);
+  const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
+  const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
+                               : reinterpret_cast<const void*>(&carries_kernel<4>);
+  if (carry_shmem > 64 * 1024 &&
+      hipFuncSetAttribute(carries, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(carry_shmem)) !=
+          hipSuccess)
     return LOGKV_ERUNTIME;
-  for (int ell = 0; ell <= c.levels; ++ell) {
-    const int parts = ell < c.levels ? std::max(1, kParts >> ell) : 1;
-    hipLaunchKernelGGL(level_kernel, dim3(ladders, parts), dim3(kThreads), level_shmem, stream, c, r, p, ws, ell);
+  for (int ell = 0; ell + 1 < c.levels; ++ell) {
+    const dim3 grid(ladders, std::max(1, kParts >> ell));
+    if (narrow)
+      hipLaunchKernelGGL(carries_kernel<2>, grid, dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
+    else
+      hipLaunchKernelGGL(carries_kernel<4>, grid, dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
   }
+  hipLaunchKernelGGL(finish_kernel, dim3(ladders, c.levels), dim3(kThreads), tok_bytes, stream, c, r, ws);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

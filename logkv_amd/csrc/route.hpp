@@ -46,15 +46,14 @@ struct Workspace {
   uint8_t* snap_alive; // [lanes, K] alive flags at the start of the flush
   uint8_t* ladder;     // per-ladder carry / staging rows
   int64_t ladder_stride;  // bytes per ladder
-  int64_t s0_rows, carry_rows[3];
+  int64_t s0_rows;        // delayed-archive staging rows per ladder
+  int64_t m0_cap;         // most rows staged at level 0 (sizes the per-level carry buffers)
   int32_t sort_width;     // keys per block for the delayed-archive sort (0 without it)
   LadderPlan* plans;      // [ladders]
   uint16_t* tok;          // [ladders, T] each ladder's flush rows in position order
 };
 
-int64_t ladder_scratch_rows(int64_t m0, int64_t& s0, int64_t* carry, int64_t existing);
-int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, const int64_t* carry);
-int64_t row_bytes(int dk, int dv);
+int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t m0);
 int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                  hipStream_t stream);
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream);
