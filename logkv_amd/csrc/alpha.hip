@@ -21,7 +21,6 @@ namespace logkv {
 namespace {
 
 constexpr int kMaxGroups = 16;
-constexpr int kJ = kMaxDim / kWave;
 
 struct Rows2 {
   const LOGKV_G uint16_t* pool;
@@ -35,11 +34,13 @@ struct Rows2 {
   }
 };
 
-__device__ __forceinline__ float canon_sum(const float* t, int J) {
+// Canonical feature sum: lane l adds its features l, l + 64, ... in order,
+// then the wave adds the lanes (wave_sum0). NJ = features per lane.
+template <int NJ>
+__device__ __forceinline__ float canon_sum(const float* t) {
   float s = t[0];
 #pragma unroll
-  for (int j = 1; j < kJ; ++j)
-    if (j < J) s = s + t[j];
+  for (int j = 1; j < NJ; ++j) s = s + t[j];
   return wave_sum0(s);
 }
 
@@ -48,48 +49,50 @@ constexpr int kTokBatch = 8;   // span rows whose loads are issued together
 // Token statistics of one component over a span: means (per lane features),
 // energy E and mean square of the means; returns R = residual / energy. Rows
 // are loaded kTokBatch at a time and then added in span order.
+template <int NJ>
 __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, const LOGKV_G int32_t* tok, int n,
                                                 int D, float* mean, float& energy, float& msq) {
-  const int l = lane_id(), J = (D + kWave - 1) / kWave;
-  float acc[kJ], e = 0.f;
+  const int l = lane_id();
+  float acc[NJ], e = 0.f;
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) acc[j] = 0.f;
+  for (int j = 0; j < NJ; ++j) acc[j] = 0.f;
   const float d_f = static_cast<float>(D);
   for (int i0 = 0; i0 < n; i0 += kTokBatch) {
-    float xb[kTokBatch][kJ];
+    float xb[kTokBatch][NJ];
 #pragma unroll
     for (int t = 0; t < kTokBatch; ++t) {
       const int i = i0 + t < n ? i0 + t : n - 1;
       const LOGKV_G uint16_t* row = src.row(b, g, tok[i]);
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) xb[t][j] = j < J ? feat_or_zero(row, l + j * kWave, D) : 0.f;
+      for (int j = 0; j < NJ; ++j) xb[t][j] = feat_or_zero(row, l + j * kWave, D);
     }
 #pragma unroll
     for (int t = 0; t < kTokBatch; ++t) {
       const int i = i0 + t;
       if (i >= n) break;
-      float sq[kJ];
+      float sq[NJ];
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         sq[j] = xb[t][j] * xb[t][j];
         acc[j] = i == 0 ? xb[t][j] : acc[j] + xb[t][j];
       }
-      const float ms = canon_sum(sq, J) / d_f;
+      const float ms = canon_sum<NJ>(sq) / d_f;
       e = i == 0 ? ms : e + ms;
     }
   }
   const float cnt = static_cast<float>(n);
-  float m2[kJ];
+  float m2[NJ];
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     mean[j] = acc[j] / cnt;
     m2[j] = (l + j * kWave < D) ? mean[j] * mean[j] : 0.f;
   }
   energy = e / cnt;
-  msq = canon_sum(m2, J) / d_f;
+  msq = canon_sum<NJ>(m2) / d_f;
   return fmaxf(energy - msq, 0.f) / fmaxf(energy, 1e-12f);
 }
 
+template <int NJ>
 __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, float* __restrict__ out) {
   __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
   const int s = blockIdx.x;
@@ -102,27 +105,26 @@ __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_ar
   if (g < G && n > 0) {
     Rows2 ks{gp(a.pool_k), a.pk_sb, a.pk_sg, a.pk_st, gp(a.flush_k), a.fk_sb, a.fk_sg, a.fk_st, a.old_width};
     Rows2 vs{gp(a.pool_v), a.pv_sb, a.pv_sg, a.pv_st, gp(a.flush_v), a.fv_sb, a.fv_sg, a.fv_st, a.old_width};
-    float mean_k[kJ], mean_v[kJ], e_k, e_v, msq_k, msq_v;
-    const float rk = span_component(ks, b, g, tok, n, a.dk, mean_k, e_k, msq_k);
-    const float rv = span_component(vs, b, g, tok, n, a.dv, mean_v, e_v, msq_v);
+    float mean_k[NJ], mean_v[NJ], e_k, e_v, msq_k, msq_v;
+    const float rk = span_component<NJ>(ks, b, g, tok, n, a.dk, mean_k, e_k, msq_k);
+    const float rv = span_component<NJ>(vs, b, g, tok, n, a.dv, mean_v, e_v, msq_v);
     float q = 0.f;
     if (a.beta_novelty) {
-      const int l = lane_id(), J = (a.dk + kWave - 1) / kWave;
+      const int l = lane_id();
       const LOGKV_G float* mu = gp(a.centroids) + (static_cast<int64_t>(b) * G + g) * a.k_max * a.dk;
       const LOGKV_G uint8_t* valid = gp(a.centroid_valid) + (static_cast<int64_t>(b) * G + g) * a.k_max;
       float nearest = __builtin_inff();
       bool any = false;
       for (int c = 0; c < a.k_max; ++c) {
-        float dt[kJ], cc[kJ];
+        float dt[NJ], cc[NJ];
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          const int d = l + j * kWave;
-          const float m = feat_or_zero(mu + c * a.dk, d, a.dk);
+        for (int j = 0; j < NJ; ++j) {
+          const float m = feat_or_zero(mu + c * a.dk, l + j * kWave, a.dk);
           dt[j] = mean_k[j] * m;
           cc[j] = m * m;
         }
-        const float dot = canon_sum(dt, J) / static_cast<float>(a.dk);
-        const float cms = canon_sum(cc, J) / static_cast<float>(a.dk);
+        const float dot = canon_sum<NJ>(dt) / static_cast<float>(a.dk);
+        const float cms = canon_sum<NJ>(cc) / static_cast<float>(a.dk);
         const float dist = fmaxf((msq_k + cms) - 2.0f * dot, 0.f);
         if (valid[c]) {
           any = true;
@@ -212,7 +214,10 @@ __global__ __launch_bounds__(256) void partition_kernel(logkv_partition_args a) 
 
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
   if (a.n_spans <= 0) return LOGKV_OK;
-  hipLaunchKernelGGL(score_kernel, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
+  if (a.dk <= 2 * kWave && a.dv <= 2 * kWave)
+    hipLaunchKernelGGL(score_kernel<2>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
+  else
+    hipLaunchKernelGGL(score_kernel<4>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
