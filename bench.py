@@ -18,8 +18,8 @@ masses ~ U(1, 64). A step attends one new token per sequence with the packed
 prefix reused, as in the reference's decode loop.
 
 Prints one JSON line: flushed tokens/s over the timed steps, the roofline of
-the dominant kernel (the per-ladder commit) from HIP events on its stream over
-the timed region, decode ms/token with its own roofline, and the oracle's CPU
+the dominant stage (the ladder commit: its prepare, per-level carries and
+finish launches) from HIP events on its stream over the timed region, decode ms/token with its own roofline, and the oracle's CPU
 throughput on a bounded sample of the flush workload.
 """
 
@@ -40,7 +40,7 @@ G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
 EXACT, SPAN = 256, 64
 
 
-def ladder_rows(counts, m, B, L):
+def ladder_rows(counts, m, B, L, staged_tokens=True):
     """(entry rows read, entry rows written, staged token rows read) of one Fenwick append.
 
     Count model of the reference append (litgpt/log_kv_cache.py:1815-1929): fill
@@ -51,7 +51,7 @@ def ladder_rows(counts, m, B, L):
     """
     counts = list(counts)
     rd = wr = tok = 0
-    staged_is_tokens = True
+    staged_is_tokens = staged_tokens
     for ell in range(L):
         if m == 0:
             break
@@ -97,24 +97,56 @@ def ladder_rows(counts, m, B, L):
     return rd, wr, tok
 
 
-def commit_bytes(before_counts, before_alive, m_rows, B, L, dk, dv):
-    """Algorithmic HBM bytes of one commit launch, from the state before it and rows per ladder.
+def commit_bytes(counts, alive, p_hi, assign, order, positions, n_rows, B, L, dk, dv):
+    """Algorithmic HBM bytes of one commit (all its launches), from the ladder state before it
+    and the attach decisions.
 
-    Entry = K and V bf16 + w f32 + p_lo, p_hi, sum_wp, order i64 + pad flag;
-    token row = K and V bf16 + position i64; plus the center read and write."""
+    Entry = K and V bf16 + w f32 + p_lo, p_hi, sum_wp, order i64 + pad flag; token row =
+    K and V bf16 + position i64. Per ladder with new rows: a dead cluster clears its L*B'
+    entries and opens with one row; a delayed-archive ladder (first new position below
+    its p_hi) reads its entries and the new rows into staging (written as entries),
+    clears every slot and re-appends everything from level 0; otherwise the new rows
+    are appended (count model above). Plus the center: new keys read, center read and
+    written."""
     import numpy as np
 
     entry = 2 * (dk + dv) + 4 + 4 * 8 + 1
     token = 2 * (dk + dv) + 8
+    n_batch, groups, K = alive.shape
     total = 0
-    for idx in map(tuple, np.argwhere(m_rows > 0)):
-        m = int(m_rows[idx])
-        counts = before_counts[idx]
-        if not before_alive[idx]:
-            total += L * B * entry            # clear of the newly opened cluster
-            counts = [0] * L
-        rd, wr, tok = ladder_rows(counts, m, B, L)
-        total += (rd + wr) * entry + tok * token + 2 * dk * 4
+    for b in range(n_batch):
+        n = int(n_rows[b])
+        rows_pos = positions[b][order[b][:n]]
+        for g in range(groups):
+            a = assign[b, g, :n]
+            for c in range(K):
+                sel = np.nonzero(a == c)[0]
+                m = len(sel)
+                if m == 0:
+                    continue
+                cnt = [int(x) for x in counts[b, g, c]]
+                pos = rows_pos[sel]
+                nn = m
+                if not alive[b, g, c]:
+                    total += L * B * entry + token + entry
+                    cnt = [1] + [0] * (L - 1)
+                    nn = m - 1
+                    hi = int(pos[0])
+                    first = 1
+                else:
+                    hi = int(p_hi[b, g, c])
+                    first = 0
+                total += nn * 2 * dk + 2 * dk * 4
+                if nn == 0:
+                    continue
+                if int(pos[first]) < hi:
+                    n_exist = sum(cnt)
+                    staged = n_exist + nn
+                    total += n_exist * entry + nn * token + staged * entry + L * B * entry
+                    rd, wr, tok = ladder_rows([0] * L, staged, B, L, staged_tokens=False)
+                else:
+                    rd, wr, tok = ladder_rows(cnt, nn, B, L)
+                total += (rd + wr) * entry + tok * token
     return total
 
 
@@ -122,12 +154,11 @@ def progress(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def span_ends_for(flush, rate=1 / 24, seed=99):
-    """Seeded natural span boundaries of the stream's flush ``flush`` (same for every layer)."""
-    import numpy as np
-
-    rng = np.random.default_rng(seed + flush)
-    return [(rng.random(F) < rate).tolist()]
+def span_ends_for(flush, batch=1):
+    """Natural span boundaries of the stream's flush ``flush`` (same for every layer): row
+    ``p`` of batch row ``b`` ends a span when ``(p + 7*b) % 32 == 0``, the rule of the
+    reference's benchmark harness (unused/benchmark_log_kv_unified.py:36-40)."""
+    return [[(p + 7 * b) % 32 == 0 for p in range(flush * F, (flush + 1) * F)] for b in range(batch)]
 
 
 def cpu_baseline(seconds: float):
@@ -167,9 +198,10 @@ def cpu_baseline(seconds: float):
 
 
 class CommitMeter:
-    """Wraps a cache's route+commit so the commit launch is bracketed by HIP events on its
-    stream, with the ladder counts it starts from copied aside on the device (no host sync);
-    algorithmic bytes are computed from those copies after the timed region."""
+    """Wraps a cache's route+commit so that the commit's launches are bracketed by HIP
+    events on their stream, with the ladder state they start from copied aside on the
+    device and the attach decisions kept (no host sync); algorithmic bytes are computed
+    from those copies after the timed region."""
 
     def __init__(self, cache, torch):
         self.cache, self.torch = cache, torch
@@ -179,27 +211,32 @@ class CommitMeter:
         from logkv_amd._lib import check, lib, ptr, stream_of
 
         cache, torch = self.cache, self.torch
-        snap = (cache.level_count.clone(), cache.alive.clone(), cache.n_total.clone())
+        dev = k_raw.device
+        snap = (cache.level_count.clone(), cache.alive.clone(), cache.p_hi_c.clone())
+        assign = torch.empty(cache.batch_size, cache.n_groups, k_raw.size(2), dtype=torch.int8, device=dev)
+        order = torch.empty(cache.batch_size, k_raw.size(2), dtype=torch.int32, device=dev)
         view = cache._ladder_view()
         rows = cache._rows_view(k_raw, v, positions, counts)
         ws = cache._workspace_for(view, rows.tokens)
-        sp = stream_of(k_raw.device)
-        stream = torch.cuda.current_stream(k_raw.device)
+        sp = stream_of(dev)
+        stream = torch.cuda.current_stream(dev)
         check(lib().logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
-                                        ptr(assign_out), ptr(order_out), sp), "attach")
+                                        ptr(assign), ptr(order), sp), "attach")
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ev[0].record(stream)
         check(lib().logkv_commit_only(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
-                                      ptr(assign_out), ptr(order_out), sp), "commit")
+                                      ptr(assign), ptr(order), sp), "commit")
         ev[1].record(stream)
-        self.records.append((snap, cache.n_total.clone(), ev))
+        n_rows = counts if counts is not None else torch.full((cache.batch_size,), k_raw.size(2), device=dev)
+        self.records.append((snap, assign, order, positions, n_rows, ev))
 
     def results(self, B_, L_):
         out = []
-        for (counts, alive, n0), n1, ev in self.records:
-            m = (n1.long() - n0.long()).cpu().numpy()
-            out.append((commit_bytes(counts.long().cpu().numpy(), alive.cpu().numpy(), m, B_, L_, D, D),
-                        ev[0].elapsed_time(ev[1])))
+        for (counts, alive, p_hi), assign, order, positions, n_rows, ev in self.records:
+            nb = commit_bytes(counts.long().cpu().numpy(), alive.cpu().numpy(), p_hi.cpu().numpy(),
+                              assign.cpu().numpy(), order.long().cpu().numpy(), positions.cpu().numpy(),
+                              n_rows.cpu().numpy(), B_, L_, D, D)
+            out.append((nb, ev[0].elapsed_time(ev[1])))
         return out
 
 
@@ -281,7 +318,8 @@ def flush_workload(args, torch, np):
                    "slots_per_level": caches[0].B_prime, "levels": caches[0].L_alloc, "exact_tokens": EXACT,
                    "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
                    "pooled_width_after_last_flush": widths[0]},
-        "roofline": {"kernel": "commit_kernel", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+        "roofline": {"kernel": "commit: commit_kernel + carries_kernel per level + finish_kernel", "bound": "hbm",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
                      "launches": len(rec)},
@@ -401,7 +439,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16 storage, f32 math",
         "data": "synthetic seeded Gaussian mixture (12 centers N(0,1)*4, noise 0.5, 10% outliers N(0,1)*12), "
-                "seeded span ends (rate 1/24)",
+                "span ends where (p + 7b) % 32 == 0",
         "config": fl["config"],
         "roofline": fl["roofline"],
     }
