@@ -7,17 +7,30 @@ has no CPU fallback.
 
 Modules and what pins them (the tests named in brackets):
 * ``numerics`` - bf16 rounding and the canonical float32 reduction orders
-  [tests/test_oracle_numerics.py: torch's bf16 cast, float64 sums];
-* ``route`` - attach decisions and commit grouping [tests/test_oracle_route.py:
-  float64 brute force with decision margins, invariants];
+  [tests/test_oracle_numerics.py: torch's bf16 cast, the 64-lane xor
+  butterfly, float64 sums];
+* ``route`` - attach decisions and seeding [tests/test_oracle_route.py: float64
+  brute force on rows with a clear decision margin, farthest-point seeds,
+  invariants];
 * ``ladder`` - pair / Beta / fold merges, Fenwick append, centroid update
-  [tests/test_oracle_ladder.py: the reference's known answers, the scalar
-  one-entry-at-a-time rule, mass and position conservation, float64 centroid];
+  [tests/test_oracle_ladder.py: the reference's known answers, the reference's
+  scalar one-entry-at-a-time rule, mass and position conservation, Beta
+  optimality, float64 centroid];
 * ``spans`` - Alpha span cutting, scoring and greedy choice
-  [tests/test_oracle_spans.py: the reference's known answers, closed forms];
+  [tests/test_spans_host.py and tests/test_oracle_spans.py: the reference's
+  known answers (whole spans, pending tails, novelty rescue, top-2 groups),
+  exact closed forms, float64 scores];
 * ``readout`` - attention plan, pack, attention [tests/test_oracle_readout.py:
-  known anchors, textbook softmax, duplicated-token equivalence];
-* ``cache`` - one layer's cache and flush driver [tests/test_oracle_cache.py].
+  known anchors, explicit RoPE and mask rows, mass slot = duplicated tokens,
+  float64 masked softmax];
+* ``cache`` - one layer's cache and flush driver [tests/test_oracle_cache.py:
+  delayed-archive known answer, budget closed form, streaming invariants].
+
+Parity unpinned: the last-ulp agreement with the reference's own float traces
+where it leaves the order to a library (Torch GEMM / cdist / segment_reduce
+summation orders, Flash SDPA). No reference code was imported or run; the
+checks above pin the formulas, the known answers and the invariants, and the
+oracle fixes one order that the device reproduces bit for bit.
 """
 
 from .cache import OracleCache, budget  # noqa: F401
