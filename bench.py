@@ -356,18 +356,19 @@ def decode_workload(args, torch, np):
     va = torch.empty_like(ka)
     # Packed prefix once (the first decode step after a flush), then one new row per step.
     _launch_pack(cache, view, plan, ks[0], vs[0], dim, ka, va, False, 0)
-    tail = cache.alpha_count + cache.recent_count + 1
+    recent = cache.recent_count
+    tail = recent + 1
     stream = torch.cuda.current_stream(dev)
     workspace = None
     events = []
 
     def step(i, timed):
         nonlocal workspace
-        _launch_pack(cache, view, plan, ks[i], vs[i], dim, ka, va, True, cache.alpha_count + cache.recent_count)
+        _launch_pack(cache, view, plan, ks[i], vs[i], dim, ka, va, True, recent)
         if timed:
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             ev[0].record(stream)
-        _, workspace = packed_attention(qs[i], ka, va, plan, tail, scale, 1, D, G, workspace)
+        _, workspace = packed_attention(qs[i], ka, va, plan, tail, scale, 1, D, G, workspace, cache.alpha_count_dev)
         if timed:
             ev[1].record(stream)
             events.append(ev)
@@ -383,7 +384,7 @@ def decode_workload(args, torch, np):
     progress(f"decode: {steps} steps in {elapsed:.3f} s")
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     width = plan.width
-    rows = width + tail
+    rows = width + cache.alpha_count + tail
     lanes = Bt * G
     # Algorithmic bytes: every packed K and V row of every lane once, queries and outputs.
     attn_bytes = lanes * rows * dim * 2 * 2 + Bt * HQ * D * 2 * 2

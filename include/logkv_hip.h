@@ -124,12 +124,53 @@ typedef struct logkv_span_args {
   const uint8_t* centroid_valid;
   int32_t k_max;
   int32_t beta_novelty;
+  const int32_t* n_spans_dev;  /* optional: only the first *n_spans_dev of the n_spans spans are scored */
 } logkv_span_args;
 
 /* Score of every candidate span (f32 [n_spans]): Alpha's normalised K/V
  * variance, or with beta_novelty the top-2 group mean of variance + novelty.
  * Replaces score_spans (litgpt/alpha_log_kv.py:125-174). */
 int logkv_score_spans(const logkv_span_args* args, float* scores, void* stream);
+
+/* Span selection of one Alpha flush on the device, with no host round trip:
+ * the candidate whole spans of [exact pool | flush] (pool width = budget P),
+ * their scores, and the bounded greedy choice. The current selection is
+ * span_len / span_closed [n_batch, P] with span_count [n_batch]; the pool's
+ * rows are those spans' tokens in order, at positions pool_pos [n_batch, P].
+ * New rows: positions new_pos and boundary flags ends [n_batch, T]. `rows`
+ * carries the K/V sources, groups, widths and centers for scoring (its
+ * old_width must be P; its token tables are filled here). Outputs: keep
+ * [n_batch, P] and archive [n_batch, P + T] source rows (indices into
+ * [pool (P rows) | flush], -1 past the end), archive_count [n_batch], the new
+ * selection's spans, alpha_count[0] = the largest kept count, and optionally
+ * the candidates' scores. At most 4096 candidates per batch row.
+ * Replaces the selection of _alpha_route_flush (litgpt/log_kv_cache.py:
+ * 3904-3940): cut_spans, score_spans and choose_spans
+ * (litgpt/alpha_log_kv.py:16-226). */
+typedef struct logkv_alpha_select_args {
+  const int32_t* span_len;
+  const uint8_t* span_closed;
+  const int32_t* span_count;
+  const int64_t* pool_pos;
+  const int64_t* new_pos;
+  int64_t np_sb;
+  const uint8_t* ends;
+  int64_t ends_sb;
+  int32_t tokens;
+  int32_t n_batch, budget, max_span;
+  logkv_span_args rows;
+  int32_t* keep;
+  int32_t* archive;
+  int32_t* archive_count;
+  int32_t* new_span_len;
+  uint8_t* new_span_closed;
+  int32_t* new_span_count;
+  int32_t* alpha_count;
+  float* scores;
+} logkv_alpha_select_args;
+
+int64_t logkv_alpha_select_workspace_bytes(const logkv_alpha_select_args* args);
+int logkv_alpha_select(const logkv_alpha_select_args* args, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Exact-pool rewrite and archive gather over the same virtual rows: keep
  * [n_batch, P] and archive [n_batch, A] list source rows (-1 = zero row).
@@ -167,9 +208,11 @@ int logkv_alpha_partition(const logkv_partition_args* args, void* stream);
 
 /* Read-only view of one cache for the attention readout. Ladder fields as in
  * logkv_ladder_view; exact pool alpha_* [n_batch, G, alpha_cap, d] with
- * positions / valid flags [n_batch, alpha_cap]; recent window (post-RoPE keys)
- * [n_batch, G, recent_cap, d]; RoPE tables cos / sin [positions, rope_n] f32 or
- * bf16 (table_bf16 = 1) with element strides. */
+ * positions / valid flags [n_batch, alpha_cap] and alpha_count rows in use
+ * (read from alpha_count_dev when that is not NULL, so a flush that chose the
+ * exact pool on the device needs no host read); recent window (post-RoPE
+ * keys) [n_batch, G, recent_cap, d]; RoPE tables cos / sin [positions, rope_n]
+ * f32 or bf16 (table_bf16 = 1) with element strides. */
 typedef struct logkv_readout_view {
   const uint16_t* level_k;
   const uint16_t* level_v;
@@ -190,6 +233,7 @@ typedef struct logkv_readout_view {
   int64_t cos_s0, cos_s1, sin_s0, sin_s1;
   int32_t rope_n, table_bf16;
   int64_t rope_rows;  /* positions in the tables; anchors beyond clamp to the last row */
+  const int32_t* alpha_count_dev;
 } logkv_readout_view;
 
 /* Ints of the plan table: per lane K*L + 1 pooled-row offsets (clusters in
@@ -201,9 +245,9 @@ int64_t logkv_plan_table_ints(const logkv_readout_view* cache);
 int logkv_mid_plan(const logkv_readout_view* cache, int32_t* table, void* stream);
 
 /* Packed rows [pooled (width) | exact | recent | current] into out_k / out_v
- * [n_batch, G, out_cap, dim] bf16. With skip_pooled, only rows from tail_start
- * of the [exact | recent | current] tail are written (a decode step re-packs
- * only its new rows). Current K/V [n_batch, G, cur_len, d] strided.
+ * [n_batch, G, out_cap, dim] bf16. With skip_pooled, only the rows from
+ * recent window row recent_start on are written (a decode step re-packs only
+ * its new rows). Current K/V [n_batch, G, cur_len, d] strided.
  * Replaces pack / pack_mid_kv (litgpt/log_kv_pack_triton.py:95-125,
  * litgpt/log_kv_pack.py:105-133). */
 typedef struct logkv_pack_args {
@@ -215,14 +259,15 @@ typedef struct logkv_pack_args {
   uint16_t* out_k;
   uint16_t* out_v;
   int32_t out_cap, dim;
-  int32_t skip_pooled, tail_start;
+  int32_t skip_pooled, recent_start;
 } logkv_pack_args;
 
 int logkv_pack(const logkv_readout_view* cache, const logkv_pack_args* args, const int32_t* table, void* stream);
 
 /* Attention of queries q [n_batch, n_heads, tq, dk] (post-RoPE, bf16, strided)
  * over the packed rows k / v [n_batch, G, cap, dim]: pooled width (read from
- * the plan table) + `tail` rows, the last causal_tail rows causal; out
+ * the plan table) + `tail` rows (+ *alpha_count_dev when that is not NULL),
+ * the last causal_tail rows causal; out
  * [n_batch, n_heads, tq, dv] bf16 strided. inv_scale_bf16 is 1/scale rounded
  * to bf16 (the packed query's bias coordinate).
  * Replaces the Flash SDPA call on the packed workspace
@@ -240,6 +285,7 @@ typedef struct logkv_attention_args {
   float scale, inv_scale_bf16;
   uint16_t* out;
   int64_t o_sb, o_sh, o_st;
+  const int32_t* alpha_count_dev;
 } logkv_attention_args;
 
 int64_t logkv_attention_workspace_bytes(const logkv_attention_args* args);

@@ -54,6 +54,17 @@ class SpanArgs(C.Structure):
         ("old_width", _i32), ("tokens", _p), ("span_offsets", _p), ("span_rows", _p), ("n_spans", _i32),
         ("n_groups", _i32), ("dk", _i32), ("dv", _i32),
         ("centroids", _p), ("centroid_valid", _p), ("k_max", _i32), ("beta_novelty", _i32),
+        ("n_spans_dev", _p),
+    ]
+
+
+class AlphaSelectArgs(C.Structure):
+    _fields_ = [
+        ("span_len", _p), ("span_closed", _p), ("span_count", _p), ("pool_pos", _p),
+        ("new_pos", _p), ("np_sb", _i64), ("ends", _p), ("ends_sb", _i64), ("tokens", _i32),
+        ("n_batch", _i32), ("budget", _i32), ("max_span", _i32), ("rows", SpanArgs),
+        ("keep", _p), ("archive", _p), ("archive_count", _p), ("new_span_len", _p), ("new_span_closed", _p),
+        ("new_span_count", _p), ("alpha_count", _p), ("scores", _p),
     ]
 
 
@@ -81,7 +92,7 @@ class ReadoutView(C.Structure):
         ("alpha_cap", _i32), ("alpha_count", _i32),
         ("recent_k", _p), ("recent_v", _p), ("recent_cap", _i32), ("recent_count", _i32),
         ("cos", _p), ("sin", _p), ("cos_s0", _i64), ("cos_s1", _i64), ("sin_s0", _i64), ("sin_s1", _i64),
-        ("rope_n", _i32), ("table_bf16", _i32), ("rope_rows", _i64),
+        ("rope_n", _i32), ("table_bf16", _i32), ("rope_rows", _i64), ("alpha_count_dev", _p),
     ]
 
 
@@ -90,7 +101,7 @@ class PackArgs(C.Structure):
         ("cur_k", _p), ("ck_sb", _i64), ("ck_sg", _i64), ("ck_st", _i64),
         ("cur_v", _p), ("cv_sb", _i64), ("cv_sg", _i64), ("cv_st", _i64),
         ("cur_len", _i32), ("out_k", _p), ("out_v", _p), ("out_cap", _i32), ("dim", _i32),
-        ("skip_pooled", _i32), ("tail_start", _i32),
+        ("skip_pooled", _i32), ("recent_start", _i32),
     ]
 
 
@@ -100,7 +111,7 @@ class AttentionArgs(C.Structure):
         ("n_batch", _i32), ("n_heads", _i32), ("n_groups", _i32), ("tq", _i32), ("dk", _i32), ("dv", _i32),
         ("dim", _i32), ("k", _p), ("v", _p), ("cap", _i32), ("tail", _i32), ("causal_tail", _i32),
         ("scale", C.c_float), ("inv_scale_bf16", C.c_float),
-        ("out", _p), ("o_sb", _i64), ("o_sh", _i64), ("o_st", _i64),
+        ("out", _p), ("o_sb", _i64), ("o_sh", _i64), ("o_st", _i64), ("alpha_count_dev", _p),
     ]
 
 
@@ -116,6 +127,8 @@ SIGNATURES = {
                                  _p, _i64, _p, _p, _p]),
     "logkv_score_spans": (_i32, [C.POINTER(SpanArgs), _p, _p]),
     "logkv_alpha_partition": (_i32, [C.POINTER(PartitionArgs), _p]),
+    "logkv_alpha_select_workspace_bytes": (_i64, [C.POINTER(AlphaSelectArgs)]),
+    "logkv_alpha_select": (_i32, [C.POINTER(AlphaSelectArgs), _p, _i64, _p]),
     "logkv_plan_table_ints": (_i64, [C.POINTER(ReadoutView)]),
     "logkv_mid_plan": (_i32, [C.POINTER(ReadoutView), _p, _p]),
     "logkv_pack": (_i32, [C.POINTER(ReadoutView), C.POINTER(PackArgs), _p, _p]),

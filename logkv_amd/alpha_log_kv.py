@@ -1,14 +1,16 @@
 """Alpha exact spans: whole-span candidates, device scoring, bounded greedy choice.
 
 Call surface of the reference module (litgpt/alpha_log_kv.py): ``SpanSelection``,
-``SpanCut``, ``cut_spans``, ``score_spans``, ``choose_spans``, ``select_spans``.
-Span cutting and the greedy choice are host logic over host position /
-boundary lists, as in the reference; scoring runs in the HIP library
-(``logkv_score_spans``) and the exact-pool / archive split in
-``logkv_alpha_partition``.
+``SpanCut``, ``cut_spans``, ``score_spans``, ``choose_spans``, ``select_spans``
+- host span cutting and greedy choice over host position / boundary lists, as
+in the reference, with scoring in the HIP library (``logkv_score_spans``).
+Indices there refer to ``[old exact pool (old_width rows) | current flush]``.
 
-Indices refer to the virtual row sequence ``[old exact pool (old_width rows) |
-current flush]`` shared by the KV groups of a batch row.
+A cache's flush (``alpha_flush``) runs the same selection on the device
+instead (``logkv_alpha_select``: candidates, scores and greedy against the
+selection state the cache keeps on the device), then the exact-pool / archive
+split (``logkv_alpha_partition``); there indices address ``[pool (P rows) |
+flush]``.
 """
 
 from __future__ import annotations
@@ -255,59 +257,74 @@ def _table(rows, width, device):
     return torch.from_numpy(t).pin_memory().to(device, non_blocking=True)
 
 
+def _pinned_upload(array: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(array).pin_memory().to(device, non_blocking=True)
+
+
 @torch.no_grad()
 def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
-    """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003).
+    """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003), all on the device.
 
-    Scores the whole candidate spans of ``[exact pool | flush]`` on the device,
-    reads the scores back once, chooses spans on the host, rewrites the exact
-    pool (into the cache's second pool buffer set, then swapped in) and archives
-    the rest, which is attach-routed with delayed joins.
+    The span selection (candidates of ``[exact pool | flush]``, scores, bounded
+    greedy) runs in ``logkv_alpha_select`` against the selection state the
+    cache keeps on the device, so the flush never waits for the host; the
+    exact pool is rewritten into the cache's second buffer set (then swapped)
+    and the archived rows are attach-routed with delayed joins. Only the
+    boundary flags travel from the host. Row indices address
+    ``[pool (P rows) | flush]``; ``positions_host`` is not needed.
     """
     if span_ends is None:
         raise ValueError("AlphaLogKV requires natural span boundaries")
     dev = k_raw.device
     n_batch, G = cache.batch_size, cache.n_groups
     P = cache.alpha_exact_tokens
-    old_width = cache.alpha_count
-    if positions_host is None:
-        positions_host = positions.cpu().tolist()
-    cut = cut_spans(cache._alpha_spans, cache._alpha_positions, positions_host, span_ends, old_width,
-                    cache.alpha_span_max_tokens)
-    if cut is None:
-        sel = SpanSelection([[] for _ in range(n_batch)], [[] for _ in range(n_batch)],
-                            [[] for _ in range(n_batch)], [[] for _ in range(n_batch)])
-    else:
-        scores = score_spans_split(cache.alpha_k_raw, cache.alpha_v, k_raw, v, old_width, cut,
-                                   beta_novelty=cache.beta_novelty, centroids=cache.centroid,
-                                   centroid_valid=cache.alive)
-        sel = choose_spans(cut, scores.cpu().tolist(), P)
-    cache._last_selection = sel
-    counts = [len(a) for a in sel.archive]
-    A = max(counts, default=0)
-    keep_t = _table(sel.keep, P, dev)
-    arch_t = _table(sel.archive, A, dev)
-    nk, nv, npos, nvalid = cache._alpha_spare
-    ak = torch.empty(n_batch, G, max(A, 1), cache.k_dim, dtype=k_raw.dtype, device=dev)
-    av = torch.empty(n_batch, G, max(A, 1), cache.v_dim, dtype=v.dtype, device=dev)
-    ap = torch.empty(n_batch, max(A, 1), dtype=torch.int64, device=dev)
+    T = k_raw.size(2)
+    ends = _pinned_upload(np.asarray(span_ends, dtype=np.uint8).reshape(n_batch, T), dev)
+    if positions.dtype != torch.int64 or positions.stride(-1) != 1:
+        positions = positions.to(torch.int64).contiguous()
+    nk, nv, npos, nvalid, nlen, nclosed, ncount = cache._alpha_spare
+    A = P + T
+    keep = torch.empty(n_batch, P, dtype=torch.int32, device=dev)
+    archive = torch.empty(n_batch, A, dtype=torch.int32, device=dev)
+    archive_count = torch.empty(n_batch, dtype=torch.int32, device=dev)
     pk, pv, ppos = cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos
-    args = _lib.PartitionArgs(
+    rows = _lib.SpanArgs(
+        _lib.ptr(pk), pk.stride(0), pk.stride(1), pk.stride(2), _lib.ptr(pv), pv.stride(0), pv.stride(1), pv.stride(2),
+        _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        P, None, None, None, 0, G, cache.k_dim, cache.v_dim,
+        _lib.ptr(cache.centroid) if cache.beta_novelty else None,
+        _lib.ptr(cache.alive) if cache.beta_novelty else None, cache.K_max, 1 if cache.beta_novelty else 0, None)
+    args = _lib.AlphaSelectArgs(
+        _lib.ptr(cache.alpha_span_len), _lib.ptr(cache.alpha_span_closed), _lib.ptr(cache.alpha_span_count),
+        _lib.ptr(ppos), _lib.ptr(positions), positions.stride(0), _lib.ptr(ends), ends.stride(0), T,
+        n_batch, P, cache.alpha_span_max_tokens, rows, _lib.ptr(keep), _lib.ptr(archive), _lib.ptr(archive_count),
+        _lib.ptr(nlen), _lib.ptr(nclosed), _lib.ptr(ncount), _lib.ptr(cache.alpha_count_dev), None)
+    need = int(_lib.lib().logkv_alpha_select_workspace_bytes(C.byref(args)))
+    if need < 0:
+        _lib.check(_lib.LOGKV_EINVAL, "logkv_alpha_select")
+    ws = cache._select_workspace
+    if ws is None or ws.numel() < need:
+        ws = cache._select_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    _lib.check(_lib.lib().logkv_alpha_select(C.byref(args), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev)),
+               "logkv_alpha_select")
+    ak = torch.empty(n_batch, G, A, cache.k_dim, dtype=k_raw.dtype, device=dev)
+    av = torch.empty(n_batch, G, A, cache.v_dim, dtype=v.dtype, device=dev)
+    ap = torch.empty(n_batch, A, dtype=torch.int64, device=dev)
+    part = _lib.PartitionArgs(
         _lib.ptr(pk), pk.stride(0), pk.stride(1), pk.stride(2),
         _lib.ptr(pv), pv.stride(0), pv.stride(1), pv.stride(2),
         _lib.ptr(ppos), ppos.stride(0),
         _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
         _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
         _lib.ptr(positions), positions.stride(0),
-        int(old_width), _lib.ptr(keep_t), _lib.ptr(arch_t), P, A, n_batch, G, cache.k_dim, cache.v_dim,
+        P, _lib.ptr(keep), _lib.ptr(archive), P, A, n_batch, G, cache.k_dim, cache.v_dim,
         _lib.ptr(nk), _lib.ptr(nv), _lib.ptr(npos), _lib.ptr(nvalid),
         _lib.ptr(ak), _lib.ptr(av), _lib.ptr(ap))
-    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(args), _lib.stream_of(dev)), "logkv_alpha_partition")
-    cache._alpha_spare = (pk, pv, ppos, cache.alpha_valid)
-    cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid = nk, nv, npos, nvalid
-    cache.alpha_count = max(map(len, sel.keep), default=0)
-    cache._alpha_spans, cache._alpha_positions = sel.spans, sel.positions
-    if A:
-        counts_t = torch.tensor(counts, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
-        cache._route_commit(ak, av, ap, counts_t)
-    return sel
+    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(part), _lib.stream_of(dev)), "logkv_alpha_partition")
+    cache._alpha_spare = (pk, pv, ppos, cache.alpha_valid, cache.alpha_span_len, cache.alpha_span_closed,
+                          cache.alpha_span_count)
+    (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid, cache.alpha_span_len,
+     cache.alpha_span_closed, cache.alpha_span_count) = nk, nv, npos, nvalid, nlen, nclosed, ncount
+    cache._alpha_keep_alive = (ends, keep, archive, positions)
+    cache._route_commit(ak, av, ap, archive_count)

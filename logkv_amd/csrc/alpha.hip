@@ -96,6 +96,7 @@ template <int NJ>
 __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, float* __restrict__ out) {
   __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
   const int s = blockIdx.x;
+  if (a.n_spans_dev && s >= *a.n_spans_dev) return;
   const int g = wave_id();
   const int G = a.n_groups;
   const LOGKV_G int32_t* offs = gp(a.span_offsets);
@@ -210,6 +211,329 @@ __global__ __launch_bounds__(256) void partition_kernel(logkv_partition_args a) 
   }
 }
 
+// ---- Span selection on the device ------------------------------------------
+//
+// Candidates (litgpt/alpha_log_kv.py:84-122): per batch row, the closed spans
+// of the current selection (old), the unfinished old span when a position
+// jump closes it, then the runs of the new rows; a run closes after a
+// boundary row, at max_span rows (the unfinished old span counts toward the
+// first run, which it prefixes) and before a position jump. Token indices
+// address [pool (P rows) | flush]. Choice (litgpt/alpha_log_kv.py:177-226):
+// unfinished spans are mandatory, old closed spans are kept first at density
+// 1.1 * score and evicted lowest density first (later span first on ties) to
+// fit the budget, then the other spans by decreasing density (earlier first)
+// take free room or replace the lowest-density kept spans whose summed
+// density * length is strictly lower. Densities and losses are doubles, as
+// the reference's Python floats.
+
+struct SelectWs {
+  int32_t* cand_row;     // [C] batch row of candidate i
+  uint8_t* cand_flags;   // [C] bit 0 old, bit 1 closed
+  int32_t* row_cand;     // [n_batch + 1] first candidate of each row
+  int32_t* offsets;      // [C + 1] candidate i's tokens: tokens[offsets[i], offsets[i + 1])
+  int32_t* tokens;       // [n_batch * (P + T)]
+  int32_t* n_spans;      // [1]
+  float* scores;         // [C]
+};
+
+constexpr int kSelectThreads = 256;
+constexpr int kMaxCandidates = 4096;   // per batch row
+
+__host__ __device__ inline int64_t select_candidates(int n_batch, int P, int T) {
+  return static_cast<int64_t>(n_batch) * (P + T + 1);
+}
+
+// One block: rows in order. The block finds segment starts (first row, after
+// a boundary, at a jump); thread 0 turns segments into candidate descriptors
+// in LDS; the block writes the candidate table and token lists.
+__global__ __launch_bounds__(kSelectThreads) void cut_kernel(logkv_alpha_select_args a, SelectWs w) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  const int T = a.tokens, P = a.budget, maxc = P + T + 1;
+  int32_t* seg = reinterpret_cast<int32_t*>(dyn);                            // [T + 1] segment starts
+  int32_t* olen = seg + T + 1;                                               // [P]
+  int32_t* c_first = olen + P;                                               // [maxc] first token of the range
+  int32_t* c_len = c_first + maxc;                                           // [maxc] range length
+  int32_t* c_pend = c_len + maxc;                                            // [maxc] prefixed pending rows
+  int32_t* c_off = c_pend + maxc;                                            // [maxc] token offset in the row
+  uint8_t* c_flags = reinterpret_cast<uint8_t*>(c_off + maxc);               // [maxc]
+  uint8_t* flags = c_flags + maxc;                                           // [T]
+  uint8_t* oclosed = flags + T;                                              // [P]
+  __shared__ int wave_cnt[kSelectThreads / kWave];
+  __shared__ int n_seg_s, nc_s, nt_s, row_nc_s, row_nt_s, pend_off_s;
+  if (threadIdx.x == 0) {
+    nc_s = 0;
+    nt_s = 0;
+    *a.alpha_count = 0;
+  }
+  for (int b = 0; b < a.n_batch; ++b) {
+    const LOGKV_G int64_t* pos = gp(a.new_pos + b * a.np_sb);
+    const LOGKV_G uint8_t* ends = gp(a.ends + b * a.ends_sb);
+    const int n_old = a.span_count[b];
+    for (int i = threadIdx.x; i < n_old; i += blockDim.x) {
+      olen[i] = a.span_len[static_cast<int64_t>(b) * P + i];
+      oclosed[i] = a.span_closed[static_cast<int64_t>(b) * P + i];
+    }
+    for (int j = threadIdx.x; j < T; j += blockDim.x) {
+      const bool end = ends[j] != 0;
+      const bool jump = j > 0 && pos[j] != pos[j - 1] + 1;
+      const bool start = j == 0 || jump || ends[j > 0 ? j - 1 : 0] != 0;
+      flags[j] = static_cast<uint8_t>((end ? 1 : 0) | (start ? 2 : 0));
+    }
+    if (threadIdx.x == 0) n_seg_s = 0;
+    __syncthreads();
+    for (int j0 = 0; j0 < T; j0 += blockDim.x) {
+      const int j = j0 + threadIdx.x;
+      const bool mine = j < T && (flags[j] & 2);
+      const uint64_t ballot = __ballot(mine);
+      const int l = lane_id(), wv = wave_id();
+      const int before = __popcll(ballot & ((l == 0) ? 0ull : (~0ull >> (kWave - l))));
+      if (l == 0) wave_cnt[wv] = __popcll(ballot);
+      __syncthreads();
+      int base = n_seg_s;
+      for (int q = 0; q < wv; ++q) base += wave_cnt[q];
+      if (mine) seg[base + before] = j;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int add = 0;
+        for (int q = 0; q < static_cast<int>(blockDim.x) / kWave; ++q) add += wave_cnt[q];
+        n_seg_s += add;
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      int nc = 0, nt = 0;
+      const int n_seg = n_seg_s;
+      seg[n_seg] = T;
+      auto emit = [&](int first, int len, int pend, bool old, bool closed) {
+        c_first[nc] = first;
+        c_len[nc] = len;
+        c_pend[nc] = pend;
+        c_off[nc] = nt;
+        c_flags[nc] = static_cast<uint8_t>((old ? 1 : 0) | (closed ? 2 : 0));
+        nt += pend + len;
+        ++nc;
+      };
+      int off = 0, pend_off = 0, pend_len = 0;
+      for (int i = 0; i < n_old; ++i) {
+        if (oclosed[i]) emit(off, olen[i], 0, true, true);
+        else {
+          pend_off = off;
+          pend_len = olen[i];
+        }
+        off += olen[i];
+      }
+      if (T == 0) {
+        if (pend_len) emit(pend_off, pend_len, 0, false, false);
+      } else {
+        const bool pend_closed =
+            pend_len > 0 && pos[0] != a.pool_pos[static_cast<int64_t>(b) * P + pend_off + pend_len - 1] + 1;
+        if (pend_closed) emit(pend_off, pend_len, 0, false, true);
+        int carry = pend_closed ? 0 : pend_len;
+        for (int sg = 0; sg < n_seg; ++sg) {
+          const int e = seg[sg + 1];
+          for (int p = seg[sg]; p < e;) {
+            const int room = a.max_span - carry;
+            const int take = min(room, e - p);
+            const bool closed = take == room || p + take < e || e < T || (flags[e - 1] & 1);
+            emit(P + p, take, carry, false, closed);
+            carry = 0;
+            p += take;
+          }
+        }
+      }
+      row_nc_s = nc;
+      row_nt_s = nt;
+      pend_off_s = pend_off;
+      w.row_cand[b] = nc_s;
+    }
+    __syncthreads();
+    const int nc = row_nc_s, cbase = nc_s, tbase = nt_s, pend_off = pend_off_s;
+    LOGKV_G int32_t* tok = gp(w.tokens) + tbase;
+    for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+      w.offsets[cbase + c] = tbase + c_off[c];
+      w.cand_row[cbase + c] = b;
+      w.cand_flags[cbase + c] = c_flags[c];
+      LOGKV_G int32_t* dst = tok + c_off[c];
+      const int pend = c_pend[c];
+      for (int t = 0; t < pend; ++t) dst[t] = pend_off + t;
+      for (int t = 0; t < c_len[c]; ++t) dst[pend + t] = c_first[c] + t;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      nc_s += nc;
+      nt_s += row_nt_s;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    w.row_cand[a.n_batch] = nc_s;
+    w.offsets[nc_s] = nt_s;
+    *w.n_spans = nc_s;
+  }
+}
+
+// Strict weak order of the eviction list: ascending density, later candidate first.
+__device__ __forceinline__ bool evict_before(double da, int ia, double db, int ib) {
+  return da < db || (da == db && ia > ib);
+}
+
+// One block per batch row: densities sorted by the block, the greedy run by
+// thread 0 over a compact sorted list of evictable spans, kept / archived rows
+// written by the block.
+__global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_select_args a, SelectWs w) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  const int b = blockIdx.x;
+  const int P = a.budget, T = a.tokens;
+  const int c0 = w.row_cand[b], n = w.row_cand[b + 1] - c0;
+  int width = 1;
+  while (width < n) width <<= 1;
+  double* key = reinterpret_cast<double*>(dyn);                      // [width] sort keys
+  double* dens = key + width;                                        // [n] density by candidate
+  int32_t* idx = reinterpret_cast<int32_t*>(dens + n);               // [width] sorted candidates
+  int32_t* size = idx + width;                                       // [n]
+  int32_t* koff = size + n;                                          // [n] keep / archive offsets
+  int32_t* rank = koff + n;                                          // [n] candidates to rank
+  int32_t* vict = rank + n;                                          // [n] evictable spans, eviction order
+  uint8_t* state = reinterpret_cast<uint8_t*>(vict + n);             // [n] bit 0 old, 1 closed, 2 chosen
+  __shared__ int kept_s, arch_s;
+  for (int i = threadIdx.x; i < width; i += blockDim.x) {
+    if (i < n) {
+      const uint8_t f = w.cand_flags[c0 + i];
+      const double d = static_cast<double>(w.scores[c0 + i]) * ((f & 1) ? 1.1 : 1.0);
+      dens[i] = d;
+      key[i] = d;
+      idx[i] = i;
+      size[i] = w.offsets[c0 + i + 1] - w.offsets[c0 + i];
+      state[i] = f;
+    } else {
+      key[i] = __builtin_inf();
+      idx[i] = 0x7fffffff;
+    }
+  }
+  __syncthreads();
+  // Eviction order (its reverse is the ranking order: decreasing density,
+  // earlier first); padding sorts last.
+  for (int sz = 2; sz <= width; sz <<= 1) {
+    for (int stride = sz >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < width; t += blockDim.x) {
+        const int partner = t ^ stride;
+        if (partner > t) {
+          const bool up = (t & sz) == 0;
+          const double ka = key[t], kb = key[partner];
+          const int ia = idx[t], ib = idx[partner];
+          const bool pa = ia == 0x7fffffff, pb = ib == 0x7fffffff;
+          const bool a_after = pa != pb ? pa : (!pa && evict_before(kb, ib, ka, ia));
+          if (a_after == up) {
+            key[t] = kb;
+            key[partner] = ka;
+            idx[t] = ib;
+            idx[partner] = ia;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (threadIdx.x == 0) {
+    int room = P;
+    for (int i = 0; i < n; ++i) {
+      if (!(state[i] & 2) || (state[i] & 1)) {
+        state[i] |= 4;
+        room -= size[i];
+      }
+    }
+    // Evictable spans (chosen and closed) in eviction order, from vict[vh].
+    int nv = 0;
+    for (int q = 0; q < n; ++q) {
+      const int i = idx[q];
+      if ((state[i] & 4) && (state[i] & 2)) vict[nv++] = i;
+    }
+    int vh = 0;
+    while (room < 0 && vh < nv) {
+      const int i = vict[vh++];
+      state[i] &= ~4;
+      room += size[i];
+    }
+    int n_rank = 0;
+    for (int q = n - 1; q >= 0; --q)
+      if (!(state[idx[q]] & 4)) rank[n_rank++] = idx[q];
+    for (int r = 0; r < n_rank; ++r) {
+      const int i = rank[r];
+      const int need = size[i];
+      int avail = room, n_taken = 0;
+      double loss = 0.0;
+      if (avail < need) {
+        for (int q = vh; q < nv; ++q) {
+          const int j = vict[q];
+          ++n_taken;
+          avail += size[j];
+          loss += dens[j] * static_cast<double>(size[j]);
+          if (avail >= need) break;
+        }
+      }
+      if (avail >= need && (n_taken == 0 || dens[i] * static_cast<double>(need) > loss)) {
+        for (int t = 0; t < n_taken; ++t) state[vict[vh + t]] &= ~4;
+        vh += n_taken;
+        state[i] |= 4;
+        room = avail - need;
+        if (state[i] & 2) {   // a closed span joins the evictable list at its place
+          int q = nv;
+          while (q > vh && evict_before(dens[i], i, dens[vict[q - 1]], vict[q - 1])) {
+            vict[q] = vict[q - 1];
+            --q;
+          }
+          vict[q] = i;
+          ++nv;
+        }
+      }
+    }
+    int kept = 0, arch = 0, spans = 0;
+    for (int i = 0; i < n; ++i) {
+      if (state[i] & 4) {
+        koff[i] = kept;
+        kept += size[i];
+        ++spans;
+      } else {
+        koff[i] = arch;
+        arch += size[i];
+      }
+    }
+    kept_s = kept;
+    arch_s = arch;
+    a.new_span_count[b] = spans;
+    a.archive_count[b] = arch;
+    atomicMax(a.alpha_count, kept);
+  }
+  __syncthreads();
+  const int A = P + T;
+  const int kept = kept_s, arch = arch_s;
+  LOGKV_G int32_t* keep = gp(a.keep + static_cast<int64_t>(b) * P);
+  LOGKV_G int32_t* archive = gp(a.archive + static_cast<int64_t>(b) * A);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int o = w.offsets[c0 + i];
+    const bool kept_i = (state[i] & 4) != 0;
+    LOGKV_G int32_t* dst = kept_i ? keep + koff[i] : archive + koff[i];
+    const int cap = kept_i ? P - koff[i] : A - koff[i];   // the greedy keeps at most P rows
+    for (int t = 0; t < size[i] && t < cap; ++t) dst[t] = w.tokens[o + t];
+  }
+  // The new selection's spans, in candidate order.
+  if (threadIdx.x == 0) {
+    int sp = 0;
+    for (int i = 0; i < n; ++i) {
+      if (state[i] & 4) {
+        a.new_span_len[static_cast<int64_t>(b) * P + sp] = size[i];
+        a.new_span_closed[static_cast<int64_t>(b) * P + sp] = (state[i] & 2) ? 1 : 0;
+        ++sp;
+      }
+    }
+  }
+  for (int i = kept + threadIdx.x; i < P; i += blockDim.x) keep[i] = -1;
+  for (int i = arch + threadIdx.x; i < A; i += blockDim.x) archive[i] = -1;
+  if (a.scores) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) a.scores[c0 + i] = w.scores[c0 + i];
+  }
+}
+
 }  // namespace
 
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
@@ -218,6 +542,60 @@ int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
     hipLaunchKernelGGL(score_kernel<2>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
   else
     hipLaunchKernelGGL(score_kernel<4>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+int64_t select_workspace_bytes(const logkv_alpha_select_args& a) {
+  const int64_t C = select_candidates(a.n_batch, a.budget, a.tokens);
+  auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
+  return al(C * 4) + al(C) + al((a.n_batch + 1) * 4) + al((C + 1) * 4) +
+         al(static_cast<int64_t>(a.n_batch) * (a.budget + a.tokens) * 4) + al(4) + al(C * 4);
+}
+
+int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream) {
+  const int64_t C = select_candidates(a.n_batch, a.budget, a.tokens);
+  auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
+  uint8_t* p = static_cast<uint8_t*>(ws);
+  SelectWs w;
+  w.cand_row = reinterpret_cast<int32_t*>(p);
+  p += al(C * 4);
+  w.cand_flags = p;
+  p += al(C);
+  w.row_cand = reinterpret_cast<int32_t*>(p);
+  p += al((a.n_batch + 1) * 4);
+  w.offsets = reinterpret_cast<int32_t*>(p);
+  p += al((C + 1) * 4);
+  w.tokens = reinterpret_cast<int32_t*>(p);
+  p += al(static_cast<int64_t>(a.n_batch) * (a.budget + a.tokens) * 4);
+  w.n_spans = reinterpret_cast<int32_t*>(p);
+  p += al(4);
+  w.scores = reinterpret_cast<float*>(p);
+  const size_t cut_c = static_cast<size_t>(a.budget) + a.tokens + 1;
+  const size_t cut_shmem = 4 * (static_cast<size_t>(a.tokens) + 1) + 5 * static_cast<size_t>(a.budget) +
+                           17 * cut_c + static_cast<size_t>(a.tokens) + 16;
+  if (cut_shmem > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&cut_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(cut_shmem)) != hipSuccess)
+    return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(cut_kernel, dim3(1), dim3(kSelectThreads), cut_shmem, stream, a, w);
+  logkv_span_args sa = a.rows;
+  sa.old_width = a.budget;
+  sa.tokens = w.tokens;
+  sa.span_offsets = w.offsets;
+  sa.span_rows = w.cand_row;
+  sa.n_spans = static_cast<int32_t>(C);
+  sa.n_spans_dev = w.n_spans;
+  int rc = launch_score(sa, w.scores, stream);
+  if (rc) return rc;
+  const int maxc = a.budget + a.tokens + 1;
+  int width = 1;
+  while (width < maxc) width <<= 1;
+  const size_t choose_shmem = static_cast<size_t>(width) * (8 + 4) + static_cast<size_t>(maxc) * (8 + 4 * 4 + 1) + 16;
+  if (choose_shmem > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&choose_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(choose_shmem)) != hipSuccess)
+    return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(choose_kernel, dim3(a.n_batch), dim3(kSelectThreads), choose_shmem, stream, a, w);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

@@ -198,6 +198,43 @@ int logkv_alpha_partition(const logkv_partition_args* a, void* stream) {
   return LOGKV_OK;
 }
 
+static int check_select(const logkv_alpha_select_args* a) {
+  if (!a) return fail(LOGKV_EINVAL, "select args are NULL");
+  if (a->n_batch < 1 || a->budget < 1 || a->max_span < 1 || a->max_span > a->budget || a->tokens < 0)
+    return fail(LOGKV_EINVAL, "bad selection sizes");
+  if (int64_t(a->budget) + a->tokens + 1 > 4096)
+    return fail(LOGKV_EINVAL, "budget + rows + 1 = %d exceeds 4096 candidates per batch row",
+                a->budget + a->tokens + 1);
+  if (!a->span_len || !a->span_closed || !a->span_count || !a->pool_pos || !a->keep || !a->archive ||
+      !a->archive_count || !a->new_span_len || !a->new_span_closed || !a->new_span_count || !a->alpha_count)
+    return fail(LOGKV_EINVAL, "selection buffer is NULL");
+  if (a->tokens && (!a->new_pos || !a->ends)) return fail(LOGKV_EINVAL, "new positions or boundaries are NULL");
+  const logkv_span_args& r = a->rows;
+  if (r.n_groups < 1 || r.n_groups > 16 || r.dk < 1 || r.dv < 1 || r.dk > logkv::kMaxDim || r.dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "bad groups or widths");
+  if (!r.pool_k || !r.pool_v || (a->tokens && (!r.flush_k || !r.flush_v)))
+    return fail(LOGKV_EINVAL, "span row tensors are NULL");
+  if (r.beta_novelty && (!r.centroids || !r.centroid_valid || r.k_max < 1))
+    return fail(LOGKV_EINVAL, "Beta novelty needs centroids");
+  if (a->span_len == a->new_span_len || a->span_closed == a->new_span_closed)
+    return fail(LOGKV_EINVAL, "the new selection must not overwrite the current one");
+  return LOGKV_OK;
+}
+
+int64_t logkv_alpha_select_workspace_bytes(const logkv_alpha_select_args* a) {
+  if (check_select(a)) return -1;
+  return logkv::select_workspace_bytes(*a);
+}
+
+int logkv_alpha_select(const logkv_alpha_select_args* a, void* ws, int64_t ws_bytes, void* stream) {
+  int rc = check_select(a);
+  if (rc) return rc;
+  if (!ws || ws_bytes < logkv::select_workspace_bytes(*a)) return fail(LOGKV_EINVAL, "selection workspace too small");
+  rc = logkv::launch_select(*a, ws, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "selection launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 int64_t logkv_plan_table_ints(const logkv_readout_view* c) {
   if (!c) return -1;
   return int64_t(c->n_batch) * c->n_groups * (int64_t(c->k_max) * c->levels + 1) + 1;
@@ -211,8 +248,8 @@ static int check_readout(const logkv_readout_view* c) {
     return fail(LOGKV_EINVAL, "readout widths must be in [1, %d]", logkv::kMaxDim);
   if (!c->level_k || !c->level_v || !c->level_w || !c->level_sum_wp || !c->level_count)
     return fail(LOGKV_EINVAL, "readout ladder buffer is NULL");
-  if (c->alpha_count < 0 || c->alpha_count > c->alpha_cap || (c->alpha_count && (!c->alpha_k || !c->alpha_v ||
-      !c->alpha_pos || !c->alpha_valid)))
+  if (c->alpha_count < 0 || c->alpha_count > c->alpha_cap ||
+      ((c->alpha_count || c->alpha_count_dev) && (!c->alpha_k || !c->alpha_v || !c->alpha_pos || !c->alpha_valid)))
     return fail(LOGKV_EINVAL, "bad exact pool view");
   if (c->recent_count < 0 || c->recent_count > c->recent_cap || (c->recent_count && (!c->recent_k || !c->recent_v)))
     return fail(LOGKV_EINVAL, "bad recent window view");
@@ -236,7 +273,8 @@ int logkv_pack(const logkv_readout_view* c, const logkv_pack_args* p, const int3
   if (!p || !table || !p->out_k || !p->out_v) return fail(LOGKV_EINVAL, "pack outputs or plan table are NULL");
   if (p->dim <= c->dk || p->dim < c->dv || p->dim % 8 || p->dim > 264)
     return fail(LOGKV_EINVAL, "packed width %d must exceed dk, hold dv, be a multiple of 8 and <= 264", p->dim);
-  if (p->cur_len < 0 || (p->cur_len && (!p->cur_k || !p->cur_v)) || p->tail_start < 0 || p->out_cap < 0)
+  if (p->cur_len < 0 || (p->cur_len && (!p->cur_k || !p->cur_v)) || p->recent_start < 0 ||
+      p->recent_start > c->recent_count || p->out_cap < 0)
     return fail(LOGKV_EINVAL, "bad current rows or output capacity");
   rc = logkv::launch_pack(*c, *p, table, static_cast<hipStream_t>(stream));
   if (rc) return fail(rc, "pack launch failed: %s", hipGetErrorString(hipGetLastError()));

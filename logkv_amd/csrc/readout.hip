@@ -95,12 +95,14 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
   const int b = lane / c.n_groups, g = lane % c.n_groups;
   const int KL = c.k_max * c.levels;
   const int width = table[static_cast<int64_t>(lanes) * (KL + 1)];
-  const int tail_rows = c.alpha_count + c.recent_count + p.cur_len;
+  const int alpha_count = c.alpha_count_dev ? *c.alpha_count_dev : c.alpha_count;
+  const int tail_rows = alpha_count + c.recent_count + p.cur_len;
   const int i0 = blockIdx.x * (blockDim.x / kWave) + wave_id();
   int s;
   if (p.skip_pooled) {
-    if (p.tail_start + i0 >= tail_rows) return;
-    s = width + p.tail_start + i0;
+    const int tail_start = alpha_count + p.recent_start;
+    if (tail_start + i0 >= tail_rows) return;
+    s = width + tail_start + i0;
   } else {
     if (i0 >= width + tail_rows) return;
     s = i0;
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
         bias = round_bf16(logf(w > 1.f ? w : 1.f));
       }
     }
-  } else if (s < width + c.alpha_count) {
+  } else if (s < width + alpha_count) {
     const int i = s - width;
     valid = gp(c.alpha_valid)[static_cast<int64_t>(b) * c.alpha_cap + i] != 0;
     if (valid) {
@@ -153,12 +155,12 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
       vr = gp(c.alpha_v) + (static_cast<int64_t>(lane) * c.alpha_cap + i) * dv;
       rotate = true;
     }
-  } else if (s < width + c.alpha_count + c.recent_count) {
-    const int i = s - width - c.alpha_count;
+  } else if (s < width + alpha_count + c.recent_count) {
+    const int i = s - width - alpha_count;
     kr = gp(c.recent_k) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dk;
     vr = gp(c.recent_v) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dv;
   } else {
-    const int i = s - width - c.alpha_count - c.recent_count;
+    const int i = s - width - alpha_count - c.recent_count;
     kr = gp(p.cur_k) + b * p.ck_sb + g * p.ck_sg + static_cast<int64_t>(i) * p.ck_st;
     vr = gp(p.cur_v) + b * p.cv_sb + g * p.cv_sg + static_cast<int64_t>(i) * p.cv_st;
   }
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(256) void decode_kernel(logkv_attention_args a, con
   const int rep = a.n_heads / G;
   const int nq = rep * a.tq;
   const int dim = a.dim;
-  const int total = min(*width_ptr + a.tail, a.cap);
+  const int total = min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
   const int r_begin = blockIdx.x * kSplitRows;
   const int r_end = min(r_begin + kSplitRows, total);
   float* out = part + (static_cast<int64_t>(lane) * gridDim.x + blockIdx.x) * nq * (a.dv + 2);
@@ -319,7 +321,9 @@ int launch_plan(const logkv_readout_view& c, int32_t* table, hipStream_t stream)
 }
 
 int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int32_t* table, hipStream_t stream) {
-  const int rows = p.skip_pooled ? c.alpha_count + c.recent_count + p.cur_len - p.tail_start : p.out_cap;
+  // With skip_pooled the rows past the recent window's first new row (at most
+  // the whole recent window and current rows; blocks past the end exit).
+  const int rows = p.skip_pooled ? c.recent_count + p.cur_len - p.recent_start : p.out_cap;
   if (rows <= 0) return LOGKV_OK;
   const int per_block = 256 / kWave;
   hipLaunchKernelGGL(pack_kernel, dim3((rows + per_block - 1) / per_block, c.n_batch * c.n_groups), dim3(256), 0,

@@ -58,6 +58,8 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
                  hipStream_t stream);
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream);
 int launch_partition(const logkv_partition_args& a, hipStream_t stream);
+int64_t select_workspace_bytes(const logkv_alpha_select_args& a);
+int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream);
 int launch_plan(const logkv_readout_view& c, int32_t* table, hipStream_t stream);
 int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int32_t* table, hipStream_t stream);
 int64_t attention_workspace_floats(const logkv_attention_args& a);

@@ -214,20 +214,26 @@ class LogStructuredKVCache(nn.Module):
         buf("recent_k_raw", torch.zeros(batch_size, n_groups, cap, k_dim, device=device, dtype=dtype))
         buf("recent_pos", torch.zeros(batch_size, cap, device=device, dtype=torch.int64))
         self._recent_pos_host = [[0] * cap for _ in range(batch_size)]
-        self.alpha_count = 0
+        self._alpha_count_host = 0
         if self.alpha_exact_tokens:
             P = self.alpha_exact_tokens
             buf("alpha_k_raw", torch.zeros(batch_size, n_groups, P, k_dim, device=device, dtype=dtype))
             buf("alpha_v", torch.zeros(batch_size, n_groups, P, v_dim, device=device, dtype=dtype))
             buf("alpha_pos", torch.zeros(batch_size, P, device=device, dtype=torch.int64))
             buf("alpha_valid", torch.zeros(batch_size, P, device=device, dtype=torch.bool))
-            # The pool is rewritten from [old pool | flush] rows into this second
-            # buffer set, then the two sets swap, so no partition reads a row it
-            # has already overwritten.
+            # The exact pool's selection lives on the device: spans (length,
+            # closed) of the kept rows and the kept count, so a flush chooses
+            # spans with no host round trip.
+            buf("alpha_span_len", torch.zeros(batch_size, P, device=device, dtype=torch.int32))
+            buf("alpha_span_closed", torch.zeros(batch_size, P, device=device, dtype=torch.uint8))
+            buf("alpha_span_count", torch.zeros(batch_size, device=device, dtype=torch.int32))
+            buf("alpha_count_dev", torch.zeros(1, device=device, dtype=torch.int32))
+            # The pool and its spans are rewritten into this second buffer set,
+            # then the sets swap, so nothing reads a row it has overwritten.
             self._alpha_spare = (torch.zeros_like(self.alpha_k_raw), torch.zeros_like(self.alpha_v),
-                                 torch.zeros_like(self.alpha_pos), torch.zeros_like(self.alpha_valid))
-            self._alpha_spans = [[] for _ in range(batch_size)]
-            self._alpha_positions = [[] for _ in range(batch_size)]
+                                 torch.zeros_like(self.alpha_pos), torch.zeros_like(self.alpha_valid),
+                                 torch.zeros_like(self.alpha_span_len), torch.zeros_like(self.alpha_span_closed),
+                                 torch.zeros_like(self.alpha_span_count))
             self._recent_span_ends = [[False] * cap for _ in range(batch_size)]
         shp = (batch_size, n_groups, self.K_max, L, B_eff)
         i64max = torch.iinfo(torch.int64).max
@@ -263,6 +269,8 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError("semantic_s_h must be finite and > 0")
         buf("s_h", s_h.contiguous())
         self._workspace = None
+        self._select_workspace = None
+        self._alpha_keep_alive = None
         self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
                                    1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0)
 
@@ -425,16 +433,16 @@ class LogStructuredKVCache(nn.Module):
         self.level_p_lo.fill_(i64max)
         self.level_p_hi.fill_(-1)
         self.p_hi_c.fill_(-1)
-        self.token_count = self.recent_count = self.alpha_count = 0
+        self.token_count = self.recent_count = 0
+        self.alpha_count = 0
         self._mid_decode_state = None
         self._recent_pos_host = [[0] * self.recent_capacity for _ in range(self.batch_size)]
         if self.alpha_exact_tokens:
-            for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid"):
+            for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid", "alpha_span_len", "alpha_span_closed",
+                         "alpha_span_count", "alpha_count_dev"):
                 getattr(self, name).zero_()
             for t in self._alpha_spare:
                 t.zero_()
-            self._alpha_spans = [[] for _ in range(self.batch_size)]
-            self._alpha_positions = [[] for _ in range(self.batch_size)]
             self._recent_span_ends = [[False] * self.recent_capacity for _ in range(self.batch_size)]
 
     def _apply(self, fn, recurse=True):
@@ -442,6 +450,7 @@ class LogStructuredKVCache(nn.Module):
         # (litgpt/log_kv_cache.py:6226-6232).
         self._mid_decode_state = None
         self._workspace = None
+        self._select_workspace = None
         return super()._apply(fn, recurse)
 
     # ------------------------------------------------------------------
@@ -459,6 +468,34 @@ class LogStructuredKVCache(nn.Module):
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand
     # ------------------------------------------------------------------
+    @property
+    def alpha_count(self) -> int:
+        """Rows of the exact pool in use (largest kept count); read from the device."""
+        if not self.alpha_exact_tokens:
+            return self._alpha_count_host
+        return int(self.alpha_count_dev.item())
+
+    @alpha_count.setter
+    def alpha_count(self, value: int) -> None:
+        if self.alpha_exact_tokens:
+            self.alpha_count_dev.fill_(int(value))
+        else:
+            self._alpha_count_host = int(value)
+
+    @property
+    def _alpha_spans(self):
+        """Per batch row, (length, closed) of the exact pool's spans (litgpt/log_kv_cache.py)."""
+        n = self.alpha_span_count.tolist()
+        lens, closed = self.alpha_span_len.tolist(), self.alpha_span_closed.tolist()
+        return [[(lens[b][i], bool(closed[b][i])) for i in range(n[b])] for b in range(self.batch_size)]
+
+    @property
+    def _alpha_positions(self):
+        """Per batch row, positions of the exact pool's kept rows in span order."""
+        rows = [sum(length for length, _ in spans) for spans in self._alpha_spans]
+        pos = self.alpha_pos.tolist()
+        return [pos[b][:rows[b]] for b in range(self.batch_size)]
+
     @property
     def _semantic_counts(self):
         return self.level_count.long().cpu().tolist()

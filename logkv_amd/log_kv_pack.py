@@ -70,7 +70,8 @@ def readout_view(cache) -> ReadoutView:
     if cache.alpha_exact_tokens:
         view.alpha_k, view.alpha_v = ptr(cache.alpha_k_raw), ptr(cache.alpha_v)
         view.alpha_pos, view.alpha_valid = ptr(cache.alpha_pos), ptr(cache.alpha_valid)
-        view.alpha_cap, view.alpha_count = cache.alpha_exact_tokens, cache.alpha_count
+        view.alpha_cap, view.alpha_count = cache.alpha_exact_tokens, 0
+        view.alpha_count_dev = ptr(cache.alpha_count_dev)     # rows in use, read on the device
     view.recent_k, view.recent_v = ptr(cache.recent_k), ptr(cache.recent_v)
     view.recent_cap, view.recent_count = cache.recent_capacity, cache.recent_count
     view.cos, view.sin = ptr(cache.cos_cache), ptr(cache.sin_cache)
@@ -106,9 +107,11 @@ def _check_kv(cache, k, v):
         raise ValueError("K/V shape, device and dtype must match the cache")
 
 
-def _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, tail_start):
+def _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, recent_start):
+    """Pack into ``ka / va``; with ``skip_pooled`` only the rows from recent window row
+    ``recent_start`` on (the exact pool's row count is read on the device)."""
     args = PackArgs(ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], k.size(2), ptr(ka), ptr(va), ka.size(2), dim,
-                    1 if skip_pooled else 0, tail_start)
+                    1 if skip_pooled else 0, recent_start)
     if k.stride(3) != 1 or v.stride(3) != 1:
         raise ValueError("current K/V rows must be contiguous in the feature dimension")
     check(lib().logkv_pack(C.byref(view), C.byref(args), ptr(plan.table), stream_of(k.device)), "logkv_pack")
@@ -147,7 +150,7 @@ def pack_mid_kv(cache, plan, k, v, dim, *, backend=None, buffers=None, skip_pool
         ka = k.new_empty((*k.shape[:2], length, dim))
         va = v.new_empty((*v.shape[:2], length, dim))
     view = readout_view(cache)
-    _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, cache.alpha_count + recent_start)
+    _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, recent_start)
     return ka[:, :, :length], va[:, :, :length]
 
 
@@ -155,11 +158,13 @@ def _inv_scale_bf16(scale: float) -> float:
     return torch.tensor(1.0 / scale, dtype=torch.float32).to(torch.bfloat16).item()
 
 
-def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups, workspace=None):
-    """Attention of ``q [Bt, Hq, Tq, Dk]`` over packed rows ``[plan width + tail]`` of ``ka / va``.
+def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups, workspace=None,
+                     alpha_count_dev=None):
+    """Attention of ``q [Bt, Hq, Tq, Dk]`` over packed rows ``[plan width + exact + tail]`` of ``ka / va``.
 
-    The pooled width is read on the device, so ``ka / va`` may be longer than
-    the packed rows (a reusable decode workspace)."""
+    The pooled width (and, given ``alpha_count_dev``, the exact pool's row
+    count) is read on the device, so ``ka / va`` may be longer than the packed
+    rows (a reusable decode workspace)."""
     bt, hq, tq, dk = q.shape
     if q.dtype != torch.bfloat16 or q.stride(3) != 1:
         raise ValueError("queries must be bfloat16 with contiguous features")
@@ -168,7 +173,7 @@ def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups,
     out = q.new_empty(bt, hq, tq, v_dim)
     args = AttentionArgs(ptr(q), *q.stride()[:3], bt, hq, n_groups, tq, dk, v_dim, ka.size(3), ptr(ka), ptr(va),
                          ka.size(2), tail, causal_tail, float(scale), _inv_scale_bf16(scale), ptr(out),
-                         *out.stride()[:3])
+                         *out.stride()[:3], ptr(alpha_count_dev))
     need = int(lib().logkv_attention_workspace_bytes(C.byref(args)))
     if need < 0:
         raise ValueError("bad attention shape")
@@ -228,10 +233,11 @@ def log_kv_chunk_attention(cache, q_b, k_b, v_b, scale, second_order_scale=1.0, 
         cap = _decode_capacity(cache, k_b.size(2))
         buffers = (k_b.new_empty(*k_b.shape[:2], cap, dim), v_b.new_empty(*v_b.shape[:2], cap, dim))
     ka, va = buffers
-    _launch_pack(cache, view, plan, k_b, v_b, dim, ka, va, skip_pooled, cache.alpha_count + recent_start)
-    tail = cache.alpha_count + cache.recent_count + k_b.size(2)
+    _launch_pack(cache, view, plan, k_b, v_b, dim, ka, va, skip_pooled, recent_start)
+    exact = cache.alpha_count_dev if cache.alpha_exact_tokens else None
+    tail = cache.recent_count + k_b.size(2)
     out, workspace = packed_attention(q_b, ka, va, plan, tail, scale, causal_tail, v_b.size(-1), cache.n_groups,
-                                      workspace)
+                                      workspace, exact)
     if reuse:
         cache._mid_decode_state = (key, plan, buffers, cache.recent_count, workspace)
     return out

@@ -74,3 +74,104 @@ def test_alpha_flush_matches_oracle(name):
     else:
         cuts = np.concatenate([c for _, log in ora_c.beta_cuts for _, c in log])
         assert (cuts != 1).any()
+
+
+def _random_selection(rng, P, max_span):
+    spans, n = [], 0
+    while True:
+        length = int(rng.integers(1, max_span + 1))
+        if n + length > P - max_span:
+            break
+        spans.append((length, True))
+        n += length
+    if rng.random() < 0.6:
+        spans.append((int(rng.integers(1, max_span)), False))
+    return spans
+
+
+@pytest.mark.parametrize("beta,seed", [(False, 0), (True, 1), (True, 2)])
+def test_device_selection_matches_oracle(beta, seed):
+    """logkv_alpha_select (candidates, scores, greedy on the device) against the oracle's
+    cut_spans / score_spans / choose_spans: pending spans closed by jumps or carried into
+    the first run, caps, single-row spans (zero scores, ties), evictions."""
+    import ctypes as C
+
+    from logkv_amd import _lib
+
+    rng = np.random.default_rng(seed)
+    Bt, G, D, P, T, ms, K = 2, 4, 64, 24, 40, 6, 3
+    dev = torch.device("cuda")
+    spans = [_random_selection(rng, P, ms) for _ in range(Bt)]
+    counts = [sum(n for n, _ in s) for s in spans]
+    pool_pos = np.zeros((Bt, P), np.int64)
+    new_pos = np.zeros((Bt, T), np.int64)
+    for b in range(Bt):
+        pool_pos[b, :counts[b]] = np.sort(rng.choice(60, counts[b], replace=False))
+        start = int(pool_pos[b, counts[b] - 1]) + 1 + int(rng.random() < 0.5)
+        steps = 1 + (rng.random(T) < 0.1) * rng.integers(1, 3, T)
+        steps[0] = 0
+        new_pos[b] = start + np.cumsum(steps)
+    ends = rng.random((Bt, T)) < 0.2
+    gen = torch.Generator().manual_seed(seed)
+    pool_k = (torch.randn(Bt, G, P, D, generator=gen) * 2).to(torch.bfloat16)
+    pool_v = torch.randn(Bt, G, P, D, generator=gen).to(torch.bfloat16)
+    flush_k = (torch.randn(Bt, G, T, D, generator=gen) * 2).to(torch.bfloat16)
+    flush_v = torch.randn(Bt, G, T, D, generator=gen).to(torch.bfloat16)
+    single = rng.random(T) < 0.3                                    # constant rows: zero-score ties
+    flush_k[:, :, single] = 1.0
+    flush_v[:, :, single] = 1.0
+    cent = torch.randn(Bt, G, K, D, generator=gen) * 2
+    alive = torch.rand(Bt, G, K, generator=gen) < 0.7
+
+    span_len = torch.zeros(Bt, P, dtype=torch.int32)
+    span_closed = torch.zeros(Bt, P, dtype=torch.uint8)
+    for b, s in enumerate(spans):
+        for i, (n, c) in enumerate(s):
+            span_len[b, i], span_closed[b, i] = n, int(c)
+    t = {k: x.to(dev) for k, x in dict(
+        span_len=span_len, span_closed=span_closed, span_count=torch.tensor([len(s) for s in spans], dtype=torch.int32),
+        pool_pos=torch.from_numpy(pool_pos), new_pos=torch.from_numpy(new_pos),
+        ends=torch.from_numpy(ends.astype(np.uint8)), pk=pool_k, pv=pool_v, fk=flush_k, fv=flush_v,
+        cent=cent, alive=alive).items()}
+    out = dict(keep=torch.empty(Bt, P, dtype=torch.int32, device=dev),
+               archive=torch.empty(Bt, P + T, dtype=torch.int32, device=dev),
+               acount=torch.empty(Bt, dtype=torch.int32, device=dev),
+               nlen=torch.empty(Bt, P, dtype=torch.int32, device=dev),
+               nclosed=torch.empty(Bt, P, dtype=torch.uint8, device=dev),
+               ncount=torch.empty(Bt, dtype=torch.int32, device=dev),
+               alpha=torch.empty(1, dtype=torch.int32, device=dev),
+               scores=torch.empty(Bt * (P + T + 1), dtype=torch.float32, device=dev))
+    pk, pv, fk, fv = t["pk"], t["pv"], t["fk"], t["fv"]
+    rows = _lib.SpanArgs(_lib.ptr(pk), *pk.stride()[:3], _lib.ptr(pv), *pv.stride()[:3], _lib.ptr(fk),
+                         *fk.stride()[:3], _lib.ptr(fv), *fv.stride()[:3], P, None, None, None, 0, G, D, D,
+                         _lib.ptr(t["cent"]), _lib.ptr(t["alive"]), K, 1 if beta else 0, None)
+    args = _lib.AlphaSelectArgs(
+        _lib.ptr(t["span_len"]), _lib.ptr(t["span_closed"]), _lib.ptr(t["span_count"]), _lib.ptr(t["pool_pos"]),
+        _lib.ptr(t["new_pos"]), T, _lib.ptr(t["ends"]), T, T, Bt, P, ms, rows, _lib.ptr(out["keep"]),
+        _lib.ptr(out["archive"]), _lib.ptr(out["acount"]), _lib.ptr(out["nlen"]), _lib.ptr(out["nclosed"]),
+        _lib.ptr(out["ncount"]), _lib.ptr(out["alpha"]), _lib.ptr(out["scores"]))
+    ws = torch.empty(int(_lib.lib().logkv_alpha_select_workspace_bytes(C.byref(args))), dtype=torch.uint8,
+                     device=dev)
+    _lib.check(_lib.lib().logkv_alpha_select(C.byref(args), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev)),
+               "select")
+    torch.cuda.synchronize()
+
+    width = max(counts)
+    keys = np.concatenate((pool_k.float().numpy()[:, :, :width], flush_k.float().numpy()), axis=2)
+    vals = np.concatenate((pool_v.float().numpy()[:, :, :width], flush_v.float().numpy()), axis=2)
+    old_pos = [pool_pos[b, :counts[b]].tolist() for b in range(Bt)]
+    cut = ora.cut_spans(spans, old_pos, new_pos.tolist(), ends.tolist(), width, ms)
+    scores = ora.score_spans(keys, vals, cut, beta, cent.numpy(), alive.numpy())
+    keep, archive, sp, _ = ora.choose_spans(cut, scores, P)
+    n_cand = len(scores)
+    np.testing.assert_array_equal(out["scores"].cpu().numpy()[:n_cand], scores)
+    remap = lambda idx: [i if i < width else i - width + P for i in idx]  # noqa: E731
+    for b in range(Bt):
+        got_keep = [x for x in out["keep"][b].tolist() if x >= 0]
+        got_arch = out["archive"][b].tolist()[:int(out["acount"][b])]
+        assert got_keep == remap(keep[b]), b
+        assert got_arch == remap(archive[b]), b
+        n = int(out["ncount"][b])
+        got_spans = list(zip(out["nlen"][b, :n].tolist(), [bool(x) for x in out["nclosed"][b, :n].tolist()]))
+        assert got_spans == sp[b], b
+    assert int(out["alpha"][0]) == max(len(k) for k in keep)
