@@ -237,7 +237,6 @@ struct SelectWs {
 };
 
 constexpr int kSelectThreads = 256;
-constexpr int kMaxCandidates = 4096;   // per batch row
 
 __host__ __device__ inline int64_t select_candidates(int n_batch, int P, int T) {
   return static_cast<int64_t>(n_batch) * (P + T + 1);

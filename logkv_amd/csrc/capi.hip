@@ -25,6 +25,9 @@ int check_ladder(const logkv_ladder_view* c) {
   if (c->n_batch < 1 || c->n_groups < 1) return fail(LOGKV_EINVAL, "batch and groups must be >= 1");
   if (c->k_max < 1 || c->k_max > logkv::kMaxClusters)
     return fail(LOGKV_EINVAL, "cluster count %d outside [1, %d]", c->k_max, logkv::kMaxClusters);
+  if (int64_t(c->n_batch) * c->n_groups * c->k_max > logkv::kMaxLadders)
+    return fail(LOGKV_EINVAL, "batch * groups * clusters = %lld exceeds %d",
+                (long long)(int64_t(c->n_batch) * c->n_groups * c->k_max), logkv::kMaxLadders);
   if (c->slots < 2) return fail(LOGKV_EINVAL, "slots per level must be >= 2, got %d", c->slots);
   if (c->levels < 1 || c->levels > logkv::kMaxLevels)
     return fail(LOGKV_EINVAL, "levels %d outside [1, %d]", c->levels, logkv::kMaxLevels);
@@ -51,7 +54,7 @@ int check_rows(const logkv_ladder_view* c, const logkv_rows_view* r) {
 }
 
 struct Plan {
-  int64_t order, assign, s_win, dist, snap, plans, tok, ladder, total;
+  int64_t order, assign, s_win, dist, snap, plans, tok, units, ladder, total;
   int64_t stride, s0, m0;
   int32_t sort_width;
 };
@@ -80,6 +83,8 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
   off += align256(ladders * int64_t(sizeof(logkv::LadderPlan)));
   p.tok = off;
   off += align256(ladders * tokens * 2);
+  p.units = off;
+  off += align256(int64_t(c->levels) * (ladders + 1) * 4);
   p.ladder = off;
   off += ladders * p.stride;
   p.total = off;
@@ -114,6 +119,7 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   ws.m0_cap = p.m0;
   ws.plans = reinterpret_cast<logkv::LadderPlan*>(base + p.plans);
   ws.tok = reinterpret_cast<uint16_t*>(base + p.tok);
+  ws.units = reinterpret_cast<int32_t*>(base + p.units);
   ws.sort_width = p.sort_width;
   return LOGKV_OK;
 }
@@ -202,9 +208,9 @@ static int check_select(const logkv_alpha_select_args* a) {
   if (!a) return fail(LOGKV_EINVAL, "select args are NULL");
   if (a->n_batch < 1 || a->budget < 1 || a->max_span < 1 || a->max_span > a->budget || a->tokens < 0)
     return fail(LOGKV_EINVAL, "bad selection sizes");
-  if (int64_t(a->budget) + a->tokens + 1 > 4096)
-    return fail(LOGKV_EINVAL, "budget + rows + 1 = %d exceeds 4096 candidates per batch row",
-                a->budget + a->tokens + 1);
+  if (int64_t(a->budget) + a->tokens + 1 > logkv::kMaxCandidates)
+    return fail(LOGKV_EINVAL, "budget + rows + 1 = %d exceeds %d candidates per batch row",
+                a->budget + a->tokens + 1, logkv::kMaxCandidates);
   if (!a->span_len || !a->span_closed || !a->span_count || !a->pool_pos || !a->keep || !a->archive ||
       !a->archive_count || !a->new_span_len || !a->new_span_closed || !a->new_span_count || !a->alpha_count)
     return fail(LOGKV_EINVAL, "selection buffer is NULL");

@@ -21,7 +21,6 @@ namespace logkv {
 namespace {
 
 constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
 constexpr int kMoveUnits = 8;    // 8-byte units per thread staged in registers per move chunk
 constexpr int kCenterRows = 128;  // key rows staged in LDS per center-update chunk
 
@@ -71,9 +70,11 @@ struct Meta {
 // Where the staged rows of the current level come from.
 //  kind 0: flush rows tok[r] of the lane (w=1, anchors = position, order = base + r)
 //  kind 1: a scratch SoA buffer
+//  kind 2: as kind 0 with the row list read from global memory
 struct Src {
   int kind;
-  const LOGKV_S uint16_t* tok;
+  const LOGKV_S uint16_t* tok;     // kind 0: row list in LDS
+  const LOGKV_G uint16_t* gtok;    // kind 2: row list in global memory
   int64_t order_base;
   const LOGKV_G uint16_t* kb;
   const LOGKV_G uint16_t* vb;
@@ -146,7 +147,8 @@ struct PoolT {
   int cnt;       // rows stored before this step
   Src src;
   __device__ __forceinline__ int64_t staged_row(int q) const {
-    return KIND == 1 ? static_cast<int64_t>(q) : static_cast<int64_t>(src.tok[q]);
+    if (KIND == 1) return static_cast<int64_t>(q);
+    return KIND == 2 ? static_cast<int64_t>(src.gtok[q]) : static_cast<int64_t>(src.tok[q]);
   }
   __device__ __forceinline__ const LOGKV_G uint16_t* k(int p) const {
     const bool st = p < cnt;
@@ -166,7 +168,7 @@ struct PoolT {
   // a staged index to row 0) and the value is selected afterwards.
   __device__ __forceinline__ float w(int p) const {
     const bool st = p < cnt;
-    if (KIND == 0) {
+    if (KIND != 1) {
       const float stored = L.w[base + (st ? p : 0)];
       return st ? stored : 1.0f;
     }
@@ -183,7 +185,7 @@ struct PoolT {
                   *(st ? L.ord + i : src.buf.ord + j), *(st ? L.pad + i : src.buf.pad + j)};
     }
     const int q = st ? 0 : p - cnt;
-    const int64_t pos = src.posb[src.tok[q]];
+    const int64_t pos = src.posb[staged_row(q)];
     const Meta stored = slot_meta(L, st ? i : base);
     return st ? stored : Meta{1.0f, pos, pos, pos, src.order_base + q, 0};
   }
@@ -297,38 +299,6 @@ __device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int6
   for (int64_t r = threadIdx.x; r < n; r += blockDim.x) put_slot_meta(L, first + r, Meta{0.f, 0, 0, 0, 0, 0});
 }
 
-// Carries j in [j_begin, j_end) from pool rows (2j, 2j+1); loads of kBatch
-// carries per thread are issued before their stores.
-template <int KIND>
-__device__ __forceinline__ void pair_carries(const PoolT<KIND>& pool, const Soa& out, int j_begin, int n_carry, int dk,
-                                             int dv) {
-  const RowUnits ru(dk, dv);
-  for (int j0 = j_begin + ru.r0; j0 < n_carry; j0 += kBatch * ru.step) {
-    uint2 a[kBatch], b[kBatch];
-    float wa[kBatch], wb[kBatch];
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int j = j0 + q * ru.step;
-      if (j < n_carry) {
-        wa[q] = pool.w(2 * j);
-        wb[q] = pool.w(2 * j + 1);
-        a[q] = load_unit(pool.k(2 * j), pool.v(2 * j), ru.u, ru.ku);
-        b[q] = load_unit(pool.k(2 * j + 1), pool.v(2 * j + 1), ru.u, ru.ku);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int j = j0 + q * ru.step;
-      if (j < n_carry) {
-        const float alpha = wa[q] / fmaxf(wa[q] + wb[q], 1e-8f);
-        store_unit(out.k + static_cast<int64_t>(j) * dk, out.v + static_cast<int64_t>(j) * dv, ru.u, ru.ku,
-                   blend_unit(a[q], b[q], alpha));
-      }
-    }
-  }
-  for (int j = j_begin + static_cast<int>(threadIdx.x); j < n_carry; j += blockDim.x)
-    put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
-}
 
 // ---- Beta 4->2 -------------------------------------------------------------
 
@@ -455,116 +425,7 @@ __device__ __forceinline__ Meta side_meta(const Meta& mine, bool member, float m
   return r;
 }
 
-// Beta groups are staged in LDS a chunk at a time: the K|V rows and metadata
-// of up to beta_chunk_groups() groups of four, loaded by the whole block with
-// many rows in flight, then one wave per group computes from LDS.
-constexpr int kBetaStageBytes = 32 * 1024;
 constexpr int kCarryThreads = 256;   // block size of the carries launches
-
-__host__ __device__ inline int beta_chunk_groups(int dk, int dv) {
-  const int g = kBetaStageBytes / (4 * (dk + dv) * 2);
-  constexpr int waves = kCarryThreads / kWave;
-  return g < waves ? waves : (g > 64 ? 64 : g);
-}
-
-__host__ __device__ inline int64_t beta_stage_bytes(int dk, int dv) {
-  const int64_t rows = 4 * static_cast<int64_t>(beta_chunk_groups(dk, dv));
-  return align16(rows * (dk + dv) * 2) + rows * static_cast<int64_t>(sizeof(Meta));
-}
-
-// One wave per group of four carry inputs (litgpt/beta_log_kv.py:29-105).
-// Features l + 64 j (j < NJ) of every row live in lane l; lane i < 4 also
-// holds row i's metadata. `stage` is LDS of beta_stage_bytes(dk, dv).
-template <int NJ, int KIND>
-__device__ __forceinline__ void beta_carries(const PoolT<KIND>& pool, const Soa& out, int n_pair, int dk, int dv,
-                                             uint8_t* stage, int g_begin, int g_end) {
-  const int l = lane_id(), w = wave_id();
-  const int n_groups = min(g_end, (n_pair + 3) / 4);
-  const int cg = beta_chunk_groups(dk, dv);
-  LOGKV_S uint16_t* sk = (LOGKV_S uint16_t*)stage;
-  LOGKV_S uint16_t* sv = sk + 4 * cg * dk;
-  LOGKV_S Meta* sm = (LOGKV_S Meta*)(stage + align16(4 * static_cast<int64_t>(cg) * (dk + dv) * 2));
-  const RowUnits ru(dk, dv);
-  for (int g0 = g_begin; g0 < n_groups; g0 += cg) {
-    const int ng = min(cg, n_groups - g0);
-    const int p0 = 4 * g0;
-    const int rows = min(4 * ng, n_pair - p0);
-    __syncthreads();   // the previous chunk is done with the stage
-    for (int r0 = ru.r0; r0 < rows; r0 += kBatch * ru.step) {
-      uint2 x[kBatch];
-#pragma unroll
-      for (int q = 0; q < kBatch; ++q) {
-        const int r = r0 + q * ru.step;
-        if (r < rows) x[q] = load_unit(pool.k(p0 + r), pool.v(p0 + r), ru.u, ru.ku);
-      }
-#pragma unroll
-      for (int q = 0; q < kBatch; ++q) {
-        const int r = r0 + q * ru.step;
-        if (r < rows) {
-          LOGKV_S uint16_t* dst = ru.u < ru.ku ? sk + r * dk + 4 * ru.u : sv + r * dv + 4 * (ru.u - ru.ku);
-          *(LOGKV_S uint2*)dst = x[q];
-        }
-      }
-    }
-    for (int r = threadIdx.x; r < rows; r += blockDim.x) sm[r] = pool.meta(p0 + r);
-    __syncthreads();
-    for (int gl = w; gl < ng; gl += static_cast<int>(blockDim.x) / kWave) {
-      const int start = p0 + 4 * gl;
-      const int width = min(4, n_pair - start);
-      const int rl = 4 * gl;
-      float xk[4][NJ], xv[4][NJ], wr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool valid = i < width;
-        const int row = rl + (valid ? i : 0);
-        const float wi = sm[row].w;
-        wr[i] = valid ? wi : 0.f;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int d = l + j * kWave;
-          const float a = bf16_to_f32(sk[row * dk + (d < dk ? d : dk - 1)]);
-          const float b = bf16_to_f32(sv[row * dv + (d < dv ? d : dv - 1)]);
-          xk[i][j] = (valid && d < dk) ? a : 0.f;
-          xv[i][j] = (valid && d < dv) ? b : 0.f;
-        }
-      }
-      const Meta ml = sm[rl + (l & 3)];
-      const Meta mine = l < width ? ml : Meta{};
-      int cut = 1;
-      if (width == 4) {
-        const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
-        float costs[3] = {0.f, 0.f, 0.f};
-        beta_component_cost<NJ>(xk, wr, total, dk, costs);
-        beta_component_cost<NJ>(xv, wr, total, dv, costs);
-        int best = 0;
-        if (costs[1] < costs[best]) best = 1;
-        if (costs[2] < costs[best]) best = 2;
-        cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
-      }
-      const int dest = start / 2;
-      for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
-        unsigned member;
-        if (width == 2) member = 0x3u;
-        else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
-        float wt[4], mk[NJ], mv[NJ], mass;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-        side_mean<NJ>(xk, wt, mk, mass);
-        side_mean<NJ>(xv, wt, mv, mass);
-        const int64_t o = dest + side;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int d = l + j * kWave;
-          if (d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
-          if (d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
-        }
-        const bool in_side = l < width && ((member >> (l & 3)) & 1u);
-        const Meta r = side_meta(mine, in_side, mass);
-        if (l == 0) put_soa_meta(out, o, r);
-      }
-    }
-  }
-}
 
 // Saturated top level: slot 0 <- left fold of P[0..mr] (bf16 after every
 // merge), slots 1..B'-1 <- P[mr+1..]. Rare (a whole ladder must be full), so
@@ -609,6 +470,90 @@ __device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
   }
 }
 
+// ---- Flat carry work ---------------------------------------------------------
+//
+// A carries launch spreads one level's carry work over every wave of the GPU:
+// a unit is one Beta group of four pair rows (two outputs) or one pair carry,
+// units are numbered ladder after ladder (prefix sums over ladders), and each
+// wave takes units by a grid stride. A unit's rows are loaded by its wave
+// directly, every load issued before its arithmetic.
+
+// One Beta group (litgpt/beta_log_kv.py:29-105): rows [4 gi, 4 gi + width) of
+// the level's pool into outputs 2 gi, 2 gi + 1. Features l + 64 j (j < NJ) of
+// every row live in lane l; lane i < 4 also holds row i's metadata. The whole
+// wave must be active.
+template <int NJ, int KIND>
+__device__ __forceinline__ void beta_group(const PoolT<KIND>& pool, const Soa& out, int n_pair, int gi, int dk,
+                                           int dv) {
+  const int l = lane_id();
+  const int start = 4 * gi;
+  const int width = min(4, n_pair - start);
+  float xk[4][NJ], xv[4][NJ], wr[4];
+  const Meta ml = pool.meta(l < width ? start + l : start);
+  const Meta mine = l < width ? ml : Meta{};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool valid = i < width;
+    const int p = valid ? start + i : start;
+    const float wp = pool.w(p);
+    wr[i] = valid ? wp : 0.f;
+    const LOGKV_G uint16_t* kr = pool.k(p);
+    const LOGKV_G uint16_t* vr = pool.v(p);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int d = l + j * kWave;
+      const float a = feat_or_zero(kr, d, dk), b = feat_or_zero(vr, d, dv);
+      xk[i][j] = valid ? a : 0.f;
+      xv[i][j] = valid ? b : 0.f;
+    }
+  }
+  int cut = 1;
+  if (width == 4) {
+    const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
+    float costs[3] = {0.f, 0.f, 0.f};
+    beta_component_cost<NJ>(xk, wr, total, dk, costs);
+    beta_component_cost<NJ>(xv, wr, total, dv, costs);
+    int best = 0;
+    if (costs[1] < costs[best]) best = 1;
+    if (costs[2] < costs[best]) best = 2;
+    cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
+  }
+  const int dest = start / 2;
+  for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
+    unsigned member;
+    if (width == 2) member = 0x3u;
+    else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
+    float wt[4], mk[NJ], mv[NJ], mass;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
+    side_mean<NJ>(xk, wt, mk, mass);
+    side_mean<NJ>(xv, wt, mv, mass);
+    const int64_t o = dest + side;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int d = l + j * kWave;
+      if (d < dk) out.k[o * dk + d] = f32_to_bf16(mk[j]);
+      if (d < dv) out.v[o * dv + d] = f32_to_bf16(mv[j]);
+    }
+    const bool in_side = l < width && ((member >> (l & 3)) & 1u);
+    const Meta r = side_meta(mine, in_side, mass);
+    if (l == 0) put_soa_meta(out, o, r);
+  }
+}
+
+// One pair carry j (pool rows 2j, 2j + 1), one wave.
+template <int KIND>
+__device__ __forceinline__ void pair_carry(const PoolT<KIND>& pool, const Soa& out, int j, int dk, int dv) {
+  const int ku = dk / 4, units = (dk + dv) / 4;
+  const float wa = pool.w(2 * j), wb = pool.w(2 * j + 1);
+  const float alpha = wa / fmaxf(wa + wb, 1e-8f);
+  const LOGKV_G uint16_t *ak = pool.k(2 * j), *av = pool.v(2 * j), *bk = pool.k(2 * j + 1), *bv = pool.v(2 * j + 1);
+  for (int u = lane_id(); u < units; u += kWave)
+    store_unit(out.k + static_cast<int64_t>(j) * dk, out.v + static_cast<int64_t>(j) * dv, u, ku,
+               blend_unit(load_unit(ak, av, u, ku), load_unit(bk, bv, u, ku), alpha));
+  if (lane_id() == 0) put_soa_meta(out, j, merge_meta(pool.meta(2 * j), pool.meta(2 * j + 1)));
+}
+
 // One level of a Fenwick append. With the virtual pool P = [stored 0..cnt |
 // staged 0..m] of n_pool = cnt + m rows:
 //  * n_pool <= B': the staged rows fill slots [cnt, n_pool);
@@ -616,30 +561,13 @@ __device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
 //    pair into carries, P[n_pair..) moves to slots [0, n_surv), the rest clears;
 //  * at the top: slot 0 = left fold of P[0..mr] (bf16 after every merge) and
 //    slots 1..B'-1 = P[mr+1..n_pool), mr = n_pool - B'.
-// The carries are computed by every block of a level launch (a slice each);
-// the slot writes (fill, move, clear, fold) by one block in the next launch,
-// after every carry of the level has read the stored slots.
+// The carries are computed by the level's carries launch (spread over the
+// grid); the slot writes (fill, move, clear, fold) by one block in the finish
+// launch, after every carry of every level has read the stored slots.
 __host__ __device__ inline int carries_of(int cnt, int m, int B, bool top) {
   const int n_pool = cnt + m;
   if (m == 0 || n_pool <= B || top) return 0;
   return (n_pool - B + 1) / 2;
-}
-
-template <int KIND, int NJ>
-__device__ __forceinline__ void level_carries(const Ladder& L, int ell, int cnt, const Src& cur, int m, const Soa& out,
-                                              bool beta, uint8_t* stage, int part, int parts) {
-  const int n_carry = carries_of(cnt, m, L.B, false);
-  const PoolT<KIND> pool{L, static_cast<int64_t>(ell) * L.B, cnt, cur};
-  if (beta) {
-    const int n_pair = 2 * n_carry, n_groups = (n_pair + 3) / 4;
-    const int g0 = static_cast<int>(static_cast<int64_t>(part) * n_groups / parts);
-    const int g1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_groups / parts);
-    beta_carries<NJ, KIND>(pool, out, n_pair, L.dk, L.dv, stage, g0, g1);
-  } else {
-    const int j0 = static_cast<int>(static_cast<int64_t>(part) * n_carry / parts);
-    const int j1 = static_cast<int>(static_cast<int64_t>(part + 1) * n_carry / parts);
-    pair_carries<KIND>(pool, out, j0, j1, L.dk, L.dv);
-  }
 }
 
 // Slot writes of one level step; returns the level's new count.
@@ -1016,27 +944,100 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   }
 }
 
-// Carries launch `ell`: block (ladder, part) computes its slice of level
-// ell's carries. Launches ell = 0..L-2 run in stream order (level ell stages
+// Carry work of every level: block ell writes units[ell][i] = work units of
+// ladders 0..i-1 at level ell (a unit is one Beta group of two carries, or one
+// pair carry), i = 0..ladders.
+__global__ __launch_bounds__(kCarryThreads) void units_kernel(LadderArgs c, RouteParams prm, Workspace ws) {
+  __shared__ int wave_total[kCarryThreads / kWave];
+  const int ell = blockIdx.x;
+  const int ladders = c.n_batch * c.n_groups * c.k_max;
+  int32_t* out = ws.units + static_cast<int64_t>(ell) * (ladders + 1);
+  const int l = lane_id(), w = wave_id();
+  if (threadIdx.x == 0) out[0] = 0;
+  int carry = 0;
+  for (int base = 0; base < ladders; base += kCarryThreads) {
+    const int i = base + static_cast<int>(threadIdx.x);
+    int n = 0;
+    if (i < ladders) {
+      const LadderPlan* pl = ws.plans + i;
+      const int nc = pl->active ? carries_of(pl->cnt[ell], pl->m[ell], c.slots, ell == c.levels - 1) : 0;
+      n = prm.beta_merge ? (nc + 1) / 2 : nc;
+    }
+    int incl = n;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int t = __shfl_up(incl, d, kWave);
+      if (l >= d) incl += t;
+    }
+    if (l == kWave - 1) wave_total[w] = incl;
+    __syncthreads();
+    int before = carry;
+    for (int q = 0; q < w; ++q) before += wave_total[q];
+    if (i < ladders) out[i + 1] = before + incl;
+    for (int q = 0; q < kCarryThreads / kWave; ++q) carry += wave_total[q];
+    __syncthreads();   // wave_total is rewritten by the next chunk
+  }
+}
+
+// The ladder's flush rows as a level-0 source, row list read from global memory.
+__device__ inline Src flush_rows_global(const LadderArgs& c, const RowsArgs& r, const Workspace& ws,
+                                        const LadderPlan* pl, int ladder) {
+  const int lane_ix = ladder / c.k_max;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  Src s{};
+  s.kind = 2;
+  s.gtok = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens + pl->first);
+  s.order_base = pl->order_base;
+  s.kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  s.vb = gp(r.v + b * r.v_sb + g * r.v_sg);
+  s.k_st = r.k_st;
+  s.v_st = r.v_st;
+  s.posb = gp(r.pos + b * r.pos_sb);
+  return s;
+}
+
+// Carries launch `ell`: the level's work units (numbered ladder after ladder
+// by units_kernel) are spread over all waves of the grid by a grid stride; a
+// wave finds its unit's ladder by binary search over the unit prefix table
+// staged in LDS. Launches ell = 0..L-2 run in stream order (level ell stages
 // level ell - 1's carries); slots are not written here.
 template <int NJ>
 __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
                                                                 Workspace ws, int ell) {
-  extern __shared__ __align__(16) uint8_t dyn[];
-  const int ladder = blockIdx.x, part = blockIdx.y, parts = gridDim.y;
-  const LadderPlan* pl = ws.plans + ladder;
-  if (!pl->active) return;
-  const int cnt = pl->cnt[ell], m = pl->m[ell];
-  if (carries_of(cnt, m, c.slots, ell == c.levels - 1) == 0) return;
-  const Ladder lad = ladder_of(c, ladder);
-  uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
-  uint8_t* stage = dyn + ((2 * r.tokens + 15) & ~15);
+  extern __shared__ __align__(16) int32_t prefix_s[];
+  const int ladders = c.n_batch * c.n_groups * c.k_max;
+  const LOGKV_G int32_t* pre = gp(ws.units + static_cast<int64_t>(ell) * (ladders + 1));
+  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  __syncthreads();
+  const int total = prefix_s[ladders];
+  const int wpb = static_cast<int>(blockDim.x) / kWave;
+  const int stride = static_cast<int>(gridDim.x) * wpb;
   const bool beta = prm.beta_merge != 0;
-  const Soa out = carry_of(ws, ladder, ell, c.dk, c.dv);
-  if (ell == 0 && pl->kind0 == 0)
-    level_carries<0, NJ>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, tok), m, out, beta, stage, part, parts);
-  else
-    level_carries<1, NJ>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m, out, beta, stage, part, parts);
+  for (int u = static_cast<int>(blockIdx.x) * wpb + wave_id(); u < total; u += stride) {
+    int lo = 0, hi = ladders;   // prefix_s[lo] <= u < prefix_s[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (prefix_s[mid] <= u) lo = mid;
+      else hi = mid;
+    }
+    const int ladder = __builtin_amdgcn_readfirstlane(lo);
+    const int lu = u - prefix_s[ladder];
+    const LadderPlan* pl = ws.plans + ladder;
+    const int cnt = pl->cnt[ell], m = pl->m[ell];
+    const int n_carry = carries_of(cnt, m, c.slots, false);
+    const Ladder lad = ladder_of(c, ladder);
+    const int64_t base = static_cast<int64_t>(ell) * c.slots;
+    const Soa out = carry_of(ws, ladder, ell, c.dk, c.dv);
+    if (ell == 0 && pl->kind0 == 0) {
+      const PoolT<2> pool{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)};
+      if (beta) beta_group<NJ, 2>(pool, out, 2 * n_carry, lu, c.dk, c.dv);
+      else pair_carry<2>(pool, out, lu, c.dk, c.dv);
+    } else {
+      const PoolT<1> pool{lad, base, cnt, staged_of(ws, ladder, ell, c.dk, c.dv)};
+      if (beta) beta_group<NJ, 1>(pool, out, 2 * n_carry, lu, c.dk, c.dv);
+      else pair_carry<1>(pool, out, lu, c.dk, c.dv);
+    }
+  }
 }
 
 // Slot writes of every level (block (ladder, level)): fill, move and clear, or
@@ -1059,7 +1060,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs
   if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * c.levels + ell] = static_cast<int16_t>(n);
 }
 
-constexpr int kParts = 32;   // blocks per ladder for level 0's carries (halved per level)
+constexpr int kCarryBlocks = 2048;   // most blocks of a carries launch (8 per CU)
 
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
@@ -1074,20 +1075,25 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
     return LOGKV_ERUNTIME;
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
-  const size_t carry_shmem = tok_bytes + (p.beta_merge ? static_cast<size_t>(beta_stage_bytes(c.dk, c.dv)) : 0);
-  const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
-  const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
-                               : reinterpret_cast<const void*>(&carries_kernel<4>);
-  if (carry_shmem > 64 * 1024 &&
-      hipFuncSetAttribute(carries, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(carry_shmem)) !=
-          hipSuccess)
-    return LOGKV_ERUNTIME;
-  for (int ell = 0; ell + 1 < c.levels; ++ell) {
-    const dim3 grid(ladders, std::max(1, kParts >> ell));
-    if (narrow)
-      hipLaunchKernelGGL(carries_kernel<2>, grid, dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
-    else
-      hipLaunchKernelGGL(carries_kernel<4>, grid, dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
+  if (c.levels > 1) {
+    hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kCarryThreads), 0, stream, c, p, ws);
+    const size_t carry_shmem = (static_cast<size_t>(ladders) + 1) * 4;
+    const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
+    const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
+                                 : reinterpret_cast<const void*>(&carries_kernel<4>);
+    if (carry_shmem > 64 * 1024 &&
+        hipFuncSetAttribute(carries, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(carry_shmem)) !=
+            hipSuccess)
+      return LOGKV_ERUNTIME;
+    for (int ell = 0; ell + 1 < c.levels; ++ell) {
+      // Units at level ell: at most ceil(carries / 2) Beta groups (or carries) per ladder.
+      const int64_t bound = static_cast<int64_t>(ladders) * carry_cap(ws.m0_cap, ell);
+      const int64_t blocks = std::min<int64_t>(kCarryBlocks, std::max<int64_t>(1, bound / (kCarryThreads / kWave)));
+      if (narrow)
+        hipLaunchKernelGGL(carries_kernel<2>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
+      else
+        hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
+    }
   }
   hipLaunchKernelGGL(finish_kernel, dim3(ladders, c.levels), dim3(kThreads), tok_bytes, stream, c, r, ws);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;

@@ -24,6 +24,8 @@ __device__ __forceinline__ int valid_rows(const logkv_rows_view& r, int b) {
 }
 
 constexpr int kMaxLevels = 32;        // ladder levels L
+constexpr int kMaxCandidates = 4096;  // Alpha span candidates per batch row (selection sorts them in LDS)
+constexpr int kMaxLadders = 32768;    // batch * groups * K (a level's carry work table is staged in LDS)
 
 // Per-ladder plan of one commit, written by the prepare launch and read by the
 // level launches: counts before each level step and the rows staged into it.
@@ -51,6 +53,7 @@ struct Workspace {
   int32_t sort_width;     // keys per block for the delayed-archive sort (0 without it)
   LadderPlan* plans;      // [ladders]
   uint16_t* tok;          // [ladders, T] each ladder's flush rows in position order
+  int32_t* units;         // [L - 1, ladders + 1] prefix sums over ladders of each level's carry work units
 };
 
 int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t m0);
