@@ -245,8 +245,10 @@ __device__ __forceinline__ void move_rows(const PoolT<KIND>& pool, int p0, int d
     uint2 buf[kMoveUnits];
 #pragma unroll
     for (int q = 0; q < kMoveUnits; ++q) {
-      const int r = ru.r0 + q * ru.step;
-      if (r < rows) buf[q] = load_unit(pool.k(p0 + c0 + r), pool.v(p0 + c0 + r), ru.u, ru.ku);
+      // Unconditional loads (a row past the chunk re-reads its last row) keep
+      // every load of the chunk in flight at once.
+      const int r = min(ru.r0 + q * ru.step, rows - 1);
+      buf[q] = load_unit(pool.k(p0 + c0 + r), pool.v(p0 + c0 + r), ru.u, ru.ku);
     }
     Meta m{};
     if (static_cast<int>(threadIdx.x) < rows) m = pool.meta(p0 + c0 + threadIdx.x);
@@ -274,8 +276,8 @@ __device__ __forceinline__ void copy_staged(const Ladder& L, int64_t base, const
     uint2 x[kBatch];
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
-      const int r = r0 + q * ru.step;
-      if (r < n) x[q] = load_unit(pool.k(s0 + r), pool.v(s0 + r), ru.u, ru.ku);
+      const int r = min(r0 + q * ru.step, n - 1);
+      x[q] = load_unit(pool.k(s0 + r), pool.v(s0 + r), ru.u, ru.ku);
     }
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
@@ -428,44 +430,88 @@ __device__ __forceinline__ Meta side_meta(const Meta& mine, bool member, float m
 constexpr int kCarryThreads = 256;   // block size of the carries launches
 
 // Saturated top level: slot 0 <- left fold of P[0..mr] (bf16 after every
-// merge), slots 1..B'-1 <- P[mr+1..]. Rare (a whole ladder must be full), so
-// it stays out of line with one wave doing the sequential fold.
+// merge), slots 1..B'-1 <- P[mr+1..]. The fold is sequential in its rows and
+// parallel in its features: wave 0 holds two 8-byte units of every lane,
+// prefetches 8 rows ahead and reads row weights from the lane that loaded
+// them. The folded metadata is an order-free reduction except for the mass,
+// which follows the fold's left-to-right sums: lo / hi are the min / max over
+// rows of positive mass (the last row's if none), sum(w*p) the sum, order the
+// min and the pad flag the AND (merge_meta applied left to right).
+__device__ __forceinline__ int64_t shfl_xor64(int64_t x, int mask) {
+  const int lo = __shfl_xor(static_cast<int>(x), mask, kWave);
+  const int hi = __shfl_xor(static_cast<int>(x >> 32), mask, kWave);
+  return (static_cast<int64_t>(hi) << 32) | static_cast<uint32_t>(lo);
+}
+
+constexpr int kFoldAhead = 8;   // rows of the top fold in flight
+
 template <int KIND>
-__device__ __noinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
+__device__ __forceinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
   const Ladder& L = pool.L;
-  constexpr int kMaxUnitsPerLane = (2 * kMaxDim / 4) / kWave;
-  const int B = L.B, ku = L.dk / 4, units = (L.dk + L.dv) / 4;
+  const int B = L.B, ku = L.dk / 4, units = (L.dk + L.dv) / 4;   // units <= 2 * kWave
   const int64_t base = pool.base;
-  uint2 acc[kMaxUnitsPerLane];
+  uint2 acc0{}, acc1{};
   Meta am{};
   if (wave_id() == 0) {
     const int l = lane_id();
-    am = pool.meta(0);
+    const int c0 = min(l, units - 1), c1 = min(l + kWave, units - 1);
+    acc0 = load_unit(pool.k(0), pool.v(0), c0, ku);
+    acc1 = load_unit(pool.k(0), pool.v(0), c1, ku);
+    float mass = pool.w(0);
+    for (int t0 = 1; t0 <= mr; t0 += kWave) {
+      const int nb = min(kWave, mr + 1 - t0);
+      const float wl = pool.w(t0 + min(l, nb - 1));
+      for (int i0 = 0; i0 < nb; i0 += kFoldAhead) {
+        uint2 x0[kFoldAhead], x1[kFoldAhead];
 #pragma unroll
-    for (int q = 0; q < kMaxUnitsPerLane; ++q) {
-      const int u = l + q * kWave;
-      if (u < units) acc[q] = load_unit(pool.k(0), pool.v(0), u, ku);
-    }
-    for (int t = 1; t <= mr; ++t) {
-      const Meta b = pool.meta(t);
-      const float alpha = am.w / fmaxf(am.w + b.w, 1e-8f);
-      const LOGKV_G uint16_t *bk = pool.k(t), *bv = pool.v(t);
+        for (int q = 0; q < kFoldAhead; ++q) {
+          const int t = t0 + min(i0 + q, nb - 1);
+          x0[q] = load_unit(pool.k(t), pool.v(t), c0, ku);
+          x1[q] = load_unit(pool.k(t), pool.v(t), c1, ku);
+        }
 #pragma unroll
-      for (int q = 0; q < kMaxUnitsPerLane; ++q) {
-        const int u = l + q * kWave;
-        if (u < units) acc[q] = blend_unit(acc[q], load_unit(bk, bv, u, ku), alpha);
+        for (int q = 0; q < kFoldAhead; ++q) {
+          if (i0 + q < nb) {
+            const float bw = __shfl(wl, i0 + q, kWave);
+            const float alpha = mass / fmaxf(mass + bw, 1e-8f);
+            acc0 = blend_unit(acc0, x0[q], alpha);
+            acc1 = blend_unit(acc1, x1[q], alpha);
+            mass = mass + bw;
+          }
+        }
       }
-      am = merge_meta(am, b);
     }
+    // Metadata of rows 0..mr, lane l taking rows l, l + 64, ...
+    bool real = false;
+    int64_t lo = INT64_MAX, hi = INT64_MIN, swp = 0, ord = INT64_MAX;
+    int pad = 1;
+    for (int t = l; t <= mr; t += kWave) {
+      const Meta m = pool.meta(t);
+      const bool rt = m.w > 0.f;
+      real = real || rt;
+      lo = rt ? imin64(lo, m.lo) : lo;
+      hi = rt ? imax64(hi, m.hi) : hi;
+      swp += m.swp;
+      ord = imin64(ord, m.ord);
+      pad &= m.pad;
+    }
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      lo = imin64(lo, shfl_xor64(lo, d));
+      hi = imax64(hi, shfl_xor64(hi, d));
+      swp += shfl_xor64(swp, d);
+      ord = imin64(ord, shfl_xor64(ord, d));
+      pad &= __shfl_xor(pad, d, kWave);
+    }
+    const bool any_real = __any(real);
+    const Meta last = pool.meta(mr);
+    am = Meta{mass, any_real ? lo : last.lo, any_real ? hi : last.hi, swp, ord, static_cast<uint8_t>(pad)};
   }
   move_rows(pool, mr + 1, 1, B - 1);
   if (wave_id() == 0) {
     const int l = lane_id();
-#pragma unroll
-    for (int q = 0; q < kMaxUnitsPerLane; ++q) {
-      const int u = l + q * kWave;
-      if (u < units) store_unit(L.k + base * L.dk, L.v + base * L.dv, u, ku, acc[q]);
-    }
+    if (l < units) store_unit(L.k + base * L.dk, L.v + base * L.dv, l, ku, acc0);
+    if (l + kWave < units) store_unit(L.k + base * L.dk, L.v + base * L.dv, l + kWave, ku, acc1);
     if (l == 0) put_slot_meta(L, base, am);
   }
 }
@@ -864,23 +910,18 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
           uint2 x[kBatch];
 #pragma unroll
           for (int qb = 0; qb < kBatch; ++qb) {
-            const int rank = r0 + qb * ru.step;
-            if (rank < total) {
-              const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
-              const LOGKV_G uint16_t *ks, *vs;
-              if (q < n_exist) {
-                int e = 0;
-                while (e + 1 < L && level_start[e + 1] <= q) ++e;
-                const int64_t slot = static_cast<int64_t>(e) * B + (q - level_start[e]);
-                ks = lad.k + slot * dk;
-                vs = lad.v + slot * dv;
-              } else {
-                const int t = tok[first + q - n_exist];
-                ks = kb + static_cast<int64_t>(t) * r.k_st;
-                vs = vb + static_cast<int64_t>(t) * r.v_st;
-              }
-              x[qb] = load_unit(ks, vs, ru.u, ru.ku);
-            }
+            // Addresses by selects and an unconditional load (a rank past the
+            // end re-reads the last one), so all kBatch loads are in flight.
+            const int rank = min(r0 + qb * ru.step, total - 1);
+            const int q = static_cast<int>(keys[rank] & kOrderIndexMask);
+            const bool ex = q < n_exist;
+            int e = 0;
+            while (e + 1 < L && level_start[e + 1] <= q) ++e;
+            const int64_t slot = static_cast<int64_t>(e) * B + (q - level_start[e]);
+            const int t = tok[first + max(q - n_exist, 0)];   // the flush rows start at tok[first]
+            const LOGKV_G uint16_t* ks = ex ? lad.k + slot * dk : kb + static_cast<int64_t>(t) * r.k_st;
+            const LOGKV_G uint16_t* vs = ex ? lad.v + slot * dv : vb + static_cast<int64_t>(t) * r.v_st;
+            x[qb] = load_unit(ks, vs, ru.u, ru.ku);
           }
 #pragma unroll
           for (int qb = 0; qb < kBatch; ++qb) {

@@ -31,15 +31,21 @@ def test_flush_matches_oracle(name):
     assert int(to_np(gpu.alive).sum()) > 0
 
 
-def test_top_level_fold_and_skewed_cluster():
+@pytest.mark.parametrize("dim,flush,max_seq,sizes", [
+    (64, 64, 64, (1, 40, 64, 64, 64, 64)),
+    # 256-wide rows (two 8-byte units per lane in the fold) and, with three
+    # levels, top folds of 70 and more rows (several weight batches)
+    (256, 512, 8, (1, 300, 512, 512)),
+])
+def test_top_level_fold_and_skewed_cluster(dim, flush, max_seq, sizes):
     """One hot cluster saturates every level, so the top level folds."""
-    batch, groups, dim, K, B = 1, 2, 64, 4, 4
-    gpu, ora = make_pair(batch, groups, dim, K, B, recent=64, flush=64, max_seq=64, s_h=1e9)
+    batch, groups, K, B = 1, 2, 4, 4
+    gpu, ora = make_pair(batch, groups, dim, K, B, recent=flush, flush=flush, max_seq=max_seq, s_h=1e9)
     assert gpu.L_alloc == ora.L
     mix = Mixture(batch, groups, dim, clusters=1, seed=3, outlier=0.0)
     dev = gpu.level_k.device
     start = 0
-    for n in (1, 40, 64, 64, 64, 64):
+    for n in sizes:
         k, v = mix.rows(n), mix.rows(n)
         pos = torch.arange(start, start + n).unsqueeze(0).expand(batch, -1).contiguous()
         gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev))
