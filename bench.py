@@ -36,6 +36,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+METER_EVERY = 7   # layers 0, 7, 14, 21 carry the commit-stage events
 G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
 EXACT, SPAN = 256, 64
 
@@ -269,29 +270,38 @@ def flush_workload(args, torch, np):
     data = [[(mixture(li), mixture(li)) for li in range(layers)] for _ in range(n_flush)]
     positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).contiguous() for j in range(n_flush)]
     positions_host = [[list(range(j * F, (j + 1) * F))] for j in range(n_flush)]
-    ends = [span_ends_for(j) for j in range(n_flush)]
+    # Boundary flags staged on the device like the rows and positions.
+    ends = [torch.tensor(span_ends_for(j), dtype=torch.uint8, device=dev) for j in range(n_flush)]
     dim = packed_dim(D, D)
     empty = torch.empty(1, G, 0, D, dtype=torch.bfloat16, device=dev)
     workspaces = [(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev),
                    torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev)) for c in caches]
     torch.cuda.synchronize()
 
+    # Layer li's flushes are issued on stream li % streams (the layers' caches are
+    # independent, so their flushes may overlap; each layer's own flushes stay in order).
+    streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(args.streams - 1)]
+
     def flush(j):
         for li, cache in enumerate(caches):
-            k, v = data[j][li]
-            cache.route_and_flush_batch(k, v, positions[j], positions_host=positions_host[j], span_ends=ends[j])
-            # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
-            view = readout_view(cache)
-            plan = cache._semantic_attention_plan()
-            _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
+            with torch.cuda.stream(streams[li % len(streams)]):
+                k, v = data[j][li]
+                cache.route_and_flush_batch(k, v, positions[j], positions_host=positions_host[j], span_ends=ends[j])
+                # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
+                view = readout_view(cache)
+                plan = cache._semantic_attention_plan()
+                _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
 
     for j in range(2 + args.warmup):
         flush(j)
     torch.cuda.synchronize()
     progress(f"flush: {2 + args.warmup} untimed flushes done")
 
-    meters = [CommitMeter(c, torch) for c in caches]
-    for c, m in zip(caches, meters):
+    # Commit launches of every METER_EVERY-th layer are bracketed by events (the
+    # meter's ladder-state copies stay off the other layers).
+    metered = caches[::METER_EVERY]
+    meters = [CommitMeter(c, torch) for c in metered]
+    for c, m in zip(metered, meters):
         c._route_commit = m
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -299,7 +309,7 @@ def flush_workload(args, torch, np):
         flush(2 + args.warmup + s)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    for c in caches:
+    for c in metered:
         del c._route_commit
     progress(f"flush: {args.steps} timed flushes in {elapsed:.3f} s")
     rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
@@ -408,6 +418,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--streams", type=int, default=1, help="HIP streams the layers' flushes are spread over")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -261,6 +261,88 @@ def _pinned_upload(array: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(array).pin_memory().to(device, non_blocking=True)
 
 
+def _span_ends_device(span_ends, n_batch: int, T: int, device) -> torch.Tensor:
+    """Boundary flags as uint8 ``[n_batch, T]`` on the device: a device tensor
+    (bool or uint8) is used in place, host lists are uploaded."""
+    if isinstance(span_ends, torch.Tensor):
+        if span_ends.device != device or span_ends.shape != (n_batch, T) or span_ends.stride(-1) != 1:
+            raise ValueError("span_ends must be [batch, T] on the cache's device with contiguous rows")
+        if span_ends.dtype == torch.bool:
+            return span_ends.view(torch.uint8)
+        if span_ends.dtype != torch.uint8:
+            raise ValueError("span_ends must be bool or uint8")
+        return span_ends
+    rows = np.zeros((n_batch, T), dtype=np.uint8)
+    for b, row in enumerate(span_ends):
+        rows[b, :len(row)] = np.frombuffer(bytes(bytearray(bool(x) for x in row)), dtype=np.uint8)
+    return _pinned_upload(rows, device)
+
+
+class _AlphaCall:
+    """Argument structs and output buffers of the Alpha flush of one cache, one
+    flush length ``T`` and one of the pool's two buffer sets (``parity``): built
+    once, then only the flush rows' pointers and strides change per call."""
+
+    def __init__(self, cache, T: int, parity_sets, bufs):
+        (pk, pv, ppos, _, slen, sclosed, scount), (nk, nv, npos, nvalid, nlen, nclosed, ncount) = parity_sets
+        n_batch, G, P = cache.batch_size, cache.n_groups, cache.alpha_exact_tokens
+        self.bufs = bufs
+        keep, archive, archive_count, ak, av, ap = bufs["keep"], bufs["archive"], bufs["count"], bufs["k"], \
+            bufs["v"], bufs["pos"]
+        self.rows = _lib.SpanArgs(
+            pk.data_ptr(), pk.stride(0), pk.stride(1), pk.stride(2), pv.data_ptr(), pv.stride(0), pv.stride(1),
+            pv.stride(2), None, 0, 0, 0, None, 0, 0, 0, P, None, None, None, 0, G, cache.k_dim, cache.v_dim,
+            cache.centroid.data_ptr() if cache.beta_novelty else None,
+            cache.alive.data_ptr() if cache.beta_novelty else None, cache.K_max, 1 if cache.beta_novelty else 0,
+            None)
+        self.select = _lib.AlphaSelectArgs(
+            slen.data_ptr(), sclosed.data_ptr(), scount.data_ptr(), ppos.data_ptr(), None, 0, None, 0, T,
+            n_batch, P, cache.alpha_span_max_tokens, self.rows, keep.data_ptr(), archive.data_ptr(),
+            archive_count.data_ptr(), nlen.data_ptr(), nclosed.data_ptr(), ncount.data_ptr(),
+            cache.alpha_count_dev.data_ptr(), None)
+        self.sized = False   # the selection workspace is sized on the first call (it checks the row pointers)
+        self.part = _lib.PartitionArgs(
+            pk.data_ptr(), pk.stride(0), pk.stride(1), pk.stride(2),
+            pv.data_ptr(), pv.stride(0), pv.stride(1), pv.stride(2),
+            ppos.data_ptr(), ppos.stride(0), None, 0, 0, 0, None, 0, 0, 0, None, 0,
+            P, keep.data_ptr(), archive.data_ptr(), P, P + T, n_batch, G, cache.k_dim, cache.v_dim,
+            nk.data_ptr(), nv.data_ptr(), npos.data_ptr(), nvalid.data_ptr(),
+            ak.data_ptr(), av.data_ptr(), ap.data_ptr())
+
+    def set_rows(self, k_raw, v, positions, ends):
+        r, sel, part = self.select.rows, self.select, self.part
+        ks, vs = k_raw.stride(), v.stride()
+        r.flush_k, r.fk_sb, r.fk_sg, r.fk_st = k_raw.data_ptr(), ks[0], ks[1], ks[2]
+        r.flush_v, r.fv_sb, r.fv_sg, r.fv_st = v.data_ptr(), vs[0], vs[1], vs[2]
+        sel.new_pos, sel.np_sb = positions.data_ptr(), positions.stride(0)
+        sel.ends, sel.ends_sb = ends.data_ptr(), ends.stride(0)
+        part.flush_k, part.fk_sb, part.fk_sg, part.fk_st = r.flush_k, ks[0], ks[1], ks[2]
+        part.flush_v, part.fv_sb, part.fv_sg, part.fv_st = r.flush_v, vs[0], vs[1], vs[2]
+        part.flush_pos, part.fp_sb = sel.new_pos, sel.np_sb
+
+
+def _alpha_call(cache, T: int, dtype) -> _AlphaCall:
+    key = ("alpha", T, cache._alpha_parity)
+    call = cache._views.get(key)
+    if call is None:
+        bufs = cache._views.get(("alpha_bufs", T))
+        if bufs is None:
+            n_batch, G, P = cache.batch_size, cache.n_groups, cache.alpha_exact_tokens
+            A, dev = P + T, cache.alpha_k_raw.device
+            bufs = cache._views[("alpha_bufs", T)] = {
+                "keep": torch.empty(n_batch, P, dtype=torch.int32, device=dev),
+                "archive": torch.empty(n_batch, A, dtype=torch.int32, device=dev),
+                "count": torch.empty(n_batch, dtype=torch.int32, device=dev),
+                "k": torch.empty(n_batch, G, A, cache.k_dim, dtype=dtype, device=dev),
+                "v": torch.empty(n_batch, G, A, cache.v_dim, dtype=dtype, device=dev),
+                "pos": torch.empty(n_batch, A, dtype=torch.int64, device=dev),
+            }
+        current = (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid, cache.alpha_span_len,
+                   cache.alpha_span_closed, cache.alpha_span_count)
+        call = cache._views[key] = _AlphaCall(cache, T, (current, cache._alpha_spare), bufs)
+    return call
+
+
 @torch.no_grad()
 def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
     """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003), all on the device.
@@ -270,61 +352,38 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
     cache keeps on the device, so the flush never waits for the host; the
     exact pool is rewritten into the cache's second buffer set (then swapped)
     and the archived rows are attach-routed with delayed joins. Only the
-    boundary flags travel from the host. Row indices address
-    ``[pool (P rows) | flush]``; ``positions_host`` is not needed.
+    boundary flags travel from the host, and not even they when given as a
+    device tensor. Row indices address ``[pool (P rows) | flush]``;
+    ``positions_host`` is not needed. The argument structs and the kept /
+    archived row buffers are built once per flush length and reused.
     """
     if span_ends is None:
         raise ValueError("AlphaLogKV requires natural span boundaries")
     dev = k_raw.device
-    n_batch, G = cache.batch_size, cache.n_groups
-    P = cache.alpha_exact_tokens
     T = k_raw.size(2)
-    ends = _pinned_upload(np.asarray(span_ends, dtype=np.uint8).reshape(n_batch, T), dev)
+    ends = _span_ends_device(span_ends, cache.batch_size, T, dev)
     if positions.dtype != torch.int64 or positions.stride(-1) != 1:
         positions = positions.to(torch.int64).contiguous()
-    nk, nv, npos, nvalid, nlen, nclosed, ncount = cache._alpha_spare
-    A = P + T
-    keep = torch.empty(n_batch, P, dtype=torch.int32, device=dev)
-    archive = torch.empty(n_batch, A, dtype=torch.int32, device=dev)
-    archive_count = torch.empty(n_batch, dtype=torch.int32, device=dev)
-    pk, pv, ppos = cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos
-    rows = _lib.SpanArgs(
-        _lib.ptr(pk), pk.stride(0), pk.stride(1), pk.stride(2), _lib.ptr(pv), pv.stride(0), pv.stride(1), pv.stride(2),
-        _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
-        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        P, None, None, None, 0, G, cache.k_dim, cache.v_dim,
-        _lib.ptr(cache.centroid) if cache.beta_novelty else None,
-        _lib.ptr(cache.alive) if cache.beta_novelty else None, cache.K_max, 1 if cache.beta_novelty else 0, None)
-    args = _lib.AlphaSelectArgs(
-        _lib.ptr(cache.alpha_span_len), _lib.ptr(cache.alpha_span_closed), _lib.ptr(cache.alpha_span_count),
-        _lib.ptr(ppos), _lib.ptr(positions), positions.stride(0), _lib.ptr(ends), ends.stride(0), T,
-        n_batch, P, cache.alpha_span_max_tokens, rows, _lib.ptr(keep), _lib.ptr(archive), _lib.ptr(archive_count),
-        _lib.ptr(nlen), _lib.ptr(nclosed), _lib.ptr(ncount), _lib.ptr(cache.alpha_count_dev), None)
-    need = int(_lib.lib().logkv_alpha_select_workspace_bytes(C.byref(args)))
-    if need < 0:
-        _lib.check(_lib.LOGKV_EINVAL, "logkv_alpha_select")
-    ws = cache._select_workspace
-    if ws is None or ws.numel() < need:
-        ws = cache._select_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    _lib.check(_lib.lib().logkv_alpha_select(C.byref(args), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev)),
+    call = _alpha_call(cache, T, k_raw.dtype)
+    call.set_rows(k_raw, v, positions, ends)
+    bufs, stream = call.bufs, _lib.stream_of(dev)
+    if not call.sized:
+        need = int(_lib.lib().logkv_alpha_select_workspace_bytes(C.byref(call.select)))
+        if need < 0:
+            _lib.check(_lib.LOGKV_EINVAL, "logkv_alpha_select")
+        if bufs.get("ws") is None or bufs["ws"].numel() < need:
+            bufs["ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
+        call.sized = True
+    ws = bufs["ws"]
+    _lib.check(_lib.lib().logkv_alpha_select(C.byref(call.select), ws.data_ptr(), ws.numel(), stream),
                "logkv_alpha_select")
-    ak = torch.empty(n_batch, G, A, cache.k_dim, dtype=k_raw.dtype, device=dev)
-    av = torch.empty(n_batch, G, A, cache.v_dim, dtype=v.dtype, device=dev)
-    ap = torch.empty(n_batch, A, dtype=torch.int64, device=dev)
-    part = _lib.PartitionArgs(
-        _lib.ptr(pk), pk.stride(0), pk.stride(1), pk.stride(2),
-        _lib.ptr(pv), pv.stride(0), pv.stride(1), pv.stride(2),
-        _lib.ptr(ppos), ppos.stride(0),
-        _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), k_raw.stride(2),
-        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        _lib.ptr(positions), positions.stride(0),
-        P, _lib.ptr(keep), _lib.ptr(archive), P, A, n_batch, G, cache.k_dim, cache.v_dim,
-        _lib.ptr(nk), _lib.ptr(nv), _lib.ptr(npos), _lib.ptr(nvalid),
-        _lib.ptr(ak), _lib.ptr(av), _lib.ptr(ap))
-    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(part), _lib.stream_of(dev)), "logkv_alpha_partition")
-    cache._alpha_spare = (pk, pv, ppos, cache.alpha_valid, cache.alpha_span_len, cache.alpha_span_closed,
-                          cache.alpha_span_count)
+    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(call.part), stream), "logkv_alpha_partition")
+    spare = cache._alpha_spare
+    cache._alpha_spare = (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid,
+                          cache.alpha_span_len, cache.alpha_span_closed, cache.alpha_span_count)
     (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid, cache.alpha_span_len,
-     cache.alpha_span_closed, cache.alpha_span_count) = nk, nv, npos, nvalid, nlen, nclosed, ncount
-    cache._alpha_keep_alive = (ends, keep, archive, positions)
-    cache._route_commit(ak, av, ap, archive_count)
+     cache.alpha_span_closed, cache.alpha_span_count) = spare
+    cache._alpha_parity ^= 1
+    # Inputs that may be temporaries stay referenced until the next flush on this stream.
+    cache._alpha_keep_alive = (ends, positions)
+    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"])

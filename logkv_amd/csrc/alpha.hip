@@ -237,6 +237,7 @@ struct SelectWs {
 };
 
 constexpr int kSelectThreads = 256;
+constexpr int kCutBatch = 8;   // boundary rows per thread in flight in the cut
 
 __host__ __device__ inline int64_t select_candidates(int n_batch, int P, int T) {
   return static_cast<int64_t>(n_batch) * (P + T + 1);
@@ -272,11 +273,29 @@ __global__ __launch_bounds__(kSelectThreads) void cut_kernel(logkv_alpha_select_
       olen[i] = a.span_len[static_cast<int64_t>(b) * P + i];
       oclosed[i] = a.span_closed[static_cast<int64_t>(b) * P + i];
     }
-    for (int j = threadIdx.x; j < T; j += blockDim.x) {
-      const bool end = ends[j] != 0;
-      const bool jump = j > 0 && pos[j] != pos[j - 1] + 1;
-      const bool start = j == 0 || jump || ends[j > 0 ? j - 1 : 0] != 0;
-      flags[j] = static_cast<uint8_t>((end ? 1 : 0) | (start ? 2 : 0));
+    // kCutBatch rows per thread loaded (clamped, unconditionally) before any flag is written.
+    for (int j0 = 0; j0 < T; j0 += kCutBatch * static_cast<int>(blockDim.x)) {
+      int64_t pc[kCutBatch], pp[kCutBatch];
+      uint8_t ec[kCutBatch], ep[kCutBatch];
+#pragma unroll
+      for (int q = 0; q < kCutBatch; ++q) {
+        const int j = min(j0 + q * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x), T - 1);
+        const int jp = j > 0 ? j - 1 : 0;
+        pc[q] = pos[j];
+        pp[q] = pos[jp];
+        ec[q] = ends[j];
+        ep[q] = ends[jp];
+      }
+#pragma unroll
+      for (int q = 0; q < kCutBatch; ++q) {
+        const int j = j0 + q * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+        if (j < T) {
+          const bool end = ec[q] != 0;
+          const bool jump = j > 0 && pc[q] != pp[q] + 1;
+          const bool start = j == 0 || jump || (j > 0 && ep[q] != 0);
+          flags[j] = static_cast<uint8_t>((end ? 1 : 0) | (start ? 2 : 0));
+        }
+      }
     }
     if (threadIdx.x == 0) n_seg_s = 0;
     __syncthreads();
@@ -376,160 +395,441 @@ __device__ __forceinline__ bool evict_before(double da, int ia, double db, int i
   return da < db || (da == db && ia > ib);
 }
 
-// One block per batch row: densities sorted by the block, the greedy run by
-// thread 0 over a compact sorted list of evictable spans, kept / archived rows
-// written by the block.
+// Exclusive block-wide scan of one int per thread (every thread of the block
+// calls it: it holds barriers); `total` receives the block's sum.
+// Inclusive wave scan by DPP: shifts 1, 2, 4, 8 within each row of 16 lanes,
+// then lane 15 of each row into the next row, lane 31 into rows 2 and 3
+// (lanes without a source add 0).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31
+  return v;
+}
+
+// Lane l receives lane l - 1's value (DPP wave_shr:1; lane 0 keeps its own).
+__device__ __forceinline__ int wave_shr1(int v) { return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false); }
+__device__ __forceinline__ double wave_shr1(double v) {
+  const long long bits = __double_as_longlong(v);
+  const int lo = wave_shr1(static_cast<int>(bits)), hi = wave_shr1(static_cast<int>(bits >> 32));
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+__device__ __forceinline__ int block_excl_scan(int v, int* wave_tmp, int& total) {
+  const int w = wave_id(), nw = static_cast<int>(blockDim.x) / kWave;
+  const int incl = wave_incl_scan(v);
+  if (lane_id() == kWave - 1) wave_tmp[w] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+  for (int q = 0; q < nw; ++q) {
+    const int x = wave_tmp[q];
+    before += q < w ? x : 0;
+    tot += x;
+  }
+  __syncthreads();   // wave_tmp is free for the next scan
+  total = tot;
+  return before + incl - v;
+}
+
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+  const long long bits = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+// Sort key of a density: NaN as +inf, so that every order below is total.
+__device__ __forceinline__ double sort_key(double d) { return d != d ? __builtin_inf() : d; }
+
+constexpr int kCopyBatch = 8;       // token loads per thread in flight in the keep / archive copy
+constexpr int kRankSortMax = 512;   // candidates sorted by counting ranks; more use a bitonic sort
+
+// Value at list position p (uniform) of a per-lane slot array: slot p / 64 of lane p % 64.
+template <int S>
+__device__ __forceinline__ int slot_lane(const int (&x)[S], int p) {
+  const int a = __builtin_amdgcn_readlane(x[0], p & (kWave - 1));
+  if (S == 1) return a;
+  const int b = __builtin_amdgcn_readlane(x[S - 1], p & (kWave - 1));
+  return p < kWave ? a : b;
+}
+template <int S>
+__device__ __forceinline__ double slot_lane(const double (&x)[S], int p) {
+  const double a = readlane_f64(x[0], p & (kWave - 1));
+  if (S == 1) return a;
+  const double b = readlane_f64(x[S - 1], p & (kWave - 1));
+  return p < kWave ? a : b;
+}
+
+// Eviction list held by one wave: list position p = 64 s + l is slot s of lane l (S <= 2).
+template <int S>
+struct EvictList {
+  int id[S], sz[S];
+  double dn[S];
+
+  // Insert (i, d, s) at position q; positions q.. move up by one.
+  __device__ __forceinline__ void insert(int q, int i, double d, int s) {
+    const int l = lane_id();
+#pragma unroll
+    for (int k = S - 1; k >= 0; --k) {
+      const int p = k * kWave + l;
+      const int up_id = wave_shr1(id[k]), up_sz = wave_shr1(sz[k]);
+      const double up_dn = wave_shr1(dn[k]);
+      // Lane 0 of slot k takes lane 63 of slot k - 1.
+      const int lo_id = k ? __builtin_amdgcn_readlane(id[k ? k - 1 : 0], kWave - 1) : 0;
+      const int lo_sz = k ? __builtin_amdgcn_readlane(sz[k ? k - 1 : 0], kWave - 1) : 0;
+      const double lo_dn = k ? readlane_f64(dn[k ? k - 1 : 0], kWave - 1) : 0.0;
+      const bool from_prev = l == 0;
+      const int pid = from_prev ? lo_id : up_id, psz = from_prev ? lo_sz : up_sz;
+      const double pdn = from_prev ? lo_dn : up_dn;
+      id[k] = p > q ? pid : (p == q ? i : id[k]);
+      sz[k] = p > q ? psz : (p == q ? s : sz[k]);
+      dn[k] = p > q ? pdn : (p == q ? d : dn[k]);
+    }
+  }
+};
+
+// The greedy over the ranked candidates (litgpt/alpha_log_kv.py:177-238) by one
+// wave, the eviction list (at most 64 S positions) in registers. Each step:
+// free room, else the shortest head of the list whose rows make room (from
+// inclusive prefix sums of list sizes, rebuilt only when the list changes),
+// its loss summed in list order; an accepted closed span is inserted at its
+// place (a ballot counts the entries that stay before it). State bits in LDS
+// follow every eviction and acceptance.
+template <int S>
+__device__ void greedy_wave(const int32_t* vict, int vh, int nv, int room, const int32_t* rank, int n_rank,
+                            const int32_t* size, const double* dens, uint8_t* state) {
+  const int l = lane_id();
+  EvictList<S> V;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int p = s * kWave + l;
+    int j = 0, sz = 0;
+    double d = 0.0;
+    if (p < nv) {
+      j = vict[p];
+      sz = size[j];
+      d = dens[j];
+    }
+    V.id[s] = j;
+    V.sz[s] = sz;
+    V.dn[s] = d;
+  }
+  int cum[S];
+  bool live[S];
+  auto rescan = [&]() {
+    int carry = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int p = s * kWave + l;
+      live[s] = p >= vh && p < nv;
+      cum[s] = wave_incl_scan(live[s] ? V.sz[s] : 0) + carry;
+      carry = __builtin_amdgcn_readlane(cum[s], kWave - 1);
+    }
+  };
+  rescan();
+  int ri = 0, rsz = 0, rfl = 0;
+  double rdn = 0.0;
+  for (int r = 0; r < n_rank; ++r) {
+    const int k = r & (kWave - 1);
+    if (k == 0 && r + l < n_rank) {
+      ri = rank[r + l];
+      rsz = size[ri];
+      rdn = dens[ri];
+      rfl = state[ri];
+    }
+    const int i = __builtin_amdgcn_readlane(ri, k), need = __builtin_amdgcn_readlane(rsz, k);
+    const double di = readlane_f64(rdn, k);
+    const bool closed = (__builtin_amdgcn_readlane(rfl, k) & 2) != 0;
+    bool ok = room >= need;
+    int last = -1, avail = room;
+    if (!ok) {
+#pragma unroll
+      for (int s = S - 1; s >= 0; --s) {
+        const uint64_t hit = __ballot(live[s] && cum[s] >= need - room);
+        if (hit) last = s * kWave + __builtin_ctzll(hit);
+      }
+      if (last >= 0) {
+        avail = room + slot_lane<S>(cum, last);
+        double loss = 0.0;
+        for (int t = vh; t <= last; ++t) loss += slot_lane<S>(V.dn, t) * static_cast<double>(slot_lane<S>(V.sz, t));
+        ok = di * static_cast<double>(need) > loss;
+      }
+    }
+    if (!ok) continue;
+    if (last >= 0) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int p = s * kWave + l;
+        if (p >= vh && p <= last) state[V.id[s]] &= ~4;
+      }
+      vh = last + 1;
+    }
+    if (l == 0) state[i] |= 4;
+    room = avail - need;
+    if (closed) {
+      int before = 0;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int p = s * kWave + l;
+        before += __popcll(__ballot(p >= vh && p < nv && !evict_before(di, i, V.dn[s], V.id[s])));
+      }
+      V.insert(vh + before, i, di, need);
+      ++nv;
+    }
+    if (last >= 0 || closed) rescan();
+  }
+}
+
+// The same greedy by one thread over the list in LDS (any list length).
+__device__ void greedy_serial(int32_t* vict, int vh, int nv, int room, const int32_t* rank, int n_rank,
+                              const int32_t* size, const double* dens, uint8_t* state) {
+  for (int r = 0; r < n_rank; ++r) {
+    const int i = rank[r];
+    const int need = size[i];
+    int avail = room, n_taken = 0;
+    double loss = 0.0;
+    if (avail < need) {
+      for (int q = vh; q < nv; ++q) {
+        const int j = vict[q];
+        ++n_taken;
+        avail += size[j];
+        loss += dens[j] * static_cast<double>(size[j]);
+        if (avail >= need) break;
+      }
+    }
+    if (avail >= need && (n_taken == 0 || dens[i] * static_cast<double>(need) > loss)) {
+      for (int t = 0; t < n_taken; ++t) state[vict[vh + t]] &= ~4;
+      vh += n_taken;
+      state[i] |= 4;
+      room = avail - need;
+      if (state[i] & 2) {   // a closed span joins the evictable list at its place
+        int q = nv;
+        while (q > vh && evict_before(dens[i], i, dens[vict[q - 1]], vict[q - 1])) {
+          vict[q] = vict[q - 1];
+          --q;
+        }
+        vict[q] = i;
+        ++nv;
+      }
+    }
+  }
+}
+
+// One block per batch row (litgpt/alpha_log_kv.py:177-238): candidates sorted
+// into eviction order (ascending density, later first; its reverse is the
+// ranking order), open and old spans taken first, the lowest-density chosen
+// spans evicted while the budget is exceeded, then the greedy over the rest in
+// ranking order; kept / archived rows and the new span list written by the
+// block. Every phase but the greedy is block-parallel.
 __global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_select_args a, SelectWs w) {
   extern __shared__ __align__(16) uint8_t dyn[];
   const int b = blockIdx.x;
   const int P = a.budget, T = a.tokens;
   const int c0 = w.row_cand[b], n = w.row_cand[b + 1] - c0;
+  const bool bitonic = n > kRankSortMax;
   int width = 1;
-  while (width < n) width <<= 1;
-  double* key = reinterpret_cast<double*>(dyn);                      // [width] sort keys
+  while (bitonic && width < n) width <<= 1;
+  double* key = reinterpret_cast<double*>(dyn);                      // [width] bitonic sort keys
   double* dens = key + width;                                        // [n] density by candidate
-  int32_t* idx = reinterpret_cast<int32_t*>(dens + n);               // [width] sorted candidates
-  int32_t* size = idx + width;                                       // [n]
+  int32_t* idx = reinterpret_cast<int32_t*>(dens + n);               // [max(width, n)] eviction order
+  int32_t* size = idx + (width > n ? width : n);                     // [n]
   int32_t* koff = size + n;                                          // [n] keep / archive offsets
   int32_t* rank = koff + n;                                          // [n] candidates to rank
-  int32_t* vict = rank + n;                                          // [n] evictable spans, eviction order
-  uint8_t* state = reinterpret_cast<uint8_t*>(vict + n);             // [n] bit 0 old, 1 closed, 2 chosen
-  __shared__ int kept_s, arch_s;
-  for (int i = threadIdx.x; i < width; i += blockDim.x) {
-    if (i < n) {
-      const uint8_t f = w.cand_flags[c0 + i];
-      const double d = static_cast<double>(w.scores[c0 + i]) * ((f & 1) ? 1.1 : 1.0);
-      dens[i] = d;
-      key[i] = d;
-      idx[i] = i;
-      size[i] = w.offsets[c0 + i + 1] - w.offsets[c0 + i];
-      state[i] = f;
-    } else {
-      key[i] = __builtin_inf();
-      idx[i] = 0x7fffffff;
+  // Evictable spans in eviction order. Entries are dropped from the head and
+  // inserted once per acceptance, so the list spans at most 2n positions.
+  int32_t* vict = rank + n;                                          // [2n]
+  int32_t* cstart = vict + 2 * n;                                    // [n] token offset in the row
+  uint8_t* state = reinterpret_cast<uint8_t*>(cstart + n);           // [n] bit 0 old, 1 closed, 2 chosen
+  __shared__ int wave_tmp[kSelectThreads / kWave];
+  __shared__ int vh_s, room_s;
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  const int o0 = w.offsets[c0];
+  // Densities (old spans x 1.1), sizes, token offsets; open and old spans are
+  // chosen up front.
+  int pre = 0;   // low 16 bits: rows chosen up front; high: closed candidates
+  for (int i = tid; i < n; i += nthr) {
+    const uint8_t f = w.cand_flags[c0 + i];
+    const double d = static_cast<double>(w.scores[c0 + i]) * ((f & 1) ? 1.1 : 1.0);
+    const int o = w.offsets[c0 + i];
+    const int sz = w.offsets[c0 + i + 1] - o;
+    const bool first = !(f & 2) || (f & 1);
+    dens[i] = d;
+    size[i] = sz;
+    cstart[i] = o - o0;
+    state[i] = static_cast<uint8_t>(f | (first ? 4 : 0));
+    pre += (first ? sz : 0) + ((f & 2) ? 1 << 16 : 0);
+  }
+  int pre_total;
+  block_excl_scan(pre, wave_tmp, pre_total);   // also the barrier after the loads
+  int room = P - (pre_total & 0xffff);
+  const int n_closed = pre_total >> 16;
+  if (!bitonic) {
+    // Counting sort: a candidate's place is the number of candidates before
+    // it (a total order: NaN keys sort as +inf, ties by index).
+    for (int i = tid; i < n; i += nthr) {
+      const double di = sort_key(dens[i]);
+      int at = 0;
+#pragma unroll 8
+      for (int j = 0; j < n; ++j) at += evict_before(sort_key(dens[j]), j, di, i) ? 1 : 0;
+      idx[at] = i;
+    }
+  } else {
+    for (int i = tid; i < width; i += nthr) {
+      key[i] = i < n ? sort_key(dens[i]) : __builtin_inf();
+      idx[i] = i < n ? i : 0x7fffffff;
+    }
+    __syncthreads();
+    for (int sz = 2; sz <= width; sz <<= 1) {
+      for (int stride = sz >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < width; t += nthr) {
+          const int partner = t ^ stride;
+          if (partner > t) {
+            const bool up = (t & sz) == 0;
+            const double ka = key[t], kb = key[partner];
+            const int ia = idx[t], ib = idx[partner];
+            const bool pa = ia == 0x7fffffff, pb = ib == 0x7fffffff;
+            const bool a_after = pa != pb ? pa : (!pa && evict_before(kb, ib, ka, ia));
+            if (a_after == up) {
+              key[t] = kb;
+              key[partner] = ka;
+              idx[t] = ib;
+              idx[partner] = ia;
+            }
+          }
+        }
+        __syncthreads();
+      }
     }
   }
   __syncthreads();
-  // Eviction order (its reverse is the ranking order: decreasing density,
-  // earlier first); padding sorts last.
-  for (int sz = 2; sz <= width; sz <<= 1) {
-    for (int stride = sz >> 1; stride > 0; stride >>= 1) {
-      for (int t = threadIdx.x; t < width; t += blockDim.x) {
-        const int partner = t ^ stride;
-        if (partner > t) {
-          const bool up = (t & sz) == 0;
-          const double ka = key[t], kb = key[partner];
-          const int ia = idx[t], ib = idx[partner];
-          const bool pa = ia == 0x7fffffff, pb = ib == 0x7fffffff;
-          const bool a_after = pa != pb ? pa : (!pa && evict_before(kb, ib, ka, ia));
-          if (a_after == up) {
-            key[t] = kb;
-            key[partner] = ka;
-            idx[t] = ib;
-            idx[partner] = ia;
-          }
-        }
-      }
-      __syncthreads();
-    }
+  // Evictable spans (chosen and closed) in eviction order.
+  int nv = 0;
+  for (int q0 = 0; q0 < n; q0 += nthr) {
+    const int q = q0 + tid;
+    const int i = q < n ? idx[q] : 0;
+    const bool ev = q < n && (state[i] & 6) == 6;
+    int tot;
+    const int at = block_excl_scan(ev ? 1 : 0, wave_tmp, tot);
+    if (ev) vict[nv + at] = i;
+    nv += tot;
   }
-  if (threadIdx.x == 0) {
-    int room = P;
-    for (int i = 0; i < n; ++i) {
-      if (!(state[i] & 2) || (state[i] & 1)) {
-        state[i] |= 4;
-        room -= size[i];
+  // Over budget: evict from the head of the list until the budget holds.
+  if (tid == 0) {
+    vh_s = room < 0 ? nv : 0;
+    room_s = room;
+  }
+  __syncthreads();
+  if (room < 0) {
+    int cum = 0;
+    for (int q0 = 0; q0 < nv; q0 += nthr) {
+      const int q = q0 + tid;
+      const int sz = q < nv ? size[vict[q]] : 0;
+      int tot;
+      const int before = cum + block_excl_scan(sz, wave_tmp, tot);
+      if (q < nv && room + before < 0 && room + before + sz >= 0) {
+        vh_s = q + 1;
+        room_s = room + before + sz;
+      }
+      cum += tot;
+    }
+    __syncthreads();
+    if (vh_s == nv && tid == 0) room_s = room + cum;
+    __syncthreads();
+    for (int q = tid; q < vh_s; q += nthr) state[vict[q]] &= ~4;
+    __syncthreads();
+  }
+  const int vh = vh_s;
+  room = room_s;
+  // Candidates to rank: the unchosen ones, decreasing density, earlier first.
+  int n_rank = 0;
+  for (int r0 = 0; r0 < n; r0 += nthr) {
+    const int q = n - 1 - (r0 + tid);
+    const int i = q >= 0 ? idx[q] : 0;
+    const bool rk = q >= 0 && !(state[i] & 4);
+    int tot;
+    const int at = block_excl_scan(rk ? 1 : 0, wave_tmp, tot);
+    if (rk) rank[n_rank + at] = i;
+    n_rank += tot;
+  }
+  // The list holds at most nv + (closed candidates ranked) <= n_closed + vh positions.
+  const int list_cap = n_closed + vh;
+  if (list_cap <= kWave) {
+    if (wave_id() == 0) greedy_wave<1>(vict, vh, nv, room, rank, n_rank, size, dens, state);
+  } else if (list_cap <= 2 * kWave) {
+    if (wave_id() == 0) greedy_wave<2>(vict, vh, nv, room, rank, n_rank, size, dens, state);
+  } else if (tid == 0) {
+    greedy_serial(vict, vh, nv, room, rank, n_rank, size, dens, state);
+  }
+  __syncthreads();
+  // Keep / archive offsets and the new span list, in candidate order.
+  LOGKV_G int32_t* keep = gp(a.keep + static_cast<int64_t>(b) * P);
+  int kept = 0, spans = 0;
+  for (int i0 = 0; i0 < n; i0 += nthr) {
+    const int i = i0 + tid;
+    const bool kp = i < n && (state[i] & 4);
+    const int sz = kp ? size[i] : 0;
+    int tot;
+    const int x = block_excl_scan(sz | (kp ? 1 << 16 : 0), wave_tmp, tot);
+    if (i < n) {
+      const int kept_before = kept + (x & 0xffff), spans_before = spans + (x >> 16);
+      koff[i] = kp ? kept_before : cstart[i] - kept_before;
+      if (kp) {
+        a.new_span_len[static_cast<int64_t>(b) * P + spans_before] = sz;
+        a.new_span_closed[static_cast<int64_t>(b) * P + spans_before] = (state[i] & 2) ? 1 : 0;
       }
     }
-    // Evictable spans (chosen and closed) in eviction order, from vict[vh].
-    int nv = 0;
-    for (int q = 0; q < n; ++q) {
-      const int i = idx[q];
-      if ((state[i] & 4) && (state[i] & 2)) vict[nv++] = i;
-    }
-    int vh = 0;
-    while (room < 0 && vh < nv) {
-      const int i = vict[vh++];
-      state[i] &= ~4;
-      room += size[i];
-    }
-    int n_rank = 0;
-    for (int q = n - 1; q >= 0; --q)
-      if (!(state[idx[q]] & 4)) rank[n_rank++] = idx[q];
-    for (int r = 0; r < n_rank; ++r) {
-      const int i = rank[r];
-      const int need = size[i];
-      int avail = room, n_taken = 0;
-      double loss = 0.0;
-      if (avail < need) {
-        for (int q = vh; q < nv; ++q) {
-          const int j = vict[q];
-          ++n_taken;
-          avail += size[j];
-          loss += dens[j] * static_cast<double>(size[j]);
-          if (avail >= need) break;
-        }
-      }
-      if (avail >= need && (n_taken == 0 || dens[i] * static_cast<double>(need) > loss)) {
-        for (int t = 0; t < n_taken; ++t) state[vict[vh + t]] &= ~4;
-        vh += n_taken;
-        state[i] |= 4;
-        room = avail - need;
-        if (state[i] & 2) {   // a closed span joins the evictable list at its place
-          int q = nv;
-          while (q > vh && evict_before(dens[i], i, dens[vict[q - 1]], vict[q - 1])) {
-            vict[q] = vict[q - 1];
-            --q;
-          }
-          vict[q] = i;
-          ++nv;
-        }
-      }
-    }
-    int kept = 0, arch = 0, spans = 0;
-    for (int i = 0; i < n; ++i) {
-      if (state[i] & 4) {
-        koff[i] = kept;
-        kept += size[i];
-        ++spans;
-      } else {
-        koff[i] = arch;
-        arch += size[i];
-      }
-    }
-    kept_s = kept;
-    arch_s = arch;
+    kept += tot & 0xffff;
+    spans += tot >> 16;
+  }
+  const int n_tok = w.offsets[c0 + n] - o0;
+  const int arch = n_tok - kept;
+  if (tid == 0) {
     a.new_span_count[b] = spans;
     a.archive_count[b] = arch;
     atomicMax(a.alpha_count, kept);
   }
   __syncthreads();
   const int A = P + T;
-  const int kept = kept_s, arch = arch_s;
-  LOGKV_G int32_t* keep = gp(a.keep + static_cast<int64_t>(b) * P);
   LOGKV_G int32_t* archive = gp(a.archive + static_cast<int64_t>(b) * A);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int o = w.offsets[c0 + i];
-    const bool kept_i = (state[i] & 4) != 0;
-    LOGKV_G int32_t* dst = kept_i ? keep + koff[i] : archive + koff[i];
-    const int cap = kept_i ? P - koff[i] : A - koff[i];   // the greedy keeps at most P rows
-    for (int t = 0; t < size[i] && t < cap; ++t) dst[t] = w.tokens[o + t];
-  }
-  // The new selection's spans, in candidate order.
-  if (threadIdx.x == 0) {
-    int sp = 0;
-    for (int i = 0; i < n; ++i) {
-      if (state[i] & 4) {
-        a.new_span_len[static_cast<int64_t>(b) * P + sp] = size[i];
-        a.new_span_closed[static_cast<int64_t>(b) * P + sp] = (state[i] & 2) ? 1 : 0;
-        ++sp;
+  // One thread per token of the row (its candidate by binary search over the
+  // candidates' token offsets), so the token loads are all in flight.
+  for (int g0 = 0; g0 < n_tok; g0 += kCopyBatch * nthr) {
+    int32_t v[kCopyBatch];
+#pragma unroll
+    for (int q = 0; q < kCopyBatch; ++q) v[q] = w.tokens[o0 + min(g0 + q * nthr + tid, n_tok - 1)];
+    // The token's candidate: the largest c with cstart[c] <= g, kCopyBatch
+    // branch-free binary searches (uniform lengths, unconditional LDS loads)
+    // advanced in lockstep.
+    int lo[kCopyBatch];
+#pragma unroll
+    for (int q = 0; q < kCopyBatch; ++q) lo[q] = 0;
+    for (int len = n; len > 1;) {
+      const int half = len >> 1;
+#pragma unroll
+      for (int q = 0; q < kCopyBatch; ++q) {
+        const int g = g0 + q * nthr + tid;
+        lo[q] = cstart[lo[q] + half] <= g ? lo[q] + half : lo[q];
+      }
+      len -= half;
+    }
+#pragma unroll
+    for (int q = 0; q < kCopyBatch; ++q) {
+      const int g = g0 + q * nthr + tid;
+      if (g < n_tok) {
+        const int c = lo[q], t = g - cstart[c];
+        const bool kept_i = (state[c] & 4) != 0;
+        const int cap = kept_i ? P - koff[c] : A - koff[c];   // the greedy keeps at most P rows
+        if (t < cap) (kept_i ? keep : archive)[koff[c] + t] = v[q];
       }
     }
   }
-  for (int i = kept + threadIdx.x; i < P; i += blockDim.x) keep[i] = -1;
-  for (int i = arch + threadIdx.x; i < A; i += blockDim.x) archive[i] = -1;
+  for (int i = kept + tid; i < P; i += nthr) keep[i] = -1;
+  for (int i = arch + tid; i < A; i += nthr) archive[i] = -1;
   if (a.scores) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) a.scores[c0 + i] = w.scores[c0 + i];
+    for (int i = tid; i < n; i += nthr) a.scores[c0 + i] = w.scores[c0 + i];
   }
 }
 
@@ -572,10 +872,7 @@ int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream
   const size_t cut_c = static_cast<size_t>(a.budget) + a.tokens + 1;
   const size_t cut_shmem = 4 * (static_cast<size_t>(a.tokens) + 1) + 5 * static_cast<size_t>(a.budget) +
                            17 * cut_c + static_cast<size_t>(a.tokens) + 16;
-  if (cut_shmem > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&cut_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(cut_shmem)) != hipSuccess)
-    return LOGKV_ERUNTIME;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&cut_kernel), cut_shmem)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(cut_kernel, dim3(1), dim3(kSelectThreads), cut_shmem, stream, a, w);
   logkv_span_args sa = a.rows;
   sa.old_width = a.budget;
@@ -589,11 +886,8 @@ int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream
   const int maxc = a.budget + a.tokens + 1;
   int width = 1;
   while (width < maxc) width <<= 1;
-  const size_t choose_shmem = static_cast<size_t>(width) * (8 + 4) + static_cast<size_t>(maxc) * (8 + 4 * 4 + 1) + 16;
-  if (choose_shmem > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&choose_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(choose_shmem)) != hipSuccess)
-    return LOGKV_ERUNTIME;
+  const size_t choose_shmem = static_cast<size_t>(width) * (8 + 4) + static_cast<size_t>(maxc) * (8 + 6 * 4 + 1) + 16;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&choose_kernel), choose_shmem)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(choose_kernel, dim3(a.n_batch), dim3(kSelectThreads), choose_shmem, stream, a, w);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }

@@ -14,9 +14,38 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <vector>
+
 #include "../../include/logkv_hip.h"
 
 namespace logkv {
+
+// Lets kernel `fn` launch with `bytes` of dynamic LDS on the current device.
+// Above the 64 KiB default the limit is raised once per (kernel, device) and
+// remembered, so steady-state launches make no attribute call.
+inline bool allow_dynamic_lds(const void* fn, size_t bytes) {
+  if (bytes <= 64 * 1024) return true;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  struct Limit {
+    const void* fn;
+    int dev;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Limit> limits;
+  std::lock_guard<std::mutex> lock(mu);
+  Limit* hit = nullptr;
+  for (Limit& e : limits)
+    if (e.fn == fn && e.dev == dev) hit = &e;
+  if (hit && hit->bytes >= bytes) return true;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess)
+    return false;
+  if (hit) hit->bytes = bytes;
+  else limits.push_back(Limit{fn, dev, bytes});
+  return true;
+}
 
 // Address-space-qualified pointers: loads and stores through them compile to
 // global_* / ds_* instructions instead of flat_* ones, which the compiler must

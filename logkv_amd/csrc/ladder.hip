@@ -1110,10 +1110,7 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
   size_t region = static_cast<size_t>(kCenterRows) * c.dk * 2;
   if (p.late_joins) region += static_cast<size_t>(ws.sort_width) * 8;
   const size_t shmem = tok_bytes + region;
-  if (shmem > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&commit_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(shmem)) != hipSuccess)
-    return LOGKV_ERUNTIME;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel), shmem)) return LOGKV_ERUNTIME;
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
   if (c.levels > 1) {
@@ -1122,10 +1119,7 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
     const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
     const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
                                  : reinterpret_cast<const void*>(&carries_kernel<4>);
-    if (carry_shmem > 64 * 1024 &&
-        hipFuncSetAttribute(carries, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(carry_shmem)) !=
-            hipSuccess)
-      return LOGKV_ERUNTIME;
+    if (!allow_dynamic_lds(carries, carry_shmem)) return LOGKV_ERUNTIME;
     for (int ell = 0; ell + 1 < c.levels; ++ell) {
       // Units at level ell: at most ceil(carries / 2) Beta groups (or carries) per ladder.
       const int64_t bound = static_cast<int64_t>(ladders) * carry_cap(ws.m0_cap, ell);

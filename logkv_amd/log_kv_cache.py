@@ -269,8 +269,11 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError("semantic_s_h must be finite and > 0")
         buf("s_h", s_h.contiguous())
         self._workspace = None
-        self._select_workspace = None
         self._alpha_keep_alive = None
+        # C-ABI argument structs and per-flush-length buffers, built once and
+        # reused (raw pointers: cleared whenever buffers move).
+        self._views = {}
+        self._alpha_parity = 0   # flips with every swap of the exact pool's two buffer sets
         self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
                                    1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0)
 
@@ -278,18 +281,24 @@ class LogStructuredKVCache(nn.Module):
     # C-ABI views
     # ------------------------------------------------------------------
     def _ladder_view(self) -> LadderView:
-        return LadderView(
-            ptr(self.level_k), ptr(self.level_v), ptr(self.level_w), ptr(self.level_p_lo), ptr(self.level_p_hi),
-            ptr(self.level_sum_wp), ptr(self.level_order), ptr(self.pad_mask), ptr(self.level_count),
-            ptr(self.centroid), ptr(self.n_eff), ptr(self.n_total), ptr(self.p_hi_c), ptr(self.level0_phase),
-            ptr(self.alive), ptr(self.s_h),
-            self.batch_size, self.n_groups, self.K_max, self.L_alloc, self.B_prime, self.k_dim, self.v_dim,
-        )
+        view = self._views.get("ladder")
+        if view is None:
+            view = self._views["ladder"] = LadderView(
+                ptr(self.level_k), ptr(self.level_v), ptr(self.level_w), ptr(self.level_p_lo), ptr(self.level_p_hi),
+                ptr(self.level_sum_wp), ptr(self.level_order), ptr(self.pad_mask), ptr(self.level_count),
+                ptr(self.centroid), ptr(self.n_eff), ptr(self.n_total), ptr(self.p_hi_c), ptr(self.level0_phase),
+                ptr(self.alive), ptr(self.s_h),
+                self.batch_size, self.n_groups, self.K_max, self.L_alloc, self.B_prime, self.k_dim, self.v_dim,
+            )
+        return view
 
     def _workspace_for(self, view: LadderView, tokens: int) -> torch.Tensor:
-        need = lib().logkv_route_workspace_bytes(C.byref(view), tokens, self._params.late_joins)
-        if need < 0:
-            raise ValueError("invalid cache layout for the HIP route")
+        need = self._views.get(("route_ws", tokens))
+        if need is None:
+            need = lib().logkv_route_workspace_bytes(C.byref(view), tokens, self._params.late_joins)
+            if need < 0:
+                raise ValueError("invalid cache layout for the HIP route")
+            self._views[("route_ws", tokens)] = need
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(need, dtype=torch.uint8, device=self.level_k.device)
         return self._workspace
@@ -450,8 +459,12 @@ class LogStructuredKVCache(nn.Module):
         # (litgpt/log_kv_cache.py:6226-6232).
         self._mid_decode_state = None
         self._workspace = None
-        self._select_workspace = None
-        return super()._apply(fn, recurse)
+        self._views = {}
+        self._alpha_keep_alive = None
+        out = super()._apply(fn, recurse)
+        if self.alpha_exact_tokens:
+            self._alpha_spare = tuple(fn(t) for t in self._alpha_spare)
+        return out
 
     # ------------------------------------------------------------------
     # Readout plan

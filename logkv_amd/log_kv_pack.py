@@ -59,6 +59,17 @@ class MidAttentionPlan:
 
 
 def readout_view(cache) -> ReadoutView:
+    """The cache's readout struct: built once per exact-pool buffer set and
+    reused (only the recent row count changes between calls)."""
+    key = ("readout", cache._alpha_parity)
+    view = cache._views.get(key)
+    if view is None:
+        view = cache._views[key] = _build_readout_view(cache)
+    view.recent_count = cache.recent_count
+    return view
+
+
+def _build_readout_view(cache) -> ReadoutView:
     table_bf16 = cache.cos_cache.dtype == torch.bfloat16
     if cache.cos_cache.dtype not in (torch.float32, torch.bfloat16) or cache.sin_cache.dtype != cache.cos_cache.dtype:
         raise ValueError("RoPE tables must both be float32 or both bfloat16")

@@ -76,21 +76,39 @@ def test_alpha_flush_matches_oracle(name):
         assert (cuts != 1).any()
 
 
-def _random_selection(rng, P, max_span):
+def _random_selection(rng, P, max_span, full=False):
+    """Closed spans up to P - max_span rows and maybe a pending one; ``full``:
+    closed spans filling all P rows (the next open candidate then forces
+    evictions before the greedy)."""
     spans, n = [], 0
     while True:
         length = int(rng.integers(1, max_span + 1))
-        if n + length > P - max_span:
+        if full:
+            length = min(length, P - n)
+        elif n + length > P - max_span:
+            break
+        if length == 0:
             break
         spans.append((length, True))
         n += length
-    if rng.random() < 0.6:
+    if not full and rng.random() < 0.6:
         spans.append((int(rng.integers(1, max_span)), False))
     return spans
 
 
-@pytest.mark.parametrize("beta,seed", [(False, 0), (True, 1), (True, 2)])
-def test_device_selection_matches_oracle(beta, seed):
+# (beta, seed, P, T, span cap, boundary rate, full pool): small rows; a full
+# pool (evictions before the greedy); 65-128 list entries (both register
+# slots of the one-wave greedy); >128 closed candidates (the one-thread
+# greedy); >512 candidates (the bitonic sort).
+SELECT_CASES = [(False, 0, 24, 40, 6, 0.2, False), (True, 1, 24, 40, 6, 0.2, False),
+                (True, 2, 24, 40, 6, 0.2, False), (False, 3, 24, 40, 6, 0.2, True),
+                (True, 4, 32, 48, 8, 0.25, True), (False, 7, 90, 60, 2, 0.5, True),
+                (True, 8, 90, 60, 2, 0.5, False), (False, 5, 64, 600, 8, 0.5, False),
+                (True, 6, 64, 1400, 8, 0.6, True)]
+
+
+@pytest.mark.parametrize("beta,seed,P,T,ms,rate,full", SELECT_CASES)
+def test_device_selection_matches_oracle(beta, seed, P, T, ms, rate, full):
     """logkv_alpha_select (candidates, scores, greedy on the device) against the oracle's
     cut_spans / score_spans / choose_spans: pending spans closed by jumps or carried into
     the first run, caps, single-row spans (zero scores, ties), evictions."""
@@ -99,19 +117,19 @@ def test_device_selection_matches_oracle(beta, seed):
     from logkv_amd import _lib
 
     rng = np.random.default_rng(seed)
-    Bt, G, D, P, T, ms, K = 2, 4, 64, 24, 40, 6, 3
+    Bt, G, D, K = 2, 4, 64, 3
     dev = torch.device("cuda")
-    spans = [_random_selection(rng, P, ms) for _ in range(Bt)]
+    spans = [_random_selection(rng, P, ms, full) for _ in range(Bt)]
     counts = [sum(n for n, _ in s) for s in spans]
     pool_pos = np.zeros((Bt, P), np.int64)
     new_pos = np.zeros((Bt, T), np.int64)
     for b in range(Bt):
-        pool_pos[b, :counts[b]] = np.sort(rng.choice(60, counts[b], replace=False))
+        pool_pos[b, :counts[b]] = np.sort(rng.choice(max(60, 3 * P), counts[b], replace=False))
         start = int(pool_pos[b, counts[b] - 1]) + 1 + int(rng.random() < 0.5)
         steps = 1 + (rng.random(T) < 0.1) * rng.integers(1, 3, T)
         steps[0] = 0
         new_pos[b] = start + np.cumsum(steps)
-    ends = rng.random((Bt, T)) < 0.2
+    ends = rng.random((Bt, T)) < rate
     gen = torch.Generator().manual_seed(seed)
     pool_k = (torch.randn(Bt, G, P, D, generator=gen) * 2).to(torch.bfloat16)
     pool_v = torch.randn(Bt, G, P, D, generator=gen).to(torch.bfloat16)
