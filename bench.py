@@ -249,13 +249,6 @@ def flush_workload(args, torch, np):
     dev = torch.device("cuda", 0)
     layers = args.layers
     cos, sin = rope_tables(N, D)
-    caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev,
-                                   dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
-                                   semantic_flush_granularity=F, semantic_anchor_mode="mid",
-                                   allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
-                                   alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
-                                   beta_adaptive_merge=True)
-              for _ in range(layers)]
     n_flush = 2 + args.warmup + args.steps
     gen = torch.Generator(device=dev).manual_seed(1234)
     centers = torch.randn(layers, G, K, D, generator=gen, device=dev) * 4
@@ -269,55 +262,70 @@ def flush_workload(args, torch, np):
 
     data = [[(mixture(li), mixture(li)) for li in range(layers)] for _ in range(n_flush)]
     positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).contiguous() for j in range(n_flush)]
-    positions_host = [[list(range(j * F, (j + 1) * F))] for j in range(n_flush)]
     # Boundary flags staged on the device like the rows and positions.
     ends = [torch.tensor(span_ends_for(j), dtype=torch.uint8, device=dev) for j in range(n_flush)]
     dim = packed_dim(D, D)
     empty = torch.empty(1, G, 0, D, dtype=torch.bfloat16, device=dev)
-    workspaces = [(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev),
-                   torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev)) for c in caches]
     torch.cuda.synchronize()
 
-    # Layer li's flushes are issued on stream li % streams (the layers' caches are
-    # independent, so their flushes may overlap; each layer's own flushes stay in order).
-    streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(args.streams - 1)]
+    def run_pass(n_streams, meter):
+        """Fresh caches, 2 + warmup untimed flushes, then `steps` timed ones. Layer li's
+        flushes go to stream li % n_streams: the layers' caches are independent, so
+        their flushes may overlap, while each layer's own flushes stay in order."""
+        caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev,
+                                       dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
+                                       semantic_s_h=64.0, semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                       allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                       alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                       beta_adaptive_merge=True)
+                  for _ in range(layers)]
+        workspaces = [(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev),
+                       torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev))
+                      for c in caches]
+        streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(n_streams - 1)]
 
-    def flush(j):
-        for li, cache in enumerate(caches):
-            with torch.cuda.stream(streams[li % len(streams)]):
-                k, v = data[j][li]
-                cache.route_and_flush_batch(k, v, positions[j], positions_host=positions_host[j], span_ends=ends[j])
-                # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
-                view = readout_view(cache)
-                plan = cache._semantic_attention_plan()
-                _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
+        def flush(j):
+            for li, cache in enumerate(caches):
+                with torch.cuda.stream(streams[li % n_streams]):
+                    k, v = data[j][li]
+                    cache.route_and_flush_batch(k, v, positions[j], span_ends=ends[j])
+                    # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
+                    view = readout_view(cache)
+                    plan = cache._semantic_attention_plan()
+                    _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
 
-    for j in range(2 + args.warmup):
-        flush(j)
-    torch.cuda.synchronize()
-    progress(f"flush: {2 + args.warmup} untimed flushes done")
+        for j in range(2 + args.warmup):
+            flush(j)
+        torch.cuda.synchronize()
+        progress(f"flush, {n_streams} stream(s): {2 + args.warmup} untimed flushes done")
+        # Commit launches of every METER_EVERY-th layer are bracketed by events (the
+        # meter's ladder-state copies stay off the other layers).
+        metered = caches[::METER_EVERY] if meter else []
+        meters = [CommitMeter(c, torch) for c in metered]
+        for c, m in zip(metered, meters):
+            c._route_commit = m
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            flush(2 + args.warmup + s)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        for c in metered:
+            del c._route_commit
+        progress(f"flush, {n_streams} stream(s): {args.steps} timed flushes in {elapsed:.3f} s")
+        rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
+        width = int(caches[0]._semantic_attention_plan().width)
+        return elapsed, rec, caches[0].B_prime, caches[0].L_alloc, width
 
-    # Commit launches of every METER_EVERY-th layer are bracketed by events (the
-    # meter's ladder-state copies stay off the other layers).
-    metered = caches[::METER_EVERY]
-    meters = [CommitMeter(c, torch) for c in metered]
-    for c, m in zip(metered, meters):
-        c._route_commit = m
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        flush(2 + args.warmup + s)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    for c in metered:
-        del c._route_commit
-    progress(f"flush: {args.steps} timed flushes in {elapsed:.3f} s")
-    rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
+    # Serial pass (one stream): per-layer latency and the commit-stage events.
+    serial, rec, B_, L_, width = run_pass(1, True)
+    elapsed = serial
+    if args.streams > 1:
+        elapsed = run_pass(args.streams, False)[0]
     launch_bytes = float(np.mean([b for b, _ in rec]))
     launch_ms = float(np.mean([t for _, t in rec]))
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     tokens = F * layers * args.steps
-    widths = [int(c._semantic_attention_plan().width) for c in caches[:1]]
     return {
         "value": tokens / elapsed,
         "ms_per_step": elapsed / args.steps * 1e3,
@@ -325,10 +333,13 @@ def flush_workload(args, torch, np):
                                f"K=12, B=128, Alpha exact pool {EXACT} / span cap {SPAN}, Beta novelty + 4->2 "
                                "split, attach route, mid-anchor plan + pack",
                    "layers": layers, "flush": F, "batch": 1, "kv_groups": G, "head_dim": D, "clusters": K,
-                   "slots_per_level": caches[0].B_prime, "levels": caches[0].L_alloc, "exact_tokens": EXACT,
+                   "slots_per_level": B_, "levels": L_, "exact_tokens": EXACT,
                    "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
-                   "pooled_width_after_last_flush": widths[0]},
-        "roofline": {"kernel": "commit: commit_kernel + carries_kernel per level + finish_kernel", "bound": "hbm",
+                   "pooled_width_after_last_flush": width, "streams": args.streams,
+                   "one_stream_tokens_per_s": tokens / serial,
+                   "one_stream_ms_per_layer_flush": serial / args.steps / layers * 1e3},
+        "roofline": {"kernel": "commit: commit_kernel + units_kernel + carries_kernel per level + finish_kernel "
+                               "(one-stream pass)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
@@ -418,7 +429,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=28)
-    ap.add_argument("--streams", type=int, default=1, help="HIP streams the layers' flushes are spread over")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="HIP streams the layers' flushes are spread over (a one-stream pass always runs first)")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -427,6 +439,9 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X, --gpus {args.gpus} is not run",
               file=sys.stderr)
+        sys.exit(2)
+    if args.streams < 1:
+        print("--streams must be at least 1", file=sys.stderr)
         sys.exit(2)
     if 2 + args.warmup + args.steps > 16:
         print("warmup + steps must fit the 32K-token stream: at most 14 flushes after the two warm-up flushes",
