@@ -92,11 +92,22 @@ __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, 
   return fmaxf(energy - msq, 0.f) / fmaxf(energy, 1e-12f);
 }
 
+// Candidate slots of the select path: row b owns slots [b * slots, (b + 1) *
+// slots), of which the first row_count[b] are candidates. NULL row_count: the
+// spans are numbered densely (the first *n_spans_dev of n_spans if given).
+struct SpanSlots {
+  const int32_t* row_count;
+  int32_t slots;
+};
+
+__device__ __forceinline__ bool span_live(const logkv_span_args& a, const SpanSlots& sl, int s) {
+  if (sl.row_count) return s % sl.slots < sl.row_count[s / sl.slots];
+  return !a.n_spans_dev || s < *a.n_spans_dev;
+}
+
 template <int NJ>
-__global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, float* __restrict__ out) {
-  __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
-  const int s = blockIdx.x;
-  if (a.n_spans_dev && s >= *a.n_spans_dev) return;
+__device__ __forceinline__ void score_span(const logkv_span_args& a, int s, float* part_k, float* part_v, float* q_s,
+                                           float* __restrict__ out) {
   const int g = wave_id();
   const int G = a.n_groups;
   const LOGKV_G int32_t* offs = gp(a.span_offsets);
@@ -169,6 +180,19 @@ __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_ar
     }
     out[s] = score;
   }
+  __syncthreads();   // part_k / part_v / q_s are rewritten by the block's next span
+}
+
+// One span per block iteration (grid-stride over the span slots), one wave
+// per KV group.
+template <int NJ>
+__global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, SpanSlots sl,
+                                                                   float* __restrict__ out) {
+  __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
+  for (int s = blockIdx.x; s < a.n_spans; s += gridDim.x) {
+    if (!span_live(a, sl, s)) continue;
+    score_span<NJ>(a, s, part_k, part_v, q_s, out);
+  }
 }
 
 // One wave per destination row (exact pool rows [0, P), then archive rows).
@@ -227,176 +251,26 @@ __global__ __launch_bounds__(256) void partition_kernel(logkv_partition_args a) 
 // the reference's Python floats.
 
 struct SelectWs {
-  int32_t* cand_row;     // [C] batch row of candidate i
+  int32_t* cand_row;     // [C] batch row of candidate slot i
   uint8_t* cand_flags;   // [C] bit 0 old, bit 1 closed
-  int32_t* row_cand;     // [n_batch + 1] first candidate of each row
-  int32_t* offsets;      // [C + 1] candidate i's tokens: tokens[offsets[i], offsets[i + 1])
+  int32_t* row_count;    // [n_batch] candidates of each row
+  int32_t* offsets;      // [C] candidate i's tokens: tokens[offsets[i], offsets[i + 1])
   int32_t* tokens;       // [n_batch * (P + T)]
-  int32_t* n_spans;      // [1]
   float* scores;         // [C]
 };
 
 constexpr int kSelectThreads = 256;
 constexpr int kCutBatch = 8;   // boundary rows per thread in flight in the cut
 
+// Candidate slots of one batch row: at most P + T + 1 candidates plus the end
+// offset of the last one. Row b owns slots [b * R, (b + 1) * R) and tokens
+// [b * (P + T), (b + 1) * (P + T)).
+__host__ __device__ inline int select_row_slots(int P, int T) { return P + T + 2; }
+
 __host__ __device__ inline int64_t select_candidates(int n_batch, int P, int T) {
-  return static_cast<int64_t>(n_batch) * (P + T + 1);
+  return static_cast<int64_t>(n_batch) * select_row_slots(P, T);
 }
 
-// One block: rows in order. The block finds segment starts (first row, after
-// a boundary, at a jump); thread 0 turns segments into candidate descriptors
-// in LDS; the block writes the candidate table and token lists.
-__global__ __launch_bounds__(kSelectThreads) void cut_kernel(logkv_alpha_select_args a, SelectWs w) {
-  extern __shared__ __align__(16) uint8_t dyn[];
-  const int T = a.tokens, P = a.budget, maxc = P + T + 1;
-  int32_t* seg = reinterpret_cast<int32_t*>(dyn);                            // [T + 1] segment starts
-  int32_t* olen = seg + T + 1;                                               // [P]
-  int32_t* c_first = olen + P;                                               // [maxc] first token of the range
-  int32_t* c_len = c_first + maxc;                                           // [maxc] range length
-  int32_t* c_pend = c_len + maxc;                                            // [maxc] prefixed pending rows
-  int32_t* c_off = c_pend + maxc;                                            // [maxc] token offset in the row
-  uint8_t* c_flags = reinterpret_cast<uint8_t*>(c_off + maxc);               // [maxc]
-  uint8_t* flags = c_flags + maxc;                                           // [T]
-  uint8_t* oclosed = flags + T;                                              // [P]
-  __shared__ int wave_cnt[kSelectThreads / kWave];
-  __shared__ int n_seg_s, nc_s, nt_s, row_nc_s, row_nt_s, pend_off_s;
-  if (threadIdx.x == 0) {
-    nc_s = 0;
-    nt_s = 0;
-    *a.alpha_count = 0;
-  }
-  for (int b = 0; b < a.n_batch; ++b) {
-    const LOGKV_G int64_t* pos = gp(a.new_pos + b * a.np_sb);
-    const LOGKV_G uint8_t* ends = gp(a.ends + b * a.ends_sb);
-    const int n_old = a.span_count[b];
-    for (int i = threadIdx.x; i < n_old; i += blockDim.x) {
-      olen[i] = a.span_len[static_cast<int64_t>(b) * P + i];
-      oclosed[i] = a.span_closed[static_cast<int64_t>(b) * P + i];
-    }
-    // kCutBatch rows per thread loaded (clamped, unconditionally) before any flag is written.
-    for (int j0 = 0; j0 < T; j0 += kCutBatch * static_cast<int>(blockDim.x)) {
-      int64_t pc[kCutBatch], pp[kCutBatch];
-      uint8_t ec[kCutBatch], ep[kCutBatch];
-#pragma unroll
-      for (int q = 0; q < kCutBatch; ++q) {
-        const int j = min(j0 + q * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x), T - 1);
-        const int jp = j > 0 ? j - 1 : 0;
-        pc[q] = pos[j];
-        pp[q] = pos[jp];
-        ec[q] = ends[j];
-        ep[q] = ends[jp];
-      }
-#pragma unroll
-      for (int q = 0; q < kCutBatch; ++q) {
-        const int j = j0 + q * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
-        if (j < T) {
-          const bool end = ec[q] != 0;
-          const bool jump = j > 0 && pc[q] != pp[q] + 1;
-          const bool start = j == 0 || jump || (j > 0 && ep[q] != 0);
-          flags[j] = static_cast<uint8_t>((end ? 1 : 0) | (start ? 2 : 0));
-        }
-      }
-    }
-    if (threadIdx.x == 0) n_seg_s = 0;
-    __syncthreads();
-    for (int j0 = 0; j0 < T; j0 += blockDim.x) {
-      const int j = j0 + threadIdx.x;
-      const bool mine = j < T && (flags[j] & 2);
-      const uint64_t ballot = __ballot(mine);
-      const int l = lane_id(), wv = wave_id();
-      const int before = __popcll(ballot & ((l == 0) ? 0ull : (~0ull >> (kWave - l))));
-      if (l == 0) wave_cnt[wv] = __popcll(ballot);
-      __syncthreads();
-      int base = n_seg_s;
-      for (int q = 0; q < wv; ++q) base += wave_cnt[q];
-      if (mine) seg[base + before] = j;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        int add = 0;
-        for (int q = 0; q < static_cast<int>(blockDim.x) / kWave; ++q) add += wave_cnt[q];
-        n_seg_s += add;
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-      int nc = 0, nt = 0;
-      const int n_seg = n_seg_s;
-      seg[n_seg] = T;
-      auto emit = [&](int first, int len, int pend, bool old, bool closed) {
-        c_first[nc] = first;
-        c_len[nc] = len;
-        c_pend[nc] = pend;
-        c_off[nc] = nt;
-        c_flags[nc] = static_cast<uint8_t>((old ? 1 : 0) | (closed ? 2 : 0));
-        nt += pend + len;
-        ++nc;
-      };
-      int off = 0, pend_off = 0, pend_len = 0;
-      for (int i = 0; i < n_old; ++i) {
-        if (oclosed[i]) emit(off, olen[i], 0, true, true);
-        else {
-          pend_off = off;
-          pend_len = olen[i];
-        }
-        off += olen[i];
-      }
-      if (T == 0) {
-        if (pend_len) emit(pend_off, pend_len, 0, false, false);
-      } else {
-        const bool pend_closed =
-            pend_len > 0 && pos[0] != a.pool_pos[static_cast<int64_t>(b) * P + pend_off + pend_len - 1] + 1;
-        if (pend_closed) emit(pend_off, pend_len, 0, false, true);
-        int carry = pend_closed ? 0 : pend_len;
-        for (int sg = 0; sg < n_seg; ++sg) {
-          const int e = seg[sg + 1];
-          for (int p = seg[sg]; p < e;) {
-            const int room = a.max_span - carry;
-            const int take = min(room, e - p);
-            const bool closed = take == room || p + take < e || e < T || (flags[e - 1] & 1);
-            emit(P + p, take, carry, false, closed);
-            carry = 0;
-            p += take;
-          }
-        }
-      }
-      row_nc_s = nc;
-      row_nt_s = nt;
-      pend_off_s = pend_off;
-      w.row_cand[b] = nc_s;
-    }
-    __syncthreads();
-    const int nc = row_nc_s, cbase = nc_s, tbase = nt_s, pend_off = pend_off_s;
-    LOGKV_G int32_t* tok = gp(w.tokens) + tbase;
-    for (int c = threadIdx.x; c < nc; c += blockDim.x) {
-      w.offsets[cbase + c] = tbase + c_off[c];
-      w.cand_row[cbase + c] = b;
-      w.cand_flags[cbase + c] = c_flags[c];
-      LOGKV_G int32_t* dst = tok + c_off[c];
-      const int pend = c_pend[c];
-      for (int t = 0; t < pend; ++t) dst[t] = pend_off + t;
-      for (int t = 0; t < c_len[c]; ++t) dst[pend + t] = c_first[c] + t;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      nc_s += nc;
-      nt_s += row_nt_s;
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    w.row_cand[a.n_batch] = nc_s;
-    w.offsets[nc_s] = nt_s;
-    *w.n_spans = nc_s;
-  }
-}
-
-// Strict weak order of the eviction list: ascending density, later candidate first.
-__device__ __forceinline__ bool evict_before(double da, int ia, double db, int ib) {
-  return da < db || (da == db && ia > ib);
-}
-
-// Exclusive block-wide scan of one int per thread (every thread of the block
-// calls it: it holds barriers); `total` receives the block's sum.
 // Inclusive wave scan by DPP: shifts 1, 2, 4, 8 within each row of 16 lanes,
 // then lane 15 of each row into the next row, lane 31 into rows 2 and 3
 // (lanes without a source add 0).
@@ -418,6 +292,8 @@ __device__ __forceinline__ double wave_shr1(double v) {
   return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
 }
 
+// Exclusive block-wide scan of one int per thread (every thread of the block
+// calls it: it holds barriers); `total` receives the block's sum.
 __device__ __forceinline__ int block_excl_scan(int v, int* wave_tmp, int& total) {
   const int w = wave_id(), nw = static_cast<int>(blockDim.x) / kWave;
   const int incl = wave_incl_scan(v);
@@ -439,6 +315,203 @@ __device__ __forceinline__ double readlane_f64(double x, int lane) {
   const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
   const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
   return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+// One block per batch row (litgpt/alpha_log_kv.py:16-53, :84-122). Closed old
+// spans become candidates in order; the last open old span is pending: closed
+// by a position jump before the first new row, else carried into the first
+// run. New rows split into hard segments (first row, after a boundary, at a
+// jump) and each segment into pieces of at most max_span rows (the carried
+// rows count toward the first piece; a carry of max_span or more does not
+// split its segment). Candidate numbers and token offsets come from block
+// scans over old spans and over segments.
+__global__ __launch_bounds__(kSelectThreads) void cut_kernel(logkv_alpha_select_args a, SelectWs w) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  const int b = blockIdx.x;
+  const int T = a.tokens, P = a.budget, maxc = P + T + 1, ms = a.max_span;
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  int32_t* seg = reinterpret_cast<int32_t*>(dyn);                            // [T + 1] segment starts
+  int32_t* olen = seg + T + 1;                                               // [P]
+  int32_t* c_first = olen + P;                                               // [maxc] first token of the range
+  int32_t* c_len = c_first + maxc;                                           // [maxc] range length
+  int32_t* c_pend = c_len + maxc;                                            // [maxc] prefixed pending rows
+  int32_t* c_off = c_pend + maxc;                                            // [maxc] token offset in the row
+  uint8_t* c_flags = reinterpret_cast<uint8_t*>(c_off + maxc);               // [maxc]
+  uint8_t* flags = c_flags + maxc;                                           // [T] bit 0 boundary, 1 segment start
+  uint8_t* oclosed = flags + T;                                              // [P]
+  __shared__ int wave_tmp[kSelectThreads / kWave];
+  __shared__ int pend_idx_s, pend_off_s, pend_len_s, carry_s, nc_s, nt_s;
+  if (b == 0 && tid == 0) *a.alpha_count = 0;
+  const LOGKV_G int64_t* pos = gp(a.new_pos + b * a.np_sb);
+  const LOGKV_G uint8_t* ends = gp(a.ends + b * a.ends_sb);
+  const int n_old = min(a.span_count[b], P);
+  if (tid == 0) pend_idx_s = -1;
+  for (int i = tid; i < n_old; i += nthr) {
+    olen[i] = a.span_len[static_cast<int64_t>(b) * P + i];
+    oclosed[i] = a.span_closed[static_cast<int64_t>(b) * P + i];
+  }
+  // Boundary flags, kCutBatch rows per thread loaded (clamped, unconditionally)
+  // before any flag is written.
+  for (int j0 = 0; j0 < T; j0 += kCutBatch * nthr) {
+    int64_t pc[kCutBatch], pp[kCutBatch];
+    uint8_t ec[kCutBatch], ep[kCutBatch];
+#pragma unroll
+    for (int q = 0; q < kCutBatch; ++q) {
+      const int j = min(j0 + q * nthr + tid, T - 1);
+      const int jp = j > 0 ? j - 1 : 0;
+      pc[q] = pos[j];
+      pp[q] = pos[jp];
+      ec[q] = ends[j];
+      ep[q] = ends[jp];
+    }
+#pragma unroll
+    for (int q = 0; q < kCutBatch; ++q) {
+      const int j = j0 + q * nthr + tid;
+      if (j < T) {
+        const bool end = ec[q] != 0;
+        const bool jump = j > 0 && pc[q] != pp[q] + 1;
+        const bool start = j == 0 || jump || (j > 0 && ep[q] != 0);
+        flags[j] = static_cast<uint8_t>((end ? 1 : 0) | (start ? 2 : 0));
+      }
+    }
+  }
+  __syncthreads();
+  // Segment starts in order (ballot compaction).
+  int n_seg = 0;
+  for (int j0 = 0; j0 < T; j0 += nthr) {
+    const int j = j0 + tid;
+    const bool mine = j < T && (flags[j] & 2);
+    int tot;
+    const int at = block_excl_scan(mine ? 1 : 0, wave_tmp, tot);
+    if (mine) seg[n_seg + at] = j;
+    n_seg += tot;
+  }
+  if (tid == 0) seg[n_seg] = T;
+  // Closed old spans -> candidates 0.. in order; the last open one is pending.
+  int n_closed = 0, closed_tok = 0, off_base = 0;
+  for (int i0 = 0; i0 < n_old; i0 += nthr) {
+    const int i = i0 + tid;
+    const bool in = i < n_old;
+    const int len = in ? olen[i] : 0;
+    const bool cl = in && oclosed[i];
+    int tot_len, tot_c, tot_t;
+    const int off = off_base + block_excl_scan(len, wave_tmp, tot_len);
+    const int ci = n_closed + block_excl_scan(cl ? 1 : 0, wave_tmp, tot_c);
+    const int ti = closed_tok + block_excl_scan(cl ? len : 0, wave_tmp, tot_t);
+    if (cl) {
+      c_first[ci] = off;
+      c_len[ci] = len;
+      c_pend[ci] = 0;
+      c_off[ci] = ti;
+      c_flags[ci] = 3;   // old, closed
+    }
+    if (in && !cl) atomicMax(&pend_idx_s, i);
+    __syncthreads();
+    if (in && !cl && i == pend_idx_s) {   // this chunk's last open span (a later chunk may replace it)
+      pend_off_s = off;
+      pend_len_s = len;
+    }
+    off_base += tot_len;
+    n_closed += tot_c;
+    closed_tok += tot_t;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const bool has_pend = pend_idx_s >= 0 && pend_len_s > 0;
+    const int pend_off = has_pend ? pend_off_s : 0, pend_len = has_pend ? pend_len_s : 0;
+    int nc = n_closed, nt = closed_tok, carry = 0;
+    if (T == 0) {
+      if (pend_len) {
+        c_first[nc] = pend_off;
+        c_len[nc] = pend_len;
+        c_pend[nc] = 0;
+        c_off[nc] = nt;
+        c_flags[nc] = 0;   // open
+        ++nc;
+        nt += pend_len;
+      }
+    } else if (pend_len) {
+      const int64_t last = a.pool_pos[static_cast<int64_t>(b) * P + min(pend_off + pend_len, P) - 1];
+      if (pos[0] != last + 1) {   // closed by the jump before the first new row
+        c_first[nc] = pend_off;
+        c_len[nc] = pend_len;
+        c_pend[nc] = 0;
+        c_off[nc] = nt;
+        c_flags[nc] = 2;   // new, closed
+        ++nc;
+        nt += pend_len;
+      } else {
+        carry = pend_len;
+      }
+    }
+    pend_off_s = pend_off;
+    carry_s = carry;
+    nc_s = nc;
+    nt_s = nt;
+  }
+  __syncthreads();
+  const int pend_off = pend_off_s, carry0 = carry_s;
+  int nc = nc_s, nt = nt_s;
+  // New segments -> pieces, numbered by block scans over the segments.
+  for (int s0 = 0; s0 < n_seg; s0 += nthr) {
+    const int sg = s0 + tid;
+    const bool in = sg < n_seg;
+    const int st = in ? seg[sg] : 0, e = in ? seg[sg + 1] : 0, len = e - st;
+    const int carry = sg == 0 ? carry0 : 0;
+    int pieces = 0;
+    if (in) {
+      if (carry >= ms) pieces = 1;
+      else if (carry > 0) pieces = 1 + (max(len - (ms - carry), 0) + ms - 1) / ms;
+      else pieces = (len + ms - 1) / ms;
+    }
+    int tot_p, tot_t;
+    const int pbase = nc + block_excl_scan(pieces, wave_tmp, tot_p);
+    const int tbase = nt + block_excl_scan(in ? len + carry : 0, wave_tmp, tot_t);
+    if (in) {
+      int p = st, cr = carry, t = tbase;
+      for (int k = 0; k < pieces; ++k) {
+        const int room = ms - cr;
+        const int take = cr >= ms ? e - p : min(room, e - p);
+        const bool closed = (cr < ms && take == room) || p + take < e || e < T || (flags[e - 1] & 1);
+        c_first[pbase + k] = P + p;
+        c_len[pbase + k] = take;
+        c_pend[pbase + k] = cr;
+        c_off[pbase + k] = t;
+        c_flags[pbase + k] = closed ? 2 : 0;
+        t += cr + take;
+        p += take;
+        cr = 0;
+      }
+    }
+    nc += tot_p;
+    nt += tot_t;
+  }
+  // Old spans claiming more than P rows are not a valid selection: the row
+  // then has no candidates (its token lists would leave the row's region).
+  if (nt > P + T) nc = nt = 0;
+  __syncthreads();
+  // Candidate table and token lists of this row's region.
+  const int64_t cbase = static_cast<int64_t>(b) * select_row_slots(P, T);
+  const int64_t tbase = static_cast<int64_t>(b) * (P + T);
+  LOGKV_G int32_t* tok = gp(w.tokens) + tbase;
+  for (int c = tid; c < nc; c += nthr) {
+    w.offsets[cbase + c] = static_cast<int32_t>(tbase + c_off[c]);
+    w.cand_row[cbase + c] = b;
+    w.cand_flags[cbase + c] = c_flags[c];
+    LOGKV_G int32_t* dst = tok + c_off[c];
+    const int pend = c_pend[c];
+    for (int t = 0; t < pend; ++t) dst[t] = pend_off + t;
+    for (int t = 0; t < c_len[c]; ++t) dst[pend + t] = c_first[c] + t;
+  }
+  if (tid == 0) {
+    w.offsets[cbase + nc] = static_cast<int32_t>(tbase + nt);
+    w.row_count[b] = nc;
+  }
+}
+
+// Strict weak order of the eviction list: ascending density, later candidate first.
+__device__ __forceinline__ bool evict_before(double da, int ia, double db, int ib) {
+  return da < db || (da == db && ia > ib);
 }
 
 // Sort key of a density: NaN as +inf, so that every order below is total.
@@ -628,7 +701,7 @@ __global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_sele
   extern __shared__ __align__(16) uint8_t dyn[];
   const int b = blockIdx.x;
   const int P = a.budget, T = a.tokens;
-  const int c0 = w.row_cand[b], n = w.row_cand[b + 1] - c0;
+  const int c0 = b * select_row_slots(P, T), n = w.row_count[b];
   const bool bitonic = n > kRankSortMax;
   int width = 1;
   while (bitonic && width < n) width <<= 1;
@@ -829,26 +902,36 @@ __global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_sele
   for (int i = kept + tid; i < P; i += nthr) keep[i] = -1;
   for (int i = arch + tid; i < A; i += nthr) archive[i] = -1;
   if (a.scores) {
-    for (int i = tid; i < n; i += nthr) a.scores[c0 + i] = w.scores[c0 + i];
+    // Scores out densely: row b's candidates follow those of rows 0..b-1.
+    int dense = 0;
+    for (int r = 0; r < b; ++r) dense += w.row_count[r];
+    for (int i = tid; i < n; i += nthr) a.scores[dense + i] = w.scores[c0 + i];
   }
 }
 
 }  // namespace
 
-int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
+constexpr int kScoreBlocks = 2048;   // most blocks of a score launch (each strides over span slots)
+
+int launch_score_slots(const logkv_span_args& a, const SpanSlots& sl, float* out, hipStream_t stream) {
   if (a.n_spans <= 0) return LOGKV_OK;
+  const dim3 grid(static_cast<unsigned>(std::min(a.n_spans, kScoreBlocks)));
   if (a.dk <= 2 * kWave && a.dv <= 2 * kWave)
-    hipLaunchKernelGGL(score_kernel<2>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
+    hipLaunchKernelGGL(score_kernel<2>, grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
   else
-    hipLaunchKernelGGL(score_kernel<4>, dim3(a.n_spans), dim3(a.n_groups * kWave), 0, stream, a, out);
+    hipLaunchKernelGGL(score_kernel<4>, grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
+  return launch_score_slots(a, SpanSlots{nullptr, 0}, out, stream);
 }
 
 int64_t select_workspace_bytes(const logkv_alpha_select_args& a) {
   const int64_t C = select_candidates(a.n_batch, a.budget, a.tokens);
   auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
-  return al(C * 4) + al(C) + al((a.n_batch + 1) * 4) + al((C + 1) * 4) +
-         al(static_cast<int64_t>(a.n_batch) * (a.budget + a.tokens) * 4) + al(4) + al(C * 4);
+  return al(C * 4) + al(C) + al(static_cast<int64_t>(a.n_batch) * 4) + al(C * 4) +
+         al(static_cast<int64_t>(a.n_batch) * (a.budget + a.tokens) * 4) + al(C * 4);
 }
 
 int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream) {
@@ -860,28 +943,26 @@ int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream
   p += al(C * 4);
   w.cand_flags = p;
   p += al(C);
-  w.row_cand = reinterpret_cast<int32_t*>(p);
-  p += al((a.n_batch + 1) * 4);
+  w.row_count = reinterpret_cast<int32_t*>(p);
+  p += al(static_cast<int64_t>(a.n_batch) * 4);
   w.offsets = reinterpret_cast<int32_t*>(p);
-  p += al((C + 1) * 4);
+  p += al(C * 4);
   w.tokens = reinterpret_cast<int32_t*>(p);
   p += al(static_cast<int64_t>(a.n_batch) * (a.budget + a.tokens) * 4);
-  w.n_spans = reinterpret_cast<int32_t*>(p);
-  p += al(4);
   w.scores = reinterpret_cast<float*>(p);
   const size_t cut_c = static_cast<size_t>(a.budget) + a.tokens + 1;
   const size_t cut_shmem = 4 * (static_cast<size_t>(a.tokens) + 1) + 5 * static_cast<size_t>(a.budget) +
                            17 * cut_c + static_cast<size_t>(a.tokens) + 16;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&cut_kernel), cut_shmem)) return LOGKV_ERUNTIME;
-  hipLaunchKernelGGL(cut_kernel, dim3(1), dim3(kSelectThreads), cut_shmem, stream, a, w);
+  hipLaunchKernelGGL(cut_kernel, dim3(a.n_batch), dim3(kSelectThreads), cut_shmem, stream, a, w);
   logkv_span_args sa = a.rows;
   sa.old_width = a.budget;
   sa.tokens = w.tokens;
   sa.span_offsets = w.offsets;
   sa.span_rows = w.cand_row;
   sa.n_spans = static_cast<int32_t>(C);
-  sa.n_spans_dev = w.n_spans;
-  int rc = launch_score(sa, w.scores, stream);
+  sa.n_spans_dev = nullptr;
+  int rc = launch_score_slots(sa, SpanSlots{w.row_count, select_row_slots(a.budget, a.tokens)}, w.scores, stream);
   if (rc) return rc;
   const int maxc = a.budget + a.tokens + 1;
   int width = 1;

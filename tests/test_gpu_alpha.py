@@ -79,7 +79,15 @@ def test_alpha_flush_matches_oracle(name):
 def _random_selection(rng, P, max_span, full=False):
     """Closed spans up to P - max_span rows and maybe a pending one; ``full``:
     closed spans filling all P rows (the next open candidate then forces
-    evictions before the greedy)."""
+    evictions before the greedy); "long": closed spans and a pending span of
+    max_span + 3 rows (a carry that does not split the first segment)."""
+    if full == "long":
+        spans, n = [], 0
+        while n + max_span + 3 + max_span <= P:
+            length = int(rng.integers(1, max_span + 1))
+            spans.append((length, True))
+            n += length
+        return spans + [(max_span + 3, False)]
     spans, n = [], 0
     while True:
         length = int(rng.integers(1, max_span + 1))
@@ -96,15 +104,17 @@ def _random_selection(rng, P, max_span, full=False):
     return spans
 
 
-# (beta, seed, P, T, span cap, boundary rate, full pool): small rows; a full
+# (beta, seed, P, T, span cap, boundary rate, pool): small rows; a full
 # pool (evictions before the greedy); 65-128 list entries (both register
 # slots of the one-wave greedy); >128 closed candidates (the one-thread
-# greedy); >512 candidates (the bitonic sort).
+# greedy); >512 candidates (the bitonic sort); a pending span longer than
+# the cap.
 SELECT_CASES = [(False, 0, 24, 40, 6, 0.2, False), (True, 1, 24, 40, 6, 0.2, False),
                 (True, 2, 24, 40, 6, 0.2, False), (False, 3, 24, 40, 6, 0.2, True),
                 (True, 4, 32, 48, 8, 0.25, True), (False, 7, 90, 60, 2, 0.5, True),
                 (True, 8, 90, 60, 2, 0.5, False), (False, 5, 64, 600, 8, 0.5, False),
-                (True, 6, 64, 1400, 8, 0.6, True)]
+                (True, 6, 64, 1400, 8, 0.6, True), (False, 9, 40, 50, 6, 0.05, "long"),
+                (True, 10, 40, 50, 6, 0.3, "long")]
 
 
 @pytest.mark.parametrize("beta,seed,P,T,ms,rate,full", SELECT_CASES)
