@@ -253,53 +253,61 @@ def flush_workload(args, torch, np):
     gen = torch.Generator(device=dev).manual_seed(1234)
     centers = torch.randn(layers, G, K, D, generator=gen, device=dev) * 4
 
-    def mixture(layer):
-        label = torch.randint(0, K, (1, G, F), generator=gen, device=dev)
-        x = torch.gather(centers[layer][None].expand(1, -1, -1, -1), 2, label[..., None].expand(-1, -1, -1, D))
-        x = x + torch.randn(1, G, F, D, generator=gen, device=dev) * 0.5
-        far = torch.rand(1, G, F, generator=gen, device=dev) < 0.1
+    def mixture():
+        """[layers, G, F, D]: layer li's rows drawn around its own 12 centers."""
+        label = torch.randint(0, K, (layers, G, F), generator=gen, device=dev)
+        x = torch.gather(centers, 2, label[..., None].expand(-1, -1, -1, D))
+        x = x + torch.randn(layers, G, F, D, generator=gen, device=dev) * 0.5
+        far = torch.rand(layers, G, F, generator=gen, device=dev) < 0.1
         return torch.where(far[..., None], torch.randn(x.shape, generator=gen, device=dev) * 12, x).to(torch.bfloat16)
 
-    data = [[(mixture(li), mixture(li)) for li in range(layers)] for _ in range(n_flush)]
-    positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).contiguous() for j in range(n_flush)]
-    # Boundary flags staged on the device like the rows and positions.
-    ends = [torch.tensor(span_ends_for(j), dtype=torch.uint8, device=dev) for j in range(n_flush)]
+    # Flush j's rows of every layer, stacked [layers, G, F, D]; layer li's rows are
+    # the batch-1 slice [li:li + 1]. Positions and boundary flags staged on the device.
+    data = [(mixture(), mixture()) for _ in range(n_flush)]
+    positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).expand(layers, -1).contiguous()
+                 for j in range(n_flush)]
+    ends = [torch.tensor(span_ends_for(j), dtype=torch.uint8, device=dev).expand(layers, -1).contiguous()
+            for j in range(n_flush)]
     dim = packed_dim(D, D)
-    empty = torch.empty(1, G, 0, D, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
 
-    def run_pass(n_streams, meter):
-        """Fresh caches, 2 + warmup untimed flushes, then `steps` timed ones. Layer li's
-        flushes go to stream li % n_streams: the layers' caches are independent, so
-        their flushes may overlap, while each layer's own flushes stay in order."""
-        caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev,
-                                       dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
-                                       semantic_s_h=64.0, semantic_flush_granularity=F, semantic_anchor_mode="mid",
-                                       allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
-                                       alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
-                                       beta_adaptive_merge=True)
-                  for _ in range(layers)]
-        workspaces = [(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev),
-                       torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev))
-                      for c in caches]
+    def new_cache(batch):
+        return LogStructuredKVCache((batch, G, N, D), (batch, G, N, D), B=B, recent_size=F, device=dev,
+                                    dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
+                                    semantic_s_h=64.0, semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                    allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                    alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                    beta_adaptive_merge=True)
+
+    def run_pass(stacked, n_streams, meter):
+        """Fresh caches, 2 + warmup untimed flushes, then `steps` timed ones, each followed
+        by the plan + pack of the next attention's packed prefix [pooled | exact | recent].
+        stacked: one cache whose batch rows are the layers, one call per flush step.
+        Otherwise one cache per layer, layer li's calls on stream li % n_streams (the
+        layers' caches are independent, so their flushes may overlap; each layer's own
+        flushes stay in order)."""
+        caches = [new_cache(layers)] if stacked else [new_cache(1) for _ in range(layers)]
+        workspaces = [tuple(torch.empty(c.batch_size, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16,
+                                        device=dev) for _ in range(2)) for c in caches]
+        empty = torch.empty(caches[0].batch_size, G, 0, D, dtype=torch.bfloat16, device=dev)
         streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(n_streams - 1)]
 
         def flush(j):
+            k, v = data[j]
             for li, cache in enumerate(caches):
+                rows = slice(None) if stacked else slice(li, li + 1)
                 with torch.cuda.stream(streams[li % n_streams]):
-                    k, v = data[j][li]
-                    cache.route_and_flush_batch(k, v, positions[j], span_ends=ends[j])
-                    # The next attention's packed prefix: plan + pack of [pooled | exact | recent].
+                    cache.route_and_flush_batch(k[rows], v[rows], positions[j][rows], span_ends=ends[j][rows])
                     view = readout_view(cache)
                     plan = cache._semantic_attention_plan()
                     _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
 
+        label = "stacked layers" if stacked else f"{n_streams} stream(s)"
         for j in range(2 + args.warmup):
             flush(j)
         torch.cuda.synchronize()
-        progress(f"flush, {n_streams} stream(s): {2 + args.warmup} untimed flushes done")
-        # Commit launches of every METER_EVERY-th layer are bracketed by events (the
-        # meter's ladder-state copies stay off the other layers).
+        progress(f"flush, {label}: {2 + args.warmup} untimed flushes done")
+        # Commit launches of every METER_EVERY-th layer cache are bracketed by events.
         metered = caches[::METER_EVERY] if meter else []
         meters = [CommitMeter(c, torch) for c in metered]
         for c, m in zip(metered, meters):
@@ -312,20 +320,24 @@ def flush_workload(args, torch, np):
         elapsed = time.perf_counter() - t0
         for c in metered:
             del c._route_commit
-        progress(f"flush, {n_streams} stream(s): {args.steps} timed flushes in {elapsed:.3f} s")
+        progress(f"flush, {label}: {args.steps} timed flushes in {elapsed:.3f} s")
         rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
         width = int(caches[0]._semantic_attention_plan().width)
         return elapsed, rec, caches[0].B_prime, caches[0].L_alloc, width
 
-    # Serial pass (one stream): per-layer latency and the commit-stage events.
-    serial, rec, B_, L_, width = run_pass(1, True)
-    elapsed = serial
-    if args.streams > 1:
-        elapsed = run_pass(args.streams, False)[0]
+    tokens = F * layers * args.steps
+    one_stream = run_pass(False, 1, args.mode == "layers")
+    per_layer = run_pass(False, args.streams, False)[0] if args.streams > 1 else one_stream[0]
+    if args.mode == "stacked":
+        elapsed, rec, B_, L_, width = run_pass(True, 1, True)
+    else:
+        _, rec, B_, L_, width = one_stream
+        elapsed = per_layer
     launch_bytes = float(np.mean([b for b, _ in rec]))
     launch_ms = float(np.mean([t for _, t in rec]))
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    tokens = F * layers * args.steps
+    how = ("the layers' caches stacked as the batch rows of one cache, one flush call per step"
+           if args.mode == "stacked" else f"one cache per layer, the layers' calls over {args.streams} streams")
     return {
         "value": tokens / elapsed,
         "ms_per_step": elapsed / args.steps * 1e3,
@@ -335,12 +347,14 @@ def flush_workload(args, torch, np):
                    "layers": layers, "flush": F, "batch": 1, "kv_groups": G, "head_dim": D, "clusters": K,
                    "slots_per_level": B_, "levels": L_, "exact_tokens": EXACT,
                    "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
-                   "pooled_width_after_last_flush": width, "streams": args.streams,
-                   "one_stream_tokens_per_s": tokens / serial,
-                   "one_stream_ms_per_layer_flush": serial / args.steps / layers * 1e3},
-        "roofline": {"kernel": "commit: commit_kernel + units_kernel + carries_kernel per level + finish_kernel "
-                               "(one-stream pass)", "bound": "hbm",
-                     "achieved": achieved, "peak": HBM_PEAK_GBS,
+                   "pooled_width_after_last_flush": width, "mode": how,
+                   "per_layer_calls_one_stream_tokens_per_s": tokens / one_stream[0],
+                   "per_layer_calls_one_stream_ms_per_layer_flush": one_stream[0] / args.steps / layers * 1e3,
+                   f"per_layer_calls_{args.streams}_streams_tokens_per_s": tokens / per_layer},
+        "roofline": {"kernel": "commit stage: commit_kernel + units_kernel + carries_kernel per level + "
+                               "finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
+                                                  else " (one-stream pass)"),
+                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
                      "launches": len(rec)},
@@ -429,8 +443,11 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--mode", choices=("stacked", "layers"), default="stacked",
+                    help="stacked: the layers' caches as batch rows of one cache (one call per flush step); "
+                         "layers: one cache per layer")
     ap.add_argument("--streams", type=int, default=4,
-                    help="HIP streams the layers' flushes are spread over (a one-stream pass always runs first)")
+                    help="HIP streams the per-layer calls are spread over (a one-stream pass always runs too)")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

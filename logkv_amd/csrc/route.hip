@@ -58,71 +58,134 @@ __global__ __launch_bounds__(1024) void order_kernel(const int64_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Frozen-center decisions: one wave per row, tiles of kAttachTile rows.
+// Frozen-center decisions (litgpt/log_kv_route_triton.py:841-917): one thread
+// per (row, cluster) pair over a tile of rows staged in LDS.
+//
+// Every distance keeps the canonical order of wave_sum0: leaf l (0..63) sums
+// features l, l + 64, ... in order; leaves fold as a balanced tree (l with
+// l + 32, then + 16, ..., + 1). One thread evaluates the whole tree, leaves
+// visited depth-first (bit-reversed leaf order), so no cross-lane reduction
+// is needed. Rows and centers are stored leaf-major: leaf l's NJ features
+// are adjacent (one LDS read), rows padded by two words against bank
+// conflicts between the rows a wave reads together.
 // ---------------------------------------------------------------------------
+template <int NJ>
+__host__ __device__ constexpr int leaf_stride() { return kWave * NJ + 2; }
+
+struct DotEx {
+  float dot, ex;
+};
+
+template <int NJ, int LEVEL, int L0>
+__device__ __forceinline__ DotEx canon_tree(const float* x, const float* m) {
+  if constexpr (LEVEL == 0) {
+    DotEx r;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float a = x[L0 * NJ + j], b = m[L0 * NJ + j];
+      const float diff = a - b;
+      r.dot = j == 0 ? a * b : r.dot + a * b;
+      r.ex = j == 0 ? diff * diff : r.ex + diff * diff;
+    }
+    return r;
+  } else {
+    const DotEx lo = canon_tree<NJ, LEVEL - 1, L0>(x, m);
+    // Subtrees of 8 leaves are scheduled one after the other, which bounds
+    // the LDS values in flight (and the registers holding them).
+    if constexpr (LEVEL == 4) __builtin_amdgcn_sched_barrier(0);
+    const DotEx hi = canon_tree<NJ, LEVEL - 1, L0 + (1 << (6 - LEVEL))>(x, m);
+    return DotEx{lo.dot + hi.dot, lo.ex + hi.ex};
+  }
+}
+
+// Canonical sum of squares of one leaf-major row.
+template <int NJ, int LEVEL, int L0>
+__device__ __forceinline__ float canon_sq(const float* x) {
+  if constexpr (LEVEL == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) s = j == 0 ? x[L0 * NJ] * x[L0 * NJ] : s + x[L0 * NJ + j] * x[L0 * NJ + j];
+    return s;
+  } else {
+    const float lo = canon_sq<NJ, LEVEL - 1, L0>(x);
+    if constexpr (LEVEL == 4) __builtin_amdgcn_sched_barrier(0);
+    return lo + canon_sq<NJ, LEVEL - 1, L0 + (1 << (6 - LEVEL))>(x);
+  }
+}
+
+template <int NJ>
+__host__ __device__ constexpr int attach_tile() { return NJ <= 2 ? 64 : 32; }
+
+template <int NJ>
+__host__ __device__ inline size_t attach_shmem(int K) {
+  constexpr int R = attach_tile<NJ>();
+  return static_cast<size_t>(R + K) * leaf_stride<NJ>() * 4 + static_cast<size_t>(R) * K * 8 +
+         static_cast<size_t>(R + K) * 4 + static_cast<size_t>(R) * 12 + 64;
+}
+
+template <int NJ>
 __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
                                                      const int32_t* __restrict__ order,
                                                      int8_t* __restrict__ assign, float* __restrict__ s_win) {
-  __shared__ float mu_s[kMaxClusters * kMaxDim];
-  __shared__ float mm_s[kMaxClusters];
+  constexpr int R = attach_tile<NJ>(), LS = leaf_stride<NJ>();
+  extern __shared__ __align__(16) float att[];
+  const int K = c.k_max, D = c.dk;
+  float* x_l = att;                        // [R][LS] rows, leaf-major
+  float* mu_l = x_l + R * LS;              // [K][LS] centers, leaf-major
+  float* dot_s = mu_l + K * LS;            // [R * K]
+  float* ex_s = dot_s + R * K;             // [R * K]
+  float* xx_s = ex_s + R * K;              // [R]
+  float* mm_s = xx_s + R;                  // [K]
+  int32_t* t_s = reinterpret_cast<int32_t*>(mm_s + K);                 // [R] row index in the flush
+  int64_t* pos_s = reinterpret_cast<int64_t*>(
+      reinterpret_cast<uintptr_t>(t_s + R + 1) & ~uintptr_t(7));       // [R]
   const int lane_ix = blockIdx.y;
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
-  const int K = c.k_max, D = c.dk;
   const int n = valid_rows(r, b);
-  const int tile0 = blockIdx.x * kAttachTile;
-  const float* mu = c.centroid + static_cast<int64_t>(lane_ix) * K * D;
-  for (int i = threadIdx.x; i < K * D; i += blockDim.x) mu_s[i] = mu[i];
-  __syncthreads();
-  const int l = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
-  const int J = (D + kWave - 1) / kWave;
-  for (int cc = w; cc < K; cc += nw) {
-    float s = 0.f;
-    for (int j = 0; j < J; ++j) {
-      const int d = l + j * kWave;
-      const float m = d < D ? mu_s[cc * D + d] : 0.f;
-      s = j == 0 ? m * m : s + m * m;
-    }
-    s = wave_sum0(s);
-    if (l == 0) mm_s[cc] = s;
+  const int tile0 = blockIdx.x * R;
+  const int rows = max(0, min(R, n - tile0));
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  // Centers and rows into LDS (features past D are zero).
+  const LOGKV_G float* mu = gp(c.centroid) + static_cast<int64_t>(lane_ix) * K * D;
+  for (int i = tid; i < K * kWave * NJ; i += nthr) {
+    const int cc = i / (kWave * NJ), f = i % (kWave * NJ), d = (f % kWave) + kWave * (f / kWave);
+    mu_l[cc * LS + (f % kWave) * NJ + f / kWave] = feat_or_zero(mu + cc * D, d, D);
+  }
+  for (int i = tid; i < rows; i += nthr) {
+    const int t = order[static_cast<int64_t>(b) * r.tokens + tile0 + i];
+    t_s[i] = t;
+    pos_s[i] = r.pos[b * r.pos_sb + t];
   }
   __syncthreads();
-  uint32_t alive_bits = 0;
-  for (int cc = 0; cc < K; ++cc) alive_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
-  const bool any_alive = alive_bits != 0;
-  const bool any_free = alive_bits != ((K >= 32) ? 0xffffffffu : ((1u << K) - 1u));
-  const float radius = prm.lam * c.s_h[lane_ix];
-  const int64_t* phi = c.p_hi_c + static_cast<int64_t>(lane_ix) * K;
-  const uint16_t* kbase = r.k + b * r.k_sb + g * r.k_sg;
-  for (int s = tile0 + w; s < tile0 + kAttachTile && s < n; s += nw) {
-    const int t = order[static_cast<int64_t>(b) * r.tokens + s];
-    const int64_t pos = r.pos[b * r.pos_sb + t];
-    const uint16_t* row = kbase + static_cast<int64_t>(t) * r.k_st;
-    float x[kMaxDim / kWave];
-    float xx = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMaxDim / kWave; ++j) {
-      const int d = l + j * kWave;
-      x[j] = feat_or_zero(gp(row), d, D);
-      if (j < J) xx = j == 0 ? x[j] * x[j] : xx + x[j] * x[j];
-    }
-    xx = wave_sum0(xx);
+  const LOGKV_G uint16_t* kbase = gp(r.k + b * r.k_sb + g * r.k_sg);
+  for (int i = tid; i < rows * kWave * NJ; i += nthr) {
+    const int rr = i / (kWave * NJ), f = i % (kWave * NJ);
+    const int d = (f % kWave) + kWave * (f / kWave);
+    x_l[rr * LS + (f % kWave) * NJ + f / kWave] = feat_or_zero(kbase + static_cast<int64_t>(t_s[rr]) * r.k_st, d, D);
+  }
+  __syncthreads();
+  if (tid < rows) xx_s[tid] = canon_sq<NJ, 6, 0>(x_l + tid * LS);
+  else if (tid >= R && tid < R + K) mm_s[tid - R] = canon_sq<NJ, 6, 0>(mu_l + (tid - R) * LS);
+  for (int p = tid; p < rows * K; p += nthr) {
+    const int rr = p / K, cc = p % K;
+    const DotEx de = canon_tree<NJ, 6, 0>(x_l + rr * LS, mu_l + cc * LS);
+    dot_s[p] = de.dot;
+    ex_s[p] = de.ex;
+  }
+  __syncthreads();
+  if (tid < rows) {
+    uint32_t alive_bits = 0;
+    for (int cc = 0; cc < K; ++cc) alive_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
+    const bool any_alive = alive_bits != 0;
+    const bool any_free = alive_bits != ((K >= 32) ? 0xffffffffu : ((1u << K) - 1u));
+    const float radius = prm.lam * c.s_h[lane_ix];
+    const LOGKV_G int64_t* phi = gp(c.p_hi_c) + static_cast<int64_t>(lane_ix) * K;
+    const float xx = xx_s[tid];
+    const int64_t pos = pos_s[tid];
     float best = __builtin_inff(), s_winner = 0.f, best_e = __builtin_inff();
     int winner = 0, nearest = 0;
     for (int cc = 0; cc < K; ++cc) {
-      float dot = 0.f, ex = 0.f;
-#pragma unroll
-      for (int j = 0; j < kMaxDim / kWave; ++j) {
-        if (j < J) {
-          const int d = l + j * kWave;
-          const float m = d < D ? mu_s[cc * D + d] : 0.f;
-          const float diff = x[j] - m;
-          dot = j == 0 ? x[j] * m : dot + x[j] * m;
-          ex = j == 0 ? diff * diff : ex + diff * diff;
-        }
-      }
-      dot = wave_sum0(dot);
-      ex = wave_sum0(ex);
-      const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot, 0.0f);
+      const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot_s[tid * K + cc], 0.0f);
       const bool live = (alive_bits >> cc) & 1u;
       if (cc == 0) s_winner = semantic;
       if (live) {
@@ -134,6 +197,7 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
           winner = cc;
           s_winner = semantic;
         }
+        const float ex = ex_s[tid * K + cc];
         if (ex < best_e) {
           best_e = ex;
           nearest = cc;
@@ -144,13 +208,12 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
     int out;
     if (!any_free) out = direct ? winner : nearest;
     else out = direct ? winner : -1;
-    if (l == 0) {
-      assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = static_cast<int8_t>(out);
-      if (any_free) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
-    }
+    const int s = tile0 + tid;
+    assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = static_cast<int8_t>(out);
+    if (any_free) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
   }
   // Padding rows of the lane keep -1.
-  for (int s = tile0 + threadIdx.x; s < tile0 + kAttachTile && s < r.tokens; s += blockDim.x)
+  for (int s = tile0 + tid; s < tile0 + R && s < r.tokens; s += nthr)
     if (s >= n) assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = -1;
 }
 
@@ -339,10 +402,20 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
   const int lanes = c.n_batch * c.n_groups;
   hipLaunchKernelGGL(order_kernel, dim3(c.n_batch), dim3(1024), 0, stream, r.pos, r.pos_sb, r.counts, r.tokens,
                      ws.order);
-  const int tiles = (r.tokens + kAttachTile - 1) / kAttachTile;
-  if (tiles > 0) {
-    hipLaunchKernelGGL(attach_kernel, dim3(tiles, lanes), dim3(256), 0, stream, c, r, p, ws.order, ws.assign,
-                       ws.s_win);
+  if (r.tokens > 0) {
+    const int nj = (c.dk + kWave - 1) / kWave;
+    auto attach = [&](auto kernel, int tile, size_t shmem) {
+      if (!allow_dynamic_lds(reinterpret_cast<const void*>(kernel), shmem)) return false;
+      hipLaunchKernelGGL(kernel, dim3((r.tokens + tile - 1) / tile, lanes), dim3(256), shmem, stream, c, r, p,
+                         ws.order, ws.assign, ws.s_win);
+      return true;
+    };
+    bool ok;
+    if (nj == 1) ok = attach(attach_kernel<1>, attach_tile<1>(), attach_shmem<1>(c.k_max));
+    else if (nj == 2) ok = attach(attach_kernel<2>, attach_tile<2>(), attach_shmem<2>(c.k_max));
+    else if (nj == 3) ok = attach(attach_kernel<3>, attach_tile<3>(), attach_shmem<3>(c.k_max));
+    else ok = attach(attach_kernel<4>, attach_tile<4>(), attach_shmem<4>(c.k_max));
+    if (!ok) return LOGKV_ERUNTIME;
     hipLaunchKernelGGL(seed_kernel, dim3(lanes), dim3(1024), 0, stream, c, r, ws.order, ws.assign, ws.s_win,
                        ws.dist, ws.snap_alive);
   }

@@ -12,7 +12,6 @@ using RouteParams = logkv_route_params;
 constexpr int kMaxOrderRows = 8192;   // rows per flush (position-order sort in LDS)
 constexpr int kOrderIndexBits = 13;
 constexpr uint64_t kOrderIndexMask = (1ull << kOrderIndexBits) - 1;
-constexpr int kAttachTile = 16;       // rows per attach block
 constexpr int kMaxClusters = 32;      // K (alive bits are a 32-bit mask)
 constexpr int kMaxDim = 256;          // dk, dv
 
