@@ -69,110 +69,151 @@ __device__ __forceinline__ float table_at(const void* t, int64_t i, int bf16) {
   return bf16 ? bf16_to_f32(gp(static_cast<const uint16_t*>(t))[i]) : gp(static_cast<const float*>(t))[i];
 }
 
-// RoPE of element d of a bf16 row at `pos` (rotate-half over the first rope_n dims).
-__device__ __forceinline__ float rope_at(const LOGKV_G uint16_t* row, int d, int64_t pos, const logkv_readout_view& c) {
-  const float x = bf16_to_f32(row[d]);
-  if (d >= c.rope_n) return x;
-  pos = pos < 0 ? 0 : (pos >= c.rope_rows ? c.rope_rows - 1 : pos);
-  const int half = c.rope_n / 2;
-  const float other = bf16_to_f32(row[d < half ? d + half : d - half]);
-  const float rot = d < half ? -other : other;
-  const float cs = table_at(c.cos, pos * c.cos_s0 + d * c.cos_s1, c.table_bf16);
-  const float sn = table_at(c.sin, pos * c.sin_s0 + d * c.sin_s1, c.table_bf16);
-  float a = x * cs, b = rot * sn;
-  if (c.table_bf16) {
-    a = round_bf16(a);
-    b = round_bf16(b);
-  }
-  return round_bf16(a + b);
-}
+constexpr int kPackRows = 64;   // packed rows per pack block
 
-// One wave per packed row; grid (row tiles, lanes).
+// Source of one packed row.
+struct PackSrc {
+  const LOGKV_G uint16_t* k;
+  const LOGKV_G uint16_t* v;
+  int64_t pos;
+  float bias;     // column dk: log(max(w, 1)) / 0 for valid rows, -10000 for invalid ones
+  int flags;      // bit 0 valid, bit 1 rotate, bit 2 row exists in the output
+};
+
+// Block (tile of kPackRows packed rows, lane). One thread per row resolves its
+// source (pooled rows by binary search over the lane's plan row, held in LDS);
+// then one thread per (row, 4-feature unit) writes the K and V units, every
+// load of a unit issued before its arithmetic.
 __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_pack_args p,
                                                    const int32_t* __restrict__ table) {
+  __shared__ int32_t prow[kMaxClusters * kMaxLevels + 1];
+  __shared__ PackSrc src[kPackRows];
   const int lanes = c.n_batch * c.n_groups;
   const int lane = blockIdx.y;
   const int b = lane / c.n_groups, g = lane % c.n_groups;
   const int KL = c.k_max * c.levels;
+  const int tid = static_cast<int>(threadIdx.x);
   const int width = table[static_cast<int64_t>(lanes) * (KL + 1)];
   const int alpha_count = c.alpha_count_dev ? *c.alpha_count_dev : c.alpha_count;
   const int tail_rows = alpha_count + c.recent_count + p.cur_len;
-  const int i0 = blockIdx.x * (blockDim.x / kWave) + wave_id();
-  int s;
-  if (p.skip_pooled) {
-    const int tail_start = alpha_count + p.recent_start;
-    if (tail_start + i0 >= tail_rows) return;
-    s = width + tail_start + i0;
-  } else {
-    if (i0 >= width + tail_rows) return;
-    s = i0;
-  }
-  if (s >= p.out_cap) return;
-  const int l = lane_id();
-  LOGKV_G uint16_t* ok = gp(p.out_k) + (static_cast<int64_t>(lane) * p.out_cap + s) * p.dim;
-  LOGKV_G uint16_t* ov = gp(p.out_v) + (static_cast<int64_t>(lane) * p.out_cap + s) * p.dim;
+  const int first = p.skip_pooled ? width + alpha_count + p.recent_start : 0;   // packed index of item 0
+  const int items = p.skip_pooled ? tail_rows - alpha_count - p.recent_start : width + tail_rows;
+  const int i0 = blockIdx.x * kPackRows;
+  if (i0 >= items) return;
+  const LOGKV_G int32_t* row_tab = gp(table) + static_cast<int64_t>(lane) * (KL + 1);
+  for (int i = tid; i <= KL; i += blockDim.x) prow[i] = row_tab[i];
+  __syncthreads();
   const int dk = c.dk, dv = c.dv;
-  const LOGKV_G uint16_t* kr = nullptr;
-  const LOGKV_G uint16_t* vr = nullptr;
-  bool rotate = false, valid = true;
-  int64_t pos = 0;
-  float bias = 0.f;
-  if (s < width) {
-    const LOGKV_G int32_t* row = gp(table) + static_cast<int64_t>(lane) * (KL + 1);
-    const int n_lane = row[KL];
-    valid = s < n_lane;
-    if (valid) {
-      // Block (cluster, level) holding pooled row s: largest prefix <= s.
-      int lo = 0, hi = KL - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (row[mid] <= s) lo = mid;
-        else hi = mid - 1;
-      }
-      // Skip empty blocks that share the prefix: the last block with prefix == row[lo].
-      const int cc = lo / c.levels, e = c.levels - 1 - lo % c.levels;
-      const int slot = s - row[lo];
-      const int64_t phys = ((static_cast<int64_t>(lane) * c.k_max + cc) * c.levels + e) * c.slots + slot;
-      const float w = gp(c.level_w)[phys];
-      valid = w > 0.f;
-      if (valid) {
-        const int64_t wi = static_cast<int64_t>(w) > 1 ? static_cast<int64_t>(w) : 1;
-        const int64_t swp = gp(c.level_sum_wp)[phys];
-        int64_t num = 2 * swp + wi, den = 2 * wi;
-        pos = num >= 0 ? num / den : -((-num + den - 1) / den);
-        kr = gp(c.level_k) + phys * dk;
-        vr = gp(c.level_v) + phys * dv;
-        rotate = true;
-        bias = round_bf16(logf(w > 1.f ? w : 1.f));
+  if (tid < kPackRows) {
+    const int s = first + i0 + tid;
+    PackSrc r{gp(c.level_k), gp(c.level_v), 0, -10000.0f, 0};
+    if (i0 + tid < items && s < p.out_cap) {
+      r.flags = 4;
+      if (s < width) {
+        if (s < prow[KL]) {
+          int lo = 0;   // largest block whose prefix is <= s (empty blocks share their successor's prefix)
+          for (int len = KL; len > 1;) {
+            const int half = len >> 1;
+            lo = prow[lo + half] <= s ? lo + half : lo;
+            len -= half;
+          }
+          const int cc = lo / c.levels, e = c.levels - 1 - lo % c.levels;
+          const int64_t phys = ((static_cast<int64_t>(lane) * c.k_max + cc) * c.levels + e) * c.slots + (s - prow[lo]);
+          const float w = gp(c.level_w)[phys];
+          if (w > 0.f) {
+            const int64_t wi = static_cast<int64_t>(w) > 1 ? static_cast<int64_t>(w) : 1;
+            const int64_t swp = gp(c.level_sum_wp)[phys];
+            const int64_t num = 2 * swp + wi, den = 2 * wi;
+            r.pos = num >= 0 ? num / den : -((-num + den - 1) / den);
+            r.k = gp(c.level_k) + phys * dk;
+            r.v = gp(c.level_v) + phys * dv;
+            r.bias = round_bf16(logf(w > 1.f ? w : 1.f));
+            r.flags |= 3;
+          }
+        }
+      } else if (s < width + alpha_count) {
+        const int i = s - width;
+        if (gp(c.alpha_valid)[static_cast<int64_t>(b) * c.alpha_cap + i] != 0) {
+          r.pos = gp(c.alpha_pos)[static_cast<int64_t>(b) * c.alpha_cap + i];
+          r.k = gp(c.alpha_k) + (static_cast<int64_t>(lane) * c.alpha_cap + i) * dk;
+          r.v = gp(c.alpha_v) + (static_cast<int64_t>(lane) * c.alpha_cap + i) * dv;
+          r.bias = 0.f;
+          r.flags |= 3;
+        }
+      } else if (s < width + alpha_count + c.recent_count) {
+        const int i = s - width - alpha_count;
+        r.k = gp(c.recent_k) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dk;
+        r.v = gp(c.recent_v) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dv;
+        r.bias = 0.f;
+        r.flags |= 1;
+      } else {
+        const int i = s - width - alpha_count - c.recent_count;
+        r.k = gp(p.cur_k) + b * p.ck_sb + g * p.ck_sg + static_cast<int64_t>(i) * p.ck_st;
+        r.v = gp(p.cur_v) + b * p.cv_sb + g * p.cv_sg + static_cast<int64_t>(i) * p.cv_st;
+        r.bias = 0.f;
+        r.flags |= 1;
       }
     }
-  } else if (s < width + alpha_count) {
-    const int i = s - width;
-    valid = gp(c.alpha_valid)[static_cast<int64_t>(b) * c.alpha_cap + i] != 0;
-    if (valid) {
-      pos = gp(c.alpha_pos)[static_cast<int64_t>(b) * c.alpha_cap + i];
-      kr = gp(c.alpha_k) + (static_cast<int64_t>(lane) * c.alpha_cap + i) * dk;
-      vr = gp(c.alpha_v) + (static_cast<int64_t>(lane) * c.alpha_cap + i) * dv;
-      rotate = true;
-    }
-  } else if (s < width + alpha_count + c.recent_count) {
-    const int i = s - width - alpha_count;
-    kr = gp(c.recent_k) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dk;
-    vr = gp(c.recent_v) + (static_cast<int64_t>(lane) * c.recent_cap + i) * dv;
-  } else {
-    const int i = s - width - alpha_count - c.recent_count;
-    kr = gp(p.cur_k) + b * p.ck_sb + g * p.ck_sg + static_cast<int64_t>(i) * p.ck_st;
-    vr = gp(p.cur_v) + b * p.cv_sb + g * p.cv_sg + static_cast<int64_t>(i) * p.cv_st;
+    src[tid] = r;
   }
-  for (int d = l; d < p.dim; d += kWave) {
-    float kx = 0.f, vx = 0.f;
-    if (valid) {
-      if (d < dk) kx = rotate ? rope_at(kr, d, pos, c) : bf16_to_f32(kr[d]);
-      if (d < dv) vx = bf16_to_f32(vr[d]);
+  __syncthreads();
+  const int units = p.dim / 4;   // per K row and per V row
+  const int half = c.rope_n / 2;
+  for (int it = tid; it < kPackRows * 2 * units; it += blockDim.x) {
+    const int rr = it / (2 * units), u = it % (2 * units);
+    const PackSrc r = src[rr];
+    if (!(r.flags & 4)) continue;
+    const int s = first + i0 + rr;
+    const bool valid = r.flags & 1;
+    float o[4];
+    if (u < units) {
+      const int d0 = 4 * u;
+      // Unconditional loads at clamped indices, selected afterwards.
+      float x[4], other[4], cs[4], sn[4];
+      const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = d0 + q, dd = d < dk ? d : dk - 1;
+        const int pd = d < half ? d + half : d - half;
+        const int pc = pd < 0 ? 0 : (pd < dk ? pd : dk - 1);
+        const int rd = d < c.rope_n ? d : 0;
+        x[q] = bf16_to_f32(r.k[dd]);
+        other[q] = bf16_to_f32(r.k[pc]);
+        cs[q] = table_at(c.cos, pos * c.cos_s0 + rd * c.cos_s1, c.table_bf16);
+        sn[q] = table_at(c.sin, pos * c.sin_s0 + rd * c.sin_s1, c.table_bf16);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = d0 + q;
+        float kx = x[q];
+        if ((r.flags & 2) && d < c.rope_n) {
+          const float rot = d < half ? -other[q] : other[q];
+          float a = kx * cs[q], bb = rot * sn[q];
+          if (c.table_bf16) {
+            a = round_bf16(a);
+            bb = round_bf16(bb);
+          }
+          kx = round_bf16(a + bb);
+        }
+        o[q] = d < dk ? (valid ? kx : 0.f) : (d == dk ? r.bias : 0.f);
+      }
+    } else {
+      const int d0 = 4 * (u - units);
+      float y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = d0 + q;
+        y[q] = bf16_to_f32(r.v[d < dv ? d : dv - 1]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = (valid && d0 + q < dv) ? y[q] : 0.f;
     }
-    if (d == dk) kx = valid ? bias : -10000.0f;
-    ok[d] = f32_to_bf16(kx);
-    ov[d] = f32_to_bf16(vx);
+    const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s) * p.dim;
+    LOGKV_G uint16_t* dst = u < units ? gp(p.out_k) + orow + 4 * u : gp(p.out_v) + orow + 4 * (u - units);
+    uint2 packed;
+    packed.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
+    packed.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
+    *reinterpret_cast<LOGKV_G uint2*>(dst) = packed;
   }
 }
 
@@ -325,8 +366,8 @@ int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int
   // the whole recent window and current rows; blocks past the end exit).
   const int rows = p.skip_pooled ? c.recent_count + p.cur_len - p.recent_start : p.out_cap;
   if (rows <= 0) return LOGKV_OK;
-  const int per_block = 256 / kWave;
-  hipLaunchKernelGGL(pack_kernel, dim3((rows + per_block - 1) / per_block, c.n_batch * c.n_groups), dim3(256), 0,
+  // Tiles past the packed rows (known on the device only) exit at once.
+  hipLaunchKernelGGL(pack_kernel, dim3((rows + kPackRows - 1) / kPackRows, c.n_batch * c.n_groups), dim3(256), 0,
                      stream, c, p, table);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
