@@ -282,6 +282,9 @@ int logkv_pack(const logkv_readout_view* c, const logkv_pack_args* p, const int3
   if (p->cur_len < 0 || (p->cur_len && (!p->cur_k || !p->cur_v)) || p->recent_start < 0 ||
       p->recent_start > c->recent_count || p->out_cap < 0)
     return fail(LOGKV_EINVAL, "bad current rows or output capacity");
+  if (p->cur_len && (reinterpret_cast<uintptr_t>(p->cur_k) % 8 || reinterpret_cast<uintptr_t>(p->cur_v) % 8 ||
+                     p->ck_sb % 4 || p->ck_sg % 4 || p->ck_st % 4 || p->cv_sb % 4 || p->cv_sg % 4 || p->cv_st % 4))
+    return fail(LOGKV_EINVAL, "current rows must be 8-byte aligned (strides multiples of 4 elements)");
   rc = logkv::launch_pack(*c, *p, table, static_cast<hipStream_t>(stream));
   if (rc) return fail(rc, "pack launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;

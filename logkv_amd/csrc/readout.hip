@@ -65,6 +65,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(logkv_readout_view c
   }
 }
 
+__device__ __forceinline__ float lo_bf16(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
 __device__ __forceinline__ float table_at(const void* t, int64_t i, int bf16) {
   return bf16 ? bf16_to_f32(gp(static_cast<const uint16_t*>(t))[i]) : gp(static_cast<const float*>(t))[i];
 }
@@ -159,6 +162,10 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
   __syncthreads();
   const int units = p.dim / 4;   // per K row and per V row
   const int half = c.rope_n / 2;
+  // Vector loads of 4 features and 4 table entries need 4-aligned rows and
+  // contiguous tables with 4-aligned position strides (the usual layout).
+  const bool vec = c.cos_s1 == 1 && c.sin_s1 == 1 && c.cos_s0 % 4 == 0 && c.sin_s0 % 4 == 0 && c.rope_n % 8 == 0 &&
+                   reinterpret_cast<uintptr_t>(c.cos) % 16 == 0 && reinterpret_cast<uintptr_t>(c.sin) % 16 == 0;
   for (int it = tid; it < kPackRows * 2 * units; it += blockDim.x) {
     const int rr = it / (2 * units), u = it % (2 * units);
     const PackSrc r = src[rr];
@@ -168,45 +175,77 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
     float o[4];
     if (u < units) {
       const int d0 = 4 * u;
-      // Unconditional loads at clamped indices, selected afterwards.
-      float x[4], other[4], cs[4], sn[4];
-      const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
+      if (d0 >= dk) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = d0 + q, dd = d < dk ? d : dk - 1;
-        const int pd = d < half ? d + half : d - half;
-        const int pc = pd < 0 ? 0 : (pd < dk ? pd : dk - 1);
-        const int rd = d < c.rope_n ? d : 0;
-        x[q] = bf16_to_f32(r.k[dd]);
-        other[q] = bf16_to_f32(r.k[pc]);
-        cs[q] = table_at(c.cos, pos * c.cos_s0 + rd * c.cos_s1, c.table_bf16);
-        sn[q] = table_at(c.sin, pos * c.sin_s0 + rd * c.sin_s1, c.table_bf16);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = d0 + q;
-        float kx = x[q];
-        if ((r.flags & 2) && d < c.rope_n) {
-          const float rot = d < half ? -other[q] : other[q];
-          float a = kx * cs[q], bb = rot * sn[q];
+        for (int q = 0; q < 4; ++q) o[q] = d0 + q == dk ? r.bias : 0.f;
+      } else {
+        const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
+        float x[4], other[4], cs[4], sn[4];
+        if (vec) {
+          // The unit's 4 features, their rotate-half partners (the same side of
+          // the half for all 4) and 4 table entries each as one vector load.
+          const int pd = d0 < c.rope_n ? (d0 < half ? d0 + half : d0 - half) : d0;
+          const int rd = d0 < c.rope_n ? d0 : 0;
+          const uint2 xu = *reinterpret_cast<const LOGKV_G uint2*>(r.k + d0);
+          const uint2 pu = *reinterpret_cast<const LOGKV_G uint2*>(r.k + pd);
+          x[0] = lo_bf16(xu.x); x[1] = hi_bf16(xu.x); x[2] = lo_bf16(xu.y); x[3] = hi_bf16(xu.y);
+          other[0] = lo_bf16(pu.x); other[1] = hi_bf16(pu.x); other[2] = lo_bf16(pu.y); other[3] = hi_bf16(pu.y);
           if (c.table_bf16) {
-            a = round_bf16(a);
-            bb = round_bf16(bb);
+            const uint2 cu = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.cos)) +
+                                                                    pos * c.cos_s0 + rd);
+            const uint2 su = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.sin)) +
+                                                                    pos * c.sin_s0 + rd);
+            cs[0] = lo_bf16(cu.x); cs[1] = hi_bf16(cu.x); cs[2] = lo_bf16(cu.y); cs[3] = hi_bf16(cu.y);
+            sn[0] = lo_bf16(su.x); sn[1] = hi_bf16(su.x); sn[2] = lo_bf16(su.y); sn[3] = hi_bf16(su.y);
+          } else {
+            const float4 cf = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.cos)) +
+                                                                      pos * c.cos_s0 + rd);
+            const float4 sf = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.sin)) +
+                                                                      pos * c.sin_s0 + rd);
+            cs[0] = cf.x; cs[1] = cf.y; cs[2] = cf.z; cs[3] = cf.w;
+            sn[0] = sf.x; sn[1] = sf.y; sn[2] = sf.z; sn[3] = sf.w;
           }
-          kx = round_bf16(a + bb);
+        } else {
+          // Unconditional scalar loads at clamped indices, selected afterwards.
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int d = d0 + q, dd = d < dk ? d : dk - 1;
+            const int pd = d < half ? d + half : d - half;
+            const int pc = pd < 0 ? 0 : (pd < dk ? pd : dk - 1);
+            const int rd = d < c.rope_n ? d : 0;
+            x[q] = bf16_to_f32(r.k[dd]);
+            other[q] = bf16_to_f32(r.k[pc]);
+            cs[q] = table_at(c.cos, pos * c.cos_s0 + rd * c.cos_s1, c.table_bf16);
+            sn[q] = table_at(c.sin, pos * c.sin_s0 + rd * c.sin_s1, c.table_bf16);
+          }
         }
-        o[q] = d < dk ? (valid ? kx : 0.f) : (d == dk ? r.bias : 0.f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = d0 + q;
+          float kx = x[q];
+          if ((r.flags & 2) && d < c.rope_n) {
+            const float rot = d < half ? -other[q] : other[q];
+            float a = kx * cs[q], bb = rot * sn[q];
+            if (c.table_bf16) {
+              a = round_bf16(a);
+              bb = round_bf16(bb);
+            }
+            kx = round_bf16(a + bb);
+          }
+          o[q] = d < dk ? (valid ? kx : 0.f) : (d == dk ? r.bias : 0.f);
+        }
       }
     } else {
       const int d0 = 4 * (u - units);
-      float y[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = d0 + q;
-        y[q] = bf16_to_f32(r.v[d < dv ? d : dv - 1]);
+      if (d0 < dv) {   // dv is a multiple of 4: the unit is whole
+        const uint2 vu = *reinterpret_cast<const LOGKV_G uint2*>(r.v + d0);
+        o[0] = valid ? lo_bf16(vu.x) : 0.f;
+        o[1] = valid ? hi_bf16(vu.x) : 0.f;
+        o[2] = valid ? lo_bf16(vu.y) : 0.f;
+        o[3] = valid ? hi_bf16(vu.y) : 0.f;
+      } else {
+        o[0] = o[1] = o[2] = o[3] = 0.f;
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = (valid && d0 + q < dv) ? y[q] : 0.f;
     }
     const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s) * p.dim;
     LOGKV_G uint16_t* dst = u < units ? gp(p.out_k) + orow + 4 * u : gp(p.out_v) + orow + 4 * (u - units);
