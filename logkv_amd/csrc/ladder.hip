@@ -1037,11 +1037,23 @@ __device__ inline Src flush_rows_global(const LadderArgs& c, const RowsArgs& r, 
   return s;
 }
 
+// Units [u, u_end) of one ladder at level ell (lu = u - first unit of the ladder).
+template <int NJ, int KIND>
+__device__ __forceinline__ void ladder_units(const PoolT<KIND>& pool, const Soa& out, int n_carry, bool beta, int lu0,
+                                             int lu1, int dk, int dv) {
+  for (int lu = lu0; lu < lu1; ++lu) {
+    if (beta) beta_group<NJ, KIND>(pool, out, 2 * n_carry, lu, dk, dv);
+    else pair_carry<KIND>(pool, out, lu, dk, dv);
+  }
+}
+
 // Carries launch `ell`: the level's work units (numbered ladder after ladder
-// by units_kernel) are spread over all waves of the grid by a grid stride; a
-// wave finds its unit's ladder by binary search over the unit prefix table
-// staged in LDS. Launches ell = 0..L-2 run in stream order (level ell stages
-// level ell - 1's carries); slots are not written here.
+// by units_kernel) are split into contiguous ranges, one per wave, so a wave
+// resolves a ladder's plan and sources once for all its units there and reads
+// the ladder's rows in order. A wave finds its first ladder by binary search
+// over the unit prefix table staged in LDS. Launches ell = 0..L-2 run in
+// stream order (level ell stages level ell - 1's carries); slots are not
+// written here.
 template <int NJ>
 __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
                                                                 Workspace ws, int ell) {
@@ -1052,32 +1064,37 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
   __syncthreads();
   const int total = prefix_s[ladders];
   const int wpb = static_cast<int>(blockDim.x) / kWave;
-  const int stride = static_cast<int>(gridDim.x) * wpb;
+  const int n_waves = static_cast<int>(gridDim.x) * wpb;
+  const int per = (total + n_waves - 1) / n_waves;
+  int u = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
+  const int u_end = min(total, u + per);
+  if (u >= u_end) return;
+  int ladder = 0;   // the ladder of unit u: prefix_s[ladder] <= u < prefix_s[ladder + 1]
+  for (int len = ladders; len > 1;) {
+    const int half = len >> 1;
+    ladder = prefix_s[ladder + half] <= u ? ladder + half : ladder;
+    len -= half;
+  }
+  ladder = __builtin_amdgcn_readfirstlane(ladder);
   const bool beta = prm.beta_merge != 0;
-  for (int u = static_cast<int>(blockIdx.x) * wpb + wave_id(); u < total; u += stride) {
-    int lo = 0, hi = ladders;   // prefix_s[lo] <= u < prefix_s[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (prefix_s[mid] <= u) lo = mid;
-      else hi = mid;
+  const int64_t base = static_cast<int64_t>(ell) * c.slots;
+  while (u < u_end) {
+    const int first = prefix_s[ladder], last = min(prefix_s[ladder + 1], u_end);
+    if (last > u) {
+      const LadderPlan* pl = ws.plans + ladder;
+      const int cnt = pl->cnt[ell], m = pl->m[ell];
+      const int n_carry = carries_of(cnt, m, c.slots, false);
+      const Ladder lad = ladder_of(c, ladder);
+      const Soa out = carry_of(ws, ladder, ell, c.dk, c.dv);
+      if (ell == 0 && pl->kind0 == 0)
+        ladder_units<NJ, 2>(PoolT<2>{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)}, out, n_carry, beta,
+                            u - first, last - first, c.dk, c.dv);
+      else
+        ladder_units<NJ, 1>(PoolT<1>{lad, base, cnt, staged_of(ws, ladder, ell, c.dk, c.dv)}, out, n_carry, beta,
+                            u - first, last - first, c.dk, c.dv);
+      u = last;
     }
-    const int ladder = __builtin_amdgcn_readfirstlane(lo);
-    const int lu = u - prefix_s[ladder];
-    const LadderPlan* pl = ws.plans + ladder;
-    const int cnt = pl->cnt[ell], m = pl->m[ell];
-    const int n_carry = carries_of(cnt, m, c.slots, false);
-    const Ladder lad = ladder_of(c, ladder);
-    const int64_t base = static_cast<int64_t>(ell) * c.slots;
-    const Soa out = carry_of(ws, ladder, ell, c.dk, c.dv);
-    if (ell == 0 && pl->kind0 == 0) {
-      const PoolT<2> pool{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)};
-      if (beta) beta_group<NJ, 2>(pool, out, 2 * n_carry, lu, c.dk, c.dv);
-      else pair_carry<2>(pool, out, lu, c.dk, c.dv);
-    } else {
-      const PoolT<1> pool{lad, base, cnt, staged_of(ws, ladder, ell, c.dk, c.dv)};
-      if (beta) beta_group<NJ, 1>(pool, out, 2 * n_carry, lu, c.dk, c.dv);
-      else pair_carry<1>(pool, out, lu, c.dk, c.dv);
-    }
+    ++ladder;
   }
 }
 
