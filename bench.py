@@ -326,8 +326,11 @@ def flush_workload(args, torch, np):
         return elapsed, rec, caches[0].B_prime, caches[0].L_alloc, width
 
     tokens = F * layers * args.steps
-    one_stream = run_pass(False, 1, args.mode == "layers")
-    per_layer = run_pass(False, args.streams, False)[0] if args.streams > 1 else one_stream[0]
+    if args.flush_passes == "stacked" and args.mode == "stacked":
+        one_stream = per_layer = None
+    else:
+        one_stream = run_pass(False, 1, args.mode == "layers")
+        per_layer = run_pass(False, args.streams, False)[0] if args.streams > 1 else one_stream[0]
     if args.mode == "stacked":
         elapsed, rec, B_, L_, width = run_pass(True, 1, True)
     else:
@@ -348,9 +351,10 @@ def flush_workload(args, torch, np):
                    "slots_per_level": B_, "levels": L_, "exact_tokens": EXACT,
                    "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
                    "pooled_width_after_last_flush": width, "mode": how,
-                   "per_layer_calls_one_stream_tokens_per_s": tokens / one_stream[0],
-                   "per_layer_calls_one_stream_ms_per_layer_flush": one_stream[0] / args.steps / layers * 1e3,
-                   f"per_layer_calls_{args.streams}_streams_tokens_per_s": tokens / per_layer},
+                   **({} if one_stream is None else {
+                       "per_layer_calls_one_stream_tokens_per_s": tokens / one_stream[0],
+                       "per_layer_calls_one_stream_ms_per_layer_flush": one_stream[0] / args.steps / layers * 1e3,
+                       f"per_layer_calls_{args.streams}_streams_tokens_per_s": tokens / per_layer})},
         "roofline": {"kernel": "commit stage: commit_kernel + units_kernel + carries_kernel per level + "
                                "finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
                                                   else " (one-stream pass)"),
@@ -452,6 +456,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (a plain copy of known size that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
+    ap.add_argument("--flush-passes", choices=("all", "stacked"), default="all",
+                    help="stacked: run only the stacked pass (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X, --gpus {args.gpus} is not run",
@@ -469,6 +478,14 @@ def main():
     import torch
 
     torch.cuda.set_device(0)
+    if args.copy_probe_mib:
+        src = torch.ones(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        progress(f"copy probe: {args.copy_probe_mib} MiB copied")
+        del src, dst
     fl = flush_workload(args, torch, np)
     result = {
         "metric": "flushed tokens/s (route+merge+pack) & decode ms/token at 32K ctx, 1 GPU",
