@@ -37,6 +37,11 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METER_EVERY = 7   # layers 0, 7, 14, 21 carry the commit-stage events
+# HBM bytes of one stacked commit stage (28 layers) from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs scaled by a 1 GiB copy probe (profiles/commit_stage_traffic_28layer_
+# stacked_qwen3_1.7b.md); counters cannot be read inside this process, so the figure is
+# the profiled one and is re-measured whenever the commit kernels change.
+STACKED_COMMIT_TRAFFIC_BYTES = 2319.5e6
 G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
 EXACT, SPAN = 256, 64
 
@@ -359,7 +364,8 @@ def flush_workload(args, torch, np):
                                "finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
                                                   else " (one-stream pass)"),
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": STACKED_COMMIT_TRAFFIC_BYTES if args.mode == "stacked" else None,
                      "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
                      "launches": len(rec)},
     }
