@@ -117,6 +117,28 @@ __device__ __forceinline__ float wave_sum0(float s) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
 }
 
+// Four canonical sums at once, each exactly wave_sum0 of its value: the first
+// permlane32 swap pairs a with b (lanes 0-31 fold a, lanes 32-63 fold b) and c
+// with d; the permlane16 swap of the two results leaves rows 0..3 folding a, c,
+// b, d; the row shifts finish all four. Every lane of the wave must be active.
+__device__ __forceinline__ void wave_sum4(float a, float b, float c, float d, float& sa, float& sb, float& sc,
+                                          float& sd) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float ab = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  const float cd = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(ab), __float_as_uint(cd), false, false);
+  float s = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x108, 0xf, 0xf, false));  // row_shl:8
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x104, 0xf, 0xf, false));  // row_shl:4
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, false));  // row_shl:2
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x101, 0xf, 0xf, false));  // row_shl:1
+  sa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16));
+  sb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+  sd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 48));
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 

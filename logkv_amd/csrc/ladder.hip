@@ -304,37 +304,13 @@ __device__ __forceinline__ void clear_slots(const Ladder& L, int64_t first, int6
 
 // ---- Beta 4->2 -------------------------------------------------------------
 
-// Canonical sum over the features held as t[j] (feature l + 64 j) in every
-// lane; called with the whole wave active.
+// Sum over j (in order) of the squares of row i's features l + 64 j held in lane l.
 template <int NJ>
-__device__ __forceinline__ float feat_sum(const float* t) {
-  float s = t[0];
+__device__ __forceinline__ float lane_sq(const float (&x)[NJ]) {
+  float s = x[0] * x[0];
 #pragma unroll
-  for (int j = 1; j < NJ; ++j) s = s + t[j];
-  return wave_sum0(s);
-}
-
-// sum_i w_i |x_i - mean|^2 over rows of one side; rows outside the side add +0.
-template <int NJ>
-__device__ __forceinline__ float side_loss(const float (&x)[4][NJ], const float* wt, const float* mean, int D, unsigned member) {
-  float loss = 0.f;
-  const int l = lane_id();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float per = 0.f;
-    if ((member >> i) & 1u) {
-      float t[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const float d = (l + j * kWave < D) ? x[i][j] - mean[j] : 0.f;
-        t[j] = d * d;
-      }
-      per = feat_sum<NJ>(t);
-    }
-    const float term = per * wt[i];
-    loss = i == 0 ? term : loss + term;
-  }
-  return loss;
+  for (int j = 1; j < NJ; ++j) s = s + x[j] * x[j];
+  return s;
 }
 
 template <int NJ>
@@ -351,33 +327,80 @@ __device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* 
   }
 }
 
-// Adds this component's normalised distortion of the cuts (2, 1, 3) to costs
-// in the Torch reference's order: left then right side, per option.
+// One component's row energies sum_d x_id^2 -> e = sum_i sq_i w_i (row order),
+// and for the cuts (2, 1, 3) the losses sum_i w_i |x_i - mean_side|^2 of the
+// left and right sides (row order; rows of the other side add w = 0 times
+// their distance to the other side's mean). Feature sums are canonical; the
+// four rows of a cut are folded together (wave_sum4).
 template <int NJ>
-__device__ __forceinline__ void beta_component_cost(const float (&x)[4][NJ], const float* wr, float total, int D, float* costs) {
-  float e = 0.f;
+__device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], const float* wr, float& e,
+                                                      float* loss) {
+  float sq[4];
+  wave_sum4(lane_sq<NJ>(x[0]), lane_sq<NJ>(x[1]), lane_sq<NJ>(x[2]), lane_sq<NJ>(x[3]), sq[0], sq[1], sq[2], sq[3]);
+  e = sq[0] * wr[0];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float t[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) t[j] = x[i][j] * x[i][j];
-    const float term = feat_sum<NJ>(t) * wr[i];
-    e = i == 0 ? term : e + term;
-  }
-  const float energy = fmaxf(e / total, 1e-12f);
+  for (int i = 1; i < 4; ++i) e = e + sq[i] * wr[i];
 #pragma unroll
   for (int opt = 0; opt < 3; ++opt) {
     const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+    float wl[4], wrt[4], ml[NJ], mr[NJ], mass;
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-      const unsigned member = side == 0 ? ((1u << c) - 1u) : (0xfu & ~((1u << c) - 1u));
-      float wt[4], mean[NJ], mass;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-      side_mean<NJ>(x, wt, mean, mass);
-      costs[opt] = costs[opt] + side_loss<NJ>(x, wt, mean, D, member) / energy;
+    for (int i = 0; i < 4; ++i) {
+      wl[i] = i < c ? wr[i] : 0.f;
+      wrt[i] = i < c ? 0.f : wr[i];
     }
+    side_mean<NJ>(x, wl, ml, mass);
+    side_mean<NJ>(x, wrt, mr, mass);
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float d[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) d[j] = x[i][j] - (i < c ? ml[j] : mr[j]);
+      t[i] = lane_sq<NJ>(d);
+    }
+    float per[4];
+    wave_sum4(t[0], t[1], t[2], t[3], per[0], per[1], per[2], per[3]);
+    float left = per[0] * wl[0], right = per[0] * wrt[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+      left = left + per[i] * wl[i];
+      right = right + per[i] * wrt[i];
+    }
+    loss[2 * opt] = left;
+    loss[2 * opt + 1] = right;
   }
+}
+
+// Cut of a full group (litgpt/beta_log_kv.py:29-85): costs of (2, 1, 3) summed
+// over K then V, left side then right, of loss / energy with energy =
+// max(e / total, 1e-12); the smallest cost wins (first on ties). The 2 + 12
+// uniform divisions run as two lane-parallel divisions.
+template <int NJ>
+__device__ __forceinline__ int beta_cut(const float (&xk)[4][NJ], const float (&xv)[4][NJ], const float* wr) {
+  const int l = lane_id();
+  const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
+  float ek, ev, lk[6], lv[6];
+  beta_component_losses<NJ>(xk, wr, ek, lk);
+  beta_component_losses<NJ>(xv, wr, ev, lv);
+  const float en = (l == 0 ? ek : ev) / total;
+  const float energy_k = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(en), 0)), 1e-12f);
+  const float energy_v = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(en), 1)), 1e-12f);
+  float num = 0.f;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    num = l == k ? lk[k] : num;
+    num = l == 6 + k ? lv[k] : num;
+  }
+  const float q = num / (l < 6 ? energy_k : energy_v);
+  float costs[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 12; ++k)
+    costs[(k % 6) / 2] = costs[(k % 6) / 2] + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), k));
+  int best = 0;
+  if (costs[1] < costs[best]) best = 1;
+  if (costs[2] < costs[best]) best = 2;
+  return best == 0 ? 2 : (best == 1 ? 1 : 3);
 }
 
 // Quad (4-lane) butterfly exchanges: lane i reads lane i ^ 1 / i ^ 2 of its quad.
@@ -553,17 +576,7 @@ __device__ __forceinline__ void beta_group(const PoolT<KIND>& pool, const Soa& o
       xv[i][j] = valid ? b : 0.f;
     }
   }
-  int cut = 1;
-  if (width == 4) {
-    const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
-    float costs[3] = {0.f, 0.f, 0.f};
-    beta_component_cost<NJ>(xk, wr, total, dk, costs);
-    beta_component_cost<NJ>(xv, wr, total, dv, costs);
-    int best = 0;
-    if (costs[1] < costs[best]) best = 1;
-    if (costs[2] < costs[best]) best = 2;
-    cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
-  }
+  const int cut = width == 4 ? beta_cut<NJ>(xk, xv, wr) : 1;
   const int dest = start / 2;
   for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
     unsigned member;
