@@ -195,42 +195,69 @@ __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_ar
   }
 }
 
-// One wave per destination row (exact pool rows [0, P), then archive rows).
+// Destination rows [exact pool rows 0..P | archive rows] of one lane, a tile
+// of kPartRows per block: the tile's source indices are read into LDS, then
+// every thread copies kPartBatch 8-byte units of K|V, all loads issued before
+// the stores (a source of -1 writes zeros).
+constexpr int kPartRows = 32;
+constexpr int kPartBatch = 8;
+
 __global__ __launch_bounds__(256) void partition_kernel(logkv_partition_args a) {
+  __shared__ int src_s[kPartRows];
   const int G = a.n_groups;
   const int lane_bg = blockIdx.y;
   const int b = lane_bg / G, g = lane_bg % G;
-  const int r = blockIdx.x * (blockDim.x / kWave) + wave_id();
-  if (r >= a.P + a.A) return;
-  const bool to_pool = r < a.P;
-  const int src = to_pool ? a.keep[static_cast<int64_t>(b) * a.P + r] : a.archive[static_cast<int64_t>(b) * a.A + r - a.P];
+  const int r0 = blockIdx.x * kPartRows;
+  const int rows = min(kPartRows, a.P + a.A - r0);
+  if (rows <= 0) return;
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  if (tid < rows) {
+    const int r = r0 + tid;
+    const bool to_pool = r < a.P;
+    const int src = to_pool ? a.keep[static_cast<int64_t>(b) * a.P + r]
+                            : a.archive[static_cast<int64_t>(b) * a.A + r - a.P];
+    src_s[tid] = src;
+    if (g == 0) {
+      int64_t pos = 0;
+      if (src >= 0)
+        pos = src < a.old_width ? a.pool_pos[b * a.pp_sb + src] : a.flush_pos[b * a.fp_sb + src - a.old_width];
+      if (to_pool) {
+        a.out_pool_pos[static_cast<int64_t>(b) * a.P + r] = pos;
+        a.out_pool_valid[static_cast<int64_t>(b) * a.P + r] = src >= 0 ? 1 : 0;
+      } else {
+        a.arch_pos[static_cast<int64_t>(b) * a.A + r - a.P] = pos;
+      }
+    }
+  }
+  __syncthreads();
   Rows2 ks{gp(a.pool_k), a.pk_sb, a.pk_sg, a.pk_st, gp(a.flush_k), a.fk_sb, a.fk_sg, a.fk_st, a.old_width};
   Rows2 vs{gp(a.pool_v), a.pv_sb, a.pv_sg, a.pv_st, gp(a.flush_v), a.fv_sb, a.fv_sg, a.fv_st, a.old_width};
-  LOGKV_G uint16_t* dk_row;
-  LOGKV_G uint16_t* dv_row;
-  if (to_pool) {
-    dk_row = gp(a.out_pool_k) + ((static_cast<int64_t>(b) * G + g) * a.P + r) * a.dk;
-    dv_row = gp(a.out_pool_v) + ((static_cast<int64_t>(b) * G + g) * a.P + r) * a.dv;
-  } else {
-    dk_row = gp(a.arch_k) + ((static_cast<int64_t>(b) * G + g) * a.A + (r - a.P)) * a.dk;
-    dv_row = gp(a.arch_v) + ((static_cast<int64_t>(b) * G + g) * a.A + (r - a.P)) * a.dv;
-  }
-  const int ku = a.dk / 4, units = (a.dk + a.dv) / 4;
-  const LOGKV_G uint16_t* sk = src >= 0 ? ks.row(b, g, src) : nullptr;
-  const LOGKV_G uint16_t* sv = src >= 0 ? vs.row(b, g, src) : nullptr;
-  for (int u = lane_id(); u < units; u += kWave) {
-    uint2 x = make_uint2(0u, 0u);
-    if (src >= 0) x = *(const LOGKV_G uint2*)(u < ku ? sk + 4 * u : sv + 4 * (u - ku));
-    *(LOGKV_G uint2*)(u < ku ? dk_row + 4 * u : dv_row + 4 * (u - ku)) = x;
-  }
-  if (g == 0 && lane_id() == 0) {
-    int64_t pos = 0;
-    if (src >= 0) pos = src < a.old_width ? a.pool_pos[b * a.pp_sb + src] : a.flush_pos[b * a.fp_sb + src - a.old_width];
-    if (to_pool) {
-      a.out_pool_pos[static_cast<int64_t>(b) * a.P + r] = pos;
-      a.out_pool_valid[static_cast<int64_t>(b) * a.P + r] = src >= 0 ? 1 : 0;
-    } else {
-      a.arch_pos[static_cast<int64_t>(b) * a.A + r - a.P] = pos;
+  const int ku = a.dk / 4, units = (a.dk + a.dv) / 4, total = rows * units;
+  const int64_t lane_row0 = (static_cast<int64_t>(b) * G + g);
+  for (int i0 = tid; i0 < total; i0 += kPartBatch * nthr) {
+    uint2 x[kPartBatch];
+#pragma unroll
+    for (int q = 0; q < kPartBatch; ++q) {
+      const int i = min(i0 + q * nthr, total - 1);
+      const int t = i / units, u = i % units;
+      const int src = src_s[t];
+      const int sr = src >= 0 ? src : 0;
+      const LOGKV_G uint16_t* p = u < ku ? ks.row(b, g, sr) + 4 * u : vs.row(b, g, sr) + 4 * (u - ku);
+      const uint2 v = *(const LOGKV_G uint2*)p;
+      x[q] = src >= 0 ? v : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int q = 0; q < kPartBatch; ++q) {
+      const int i = i0 + q * nthr;
+      if (i < total) {
+        const int t = i / units, u = i % units, r = r0 + t;
+        LOGKV_G uint16_t* dst;
+        if (r < a.P) dst = u < ku ? gp(a.out_pool_k) + (lane_row0 * a.P + r) * a.dk + 4 * u
+                                  : gp(a.out_pool_v) + (lane_row0 * a.P + r) * a.dv + 4 * (u - ku);
+        else dst = u < ku ? gp(a.arch_k) + (lane_row0 * a.A + (r - a.P)) * a.dk + 4 * u
+                          : gp(a.arch_v) + (lane_row0 * a.A + (r - a.P)) * a.dv + 4 * (u - ku);
+        *(LOGKV_G uint2*)dst = x[q];
+      }
     }
   }
 }
@@ -976,8 +1003,7 @@ int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream
 int launch_partition(const logkv_partition_args& a, hipStream_t stream) {
   const int rows = a.P + a.A;
   if (rows <= 0) return LOGKV_OK;
-  const int per_block = 256 / kWave;
-  hipLaunchKernelGGL(partition_kernel, dim3((rows + per_block - 1) / per_block, a.n_batch * a.n_groups), dim3(256), 0,
+  hipLaunchKernelGGL(partition_kernel, dim3((rows + kPartRows - 1) / kPartRows, a.n_batch * a.n_groups), dim3(256), 0,
                      stream, a);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
