@@ -18,6 +18,8 @@
 // h / (Hq / G). Flash-decoding: row splits per lane, each staging 64-row K and
 // V tiles in LDS with an online softmax; a second kernel combines the splits in
 // a fixed order.
+#include <type_traits>
+
 #include "route.hpp"
 
 namespace logkv {
@@ -73,6 +75,7 @@ __device__ __forceinline__ float table_at(const void* t, int64_t i, int bf16) {
 }
 
 constexpr int kPackRows = 64;   // packed rows per pack block
+constexpr int kPackBatch = 4;   // units per thread whose loads are issued before their arithmetic
 
 // Source of one packed row.
 struct PackSrc {
@@ -82,6 +85,111 @@ struct PackSrc {
   float bias;     // column dk: log(max(w, 1)) / 0 for valid rows, -10000 for invalid ones
   int flags;      // bit 0 valid, bit 1 rotate, bit 2 row exists in the output
 };
+
+__device__ __forceinline__ void store_bf16x4(LOGKV_G uint16_t* dst, const float* o) {
+  uint2 packed;
+  packed.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
+  packed.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
+  *reinterpret_cast<LOGKV_G uint2*>(dst) = packed;
+}
+
+// Packed key feature d: rotate-half RoPE at the row's anchor for rotated rows
+// (products rounded to bf16 first with bf16 tables), the row's bias at column
+// dk, zero past it and for invalid rows.
+__device__ __forceinline__ float rope_out(const logkv_readout_view& c, const PackSrc& r, int d, float x, float other,
+                                          float cs, float sn, int half, bool valid) {
+  float kx = x;
+  if ((r.flags & 2) && d < c.rope_n) {
+    const float rot = d < half ? -other : other;
+    float a = kx * cs, bb = rot * sn;
+    if (c.table_bf16) {
+      a = round_bf16(a);
+      bb = round_bf16(bb);
+    }
+    kx = round_bf16(a + bb);
+  }
+  return d < c.dk ? (valid ? kx : 0.f) : (d == c.dk ? r.bias : 0.f);
+}
+
+// K then V units of a tile, kPackBatch per thread with all their loads (row
+// features, rotate-half partners, table entries: one vector load each) issued
+// before the arithmetic. Needs contiguous tables with 4-aligned position strides.
+template <bool BF16_TABLE>
+__device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, const logkv_pack_args& p,
+                                               const PackSrc* src, int s0, int lane, int units, int half) {
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  const int items = kPackRows * units;
+  using TableUnit = typename std::conditional<BF16_TABLE, uint2, float4>::type;
+  for (int i0 = tid; i0 < items; i0 += kPackBatch * nthr) {
+    uint2 xu[kPackBatch], pu[kPackBatch];
+    TableUnit cu[kPackBatch], su[kPackBatch];
+#pragma unroll
+    for (int q = 0; q < kPackBatch; ++q) {
+      const int i = min(i0 + q * nthr, items - 1);
+      const PackSrc& r = src[i / units];
+      const int d0r = 4 * (i % units);
+      const int d0 = d0r < c.dk ? d0r : 0;
+      const int pd = d0 < c.rope_n ? (d0 < half ? d0 + half : d0 - half) : d0;
+      const int rd = d0 < c.rope_n ? d0 : 0;
+      const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
+      xu[q] = *reinterpret_cast<const LOGKV_G uint2*>(r.k + d0);
+      pu[q] = *reinterpret_cast<const LOGKV_G uint2*>(r.k + pd);
+      if constexpr (BF16_TABLE) {
+        cu[q] = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.cos)) + pos * c.cos_s0 + rd);
+        su[q] = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.sin)) + pos * c.sin_s0 + rd);
+      } else {
+        cu[q] = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.cos)) + pos * c.cos_s0 + rd);
+        su[q] = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.sin)) + pos * c.sin_s0 + rd);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kPackBatch; ++q) {
+      const int i = i0 + q * nthr;
+      if (i >= items) break;
+      const PackSrc& r = src[i / units];
+      if (!(r.flags & 4)) continue;
+      const int u = i % units, d0 = 4 * u;
+      const bool valid = r.flags & 1;
+      const float x[4] = {lo_bf16(xu[q].x), hi_bf16(xu[q].x), lo_bf16(xu[q].y), hi_bf16(xu[q].y)};
+      const float other[4] = {lo_bf16(pu[q].x), hi_bf16(pu[q].x), lo_bf16(pu[q].y), hi_bf16(pu[q].y)};
+      float cs[4], sn[4];
+      if constexpr (BF16_TABLE) {
+        cs[0] = lo_bf16(cu[q].x); cs[1] = hi_bf16(cu[q].x); cs[2] = lo_bf16(cu[q].y); cs[3] = hi_bf16(cu[q].y);
+        sn[0] = lo_bf16(su[q].x); sn[1] = hi_bf16(su[q].x); sn[2] = lo_bf16(su[q].y); sn[3] = hi_bf16(su[q].y);
+      } else {
+        cs[0] = cu[q].x; cs[1] = cu[q].y; cs[2] = cu[q].z; cs[3] = cu[q].w;
+        sn[0] = su[q].x; sn[1] = su[q].y; sn[2] = su[q].z; sn[3] = su[q].w;
+      }
+      float o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = rope_out(c, r, d0 + k, x[k], other[k], cs[k], sn[k], half, valid);
+      const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + i / units) * p.dim;
+      store_bf16x4(gp(p.out_k) + orow + d0, o);
+    }
+  }
+  for (int i0 = tid; i0 < items; i0 += kPackBatch * nthr) {
+    uint2 vu[kPackBatch];
+#pragma unroll
+    for (int q = 0; q < kPackBatch; ++q) {
+      const int i = min(i0 + q * nthr, items - 1);
+      const int d0r = 4 * (i % units);
+      vu[q] = *reinterpret_cast<const LOGKV_G uint2*>(src[i / units].v + (d0r < c.dv ? d0r : 0));
+    }
+#pragma unroll
+    for (int q = 0; q < kPackBatch; ++q) {
+      const int i = i0 + q * nthr;
+      if (i >= items) break;
+      const PackSrc& r = src[i / units];
+      if (!(r.flags & 4)) continue;
+      const int d0 = 4 * (i % units);
+      const bool keep = (r.flags & 1) && d0 < c.dv;
+      const float o[4] = {keep ? lo_bf16(vu[q].x) : 0.f, keep ? hi_bf16(vu[q].x) : 0.f,
+                          keep ? lo_bf16(vu[q].y) : 0.f, keep ? hi_bf16(vu[q].y) : 0.f};
+      const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + i / units) * p.dim;
+      store_bf16x4(gp(p.out_v) + orow + d0, o);
+    }
+  }
+}
 
 // Block (tile of kPackRows packed rows, lane). One thread per row resolves its
 // source (pooled rows by binary search over the lane's plan row, held in LDS);
@@ -166,6 +274,11 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
   // contiguous tables with 4-aligned position strides (the usual layout).
   const bool vec = c.cos_s1 == 1 && c.sin_s1 == 1 && c.cos_s0 % 4 == 0 && c.sin_s0 % 4 == 0 && c.rope_n % 8 == 0 &&
                    reinterpret_cast<uintptr_t>(c.cos) % 16 == 0 && reinterpret_cast<uintptr_t>(c.sin) % 16 == 0;
+  if (vec) {
+    if (c.table_bf16) pack_units_vec<true>(c, p, src, first + i0, lane, units, half);
+    else pack_units_vec<false>(c, p, src, first + i0, lane, units, half);
+    return;
+  }
   for (int it = tid; it < kPackRows * 2 * units; it += blockDim.x) {
     const int rr = it / (2 * units), u = it % (2 * units);
     const PackSrc r = src[rr];
@@ -181,59 +294,20 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
       } else {
         const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
         float x[4], other[4], cs[4], sn[4];
-        if (vec) {
-          // The unit's 4 features, their rotate-half partners (the same side of
-          // the half for all 4) and 4 table entries each as one vector load.
-          const int pd = d0 < c.rope_n ? (d0 < half ? d0 + half : d0 - half) : d0;
-          const int rd = d0 < c.rope_n ? d0 : 0;
-          const uint2 xu = *reinterpret_cast<const LOGKV_G uint2*>(r.k + d0);
-          const uint2 pu = *reinterpret_cast<const LOGKV_G uint2*>(r.k + pd);
-          x[0] = lo_bf16(xu.x); x[1] = hi_bf16(xu.x); x[2] = lo_bf16(xu.y); x[3] = hi_bf16(xu.y);
-          other[0] = lo_bf16(pu.x); other[1] = hi_bf16(pu.x); other[2] = lo_bf16(pu.y); other[3] = hi_bf16(pu.y);
-          if (c.table_bf16) {
-            const uint2 cu = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.cos)) +
-                                                                    pos * c.cos_s0 + rd);
-            const uint2 su = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.sin)) +
-                                                                    pos * c.sin_s0 + rd);
-            cs[0] = lo_bf16(cu.x); cs[1] = hi_bf16(cu.x); cs[2] = lo_bf16(cu.y); cs[3] = hi_bf16(cu.y);
-            sn[0] = lo_bf16(su.x); sn[1] = hi_bf16(su.x); sn[2] = lo_bf16(su.y); sn[3] = hi_bf16(su.y);
-          } else {
-            const float4 cf = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.cos)) +
-                                                                      pos * c.cos_s0 + rd);
-            const float4 sf = *reinterpret_cast<const LOGKV_G float4*>(gp(static_cast<const float*>(c.sin)) +
-                                                                      pos * c.sin_s0 + rd);
-            cs[0] = cf.x; cs[1] = cf.y; cs[2] = cf.z; cs[3] = cf.w;
-            sn[0] = sf.x; sn[1] = sf.y; sn[2] = sf.z; sn[3] = sf.w;
-          }
-        } else {
-          // Unconditional scalar loads at clamped indices, selected afterwards.
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int d = d0 + q, dd = d < dk ? d : dk - 1;
-            const int pd = d < half ? d + half : d - half;
-            const int pc = pd < 0 ? 0 : (pd < dk ? pd : dk - 1);
-            const int rd = d < c.rope_n ? d : 0;
-            x[q] = bf16_to_f32(r.k[dd]);
-            other[q] = bf16_to_f32(r.k[pc]);
-            cs[q] = table_at(c.cos, pos * c.cos_s0 + rd * c.cos_s1, c.table_bf16);
-            sn[q] = table_at(c.sin, pos * c.sin_s0 + rd * c.sin_s1, c.table_bf16);
-          }
-        }
+        // Unconditional scalar loads at clamped indices, selected afterwards.
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int d = d0 + q;
-          float kx = x[q];
-          if ((r.flags & 2) && d < c.rope_n) {
-            const float rot = d < half ? -other[q] : other[q];
-            float a = kx * cs[q], bb = rot * sn[q];
-            if (c.table_bf16) {
-              a = round_bf16(a);
-              bb = round_bf16(bb);
-            }
-            kx = round_bf16(a + bb);
-          }
-          o[q] = d < dk ? (valid ? kx : 0.f) : (d == dk ? r.bias : 0.f);
+          const int d = d0 + q, dd = d < dk ? d : dk - 1;
+          const int pd = d < half ? d + half : d - half;
+          const int pc = pd < 0 ? 0 : (pd < dk ? pd : dk - 1);
+          const int rd = d < c.rope_n ? d : 0;
+          x[q] = bf16_to_f32(r.k[dd]);
+          other[q] = bf16_to_f32(r.k[pc]);
+          cs[q] = table_at(c.cos, pos * c.cos_s0 + rd * c.cos_s1, c.table_bf16);
+          sn[q] = table_at(c.sin, pos * c.sin_s0 + rd * c.sin_s1, c.table_bf16);
         }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = rope_out(c, r, d0 + q, x[q], other[q], cs[q], sn[q], half, valid);
       }
     } else {
       const int d0 = 4 * (u - units);
@@ -248,11 +322,7 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
       }
     }
     const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s) * p.dim;
-    LOGKV_G uint16_t* dst = u < units ? gp(p.out_k) + orow + 4 * u : gp(p.out_v) + orow + 4 * (u - units);
-    uint2 packed;
-    packed.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
-    packed.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
-    *reinterpret_cast<LOGKV_G uint2*>(dst) = packed;
+    store_bf16x4(u < units ? gp(p.out_k) + orow + 4 * u : gp(p.out_v) + orow + 4 * (u - units), o);
   }
 }
 
