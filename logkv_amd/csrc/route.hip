@@ -114,7 +114,7 @@ __device__ __forceinline__ float canon_sq(const float* x) {
 }
 
 template <int NJ>
-__host__ __device__ constexpr int attach_tile() { return NJ <= 2 ? 64 : 32; }
+__host__ __device__ constexpr int attach_tile() { return NJ <= 2 ? 32 : 16; }
 
 template <int NJ>
 __host__ __device__ inline size_t attach_shmem(int K) {
@@ -156,6 +156,15 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
     t_s[i] = t;
     pos_s[i] = r.pos[b * r.pos_sb + t];
   }
+  // The lane's cluster state for the decisions (alive bits, p_hi per cluster).
+  __shared__ int64_t phi_s[kMaxClusters];
+  __shared__ uint32_t alive_s;
+  if (tid < kWave) {
+    const bool live = tid < K && c.alive[lane_ix * K + tid];
+    const uint64_t bits = __ballot(live);
+    if (tid < K) phi_s[tid] = c.p_hi_c[static_cast<int64_t>(lane_ix) * K + tid];
+    if (tid == 0) alive_s = static_cast<uint32_t>(bits);
+  }
   __syncthreads();
   const LOGKV_G uint16_t* kbase = gp(r.k + b * r.k_sb + g * r.k_sg);
   for (int i = tid; i < rows * kWave * NJ; i += nthr) {
@@ -174,12 +183,11 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
   }
   __syncthreads();
   if (tid < rows) {
-    uint32_t alive_bits = 0;
-    for (int cc = 0; cc < K; ++cc) alive_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
+    const uint32_t alive_bits = alive_s;
     const bool any_alive = alive_bits != 0;
     const bool any_free = alive_bits != ((K >= 32) ? 0xffffffffu : ((1u << K) - 1u));
     const float radius = prm.lam * c.s_h[lane_ix];
-    const LOGKV_G int64_t* phi = gp(c.p_hi_c) + static_cast<int64_t>(lane_ix) * K;
+    const int64_t* phi = phi_s;
     const float xx = xx_s[tid];
     const int64_t pos = pos_s[tid];
     float best = __builtin_inff(), s_winner = 0.f, best_e = __builtin_inff();
