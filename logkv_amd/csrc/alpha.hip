@@ -66,17 +66,31 @@ __device__ __forceinline__ float span_component(const Rows2& src, int b, int g, 
 #pragma unroll
       for (int j = 0; j < NJ; ++j) xb[t][j] = feat_or_zero(row, l + j * kWave, D);
     }
+    // Per-row canonical sums of squares, four rows per fold; the rows' mean
+    // squares (sum / D) as one lane-parallel division, added in span order.
+    float ss[kTokBatch];
+#pragma unroll
+    for (int t = 0; t < kTokBatch; t += 4) {
+      float part[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        part[k] = xb[t + k][0] * xb[t + k][0];
+#pragma unroll
+        for (int j = 1; j < NJ; ++j) part[k] = part[k] + xb[t + k][j] * xb[t + k][j];
+      }
+      wave_sum4(part[0], part[1], part[2], part[3], ss[t], ss[t + 1], ss[t + 2], ss[t + 3]);
+    }
+    float num = 0.f;
+#pragma unroll
+    for (int t = 0; t < kTokBatch; ++t) num = l == t ? ss[t] : num;
+    const float msl = num / d_f;
 #pragma unroll
     for (int t = 0; t < kTokBatch; ++t) {
       const int i = i0 + t;
       if (i >= n) break;
-      float sq[NJ];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        sq[j] = xb[t][j] * xb[t][j];
-        acc[j] = i == 0 ? xb[t][j] : acc[j] + xb[t][j];
-      }
-      const float ms = canon_sum<NJ>(sq) / d_f;
+      for (int j = 0; j < NJ; ++j) acc[j] = i == 0 ? xb[t][j] : acc[j] + xb[t][j];
+      const float ms = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(msl), t));
       e = i == 0 ? ms : e + ms;
     }
   }
@@ -101,7 +115,6 @@ struct SpanSlots {
 };
 
 __device__ __forceinline__ bool span_live(const logkv_span_args& a, const SpanSlots& sl, int s) {
-  if (sl.row_count) return s % sl.slots < sl.row_count[s / sl.slots];
   return !a.n_spans_dev || s < *a.n_spans_dev;
 }
 
@@ -189,6 +202,12 @@ template <int NJ>
 __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, SpanSlots sl,
                                                                    float* __restrict__ out) {
   __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
+  if (sl.row_count) {   // grid (x, batch row): row b's candidates x, x + gridDim.x, ...
+    const int b = blockIdx.y, n = sl.row_count[b];
+    for (int i = blockIdx.x; i < n; i += gridDim.x)
+      score_span<NJ>(a, b * sl.slots + i, part_k, part_v, q_s, out);
+    return;
+  }
   for (int s = blockIdx.x; s < a.n_spans; s += gridDim.x) {
     if (!span_live(a, sl, s)) continue;
     score_span<NJ>(a, s, part_k, part_v, q_s, out);
@@ -940,9 +959,14 @@ __global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_sele
 
 constexpr int kScoreBlocks = 2048;   // most blocks of a score launch (each strides over span slots)
 
-int launch_score_slots(const logkv_span_args& a, const SpanSlots& sl, float* out, hipStream_t stream) {
+int launch_score_slots(const logkv_span_args& a, const SpanSlots& sl, float* out, int n_rows, hipStream_t stream) {
   if (a.n_spans <= 0) return LOGKV_OK;
-  const dim3 grid(static_cast<unsigned>(std::min(a.n_spans, kScoreBlocks)));
+  // Per-row slots: kScoreBlocks spread over the rows, at least 32 per row and
+  // no more than a row's slots.
+  const dim3 grid = sl.row_count
+                        ? dim3(static_cast<unsigned>(std::min(sl.slots, std::max(32, kScoreBlocks / n_rows))),
+                               static_cast<unsigned>(n_rows))
+                        : dim3(static_cast<unsigned>(std::min(a.n_spans, kScoreBlocks)));
   if (a.dk <= 2 * kWave && a.dv <= 2 * kWave)
     hipLaunchKernelGGL(score_kernel<2>, grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
   else
@@ -951,7 +975,7 @@ int launch_score_slots(const logkv_span_args& a, const SpanSlots& sl, float* out
 }
 
 int launch_score(const logkv_span_args& a, float* out, hipStream_t stream) {
-  return launch_score_slots(a, SpanSlots{nullptr, 0}, out, stream);
+  return launch_score_slots(a, SpanSlots{nullptr, 0}, out, 1, stream);
 }
 
 int64_t select_workspace_bytes(const logkv_alpha_select_args& a) {
@@ -989,7 +1013,8 @@ int launch_select(const logkv_alpha_select_args& a, void* ws, hipStream_t stream
   sa.span_rows = w.cand_row;
   sa.n_spans = static_cast<int32_t>(C);
   sa.n_spans_dev = nullptr;
-  int rc = launch_score_slots(sa, SpanSlots{w.row_count, select_row_slots(a.budget, a.tokens)}, w.scores, stream);
+  int rc = launch_score_slots(sa, SpanSlots{w.row_count, select_row_slots(a.budget, a.tokens)}, w.scores, a.n_batch,
+                              stream);
   if (rc) return rc;
   const int maxc = a.budget + a.tokens + 1;
   int width = 1;
