@@ -356,12 +356,6 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wave_tmp, int& total)
   return before + incl - v;
 }
 
-__device__ __forceinline__ double readlane_f64(double x, int lane) {
-  const long long bits = __double_as_longlong(x);
-  const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
-  const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
-  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
-}
 
 // One block per batch row (litgpt/alpha_log_kv.py:16-53, :84-122). Closed old
 // spans become candidates in order; the last open old span is pending: closed

@@ -139,6 +139,24 @@ __device__ __forceinline__ void wave_sum4(float a, float b, float c, float d, fl
   sd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 48));
 }
 
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+  const long long bits = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+// a / b rounded to float exactly as IEEE float division, from b's double
+// reciprocal r = 1 / (double)b: the double product a * r is within 2^-52
+// (relative) of a / b, while a quotient of two floats that is not itself a
+// float lies at least 2^-50 (relative) from every float rounding boundary,
+// normal or subnormal; so rounding the product to float gives the correctly
+// rounded quotient (and an exact quotient stays exact). Three instructions
+// per quotient once r is known.
+__device__ __forceinline__ float div_by_rcp(float a, double r) {
+  return static_cast<float>(static_cast<double>(a) * r);
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 

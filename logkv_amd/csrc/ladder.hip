@@ -313,18 +313,48 @@ __device__ __forceinline__ float lane_sq(const float (&x)[NJ]) {
   return s;
 }
 
+// Side mass ((w0 + w1) + w2) + w3 (zero weights outside the side).
+__device__ __forceinline__ float side_mass(const float* wt) { return ((wt[0] + wt[1]) + wt[2]) + wt[3]; }
+
+// Weighted mean of a side: sum_i x_i w_i (row order) / max(mass, 1e-12), the
+// division through the side's double reciprocal `rcp` (div_by_rcp).
 template <int NJ>
-__device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* wt, float* mean, float& mass) {
-  mass = ((wt[0] + wt[1]) + wt[2]) + wt[3];
-  const float den = fmaxf(mass, 1e-12f);
+__device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* wt, double rcp, float* mean) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     float acc = x[0][j] * wt[0];
     acc = acc + x[1][j] * wt[1];
     acc = acc + x[2][j] * wt[2];
     acc = acc + x[3][j] * wt[3];
-    mean[j] = acc / den;
+    mean[j] = div_by_rcp(acc, rcp);
   }
+}
+
+// Split weights of cut c: left rows i < c, right rows i >= c.
+__device__ __forceinline__ void cut_weights(const float* wr, int c, float* wl, float* wrt) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wl[i] = i < c ? wr[i] : 0.f;
+    wrt[i] = i < c ? 0.f : wr[i];
+  }
+}
+
+// Double reciprocals of max(mass, 1e-12) of the six sides of the cuts
+// (2, 1, 3), left then right, from one lane-parallel division.
+__device__ __forceinline__ void side_rcps(const float* wr, double* rcp) {
+  const int l = lane_id();
+  float mine = 1.f;
+#pragma unroll
+  for (int opt = 0; opt < 3; ++opt) {
+    const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+    float wl[4], wrt[4];
+    cut_weights(wr, c, wl, wrt);
+    mine = l == 2 * opt ? side_mass(wl) : mine;
+    mine = l == 2 * opt + 1 ? side_mass(wrt) : mine;
+  }
+  const double r = 1.0 / static_cast<double>(fmaxf(mine, 1e-12f));
+#pragma unroll
+  for (int k = 0; k < 6; ++k) rcp[k] = readlane_f64(r, k);
 }
 
 // One component's row energies sum_d x_id^2 -> e = sum_i sq_i w_i (row order),
@@ -333,8 +363,8 @@ __device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* 
 // their distance to the other side's mean). Feature sums are canonical; the
 // four rows of a cut are folded together (wave_sum4).
 template <int NJ>
-__device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], const float* wr, float& e,
-                                                      float* loss) {
+__device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], const float* wr, const double* rcp,
+                                                      float& e, float* loss) {
   float sq[4];
   wave_sum4(lane_sq<NJ>(x[0]), lane_sq<NJ>(x[1]), lane_sq<NJ>(x[2]), lane_sq<NJ>(x[3]), sq[0], sq[1], sq[2], sq[3]);
   e = sq[0] * wr[0];
@@ -343,14 +373,10 @@ __device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], c
 #pragma unroll
   for (int opt = 0; opt < 3; ++opt) {
     const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
-    float wl[4], wrt[4], ml[NJ], mr[NJ], mass;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      wl[i] = i < c ? wr[i] : 0.f;
-      wrt[i] = i < c ? 0.f : wr[i];
-    }
-    side_mean<NJ>(x, wl, ml, mass);
-    side_mean<NJ>(x, wrt, mr, mass);
+    float wl[4], wrt[4], ml[NJ], mr[NJ];
+    cut_weights(wr, c, wl, wrt);
+    side_mean<NJ>(x, wl, rcp[2 * opt], ml);
+    side_mean<NJ>(x, wrt, rcp[2 * opt + 1], mr);
     float t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -377,12 +403,13 @@ __device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], c
 // max(e / total, 1e-12); the smallest cost wins (first on ties). The 2 + 12
 // uniform divisions run as two lane-parallel divisions.
 template <int NJ>
-__device__ __forceinline__ int beta_cut(const float (&xk)[4][NJ], const float (&xv)[4][NJ], const float* wr) {
+__device__ __forceinline__ int beta_cut(const float (&xk)[4][NJ], const float (&xv)[4][NJ], const float* wr,
+                                        const double* rcp) {
   const int l = lane_id();
   const float total = fmaxf(((wr[0] + wr[1]) + wr[2]) + wr[3], 1e-12f);
   float ek, ev, lk[6], lv[6];
-  beta_component_losses<NJ>(xk, wr, ek, lk);
-  beta_component_losses<NJ>(xv, wr, ev, lv);
+  beta_component_losses<NJ>(xk, wr, rcp, ek, lk);
+  beta_component_losses<NJ>(xv, wr, rcp, ev, lv);
   const float en = (l == 0 ? ek : ev) / total;
   const float energy_k = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(en), 0)), 1e-12f);
   const float energy_v = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(en), 1)), 1e-12f);
@@ -576,17 +603,25 @@ __device__ __forceinline__ void beta_group(const PoolT<KIND>& pool, const Soa& o
       xv[i][j] = valid ? b : 0.f;
     }
   }
-  const int cut = width == 4 ? beta_cut<NJ>(xk, xv, wr) : 1;
+  // Side reciprocals of the cuts (2, 1, 3); a 2-row tail group (rows 2, 3 of
+  // weight 0) is the left side of cut 2.
+  double rcp[6];
+  side_rcps(wr, rcp);
+  const int cut = width == 4 ? beta_cut<NJ>(xk, xv, wr, rcp) : 2;
+  const int opt = cut == 2 ? 0 : (cut == 1 ? 1 : 2);
   const int dest = start / 2;
   for (int side = 0; side < (width == 4 ? 2 : 1); ++side) {
-    unsigned member;
-    if (width == 2) member = 0x3u;
-    else member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
-    float wt[4], mk[NJ], mv[NJ], mass;
+    const unsigned member = side == 0 ? ((1u << cut) - 1u) : (0xfu & ~((1u << cut) - 1u));
+    float wt[4], mk[NJ], mv[NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
-    side_mean<NJ>(xk, wt, mk, mass);
-    side_mean<NJ>(xv, wt, mv, mass);
+    const float mass = side_mass(wt);
+    // Selected without indexing the array by a run-time value (which would place it in scratch).
+    const double left = opt == 0 ? rcp[0] : (opt == 1 ? rcp[2] : rcp[4]);
+    const double right = opt == 0 ? rcp[1] : (opt == 1 ? rcp[3] : rcp[5]);
+    const double side_rcp = side == 0 ? left : right;
+    side_mean<NJ>(xk, wt, side_rcp, mk);
+    side_mean<NJ>(xv, wt, side_rcp, mv);
     const int64_t o = dest + side;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {

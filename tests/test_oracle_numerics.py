@@ -64,3 +64,28 @@ def test_seqsum_is_left_to_right():
     t = np.asarray([1e8, 1.0, -1e8, 1.0], np.float32)
     assert seqsum(t) == np.float32(np.float32(np.float32(1e8 + 1.0) - 1e8) + 1.0)
     assert seqsum(np.zeros((0, 3), np.float32)).tolist() == [0.0, 0.0, 0.0]
+
+
+def test_division_through_double_reciprocal_is_ieee_float_division():
+    """The kernels divide by a weight mass as float(double(a) * (1 / double(b))):
+    the double product is within 2^-52 of a / b and a float quotient that is not
+    a float lies at least 2^-50 from any rounding boundary, so the result must
+    equal IEEE float division. Checked here on random pairs over the whole
+    exponent range, subnormal numerators and quotients, integer masses (the
+    kernels' denominators) and exact quotients."""
+    rng = np.random.default_rng(7)
+    n = 2_000_000
+    bits = rng.integers(0, 0x7F800000, n, dtype=np.int64).astype(np.uint32)
+    a = bits.view(np.float32) * np.where(rng.random(n) < 0.5, -1, 1).astype(np.float32)
+    b = rng.integers(1, 0x7F800000, n, dtype=np.int64).astype(np.uint32).view(np.float32)
+    masses = rng.integers(1, 1 << 20, n).astype(np.float32)
+    small = (rng.standard_normal(n) * 1e-40).astype(np.float32)          # subnormal numerators
+    exact = (rng.integers(-1000, 1000, n) * masses).astype(np.float32)   # exact quotients
+    for num, den in ((a, b), (a, masses), (small, masses), (exact, masses),
+                     (rng.standard_normal(n).astype(np.float32), np.float32(1e-12) + masses * 0)):
+        with np.errstate(over="ignore", under="ignore", invalid="ignore", divide="ignore"):
+            want = num / den
+            got = (num.astype(np.float64) * (1.0 / den.astype(np.float64))).astype(np.float32)
+        same = (got == want) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), (num[~same][:5], den[~same][:5])
+        assert (np.signbit(got) == np.signbit(want))[~np.isnan(want)].all()
