@@ -266,6 +266,7 @@ __device__ __forceinline__ void move_rows(const PoolT<KIND>& pool, int p0, int d
 }
 
 constexpr int kBatch = 4;   // rows per thread whose loads are issued before any of their stores
+constexpr int kCompactChunks = 8;   // 512-row chunks of decisions prefetched by the prepare compaction
 
 // Staged rows [s0, s0 + n) -> slots [d0, d0 + n); the staged rows never alias the level.
 template <int KIND>
@@ -769,27 +770,42 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_G int8_t* as = gp(ws.assign + static_cast<int64_t>(lane_ix) * r.tokens);
   const LOGKV_G int32_t* ord = gp(ws.order + static_cast<int64_t>(b) * r.tokens);
 
-  // 1. This cluster's rows in position order (stable compaction).
+  // 1. This cluster's rows in position order (stable compaction). The
+  // decisions and order entries of kCompactChunks chunks are loaded (clamped,
+  // unconditionally) before the chunks are scanned.
   if (threadIdx.x == 0) m_s = 0;
   __syncthreads();
-  for (int s0 = 0; s0 < n; s0 += kThreads) {
-    const int s = s0 + threadIdx.x;
-    const bool mine = s < n && as[s] == cc;
-    const uint64_t ballot = __ballot(mine);
-    const int l = lane_id(), w = wave_id();
-    const int before = __popcll(ballot & ((l == 0) ? 0ull : (~0ull >> (kWave - l))));
-    if (l == 0) wave_sum[w] = __popcll(ballot);
-    __syncthreads();
-    int base = m_s;
-    for (int q = 0; q < w; ++q) base += wave_sum[q];
-    if (mine) tok[base + before] = static_cast<uint16_t>(ord[s]);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int add = 0;
-      for (int q = 0; q < kThreads / kWave; ++q) add += wave_sum[q];
-      m_s = m_s + add;
+  for (int g0 = 0; g0 < n; g0 += kCompactChunks * kThreads) {
+    int8_t a_q[kCompactChunks];
+    int32_t o_q[kCompactChunks];
+#pragma unroll
+    for (int q = 0; q < kCompactChunks; ++q) {
+      const int s = min(g0 + q * kThreads + static_cast<int>(threadIdx.x), n - 1);
+      a_q[q] = as[s];
+      o_q[q] = ord[s];
     }
-    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kCompactChunks; ++q) {
+      const int s0 = g0 + q * kThreads;
+      if (s0 >= n) break;
+      const int s = s0 + threadIdx.x;
+      const bool mine = s < n && a_q[q] == cc;
+      const uint64_t ballot = __ballot(mine);
+      const int l = lane_id(), w = wave_id();
+      const int before = __popcll(ballot & ((l == 0) ? 0ull : (~0ull >> (kWave - l))));
+      if (l == 0) wave_sum[w] = __popcll(ballot);
+      __syncthreads();
+      int base = m_s;
+      for (int q2 = 0; q2 < w; ++q2) base += wave_sum[q2];
+      if (mine) tok[base + before] = static_cast<uint16_t>(o_q[q]);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int add = 0;
+        for (int q2 = 0; q2 < kThreads / kWave; ++q2) add += wave_sum[q2];
+        m_s = m_s + add;
+      }
+      __syncthreads();
+    }
   }
   const int m = m_s;
   if (m == 0) {
@@ -829,10 +845,23 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       float acc = 0.f;
       for (int c0 = first; c0 < m; c0 += kCenterRows) {
         const int rows = min(kCenterRows, m - c0);
-        for (int i = threadIdx.x; i < rows * ku; i += kThreads) {
-          const int rr = i / ku, u = i - rr * ku;
-          *reinterpret_cast<uint2*>(stage + rr * dk + 4 * u) =
-              *(const LOGKV_G uint2*)(kb + static_cast<int64_t>(tok[c0 + rr]) * r.k_st + 4 * u);
+        // kBatch units per thread loaded (clamped, unconditionally) before any store.
+        for (int i0 = threadIdx.x; i0 < rows * ku; i0 += kBatch * kThreads) {
+          uint2 x[kBatch];
+#pragma unroll
+          for (int q = 0; q < kBatch; ++q) {
+            const int i = min(i0 + q * kThreads, rows * ku - 1);
+            const int rr = i / ku, u = i - rr * ku;
+            x[q] = *(const LOGKV_G uint2*)(kb + static_cast<int64_t>(tok[c0 + rr]) * r.k_st + 4 * u);
+          }
+#pragma unroll
+          for (int q = 0; q < kBatch; ++q) {
+            const int i = i0 + q * kThreads;
+            if (i < rows * ku) {
+              const int rr = i / ku, u = i - rr * ku;
+              *reinterpret_cast<uint2*>(stage + rr * dk + 4 * u) = x[q];
+            }
+          }
         }
         __syncthreads();
         if (d < dk) {
