@@ -497,7 +497,7 @@ __device__ __forceinline__ int64_t shfl_xor64(int64_t x, int mask) {
 constexpr int kFoldAhead = 8;   // rows of the top fold in flight
 
 template <int KIND>
-__device__ __forceinline__ void fold_top(const PoolT<KIND>& pool, int mr) {
+__device__ __forceinline__ void fold_top(const PoolT<KIND> pool, int mr) {
   const Ladder& L = pool.L;
   const int B = L.B, ku = L.dk / 4, units = (L.dk + L.dv) / 4;   // units <= 2 * kWave
   const int64_t base = pool.base;
@@ -666,8 +666,8 @@ __host__ __device__ inline int carries_of(int cnt, int m, int B, bool top) {
 }
 
 // Slot writes of one level step; returns the level's new count.
-template <int KIND>
-__device__ __forceinline__ int level_finish(const Ladder& L, int ell, int cnt, const Src& cur, int m, bool top) {
+template <int KIND, bool TOP>
+__device__ __forceinline__ int level_finish(const Ladder& L, int ell, int cnt, const Src& cur, int m) {
   const int B = L.B;
   const int64_t base = static_cast<int64_t>(ell) * B;
   const int n_pool = cnt + m;
@@ -677,7 +677,7 @@ __device__ __forceinline__ int level_finish(const Ladder& L, int ell, int cnt, c
     return n_pool;
   }
   const int mr = n_pool - B;
-  if (top) {
+  if (TOP) {
     fold_top<KIND>(pool, mr);
     return B;
   }
@@ -1178,20 +1178,23 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
 // Slot writes of every level (block (ladder, level)): fill, move and clear, or
 // top fold. A level's writes read only its own stored slots and its staged
 // rows (the previous level's carries), so the levels run side by side.
+// TOP = false: levels 0..L-2 (grid y = L - 1); TOP = true: the top level
+// (grid y = 1), whose saturated fold keeps its registers out of the other
+// levels' launch.
+template <bool TOP>
 __global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs r, Workspace ws) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  const int ladder = blockIdx.x, ell = blockIdx.y;
+  const int ladder = blockIdx.x, ell = TOP ? c.levels - 1 : static_cast<int>(blockIdx.y);
   const LadderPlan* pl = ws.plans + ladder;
   if (!pl->active) return;
   const int cnt = pl->cnt[ell], m = pl->m[ell];
   if (m == 0) return;
   const Ladder lad = ladder_of(c, ladder);
-  const bool top = ell == c.levels - 1;
   int n;
   if (ell == 0 && pl->kind0 == 0)
-    n = level_finish<0>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m, top);
+    n = level_finish<0, TOP>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m);
   else
-    n = level_finish<1>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m, top);
+    n = level_finish<1, TOP>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m);
   if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * c.levels + ell] = static_cast<int16_t>(n);
 }
 
@@ -1224,7 +1227,9 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
         hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
     }
   }
-  hipLaunchKernelGGL(finish_kernel, dim3(ladders, c.levels), dim3(kThreads), tok_bytes, stream, c, r, ws);
+  if (c.levels > 1)
+    hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, c.levels - 1), dim3(kThreads), tok_bytes, stream, c, r, ws);
+  hipLaunchKernelGGL(finish_kernel<true>, dim3(ladders, 1), dim3(kThreads), tok_bytes, stream, c, r, ws);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
