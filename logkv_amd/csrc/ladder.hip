@@ -317,16 +317,33 @@ __device__ __forceinline__ float lane_sq(const float (&x)[NJ]) {
 // Side mass ((w0 + w1) + w2) + w3 (zero weights outside the side).
 __device__ __forceinline__ float side_mass(const float* wt) { return ((wt[0] + wt[1]) + wt[2]) + wt[3]; }
 
-// Weighted mean of a side: sum_i x_i w_i (row order) / max(mass, 1e-12), the
-// division through the side's double reciprocal `rcp` (div_by_rcp).
+// Products of one component's rows with their weights (p = x w) and with a
+// zero weight (z = x * 0, which carries x's sign and turns inf / NaN into NaN).
 template <int NJ>
-__device__ __forceinline__ void side_mean(const float (&x)[4][NJ], const float* wt, double rcp, float* mean) {
+struct RowProducts {
+  float p[4][NJ], z[4][NJ];
+  __device__ __forceinline__ RowProducts(const float (&x)[4][NJ], const float* w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        p[i][j] = x[i][j] * w[i];
+        z[i][j] = x[i][j] * 0.f;
+      }
+  }
+};
+
+// Weighted mean of a side: sum_i x_i w_i (row order, rows outside the side
+// with weight 0) / max(mass, 1e-12), the division through the side's double
+// reciprocal `rcp` (div_by_rcp).
+template <int NJ>
+__device__ __forceinline__ void side_mean(const RowProducts<NJ>& pr, unsigned member, double rcp, float* mean) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    float acc = x[0][j] * wt[0];
-    acc = acc + x[1][j] * wt[1];
-    acc = acc + x[2][j] * wt[2];
-    acc = acc + x[3][j] * wt[3];
+    float acc = (member & 1u) ? pr.p[0][j] : pr.z[0][j];
+    acc = acc + ((member & 2u) ? pr.p[1][j] : pr.z[1][j]);
+    acc = acc + ((member & 4u) ? pr.p[2][j] : pr.z[2][j]);
+    acc = acc + ((member & 8u) ? pr.p[3][j] : pr.z[3][j]);
     mean[j] = div_by_rcp(acc, rcp);
   }
 }
@@ -366,6 +383,7 @@ __device__ __forceinline__ void side_rcps(const float* wr, double* rcp) {
 template <int NJ>
 __device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], const float* wr, const double* rcp,
                                                       float& e, float* loss) {
+  const RowProducts<NJ> pr(x, wr);
   float sq[4];
   wave_sum4(lane_sq<NJ>(x[0]), lane_sq<NJ>(x[1]), lane_sq<NJ>(x[2]), lane_sq<NJ>(x[3]), sq[0], sq[1], sq[2], sq[3]);
   e = sq[0] * wr[0];
@@ -376,8 +394,9 @@ __device__ __forceinline__ void beta_component_losses(const float (&x)[4][NJ], c
     const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
     float wl[4], wrt[4], ml[NJ], mr[NJ];
     cut_weights(wr, c, wl, wrt);
-    side_mean<NJ>(x, wl, rcp[2 * opt], ml);
-    side_mean<NJ>(x, wrt, rcp[2 * opt + 1], mr);
+    const unsigned left_rows = (1u << c) - 1u;
+    side_mean<NJ>(pr, left_rows, rcp[2 * opt], ml);
+    side_mean<NJ>(pr, 0xfu & ~left_rows, rcp[2 * opt + 1], mr);
     float t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -617,12 +636,13 @@ __device__ __forceinline__ void beta_group(const PoolT<KIND>& pool, const Soa& o
 #pragma unroll
     for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? wr[i] : 0.f;
     const float mass = side_mass(wt);
+    const RowProducts<NJ> pk(xk, wr), pv(xv, wr);
     // Selected without indexing the array by a run-time value (which would place it in scratch).
     const double left = opt == 0 ? rcp[0] : (opt == 1 ? rcp[2] : rcp[4]);
     const double right = opt == 0 ? rcp[1] : (opt == 1 ? rcp[3] : rcp[5]);
     const double side_rcp = side == 0 ? left : right;
-    side_mean<NJ>(xk, wt, side_rcp, mk);
-    side_mean<NJ>(xv, wt, side_rcp, mv);
+    side_mean<NJ>(pk, member, side_rcp, mk);
+    side_mean<NJ>(pv, member, side_rcp, mv);
     const int64_t o = dest + side;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
