@@ -123,8 +123,11 @@ __host__ __device__ inline size_t attach_shmem(int K) {
          static_cast<size_t>(R + K) * 4 + static_cast<size_t>(R) * 12 + 64;
 }
 
+constexpr int kAttachMaxThreads = 512;
+constexpr int kStageBatch = 8;   // staged values per thread whose loads are issued before their LDS stores
+
 template <int NJ>
-__global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+__global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
                                                      const int32_t* __restrict__ order,
                                                      int8_t* __restrict__ assign, float* __restrict__ s_win) {
   constexpr int R = attach_tile<NJ>(), LS = leaf_stride<NJ>();
@@ -147,9 +150,19 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
   const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
   // Centers and rows into LDS (features past D are zero).
   const LOGKV_G float* mu = gp(c.centroid) + static_cast<int64_t>(lane_ix) * K * D;
-  for (int i = tid; i < K * kWave * NJ; i += nthr) {
-    const int cc = i / (kWave * NJ), f = i % (kWave * NJ), d = (f % kWave) + kWave * (f / kWave);
-    mu_l[cc * LS + (f % kWave) * NJ + f / kWave] = feat_or_zero(mu + cc * D, d, D);
+  constexpr int F = kWave * NJ;   // staged features per row (zero past D)
+  for (int i0 = tid; i0 < K * F; i0 += kStageBatch * nthr) {
+    float v[kStageBatch];
+#pragma unroll
+    for (int q = 0; q < kStageBatch; ++q) {
+      const int i = min(i0 + q * nthr, K * F - 1), cc = i / F, f = i % F;
+      v[q] = feat_or_zero(mu + cc * D, f, D);
+    }
+#pragma unroll
+    for (int q = 0; q < kStageBatch; ++q) {
+      const int i = i0 + q * nthr;
+      if (i < K * F) mu_l[(i / F) * LS + ((i % F) % kWave) * NJ + (i % F) / kWave] = v[q];
+    }
   }
   for (int i = tid; i < rows; i += nthr) {
     const int t = order[static_cast<int64_t>(b) * r.tokens + tile0 + i];
@@ -167,10 +180,18 @@ __global__ __launch_bounds__(256) void attach_kernel(LadderArgs c, RowsArgs r, R
   }
   __syncthreads();
   const LOGKV_G uint16_t* kbase = gp(r.k + b * r.k_sb + g * r.k_sg);
-  for (int i = tid; i < rows * kWave * NJ; i += nthr) {
-    const int rr = i / (kWave * NJ), f = i % (kWave * NJ);
-    const int d = (f % kWave) + kWave * (f / kWave);
-    x_l[rr * LS + (f % kWave) * NJ + f / kWave] = feat_or_zero(kbase + static_cast<int64_t>(t_s[rr]) * r.k_st, d, D);
+  for (int i0 = tid; i0 < rows * F; i0 += kStageBatch * nthr) {
+    float v[kStageBatch];
+#pragma unroll
+    for (int q = 0; q < kStageBatch; ++q) {
+      const int i = min(i0 + q * nthr, rows * F - 1), rr = i / F, f = i % F;
+      v[q] = feat_or_zero(kbase + static_cast<int64_t>(t_s[rr]) * r.k_st, f, D);
+    }
+#pragma unroll
+    for (int q = 0; q < kStageBatch; ++q) {
+      const int i = i0 + q * nthr;
+      if (i < rows * F) x_l[(i / F) * LS + ((i % F) % kWave) * NJ + (i % F) / kWave] = v[q];
+    }
   }
   __syncthreads();
   if (tid < rows) xx_s[tid] = canon_sq<NJ, 6, 0>(x_l + tid * LS);
@@ -414,7 +435,9 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
     const int nj = (c.dk + kWave - 1) / kWave;
     auto attach = [&](auto kernel, int tile, size_t shmem) {
       if (!allow_dynamic_lds(reinterpret_cast<const void*>(kernel), shmem)) return false;
-      hipLaunchKernelGGL(kernel, dim3((r.tokens + tile - 1) / tile, lanes), dim3(256), shmem, stream, c, r, p,
+      // One thread per (row, cluster) pair of a tile where it fits.
+      const int threads = std::min(kAttachMaxThreads, std::max(256, (tile * c.k_max + kWave - 1) / kWave * kWave));
+      hipLaunchKernelGGL(kernel, dim3((r.tokens + tile - 1) / tile, lanes), dim3(threads), shmem, stream, c, r, p,
                          ws.order, ws.assign, ws.s_win);
       return true;
     };
