@@ -100,6 +100,57 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
                       const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
                       const int8_t* assign, const int32_t* order, void* stream);
 
+/* Route op-log of a cache (litgpt/log_kv_cache.py:2006-2096): per lane (batch
+ * row, KV group) int32 rows (op, cluster, arg, position) at rows[lane,
+ * 0 .. lengths[lane]), op codes as the reference's (litgpt/log_kv_cache.py:
+ * 90-94). lengths may pass capacity: rows past it are counted, not written
+ * (the reference's "op_log overflow"; the caller reports it). */
+typedef struct logkv_op_log_view {
+  int32_t* rows;        /* [n_batch, G, capacity, 4] */
+  int32_t* lengths;     /* [n_batch, G] */
+  int64_t capacity;
+} logkv_op_log_view;
+
+enum {
+  LOGKV_OP_NEW_CLUSTER = 0, LOGKV_OP_NEW_SEGMENT = 1, LOGKV_OP_JOIN = 2, LOGKV_OP_WARD_MERGE = 3,
+  LOGKV_OP_PAD_INSERT = 4
+};
+
+/* Appends the op rows of the flush that logkv_route_commit / logkv_commit_only
+ * just committed with the same workspace and rows: per lane, NEW_CLUSTER
+ * (cluster, 0, earliest position) for every cluster it opened (ascending
+ * cluster), then JOIN (cluster, 0, position) for the other rows of ordinary
+ * joins (cluster ascending, rows in position order), then the same for
+ * delayed-archive joins. Replaces the recording of _semantic_new_clusters,
+ * _semantic_commit_joins_unsegmented and _alpha_commit_joins
+ * (litgpt/log_kv_cache.py:2286-2297, :4153-4166, :3782-3788) with
+ * _record_ops / _flush_recorded_ops (litgpt/log_kv_cache.py:2043-2096). */
+int logkv_record_ops(const logkv_ladder_view* cache, const logkv_rows_view* rows, void* workspace,
+                     int64_t workspace_bytes, const logkv_op_log_view* log, void* stream);
+
+/* Replay status bits (logkv_replay_commit writes their OR to *status). */
+enum {
+  LOGKV_REPLAY_BAD_OP = 1,             /* not NEW_CLUSTER / JOIN of segment 0, or cluster out of range */
+  LOGKV_REPLAY_UNKNOWN_POSITION = 2,   /* a row's position is not a row of this flush */
+  LOGKV_REPLAY_DUPLICATE_POSITION = 4, /* two flush rows share a position */
+  LOGKV_REPLAY_SHORT_LOG = 8,          /* fewer than the flush's rows logged past the cursor */
+  LOGKV_REPLAY_UNCONSUMED = 16,        /* a flush row is named by no log row (another by two) */
+  LOGKV_REPLAY_BAD_CLUSTER = 32,       /* NEW_CLUSTER of a live cluster, or JOIN of a dead one */
+  LOGKV_REPLAY_BAD_ORDER = 64          /* a cluster's rows are not in increasing position order */
+};
+
+/* Re-applies the logged decisions of one flush without routing: per lane, the
+ * rows [cursor, cursor + valid rows) of the log name each flush row's cluster
+ * (by position), then the commit of logkv_route_commit runs on them. The
+ * checks above are made on the device; on any failure *status (device int32)
+ * gets the bits and no cache field is written. Replaces the replay branch of
+ * _route_and_flush_batch with _semantic_build_replay_plan and
+ * _semantic_commit_runs (litgpt/log_kv_cache.py:5067-5114, :4856-4926,
+ * :4178-4223) for logs of attach-routed flushes. */
+int logkv_replay_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                        const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                        const logkv_op_log_view* log, int64_t cursor, int32_t* status, void* stream);
+
 /* Candidate span table over the virtual rows [old exact pool (old_width rows) |
  * flush]: pool_* / flush_* are [n_batch, G, rows, d] bf16 with element strides;
  * span i covers tokens[span_offsets[i] .. span_offsets[i+1]) of batch row

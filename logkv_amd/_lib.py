@@ -115,6 +115,25 @@ class AttentionArgs(C.Structure):
     ]
 
 
+class OpLogView(C.Structure):
+    _fields_ = [("rows", _p), ("lengths", _p), ("capacity", _i64)]
+
+
+# Op codes of the route op-log (litgpt/log_kv_cache.py:90-94).
+OP_NEW_CLUSTER, OP_NEW_SEGMENT, OP_JOIN, OP_WARD_MERGE, OP_PAD_INSERT = 0, 1, 2, 3, 4
+
+# Replay status bits of logkv_replay_commit -> what failed.
+REPLAY_ERRORS = {
+    1: "a log row is not a NEW_CLUSTER / JOIN of segment 0 of a cluster in range (segment pads and Ward merges "
+       "are not recorded by the attach route)",
+    2: "a logged position is not in the current flush positions",
+    4: "the current flush positions contain duplicate token ids",
+    8: "the log holds fewer rows than the flush has tokens",
+    16: "a flush token is not consumed exactly once by the log",
+    32: "a NEW_CLUSTER names a live cluster or a JOIN names a dead one",
+    64: "a cluster's logged rows are not in increasing position order",
+}
+
 # Exported symbol -> (restype, argtypes); the tests check this table against the header.
 SIGNATURES = {
     "logkv_last_error": (C.c_char_p, []),
@@ -125,6 +144,9 @@ SIGNATURES = {
                                   _p, _i64, _p, _p, _p]),
     "logkv_commit_only": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
                                  _p, _i64, _p, _p, _p]),
+    "logkv_record_ops": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), _p, _i64, C.POINTER(OpLogView), _p]),
+    "logkv_replay_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
+                                   _p, _i64, C.POINTER(OpLogView), _i64, _p, _p]),
     "logkv_score_spans": (_i32, [C.POINTER(SpanArgs), _p, _p]),
     "logkv_alpha_partition": (_i32, [C.POINTER(PartitionArgs), _p]),
     "logkv_alpha_select_workspace_bytes": (_i64, [C.POINTER(AlphaSelectArgs)]),

@@ -344,7 +344,7 @@ def _alpha_call(cache, T: int, dtype) -> _AlphaCall:
 
 
 @torch.no_grad()
-def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
+def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=False):
     """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003), all on the device.
 
     The span selection (candidates of ``[exact pool | flush]``, scores, bounded
@@ -355,7 +355,9 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
     boundary flags travel from the host, and not even they when given as a
     device tensor. Row indices address ``[pool (P rows) | flush]``;
     ``positions_host`` is not needed. The argument structs and the kept /
-    archived row buffers are built once per flush length and reused.
+    archived row buffers are built once per flush length and reused. With
+    ``record`` the archived rows' route decisions are appended to the op-log
+    (litgpt/log_kv_cache.py:3782-3788).
     """
     if span_ends is None:
         raise ValueError("AlphaLogKV requires natural span boundaries")
@@ -386,4 +388,4 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends):
     cache._alpha_parity ^= 1
     # Inputs that may be temporaries stay referenced until the next flush on this stream.
     cache._alpha_keep_alive = (ends, positions)
-    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"])
+    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], record=record)

@@ -169,8 +169,56 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
                  const_cast<int32_t*>(order), ws);
   if (rc) return rc;
   if (!rows->tokens) return LOGKV_OK;
-  rc = logkv::launch_commit(*cache, *rows, *params, ws, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The commit reads the alive flags as they were before it (decisions made elsewhere).
+  rc = logkv::launch_snapshot(*cache, ws, s);
+  if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
   if (rc) return fail(rc, "commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+namespace {
+
+int check_log(const logkv_ladder_view* c, const logkv_op_log_view* log) {
+  if (!log || !log->rows || !log->lengths) return fail(LOGKV_EINVAL, "op-log view or its buffers are NULL");
+  if (log->capacity < 1) return fail(LOGKV_EINVAL, "op-log capacity must be positive");
+  if (reinterpret_cast<uintptr_t>(log->rows) % 16) return fail(LOGKV_EINVAL, "op-log rows must be 16-byte aligned");
+  (void)c;
+  return LOGKV_OK;
+}
+
+}  // namespace
+
+int logkv_record_ops(const logkv_ladder_view* cache, const logkv_rows_view* rows, void* workspace,
+                     int64_t workspace_bytes, const logkv_op_log_view* log, void* stream) {
+  // The plan, row-list and alive-snapshot regions sit before the delayed-archive
+  // staging, at offsets that do not depend on late joins.
+  const logkv_route_params plain{1.f, 1.f, 1.f, 0, 0};
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, &plain, workspace, workspace_bytes, nullptr, nullptr, ws);
+  if (rc) return rc;
+  if ((rc = check_log(cache, log))) return rc;
+  if (!rows->tokens) return LOGKV_OK;
+  rc = logkv::launch_record(*cache, *rows, ws, *log, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "op-log record launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_replay_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                        const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                        const logkv_op_log_view* log, int64_t cursor, int32_t* status, void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, nullptr, nullptr, ws);
+  if (rc) return rc;
+  if ((rc = check_log(cache, log))) return rc;
+  if (!status) return fail(LOGKV_EINVAL, "replay status pointer is NULL");
+  if (cursor < 0) return fail(LOGKV_EINVAL, "replay cursor must be >= 0");
+  if (!rows->tokens) return LOGKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = logkv::launch_replay(*cache, *rows, ws, *log, cursor, status, s);
+  ws.abort = status;
+  if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
+  if (rc) return fail(rc, "replay launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;
 }
 

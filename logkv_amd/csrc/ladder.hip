@@ -790,6 +790,15 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_G int8_t* as = gp(ws.assign + static_cast<int64_t>(lane_ix) * r.tokens);
   const LOGKV_G int32_t* ord = gp(ws.order + static_cast<int64_t>(b) * r.tokens);
 
+  if (ws.abort && *ws.abort) {
+    // A failed replay check: no rows, nothing written (the later launches read the plan).
+    if (blockIdx.y == 0 && threadIdx.x == 0) {
+      ws.plans[ladder].active = 0;
+      ws.plans[ladder].m_tok = 0;
+    }
+    return;
+  }
+
   // 1. This cluster's rows in position order (stable compaction). The
   // decisions and order entries of kCompactChunks chunks are loaded (clamped,
   // unconditionally) before the chunks are scanned.
@@ -829,7 +838,10 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   }
   const int m = m_s;
   if (m == 0) {
-    if (blockIdx.y == 0 && threadIdx.x == 0) ws.plans[ladder].active = 0;
+    if (blockIdx.y == 0 && threadIdx.x == 0) {
+      ws.plans[ladder].active = 0;
+      ws.plans[ladder].m_tok = 0;
+    }
     return;
   }
 

@@ -53,6 +53,7 @@ struct Workspace {
   LadderPlan* plans;      // [ladders]
   uint16_t* tok;          // [ladders, T] each ladder's flush rows in position order
   int32_t* units;         // [L - 1, ladders + 1] prefix sums over ladders of each level's carry work units
+  const int32_t* abort;   // optional: a nonzero value stops the commit before it writes anything
 };
 
 int64_t ladder_scratch_bytes(const LadderArgs& c, int64_t s0, int64_t m0);
@@ -68,5 +69,11 @@ int64_t attention_workspace_floats(const logkv_attention_args& a);
 int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream);
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
+int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream);
+int launch_snapshot(const LadderArgs& c, const Workspace& ws, hipStream_t stream);
+int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
+                  hipStream_t stream);
+int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
+                  int64_t cursor, int32_t* status, hipStream_t stream);
 
 }  // namespace logkv

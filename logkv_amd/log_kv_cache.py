@@ -46,6 +46,22 @@ def ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, K, exac
     raise ValueError("compressed ladder budget is too small for alpha_exact_tokens; increase B or reduce exact capacity")
 
 
+class _SemanticReplayPlans:
+    """Host-only replay state of one invocation (litgpt/log_kv_cache.py:97-108).
+
+    Freezes the CPU op-log so later caller mutations cannot change it, and
+    remembers the flush positions seen at each replay cursor, so a replay with
+    different positions at the same cursor is rejected. The log itself is
+    parsed on the device; this object holds no tensors and no cache reference.
+    """
+
+    def __init__(self, host_log):
+        if host_log is None:
+            raise RuntimeError("semantic replay plans require an existing CPU op-log")
+        self.host_log = tuple(tuple(tuple(map(tuple, lane)) for lane in batch) for batch in host_log)
+        self.plans = {}
+
+
 class LogStructuredKVCache(nn.Module):
     """Semantic LogKV cache whose flush runs as HIP kernels on one MI355X.
 
@@ -276,6 +292,10 @@ class LogStructuredKVCache(nn.Module):
         self._alpha_parity = 0   # flips with every swap of the exact pool's two buffer sets
         self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
                                    1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0)
+        self.op_log: torch.Tensor | None = None
+        self.op_log_len: torch.Tensor | None = None
+        self._op_replay_cursor_host = None
+        self._last_op_log_host = None
 
     # ------------------------------------------------------------------
     # C-ABI views
@@ -323,33 +343,141 @@ class LogStructuredKVCache(nn.Module):
     def route_and_flush_batch(self, k_raw, v, positions, *, positions_host=None, record_op_log=False,
                               replay_op_log=None, replay_op_log_len=None, replay_op_log_host=None,
                               replay_plans=None, span_ends=None, counts=None, assign_out=None, order_out=None):
-        """Route one flush of rows ``[Bt, G, T, D]`` and commit them (litgpt/log_kv_cache.py:4946-5128)."""
-        if record_op_log or replay_op_log is not None or replay_plans is not None:
-            raise NotImplementedError("op-log record/replay is not part of the logkv_amd flush path")
+        """Route one flush of rows ``[Bt, G, T, D]`` and commit them (litgpt/log_kv_cache.py:4946-5128).
+
+        ``record_op_log`` appends the flush's decisions to the op-log
+        (``begin_op_log``); ``replay_op_log`` / ``replay_op_log_len`` re-apply
+        a logged flush without routing (litgpt/log_kv_cache.py:5049-5114).
+        """
+        if replay_plans is not None and replay_op_log is None:
+            raise RuntimeError("semantic replay plans require the matching op-log; rerouting is not allowed")
+        if record_op_log and self.op_log is None:
+            self.begin_op_log()
         if positions.dim() == 1:
             positions = positions.unsqueeze(0).expand(k_raw.size(0), -1)
         for t, what in ((k_raw, "k_raw"), (v, "v"), (positions, "positions")):
             require_device(t, what)
         if k_raw.shape[:2] != (self.batch_size, self.n_groups) or v.shape[:3] != k_raw.shape[:3]:
             raise ValueError("flush rows must be [batch, groups, T, dim] matching the cache")
+        if positions_host is None and replay_plans is not None:
+            raise RuntimeError("semantic replay plans require CPU positions; device readback is not allowed")
         self._mid_decode_state = None
         if self.alpha_exact_tokens:
-            return self._alpha_route_flush(k_raw, v, positions, positions_host, span_ends)
-        self._route_commit(k_raw, v, positions, counts, assign_out, order_out)
+            if replay_op_log is not None:
+                raise RuntimeError("AlphaLogKV replay requires semantic_replay_updates; reranking is not allowed")
+            return self._alpha_route_flush(k_raw, v, positions, positions_host, span_ends, record=record_op_log)
+        if replay_op_log is not None:
+            return self._replay_flush(k_raw, v, positions, positions_host, counts, replay_op_log, replay_op_log_len,
+                                      replay_op_log_host, replay_plans)
+        self._route_commit(k_raw, v, positions, counts, assign_out, order_out, record=record_op_log)
 
-    def _route_commit(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None):
+    def _route_commit(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None, record=False):
         view = self._ladder_view()
         rows = self._rows_view(k_raw, v, positions, counts)
         ws = self._workspace_for(view, rows.tokens)
+        stream = stream_of(k_raw.device)
         rc = lib().logkv_route_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
-                                      ptr(assign_out), ptr(order_out), stream_of(k_raw.device))
+                                      ptr(assign_out), ptr(order_out), stream)
         check(rc, "logkv_route_commit")
+        if record:
+            log = self._op_log_view()
+            check(lib().logkv_record_ops(C.byref(view), C.byref(rows), ptr(ws), ws.numel(), C.byref(log), stream),
+                  "logkv_record_ops")
 
-    def _alpha_route_flush(self, k_raw, v, positions, positions_host, span_ends):
+    def _alpha_route_flush(self, k_raw, v, positions, positions_host, span_ends, record=False):
         from .alpha_log_kv import alpha_flush
-        return alpha_flush(self, k_raw, v, positions, positions_host, span_ends)
+        return alpha_flush(self, k_raw, v, positions, positions_host, span_ends, record=record)
 
-    def _semantic_flush_tokens(self, flush_len: int, span_ends=None) -> None:
+    # ------------------------------------------------------------------
+    # Op-log record / replay (litgpt/log_kv_cache.py:2006-2096, :4856-4926)
+    # ------------------------------------------------------------------
+    def begin_op_log(self) -> None:
+        """Bind a fresh per-(batch, group) route log (litgpt/log_kv_cache.py:2006-2028).
+
+        ``op_log`` ``[Bt, G, 3 * max_seq_length, 4]`` int32 rows (op, cluster,
+        arg, position) and ``op_log_len`` ``[Bt, G]``, written on the device by
+        every flush routed with ``record_op_log=True``.
+        """
+        cap = max(1, self.max_seq_length * 3)
+        dev = self.level_count.device
+        self.op_log = torch.zeros(self.batch_size, self.n_groups, cap, 4, device=dev, dtype=torch.int32)
+        self.op_log_len = torch.zeros(self.batch_size, self.n_groups, device=dev, dtype=torch.int32)
+        self._op_replay_cursor_host = None
+
+    def _op_log_view(self, log=None, lengths=None) -> _lib.OpLogView:
+        log = self.op_log if log is None else log
+        lengths = self.op_log_len if lengths is None else lengths
+        return _lib.OpLogView(ptr(log), ptr(lengths), log.size(2))
+
+    def take_op_log(self):
+        """(log ``[Bt, G, max_len, 4]``, lengths ``[Bt, G]``) copies (litgpt/log_kv_cache.py:2029-2038).
+
+        Reads the lengths back (one synchronisation) and keeps the rows as host
+        tuples in ``_last_op_log_host``. Raises ``RuntimeError`` when a lane
+        logged more rows than the capacity (the rows past it were not written).
+        """
+        if getattr(self, "op_log", None) is None or getattr(self, "op_log_len", None) is None:
+            return None, None
+        lengths = self.op_log_len.cpu()
+        if int(lengths.max()) > self.op_log.size(2):
+            raise RuntimeError("semantic LogKV op_log overflow")
+        max_len = int(lengths.max())
+        rows = self.op_log[:, :, :max_len].cpu().tolist()
+        lens = lengths.tolist()
+        self._last_op_log_host = [[[tuple(r) for r in rows[b][g][:lens[b][g]]] for g in range(self.n_groups)]
+                                  for b in range(self.batch_size)]
+        return self.op_log[:, :, :max_len].clone(), self.op_log_len.clone()
+
+    def _replay_flush(self, k_raw, v, positions, positions_host, counts, log, lengths, log_host, plans):
+        """Re-apply one logged flush (litgpt/log_kv_cache.py:5067-5114) on the device.
+
+        Every lane of an attach-routed log consumes one row per flushed token,
+        so the lanes share one cursor. The checks run on the device; their
+        status is read back (one synchronisation) and a failed check raises
+        ``RuntimeError`` with the cache left as it was.
+        """
+        if lengths is None:
+            raise ValueError("replay_op_log_len is required with replay_op_log")
+        if plans is not None and log_host is not plans.host_log:
+            raise RuntimeError("semantic replay plan does not match the CPU op-log")
+        B, G, T = k_raw.shape[:3]
+        if (log.dim() != 4 or tuple(log.shape[:2]) != (B, G) or log.size(3) != 4 or log.dtype != torch.int32
+                or tuple(lengths.shape) != (B, G) or lengths.dtype != torch.int32):
+            raise RuntimeError("semantic replay log does not match the current batch/groups")
+        require_device(log, "replay_op_log")
+        require_device(lengths, "replay_op_log_len")
+        log, lengths = log.contiguous(), lengths.contiguous()
+        if getattr(self, "_op_replay_cursor_host", None) is None:
+            self._op_replay_cursor_host = [[0] * G for _ in range(B)]
+        cursors = self._op_replay_cursor_host
+        cursor = cursors[0][0]
+        if any(c != cursor for row in cursors for c in row):
+            raise RuntimeError("semantic LogKV replay cursors differ across lanes")
+        if plans is not None:
+            current = tuple(tuple(int(x) for x in row) for row in positions_host[:B])
+            key = tuple(tuple(row[:G]) for row in cursors[:B])
+            seen = plans.plans.setdefault(key, current)
+            if seen != current:
+                raise RuntimeError("semantic replay plan does not match the current flush positions")
+        view = self._ladder_view()
+        rows = self._rows_view(k_raw, v, positions, counts)
+        ws = self._workspace_for(view, rows.tokens)
+        status = self._views.get("replay_status")
+        if status is None:
+            status = self._views["replay_status"] = torch.zeros(1, dtype=torch.int32, device=self.level_k.device)
+        lv = self._op_log_view(log, lengths)
+        check(lib().logkv_replay_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                        C.byref(lv), cursor, ptr(status), stream_of(k_raw.device)),
+              "logkv_replay_commit")
+        bits = int(status.item())
+        if bits:
+            why = "; ".join(msg for bit, msg in _lib.REPLAY_ERRORS.items() if bits & bit)
+            raise RuntimeError(f"semantic LogKV replay of rows {cursor}.. failed (nothing was written): {why}")
+        taken = [T] * B if counts is None else [max(0, min(T, int(c))) for c in counts.tolist()]
+        for b in range(B):
+            cursors[b][:G] = [cursors[b][g] + taken[b] for g in range(G)]
+
+    def _semantic_flush_tokens(self, flush_len: int, span_ends=None, **route) -> None:
         pending = int(flush_len)
         while pending > 0:
             take = min(self.semantic_flush_granularity, pending)
@@ -359,6 +487,7 @@ class LogStructuredKVCache(nn.Module):
                 self.recent_k_raw[:, :, :take], self.recent_v[:, :, :take], self.recent_pos[:, :take],
                 positions_host=[row[:take] for row in self._recent_pos_host],
                 span_ends=[row[:take] for row in self._recent_span_ends] if self.alpha_exact_tokens else None,
+                **route,
             )
             remaining = self.recent_count - take
             if remaining > 0:
@@ -371,6 +500,14 @@ class LogStructuredKVCache(nn.Module):
                     self._recent_pos_host[b][:remaining] = self._recent_pos_host[b][take:self.recent_count]
                     if self.alpha_exact_tokens:
                         self._recent_span_ends[b][:remaining] = self._recent_span_ends[b][take:self.recent_count]
+            # The vacated rows are cleared (litgpt/log_kv_cache.py:5652-5659).
+            for b in range(self.batch_size):
+                self._recent_pos_host[b][remaining:self.recent_count] = [0] * (self.recent_count - remaining)
+                if self.alpha_exact_tokens:
+                    self._recent_span_ends[b][remaining:self.recent_count] = [False] * (self.recent_count - remaining)
+            for name in ("recent_k", "recent_k_raw", "recent_v"):
+                getattr(self, name)[:, :, remaining:self.recent_count].zero_()
+            self.recent_pos[:, remaining:self.recent_count].zero_()
             self.recent_count = remaining
             pending -= take
 
@@ -397,8 +534,6 @@ class LogStructuredKVCache(nn.Module):
         (litgpt/log_kv_cache.py:5668-5718, :5847)."""
         if k_raw is None:
             raise ValueError("semantic LogKV add_recent requires pre-RoPE k_raw")
-        if record_op_log or replay_op_log is not None or replay_plans is not None:
-            raise NotImplementedError("op-log record/replay is not part of the logkv_amd flush path")
         n = k.size(2)
         if n > self.recent_size:
             raise ValueError(f"chunk size {n} exceeds recent_size {self.recent_size}")
@@ -430,7 +565,9 @@ class LogStructuredKVCache(nn.Module):
         overflow = self.recent_count - self.recent_size
         if overflow > 0:
             F = self.semantic_flush_granularity
-            self._semantic_flush_tokens(F * ((overflow + F - 1) // F))
+            self._semantic_flush_tokens(F * ((overflow + F - 1) // F), record_op_log=record_op_log,
+                                        replay_op_log=replay_op_log, replay_op_log_len=replay_op_log_len,
+                                        replay_op_log_host=replay_op_log_host, replay_plans=replay_plans)
 
     def reset_parameters(self) -> None:
         """Empty cache (litgpt/log_kv_cache.py:6270)."""
@@ -445,6 +582,8 @@ class LogStructuredKVCache(nn.Module):
         self.token_count = self.recent_count = 0
         self.alpha_count = 0
         self._mid_decode_state = None
+        self.op_log = self.op_log_len = None
+        self._op_replay_cursor_host = None
         self._recent_pos_host = [[0] * self.recent_capacity for _ in range(self.batch_size)]
         if self.alpha_exact_tokens:
             for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid", "alpha_span_len", "alpha_span_closed",

@@ -24,7 +24,10 @@ Modules and what pins them (the tests named in brackets):
   known anchors, explicit RoPE and mask rows, mass slot = duplicated tokens,
   float64 masked softmax];
 * ``cache`` - one layer's cache and flush driver [tests/test_oracle_cache.py:
-  delayed-archive known answer, budget closed form, streaming invariants].
+  delayed-archive known answer, budget closed form, streaming invariants];
+* ``oplog`` - op-log rows of a flush and the replay parse
+  [tests/test_oracle_oplog.py: hand-derived logs of small flushes, replay
+  reproducing the recorded state bit for bit, the reference's parse errors].
 
 Parity unpinned: the last-ulp agreement with the reference's own float traces
 where it leaves the order to a library (Torch GEMM / cdist / segment_reduce

@@ -29,7 +29,7 @@ import math
 import numpy as np
 
 from . import ladder as lad
-from . import readout, route, spans
+from . import oplog, readout, route, spans
 from .numerics import bf16_round, f32
 
 I64_MAX = np.iinfo(np.int64).max
@@ -102,6 +102,8 @@ class OracleCache:
         self.alpha_positions = [[] for _ in range(batch)]
         self.beta_cuts = []
         self.late_joins = 0       # delayed-archive re-sorts performed (test coverage evidence)
+        self.op_log = None        # per lane lists of (op, cluster, arg, position), see oracle.oplog
+        self.replay_cursor = None
 
     # ---- ladder access -------------------------------------------------
     def ladder(self, b, g, c) -> lad.Ladder:
@@ -167,10 +169,12 @@ class OracleCache:
         self._append(b, g, c, rows)
 
     def route_and_commit(self, ak, av, ap, counts):
-        """Attach-route ``counts[b]`` rows of ``ak/av/ap`` and commit them."""
+        """Attach-route ``counts[b]`` rows of ``ak/av/ap`` and commit them; with
+        ``op_log`` bound (``begin_op_log``) the flush's rows are appended to it."""
         assign, order = route.attach_assign(ak, ap, counts, self.centroid, self.alive, self.p_hi_c, self.s_h,
                                             self.eta, self.g0, self.lam)
         jobs = route.commit_jobs(assign, order, counts, self.alive)
+        late = set()
         for (b, g, c), (new, rows) in sorted(jobs.items()):
             if new:
                 t = rows[0]
@@ -180,10 +184,39 @@ class OracleCache:
                 continue
             pos = ap[b, rows].astype(np.int64)
             if self.P and pos.min() < self.p_hi_c[b, g, c]:
+                late.add((b, g, c))
                 self.join_late(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
             else:
                 self.join(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
+        if self.op_log is not None:
+            for (b, g), rows in oplog.flush_rows(jobs, ap, late).items():
+                self.op_log[b][g].extend(rows)
         return assign, order
+
+    # ---- op-log ----------------------------------------------------------
+    def begin_op_log(self):
+        self.op_log = [[[] for _ in range(self.groups)] for _ in range(self.batch)]
+        self.replay_cursor = None
+
+    def replay_rows(self, k_raw, v, pos, host_log):
+        """Re-apply one logged flush of ``T`` rows without routing
+        (litgpt/log_kv_cache.py:5067-5114, :4178-4223): each run appends its rows
+        in log order, each new cluster opens with its row."""
+        k_raw, v = f32(k_raw), f32(v)
+        pos = np.asarray(pos, np.int64)
+        n_batch, n_groups, T, _ = k_raw.shape
+        if self.replay_cursor is None:
+            self.replay_cursor = [[0] * n_groups for _ in range(n_batch)]
+        ends, rounds = oplog.replay_plan(host_log, self.replay_cursor, pos.tolist(), n_groups, T)
+        self.replay_cursor = [list(row) for row in ends]
+        for joins, specials in rounds:
+            for b, g, c, _arg, _new_segment, offsets in joins:
+                rows = np.asarray(offsets, np.int64)
+                self.join(b, g, c, k_raw[b, g, rows], v[b, g, rows], pos[b, rows])
+            for b, g, (kind, c, token, offset, _) in specials:
+                if kind != "new":
+                    raise NotImplementedError("segment pads and Ward merges are not part of the attach route")
+                self.new_cluster(b, g, c, k_raw[b, g, offset], v[b, g, offset], int(token))
 
     # ---- flush -----------------------------------------------------------
     def flush_rows(self, k_raw, v, pos, ends=None):
