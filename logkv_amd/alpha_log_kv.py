@@ -344,7 +344,7 @@ def _alpha_call(cache, T: int, dtype) -> _AlphaCall:
 
 
 @torch.no_grad()
-def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=False):
+def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=False, tape=None):
     """One Alpha flush of ``cache`` (litgpt/log_kv_cache.py:3904-4003), all on the device.
 
     The span selection (candidates of ``[exact pool | flush]``, scores, bounded
@@ -357,7 +357,8 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=Fa
     ``positions_host`` is not needed. The argument structs and the kept /
     archived row buffers are built once per flush length and reused. With
     ``record`` the archived rows' route decisions are appended to the op-log
-    (litgpt/log_kv_cache.py:3782-3788).
+    (litgpt/log_kv_cache.py:3782-3788). With an update ``tape`` the flush's
+    rows, selection and decisions are saved there and their indices returned.
     """
     if span_ends is None:
         raise ValueError("AlphaLogKV requires natural span boundaries")
@@ -380,12 +381,52 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=Fa
     _lib.check(_lib.lib().logkv_alpha_select(C.byref(call.select), ws.data_ptr(), ws.numel(), stream),
                "logkv_alpha_select")
     _lib.check(_lib.lib().logkv_alpha_partition(C.byref(call.part), stream), "logkv_alpha_partition")
+    _swap_pool(cache)
+    # Inputs that may be temporaries stay referenced until the next flush on this stream.
+    cache._alpha_keep_alive = (ends, positions)
+    assign = order = None
+    if tape is not None:
+        A = bufs["k"].size(2)
+        assign = torch.empty(cache.batch_size * cache.n_groups, A, dtype=torch.int8, device=dev)
+        order = torch.empty(cache.batch_size, A, dtype=torch.int32, device=dev)
+    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], assign, order, record=record)
+    if tape is None:
+        return None
+    return {"k": tape.save(k_raw), "v": tape.save(v), "pos": tape.save(positions), "ends": tape.save(ends),
+            "keep": tape.save(bufs["keep"]), "archive": tape.save(bufs["archive"]), "count": tape.save(bufs["count"]),
+            "span_len": tape.save(cache.alpha_span_len), "span_closed": tape.save(cache.alpha_span_closed),
+            "span_count": tape.save(cache.alpha_span_count), "alpha_count": tape.save(cache.alpha_count_dev),
+            "assign": tape.save(assign, owned=True), "order": tape.save(order, owned=True)}
+
+
+def _swap_pool(cache):
+    """The rewritten exact pool (second buffer set) becomes the current one."""
     spare = cache._alpha_spare
     cache._alpha_spare = (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid,
                           cache.alpha_span_len, cache.alpha_span_closed, cache.alpha_span_count)
     (cache.alpha_k_raw, cache.alpha_v, cache.alpha_pos, cache.alpha_valid, cache.alpha_span_len,
      cache.alpha_span_closed, cache.alpha_span_count) = spare
     cache._alpha_parity ^= 1
-    # Inputs that may be temporaries stay referenced until the next flush on this stream.
+
+
+@torch.no_grad()
+def alpha_replay(cache, saved):
+    """Re-apply a recorded Alpha flush without selecting: the exact-pool rewrite
+    and archive gather with the recorded keep / archive tables, the recorded
+    span state, then the commit of the archived rows with their recorded attach
+    decisions (the replay half of litgpt/log_kv_cache.py:4946-5011)."""
+    k_raw, v, positions, ends = saved["k"], saved["v"], saved["pos"], saved["ends"]
+    call = _alpha_call(cache, k_raw.size(2), k_raw.dtype)
+    call.set_rows(k_raw, v, positions, ends)
+    bufs = call.bufs
+    for name in ("keep", "archive", "count"):
+        bufs[name].copy_(saved[name])
+    _lib.check(_lib.lib().logkv_alpha_partition(C.byref(call.part), _lib.stream_of(k_raw.device)),
+               "logkv_alpha_partition")
+    _swap_pool(cache)
+    cache.alpha_span_len.copy_(saved["span_len"])
+    cache.alpha_span_closed.copy_(saved["span_closed"])
+    cache.alpha_span_count.copy_(saved["span_count"])
+    cache.alpha_count_dev.copy_(saved["alpha_count"])
     cache._alpha_keep_alive = (ends, positions)
-    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], record=record)
+    cache._commit_only(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], saved["assign"], saved["order"])

@@ -16,6 +16,7 @@ read-only properties that copy from the device when asked.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import math
 
@@ -44,6 +45,36 @@ def ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, K, exac
         if need <= baseline:
             return cand, lv, (batch_size * baseline, batch_size * need)
     raise ValueError("compressed ladder budget is too small for alpha_exact_tokens; increase B or reduce exact capacity")
+
+
+class _SemanticReplayUpdates:
+    """One training invocation's flush records, replayed without routing
+    (litgpt/log_kv_cache.py:111-139).
+
+    A record holds a flush's rows and its decisions as detached device
+    tensors: the attach cluster of every row and the position order, and with
+    Alpha the exact-pool selection (kept / archived rows, span state). A replay
+    re-runs only the kernels that write the cache from those decisions, so the
+    restored state is the recorded one bit for bit.
+    """
+
+    def __init__(self, flushes=None, tensors=None):
+        self.flushes = {} if flushes is None else flushes
+        self.tensors = [] if tensors is None else tensors
+
+    def wait(self, device):
+        if device.type == "cuda":
+            stream = torch.cuda.current_stream(device)
+            for record in self.flushes.values():
+                if record[-1] is not None:
+                    stream.wait_event(record[-1])
+
+    def save(self, tensor, owned=False):
+        """Keep ``tensor`` for replay (a copy unless the caller owns it outright); returns its index."""
+        if tensor is None:
+            return None
+        self.tensors.append(tensor.detach() if owned else tensor.detach().clone())
+        return len(self.tensors) - 1
 
 
 class _SemanticReplayPlans:
@@ -296,6 +327,12 @@ class LogStructuredKVCache(nn.Module):
         self.op_log_len: torch.Tensor | None = None
         self._op_replay_cursor_host = None
         self._last_op_log_host = None
+        # Update tape (semantic_replay_updates): the bound tape, whether it is
+        # replayed, and the flushes recorded / replayed since the log began.
+        self._active_updates = None
+        self._replaying_updates = False
+        self._update_actions = None
+        self._tape_index = 0
 
     # ------------------------------------------------------------------
     # C-ABI views
@@ -349,6 +386,9 @@ class LogStructuredKVCache(nn.Module):
         (``begin_op_log``); ``replay_op_log`` / ``replay_op_log_len`` re-apply
         a logged flush without routing (litgpt/log_kv_cache.py:5049-5114).
         """
+        if self._active_updates is not None:
+            return self._tape_flush(self._active_updates, k_raw, v, positions, positions_host, span_ends, counts,
+                                    record_op_log, replay_op_log is not None or replay_op_log_host is not None)
         if replay_plans is not None and replay_op_log is None:
             raise RuntimeError("semantic replay plans require the matching op-log; rerouting is not allowed")
         if record_op_log and self.op_log is None:
@@ -384,9 +424,100 @@ class LogStructuredKVCache(nn.Module):
             check(lib().logkv_record_ops(C.byref(view), C.byref(rows), ptr(ws), ws.numel(), C.byref(log), stream),
                   "logkv_record_ops")
 
-    def _alpha_route_flush(self, k_raw, v, positions, positions_host, span_ends, record=False):
+    def _commit_only(self, k_raw, v, positions, counts, assign, order):
+        view = self._ladder_view()
+        rows = self._rows_view(k_raw, v, positions, counts)
+        ws = self._workspace_for(view, rows.tokens)
+        check(lib().logkv_commit_only(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                      ptr(assign), ptr(order), stream_of(k_raw.device)), "logkv_commit_only")
+
+    def _alpha_route_flush(self, k_raw, v, positions, positions_host, span_ends, record=False, tape=None):
         from .alpha_log_kv import alpha_flush
-        return alpha_flush(self, k_raw, v, positions, positions_host, span_ends, record=record)
+        return alpha_flush(self, k_raw, v, positions, positions_host, span_ends, record=record, tape=tape)
+
+    # ------------------------------------------------------------------
+    # Update tape (litgpt/log_kv_cache.py:4932-5031)
+    # ------------------------------------------------------------------
+    @contextlib.contextmanager
+    def _semantic_update_context(self, updates, *, replay=False):
+        previous = self._active_updates, self._replaying_updates
+        self._active_updates, self._replaying_updates = updates, replay
+        try:
+            yield
+        finally:
+            self._active_updates, self._replaying_updates = previous
+
+    def _tape_signature(self, k_raw, v, span_ends):
+        ends = None
+        if span_ends is not None and not isinstance(span_ends, torch.Tensor):
+            ends = tuple(tuple(bool(x) for x in row) for row in span_ends)
+        return (tuple(k_raw.shape), tuple(v.shape), k_raw.dtype, v.dtype, k_raw.device, self.K_max, self.B,
+                self.L_alloc, self.recent_size, self.semantic_flush_granularity, self.alpha_exact_tokens,
+                self.alpha_span_max_tokens, self.beta_novelty, self.beta_adaptive_merge, ends)
+
+    def _tape_flush(self, updates, k_raw, v, positions, positions_host, span_ends, counts, record_op_log, replay):
+        """Record a flush on the bound tape, or replay it from there
+        (litgpt/log_kv_cache.py:4946-5031): keyed by the flush's CPU positions,
+        replayed in recording order with the same shapes and configuration."""
+        if positions.dim() == 1:
+            positions = positions.unsqueeze(0).expand(k_raw.size(0), -1)
+        host = positions_host
+        if host is None:
+            raise RuntimeError("update replay requires CPU flush positions; no device readback is allowed")
+        if len(host) != k_raw.size(0) or any(len(row) != k_raw.size(2) for row in host):
+            raise RuntimeError("update replay CPU positions do not match the flush shape")
+        key = tuple(tuple(int(x) for x in row) for row in host)
+        signature = self._tape_signature(k_raw, v, span_ends)
+        dev = k_raw.device
+        if self._replaying_updates:
+            if not replay or key not in updates.flushes:
+                raise RuntimeError("missing semantic update record; rerouting is not allowed")
+            expected, index, saved, ready = updates.flushes[key]
+            if index != self._tape_index:
+                raise RuntimeError("semantic update replay flushes are out of order")
+            if signature != expected:
+                raise RuntimeError("semantic update record does not match this flush/configuration")
+            stream = torch.cuda.current_stream(dev)
+            if ready is not None:
+                stream.wait_event(ready)   # device-side wait only
+            tensors = {name: None if i is None else updates.tensors[i] for name, i in saved.items()}
+            for t in tensors.values():
+                if t is not None:
+                    t.record_stream(stream)
+            self._mid_decode_state = None
+            if self.alpha_exact_tokens:
+                from .alpha_log_kv import alpha_replay
+                alpha_replay(self, tensors)
+            else:
+                self._commit_only(tensors["k"], tensors["v"], tensors["pos"], tensors["counts"], tensors["assign"],
+                                  tensors["order"])
+            self._tape_index += 1
+            return
+        if replay or key in updates.flushes:
+            raise RuntimeError("duplicate or incorrectly bound semantic update recording")
+        if record_op_log and self.op_log is None:
+            self.begin_op_log()
+        if not record_op_log:
+            raise RuntimeError("semantic update recording requires record_op_log=True")
+        for t, what in ((k_raw, "k_raw"), (v, "v"), (positions, "positions")):
+            require_device(t, what)
+        if k_raw.shape[:2] != (self.batch_size, self.n_groups) or v.shape[:3] != k_raw.shape[:3]:
+            raise ValueError("flush rows must be [batch, groups, T, dim] matching the cache")
+        self._mid_decode_state = None
+        if self.alpha_exact_tokens:
+            saved = self._alpha_route_flush(k_raw, v, positions, positions_host, span_ends, record=True, tape=updates)
+        else:
+            T = k_raw.size(2)
+            assign = torch.empty(self.batch_size * self.n_groups, T, dtype=torch.int8, device=dev)
+            order = torch.empty(self.batch_size, T, dtype=torch.int32, device=dev)
+            self._route_commit(k_raw, v, positions, counts, assign, order, record=True)
+            saved = {"k": updates.save(k_raw), "v": updates.save(v), "pos": updates.save(positions),
+                     "counts": updates.save(counts), "assign": updates.save(assign, owned=True),
+                     "order": updates.save(order, owned=True)}
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(dev))
+        updates.flushes[key] = (signature, self._tape_index, saved, ready)
+        self._tape_index += 1
 
     # ------------------------------------------------------------------
     # Op-log record / replay (litgpt/log_kv_cache.py:2006-2096, :4856-4926)
@@ -403,6 +534,7 @@ class LogStructuredKVCache(nn.Module):
         self.op_log = torch.zeros(self.batch_size, self.n_groups, cap, 4, device=dev, dtype=torch.int32)
         self.op_log_len = torch.zeros(self.batch_size, self.n_groups, device=dev, dtype=torch.int32)
         self._op_replay_cursor_host = None
+        self._tape_index = 0
 
     def _op_log_view(self, log=None, lengths=None) -> _lib.OpLogView:
         log = self.op_log if log is None else log
@@ -584,6 +716,7 @@ class LogStructuredKVCache(nn.Module):
         self._mid_decode_state = None
         self.op_log = self.op_log_len = None
         self._op_replay_cursor_host = None
+        self._tape_index = 0
         self._recent_pos_host = [[0] * self.recent_capacity for _ in range(self.batch_size)]
         if self.alpha_exact_tokens:
             for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid", "alpha_span_len", "alpha_span_closed",
