@@ -12,15 +12,23 @@ import torch
 
 
 class Mixture:
+    """``drift_every``: the centers are redrawn each time that many rows have
+    been drawn (counted over every ``rows`` call, checked at call boundaries)."""
+
     def __init__(self, batch, groups, dim, clusters=12, seed=0, center_scale=4.0, noise=0.5, outlier=0.1,
-                 outlier_scale=12.0):
+                 outlier_scale=12.0, drift_every=0):
         self.g = torch.Generator().manual_seed(seed)
         self.batch, self.groups, self.dim = batch, groups, dim
         self.noise, self.outlier, self.outlier_scale = noise, outlier, outlier_scale
+        self.center_scale, self.drift_every, self.drawn, self.epoch = center_scale, int(drift_every), 0, 0
         self.centers = torch.randn(batch, groups, clusters, dim, generator=self.g) * center_scale
 
     def rows(self, n):
         """bf16 rows ``[batch, groups, n, dim]``."""
+        if self.drift_every and self.drawn // self.drift_every != self.epoch:
+            self.epoch = self.drawn // self.drift_every
+            self.centers = torch.randn(self.centers.shape, generator=self.g) * self.center_scale
+        self.drawn += n
         k = self.centers.size(2)
         label = torch.randint(0, k, (self.batch, self.groups, n), generator=self.g)
         x = torch.gather(self.centers, 2, label[..., None].expand(-1, -1, -1, self.dim))

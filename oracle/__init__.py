@@ -25,6 +25,10 @@ Modules and what pins them (the tests named in brackets):
   float64 masked softmax];
 * ``cache`` - one layer's cache and flush driver [tests/test_oracle_cache.py:
   delayed-archive known answer, budget closed form, streaming invariants];
+* ``unified`` - the unified Ward / radius route [tests/test_oracle_unified.py:
+  hand-worked reducer answers (Ward cost, Lance-Williams update, radius
+  bound, xor tie rule, budget order), incremental rounds equal to a full
+  recompute, labels and Ward entry order, route invariants, an old-old merge];
 * ``oplog`` - op-log rows of a flush and the replay parse
   [tests/test_oracle_oplog.py: hand-derived logs of small flushes, replay
   reproducing the recorded state bit for bit, the reference's parse errors].

@@ -29,7 +29,7 @@ import math
 import numpy as np
 
 from . import ladder as lad
-from . import oplog, readout, route, spans
+from . import oplog, readout, route, spans, unified
 from .numerics import bf16_round, f32
 
 I64_MAX = np.iinfo(np.int64).max
@@ -58,7 +58,7 @@ def budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens, element=2):
 class OracleCache:
     def __init__(self, batch, groups, max_seq, dk, dv, *, B=128, recent_size=2048, K=12, lam=1.0, eta=1.0,
                  g0=2048.0, s_h=1.0, flush=2048, exact_tokens=0, span_max=64, beta_novelty=False,
-                 beta_adaptive=False, cos=None, sin=None, table_bf16=False):
+                 beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False):
         self.batch, self.groups, self.max_seq, self.dk, self.dv = batch, groups, max_seq, dk, dv
         self.K, self.lam, self.eta, self.g0 = K, lam, eta, g0
         self.B, self.L, *_ = budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens)
@@ -103,6 +103,7 @@ class OracleCache:
         self.beta_cuts = []
         self.late_joins = 0       # delayed-archive re-sorts performed (test coverage evidence)
         self.op_log = None        # per lane lists of (op, cluster, arg, position), see oracle.oplog
+        self.unified = unified    # the unified Ward / radius route (oracle.unified) instead of attach
         self.replay_cursor = None
 
     # ---- ladder access -------------------------------------------------
@@ -170,7 +171,10 @@ class OracleCache:
 
     def route_and_commit(self, ak, av, ap, counts):
         """Attach-route ``counts[b]`` rows of ``ak/av/ap`` and commit them; with
-        ``op_log`` bound (``begin_op_log``) the flush's rows are appended to it."""
+        ``op_log`` bound (``begin_op_log``) the flush's rows are appended to it.
+        With ``unified`` the rows take the unified route instead."""
+        if self.unified:
+            return unified.route_unified(self, ak, av, ap, counts)
         assign, order = route.attach_assign(ak, ap, counts, self.centroid, self.alive, self.p_hi_c, self.s_h,
                                             self.eta, self.g0, self.lam)
         jobs = route.commit_jobs(assign, order, counts, self.alive)

@@ -1,0 +1,352 @@
+"""CPU restatement of the unified (Ward / radius) route.
+
+TEST INFRASTRUCTURE ONLY (the oracle): used by ``tests/`` and never by the
+product package.
+
+Follows litgpt/log_kv_cache.py:3589-3688 (the route), :448-637 (the
+incremental reducer ``_UnifiedReduceTorch``, restated per lane),
+:3544-3568 (labels), :2517-2580 and :2395-2447 (Ward merge of old clusters
+and its entry order), docs/semantic-unified-routing.md:11-96.
+
+Two stages per lane (batch row, KV group):
+1. candidates: the flushed rows start as singletons (mass 1, radius 0) and
+   mutual-nearest Ward pairs merge while the radius bound
+   ``max(r_a + beta d, r_b + alpha d) <= sqrt(lambda s_h)`` holds;
+2. global budget: old live clusters (mass n_total) and the candidates compete
+   until at most K remain, the ``count - K`` cheapest mutual pairs per round.
+Old-old merges re-append both ladders into the lower cluster id; new roots
+open the free cluster ids in ascending order; the rows are then committed as
+attach-routed rows are.
+
+Float order. Every element operation is one IEEE float32 operation in the
+reference's order (``_unified_pair_cost``, ``_merge``). Where the reference
+leaves an order to a library, one order is fixed here and on the device:
+initial squared distances are canonical feature sums (``numerics.dsum``) of
+squared differences, ``sum((x_i - x_j)^2)`` (the reference's small-matrix
+``cdist`` form; it uses a centred Gram GEMM above 32 nodes), and the exact
+radius check's squared distance likewise.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import ladder as lad
+from .numerics import dsum, f32
+
+INF = np.float32(np.inf)
+INF_KEY = np.uint64(0x7F800000) << np.uint64(32)
+LOW = np.uint64(0xFFFFFFFF)
+
+
+def pack(cost, key):
+    """(cost bits << 32) | key, +0.0 for a zero cost (litgpt/log_kv_cache.py:431-434)."""
+    cost = np.where(cost == 0, np.float32(0), cost).astype(np.float32)
+    return (cost.view(np.uint32).astype(np.uint64) << np.uint64(32)) | np.asarray(key).astype(np.uint64)
+
+
+def pair_cost(d2, mi, mj, ri, rj, limit, valid):
+    """Ward cost and validity (litgpt/log_kv_cache.py:437-445)."""
+    one = np.float32(1)
+    denom = np.maximum(mi + mj, one)
+    valid = valid & (mi > 0) & (mj > 0)
+    if limit is not None:
+        distance = np.sqrt(d2)
+        bound = np.maximum(ri + (mj / denom) * distance, rj + (mi / denom) * distance)
+        valid = valid & (bound <= limit)
+    cost = np.where(valid, d2 * (mi * mj / denom), INF).astype(np.float32)
+    return cost, valid
+
+
+def pair_distances(mu):
+    """Squared distances ``[M, M]``: canonical sums of squared differences for
+    i < j, mirrored, zero diagonal."""
+    mu = f32(mu)
+    m = mu.shape[0]
+    out = np.zeros((m, m), np.float32)
+    for i in range(m - 1):
+        diff = mu[i][None, :] - mu[i + 1:]
+        out[i, i + 1:] = dsum(diff * diff)
+    iu = np.triu_indices(m, 1)
+    out[iu[1], iu[0]] = out[iu]
+    return out
+
+
+def clamp0(x):
+    return np.where(x < 0, np.float32(0), x).astype(np.float32)
+
+
+class Reducer:
+    """One lane's incremental rounds (litgpt/log_kv_cache.py:448-637)."""
+
+    def __init__(self, dist, mu, mass, count, limit, target):
+        self.dist, self.mu, self.mass = f32(dist).copy(), f32(mu).copy(), f32(mass).copy()
+        self.limit = None if limit is None else np.float32(limit)
+        self.target = int(target)
+        size = self.mass.shape[0]
+        self.ids = np.arange(size)
+        self.alive = self.ids < count
+        self.radius = np.zeros(size, np.float32)
+        self.count = int(count)
+        self.stuck = False
+        self.trace = []
+        self.packed = np.full(size, INF_KEY, np.uint64)
+        rows = np.flatnonzero(self.alive)
+        if len(rows):
+            self.packed[rows] = self._scan(rows)
+
+    def _scan(self, rows):
+        lim = self.limit is not None
+        cost, _ = pair_cost(self.dist[rows], self.mass[rows][:, None], self.mass[None, :],
+                            self.radius[rows][:, None] if lim else None, self.radius[None, :] if lim else None,
+                            self.limit, self.ids[None, :] != rows[:, None])
+        return pack(cost, rows[:, None] ^ self.ids[None, :]).min(1)
+
+    def step(self):
+        size = self.mass.shape[0]
+        ids = self.ids
+        best = np.clip(((self.packed & LOW).astype(np.int64)) ^ ids, 0, size - 1)
+        cost = (self.packed >> np.uint64(32)).astype(np.uint32).view(np.float32)
+        valid = self.alive & (ids < best) & (best[best] == ids) & (cost < INF)
+        nprop = int(valid.sum())
+        rejected = np.zeros(size, bool)
+        bound = None
+        if self.limit is not None:
+            rows = np.flatnonzero(valid)
+            other = best[rows]
+            diff = self.mu[rows] - self.mu[other]
+            exact2 = dsum(diff * diff)
+            exact = np.sqrt(exact2)
+            ma, mb = self.mass[rows], self.mass[other]
+            denom = np.maximum(ma + mb, np.float32(1))
+            verified = np.maximum(self.radius[rows] + (mb / denom) * exact,
+                                  self.radius[other] + (ma / denom) * exact).astype(np.float32)
+            bad = verified > self.limit
+            self.dist[rows[bad], other[bad]] = exact2[bad]
+            self.dist[other[bad], rows[bad]] = exact2[bad]
+            rejected[rows[bad]] = True
+            rejected[other[bad]] = True
+            valid[rows[bad]] = False
+            bound = np.zeros(size, np.float32)
+            bound[rows] = verified
+        pair = np.where(valid, cost, INF).astype(np.float32)
+        order = np.argsort(pair, kind="stable")[:size // 2]
+        ok = pair[order] < INF
+        ok &= np.cumsum(ok) <= self.count - self.target
+        a = order[ok]
+        b = best[a]
+        keep = np.zeros(size, bool)
+        merged = np.zeros(size, bool)
+        if len(a):
+            self._merge(a, b, bound, keep, merged)
+        dirty = self.alive & ~keep & (merged[best] | rejected)
+        rows = np.flatnonzero(dirty)
+        if len(rows):
+            self.packed[rows] = self._scan(rows)
+        self.count -= int(ok.sum())
+        remaining = self.count > self.target
+        if remaining and nprop == 0:
+            self.stuck = True
+        return remaining and nprop > 0
+
+    def _merge(self, a, b, bound, keep, merged):
+        size = self.mass.shape[0]
+        ids = self.ids
+        ma, mb = self.mass[a], self.mass[b]
+        dab = self.dist[a, b]
+        total = ma + mb
+        alpha, beta = ma / total, mb / total
+        shift = alpha * beta * dab
+        keep[a] = True
+        merged[a] = True
+        merged[b] = True
+        partner = np.zeros(size, np.int64)
+        partner[a] = b
+        pma, pmb, pdab = np.ones(size, np.float32), np.zeros(size, np.float32), np.zeros(size, np.float32)
+        pma[a], pmb[a], pdab[a] = ma, mb, dab
+        self.mass[a] = total
+        self.mass[b] = 0
+        self.alive[b] = False
+        if bound is not None:
+            self.radius[a] = bound[a]
+        self.mu[a] = (ma[:, None] * self.mu[a] + mb[:, None] * self.mu[b]) / np.maximum(total, np.float32(1))[:, None]
+        al, be, sh = alpha[:, None], beta[:, None], shift[:, None]
+        x_aa, x_ba = self.dist[a], self.dist[b]
+        new = al * x_aa + be * x_ba - sh
+        q = partner
+        x_ab, x_bb = self.dist[a[:, None], q[None, :]], self.dist[b[:, None], q[None, :]]
+        qalpha, qbeta = pma / (pma + pmb), pmb / (pma + pmb)
+        qshift = qalpha * qbeta * pdab
+        own_first = qalpha * new + qbeta * (al * x_ab + be * x_bb - sh) - qshift
+        other_first = al * (qalpha * x_aa + qbeta * x_ab - qshift) + be * (qalpha * x_ba + qbeta * x_bb - qshift) - sh
+        both = np.where(a[:, None] < ids[None, :], own_first, other_first)
+        new = clamp0(np.where(keep[None, :], both, new))
+        new[np.arange(len(a)), a] = 0
+        alive = self.alive
+        cols = np.flatnonzero(alive & ~keep)
+        for p in range(len(a)):
+            self.dist[cols, a[p]] = new[p, cols]
+        cols = np.flatnonzero(alive)
+        for p in range(len(a)):
+            self.dist[a[p], cols] = new[p, cols]
+        lim = self.limit is not None
+        cost, valid = pair_cost(new, total[:, None], self.mass[None, :],
+                                self.radius[a][:, None] if lim else None, self.radius[None, :] if lim else None,
+                                self.limit, alive[None, :] & (ids[None, :] != a[:, None]))
+        packed = pack(cost, ids[None, :] ^ a[:, None])
+        push = valid & ~keep[None, :]
+        for p in range(len(a)):
+            cols = np.flatnonzero(push[p])
+            self.packed[cols] = np.minimum(self.packed[cols], packed[p, cols])
+        self.packed[a] = packed.min(1)
+        self.trace.extend(zip(a.tolist(), b.tolist()))
+
+
+def reduce(mu, mass, count, limit, target, strict=False):
+    """Rounds until no mutual pair is left or ``count <= target``
+    (litgpt/log_kv_cache.py:3303-3376). Returns (survivors, trace, centers)."""
+    if count <= target:
+        return np.arange(count), [], f32(mu).copy()
+    r = Reducer(pair_distances(mu), mu, mass, count, limit, target)
+    size = r.mass.shape[0]
+    for _ in range(2 * size + 7):
+        if not r.step():
+            break
+    if strict and r.stuck:
+        raise RuntimeError("unified route: no mutual pair below the cluster budget")
+    return np.flatnonzero(r.alive), r.trace, r.mu
+
+
+def labels(size, survivors, trace):
+    """Leaf -> compact surviving row (litgpt/log_kv_cache.py:3544-3568)."""
+    parent = np.arange(size)
+    for a, b in trace:
+        parent[b] = a
+    while True:
+        nxt = parent[parent]
+        if np.array_equal(nxt, parent):
+            break
+        parent = nxt
+    compact = np.full(size, -1, np.int64)
+    compact[np.asarray(survivors, np.int64)] = np.arange(len(survivors))
+    return compact[parent]
+
+
+def ward_entry_order(order, p_lo, has_mass, split):
+    """Two-way stable merge of the keep (``[:split]``) and free entries
+    (litgpt/log_kv_cache.py:2425-2447)."""
+    left = sorted(range(split), key=lambda i: order[i])
+    right = sorted(range(split, len(order)), key=lambda i: order[i])
+    effective = [0] * len(order)
+    for seq in (left, right):
+        nxt = None
+        for i in reversed(seq):
+            if has_mass[i]:
+                nxt = p_lo[i]
+            effective[i] = order[i] if nxt is None else nxt
+    merged, i, j = [], 0, 0
+    while i < len(left) and j < len(right):
+        if effective[left[i]] <= effective[right[j]]:
+            merged.append(left[i])
+            i += 1
+        else:
+            merged.append(right[j])
+            j += 1
+    return merged + left[i:] + right[j:]
+
+
+def ward_merge(cache, b, g, keep, free):
+    """Merge old cluster ``free`` into ``keep`` (litgpt/log_kv_cache.py:2517-2580)."""
+    ents = [cache.ladder(b, g, c).entries() for c in (keep, free)]
+    rows = lad.concat(ents)
+    split = len(ents[0]["w"])
+    idx = ward_entry_order(rows["order"].tolist(), rows["p_lo"].tolist(), (rows["w"] > 0).tolist(), split)
+    rows = lad.take(rows, np.asarray(idx, np.int64))
+    rows["order"] = np.arange(len(idx), dtype=np.int64)
+    nk, nf = np.float32(cache.n_total[b, g, keep]), np.float32(cache.n_total[b, g, free])
+    mu = (nk * cache.centroid[b, g, keep] + nf * cache.centroid[b, g, free]) / np.maximum(nk + nf, np.float32(1))
+    ne = cache.n_eff[b, g, keep] + cache.n_eff[b, g, free]
+    total = int(cache.n_total[b, g, keep]) + int(cache.n_total[b, g, free])
+    high = max(int(cache.p_hi_c[b, g, keep]), int(cache.p_hi_c[b, g, free]))
+    for c in (keep, free):
+        cache.ladder(b, g, c).clear()
+        cache.alive[b, g, c] = False
+        cache.n_total[b, g, c] = 0
+        cache.p_hi_c[b, g, c] = -1
+        cache.level0_phase[b, g, c] = 0
+    cache.centroid[b, g, keep] = mu.astype(np.float32)
+    cache.n_eff[b, g, keep] = ne
+    cache.n_eff[b, g, free] = 0
+    cache.alive[b, g, keep] = True
+    cache.n_total[b, g, keep] = total
+    cache.p_hi_c[b, g, keep] = high
+    cache.level0_phase[b, g, keep] = len(idx)
+    if len(idx):
+        cache._append(b, g, keep, rows)
+
+
+def plan_lane(cache, keys, n, b, g):
+    """Both stages of one lane: (ward jobs [(keep, free)], target cluster root
+    per row as (root index, n_old, old ids, survivors))."""
+    limit = np.float32(math.sqrt(float(cache.lam) * float(cache.s_h[b, g])))
+    mu = f32(keys[:n])
+    surv1, trace1, mu1 = reduce(mu, np.ones(n, np.float32), n, limit, 1)
+    lab1 = labels(n, surv1, trace1)
+    old = np.flatnonzero(cache.alive[b, g])
+    weights = np.concatenate((cache.n_total[b, g, old].astype(np.float32),
+                              np.bincount(lab1, minlength=len(surv1)).astype(np.float32)))
+    centers = np.concatenate((cache.centroid[b, g, old].astype(np.float32), mu1[surv1]))
+    m2 = len(weights)
+    surv2, trace2, _ = reduce(centers, weights, m2, None, cache.K, strict=True)
+    lab2 = labels(m2, surv2, trace2)
+    jobs = [(int(old[a]), int(old[c])) for a, c in trace2 if c < len(old)]
+    root = lab2[len(old) + lab1]
+    return jobs, root, old, np.asarray(surv2)
+
+
+def route_unified(cache, ak, av, ap, counts):
+    """Unified route + commit of ``counts[b]`` rows of ``ak/av/ap``
+    (litgpt/log_kv_cache.py:3589-3688). Returns per lane the cluster of every
+    row (offset order), -1 past the count."""
+    ak, av = f32(ak), f32(av)
+    n_batch, n_groups, width, _ = ak.shape
+    out = np.full((n_batch, n_groups, width), -1, np.int64)
+    plans = {}
+    for b in range(n_batch):
+        n = int(counts[b])
+        if not n:
+            continue
+        for g in range(n_groups):
+            plans[(b, g)] = plan_lane(cache, ak[b, g], n, b, g)
+    for (b, g), (jobs, _, _, _) in plans.items():
+        for keep, free in jobs:
+            ward_merge(cache, b, g, keep, free)
+    jobs_all = {}
+    for (b, g), (_, root, old, surv2) in plans.items():
+        n = int(counts[b])
+        free_slots = iter(np.flatnonzero(~cache.alive[b, g]).tolist())
+        rows = np.argsort(ap[b, :n], kind="stable")   # the lane's rows in position order
+        by_root = root[rows]
+        for r in range(len(surv2)):
+            sel = rows[by_root == r]
+            if not len(sel):
+                continue
+            opened = surv2[r] >= len(old)
+            c = next(free_slots) if opened else int(old[surv2[r]])
+            jobs_all[(b, g, c)] = (opened, sel)
+            out[b, g, sel] = c
+    for (b, g, c), (new, rows) in sorted(jobs_all.items()):
+        if new:
+            t = rows[0]
+            cache.new_cluster(b, g, c, ak[b, g, t], av[b, g, t], int(ap[b, t]))
+            rows = rows[1:]
+        if not len(rows):
+            continue
+        pos = ap[b, rows].astype(np.int64)
+        if cache.P and pos.min() < cache.p_hi_c[b, g, c]:
+            cache.join_late(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
+        else:
+            cache.join(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
+    return out

@@ -1,0 +1,151 @@
+"""Pins of the oracle's unified route (oracle/unified.py) without the device.
+
+* known answers of the reducer, worked by hand from the reference's rules
+  (litgpt/log_kv_cache.py:437-637, docs/semantic-unified-routing.md:11-60):
+  Ward cost n_a n_b / (n_a + n_b) d^2 and the Lance-Williams update (three
+  points on a line merge at 0.5 then at 60.17 = 2/3 * 9.5^2); the radius bound
+  max(r_a + beta d, r_b + alpha d) stops the second merge under a limit of 0.6;
+  the symmetric ``row ^ col`` tie rule pairs (0,1) and (2,3) of four equally
+  spaced points in one round (a lowest-index rule would not); the budget takes
+  the cheapest pairs first;
+* the incremental rounds equal a full recompute (centers and distances rebuilt
+  from scratch every round) on separated data, as the reference states
+  (litgpt/log_kv_cache.py:449-455);
+* labels and the Ward entry order on hand-built cases;
+* route invariants: at most K live clusters, every row accounted for once,
+  n_total equal to the ladder mass, each candidate's rows within the radius
+  limit of its center; an old-old merge frees a cluster id that a new
+  candidate then opens.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from logkv_amd.workloads import Mixture
+from oracle import OracleCache
+from oracle import unified as U
+
+ONES = lambda n: np.ones(n, np.float32)  # noqa: E731
+
+
+def line(*x):
+    return np.asarray(x, np.float32)[:, None]
+
+
+def test_reducer_known_answers():
+    s, t, mu = U.reduce(line(0, 1, 10), ONES(3), 3, None, 1)
+    assert s.tolist() == [0] and t == [(0, 1), (0, 2)]
+    assert np.allclose(mu[0], [11 / 3])
+    s, t, _ = U.reduce(line(0, 1, 10), ONES(3), 3, 0.6, 1)
+    assert s.tolist() == [0, 2] and t == [(0, 1)]
+    s, t, _ = U.reduce(line(0, 1, 2, 3), ONES(4), 4, None, 1)
+    assert t == [(0, 1), (2, 3), (0, 2)]
+    s, t, _ = U.reduce(line(0, 1, 10, 10.5), ONES(4), 4, None, 2)
+    assert s.tolist() == [0, 2] and t == [(2, 3), (0, 1)]
+    s, t, _ = U.reduce(line(0, 1, 10, 10.5), ONES(4), 4, None, 3)
+    assert s.tolist() == [0, 1, 2] and t == [(2, 3)]
+
+
+def test_lance_williams_distance_is_the_merged_center_distance():
+    r = U.Reducer(U.pair_distances(line(0, 1, 10)), line(0, 1, 10), ONES(3), 3, None, 1)
+    r.step()
+    assert r.dist[0, 2] == r.dist[2, 0] == np.float32(90.25)
+    assert r.mass.tolist() == [2, 0, 1] and r.alive.tolist() == [True, False, True]
+    cost = (r.packed[0] >> np.uint64(32)).astype(np.uint32).view(np.float32)
+    assert cost == np.float32(np.float32(90.25) * (np.float32(2) / np.float32(3)))
+
+
+class _FullRecompute(U.Reducer):
+    """Every round rebuilds distances from the current centers and rescans every row."""
+
+    def step(self):
+        live = np.flatnonzero(self.alive)
+        d = U.pair_distances(self.mu)
+        self.dist[np.ix_(live, live)] = d[np.ix_(live, live)]
+        self.packed[live] = self._scan(live)
+        return super().step()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("limit", [None, 6.0])
+def test_incremental_rounds_equal_full_recompute(seed, limit):
+    rng = np.random.default_rng(seed)
+    centers = rng.standard_normal((6, 16)).astype(np.float32) * 8
+    x = (centers[rng.integers(0, 6, 40)] + rng.standard_normal((40, 16)) * 0.7).astype(np.float32)
+    mass = np.ones(40, np.float32)
+    runs = []
+    for cls in (U.Reducer, _FullRecompute):
+        r = cls(U.pair_distances(x), x, mass, 40, limit, 4 if limit is None else 1)
+        for _ in range(200):
+            if not r.step():
+                break
+        runs.append((np.flatnonzero(r.alive).tolist(), r.trace))
+    assert runs[0] == runs[1]
+    assert len(runs[0][1]) > 10
+
+
+def test_labels_and_ward_entry_order():
+    assert U.labels(5, [0, 4], [(0, 1), (2, 3), (0, 2)]).tolist() == [0, 0, 0, 0, 1]
+    # keep entries: order 0..2 at p_lo 5, 7, 9; free: order 0..1 at p_lo 6, 8
+    assert U.ward_entry_order([0, 1, 2, 0, 1], [5, 7, 9, 6, 8], [1, 1, 1, 1, 1], 3) == [0, 3, 1, 4, 2]
+    # a massless keep entry takes the p_lo of the next massive entry (9)
+    assert U.ward_entry_order([0, 1, 2, 0, 1], [5, 7, 9, 6, 8], [1, 0, 1, 1, 1], 3) == [0, 3, 4, 1, 2]
+    # stored out of order: each side is sorted by order first
+    assert U.ward_entry_order([2, 0, 1, 0], [9, 5, 7, 6], [1, 1, 1, 1], 3) == [1, 3, 2, 0]
+
+
+def _stream(cache, batch, groups, dim, T, n, exact, seed=3):
+    mix = Mixture(batch, groups, dim, clusters=6, seed=seed, drift_every=3 * T)
+    total = 0
+    for i in range(n):
+        k, v = mix.rows(T).float().numpy(), mix.rows(T).float().numpy()
+        pos = np.broadcast_to(np.arange(i * T, (i + 1) * T), (batch, T)).copy()
+        ends = [[(p + 3 * b) % 5 == 0 for p in range(i * T, (i + 1) * T)] for b in range(batch)] if exact else None
+        cache.flush_rows(k, v, pos, ends)
+        total += T
+        yield total
+
+
+@pytest.mark.parametrize("exact", [0, 8])
+def test_route_invariants(exact):
+    batch, groups, dim, T, K = 2, 2, 16, 24, 4
+    c = OracleCache(batch, groups, 4096, dim, dim, B=8, recent_size=T, K=K, s_h=4.0, flush=T, exact_tokens=exact,
+                    span_max=4, unified=True)
+    for total in _stream(c, batch, groups, dim, T, 8, exact):
+        assert (c.alive.sum(-1) <= K).all()
+        mass = c.level_w.sum((2, 3, 4)) + (c.alpha_valid.sum(-1)[:, None] if exact else 0)
+        assert (mass == total).all()
+        assert (c.level_w.sum((-1, -2)) == c.n_total).all()
+        assert ((c.level_w.sum((-1, -2)) > 0) == c.alive).all()
+
+
+def test_candidates_respect_the_radius():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 8))[rng.integers(0, 3, 60)] * 6 + rng.standard_normal((60, 8))).astype(np.float32)
+    limit = np.float32(math.sqrt(4.0))
+    surv, trace, mu = U.reduce(x, ONES(60), 60, limit, 1)
+    lab = U.labels(60, surv, trace)
+    assert len(trace) > 20
+    for r, root in enumerate(surv):
+        members = x[lab == r]
+        far = np.sqrt(((members - mu[root]) ** 2).sum(-1)).max()
+        assert far <= limit * (1 + 1e-5)
+
+
+def test_old_old_merge_frees_a_cluster_for_a_new_candidate():
+    dim = 8
+    c = OracleCache(1, 1, 256, dim, dim, B=4, recent_size=4, K=2, s_h=1.0, flush=4, unified=True)
+    e = np.eye(dim, dtype=np.float32)
+    c.new_cluster(0, 0, 0, e[0] * 1, e[0], 10)
+    c.join(0, 0, 0, np.stack([e[0] * 1.1]), np.stack([e[0]]), np.asarray([11]))
+    c.new_cluster(0, 0, 1, e[0] * 2, e[1], 12)
+    rows = np.stack([e[2] * 50, e[2] * 50.2, e[2] * 50.1, e[2] * 49.9])[None, None]
+    out = c.flush_rows(rows, rows, np.arange(20, 24)[None])
+    # the two old clusters (1.05 e0 and 2 e0) are the cheapest pair: 1 merges into 0
+    assert c.n_total[0, 0].tolist() == [3, 4]
+    assert c.p_hi_c[0, 0].tolist() == [12, 23]
+    assert out[0, 0].tolist() == [1, 1, 1, 1]
+    w = c.level_w[0, 0, 0].reshape(-1)
+    assert sorted(c.level_p_lo[0, 0, 0].reshape(-1)[w > 0].tolist()) == [10, 11, 12]
