@@ -100,6 +100,37 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
                       const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
                       const int8_t* assign, const int32_t* order, void* stream);
 
+/* Unified (Ward / radius) route: bytes of scratch for logkv_unified_plan /
+ * logkv_unified_commit (the route workspace sized for old-old merges, then
+ * the reducer's per-lane distance matrices [T + K]^2 f32, centers and traces).
+ * At most T + K <= 4608 per flush. */
+int64_t logkv_unified_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins);
+
+/* The decisions of one unified-routed flush, per lane (batch row, KV group):
+ * the valid rows merge into candidates by mutual-nearest Ward rounds under
+ * the radius limit limits[lane] (f32 [lanes] = sqrt(lambda * s_h)), then old
+ * live clusters and candidates merge until at most K remain; every row's
+ * final cluster and the lane's old-old merges stay in the workspace.
+ * summary (device int32[2]) receives the most old-old merges of any lane and
+ * 1 if a budget stage stopped above K with no pair left (an error).
+ * Replaces _semantic_route_unified's planning (litgpt/log_kv_cache.py:
+ * 3589-3660) with _semantic_unified_reduce_device / _incremental and
+ * _UnifiedReduceTorch / UnifiedReduce (litgpt/log_kv_cache.py:3225-3376,
+ * :448-637; litgpt/log_kv_route_triton.py:197-838) and the labels
+ * (litgpt/log_kv_cache.py:3544-3568). */
+int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
+                       const float* limits, void* workspace, int64_t workspace_bytes, int32_t* summary, void* stream);
+
+/* Applies a plan left in the same workspace by logkv_unified_plan: merge_steps
+ * (summary[0]) rounds of old-old merges, each the lane's next merge (both
+ * ladders' entries re-appended into the lower cluster), then the commit of
+ * the rows into their clusters (new clusters open the free ids in root
+ * order). Replaces _semantic_ward_merge_batch (litgpt/log_kv_cache.py:
+ * 2517-2580) and the commit tail of _semantic_route_unified (:3661-3688). */
+int logkv_unified_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                         const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                         int32_t merge_steps, void* stream);
+
 /* Route op-log of a cache (litgpt/log_kv_cache.py:2006-2096): per lane (batch
  * row, KV group) int32 rows (op, cluster, arg, position) at rows[lane,
  * 0 .. lengths[lane]), op codes as the reference's (litgpt/log_kv_cache.py:

@@ -3,7 +3,10 @@
 #include <cstdarg>
 #include <cstring>
 
+#include <algorithm>
+
 #include "route.hpp"
+#include "unified.hpp"
 
 namespace {
 
@@ -59,13 +62,14 @@ struct Plan {
   int32_t sort_width;
 };
 
-Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
+// ward: the unified route's old-old merges stage both ladders' entries at level 0.
+Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late, int32_t ward = 0) {
   Plan p{};
   const int64_t lanes = int64_t(c->n_batch) * c->n_groups;
   const int64_t ladders = lanes * c->k_max;
   const int64_t existing = late ? int64_t(c->levels) * c->slots : 0;
-  const int64_t m0 = tokens + existing;
-  p.s0 = late ? m0 : 0;
+  const int64_t m0 = std::max<int64_t>(tokens + existing, ward ? 2 * int64_t(c->levels) * c->slots : 0);
+  p.s0 = late || ward ? m0 : 0;
   p.m0 = m0;
   p.stride = align256(logkv::ladder_scratch_bytes(*c, p.s0, p.m0));
   int64_t off = 0;
@@ -95,7 +99,7 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late) {
 }
 
 int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_route_params* prm, void* workspace,
-          int64_t bytes, int8_t* assign, int32_t* order, logkv::Workspace& ws) {
+          int64_t bytes, int8_t* assign, int32_t* order, logkv::Workspace& ws, int ward = 0) {
   int rc = check_ladder(c);
   if (rc) return rc;
   if ((rc = check_rows(c, r))) return rc;
@@ -103,7 +107,9 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   const int late = prm->late_joins ? 1 : 0;
   if (late && int64_t(c->levels) * c->slots + r->tokens > logkv::kMaxOrderRows)
     return fail(LOGKV_EINVAL, "delayed archive sort needs L*B' + T <= %d", logkv::kMaxOrderRows);
-  const Plan p = plan_for(c, r->tokens, late);
+  if (ward && 2 * int64_t(c->levels) * c->slots > logkv::kMaxOrderRows)
+    return fail(LOGKV_EINVAL, "old-old merges need 2*L*B' <= %d", logkv::kMaxOrderRows);
+  const Plan p = plan_for(c, r->tokens, late, ward);
   if (!workspace || bytes < p.total)
     return fail(LOGKV_EINVAL, "workspace of %lld bytes is smaller than the %lld required", (long long)bytes,
                 (long long)p.total);
@@ -124,11 +130,110 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   return LOGKV_OK;
 }
 
+// The unified route's region, after the route workspace sized for old-old
+// merges. With base == NULL only the size is computed.
+int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late, uint8_t* base,
+                       logkv::UnifiedBufs* u) {
+  const int64_t lanes = int64_t(c->n_batch) * c->n_groups;
+  const int64_t M = int64_t(tokens) + c->k_max, D = c->dk;
+  int64_t off = align256(plan_for(c, tokens, late, 1).total);
+  auto take = [&](int64_t bytes) {
+    uint8_t* at = base ? base + off : nullptr;
+    off += align256(bytes);
+    return at;
+  };
+  logkv::UnifiedBufs b{};
+  b.M = static_cast<int32_t>(M);
+  b.D = static_cast<int32_t>(D);
+  b.mu1 = reinterpret_cast<float*>(take(lanes * M * D * 4));
+  b.mass1 = reinterpret_cast<float*>(take(lanes * M * 4));
+  b.count1 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.mu2 = reinterpret_cast<float*>(take(lanes * M * D * 4));
+  b.mass2 = reinterpret_cast<float*>(take(lanes * M * 4));
+  b.count2 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.dist = reinterpret_cast<float*>(take(lanes * M * M * 4));
+  b.bound = reinterpret_cast<float*>(take(lanes * M * 4));
+  b.alive1 = take(lanes * M);
+  b.alive2 = take(lanes * M);
+  b.trace1 = reinterpret_cast<int32_t*>(take(lanes * M * 8));
+  b.trace2 = reinterpret_cast<int32_t*>(take(lanes * M * 8));
+  b.n_trace1 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.n_trace2 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.stuck1 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.stuck2 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.label1 = reinterpret_cast<int32_t*>(take(lanes * M * 4));
+  b.label2 = reinterpret_cast<int32_t*>(take(lanes * M * 4));
+  b.n_roots1 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.n_roots2 = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.n_old = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.old_ids = reinterpret_cast<int32_t*>(take(lanes * logkv::kMaxClusters * 4));
+  b.jobs = reinterpret_cast<int32_t*>(take(lanes * logkv::kMaxClusters * 8));
+  b.n_jobs = reinterpret_cast<int32_t*>(take(lanes * 4));
+  if (u) *u = b;
+  return off;
+}
+
+int check_unified(const logkv_ladder_view* c, const logkv_rows_view* r) {
+  if (int64_t(r->tokens) + c->k_max > logkv::kMaxNodes)
+    return fail(LOGKV_EINVAL, "the unified route takes at most %d rows + clusters per flush, got %d + %d",
+                logkv::kMaxNodes, r->tokens, c->k_max);
+  if (logkv::unified_reduce_lds(r->tokens + c->k_max) > 160 * 1024)
+    return fail(LOGKV_EINVAL, "unified reducer state exceeds the LDS of a CU");
+  return LOGKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* logkv_last_error(void) { return g_error; }
+
+int64_t logkv_unified_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins) {
+  if (check_ladder(cache) || tokens < 0) return -1;
+  return unified_layout(cache, tokens, late_joins ? 1 : 0, nullptr, nullptr);
+}
+
+int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
+                       const float* limits, void* workspace, int64_t workspace_bytes, int32_t* summary, void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, nullptr, nullptr, ws, 1);
+  if (rc) return rc;
+  if ((rc = check_unified(cache, rows))) return rc;
+  if (!limits || !summary) return fail(LOGKV_EINVAL, "radius limits or summary are NULL");
+  const int64_t need = unified_layout(cache, rows->tokens, params->late_joins ? 1 : 0, nullptr, nullptr);
+  if (workspace_bytes < need)
+    return fail(LOGKV_EINVAL, "workspace of %lld bytes is smaller than the %lld required", (long long)workspace_bytes,
+                (long long)need);
+  logkv::UnifiedBufs u{};
+  unified_layout(cache, rows->tokens, params->late_joins ? 1 : 0, static_cast<uint8_t*>(workspace), &u);
+  u.limit = limits;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = rows->tokens ? logkv::launch_unified_plan(*cache, *rows, u, ws, s) : LOGKV_OK;
+  if (!rc) rc = logkv::launch_unified_summary(*cache, u, summary, rows->tokens, s);
+  if (rc) return fail(rc, "unified plan launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_unified_commit(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
+                         void* workspace, int64_t workspace_bytes, int32_t merge_steps, void* stream) {
+  logkv::Workspace ws{};
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, nullptr, nullptr, ws, 1);
+  if (rc) return rc;
+  if ((rc = check_unified(cache, rows))) return rc;
+  if (merge_steps < 0 || merge_steps > cache->k_max) return fail(LOGKV_EINVAL, "merge steps outside [0, K]");
+  if (!rows->tokens) return LOGKV_OK;
+  logkv::UnifiedBufs u{};
+  unified_layout(cache, rows->tokens, params->late_joins ? 1 : 0, static_cast<uint8_t*>(workspace), &u);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int step = 0; step < merge_steps && !rc; ++step) {
+    rc = logkv::launch_ward_step(*cache, ws, u.jobs, u.n_jobs, step, s);
+    if (!rc) rc = logkv::launch_levels(*cache, *rows, *params, ws, s);
+  }
+  if (!rc) rc = logkv::launch_snapshot(*cache, ws, s);
+  if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
+  if (rc) return fail(rc, "unified commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
 
 int64_t logkv_route_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins) {
   if (check_ladder(cache) || tokens < 0) return -1;

@@ -15,6 +15,7 @@
 #include <algorithm>
 
 #include "route.hpp"
+#include "unified.hpp"
 
 namespace logkv {
 
@@ -1230,7 +1231,185 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs
   if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * c.levels + ell] = static_cast<int16_t>(n);
 }
 
+// Old-old merge of the unified route (litgpt/log_kv_cache.py:2517-2580), one
+// block per lane: the lane's step-th merge (keep, retire), if it has one. The
+// two ladders' entries are ordered by the reference's entry rule
+// (litgpt/log_kv_cache.py:2395-2447): each side stably by order, an entry's
+// key the p_lo of the next massive entry at or after it on its side (its own
+// order if there is none), the sides merged keep-first on ties. They are
+// gathered in that order into the keep ladder's level-0 staging with order =
+// rank, both ladders are cleared, the keep cluster takes the n_total-weighted
+// center, the summed n_eff and n_total, the larger p_hi and phase = entries,
+// the retired cluster is emptied (its center is left as it was), and the level
+// launches re-append the staged rows. Every other ladder of the lane gets an
+// inactive plan.
+__global__ __launch_bounds__(kThreads) void ward_kernel(LadderArgs c, Workspace ws, const int32_t* jobs,
+                                                        const int32_t* n_jobs, int step) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int start_s[2 * kMaxLevels + 2];
+  __shared__ int16_t cnt_s[2 * kMaxLevels];
+  const int lane = blockIdx.x, K = c.k_max, L = c.levels, B = c.slots, dk = c.dk, dv = c.dv;
+  for (int cc = threadIdx.x; cc < K; cc += kThreads) {
+    ws.plans[static_cast<int64_t>(lane) * K + cc].active = 0;
+    ws.plans[static_cast<int64_t>(lane) * K + cc].m_tok = 0;
+  }
+  if (step >= n_jobs[lane]) return;
+  const int keep = jobs[(static_cast<int64_t>(lane) * kMaxClusters + step) * 2];
+  const int retire = jobs[(static_cast<int64_t>(lane) * kMaxClusters + step) * 2 + 1];
+  const int kl = lane * K + keep, fl = lane * K + retire;
+  const Ladder side[2] = {ladder_of(c, kl), ladder_of(c, fl)};
+  for (int e = threadIdx.x; e < L; e += kThreads) {
+    cnt_s[e] = c.level_count[static_cast<int64_t>(kl) * L + e];
+    cnt_s[L + e] = c.level_count[static_cast<int64_t>(fl) * L + e];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int e = 0; e < 2 * L; ++e) {
+      start_s[e] = acc;
+      acc += cnt_s[e];
+    }
+    start_s[2 * L] = acc;
+  }
+  __syncthreads();
+  const int n_k = start_s[L], total = start_s[2 * L];
+  // Entry i -> (side, slot): levels of the keep ladder, then of the retired one.
+  auto where = [&](int i, int& sd, int64_t& slot) {
+    int e = 0;
+    while (e + 1 < 2 * L && start_s[e + 1] <= i) ++e;
+    sd = e >= L ? 1 : 0;
+    slot = static_cast<int64_t>(e - sd * L) * B + (i - start_s[e]);
+  };
+  int width = 1;
+  while (width < total) width <<= 1;
+  uint64_t* keys = reinterpret_cast<uint64_t*>(dyn);
+  int64_t* eff = reinterpret_cast<int64_t*>(keys + width);
+  int16_t* merged = reinterpret_cast<int16_t*>(eff + total);
+  for (int i = threadIdx.x; i < width; i += kThreads) {
+    uint64_t key = ~0ull;
+    if (i < total) {
+      int sd;
+      int64_t slot;
+      where(i, sd, slot);
+      key = (static_cast<uint64_t>(sd) << 63) | (static_cast<uint64_t>(side[sd].ord[slot]) << kOrderIndexBits) |
+            static_cast<uint64_t>(i);
+    }
+    keys[i] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= width; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < width; t += kThreads) {
+        const int partner = t ^ stride;
+        if (partner > t) {
+          const bool up = (t & size) == 0;
+          const uint64_t a = keys[t], bk = keys[partner];
+          if ((a > bk) == up) {
+            keys[t] = bk;
+            keys[partner] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (threadIdx.x == 0) {
+    // Keys: the next massive entry's p_lo on the same side, else the entry's order.
+    for (int sd = 0; sd < 2; ++sd) {
+      const int lo = sd ? n_k : 0, hi = sd ? total : n_k;
+      bool have = false;
+      int64_t next = 0;
+      for (int j = hi - 1; j >= lo; --j) {
+        int s2;
+        int64_t slot;
+        where(static_cast<int>(keys[j] & kOrderIndexMask), s2, slot);
+        if (side[s2].w[slot] > 0.f) {
+          have = true;
+          next = side[s2].lo[slot];
+        }
+        eff[j] = have ? next : side[s2].ord[slot];
+      }
+    }
+    int i = 0, j = n_k, rank = 0;
+    while (i < n_k && j < total) merged[rank++] = static_cast<int16_t>(eff[i] <= eff[j] ? i++ : j++);
+    while (i < n_k) merged[rank++] = static_cast<int16_t>(i++);
+    while (j < total) merged[rank++] = static_cast<int16_t>(j++);
+  }
+  __syncthreads();
+  const Soa S0 = s0_of(ws, kl, dk, dv);
+  {
+    const RowUnits ru(dk, dv);
+    for (int r0 = ru.r0; r0 < total; r0 += ru.step) {
+      int sd;
+      int64_t slot;
+      where(static_cast<int>(keys[merged[r0]] & kOrderIndexMask), sd, slot);
+      const uint2 x = load_unit(side[sd].k + slot * dk, side[sd].v + slot * dv, ru.u, ru.ku);
+      store_unit(S0.k + static_cast<int64_t>(r0) * dk, S0.v + static_cast<int64_t>(r0) * dv, ru.u, ru.ku, x);
+    }
+  }
+  for (int rank = threadIdx.x; rank < total; rank += kThreads) {
+    int sd;
+    int64_t slot;
+    where(static_cast<int>(keys[merged[rank]] & kOrderIndexMask), sd, slot);
+    Meta mt = slot_meta(side[sd], slot);
+    mt.ord = rank;
+    put_soa_meta(S0, rank, mt);
+  }
+  // Center and scalars (the reads precede every write of the same value).
+  const int64_t ck = static_cast<int64_t>(kl), cf = static_cast<int64_t>(fl);
+  const float nk = static_cast<float>(c.n_total[ck]), nf = static_cast<float>(c.n_total[cf]);
+  for (int d = threadIdx.x; d < dk; d += kThreads) {
+    const float mk = c.centroid[ck * dk + d], mf = c.centroid[cf * dk + d];
+    const float den = nk + nf;
+    c.centroid[ck * dk + d] = (nk * mk + nf * mf) / (den < 1.f ? 1.f : den);
+  }
+  __syncthreads();
+  clear_slots(side[0], 0, static_cast<int64_t>(L) * B);
+  clear_slots(side[1], 0, static_cast<int64_t>(L) * B);
+  for (int e = threadIdx.x; e < L; e += kThreads) {
+    c.level_count[ck * L + e] = 0;
+    c.level_count[cf * L + e] = 0;
+  }
+  if (threadIdx.x == 0) {
+    c.n_eff[ck] = c.n_eff[ck] + c.n_eff[cf];
+    c.n_eff[cf] = 0.f;
+    c.n_total[ck] = c.n_total[ck] + c.n_total[cf];
+    c.n_total[cf] = 0;
+    c.p_hi_c[ck] = imax64(c.p_hi_c[ck], c.p_hi_c[cf]);
+    c.p_hi_c[cf] = -1;
+    c.level0_phase[ck] = total;
+    c.level0_phase[cf] = 0;
+    c.alive[ck] = 1;
+    c.alive[cf] = 0;
+    LadderPlan pl;
+    pl.active = total > 0 ? 1 : 0;
+    pl.kind0 = 1;
+    pl.m_tok = 0;
+    pl.first = 0;
+    pl.order_base = 0;
+    int mm = total;
+    for (int e = 0; e < kMaxLevels; ++e) {
+      const bool used = e < L;
+      pl.cnt[e] = 0;
+      pl.m[e] = used ? mm : 0;
+      mm = used ? carries_of(0, mm, B, e == L - 1) : 0;
+    }
+    ws.plans[ck] = pl;
+  }
+}
+
 constexpr int kCarryBlocks = 2048;   // most blocks of a carries launch (8 per CU)
+
+int launch_ward_step(const LadderArgs& c, const Workspace& ws, const int32_t* jobs, const int32_t* n_jobs, int step,
+                     hipStream_t stream) {
+  const int lanes = c.n_batch * c.n_groups;
+  int width = 1;
+  while (width < 2 * c.levels * c.slots) width <<= 1;
+  const size_t shmem = static_cast<size_t>(width) * 8 + static_cast<size_t>(2 * c.levels * c.slots) * 10 + 16;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&ward_kernel), shmem)) return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(ward_kernel, dim3(lanes), dim3(kThreads), shmem, stream, c, ws, jobs, n_jobs, step);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
 
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
@@ -1242,6 +1421,15 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel), shmem)) return LOGKV_ERUNTIME;
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
+  return launch_levels(c, r, p, ws, stream);
+}
+
+// The level launches that follow a prepare step (commit_kernel or ward_kernel):
+// carry work units, carries per level, then the slot writes of every level.
+int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
+                  hipStream_t stream) {
+  const int ladders = c.n_batch * c.n_groups * c.k_max;
+  const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
   if (c.levels > 1) {
     hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kCarryThreads), 0, stream, c, p, ws);
     const size_t carry_shmem = (static_cast<size_t>(ladders) + 1) * 4;

@@ -1,0 +1,624 @@
+// Unified (Ward / radius) route on the device.
+//
+// Follows litgpt/log_kv_cache.py:3589-3688 (the route), :448-637 (the
+// incremental mutual-nearest rounds of _UnifiedReduceTorch and the Triton
+// UnifiedReduce, litgpt/log_kv_route_triton.py:197-838), :3544-3568 (labels),
+// docs/semantic-unified-routing.md:11-96. Per lane (batch row, KV group):
+//   1. candidates: the flushed rows start as singletons and merge in mutual-
+//      nearest Ward pairs while the radius bound stays under sqrt(lambda s_h);
+//   2. budget: old live clusters and candidates merge until at most K remain;
+//   3. old-old merges (ladder re-appends, in ladder.hip) and the commit of the
+//      rows into their final clusters (the attach commit).
+// One workgroup per lane runs every round of a stage, with the per-row state
+// (cached row minima, masses, radii, flags, pair table) in LDS and the squared
+// distance matrix in HBM; a round's phases are separated by barriers, so a
+// stage is one launch with no host round trip. Every element operation keeps
+// the reference's float32 order (_unified_pair_cost, _merge); the initial
+// squared distances and the radius check's exact distances are canonical
+// wave sums of squared differences (common.hpp).
+#include "route.hpp"
+#include "unified.hpp"
+
+namespace logkv {
+
+namespace {
+
+constexpr int kReduceThreads = 1024;
+constexpr int kReduceWaves = kReduceThreads / kWave;
+constexpr uint64_t kInfKey = 0x7F800000ull << 32;
+constexpr uint8_t kAlive = 1, kValid = 2, kKeep = 4, kMerged = 8, kRejected = 16;
+
+__device__ __forceinline__ uint64_t pack_cost(float cost, int key) {
+  const uint32_t bits = cost == 0.f ? 0u : __float_as_uint(cost);
+  return (static_cast<uint64_t>(bits) << 32) | static_cast<uint32_t>(key);
+}
+
+__device__ __forceinline__ float key_cost(uint64_t k) { return __uint_as_float(static_cast<uint32_t>(k >> 32)); }
+
+// Ward cost of merging rows of masses mi, mj at squared distance d2, +inf when
+// not allowed (litgpt/log_kv_cache.py:437-445, same operation order).
+template <bool LIMIT>
+__device__ __forceinline__ float ward_cost(float d2, float mi, float mj, float ri, float rj, float limit,
+                                           bool valid) {
+  const float sum = mi + mj;
+  const float denom = sum < 1.f ? 1.f : sum;
+  valid = valid && mi > 0.f && mj > 0.f;
+  if (LIMIT) {
+    const float distance = sqrtf(d2);
+    const float x = ri + (mj / denom) * distance, y = rj + (mi / denom) * distance;
+    valid = valid && (x < y ? y : x) <= limit;
+  }
+  return valid ? d2 * (mi * mj / denom) : __builtin_inff();
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, kWave);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+struct ReduceLds {
+  uint64_t* packed;   // [M] cached row minimum: cost bits << 32 | (row ^ col)
+  uint64_t* keys;     // [P2] proposals sorted by (cost, row)
+  float* mass;        // [M]
+  float* radius;      // [M]
+  float* p_alpha;     // [M/2] per merge of the round
+  float* p_beta;
+  float* p_shift;
+  int16_t* best;      // [M]
+  int16_t* pair_of;   // [M] merge index of a kept row
+  uint8_t* flags;     // [M]
+};
+
+__host__ __device__ inline int half_up(int m) { return (m + 1) / 2; }
+__host__ __device__ inline int pow2_at_least(int n) {
+  int w = 1;
+  while (w < n) w <<= 1;
+  return w;
+}
+
+__host__ __device__ inline size_t reduce_lds_bytes(int M) {
+  const int H = half_up(M), P2 = pow2_at_least(H > 0 ? H : 1);
+  return static_cast<size_t>(M) * 8 + static_cast<size_t>(P2) * 8 + static_cast<size_t>(M) * 8 +
+         static_cast<size_t>(H) * 12 + static_cast<size_t>(M) * 5 + 64;
+}
+
+__device__ inline ReduceLds carve_lds(uint8_t* dyn, int M) {
+  const int H = half_up(M), P2 = pow2_at_least(H > 0 ? H : 1);
+  ReduceLds s;
+  s.packed = reinterpret_cast<uint64_t*>(dyn);
+  s.keys = s.packed + M;
+  s.mass = reinterpret_cast<float*>(s.keys + P2);
+  s.radius = s.mass + M;
+  s.p_alpha = s.radius + M;
+  s.p_beta = s.p_alpha + H;
+  s.p_shift = s.p_beta + H;
+  s.best = reinterpret_cast<int16_t*>(s.p_shift + H);
+  s.pair_of = s.best + M;
+  s.flags = reinterpret_cast<uint8_t*>(s.pair_of + M);
+  return s;
+}
+
+// Packed minimum of row r over the live columns (litgpt/log_kv_cache.py:
+// 473-488); the row's own column contributes (inf, key 0), so a row without a
+// finite cost packs to the infinite key.
+template <bool LIMIT>
+__device__ uint64_t scan_row(const ReduceLds& s, const float* dist, int M, int n, int r, float limit) {
+  const float mr = s.mass[r], rr = s.radius[r];
+  uint64_t best = kInfKey;
+  const float* row = dist + static_cast<int64_t>(r) * M;
+  for (int c = lane_id(); c < n; c += kWave) {
+    const float cost = ward_cost<LIMIT>(row[c], mr, s.mass[c], rr, s.radius[c], limit, c != r);
+    const uint64_t k = pack_cost(cost, r ^ c);
+    best = k < best ? k : best;
+  }
+  return wave_min_u64(best);
+}
+
+}  // namespace
+
+// Rows -> f32 nodes with mass 1 (rows past the lane's count: mass 0), one block per (row tile, lane).
+__global__ __launch_bounds__(256) void load_nodes_kernel(RowsArgs r, int n_groups, UnifiedBufs u) {
+  const int lane = blockIdx.y, b = lane / n_groups, g = lane % n_groups;
+  const int n = valid_rows(r, b), M = u.M, D = u.D;
+  const uint16_t* kb = r.k + b * r.k_sb + g * r.k_sg;
+  float* mu = u.mu1 + static_cast<int64_t>(lane) * M * D;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < M * D; i += gridDim.x * 256) {
+    const int row = i / D, d = i - row * D;
+    mu[i] = row < n ? bf16_to_f32(kb[static_cast<int64_t>(row) * r.k_st + d]) : 0.f;
+  }
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < M; i += gridDim.x * 256)
+    u.mass1[static_cast<int64_t>(lane) * M + i] = i < n ? 1.f : 0.f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) u.count1[lane] = n;
+}
+
+// Squared distances of one row i against columns j > i (canonical wave sums of
+// squared differences, four columns folded at once), mirrored; zero diagonal.
+// Block = 4 waves per (row, lane).
+__global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu, const int32_t* __restrict__ count,
+                                                   float* __restrict__ dist, int M, int D) {
+  const int lane = blockIdx.y, i = blockIdx.x, n = count[lane];
+  if (i >= n) return;
+  const float* base = mu + static_cast<int64_t>(lane) * M * D;
+  float* dl = dist + static_cast<int64_t>(lane) * M * M;
+  const int l = lane_id(), w = wave_id();
+  float xi[kMaxDim / kWave];
+#pragma unroll
+  for (int q = 0; q < kMaxDim / kWave; ++q) xi[q] = feat_or_zero(gp(base + static_cast<int64_t>(i) * D), l + q * kWave, D);
+  if (w == 0 && l == 0) dl[static_cast<int64_t>(i) * M + i] = 0.f;
+  const int J = (D + kWave - 1) / kWave;
+  for (int j0 = i + 1 + 4 * w; j0 < n; j0 += 16) {
+    float s[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j = min(j0 + c, n - 1);
+      const LOGKV_G float* xj = gp(base + static_cast<int64_t>(j) * D);
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < kMaxDim / kWave; ++q) {
+        if (q < J) {
+          const float diff = xi[q] - feat_or_zero(xj, l + q * kWave, D);
+          acc = q == 0 ? diff * diff : acc + diff * diff;
+        }
+      }
+      s[c] = acc;
+    }
+    float t[4];
+    wave_sum4(s[0], s[1], s[2], s[3], t[0], t[1], t[2], t[3]);
+    if (l < 4 && j0 + l < n) {
+      const float v = l == 0 ? t[0] : l == 1 ? t[1] : l == 2 ? t[2] : t[3];
+      const int j = j0 + l;
+      dl[static_cast<int64_t>(i) * M + j] = v;
+      dl[static_cast<int64_t>(j) * M + i] = v;
+    }
+  }
+}
+
+// All rounds of one stage for one lane (litgpt/log_kv_cache.py:490-637).
+template <bool LIMIT>
+__global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceArgs a) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int s_count, s_nprop, s_nvalid, s_ntrace;
+  const int lane = blockIdx.x, M = a.M, D = a.D, t = threadIdx.x, l = lane_id(), w = wave_id();
+  const int n = a.count[lane];
+  const ReduceLds s = carve_lds(dyn, M);
+  float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  float* mu = a.mu + static_cast<int64_t>(lane) * M * D;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  int32_t* trace = a.trace + static_cast<int64_t>(lane) * M * 2;
+  for (int i = t; i < M; i += kReduceThreads) {
+    s.mass[i] = i < n ? a.mass[static_cast<int64_t>(lane) * M + i] : 0.f;
+    s.radius[i] = 0.f;
+    s.flags[i] = i < n ? kAlive : 0;
+    s.packed[i] = kInfKey;
+    s.best[i] = static_cast<int16_t>(i);
+  }
+  if (t == 0) {
+    s_count = n;
+    s_ntrace = 0;
+  }
+  __syncthreads();
+  bool stuck = false;
+  if (n > a.target) {
+    for (int r = w; r < n; r += kReduceWaves) {
+      const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
+      if (l == 0) s.packed[r] = k;
+    }
+    __syncthreads();
+    for (int round = 0; round < 2 * M + 7; ++round) {
+      // Proposals: every row's cached partner; a pair is proposed by its lower row.
+      for (int r = t; r < M; r += kReduceThreads) {
+        int bst = static_cast<int>(static_cast<uint32_t>(s.packed[r]) ^ static_cast<uint32_t>(r));
+        bst = bst < 0 ? 0 : (bst > M - 1 ? M - 1 : bst);
+        s.best[r] = static_cast<int16_t>(bst);
+      }
+      if (t == 0) {
+        s_nprop = 0;
+        s_nvalid = 0;
+      }
+      __syncthreads();
+      int mine = 0;
+      for (int r = t; r < n; r += kReduceThreads) {
+        const int bst = s.best[r];
+        const bool v = (s.flags[r] & kAlive) && r < bst && s.best[bst] == r && key_cost(s.packed[r]) < __builtin_inff();
+        if (v) {
+          s.flags[r] |= kValid;
+          ++mine;
+        }
+      }
+      if (mine) atomicAdd(&s_nprop, mine);
+      __syncthreads();
+      const int nprop = s_nprop;
+      if (LIMIT) {
+        // Exact radius check of every proposal (litgpt/log_kv_cache.py:503-525).
+        for (int r = w; r < n; r += kReduceWaves) {
+          if (!(s.flags[r] & kValid)) continue;
+          const int o = s.best[r];
+          const float* xr = mu + static_cast<int64_t>(r) * D;
+          const float* xo = mu + static_cast<int64_t>(o) * D;
+          float acc = 0.f;
+          for (int q = 0; q * kWave < D; ++q) {
+            const int d = l + q * kWave;
+            const float diff = feat_or_zero(gp(xr), d, D) - feat_or_zero(gp(xo), d, D);
+            acc = q == 0 ? diff * diff : acc + diff * diff;
+          }
+          const float exact2 = wave_sum0(acc);
+          if (l == 0) {
+            const float exact = sqrtf(exact2);
+            const float ma = s.mass[r], mb = s.mass[o];
+            const float sum = ma + mb;
+            const float denom = sum < 1.f ? 1.f : sum;
+            const float x = s.radius[r] + (mb / denom) * exact, y = s.radius[o] + (ma / denom) * exact;
+            const float verified = x < y ? y : x;
+            a.bound[static_cast<int64_t>(lane) * M + r] = verified;
+            if (verified > limit) {
+              dist[static_cast<int64_t>(r) * M + o] = exact2;
+              dist[static_cast<int64_t>(o) * M + r] = exact2;
+              s.flags[r] = static_cast<uint8_t>((s.flags[r] | kRejected) & ~kValid);
+              s.flags[o] |= kRejected;
+            }
+          }
+        }
+        __syncthreads();
+      }
+      // Surviving proposals sorted by (cost, row) (a stable argsort by cost).
+      for (int r = t; r < n; r += kReduceThreads) {
+        if (s.flags[r] & kValid) {
+          const int at = atomicAdd(&s_nvalid, 1);
+          s.keys[at] = (s.packed[r] & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
+        }
+      }
+      __syncthreads();
+      const int nv = s_nvalid;
+      const int width = pow2_at_least(nv > 0 ? nv : 1);
+      for (int i = nv + t; i < width; i += kReduceThreads) s.keys[i] = ~0ull;
+      __syncthreads();
+      for (int size = 2; size <= width; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int i = t; i < width; i += kReduceThreads) {
+            const int p = i ^ stride;
+            if (p > i) {
+              const bool up = (i & size) == 0;
+              const uint64_t x = s.keys[i], y = s.keys[p];
+              if ((x > y) == up) {
+                s.keys[i] = y;
+                s.keys[p] = x;
+              }
+            }
+          }
+          __syncthreads();
+        }
+      }
+      const int budget = s_count - a.target;
+      const int n_ok = nv < budget ? nv : (budget > 0 ? budget : 0);
+      // Merges: pair scalars, masses, radii, centers (litgpt/log_kv_cache.py:589-606).
+      for (int p = t; p < n_ok; p += kReduceThreads) {
+        const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+        const float ma = s.mass[ra], mb = s.mass[rb];
+        const float dab = dist[static_cast<int64_t>(ra) * M + rb];
+        const float total = ma + mb;
+        const float alpha = ma / total, beta = mb / total;
+        s.p_alpha[p] = alpha;
+        s.p_beta[p] = beta;
+        s.p_shift[p] = alpha * beta * dab;
+        s.pair_of[ra] = static_cast<int16_t>(p);
+        s.flags[ra] |= kKeep | kMerged;
+        s.flags[rb] = static_cast<uint8_t>((s.flags[rb] | kMerged) & ~kAlive);
+        s.mass[ra] = total;
+        s.mass[rb] = 0.f;
+        if (LIMIT) s.radius[ra] = a.bound[static_cast<int64_t>(lane) * M + ra];
+        const float scale = total < 1.f ? 1.f : total;
+        float* ua = mu + static_cast<int64_t>(ra) * D;
+        const float* ub = mu + static_cast<int64_t>(rb) * D;
+        for (int d = 0; d < D; ++d) ua[d] = (ma * ua[d] + mb * ub[d]) / scale;
+        trace[2 * (s_ntrace + p)] = ra;
+        trace[2 * (s_ntrace + p) + 1] = rb;
+      }
+      __syncthreads();
+      // Lance-Williams rows of the kept rows, mirrored into the other live rows,
+      // costs pushed into their cached minima (litgpt/log_kv_cache.py:607-626).
+      for (int p = w; p < n_ok; p += kReduceWaves) {
+        const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+        const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
+        const float total = s.mass[ra], rad = s.radius[ra];
+        float* row_a = dist + static_cast<int64_t>(ra) * M;
+        const float* row_b = dist + static_cast<int64_t>(rb) * M;
+        uint64_t rmin = kInfKey;
+        for (int c = l; c < n; c += kWave) {
+          const uint8_t fl = s.flags[c];
+          const bool alive_c = fl & kAlive, keep_c = fl & kKeep;
+          const float x_aa = row_a[c], x_ba = row_b[c];
+          float nw = alpha * x_aa + beta * x_ba - shift;
+          if (keep_c && c != ra) {
+            const int q = s.best[c], pc = s.pair_of[c];
+            const float qa = s.p_alpha[pc], qb = s.p_beta[pc], qs = s.p_shift[pc];
+            const float x_ab = row_a[q], x_bb = row_b[q];
+            const float own = qa * nw + qb * (alpha * x_ab + beta * x_bb - shift) - qs;
+            const float other = alpha * (qa * x_aa + qb * x_ab - qs) + beta * (qa * x_ba + qb * x_bb - qs) - shift;
+            nw = ra < c ? own : other;
+          }
+          nw = nw < 0.f ? 0.f : nw;
+          if (c == ra) nw = 0.f;
+          if (alive_c) {
+            row_a[c] = nw;
+            if (!keep_c) dist[static_cast<int64_t>(c) * M + ra] = nw;
+          }
+          const bool valid = alive_c && c != ra;
+          const float cost = ward_cost<LIMIT>(nw, total, s.mass[c], rad, s.radius[c], limit, valid);
+          const uint64_t k = pack_cost(cost, ra ^ c);
+          if (cost < __builtin_inff() && !keep_c) atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]),
+                                                            static_cast<unsigned long long>(k));
+          rmin = k < rmin ? k : rmin;
+        }
+        rmin = wave_min_u64(rmin);
+        if (l == 0) s.packed[ra] = rmin;
+      }
+      __syncthreads();
+      // Rows whose partner merged or whose proposal was rejected rescan.
+      for (int r = w; r < n; r += kReduceWaves) {
+        const uint8_t fl = s.flags[r];
+        const bool dirty = (fl & kAlive) && !(fl & kKeep) && ((s.flags[s.best[r]] & kMerged) || (fl & kRejected));
+        if (!dirty) continue;
+        const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
+        if (l == 0) s.packed[r] = k;
+      }
+      __syncthreads();
+      const int count = s_count - n_ok;
+      for (int i = t; i < M; i += kReduceThreads) s.flags[i] &= kAlive;
+      __syncthreads();
+      if (t == 0) {
+        s_count = count;
+        s_ntrace += n_ok;
+      }
+      const bool remaining = count > a.target;
+      if (!(remaining && nprop > 0)) {
+        stuck = remaining && nprop == 0;
+        break;
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < M; i += kReduceThreads) a.alive_out[static_cast<int64_t>(lane) * M + i] = s.flags[i] & kAlive;
+  if (t == 0) {
+    a.n_trace[lane] = s_ntrace;
+    a.stuck[lane] = stuck ? 1 : 0;
+  }
+}
+
+// Leaf -> compact surviving row (litgpt/log_kv_cache.py:3553-3568): parents
+// from the trace, pointer jumping to the roots, roots numbered in order.
+__global__ __launch_bounds__(1024) void labels_kernel(const uint8_t* __restrict__ alive, const int32_t* __restrict__ trace,
+                                                      const int32_t* __restrict__ n_trace,
+                                                      const int32_t* __restrict__ count, int M,
+                                                      int32_t* __restrict__ label, int32_t* __restrict__ n_roots) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int wave_sum[16];
+  int32_t* parent = reinterpret_cast<int32_t*>(dyn);
+  int32_t* compact = parent + M;
+  const int lane = blockIdx.x, n = count[lane], t = threadIdx.x;
+  const uint8_t* al = alive + static_cast<int64_t>(lane) * M;
+  const int32_t* tr = trace + static_cast<int64_t>(lane) * M * 2;
+  for (int i = t; i < n; i += 1024) parent[i] = i;
+  __syncthreads();
+  for (int p = t; p < n_trace[lane]; p += 1024) parent[tr[2 * p + 1]] = tr[2 * p];
+  __syncthreads();
+  for (;;) {
+    int changed = 0;
+    for (int i = t; i < n; i += 1024) {
+      const int up = parent[parent[i]];
+      if (up != parent[i]) {
+        parent[i] = up;
+        changed = 1;
+      }
+    }
+    if (!__syncthreads_or(changed)) break;
+  }
+  // Ranks of the roots among the survivors, in row order.
+  int carry = 0;
+  for (int base = 0; base < n; base += 1024) {
+    const int i = base + t;
+    const int v = i < n && al[i] ? 1 : 0;
+    const uint64_t ballot = __ballot(v);
+    const int ln = lane_id(), wv = wave_id();
+    const int before = __popcll(ballot & ((ln == 0) ? 0ull : (~0ull >> (kWave - ln))));
+    if (ln == 0) wave_sum[wv] = __popcll(ballot);
+    __syncthreads();
+    int off = carry;
+    for (int q = 0; q < wv; ++q) off += wave_sum[q];
+    if (v) compact[i] = off + before;
+    int tot = 0;
+    for (int q = 0; q < 16; ++q) tot += wave_sum[q];
+    carry += tot;
+    __syncthreads();
+  }
+  for (int i = t; i < n; i += 1024) label[static_cast<int64_t>(lane) * M + i] = compact[parent[i]];
+  if (t == 0) n_roots[lane] = carry;
+}
+
+// Stage-2 nodes of a lane (litgpt/log_kv_cache.py:3624-3655): old live
+// clusters in ascending id (center, mass n_total), then the candidates in
+// root order (center, mass = member count).
+__global__ __launch_bounds__(256) void stage2_kernel(LadderArgs c, UnifiedBufs u) {
+  __shared__ int old_s[kMaxClusters];
+  __shared__ int n_old_s;
+  extern __shared__ __align__(16) uint8_t dyn[];
+  int32_t* members = reinterpret_cast<int32_t*>(dyn);   // [M]
+  int32_t* roots = members + u.M;                       // [M]
+  const int lane = blockIdx.x, K = c.k_max, M = u.M, D = u.D, t = threadIdx.x;
+  const int n1 = u.count1[lane];
+  if (n1 == 0) {
+    if (t == 0) {
+      u.count2[lane] = 0;
+      u.n_old[lane] = 0;
+    }
+    return;
+  }
+  if (t == 0) {
+    int k = 0;
+    for (int cc = 0; cc < K; ++cc)
+      if (c.alive[static_cast<int64_t>(lane) * K + cc]) {
+        old_s[k] = cc;
+        u.old_ids[static_cast<int64_t>(lane) * kMaxClusters + k] = cc;
+        ++k;
+      }
+    n_old_s = k;
+  }
+  const int nr = u.n_roots1[lane];
+  for (int i = t; i < nr; i += 256) members[i] = 0;
+  __syncthreads();
+  const int n_old = n_old_s;
+  const uint8_t* al = u.alive1 + static_cast<int64_t>(lane) * M;
+  const int32_t* lab = u.label1 + static_cast<int64_t>(lane) * M;
+  for (int i = t; i < n1; i += 256) {
+    atomicAdd(&members[lab[i]], 1);
+    if (al[i]) roots[lab[i]] = i;
+  }
+  __syncthreads();
+  float* mu2 = u.mu2 + static_cast<int64_t>(lane) * M * D;
+  const float* mu1 = u.mu1 + static_cast<int64_t>(lane) * M * D;
+  float* mass2 = u.mass2 + static_cast<int64_t>(lane) * M;
+  const int m2 = n_old + nr;
+  for (int i = t; i < m2 * D; i += 256) {
+    const int row = i / D, d = i - row * D;
+    mu2[i] = row < n_old ? c.centroid[(static_cast<int64_t>(lane) * K + old_s[row]) * c.dk + d]
+                         : mu1[static_cast<int64_t>(roots[row - n_old]) * D + d];
+  }
+  for (int i = t; i < m2; i += 256)
+    mass2[i] = i < n_old ? static_cast<float>(c.n_total[static_cast<int64_t>(lane) * K + old_s[i]])
+                         : static_cast<float>(members[i - n_old]);
+  if (t == 0) {
+    u.count2[lane] = m2;
+    u.n_old[lane] = n_old;
+  }
+}
+
+// Final cluster of every row (position order, as the attach decisions) and
+// the lane's old-old merges in trace order (litgpt/log_kv_cache.py:3656-3686):
+// a root that is an old cluster keeps its id, a new root opens the next free
+// id (free after the old-old merges), in root order.
+__global__ __launch_bounds__(256) void final_kernel(LadderArgs c, RowsArgs r, UnifiedBufs u, const int32_t* order,
+                                                    int8_t* assign) {
+  __shared__ int target_s[kMaxClusters];
+  __shared__ int n_target_s;
+  const int lane = blockIdx.x, K = c.k_max, M = u.M, t = threadIdx.x;
+  const int b = lane / c.n_groups;
+  const int n1 = u.count1[lane];
+  int32_t* jobs = u.jobs + static_cast<int64_t>(lane) * kMaxClusters * 2;
+  if (n1 == 0) {
+    if (t == 0) u.n_jobs[lane] = 0;
+    return;
+  }
+  const int n_old = u.n_old[lane], m2 = u.count2[lane];
+  const int32_t* old = u.old_ids + static_cast<int64_t>(lane) * kMaxClusters;
+  if (t == 0) {
+    const int32_t* tr = u.trace2 + static_cast<int64_t>(lane) * M * 2;
+    uint32_t alive = 0;
+    for (int cc = 0; cc < K; ++cc) alive |= (c.alive[static_cast<int64_t>(lane) * K + cc] ? 1u : 0u) << cc;
+    int nj = 0;
+    for (int p = 0; p < u.n_trace2[lane]; ++p) {
+      const int x = tr[2 * p], y = tr[2 * p + 1];
+      if (y < n_old) {
+        jobs[2 * nj] = old[x];
+        jobs[2 * nj + 1] = old[y];
+        alive &= ~(1u << old[y]);
+        ++nj;
+      }
+    }
+    u.n_jobs[lane] = nj;
+    const uint8_t* al = u.alive2 + static_cast<int64_t>(lane) * M;
+    int k = 0, next_free = 0;
+    for (int i = 0; i < m2 && k < kMaxClusters; ++i) {
+      if (!al[i]) continue;
+      if (i < n_old) {
+        target_s[k] = old[i];
+      } else {
+        while (next_free < K && ((alive >> next_free) & 1u)) ++next_free;
+        target_s[k] = next_free;
+        alive |= 1u << next_free;
+      }
+      ++k;
+    }
+    n_target_s = k;
+  }
+  __syncthreads();
+  const int n_target = n_target_s;
+  const int T = r.tokens;
+  const int32_t* ord = order + static_cast<int64_t>(b) * T;
+  const int32_t* lab1 = u.label1 + static_cast<int64_t>(lane) * M;
+  const int32_t* lab2 = u.label2 + static_cast<int64_t>(lane) * M;
+  int8_t* as = assign + static_cast<int64_t>(lane) * T;
+  // (A root past the table only arises when the budget stage is stuck, which the host rejects.)
+  for (int s = t; s < T; s += 256) {
+    const int root = s < n1 ? lab2[n_old + lab1[ord[s]]] : -1;
+    as[s] = root >= 0 && root < n_target ? static_cast<int8_t>(target_s[root]) : -1;
+  }
+}
+
+int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
+                        hipStream_t stream) {
+  const int lanes = c.n_batch * c.n_groups, M = u.M, D = u.D;
+  int rc = launch_order(r, c.n_batch, ws.order, nullptr, stream);
+  if (rc) return rc;
+  const size_t lds = reduce_lds_bytes(M);
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_kernel<true>), lds) ||
+      !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_kernel<false>), lds))
+    return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(load_nodes_kernel, dim3(std::max(1, std::min(64, M * D / 4096)), lanes), dim3(256), 0, stream, r,
+                     c.n_groups, u);
+  hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu1, u.count1, u.dist, M, D);
+  ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound};
+  hipLaunchKernelGGL(reduce_kernel<true>, dim3(lanes), dim3(kReduceThreads), lds, stream, a1);
+  const size_t lab_lds = static_cast<size_t>(M) * 8;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive1, u.trace1, u.n_trace1, u.count1,
+                     M, u.label1, u.n_roots1);
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&stage2_kernel), lab_lds)) return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
+  hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu2, u.count2, u.dist, M, D);
+  ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
+                u.bound};
+  hipLaunchKernelGGL(reduce_kernel<false>, dim3(lanes), dim3(kReduceThreads), lds, stream, a2);
+  hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
+                     M, u.label2, u.n_roots2);
+  hipLaunchKernelGGL(final_kernel, dim3(lanes), dim3(256), 0, stream, c, r, u, ws.order, ws.assign);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+size_t unified_reduce_lds(int M) { return reduce_lds_bytes(M); }
+
+__global__ __launch_bounds__(256) void summary_kernel(const int32_t* __restrict__ n_jobs,
+                                                      const int32_t* __restrict__ stuck, int lanes, int tokens,
+                                                      int32_t* __restrict__ summary) {
+  int most = 0, any = 0;
+  for (int i = threadIdx.x; tokens && i < lanes; i += 256) {
+    most = max(most, n_jobs[i]);
+    any |= stuck[i];
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    most = max(most, __shfl_xor(most, off, kWave));
+    any |= __shfl_xor(any, off, kWave);
+  }
+  __shared__ int m_s[4], a_s[4];
+  if (lane_id() == 0) {
+    m_s[wave_id()] = most;
+    a_s[wave_id()] = any;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    summary[0] = max(max(m_s[0], m_s[1]), max(m_s[2], m_s[3]));
+    summary[1] = a_s[0] | a_s[1] | a_s[2] | a_s[3];
+  }
+}
+
+int launch_unified_summary(const LadderArgs& c, const UnifiedBufs& u, int32_t* summary, int tokens,
+                           hipStream_t stream) {
+  hipLaunchKernelGGL(summary_kernel, dim3(1), dim3(256), 0, stream, u.n_jobs, u.stuck2, c.n_batch * c.n_groups,
+                     tokens, summary);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+}  // namespace logkv

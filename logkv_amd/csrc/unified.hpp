@@ -1,0 +1,67 @@
+// Internal declarations of the unified (Ward / radius) route.
+#pragma once
+
+#include "route.hpp"
+
+namespace logkv {
+
+constexpr int kMaxNodes = 4608;   // rows of a flush + K (one lane's reducer state lives in LDS)
+
+// Arguments of one reducer stage over `lanes` lanes of M padded nodes.
+struct ReduceArgs {
+  float* dist;            // [lanes, M, M] squared distances (updated in place)
+  float* mu;              // [lanes, M, D] centers (updated in place)
+  const float* mass;      // [lanes, M] initial masses
+  const int32_t* count;   // [lanes] nodes in use (the rest are padding)
+  const float* limit;     // [lanes] radius limit, or NULL for none
+  int32_t target;         // stop at this many clusters
+  int32_t M, D;
+  uint8_t* alive_out;     // [lanes, M] survivors
+  int32_t* trace;         // [lanes, M, 2] merges (kept row, retired row) in round order
+  int32_t* n_trace;       // [lanes]
+  int32_t* stuck;         // [lanes] 1: clusters above the target and no pair left
+  float* bound;           // [lanes, M] scratch: verified radius bounds of a round
+};
+
+// Device buffers of one unified plan (carved from the caller's workspace).
+struct UnifiedBufs {
+  int32_t M, D;
+  const float* limit;     // [lanes]
+  float* mu1;             // [lanes, M, D]
+  float* mass1;           // [lanes, M]
+  int32_t* count1;        // [lanes]
+  float* mu2;
+  float* mass2;
+  int32_t* count2;
+  float* dist;            // [lanes, M, M] (both stages)
+  float* bound;           // [lanes, M]
+  uint8_t* alive1;        // [lanes, M]
+  uint8_t* alive2;
+  int32_t* trace1;        // [lanes, M, 2]
+  int32_t* trace2;
+  int32_t* n_trace1;      // [lanes]
+  int32_t* n_trace2;
+  int32_t* stuck1;
+  int32_t* stuck2;        // [lanes] read by the host: a stuck budget stage is an error
+  int32_t* label1;        // [lanes, M]
+  int32_t* label2;
+  int32_t* n_roots1;
+  int32_t* n_roots2;
+  int32_t* n_old;         // [lanes]
+  int32_t* old_ids;       // [lanes, kMaxClusters]
+  int32_t* jobs;          // [lanes, kMaxClusters, 2] old-old merges (keep, retire) in order
+  int32_t* n_jobs;        // [lanes]
+};
+
+int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
+                        hipStream_t stream);
+size_t unified_reduce_lds(int M);
+// summary[0] = most old-old merges of a lane, summary[1] = 1 if a budget stage found no pair.
+int launch_unified_summary(const LadderArgs& c, const UnifiedBufs& u, int32_t* summary, int tokens,
+                           hipStream_t stream);
+int launch_ward_step(const LadderArgs& c, const Workspace& ws, const int32_t* jobs, const int32_t* n_jobs, int step,
+                     hipStream_t stream);
+int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
+                  hipStream_t stream);
+
+}  // namespace logkv

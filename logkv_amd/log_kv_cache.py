@@ -198,8 +198,10 @@ class LogStructuredKVCache(nn.Module):
         unsupported = []
         if not semantic_clusters or cluster_k_max <= 1:
             unsupported.append("semantic_clusters with cluster_k_max > 1")
-        if semantic_unified_route:
-            unsupported.append("semantic_unified_route=False (the unified Ward route is not built)")
+        if semantic_unified_route and semantic_merge_passes != 1:
+            unsupported.append("semantic_merge_passes=1 with the unified route (frozen-center sweeps)")
+        if semantic_unified_route and semantic_replay_updates:
+            unsupported.append("no update tape with the unified route")
         if semantic_legacy_route or semantic_cluster_chunk_size:
             unsupported.append("attach routing (no legacy / chunk-tree route)")
         if semantic_capacity_beta or semantic_capacity_hard_cap_mult:
@@ -232,7 +234,8 @@ class LogStructuredKVCache(nn.Module):
         self.semantic_pack_backend = semantic_pack_backend
         self.semantic_centroid_backend = semantic_centroid_backend
         self.semantic_replay_updates = bool(semantic_replay_updates)
-        self.semantic_unified_route = False
+        self.semantic_unified_route = bool(semantic_unified_route)
+        self.semantic_merge_passes = int(semantic_merge_passes)
         self.semantic_legacy_route = False
         self.rope_n_elem = int(rope_n_elem)
         self.register_buffer("cos_cache", cos_cache.to(device=device), persistent=False)
@@ -315,6 +318,11 @@ class LogStructuredKVCache(nn.Module):
         if not bool(torch.isfinite(s_h).all().item()) or not bool((s_h > 0).all().item()):
             raise ValueError("semantic_s_h must be finite and > 0")
         buf("s_h", s_h.contiguous())
+        # Radius limits of the unified route's candidates, sqrt(lambda * s_h) per
+        # lane (litgpt/log_kv_cache.py:3617-3620, :2728-2729).
+        lam = float(cluster_lambda_rel)
+        limits = [math.sqrt(lam * float(x)) for x in s_h.reshape(-1).cpu().tolist()]
+        buf("_unified_limits", torch.tensor(limits, dtype=torch.float32, device=device))
         self._workspace = None
         self._alpha_keep_alive = None
         # C-ABI argument structs and per-flush-length buffers, built once and
@@ -412,6 +420,10 @@ class LogStructuredKVCache(nn.Module):
         self._route_commit(k_raw, v, positions, counts, assign_out, order_out, record=record_op_log)
 
     def _route_commit(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None, record=False):
+        if self.semantic_unified_route:
+            if record:
+                raise NotImplementedError("op-log recording of the unified route is not built")
+            return self._unified_route_commit(k_raw, v, positions, counts)
         view = self._ladder_view()
         rows = self._rows_view(k_raw, v, positions, counts)
         ws = self._workspace_for(view, rows.tokens)
@@ -423,6 +435,35 @@ class LogStructuredKVCache(nn.Module):
             log = self._op_log_view()
             check(lib().logkv_record_ops(C.byref(view), C.byref(rows), ptr(ws), ws.numel(), C.byref(log), stream),
                   "logkv_record_ops")
+
+    def _unified_route_commit(self, k_raw, v, positions, counts=None):
+        """Unified route of one flush (litgpt/log_kv_cache.py:3589-3688): the plan
+        on the device, one read of its two-word summary (the old-old merge
+        rounds to launch and the budget stage's failure flag), then the merges
+        and the commit."""
+        view = self._ladder_view()
+        rows = self._rows_view(k_raw, v, positions, counts)
+        key = ("unified_ws", rows.tokens)
+        need = self._views.get(key)
+        if need is None:
+            need = lib().logkv_unified_workspace_bytes(C.byref(view), rows.tokens, self._params.late_joins)
+            if need < 0:
+                raise ValueError("invalid cache layout for the unified route")
+            self._views[key] = need
+        if self._workspace is None or self._workspace.numel() < need:
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.level_k.device)
+        ws = self._workspace
+        summary = self._views.get("unified_summary")
+        if summary is None:
+            summary = self._views["unified_summary"] = torch.zeros(2, dtype=torch.int32, device=self.level_k.device)
+        stream = stream_of(k_raw.device)
+        check(lib().logkv_unified_plan(C.byref(view), C.byref(rows), C.byref(self._params), ptr(self._unified_limits),
+                                       ptr(ws), ws.numel(), ptr(summary), stream), "logkv_unified_plan")
+        steps, stuck = summary.tolist()
+        if stuck:
+            raise RuntimeError("unified route: a budget stage found no mutual pair above the cluster budget")
+        check(lib().logkv_unified_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                         int(steps), stream), "logkv_unified_commit")
 
     def _commit_only(self, k_raw, v, positions, counts, assign, order):
         view = self._ladder_view()

@@ -104,6 +104,7 @@ class OracleCache:
         self.late_joins = 0       # delayed-archive re-sorts performed (test coverage evidence)
         self.op_log = None        # per lane lists of (op, cluster, arg, position), see oracle.oplog
         self.unified = unified    # the unified Ward / radius route (oracle.unified) instead of attach
+        self.ward_merges = 0      # old-old merges performed by the unified route (test coverage evidence)
         self.replay_cursor = None
 
     # ---- ladder access -------------------------------------------------

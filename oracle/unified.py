@@ -259,6 +259,7 @@ def ward_entry_order(order, p_lo, has_mass, split):
 
 def ward_merge(cache, b, g, keep, free):
     """Merge old cluster ``free`` into ``keep`` (litgpt/log_kv_cache.py:2517-2580)."""
+    cache.ward_merges += 1
     ents = [cache.ladder(b, g, c).entries() for c in (keep, free)]
     rows = lad.concat(ents)
     split = len(ents[0]["w"])

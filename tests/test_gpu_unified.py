@@ -1,0 +1,83 @@
+"""Device unified (Ward / radius) route against the oracle, bit for bit: the
+cluster state after every flush (ladders, centers, n_eff, n_total, p_hi,
+phase, alive), with drifting mixtures that force old-old merges, with Alpha's
+ragged archives and delayed joins, and with Beta carries."""
+
+import numpy as np
+import pytest
+import torch
+
+from harness import compare_state
+from logkv_amd.workloads import Mixture, rope_tables
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False):
+    from logkv_amd import LogStructuredKVCache
+    from oracle import OracleCache
+
+    cos, sin = rope_tables(max_seq, dim)
+    gpu = LogStructuredKVCache(
+        (batch, groups, max_seq, dim), (batch, groups, max_seq, dim), B=B, recent_size=T, device="cuda",
+        dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=s_h,
+        semantic_flush_granularity=T, semantic_anchor_mode="mid", allocate_second_order=False,
+        semantic_unified_route=True, semantic_merge_passes=1, cos_cache=cos, sin_cache=sin, rope_n_elem=dim,
+        alpha_exact_tokens=exact, alpha_span_max_tokens=span, beta_novelty=beta, beta_adaptive_merge=beta)
+    ora = OracleCache(batch, groups, max_seq, dim, dim, B=B, recent_size=T, K=K, s_h=s_h, flush=T,
+                      exact_tokens=exact, span_max=span, beta_novelty=beta, beta_adaptive=beta,
+                      cos=cos.numpy(), sin=sin.numpy(), unified=True)
+    return gpu, ora
+
+
+CASES = {
+    # name: (batch, groups, dim, K, B, T, flushes, s_h, exact, beta, drift)
+    "small": (2, 2, 16, 4, 8, 24, 8, 4.0, 0, False, 48),
+    "wide": (1, 2, 128, 12, 16, 256, 5, 64.0, 0, False, 512),
+    "alpha_beta": (2, 2, 16, 4, 8, 24, 10, 4.0, 8, True, 48),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_unified_route_matches_oracle(name):
+    batch, groups, dim, K, B, T, n, s_h, exact, beta, drift = CASES[name]
+    print(f"case {name}", flush=True)
+    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h, exact=exact, beta=beta)
+    mix = Mixture(batch, groups, dim, clusters=K + 2, seed=17, drift_every=drift)
+    dev = gpu.level_k.device
+    for i in range(n):
+        k, v = mix.rows(T), mix.rows(T)
+        pos = torch.arange(i * T, (i + 1) * T).unsqueeze(0).expand(batch, -1).contiguous()
+        ends = [[(p + 3 * b) % 5 == 0 for p in range(i * T, (i + 1) * T)] for b in range(batch)] if exact else None
+        gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev), span_ends=ends)
+        ora.flush_rows(k.float().numpy(), v.float().numpy(), pos.numpy(), ends)
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"flush {i}: " + "; ".join(bad)
+        assert (ora.alive.sum(-1) <= K).all()
+    assert ora.ward_merges > 0, "no old-old merge was exercised"
+
+
+def test_old_old_merge_frees_a_cluster():
+    dim = 8
+    gpu, ora = _pair(1, 1, dim, 2, 4, 4, 256, 1.0)
+    e = np.eye(dim, dtype=np.float32)
+    dev = gpu.level_k.device
+    # Two old clusters (1 e0 and 5 e0: farther apart than the radius allows),
+    # then a far candidate: the old pair is the cheapest merge, so cluster 1
+    # merges into 0 and the candidate opens 1.
+    first = np.stack([e[0] * 1, e[0] * 1.1, e[0] * 5, e[0] * 5.1])[None, None]
+    second = np.stack([e[2] * 50, e[2] * 50.2, e[2] * 50.1, e[2] * 49.9])[None, None]
+    for i, rows in enumerate((first, second)):
+        t = torch.from_numpy(rows).to(torch.bfloat16)
+        pos = torch.arange(10 * i, 10 * i + 4).unsqueeze(0)
+        gpu.route_and_flush_batch(t.to(dev), t.to(dev), pos.to(dev))
+        ora.flush_rows(t.float().numpy(), t.float().numpy(), pos.numpy())
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"flush {i}: " + "; ".join(bad)
+        if i == 0:
+            assert ora.n_total[0, 0].tolist() == [2, 2]
+    assert ora.ward_merges == 1
+    assert ora.alive[0, 0].tolist() == [True, True]
+    assert ora.n_total[0, 0].tolist() == [4, 4]
