@@ -17,6 +17,10 @@ Qwen3-1.7B GQA (16 query / 8 KV heads x 128): recent window 2048, exact pool
 masses ~ U(1, 64). A step attends one new token per sequence with the packed
 prefix reused, as in the reference's decode loop.
 
+Unified-route control: the Ward / radius route at batch 4 x 8 KV groups with
+4096-row flushes over a 131,072-token drifting stream (one layer), reported
+beside the headline as flushed tokens/s and ms per flush.
+
 Prints one JSON line: flushed tokens/s over the timed steps, the roofline of
 the dominant stage (the ladder commit: its prepare, per-level carries and
 finish launches) from HIP events on its stream over the timed region, decode ms/token with its own roofline, and the oracle's CPU
@@ -213,8 +217,11 @@ class CommitMeter:
         self.cache, self.torch = cache, torch
         self.records = []
 
-    def __call__(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None):
+    def __call__(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None, record=False):
         from logkv_amd._lib import check, lib, ptr, stream_of
+
+        if record:
+            raise ValueError("the commit meter does not record op-logs")
 
         cache, torch = self.cache, self.torch
         dev = k_raw.device
@@ -447,6 +454,54 @@ def decode_workload(args, torch, np):
     }
 
 
+def unified_workload(args, torch, np):
+    """The unified (Ward / radius) route control: batch 4 x 8 KV groups, recent = flush = 4096 rows, a
+    131,072-token stream (31 flush events) of a 12-Gaussian mixture that drifts every 16K tokens."""
+    from logkv_amd import LogStructuredKVCache
+    from logkv_amd.workloads import Mixture, rope_tables
+
+    dev = torch.device("cuda", 0)
+    Bt, T, stream_tokens, s_h = 4, 4096, 131072, 64.0
+    cos, sin = rope_tables(stream_tokens, D)
+    cache = LogStructuredKVCache((Bt, G, stream_tokens, D), (Bt, G, stream_tokens, D), B=B, recent_size=T,
+                                 device=dev, dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
+                                 semantic_s_h=s_h, semantic_flush_granularity=T, semantic_anchor_mode="mid",
+                                 allocate_second_order=False, semantic_unified_route=True, cos_cache=cos, sin_cache=sin,
+                                 rope_n_elem=D)
+    # Each flush draws T key rows and T value rows, so the centers move every 16K tokens.
+    mix = Mixture(Bt, G, D, clusters=12, seed=31, drift_every=2 * 16384)
+    flushes = stream_tokens // T - 1
+    warm = 2
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    t_all = 0.0
+    for i in range(flushes):
+        k, v = mix.rows(T).to(dev), mix.rows(T).to(dev)
+        pos = torch.arange(i * T, (i + 1) * T, device=dev).unsqueeze(0).expand(Bt, -1).contiguous()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev[0].record(stream)
+        cache.route_and_flush_batch(k, v, pos)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        if i >= warm:
+            t_all += time.perf_counter() - t0
+            times.append(ev[0].elapsed_time(ev[1]))
+    timed = flushes - warm
+    ms = t_all / timed * 1e3
+    progress(f"unified route: {timed} timed flushes, {ms:.1f} ms per flush")
+    return {
+        "workload": "unified Ward / radius route control, Qwen3-1.7B KV shape (8 x 128 bf16), batch 4, "
+                    f"recent = flush = {T}, {stream_tokens}-token stream ({flushes} flush events), 12-Gaussian "
+                    f"mixture drifting every 16K tokens, K={K}, B={B}, L={cache.L_alloc}, s_h={s_h}",
+        "flushed_tokens_per_s": Bt * T / (ms * 1e-3), "ms_per_flush": ms,
+        "device_ms_per_flush": float(np.mean(times)), "timed_flushes": timed, "warmup_flushes": warm,
+        "live_clusters_per_lane": float(cache.alive.float().sum(-1).mean()),
+        "note": "one layer; the reducer runs one workgroup per lane, all rounds of a stage in one launch",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -462,6 +517,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-unified", action="store_true", help="skip the unified-route control measurement")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a plain copy of known size that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
@@ -513,6 +569,8 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_workload(args, torch, np)
         result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
+    if not args.no_unified and args.flush_passes == "all":
+        result["unified"] = unified_workload(args, torch, np)
     if not args.no_cpu_baseline:
         progress("cpu baseline: oracle flushes on the host")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -229,7 +229,6 @@ int logkv_unified_commit(const logkv_ladder_view* cache, const logkv_rows_view* 
     rc = logkv::launch_ward_step(*cache, ws, u.jobs, u.n_jobs, step, s);
     if (!rc) rc = logkv::launch_levels(*cache, *rows, *params, ws, s);
   }
-  if (!rc) rc = logkv::launch_snapshot(*cache, ws, s);
   if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
   if (rc) return fail(rc, "unified commit launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;
@@ -275,9 +274,7 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
   if (rc) return rc;
   if (!rows->tokens) return LOGKV_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // The commit reads the alive flags as they were before it (decisions made elsewhere).
-  rc = logkv::launch_snapshot(*cache, ws, s);
-  if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
+  rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
   if (rc) return fail(rc, "commit launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;
 }

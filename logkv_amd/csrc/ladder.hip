@@ -858,7 +858,11 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_S uint16_t* tok_s = (const LOGKV_S uint16_t*)tok;
   const Soa S0 = s0_of(ws, ladder, dk, dv);
 
-  const bool was_alive = ws.snap_alive[cl] != 0;
+  // No launch of the commit writes `alive` before the top-level finish, so both
+  // roles read the flags as they were before the flush; the ladder role keeps
+  // a copy for the op-log record.
+  const bool was_alive = c.alive[cl] != 0;
+  if (blockIdx.y == 0 && threadIdx.x == 0) ws.snap_alive[cl] = was_alive ? 1 : 0;
   const int first = was_alive ? 0 : 1;   // a dead cluster opens with its earliest row
   const int nn = m - first;
 
@@ -1088,7 +1092,6 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       mm = used ? carries_of(counts_s[e], mm, B, e == L - 1) : 0;
     }
     ws.plans[ladder] = pl;
-    c.alive[cl] = 1;
     c.n_total[cl] = n_total;
     c.p_hi_c[cl] = p_hi;
     c.level0_phase[cl] = phase;
@@ -1219,6 +1222,8 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs
   extern __shared__ __align__(16) uint8_t dyn[];
   const int ladder = blockIdx.x, ell = TOP ? c.levels - 1 : static_cast<int>(blockIdx.y);
   const LadderPlan* pl = ws.plans + ladder;
+  // The last launch of a commit marks every cluster that took rows as live.
+  if (TOP && threadIdx.x == 0 && pl->m_tok > 0) c.alive[ladder] = 1;
   if (!pl->active) return;
   const int cnt = pl->cnt[ell], m = pl->m[ell];
   if (m == 0) return;

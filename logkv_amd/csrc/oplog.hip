@@ -87,8 +87,7 @@ __global__ __launch_bounds__(kRecordThreads) void record_kernel(LadderArgs c, Ro
 // Replay parse, one wave per lane: the log rows [cursor, cursor + n) name the
 // cluster of every valid flush row by position (litgpt/log_kv_cache.py:
 // 4856-4904, one row per consumed token). Writes the decision array in
-// position order (assign[lane, s] for the row order[b, s]) and the alive
-// snapshot the commit reads, and checks what the reference's parse and commit
+// position order (assign[lane, s] for the row order[b, s]) and checks what the reference's parse and commit
 // would reject or could not reproduce: unknown ops, positions missing from or
 // repeated in the flush, a short log, a NEW_CLUSTER of a live cluster or a
 // JOIN into a dead one, a cluster's rows out of position order (the commit
@@ -110,7 +109,6 @@ __global__ __launch_bounds__(kWave) void replay_kernel(LadderArgs c, RowsArgs r,
   uint32_t alive = 0;
   for (int cc = 0; cc < K; ++cc) alive |= (c.alive[ladder0 + cc] ? 1u : 0u) << cc;
   if (l < K) {
-    ws.snap_alive[ladder0 + l] = c.alive[ladder0 + l];
     seen[l] = 0;
     last_pos[l] = 0;
   }
@@ -179,20 +177,6 @@ __global__ __launch_bounds__(kWave) void replay_kernel(LadderArgs c, RowsArgs r,
     if (as[s] < 0) err |= LOGKV_REPLAY_UNCONSUMED;
   for (int d = 1; d < kWave; d <<= 1) err |= __shfl_xor(err, d, kWave);
   if (l == 0 && err) atomicOr(status, err);
-}
-
-// Alive flags before a commit whose decisions came from elsewhere (the attach
-// launches write the same snapshot themselves).
-__global__ __launch_bounds__(256) void snapshot_kernel(const uint8_t* __restrict__ alive, uint8_t* __restrict__ snap,
-                                                       int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) snap[i] = alive[i];
-}
-
-int launch_snapshot(const LadderArgs& c, const Workspace& ws, hipStream_t stream) {
-  const int64_t n = static_cast<int64_t>(c.n_batch) * c.n_groups * c.k_max;
-  hipLaunchKernelGGL(snapshot_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, c.alive, ws.snap_alive, n);
-  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,

@@ -295,7 +295,7 @@ __device__ __forceinline__ void block_argmax(float& v, int& i, float* sv, int* s
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, const int32_t* __restrict__ order,
                                                     int8_t* __restrict__ assign, const float* __restrict__ s_win,
-                                                    float* __restrict__ dist, uint8_t* __restrict__ snap_alive) {
+                                                    float* __restrict__ dist) {
   __shared__ float cand_s[kMaxClusters * kMaxDim];
   __shared__ float red_v[16];
   __shared__ int red_i[16];
@@ -306,9 +306,6 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   const int K = c.k_max, D = c.dk, J = (D + kWave - 1) / kWave;
   const int n = valid_rows(r, b);
-  // Alive flags as they were before this flush: the commit's ladder and center
-  // blocks both read them while the ladder block rewrites `alive`.
-  for (int cc = threadIdx.x; cc < K; cc += blockDim.x) snap_alive[lane_ix * K + cc] = c.alive[lane_ix * K + cc];
   int n_free = 0;
   for (int cc = 0; cc < K; ++cc)
     if (!c.alive[lane_ix * K + cc]) {
@@ -456,7 +453,7 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
     else ok = attach(attach_kernel<4>, attach_tile<4>(), attach_shmem<4>(c.k_max));
     if (!ok) return LOGKV_ERUNTIME;
     hipLaunchKernelGGL(seed_kernel, dim3(lanes), dim3(1024), 0, stream, c, r, ws.order, ws.assign, ws.s_win,
-                       ws.dist, ws.snap_alive);
+                       ws.dist);
   }
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }

@@ -44,7 +44,7 @@ struct Workspace {
   int8_t* assign;      // [lanes, T]
   float* s_win;        // [lanes, T]
   float* dist;         // [lanes, T]
-  uint8_t* snap_alive; // [lanes, K] alive flags at the start of the flush
+  uint8_t* snap_alive; // [lanes, K] alive flags before the commit (written by its ladder blocks)
   uint8_t* ladder;     // per-ladder carry / staging rows
   int64_t ladder_stride;  // bytes per ladder
   int64_t s0_rows;        // delayed-archive staging rows per ladder
@@ -70,7 +70,6 @@ int launch_attention(const logkv_attention_args& a, const int32_t* width, float*
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
 int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream);
-int launch_snapshot(const LadderArgs& c, const Workspace& ws, hipStream_t stream);
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   hipStream_t stream);
 int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
