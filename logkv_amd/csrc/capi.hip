@@ -464,4 +464,23 @@ int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, 
   return LOGKV_OK;
 }
 
+int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, int64_t table_ints, void* stream) {
+  if (!a || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention args or plan table are NULL");
+  if (a->n_groups < 1 || a->n_heads % a->n_groups) return fail(LOGKV_EINVAL, "heads must be a multiple of groups");
+  if (a->tq < 1) return fail(LOGKV_EINVAL, "query length must be >= 1");
+  if (a->dim % 8 || a->dim > 144 || a->dim <= a->dk || a->dim < a->dv)
+    return fail(LOGKV_EINVAL, "chunk attention takes packed widths up to 144 (multiples of 8), got %d", a->dim);
+  if (a->dv % 32 || a->dv < 32 || a->dv > 128) return fail(LOGKV_EINVAL, "chunk attention takes dv in {32, 64, 96, 128}");
+  if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
+    return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
+  if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
+  if (reinterpret_cast<uintptr_t>(a->out) % 8 || a->o_st % 4 || a->o_sh % 4 || a->o_sb % 4)
+    return fail(LOGKV_EINVAL, "chunk attention output rows must be 8-byte aligned");
+  if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
+    return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
+  const int rc = logkv::launch_chunk_attention(*a, table + table_ints - 1, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "chunk attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"

@@ -185,6 +185,11 @@ def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups,
     args = AttentionArgs(ptr(q), *q.stride()[:3], bt, hq, n_groups, tq, dk, v_dim, ka.size(3), ptr(ka), ptr(va),
                          ka.size(2), tail, causal_tail, float(scale), _inv_scale_bf16(scale), ptr(out),
                          *out.stride()[:3], ptr(alpha_count_dev))
+    if (hq // n_groups) * tq > 16:
+        # Many query rows per KV group: the matrix-core chunk kernel (no workspace).
+        check(lib().logkv_chunk_attention(C.byref(args), ptr(plan.table), plan.table.numel(), stream_of(q.device)),
+              "logkv_chunk_attention")
+        return out, workspace
     need = int(lib().logkv_attention_workspace_bytes(C.byref(args)))
     if need < 0:
         raise ValueError("bad attention shape")

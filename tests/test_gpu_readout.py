@@ -197,3 +197,39 @@ def test_causal_chunk():
     q = rand_bf16(g, 1, 4, 8, dk)
     k, v = rand_bf16(g, 1, 2, 8, dk), rand_bf16(g, 1, 2, 8, dk)
     check_step(cache, cos, sin, q, k, v, dk ** -0.5)
+
+
+@pytest.mark.parametrize("dk,heads,groups,tq,recent", [
+    (64, 4, 2, 128, 40),      # 256 query rows per KV group, packed width 72 (five 16-wide steps)
+    (128, 16, 8, 300, 100),   # Qwen3-1.7B heads; query tiles that span two heads
+])
+def test_matrix_core_chunk_attention(dk, heads, groups, tq, recent):
+    """Chunks of many query rows take the MFMA chunk kernel; same math, same tolerance."""
+    print(f"case dk={dk} heads={heads} tq={tq}", flush=True)
+    cos, sin = rope_tables(4096, dk)
+    cache = LogStructuredKVCache(
+        (1, groups, 4096, dk), (1, groups, 4096, dk), B=16, recent_size=512, device="cuda", dtype=torch.bfloat16,
+        semantic_clusters=True, cluster_k_max=4, semantic_flush_granularity=512, semantic_anchor_mode="mid",
+        allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk)
+    fill_readout_state(cache, seed=9, recent=recent)
+    g = torch.Generator().manual_seed(3)
+    q = rand_bf16(g, 1, heads, tq, dk)
+    k, v = rand_bf16(g, 1, groups, tq, dk), rand_bf16(g, 1, groups, tq, dk)
+    check_step(cache, cos, sin, q, k, v, dk ** -0.5)
+
+
+def test_matrix_core_chunk_attention_alpha_pool():
+    """With an exact pool (masked rows) and after real flushes."""
+    gpu, _ = make_pair(batch=2, groups=2, dim=64, K=4, B=16, recent=64, flush=64, max_seq=2048, s_h=16.0, exact=32,
+                       span=8, beta_novelty=True, beta_adaptive=True)
+    mix = Mixture(2, 2, 64, clusters=4, seed=5)
+    dev = gpu.level_k.device
+    for blk in range(5):
+        k, v = mix.rows(64), mix.rows(64)
+        pos = torch.arange(blk * 64, (blk + 1) * 64).unsqueeze(0).expand(2, -1).contiguous()
+        gpu.add_recent(k.to(dev), v.to(dev), k_raw=k.to(dev), input_pos=pos.to(dev), span_ends=mix.span_ends(blk * 64, 64, 8))
+    g = torch.Generator().manual_seed(4)
+    q = rand_bf16(g, 2, 4, 96, 64)
+    k, v = rand_bf16(g, 2, 2, 96, 64), rand_bf16(g, 2, 2, 96, 64)
+    cos, sin = gpu.cos_cache.cpu(), gpu.sin_cache.cpu()
+    check_step(gpu, cos, sin, q, k, v, 64 ** -0.5)
