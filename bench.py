@@ -17,6 +17,11 @@ Qwen3-1.7B GQA (16 query / 8 KV heads x 128): recent window 2048, exact pool
 masses ~ U(1, 64). A step attends one new token per sequence with the packed
 prefix reused, as in the reference's decode loop.
 
+Streaming prefill: 32,768 tokens in 2048-token blocks through 28 layer caches
+with per-layer calls: the chunk attention of each block (matrix-core kernel)
+and the flush it triggers; ms per block, the attention's TFLOP/s, and the
+slots per cluster after each block (the O(log N) growth).
+
 Unified-route control: the Ward / radius route at batch 4 x 8 KV groups with
 4096-row flushes over a 131,072-token drifting stream (one layer), reported
 beside the headline as flushed tokens/s and ms per flush.
@@ -454,6 +459,69 @@ def decode_workload(args, torch, np):
     }
 
 
+def prefill_workload(args, torch, np):
+    """Streaming prefill of a 32,768-token sequence through 28 Qwen3-1.7B-shaped layer caches, one call per layer
+    as a model makes them: per 2048-token block and layer, the chunk attention of the block's 16 query heads over
+    [compressed cache | block] (causal within the block) and add_recent, which flushes 2048 rows into the ladders
+    once the recent window is full. Queries, keys and values are seeded random bf16 (the model's projections are
+    not on this path)."""
+    from logkv_amd import LogStructuredKVCache, log_kv_chunk_attention
+    from logkv_amd.workloads import Mixture, rope_tables
+
+    dev = torch.device("cuda", 0)
+    layers, HQ, blocks = args.layers, 16, N // F
+    cos, sin = rope_tables(N, D)
+    caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev, dtype=torch.bfloat16,
+                                   semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
+                                   semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                   allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                   alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                   beta_adaptive_merge=True) for _ in range(layers)]
+    gen = torch.Generator(device=dev).manual_seed(41)
+    mix = Mixture(1, G, D, clusters=K, seed=43)
+    q = torch.randn(1, HQ, F, D, generator=gen, device=dev).to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    scale = D ** -0.5
+    block_ms, attn_ms, slots, attn_flops = [], [], [], []
+    for blk in range(blocks):
+        k_raw, v = mix.rows(F).to(dev), mix.rows(F).to(dev)
+        pos = torch.arange(blk * F, (blk + 1) * F, device=dev).unsqueeze(0)
+        ends = torch.tensor([[(p + 7) % 32 == 0 for p in range(blk * F, (blk + 1) * F)]], dtype=torch.uint8,
+                            device=dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        events = []
+        for cache in caches:
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record(stream)
+            log_kv_chunk_attention(cache, q, k_raw, v, scale, second_order_scale=0.0)
+            ev[1].record(stream)
+            events.append(ev)
+            cache.add_recent(k_raw, v, k_raw=k_raw, input_pos=pos, span_ends=ends)
+        torch.cuda.synchronize()
+        block_ms.append((time.perf_counter() - t0) * 1e3)
+        attn_ms.append(float(np.sum([e[0].elapsed_time(e[1]) for e in events])))
+        c0 = caches[0]
+        rows = int(c0.level_count.long().sum(-1).max()) + c0.alpha_count + c0.recent_count
+        attn_flops.append(layers * 4 * F * rows * D * HQ)
+        slots.append(float(c0.level_count.float().sum() / (G * K)))
+    attn_s = float(np.sum(attn_ms)) * 1e-3
+    tflops = float(np.sum(attn_flops)) / attn_s / 1e12
+    progress(f"prefill: {blocks} blocks, {np.mean(block_ms):.1f} ms per block over {layers} layers")
+    return {
+        "workload": f"streaming prefill of {N} tokens through {layers} Qwen3-1.7B-shaped layer caches (16 q / 8 KV "
+                    f"heads x 128, bf16), batch 1, {F}-token blocks, recent {F}, K={K}, B={B}, Alpha {EXACT}/{SPAN}, "
+                    "Beta, mid anchor; per block and layer: chunk attention (matrix cores) + add_recent (flush)",
+        "ms_per_block": float(np.mean(block_ms)), "ms_per_block_by_block": [round(x, 2) for x in block_ms],
+        "attention_ms_per_block": float(np.mean(attn_ms)),
+        "attention_roofline": {"kernel": "chunk_kernel", "bound": "mfma", "achieved": tflops, "peak": 2500.0,
+                               "unit": "TFLOP/s", "frac": tflops / 2500.0,
+                               "flops": "4 * T_q * S * D per query head (S = packed rows)"},
+        "flushes": sum(1 for x in slots if x > 0),
+        "slots_per_cluster_after_each_block": [round(x, 1) for x in slots],
+    }
+
+
 def unified_workload(args, torch, np):
     """The unified (Ward / radius) route control: batch 4 x 8 KV groups, recent = flush = 4096 rows, a
     131,072-token stream (31 flush events) of a 12-Gaussian mixture that drifts every 16K tokens."""
@@ -518,6 +586,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-unified", action="store_true", help="skip the unified-route control measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the streaming-prefill measurement")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a plain copy of known size that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
@@ -569,6 +638,8 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_workload(args, torch, np)
         result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
+    if not args.no_prefill and args.flush_passes == "all":
+        result["prefill"] = prefill_workload(args, torch, np)
     if not args.no_unified and args.flush_passes == "all":
         result["unified"] = unified_workload(args, torch, np)
     if not args.no_cpu_baseline:

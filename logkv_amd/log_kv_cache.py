@@ -263,7 +263,6 @@ class LogStructuredKVCache(nn.Module):
         buf("recent_v", torch.zeros(batch_size, n_groups, cap, v_dim, device=device, dtype=dtype))
         buf("recent_k_raw", torch.zeros(batch_size, n_groups, cap, k_dim, device=device, dtype=dtype))
         buf("recent_pos", torch.zeros(batch_size, cap, device=device, dtype=torch.int64))
-        self._recent_pos_host = [[0] * cap for _ in range(batch_size)]
         self._alpha_count_host = 0
         if self.alpha_exact_tokens:
             P = self.alpha_exact_tokens
@@ -284,7 +283,8 @@ class LogStructuredKVCache(nn.Module):
                                  torch.zeros_like(self.alpha_pos), torch.zeros_like(self.alpha_valid),
                                  torch.zeros_like(self.alpha_span_len), torch.zeros_like(self.alpha_span_closed),
                                  torch.zeros_like(self.alpha_span_count))
-            self._recent_span_ends = [[False] * cap for _ in range(batch_size)]
+            # Natural span boundary flags of the recent rows, shifted with them.
+            buf("recent_span_ends", torch.zeros(batch_size, cap, device=device, dtype=torch.uint8))
         shp = (batch_size, n_groups, self.K_max, L, B_eff)
         i64max = torch.iinfo(torch.int64).max
         buf("level_k", torch.zeros(*shp, k_dim, device=device, dtype=dtype))
@@ -656,10 +656,12 @@ class LogStructuredKVCache(nn.Module):
             take = min(self.semantic_flush_granularity, pending)
             if take > self.recent_count:
                 raise RuntimeError(f"semantic LogKV cannot flush {take} tokens from recent_count={self.recent_count}")
+            # CPU positions are read only where a caller needs them (update tape, replay plans).
+            needs_host = self._active_updates is not None or route.get("replay_plans") is not None
             self.route_and_flush_batch(
                 self.recent_k_raw[:, :, :take], self.recent_v[:, :, :take], self.recent_pos[:, :take],
-                positions_host=[row[:take] for row in self._recent_pos_host],
-                span_ends=[row[:take] for row in self._recent_span_ends] if self.alpha_exact_tokens else None,
+                positions_host=self.recent_pos[:, :take].tolist() if needs_host else None,
+                span_ends=self.recent_span_ends[:, :take] if self.alpha_exact_tokens else None,
                 **route,
             )
             remaining = self.recent_count - take
@@ -669,36 +671,41 @@ class LogStructuredKVCache(nn.Module):
                     t = getattr(self, name)
                     t[:, :, :remaining].copy_(stage(t[:, :, take:self.recent_count]))
                 self.recent_pos[:, :remaining].copy_(stage(self.recent_pos[:, take:self.recent_count]))
-                for b in range(self.batch_size):
-                    self._recent_pos_host[b][:remaining] = self._recent_pos_host[b][take:self.recent_count]
-                    if self.alpha_exact_tokens:
-                        self._recent_span_ends[b][:remaining] = self._recent_span_ends[b][take:self.recent_count]
-            # The vacated rows are cleared (litgpt/log_kv_cache.py:5652-5659).
-            for b in range(self.batch_size):
-                self._recent_pos_host[b][remaining:self.recent_count] = [0] * (self.recent_count - remaining)
                 if self.alpha_exact_tokens:
-                    self._recent_span_ends[b][remaining:self.recent_count] = [False] * (self.recent_count - remaining)
+                    self.recent_span_ends[:, :remaining].copy_(stage(self.recent_span_ends[:, take:self.recent_count]))
+            # The vacated rows are cleared (litgpt/log_kv_cache.py:5652-5659).
             for name in ("recent_k", "recent_k_raw", "recent_v"):
                 getattr(self, name)[:, :, remaining:self.recent_count].zero_()
             self.recent_pos[:, remaining:self.recent_count].zero_()
+            if self.alpha_exact_tokens:
+                self.recent_span_ends[:, remaining:self.recent_count].zero_()
             self.recent_count = remaining
             pending -= take
 
     def _input_positions(self, n, input_pos):
+        """Positions of an appended block as a device tensor ``[Bt, n]`` (no host read)."""
         dev = self.recent_k.device
         if input_pos is None:
-            host = list(range(self.token_count, self.token_count + n))
-            return (torch.arange(self.token_count, self.token_count + n, device=dev).unsqueeze(0)
-                    .expand(self.batch_size, -1), [host[:] for _ in range(self.batch_size)])
+            return torch.arange(self.token_count, self.token_count + n, device=dev).unsqueeze(0).expand(
+                self.batch_size, -1)
         if input_pos.dim() == 1:
-            values = [int(x) for x in input_pos.detach().cpu().tolist()] if self.alpha_exact_tokens else None
-            dev_pos = input_pos.to(dev, torch.int64).unsqueeze(0).expand(self.batch_size, -1)
-            return dev_pos, None if values is None else [values[:] for _ in range(self.batch_size)]
+            return input_pos.to(dev, torch.int64).unsqueeze(0).expand(self.batch_size, -1)
         if input_pos.dim() == 2:
-            host = ([[int(x) for x in row] for row in input_pos.detach().cpu().tolist()]
-                    if self.alpha_exact_tokens else None)
-            return input_pos.to(dev, torch.int64), host
+            return input_pos.to(dev, torch.int64)
         raise ValueError(f"input_pos must be 1-D or 2-D, got shape {tuple(input_pos.shape)}")
+
+    def _span_ends_block(self, span_ends, n):
+        """Boundary flags of an appended block as uint8 ``[Bt, n]`` on the device: a tensor (bool or
+        integer, any device) or per-row host lists, as the reference takes them."""
+        dev = self.recent_k.device
+        if isinstance(span_ends, torch.Tensor):
+            if tuple(span_ends.shape) != (self.batch_size, n):
+                raise ValueError("AlphaLogKV span boundaries must match the input batch and token count")
+            return span_ends.to(dev, torch.uint8)
+        if span_ends is None or len(span_ends) != self.batch_size or any(len(row) != n for row in span_ends):
+            raise ValueError("AlphaLogKV span boundaries must match the input batch and token count")
+        host = torch.tensor([[bool(x) for x in row] for row in span_ends], dtype=torch.uint8)
+        return host.pin_memory().to(dev, non_blocking=True)
 
     @torch.no_grad()
     def add_recent(self, k, v, *, k_raw=None, input_pos=None, record_op_log=False, replay_op_log=None,
@@ -712,12 +719,8 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError(f"chunk size {n} exceeds recent_size {self.recent_size}")
         if k_raw.shape[:3] != k.shape[:3] or k_raw.size(-1) != self.k_dim:
             raise ValueError(f"k_raw shape {tuple(k_raw.shape)} does not match semantic cache shape")
-        positions, positions_host = self._input_positions(n, input_pos)
-        if self.alpha_exact_tokens:
-            if span_ends is None or len(span_ends) != self.batch_size or any(len(row) != n for row in span_ends):
-                raise ValueError("AlphaLogKV span boundaries must match the input batch and token count")
-            for b in range(self.batch_size):
-                self._recent_span_ends[b][self.recent_count:self.recent_count + n] = list(span_ends[b])
+        positions = self._input_positions(n, input_pos)
+        ends = self._span_ends_block(span_ends, n) if self.alpha_exact_tokens else None
         if self.token_count + n > self.max_seq_length:
             raise RuntimeError(
                 f"LogStructuredKVCache: token overflow! token_count={self.token_count}, n={n}, "
@@ -731,9 +734,8 @@ class LogStructuredKVCache(nn.Module):
         self.recent_k_raw[:, :, dst] = k_raw
         self.recent_v[:, :, dst] = v
         self.recent_pos[:, dst] = positions
-        if positions_host is not None:
-            for b in range(self.batch_size):
-                self._recent_pos_host[b][self.recent_count:self.recent_count + n] = positions_host[b]
+        if ends is not None:
+            self.recent_span_ends[:, dst] = ends
         self.recent_count += n
         overflow = self.recent_count - self.recent_size
         if overflow > 0:
@@ -758,14 +760,13 @@ class LogStructuredKVCache(nn.Module):
         self.op_log = self.op_log_len = None
         self._op_replay_cursor_host = None
         self._tape_index = 0
-        self._recent_pos_host = [[0] * self.recent_capacity for _ in range(self.batch_size)]
         if self.alpha_exact_tokens:
             for name in ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid", "alpha_span_len", "alpha_span_closed",
                          "alpha_span_count", "alpha_count_dev"):
                 getattr(self, name).zero_()
             for t in self._alpha_spare:
                 t.zero_()
-            self._recent_span_ends = [[False] * self.recent_capacity for _ in range(self.batch_size)]
+            self.recent_span_ends.zero_()
 
     def _apply(self, fn, recurse=True):
         # Moving or casting buffers invalidates raw pointers held in workspaces
