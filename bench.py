@@ -488,6 +488,11 @@ def prefill_workload(args, torch, np):
         pos = torch.arange(blk * F, (blk + 1) * F, device=dev).unsqueeze(0)
         ends = torch.tensor([[(p + 7) % 32 == 0 for p in range(blk * F, (blk + 1) * F)]], dtype=torch.uint8,
                             device=dev)
+        # Rows the block's attention reads in layer 0 (every layer holds the same counts):
+        # the pooled width (largest lane), the exact pool, the recent window and the block.
+        c0 = caches[0]
+        rows = int(c0.level_count.long().sum((-1, -2)).max()) + c0.alpha_count + c0.recent_count + F
+        attn_flops.append(layers * 4 * F * rows * D * HQ)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         events = []
@@ -501,9 +506,6 @@ def prefill_workload(args, torch, np):
         torch.cuda.synchronize()
         block_ms.append((time.perf_counter() - t0) * 1e3)
         attn_ms.append(float(np.sum([e[0].elapsed_time(e[1]) for e in events])))
-        c0 = caches[0]
-        rows = int(c0.level_count.long().sum(-1).max()) + c0.alpha_count + c0.recent_count
-        attn_flops.append(layers * 4 * F * rows * D * HQ)
         slots.append(float(c0.level_count.float().sum() / (G * K)))
     attn_s = float(np.sum(attn_ms)) * 1e-3
     tflops = float(np.sum(attn_flops)) / attn_s / 1e12

@@ -376,10 +376,15 @@ int logkv_decode_attention(const logkv_attention_args* args, const int32_t* tabl
 
 /* The same attention for many query rows per KV group (a prefill or training
  * chunk), on the matrix cores (bf16 MFMA, fp32 accumulation, P split into two
- * bf16 parts): packed width <= 144, dv in {32, 64, 96, 128}, no workspace.
+ * bf16 parts): packed width <= 144, dv in {32, 64, 96, 128}. The key range is
+ * split over several blocks per query tile when that fills the GPU better;
+ * their partials go to the workspace (logkv_chunk_workspace_bytes, 0 when
+ * not split) and are combined in split order.
  * Replaces the Flash SDPA call of _packed_flash_attention / _mid_chunk_attention
  * on a chunk (litgpt/log_kv_cache.py:6751-6758, :6802-6836). */
-int logkv_chunk_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints, void* stream);
+int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* args);
+int logkv_chunk_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
+                          void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

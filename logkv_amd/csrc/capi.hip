@@ -464,7 +464,13 @@ int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, 
   return LOGKV_OK;
 }
 
-int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, int64_t table_ints, void* stream) {
+int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* a) {
+  if (!a || a->n_groups < 1 || a->n_heads % a->n_groups) return -1;
+  return logkv::chunk_workspace_floats(*a) * 4;
+}
+
+int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, int64_t table_ints, void* ws,
+                          int64_t ws_bytes, void* stream) {
   if (!a || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention args or plan table are NULL");
   if (a->n_groups < 1 || a->n_heads % a->n_groups) return fail(LOGKV_EINVAL, "heads must be a multiple of groups");
   if (a->tq < 1) return fail(LOGKV_EINVAL, "query length must be >= 1");
@@ -478,7 +484,10 @@ int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, i
     return fail(LOGKV_EINVAL, "chunk attention output rows must be 8-byte aligned");
   if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
     return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
-  const int rc = logkv::launch_chunk_attention(*a, table + table_ints - 1, static_cast<hipStream_t>(stream));
+  if (ws_bytes < logkv::chunk_workspace_floats(*a) * 4 || (logkv::chunk_workspace_floats(*a) && !ws))
+    return fail(LOGKV_EINVAL, "chunk attention workspace too small");
+  const int rc = logkv::launch_chunk_attention(*a, table + table_ints - 1, static_cast<float*>(ws),
+                                               static_cast<hipStream_t>(stream));
   if (rc) return fail(rc, "chunk attention launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;
 }

@@ -16,6 +16,8 @@
 // of a 16-key step s is key 16s + 8(j/4) + 4(lane/32) + j%4, which is exactly
 // accumulator element 8(s%2) + j of S^T block s/2, so V^T is read with the same
 // key order and no data moves between lanes.
+#include <algorithm>
+
 #include "route.hpp"
 
 namespace logkv {
@@ -24,6 +26,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kQRows = 128;      // query rows per block (4 waves x 32)
 constexpr int kKeys = 64;        // key rows per staged tile
@@ -36,10 +40,15 @@ __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(
 
 }  // namespace
 
-__global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr) {
+// splits == 1: the block writes the output. splits > 1: block (x, s) covers the
+// s-th of `splits` equal parts (whole 64-row tiles) of its queries' key range
+// and writes partials [m, l, acc[dv]] per query in the decode combine's layout.
+__global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+                                                       int splits, float* __restrict__ part) {
   __shared__ __align__(16) uint16_t k_s[kKeys * kLdK];
   __shared__ __align__(16) uint16_t vt_s[kMaxDvBlocks * 32 * kLdV];
-  const int lane_ix = blockIdx.y, G = a.n_groups;
+  __shared__ __align__(16) uint16_t q_s[kQRows * kLdK];
+  const int lane_ix = blockIdx.z, split = blockIdx.y, G = a.n_groups;
   const int b = lane_ix / G, g = lane_ix % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
   const int w = wave_id(), l = lane_id(), h = l >> 5, col = l & 31;
@@ -54,18 +63,19 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
   const int q_first = blockIdx.x * kQRows, q_last = min(q_first + kQRows, nq) - 1;
   const int t_max = q_first / a.tq == q_last / a.tq ? q_last % a.tq : a.tq - 1;
   const int key_end = a.causal_tail ? min(total, tail0 + t_max + 1) : total;
+  // This block's part of the key range, in whole tiles.
+  const int tiles = (key_end + kKeys - 1) / kKeys, per = (tiles + splits - 1) / splits;
+  const int k_begin = min(split * per, tiles) * kKeys, k_stop = min(min((split + 1) * per, tiles) * kKeys, key_end);
 
-  // Query fragments [q, 1/scale, 0...] (B operand: dims 16 ks + 8 h + j of this lane's query).
-  bf16x8 qf[kMaxSteps];
-  const LOGKV_G uint16_t* qrow = gp(a.q) + b * a.q_sb + head * a.q_sh + t * a.q_st;
-#pragma unroll
-  for (int ks = 0; ks < kMaxSteps; ++ks) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 16 * ks + 8 * h + j;
-      const float x = d < a.dk ? bf16_to_f32(qrow[d < a.dk ? d : 0]) : (d == a.dk ? a.inv_scale_bf16 : 0.f);
-      qf[ks][j] = to_bf16(x);
-    }
+  // Queries [q, 1/scale, 0...] in LDS, row-major (the B operand reads dims
+  // 16 ks + 8 h .. + 8 of the lane's query).
+  for (int i = threadIdx.x; i < kQRows * kLdK; i += blockDim.x) {
+    const int r = i / kLdK, d = i - r * kLdK;
+    const int qr = min(blockIdx.x * kQRows + r, nq - 1);
+    const int hr = g * rep + qr / a.tq, tr = qr % a.tq;
+    const float x = d < a.dk ? bf16_to_f32(gp(a.q)[b * a.q_sb + hr * a.q_sh + tr * a.q_st + (d < a.dk ? d : 0)])
+                             : (d == a.dk ? a.inv_scale_bf16 : 0.f);
+    q_s[i] = f32_to_bf16(x);
   }
   // Columns past the packed width stay zero in every tile.
   for (int i = threadIdx.x; i < kKeys * (kLdK - dim); i += blockDim.x) {
@@ -77,42 +87,77 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
   for (int blk = 0; blk < kMaxDvBlocks; ++blk)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[blk][i] = 0.f;
-  float m = -__builtin_inff(), lsum = 0.f;
+  float m = -__builtin_inff(), lsum = 0.f;   // running maximum of s * scale * log2(e), and the sum
   const LOGKV_G uint16_t* kbase = gp(a.k) + static_cast<int64_t>(lane_ix) * a.cap * dim;
   const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * dim;
   const int units = dim / 8;
   const int vunits = a.dv / 8;
-
-  for (int t0 = 0; t0 < key_end; t0 += kKeys) {
-    const int rows = min(kKeys, key_end - t0);
-    __syncthreads();
-    // K rows (16-byte units), zero rows past the end.
-    for (int i = threadIdx.x; i < kKeys * units; i += blockDim.x) {
-      const int r = i / units, u = i - r * units;
-      const int src = t0 + min(r, rows - 1);
-      uint4 x = *(const LOGKV_G uint4*)(kbase + static_cast<int64_t>(src) * dim + 8 * u);
-      if (r >= rows) x = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(k_s + r * kLdK + 8 * u) = x;
+  // Each thread's staging tasks are the same in every tile: up to kKTasks
+  // 16-byte K units (row, unit) and kVTasks V tasks (key pair, 8-wide dv unit).
+  constexpr int kKTasks = (kKeys * kMaxSteps * 2 + 255) / 256, kVTasks = (kKeys / 2) * 16 / 256;
+  int k_row[kKTasks], k_goff[kKTasks], k_loff[kKTasks];
+#pragma unroll
+  for (int q = 0; q < kKTasks; ++q) {
+    const int i = threadIdx.x + 256 * q;
+    const bool ok = i < kKeys * units;
+    const int r = ok ? i / units : kKeys, u = ok ? i - (i / units) * units : 0;
+    k_row[q] = r;
+    k_goff[q] = 8 * u;
+    k_loff[q] = r * kLdK + 8 * u;
+  }
+  int v_pair[kVTasks], v_unit[kVTasks];
+#pragma unroll
+  for (int q = 0; q < kVTasks; ++q) {
+    const int i = threadIdx.x + 256 * q;
+    v_pair[q] = i < (kKeys / 2) * vunits ? i % (kKeys / 2) : -1;
+    v_unit[q] = i / (kKeys / 2);
+  }
+  // Registers of the next tile (loaded while the current one is computed).
+  uint4 kx[kKTasks], vx[kVTasks][2];
+  auto load_tile = [&](int t0) {
+    const int rows = min(kKeys, k_stop - t0);
+#pragma unroll
+    for (int q = 0; q < kKTasks; ++q) {
+      const int r = min(k_row[q], rows - 1);
+      kx[q] = *(const LOGKV_G uint4*)(kbase + static_cast<int64_t>(t0 + r) * dim + k_goff[q]);
+      if (k_row[q] >= rows) kx[q] = make_uint4(0, 0, 0, 0);
     }
-    // V^T: each task takes two consecutive key rows of one 8-wide dv unit and
-    // writes 8 dwords (key pairs), zero rows past the end.
-    for (int i = threadIdx.x; i < (kKeys / 2) * vunits; i += blockDim.x) {
-      const int kp = i % (kKeys / 2), u = i / (kKeys / 2);
-      const int r0 = 2 * kp, r1 = 2 * kp + 1;
-      uint4 x0 = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + min(r0, rows - 1)) * dim + 8 * u);
-      uint4 x1 = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + min(r1, rows - 1)) * dim + 8 * u);
-      if (r0 >= rows) x0 = make_uint4(0, 0, 0, 0);
-      if (r1 >= rows) x1 = make_uint4(0, 0, 0, 0);
-      const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w}, a1[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int q = 0; q < kVTasks; ++q) {
+      const int kp = v_pair[q] < 0 ? 0 : v_pair[q];
+      const int r0 = min(2 * kp, rows - 1), r1 = min(2 * kp + 1, rows - 1);
+      vx[q][0] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r0) * dim + 8 * v_unit[q]);
+      vx[q][1] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r1) * dim + 8 * v_unit[q]);
+      if (2 * kp >= rows) vx[q][0] = make_uint4(0, 0, 0, 0);
+      if (2 * kp + 1 >= rows) vx[q][1] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  if (k_begin < k_stop) load_tile(k_begin);
+
+  for (int t0 = k_begin; t0 < k_stop; t0 += kKeys) {
+    const int rows = min(kKeys, k_stop - t0);
+    __syncthreads();
+    // K rows row-major; V transposed: each task's two key rows of one 8-wide dv
+    // unit become 8 dwords (key pairs). Rows past the end are zeros.
+#pragma unroll
+    for (int q = 0; q < kKTasks; ++q)
+      if (k_row[q] < kKeys) *reinterpret_cast<uint4*>(k_s + k_loff[q]) = kx[q];
+#pragma unroll
+    for (int q = 0; q < kVTasks; ++q) {
+      if (v_pair[q] < 0) continue;
+      const uint32_t a0[4] = {vx[q][0].x, vx[q][0].y, vx[q][0].z, vx[q][0].w};
+      const uint32_t a1[4] = {vx[q][1].x, vx[q][1].y, vx[q][1].z, vx[q][1].w};
+      const int r0 = 2 * v_pair[q], u = v_unit[q];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = (a0[j] & 0xffffu) | (a1[j] << 16);
-        const uint32_t hi = (a0[j] >> 16) | (a1[j] & 0xffff0000u);
+        const uint32_t lo = __builtin_amdgcn_perm(a1[j], a0[j], 0x05040100u);   // low halves of rows r0, r0 + 1
+        const uint32_t hi = __builtin_amdgcn_perm(a1[j], a0[j], 0x07060302u);   // high halves
         *reinterpret_cast<uint32_t*>(vt_s + (8 * u + 2 * j) * kLdV + r0) = lo;
         *reinterpret_cast<uint32_t*>(vt_s + (8 * u + 2 * j + 1) * kLdV + r0) = hi;
       }
     }
     __syncthreads();
+    if (t0 + kKeys < k_stop) load_tile(t0 + kKeys);
     // S^T = K Q^T over the packed width.
     f32x16 s[2];
 #pragma unroll
@@ -123,33 +168,44 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
       for (int ks = 0; ks < kMaxSteps; ++ks) {
         if (ks < nks) {
           const bf16x8 kf = *reinterpret_cast<const bf16x8*>(k_s + (32 * kb + col) * kLdK + 16 * ks + 8 * h);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
+          const bf16x8 qf = *reinterpret_cast<const bf16x8*>(q_s + (32 * w + col) * kLdK + 16 * ks + 8 * h);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf, s[kb], 0, 0, 0);
         }
       }
     }
-    // Scores, masks, online softmax of this lane's query.
+    // Online softmax of this lane's query in the base-2 domain: with c2 = scale
+    // * log2(e), p = 2^(s c2 - m) where m is the running maximum of s c2. Masks
+    // (past the rows, causal) are evaluated only on tiles that need them.
+    const float c2 = a.scale * 1.44269504088896341f;
+    const bool full = rows == kKeys && !(a.causal_tail && t0 + kKeys > tail0);
     float mx = -__builtin_inff();
+    if (full) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = t0 + 32 * kb + 8 * (i / 4) + 4 * h + (i % 4);
-        float sc = a.scale * s[kb][i];
-        const bool masked = !q_ok || key >= t0 + rows || (a.causal_tail && key >= tail0 && key - tail0 > t);
-        sc = masked ? -__builtin_inff() : sc;
-        s[kb][i] = sc;
-        mx = fmaxf(mx, sc);
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = t0 + 32 * kb + 8 * (i / 4) + 4 * h + (i % 4);
+          const bool masked = key >= t0 + rows || (a.causal_tail && key >= tail0 && key - tail0 > t);
+          s[kb][i] = masked ? -__builtin_inff() : s[kb][i];
+          mx = fmaxf(mx, s[kb][i]);
+        }
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m, mx);
-    const float corr = m_new == -__builtin_inff() ? 1.f : __expf(m - m_new);
+    const float m_new = fmaxf(m, mx * c2);
+    const float mb = m_new == -__builtin_inff() ? 0.f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m - mb);
     float sum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = s[kb][i] == -__builtin_inff() ? 0.f : __expf(s[kb][i] - m_new);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], c2, -mb));
         s[kb][i] = p;
         sum += p;
       }
@@ -157,34 +213,34 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
     sum += __shfl_xor(sum, 32, kWave);
     lsum = lsum * corr + sum;
     m = m_new;
+    if (__ballot(corr != 1.f)) {
 #pragma unroll
-    for (int blk = 0; blk < kMaxDvBlocks; ++blk)
+      for (int blk = 0; blk < kMaxDvBlocks; ++blk)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[blk][i] *= corr;
-    // O^T += V^T P^T, four 16-key steps, P as high + low bf16 parts.
+        for (int i = 0; i < 16; ++i) o[blk][i] *= corr;
+    }
+    // O^T += V^T P^T, four 16-key steps, P as a truncated high bf16 part plus
+    // the rounded remainder (together ~16 significant bits of P).
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      bf16x8 ph, pl;
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = s[st / 2][8 * (st % 2) + j];
-        const __bf16 hi = to_bf16(p);
-        ph[j] = hi;
-        pl[j] = to_bf16(p - static_cast<float>(hi));
+      for (int j = 0; j < 4; ++j) {
+        const float p0 = s[st / 2][8 * (st % 2) + 2 * j], p1 = s[st / 2][8 * (st % 2) + 2 * j + 1];
+        const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+        hw[j] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+        const float r0 = p0 - __uint_as_float(u0 & 0xffff0000u), r1 = p1 - __uint_as_float(u1 & 0xffff0000u);
+        lw[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{r0, r1}, bf16x2));   // one packed RNE
       }
+      const bf16x8 ph = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+      const bf16x8 pl = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
       for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
         if (blk < ndv) {
           const uint16_t* vr = vt_s + (32 * blk + col) * kLdV + 16 * st + 4 * h;
           const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
           const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
-          bf16x8 vf;
-          const uint32_t wv[4] = {v0.x, v0.y, v1.x, v1.y};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            vf[2 * j] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(wv[j] & 0xffffu));
-            vf[2 * j + 1] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(wv[j] >> 16));
-          }
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
           o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[blk], 0, 0, 0);
           o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[blk], 0, 0, 0);
         }
@@ -192,6 +248,25 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
     }
   }
   if (!q_ok) return;
+  if (splits > 1) {
+    float* pp = part + ((static_cast<int64_t>(lane_ix) * splits + split) * nq + qi) * (a.dv + 2);
+    if (h == 0) {
+      pp[0] = m;
+      pp[1] = lsum;
+    }
+#pragma unroll
+    for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
+      if (blk < ndv) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int d = 32 * blk + 8 * i4 + 4 * h;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pp[2 + d + j] = o[blk][4 * i4 + j];
+        }
+      }
+    }
+    return;
+  }
   LOGKV_G uint16_t* orow = gp(a.out) + b * a.o_sb + head * a.o_sh + t * a.o_st;
 #pragma unroll
   for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
@@ -209,10 +284,57 @@ __global__ __launch_bounds__(256) void chunk_kernel(logkv_attention_args a, cons
   }
 }
 
-int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, hipStream_t stream) {
+// Partials of the key-range splits combined in split order: two queries per
+// block, one output feature per thread.
+__global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args a, const float* __restrict__ part,
+                                                            int splits) {
+  const int lane_ix = blockIdx.y, G = a.n_groups;
+  const int b = lane_ix / G, g = lane_ix % G;
+  const int rep = a.n_heads / G, nq = rep * a.tq;
+  const int qi = blockIdx.x * 2 + static_cast<int>(threadIdx.x) / 128, d = threadIdx.x % 128;
+  if (qi >= nq || d >= a.dv) return;
+  const int stride = a.dv + 2;
+  const float* base = part + (static_cast<int64_t>(lane_ix) * splits * nq + qi) * stride;
+  const int64_t step = static_cast<int64_t>(nq) * stride;
+  float m = -__builtin_inff();
+  for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, base[sp * step]);
+  float lsum = 0.f, acc = 0.f;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* pp = base + sp * step;
+    if (pp[0] == -__builtin_inff()) continue;
+    const float f = __expf(pp[0] - m);
+    lsum += pp[1] * f;
+    acc += pp[2 + d] * f;
+  }
+  const int head = g * rep + qi / a.tq, t = qi % a.tq;
+  gp(a.out)[b * a.o_sb + head * a.o_sh + t * a.o_st + d] = f32_to_bf16(acc / lsum);
+}
+
+// Key-range splits: enough blocks for about four per CU, at most one per
+// 1024 rows of the packed capacity.
+int chunk_splits(const logkv_attention_args& a) {
   const int nq = (a.n_heads / a.n_groups) * a.tq;
-  hipLaunchKernelGGL(chunk_kernel, dim3((nq + kQRows - 1) / kQRows, a.n_batch * a.n_groups), dim3(256), 0, stream, a,
-                     width);
+  const int64_t blocks = static_cast<int64_t>((nq + kQRows - 1) / kQRows) * a.n_batch * a.n_groups;
+  int splits = static_cast<int>((1024 + blocks - 1) / blocks);
+  splits = std::min(splits, std::max(1, a.cap / 1024));
+  return std::max(1, std::min(splits, 16));
+}
+
+int64_t chunk_workspace_floats(const logkv_attention_args& a) {
+  const int splits = chunk_splits(a);
+  if (splits == 1) return 0;
+  const int nq = (a.n_heads / a.n_groups) * a.tq;
+  return static_cast<int64_t>(a.n_batch) * a.n_groups * splits * nq * (a.dv + 2);
+}
+
+int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
+  const int nq = (a.n_heads / a.n_groups) * a.tq;
+  const int splits = chunk_splits(a);
+  hipLaunchKernelGGL(chunk_kernel, dim3((nq + kQRows - 1) / kQRows, splits, a.n_batch * a.n_groups), dim3(256), 0,
+                     stream, a, width, splits, part);
+  if (splits > 1)
+    hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a, part,
+                       splits);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

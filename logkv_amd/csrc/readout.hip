@@ -487,6 +487,11 @@ int64_t attention_workspace_floats(const logkv_attention_args& a) {
   return static_cast<int64_t>(a.n_batch) * a.n_groups * n_split * nq * (a.dv + 2);
 }
 
+int launch_combine(const logkv_attention_args& a, const float* part, int n_split, hipStream_t stream) {
+  hipLaunchKernelGGL(combine_kernel, dim3(a.n_batch * a.n_groups), dim3(256), 0, stream, a, part, n_split);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
 int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
   const int n_split = (a.cap + kSplitRows - 1) / kSplitRows;
   const int lanes = a.n_batch * a.n_groups;

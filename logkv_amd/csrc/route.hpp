@@ -67,7 +67,9 @@ int launch_plan(const logkv_readout_view& c, int32_t* table, hipStream_t stream)
 int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int32_t* table, hipStream_t stream);
 int64_t attention_workspace_floats(const logkv_attention_args& a);
 int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream);
-int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, hipStream_t stream);
+int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream);
+int64_t chunk_workspace_floats(const logkv_attention_args& a);
+int launch_combine(const logkv_attention_args& a, const float* part, int n_split, hipStream_t stream);
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
 int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream);

@@ -186,8 +186,14 @@ def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups,
                          ka.size(2), tail, causal_tail, float(scale), _inv_scale_bf16(scale), ptr(out),
                          *out.stride()[:3], ptr(alpha_count_dev))
     if (hq // n_groups) * tq > 16:
-        # Many query rows per KV group: the matrix-core chunk kernel (no workspace).
-        check(lib().logkv_chunk_attention(C.byref(args), ptr(plan.table), plan.table.numel(), stream_of(q.device)),
+        # Many query rows per KV group: the matrix-core chunk kernel.
+        need = int(lib().logkv_chunk_workspace_bytes(C.byref(args)))
+        if need < 0:
+            raise ValueError("bad attention shape")
+        if need and (workspace is None or workspace.numel() < need):
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        check(lib().logkv_chunk_attention(C.byref(args), ptr(plan.table), plan.table.numel(),
+                                          ptr(workspace) if need else None, need, stream_of(q.device)),
               "logkv_chunk_attention")
         return out, workspace
     need = int(lib().logkv_attention_workspace_bytes(C.byref(args)))
