@@ -28,7 +28,8 @@ namespace {
 
 constexpr int kPlanThreads = 256;
 constexpr int kTile = 64;          // rows per staged K/V tile
-constexpr int kSplitRows = 512;    // rows per attention split
+constexpr int kSplitRows = 512;    // rows per attention split (staged decode kernel)
+constexpr int kStreamRows = 512;   // rows per split of the streaming kernel (256 measured slower)
 constexpr int kMaxQ = 16;          // queries per KV group (heads per group x query rows)
 constexpr int kMaxPacked = 264;    // packed row width limit (dk + 1 rounded to 8, dv)
 constexpr int kAccPerThread = kMaxQ * kMaxDim / 256;   // outputs per thread of a 256-thread split block
@@ -439,6 +440,145 @@ __global__ __launch_bounds__(256) void decode_kernel(logkv_attention_args a, con
   }
 }
 
+// Streaming decode for at most 4 queries per KV group (a decode step of GQA
+// heads): no staging of K / V in LDS. A block is 16 row groups of 16 lanes; a
+// group reads one packed row at a time (its 16-byte units spread over the 16
+// lanes: [q, 1/scale] . [k, bias] folded over the group), keeps its own online
+// softmax per query and accumulates its lanes' 8-wide slices of V, rows
+// 4 at a time with all loads issued first; 512-row splits. At the end of the split the 16
+// groups are combined in LDS in group order and the split's partials go to
+// the workspace in the layout the split combine reads.
+template <int NQ, int UJ>
+__global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+                                                     float* __restrict__ part) {
+  constexpr int kGroups = 16, kGl = 16, kRows = 4;
+  __shared__ float m_s[kGroups][NQ], l_s[kGroups][NQ];
+  __shared__ float acc_s[kGroups][NQ][128];
+  const int lane = blockIdx.y, G = a.n_groups;
+  const int b = lane / G, g = lane % G;
+  const int rep = a.n_heads / G, nq = rep * a.tq;
+  const int grp = threadIdx.x / kGl, gl = threadIdx.x % kGl;
+  const int dim = a.dim, units = dim / 8, vunits = a.dv / 8;
+  const int total = min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
+  const int tail0 = total - a.causal_tail;
+  const int r_begin = blockIdx.x * kStreamRows, r_end = min(r_begin + kStreamRows, total);
+  float* out = part + (static_cast<int64_t>(lane) * gridDim.x + blockIdx.x) * nq * (a.dv + 2);
+  // This lane's slices of the queries [q, 1/scale (bf16), 0...]: units gl + 16 j.
+  float qv[NQ][UJ][8];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int qq = q < nq ? q : nq - 1;
+    const int h = g * rep + qq / a.tq, t = qq % a.tq;
+#pragma unroll
+    for (int j = 0; j < UJ; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * (gl + kGl * j) + e;
+        float x = 0.f;
+        if (d < a.dk) x = bf16_to_f32(gp(a.q)[b * a.q_sb + h * a.q_sh + t * a.q_st + d]);
+        else if (d == a.dk) x = a.inv_scale_bf16;
+        qv[q][j][e] = q < nq ? x : 0.f;
+      }
+    }
+  }
+  float m[NQ], l[NQ], acc[NQ][8];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    m[q] = -__builtin_inff();
+    l[q] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[q][e] = 0.f;
+  }
+  const LOGKV_G uint16_t* kbase = gp(a.k) + static_cast<int64_t>(lane) * a.cap * dim;
+  const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane) * a.cap * dim;
+  const bool v_on = gl < vunits;
+  for (int r0 = r_begin + grp; r0 < r_end; r0 += kGroups * kRows) {
+    uint4 kx[kRows][UJ], vx[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int row = min(r0 + kGroups * i, r_end - 1);
+#pragma unroll
+      for (int j = 0; j < UJ; ++j) {
+        const int u = min(gl + kGl * j, units - 1);
+        kx[i][j] = *(const LOGKV_G uint4*)(kbase + static_cast<int64_t>(row) * dim + 8 * u);
+      }
+      vx[i] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * dim + 8 * (v_on ? gl : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int row = r0 + kGroups * i;
+      if (row >= r_end) break;
+      float dot[NQ];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) dot[q] = 0.f;
+#pragma unroll
+      for (int j = 0; j < UJ; ++j) {
+        if (gl + kGl * j < units) {
+          const uint32_t w4[4] = {kx[i][j].x, kx[i][j].y, kx[i][j].z, kx[i][j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float k0 = __uint_as_float(w4[e] << 16), k1 = __uint_as_float(w4[e] & 0xffff0000u);
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+              dot[q] = __builtin_fmaf(qv[q][j][2 * e], k0, dot[q]);
+              dot[q] = __builtin_fmaf(qv[q][j][2 * e + 1], k1, dot[q]);
+            }
+          }
+        }
+      }
+      const uint32_t v4[4] = {vx[i].x, vx[i].y, vx[i].z, vx[i].w};
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+        for (int off = kGl / 2; off >= 1; off >>= 1) dot[q] += __shfl_xor(dot[q], off, kGl);
+        float sc = a.scale * dot[q];
+        const int t = (q < nq ? q : nq - 1) % a.tq;
+        if (q >= nq || (a.causal_tail && row >= tail0 && row - tail0 > t)) sc = -__builtin_inff();
+        const float m_new = fmaxf(m[q], sc);
+        const float corr = m_new == -__builtin_inff() ? 1.f : __expf(m[q] - m_new);
+        const float p = sc == -__builtin_inff() ? 0.f : __expf(sc - m_new);
+        l[q] = l[q] * corr + p;
+        m[q] = m_new;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[q][2 * e] = __builtin_fmaf(p, __uint_as_float(v4[e] << 16), acc[q][2 * e] * corr);
+          acc[q][2 * e + 1] = __builtin_fmaf(p, __uint_as_float(v4[e] & 0xffff0000u), acc[q][2 * e + 1] * corr);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (gl == 0) {
+      m_s[grp][q] = m[q];
+      l_s[grp][q] = l[q];
+    }
+    if (v_on) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc_s[grp][q][8 * gl + e] = acc[q][e];
+    }
+  }
+  __syncthreads();
+  // Groups combined in group order: [m, l, acc[dv]] per query of this split.
+  for (int o = threadIdx.x; o < nq * (a.dv + 2); o += blockDim.x) {
+    const int q = o / (a.dv + 2), c = o % (a.dv + 2);
+    float mx = -__builtin_inff();
+    for (int gg = 0; gg < kGroups; ++gg) mx = fmaxf(mx, m_s[gg][q]);
+    float val;
+    if (c == 0) {
+      val = mx;
+    } else {
+      val = 0.f;
+      for (int gg = 0; gg < kGroups; ++gg) {
+        if (m_s[gg][q] == -__builtin_inff()) continue;
+        const float f = __expf(m_s[gg][q] - mx);
+        val += (c == 1 ? l_s[gg][q] : acc_s[gg][q][c - 2]) * f;
+      }
+    }
+    out[o] = val;
+  }
+}
+
 // Combine the splits of each (lane, query) in split order.
 __global__ __launch_bounds__(256) void combine_kernel(logkv_attention_args a, const float* __restrict__ part,
                                                       int n_split) {
@@ -481,8 +621,13 @@ int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
+bool use_stream(const logkv_attention_args& a) {
+  const int nq = (a.n_heads / a.n_groups) * a.tq;
+  return nq <= 4 && a.dv <= 128 && (a.dim / 8 + 15) / 16 <= 3;
+}
+
 int64_t attention_workspace_floats(const logkv_attention_args& a) {
-  const int n_split = (a.cap + kSplitRows - 1) / kSplitRows;
+  const int n_split = (a.cap + (use_stream(a) ? kStreamRows : kSplitRows) - 1) / (use_stream(a) ? kStreamRows : kSplitRows);
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   return static_cast<int64_t>(a.n_batch) * a.n_groups * n_split * nq * (a.dv + 2);
 }
@@ -493,9 +638,32 @@ int launch_combine(const logkv_attention_args& a, const float* part, int n_split
 }
 
 int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
-  const int n_split = (a.cap + kSplitRows - 1) / kSplitRows;
+  const int rows = use_stream(a) ? kStreamRows : kSplitRows;
+  const int n_split = (a.cap + rows - 1) / rows;
   const int lanes = a.n_batch * a.n_groups;
-  hipLaunchKernelGGL(decode_kernel, dim3(n_split, lanes), dim3(256), 0, stream, a, width, part);
+  const int nq = (a.n_heads / a.n_groups) * a.tq;
+  const int uj = (a.dim / 8 + 15) / 16;
+  const dim3 grid(n_split, lanes);
+  auto stream_launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a, width, part);
+  };
+  if (use_stream(a)) {
+    if (nq == 1) {
+      if (uj == 1) stream_launch(stream_kernel<1, 1>);
+      else if (uj == 2) stream_launch(stream_kernel<1, 2>);
+      else stream_launch(stream_kernel<1, 3>);
+    } else if (nq == 2) {
+      if (uj == 1) stream_launch(stream_kernel<2, 1>);
+      else if (uj == 2) stream_launch(stream_kernel<2, 2>);
+      else stream_launch(stream_kernel<2, 3>);
+    } else {
+      if (uj == 1) stream_launch(stream_kernel<4, 1>);
+      else if (uj == 2) stream_launch(stream_kernel<4, 2>);
+      else stream_launch(stream_kernel<4, 3>);
+    }
+  } else {
+    hipLaunchKernelGGL(decode_kernel, grid, dim3(256), 0, stream, a, width, part);
+  }
   hipLaunchKernelGGL(combine_kernel, dim3(lanes), dim3(256), 0, stream, a, part, n_split);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
