@@ -453,7 +453,7 @@ def decode_workload(args, torch, np):
                     "tokens per lane, masses ~ U(1,64); packed prefix reused, one new row per step",
         "ms_per_token": ms, "ms_per_token_28_layers": 28 * ms, "steps": steps,
         "packed_rows_per_lane": rows, "pooled_width": width,
-        "roofline": {"kernel": "decode_kernel + combine_kernel", "bound": "hbm", "achieved": achieved,
+        "roofline": {"kernel": "stream_kernel + combine_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": attn_ms},
     }

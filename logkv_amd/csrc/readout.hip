@@ -448,7 +448,12 @@ __global__ __launch_bounds__(256) void decode_kernel(logkv_attention_args a, con
 // 4 at a time with all loads issued first; 512-row splits. At the end of the split the 16
 // groups are combined in LDS in group order and the split's partials go to
 // the workspace in the layout the split combine reads.
-template <int NQ, int UJ>
+//
+// SPLIT (dk a multiple of 8): the key's bias column dk starts a unit of its
+// own, so the 16-byte units cover only the dk features and the bias is one
+// 2-byte load per row, added after the group fold as q[dk] * bias; UJ then
+// counts units of the dk features only (8 registers per row and query fewer).
+template <int NQ, int UJ, bool SPLIT>
 __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
                                                      float* __restrict__ part) {
   constexpr int kGroups = 16, kGl = 16, kRows = 4;
@@ -458,7 +463,8 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
   const int b = lane / G, g = lane % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
   const int grp = threadIdx.x / kGl, gl = threadIdx.x % kGl;
-  const int dim = a.dim, units = dim / 8, vunits = a.dv / 8;
+  const int dim = a.dim, units = SPLIT ? a.dk / 8 : dim / 8, vunits = (a.dv + 7) / 8;   // the last unit may run into the zero pad (dim >= 8 * vunits)
+  const float q_bias = a.inv_scale_bf16;
   const int total = min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
   const int tail0 = total - a.causal_tail;
   const int r_begin = blockIdx.x * kStreamRows, r_end = min(r_begin + kStreamRows, total);
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
         const int d = 8 * (gl + kGl * j) + e;
         float x = 0.f;
         if (d < a.dk) x = bf16_to_f32(gp(a.q)[b * a.q_sb + h * a.q_sh + t * a.q_st + d]);
-        else if (d == a.dk) x = a.inv_scale_bf16;
+        else if (!SPLIT && d == a.dk) x = a.inv_scale_bf16;
         qv[q][j][e] = q < nq ? x : 0.f;
       }
     }
@@ -494,6 +500,7 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
   const bool v_on = gl < vunits;
   for (int r0 = r_begin + grp; r0 < r_end; r0 += kGroups * kRows) {
     uint4 kx[kRows][UJ], vx[kRows];
+    uint16_t kb[kRows];
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
       const int row = min(r0 + kGroups * i, r_end - 1);
@@ -502,6 +509,7 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
         const int u = min(gl + kGl * j, units - 1);
         kx[i][j] = *(const LOGKV_G uint4*)(kbase + static_cast<int64_t>(row) * dim + 8 * u);
       }
+      if (SPLIT) kb[i] = kbase[static_cast<int64_t>(row) * dim + a.dk];
       vx[i] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * dim + 8 * (v_on ? gl : 0));
     }
 #pragma unroll
@@ -531,6 +539,7 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
       for (int q = 0; q < NQ; ++q) {
 #pragma unroll
         for (int off = kGl / 2; off >= 1; off >>= 1) dot[q] += __shfl_xor(dot[q], off, kGl);
+        if (SPLIT) dot[q] = __builtin_fmaf(q_bias, bf16_to_f32(kb[i]), dot[q]);
         float sc = a.scale * dot[q];
         const int t = (q < nq ? q : nq - 1) % a.tq;
         if (q >= nq || (a.causal_tail && row >= tail0 && row - tail0 > t)) sc = -__builtin_inff();
@@ -579,21 +588,25 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
   }
 }
 
-// Combine the splits of each (lane, query) in split order.
+// Combine the splits of each (lane, query) in split order: one block per
+// (lane, query), one output feature per thread. An empty split carries
+// m = -inf with zero sums, so it adds exp(-inf) * 0 = 0 and needs no test.
 __global__ __launch_bounds__(256) void combine_kernel(logkv_attention_args a, const float* __restrict__ part,
                                                       int n_split) {
-  const int lane = blockIdx.x;
+  const int lane = blockIdx.x, qi = blockIdx.y;
   const int G = a.n_groups, rep = a.n_heads / G, nq = rep * a.tq;
   const int b = lane / G, g = lane % G;
-  for (int o = threadIdx.x; o < nq * a.dv; o += blockDim.x) {
-    const int qi = o / a.dv, d = o % a.dv;
+  const int stride = a.dv + 2;
+  const float* base = part + (static_cast<int64_t>(lane) * n_split * nq + qi) * stride;
+  const int64_t step = static_cast<int64_t>(nq) * stride;
+  for (int d = threadIdx.x; d < a.dv; d += blockDim.x) {
     float m = -__builtin_inff();
-    for (int sp = 0; sp < n_split; ++sp)
-      m = fmaxf(m, part[((static_cast<int64_t>(lane) * n_split + sp) * nq + qi) * (a.dv + 2)]);
+#pragma unroll 8
+    for (int sp = 0; sp < n_split; ++sp) m = fmaxf(m, base[sp * step]);
     float lsum = 0.f, acc = 0.f;
+#pragma unroll 8
     for (int sp = 0; sp < n_split; ++sp) {
-      const float* pp = part + ((static_cast<int64_t>(lane) * n_split + sp) * nq + qi) * (a.dv + 2);
-      if (pp[0] == -__builtin_inff()) continue;
+      const float* pp = base + sp * step;
       const float f = __expf(pp[0] - m);
       lsum += pp[1] * f;
       acc += pp[2 + d] * f;
@@ -621,9 +634,16 @@ int launch_pack(const logkv_readout_view& c, const logkv_pack_args& p, const int
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
+// 16-byte key units per row group lane of the streaming kernel (the bias
+// column excluded when it starts a unit of its own).
+int stream_key_units(const logkv_attention_args& a) {
+  const int units = a.dk % 8 == 0 ? a.dk / 8 : a.dim / 8;
+  return (units + 15) / 16;
+}
+
 bool use_stream(const logkv_attention_args& a) {
   const int nq = (a.n_heads / a.n_groups) * a.tq;
-  return nq <= 4 && a.dv <= 128 && (a.dim / 8 + 15) / 16 <= 3;
+  return nq <= 4 && a.dv <= 128 && a.dk >= 8 && stream_key_units(a) <= 3;
 }
 
 int64_t attention_workspace_floats(const logkv_attention_args& a) {
@@ -633,7 +653,8 @@ int64_t attention_workspace_floats(const logkv_attention_args& a) {
 }
 
 int launch_combine(const logkv_attention_args& a, const float* part, int n_split, hipStream_t stream) {
-  hipLaunchKernelGGL(combine_kernel, dim3(a.n_batch * a.n_groups), dim3(256), 0, stream, a, part, n_split);
+  hipLaunchKernelGGL(combine_kernel, dim3(a.n_batch * a.n_groups, (a.n_heads / a.n_groups) * a.tq),
+                     dim3(a.dv <= 64 ? 64 : 128), 0, stream, a, part, n_split);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
@@ -642,29 +663,30 @@ int launch_attention(const logkv_attention_args& a, const int32_t* width, float*
   const int n_split = (a.cap + rows - 1) / rows;
   const int lanes = a.n_batch * a.n_groups;
   const int nq = (a.n_heads / a.n_groups) * a.tq;
-  const int uj = (a.dim / 8 + 15) / 16;
+  const int uj = stream_key_units(a);
   const dim3 grid(n_split, lanes);
   auto stream_launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a, width, part);
   };
+  auto by_units = [&](auto one, auto two, auto three) {
+    if (uj == 1) stream_launch(one);
+    else if (uj == 2) stream_launch(two);
+    else stream_launch(three);
+  };
   if (use_stream(a)) {
-    if (nq == 1) {
-      if (uj == 1) stream_launch(stream_kernel<1, 1>);
-      else if (uj == 2) stream_launch(stream_kernel<1, 2>);
-      else stream_launch(stream_kernel<1, 3>);
-    } else if (nq == 2) {
-      if (uj == 1) stream_launch(stream_kernel<2, 1>);
-      else if (uj == 2) stream_launch(stream_kernel<2, 2>);
-      else stream_launch(stream_kernel<2, 3>);
+    if (a.dk % 8 == 0) {
+      if (nq == 1) by_units(stream_kernel<1, 1, true>, stream_kernel<1, 2, true>, stream_kernel<1, 3, true>);
+      else if (nq == 2) by_units(stream_kernel<2, 1, true>, stream_kernel<2, 2, true>, stream_kernel<2, 3, true>);
+      else by_units(stream_kernel<4, 1, true>, stream_kernel<4, 2, true>, stream_kernel<4, 3, true>);
     } else {
-      if (uj == 1) stream_launch(stream_kernel<4, 1>);
-      else if (uj == 2) stream_launch(stream_kernel<4, 2>);
-      else stream_launch(stream_kernel<4, 3>);
+      if (nq == 1) by_units(stream_kernel<1, 1, false>, stream_kernel<1, 2, false>, stream_kernel<1, 3, false>);
+      else if (nq == 2) by_units(stream_kernel<2, 1, false>, stream_kernel<2, 2, false>, stream_kernel<2, 3, false>);
+      else by_units(stream_kernel<4, 1, false>, stream_kernel<4, 2, false>, stream_kernel<4, 3, false>);
     }
   } else {
     hipLaunchKernelGGL(decode_kernel, grid, dim3(256), 0, stream, a, width, part);
   }
-  hipLaunchKernelGGL(combine_kernel, dim3(lanes), dim3(256), 0, stream, a, part, n_split);
+  hipLaunchKernelGGL(combine_kernel, dim3(lanes, nq), dim3(a.dv <= 64 ? 64 : 128), 0, stream, a, part, n_split);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

@@ -184,6 +184,31 @@ def test_decode_qwen_shape():
     check_step(cache, cos, sin, q, k, v, dk ** -0.5, reuse=True)
 
 
+@pytest.mark.parametrize("dk,dv,heads,groups,tq", [
+    (128, 128, 8, 8, 1),    # one query per KV group; the bias column starts a 16-byte unit of its own
+    (120, 120, 6, 2, 1),    # three queries per group (one idle query slot)
+    (128, 128, 8, 2, 1),    # four queries per group
+    (60, 60, 4, 2, 1),      # dk not a multiple of 8: the bias shares a unit with the last key features
+    (200, 104, 2, 2, 1),    # two key units per lane, narrower values
+    (132, 128, 2, 2, 2),    # two current rows (causal), bias sharing a unit, two key units per lane
+])
+def test_streaming_decode_shapes(dk, dv, heads, groups, tq):
+    """Decode steps of up to 4 query rows per KV group take the streaming kernel; every variant of it
+    (queries per group, key units per lane, bias column on its own or not) against the oracle."""
+    print(f"case dk={dk} dv={dv} heads={heads} groups={groups} tq={tq}", flush=True)
+    cos, sin = rope_tables(2048, dk)
+    cache = LogStructuredKVCache(
+        (2, groups, 2048, dk), (2, groups, 2048, dv), B=16, recent_size=128, device="cuda", dtype=torch.bfloat16,
+        semantic_clusters=True, cluster_k_max=4, semantic_flush_granularity=128, semantic_anchor_mode="mid",
+        allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk, alpha_exact_tokens=16,
+        alpha_span_max_tokens=8)
+    fill_readout_state(cache, seed=dk + tq, recent=100)
+    g = torch.Generator().manual_seed(dk)
+    q = rand_bf16(g, 2, heads, tq, dk)
+    k, v = rand_bf16(g, 2, groups, tq, dk), rand_bf16(g, 2, groups, tq, dv)
+    check_step(cache, cos, sin, q, k, v, dk ** -0.5)
+
+
 def test_causal_chunk():
     """A multi-row chunk: row i sees the prefix and current rows 0..i only."""
     dk = 64
