@@ -24,7 +24,8 @@ extern "C" {
 
 enum { LOGKV_OK = 0, LOGKV_EINVAL = 1, LOGKV_ERUNTIME = 2 };
 
-/* Persistent ladder and cluster state (all device pointers). */
+/* Persistent ladder and cluster state (all device pointers; level_k, level_v and
+ * centroid 16-byte aligned). */
 typedef struct logkv_ladder_view {
   uint16_t* level_k;      /* bf16 [lanes, K, L, B', dk] */
   uint16_t* level_v;      /* bf16 [lanes, K, L, B', dv] */

@@ -41,6 +41,9 @@ int check_ladder(const logkv_ladder_view* c) {
       !c->level_order || !c->pad_mask || !c->level_count || !c->centroid || !c->n_eff || !c->n_total ||
       !c->p_hi_c || !c->level0_phase || !c->alive || !c->s_h)
     return fail(LOGKV_EINVAL, "ladder view has a NULL buffer");
+  if (reinterpret_cast<uintptr_t>(c->level_k) % 16 || reinterpret_cast<uintptr_t>(c->level_v) % 16 ||
+      reinterpret_cast<uintptr_t>(c->centroid) % 16)
+    return fail(LOGKV_EINVAL, "level_k, level_v and centroid must be 16-byte aligned");
   return LOGKV_OK;
 }
 

@@ -112,29 +112,40 @@ __device__ __forceinline__ float rope_out(const logkv_readout_view& c, const Pac
   return d < c.dk ? (valid ? kx : 0.f) : (d == c.dk ? r.bias : 0.f);
 }
 
-// K then V units of a tile, kPackBatch per thread with all their loads (row
-// features, rotate-half partners, table entries: one vector load each) issued
-// before the arithmetic. Needs contiguous tables with 4-aligned position strides.
+// The K and V units (4 features each) of a tile: kPackBatch (row, unit)
+// items per thread with all their loads (row features, rotate-half partners,
+// table entries, value features: one vector load each) issued before the
+// arithmetic. Needs contiguous tables with 4-aligned position strides and
+// rope_n a multiple of 8, so a unit lies wholly on one side of half, of
+// rope_n and of dk (dk, dv multiples of 4).
 template <bool BF16_TABLE>
 __device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, const logkv_pack_args& p,
                                                const PackSrc* src, int s0, int lane, int units, int half) {
   const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
   const int items = kPackRows * units;
+  // Row of item i = floor((i + 0.5) / units) in float: the quotient is at
+  // least 0.5 / units (>= 1/132) from an integer and the float error is below
+  // 64 * 2^-23, so truncation gives the exact row.
+  const float inv_units = 1.0f / static_cast<float>(units);
   using TableUnit = typename std::conditional<BF16_TABLE, uint2, float4>::type;
   for (int i0 = tid; i0 < items; i0 += kPackBatch * nthr) {
-    uint2 xu[kPackBatch], pu[kPackBatch];
+    uint2 xu[kPackBatch], pu[kPackBatch], vu[kPackBatch];
     TableUnit cu[kPackBatch], su[kPackBatch];
+    int rr[kPackBatch], d0s[kPackBatch];
 #pragma unroll
     for (int q = 0; q < kPackBatch; ++q) {
       const int i = min(i0 + q * nthr, items - 1);
-      const PackSrc& r = src[i / units];
-      const int d0r = 4 * (i % units);
+      rr[q] = static_cast<int>((static_cast<float>(i) + 0.5f) * inv_units);
+      d0s[q] = 4 * (i - rr[q] * units);
+      const PackSrc& r = src[rr[q]];
+      const int d0r = d0s[q];
       const int d0 = d0r < c.dk ? d0r : 0;
       const int pd = d0 < c.rope_n ? (d0 < half ? d0 + half : d0 - half) : d0;
       const int rd = d0 < c.rope_n ? d0 : 0;
       const int64_t pos = r.pos < 0 ? 0 : (r.pos >= c.rope_rows ? c.rope_rows - 1 : r.pos);
       xu[q] = *reinterpret_cast<const LOGKV_G uint2*>(r.k + d0);
       pu[q] = *reinterpret_cast<const LOGKV_G uint2*>(r.k + pd);
+      vu[q] = *reinterpret_cast<const LOGKV_G uint2*>(r.v + (d0r < c.dv ? d0r : 0));
       if constexpr (BF16_TABLE) {
         cu[q] = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.cos)) + pos * c.cos_s0 + rd);
         su[q] = *reinterpret_cast<const LOGKV_G uint2*>(gp(static_cast<const uint16_t*>(c.sin)) + pos * c.sin_s0 + rd);
@@ -145,49 +156,50 @@ __device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, cons
     }
 #pragma unroll
     for (int q = 0; q < kPackBatch; ++q) {
-      const int i = i0 + q * nthr;
-      if (i >= items) break;
-      const PackSrc& r = src[i / units];
+      if (i0 + q * nthr >= items) break;
+      const PackSrc& r = src[rr[q]];
       if (!(r.flags & 4)) continue;
-      const int u = i % units, d0 = 4 * u;
+      const int d0 = d0s[q];
       const bool valid = r.flags & 1;
-      const float x[4] = {lo_bf16(xu[q].x), hi_bf16(xu[q].x), lo_bf16(xu[q].y), hi_bf16(xu[q].y)};
-      const float other[4] = {lo_bf16(pu[q].x), hi_bf16(pu[q].x), lo_bf16(pu[q].y), hi_bf16(pu[q].y)};
-      float cs[4], sn[4];
-      if constexpr (BF16_TABLE) {
-        cs[0] = lo_bf16(cu[q].x); cs[1] = hi_bf16(cu[q].x); cs[2] = lo_bf16(cu[q].y); cs[3] = hi_bf16(cu[q].y);
-        sn[0] = lo_bf16(su[q].x); sn[1] = hi_bf16(su[q].x); sn[2] = lo_bf16(su[q].y); sn[3] = hi_bf16(su[q].y);
-      } else {
-        cs[0] = cu[q].x; cs[1] = cu[q].y; cs[2] = cu[q].z; cs[3] = cu[q].w;
-        sn[0] = su[q].x; sn[1] = su[q].y; sn[2] = su[q].z; sn[3] = su[q].w;
-      }
       float o[4];
+      if (d0 < c.dk) {
+        const float x[4] = {lo_bf16(xu[q].x), hi_bf16(xu[q].x), lo_bf16(xu[q].y), hi_bf16(xu[q].y)};
+        if ((r.flags & 2) && d0 < c.rope_n) {
+          // Rotate-half RoPE: x cos + rot sin, rot = -partner below half (products
+          // rounded to bf16 first with bf16 tables), rounded to bf16.
+          const float sign = d0 < half ? -1.f : 1.f;
+          const float other[4] = {lo_bf16(pu[q].x), hi_bf16(pu[q].x), lo_bf16(pu[q].y), hi_bf16(pu[q].y)};
+          float cs[4], sn[4];
+          if constexpr (BF16_TABLE) {
+            cs[0] = lo_bf16(cu[q].x); cs[1] = hi_bf16(cu[q].x); cs[2] = lo_bf16(cu[q].y); cs[3] = hi_bf16(cu[q].y);
+            sn[0] = lo_bf16(su[q].x); sn[1] = hi_bf16(su[q].x); sn[2] = lo_bf16(su[q].y); sn[3] = hi_bf16(su[q].y);
+          } else {
+            cs[0] = cu[q].x; cs[1] = cu[q].y; cs[2] = cu[q].z; cs[3] = cu[q].w;
+            sn[0] = su[q].x; sn[1] = su[q].y; sn[2] = su[q].z; sn[3] = su[q].w;
+          }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = rope_out(c, r, d0 + k, x[k], other[k], cs[k], sn[k], half, valid);
-      const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + i / units) * p.dim;
+          for (int k = 0; k < 4; ++k) {
+            float a = x[k] * cs[k], bb = (sign * other[k]) * sn[k];
+            if constexpr (BF16_TABLE) {
+              a = round_bf16(a);
+              bb = round_bf16(bb);
+            }
+            o[k] = valid ? round_bf16(a + bb) : 0.f;
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) o[k] = valid ? x[k] : 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = d0 + k == c.dk ? r.bias : 0.f;
+      }
+      const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + rr[q]) * p.dim;
       store_bf16x4(gp(p.out_k) + orow + d0, o);
-    }
-  }
-  for (int i0 = tid; i0 < items; i0 += kPackBatch * nthr) {
-    uint2 vu[kPackBatch];
-#pragma unroll
-    for (int q = 0; q < kPackBatch; ++q) {
-      const int i = min(i0 + q * nthr, items - 1);
-      const int d0r = 4 * (i % units);
-      vu[q] = *reinterpret_cast<const LOGKV_G uint2*>(src[i / units].v + (d0r < c.dv ? d0r : 0));
-    }
-#pragma unroll
-    for (int q = 0; q < kPackBatch; ++q) {
-      const int i = i0 + q * nthr;
-      if (i >= items) break;
-      const PackSrc& r = src[i / units];
-      if (!(r.flags & 4)) continue;
-      const int d0 = 4 * (i % units);
-      const bool keep = (r.flags & 1) && d0 < c.dv;
-      const float o[4] = {keep ? lo_bf16(vu[q].x) : 0.f, keep ? hi_bf16(vu[q].x) : 0.f,
-                          keep ? lo_bf16(vu[q].y) : 0.f, keep ? hi_bf16(vu[q].y) : 0.f};
-      const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + i / units) * p.dim;
-      store_bf16x4(gp(p.out_v) + orow + d0, o);
+      const bool keep = valid && d0 < c.dv;
+      const float ov[4] = {keep ? lo_bf16(vu[q].x) : 0.f, keep ? hi_bf16(vu[q].x) : 0.f,
+                           keep ? lo_bf16(vu[q].y) : 0.f, keep ? hi_bf16(vu[q].y) : 0.f};
+      store_bf16x4(gp(p.out_v) + orow + d0, ov);
     }
   }
 }

@@ -126,7 +126,16 @@ __host__ __device__ inline size_t attach_shmem(int K) {
 }
 
 constexpr int kAttachMaxThreads = 512;
-constexpr int kStageBatch = 8;   // staged values per thread whose loads are issued before their LDS stores
+
+// Leaves 4 lq .. 4 lq + 3 of a leaf-major row: v[j][e] is feature 4 lq + e + 64 j.
+template <int NJ>
+__device__ __forceinline__ void stage_leaves(float* row, const float (&v)[NJ][4], int lq) {
+  float* p = row + 4 * lq * NJ;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) p[e * NJ + j] = v[j][e];
+}
 
 template <int NJ>
 __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
@@ -152,19 +161,23 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
   const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
   // Centers and rows into LDS (features past D are zero).
   const LOGKV_G float* mu = gp(c.centroid) + static_cast<int64_t>(lane_ix) * K * D;
-  constexpr int F = kWave * NJ;   // staged features per row (zero past D)
-  for (int i0 = tid; i0 < K * F; i0 += kStageBatch * nthr) {
-    float v[kStageBatch];
+  // Staged four leaves at a time: features 4 lq + e + 64 j (e < 4) of every
+  // j are one 16-byte (center, f32) or 8-byte (row, bf16) load each.
+  constexpr int LQ = kWave / 4;
+  for (int i = tid; i < K * LQ; i += nthr) {
+    const int cc = i / LQ, lq = i % LQ;
+    float v[NJ][4];
 #pragma unroll
-    for (int q = 0; q < kStageBatch; ++q) {
-      const int i = min(i0 + q * nthr, K * F - 1), cc = i / F, f = i % F;
-      v[q] = feat_or_zero(mu + cc * D, f, D);
+    for (int j = 0; j < NJ; ++j) {
+      const int f = 4 * lq + kWave * j;
+      float4 x = {0.f, 0.f, 0.f, 0.f};
+      if (f < D) x = *reinterpret_cast<const LOGKV_G float4*>(mu + cc * D + f);
+      v[j][0] = x.x;
+      v[j][1] = x.y;
+      v[j][2] = x.z;
+      v[j][3] = x.w;
     }
-#pragma unroll
-    for (int q = 0; q < kStageBatch; ++q) {
-      const int i = i0 + q * nthr;
-      if (i < K * F) mu_l[(i / F) * LS + ((i % F) % kWave) * NJ + (i % F) / kWave] = v[q];
-    }
+    stage_leaves<NJ>(mu_l + cc * LS, v, lq);
   }
   for (int i = tid; i < rows; i += nthr) {
     const int t = order[static_cast<int64_t>(b) * r.tokens + tile0 + i];
@@ -182,18 +195,21 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
   }
   __syncthreads();
   const LOGKV_G uint16_t* kbase = gp(r.k + b * r.k_sb + g * r.k_sg);
-  for (int i0 = tid; i0 < rows * F; i0 += kStageBatch * nthr) {
-    float v[kStageBatch];
+  for (int i = tid; i < rows * LQ; i += nthr) {
+    const int rr = i / LQ, lq = i % LQ;
+    const LOGKV_G uint16_t* row = kbase + static_cast<int64_t>(t_s[rr]) * r.k_st;
+    float v[NJ][4];
 #pragma unroll
-    for (int q = 0; q < kStageBatch; ++q) {
-      const int i = min(i0 + q * nthr, rows * F - 1), rr = i / F, f = i % F;
-      v[q] = feat_or_zero(kbase + static_cast<int64_t>(t_s[rr]) * r.k_st, f, D);
+    for (int j = 0; j < NJ; ++j) {
+      const int f = 4 * lq + kWave * j;
+      uint2 x = {0u, 0u};
+      if (f < D) x = *reinterpret_cast<const LOGKV_G uint2*>(row + f);
+      v[j][0] = __uint_as_float(x.x << 16);
+      v[j][1] = __uint_as_float(x.x & 0xffff0000u);
+      v[j][2] = __uint_as_float(x.y << 16);
+      v[j][3] = __uint_as_float(x.y & 0xffff0000u);
     }
-#pragma unroll
-    for (int q = 0; q < kStageBatch; ++q) {
-      const int i = i0 + q * nthr;
-      if (i < rows * F) x_l[(i / F) * LS + ((i % F) % kWave) * NJ + (i % F) / kWave] = v[q];
-    }
+    stage_leaves<NJ>(x_l + rr * LS, v, lq);
   }
   __syncthreads();
   if (tid < rows) xx_s[tid] = canon_sq<NJ, 6, 0>(x_l + tid * LS);
