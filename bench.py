@@ -372,8 +372,8 @@ def flush_workload(args, torch, np):
                        "per_layer_calls_one_stream_tokens_per_s": tokens / one_stream[0],
                        "per_layer_calls_one_stream_ms_per_layer_flush": one_stream[0] / args.steps / layers * 1e3,
                        f"per_layer_calls_{args.streams}_streams_tokens_per_s": tokens / per_layer})},
-        "roofline": {"kernel": "commit stage: commit_kernel + units_kernel + carries_kernel per level + "
-                               "finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
+        "roofline": {"kernel": "commit stage: bucket_kernel + commit_kernel + units_kernel + carries_kernel per "
+                               "level + finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
                                                   else " (one-stream pass)"),
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,

@@ -267,7 +267,6 @@ __device__ __forceinline__ void move_rows(const PoolT<KIND>& pool, int p0, int d
 }
 
 constexpr int kBatch = 4;   // rows per thread whose loads are issued before any of their stores
-constexpr int kCompactChunks = 8;   // 512-row chunks of decisions prefetched by the prepare compaction
 
 // Staged rows [s0, s0 + n) -> slots [d0, d0 + n); the staged rows never alias the level.
 template <int KIND>
@@ -774,22 +773,64 @@ __device__ inline Ladder ladder_of(const LadderArgs& c, int ladder) {
 
 }  // namespace
 
+constexpr int kBucketThreads = 1024;
+
+// Each lane's flush rows bucketed by cluster, stably in position order: one
+// block per lane, 1024 positions at a time, one ballot per cluster and wave.
+// Cluster cc's rows (indices into the flush) go to the ladder's row list
+// ws.tok[(lane K + cc) T ..] and their count to plans[lane K + cc].m_tok, which
+// commit_kernel reads.
+__global__ __launch_bounds__(kBucketThreads) void bucket_kernel(LadderArgs c, RowsArgs r, Workspace ws) {
+  __shared__ int wave_cnt[kBucketThreads / kWave][kMaxClusters];
+  __shared__ int base_s[kMaxClusters];
+  const int K = c.k_max, T = r.tokens;
+  const int lane_ix = blockIdx.x, b = lane_ix / c.n_groups;
+  const int n = valid_rows(r, b);
+  const int tid = static_cast<int>(threadIdx.x), l = lane_id(), w = wave_id();
+  const LOGKV_G int8_t* as = gp(ws.assign + static_cast<int64_t>(lane_ix) * T);
+  const LOGKV_G int32_t* ord = gp(ws.order + static_cast<int64_t>(b) * T);
+  LOGKV_G uint16_t* tok = gp(ws.tok + static_cast<int64_t>(lane_ix) * K * T);
+  if (tid < K) base_s[tid] = 0;
+  __syncthreads();
+  const uint64_t below = l == 0 ? 0ull : (~0ull >> (kWave - l));
+  for (int g0 = 0; g0 < n; g0 += kBucketThreads) {
+    const int s = g0 + tid;
+    const int a = s < n ? as[s] : -1;
+    const int o = s < n ? ord[s] : 0;
+    int before = 0;
+    for (int cc = 0; cc < K; ++cc) {
+      const uint64_t bal = __ballot(a == cc);
+      if (a == cc) before = __popcll(bal & below);
+      if (l == 0) wave_cnt[w][cc] = __popcll(bal);
+    }
+    __syncthreads();
+    if (a >= 0 && a < K) {
+      int off = base_s[a] + before;
+      for (int q = 0; q < w; ++q) off += wave_cnt[q][a];
+      tok[static_cast<int64_t>(a) * T + off] = static_cast<uint16_t>(o);
+    }
+    __syncthreads();
+    if (tid < K) {
+      int add = 0;
+      for (int q = 0; q < kBucketThreads / kWave; ++q) add += wave_cnt[q][tid];
+      base_s[tid] += add;
+    }
+    __syncthreads();
+  }
+  if (tid < K) ws.plans[static_cast<int64_t>(lane_ix) * K + tid].m_tok = base_s[tid];
+}
+
 __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  __shared__ int wave_sum[kThreads / kWave];
   __shared__ int16_t counts_s[64];
   __shared__ int level_start_s[64];
-  __shared__ int m_s;
   const int K = c.k_max, L = c.levels, B = c.slots, dk = c.dk, dv = c.dv;
   const int ladder = blockIdx.x;
-  const int lane_ix = ladder / K, cc = ladder % K;
+  const int lane_ix = ladder / K;
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
-  const int n = valid_rows(r, b);
   uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
   const int c_stage_off = (2 * r.tokens + 15) & ~15;
   const int keys_off = c_stage_off + kCenterRows * dk * 2;
-  const LOGKV_G int8_t* as = gp(ws.assign + static_cast<int64_t>(lane_ix) * r.tokens);
-  const LOGKV_G int32_t* ord = gp(ws.order + static_cast<int64_t>(b) * r.tokens);
 
   if (ws.abort && *ws.abort) {
     // A failed replay check: no rows, nothing written (the later launches read the plan).
@@ -800,44 +841,13 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     return;
   }
 
-  // 1. This cluster's rows in position order (stable compaction). The
-  // decisions and order entries of kCompactChunks chunks are loaded (clamped,
-  // unconditionally) before the chunks are scanned.
-  if (threadIdx.x == 0) m_s = 0;
-  __syncthreads();
-  for (int g0 = 0; g0 < n; g0 += kCompactChunks * kThreads) {
-    int8_t a_q[kCompactChunks];
-    int32_t o_q[kCompactChunks];
-#pragma unroll
-    for (int q = 0; q < kCompactChunks; ++q) {
-      const int s = min(g0 + q * kThreads + static_cast<int>(threadIdx.x), n - 1);
-      a_q[q] = as[s];
-      o_q[q] = ord[s];
-    }
-#pragma unroll
-    for (int q = 0; q < kCompactChunks; ++q) {
-      const int s0 = g0 + q * kThreads;
-      if (s0 >= n) break;
-      const int s = s0 + threadIdx.x;
-      const bool mine = s < n && a_q[q] == cc;
-      const uint64_t ballot = __ballot(mine);
-      const int l = lane_id(), w = wave_id();
-      const int before = __popcll(ballot & ((l == 0) ? 0ull : (~0ull >> (kWave - l))));
-      if (l == 0) wave_sum[w] = __popcll(ballot);
-      __syncthreads();
-      int base = m_s;
-      for (int q2 = 0; q2 < w; ++q2) base += wave_sum[q2];
-      if (mine) tok[base + before] = static_cast<uint16_t>(o_q[q]);
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        int add = 0;
-        for (int q2 = 0; q2 < kThreads / kWave; ++q2) add += wave_sum[q2];
-        m_s = m_s + add;
-      }
-      __syncthreads();
-    }
+  // 1. This cluster's rows in position order, bucketed by bucket_kernel.
+  const int m = ws.plans[ladder].m_tok;
+  {
+    const LOGKV_G uint16_t* list = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
+    for (int i = threadIdx.x; i < m; i += kThreads) tok[i] = list[i];
   }
-  const int m = m_s;
+  __syncthreads();
   if (m == 0) {
     if (blockIdx.y == 0 && threadIdx.x == 0) {
       ws.plans[ladder].active = 0;
@@ -846,7 +856,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     return;
   }
 
-  const int64_t cl = static_cast<int64_t>(lane_ix) * K + cc;
+  const int64_t cl = ladder;   // lane_ix * K + cluster
   const int64_t row0 = cl * L * B;
   Ladder lad{gp(c.level_k + row0 * dk), gp(c.level_v + row0 * dv), gp(c.level_w + row0), gp(c.level_p_lo + row0),
              gp(c.level_p_hi + row0), gp(c.level_sum_wp + row0), gp(c.level_order + row0), gp(c.pad_mask + row0),
@@ -1071,10 +1081,9 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     }
     n_total += nn;
   }
-  // Hand-off to the level launches: this ladder's rows in position order, the
-  // counts before the append (the level launches rewrite the levels they
-  // touch) and the per-level plan of the cascade.
-  for (int i = threadIdx.x; i < m; i += kThreads) ws.tok[static_cast<int64_t>(ladder) * r.tokens + i] = tok[i];
+  // Hand-off to the level launches (the rows in position order are already in
+  // ws.tok): the counts before the append (the level launches rewrite the
+  // levels they touch) and the per-level plan of the cascade.
   __syncthreads();
   for (int e = threadIdx.x; e < L; e += kThreads) c.level_count[cl * L + e] = counts_s[e];
   if (threadIdx.x == 0) {
@@ -1424,6 +1433,7 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
   if (p.late_joins) region += static_cast<size_t>(ws.sort_width) * 8;
   const size_t shmem = tok_bytes + region;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel), shmem)) return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(bucket_kernel, dim3(c.n_batch * c.n_groups), dim3(kBucketThreads), 0, stream, c, r, ws);
   // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
   hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
   return launch_levels(c, r, p, ws, stream);
