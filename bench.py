@@ -349,7 +349,11 @@ def flush_workload(args, torch, np):
         one_stream = run_pass(False, 1, args.mode == "layers")
         per_layer = run_pass(False, args.streams, False)[0] if args.streams > 1 else one_stream[0]
     if args.mode == "stacked":
-        elapsed, rec, B_, L_, width = run_pass(True, 1, True)
+        # The timed value comes from a pass without the commit meter (whose
+        # state snapshots are copies inside the loop); a second pass over the
+        # same flushes brackets the commit launches for the roofline.
+        elapsed, _, B_, L_, width = run_pass(True, 1, False)
+        rec = run_pass(True, 1, True)[1]
     else:
         _, rec, B_, L_, width = one_stream
         elapsed = per_layer

@@ -161,13 +161,15 @@ __device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, cons
       if (!(r.flags & 4)) continue;
       const int d0 = d0s[q];
       const bool valid = r.flags & 1;
-      float o[4];
+      // Copied rows keep their bf16 bits; rotated features and the bias are
+      // bf16-exact floats (rounded already), whose high halves are the bits.
+      uint2 ok = valid ? xu[q] : make_uint2(0u, 0u);
       if (d0 < c.dk) {
-        const float x[4] = {lo_bf16(xu[q].x), hi_bf16(xu[q].x), lo_bf16(xu[q].y), hi_bf16(xu[q].y)};
-        if ((r.flags & 2) && d0 < c.rope_n) {
+        if (valid && (r.flags & 2) && d0 < c.rope_n) {
           // Rotate-half RoPE: x cos + rot sin, rot = -partner below half (products
           // rounded to bf16 first with bf16 tables), rounded to bf16.
           const float sign = d0 < half ? -1.f : 1.f;
+          const float x[4] = {lo_bf16(xu[q].x), hi_bf16(xu[q].x), lo_bf16(xu[q].y), hi_bf16(xu[q].y)};
           const float other[4] = {lo_bf16(pu[q].x), hi_bf16(pu[q].x), lo_bf16(pu[q].y), hi_bf16(pu[q].y)};
           float cs[4], sn[4];
           if constexpr (BF16_TABLE) {
@@ -177,6 +179,7 @@ __device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, cons
             cs[0] = cu[q].x; cs[1] = cu[q].y; cs[2] = cu[q].z; cs[3] = cu[q].w;
             sn[0] = su[q].x; sn[1] = su[q].y; sn[2] = su[q].z; sn[3] = su[q].w;
           }
+          uint32_t o[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             float a = x[k] * cs[k], bb = (sign * other[k]) * sn[k];
@@ -184,22 +187,18 @@ __device__ __forceinline__ void pack_units_vec(const logkv_readout_view& c, cons
               a = round_bf16(a);
               bb = round_bf16(bb);
             }
-            o[k] = valid ? round_bf16(a + bb) : 0.f;
+            o[k] = f32_to_bf16(a + bb);
           }
-        } else {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) o[k] = valid ? x[k] : 0.f;
+          ok = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
         }
       } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = d0 + k == c.dk ? r.bias : 0.f;
+        // Column dk holds the bias (dk is a multiple of 4: first of its unit).
+        ok = make_uint2(d0 == c.dk ? static_cast<uint32_t>(f32_to_bf16(r.bias)) : 0u, 0u);
       }
       const int64_t orow = (static_cast<int64_t>(lane) * p.out_cap + s0 + rr[q]) * p.dim;
-      store_bf16x4(gp(p.out_k) + orow + d0, o);
-      const bool keep = valid && d0 < c.dv;
-      const float ov[4] = {keep ? lo_bf16(vu[q].x) : 0.f, keep ? hi_bf16(vu[q].x) : 0.f,
-                           keep ? lo_bf16(vu[q].y) : 0.f, keep ? hi_bf16(vu[q].y) : 0.f};
-      store_bf16x4(gp(p.out_v) + orow + d0, ov);
+      *reinterpret_cast<LOGKV_G uint2*>(gp(p.out_k) + orow + d0) = ok;
+      const uint2 ov = valid && d0 < c.dv ? vu[q] : make_uint2(0u, 0u);
+      *reinterpret_cast<LOGKV_G uint2*>(gp(p.out_v) + orow + d0) = ov;
     }
   }
 }
