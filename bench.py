@@ -50,7 +50,7 @@ METER_EVERY = 7   # layers 0, 7, 14, 21 carry the commit-stage events
 # WRITE_SIZE runs scaled by a 1 GiB copy probe (profiles/commit_stage_traffic_28layer_
 # stacked_qwen3_1.7b.md); counters cannot be read inside this process, so the figure is
 # the profiled one and is re-measured whenever the commit kernels change.
-STACKED_COMMIT_TRAFFIC_BYTES = 1585.7e6
+STACKED_COMMIT_TRAFFIC_BYTES = 1582.0e6
 G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
 EXACT, SPAN = 256, 64
 
