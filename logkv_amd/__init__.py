@@ -8,3 +8,4 @@ compute runs in liblogkv_hip.so through the C ABI in include/logkv_hip.h.
 from .log_kv_cache import LogStructuredKVCache, ladder_budget  # noqa: F401
 from .log_kv_pack import log_kv_chunk_attention, pack_mid_kv, packed_dim  # noqa: F401
 from .kv_compression import cache_compression_snapshot, summarize_compression  # noqa: F401
+from .streaming import LogKVStreamingAttention  # noqa: F401
