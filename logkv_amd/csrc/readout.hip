@@ -18,6 +18,7 @@
 // h / (Hq / G). Flash-decoding: row splits per lane, each staging 64-row K and
 // V tiles in LDS with an online softmax; a second kernel combines the splits in
 // a fixed order.
+#include <algorithm>
 #include <type_traits>
 
 #include "route.hpp"
@@ -29,7 +30,8 @@ namespace {
 constexpr int kPlanThreads = 256;
 constexpr int kTile = 64;          // rows per staged K/V tile
 constexpr int kSplitRows = 512;    // rows per attention split (staged decode kernel)
-constexpr int kStreamRows = 512;   // rows per split of the streaming kernel (256 measured slower)
+constexpr int kStreamRows = 512;   // most rows per split of the streaming kernel when the grid is not the limit
+constexpr int kStreamBlocks = 1280;   // streaming blocks resident at once (256 CUs x 5 blocks of 4 waves; 2560 measured slower)
 constexpr int kMaxQ = 16;          // queries per KV group (heads per group x query rows)
 constexpr int kMaxPacked = 264;    // packed row width limit (dk + 1 rounded to 8, dv)
 constexpr int kAccPerThread = kMaxQ * kMaxDim / 256;   // outputs per thread of a 256-thread split block
@@ -478,7 +480,10 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
   const float q_bias = a.inv_scale_bf16;
   const int total = min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
   const int tail0 = total - a.causal_tail;
-  const int r_begin = blockIdx.x * kStreamRows, r_end = min(r_begin + kStreamRows, total);
+  // The lane's rows in gridDim.x equal shares, multiples of 64 (a pass of the
+  // 16 row groups x 4 rows); splits past the rows write empty partials.
+  const int share = max(64, (total + 64 * static_cast<int>(gridDim.x) - 1) / (64 * static_cast<int>(gridDim.x)) * 64);
+  const int r_begin = blockIdx.x * share, r_end = min(r_begin + share, total);
   float* out = part + (static_cast<int64_t>(lane) * gridDim.x + blockIdx.x) * nq * (a.dv + 2);
   // This lane's slices of the queries [q, 1/scale (bf16), 0...]: units gl + 16 j.
   float qv[NQ][UJ][8];
@@ -657,8 +662,17 @@ bool use_stream(const logkv_attention_args& a) {
   return nq <= 4 && a.dv <= 128 && a.dk >= 8 && stream_key_units(a) <= 3;
 }
 
+// Splits per lane: the staged kernel takes kSplitRows rows each; the streaming
+// kernel takes up to kStreamRows each, but no more splits than keep every block
+// of the launch resident at once (its splits then share the rows equally).
+int attention_splits(const logkv_attention_args& a) {
+  if (!use_stream(a)) return (a.cap + kSplitRows - 1) / kSplitRows;
+  const int lanes = a.n_batch * a.n_groups;
+  return std::max(1, std::min((a.cap + kStreamRows - 1) / kStreamRows, kStreamBlocks / std::max(1, lanes)));
+}
+
 int64_t attention_workspace_floats(const logkv_attention_args& a) {
-  const int n_split = (a.cap + (use_stream(a) ? kStreamRows : kSplitRows) - 1) / (use_stream(a) ? kStreamRows : kSplitRows);
+  const int n_split = attention_splits(a);
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   return static_cast<int64_t>(a.n_batch) * a.n_groups * n_split * nq * (a.dv + 2);
 }
@@ -670,8 +684,7 @@ int launch_combine(const logkv_attention_args& a, const float* part, int n_split
 }
 
 int launch_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
-  const int rows = use_stream(a) ? kStreamRows : kSplitRows;
-  const int n_split = (a.cap + rows - 1) / rows;
+  const int n_split = attention_splits(a);
   const int lanes = a.n_batch * a.n_groups;
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   const int uj = stream_key_units(a);
