@@ -1110,35 +1110,51 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
 // Carry work of every level: block ell writes units[ell][i] = work units of
 // ladders 0..i-1 at level ell (a unit is one Beta group of two carries, or one
 // pair carry), i = 0..ladders.
-__global__ __launch_bounds__(kCarryThreads) void units_kernel(LadderArgs c, RouteParams prm, Workspace ws) {
-  __shared__ int wave_total[kCarryThreads / kWave];
+constexpr int kUnitsThreads = 1024;
+constexpr int kUnitsPer = kMaxLadders / kUnitsThreads;   // consecutive ladders per thread at most
+
+// One block per level: thread t owns ladders [t per, (t + 1) per) (per = the
+// ladder count over 1024, rounded up), loads all their plans first, then one
+// block scan of the threads' totals gives every prefix.
+__global__ __launch_bounds__(kUnitsThreads) void units_kernel(LadderArgs c, RouteParams prm, Workspace ws) {
+  __shared__ int wave_total[kUnitsThreads / kWave];
   const int ell = blockIdx.x;
   const int ladders = c.n_batch * c.n_groups * c.k_max;
+  const int per = (ladders + kUnitsThreads - 1) / kUnitsThreads;
   int32_t* out = ws.units + static_cast<int64_t>(ell) * (ladders + 1);
   const int l = lane_id(), w = wave_id();
-  if (threadIdx.x == 0) out[0] = 0;
-  int carry = 0;
-  for (int base = 0; base < ladders; base += kCarryThreads) {
-    const int i = base + static_cast<int>(threadIdx.x);
-    int n = 0;
-    if (i < ladders) {
+  const int i0 = static_cast<int>(threadIdx.x) * per;
+  int n[kUnitsPer];
+  int mine = 0;
+#pragma unroll
+  for (int q = 0; q < kUnitsPer; ++q) {
+    n[q] = 0;
+    const int i = i0 + q;
+    if (q < per && i < ladders) {
       const LadderPlan* pl = ws.plans + i;
       const int nc = pl->active ? carries_of(pl->cnt[ell], pl->m[ell], c.slots, ell == c.levels - 1) : 0;
-      n = prm.beta_merge ? (nc + 1) / 2 : nc;
+      n[q] = prm.beta_merge ? (nc + 1) / 2 : nc;
     }
-    int incl = n;
+    mine += n[q];
+  }
+  int incl = mine;
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int t = __shfl_up(incl, d, kWave);
-      if (l >= d) incl += t;
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(incl, d, kWave);
+    if (l >= d) incl += t;
+  }
+  if (l == kWave - 1) wave_total[w] = incl;
+  __syncthreads();
+  int acc = incl - mine;
+  for (int q = 0; q < w; ++q) acc += wave_total[q];
+  if (threadIdx.x == 0) out[0] = 0;
+#pragma unroll
+  for (int q = 0; q < kUnitsPer; ++q) {
+    const int i = i0 + q;
+    if (q < per && i < ladders) {
+      acc += n[q];
+      out[i + 1] = acc;
     }
-    if (l == kWave - 1) wave_total[w] = incl;
-    __syncthreads();
-    int before = carry;
-    for (int q = 0; q < w; ++q) before += wave_total[q];
-    if (i < ladders) out[i + 1] = before + incl;
-    for (int q = 0; q < kCarryThreads / kWave; ++q) carry += wave_total[q];
-    __syncthreads();   // wave_total is rewritten by the next chunk
   }
 }
 
@@ -1446,7 +1462,7 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
   if (c.levels > 1) {
-    hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kCarryThreads), 0, stream, c, p, ws);
+    hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kUnitsThreads), 0, stream, c, p, ws);
     const size_t carry_shmem = (static_cast<size_t>(ladders) + 1) * 4;
     const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
     const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
