@@ -1,35 +1,37 @@
-"""Benchmark of the SemanticLogKV flush path and its decode readout on one MI355X.
+"""Benchmark of the SemanticLogKV flush path and its readout on one MI355X.
 
-Flush (the headline): a step is one flush of 2048 rows into every layer cache
-of a 28-layer Qwen3-1.7B-shaped KV stack (8 KV groups x 128, bf16, batch 1,
-K=12, B=128 with a 256-token Alpha exact pool and 64-token span cap, so
-B'=125 and L=7; Beta novelty scoring and the 4->2 split on): Alpha span
-scoring and choice, exact-pool partition, attach route of the archived rows,
-per-ladder commit (merges, carries, centers), then the mid-anchor plan and the
-pack of the new packed prefix that the next attention reads. Rows are seeded
-synthetic Gaussian-mixture keys/values already resident in HBM; span ends are
-seeded natural boundaries. The caches first take two untimed flushes; the
-steps continue the same 32K-token stream.
+Headline (a step): one flush of 2048 rows into every layer cache of a
+28-layer Qwen3-1.7B-shaped KV stack (8 KV groups x 128, bf16, batch 1, K=12,
+B=128 with a 256-token Alpha exact pool and a 64-token span cap, so B'=125 and
+L=7; Beta novelty scoring and the 4->2 split on): Alpha span scoring and
+choice, exact-pool partition, attach route of the archived rows, per-ladder
+commit (merges, carries, centers), then the mid-anchor plan and the pack of the
+new packed prefix the next attention reads. Rows are seeded synthetic
+Gaussian-mixture keys / values already resident in HBM, span ends follow the
+reference harness's rule. A 32K-token stream holds 16 flushes: its first two
+are untimed (they fill empty ladders), flushes 3..16 are steady-state steps.
+Any --warmup / --steps is served by chaining fresh 32K-token streams: the
+warm-up steps come first, then the timed ones; every stream's own two first
+flushes run outside the timed region.
 
-Decode: one attention layer over a compressed 32K-token cache, batch 8,
-Qwen3-1.7B GQA (16 query / 8 KV heads x 128): recent window 2048, exact pool
-256, 12 clusters per lane with the ladder occupancy of 30,464 archived tokens,
-masses ~ U(1, 64). A step attends one new token per sequence with the packed
-prefix reused, as in the reference's decode loop.
+Beside the headline, each in its own guarded leg (a failing leg is recorded in
+the line and never loses the headline): the one-layer flush of the CPU
+reference configuration on the GPU, decode at 32K context (batch 8, GQA
+16/8) through the streaming attention engine, streaming prefill of 32,768
+tokens through 28 layer caches (chunk attention on the matrix cores + the
+flushes), the unified Ward / radius route control, and the CPU baseline.
 
-Streaming prefill: 32,768 tokens in 2048-token blocks through 28 layer caches
-with per-layer calls: the chunk attention of each block (matrix-core kernel)
-and the flush it triggers; ms per block, the attention's TFLOP/s, and the
-slots per cluster after each block (the O(log N) growth).
+Prints one JSON line. ``roofline`` is the whole flush step: algorithmic bytes
+of every stage (byte model below) over the step's duration from HIP events
+on its stream over the timed region; ``roofline.stages`` splits it into the
+Alpha selection + partition, the attach route, the ladder commit and the plan
++ pack, each timed by its own event pairs in a second pass over the same
+flushes (the kernels are deterministic, so that pass reproduces the timed
+pass's states).
 
-Unified-route control: the Ward / radius route at batch 4 x 8 KV groups with
-4096-row flushes over a 131,072-token drifting stream (one layer), reported
-beside the headline as flushed tokens/s and ms per flush.
-
-Prints one JSON line: flushed tokens/s over the timed steps, the roofline of
-the dominant stage (the ladder commit: its prepare, per-level carries and
-finish launches) from HIP events on its stream over the timed region, decode ms/token with its own roofline, and the oracle's CPU
-throughput on a bounded sample of the flush workload.
+``python bench.py --pmc-summary FETCH_DIR WRITE_DIR`` turns the counter
+output of two ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` runs of
+``bench.py --profile-flush`` into HBM bytes per step.
 """
 
 from __future__ import annotations
@@ -37,23 +39,74 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
+import math
+import os
+import platform
 import sys
 import time
+import traceback
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
-METER_EVERY = 7   # layers 0, 7, 14, 21 carry the commit-stage events
-# HBM bytes of one stacked commit stage (28 layers) from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE runs scaled by a 1 GiB copy probe (profiles/commit_stage_traffic_28layer_
-# stacked_qwen3_1.7b.md); counters cannot be read inside this process, so the figure is
-# the profiled one and is re-measured whenever the commit kernels change.
-STACKED_COMMIT_TRAFFIC_BYTES = 1582.0e6
+BF16_PEAK_TFLOPS = 2500.0
 G, D, K, B, F, N = 8, 128, 12, 128, 2048, 32768
 EXACT, SPAN = 256, 64
+STREAM_FLUSHES = N // F          # 16 flushes per 32K-token stream
+PREP_FLUSHES = 2                 # each stream's first two flushes: untimed
+STEADY_FLUSHES = STREAM_FLUSHES - PREP_FLUSHES
+MAX_LIVE_STREAMS = 6             # stacked caches alive at once (about 1.4 GB each)
+ROPE_TABLE_BYTES = 4             # float32 cos / sin tables
 
+
+def progress(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------
+# Schedule: warm-up and timed steps over chained 32K-token streams
+# ----------------------------------------------------------------------
+
+def flush_schedule(warmup: int, steps: int, max_live: int = MAX_LIVE_STREAMS):
+    """Segments of the headline run for any warmup / steps.
+
+    Step w (0-based over warm-up then timed steps) is flush 3 + (w % 14) of
+    stream w // 14. A segment is a group of at most ``max_live`` streams whose
+    caches are alive together: their two prep flushes, then their warm-up
+    steps, then their timed steps (one bracketed region). Returns a list of
+    segments ``{"streams": [...], "warm": [(stream, flush)], "timed": [...]}``
+    whose timed lists, concatenated, hold exactly ``steps`` flushes."""
+    if warmup < 0 or steps < 1:
+        raise ValueError("--warmup must be >= 0 and --steps >= 1")
+    total = warmup + steps
+    n_streams = (total + STEADY_FLUSHES - 1) // STEADY_FLUSHES
+    segments = []
+    for first in range(0, n_streams, max_live):
+        streams = list(range(first, min(n_streams, first + max_live)))
+        warm, timed = [], []
+        for s in streams:
+            for j in range(STEADY_FLUSHES):
+                w = s * STEADY_FLUSHES + j
+                if w >= total:
+                    break
+                (warm if w < warmup else timed).append((s, PREP_FLUSHES + j))
+        segments.append({"streams": streams, "warm": warm, "timed": timed})
+    return segments
+
+
+def span_ends_for(flush, batch=1):
+    """Natural span boundaries of the stream's flush ``flush``: row ``p`` of batch row ``b`` ends a
+    span when ``(p + 7*b) % 32 == 0``, the rule of the reference's benchmark harness
+    (unused/benchmark_log_kv_unified.py:36-40)."""
+    return [[(p + 7 * b) % 32 == 0 for p in range(flush * F, (flush + 1) * F)] for b in range(batch)]
+
+
+# ----------------------------------------------------------------------
+# Byte model (algorithmic HBM bytes)
+# ----------------------------------------------------------------------
 
 def ladder_rows(counts, m, B, L, staged_tokens=True):
     """(entry rows read, entry rows written, staged token rows read) of one Fenwick append.
@@ -81,8 +134,7 @@ def ladder_rows(counts, m, B, L, staged_tokens=True):
             counts[ell] += take
             break
         if ell == L - 1:
-            pool_staged = mr
-            rd += B + pool_staged - 1   # fold reads pool[0..mr], tail reads the rest
+            rd += B + mr - 1   # fold reads pool[0..mr], tail reads the rest
             wr += B
             counts[ell] = B
             break
@@ -127,14 +179,14 @@ def commit_bytes(counts, alive, p_hi, assign, order, positions, n_rows, B, L, dk
 
     entry = 2 * (dk + dv) + 4 + 4 * 8 + 1
     token = 2 * (dk + dv) + 8
-    n_batch, groups, K = alive.shape
+    n_batch, groups, K_ = alive.shape
     total = 0
     for b in range(n_batch):
         n = int(n_rows[b])
         rows_pos = positions[b][order[b][:n]]
         for g in range(groups):
-            a = assign[b, g, :n]
-            for c in range(K):
+            a = assign[b * groups + g, :n] if assign.ndim == 2 else assign[b, g, :n]
+            for c in range(K_):
                 sel = np.nonzero(a == c)[0]
                 m = len(sel)
                 if m == 0:
@@ -165,108 +217,157 @@ def commit_bytes(counts, alive, p_hi, assign, order, positions, n_rows, B, L, dk
     return total
 
 
-def progress(msg):
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+def alpha_bytes(p0, keep, archived, T, P, groups, dk, dv, k_max):
+    """Algorithmic bytes of the Alpha stage of one batch row: scoring reads the K and V rows of
+    every candidate token of [exact pool | flush] (all p0 + T rows) plus positions, flags and the
+    live centers; the partition reads each source row once and writes the P-row pool (kept rows,
+    zero fill) and the archived rows, with their positions."""
+    row = groups * 2 * (dk + dv)
+    score = (p0 + T) * row + T * (8 + 1) + p0 * 8 + groups * k_max * (dk * 4 + 1)
+    part = (keep + archived) * (row + 8) + P * (row + 8 + 1) + archived * (row + 8)
+    return score, part
 
 
-def span_ends_for(flush, batch=1):
-    """Natural span boundaries of the stream's flush ``flush`` (same for every layer): row
-    ``p`` of batch row ``b`` ends a span when ``(p + 7*b) % 32 == 0``, the rule of the
-    reference's benchmark harness (unused/benchmark_log_kv_unified.py:36-40)."""
-    return [[(p + 7 * b) % 32 == 0 for p in range(flush * F, (flush + 1) * F)] for b in range(batch)]
+def route_bytes(archived, groups, dk, k_max):
+    """Attach route of one batch row: positions read, every archived key read once per KV group,
+    one decision byte written per (group, row), the centers read."""
+    return archived * 8 + groups * archived * (2 * dk + 1) + groups * k_max * (dk * 4 + 1 + 8)
 
 
-def cpu_baseline(seconds: float):
-    """Oracle (numpy restatement) of the same flush for one layer on the host: Alpha/Beta, route,
-    commit and the pack of the new prefix."""
-    import numpy as np
-    import torch
-
-    from logkv_amd.workloads import Mixture, rope_tables
-    from oracle import OracleCache
-
-    torch.set_num_threads(1)
-    cos, sin = (t.numpy() for t in rope_tables(N, D))
-    mix = Mixture(1, G, D, clusters=K, seed=1)
-    rows = lambda: mix.rows(F).float().numpy()  # noqa: E731
-    n, t, streams = 0, 0.0, 0
-    while t < seconds:
-        # One 32K-token stream per cache: two untimed warm-up flushes, then flushes 3..16.
-        ora = OracleCache(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, exact_tokens=EXACT,
-                          span_max=SPAN, beta_novelty=True, beta_adaptive=True, cos=cos, sin=sin)
-        streams += 1
-        for j in range(16):
-            k, v = rows(), rows()
-            pos = np.arange(j * F, (j + 1) * F)[None]
-            t0 = time.perf_counter()
-            ora.flush_rows(k, v, pos, span_ends_for(j))
-            ora.pack(None, None)
-            if j >= 2:
-                t += time.perf_counter() - t0
-                n += 1
-            if t >= seconds:
-                break
-    return {"value": F * n / t, "unit": "flushed tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle (numpy) Alpha/Beta + route + commit + pack of {n} flushes (flushes 3..16 of "
-                      f"{streams} 32K-token streams) of one layer, batch 1, 8 groups x 128, K=12, B=128, "
-                      f"exact pool 256, {F} rows each, {t:.1f} s, 1 thread"}
+def pack_bytes(lane_slots, exact_rows, recent_rows, dk, dv, dim, rope_n):
+    """Plan + pack of one batch row's packed prefix [pooled | exact | recent]: pooled slots read
+    K, V, w, sum(w*p) and the cos / sin rows at their anchor; exact rows read K, V, position,
+    valid flag and their table rows; recent rows read K and V; every lane writes K and V packed
+    rows of width ``dim`` for the widest lane's pooled count plus the exact and recent rows."""
+    table = 2 * rope_n * ROPE_TABLE_BYTES
+    width = max(lane_slots) if lane_slots else 0
+    rd = sum(lane_slots) * (2 * (dk + dv) + 4 + 8 + table)
+    rd += len(lane_slots) * (exact_rows * (2 * (dk + dv) + 8 + 1 + table) + recent_rows * 2 * (dk + dv))
+    wr = len(lane_slots) * (width + exact_rows + recent_rows) * 2 * dim * 2
+    return rd + wr
 
 
-class CommitMeter:
-    """Wraps a cache's route+commit so that the commit's launches are bracketed by HIP
-    events on their stream, with the ladder state they start from copied aside on the
-    device and the attach decisions kept (no host sync); algorithmic bytes are computed
-    from those copies after the timed region."""
+def gbs(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+
+
+# ----------------------------------------------------------------------
+# Headline: 28-layer flush
+# ----------------------------------------------------------------------
+
+def new_flush_cache(torch, dev, batch, cos, sin, seq=N):
+    from logkv_amd import LogStructuredKVCache
+
+    return LogStructuredKVCache((batch, G, seq, D), (batch, G, seq, D), B=B, recent_size=F, device=dev,
+                                dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
+                                semantic_s_h=64.0, semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
+                                alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
+                                beta_adaptive_merge=True)
+
+
+class FlushMeter:
+    """A metered flush step of one stacked cache: HIP events around each stage's launches on the
+    cache's stream and the state the byte model needs, copied aside on the device (no host sync
+    inside the loop; bytes are computed afterwards)."""
 
     def __init__(self, cache, torch):
         self.cache, self.torch = cache, torch
         self.records = []
+        self._cur = None
+
+    def _event(self):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record(self.torch.cuda.current_stream(self.cache.level_k.device))
+        return ev
+
+    def begin(self):
+        c = self.cache
+        self._cur = {"span_len": c.alpha_span_len.clone(), "span_count": c.alpha_span_count.clone()}
+        self._cur["ev"] = [self._event()]
 
     def __call__(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None, record=False):
+        """Replaces the cache's route + commit for the metered pass: attach and commit as separate launches."""
         from logkv_amd._lib import check, lib, ptr, stream_of
 
-        if record:
-            raise ValueError("the commit meter does not record op-logs")
-
-        cache, torch = self.cache, self.torch
+        cache, torch, cur = self.cache, self.torch, self._cur
+        if cur is None:   # an unmetered flush (the stream's prep and warm-up flushes)
+            return type(cache)._route_commit(cache, k_raw, v, positions, counts, assign_out, order_out, record)
+        cur["ev"].append(self._event())                      # end of the Alpha stage
         dev = k_raw.device
-        snap = (cache.level_count.clone(), cache.alive.clone(), cache.p_hi_c.clone())
-        assign = torch.empty(cache.batch_size, cache.n_groups, k_raw.size(2), dtype=torch.int8, device=dev)
+        cur["counts"] = cache.level_count.clone()
+        cur["alive"] = cache.alive.clone()
+        cur["p_hi"] = cache.p_hi_c.clone()
+        cur["archived"] = counts.clone()
+        cur["positions"] = positions.clone()
+        assign = torch.empty(cache.batch_size * cache.n_groups, k_raw.size(2), dtype=torch.int8, device=dev)
         order = torch.empty(cache.batch_size, k_raw.size(2), dtype=torch.int32, device=dev)
         view = cache._ladder_view()
         rows = cache._rows_view(k_raw, v, positions, counts)
         ws = cache._workspace_for(view, rows.tokens)
         sp = stream_of(dev)
-        stream = torch.cuda.current_stream(dev)
+        cur["ev"].append(self._event())
         check(lib().logkv_attach_assign(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
                                         ptr(assign), ptr(order), sp), "attach")
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ev[0].record(stream)
+        cur["ev"].append(self._event())
         check(lib().logkv_commit_only(C.byref(view), C.byref(rows), C.byref(cache._params), ptr(ws), ws.numel(),
                                       ptr(assign), ptr(order), sp), "commit")
-        ev[1].record(stream)
-        n_rows = counts if counts is not None else torch.full((cache.batch_size,), k_raw.size(2), device=dev)
-        self.records.append((snap, assign, order, positions, n_rows, ev))
+        cur["ev"].append(self._event())
+        cur["assign"], cur["order"] = assign, order
 
-    def results(self, B_, L_):
+    def before_pack(self):
+        self._cur["ev"].append(self._event())
+
+    def end(self):
+        c, cur = self.cache, self._cur
+        cur["ev"].append(self._event())
+        cur["counts_after"] = c.level_count.clone()
+        cur["new_span_len"] = c.alpha_span_len.clone()
+        cur["new_span_count"] = c.alpha_span_count.clone()
+        self.records.append(cur)
+        self._cur = None
+
+    def results(self):
+        """Per metered step: bytes and milliseconds of each stage."""
+        import numpy as np
+
+        c = self.cache
         out = []
-        for (counts, alive, p_hi), assign, order, positions, n_rows, ev in self.records:
-            nb = commit_bytes(counts.long().cpu().numpy(), alive.cpu().numpy(), p_hi.cpu().numpy(),
-                              assign.cpu().numpy(), order.long().cpu().numpy(), positions.cpu().numpy(),
-                              n_rows.cpu().numpy(), B_, L_, D, D)
-            out.append((nb, ev[0].elapsed_time(ev[1])))
+        for r in self.records:
+            ev = r["ev"]
+            ms = {"alpha": ev[0].elapsed_time(ev[1]), "route": ev[2].elapsed_time(ev[3]),
+                  "commit": ev[3].elapsed_time(ev[4]), "pack": ev[5].elapsed_time(ev[6])}
+            span_len, span_count = r["span_len"].cpu().numpy(), r["span_count"].cpu().numpy()
+            new_len, new_count = r["new_span_len"].cpu().numpy(), r["new_span_count"].cpu().numpy()
+            archived = r["archived"].cpu().numpy()
+            counts_after = r["counts_after"].long().cpu().numpy()
+            T = F
+            by = {"alpha": 0, "route": 0, "commit": 0, "pack": 0}
+            for b in range(c.batch_size):
+                p0 = int(span_len[b, :span_count[b]].sum())
+                keep = int(new_len[b, :new_count[b]].sum())
+                if keep + int(archived[b]) != p0 + T:
+                    raise RuntimeError(f"kept {keep} + archived {archived[b]} rows != pool {p0} + flush {T}")
+                score, part = alpha_bytes(p0, keep, int(archived[b]), T, EXACT, G, D, D, K)
+                by["alpha"] += score + part
+                by["route"] += route_bytes(int(archived[b]), G, D, K)
+                lanes = counts_after[b].sum(axis=(-1, -2)).tolist()
+                by["pack"] += pack_bytes(lanes, keep, 0, D, D, 136, D)
+            by["commit"] = commit_bytes(r["counts"].long().cpu().numpy(), r["alive"].cpu().numpy(),
+                                        r["p_hi"].cpu().numpy(), r["assign"].cpu().numpy(),
+                                        r["order"].long().cpu().numpy(), r["positions"].cpu().numpy(), archived,
+                                        c.B_prime, c.L_alloc, D, D)
+            out.append((by, ms))
         return out
 
 
 def flush_workload(args, torch, np):
-    from logkv_amd import LogStructuredKVCache
     from logkv_amd.log_kv_pack import _decode_capacity, _launch_pack, packed_dim, readout_view
-    from logkv_amd.workloads import rope_tables
+    from workloads import rope_tables
 
     dev = torch.device("cuda", 0)
     layers = args.layers
     cos, sin = rope_tables(N, D)
-    n_flush = 2 + args.warmup + args.steps
     gen = torch.Generator(device=dev).manual_seed(1234)
     centers = torch.randn(layers, G, K, D, generator=gen, device=dev) * 4
 
@@ -278,119 +379,217 @@ def flush_workload(args, torch, np):
         far = torch.rand(layers, G, F, generator=gen, device=dev) < 0.1
         return torch.where(far[..., None], torch.randn(x.shape, generator=gen, device=dev) * 12, x).to(torch.bfloat16)
 
-    # Flush j's rows of every layer, stacked [layers, G, F, D]; layer li's rows are
-    # the batch-1 slice [li:li + 1]. Positions and boundary flags staged on the device.
-    data = [(mixture(), mixture()) for _ in range(n_flush)]
+    # Flush j of the stream for every layer, stacked [layers, G, F, D]; layer li's rows are the
+    # batch-1 slice [li:li + 1]. Every chained stream replays the same rows into fresh caches.
+    data = [(mixture(), mixture()) for _ in range(STREAM_FLUSHES)]
     positions = [torch.arange(j * F, (j + 1) * F, device=dev).unsqueeze(0).expand(layers, -1).contiguous()
-                 for j in range(n_flush)]
+                 for j in range(STREAM_FLUSHES)]
     ends = [torch.tensor(span_ends_for(j), dtype=torch.uint8, device=dev).expand(layers, -1).contiguous()
-            for j in range(n_flush)]
+            for j in range(STREAM_FLUSHES)]
     dim = packed_dim(D, D)
     torch.cuda.synchronize()
+    segments = flush_schedule(args.warmup, args.steps)
 
-    def new_cache(batch):
-        return LogStructuredKVCache((batch, G, N, D), (batch, G, N, D), B=B, recent_size=F, device=dev,
-                                    dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K,
-                                    semantic_s_h=64.0, semantic_flush_granularity=F, semantic_anchor_mode="mid",
-                                    allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
-                                    alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
-                                    beta_adaptive_merge=True)
+    def run_pass(stacked, n_streams, meter=False):
+        """The schedule over fresh caches. stacked: one cache per stream whose batch rows are the
+        layers (one call per flush step). Otherwise one cache per layer and stream, layer li's calls
+        on HIP stream li % n_streams (the layers' caches are independent, so their flushes may
+        overlap; each layer's own flushes stay in order)."""
+        hip_streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(n_streams - 1)]
+        elapsed, step_ms, records, last = 0.0, [], [], None
+        empty = torch.empty(layers if stacked else 1, G, 0, D, dtype=torch.bfloat16, device=dev)
+        for seg in segments:
+            live = {}
+            for s in seg["streams"]:
+                caches = [new_flush_cache(torch, dev, layers, cos, sin)] if stacked else \
+                    [new_flush_cache(torch, dev, 1, cos, sin) for _ in range(layers)]
+                packs = [tuple(torch.empty(c.batch_size, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16,
+                                           device=dev) for _ in range(2)) for c in caches]
+                meters = [FlushMeter(c, torch) for c in caches] if meter else None
+                if meters:
+                    for c, m in zip(caches, meters):
+                        c._route_commit = m
+                live[s] = (caches, packs, meters)
 
-    def run_pass(stacked, n_streams, meter):
-        """Fresh caches, 2 + warmup untimed flushes, then `steps` timed ones, each followed
-        by the plan + pack of the next attention's packed prefix [pooled | exact | recent].
-        stacked: one cache whose batch rows are the layers, one call per flush step.
-        Otherwise one cache per layer, layer li's calls on stream li % n_streams (the
-        layers' caches are independent, so their flushes may overlap; each layer's own
-        flushes stay in order)."""
-        caches = [new_cache(layers)] if stacked else [new_cache(1) for _ in range(layers)]
-        workspaces = [tuple(torch.empty(c.batch_size, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16,
-                                        device=dev) for _ in range(2)) for c in caches]
-        empty = torch.empty(caches[0].batch_size, G, 0, D, dtype=torch.bfloat16, device=dev)
-        streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(n_streams - 1)]
+            def flush(s, j, events=None, metered=False):
+                caches, packs, meters = live[s]
+                k, v = data[j]
+                if events is not None:
+                    events[0].record(hip_streams[0])
+                for li, cache in enumerate(caches):
+                    rows = slice(None) if stacked else slice(li, li + 1)
+                    with torch.cuda.stream(hip_streams[li % n_streams]):
+                        m = meters[li] if metered else None
+                        if m is not None:
+                            m.begin()
+                        cache.route_and_flush_batch(k[rows], v[rows], positions[j][rows], span_ends=ends[j][rows])
+                        if m is not None:
+                            m.before_pack()
+                        view = readout_view(cache)
+                        plan = cache._semantic_attention_plan()
+                        _launch_pack(cache, view, plan, empty, empty, dim, *packs[li], False, 0)
+                        if m is not None:
+                            m.end()
+                if events is not None:
+                    events[1].record(hip_streams[0])
 
-        def flush(j):
-            k, v = data[j]
-            for li, cache in enumerate(caches):
-                rows = slice(None) if stacked else slice(li, li + 1)
-                with torch.cuda.stream(streams[li % n_streams]):
-                    cache.route_and_flush_batch(k[rows], v[rows], positions[j][rows], span_ends=ends[j][rows])
-                    view = readout_view(cache)
-                    plan = cache._semantic_attention_plan()
-                    _launch_pack(cache, view, plan, empty, empty, dim, *workspaces[li], False, 0)
-
+            for s in seg["streams"]:
+                for j in range(PREP_FLUSHES):
+                    flush(s, j)
+            for s, j in seg["warm"]:
+                flush(s, j)
+            torch.cuda.synchronize()
+            evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in seg["timed"]] \
+                if stacked and n_streams == 1 else [None] * len(seg["timed"])
+            t0 = time.perf_counter()
+            for (s, j), ev in zip(seg["timed"], evs):
+                flush(s, j, ev, metered=meter)
+            torch.cuda.synchronize()
+            elapsed += time.perf_counter() - t0
+            step_ms += [ev[0].elapsed_time(ev[1]) for ev in evs if ev is not None]
+            if meter:
+                for caches, _, meters in live.values():
+                    for c, m in zip(caches, meters):
+                        del c._route_commit
+                        records += m.results()
+            s_last = seg["timed"][-1][0] if seg["timed"] else seg["streams"][-1]
+            last = live[s_last][0][0]
+            width = int(last._semantic_attention_plan().width)
+            B_, L_ = last.B_prime, last.L_alloc
+            del live
         label = "stacked layers" if stacked else f"{n_streams} stream(s)"
-        for j in range(2 + args.warmup):
-            flush(j)
-        torch.cuda.synchronize()
-        progress(f"flush, {label}: {2 + args.warmup} untimed flushes done")
-        # Commit launches of every METER_EVERY-th layer cache are bracketed by events.
-        metered = caches[::METER_EVERY] if meter else []
-        meters = [CommitMeter(c, torch) for c in metered]
-        for c, m in zip(metered, meters):
-            c._route_commit = m
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for s in range(args.steps):
-            flush(2 + args.warmup + s)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        for c in metered:
-            del c._route_commit
-        progress(f"flush, {label}: {args.steps} timed flushes in {elapsed:.3f} s")
-        rec = [r for m in meters for r in m.results(caches[0].B_prime, caches[0].L_alloc)]
-        width = int(caches[0]._semantic_attention_plan().width)
-        return elapsed, rec, caches[0].B_prime, caches[0].L_alloc, width
+        progress(f"flush, {label}{' (metered)' if meter else ''}: {args.steps} timed flushes in {elapsed:.3f} s "
+                 f"over {len(segments)} segment(s)")
+        return {"elapsed": elapsed, "step_ms": step_ms, "records": records, "B": B_, "L": L_, "width": width}
 
     tokens = F * layers * args.steps
-    if args.flush_passes == "stacked" and args.mode == "stacked":
-        one_stream = per_layer = None
-    else:
-        one_stream = run_pass(False, 1, args.mode == "layers")
-        per_layer = run_pass(False, args.streams, False)[0] if args.streams > 1 else one_stream[0]
-    if args.mode == "stacked":
-        # The timed value comes from a pass without the commit meter (whose
-        # state snapshots are copies inside the loop); a second pass over the
-        # same flushes brackets the commit launches for the roofline.
-        elapsed, _, B_, L_, width = run_pass(True, 1, False)
-        rec = run_pass(True, 1, True)[1]
-    else:
-        _, rec, B_, L_, width = one_stream
-        elapsed = per_layer
-    launch_bytes = float(np.mean([b for b, _ in rec]))
-    launch_ms = float(np.mean([t for _, t in rec]))
-    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    how = ("the layers' caches stacked as the batch rows of one cache, one flush call per step"
-           if args.mode == "stacked" else f"one cache per layer, the layers' calls over {args.streams} streams")
+    timed = run_pass(True, 1)
+    if args.profile_flush:
+        # A counter run profiles the timed pass alone: its steps are the last cut_kernel ranges.
+        return {"value": tokens / timed["elapsed"], "ms_per_step": timed["elapsed"] / args.steps * 1e3,
+                "config": {"workload": "profiling run of the headline's timed stacked pass"},
+                "roofline": {"avg_launch_ms": float(np.mean(timed["step_ms"]))}}
+    metered = run_pass(True, 1, meter=True)
+    per_layer = {}
+    if args.flush_passes == "all":
+        for n_streams in sorted({1, args.streams}):
+            try:
+                r = run_pass(False, n_streams)
+                per_layer[f"per_layer_calls_{n_streams}_stream_tokens_per_s"] = tokens / r["elapsed"]
+                per_layer[f"per_layer_calls_{n_streams}_stream_ms_per_layer_flush"] = \
+                    r["elapsed"] / args.steps / layers * 1e3
+            except Exception as e:   # a secondary pass never loses the headline
+                per_layer[f"per_layer_calls_{n_streams}_stream_error"] = f"{type(e).__name__}: {e}"
+    recs = metered["records"]
+    stage_bytes = {k: float(np.mean([by[k] for by, _ in recs])) for k in ("alpha", "route", "commit", "pack")}
+    stage_ms = {k: float(np.mean([ms[k] for _, ms in recs])) for k in ("alpha", "route", "commit", "pack")}
+    step_bytes = sum(stage_bytes.values())
+    step_ms = float(np.mean(timed["step_ms"]))
+    achieved = gbs(step_bytes, step_ms)
+    stages = {k: {"bytes": stage_bytes[k], "ms": stage_ms[k], "achieved": gbs(stage_bytes[k], stage_ms[k]),
+                  "frac": gbs(stage_bytes[k], stage_ms[k]) / HBM_PEAK_GBS} for k in stage_bytes}
     return {
-        "value": tokens / elapsed,
-        "ms_per_step": elapsed / args.steps * 1e3,
+        "value": tokens / timed["elapsed"],
+        "ms_per_step": timed["elapsed"] / args.steps * 1e3,
         "config": {"workload": f"{layers}-layer flush, Qwen3-1.7B KV shape (8x128 bf16), batch 1, flush {F}, "
                                f"K=12, B=128, Alpha exact pool {EXACT} / span cap {SPAN}, Beta novelty + 4->2 "
                                "split, attach route, mid-anchor plan + pack",
                    "layers": layers, "flush": F, "batch": 1, "kv_groups": G, "head_dim": D, "clusters": K,
-                   "slots_per_level": B_, "levels": L_, "exact_tokens": EXACT,
-                   "span_cap": SPAN, "stream_flushes": f"{3 + args.warmup}..{2 + args.warmup + args.steps}",
-                   "pooled_width_after_last_flush": width, "mode": how,
-                   **({} if one_stream is None else {
-                       "per_layer_calls_one_stream_tokens_per_s": tokens / one_stream[0],
-                       "per_layer_calls_one_stream_ms_per_layer_flush": one_stream[0] / args.steps / layers * 1e3,
-                       f"per_layer_calls_{args.streams}_streams_tokens_per_s": tokens / per_layer})},
-        "roofline": {"kernel": "commit stage: bucket_kernel + commit_kernel + units_kernel + carries_kernel per "
-                               "level + finish_kernel" + (" (one launch sequence for all layers)" if args.mode == "stacked"
-                                                  else " (one-stream pass)"),
-                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": STACKED_COMMIT_TRAFFIC_BYTES if args.mode == "stacked" else None,
-                     "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": launch_ms,
-                     "launches": len(rec)},
+                   "slots_per_level": timed["B"], "levels": timed["L"], "exact_tokens": EXACT, "span_cap": SPAN,
+                   "steps_are": f"flushes 3..16 of chained 32K-token streams ({len(segments)} segment(s), "
+                                f"{args.warmup} warm-up + {args.steps} timed steps)",
+                   "pooled_width_after_last_flush": timed["width"],
+                   "mode": "the layers' caches stacked as the batch rows of one cache, one flush call per step",
+                   **per_layer},
+        "roofline": {"kernel": "whole flush step: cut/score/choose + partition, order/attach/seed, "
+                               "bucket/commit/units/carries x6/finish x2, plan + pack (one launch sequence "
+                               "for all layers)",
+                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": args.step_traffic,
+                     "algorithmic_bytes_per_launch": step_bytes, "avg_launch_ms": step_ms,
+                     "launches": len(timed["step_ms"]),
+                     "timing": "HIP events around each timed step on its stream",
+                     "stages": stages},
     }
 
 
-def decode_workload(args, torch, np):
+# ----------------------------------------------------------------------
+# Config 1: one flush of one layer (the CPU reference configuration) on the GPU
+# ----------------------------------------------------------------------
+
+def config1_setup(torch, dev, seed=7):
+    """Qwen3-0.6B KV shape (8 x 128), batch 1, K=12 frozen centers N(0,1)*4 opened by a first flush of
+    the 12 center rows at positions 0..11, then the timed flush: 2048 rows at positions 2048..4095,
+    90% a center plus N(0, 0.5^2) noise, 10% outliers N(0,1)*12 (orphans). B=128, Alpha / Beta off,
+    s_h = 64 (lambda * s_h separates noise, about 32, from outliers, about 2e4)."""
     from logkv_amd import LogStructuredKVCache
+    from workloads import rope_tables
+
+    cos, sin = rope_tables(N, D)
+    cache = LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev, dtype=torch.bfloat16,
+                                 semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
+                                 semantic_flush_granularity=F, semantic_anchor_mode="mid",
+                                 allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D)
+    g = torch.Generator().manual_seed(seed)
+    centers = torch.randn(1, G, K, D, generator=g) * 4
+    label = torch.randint(0, K, (1, G, F), generator=g)
+    x = torch.gather(centers, 2, label[..., None].expand(-1, -1, -1, D)) + torch.randn(1, G, F, D, generator=g) * 0.5
+    far = torch.rand(1, G, F, generator=g) < 0.1
+    k = torch.where(far[..., None], torch.randn(1, G, F, D, generator=g) * 12, x).to(torch.bfloat16)
+    v = (torch.randn(1, G, F, D, generator=g)).to(torch.bfloat16)
+    return cache, centers.to(torch.bfloat16), k, v
+
+
+def config1_workload(args, torch, np):
+    dev = torch.device("cuda", 0)
+    cache, centers, k, v = config1_setup(torch, dev)
+    seed_pos = torch.arange(K, device=dev).unsqueeze(0)
+    cache.route_and_flush_batch(centers.to(dev), centers.to(dev), seed_pos)
+    state = {n: b.clone() for n, b in cache.named_buffers()}
+    kd, vd = k.to(dev), v.to(dev)
+    pos = torch.arange(F, 2 * F, device=dev).unsqueeze(0)
+    assign = torch.empty(G, F, dtype=torch.int8, device=dev)
+    order = torch.empty(1, F, dtype=torch.int32, device=dev)
+    snap = (cache.level_count.long().cpu().numpy(), cache.alive.cpu().numpy(), cache.p_hi_c.cpu().numpy())
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    reps = 50
+    for i in range(reps + 5):
+        for n, b in cache.named_buffers():
+            b.copy_(state[n])
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(stream)
+        cache.route_and_flush_batch(kd, vd, pos, assign_out=assign, order_out=order)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        if i >= 5:
+            times.append(ev[0].elapsed_time(ev[1]))
+    ms = float(np.median(times))
+    nbytes = route_bytes(F, G, D, K) + commit_bytes(*snap, assign.cpu().numpy(), order.long().cpu().numpy(),
+                                                    pos.cpu().numpy(), np.array([F]), cache.B_prime,
+                                                    cache.L_alloc, D, D)
+    orphans = int((~cache.alive.cpu()).sum())
+    return {"workload": "one flush of one layer, Qwen3-0.6B KV shape (8 x 128 bf16), batch 1, 2048 rows, 12 live "
+                        "clusters with frozen centers N(0,1)*4, 90% center + N(0,0.5^2), 10% outliers N(0,1)*12, "
+                        "B=128, Alpha / Beta off, s_h=64; device time of the route + commit from HIP events, "
+                        f"median of {reps} flushes from the same restored state",
+            "ms_per_flush": ms, "flushed_tokens_per_s": F / (ms * 1e-3),
+            "slots_per_level": cache.B_prime, "levels": cache.L_alloc, "clusters_alive_after": K * G - orphans,
+            "roofline": {"kernel": "order/attach/seed + bucket/commit/units/carries/finish", "bound": "hbm",
+                         "achieved": gbs(nbytes, ms), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs(nbytes, ms) / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes,
+                         "note": "a single small flush is launch- and latency-bound"}}
+
+
+# ----------------------------------------------------------------------
+# Config 4: decode at 32K context through the streaming engine
+# ----------------------------------------------------------------------
+
+def decode_workload(args, torch, np):
+    from logkv_amd import LogKVStreamingAttention, LogStructuredKVCache
     from logkv_amd.log_kv_pack import _launch_pack, packed_attention, packed_dim, readout_view
-    from logkv_amd.workloads import fill_readout_state, rope_tables
+    from workloads import fill_readout_state, rope_tables
 
     dev = torch.device("cuda", 0)
     Bt, HQ = 8, 16
@@ -401,56 +600,47 @@ def decode_workload(args, torch, np):
                                  allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D,
                                  alpha_exact_tokens=EXACT, alpha_span_max_tokens=SPAN, beta_novelty=True,
                                  beta_adaptive_merge=True)
-    archived = N - F - EXACT
-    fill_readout_state(cache, seed=21, recent=F, archived=archived)
     steps, warm = args.decode_steps, 8
-    gen = torch.Generator(device=dev).manual_seed(77)
-    qs = torch.randn(steps + warm, Bt, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16)
-    ks = torch.randn(steps + warm, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
-    vs = torch.randn(steps + warm, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
-    dim = packed_dim(D, D)
+    archived = N - F - EXACT
+    # The recent window starts short by the decoded tokens, so it ends full and no flush falls inside.
+    fill_readout_state(cache, seed=21, recent=F - steps - warm, archived=archived)
     scale = D ** -0.5
+    engine = LogKVStreamingAttention(cache, scale)
+    gen = torch.Generator(device=dev).manual_seed(77)
+    n = steps + warm
+    qs = torch.randn(n, Bt, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    ks = torch.randn(n, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    vs = torch.randn(n, Bt, G, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    start = cache.token_count
+    pos = torch.arange(start, start + n, device=dev)
+    ends = (torch.rand(n, Bt, 1, generator=gen, device=dev) < 1 / 32).to(torch.uint8)
+    for i in range(warm):
+        engine(qs[i], ks[i], vs[i], ks[i], input_pos=pos[i:i + 1], span_ends=ends[i])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warm, n):
+        engine(qs[i], ks[i], vs[i], ks[i], input_pos=pos[i:i + 1], span_ends=ends[i])
+    torch.cuda.synchronize()
+    eng_ms = (time.perf_counter() - t0) / steps * 1e3
+    progress(f"decode: {steps} tokens through the streaming engine, {eng_ms:.4f} ms per token")
+    if cache.recent_count != F and cache.recent_count + (1 if engine._log_kv_pending else 0) != F:
+        raise RuntimeError(f"decode window ended at {cache.recent_count} rows, expected {F}")
+
+    # The attention kernels apart from the host: one decode step (pack of the new row, attention)
+    # and its attention alone captured in HIP graphs from static inputs, checked bit for bit
+    # against the eager calls, and replayed back to back.
+    dim = packed_dim(D, D)
     view = readout_view(cache)
     plan = cache._semantic_attention_plan()
     cap = cache.K_max * cache.L_alloc * cache.B_prime + EXACT + cache.recent_capacity + 2
     ka = torch.empty(Bt, G, cap, dim, dtype=torch.bfloat16, device=dev)
     va = torch.empty_like(ka)
-    # Packed prefix once (the first decode step after a flush), then one new row per step.
-    _launch_pack(cache, view, plan, ks[0], vs[0], dim, ka, va, False, 0)
+    q_s, k_s, v_s = qs[-1].clone(), ks[-1].clone(), vs[-1].clone()
     recent = cache.recent_count
     tail = recent + 1
+    _launch_pack(cache, view, plan, k_s, v_s, dim, ka, va, False, 0)
+    _, workspace = packed_attention(q_s, ka, va, plan, tail, scale, 1, D, G, None, cache.alpha_count_dev)
     stream = torch.cuda.current_stream(dev)
-    workspace = None
-    events = []
-
-    def step(i, timed):
-        nonlocal workspace
-        _launch_pack(cache, view, plan, ks[i], vs[i], dim, ka, va, True, recent)
-        if timed:
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            ev[0].record(stream)
-        _, workspace = packed_attention(qs[i], ka, va, plan, tail, scale, 1, D, G, workspace, cache.alpha_count_dev)
-        if timed:
-            ev[1].record(stream)
-            events.append(ev)
-
-    for i in range(warm):
-        step(i, False)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(warm + i, True)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    progress(f"decode: {steps} steps in {elapsed:.3f} s")
-    step_event_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
-    # Launch durations apart from the host: the per-step events above also hold the
-    # host's launch gaps whenever Python issues slower than the device runs (a serving
-    # loop captures its step instead). One step (pack of the new row, then the
-    # attention) and its attention alone are captured in HIP graphs from static
-    # inputs, checked bit for bit against the eager calls, and replayed back to back.
-    i_last = warm + steps - 1
-    q_s, k_s, v_s = qs[i_last].clone(), ks[i_last].clone(), vs[i_last].clone()
 
     def full_step():
         _launch_pack(cache, view, plan, k_s, v_s, dim, ka, va, True, recent)
@@ -481,39 +671,45 @@ def decode_workload(args, torch, np):
 
     step_ms = replayed_ms(full_step)
     attn_ms = replayed_ms(attention_only)
-    reps = 64
     width = plan.width
     rows = width + cache.alpha_count + tail
     lanes = Bt * G
-    # Algorithmic bytes: every packed K and V row of every lane once, queries and outputs.
-    attn_bytes = lanes * rows * dim * 2 * 2 + Bt * HQ * D * 2 * 2
-    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
-    eager_ms = elapsed / steps * 1e3
+    # Algorithmic bytes: every packed row of every lane once as the kernel needs it - the key's
+    # D features and its bias column, the value's D features (2 * (D + 1) + 2 * D = 514 B) - plus
+    # the queries and outputs.
+    row_bytes = 2 * (D + 1) + 2 * D
+    attn_bytes = lanes * rows * row_bytes + Bt * HQ * D * 2 * 2
+    achieved = gbs(attn_bytes, attn_ms)
     return {
-        "workload": "decode attention, one layer, batch 8, Qwen3-1.7B GQA (16 q / 8 KV heads x 128, bf16), "
-                    f"32K-token cache: recent {F}, exact pool {EXACT}, 12 clusters holding {archived} archived "
-                    "tokens per lane, masses ~ U(1,64); packed prefix reused, one new row per step; ms_per_token "
-                    "= one step (pack of the new row + attention) replayed from a HIP graph, ms_per_token_eager = "
-                    "the same steps launched from Python one by one",
-        "ms_per_token": step_ms, "ms_per_token_28_layers": 28 * step_ms, "ms_per_token_eager": eager_ms,
-        "steps": steps,
+        "workload": "decode, one layer, batch 8, Qwen3-1.7B GQA (16 q / 8 KV heads x 128, bf16), 32K-token cache: "
+                    f"recent window ending at {F} rows, exact pool {EXACT}, 12 clusters holding {archived} archived "
+                    "tokens per lane, masses ~ U(1,64); ms_per_token = wall time per token through "
+                    "LogKVStreamingAttention (pending-token pairing, pack of the new rows, attention, add_recent "
+                    "of every token pair), launched from Python",
+        "ms_per_token": eng_ms, "ms_per_token_28_layers": 28 * eng_ms, "steps": steps,
+        "device_ms_per_token": step_ms,
+        "device_ms_per_token_note": "one step's pack + attention replayed from a HIP graph (no host work)",
         "packed_rows_per_lane": rows, "pooled_width": width,
         "roofline": {"kernel": "stream_kernel + combine_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": attn_ms,
-                     "timing": f"{reps} back-to-back replays of one step's attention launches (HIP graph)",
-                     "avg_step_event_ms": step_event_ms},
+                     "algorithmic_bytes_per_launch": attn_bytes, "bytes_per_packed_row": row_bytes,
+                     "avg_launch_ms": attn_ms,
+                     "timing": "64 back-to-back replays of one step's attention launches (HIP graph)"},
     }
 
 
+# ----------------------------------------------------------------------
+# Config 3: streaming prefill
+# ----------------------------------------------------------------------
+
 def prefill_workload(args, torch, np):
-    """Streaming prefill of a 32,768-token sequence through 28 Qwen3-1.7B-shaped layer caches, one call per layer
-    as a model makes them: per 2048-token block and layer, the chunk attention of the block's 16 query heads over
-    [compressed cache | block] (causal within the block) and add_recent, which flushes 2048 rows into the ladders
-    once the recent window is full. Queries, keys and values are seeded random bf16 (the model's projections are
-    not on this path)."""
+    """Streaming prefill of a 32,768-token sequence through 28 Qwen3-1.7B-shaped layer caches, one call per
+    layer as a model makes them: per 2048-token block and layer, the chunk attention of the block's 16 query
+    heads over [compressed cache | block] (causal within the block) and add_recent, which flushes 2048 rows
+    into the ladders once the recent window is full. Queries, keys and values are seeded random bf16 (the
+    model's projections are not on this path)."""
     from logkv_amd import LogStructuredKVCache, log_kv_chunk_attention
-    from logkv_amd.workloads import Mixture, rope_tables
+    from workloads import Mixture, rope_tables
 
     dev = torch.device("cuda", 0)
     layers, HQ, blocks = args.layers, 16, N // F
@@ -535,11 +731,11 @@ def prefill_workload(args, torch, np):
         pos = torch.arange(blk * F, (blk + 1) * F, device=dev).unsqueeze(0)
         ends = torch.tensor([[(p + 7) % 32 == 0 for p in range(blk * F, (blk + 1) * F)]], dtype=torch.uint8,
                             device=dev)
-        # Rows the block's attention reads in layer 0 (every layer holds the same counts):
-        # the pooled width (largest lane), the exact pool, the recent window and the block.
+        # Rows the block's attention reads (every layer holds the same counts): the pooled width of the
+        # widest lane, the exact pool, the recent window, then the block causally.
         c0 = caches[0]
-        rows = int(c0.level_count.long().sum((-1, -2)).max()) + c0.alpha_count + c0.recent_count + F
-        attn_flops.append(layers * 4 * F * rows * D * HQ)
+        prefix = int(c0.level_count.long().sum((-1, -2)).max()) + c0.alpha_count + c0.recent_count
+        attn_flops.append(layers * HQ * 4 * D * (F * prefix + F * (F + 1) // 2))
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         events = []
@@ -562,20 +758,26 @@ def prefill_workload(args, torch, np):
                     f"heads x 128, bf16), batch 1, {F}-token blocks, recent {F}, K={K}, B={B}, Alpha {EXACT}/{SPAN}, "
                     "Beta, mid anchor; per block and layer: chunk attention (matrix cores) + add_recent (flush)",
         "ms_per_block": float(np.mean(block_ms)), "ms_per_block_by_block": [round(x, 2) for x in block_ms],
+        "tokens_per_s": N / (float(np.sum(block_ms)) * 1e-3),
         "attention_ms_per_block": float(np.mean(attn_ms)),
-        "attention_roofline": {"kernel": "chunk_kernel", "bound": "mfma", "achieved": tflops, "peak": 2500.0,
-                               "unit": "TFLOP/s", "frac": tflops / 2500.0,
-                               "flops": "4 * T_q * S * D per query head (S = packed rows)"},
+        "attention_roofline": {"kernel": "chunk_kernel + chunk_combine_kernel", "bound": "mfma", "achieved": tflops,
+                               "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / BF16_PEAK_TFLOPS,
+                               "flops": "4 * D per (query row, visible key) per query head: every prefix row and "
+                                        "the block causally (T_q * (T_q + 1) / 2 pairs)"},
         "flushes": sum(1 for x in slots if x > 0),
         "slots_per_cluster_after_each_block": [round(x, 1) for x in slots],
     }
 
 
+# ----------------------------------------------------------------------
+# Config 5: unified route control
+# ----------------------------------------------------------------------
+
 def unified_workload(args, torch, np):
     """The unified (Ward / radius) route control: batch 4 x 8 KV groups, recent = flush = 4096 rows, a
     131,072-token stream (31 flush events) of a 12-Gaussian mixture that drifts every 16K tokens."""
     from logkv_amd import LogStructuredKVCache
-    from logkv_amd.workloads import Mixture, rope_tables
+    from workloads import Mixture, rope_tables
 
     dev = torch.device("cuda", 0)
     Bt, T, stream_tokens, s_h = 4, 4096, 131072, 64.0
@@ -615,19 +817,135 @@ def unified_workload(args, torch, np):
         "flushed_tokens_per_s": Bt * T / (ms * 1e-3), "ms_per_flush": ms,
         "device_ms_per_flush": float(np.mean(times)), "timed_flushes": timed, "warmup_flushes": warm,
         "live_clusters_per_lane": float(cache.alive.float().sum(-1).mean()),
-        "note": "one layer; the reducer runs one workgroup per lane, all rounds of a stage in one launch",
     }
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__)
+# ----------------------------------------------------------------------
+# CPU baseline
+# ----------------------------------------------------------------------
+
+def host_info():
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return model, cores
+
+
+def cpu_baseline(seconds: float):
+    """The oracle (numpy restatement) of the headline flush for one layer on the host: Alpha / Beta,
+    route, commit and the pack of the new prefix, on flushes 3..16 of fresh 32K-token streams."""
+    import numpy as np
+    import torch
+
+    from oracle import OracleCache
+    from workloads import Mixture, rope_tables
+
+    torch.set_num_threads(1)
+    model, cores = host_info()
+    cos, sin = (t.numpy() for t in rope_tables(N, D))
+    mix = Mixture(1, G, D, clusters=K, seed=1)
+    rows = lambda: mix.rows(F).float().numpy()  # noqa: E731
+    n, t, streams = 0, 0.0, 0
+    while t < seconds:
+        ora = OracleCache(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, exact_tokens=EXACT,
+                          span_max=SPAN, beta_novelty=True, beta_adaptive=True, cos=cos, sin=sin)
+        streams += 1
+        for j in range(STREAM_FLUSHES):
+            k, v = rows(), rows()
+            pos = np.arange(j * F, (j + 1) * F)[None]
+            t0 = time.perf_counter()
+            ora.flush_rows(k, v, pos, span_ends_for(j))
+            ora.pack(None, None)
+            if j >= PREP_FLUSHES:
+                t += time.perf_counter() - t0
+                n += 1
+            if t >= seconds:
+                break
+    return {"value": F * n / t, "unit": "flushed tokens/s", "cores": 1, "kind": "port",
+            "host_cpu": model, "host_cores_available": cores, "torch_threads": torch.get_num_threads(),
+            "sample": f"oracle (numpy) Alpha/Beta + route + commit + pack of {n} flushes (flushes 3..16 of "
+                      f"{streams} 32K-token streams) of one layer, batch 1, 8 groups x 128, K=12, B=128, "
+                      f"exact pool 256, {F} rows each, {t:.1f} s, 1 thread"}
+
+
+# ----------------------------------------------------------------------
+# rocprofv3 counter summary
+# ----------------------------------------------------------------------
+
+def _counter_rows(path):
+    import csv
+
+    p = Path(path)
+    files = [p] if p.is_file() else sorted(p.rglob("*counter_collection.csv"))
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {path}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    return rows
+
+
+def _short(name):
+    return name.replace("(anonymous namespace)::", "").split("(")[0].replace("logkv::", "").replace("void ", "")
+
+
+def pmc_summary(fetch_dir, write_dir, steps, probe_mib):
+    """HBM bytes per timed headline step from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
+    its reading of the copy probe of ``probe_mib`` MiB; a step runs from one cut_kernel to the next."""
+    out = {}
+    for name, path in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _counter_rows(path)
+        probe = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        factor = probe_mib * 1024 / probe[0] if probe else 1.0
+        starts = [i for i, r in enumerate(rows) if _short(r["Kernel_Name"]) == "cut_kernel"]
+        bounds = list(zip(starts, starts[1:] + [len(rows)]))[-steps:]
+        per_step, per_kernel = [], {}
+        for a, b in bounds:
+            total = 0.0
+            for r in rows[a:b]:
+                k = _short(r["Kernel_Name"])
+                if "copyBuffer" in k or "elementwise" in k or "fill" in k.lower():
+                    continue
+                v = float(r["Counter_Value"]) * factor * 1024
+                total += v
+                per_kernel[k] = per_kernel.get(k, 0.0) + v / len(bounds)
+            per_step.append(total)
+        out[name] = {"bytes_per_step": sum(per_step) / len(per_step), "factor": factor,
+                     "probe_kib": probe[0] if probe else None, "per_kernel": per_kernel}
+    out["traffic_per_step"] = out["FETCH_SIZE"]["bytes_per_step"] + out["WRITE_SIZE"]["bytes_per_step"]
+    return out
+
+
+# ----------------------------------------------------------------------
+
+def run_leg(result, key, fn, *args):
+    """A secondary measurement: its failure is recorded in the line, never fatal."""
+    try:
+        result[key] = fn(*args)
+    except Exception as e:
+        traceback.print_exc()
+        result[key] = {"error": f"{type(e).__name__}: {e}"}
+        progress(f"{key}: failed ({type(e).__name__}: {e})")
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=28)
-    ap.add_argument("--mode", choices=("stacked", "layers"), default="stacked",
-                    help="stacked: the layers' caches as batch rows of one cache (one call per flush step); "
-                         "layers: one cache per layer")
     ap.add_argument("--streams", type=int, default=4,
                     help="HIP streams the per-layer calls are spread over (a one-stream pass always runs too)")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -636,22 +954,37 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-unified", action="store_true", help="skip the unified-route control measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the streaming-prefill measurement")
+    ap.add_argument("--no-config1", action="store_true", help="skip the one-layer flush of the CPU configuration")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a plain copy of known size that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
     ap.add_argument("--flush-passes", choices=("all", "stacked"), default="all",
-                    help="stacked: run only the stacked pass (profiling runs)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box here has one MI355X, --gpus {args.gpus} is not run",
-              file=sys.stderr)
-        sys.exit(2)
+                    help="stacked: only the stacked passes of the headline (profiling runs)")
+    ap.add_argument("--profile-flush", action="store_true",
+                    help="profiling run: the timed stacked pass of the headline only (no metered pass, no legs)")
+    ap.add_argument("--decode-only", action="store_true", help="profiling run: only the decode measurement")
+    ap.add_argument("--step-traffic", type=float, default=None,
+                    help="HBM bytes per headline step measured by counter runs (reported as roofline.traffic)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc runs of --profile-flush and exit")
+    args = ap.parse_args(argv)
+    if args.warmup < 0:
+        ap.error("--warmup must be >= 0")
+    if args.steps < 1:
+        ap.error("--steps must be >= 1")
     if args.streams < 1:
-        print("--streams must be at least 1", file=sys.stderr)
-        sys.exit(2)
-    if 2 + args.warmup + args.steps > 16:
-        print("warmup + steps must fit the 32K-token stream: at most 14 flushes after the two warm-up flushes",
-              file=sys.stderr)
+        ap.error("--streams must be at least 1")
+    return args
+
+
+def main():
+    args = parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.steps, args.copy_probe_mib or 1024), indent=1))
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box here has one MI355X, so --gpus {args.gpus} is not run; the "
+              "path shards by layer and lane with no exchange in the flush (see the sharding notes)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -666,6 +999,11 @@ def main():
         torch.cuda.synchronize()
         progress(f"copy probe: {args.copy_probe_mib} MiB copied")
         del src, dst
+    if args.decode_only:
+        print(json.dumps(decode_workload(args, torch, np)), flush=True)
+        return
+    if args.profile_flush:
+        args.flush_passes = "stacked"
     fl = flush_workload(args, torch, np)
     result = {
         "metric": "flushed tokens/s (route+merge+pack) & decode ms/token at 32K ctx, 1 GPU",
@@ -684,16 +1022,20 @@ def main():
         "config": fl["config"],
         "roofline": fl["roofline"],
     }
-    if not args.no_decode:
-        result["decode"] = decode_workload(args, torch, np)
-        result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
-    if not args.no_prefill and args.flush_passes == "all":
-        result["prefill"] = prefill_workload(args, torch, np)
-    if not args.no_unified and args.flush_passes == "all":
-        result["unified"] = unified_workload(args, torch, np)
-    if not args.no_cpu_baseline:
-        progress("cpu baseline: oracle flushes on the host")
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if not args.profile_flush:
+        if not args.no_config1:
+            run_leg(result, "config1", config1_workload, args, torch, np)
+        if not args.no_decode:
+            run_leg(result, "decode", decode_workload, args, torch, np)
+            if "ms_per_token" in result["decode"]:
+                result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
+        if not args.no_prefill and args.flush_passes == "all":
+            run_leg(result, "prefill", prefill_workload, args, torch, np)
+        if not args.no_unified and args.flush_passes == "all":
+            run_leg(result, "unified", unified_workload, args, torch, np)
+        if not args.no_cpu_baseline:
+            progress("cpu baseline: oracle flushes on the host")
+            run_leg(result, "cpu_baseline", cpu_baseline, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

@@ -1,6 +1,7 @@
 // extern "C" entry points: argument validation, workspace carving, launches.
 #include <cstdio>
 #include <cstdarg>
+#include <cstdint>
 #include <cstring>
 
 #include <algorithm>
@@ -31,7 +32,9 @@ int check_ladder(const logkv_ladder_view* c) {
   if (int64_t(c->n_batch) * c->n_groups * c->k_max > logkv::kMaxLadders)
     return fail(LOGKV_EINVAL, "batch * groups * clusters = %lld exceeds %d",
                 (long long)(int64_t(c->n_batch) * c->n_groups * c->k_max), logkv::kMaxLadders);
-  if (c->slots < 2) return fail(LOGKV_EINVAL, "slots per level must be >= 2, got %d", c->slots);
+  // level_count and the ladder plans hold per-level counts in int16.
+  if (c->slots < 2 || c->slots > INT16_MAX)
+    return fail(LOGKV_EINVAL, "slots per level must be in [2, %d], got %d", INT16_MAX, c->slots);
   if (c->levels < 1 || c->levels > logkv::kMaxLevels)
     return fail(LOGKV_EINVAL, "levels %d outside [1, %d]", c->levels, logkv::kMaxLevels);
   if (c->dk < 4 || c->dv < 4 || c->dk % 4 || c->dv % 4 || c->dk > logkv::kMaxDim || c->dv > logkv::kMaxDim)
@@ -458,7 +461,12 @@ int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, 
     return fail(LOGKV_EINVAL, "bad packed width %d", a->dim);
   if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
     return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
+  if (a->n_batch < 1 || a->cap < 1 || a->tail < 0 || a->tail > a->cap)
+    return fail(LOGKV_EINVAL, "attention needs n_batch >= 1 and 0 <= tail <= cap (cap >= 1)");
   if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
+  // The streaming and tiled kernels read packed rows in 16-byte units.
+  if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
+    return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
   if (!ws || ws_bytes < logkv::attention_workspace_floats(*a) * 4)
     return fail(LOGKV_EINVAL, "attention workspace too small");
   const int rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(ws),

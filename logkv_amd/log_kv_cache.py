@@ -247,6 +247,9 @@ class LogStructuredKVCache(nn.Module):
         if budget is not None:
             self.alpha_baseline_B = B
             self.alpha_budget_bytes = budget
+        if not 2 <= B_eff <= 32767:
+            # Per-level slot counts are int16 (level_count and the device's ladder plans).
+            raise ValueError(f"slots per level B'={B_eff} must be in [2, 32767]")
         self.B = self.B_prime = B_eff
         self.max_levels = self.L_alloc = L
         self.recent_capacity = 2 * recent
@@ -319,10 +322,9 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError("semantic_s_h must be finite and > 0")
         buf("s_h", s_h.contiguous())
         # Radius limits of the unified route's candidates, sqrt(lambda * s_h) per
-        # lane (litgpt/log_kv_cache.py:3617-3620, :2728-2729).
-        lam = float(cluster_lambda_rel)
-        limits = [math.sqrt(lam * float(x)) for x in s_h.reshape(-1).cpu().tolist()]
-        buf("_unified_limits", torch.tensor(limits, dtype=torch.float32, device=device))
+        # lane (litgpt/log_kv_cache.py:3617-3620, :2728-2729), refreshed from the
+        # live s_h before every unified flush.
+        buf("_unified_limits", torch.zeros(batch_size * n_groups, dtype=torch.float32, device=device))
         self._workspace = None
         self._alpha_keep_alive = None
         # C-ABI argument structs and per-flush-length buffers, built once and
@@ -457,6 +459,10 @@ class LogStructuredKVCache(nn.Module):
         if summary is None:
             summary = self._views["unified_summary"] = torch.zeros(2, dtype=torch.int32, device=self.level_k.device)
         stream = stream_of(k_raw.device)
+        # sqrt(lambda * s_h) in double, rounded once to float32, as the reference's host
+        # math.sqrt(lambda * s_h) (litgpt/log_kv_cache.py:3620-3621), from the s_h the attach
+        # route also reads, so both routes follow a caller's update of s_h.
+        self._unified_limits.copy_(self.s_h.reshape(-1).double().mul(self.cluster_lambda_rel).sqrt())
         check(lib().logkv_unified_plan(C.byref(view), C.byref(rows), C.byref(self._params), ptr(self._unified_limits),
                                        ptr(ws), ws.numel(), ptr(summary), stream), "logkv_unified_plan")
         steps, stuck = summary.tolist()

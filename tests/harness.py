@@ -5,7 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from logkv_amd.workloads import Mixture, rope_tables
+from workloads import Mixture, rope_tables
 
 STATE_FIELDS = ("level_k", "level_v", "level_w", "level_p_lo", "level_p_hi", "level_sum_wp", "level_order",
                 "pad_mask", "level_count", "centroid", "n_eff", "n_total", "p_hi_c", "level0_phase", "alive")

@@ -1,13 +1,21 @@
 """The C ABI's argument checks without a GPU: malformed views and arguments are
 rejected with LOGKV_EINVAL (or a negative size) and a message in logkv_last_error,
 before anything is launched. Every case here fails a check that precedes the first
-HIP call of its entry point; the pointers are never dereferenced."""
+HIP call of its entry point; the pointers are never dereferenced.
+
+The fake device addresses are only safe while no kernel can launch, so the module
+runs only where no HIP device is visible (the CPU suite); on a GPU box the same
+checks are exercised through real tensors by the GPU tests."""
 
 import ctypes as C
 
 import pytest
+import torch
 
 from logkv_amd import _lib
+
+pytestmark = pytest.mark.skipif(torch.cuda.is_available(),
+                                reason="fake device addresses are only passed where no HIP device is visible")
 
 FAKE = 0x10000   # a 64 KiB-aligned address that the checks accept and nothing reads
 
@@ -39,6 +47,7 @@ def test_valid_ladder_view_sizes_a_workspace(lib):
     ({"k_max": 0}, "cluster count"),
     ({"k_max": 33}, "cluster count"),
     ({"slots": 1}, "slots per level"),
+    ({"slots": 40000}, "slots per level"),
     ({"levels": 0}, "levels"),
     ({"dk": 6}, "multiples of 4"),
     ({"dv": 0}, "multiples of 4"),
@@ -94,6 +103,11 @@ def test_attention_arguments_are_checked(lib):
     assert decode(dim=136, n_heads=3) == _lib.LOGKV_EINVAL and "multiple of groups" in last_error(lib)
     assert decode(n_heads=4, tq=9) == _lib.LOGKV_EINVAL and "queries per KV group" in last_error(lib)
     assert decode(tq=1, causal_tail=2) == _lib.LOGKV_EINVAL and "causal_tail" in last_error(lib)
+    assert decode(causal_tail=0, n_batch=0) == _lib.LOGKV_EINVAL and "n_batch" in last_error(lib)
+    assert decode(n_batch=1, cap=0, tail=0) == _lib.LOGKV_EINVAL and "cap" in last_error(lib)
+    assert decode(cap=64, tail=1, k=FAKE + 8) == _lib.LOGKV_EINVAL and "16-byte aligned" in last_error(lib)
+    assert decode(k=FAKE, v=FAKE + 8) == _lib.LOGKV_EINVAL and "16-byte aligned" in last_error(lib)
+    a.v = FAKE
     a.causal_tail = 0
     assert lib.logkv_decode_attention(C.byref(a), table, 4, FAKE, need - 1, None) == _lib.LOGKV_EINVAL
     assert "workspace too small" in last_error(lib)

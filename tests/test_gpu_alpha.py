@@ -6,7 +6,7 @@ import torch
 
 from harness import STATE_FIELDS, compare_state, feed, make_pair, to_np
 from logkv_amd import alpha_log_kv as prod
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 from oracle import spans as ora
 
 pytestmark = pytest.mark.gpu

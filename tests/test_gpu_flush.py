@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from harness import compare_state, feed, make_pair, to_np
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 
 pytestmark = pytest.mark.gpu
 

@@ -55,7 +55,7 @@ def test_alpha_counts_unfinished_spans_and_each_group():
 def test_two_layers_and_retention_falls_with_length():
     """Two layer caches of a Qwen3-shaped stream (8 groups x 128, K=12, B=32, Alpha 32 / 16):
     the counts add over layers, and the retained share shrinks as the stream grows."""
-    from logkv_amd.workloads import Mixture, rope_tables
+    from workloads import Mixture, rope_tables
 
     cos, sin = rope_tables(8192, 128)
     caches = [LogStructuredKVCache(

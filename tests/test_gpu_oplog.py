@@ -9,7 +9,7 @@ import torch
 
 from harness import compare_state, make_pair, to_np
 from logkv_amd.log_kv_cache import _SemanticReplayPlans
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 from oracle import oplog as ora_oplog
 
 pytestmark = pytest.mark.gpu

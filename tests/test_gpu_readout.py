@@ -16,7 +16,7 @@ import torch
 
 from harness import feed, make_pair, to_np
 from logkv_amd import LogStructuredKVCache, log_kv_chunk_attention, pack_mid_kv, packed_dim
-from logkv_amd.workloads import Mixture, fill_readout_state, rope_tables
+from workloads import Mixture, fill_readout_state, rope_tables
 from oracle import readout as ro
 from oracle.numerics import bf16_round
 

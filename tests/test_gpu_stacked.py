@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from harness import STATE_FIELDS, to_np
-from logkv_amd.workloads import Mixture, rope_tables
+from workloads import Mixture, rope_tables
 
 pytestmark = pytest.mark.gpu
 

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from harness import compare_state
-from logkv_amd.workloads import Mixture, rope_tables
+from workloads import Mixture, rope_tables
 
 pytestmark = pytest.mark.gpu
 

@@ -10,7 +10,7 @@ import torch
 
 from logkv_amd import LogStructuredKVCache, alpha_log_kv
 from logkv_amd.log_kv_cache import _SemanticReplayUpdates
-from logkv_amd.workloads import Mixture, rope_tables
+from workloads import Mixture, rope_tables
 
 pytestmark = pytest.mark.gpu
 

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from logkv_amd.log_kv_cache import ladder_budget
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 from oracle import OracleCache, budget
 
 

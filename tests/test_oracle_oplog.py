@@ -17,7 +17,7 @@
 import numpy as np
 import pytest
 
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 from oracle import OracleCache, oplog
 
 FIELDS = ("level_k", "level_v", "level_w", "level_p_lo", "level_p_hi", "level_sum_wp", "level_order", "pad_mask",

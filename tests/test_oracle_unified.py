@@ -23,7 +23,7 @@ import math
 import numpy as np
 import pytest
 
-from logkv_amd.workloads import Mixture
+from workloads import Mixture
 from oracle import OracleCache
 from oracle import unified as U
 
