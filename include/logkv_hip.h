@@ -375,6 +375,23 @@ int64_t logkv_attention_workspace_bytes(const logkv_attention_args* args);
 int logkv_decode_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
+/* logkv_decode_attention without a workspace argument and without any
+ * allocation: the split partials live in a device-resident scratch array of
+ * the library (16 MiB per GPU, held until the process ends; its address is
+ * looked up once per device on the first call there, with that device
+ * current). No counterpart in the reference: it is for callers that cannot
+ * allocate - code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. Same arguments and result as logkv_decode_attention
+ * (the same kernels); a call whose partials
+ * (logkv_attention_workspace_bytes) exceed 16 MiB is rejected with
+ * LOGKV_EINVAL. The stream must belong to the current device. Every call on
+ * one GPU shares that GPU's scratch, so calls that overlap on one GPU (other
+ * streams, other threads) race; serialize them. Each split writes its whole
+ * partial before the combine reads it, so nothing needs clearing between
+ * calls. */
+int logkv_decode_attention_static(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
+                                  void* stream);
+
 /* The same attention for many query rows per KV group (a prefill or training
  * chunk), on the matrix cores (bf16 MFMA, fp32 accumulation, P split into two
  * bf16 parts): packed width <= 144, dv in {32, 64, 96, 128}. The key range is

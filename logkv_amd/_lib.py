@@ -161,6 +161,7 @@ SIGNATURES = {
     "logkv_pack": (_i32, [C.POINTER(ReadoutView), C.POINTER(PackArgs), _p, _p]),
     "logkv_attention_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
     "logkv_decode_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
+    "logkv_decode_attention_static": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p]),
     "logkv_chunk_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
     "logkv_chunk_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
 }

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include <algorithm>
+#include <mutex>
 
 #include "route.hpp"
 #include "unified.hpp"
@@ -185,6 +186,60 @@ int check_unified(const logkv_ladder_view* c, const logkv_rows_view* r) {
                 logkv::kMaxNodes, r->tokens, c->k_max);
   if (logkv::unified_reduce_lds(r->tokens + c->k_max) > 160 * 1024)
     return fail(LOGKV_EINVAL, "unified reducer state exceeds the LDS of a CU");
+  return LOGKV_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// Argument checks shared by the two decode entry points (workspace and static scratch).
+int check_decode(const logkv_attention_args* a, const int32_t* table, int64_t table_ints) {
+  if (!a || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention args or plan table are NULL");
+  if (a->n_groups < 1 || a->n_heads % a->n_groups) return fail(LOGKV_EINVAL, "heads must be a multiple of groups");
+  const int nq = (a->n_heads / a->n_groups) * a->tq;
+  if (a->tq < 1 || nq > 16) return fail(LOGKV_EINVAL, "queries per KV group (%d) must be in [1, 16]", nq);
+  if (a->dim % 8 || a->dim > 264 || a->dim <= a->dk || a->dim < a->dv || a->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "bad packed width %d", a->dim);
+  if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
+    return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
+  if (a->n_batch < 1 || a->cap < 1 || a->tail < 0 || a->tail > a->cap)
+    return fail(LOGKV_EINVAL, "attention needs n_batch >= 1 and 0 <= tail <= cap (cap >= 1)");
+  if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
+  // The streaming and tiled kernels read packed rows in 16-byte units.
+  if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
+    return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
+  return LOGKV_OK;
+}
+
+// Device-resident scratch of logkv_decode_attention_static: the split partials of one
+// decode call, for callers that cannot allocate. Each GPU holds its own copy for the
+// life of the process; in host code the array's name is not a device address, so its
+// address is taken once per device with hipGetSymbolAddress and only that is used.
+constexpr int64_t kStaticScratchBytes = int64_t(16) << 20;
+constexpr int kMaxScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+std::mutex g_scratch_mutex;
+
+int static_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(LOGKV_ERUNTIME, "no current HIP device for the static scratch");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(LOGKV_ERUNTIME, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return LOGKV_OK;
 }
 
@@ -453,24 +508,28 @@ int64_t logkv_attention_workspace_bytes(const logkv_attention_args* a) {
 
 int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, int64_t table_ints, void* ws,
                            int64_t ws_bytes, void* stream) {
-  if (!a || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention args or plan table are NULL");
-  if (a->n_groups < 1 || a->n_heads % a->n_groups) return fail(LOGKV_EINVAL, "heads must be a multiple of groups");
-  const int nq = (a->n_heads / a->n_groups) * a->tq;
-  if (a->tq < 1 || nq > 16) return fail(LOGKV_EINVAL, "queries per KV group (%d) must be in [1, 16]", nq);
-  if (a->dim % 8 || a->dim > 264 || a->dim <= a->dk || a->dim < a->dv || a->dv > logkv::kMaxDim)
-    return fail(LOGKV_EINVAL, "bad packed width %d", a->dim);
-  if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
-    return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
-  if (a->n_batch < 1 || a->cap < 1 || a->tail < 0 || a->tail > a->cap)
-    return fail(LOGKV_EINVAL, "attention needs n_batch >= 1 and 0 <= tail <= cap (cap >= 1)");
-  if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
-  // The streaming and tiled kernels read packed rows in 16-byte units.
-  if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
-    return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
+  int rc = check_decode(a, table, table_ints);
+  if (rc) return rc;
   if (!ws || ws_bytes < logkv::attention_workspace_floats(*a) * 4)
     return fail(LOGKV_EINVAL, "attention workspace too small");
-  const int rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(ws),
-                                         static_cast<hipStream_t>(stream));
+  rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(ws), static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_decode_attention_static(const logkv_attention_args* a, const int32_t* table, int64_t table_ints,
+                                  void* stream) {
+  int rc = check_decode(a, table, table_ints);
+  if (rc) return rc;
+  const int64_t need = logkv::attention_workspace_floats(*a) * 4;
+  if (need > kStaticScratchBytes)
+    return fail(LOGKV_EINVAL, "decode partials need %lld bytes, above the static scratch of %lld bytes",
+                (long long)need, (long long)kStaticScratchBytes);
+  void* scratch_ptr = nullptr;
+  rc = static_scratch(&scratch_ptr);
+  if (rc) return rc;
+  rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(scratch_ptr),
+                               static_cast<hipStream_t>(stream));
   if (rc) return fail(rc, "attention launch failed: %s", hipGetErrorString(hipGetLastError()));
   return LOGKV_OK;
 }
