@@ -712,7 +712,7 @@ def prefill_workload(args, torch, np):
     from workloads import Mixture, rope_tables
 
     dev = torch.device("cuda", 0)
-    layers, HQ, blocks = args.layers, 16, N // F
+    layers, HQ, blocks = args.layers, 16, max(1, min(N // F, args.prefill_blocks))
     cos, sin = rope_tables(N, D)
     caches = [LogStructuredKVCache((1, G, N, D), (1, G, N, D), B=B, recent_size=F, device=dev, dtype=torch.bfloat16,
                                    semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
@@ -754,7 +754,7 @@ def prefill_workload(args, torch, np):
     tflops = float(np.sum(attn_flops)) / attn_s / 1e12
     progress(f"prefill: {blocks} blocks, {np.mean(block_ms):.1f} ms per block over {layers} layers")
     return {
-        "workload": f"streaming prefill of {N} tokens through {layers} Qwen3-1.7B-shaped layer caches (16 q / 8 KV "
+        "workload": f"streaming prefill of {blocks * F} tokens through {layers} Qwen3-1.7B-shaped layer caches (16 q / 8 KV "
                     f"heads x 128, bf16), batch 1, {F}-token blocks, recent {F}, K={K}, B={B}, Alpha {EXACT}/{SPAN}, "
                     "Beta, mid anchor; per block and layer: chunk attention (matrix cores) + add_recent (flush)",
         "ms_per_block": float(np.mean(block_ms)), "ms_per_block_by_block": [round(x, 2) for x in block_ms],
@@ -962,7 +962,10 @@ def parse_args(argv=None):
                     help="stacked: only the stacked passes of the headline (profiling runs)")
     ap.add_argument("--profile-flush", action="store_true",
                     help="profiling run: the timed stacked pass of the headline only (no metered pass, no legs)")
-    ap.add_argument("--decode-only", action="store_true", help="profiling run: only the decode measurement")
+    ap.add_argument("--only", choices=("config1", "decode", "prefill", "unified"),
+                    help="profiling run: only this measurement, printed as its own JSON line")
+    ap.add_argument("--prefill-blocks", type=int, default=N // F,
+                    help="2048-token blocks of the streaming prefill (16 = the whole 32K-token sequence)")
     ap.add_argument("--step-traffic", type=float, default=None,
                     help="HBM bytes per headline step measured by counter runs (reported as roofline.traffic)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -999,8 +1002,10 @@ def main():
         torch.cuda.synchronize()
         progress(f"copy probe: {args.copy_probe_mib} MiB copied")
         del src, dst
-    if args.decode_only:
-        print(json.dumps(decode_workload(args, torch, np)), flush=True)
+    if args.only:
+        legs = {"config1": config1_workload, "decode": decode_workload, "prefill": prefill_workload,
+                "unified": unified_workload}
+        print(json.dumps(legs[args.only](args, torch, np)), flush=True)
         return
     if args.profile_flush:
         args.flush_passes = "stacked"

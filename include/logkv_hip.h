@@ -343,9 +343,44 @@ typedef struct logkv_pack_args {
   uint16_t* out_v;
   int32_t out_cap, dim;
   int32_t skip_pooled, recent_start;
+  /* Optional (NULL: not written): per packed row, float mass [n_batch, G, out_cap]
+   * (a pooled slot's stored w, 0 for padding; 1 or 0 for an exact row by its
+   * valid flag; 1 for recent and current rows) and uint8 validity. */
+  float* out_w;
+  uint8_t* out_valid;
 } logkv_pack_args;
 
 int logkv_pack(const logkv_readout_view* cache, const logkv_pack_args* args, const int32_t* table, void* stream);
+
+/* Packed rows [n_batch, G, out_cap, dim] bf16 of unpacked attention slots: keys
+ * k [n_batch, G, slots, dk] and values v (bf16, strided), masses w float
+ * [n_batch, G, slots]; column dk of a key row is the mass bias lam * log(w), or
+ * for the first s_m slots (anchor counts m int64 given) -log(max(m, 1)) +
+ * lam * log(max(w, 1)); among the first s_valid slots, those whose uint8 valid
+ * flag is 0 become zero rows with bias -10000. Bias rounded to bf16.
+ * Replaces the slot encoding of log_kv_slot_attention's Flash path
+ * (_slot_sdpa_inputs / _slot_mass_bias, litgpt/log_kv_cache.py:6418-6464,
+ * anchor_mass_bias litgpt/log_kv_position.py:128-133). */
+typedef struct logkv_slot_pack_args {
+  const uint16_t* k;
+  int64_t k_sb, k_sg, k_st;
+  const uint16_t* v;
+  int64_t v_sb, v_sg, v_st;
+  const float* w;
+  int64_t w_sb, w_sg;
+  const int64_t* m;
+  int64_t m_sb, m_sg;
+  int32_t s_m;
+  const uint8_t* valid;
+  int64_t valid_sb, valid_sg;
+  int32_t s_valid;
+  float lam;
+  int32_t n_batch, n_groups, slots, dk, dv, dim, out_cap;
+  uint16_t* out_k;
+  uint16_t* out_v;
+} logkv_slot_pack_args;
+
+int logkv_pack_slots(const logkv_slot_pack_args* args, void* stream);
 
 /* Attention of queries q [n_batch, n_heads, tq, dk] (post-RoPE, bf16, strided)
  * over the packed rows k / v [n_batch, G, cap, dim]: pooled width (read from
@@ -403,6 +438,53 @@ int logkv_decode_attention_static(const logkv_attention_args* args, const int32_
 int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* args);
 int logkv_chunk_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Beta 4->2 compaction of a block of n_rows entries (rows of each field
+ * contiguous per row, K / V bf16 or float32 with row strides k_st / v_st in
+ * elements): each layout row (start, width, out_start) of n_groups int64
+ * triples is a group of width 4 or 2. apply = 0 chooses each full group's cut
+ * in (2, 1, 3) of smallest normalised K + V distortion (ties keep the earlier)
+ * and writes it to cuts (1 for a two-row tail); apply = 1 reads recorded cuts.
+ * Outputs at out_start (+1 for the right side of a full group): float32
+ * weighted means of K and V [n_rows / 2, d], mass, p_lo / p_hi over the side's
+ * rows of positive mass (0 when the side has no mass), sum of sum_wp, smallest
+ * order, AND of pad. With out_k NULL only the cuts are chosen. Metadata
+ * pointers may be NULL (their outputs are skipped). A group whose layout or
+ * recorded cut is out of range is skipped and sets bit 0 of *status (when not
+ * NULL; the caller clears it).
+ * Replaces beta_log_kv.select_cuts / apply_cuts / merge_blocks
+ * (litgpt/beta_log_kv.py:29-105) and the fused _beta_merge kernel
+ * (litgpt/log_kv_updates_triton.py:90-173). */
+typedef struct logkv_beta_args {
+  const void* k;
+  int64_t k_st;
+  int32_t k_f32;
+  const void* v;
+  int64_t v_st;
+  int32_t v_f32;
+  const float* w;
+  const int64_t* p_lo;
+  const int64_t* p_hi;
+  const int64_t* sum_wp;
+  const int64_t* order;
+  const uint8_t* pad;
+  int64_t n_rows;
+  int32_t dk, dv;
+  const int64_t* layout;
+  int64_t n_groups;
+  uint8_t* cuts;
+  int32_t apply;
+  float* out_k;
+  float* out_v;
+  float* out_w;
+  int64_t* out_p_lo;
+  int64_t* out_p_hi;
+  int64_t* out_sum_wp;
+  int64_t* out_order;
+  uint8_t* out_pad;
+} logkv_beta_args;
+
+int logkv_beta_merge(const logkv_beta_args* args, int32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -101,7 +101,20 @@ class PackArgs(C.Structure):
         ("cur_k", _p), ("ck_sb", _i64), ("ck_sg", _i64), ("ck_st", _i64),
         ("cur_v", _p), ("cv_sb", _i64), ("cv_sg", _i64), ("cv_st", _i64),
         ("cur_len", _i32), ("out_k", _p), ("out_v", _p), ("out_cap", _i32), ("dim", _i32),
-        ("skip_pooled", _i32), ("recent_start", _i32),
+        ("skip_pooled", _i32), ("recent_start", _i32), ("out_w", _p), ("out_valid", _p),
+    ]
+
+
+class SlotPackArgs(C.Structure):
+    _fields_ = [
+        ("k", _p), ("k_sb", _i64), ("k_sg", _i64), ("k_st", _i64),
+        ("v", _p), ("v_sb", _i64), ("v_sg", _i64), ("v_st", _i64),
+        ("w", _p), ("w_sb", _i64), ("w_sg", _i64),
+        ("m", _p), ("m_sb", _i64), ("m_sg", _i64), ("s_m", _i32),
+        ("valid", _p), ("valid_sb", _i64), ("valid_sg", _i64), ("s_valid", _i32),
+        ("lam", C.c_float),
+        ("n_batch", _i32), ("n_groups", _i32), ("slots", _i32), ("dk", _i32), ("dv", _i32), ("dim", _i32),
+        ("out_cap", _i32), ("out_k", _p), ("out_v", _p),
     ]
 
 
@@ -112,6 +125,16 @@ class AttentionArgs(C.Structure):
         ("dim", _i32), ("k", _p), ("v", _p), ("cap", _i32), ("tail", _i32), ("causal_tail", _i32),
         ("scale", C.c_float), ("inv_scale_bf16", C.c_float),
         ("out", _p), ("o_sb", _i64), ("o_sh", _i64), ("o_st", _i64), ("alpha_count_dev", _p),
+    ]
+
+
+class BetaArgs(C.Structure):
+    _fields_ = [
+        ("k", _p), ("k_st", _i64), ("k_f32", _i32), ("v", _p), ("v_st", _i64), ("v_f32", _i32),
+        ("w", _p), ("p_lo", _p), ("p_hi", _p), ("sum_wp", _p), ("order", _p), ("pad", _p),
+        ("n_rows", _i64), ("dk", _i32), ("dv", _i32), ("layout", _p), ("n_groups", _i64), ("cuts", _p),
+        ("apply", _i32), ("out_k", _p), ("out_v", _p), ("out_w", _p), ("out_p_lo", _p), ("out_p_hi", _p),
+        ("out_sum_wp", _p), ("out_order", _p), ("out_pad", _p),
     ]
 
 
@@ -159,9 +182,11 @@ SIGNATURES = {
     "logkv_plan_table_ints": (_i64, [C.POINTER(ReadoutView)]),
     "logkv_mid_plan": (_i32, [C.POINTER(ReadoutView), _p, _p]),
     "logkv_pack": (_i32, [C.POINTER(ReadoutView), C.POINTER(PackArgs), _p, _p]),
+    "logkv_pack_slots": (_i32, [C.POINTER(SlotPackArgs), _p]),
     "logkv_attention_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
     "logkv_decode_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
     "logkv_decode_attention_static": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p]),
+    "logkv_beta_merge": (_i32, [C.POINTER(BetaArgs), _p, _p]),
     "logkv_chunk_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
     "logkv_chunk_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
 }

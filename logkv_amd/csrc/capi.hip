@@ -562,4 +562,44 @@ int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, i
   return LOGKV_OK;
 }
 
+int logkv_beta_merge(const logkv_beta_args* a, int32_t* status, void* stream) {
+  if (!a) return fail(LOGKV_EINVAL, "Beta merge args are NULL");
+  if (a->n_rows < 0 || a->n_rows % 2) return fail(LOGKV_EINVAL, "Beta merge needs an even row count, got %lld",
+                                                  (long long)a->n_rows);
+  if (a->dk < 1 || a->dv < 1 || a->dk > logkv::kMaxDim || a->dv > logkv::kMaxDim)
+    return fail(LOGKV_EINVAL, "Beta merge widths must be in [1, %d], got %d/%d", logkv::kMaxDim, a->dk, a->dv);
+  if (a->k_st < a->dk || a->v_st < a->dv) return fail(LOGKV_EINVAL, "Beta merge row strides below the widths");
+  if (a->n_groups < 0 || a->n_groups > a->n_rows / 2 + 1)
+    return fail(LOGKV_EINVAL, "Beta merge layout of %lld groups for %lld rows", (long long)a->n_groups,
+                (long long)a->n_rows);
+  if (a->n_groups == 0) return LOGKV_OK;
+  if (!a->k || !a->v || !a->w || !a->layout || !a->cuts)
+    return fail(LOGKV_EINVAL, "Beta merge rows, masses, layout or cuts are NULL");
+  if (a->out_k && (!a->out_v || !a->out_w)) return fail(LOGKV_EINVAL, "Beta merge outputs K, V and w go together");
+  if (a->apply && !a->out_k) return fail(LOGKV_EINVAL, "applying recorded cuts needs the outputs");
+  const int rc = logkv::launch_beta_merge(*a, status, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "Beta merge launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_pack_slots(const logkv_slot_pack_args* a, void* stream) {
+  if (!a) return fail(LOGKV_EINVAL, "slot pack args are NULL");
+  if (a->n_batch < 1 || a->n_groups < 1 || a->slots < 0 || a->slots > a->out_cap)
+    return fail(LOGKV_EINVAL, "slot pack shape: batch %d, groups %d, %d slots into %d rows", a->n_batch,
+                a->n_groups, a->slots, a->out_cap);
+  if (a->dk < 4 || a->dv < 4 || a->dk % 4 || a->dv % 4 || a->dim % 8 || a->dim <= a->dk || a->dim < a->dv ||
+      a->dim > 264)
+    return fail(LOGKV_EINVAL, "slot pack widths dk %d, dv %d, dim %d", a->dk, a->dv, a->dim);
+  if (a->s_m < 0 || a->s_m > a->slots || a->s_valid < 0 || a->s_valid > a->slots)
+    return fail(LOGKV_EINVAL, "slot pack prefix lengths out of range");
+  if (a->slots && (!a->k || !a->v || !a->w || !a->out_k || !a->out_v || (a->s_m && !a->m) ||
+                   (a->s_valid && !a->valid)))
+    return fail(LOGKV_EINVAL, "slot pack buffer is NULL");
+  if (reinterpret_cast<uintptr_t>(a->out_k) % 8 || reinterpret_cast<uintptr_t>(a->out_v) % 8)
+    return fail(LOGKV_EINVAL, "packed rows must be 8-byte aligned");
+  const int rc = logkv::launch_slot_pack(*a, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "slot pack launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"

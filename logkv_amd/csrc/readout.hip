@@ -280,6 +280,24 @@ __global__ __launch_bounds__(256) void pack_kernel(logkv_readout_view c, logkv_p
       }
     }
     src[tid] = r;
+    if (p.out_w && (r.flags & 4)) {
+      // Per-row mass and validity of the packed rows (an attention state's slot_w /
+      // slot_valid): a pooled slot's stored mass (0 for padding), 1 or 0 for an
+      // exact row by its flag, 1 for recent and current rows.
+      float w_out = 1.f;
+      if (s < width) {
+        w_out = 0.f;
+        if (r.flags & 1) {
+          const int64_t phys = (r.k - gp(c.level_k)) / dk;
+          w_out = gp(c.level_w)[phys];
+        }
+      } else if (s < width + alpha_count) {
+        w_out = (r.flags & 1) ? 1.f : 0.f;
+      }
+      const int64_t o = static_cast<int64_t>(lane) * p.out_cap + s;
+      gp(p.out_w)[o] = w_out;
+      if (p.out_valid) gp(p.out_valid)[o] = static_cast<uint8_t>(r.flags & 1);
+    }
   }
   __syncthreads();
   const int units = p.dim / 4;   // per K row and per V row
@@ -632,7 +650,72 @@ __global__ __launch_bounds__(256) void combine_kernel(logkv_attention_args a, co
   }
 }
 
+// Packed rows [B, G, S, dim] of unpacked attention slots (log_kv_slot_attention's
+// inputs, litgpt/log_kv_cache.py:6439-6464): keys and values copied (bf16 bits),
+// column dk the mass bias lam * log(w) - or, for the first s_m slots when
+// anchor counts are given, -log(max(M, 1)) + lam * log(max(w, 1))
+// (litgpt/log_kv_position.py:128-133) - rounded to bf16; the first s_valid
+// slots with a false valid flag become all-zero rows with bias -10000. One
+// thread per (row, 4-feature unit) of K, then of V.
+__global__ __launch_bounds__(256) void slot_pack_kernel(logkv_slot_pack_args a) {
+  const int units = a.dim / 4;
+  const int64_t lane = blockIdx.y;
+  const int b = static_cast<int>(lane / a.n_groups), g = static_cast<int>(lane % a.n_groups);
+  const int64_t items = static_cast<int64_t>(a.slots) * 2 * units;
+  for (int64_t it = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; it < items;
+       it += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int s = static_cast<int>(it / (2 * units)), u = static_cast<int>(it % (2 * units));
+    const bool valid = s >= a.s_valid || gp(a.valid)[b * a.valid_sb + g * a.valid_sg + s] != 0;
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+    if (u < units) {
+      const int d0 = 4 * u;
+      const LOGKV_G uint16_t* row = gp(a.k) + b * a.k_sb + g * a.k_sg + static_cast<int64_t>(s) * a.k_st;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = d0 + q;
+        if (d < a.dk) {
+          o[q] = valid ? row[d] : 0u;
+        } else if (d == a.dk) {
+          float bias = -10000.f;
+          if (valid) {
+            const float w = gp(a.w)[b * a.w_sb + g * a.w_sg + s];
+            if (s < a.s_m) {
+              const float m = static_cast<float>(gp(a.m)[b * a.m_sb + g * a.m_sg + s]);
+              bias = -logf(m > 1.f ? m : 1.f);
+              if (a.lam != 0.f) bias = bias + a.lam * logf(w > 1.f ? w : 1.f);
+            } else {
+              bias = a.lam != 0.f ? a.lam * logf(w) : 0.f;
+            }
+          }
+          o[q] = f32_to_bf16(bias);
+        }
+      }
+      const int64_t orow = (lane * a.out_cap + s) * a.dim;
+      *reinterpret_cast<LOGKV_G uint2*>(gp(a.out_k) + orow + d0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    } else {
+      const int d0 = 4 * (u - units);
+      const LOGKV_G uint16_t* row = gp(a.v) + b * a.v_sb + g * a.v_sg + static_cast<int64_t>(s) * a.v_st;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = d0 + q;
+        o[q] = valid && d < a.dv ? row[d] : 0u;
+      }
+      const int64_t orow = (lane * a.out_cap + s) * a.dim;
+      *reinterpret_cast<LOGKV_G uint2*>(gp(a.out_v) + orow + d0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    }
+  }
+}
+
 }  // namespace
+
+int launch_slot_pack(const logkv_slot_pack_args& a, hipStream_t stream) {
+  const int64_t items = static_cast<int64_t>(a.slots) * 2 * (a.dim / 4);
+  if (items == 0) return LOGKV_OK;
+  const int64_t blocks = std::min<int64_t>((items + 255) / 256, 4096);
+  hipLaunchKernelGGL(slot_pack_kernel, dim3(static_cast<unsigned>(blocks), a.n_batch * a.n_groups), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
 
 int launch_plan(const logkv_readout_view& c, int32_t* table, hipStream_t stream) {
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, c, table);

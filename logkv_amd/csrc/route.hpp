@@ -75,6 +75,8 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
 int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream);
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   hipStream_t stream);
+int launch_beta_merge(const logkv_beta_args& a, int32_t* status, hipStream_t stream);
+int launch_slot_pack(const logkv_slot_pack_args& a, hipStream_t stream);
 int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   int64_t cursor, int32_t* status, hipStream_t stream);
 

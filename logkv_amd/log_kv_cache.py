@@ -19,12 +19,29 @@ from __future__ import annotations
 import contextlib
 import ctypes as C
 import math
+from typing import NamedTuple
 
 import torch
 import torch.nn as nn
 
 from . import _lib
 from ._lib import LadderView, RouteParams, RowsView, check, lib, ptr, require_device, stream_of
+
+
+class CacheAttentionState(NamedTuple):
+    """Unpacked attention slots of a cache (litgpt/log_kv_cache.py:151-161): keys, values and masses
+    ``[B, G, S(, d)]``, validity and anchor counts of the pooled (+ exact) prefix, and the rank-1
+    statistics (always None here: first-order entries only)."""
+    slot_k: torch.Tensor
+    slot_v: torch.Tensor
+    slot_w: torch.Tensor
+    slot_valid: torch.Tensor | None = None
+    M_s: torch.Tensor | None = None
+    slot_sigma_u: torch.Tensor | None = None
+    slot_sigma2: torch.Tensor | None = None
+    slot_gamma_a: torch.Tensor | None = None
+    slot_gamma_b: torch.Tensor | None = None
+    slot_gamma: torch.Tensor | None = None
 
 
 def ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, K, exact_tokens, element):
@@ -798,6 +815,24 @@ class LogStructuredKVCache(nn.Module):
         """Mid-anchor plan (litgpt/log_kv_cache.py:5955-5958); the only anchor mode built."""
         return self._semantic_mid_attention_plan()
 
+    def get_attention_state(self, with_stats: bool = False, *, plan=None) -> CacheAttentionState:
+        """Unpacked slots for ``log_kv_slot_attention`` (litgpt/log_kv_cache.py:6116-6120): pooled slots in
+        plan order, the exact pool, the recent window. Entries are first order, so ``with_stats`` yields
+        no statistics (as the reference does without second-order storage)."""
+        from .log_kv_pack import attention_state
+        return attention_state(self, self._semantic_attention_plan() if plan is None else plan)
+
+    def _semantic_attention_state(self, with_stats: bool = False, plan=None) -> CacheAttentionState:
+        return self.get_attention_state(with_stats, plan=plan)
+
+    def _convert_dtype(self, dtype: torch.dtype) -> None:
+        """Reconcile the data buffers with the activation dtype (litgpt/log_kv_cache.py:6236-6268): a
+        no-op when they match. The HIP kernels store and read bfloat16 entries only, so another
+        activation dtype raises instead of converting the buffers."""
+        if self.recent_k.dtype == dtype:
+            return
+        raise NotImplementedError(f"logkv_amd caches hold bfloat16 entries; activations are {dtype}")
+
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand
     # ------------------------------------------------------------------
@@ -857,3 +892,21 @@ class LogStructuredKVCache(nn.Module):
     def second_order(self, value: bool) -> None:
         if value:
             raise RuntimeError("Second-order storage is disabled; rebuild the cache with allocate_second_order=True")
+
+
+def append_exact_tokens(state, k_new, v_new):
+    """Exact entries appended after a state's slots (litgpt/log_kv_cache.py:6391-6425)."""
+    from .log_kv_pack import append_exact_tokens as _append
+    return _append(state, k_new, v_new)
+
+
+def log_kv_slot_attention(*args, **kwargs):
+    """Slot attention over unpacked slots (litgpt/log_kv_cache.py:6501-6721); see log_kv_pack."""
+    from .log_kv_pack import log_kv_slot_attention as _attend
+    return _attend(*args, **kwargs)
+
+
+def log_kv_chunk_attention(*args, **kwargs):
+    """One streaming attention step over [cache | chunk] (litgpt/log_kv_cache.py:6802-6836); see log_kv_pack."""
+    from .log_kv_pack import log_kv_chunk_attention as _chunk
+    return _chunk(*args, **kwargs)

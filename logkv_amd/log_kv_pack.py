@@ -22,10 +22,11 @@ a slot is ``scale * q.k + log w`` (litgpt/log_kv_cache.py:6428-6464).
 from __future__ import annotations
 
 import ctypes as C
+import math
 
 import torch
 
-from ._lib import AttentionArgs, PackArgs, ReadoutView, check, lib, ptr, stream_of
+from ._lib import AttentionArgs, PackArgs, ReadoutView, SlotPackArgs, check, lib, ptr, require_device, stream_of
 
 _BACKENDS = ("auto", "triton", "hip")
 
@@ -118,11 +119,12 @@ def _check_kv(cache, k, v):
         raise ValueError("K/V shape, device and dtype must match the cache")
 
 
-def _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, recent_start):
+def _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, recent_start, out_w=None, out_valid=None):
     """Pack into ``ka / va``; with ``skip_pooled`` only the rows from recent window row
-    ``recent_start`` on (the exact pool's row count is read on the device)."""
+    ``recent_start`` on (the exact pool's row count is read on the device). ``out_w`` /
+    ``out_valid`` (float / uint8 ``[Bt, G, cap]``) also receive each row's mass and validity."""
     args = PackArgs(ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], k.size(2), ptr(ka), ptr(va), ka.size(2), dim,
-                    1 if skip_pooled else 0, recent_start)
+                    1 if skip_pooled else 0, recent_start, ptr(out_w), ptr(out_valid))
     if k.stride(3) != 1 or v.stride(3) != 1:
         raise ValueError("current K/V rows must be contiguous in the feature dimension")
     check(lib().logkv_pack(C.byref(view), C.byref(args), ptr(plan.table), stream_of(k.device)), "logkv_pack")
@@ -263,3 +265,124 @@ def log_kv_chunk_attention(cache, q_b, k_b, v_b, scale, second_order_scale=1.0, 
     if reuse:
         cache._mid_decode_state = (key, plan, buffers, cache.recent_count, workspace)
     return out
+
+
+def attention_state(cache, plan):
+    """The cache's attention state as unpacked slots (litgpt/log_kv_cache.py:6009-6114, first order):
+    ``slot_k`` the pooled keys RoPE'd at their mid anchors, the exact pool's keys RoPE'd at their
+    positions and the recent window's keys, ``slot_v`` the values, ``slot_w`` the pooled masses (1 for
+    exact valid and recent rows), ``slot_valid`` over [pooled | exact] and ``M_s`` ones. Built by one
+    pack launch that also writes every row's mass and validity; rows that are masked (pooled padding,
+    invalid exact rows) are zero."""
+    from .log_kv_cache import CacheAttentionState
+
+    B, G, dk, dv = cache.batch_size, cache.n_groups, cache.k_dim, cache.v_dim
+    dev = cache.level_k.device
+    width, exact, recent = plan.width, cache.alpha_count, cache.recent_count
+    rows = width + exact + recent
+    dim = packed_dim(dk, dv)
+    ka = torch.empty(B, G, max(rows, 1), dim, dtype=cache.level_k.dtype, device=dev)
+    va = torch.empty_like(ka)
+    w = torch.empty(B, G, max(rows, 1), dtype=torch.float32, device=dev)
+    valid = torch.empty(B, G, max(rows, 1), dtype=torch.uint8, device=dev)
+    empty = torch.empty(B, G, 0, dk, dtype=cache.level_k.dtype, device=dev)
+    if rows:
+        _launch_pack(cache, readout_view(cache), plan, empty, empty, dim, ka, va, False, 0, w, valid)
+    slot_valid = valid[:, :, :width + exact].bool()
+    return CacheAttentionState(ka[:, :, :rows, :dk], va[:, :, :rows, :dv], w[:, :, :rows], slot_valid=slot_valid,
+                               M_s=torch.ones(B, G, width + exact, dtype=torch.int64, device=dev))
+
+
+def append_exact_tokens(state, k_new, v_new):
+    """The state with exact entries (mass 1) appended after its slots (litgpt/log_kv_cache.py:6391-6425):
+    the in-flight chunk attends before it is committed. ``slot_valid`` / ``M_s`` cover the prefix only and
+    pass through; appended entries get zero rank-1 statistics when the state carries them."""
+    stats = (state.slot_sigma_u, state.slot_sigma2, state.slot_gamma_a, state.slot_gamma_b, state.slot_gamma)
+    have = [x is not None for x in stats]
+    if any(have) and not all(have):
+        raise ValueError("append_exact_tokens() requires either all rank-1 stats or none")
+    n = k_new.size(2)
+    mass = state.slot_w.new_ones(state.slot_w.size(0), state.slot_w.size(1), n)
+    grown = state._replace(slot_k=torch.cat([state.slot_k, k_new], dim=2), slot_v=torch.cat([state.slot_v, v_new], dim=2),
+                           slot_w=torch.cat([state.slot_w, mass], dim=-1))
+    if not all(have):
+        return grown
+    zero_row = mass.new_zeros(mass.shape)
+    return grown._replace(
+        slot_sigma_u=torch.cat([state.slot_sigma_u, torch.zeros_like(k_new)], dim=2),
+        slot_sigma2=torch.cat([state.slot_sigma2, zero_row], dim=-1),
+        slot_gamma_a=torch.cat([state.slot_gamma_a, torch.zeros_like(k_new)], dim=2),
+        slot_gamma_b=torch.cat([state.slot_gamma_b, torch.zeros_like(v_new)], dim=2),
+        slot_gamma=torch.cat([state.slot_gamma, zero_row], dim=-1))
+
+
+def _slot_rows_visible(slot_valid, slots, tq, causal_tail):
+    """Whether every query row keeps at least one visible valid slot (host check)."""
+    s_valid = slot_valid.size(-1)
+    if s_valid < slots - causal_tail or (causal_tail and s_valid < slots):
+        return True   # an always-valid slot past the prefix is visible to every query
+    dev = slot_valid.device
+    cols = torch.arange(slots, device=dev)
+    rows = torch.arange(tq, device=dev)
+    visible = torch.ones(tq, slots, dtype=torch.bool, device=dev)
+    if causal_tail:
+        visible = (cols[None, :] < slots - causal_tail) | (cols[None, :] - (slots - causal_tail) <= rows[:, None])
+    valid = torch.ones(*slot_valid.shape[:2], slots, dtype=torch.bool, device=dev)
+    valid[..., :s_valid] = slot_valid
+    return bool((valid[:, :, None, :] & visible).any(-1).all())
+
+
+def log_kv_slot_attention(q, slot_k, slot_v, slot_w, scale, mask=None, lam=1.0, causal_tail=0, slot_M=None,
+                          slot_valid=None, check_valid=True, slot_sigma_u=None, slot_sigma2=None, slot_gamma_a=None,
+                          slot_gamma_b=None, slot_gamma=None, second_order_scale=1.0):
+    """First-order slot attention ``softmax(scale * q.k_s + lam * log w_s - log M_s) . v_s`` over unpacked
+    slots (litgpt/log_kv_cache.py:6501-6721), evaluated as the reference's Flash path does: each slot's
+    bias rides in an extra key coordinate (rounded to bf16) against ``1/scale`` in the query, invalid
+    slots carry -10000. The slots are packed on the device (``logkv_pack_slots``) and read by the
+    decode / matrix-core attention kernels. ``q [B, nh, T_q, dk]``, slots ``[B, G, S, .]``; the last
+    ``causal_tail`` slots are the in-flight chunk, causal against the queries."""
+    B, nh, tq, dk = q.shape
+    S = slot_k.size(2)
+    if S == 0:
+        return torch.zeros(B, nh, tq, slot_v.size(-1), device=q.device, dtype=q.dtype)
+    stats = (slot_sigma_u, slot_sigma2, slot_gamma_a, slot_gamma_b, slot_gamma)
+    if slot_sigma_u is not None and any(x is None for x in stats):
+        raise ValueError("log_kv_slot_attention() requires either all rank-1 stats or none")
+    if causal_tail:
+        if mask is not None:
+            raise ValueError("causal_tail and mask are mutually exclusive")
+        if causal_tail != tq:
+            raise ValueError(f"causal_tail ({causal_tail}) must equal T_q ({tq}): the tail entries are the "
+                             "appended in-flight chunk, aligned one-to-one with the queries")
+    if slot_sigma_u is not None and second_order_scale != 0.0:
+        raise NotImplementedError("logkv_amd reads out first-order slots only (no rank-1 statistics)")
+    if mask is not None:
+        raise NotImplementedError("logkv_amd masks through causal_tail and slot_valid, not a (T_q, S) mask")
+    if q.dtype != torch.bfloat16 or slot_k.dtype != torch.bfloat16 or slot_v.dtype != torch.bfloat16:
+        raise NotImplementedError("logkv_amd slot attention takes bfloat16 queries and slots")
+    if not math.isfinite(scale) or not 1e-3 <= scale <= 1.0:
+        raise NotImplementedError("attention scale must lie in [1e-3, 1]")
+    G = slot_k.size(1)
+    if nh % G or slot_k.shape[:3] != (B, G, S) or slot_v.shape[:3] != (B, G, S) or slot_w.shape != (B, G, S) \
+            or slot_k.size(-1) != dk:
+        raise ValueError("slots must be [B, G, S, d] with G dividing the query heads and masses [B, G, S]")
+    for t, what in ((q, "q"), (slot_k, "slot_k"), (slot_v, "slot_v"), (slot_w, "slot_w")):
+        require_device(t, what)
+    if slot_valid is not None and check_valid and not _slot_rows_visible(slot_valid, S, tq, causal_tail):
+        raise ValueError("log_kv_slot_attention(): a query row has no valid slot")
+    dv = slot_v.size(-1)
+    dim = packed_dim(dk, dv)
+    ka = q.new_empty(B, G, S, dim)
+    va = q.new_empty(B, G, S, dim)
+    w = slot_w.float()
+    if slot_k.stride(-1) != 1 or slot_v.stride(-1) != 1:
+        raise ValueError("slot keys and values need contiguous features")
+    m = None if slot_M is None else slot_M.to(torch.int64)
+    valid = None if slot_valid is None else slot_valid.to(torch.uint8)
+    args = SlotPackArgs(ptr(slot_k), *slot_k.stride()[:3], ptr(slot_v), *slot_v.stride()[:3], ptr(w), *w.stride()[:2],
+                        ptr(m), *(m.stride()[:2] if m is not None else (0, 0)), 0 if m is None else m.size(-1),
+                        ptr(valid), *(valid.stride()[:2] if valid is not None else (0, 0)),
+                        0 if valid is None else valid.size(-1), float(lam), B, G, S, dk, dv, dim, S, ptr(ka), ptr(va))
+    check(lib().logkv_pack_slots(C.byref(args), stream_of(q.device)), "logkv_pack_slots")
+    plan = MidAttentionPlan(torch.zeros(1, dtype=torch.int32, device=q.device), 0, 0)
+    return packed_attention(q, ka, va, plan, S, scale, causal_tail, dv, G)[0]

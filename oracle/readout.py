@@ -141,3 +141,32 @@ def attention(q, ka, va, scale, causal_tail, dv):
     p = np.exp(scores)
     p /= p.sum(axis=-1, keepdims=True)
     return np.einsum("bhqs,bhsd->bhqd", p, vv)[..., :dv]
+
+
+def slot_pack(slot_k, slot_v, slot_w, lam=1.0, slot_M=None, slot_valid=None):
+    """Packed rows of unpacked slots, the Flash encoding of log_kv_slot_attention
+    (litgpt/log_kv_cache.py:6418-6464, anchor_mass_bias litgpt/log_kv_position.py:128-133):
+    keys and values copied, column Dk = ``lam * log(w)`` (0 when ``lam == 0``), or for the first
+    ``slot_M`` columns ``-log(max(M, 1)) + lam * log(max(w, 1))``, in float32 and rounded to
+    bf16; among the first ``slot_valid`` columns, invalid slots are zero rows with bias -10000."""
+    slot_k, slot_v, w = f32(slot_k), f32(slot_v), f32(slot_w)
+    n_batch, n_groups, S, dk = slot_k.shape
+    dv = slot_v.shape[-1]
+    dim = packed_dim(dk, dv)
+    ka = np.zeros((n_batch, n_groups, S, dim), np.float32)
+    va = np.zeros_like(ka)
+    with np.errstate(divide="ignore"):
+        bias = (np.float32(lam) * np.log(w)).astype(np.float32) if lam != 0.0 else np.zeros_like(w)
+        if slot_M is not None:
+            s_m = slot_M.shape[-1]
+            m = -np.log(np.maximum(np.asarray(slot_M, np.float32), np.float32(1.0))).astype(np.float32)
+            if lam != 0.0:
+                m = (m + np.float32(lam) * np.log(np.maximum(w[..., :s_m], np.float32(1.0)))).astype(np.float32)
+            bias[..., :s_m] = m
+    valid = np.ones((n_batch, n_groups, S), bool)
+    if slot_valid is not None:
+        valid[..., :slot_valid.shape[-1]] = np.asarray(slot_valid, bool)
+    ka[..., :dk] = np.where(valid[..., None], slot_k, 0)
+    va[..., :dv] = np.where(valid[..., None], slot_v, 0)
+    ka[..., dk] = np.where(valid, bf16_round(bias), bf16_round(np.float32(-10000.0)))
+    return ka, va

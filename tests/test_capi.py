@@ -59,6 +59,7 @@ STRUCTS = {
     "logkv_partition_args": _lib.PartitionArgs, "logkv_readout_view": _lib.ReadoutView,
     "logkv_pack_args": _lib.PackArgs, "logkv_attention_args": _lib.AttentionArgs,
     "logkv_alpha_select_args": _lib.AlphaSelectArgs, "logkv_op_log_view": _lib.OpLogView,
+    "logkv_beta_args": _lib.BetaArgs, "logkv_slot_pack_args": _lib.SlotPackArgs,
 }
 
 

@@ -125,3 +125,49 @@ def test_masked_softmax_with_causal_tail():
             p /= p.sum()
             want = p @ va[0, 0, visible, :dv].astype(np.float64)
             np.testing.assert_allclose(got[0, h, i], want, rtol=1e-12, atol=1e-12)
+
+
+def test_slot_encoding_equals_pack_of_the_materialized_state():
+    """The reference packs a cache two ways that must agree on every visible row: the mid fast path
+    (log(max(w, 1)) pooled, 0 exact / recent, -10000 invalid; litgpt/log_kv_pack.py:27-72) and the slot
+    encoding of log_kv_slot_attention over the materialized state (lam*log(w), slot_valid;
+    litgpt/log_kv_cache.py:6418-6464). Masses of valid pooled slots are integers >= 1."""
+    rng = np.random.default_rng(12)
+    Bt, G, K, L, B, dk, dv, P, R = 2, 2, 3, 3, 4, 16, 16, 5, 3
+    s = empty_state(Bt, G, K, L, B, dk, dv, P=P, recent=R)
+    s.level_count[:] = rng.integers(0, B + 1, size=s.level_count.shape)
+    s.level_w[:] = rng.integers(0, 9, size=s.level_w.shape)          # some zero masses: invalid slots
+    s.level_sum_wp[:] = s.level_w.astype(np.int64) * rng.integers(0, 500, size=s.level_w.shape)
+    s.level_k[:] = bf16_round(rng.standard_normal(s.level_k.shape))
+    s.level_v[:] = bf16_round(rng.standard_normal(s.level_v.shape))
+    s.alpha_k_raw[:] = bf16_round(rng.standard_normal(s.alpha_k_raw.shape))
+    s.alpha_v[:] = bf16_round(rng.standard_normal(s.alpha_v.shape))
+    s.alpha_pos[:] = rng.integers(0, 500, size=s.alpha_pos.shape)
+    s.alpha_valid[:] = rng.random(s.alpha_valid.shape) < 0.7
+    s.alpha_count = P
+    s.recent_k[:] = bf16_round(rng.standard_normal(s.recent_k.shape))
+    s.recent_v[:] = bf16_round(rng.standard_normal(s.recent_v.shape))
+    s.recent_count = R
+    cos = rng.standard_normal((512, dk)).astype(np.float32)
+    sin = rng.standard_normal((512, dk)).astype(np.float32)
+    ka, va = ro.pack(s, None, None, cos, sin)
+    idx, _, valid = ro.mid_plan(s.level_count, s.level_w, s.level_sum_wp)
+    w_pooled = np.take_along_axis(s.level_w.reshape(Bt, G, -1), idx, axis=2)
+    ev = np.broadcast_to(s.alpha_valid[:, None, :P], (Bt, G, P))
+    slot_w = np.concatenate([np.where(valid, w_pooled, 1.0), ev.astype(np.float32),
+                             np.ones((Bt, G, R), np.float32)], axis=-1)
+    slot_valid = np.concatenate([valid, ev], axis=-1)
+    sk, sv = ro.slot_pack(ka[..., :dk], va[..., :dv], slot_w, slot_valid=slot_valid)
+    np.testing.assert_array_equal(sk, ka)
+    np.testing.assert_array_equal(sv, va)
+
+
+def test_slot_encoding_anchor_counts_and_lam():
+    # M-expanded slots lose log(M) of mass whatever lam is (litgpt/log_kv_position.py:128-133).
+    k = np.zeros((1, 1, 3, 8), np.float32)
+    w = np.array([[[4.0, 0.5, 2.0]]], np.float32)
+    ka, _ = ro.slot_pack(k, k, w, lam=0.0, slot_M=np.array([[[2, 0]]]))
+    assert ka[0, 0, :, 8].tolist() == [bf16_round(np.float32(-np.log(2.0))).item(), 0.0, 0.0]
+    ka, _ = ro.slot_pack(k, k, w, lam=1.0, slot_M=np.array([[[2, 0]]]))
+    expect = [-np.log(np.float32(2)) + np.log(np.float32(4)), np.log(np.float32(1)), np.log(np.float32(2))]
+    assert np.allclose(ka[0, 0, :, 8], bf16_round(np.asarray(expect, np.float32)))
