@@ -439,6 +439,33 @@ int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* args);
 int logkv_chunk_attention(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
                           void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Gradient of that attention (matrix cores): given dout [n_batch, n_heads, tq, dv]
+ * (bf16, strided) and the forward's output in args->out, writes dq
+ * [n_batch, n_heads, tq, dk] (bf16, strided; the bias coordinate has no gradient)
+ * and, for the last grad_rows packed rows of each lane (the in-flight chunk of a
+ * training block, or every slot), dk [n_batch, G, grad_rows, dk] and dv
+ * [n_batch, G, grad_rows, dv] (bf16, contiguous). grad_rows <= tail. dk a multiple
+ * of 8 up to 128, dv in {32, 64, 96, 128}, packed width up to 144. The workspace
+ * (logkv_chunk_backward_workspace_bytes) holds each query's log-sum-exp and
+ * dout . out between the two launches.
+ * Replaces the autograd backward of the Flash SDPA call on the packed workspace
+ * (litgpt/log_kv_cache.py:6751-6758) that LogKVStreamTrainingAttention.backward
+ * runs per block (litgpt/log_kv_cache.py:7032-7098). */
+typedef struct logkv_attention_grad_args {
+  const uint16_t* dout;
+  int64_t do_sb, do_sh, do_st;
+  uint16_t* dq;
+  int64_t dq_sb, dq_sh, dq_st;
+  uint16_t* dk;
+  uint16_t* dv;
+  int32_t grad_rows;
+} logkv_attention_grad_args;
+
+int64_t logkv_chunk_backward_workspace_bytes(const logkv_attention_args* args);
+int logkv_chunk_attention_backward(const logkv_attention_args* args, const int32_t* table, int64_t table_ints,
+                                   const logkv_attention_grad_args* grads, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
+
 /* Beta 4->2 compaction of a block of n_rows entries (rows of each field
  * contiguous per row, K / V bf16 or float32 with row strides k_st / v_st in
  * elements): each layout row (start, width, out_start) of n_groups int64

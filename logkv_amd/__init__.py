@@ -5,7 +5,8 @@ litgpt/alpha_log_kv.py, litgpt/beta_log_kv.py, litgpt/log_kv_pack.py);
 compute runs in liblogkv_hip.so through the C ABI in include/logkv_hip.h.
 """
 
-from .log_kv_cache import CacheAttentionState, LogStructuredKVCache, ladder_budget  # noqa: F401
+from .log_kv_cache import (CacheAttentionState, LogKVStreamTrainingAttention, LogStructuredKVCache,  # noqa: F401
+                           ladder_budget)
 from .log_kv_pack import (append_exact_tokens, log_kv_chunk_attention, log_kv_slot_attention,  # noqa: F401
                           pack_mid_kv, packed_dim)
 from . import beta_log_kv  # noqa: F401

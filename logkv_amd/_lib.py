@@ -138,6 +138,14 @@ class BetaArgs(C.Structure):
     ]
 
 
+class AttentionGradArgs(C.Structure):
+    _fields_ = [
+        ("dout", _p), ("do_sb", _i64), ("do_sh", _i64), ("do_st", _i64),
+        ("dq", _p), ("dq_sb", _i64), ("dq_sh", _i64), ("dq_st", _i64),
+        ("dk", _p), ("dv", _p), ("grad_rows", _i32),
+    ]
+
+
 class OpLogView(C.Structure):
     _fields_ = [("rows", _p), ("lengths", _p), ("capacity", _i64)]
 
@@ -187,6 +195,9 @@ SIGNATURES = {
     "logkv_decode_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
     "logkv_decode_attention_static": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p]),
     "logkv_beta_merge": (_i32, [C.POINTER(BetaArgs), _p, _p]),
+    "logkv_chunk_backward_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
+    "logkv_chunk_attention_backward": (_i32, [C.POINTER(AttentionArgs), _p, _i64, C.POINTER(AttentionGradArgs), _p,
+                                              _i64, _p]),
     "logkv_chunk_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
     "logkv_chunk_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
 }

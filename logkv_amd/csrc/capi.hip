@@ -602,4 +602,37 @@ int logkv_pack_slots(const logkv_slot_pack_args* a, void* stream) {
   return LOGKV_OK;
 }
 
+int64_t logkv_chunk_backward_workspace_bytes(const logkv_attention_args* a) {
+  if (!a || a->n_groups < 1 || a->n_heads % a->n_groups) return -1;
+  return logkv::chunk_backward_workspace_floats(*a) * 4;
+}
+
+int logkv_chunk_attention_backward(const logkv_attention_args* a, const int32_t* table, int64_t table_ints,
+                                   const logkv_attention_grad_args* gr, void* ws, int64_t ws_bytes, void* stream) {
+  if (!a || !gr || !table || table_ints < 1) return fail(LOGKV_EINVAL, "attention backward args or plan table are NULL");
+  if (a->n_batch < 1 || a->n_groups < 1 || a->n_heads % a->n_groups || a->tq < 1)
+    return fail(LOGKV_EINVAL, "attention backward shape: batch %d, heads %d, groups %d, tq %d", a->n_batch,
+                a->n_heads, a->n_groups, a->tq);
+  if (a->dk < 8 || a->dk % 8 || a->dk > 128 || a->dv % 32 || a->dv < 32 || a->dv > 128 || a->dim % 8 ||
+      a->dim > 144 || a->dim <= a->dk || a->dim < a->dv)
+    return fail(LOGKV_EINVAL, "attention backward takes dk a multiple of 8 up to 128, dv in {32, 64, 96, 128} and "
+                "packed widths up to 144; got %d/%d/%d", a->dk, a->dv, a->dim);
+  if (a->cap < 1 || a->tail < 0 || a->tail > a->cap || a->causal_tail < 0 || a->causal_tail > a->tail ||
+      (a->causal_tail && a->causal_tail != a->tq))
+    return fail(LOGKV_EINVAL, "attention backward rows: cap %d, tail %d, causal_tail %d", a->cap, a->tail,
+                a->causal_tail);
+  if (gr->grad_rows < 0 || gr->grad_rows > a->tail)
+    return fail(LOGKV_EINVAL, "gradient rows %d outside [0, tail %d]", gr->grad_rows, a->tail);
+  if (!a->q || !a->k || !a->v || !a->out || !gr->dout || !gr->dq || (gr->grad_rows && (!gr->dk || !gr->dv)))
+    return fail(LOGKV_EINVAL, "attention backward buffer is NULL");
+  if (reinterpret_cast<uintptr_t>(a->k) % 16 || reinterpret_cast<uintptr_t>(a->v) % 16)
+    return fail(LOGKV_EINVAL, "packed K/V must be 16-byte aligned");
+  if (!ws || ws_bytes < logkv::chunk_backward_workspace_floats(*a) * 4)
+    return fail(LOGKV_EINVAL, "attention backward workspace too small");
+  const int rc = logkv::launch_chunk_backward(*a, table + table_ints - 1, *gr, static_cast<float*>(ws),
+                                              static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "attention backward launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 }  // extern "C"

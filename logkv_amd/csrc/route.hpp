@@ -77,6 +77,9 @@ int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, c
                   hipStream_t stream);
 int launch_beta_merge(const logkv_beta_args& a, int32_t* status, hipStream_t stream);
 int launch_slot_pack(const logkv_slot_pack_args& a, hipStream_t stream);
+int64_t chunk_backward_workspace_floats(const logkv_attention_args& a);
+int launch_chunk_backward(const logkv_attention_args& a, const int32_t* width, const logkv_attention_grad_args& g,
+                          float* stats, hipStream_t stream);
 int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   int64_t cursor, int32_t* status, hipStream_t stream);
 

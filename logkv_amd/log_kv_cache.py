@@ -910,3 +910,94 @@ def log_kv_chunk_attention(*args, **kwargs):
     """One streaming attention step over [cache | chunk] (litgpt/log_kv_cache.py:6802-6836); see log_kv_pack."""
     from .log_kv_pack import log_kv_chunk_attention as _chunk
     return _chunk(*args, **kwargs)
+
+
+class LogKVStreamTrainingAttention(torch.autograd.Function):
+    """Streaming training attention with memory independent of T * S (litgpt/log_kv_cache.py:6867-7098).
+
+    Forward streams the sequence in ``train_block`` blocks with no recorded graph: each block's queries
+    attend to the cache state at the block's start plus the block causally, then the block is committed
+    while the route decisions are recorded (the op-log, and with ``semantic_replay_updates`` the update
+    tape: rows, attach decisions, Alpha selections). Backward resets the cache and replays the same
+    flushes from the records - no re-routing, no re-selection - recomputing each block's attention with
+    a gradient (the matrix-core backward kernels) on exactly the state forward attended over. Gradients
+    reach q, k and v through each token's own block only (the cache commits detached copies).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, cache, scale, train_block, second_order_scale, k_raw=None, span_ends=None):
+        commit_k_raw = k if k_raw is None else k_raw
+        ctx.input_count = len(ctx.needs_input_grad)
+        ctx.span_ends = None if span_ends is None else tuple(tuple(bool(x) for x in row) for row in span_ends)
+        if cache.alpha_exact_tokens and (not cache.semantic_replay_updates or second_order_scale != 0.0):
+            raise ValueError("AlphaLogKV training requires semantic_replay_updates and second_order_scale=0")
+        if cache.semantic_unified_route:
+            raise NotImplementedError("training replay of the unified route is not built (no op-log recording)")
+        T = q.size(2)
+        train_block = int(train_block)
+        if train_block < 2:
+            raise ValueError(f"logKV train_block must be >= 2, got {train_block}")
+        if train_block > cache.recent_size:
+            raise ValueError(f"logKV train_block ({train_block}) must be <= recent_size ({cache.recent_size})")
+        updates = _SemanticReplayUpdates() if cache.semantic_replay_updates else None
+        outputs, plans = [], []
+        with torch.no_grad():
+            if updates is not None:
+                updates.wait(q.device)
+            cache.reset_parameters()
+            cache.begin_op_log()
+            for start in range(0, T, train_block):
+                end = min(start + train_block, T)
+                plan = cache._semantic_attention_plan()
+                plans.append(plan)
+                outputs.append(log_kv_chunk_attention(cache, q[:, :, start:end], k[:, :, start:end],
+                                                      v[:, :, start:end], scale, second_order_scale,
+                                                      attention_plan=plan))
+                with cache._semantic_update_context(updates):
+                    cache.add_recent(k[:, :, start:end], v[:, :, start:end], k_raw=commit_k_raw[:, :, start:end],
+                                     record_op_log=True, span_ends=None if ctx.span_ends is None else
+                                     [row[start:end] for row in ctx.span_ends])
+        op_log, op_log_len = cache.take_op_log()
+        ctx.replay_plans = _SemanticReplayPlans(cache._last_op_log_host)
+        ctx.op_log, ctx.op_log_len, ctx.op_log_host = op_log, op_log_len, ctx.replay_plans.host_log
+        ctx.updates, ctx.plans, ctx.cache = updates, plans, cache
+        ctx.scale, ctx.train_block, ctx.second_order_scale = scale, train_block, second_order_scale
+        ctx.config = (cache.semantic_anchor_mode, cache.semantic_centroid_backend, cache.semantic_replay_updates,
+                      cache.semantic_unified_route, cache.semantic_merge_passes, cache.alpha_exact_tokens,
+                      cache.alpha_span_max_tokens, cache.beta_novelty, cache.beta_adaptive_merge)
+        ctx.save_for_backward(q, k, v, commit_k_raw)
+        return torch.cat(outputs, dim=2)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        q, k, v, k_raw = ctx.saved_tensors
+        cache, updates = ctx.cache, ctx.updates
+        if ctx.config != (cache.semantic_anchor_mode, cache.semantic_centroid_backend, cache.semantic_replay_updates,
+                          cache.semantic_unified_route, cache.semantic_merge_passes, cache.alpha_exact_tokens,
+                          cache.alpha_span_max_tokens, cache.beta_novelty, cache.beta_adaptive_merge):
+            raise RuntimeError("semantic cache configuration changed between forward and backward")
+        T = q.size(2)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        with torch.no_grad():
+            if updates is not None:
+                updates.wait(q.device)
+            cache.reset_parameters()
+        for i, start in enumerate(range(0, T, ctx.train_block)):
+            end = min(start + ctx.train_block, T)
+            q_b = q[:, :, start:end].detach().requires_grad_(True)
+            k_b = k[:, :, start:end].detach().requires_grad_(True)
+            v_b = v[:, :, start:end].detach().requires_grad_(True)
+            with torch.enable_grad():
+                y_b = log_kv_chunk_attention(cache, q_b, k_b, v_b, ctx.scale, ctx.second_order_scale,
+                                             attention_plan=ctx.plans[i])
+            g_q, g_k, g_v = torch.autograd.grad(y_b, (q_b, k_b, v_b), grad_y[:, :, start:end])
+            dq[:, :, start:end] = g_q
+            dk[:, :, start:end] = g_k
+            dv[:, :, start:end] = g_v
+            with torch.no_grad(), cache._semantic_update_context(updates, replay=True):
+                cache.add_recent(k[:, :, start:end], v[:, :, start:end], k_raw=k_raw[:, :, start:end],
+                                 replay_op_log=ctx.op_log, replay_op_log_len=ctx.op_log_len,
+                                 replay_op_log_host=ctx.op_log_host, replay_plans=ctx.replay_plans,
+                                 span_ends=None if ctx.span_ends is None else
+                                 [row[start:end] for row in ctx.span_ends])
+        return (dq, dk, dv) + (None,) * (ctx.input_count - 3)

@@ -26,7 +26,8 @@ import math
 
 import torch
 
-from ._lib import AttentionArgs, PackArgs, ReadoutView, SlotPackArgs, check, lib, ptr, require_device, stream_of
+from ._lib import (AttentionArgs, AttentionGradArgs, PackArgs, ReadoutView, SlotPackArgs, check, lib, ptr,
+                   require_device, stream_of)
 
 _BACKENDS = ("auto", "triton", "hip")
 
@@ -150,8 +151,10 @@ def pack_mid_kv(cache, plan, k, v, dim, *, backend=None, buffers=None, skip_pool
     if ((skip_pooled and buffers is None) or (recent_start and not skip_pooled)
             or not 0 <= recent_start <= cache.recent_count):
         raise ValueError("prefix reuse requires a workspace and a valid recent offset")
-    if k.requires_grad or v.requires_grad:
-        raise NotImplementedError("logkv_amd packs for inference; K/V must not require grad")
+    if buffers is not None and (k.requires_grad or v.requires_grad):
+        raise ValueError("reusable decode buffers cannot hold differentiable K/V")
+    if torch.is_grad_enabled() and (k.requires_grad or v.requires_grad):
+        return _PackMidKV.apply(k, v, cache, plan, dim)
     length = plan.width + cache.alpha_count + cache.recent_count + k.size(2)
     if buffers is not None:
         if len(buffers) != 2 or any(buf.ndim != 4 or buf.shape[:2] != k.shape[:2] or buf.size(2) < length
@@ -165,6 +168,25 @@ def pack_mid_kv(cache, plan, k, v, dim, *, backend=None, buffers=None, skip_pool
     view = readout_view(cache)
     _launch_pack(cache, view, plan, k, v, dim, ka, va, skip_pooled, recent_start)
     return ka[:, :, :length], va[:, :, :length]
+
+
+class _PackMidKV(torch.autograd.Function):
+    """pack_mid_kv with a gradient for the current rows (litgpt/log_kv_pack.py:75-97): the packed
+    prefix is detached state, each current row is copied once, so the backward is the slice of the
+    current rows' key and value features."""
+
+    @staticmethod
+    def forward(ctx, k, v, cache, plan, dim):
+        ctx.start = plan.width + cache.alpha_count + cache.recent_count
+        ctx.k_dim, ctx.v_dim = k.size(-1), v.size(-1)
+        with torch.no_grad():
+            return pack_mid_kv(cache, plan, k.detach(), v.detach(), dim)
+
+    @staticmethod
+    def backward(ctx, gka, gva):
+        gk = gka[:, :, ctx.start:, :ctx.k_dim].contiguous() if ctx.needs_input_grad[0] and gka is not None else None
+        gv = gva[:, :, ctx.start:, :ctx.v_dim].contiguous() if ctx.needs_input_grad[1] and gva is not None else None
+        return gk, gv, None, None, None
 
 
 def _inv_scale_bf16(scale: float) -> float:
@@ -208,6 +230,64 @@ def packed_attention(q, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups,
     return out, workspace
 
 
+def packed_attention_backward(q, ka, va, out, dout, plan, tail, scale, causal_tail, v_dim, n_groups, grad_rows,
+                              alpha_count_dev=None):
+    """Gradients of ``packed_attention``: dq ``[Bt, Hq, Tq, Dk]`` and, for the last ``grad_rows`` packed
+    rows of every lane, dk / dv ``[Bt, G, grad_rows, D]`` (the matrix-core backward kernels)."""
+    bt, hq, tq, dk = q.shape
+    if dout.dtype != torch.bfloat16:
+        dout = dout.to(torch.bfloat16)
+    if dout.stride(-1) != 1:
+        dout = dout.contiguous()
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    gk = q.new_empty(bt, n_groups, grad_rows, dk)
+    gv = q.new_empty(bt, n_groups, grad_rows, v_dim)
+    args = AttentionArgs(ptr(q), *q.stride()[:3], bt, hq, n_groups, tq, dk, v_dim, ka.size(3), ptr(ka), ptr(va),
+                         ka.size(2), tail, causal_tail, float(scale), _inv_scale_bf16(scale), ptr(out),
+                         *out.stride()[:3], ptr(alpha_count_dev))
+    grads = AttentionGradArgs(ptr(dout), *dout.stride()[:3], ptr(dq), *dq.stride()[:3], ptr(gk), ptr(gv), grad_rows)
+    need = int(lib().logkv_chunk_backward_workspace_bytes(C.byref(args)))
+    if need < 0:
+        raise ValueError("bad attention shape")
+    ws = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    check(lib().logkv_chunk_attention_backward(C.byref(args), ptr(plan.table), plan.table.numel(), C.byref(grads),
+                                               ptr(ws), ws.numel(), stream_of(q.device)),
+          "logkv_chunk_attention_backward")
+    return dq, gk, gv
+
+
+class _PackedAttention(torch.autograd.Function):
+    """Attention over packed rows whose gradient reaches the queries and the last ``grad_rows`` rows
+    (the in-flight chunk, or every slot of a slot attention): forward by the decode / matrix-core
+    kernels, backward by the matrix-core backward kernels. ``k_rows`` / ``v_rows`` are the tensors the
+    gradient rows were packed from (their features only; masked rows get zero gradient through
+    ``row_mask``)."""
+
+    @staticmethod
+    def forward(ctx, q, k_rows, v_rows, ka, va, plan, tail, scale, causal_tail, v_dim, n_groups, alpha_count_dev,
+                row_mask):
+        out, _ = packed_attention(q.detach(), ka, va, plan, tail, scale, causal_tail, v_dim, n_groups, None,
+                                  alpha_count_dev)
+        ctx.save_for_backward(q.detach(), ka, va, out)
+        # The exact pool's row count as it was for these packed rows: the cache's counter moves on
+        # with later flushes, and a graph may be differentiated after them.
+        exact = None if alpha_count_dev is None else alpha_count_dev.clone()
+        ctx.meta = (plan, tail, scale, causal_tail, v_dim, n_groups, exact, k_rows.size(2), row_mask)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, ka, va, out = ctx.saved_tensors
+        plan, tail, scale, causal_tail, v_dim, n_groups, exact, rows, row_mask = ctx.meta
+        dq, gk, gv = packed_attention_backward(q, ka, va, out, dout, plan, tail, scale, causal_tail, v_dim, n_groups,
+                                               rows, exact)
+        if row_mask is not None:
+            gk = gk * row_mask[..., None]
+            gv = gv * row_mask[..., None]
+        return (dq if ctx.needs_input_grad[0] else None, gk if ctx.needs_input_grad[1] else None,
+                gv if ctx.needs_input_grad[2] else None) + (None,) * 10
+
+
 def _decode_capacity(cache, t: int) -> int:
     return cache.K_max * cache.L_alloc * cache.B_prime + cache.alpha_exact_tokens + cache.recent_capacity + max(2, t)
 
@@ -236,6 +316,16 @@ def log_kv_chunk_attention(cache, q_b, k_b, v_b, scale, second_order_scale=1.0, 
         raise ValueError("queries must be [B, n_heads, t, k_dim] on the cache's device with n_heads % n_groups == 0")
     dim = packed_dim(k_b.size(-1), v_b.size(-1))
     view = readout_view(cache)
+    if torch.is_grad_enabled() and (q_b.requires_grad or k_b.requires_grad or v_b.requires_grad):
+        # Training: the prefix is detached state; the gradient reaches the queries and the chunk.
+        plan = semantic_mid_attention_plan(cache, view) if attention_plan is None else attention_plan
+        cap = _decode_capacity(cache, k_b.size(2))
+        ka = k_b.new_empty(*k_b.shape[:2], cap, dim)
+        va = v_b.new_empty(*v_b.shape[:2], cap, dim)
+        _launch_pack(cache, view, plan, k_b.detach(), v_b.detach(), dim, ka, va, False, 0)
+        exact = cache.alpha_count_dev if cache.alpha_exact_tokens else None
+        return _PackedAttention.apply(q_b, k_b, v_b, ka, va, plan, cache.recent_count + k_b.size(2), scale,
+                                      causal_tail, v_b.size(-1), cache.n_groups, exact, None)
     reuse = (reuse_prefix and not torch.is_grad_enabled() and q_b.size(2) <= 2
              and not k_b.requires_grad and not v_b.requires_grad)
     key = (k_b.device, k_b.dtype, dim, id(cache.cos_cache), id(cache.sin_cache))
@@ -379,10 +469,17 @@ def log_kv_slot_attention(q, slot_k, slot_v, slot_w, scale, mask=None, lam=1.0, 
         raise ValueError("slot keys and values need contiguous features")
     m = None if slot_M is None else slot_M.to(torch.int64)
     valid = None if slot_valid is None else slot_valid.to(torch.uint8)
-    args = SlotPackArgs(ptr(slot_k), *slot_k.stride()[:3], ptr(slot_v), *slot_v.stride()[:3], ptr(w), *w.stride()[:2],
+    slot_k_d, slot_v_d = slot_k.detach(), slot_v.detach()
+    args = SlotPackArgs(ptr(slot_k_d), *slot_k.stride()[:3], ptr(slot_v_d), *slot_v.stride()[:3], ptr(w), *w.stride()[:2],
                         ptr(m), *(m.stride()[:2] if m is not None else (0, 0)), 0 if m is None else m.size(-1),
                         ptr(valid), *(valid.stride()[:2] if valid is not None else (0, 0)),
                         0 if valid is None else valid.size(-1), float(lam), B, G, S, dk, dv, dim, S, ptr(ka), ptr(va))
     check(lib().logkv_pack_slots(C.byref(args), stream_of(q.device)), "logkv_pack_slots")
     plan = MidAttentionPlan(torch.zeros(1, dtype=torch.int32, device=q.device), 0, 0)
+    if torch.is_grad_enabled() and (q.requires_grad or slot_k.requires_grad or slot_v.requires_grad):
+        mask = None
+        if valid is not None:
+            mask = torch.ones(B, G, S, dtype=q.dtype, device=q.device)
+            mask[..., :valid.size(-1)] = valid.to(q.dtype)
+        return _PackedAttention.apply(q, slot_k, slot_v, ka, va, plan, S, scale, causal_tail, dv, G, None, mask)
     return packed_attention(q, ka, va, plan, S, scale, causal_tail, dv, G)[0]

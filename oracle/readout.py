@@ -170,3 +170,39 @@ def slot_pack(slot_k, slot_v, slot_w, lam=1.0, slot_M=None, slot_valid=None):
     va[..., :dv] = np.where(valid[..., None], slot_v, 0)
     ka[..., dk] = np.where(valid, bf16_round(bias), bf16_round(np.float32(-10000.0)))
     return ka, va
+
+
+def attention_grad(q, ka, va, scale, causal_tail, dv, dout, grad_rows):
+    """float64 gradients of ``attention``: (dq ``[Bt, Hq, Tq, Dk]``, dk and dv of the last
+    ``grad_rows`` packed rows ``[Bt, G, grad_rows, D]``), the textbook softmax backward
+    (litgpt/log_kv_cache.py:6867-7098 takes them per block through autograd): with
+    ``p = softmax(scale * qa . ka)``, ``D = dout . o`` and ``ds = p * (dout . va - D)``,
+    ``dq = scale * ds . ka[:Dk]``, ``dk = scale * ds^T . q`` and ``dv = p^T . dout``, summed over
+    the query heads of a KV group; the bias coordinate carries no gradient."""
+    q = f32(q).astype(np.float64)
+    dout = f32(dout).astype(np.float64)
+    n_batch, hq, tq, dk = q.shape
+    n_groups, total, dim = ka.shape[1], ka.shape[2], ka.shape[3]
+    rep = hq // n_groups
+    qa = np.zeros((n_batch, hq, tq, dim), np.float64)
+    qa[..., :dk] = q
+    qa[..., dk] = float(np.asarray(bf16_round(np.float32(1.0 / scale))).reshape(-1)[0])
+    kk = np.repeat(ka.astype(np.float64), rep, axis=1)
+    vv = np.repeat(va.astype(np.float64), rep, axis=1)
+    scores = scale * np.einsum("bhqd,bhsd->bhqs", qa, kk)
+    if causal_tail:
+        start = total - causal_tail
+        for i in range(tq):
+            scores[:, :, i, start + i + 1:] = -np.inf
+    scores -= scores.max(axis=-1, keepdims=True)
+    p = np.exp(scores)
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhqs,bhsd->bhqd", p, vv[..., :dv])
+    dp = np.einsum("bhqd,bhsd->bhqs", dout, vv[..., :dv])
+    ds = p * (dp - (dout * o).sum(-1, keepdims=True))
+    dq = scale * np.einsum("bhqs,bhsd->bhqd", ds, kk[..., :dk])
+    dk_all = scale * np.einsum("bhqs,bhqd->bhsd", ds, q)
+    dv_all = np.einsum("bhqs,bhqd->bhsd", p, dout)
+    dk_g = dk_all.reshape(n_batch, n_groups, rep, total, dk).sum(2)
+    dv_g = dv_all.reshape(n_batch, n_groups, rep, total, dv).sum(2)
+    return dq, dk_g[:, :, total - grad_rows:], dv_g[:, :, total - grad_rows:]

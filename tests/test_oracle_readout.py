@@ -171,3 +171,37 @@ def test_slot_encoding_anchor_counts_and_lam():
     ka, _ = ro.slot_pack(k, k, w, lam=1.0, slot_M=np.array([[[2, 0]]]))
     expect = [-np.log(np.float32(2)) + np.log(np.float32(4)), np.log(np.float32(1)), np.log(np.float32(2))]
     assert np.allclose(ka[0, 0, :, 8], bf16_round(np.asarray(expect, np.float32)))
+
+
+def test_attention_gradient_matches_autograd():
+    """The oracle's hand-written softmax backward against torch autograd of its own forward formula
+    (float64, CPU): a dropped term, a transposed operand or a missed head sum fails here."""
+    import torch
+
+    rng = np.random.default_rng(4)
+    Bt, G, rep, tq, total, dk, dv = 2, 2, 3, 5, 17, 8, 8
+    dim = ro.packed_dim(dk, dv)
+    q = bf16_round(rng.standard_normal((Bt, G * rep, tq, dk)))
+    ka = bf16_round(rng.standard_normal((Bt, G, total, dim)))
+    ka[..., dk + 1:] = 0
+    va = bf16_round(rng.standard_normal((Bt, G, total, dim)))
+    va[..., dv:] = 0
+    dout = rng.standard_normal((Bt, G * rep, tq, dv)).astype(np.float32)
+    scale = 0.3
+    for causal in (0, tq):
+        grads = ro.attention_grad(q, ka, va, scale, causal, dv, dout, grad_rows=7)
+        qt = torch.tensor(q, dtype=torch.float64, requires_grad=True)
+        kt = torch.tensor(ka, dtype=torch.float64, requires_grad=True)
+        vt = torch.tensor(va, dtype=torch.float64, requires_grad=True)
+        qa = torch.cat([qt, torch.full((Bt, G * rep, tq, 1), float(bf16_round(np.float32(1 / scale)).reshape(-1)[0]),
+                                       dtype=torch.float64), torch.zeros(Bt, G * rep, tq, dim - dk - 1,
+                                                                          dtype=torch.float64)], -1)
+        s = scale * qa @ kt.repeat_interleave(rep, 1).transpose(-1, -2)
+        if causal:
+            for i in range(tq):
+                s[:, :, i, total - causal + i + 1:] = float("-inf")
+        out = torch.softmax(s, -1) @ vt.repeat_interleave(rep, 1)[..., :dv]
+        out.backward(torch.tensor(dout))
+        np.testing.assert_allclose(grads[0], qt.grad.numpy(), rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(grads[1], kt.grad.numpy()[:, :, total - 7:, :dk], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(grads[2], vt.grad.numpy()[:, :, total - 7:, :dv], rtol=1e-10, atol=1e-12)
