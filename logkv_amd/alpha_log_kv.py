@@ -45,89 +45,77 @@ class SpanCut:
     length_rows: list
 
 
-_EMPTY = np.empty(0, dtype=np.int64)
+def _scan_runs(new_pos, ends, pending, pending_pos, max_span):
+    """Runs of a flush's tokens, scanned once in order: ``(pending_closed, [(start, stop, closed)])``
+    (the run rule of litgpt/alpha_log_kv.py:16-53).
 
-
-def _ranges(spans) -> np.ndarray:
-    """Concatenated half-open ``[start, stop)`` ranges as one int64 array."""
-    if not spans:
-        return _EMPTY
-    b = np.asarray(spans, dtype=np.int64).reshape(-1, 2)
-    n = np.maximum(b[:, 1] - b[:, 0], 0)
-    total = int(n.sum())
-    if not total:
-        return _EMPTY
-    return np.repeat(b[:, 0] - (np.cumsum(n) - n), n) + np.arange(total, dtype=np.int64)
-
-
-def _new_runs(new_pos, ends, pending, pending_pos, max_span):
-    """Runs of new tokens: (pending_closed, starts, stops, closed) (litgpt/alpha_log_kv.py:16-53).
-
-    A run closes after a boundary token or when it reaches ``max_span`` tokens
-    (an unfinished old span counts toward the first run), and is closed by a
-    position jump before the next token. A jump right after the old unfinished
-    span closes that span instead.
+    A run ends after a boundary token, when its hard segment (tokens since the flush start, a
+    boundary or a position jump; the unfinished old span of ``pending`` tokens counts toward the
+    flush's first segment) reaches a multiple of ``max_span`` tokens, or before a position jump;
+    the last run ends with the flush, closed only if its last token closed it. A jump between the
+    old span's last position and the first token closes the old span instead of extending it. An
+    old span of ``max_span`` tokens or more only ends at a boundary or a jump.
     """
-    pos = np.asarray(new_pos, dtype=np.int64)
-    end = np.asarray(ends, dtype=bool)
-    n = len(pos)
+    n = len(new_pos)
     if n == 0:
-        return False, _EMPTY, _EMPTY, np.empty(0, dtype=bool)
-    pending_closed = bool(pending) and int(pos[0]) != pending_pos + 1
-    carry = 0 if pending_closed else int(pending)
-    jump_before = np.zeros(n, dtype=bool)
-    jump_before[1:] = pos[1:] != pos[:-1] + 1
-    # Hard segments start at the first token, after a boundary and at a jump.
-    seg_start = np.ones(n, dtype=bool)
-    seg_start[1:] = jump_before[1:] | end[:-1]
-    seg = np.cumsum(seg_start) - 1
-    starts_of_seg = np.flatnonzero(seg_start)
-    depth = np.arange(n) - starts_of_seg[seg] + 1 + np.where(seg == 0, carry, 0)
-    at_cap = depth % max_span == 0
-    if carry >= max_span:
-        at_cap &= seg != 0      # an over-long carried span only closes at a boundary or jump
-    close = end | at_cap
-    last = close.copy()
-    last[:-1] |= jump_before[1:]
-    last[-1] = True
-    stops = np.flatnonzero(last) + 1
-    starts = np.concatenate(([0], stops[:-1]))
-    closed = close[stops - 1].copy()
-    closed[:-1] |= jump_before[stops[:-1]]
-    return pending_closed, starts.astype(np.int64), stops.astype(np.int64), closed
+        return False, []
+    pending_closed = bool(pending) and int(new_pos[0]) != pending_pos + 1
+    depth = 0 if pending_closed else int(pending)   # tokens of the current hard segment so far
+    capped = depth < max_span                        # whether cap closes apply in this segment
+    runs, start = [], 0
+    for i in range(n):
+        if i and int(new_pos[i]) != int(new_pos[i - 1]) + 1:
+            if start < i:
+                runs.append((start, i, True))        # a jump closes the open run
+            start, depth, capped = i, 0, True
+        depth += 1
+        if ends[i] or (capped and depth % max_span == 0):
+            runs.append((start, i + 1, True))
+            start = i + 1
+            if ends[i]:
+                depth, capped = 0, True
+    if start < n:
+        runs.append((start, n, False))
+    return pending_closed, runs
 
 
 def cut_spans(old_spans, old_positions, new_positions, ends, old_width, max_span):
     """Whole candidate spans per row (host only); None when no row has one
-    (litgpt/alpha_log_kv.py:84-122)."""
+    (litgpt/alpha_log_kv.py:84-122).
+
+    Row indices address ``[old exact pool (old_width rows) | current flush]``. A row's candidates:
+    its closed old spans (old), then the old unfinished span when a position jump closes it, then
+    the flush's runs - the first one prefixed by the unfinished old span when that continues - and
+    an unfinished old span the flush leaves untouched. Each candidate is ``(ranges, old, closed)``.
+    """
     candidates, token_rows, length_rows = [], [], []
-    for spans, old_pos, new_pos, boundaries in zip(old_spans, old_positions, new_positions, ends):
-        row, offset, pending = [], 0, None
+    for spans, old_pos, new_pos, flags in zip(old_spans, old_positions, new_positions, ends):
+        row = []
+        offset, tail = 0, None
         for length, closed in spans:
             if closed:
                 row.append(([(offset, offset + length)], True, True))
             else:
-                pending = (offset, offset + length)
+                tail = (offset, offset + length)
             offset += length
-        all_pos = np.zeros(old_width + len(new_pos), dtype=np.int64)
-        all_pos[:len(old_pos)] = old_pos
-        all_pos[old_width:] = new_pos
-        pending_len = 0 if pending is None else pending[1] - pending[0]
-        pending_pos = int(all_pos[pending[1] - 1]) if pending_len else 0
-        pending_closed, starts, stops, closed = _new_runs(new_pos, boundaries, pending_len, pending_pos, max_span)
-        if pending_closed:
-            row.append(([pending], False, True))
-        for i, (a, z, done) in enumerate(zip((starts + old_width).tolist(), (stops + old_width).tolist(),
-                                              closed.tolist())):
-            ranges = [(a, z)]
-            if i == 0 and pending_len and not pending_closed:
-                ranges.insert(0, pending)
-            row.append((ranges, False, done))
-        if pending_len and not pending_closed and not len(starts):
-            row.append(([pending], False, False))
-        token_rows.append(_ranges([r for rs, _, _ in row for r in rs]))
-        length_rows.append([sum(z - a for a, z in rs) for rs, _, _ in row])
-        candidates.append((row, all_pos))
+        positions = np.zeros(old_width + len(new_pos), dtype=np.int64)
+        positions[:len(old_pos)] = old_pos
+        positions[old_width:] = new_pos
+        tail_len = 0 if tail is None else tail[1] - tail[0]
+        tail_pos = int(positions[tail[1] - 1]) if tail_len else 0
+        tail_closed, runs = _scan_runs(new_pos, flags, tail_len, tail_pos, max_span)
+        if tail_closed:
+            row.append(([tail], False, True))
+        for i, (a, z, done) in enumerate(runs):
+            joined = i == 0 and tail_len and not tail_closed
+            row.append(([tail, (old_width + a, old_width + z)] if joined else [(old_width + a, old_width + z)],
+                        False, done))
+        if tail_len and not tail_closed and not runs:
+            row.append(([tail], False, False))
+        tokens = [t for ranges, _, _ in row for a, z in ranges for t in range(a, z)]
+        token_rows.append(np.asarray(tokens, dtype=np.int64))
+        length_rows.append([sum(z - a for a, z in ranges) for ranges, _, _ in row])
+        candidates.append((row, positions))
     if not any(length_rows):
         return None
     return SpanCut(candidates, token_rows, length_rows)
@@ -187,54 +175,51 @@ def score_spans(k, v, cut, *, beta_novelty=False, centroids=None, centroid_valid
 def choose_spans(cut: SpanCut, host_scores, budget) -> SpanSelection:
     """Bounded whole-span greedy from host scores in candidate order (litgpt/alpha_log_kv.py:177-226).
 
-    Unfinished spans are mandatory; old closed spans are kept first (density x1.1)
-    and evicted lowest density first (ties: later span first) to make room; a new
-    span replaces whole victims only if its density * length strictly exceeds
-    their summed density * length.
+    Per row, a candidate's density is its score, times 1.1 for an old span. Unfinished spans are
+    kept unconditionally and old closed spans start kept; while over budget, kept closed spans are
+    evicted cheapest first (lowest density, later candidate on ties). The remaining candidates are
+    then offered densest first (earlier on ties): one fits in the free room, or displaces the
+    cheapest kept closed spans only if its density * length strictly exceeds their summed
+    density * length. A span kept this way may itself be displaced later.
     """
     keep, archive, out_spans, out_pos = [], [], [], []
-    offset = 0
-    for (row, positions), tokens, size in zip(cut.candidates, cut.token_rows, cut.length_rows):
+    base = 0
+    for (row, positions), tokens, sizes in zip(cut.candidates, cut.token_rows, cut.length_rows):
         n = len(row)
-        old = [c[1] for c in row]
-        open_ = [not c[2] for c in row]
-        density = [float(host_scores[offset + i]) * (1.1 if old[i] else 1.0) for i in range(n)]
-        offset += n
-        chosen = [open_[i] or old[i] for i in range(n)]
-        room = budget - sum(size[i] for i in range(n) if chosen[i])
-
-        def evictable():
-            return sorted((i for i in range(n) if chosen[i] and not open_[i]), key=lambda i: (density[i], -i))
-
-        for i in evictable():
-            if room >= 0:
-                break
-            chosen[i] = False
-            room += size[i]
-        victims = None
-        for i in sorted((i for i in range(n) if not chosen[i]), key=lambda i: (-density[i], i)):
-            need = size[i]
-            free, lost, taken = room, 0.0, []
-            if free < need:
-                if victims is None:
-                    victims = evictable()
-                for j in victims:
-                    taken.append(j)
-                    free += size[j]
-                    lost += density[j] * size[j]
-                    if free >= need:
-                        break
-            if free >= need and (not taken or density[i] * need > lost):
-                for j in taken:
-                    chosen[j] = False
-                chosen[i] = True
-                room = free - need
-                victims = None
-        sel = np.repeat(np.asarray(chosen, dtype=bool), size) if n else np.zeros(0, dtype=bool)
-        keep.append(tokens[sel].tolist())
-        archive.append(tokens[~sel].tolist())
-        out_spans.append([(size[i], row[i][2]) for i in range(n) if chosen[i]])
-        out_pos.append(positions[tokens[sel]].tolist())
+        dens = [float(host_scores[base + i]) * (1.1 if row[i][1] else 1.0) for i in range(n)]
+        base += n
+        cost_key = lambda i: (dens[i], -i)  # noqa: E731  cheapest victim first
+        kept = [row[i][1] or not row[i][2] for i in range(n)]
+        room = budget - sum(sizes[i] for i in range(n) if kept[i])
+        # Kept closed spans in eviction order; kept in order as candidates join it.
+        victims = sorted((i for i in range(n) if kept[i] and row[i][2]), key=cost_key)
+        while room < 0 and victims:
+            j = victims.pop(0)
+            kept[j] = False
+            room += sizes[j]
+        for i in sorted((i for i in range(n) if not kept[i]), key=lambda i: (-dens[i], i)):
+            need, free, lost, taken = sizes[i], room, 0.0, 0
+            while free < need and taken < len(victims):
+                j = victims[taken]
+                free += sizes[j]
+                lost += dens[j] * sizes[j]
+                taken += 1
+            if free < need or (taken and not dens[i] * need > lost):
+                continue
+            for j in victims[:taken]:
+                kept[j] = False
+            del victims[:taken]
+            kept[i] = True
+            room = free - need
+            at = 0
+            while at < len(victims) and cost_key(victims[at]) < cost_key(i):
+                at += 1
+            victims.insert(at, i)
+        mask = np.repeat(np.asarray(kept, dtype=bool), sizes) if n else np.zeros(0, dtype=bool)
+        keep.append(tokens[mask].tolist())
+        archive.append(tokens[~mask].tolist())
+        out_spans.append([(sizes[i], row[i][2]) for i in range(n) if kept[i]])
+        out_pos.append(positions[tokens[mask]].tolist())
     return SpanSelection(keep, archive, out_spans, out_pos)
 
 

@@ -15,6 +15,8 @@ reference does.
 
 from __future__ import annotations
 
+from typing import NamedTuple
+
 _TOTAL_FIELDS = (
     "processed_tokens",
     "layer_group_count",
@@ -40,62 +42,65 @@ def _with_ratios(counts: dict) -> dict:
     }
 
 
-def _log_cache_counts(cache, pending_len: int) -> tuple[int, int, int, int]:
-    """(lanes, recent, exact, hierarchical) entries of one log-structured layer cache."""
-    lanes = cache.batch_size * cache.n_groups
-    recent = (cache.recent_count + pending_len) * lanes
-    exact = 0
-    if cache.alpha_exact_tokens:
-        # Valid exact-pool rows per batch item, each stored once per KV group.
-        exact = int(cache.alpha_valid.sum().item()) * cache.n_groups
-    hierarchical = int((cache.level_w > 0).sum().item())
-    return lanes, recent, exact, hierarchical
+class _LayerCount(NamedTuple):
+    tokens: int        # the layer's token count (what a dense cache would hold per lane)
+    lanes: int         # batch items x KV groups
+    recent: int
+    exact: int
+    hierarchical: int
+
+
+def _count_layer(attn, processed_tokens: int) -> _LayerCount:
+    """One attention layer's retained entries. A log-structured cache (it tracks ``token_count``)
+    counts its recent window plus a pending tail the attention module holds, the valid exact-pool
+    rows of every KV group and the ladder slots of positive mass (device reductions, one host read);
+    a dense cache holds ``processed_tokens`` per lane, or its populated positions when it is a
+    sliding window."""
+    cache = attn.kv_cache
+    if cache is None:
+        raise ValueError("every attention layer needs an initialized KV cache to measure compression")
+    if hasattr(cache, "token_count"):
+        tail = getattr(attn, "_log_kv_pending", None)
+        tail_len = 0 if tail is None else tail[0].size(2)
+        lanes = cache.batch_size * cache.n_groups
+        exact = int(cache.alpha_valid.sum().item()) * cache.n_groups if cache.alpha_exact_tokens else 0
+        live = int((cache.level_w > 0).sum().item())
+        return _LayerCount(cache.token_count + tail_len, lanes, (cache.recent_count + tail_len) * lanes, exact, live)
+    batch, groups = cache.k.shape[:2]
+    lanes = batch * groups
+    if getattr(cache, "is_sliding_window", False):
+        held = int((cache.positions >= 0).sum().item()) * groups
+    else:
+        held = processed_tokens * lanes
+    return _LayerCount(processed_tokens, lanes, held, 0, 0)
 
 
 def cache_compression_snapshot(model, processed_tokens: int) -> dict:
-    """Count every layer and batch / group lane of ``model`` (``model.transformer.h[i].attn.kv_cache``)
-    before its request cache is reset (litgpt/kv_compression.py:32-76).
+    """Retained entries of every layer and batch / group lane of ``model``
+    (``model.transformer.h[i].attn.kv_cache``), counted before the request's caches are reset
+    (litgpt/kv_compression.py:32-76).
 
-    A log-structured cache's own token count plus the pending tail its attention module
-    holds (``attn._log_kv_pending``, keys first) is authoritative; ``processed_tokens`` is
-    the count for dense caches, which do not track it (tokens actually forwarded, without
-    an unforwarded final output). ``layer_group_count`` includes the batch dimension.
-    Raises ValueError when a layer has no cache, when the layers' token counts differ or
-    when the model has no attention layers.
+    A log-structured layer's own token count (with its attention module's pending tail) is
+    authoritative; ``processed_tokens`` counts dense layers, which do not track it.
+    ``layer_group_count`` includes the batch dimension. Raises ValueError for a layer without a
+    cache, for layers whose token counts disagree and for a model without attention layers.
     """
-    counts = dict.fromkeys(_TOTAL_FIELDS, 0)
-    token_count = None
-    for block in model.transformer.h:
-        cache = block.attn.kv_cache
-        if cache is None:
-            raise ValueError("Cannot measure KV compression without an initialized cache in every layer")
-        log_structured = hasattr(cache, "token_count")
-        pending = getattr(block.attn, "_log_kv_pending", None) if log_structured else None
-        pending_len = 0 if pending is None else pending[0].size(2)
-        current = cache.token_count + pending_len if log_structured else processed_tokens
-        if token_count is not None and current != token_count:
-            raise ValueError("KV cache token counts differ between layers")
-        token_count = current
-        if log_structured:
-            lanes, recent, exact, hierarchical = _log_cache_counts(cache, pending_len)
-        else:
-            batch_size, n_groups = cache.k.shape[:2]
-            lanes = batch_size * n_groups
-            if getattr(cache, "is_sliding_window", False):
-                recent = int((cache.positions >= 0).sum().item()) * n_groups
-            else:
-                recent = current * lanes
-            exact = hierarchical = 0
-        counts["layer_group_count"] += lanes
-        counts["recent_slots"] += recent
-        counts["exact_slots"] += exact
-        counts["hierarchical_slots"] += hierarchical
-        counts["dense_slots"] += current * lanes
-    if token_count is None:
-        raise ValueError("Cannot measure KV compression for a model without attention layers")
-    counts["processed_tokens"] = token_count
+    layers = [_count_layer(block.attn, processed_tokens) for block in model.transformer.h]
+    if not layers:
+        raise ValueError("the model has no attention layers to measure KV compression on")
+    if len({layer.tokens for layer in layers}) != 1:
+        raise ValueError("the layers' KV caches disagree on their token counts")
+    tokens = layers[0].tokens
+    counts = {
+        "processed_tokens": tokens,
+        "layer_group_count": sum(layer.lanes for layer in layers),
+        "recent_slots": sum(layer.recent for layer in layers),
+        "exact_slots": sum(layer.exact for layer in layers),
+        "hierarchical_slots": sum(layer.hierarchical for layer in layers),
+        "dense_slots": sum(tokens * layer.lanes for layer in layers),
+    }
     counts["retained_slots"] = counts["recent_slots"] + counts["exact_slots"] + counts["hierarchical_slots"]
-    return _with_ratios(counts)
+    return _with_ratios({field: counts[field] for field in _TOTAL_FIELDS})
 
 
 def summarize_compression(records: list[dict]) -> dict:

@@ -1,11 +1,13 @@
 """Retained-entry accounting on the device cache (litgpt/kv_compression.py:32-76): after
-every add_recent of an Alpha stream, the snapshot's exact and hierarchical counts equal
-direct reductions of the cache's buffers, unfinished spans count, and the KV groups'
-ladders are counted separately (the reference's test_alpha_counts_unfinished_spans_and_each_group
-workload: batch 2, 2 groups x 8, B=8, recent 8, K=4, P=8, span cap 4)."""
+every add_recent of an Alpha stream the snapshot's counts equal those of an oracle cache fed
+the same stream (its exact-pool validity, live ladder slots and recent rows, computed on the
+CPU), unfinished spans count, and the KV groups' ladders are counted separately (the
+reference's test_alpha_counts_unfinished_spans_and_each_group workload: batch 2, 2 groups x 8,
+B=8, recent 8, K=4, P=8, span cap 4)."""
 
 from types import SimpleNamespace
 
+import numpy as np
 import pytest
 import torch
 
@@ -27,26 +29,34 @@ def test_alpha_counts_unfinished_spans_and_each_group():
         cluster_k_max=4, semantic_anchor_mode="mid", allocate_second_order=False, semantic_flush_granularity=8,
         cos_cache=torch.ones(128, 8), sin_cache=torch.zeros(128, 8), rope_n_elem=8, alpha_exact_tokens=8,
         alpha_span_max_tokens=4)
+    from oracle import OracleCache
+
+    ora = OracleCache(2, 2, 128, 8, 8, B=8, recent_size=8, K=4, flush=8, exact_tokens=8, span_max=4,
+                      cos=np.ones((128, 8), np.float32), sin=np.zeros((128, 8), np.float32))
     g = torch.Generator().manual_seed(17)
     k, v = (torch.randn(2, 2, 96, 8, generator=g).to(torch.bfloat16).cuda() for _ in range(2))
     ends = [[i % 3 == 2 for i in range(96)], [i % 4 == 3 for i in range(96)]]
     saw_unfinished = saw_unequal_groups = False
     for start in range(0, 96, 8):
         pos = torch.arange(start, start + 8, device="cuda").unsqueeze(0).expand(2, -1).contiguous()
+        block_ends = [row[start:start + 8] for row in ends]
         cache.add_recent(k[:, :, start:start + 8], v[:, :, start:start + 8], k_raw=k[:, :, start:start + 8],
-                         input_pos=pos, span_ends=[row[start:start + 8] for row in ends])
+                         input_pos=pos, span_ends=block_ends)
+        kb, vb = (x[:, :, start:start + 8].float().cpu().numpy() for x in (k, v))
+        ora.add_recent(kb, vb, kb, pos.cpu().numpy(), block_ends)
         snap = cache_compression_snapshot(model_with(cache), start + 8)
-        exact = int(cache.alpha_valid.sum().item()) * 2
-        hierarchical = int((cache.level_w > 0).sum().item())
-        assert snap["processed_tokens"] == start + 8
+        exact = int(ora.alpha_valid.sum()) * 2
+        hierarchical = int((ora.level_w > 0).sum())
+        assert snap["processed_tokens"] == ora.token_count == start + 8
         assert snap["exact_slots"] == exact
         assert snap["hierarchical_slots"] == hierarchical
-        assert snap["retained_slots"] == cache.recent_count * 4 + exact + hierarchical
+        assert snap["recent_slots"] == ora.recent_count * 4
+        assert snap["retained_slots"] == ora.recent_count * 4 + exact + hierarchical
         assert snap["dense_slots"] == (start + 8) * 4
         counts = cache.alpha_span_count.tolist()
         closed = cache.alpha_span_closed.cpu()
         saw_unfinished |= any(not bool(closed[b, i]) for b in range(2) for i in range(counts[b]))
-        saw_unequal_groups |= hierarchical != int((cache.level_w[0, 0] > 0).sum().item()) * 4
+        saw_unequal_groups |= hierarchical != int((ora.level_w[0, 0] > 0).sum()) * 4
     assert saw_unfinished
     assert saw_unequal_groups
     assert snap["kv_retention_ratio"] < 1

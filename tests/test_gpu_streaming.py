@@ -96,3 +96,54 @@ def test_block_two_prefill_is_strict_streaming():
           span_ends=ends)
         assert e._log_kv_pending is None
     assert_same_state(pairs.cache, single.cache)
+
+
+def test_stream_matches_the_oracle():
+    """Oracle evidence for the engine (litgpt/model.py:1219-1340): after an odd block prefill and
+    token-by-token decode, the device cache equals an oracle cache fed the same tokens in 2-token
+    commits, bit for bit; every decode output equals the float64 attention of its query over the
+    oracle's state then plus the pending-and-current pair (non-causal among the two) or, for a
+    token left pending, over the state plus itself."""
+    from oracle import OracleCache
+    from oracle import readout as ro
+
+    T, prefill = 44, 29
+    q, k, v, k_raw, ends = stream_inputs(T, seed=21)
+    engine = new_engine(8)
+    cache = engine.cache
+    cos, sin = cache.cos_cache.cpu().numpy(), cache.sin_cache.cpu().numpy()
+    ora = OracleCache(B, G, N, D, D, B=8, recent_size=R, K=4, s_h=16.0, flush=R, exact_tokens=8, span_max=4,
+                      beta_novelty=True, beta_adaptive=True, cos=cos, sin=sin)
+    qn, kn, vn, krn = to_np(q), to_np(k), to_np(v), to_np(k_raw)
+    pos = np.arange(T)[None].repeat(B, 0)
+
+    def commit(a, b):
+        ora.add_recent(kn[:, :, a:b], vn[:, :, a:b], krn[:, :, a:b], pos[:, a:b], [row[a:b] for row in ends])
+
+    run(engine, (q, k, v, k_raw, ends), [0, prefill])
+    for a in range(0, prefill - 1, 2):        # the prefill commits every pair; its last token waits
+        commit(a, a + 2)
+    scale = D ** -0.5
+    pending = prefill - 1
+    for i in range(prefill, T):
+        out = run(engine, (q, k, v, k_raw, ends), [i, i + 1])
+        if pending is not None:
+            ka, va = ora.pack(kn[:, :, pending:i + 1], vn[:, :, pending:i + 1])
+            ref = ro.attention(qn[:, :, i:i + 1], ka, va, scale, 0, D)
+            commit(pending, i + 1)
+            pending = None
+        else:
+            ka, va = ora.pack(kn[:, :, i:i + 1], vn[:, :, i:i + 1])
+            ref = ro.attention(qn[:, :, i:i + 1], ka, va, scale, 1, D)
+            pending = i
+        ref = torch.from_numpy(ref.transpose(0, 2, 1, 3).reshape(B, 1, HQ * D)).float()
+        assert_close(out.cpu(), ref, f"decode token {i}")
+    assert ora.token_count + (1 if pending is not None else 0) == T
+    torch.cuda.synchronize()
+    for f in STATE_FIELDS:
+        a = to_np(getattr(cache, f))
+        b = np.asarray(getattr(ora, f))
+        assert np.array_equal(a.astype(np.float64), b.astype(np.float64)), f"field {f} differs from the oracle"
+    assert cache.recent_count == ora.recent_count
+    np.testing.assert_array_equal(to_np(cache.alpha_pos), ora.alpha_pos)
+    np.testing.assert_array_equal(to_np(cache.alpha_valid).astype(bool), ora.alpha_valid)

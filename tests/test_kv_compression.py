@@ -99,12 +99,12 @@ def test_empty_cache_and_empty_summary_have_no_ratio():
 
 def test_inconsistent_layer_token_counts_are_rejected():
     caches = [log_like(4, 4, torch.zeros(1, 3, 1, 1, 1)), log_like(8, 0, torch.zeros(1, 3, 1, 1, 1))]
-    with pytest.raises(ValueError, match="token counts differ"):
+    with pytest.raises(ValueError, match="disagree on their token counts"):
         cache_compression_snapshot(model_with(*caches), 4)
 
 
 def test_missing_cache_and_no_layers_are_rejected():
-    with pytest.raises(ValueError, match="initialized cache"):
+    with pytest.raises(ValueError, match="initialized KV cache"):
         cache_compression_snapshot(model_with(None), 4)
-    with pytest.raises(ValueError, match="without attention layers"):
+    with pytest.raises(ValueError, match="no attention layers"):
         cache_compression_snapshot(model_with(), 4)

@@ -1,4 +1,5 @@
-"""Host span logic: product (vectorised) vs oracle (per-token / per-span loops), known answers."""
+"""Host span logic: product (one token scan, eviction queue) vs oracle (its own per-token and
+per-span loops, pinned by the reference's known answers), and the known answers."""
 
 import numpy as np
 import pytest
@@ -17,9 +18,9 @@ def test_new_runs_match_token_loop():
         new_pos = (100 + np.cumsum(steps)).tolist()
         ends = (rng.random(count) < 0.2).tolist()
         pending_pos = new_pos[0] - int(rng.integers(1, 3)) if count else 0
-        closed, starts, stops, done = prod._new_runs(new_pos, ends, pending, pending_pos, max_span)
+        got = prod._scan_runs(new_pos, ends, pending, pending_pos, max_span)
         want = ora.new_runs(new_pos, ends, pending, pending_pos, max_span)
-        assert (closed, list(zip(starts.tolist(), stops.tolist(), done.tolist()))) == want
+        assert got == want
 
 
 def _random_pool(rng, rows, max_span):
