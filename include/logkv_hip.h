@@ -65,6 +65,10 @@ typedef struct logkv_route_params {
   float lam;            /* radius multiplier (cluster_lambda_rel) */
   int32_t late_joins;   /* 1 with Alpha: re-sort clusters whose p_hi passes a new row */
   int32_t beta_merge;   /* 1: Beta 4->2 merges at non-top carry levels */
+  int32_t center_tile;  /* 0 or 1: a center sums its new keys one row at a time in position order
+                         * (semantic_centroid_backend="sequential"); 32: in position-ordered tiles of
+                         * 32 rows, each tile summed by a halving tree, tiles added in order
+                         * ("parallel", litgpt/log_kv_updates_triton.py:236-241, 274-275) */
 } logkv_route_params;
 
 const char* logkv_last_error(void);

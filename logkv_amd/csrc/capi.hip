@@ -111,6 +111,8 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   if (rc) return rc;
   if ((rc = check_rows(c, r))) return rc;
   if (!prm) return fail(LOGKV_EINVAL, "route params are NULL");
+  if (prm->center_tile != 0 && prm->center_tile != 1 && prm->center_tile != logkv::kCenterTile)
+    return fail(LOGKV_EINVAL, "center_tile must be 0, 1 or %d", logkv::kCenterTile);
   const int late = prm->late_joins ? 1 : 0;
   if (late && int64_t(c->levels) * c->slots + r->tokens > logkv::kMaxOrderRows)
     return fail(LOGKV_EINVAL, "delayed archive sort needs L*B' + T <= %d", logkv::kMaxOrderRows);

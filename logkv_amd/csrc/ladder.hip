@@ -679,7 +679,8 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
 
   if (blockIdx.y == 1) {
     // Center role: mu <- (pre*mu + sum k) / (pre + n), pre = n_eff, the new
-    // rows' keys summed in position order (litgpt/log_kv_cache.py:4344-4359);
+    // rows' keys summed in position order (litgpt/log_kv_cache.py:4344-4359),
+    // one at a time or in tiles (prm.center_tile, the centroid backend);
     // a new cluster starts from its first row's key with n_eff = 1
     // (litgpt/log_kv_cache.py:2276-2278). Key rows are staged in LDS by all
     // threads; one thread per feature adds them in order.
@@ -712,7 +713,24 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
           }
         }
         __syncthreads();
-        if (d < dk) {
+        if (d < dk && prm.center_tile == kCenterTile) {
+          // Tiles of kCenterTile rows from the first new row (kCenterRows is a
+          // multiple, so chunks start on tile boundaries), each summed by a
+          // halving tree with zeros past the last row, then added in order.
+          static_assert(kCenterRows % kCenterTile == 0, "center chunks hold whole tiles");
+          for (int t0 = 0; t0 < rows; t0 += kCenterTile) {
+            float x[kCenterTile];
+#pragma unroll
+            for (int q = 0; q < kCenterTile; ++q)
+              x[q] = t0 + q < rows ? bf16_to_f32(stage[(t0 + q) * dk + d]) : 0.f;
+#pragma unroll
+            for (int h = kCenterTile / 2; h >= 1; h /= 2) {
+#pragma unroll
+              for (int q = 0; q < h; ++q) x[q] = x[q] + x[q + h];
+            }
+            acc = (c0 == first && t0 == 0) ? x[0] : acc + x[0];
+          }
+        } else if (d < dk) {
           int rr = 0;
           if (c0 == first) {
             acc = bf16_to_f32(stage[d]);

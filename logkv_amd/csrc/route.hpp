@@ -10,6 +10,7 @@ using RowsArgs = logkv_rows_view;
 using RouteParams = logkv_route_params;
 
 constexpr int kMaxOrderRows = 8192;   // rows per flush (position-order sort in LDS)
+constexpr int kCenterTile = 32;       // rows per tile of the tiled center sum
 constexpr int kOrderIndexBits = 13;
 constexpr uint64_t kOrderIndexMask = (1ull << kOrderIndexBits) - 1;
 constexpr int kMaxClusters = 32;      // K (alive bits are a 32-bit mask)

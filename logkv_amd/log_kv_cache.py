@@ -27,6 +27,9 @@ import torch.nn as nn
 from . import _lib
 from ._lib import LadderView, RouteParams, RowsView, check, lib, ptr, require_device, stream_of
 
+# Rows per tile of a center's new-key sum, by semantic_centroid_backend.
+_CENTER_TILES = {"sequential": 1, "parallel": 32}
+
 
 class CacheAttentionState(NamedTuple):
     """Unpacked attention slots of a cache (litgpt/log_kv_cache.py:151-161): keys, values and masses
@@ -349,7 +352,8 @@ class LogStructuredKVCache(nn.Module):
         self._views = {}
         self._alpha_parity = 0   # flips with every swap of the exact pool's two buffer sets
         self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
-                                   1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0)
+                                   1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0,
+                                   _CENTER_TILES[self._centroid_backend])
         self.op_log: torch.Tensor | None = None
         self.op_log_len: torch.Tensor | None = None
         self._op_replay_cursor_host = None
@@ -836,6 +840,21 @@ class LogStructuredKVCache(nn.Module):
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand
     # ------------------------------------------------------------------
+    @property
+    def semantic_centroid_backend(self) -> str:
+        """Order of a center's new-key sum: "sequential" (one row at a time in position order) or
+        "parallel" (position-ordered tiles of 32 rows, each summed by a halving tree, tiles added in
+        order; litgpt/log_kv_updates_triton.py:236-241). Read by every later flush."""
+        return self._centroid_backend
+
+    @semantic_centroid_backend.setter
+    def semantic_centroid_backend(self, value: str) -> None:
+        if value not in _CENTER_TILES:
+            raise ValueError("semantic_centroid_backend must be sequential or parallel")
+        self._centroid_backend = value
+        if "_params" in self.__dict__:
+            self._params.center_tile = _CENTER_TILES[value]
+
     @property
     def alpha_count(self) -> int:
         """Rows of the exact pool in use (largest kept count); read from the device."""

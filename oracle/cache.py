@@ -58,7 +58,7 @@ def budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens, element=2):
 class OracleCache:
     def __init__(self, batch, groups, max_seq, dk, dv, *, B=128, recent_size=2048, K=12, lam=1.0, eta=1.0,
                  g0=2048.0, s_h=1.0, flush=2048, exact_tokens=0, span_max=64, beta_novelty=False,
-                 beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False):
+                 beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False, centroid_tile=1):
         self.batch, self.groups, self.max_seq, self.dk, self.dv = batch, groups, max_seq, dk, dv
         self.K, self.lam, self.eta, self.g0 = K, lam, eta, g0
         self.B, self.L, *_ = budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens)
@@ -67,6 +67,7 @@ class OracleCache:
         self.P, self.span_max = exact_tokens, span_max
         self.beta_novelty, self.beta_adaptive = beta_novelty, beta_adaptive
         self.cos, self.sin, self.table_bf16 = cos, sin, table_bf16
+        self.centroid_tile = centroid_tile       # 1: sequential centroid backend, 32: parallel
         shp = (batch, groups, K, self.L, self.B)
         self.level_k = np.zeros(shp + (dk,), np.float32)
         self.level_v = np.zeros(shp + (dv,), np.float32)
@@ -144,7 +145,7 @@ class OracleCache:
         phase = int(self.level0_phase[b, g, c])
         self._append(b, g, c, self._token_rows(keys, values, pos, phase))
         self.centroid[b, g, c], self.n_eff[b, g, c] = lad.centroid_update(
-            self.centroid[b, g, c], self.n_eff[b, g, c], keys)
+            self.centroid[b, g, c], self.n_eff[b, g, c], keys, tile=self.centroid_tile)
         self.level0_phase[b, g, c] = phase + n
         self.p_hi_c[b, g, c] = pos[-1]
         self.n_total[b, g, c] += n
@@ -159,7 +160,7 @@ class OracleCache:
         sort = np.argsort(combined["p_lo"], kind="stable")
         rows = lad.take(combined, sort)
         rows["order"] = np.arange(len(sort), dtype=np.int64)
-        mu, ne = lad.centroid_update(self.centroid[b, g, c], self.n_eff[b, g, c], keys)
+        mu, ne = lad.centroid_update(self.centroid[b, g, c], self.n_eff[b, g, c], keys, tile=self.centroid_tile)
         high = max(int(self.p_hi_c[b, g, c]), int(pos.max()))
         total = int(self.n_total[b, g, c]) + len(pos)
         ladder.clear()

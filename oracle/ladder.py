@@ -288,12 +288,31 @@ class Ladder:
         return take(self.rows, idx.astype(np.int64))
 
 
-def centroid_update(mu, n_eff, keys, forget: float = 1.0):
+def tiled_sum(keys, tile: int):
+    """Row sum of ``keys`` in position-ordered tiles of ``tile`` rows: each tile (zeros past the
+    last row) summed by a halving tree (row i with row i + tile/2, then + tile/4, ...), the tile
+    sums added in order (the "parallel" centroid backend, litgpt/log_kv_updates_triton.py:236-241)."""
+    keys = f32(keys)
+    acc = None
+    for t0 in range(0, len(keys), tile):
+        x = np.zeros((tile, keys.shape[1]), np.float32)
+        part = keys[t0:t0 + tile]
+        x[:len(part)] = part
+        h = tile // 2
+        while h >= 1:
+            x[:h] = x[:h] + x[h:2 * h]
+            h //= 2
+        acc = x[0].copy() if acc is None else np.float32(acc + x[0])
+    return acc
+
+
+def centroid_update(mu, n_eff, keys, forget: float = 1.0, tile: int = 1):
     """Ordered run update ``mu <- (pre*mu + sum k) / (pre + n)``, ``pre = n_eff*forget``
-    (litgpt/log_kv_cache.py:4344-4359); keys summed sequentially in row order."""
+    (litgpt/log_kv_cache.py:4344-4359); keys summed one row at a time in row order, or with
+    ``tile`` > 1 by ``tiled_sum``."""
     keys = f32(keys)
     n = np.float32(len(keys))
-    acc = np.add.accumulate(keys, axis=0, dtype=np.float32)[-1]
+    acc = np.add.accumulate(keys, axis=0, dtype=np.float32)[-1] if tile == 1 else tiled_sum(keys, tile)
     pre = np.float32(n_eff) * np.float32(forget)
     denom = np.float32(pre + n)
     if pre > 0:

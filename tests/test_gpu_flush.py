@@ -31,6 +31,44 @@ def test_flush_matches_oracle(name):
     assert int(to_np(gpu.alive).sum()) > 0
 
 
+def test_parallel_centroid_backend_matches_oracle():
+    """semantic_centroid_backend="parallel": centers sum their new keys in 32-row tiles (each by a
+    halving tree); the device equals an oracle cache with that order bit for bit, the sequential
+    device run differs from it in some center's last bits (rows scaled by powers of two from 2^-6
+    to 2^6, so float32 sums round and the order shows), and switching the backend on a live cache
+    takes effect at the next flush."""
+    print("case parallel centroid", flush=True)
+    args = (1, 4, 128, 4, 16, 256, 256, 4096, 64.0)
+    gpu, ora = make_pair(*args, centroid_backend="parallel")
+    seq, _ = make_pair(*args)
+    mix = Mixture(1, 4, 128, clusters=4, seed=12)
+    g = torch.Generator().manual_seed(12)
+
+    def block(start):
+        scale = torch.exp2(torch.randint(-6, 7, (1, 1, 256, 1), generator=g).float())
+        k_raw, v, k = ((mix.rows(256).float() * scale).to(torch.bfloat16) for _ in range(3))
+        pos = torch.arange(start, start + 256).unsqueeze(0)
+        return k_raw, v, k, pos
+
+    def commit(caches, oracle, rows):
+        k_raw, v, k, pos = rows
+        for c in caches:
+            c.add_recent(k.cuda(), v.cuda(), k_raw=k_raw.cuda(), input_pos=pos.cuda())
+        oracle.add_recent(k.float().numpy(), v.float().numpy(), k_raw.float().numpy(), pos.numpy(), None)
+        torch.cuda.synchronize()
+
+    for blk in range(5):
+        commit((gpu, seq), ora, block(blk * 256))
+        bad = compare_state(gpu, ora)
+        assert not bad, f"block {blk}: " + "; ".join(bad)
+    assert not np.array_equal(to_np(gpu.centroid), to_np(seq.centroid))
+    gpu.semantic_centroid_backend = "sequential"
+    ora.centroid_tile = 1
+    commit((gpu,), ora, block(5 * 256))
+    bad = compare_state(gpu, ora)
+    assert not bad, "after switching to sequential: " + "; ".join(bad)
+
+
 @pytest.mark.parametrize("dim,flush,max_seq,sizes", [
     (64, 64, 64, (1, 40, 64, 64, 64, 64)),
     # 256-wide rows (two 8-byte units per lane in the fold) and, with three

@@ -193,3 +193,22 @@ def test_centroid_update_matches_float64():
     got0, n0 = lad.centroid_update(mu, np.float32(0.0), keys)
     np.testing.assert_allclose(got0, keys.astype(np.float64).mean(0), rtol=1e-6, atol=3e-6)
     assert n0 == np.float32(37.0)
+
+
+def test_tiled_center_sum_hand_worked():
+    """The parallel backend's order, worked by hand in float32: 2^24 followed by 32 ones. One row at
+    a time every +1 rounds back to 2^24 (ties to even). In tiles of 32 the first tile's halving tree
+    pairs 2^24 with a one (2^24 again), then adds 2 + 4 + 8 + 16 exactly: 2^24 + 30; the second tile
+    is the last one, and 2^24 + 31 rounds to the even 2^24 + 32."""
+    keys = np.asarray([[2.0 ** 24]] + [[1.0]] * 32, np.float32)
+    assert lad.tiled_sum(keys[:32], 32)[0] == 2.0 ** 24 + 30
+    assert lad.tiled_sum(keys, 32)[0] == 2.0 ** 24 + 32
+    assert np.add.accumulate(keys, axis=0, dtype=np.float32)[-1][0] == 2.0 ** 24
+    mu, n_eff = lad.centroid_update(np.zeros(1, np.float32), np.float32(0.0), keys, tile=32)
+    assert n_eff == 33 and mu[0] == np.float32(np.float32(2.0 ** 24 + 32) / np.float32(33))
+    seq, _ = lad.centroid_update(np.zeros(1, np.float32), np.float32(0.0), keys)
+    assert seq[0] == np.float32(np.float32(2.0 ** 24) / np.float32(33))
+    # Small integers sum exactly in any order: the tiles must then equal the float64 sum.
+    rng = np.random.default_rng(3)
+    ints = rng.integers(-50, 50, (75, 16)).astype(np.float32)
+    np.testing.assert_array_equal(lad.tiled_sum(ints, 32), ints.astype(np.float64).sum(0))
