@@ -285,7 +285,8 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
 }
 
 // Partials of the key-range splits combined in split order: two queries per
-// block, one output feature per thread.
+// block, one output feature per thread. A partial's maximum m is of s * scale *
+// log2(e), so a split's weight is 2^(m_split - m).
 __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args a, const float* __restrict__ part,
                                                             int splits) {
   const int lane_ix = blockIdx.y, G = a.n_groups;
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args
   for (int sp = 0; sp < splits; ++sp) {
     const float* pp = base + sp * step;
     if (pp[0] == -__builtin_inff()) continue;
-    const float f = __expf(pp[0] - m);
+    const float f = __builtin_amdgcn_exp2f(pp[0] - m);   // maxima are in the base-2 domain
     lsum += pp[1] * f;
     acc += pp[2 + d] * f;
   }
