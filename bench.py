@@ -31,7 +31,9 @@ pass's states).
 
 ``python bench.py --pmc-summary FETCH_DIR WRITE_DIR`` turns the counter
 output of two ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` runs of
-``bench.py --profile-flush`` into HBM bytes per step.
+``bench.py --profile-flush`` into HBM bytes per step; ``--trace-summary CSV``
+gives the kernel time per step of a ``--kernel-trace`` run of it and
+``--kernel-counters DIR`` every kernel's mean counters of a ``--pmc`` run.
 """
 
 from __future__ import annotations
@@ -928,6 +930,40 @@ def pmc_summary(fetch_dir, write_dir, steps, probe_mib):
     return out
 
 
+def trace_summary(trace_csv, steps):
+    """Kernel time per headline step from a ``rocprofv3 --kernel-trace`` CSV of a ``--profile-flush`` run:
+    the last ``steps`` ranges from one cut_kernel to the next, per kernel (mean us per step) and the span
+    from the first kernel's start to the last kernel's end."""
+    import csv
+
+    with open(trace_csv) as fh:
+        rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if _short(r["Kernel_Name"]) == "cut_kernel"]
+    bounds = list(zip(starts, starts[1:] + [len(rows)]))[-steps:]
+    per_kernel, spans = {}, []
+    for a, b in bounds:
+        keep = [r for r in rows[a:b] if "copyBuffer" not in r["Kernel_Name"]]
+        for r in keep:
+            k = _short(r["Kernel_Name"])
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            per_kernel[k] = per_kernel.get(k, 0.0) + us / len(bounds)
+        spans.append((int(keep[-1]["End_Timestamp"]) - int(keep[0]["Start_Timestamp"])) / 1e3)
+    return {"steps": len(bounds), "span_us": sum(spans) / len(spans), "kernel_us": sum(per_kernel.values()),
+            "per_kernel_us": dict(sorted(per_kernel.items(), key=lambda kv: -kv[1]))}
+
+
+def kernel_counters(counter_dir):
+    """Mean of every counter per dispatch of each kernel in a ``rocprofv3 --pmc`` run, with the dispatch count."""
+    out = {}
+    for r in _counter_rows(counter_dir):
+        k = _short(r["Kernel_Name"])
+        e = out.setdefault(k, {"dispatches": set(), "counters": {}})
+        e["dispatches"].add(r["Dispatch_Id"])
+        e["counters"].setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return {k: {"dispatches": len(e["dispatches"]),
+                **{c: sum(v) / len(v) for c, v in sorted(e["counters"].items())}} for k, e in out.items()}
+
+
 # ----------------------------------------------------------------------
 
 def run_leg(result, key, fn, *args):
@@ -970,6 +1006,10 @@ def parse_args(argv=None):
                     help="HBM bytes per headline step measured by counter runs (reported as roofline.traffic)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --profile-flush and exit")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="kernel time per headline step of a rocprofv3 --kernel-trace run of --profile-flush, and exit")
+    ap.add_argument("--kernel-counters", metavar="PMC_DIR",
+                    help="mean counter values per dispatch of each kernel of a rocprofv3 --pmc run, and exit")
     args = ap.parse_args(argv)
     if args.warmup < 0:
         ap.error("--warmup must be >= 0")
@@ -984,6 +1024,12 @@ def main():
     args = parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.steps, args.copy_probe_mib or 1024), indent=1))
+        return
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary, args.steps), indent=1))
+        return
+    if args.kernel_counters:
+        print(json.dumps(kernel_counters(args.kernel_counters), indent=1))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X, so --gpus {args.gpus} is not run; the "

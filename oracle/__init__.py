@@ -20,9 +20,10 @@ Modules and what pins them (the tests named in brackets):
   [tests/test_spans_host.py and tests/test_oracle_spans.py: the reference's
   known answers (whole spans, pending tails, novelty rescue, top-2 groups),
   exact closed forms, float64 scores];
-* ``readout`` - attention plan, pack, attention [tests/test_oracle_readout.py:
-  known anchors, explicit RoPE and mask rows, mass slot = duplicated tokens,
-  float64 masked softmax];
+* ``readout`` - attention plan, pack, attention, slot encoding, attention gradients
+  [tests/test_oracle_readout.py: known anchors, explicit RoPE and mask rows, mass
+  slot = duplicated tokens, float64 masked softmax, the slot encoding against the
+  pack, gradients against torch autograd in float64];
 * ``cache`` - one layer's cache and flush driver [tests/test_oracle_cache.py:
   delayed-archive known answer, budget closed form, streaming invariants];
 * ``unified`` - the unified Ward / radius route [tests/test_oracle_unified.py:
@@ -33,11 +34,19 @@ Modules and what pins them (the tests named in brackets):
   [tests/test_oracle_oplog.py: hand-derived logs of small flushes, replay
   reproducing the recorded state bit for bit, the reference's parse errors].
 
-Parity unpinned: the last-ulp agreement with the reference's own float traces
-where it leaves the order to a library (Torch GEMM / cdist / segment_reduce
-summation orders, Flash SDPA). No reference code was imported or run; the
-checks above pin the formulas, the known answers and the invariants, and the
-oracle fixes one order that the device reproduces bit for bit.
+Golden fixtures from the reference's own CPU Torch path (tests/golden, written by
+tests/golden/make_fixtures.py in the build container) pin ``cache``, ``ladder``,
+``spans`` and ``readout`` end to end [tests/test_golden_oracle.py: two streamed flush
+sequences with every state field after every block, 299 span choices with tied scores,
+Beta cuts with near ties and tails, the packer with bf16 RoPE tables]; the centroid's
+tiled ("parallel") order is pinned by a hand-worked float32 case
+[tests/test_oracle_ladder.py].
+
+Parity unpinned: last-ulp agreement with the reference's own float traces on inputs
+beyond the fixtures, where it leaves the order to a library (Torch GEMM / cdist /
+segment_reduce summation orders, Triton ``tl.sum``, Flash SDPA): the oracle fixes one
+order that the device reproduces bit for bit, and the fixtures show it giving the
+reference's values and decisions on their inputs.
 """
 
 from .cache import OracleCache, budget  # noqa: F401
