@@ -12,6 +12,8 @@
 //   32-key block in lane ^ 32),
 //   O^T += V^T P^T (dv x queries), P split into bf16 high and low parts so the
 //   product keeps ~16 significant bits of P (two MFMAs per step).
+// Queries live in registers for the whole key range; the K / V tiles are
+// double-buffered in LDS with one barrier per tile.
 // The P^T operand is the lane's own score registers: MFMA B operand element j
 // of a 16-key step s is key 16s + 8(j/4) + 4(lane/32) + j%4, which is exactly
 // accumulator element 8(s%2) + j of S^T block s/2, so V^T is read with the same
@@ -42,17 +44,23 @@ __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(
 
 // splits == 1: the block writes the output. splits > 1: block (x, s) covers the
 // s-th of `splits` equal parts (whole 64-row tiles) of its queries' key range
-// and writes partials [m, l, acc[dv]] per query in the decode combine's layout.
+// and writes partials [m, l, acc[dv]] per query (m in the base-2 domain).
+// NKS 16-wide steps of the packed width and NDV 32-wide blocks of dv at
+// compile time (straight-line tile code); columns past the packed width and
+// V^T rows past dv are zero, so a kernel with more steps or blocks than the
+// shape needs gives the same result.
+template <int NKS, int NDV>
 __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
                                                        int splits, float* __restrict__ part) {
-  __shared__ __align__(16) uint16_t k_s[kKeys * kLdK];
-  __shared__ __align__(16) uint16_t vt_s[kMaxDvBlocks * 32 * kLdV];
-  __shared__ __align__(16) uint16_t q_s[kQRows * kLdK];
+  // Two K / V^T tile buffers: tile i + 1 is written into the other buffer while
+  // tile i is read, so one barrier per tile orders both.
+  __shared__ __align__(16) uint16_t k_s[2][kKeys * kLdK];
+  __shared__ __align__(16) uint16_t vt_s[2][kMaxDvBlocks * 32 * kLdV];
   const int lane_ix = blockIdx.z, split = blockIdx.y, G = a.n_groups;
   const int b = lane_ix / G, g = lane_ix % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
   const int w = wave_id(), l = lane_id(), h = l >> 5, col = l & 31;
-  const int dim = a.dim, nks = (dim + 15) / 16, ndv = a.dv / 32;
+  const int dim = a.dim, ndv = a.dv / 32;
   const int qi = blockIdx.x * kQRows + w * 32 + col;
   const bool q_ok = qi < nq;
   const int qc = q_ok ? qi : nq - 1;
@@ -67,24 +75,37 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
   const int tiles = (key_end + kKeys - 1) / kKeys, per = (tiles + splits - 1) / splits;
   const int k_begin = min(split * per, tiles) * kKeys, k_stop = min(min((split + 1) * per, tiles) * kKeys, key_end);
 
-  // Queries [q, 1/scale, 0...] in LDS, row-major (the B operand reads dims
-  // 16 ks + 8 h .. + 8 of the lane's query).
-  for (int i = threadIdx.x; i < kQRows * kLdK; i += blockDim.x) {
-    const int r = i / kLdK, d = i - r * kLdK;
-    const int qr = min(blockIdx.x * kQRows + r, nq - 1);
-    const int hr = g * rep + qr / a.tq, tr = qr % a.tq;
-    const float x = d < a.dk ? bf16_to_f32(gp(a.q)[b * a.q_sb + hr * a.q_sh + tr * a.q_st + (d < a.dk ? d : 0)])
-                             : (d == a.dk ? a.inv_scale_bf16 : 0.f);
-    q_s[i] = f32_to_bf16(x);
-  }
-  // Columns past the packed width stay zero in every tile.
-  for (int i = threadIdx.x; i < kKeys * (kLdK - dim); i += blockDim.x) {
-    const int r = i / (kLdK - dim), c = dim + i % (kLdK - dim);
-    k_s[r * kLdK + c] = 0;
-  }
-  f32x16 o[kMaxDvBlocks];
+  // The lane's query [q, 1/scale, 0...] as MFMA B fragments (dims 16 ks + 8 h
+  // .. + 8), held in registers for the whole key range.
+  bf16x8 qf[NKS];
+  {
+    const LOGKV_G uint16_t* qrow = gp(a.q) + b * a.q_sb + head * a.q_sh + t * a.q_st;
 #pragma unroll
-  for (int blk = 0; blk < kMaxDvBlocks; ++blk)
+    for (int ks = 0; ks < NKS; ++ks) {
+      uint16_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = 16 * ks + 8 * h + j;
+        e[j] = d < a.dk ? qrow[d] : (d == a.dk ? f32_to_bf16(a.inv_scale_bf16) : uint16_t(0));
+      }
+      qf[ks] = __builtin_bit_cast(bf16x8, make_uint4(e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16),
+                                                     e[4] | (uint32_t(e[5]) << 16), e[6] | (uint32_t(e[7]) << 16)));
+    }
+  }
+  // Columns past the packed width and V^T rows past dv stay zero in every
+  // tile of both buffers.
+  for (int i = threadIdx.x; i < 2 * kKeys * (kLdK - dim); i += blockDim.x) {
+    const int bf = i / (kKeys * (kLdK - dim)), rest = i - bf * kKeys * (kLdK - dim);
+    const int r = rest / (kLdK - dim), c = dim + rest % (kLdK - dim);
+    k_s[bf][r * kLdK + c] = 0;
+  }
+  for (int i = threadIdx.x; i < 2 * (32 * NDV - a.dv) * kLdV; i += blockDim.x) {
+    const int bf = i / ((32 * NDV - a.dv) * kLdV), rest = i - bf * (32 * NDV - a.dv) * kLdV;
+    vt_s[bf][a.dv * kLdV + rest] = 0;
+  }
+  f32x16 o[NDV];
+#pragma unroll
+  for (int blk = 0; blk < NDV; ++blk)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[blk][i] = 0.f;
   float m = -__builtin_inff(), lsum = 0.f;   // running maximum of s * scale * log2(e), and the sum
@@ -132,16 +153,12 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       if (2 * kp + 1 >= rows) vx[q][1] = make_uint4(0, 0, 0, 0);
     }
   };
-  if (k_begin < k_stop) load_tile(k_begin);
-
-  for (int t0 = k_begin; t0 < k_stop; t0 += kKeys) {
-    const int rows = min(kKeys, k_stop - t0);
-    __syncthreads();
-    // K rows row-major; V transposed: each task's two key rows of one 8-wide dv
-    // unit become 8 dwords (key pairs). Rows past the end are zeros.
+  // K rows row-major; V transposed: each task's two key rows of one 8-wide dv
+  // unit become 8 dwords (key pairs). Rows past the end are zeros.
+  auto store_tile = [&](int bf) {
 #pragma unroll
     for (int q = 0; q < kKTasks; ++q)
-      if (k_row[q] < kKeys) *reinterpret_cast<uint4*>(k_s + k_loff[q]) = kx[q];
+      if (k_row[q] < kKeys) *reinterpret_cast<uint4*>(&k_s[bf][k_loff[q]]) = kx[q];
 #pragma unroll
     for (int q = 0; q < kVTasks; ++q) {
       if (v_pair[q] < 0) continue;
@@ -152,31 +169,42 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       for (int j = 0; j < 4; ++j) {
         const uint32_t lo = __builtin_amdgcn_perm(a1[j], a0[j], 0x05040100u);   // low halves of rows r0, r0 + 1
         const uint32_t hi = __builtin_amdgcn_perm(a1[j], a0[j], 0x07060302u);   // high halves
-        *reinterpret_cast<uint32_t*>(vt_s + (8 * u + 2 * j) * kLdV + r0) = lo;
-        *reinterpret_cast<uint32_t*>(vt_s + (8 * u + 2 * j + 1) * kLdV + r0) = hi;
+        *reinterpret_cast<uint32_t*>(&vt_s[bf][(8 * u + 2 * j) * kLdV + r0]) = lo;
+        *reinterpret_cast<uint32_t*>(&vt_s[bf][(8 * u + 2 * j + 1) * kLdV + r0]) = hi;
       }
     }
-    __syncthreads();
-    if (t0 + kKeys < k_stop) load_tile(t0 + kKeys);
-    // S^T = K Q^T over the packed width.
+  };
+  const int ntiles = k_begin < k_stop ? (k_stop - k_begin + kKeys - 1) / kKeys : 0;
+  if (ntiles > 0) {
+    load_tile(k_begin);
+    store_tile(0);
+    if (ntiles > 1) load_tile(k_begin + kKeys);
+  }
+  __syncthreads();
+
+  const float c2 = a.scale * 1.44269504088896341f;
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = k_begin + it * kKeys, bf = it & 1;
+    const int rows = min(kKeys, k_stop - t0);
+    const uint16_t* kt = k_s[bf];
+    const uint16_t* vt = vt_s[bf];
+    // S^T = K Q^T over the packed width, the two 32-key blocks' chains
+    // interleaved.
     f32x16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < kMaxSteps; ++ks) {
-        if (ks < nks) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(k_s + (32 * kb + col) * kLdK + 16 * ks + 8 * h);
-          const bf16x8 qf = *reinterpret_cast<const bf16x8*>(q_s + (32 * w + col) * kLdK + 16 * ks + 8 * h);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf, s[kb], 0, 0, 0);
-        }
-      }
+    for (int ks = 0; ks < NKS; ++ks) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kt + col * kLdK + 16 * ks + 8 * h);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kt + (32 + col) * kLdK + 16 * ks + 8 * h);
+      s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qf[ks], s[0], 0, 0, 0);
+      s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qf[ks], s[1], 0, 0, 0);
     }
     // Online softmax of this lane's query in the base-2 domain: with c2 = scale
     // * log2(e), p = 2^(s c2 - m) where m is the running maximum of s c2. Masks
     // (past the rows, causal) are evaluated only on tiles that need them.
-    const float c2 = a.scale * 1.44269504088896341f;
     const bool full = rows == kKeys && !(a.causal_tail && t0 + kKeys > tail0);
     float mx = -__builtin_inff();
     if (full) {
@@ -185,13 +213,15 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
     } else {
+      // Visible keys of this lane's query: t0 .. t0 + lim - 1 (past the rows,
+      // and past tail0 + t under the causal mask, are masked); element i of
+      // block kb is key t0 + 32 kb + 8 (i / 4) + 4 h + i % 4.
+      const int lim = (a.causal_tail ? min(rows, tail0 + t + 1 - t0) : rows) - 4 * h;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = t0 + 32 * kb + 8 * (i / 4) + 4 * h + (i % 4);
-          const bool masked = key >= t0 + rows || (a.causal_tail && key >= tail0 && key - tail0 > t);
-          s[kb][i] = masked ? -__builtin_inff() : s[kb][i];
+          s[kb][i] = 32 * kb + 8 * (i / 4) + (i % 4) < lim ? s[kb][i] : -__builtin_inff();
           mx = fmaxf(mx, s[kb][i]);
         }
       }
@@ -215,12 +245,13 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
     m = m_new;
     if (__ballot(corr != 1.f)) {
 #pragma unroll
-      for (int blk = 0; blk < kMaxDvBlocks; ++blk)
+      for (int blk = 0; blk < NDV; ++blk)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[blk][i] *= corr;
     }
     // O^T += V^T P^T, four 16-key steps, P as a truncated high bf16 part plus
-    // the rounded remainder (together ~16 significant bits of P).
+    // the rounded remainder (together ~16 significant bits of P: one bf16 P
+    // misses the 2e-3 bar when values of opposite signs nearly cancel).
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       uint32_t hw[4], lw[4];
@@ -234,18 +265,24 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       }
       const bf16x8 ph = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
       const bf16x8 pl = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+      bf16x8 vf[NDV];
 #pragma unroll
-      for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
-        if (blk < ndv) {
-          const uint16_t* vr = vt_s + (32 * blk + col) * kLdV + 16 * st + 4 * h;
-          const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
-          const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
-          o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[blk], 0, 0, 0);
-          o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[blk], 0, 0, 0);
-        }
+      for (int blk = 0; blk < NDV; ++blk) {
+        const uint16_t* vr = vt + (32 * blk + col) * kLdV + 16 * st + 4 * h;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+        vf[blk] = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
       }
+#pragma unroll
+      for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[blk], ph, o[blk], 0, 0, 0);
+#pragma unroll
+      for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[blk], pl, o[blk], 0, 0, 0);
     }
+    if (it + 1 < ntiles) {
+      store_tile(bf ^ 1);
+      if (it + 2 < ntiles) load_tile(t0 + 2 * kKeys);
+    }
+    __syncthreads();
   }
   if (!q_ok) return;
   if (splits > 1) {
@@ -255,7 +292,7 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       pp[1] = lsum;
     }
 #pragma unroll
-    for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
+    for (int blk = 0; blk < NDV; ++blk) {
       if (blk < ndv) {
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
@@ -269,7 +306,7 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
   }
   LOGKV_G uint16_t* orow = gp(a.out) + b * a.o_sb + head * a.o_sh + t * a.o_st;
 #pragma unroll
-  for (int blk = 0; blk < kMaxDvBlocks; ++blk) {
+  for (int blk = 0; blk < NDV; ++blk) {
     if (blk < ndv) {
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
@@ -331,8 +368,13 @@ int64_t chunk_workspace_floats(const logkv_attention_args& a) {
 int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   const int splits = chunk_splits(a);
-  hipLaunchKernelGGL(chunk_kernel, dim3((nq + kQRows - 1) / kQRows, splits, a.n_batch * a.n_groups), dim3(256), 0,
-                     stream, a, width, splits, part);
+  const dim3 grid((nq + kQRows - 1) / kQRows, splits, a.n_batch * a.n_groups);
+  // Shapes with at most 5 steps and 2 dv blocks (head dim 64) take the
+  // smaller kernel; every other shape runs the full 9 x 4 one on zero padding.
+  if (a.dim <= 80 && a.dv <= 64)
+    hipLaunchKernelGGL((chunk_kernel<5, 2>), grid, dim3(256), 0, stream, a, width, splits, part);
+  else
+    hipLaunchKernelGGL((chunk_kernel<kMaxSteps, kMaxDvBlocks>), grid, dim3(256), 0, stream, a, width, splits, part);
   if (splits > 1)
     hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a, part,
                        splits);
