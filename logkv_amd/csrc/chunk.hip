@@ -4,9 +4,10 @@
 // Same math as the decode kernel (litgpt/log_kv_cache.py:6428-6464, :6751-6758):
 // softmax(scale * [q, 1/scale] . [k, bias]) v, the last `causal_tail` rows
 // causal against the query rows. Flash attention with gfx950's
-// v_mfma_f32_32x32x16_bf16: a block of 4 waves owns 128 query rows of one KV
-// group, a wave 32 of them (one per lane column). Per 64-row key tile, staged
-// in LDS (K row-major, V transposed):
+// v_mfma_f32_32x32x16_bf16: a block of 8 waves (one per CU, two per SIMD)
+// owns 256 query rows of one KV group, a wave 32 of them (one per lane
+// column), so each staged K / V tile serves 256 queries. Per 64-row key tile,
+// staged in LDS (K row-major, V transposed):
 //   S^T = K Q^T   (keys x queries; each lane holds 16 keys of its own query),
 //   online softmax per lane (its query's max and sum, the other 16 keys of the
 //   32-key block in lane ^ 32),
@@ -19,6 +20,7 @@
 // accumulator element 8(s%2) + j of S^T block s/2, so V^T is read with the same
 // key order and no data moves between lanes.
 #include <algorithm>
+#include <type_traits>
 
 #include "route.hpp"
 
@@ -31,14 +33,29 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kQRows = 128;      // query rows per block (4 waves x 32)
+constexpr int kWavesPerBlock = 8;                 // waves per block, each owning 32 query rows
+constexpr int kThreads = 64 * kWavesPerBlock;
+constexpr int kQRows = 32 * kWavesPerBlock;       // query rows per block
+constexpr int kBlocksPerCu = 8 / kWavesPerBlock;  // resident blocks per CU (two waves per SIMD)
 constexpr int kKeys = 64;        // key rows per staged tile
 constexpr int kMaxSteps = 9;     // 16-wide steps of the packed width (<= 144)
 constexpr int kLdK = 152;        // K tile row stride in LDS (bf16)
-constexpr int kLdV = kKeys + 8;  // V^T row stride in LDS (bf16)
+constexpr int kLdV = kKeys + 4;  // V^T row stride in LDS (bf16; 34 dwords: 16 rows' 8-byte reads hit distinct banks)
 constexpr int kMaxDvBlocks = 4;  // dv <= 128
 
 __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(x); }
+
+// max / sum of the values of lanes l and l ^ 32, in every lane: one permlane
+// swap leaves {x[l], x[l ^ 32]} in its two results (lower-half lane's value
+// first), no LDS round trip.
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 }  // namespace
 
@@ -50,7 +67,7 @@ __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(
 // V^T rows past dv are zero, so a kernel with more steps or blocks than the
 // shape needs gives the same result.
 template <int NKS, int NDV>
-__global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+__global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
                                                        int splits, float* __restrict__ part) {
   // Two K / V^T tile buffers: tile i + 1 is written into the other buffer while
   // tile i is read, so one barrier per tile orders both.
@@ -115,11 +132,11 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
   const int vunits = a.dv / 8;
   // Each thread's staging tasks are the same in every tile: up to kKTasks
   // 16-byte K units (row, unit) and kVTasks V tasks (key pair, 8-wide dv unit).
-  constexpr int kKTasks = (kKeys * kMaxSteps * 2 + 255) / 256, kVTasks = (kKeys / 2) * 16 / 256;
+  constexpr int kKTasks = (kKeys * kMaxSteps * 2 + kThreads - 1) / kThreads, kVTasks = (kKeys / 2) * 16 / kThreads;
   int k_row[kKTasks], k_goff[kKTasks], k_loff[kKTasks];
 #pragma unroll
   for (int q = 0; q < kKTasks; ++q) {
-    const int i = threadIdx.x + 256 * q;
+    const int i = threadIdx.x + kThreads * q;
     const bool ok = i < kKeys * units;
     const int r = ok ? i / units : kKeys, u = ok ? i - (i / units) * units : 0;
     k_row[q] = r;
@@ -129,7 +146,7 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
   int v_pair[kVTasks], v_unit[kVTasks];
 #pragma unroll
   for (int q = 0; q < kVTasks; ++q) {
-    const int i = threadIdx.x + 256 * q;
+    const int i = threadIdx.x + kThreads * q;
     v_pair[q] = i < (kKeys / 2) * vunits ? i % (kKeys / 2) : -1;
     v_unit[q] = i / (kKeys / 2);
   }
@@ -183,7 +200,10 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
   __syncthreads();
 
   const float c2 = a.scale * 1.44269504088896341f;
-  for (int it = 0; it < ntiles; ++it) {
+  // One key tile; MASKED tiles evaluate the row and causal masks, the others
+  // (every row present, none past the causal limit) skip them.
+  auto tile = [&](int it, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     const int t0 = k_begin + it * kKeys, bf = it & 1;
     const int rows = min(kKeys, k_stop - t0);
     const uint16_t* kt = k_s[bf];
@@ -203,16 +223,9 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qf[ks], s[1], 0, 0, 0);
     }
     // Online softmax of this lane's query in the base-2 domain: with c2 = scale
-    // * log2(e), p = 2^(s c2 - m) where m is the running maximum of s c2. Masks
-    // (past the rows, causal) are evaluated only on tiles that need them.
-    const bool full = rows == kKeys && !(a.causal_tail && t0 + kKeys > tail0);
+    // * log2(e), p = 2^(s c2 - m) where m is the running maximum of s c2.
     float mx = -__builtin_inff();
-    if (full) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    } else {
+    if constexpr (MASKED) {
       // Visible keys of this lane's query: t0 .. t0 + lim - 1 (past the rows,
       // and past tail0 + t under the causal mask, are masked); element i of
       // block kb is key t0 + 32 kb + 8 (i / 4) + 4 h + i % 4.
@@ -225,8 +238,13 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
           mx = fmaxf(mx, s[kb][i]);
         }
       }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = pair_max32(mx);
     const float m_new = fmaxf(m, mx * c2);
     const float mb = m_new == -__builtin_inff() ? 0.f : m_new;
     const float corr = __builtin_amdgcn_exp2f(m - mb);
@@ -240,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
         sum += p;
       }
     }
-    sum += __shfl_xor(sum, 32, kWave);
+    sum = pair_sum32(sum);
     lsum = lsum * corr + sum;
     m = m_new;
     if (__ballot(corr != 1.f)) {
@@ -283,7 +301,12 @@ __global__ __launch_bounds__(256, 2) void chunk_kernel(logkv_attention_args a, c
       if (it + 2 < ntiles) load_tile(t0 + 2 * kKeys);
     }
     __syncthreads();
-  }
+  };
+  // Tiles below min(k_stop, tail0) (tail0 only under the causal mask) are full.
+  const int full_end = a.causal_tail ? min(k_stop, tail0) : k_stop;
+  const int n_full = min(ntiles, full_end > k_begin ? (full_end - k_begin) / kKeys : 0);
+  for (int it = 0; it < n_full; ++it) tile(it, std::false_type{});
+  for (int it = n_full; it < ntiles; ++it) tile(it, std::true_type{});
   if (!q_ok) return;
   if (splits > 1) {
     float* pp = part + ((static_cast<int64_t>(lane_ix) * splits + split) * nq + qi) * (a.dv + 2);
@@ -348,12 +371,13 @@ __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args
   gp(a.out)[b * a.o_sb + head * a.o_sh + t * a.o_st + d] = f32_to_bf16(acc / lsum);
 }
 
-// Key-range splits: enough blocks for about four per CU, at most one per
-// 1024 rows of the packed capacity.
+// Key-range splits: enough blocks for one resident round (kBlocksPerCu per
+// CU of the 256), at most one split per 1024 rows of the packed capacity.
 int chunk_splits(const logkv_attention_args& a) {
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   const int64_t blocks = static_cast<int64_t>((nq + kQRows - 1) / kQRows) * a.n_batch * a.n_groups;
-  int splits = static_cast<int>((1024 + blocks - 1) / blocks);
+  const int64_t target = 256 * kBlocksPerCu;
+  int splits = static_cast<int>((target + blocks - 1) / blocks);
   splits = std::min(splits, std::max(1, a.cap / 1024));
   return std::max(1, std::min(splits, 16));
 }
@@ -372,9 +396,10 @@ int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, 
   // Shapes with at most 5 steps and 2 dv blocks (head dim 64) take the
   // smaller kernel; every other shape runs the full 9 x 4 one on zero padding.
   if (a.dim <= 80 && a.dv <= 64)
-    hipLaunchKernelGGL((chunk_kernel<5, 2>), grid, dim3(256), 0, stream, a, width, splits, part);
+    hipLaunchKernelGGL((chunk_kernel<5, 2>), grid, dim3(kThreads), 0, stream, a, width, splits, part);
   else
-    hipLaunchKernelGGL((chunk_kernel<kMaxSteps, kMaxDvBlocks>), grid, dim3(256), 0, stream, a, width, splits, part);
+    hipLaunchKernelGGL((chunk_kernel<kMaxSteps, kMaxDvBlocks>), grid, dim3(kThreads), 0, stream, a, width, splits,
+                       part);
   if (splits > 1)
     hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a, part,
                        splits);
