@@ -520,6 +520,19 @@ def flush_workload(args, torch, np):
 # Config 1: one flush of one layer (the CPU reference configuration) on the GPU
 # ----------------------------------------------------------------------
 
+def config1_rows(torch, seed=7):
+    """Qwen3-0.6B KV shape (8 x 128), batch 1: K=12 centers N(0,1)*4 (bf16) and the timed flush's 2048
+    rows, 90% a center plus N(0, 0.5^2) noise, 10% outliers N(0,1)*12 (orphans); values N(0,1)."""
+    g = torch.Generator().manual_seed(seed)
+    centers = torch.randn(1, G, K, D, generator=g) * 4
+    label = torch.randint(0, K, (1, G, F), generator=g)
+    x = torch.gather(centers, 2, label[..., None].expand(-1, -1, -1, D)) + torch.randn(1, G, F, D, generator=g) * 0.5
+    far = torch.rand(1, G, F, generator=g) < 0.1
+    k = torch.where(far[..., None], torch.randn(1, G, F, D, generator=g) * 12, x).to(torch.bfloat16)
+    v = (torch.randn(1, G, F, D, generator=g)).to(torch.bfloat16)
+    return centers.to(torch.bfloat16), k, v
+
+
 def config1_setup(torch, dev, seed=7):
     """Qwen3-0.6B KV shape (8 x 128), batch 1, K=12 frozen centers N(0,1)*4 opened by a first flush of
     the 12 center rows at positions 0..11, then the timed flush: 2048 rows at positions 2048..4095,
@@ -533,14 +546,8 @@ def config1_setup(torch, dev, seed=7):
                                  semantic_clusters=True, cluster_k_max=K, semantic_s_h=64.0,
                                  semantic_flush_granularity=F, semantic_anchor_mode="mid",
                                  allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=D)
-    g = torch.Generator().manual_seed(seed)
-    centers = torch.randn(1, G, K, D, generator=g) * 4
-    label = torch.randint(0, K, (1, G, F), generator=g)
-    x = torch.gather(centers, 2, label[..., None].expand(-1, -1, -1, D)) + torch.randn(1, G, F, D, generator=g) * 0.5
-    far = torch.rand(1, G, F, generator=g) < 0.1
-    k = torch.where(far[..., None], torch.randn(1, G, F, D, generator=g) * 12, x).to(torch.bfloat16)
-    v = (torch.randn(1, G, F, D, generator=g)).to(torch.bfloat16)
-    return cache, centers.to(torch.bfloat16), k, v
+    centers, k, v = config1_rows(torch, seed)
+    return cache, centers, k, v
 
 
 def config1_workload(args, torch, np):
@@ -861,41 +868,87 @@ def host_info():
     return model, cores
 
 
-def cpu_baseline(seconds: float):
-    """The oracle (numpy restatement) of the headline flush for one layer on the host: Alpha / Beta,
-    route, commit and the pack of the new prefix, on flushes 3..16 of fresh 32K-token streams."""
+def _cpu_stream_flushes(cache_cls, seconds, threads):
+    """Headline flushes (3..16 of fresh 32K-token streams) of one layer through ``cache_cls`` on the
+    host with ``threads`` torch threads, until ``seconds`` of timed flush work: (tokens/s, flushes, s)."""
     import numpy as np
     import torch
 
-    from oracle import OracleCache
     from workloads import Mixture, rope_tables
 
-    torch.set_num_threads(1)
-    model, cores = host_info()
+    torch.set_num_threads(threads)
     cos, sin = (t.numpy() for t in rope_tables(N, D))
     mix = Mixture(1, G, D, clusters=K, seed=1)
-    rows = lambda: mix.rows(F).float().numpy()  # noqa: E731
-    n, t, streams = 0, 0.0, 0
+    n, t = 0, 0.0
     while t < seconds:
-        ora = OracleCache(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, exact_tokens=EXACT,
+        cache = cache_cls(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, exact_tokens=EXACT,
                           span_max=SPAN, beta_novelty=True, beta_adaptive=True, cos=cos, sin=sin)
-        streams += 1
         for j in range(STREAM_FLUSHES):
-            k, v = rows(), rows()
+            k, v = mix.rows(F).float().numpy(), mix.rows(F).float().numpy()
             pos = np.arange(j * F, (j + 1) * F)[None]
             t0 = time.perf_counter()
-            ora.flush_rows(k, v, pos, span_ends_for(j))
-            ora.pack(None, None)
+            cache.flush_rows(k, v, pos, span_ends_for(j))
+            cache.pack(None, None)
             if j >= PREP_FLUSHES:
                 t += time.perf_counter() - t0
                 n += 1
             if t >= seconds:
                 break
-    return {"value": F * n / t, "unit": "flushed tokens/s", "cores": 1, "kind": "port",
-            "host_cpu": model, "host_cores_available": cores, "torch_threads": torch.get_num_threads(),
-            "sample": f"oracle (numpy) Alpha/Beta + route + commit + pack of {n} flushes (flushes 3..16 of "
-                      f"{streams} 32K-token streams) of one layer, batch 1, 8 groups x 128, K=12, B=128, "
-                      f"exact pool 256, {F} rows each, {t:.1f} s, 1 thread"}
+    return F * n / t, n, t
+
+
+def _cpu_config1(threads, reps=5):
+    """Config 1 on the host: the one-layer flush of ``config1_rows`` from its restored state (the 12
+    centers opened by a first flush), median of ``reps`` flushes."""
+    import copy
+
+    import numpy as np
+    import torch
+
+    from oracle.torch_cpu import TorchCpuCache
+    from workloads import rope_tables
+
+    torch.set_num_threads(threads)
+    centers, k, v = config1_rows(torch)
+    cos, sin = (t.numpy() for t in rope_tables(N, D))
+    base = TorchCpuCache(1, G, N, D, D, B=B, recent_size=F, K=K, s_h=64.0, flush=F, cos=cos, sin=sin)
+    c = centers.float().numpy()
+    base.flush_rows(c, c, np.arange(K)[None])
+    times = []
+    for _ in range(reps):
+        cache = copy.deepcopy(base)
+        t0 = time.perf_counter()
+        cache.flush_rows(k.float().numpy(), v.float().numpy(), np.arange(F, 2 * F)[None])
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    return {"ms_per_flush": ms, "flushed_tokens_per_s": F / (ms * 1e-3), "threads": threads,
+            "clusters_alive_after": int(cache.alive.sum())}
+
+
+def cpu_baseline(seconds: float):
+    """The CPU baseline: the batched Torch-CPU port of the flush (oracle/torch_cpu.py, every ladder of
+    a flush appended level by level, Beta groups as tensor operations, bit-identical to the oracle) on
+    the host cores: the headline flush of one layer (Alpha / Beta, route, commit and the pack of the
+    new prefix, flushes 3..16 of fresh 32K-token streams) with every available core and with one
+    thread, and config 1's one-layer flush; the per-token numpy oracle is timed beside it."""
+    import torch
+
+    from oracle import OracleCache
+    from oracle.torch_cpu import TorchCpuCache
+
+    model, cores = host_info()
+    all_rate, all_n, all_t = _cpu_stream_flushes(TorchCpuCache, seconds * 0.4, cores)
+    one_rate, one_n, one_t = _cpu_stream_flushes(TorchCpuCache, seconds * 0.3, 1)
+    ora_rate, ora_n, ora_t = _cpu_stream_flushes(OracleCache, seconds * 0.2, 1)
+    config1 = _cpu_config1(cores)
+    threads = torch.get_num_threads()
+    return {"value": all_rate, "unit": "flushed tokens/s", "cores": cores, "kind": "port",
+            "value_1_thread": one_rate, "oracle_1_thread": ora_rate, "config1": config1,
+            "host_cpu": model, "host_cores_available": cores, "torch_threads": threads,
+            "sample": f"batched Torch-CPU port: Alpha/Beta + route + commit + pack of {all_n} flushes of one layer "
+                      f"(flushes 3..16 of 32K-token streams; batch 1, 8 groups x 128, K=12, B=128, exact pool 256, "
+                      f"{F} rows each) in {all_t:.1f} s on {cores} threads; {one_n} flushes in {one_t:.1f} s on 1 "
+                      f"thread; the per-token numpy oracle: {ora_n} flushes in {ora_t:.1f} s on 1 thread"}
 
 
 # ----------------------------------------------------------------------
