@@ -178,6 +178,9 @@ int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late,
   b.old_ids = reinterpret_cast<int32_t*>(take(lanes * logkv::kMaxClusters * 4));
   b.jobs = reinterpret_cast<int32_t*>(take(lanes * logkv::kMaxClusters * 8));
   b.n_jobs = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.image_stride = logkv::unified_image_stride(static_cast<int>(M));
+  b.image = take(lanes * b.image_stride);
+  b.ctl = reinterpret_cast<logkv::LaneCtl*>(take(lanes * static_cast<int64_t>(sizeof(logkv::LaneCtl))));
   if (u) *u = b;
   return off;
 }

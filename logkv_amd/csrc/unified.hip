@@ -9,10 +9,11 @@
 //   2. budget: old live clusters and candidates merge until at most K remain;
 //   3. old-old merges (ladder re-appends, in ladder.hip) and the commit of the
 //      rows into their final clusters (the attach commit).
-// One workgroup per lane runs every round of a stage, with the per-row state
-// (cached row minima, masses, radii, flags, pair table) in LDS and the squared
-// distance matrix in HBM; a round's phases are separated by barriers, so a
-// stage is one launch with no host round trip. Every element operation keeps
+// A round's plan runs on one workgroup per lane with the per-row state (cached
+// row minima, masses, radii, flags, pair table) in LDS; its Lance-Williams
+// updates and rescans, which read and write the squared distance matrix in
+// HBM, run on many workgroups per lane; the state passes between the launches
+// through a per-lane global image, and no launch waits on the host. Every element operation keeps
 // the reference's float32 order (_unified_pair_cost, _merge); the initial
 // squared distances and the radius check's exact distances are canonical
 // wave sums of squared differences (common.hpp).
@@ -177,216 +178,398 @@ __global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu,
   }
 }
 
-// All rounds of one stage for one lane (litgpt/log_kv_cache.py:490-637).
+// ---------------------------------------------------------------------------
+// One stage's rounds (litgpt/log_kv_cache.py:490-637). A round is three
+// phases: the plan (proposals, exact radius check, the stable sort by cost,
+// merges of masses, radii and centers), one block per lane with the lane's row
+// state in LDS; the Lance-Williams rows of the kept rows with their cost
+// pushes, and the rescans of the rows whose partner merged or whose proposal
+// was rejected, both spread over many blocks per lane. Between launches the
+// row state lives in a per-lane global image with the LDS layout. A fixed
+// number of rounds is enqueued (a finished lane's launches return at once);
+// the finish kernel runs any rounds left on one block per lane, so nothing
+// waits on the host. Every element operation is the one-block reducer's.
+
+constexpr int kPhaseThreads = 256;
+constexpr int kPhaseWaves = kPhaseThreads / kWave;
+constexpr int kPhaseBlocks = 64;      // blocks per lane of the Lance-Williams / rescan phases
+constexpr int kLwChunk = 256;         // columns per Lance-Williams work item
+constexpr int kPipelinedRounds = 40;  // rounds enqueued as phase launches before the finish kernel
+
+__device__ inline ReduceLds image_of(const ReduceArgs& a, int lane) {
+  return carve_lds(a.image + static_cast<int64_t>(lane) * a.image_stride, a.M);
+}
+
+// Proposals .. merges of one round on state `s` (the block's LDS). Returns the
+// round's merge count; sh[0] = count, sh[1] = ntrace on entry and exit.
 template <bool LIMIT>
-__global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceArgs a) {
-  extern __shared__ __align__(16) uint8_t dyn[];
-  __shared__ int s_count, s_nprop, s_nvalid, s_ntrace;
-  const int lane = blockIdx.x, M = a.M, D = a.D, t = threadIdx.x, l = lane_id(), w = wave_id();
-  const int n = a.count[lane];
-  const ReduceLds s = carve_lds(dyn, M);
+__device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, int n, float limit, int* sh,
+                           int* s_nprop, int* s_nvalid, int& nprop_out, int& n_ok_out) {
+  const int M = a.M, D = a.D, t = threadIdx.x, l = lane_id(), w = wave_id();
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   float* mu = a.mu + static_cast<int64_t>(lane) * M * D;
-  const float limit = LIMIT ? a.limit[lane] : 0.f;
   int32_t* trace = a.trace + static_cast<int64_t>(lane) * M * 2;
-  for (int i = t; i < M; i += kReduceThreads) {
+  for (int i = t; i < M; i += kReduceThreads) s.flags[i] &= kAlive;
+  // Proposals: every row's cached partner; a pair is proposed by its lower row.
+  for (int r = t; r < M; r += kReduceThreads) {
+    int bst = static_cast<int>(static_cast<uint32_t>(s.packed[r]) ^ static_cast<uint32_t>(r));
+    bst = bst < 0 ? 0 : (bst > M - 1 ? M - 1 : bst);
+    s.best[r] = static_cast<int16_t>(bst);
+  }
+  if (t == 0) {
+    *s_nprop = 0;
+    *s_nvalid = 0;
+  }
+  __syncthreads();
+  int mine = 0;
+  for (int r = t; r < n; r += kReduceThreads) {
+    const int bst = s.best[r];
+    const bool v = (s.flags[r] & kAlive) && r < bst && s.best[bst] == r && key_cost(s.packed[r]) < __builtin_inff();
+    if (v) {
+      s.flags[r] |= kValid;
+      ++mine;
+    }
+  }
+  if (mine) atomicAdd(s_nprop, mine);
+  __syncthreads();
+  const int nprop = *s_nprop;
+  if (LIMIT) {
+    // Exact radius check of every proposal (litgpt/log_kv_cache.py:503-525).
+    for (int r = w; r < n; r += kReduceWaves) {
+      if (!(s.flags[r] & kValid)) continue;
+      const int o = s.best[r];
+      const float* xr = mu + static_cast<int64_t>(r) * D;
+      const float* xo = mu + static_cast<int64_t>(o) * D;
+      float acc = 0.f;
+      for (int q = 0; q * kWave < D; ++q) {
+        const int d = l + q * kWave;
+        const float diff = feat_or_zero(gp(xr), d, D) - feat_or_zero(gp(xo), d, D);
+        acc = q == 0 ? diff * diff : acc + diff * diff;
+      }
+      const float exact2 = wave_sum0(acc);
+      if (l == 0) {
+        const float exact = sqrtf(exact2);
+        const float ma = s.mass[r], mb = s.mass[o];
+        const float sum = ma + mb;
+        const float denom = sum < 1.f ? 1.f : sum;
+        const float x = s.radius[r] + (mb / denom) * exact, y = s.radius[o] + (ma / denom) * exact;
+        const float verified = x < y ? y : x;
+        a.bound[static_cast<int64_t>(lane) * M + r] = verified;
+        if (verified > limit) {
+          dist[static_cast<int64_t>(r) * M + o] = exact2;
+          dist[static_cast<int64_t>(o) * M + r] = exact2;
+          s.flags[r] = static_cast<uint8_t>((s.flags[r] | kRejected) & ~kValid);
+          s.flags[o] |= kRejected;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // Surviving proposals sorted by (cost, row) (a stable argsort by cost).
+  for (int r = t; r < n; r += kReduceThreads) {
+    if (s.flags[r] & kValid) {
+      const int at = atomicAdd(s_nvalid, 1);
+      s.keys[at] = (s.packed[r] & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
+    }
+  }
+  __syncthreads();
+  const int nv = *s_nvalid;
+  const int width = pow2_at_least(nv > 0 ? nv : 1);
+  for (int i = nv + t; i < width; i += kReduceThreads) s.keys[i] = ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= width; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < width; i += kReduceThreads) {
+        const int p = i ^ stride;
+        if (p > i) {
+          const bool up = (i & size) == 0;
+          const uint64_t x = s.keys[i], y = s.keys[p];
+          if ((x > y) == up) {
+            s.keys[i] = y;
+            s.keys[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int budget = sh[0] - a.target;
+  const int n_ok = nv < budget ? nv : (budget > 0 ? budget : 0);
+  // Merges: pair scalars, masses, radii, centers (litgpt/log_kv_cache.py:589-606).
+  for (int p = t; p < n_ok; p += kReduceThreads) {
+    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+    const float ma = s.mass[ra], mb = s.mass[rb];
+    const float dab = dist[static_cast<int64_t>(ra) * M + rb];
+    const float total = ma + mb;
+    const float alpha = ma / total, beta = mb / total;
+    s.p_alpha[p] = alpha;
+    s.p_beta[p] = beta;
+    s.p_shift[p] = alpha * beta * dab;
+    s.pair_of[ra] = static_cast<int16_t>(p);
+    s.flags[ra] |= kKeep | kMerged;
+    s.flags[rb] = static_cast<uint8_t>((s.flags[rb] | kMerged) & ~kAlive);
+    s.mass[ra] = total;
+    s.mass[rb] = 0.f;
+    if (LIMIT) s.radius[ra] = a.bound[static_cast<int64_t>(lane) * M + ra];
+    const float scale = total < 1.f ? 1.f : total;
+    float* ua = mu + static_cast<int64_t>(ra) * D;
+    const float* ub = mu + static_cast<int64_t>(rb) * D;
+    for (int d = 0; d < D; ++d) ua[d] = (ma * ua[d] + mb * ub[d]) / scale;
+    trace[2 * (sh[1] + p)] = ra;
+    trace[2 * (sh[1] + p) + 1] = rb;
+  }
+  __syncthreads();
+  nprop_out = nprop;
+  n_ok_out = n_ok;
+}
+
+// Lance-Williams updates of merge p's kept row over columns [c0, c1) (one wave,
+// litgpt/log_kv_cache.py:607-626): the row and its mirror, each column's cost
+// pushed into the column's cached minimum; returns the row's minimum key over
+// those columns.
+template <bool LIMIT>
+__device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, int p, int c0, int c1, float limit) {
+  const int l = lane_id();
+  const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+  const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
+  const float total = s.mass[ra], rad = s.radius[ra];
+  float* row_a = dist + static_cast<int64_t>(ra) * M;
+  const float* row_b = dist + static_cast<int64_t>(rb) * M;
+  uint64_t rmin = kInfKey;
+  for (int c = c0 + l; c < c1; c += kWave) {
+    const uint8_t fl = s.flags[c];
+    const bool alive_c = fl & kAlive, keep_c = fl & kKeep;
+    const float x_aa = row_a[c], x_ba = row_b[c];
+    float nw = alpha * x_aa + beta * x_ba - shift;
+    if (keep_c && c != ra) {
+      const int q = s.best[c], pc = s.pair_of[c];
+      const float qa = s.p_alpha[pc], qb = s.p_beta[pc], qs = s.p_shift[pc];
+      const float x_ab = row_a[q], x_bb = row_b[q];
+      const float own = qa * nw + qb * (alpha * x_ab + beta * x_bb - shift) - qs;
+      const float other = alpha * (qa * x_aa + qb * x_ab - qs) + beta * (qa * x_ba + qb * x_bb - qs) - shift;
+      nw = ra < c ? own : other;
+    }
+    nw = nw < 0.f ? 0.f : nw;
+    if (c == ra) nw = 0.f;
+    if (alive_c) {
+      row_a[c] = nw;
+      if (!keep_c) dist[static_cast<int64_t>(c) * M + ra] = nw;
+    }
+    const bool valid = alive_c && c != ra;
+    const float cost = ward_cost<LIMIT>(nw, total, s.mass[c], rad, s.radius[c], limit, valid);
+    const uint64_t k = pack_cost(cost, ra ^ c);
+    if (cost < __builtin_inff() && !keep_c) atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]),
+                                                      static_cast<unsigned long long>(k));
+    rmin = k < rmin ? k : rmin;
+  }
+  return wave_min_u64(rmin);
+}
+
+// A row rescans when its partner merged or its proposal was rejected.
+__device__ __forceinline__ bool is_dirty(const ReduceLds& s, int r) {
+  const uint8_t fl = s.flags[r];
+  return (fl & kAlive) && !(fl & kKeep) && ((s.flags[s.best[r]] & kMerged) || (fl & kRejected));
+}
+
+// Stage setup: every lane's image (masses, zero radii, live flags, infinite
+// keys) and round bookkeeping.
+__global__ __launch_bounds__(kPhaseThreads) void reduce_init_kernel(ReduceArgs a) {
+  const int lane = blockIdx.y, M = a.M;
+  const int n = a.count[lane];
+  const ReduceLds s = image_of(a, lane);
+  for (int i = blockIdx.x * kPhaseThreads + threadIdx.x; i < M; i += gridDim.x * kPhaseThreads) {
     s.mass[i] = i < n ? a.mass[static_cast<int64_t>(lane) * M + i] : 0.f;
     s.radius[i] = 0.f;
     s.flags[i] = i < n ? kAlive : 0;
     s.packed[i] = kInfKey;
     s.best[i] = static_cast<int16_t>(i);
   }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    LaneCtl c{};
+    c.count = n;
+    c.active = n > a.target ? 1 : 0;
+    a.ctl[lane] = c;
+  }
+}
+
+// Every live row's initial cached minimum, rows spread over the lane's blocks.
+template <bool LIMIT>
+__global__ __launch_bounds__(kPhaseThreads) void reduce_scan_kernel(ReduceArgs a) {
+  const int lane = blockIdx.y, M = a.M;
+  if (!a.ctl[lane].active) return;
+  const int n = a.count[lane];
+  const ReduceLds s = image_of(a, lane);
+  const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
+  for (int r = gw; r < n; r += nw) {
+    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
+    if (lane_id() == 0) s.packed[r] = k;
+  }
+}
+
+// Round phase 1: the plan on one block per lane (image -> LDS -> image). Kept
+// rows' keys are reset to +inf for the Lance-Williams phase's minima.
+template <bool LIMIT>
+__global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs a) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int sh[2], s_nprop, s_nvalid;
+  const int lane = blockIdx.x, M = a.M, t = threadIdx.x;
+  LaneCtl ctl = a.ctl[lane];
+  if (!ctl.active) {
+    if (t == 0) a.ctl[lane].work = 0;
+    return;
+  }
+  const int n = a.count[lane];
+  const size_t bytes = reduce_lds_bytes(M);
+  const uint8_t* img = a.image + static_cast<int64_t>(lane) * a.image_stride;
+  for (size_t i = t * 16; i + 16 <= bytes; i += kReduceThreads * 16)
+    *reinterpret_cast<uint4*>(dyn + i) = *reinterpret_cast<const uint4*>(img + i);
   if (t == 0) {
-    s_count = n;
-    s_ntrace = 0;
+    sh[0] = ctl.count;
+    sh[1] = ctl.ntrace;
   }
   __syncthreads();
-  bool stuck = false;
-  if (n > a.target) {
+  const ReduceLds s = carve_lds(dyn, M);
+  int nprop, n_ok;
+  plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok);
+  for (int p = t; p < n_ok; p += kReduceThreads) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = kInfKey;
+  __syncthreads();
+  uint8_t* out = a.image + static_cast<int64_t>(lane) * a.image_stride;
+  for (size_t i = t * 16; i + 16 <= bytes; i += kReduceThreads * 16)
+    *reinterpret_cast<uint4*>(out + i) = *reinterpret_cast<const uint4*>(dyn + i);
+  if (t == 0) {
+    const int count = ctl.count - n_ok;
+    const bool remaining = count > a.target;
+    ctl.count = count;
+    ctl.ntrace += n_ok;
+    ctl.n_ok = n_ok;
+    ctl.nprop = nprop;
+    ctl.work = nprop > 0 ? 1 : 0;
+    ctl.active = remaining && nprop > 0 ? 1 : 0;
+    ctl.stuck = remaining && nprop == 0 ? 1 : 0;
+    ctl.rounds += 1;
+    if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
+    a.ctl[lane] = ctl;
+  }
+}
+
+// Round phase 2: Lance-Williams rows of the round's kept rows, (merge, column
+// chunk) items spread over the lane's blocks.
+template <bool LIMIT>
+__global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) {
+  const int lane = blockIdx.y, M = a.M;
+  const LaneCtl ctl = a.ctl[lane];
+  if (!ctl.work) return;
+  const int n = a.count[lane];
+  const ReduceLds s = image_of(a, lane);
+  float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  const int chunks = (n + kLwChunk - 1) / kLwChunk, items = ctl.n_ok * chunks;
+  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
+  for (int it = gw; it < items; it += nw) {
+    const int p = it / chunks, ch = it - p * chunks;
+    const int c0 = ch * kLwChunk, c1 = min(n, c0 + kLwChunk);
+    const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, c0, c1, limit);
+    if (lane_id() == 0)
+      atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)]),
+                static_cast<unsigned long long>(rmin));
+  }
+}
+
+// Round phase 3: rescans of the dirty rows, spread over the lane's blocks.
+template <bool LIMIT>
+__global__ __launch_bounds__(kPhaseThreads) void reduce_rescan_kernel(ReduceArgs a) {
+  const int lane = blockIdx.y, M = a.M;
+  if (!a.ctl[lane].work) return;
+  const int n = a.count[lane];
+  const ReduceLds s = image_of(a, lane);
+  const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
+  for (int r = gw; r < n; r += nw) {
+    if (!is_dirty(s, r)) continue;
+    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
+    if (lane_id() == 0) s.packed[r] = k;
+  }
+}
+
+// The stage's end on one block per lane: any rounds left (one block runs
+// every phase, the image in LDS), then the survivors, merge count and stuck
+// flag.
+template <bool LIMIT>
+__global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArgs a) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int sh[2], s_nprop, s_nvalid;
+  const int lane = blockIdx.x, M = a.M, t = threadIdx.x, l = lane_id(), w = wave_id();
+  const int n = a.count[lane];
+  LaneCtl ctl = a.ctl[lane];
+  const size_t bytes = reduce_lds_bytes(M);
+  const uint8_t* img = a.image + static_cast<int64_t>(lane) * a.image_stride;
+  for (size_t i = t * 16; i + 16 <= bytes; i += kReduceThreads * 16)
+    *reinterpret_cast<uint4*>(dyn + i) = *reinterpret_cast<const uint4*>(img + i);
+  if (t == 0) {
+    sh[0] = ctl.count;
+    sh[1] = ctl.ntrace;
+  }
+  __syncthreads();
+  const ReduceLds s = carve_lds(dyn, M);
+  float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  while (ctl.active) {
+    int nprop, n_ok;
+    plan_phase<LIMIT>(s, a, lane, n, limit, sh, &s_nprop, &s_nvalid, nprop, n_ok);
+    for (int p = w; p < n_ok; p += kReduceWaves) {
+      const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, 0, n, limit);
+      if (l == 0) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = rmin;
+    }
+    __syncthreads();
     for (int r = w; r < n; r += kReduceWaves) {
+      if (!is_dirty(s, r)) continue;
       const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
       if (l == 0) s.packed[r] = k;
     }
     __syncthreads();
-    for (int round = 0; round < 2 * M + 7; ++round) {
-      // Proposals: every row's cached partner; a pair is proposed by its lower row.
-      for (int r = t; r < M; r += kReduceThreads) {
-        int bst = static_cast<int>(static_cast<uint32_t>(s.packed[r]) ^ static_cast<uint32_t>(r));
-        bst = bst < 0 ? 0 : (bst > M - 1 ? M - 1 : bst);
-        s.best[r] = static_cast<int16_t>(bst);
-      }
-      if (t == 0) {
-        s_nprop = 0;
-        s_nvalid = 0;
-      }
-      __syncthreads();
-      int mine = 0;
-      for (int r = t; r < n; r += kReduceThreads) {
-        const int bst = s.best[r];
-        const bool v = (s.flags[r] & kAlive) && r < bst && s.best[bst] == r && key_cost(s.packed[r]) < __builtin_inff();
-        if (v) {
-          s.flags[r] |= kValid;
-          ++mine;
-        }
-      }
-      if (mine) atomicAdd(&s_nprop, mine);
-      __syncthreads();
-      const int nprop = s_nprop;
-      if (LIMIT) {
-        // Exact radius check of every proposal (litgpt/log_kv_cache.py:503-525).
-        for (int r = w; r < n; r += kReduceWaves) {
-          if (!(s.flags[r] & kValid)) continue;
-          const int o = s.best[r];
-          const float* xr = mu + static_cast<int64_t>(r) * D;
-          const float* xo = mu + static_cast<int64_t>(o) * D;
-          float acc = 0.f;
-          for (int q = 0; q * kWave < D; ++q) {
-            const int d = l + q * kWave;
-            const float diff = feat_or_zero(gp(xr), d, D) - feat_or_zero(gp(xo), d, D);
-            acc = q == 0 ? diff * diff : acc + diff * diff;
-          }
-          const float exact2 = wave_sum0(acc);
-          if (l == 0) {
-            const float exact = sqrtf(exact2);
-            const float ma = s.mass[r], mb = s.mass[o];
-            const float sum = ma + mb;
-            const float denom = sum < 1.f ? 1.f : sum;
-            const float x = s.radius[r] + (mb / denom) * exact, y = s.radius[o] + (ma / denom) * exact;
-            const float verified = x < y ? y : x;
-            a.bound[static_cast<int64_t>(lane) * M + r] = verified;
-            if (verified > limit) {
-              dist[static_cast<int64_t>(r) * M + o] = exact2;
-              dist[static_cast<int64_t>(o) * M + r] = exact2;
-              s.flags[r] = static_cast<uint8_t>((s.flags[r] | kRejected) & ~kValid);
-              s.flags[o] |= kRejected;
-            }
-          }
-        }
-        __syncthreads();
-      }
-      // Surviving proposals sorted by (cost, row) (a stable argsort by cost).
-      for (int r = t; r < n; r += kReduceThreads) {
-        if (s.flags[r] & kValid) {
-          const int at = atomicAdd(&s_nvalid, 1);
-          s.keys[at] = (s.packed[r] & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
-        }
-      }
-      __syncthreads();
-      const int nv = s_nvalid;
-      const int width = pow2_at_least(nv > 0 ? nv : 1);
-      for (int i = nv + t; i < width; i += kReduceThreads) s.keys[i] = ~0ull;
-      __syncthreads();
-      for (int size = 2; size <= width; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int i = t; i < width; i += kReduceThreads) {
-            const int p = i ^ stride;
-            if (p > i) {
-              const bool up = (i & size) == 0;
-              const uint64_t x = s.keys[i], y = s.keys[p];
-              if ((x > y) == up) {
-                s.keys[i] = y;
-                s.keys[p] = x;
-              }
-            }
-          }
-          __syncthreads();
-        }
-      }
-      const int budget = s_count - a.target;
-      const int n_ok = nv < budget ? nv : (budget > 0 ? budget : 0);
-      // Merges: pair scalars, masses, radii, centers (litgpt/log_kv_cache.py:589-606).
-      for (int p = t; p < n_ok; p += kReduceThreads) {
-        const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
-        const float ma = s.mass[ra], mb = s.mass[rb];
-        const float dab = dist[static_cast<int64_t>(ra) * M + rb];
-        const float total = ma + mb;
-        const float alpha = ma / total, beta = mb / total;
-        s.p_alpha[p] = alpha;
-        s.p_beta[p] = beta;
-        s.p_shift[p] = alpha * beta * dab;
-        s.pair_of[ra] = static_cast<int16_t>(p);
-        s.flags[ra] |= kKeep | kMerged;
-        s.flags[rb] = static_cast<uint8_t>((s.flags[rb] | kMerged) & ~kAlive);
-        s.mass[ra] = total;
-        s.mass[rb] = 0.f;
-        if (LIMIT) s.radius[ra] = a.bound[static_cast<int64_t>(lane) * M + ra];
-        const float scale = total < 1.f ? 1.f : total;
-        float* ua = mu + static_cast<int64_t>(ra) * D;
-        const float* ub = mu + static_cast<int64_t>(rb) * D;
-        for (int d = 0; d < D; ++d) ua[d] = (ma * ua[d] + mb * ub[d]) / scale;
-        trace[2 * (s_ntrace + p)] = ra;
-        trace[2 * (s_ntrace + p) + 1] = rb;
-      }
-      __syncthreads();
-      // Lance-Williams rows of the kept rows, mirrored into the other live rows,
-      // costs pushed into their cached minima (litgpt/log_kv_cache.py:607-626).
-      for (int p = w; p < n_ok; p += kReduceWaves) {
-        const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
-        const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
-        const float total = s.mass[ra], rad = s.radius[ra];
-        float* row_a = dist + static_cast<int64_t>(ra) * M;
-        const float* row_b = dist + static_cast<int64_t>(rb) * M;
-        uint64_t rmin = kInfKey;
-        for (int c = l; c < n; c += kWave) {
-          const uint8_t fl = s.flags[c];
-          const bool alive_c = fl & kAlive, keep_c = fl & kKeep;
-          const float x_aa = row_a[c], x_ba = row_b[c];
-          float nw = alpha * x_aa + beta * x_ba - shift;
-          if (keep_c && c != ra) {
-            const int q = s.best[c], pc = s.pair_of[c];
-            const float qa = s.p_alpha[pc], qb = s.p_beta[pc], qs = s.p_shift[pc];
-            const float x_ab = row_a[q], x_bb = row_b[q];
-            const float own = qa * nw + qb * (alpha * x_ab + beta * x_bb - shift) - qs;
-            const float other = alpha * (qa * x_aa + qb * x_ab - qs) + beta * (qa * x_ba + qb * x_bb - qs) - shift;
-            nw = ra < c ? own : other;
-          }
-          nw = nw < 0.f ? 0.f : nw;
-          if (c == ra) nw = 0.f;
-          if (alive_c) {
-            row_a[c] = nw;
-            if (!keep_c) dist[static_cast<int64_t>(c) * M + ra] = nw;
-          }
-          const bool valid = alive_c && c != ra;
-          const float cost = ward_cost<LIMIT>(nw, total, s.mass[c], rad, s.radius[c], limit, valid);
-          const uint64_t k = pack_cost(cost, ra ^ c);
-          if (cost < __builtin_inff() && !keep_c) atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]),
-                                                            static_cast<unsigned long long>(k));
-          rmin = k < rmin ? k : rmin;
-        }
-        rmin = wave_min_u64(rmin);
-        if (l == 0) s.packed[ra] = rmin;
-      }
-      __syncthreads();
-      // Rows whose partner merged or whose proposal was rejected rescan.
-      for (int r = w; r < n; r += kReduceWaves) {
-        const uint8_t fl = s.flags[r];
-        const bool dirty = (fl & kAlive) && !(fl & kKeep) && ((s.flags[s.best[r]] & kMerged) || (fl & kRejected));
-        if (!dirty) continue;
-        const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
-        if (l == 0) s.packed[r] = k;
-      }
-      __syncthreads();
-      const int count = s_count - n_ok;
-      for (int i = t; i < M; i += kReduceThreads) s.flags[i] &= kAlive;
-      __syncthreads();
-      if (t == 0) {
-        s_count = count;
-        s_ntrace += n_ok;
-      }
-      const bool remaining = count > a.target;
-      if (!(remaining && nprop > 0)) {
-        stuck = remaining && nprop == 0;
-        break;
-      }
-      __syncthreads();
+    const int count = ctl.count - n_ok;
+    const bool remaining = count > a.target;
+    ctl.count = count;
+    ctl.ntrace += n_ok;
+    ctl.stuck = remaining && nprop == 0 ? 1 : 0;
+    ctl.active = remaining && nprop > 0 ? 1 : 0;
+    ctl.rounds += 1;
+    if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
+    if (t == 0) {
+      sh[0] = ctl.count;
+      sh[1] = ctl.ntrace;
     }
+    __syncthreads();
   }
-  __syncthreads();
-  for (int i = t; i < M; i += kReduceThreads) a.alive_out[static_cast<int64_t>(lane) * M + i] = s.flags[i] & kAlive;
+  for (int i = t; i < M; i += kReduceThreads)
+    a.alive_out[static_cast<int64_t>(lane) * M + i] = (s.flags[i] & kAlive) ? 1 : 0;
   if (t == 0) {
-    a.n_trace[lane] = s_ntrace;
-    a.stuck[lane] = stuck ? 1 : 0;
+    a.n_trace[lane] = ctl.ntrace;
+    a.stuck[lane] = ctl.stuck;
   }
+}
+
+// One stage: setup, the pipelined rounds, the finish.
+template <bool LIMIT>
+int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
+  const size_t lds = reduce_lds_bytes(a.M);
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_plan_kernel<LIMIT>), lds) ||
+      !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_finish_kernel<LIMIT>), lds))
+    return LOGKV_ERUNTIME;
+  const dim3 phase(kPhaseBlocks, lanes);
+  hipLaunchKernelGGL(reduce_init_kernel, dim3(std::max(1, std::min(16, a.M / kPhaseThreads)), lanes),
+                     dim3(kPhaseThreads), 0, stream, a);
+  hipLaunchKernelGGL(reduce_scan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
+  for (int round = 0; round < kPipelinedRounds; ++round) {
+    hipLaunchKernelGGL(reduce_plan_kernel<LIMIT>, dim3(lanes), dim3(kReduceThreads), lds, stream, a);
+    hipLaunchKernelGGL(reduce_lw_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
+    hipLaunchKernelGGL(reduce_rescan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
+  }
+  hipLaunchKernelGGL(reduce_finish_kernel<LIMIT>, dim3(lanes), dim3(kReduceThreads), lds, stream, a);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
 // Leaf -> compact surviving row (litgpt/log_kv_cache.py:3553-3568): parents
@@ -563,15 +746,12 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   const int lanes = c.n_batch * c.n_groups, M = u.M, D = u.D;
   int rc = launch_order(r, c.n_batch, ws.order, nullptr, stream);
   if (rc) return rc;
-  const size_t lds = reduce_lds_bytes(M);
-  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_kernel<true>), lds) ||
-      !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_kernel<false>), lds))
-    return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(load_nodes_kernel, dim3(std::max(1, std::min(64, M * D / 4096)), lanes), dim3(256), 0, stream, r,
                      c.n_groups, u);
   hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu1, u.count1, u.dist, M, D);
-  ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound};
-  hipLaunchKernelGGL(reduce_kernel<true>, dim3(lanes), dim3(kReduceThreads), lds, stream, a1);
+  ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
+                u.image, u.image_stride, u.ctl};
+  if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
   const size_t lab_lds = static_cast<size_t>(M) * 8;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive1, u.trace1, u.n_trace1, u.count1,
@@ -580,8 +760,8 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
   hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu2, u.count2, u.dist, M, D);
   ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
-                u.bound};
-  hipLaunchKernelGGL(reduce_kernel<false>, dim3(lanes), dim3(kReduceThreads), lds, stream, a2);
+                u.bound, u.image, u.image_stride, u.ctl};
+  if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
                      M, u.label2, u.n_roots2);
   hipLaunchKernelGGL(final_kernel, dim3(lanes), dim3(256), 0, stream, c, r, u, ws.order, ws.assign);
@@ -589,6 +769,8 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
 }
 
 size_t unified_reduce_lds(int M) { return reduce_lds_bytes(M); }
+
+int64_t unified_image_stride(int M) { return (static_cast<int64_t>(reduce_lds_bytes(M)) + 255) / 256 * 256; }
 
 __global__ __launch_bounds__(256) void summary_kernel(const int32_t* __restrict__ n_jobs,
                                                       const int32_t* __restrict__ stuck, int lanes, int tokens,

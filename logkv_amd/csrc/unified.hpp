@@ -7,6 +7,19 @@ namespace logkv {
 
 constexpr int kMaxNodes = 4608;   // rows of a flush + K (one lane's reducer state lives in LDS)
 
+// Round bookkeeping of one lane's reducer stage (global memory, read by every
+// phase launch of a round).
+struct LaneCtl {
+  int32_t count;    // live nodes
+  int32_t ntrace;   // merges so far
+  int32_t n_ok;     // merges of the current round
+  int32_t nprop;    // mutual proposals of the current round
+  int32_t active;   // 1: another round follows
+  int32_t work;     // 1: the current round's Lance-Williams / rescan phases have work
+  int32_t stuck;    // 1: clusters above the target and no pair left
+  int32_t rounds;   // rounds run
+};
+
 // Arguments of one reducer stage over `lanes` lanes of M padded nodes.
 struct ReduceArgs {
   float* dist;            // [lanes, M, M] squared distances (updated in place)
@@ -21,6 +34,9 @@ struct ReduceArgs {
   int32_t* n_trace;       // [lanes]
   int32_t* stuck;         // [lanes] 1: clusters above the target and no pair left
   float* bound;           // [lanes, M] scratch: verified radius bounds of a round
+  uint8_t* image;         // [lanes, image_stride] the reducer state (the LDS layout) between launches
+  int64_t image_stride;
+  LaneCtl* ctl;           // [lanes]
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -51,11 +67,15 @@ struct UnifiedBufs {
   int32_t* old_ids;       // [lanes, kMaxClusters]
   int32_t* jobs;          // [lanes, kMaxClusters, 2] old-old merges (keep, retire) in order
   int32_t* n_jobs;        // [lanes]
+  uint8_t* image;         // [lanes, image_stride] reducer state between the round launches
+  int64_t image_stride;
+  LaneCtl* ctl;           // [lanes]
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
                         hipStream_t stream);
 size_t unified_reduce_lds(int M);
+int64_t unified_image_stride(int M);
 // summary[0] = most old-old merges of a lane, summary[1] = 1 if a budget stage found no pair.
 int launch_unified_summary(const LadderArgs& c, const UnifiedBufs& u, int32_t* summary, int tokens,
                            hipStream_t stream);
