@@ -136,46 +136,165 @@ __global__ __launch_bounds__(256) void load_nodes_kernel(RowsArgs r, int n_group
   if (blockIdx.x == 0 && threadIdx.x == 0) u.count1[lane] = n;
 }
 
-// Squared distances of one row i against columns j > i (canonical wave sums of
-// squared differences, four columns folded at once), mirrored; zero diagonal.
-// Block = 4 waves per (row, lane).
-__global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu, const int32_t* __restrict__ count,
-                                                   float* __restrict__ dist, int M, int D) {
-  const int lane = blockIdx.y, i = blockIdx.x, n = count[lane];
-  if (i >= n) return;
-  const float* base = mu + static_cast<int64_t>(lane) * M * D;
-  float* dl = dist + static_cast<int64_t>(lane) * M * M;
-  const int l = lane_id(), w = wave_id();
-  float xi[kMaxDim / kWave];
+// Squared distances of every pair of a lane's nodes, as the canonical wave sum
+// of squared differences of the one-row-per-wave form: leaf l adds the
+// squared differences of features l, l + 64, ... in order, and the 64 leaves
+// fold as a halving tree (l with l + 32, then + 16, ..., + 1). Here a thread
+// evaluates whole pairs: the tree depth first (the left subtree, lower leaf
+// indices, before the right), which is the same sum. A block takes a tile of
+// kDistRows rows x kDistCols columns (features staged in LDS, feature-major),
+// a thread kDistR x kDistC pairs; every pair (i, j) with i < j < n is written
+// to both (i, j) and (j, i), the diagonal is zero. Tiles wholly below the
+// diagonal or past the node count return at once.
+constexpr int kDistRows = 32, kDistCols = 64, kDistR = 2, kDistC = 4;
+constexpr int kDistRowLd = kDistRows + 1, kDistColLd = kDistCols + 1;
+
+template <int J>
+struct DistTile {
+  const float* xs;   // [64 J][kDistRowLd]
+  const float* ys;   // [64 J][kDistColLd]
+  int r0, c0;        // the thread's first row / column in the tile
+  // Leaf `leaf` of every pair of the thread: sum over q < J of (x - y)^2 at
+  // feature leaf + 64 q, in q order.
+  __device__ __forceinline__ void leaf(int leaf, float (&out)[kDistR * kDistC]) const {
 #pragma unroll
-  for (int q = 0; q < kMaxDim / kWave; ++q) xi[q] = feat_or_zero(gp(base + static_cast<int64_t>(i) * D), l + q * kWave, D);
-  if (w == 0 && l == 0) dl[static_cast<int64_t>(i) * M + i] = 0.f;
-  const int J = (D + kWave - 1) / kWave;
-  for (int j0 = i + 1 + 4 * w; j0 < n; j0 += 16) {
-    float s[4];
+    for (int q = 0; q < J; ++q) {
+      float x[kDistR], y[kDistC];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = min(j0 + c, n - 1);
-      const LOGKV_G float* xj = gp(base + static_cast<int64_t>(j) * D);
-      float acc = 0.f;
+      for (int r = 0; r < kDistR; ++r) x[r] = xs[(leaf + 64 * q) * kDistRowLd + r0 + r];
 #pragma unroll
-      for (int q = 0; q < kMaxDim / kWave; ++q) {
-        if (q < J) {
-          const float diff = xi[q] - feat_or_zero(xj, l + q * kWave, D);
-          acc = q == 0 ? diff * diff : acc + diff * diff;
+      for (int c = 0; c < kDistC; ++c) y[c] = ys[(leaf + 64 * q) * kDistColLd + c0 + c];
+#pragma unroll
+      for (int r = 0; r < kDistR; ++r)
+#pragma unroll
+        for (int c = 0; c < kDistC; ++c) {
+          const float diff = x[r] - y[c];
+          out[r * kDistC + c] = q == 0 ? diff * diff : out[r * kDistC + c] + diff * diff;
         }
-      }
-      s[c] = acc;
-    }
-    float t[4];
-    wave_sum4(s[0], s[1], s[2], s[3], t[0], t[1], t[2], t[3]);
-    if (l < 4 && j0 + l < n) {
-      const float v = l == 0 ? t[0] : l == 1 ? t[1] : l == 2 ? t[2] : t[3];
-      const int j = j0 + l;
-      dl[static_cast<int64_t>(i) * M + j] = v;
-      dl[static_cast<int64_t>(j) * M + i] = v;
     }
   }
+  // The 64-leaf tree, depth first: position k = 8 kk + j of the depth-first
+  // order is leaf 8 bitrev3(j) + bitrev3(kk); positions are combined as a
+  // binary counter (a carry folds into the pending left sibling, left + right),
+  // levels 0-2 inside a group of eight positions, levels 3-5 across groups.
+  __device__ __forceinline__ void tree(float (&root)[kDistR * kDistC]) const {
+    constexpr int E = kDistR * kDistC;
+    float s3[E], s4[E], s5[E];
+    for (int kk = 0; kk < 8; ++kk) {
+      const int low = ((kk & 1) << 2) | (kk & 2) | ((kk >> 2) & 1);   // bitrev3(kk)
+      float s0[E], s1[E], s2[E], c[E];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int hi = ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1);     // bitrev3(j)
+        leaf(8 * hi + low, c);
+        if ((j & 1) == 0) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) s0[e] = c[e];
+          continue;
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) c[e] = s0[e] + c[e];
+        if ((j & 2) == 0) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) s1[e] = c[e];
+          continue;
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) c[e] = s1[e] + c[e];
+        if ((j & 4) == 0) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) s2[e] = c[e];
+          continue;
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) c[e] = s2[e] + c[e];
+      }
+      // c: the level-3 node of this group of eight.
+      if ((kk & 1) == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) s3[e] = c[e];
+        continue;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) c[e] = s3[e] + c[e];
+      if ((kk & 2) == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) s4[e] = c[e];
+        continue;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) c[e] = s4[e] + c[e];
+      if ((kk & 4) == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) s5[e] = c[e];
+        continue;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) root[e] = s5[e] + c[e];
+    }
+  }
+};
+
+template <int J>
+__global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu, const int32_t* __restrict__ count,
+                                                   float* __restrict__ dist, int M, int D) {
+  extern __shared__ __align__(16) float tile_s[];
+  const int lane = blockIdx.z, n = count[lane];
+  const int i0 = blockIdx.x * kDistRows, j0 = blockIdx.y * kDistCols;
+  if (i0 >= n || j0 >= n || j0 + kDistCols - 1 < i0) return;
+  const float* base = mu + static_cast<int64_t>(lane) * M * D;
+  float* xs = tile_s;
+  float* ys = tile_s + 64 * J * kDistRowLd;
+  const int t = threadIdx.x;
+  for (int e = t; e < kDistRows * 64 * J; e += 256) {
+    const int r = e / (64 * J), d = e - r * (64 * J);
+    xs[d * kDistRowLd + r] = i0 + r < n && d < D ? base[static_cast<int64_t>(i0 + r) * D + d] : 0.f;
+  }
+  for (int e = t; e < kDistCols * 64 * J; e += 256) {
+    const int c = e / (64 * J), d = e - c * (64 * J);
+    ys[d * kDistColLd + c] = j0 + c < n && d < D ? base[static_cast<int64_t>(j0 + c) * D + d] : 0.f;
+  }
+  __syncthreads();
+  const int tr = t / (kDistCols / kDistC), tc = t % (kDistCols / kDistC);
+  const DistTile<J> tl{xs, ys, kDistR * tr, kDistC * tc};
+  float v[kDistR * kDistC];
+  tl.tree(v);
+  float* dl = dist + static_cast<int64_t>(lane) * M * M;
+#pragma unroll
+  for (int r = 0; r < kDistR; ++r) {
+    const int i = i0 + kDistR * tr + r;
+#pragma unroll
+    for (int c = 0; c < kDistC; ++c) {
+      const int j = j0 + kDistC * tc + c;
+      if (i < n && j < n && j > i) {
+        dl[static_cast<int64_t>(i) * M + j] = v[r * kDistC + c];
+        dl[static_cast<int64_t>(j) * M + i] = v[r * kDistC + c];
+      } else if (i < n && j == i) {
+        dl[static_cast<int64_t>(i) * M + i] = 0.f;
+      }
+    }
+  }
+}
+
+size_t dist_lds_bytes(int D) {
+  const int J = (D + 63) / 64;
+  return static_cast<size_t>(64) * J * (kDistRowLd + kDistColLd) * 4;
+}
+
+int launch_dist(const float* mu, const int32_t* count, float* dist, int M, int D, int lanes, hipStream_t stream) {
+  const dim3 grid((M + kDistRows - 1) / kDistRows, (M + kDistCols - 1) / kDistCols, lanes);
+  const size_t lds = dist_lds_bytes(D);
+  const int J = (D + 63) / 64;
+  const void* fn = J == 1 ? reinterpret_cast<const void*>(&dist_kernel<1>)
+                 : J == 2 ? reinterpret_cast<const void*>(&dist_kernel<2>)
+                 : J == 3 ? reinterpret_cast<const void*>(&dist_kernel<3>)
+                          : reinterpret_cast<const void*>(&dist_kernel<4>);
+  if (!allow_dynamic_lds(fn, lds)) return LOGKV_ERUNTIME;
+  if (J == 1) hipLaunchKernelGGL(dist_kernel<1>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
+  else if (J == 2) hipLaunchKernelGGL(dist_kernel<2>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
+  else if (J == 3) hipLaunchKernelGGL(dist_kernel<3>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
+  else hipLaunchKernelGGL(dist_kernel<4>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
 // ---------------------------------------------------------------------------
@@ -748,7 +867,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   if (rc) return rc;
   hipLaunchKernelGGL(load_nodes_kernel, dim3(std::max(1, std::min(64, M * D / 4096)), lanes), dim3(256), 0, stream, r,
                      c.n_groups, u);
-  hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu1, u.count1, u.dist, M, D);
+  if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
                 u.image, u.image_stride, u.ctl};
   if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
@@ -758,7 +877,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
                      M, u.label1, u.n_roots1);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&stage2_kernel), lab_lds)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
-  hipLaunchKernelGGL(dist_kernel, dim3(M, lanes), dim3(256), 0, stream, u.mu2, u.count2, u.dist, M, D);
+  if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
                 u.bound, u.image, u.image_stride, u.ctl};
   if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
