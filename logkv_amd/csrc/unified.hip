@@ -105,13 +105,18 @@ __device__ inline ReduceLds carve_lds(uint8_t* dyn, int M) {
 
 // Packed minimum of row r over the live columns (litgpt/log_kv_cache.py:
 // 473-488); the row's own column contributes (inf, key 0), so a row without a
-// finite cost packs to the infinite key.
+// finite cost packs to the infinite key (the minimum starts there). With
+// `live`, only the listed columns are visited: a dead column has mass 0, so
+// its key is (inf, r ^ c) >= the infinite key and never the minimum.
 template <bool LIMIT>
-__device__ uint64_t scan_row(const ReduceLds& s, const float* dist, int M, int n, int r, float limit) {
+__device__ uint64_t scan_row(const ReduceLds& s, const float* dist, int M, int n, int r, float limit,
+                             const int16_t* live = nullptr, int n_live = 0) {
   const float mr = s.mass[r], rr = s.radius[r];
   uint64_t best = kInfKey;
   const float* row = dist + static_cast<int64_t>(r) * M;
-  for (int c = lane_id(); c < n; c += kWave) {
+  const int end = live ? n_live : n;
+  for (int idx = lane_id(); idx < end; idx += kWave) {
+    const int c = live ? live[idx] : idx;
     const float cost = ward_cost<LIMIT>(row[c], mr, s.mass[c], rr, s.radius[c], limit, c != r);
     const uint64_t k = pack_cost(cost, r ^ c);
     best = k < best ? k : best;
@@ -442,12 +447,14 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
   n_ok_out = n_ok;
 }
 
-// Lance-Williams updates of merge p's kept row over columns [c0, c1) (one wave,
-// litgpt/log_kv_cache.py:607-626): the row and its mirror, each column's cost
-// pushed into the column's cached minimum; returns the row's minimum key over
-// those columns.
+// Lance-Williams updates of merge p's kept row over columns [c0, c1) (or live
+// columns live[c0 .. c1) when `live` is given; a dead column is never written
+// and its key is never a minimum) (one wave, litgpt/log_kv_cache.py:607-626):
+// the row and its mirror, each column's cost pushed into the column's cached
+// minimum; returns the row's minimum key over those columns.
 template <bool LIMIT>
-__device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, int p, int c0, int c1, float limit) {
+__device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, int p, int c0, int c1, float limit,
+                               const int16_t* live = nullptr) {
   const int l = lane_id();
   const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
   const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
@@ -455,7 +462,8 @@ __device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, in
   float* row_a = dist + static_cast<int64_t>(ra) * M;
   const float* row_b = dist + static_cast<int64_t>(rb) * M;
   uint64_t rmin = kInfKey;
-  for (int c = c0 + l; c < c1; c += kWave) {
+  for (int idx = c0 + l; idx < c1; idx += kWave) {
+    const int c = live ? live[idx] : idx;
     const uint8_t fl = s.flags[c];
     const bool alive_c = fl & kAlive, keep_c = fl & kKeep;
     const float x_aa = row_a[c], x_ba = row_b[c];
@@ -477,8 +485,10 @@ __device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, in
     const bool valid = alive_c && c != ra;
     const float cost = ward_cost<LIMIT>(nw, total, s.mass[c], rad, s.radius[c], limit, valid);
     const uint64_t k = pack_cost(cost, ra ^ c);
-    if (cost < __builtin_inff() && !keep_c) atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]),
-                                                      static_cast<unsigned long long>(k));
+    // Keys only fall during the phase, so a key at or above the one read now
+    // cannot be the final minimum: the atomic is issued only when it can lower it.
+    if (cost < __builtin_inff() && !keep_c && k < s.packed[c])
+      atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]), static_cast<unsigned long long>(k));
     rmin = k < rmin ? k : rmin;
   }
   return wave_min_u64(rmin);
@@ -553,7 +563,30 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
   int nprop, n_ok;
   plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok);
   for (int p = t; p < n_ok; p += kReduceThreads) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = kInfKey;
+  // The live rows after the merges, ascending: the columns the Lance-Williams
+  // and rescan phases visit (a dead column's key is never a minimum).
+  __shared__ int s_live, part_s[kReduceWaves];
+  int16_t* live = a.live + static_cast<int64_t>(lane) * M;
+  if (t == 0) s_live = 0;
   __syncthreads();
+  for (int c0 = 0; c0 < n; c0 += kReduceThreads) {
+    const int c = c0 + t;
+    const bool on = c < n && (s.flags[c] & kAlive);
+    const uint64_t mask = __ballot(on);
+    const int before = __popcll(mask & ((1ull << lane_id()) - 1ull));
+    if (lane_id() == 0) part_s[wave_id()] = __popcll(mask);
+    __syncthreads();
+    int base = s_live;
+    for (int q = 0; q < wave_id(); ++q) base += part_s[q];
+    if (on) live[base + before] = static_cast<int16_t>(c);
+    __syncthreads();
+    if (t == 0) {
+      int total = 0;
+      for (int q = 0; q < kReduceWaves; ++q) total += part_s[q];
+      s_live += total;
+    }
+    __syncthreads();
+  }
   uint8_t* out = a.image + static_cast<int64_t>(lane) * a.image_stride;
   for (size_t i = t * 16; i + 16 <= bytes; i += kReduceThreads * 16)
     *reinterpret_cast<uint4*>(out + i) = *reinterpret_cast<const uint4*>(dyn + i);
@@ -568,6 +601,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
     ctl.active = remaining && nprop > 0 ? 1 : 0;
     ctl.stuck = remaining && nprop == 0 ? 1 : 0;
     ctl.rounds += 1;
+    ctl.n_live = s_live;
     if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
     a.ctl[lane] = ctl;
   }
@@ -584,12 +618,14 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
   const ReduceLds s = image_of(a, lane);
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int chunks = (n + kLwChunk - 1) / kLwChunk, items = ctl.n_ok * chunks;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * M;
+  const int n_live = ctl.n_live;
+  const int chunks = (n_live + kLwChunk - 1) / kLwChunk, items = ctl.n_ok * chunks;
   const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
   for (int it = gw; it < items; it += nw) {
     const int p = it / chunks, ch = it - p * chunks;
-    const int c0 = ch * kLwChunk, c1 = min(n, c0 + kLwChunk);
-    const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, c0, c1, limit);
+    const int c0 = ch * kLwChunk, c1 = min(n_live, c0 + kLwChunk);
+    const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, c0, c1, limit, live);
     if (lane_id() == 0)
       atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)]),
                 static_cast<unsigned long long>(rmin));
@@ -600,15 +636,18 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
 template <bool LIMIT>
 __global__ __launch_bounds__(kPhaseThreads) void reduce_rescan_kernel(ReduceArgs a) {
   const int lane = blockIdx.y, M = a.M;
-  if (!a.ctl[lane].work) return;
+  const LaneCtl ctl = a.ctl[lane];
+  if (!ctl.work) return;
   const int n = a.count[lane];
   const ReduceLds s = image_of(a, lane);
   const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * M;
   const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
-  for (int r = gw; r < n; r += nw) {
+  for (int q = gw; q < ctl.n_live; q += nw) {
+    const int r = live[q];
     if (!is_dirty(s, r)) continue;
-    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
+    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit, live, ctl.n_live);
     if (lane_id() == 0) s.packed[r] = k;
   }
 }
@@ -674,6 +713,9 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
 // One stage: setup, the pipelined rounds, the finish.
 template <bool LIMIT>
 int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
+  if (!a.dist || !a.mu || !a.mass || !a.count || !a.image || !a.ctl || !a.live || !a.alive_out || !a.trace ||
+      !a.n_trace || !a.stuck || !a.bound || (LIMIT && !a.limit) || a.image_stride < static_cast<int64_t>(reduce_lds_bytes(a.M)))
+    return LOGKV_ERUNTIME;
   const size_t lds = reduce_lds_bytes(a.M);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_plan_kernel<LIMIT>), lds) ||
       !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_finish_kernel<LIMIT>), lds))
@@ -869,7 +911,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
                      c.n_groups, u);
   if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
-                u.image, u.image_stride, u.ctl};
+                u.image, u.image_stride, u.ctl, u.live};
   if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
   const size_t lab_lds = static_cast<size_t>(M) * 8;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
@@ -879,7 +921,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
   if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
-                u.bound, u.image, u.image_stride, u.ctl};
+                u.bound, u.image, u.image_stride, u.ctl, u.live};
   if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
                      M, u.label2, u.n_roots2);

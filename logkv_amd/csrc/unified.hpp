@@ -18,6 +18,8 @@ struct LaneCtl {
   int32_t work;     // 1: the current round's Lance-Williams / rescan phases have work
   int32_t stuck;    // 1: clusters above the target and no pair left
   int32_t rounds;   // rounds run
+  int32_t n_live;   // live rows after the current round's merges
+  int32_t pad[3];
 };
 
 // Arguments of one reducer stage over `lanes` lanes of M padded nodes.
@@ -37,6 +39,7 @@ struct ReduceArgs {
   uint8_t* image;         // [lanes, image_stride] the reducer state (the LDS layout) between launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
+  int16_t* live;          // [lanes, M] the round's live rows in ascending order (ctl.n_live of them)
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -70,6 +73,7 @@ struct UnifiedBufs {
   uint8_t* image;         // [lanes, image_stride] reducer state between the round launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
+  int16_t* live;          // [lanes, M]
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
