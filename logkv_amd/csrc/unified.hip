@@ -27,7 +27,7 @@ namespace {
 constexpr int kReduceThreads = 1024;
 constexpr int kReduceWaves = kReduceThreads / kWave;
 constexpr uint64_t kInfKey = 0x7F800000ull << 32;
-constexpr uint8_t kAlive = 1, kValid = 2, kKeep = 4, kMerged = 8, kRejected = 16;
+constexpr uint8_t kAlive = 1, kValid = 2, kKeep = 4, kMerged = 8, kRejected = 16, kDirty = 32;
 
 __device__ __forceinline__ uint64_t pack_cost(float cost, int key) {
   const uint32_t bits = cost == 0.f ? 0u : __float_as_uint(cost);
@@ -52,6 +52,40 @@ __device__ __forceinline__ float ward_cost(float d2, float mi, float mj, float r
   return valid ? d2 * (mi * mj / denom) : __builtin_inff();
 }
 
+// Screening form of ward_cost: the quotients from v_rcp_f32 and the distance
+// from v_sqrt_f32 (each within 1 ulp), so a finite result is within 2^-20
+// (relative) of ward_cost's, and +inf means the pair is certainly not allowed.
+// `border` is set for an allowed-looking pair whose radius test lies within
+// 2^-16 of the limit, or whose d2 is below 2^-96 (where v_sqrt_f32 and the
+// relative bound do not hold): only ward_cost decides those. A result of 0
+// is +0.
+template <bool LIMIT>
+__device__ __forceinline__ float screen_cost(float d2, float mi, float mj, float ri, float rj, float limit, bool valid,
+                                             bool& border) {
+  const float sum = mi + mj;
+  const float denom = sum < 1.f ? 1.f : sum;
+  valid = valid && mi > 0.f && mj > 0.f;
+  const float inv = __builtin_amdgcn_rcpf(denom);
+  bool near_edge = d2 < 0x1p-96f;
+  if (LIMIT) {
+    const float distance = __builtin_amdgcn_sqrtf(d2);
+    const float x = ri + (mj * inv) * distance, y = rj + (mi * inv) * distance;
+    const float mx = x < y ? y : x;
+    const bool over = mx > limit * (1.f + 0x1p-16f);
+    near_edge = near_edge || mx >= limit * (1.f - 0x1p-16f);
+    valid = valid && !over;
+  }
+  border = valid && near_edge;
+  const float c = d2 * ((mi * mj) * inv);
+  return valid ? (c > 0.f ? c : 0.f) : __builtin_inff();
+}
+
+// Cut-off of the screen: a pair whose screened cost exceeds m (1 + 2^-16),
+// where m is the least screened cost of a non-border pair of the same set,
+// has an exact cost above that pair's exact cost, so it cannot hold the
+// set's minimum key.
+__device__ __forceinline__ float screen_cutoff(float m) { return m * (1.f + 0x1p-16f); }
+
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -59,6 +93,32 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     v = o < v ? o : v;
   }
   return v;
+}
+
+// Minimum over the 64 lanes, formed toward lane 0 with the permlane swaps and
+// DPP row shifts of wave_sum0 and read from lane 0 (uniform result). Every
+// lane of the wave must be active.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  auto mn = [](uint32_t x, uint32_t y) { return x < y ? x : y; };
+  v = mn(v, __builtin_amdgcn_permlane32_swap(v, v, false, false)[1]);
+  v = mn(v, __builtin_amdgcn_permlane16_swap(v, v, false, false)[1]);
+  const int i = static_cast<int>(v);
+  v = mn(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(i, i, 0x108, 0xf, 0xf, false)));  // row_shl:8
+  const int j = static_cast<int>(v);
+  v = mn(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(j, j, 0x104, 0xf, 0xf, false)));  // row_shl:4
+  const int k = static_cast<int>(v);
+  v = mn(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(k, k, 0x102, 0xf, 0xf, false)));  // row_shl:2
+  const int m = static_cast<int>(v);
+  v = mn(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(m, m, 0x101, 0xf, 0xf, false)));  // row_shl:1
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// Minimum packed key over the 64 lanes (uniform): the least cost bits, then
+// the least low word among the lanes that hold them. Every lane must be active.
+__device__ __forceinline__ uint64_t wave_min_key(uint64_t k) {
+  const uint32_t hi = wave_min_u32(static_cast<uint32_t>(k >> 32));
+  const uint32_t lo = wave_min_u32(static_cast<uint32_t>(k >> 32) == hi ? static_cast<uint32_t>(k) : 0xFFFFFFFFu);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 struct ReduceLds {
@@ -419,7 +479,18 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
   }
   const int budget = sh[0] - a.target;
   const int n_ok = nv < budget ? nv : (budget > 0 ? budget : 0);
-  // Merges: pair scalars, masses, radii, centers (litgpt/log_kv_cache.py:589-606).
+  // Merges: centers (one wave per merge, lanes over the features), then pair
+  // scalars, masses and radii (litgpt/log_kv_cache.py:589-606).
+  for (int p = w; p < n_ok; p += kReduceWaves) {
+    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+    const float ma = s.mass[ra], mb = s.mass[rb];
+    const float total = ma + mb;
+    const float scale = total < 1.f ? 1.f : total;
+    float* ua = mu + static_cast<int64_t>(ra) * D;
+    const float* ub = mu + static_cast<int64_t>(rb) * D;
+    for (int d = l; d < D; d += kWave) ua[d] = (ma * ua[d] + mb * ub[d]) / scale;
+  }
+  __syncthreads();
   for (int p = t; p < n_ok; p += kReduceThreads) {
     const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
     const float ma = s.mass[ra], mb = s.mass[rb];
@@ -435,10 +506,6 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
     s.mass[ra] = total;
     s.mass[rb] = 0.f;
     if (LIMIT) s.radius[ra] = a.bound[static_cast<int64_t>(lane) * M + ra];
-    const float scale = total < 1.f ? 1.f : total;
-    float* ua = mu + static_cast<int64_t>(ra) * D;
-    const float* ub = mu + static_cast<int64_t>(rb) * D;
-    for (int d = 0; d < D; ++d) ua[d] = (ma * ua[d] + mb * ub[d]) / scale;
     trace[2 * (sh[1] + p)] = ra;
     trace[2 * (sh[1] + p) + 1] = rb;
   }
@@ -486,8 +553,9 @@ __device__ uint64_t lw_columns(const ReduceLds& s, float* dist, int M, int n, in
     const float cost = ward_cost<LIMIT>(nw, total, s.mass[c], rad, s.radius[c], limit, valid);
     const uint64_t k = pack_cost(cost, ra ^ c);
     // Keys only fall during the phase, so a key at or above the one read now
-    // cannot be the final minimum: the atomic is issued only when it can lower it.
-    if (cost < __builtin_inff() && !keep_c && k < s.packed[c])
+    // cannot be the final minimum: the atomic is issued only when it can lower
+    // it, and never for a row the round rescans.
+    if (cost < __builtin_inff() && !keep_c && !(fl & kDirty) && k < s.packed[c])
       atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[c]), static_cast<unsigned long long>(k));
     rmin = k < rmin ? k : rmin;
   }
@@ -501,39 +569,32 @@ __device__ __forceinline__ bool is_dirty(const ReduceLds& s, int r) {
 }
 
 // Stage setup: every lane's image (masses, zero radii, live flags, infinite
-// keys) and round bookkeeping.
+// keys), every row in both lists (the first scan is a rescan of every row
+// over every column) and round bookkeeping.
 __global__ __launch_bounds__(kPhaseThreads) void reduce_init_kernel(ReduceArgs a) {
   const int lane = blockIdx.y, M = a.M;
   const int n = a.count[lane];
   const ReduceLds s = image_of(a, lane);
+  int16_t* lists = a.live + static_cast<int64_t>(lane) * 2 * M;
   for (int i = blockIdx.x * kPhaseThreads + threadIdx.x; i < M; i += gridDim.x * kPhaseThreads) {
     s.mass[i] = i < n ? a.mass[static_cast<int64_t>(lane) * M + i] : 0.f;
     s.radius[i] = 0.f;
     s.flags[i] = i < n ? kAlive : 0;
     s.packed[i] = kInfKey;
     s.best[i] = static_cast<int16_t>(i);
+    if (i < n) {
+      lists[i] = static_cast<int16_t>(i);
+      lists[M + i] = static_cast<int16_t>(i);
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     LaneCtl c{};
     c.count = n;
     c.active = n > a.target ? 1 : 0;
+    c.work = c.active;
+    c.n_live = n;
+    c.n_dirty = n;
     a.ctl[lane] = c;
-  }
-}
-
-// Every live row's initial cached minimum, rows spread over the lane's blocks.
-template <bool LIMIT>
-__global__ __launch_bounds__(kPhaseThreads) void reduce_scan_kernel(ReduceArgs a) {
-  const int lane = blockIdx.y, M = a.M;
-  if (!a.ctl[lane].active) return;
-  const int n = a.count[lane];
-  const ReduceLds s = image_of(a, lane);
-  const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
-  const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
-  for (int r = gw; r < n; r += nw) {
-    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
-    if (lane_id() == 0) s.packed[r] = k;
   }
 }
 
@@ -563,27 +624,49 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
   int nprop, n_ok;
   plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok);
   for (int p = t; p < n_ok; p += kReduceThreads) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = kInfKey;
-  // The live rows after the merges, ascending: the columns the Lance-Williams
-  // and rescan phases visit (a dead column's key is never a minimum).
-  __shared__ int s_live, part_s[kReduceWaves];
-  int16_t* live = a.live + static_cast<int64_t>(lane) * M;
-  if (t == 0) s_live = 0;
+  // The live rows after the merges, ascending (the columns the Lance-Williams
+  // and rescan phases visit: a dead column's key is never a minimum), and the
+  // rows to rescan, ascending, their cached minima reset for the rescan's
+  // atomic minima.
+  __shared__ int s_live, s_dirty, part_s[2 * kReduceWaves];
+  int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
+  int16_t* dirty = live + M;
+  if (t == 0) {
+    s_live = 0;
+    s_dirty = 0;
+  }
   __syncthreads();
   for (int c0 = 0; c0 < n; c0 += kReduceThreads) {
     const int c = c0 + t;
     const bool on = c < n && (s.flags[c] & kAlive);
-    const uint64_t mask = __ballot(on);
-    const int before = __popcll(mask & ((1ull << lane_id()) - 1ull));
-    if (lane_id() == 0) part_s[wave_id()] = __popcll(mask);
+    const bool re = c < n && is_dirty(s, c);
+    const uint64_t below = (1ull << lane_id()) - 1ull;
+    const uint64_t mask = __ballot(on), mask_re = __ballot(re);
+    if (lane_id() == 0) {
+      part_s[wave_id()] = __popcll(mask);
+      part_s[kReduceWaves + wave_id()] = __popcll(mask_re);
+    }
     __syncthreads();
-    int base = s_live;
-    for (int q = 0; q < wave_id(); ++q) base += part_s[q];
-    if (on) live[base + before] = static_cast<int16_t>(c);
+    int base = s_live, base_re = s_dirty;
+    for (int q = 0; q < wave_id(); ++q) {
+      base += part_s[q];
+      base_re += part_s[kReduceWaves + q];
+    }
+    if (on) live[base + __popcll(mask & below)] = static_cast<int16_t>(c);
+    if (re) {
+      dirty[base_re + __popcll(mask_re & below)] = static_cast<int16_t>(c);
+      s.packed[c] = kInfKey;
+      s.flags[c] |= kDirty;
+    }
     __syncthreads();
     if (t == 0) {
-      int total = 0;
-      for (int q = 0; q < kReduceWaves; ++q) total += part_s[q];
+      int total = 0, total_re = 0;
+      for (int q = 0; q < kReduceWaves; ++q) {
+        total += part_s[q];
+        total_re += part_s[kReduceWaves + q];
+      }
       s_live += total;
+      s_dirty += total_re;
     }
     __syncthreads();
   }
@@ -602,6 +685,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
     ctl.stuck = remaining && nprop == 0 ? 1 : 0;
     ctl.rounds += 1;
     ctl.n_live = s_live;
+    ctl.n_dirty = s_dirty;
     if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
     a.ctl[lane] = ctl;
   }
@@ -618,7 +702,7 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
   const ReduceLds s = image_of(a, lane);
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int16_t* live = a.live + static_cast<int64_t>(lane) * M;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
   const int n_live = ctl.n_live;
   const int chunks = (n_live + kLwChunk - 1) / kLwChunk, items = ctl.n_ok * chunks;
   const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
@@ -632,23 +716,68 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
   }
 }
 
-// Round phase 3: rescans of the dirty rows, spread over the lane's blocks.
+// Round phase 3 (and the stage's first scan): the cached minimum of every
+// listed row over the live columns, as atomic minima of wave tiles. A wave
+// takes up to kScanRows listed rows x kScanCols * 64 live columns (kScanCols per
+// lane, the columns' masses and radii held across the rows); per row, the
+// screen leaves only the lanes whose pairs can hold the tile's minimum key
+// to evaluate ward_cost.
+constexpr int kScanCols = 8, kScanRows = 16, kScanChunk = kScanCols * kWave;
+
 template <bool LIMIT>
 __global__ __launch_bounds__(kPhaseThreads) void reduce_rescan_kernel(ReduceArgs a) {
-  const int lane = blockIdx.y, M = a.M;
+  const int lane = blockIdx.y, M = a.M, l = lane_id();
   const LaneCtl ctl = a.ctl[lane];
   if (!ctl.work) return;
-  const int n = a.count[lane];
   const ReduceLds s = image_of(a, lane);
   const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int16_t* live = a.live + static_cast<int64_t>(lane) * M;
-  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
-  for (int q = gw; q < ctl.n_live; q += nw) {
-    const int r = live[q];
-    if (!is_dirty(s, r)) continue;
-    const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit, live, ctl.n_live);
-    if (lane_id() == 0) s.packed[r] = k;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
+  const int16_t* dirty = live + M;
+  const int n_live = ctl.n_live, n_dirty = ctl.n_dirty;
+  const int col_chunks = (n_live + kScanChunk - 1) / kScanChunk, waves = gridDim.x * kPhaseWaves;
+  // Rows per item: up to kScanRows, fewer when that would leave waves idle.
+  const int rows = max(1, min(kScanRows, n_dirty * col_chunks / waves));
+  const int items = col_chunks * ((n_dirty + rows - 1) / rows);
+  for (int it = blockIdx.x * kPhaseWaves + wave_id(); it < items; it += waves) {
+    const int rg = it / col_chunks, cc = it - rg * col_chunks;
+    int col[kScanCols];
+    float mc[kScanCols], rc[kScanCols];
+#pragma unroll
+    for (int e = 0; e < kScanCols; ++e) {
+      const int idx = cc * kScanChunk + e * kWave + l;
+      col[e] = idx < n_live ? live[idx] : -1;
+      mc[e] = col[e] >= 0 ? s.mass[col[e]] : 0.f;
+      rc[e] = col[e] >= 0 ? s.radius[col[e]] : 0.f;
+    }
+    const int q1 = min(n_dirty, (rg + 1) * rows);
+    for (int q = rg * rows; q < q1; ++q) {
+      const int r = dirty[q];
+      const float mr = s.mass[r], rr = s.radius[r];
+      const float* row = dist + static_cast<int64_t>(r) * M;
+      float d2[kScanCols], sc[kScanCols];
+      bool border[kScanCols];
+#pragma unroll
+      for (int e = 0; e < kScanCols; ++e) d2[e] = row[col[e] >= 0 ? col[e] : 0];
+      float m = __builtin_inff();
+#pragma unroll
+      for (int e = 0; e < kScanCols; ++e) {
+        sc[e] = screen_cost<LIMIT>(d2[e], mr, mc[e], rr, rc[e], limit, col[e] >= 0 && col[e] != r, border[e]);
+        if (!border[e]) m = sc[e] < m ? sc[e] : m;
+      }
+      const float cut = screen_cutoff(__uint_as_float(wave_min_u32(__float_as_uint(m))));
+      uint64_t best = kInfKey;
+#pragma unroll
+      for (int e = 0; e < kScanCols; ++e) {
+        if (border[e] || (sc[e] < __builtin_inff() && sc[e] <= cut)) {
+          const uint64_t k = pack_cost(ward_cost<LIMIT>(d2[e], mr, mc[e], rr, rc[e], limit, true), r ^ col[e]);
+          best = k < best ? k : best;
+        }
+      }
+      best = wave_min_key(best);
+      if (l == 0 && best < kInfKey)
+        atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[r]), static_cast<unsigned long long>(best));
+    }
   }
 }
 
@@ -723,7 +852,7 @@ int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
   const dim3 phase(kPhaseBlocks, lanes);
   hipLaunchKernelGGL(reduce_init_kernel, dim3(std::max(1, std::min(16, a.M / kPhaseThreads)), lanes),
                      dim3(kPhaseThreads), 0, stream, a);
-  hipLaunchKernelGGL(reduce_scan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
+  hipLaunchKernelGGL(reduce_rescan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
   for (int round = 0; round < kPipelinedRounds; ++round) {
     hipLaunchKernelGGL(reduce_plan_kernel<LIMIT>, dim3(lanes), dim3(kReduceThreads), lds, stream, a);
     hipLaunchKernelGGL(reduce_lw_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);

@@ -19,7 +19,8 @@ struct LaneCtl {
   int32_t stuck;    // 1: clusters above the target and no pair left
   int32_t rounds;   // rounds run
   int32_t n_live;   // live rows after the current round's merges
-  int32_t pad[3];
+  int32_t n_dirty;  // rows to rescan after the current round's merges
+  int32_t pad[2];
 };
 
 // Arguments of one reducer stage over `lanes` lanes of M padded nodes.
@@ -39,7 +40,8 @@ struct ReduceArgs {
   uint8_t* image;         // [lanes, image_stride] the reducer state (the LDS layout) between launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
-  int16_t* live;          // [lanes, M] the round's live rows in ascending order (ctl.n_live of them)
+  int16_t* live;          // [lanes, 2, M] the round's live rows (ctl.n_live) and rows to rescan
+                          // (ctl.n_dirty), each list ascending
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -73,7 +75,7 @@ struct UnifiedBufs {
   uint8_t* image;         // [lanes, image_stride] reducer state between the round launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
-  int16_t* live;          // [lanes, M]
+  int16_t* live;          // [lanes, 2, M]
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
