@@ -81,3 +81,27 @@ def test_old_old_merge_frees_a_cluster():
     assert ora.ward_merges == 1
     assert ora.alive[0, 0].tolist() == [True, True]
     assert ora.n_total[0, 0].tolist() == [4, 4]
+
+
+@pytest.mark.parametrize("scale", [1.0, 2.0])
+def test_lattice_ties_and_radius_edge(scale):
+    """Rows on a binary lattice: duplicates (zero distances), many exactly
+    equal costs, and with s_h = 1 (radius limit 1) singleton pairs at squared
+    distance 4 whose radius bound equals the limit exactly, so the rescan
+    screen's border and tie cases decide real rows."""
+    print(f"case lattice scale {scale}", flush=True)
+    dim, T, K = 16, 64, 4
+    gpu, ora = _pair(2, 2, dim, K, 8, T, T * 6, 1.0)
+    g = torch.Generator().manual_seed(int(scale * 10))
+    dev = gpu.level_k.device
+    for i in range(4):
+        bits = torch.randint(0, 2, (2, 2, T, 5), generator=g).float() * scale
+        rows = torch.zeros(2, 2, T, dim)
+        rows[..., :5] = bits
+        rows = rows.to(torch.bfloat16)
+        pos = torch.arange(i * T, (i + 1) * T).unsqueeze(0).expand(2, -1).contiguous()
+        gpu.route_and_flush_batch(rows.to(dev), rows.to(dev), pos.to(dev))
+        ora.flush_rows(rows.float().numpy(), rows.float().numpy(), pos.numpy())
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"flush {i}: " + "; ".join(bad)
