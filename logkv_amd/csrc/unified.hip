@@ -212,23 +212,27 @@ __global__ __launch_bounds__(256) void load_nodes_kernel(RowsArgs r, int n_group
 // to both (i, j) and (j, i), the diagonal is zero. Tiles wholly below the
 // diagonal or past the node count return at once.
 constexpr int kDistRows = 32, kDistCols = 64, kDistR = 2, kDistC = 4;
-constexpr int kDistRowLd = kDistRows + 1, kDistColLd = kDistCols + 1;
+// Feature-major LDS rows padded so a thread's kDistR row values and kDistC
+// column values of one feature are one aligned 8-byte and one aligned 16-byte
+// read.
+constexpr int kDistRowLd = kDistRows + 2, kDistColLd = kDistCols + 4;
+static_assert(kDistR == 2 && kDistC == 4, "the tile reads are float2 / float4");
 
 template <int J>
 struct DistTile {
   const float* xs;   // [64 J][kDistRowLd]
   const float* ys;   // [64 J][kDistColLd]
   int r0, c0;        // the thread's first row / column in the tile
-  // Leaf `leaf` of every pair of the thread: sum over q < J of (x - y)^2 at
-  // feature leaf + 64 q, in q order.
-  __device__ __forceinline__ void leaf(int leaf, float (&out)[kDistR * kDistC]) const {
+  // Leaf 8 hi + low of every pair of the thread: sum over q < J of (x - y)^2
+  // at feature leaf + 64 q, in q order. xb / yb point at feature `low` of the
+  // thread's rows / columns, so the reads take compile-time offsets.
+  __device__ __forceinline__ void leaf(const float* xb, const float* yb, int hi, float (&out)[kDistR * kDistC]) const {
 #pragma unroll
     for (int q = 0; q < J; ++q) {
-      float x[kDistR], y[kDistC];
-#pragma unroll
-      for (int r = 0; r < kDistR; ++r) x[r] = xs[(leaf + 64 * q) * kDistRowLd + r0 + r];
-#pragma unroll
-      for (int c = 0; c < kDistC; ++c) y[c] = ys[(leaf + 64 * q) * kDistColLd + c0 + c];
+      const float2 x2 = *reinterpret_cast<const float2*>(xb + (8 * hi + 64 * q) * kDistRowLd);
+      const float4 y4 = *reinterpret_cast<const float4*>(yb + (8 * hi + 64 * q) * kDistColLd);
+      const float x[kDistR] = {x2.x, x2.y};
+      const float y[kDistC] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
       for (int r = 0; r < kDistR; ++r)
 #pragma unroll
@@ -247,11 +251,13 @@ struct DistTile {
     float s3[E], s4[E], s5[E];
     for (int kk = 0; kk < 8; ++kk) {
       const int low = ((kk & 1) << 2) | (kk & 2) | ((kk >> 2) & 1);   // bitrev3(kk)
+      const float* xb = xs + low * kDistRowLd + r0;
+      const float* yb = ys + low * kDistColLd + c0;
       float s0[E], s1[E], s2[E], c[E];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int hi = ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1);     // bitrev3(j)
-        leaf(8 * hi + low, c);
+        leaf(xb, yb, hi, c);
         if ((j & 1) == 0) {
 #pragma unroll
           for (int e = 0; e < E; ++e) s0[e] = c[e];
