@@ -383,7 +383,6 @@ int launch_dist(const float* mu, const int32_t* count, float* dist, int M, int D
 constexpr int kPhaseThreads = 256;
 constexpr int kPhaseWaves = kPhaseThreads / kWave;
 constexpr int kPhaseBlocks = 64;      // blocks per lane of the Lance-Williams / rescan phases
-constexpr int kLwChunk = 256;         // columns per Lance-Williams work item
 constexpr int kPipelinedRounds = 40;  // rounds enqueued as phase launches before the finish kernel
 
 __device__ inline ReduceLds image_of(const ReduceArgs& a, int lane) {
@@ -697,28 +696,103 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
   }
 }
 
-// Round phase 2: Lance-Williams rows of the round's kept rows, (merge, column
-// chunk) items spread over the lane's blocks.
+// Round phase 2: the Lance-Williams rows of the round's kept rows
+// (litgpt/log_kv_cache.py:607-626) as wave tiles: up to kLwRows merges x
+// kLwCols * 64 live columns (kLwCols per lane, the columns' state held across
+// the merges). Each element is lw_columns' update: the row and, for a column
+// that is not kept, its mirror; the screen leaves only the elements that can
+// hold the kept row's minimum key (an atomic minimum per tile) or lower a
+// column's cached minimum to evaluate ward_cost.
+constexpr int kLwCols = 4, kLwRows = 16, kLwTile = kLwCols * kWave;
+
 template <bool LIMIT>
 __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) {
-  const int lane = blockIdx.y, M = a.M;
+  const int lane = blockIdx.y, M = a.M, l = lane_id();
   const LaneCtl ctl = a.ctl[lane];
   if (!ctl.work) return;
-  const int n = a.count[lane];
   const ReduceLds s = image_of(a, lane);
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
   const int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
-  const int n_live = ctl.n_live;
-  const int chunks = (n_live + kLwChunk - 1) / kLwChunk, items = ctl.n_ok * chunks;
-  const int gw = blockIdx.x * kPhaseWaves + wave_id(), nw = gridDim.x * kPhaseWaves;
-  for (int it = gw; it < items; it += nw) {
-    const int p = it / chunks, ch = it - p * chunks;
-    const int c0 = ch * kLwChunk, c1 = min(n_live, c0 + kLwChunk);
-    const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, c0, c1, limit, live);
-    if (lane_id() == 0)
-      atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)]),
-                static_cast<unsigned long long>(rmin));
+  const int n_live = ctl.n_live, n_ok = ctl.n_ok;
+  const int col_chunks = (n_live + kLwTile - 1) / kLwTile, waves = gridDim.x * kPhaseWaves;
+  // Merges per item: up to kLwRows, fewer when that would leave waves idle.
+  const int rows = max(1, min(kLwRows, n_ok * col_chunks / waves));
+  const int items = col_chunks * ((n_ok + rows - 1) / rows);
+  for (int it = blockIdx.x * kPhaseWaves + wave_id(); it < items; it += waves) {
+    const int pg = it / col_chunks, cc = it - pg * col_chunks;
+    int col[kLwCols];
+    uint8_t fl[kLwCols];
+    float mc[kLwCols], rc[kLwCols], thr[kLwCols];
+#pragma unroll
+    for (int e = 0; e < kLwCols; ++e) {
+      const int idx = cc * kLwTile + e * kWave + l;
+      col[e] = idx < n_live ? live[idx] : -1;
+      const int c = col[e] >= 0 ? col[e] : 0;
+      fl[e] = col[e] >= 0 ? s.flags[c] : 0;
+      mc[e] = s.mass[c];
+      rc[e] = s.radius[c];
+      // A kept or rescanned column takes no push (-1); keys only fall during
+      // the phase, so the cost read now bounds every key that can still lower it.
+      thr[e] = col[e] >= 0 && !(fl[e] & (kKeep | kDirty)) ? key_cost(s.packed[c]) : -1.f;
+    }
+    const int p1 = min(n_ok, (pg + 1) * rows);
+    for (int p = pg * rows; p < p1; ++p) {
+      const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+      const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
+      const float total = s.mass[ra], rad = s.radius[ra];
+      float* row_a = dist + static_cast<int64_t>(ra) * M;
+      const float* row_b = dist + static_cast<int64_t>(rb) * M;
+      float x_aa[kLwCols], x_ba[kLwCols], nw[kLwCols], sc[kLwCols];
+      bool border[kLwCols];
+#pragma unroll
+      for (int e = 0; e < kLwCols; ++e) {
+        const int c = col[e] >= 0 ? col[e] : ra;
+        x_aa[e] = row_a[c];
+        x_ba[e] = row_b[c];
+      }
+      float m = __builtin_inff();
+#pragma unroll
+      for (int e = 0; e < kLwCols; ++e) {
+        const int c = col[e];
+        float v = alpha * x_aa[e] + beta * x_ba[e] - shift;
+        if (c >= 0 && (fl[e] & kKeep) && c != ra) {
+          const int q = s.best[c], pc = s.pair_of[c];
+          const float qa = s.p_alpha[pc], qb = s.p_beta[pc], qs = s.p_shift[pc];
+          const float x_ab = row_a[q], x_bb = row_b[q];
+          const float own = qa * v + qb * (alpha * x_ab + beta * x_bb - shift) - qs;
+          const float other = alpha * (qa * x_aa[e] + qb * x_ab - qs) + beta * (qa * x_ba[e] + qb * x_bb - qs) - shift;
+          v = ra < c ? own : other;
+        }
+        v = v < 0.f ? 0.f : v;
+        if (c == ra) v = 0.f;
+        nw[e] = v;
+        if (c >= 0) {
+          row_a[c] = v;
+          if (!(fl[e] & kKeep)) dist[static_cast<int64_t>(c) * M + ra] = v;
+        }
+        sc[e] = screen_cost<LIMIT>(v, total, mc[e], rad, rc[e], limit, c >= 0 && c != ra, border[e]);
+        if (!border[e]) m = sc[e] < m ? sc[e] : m;
+      }
+      const float cut = screen_cutoff(__uint_as_float(wave_min_u32(__float_as_uint(m))));
+      uint64_t best = kInfKey;
+#pragma unroll
+      for (int e = 0; e < kLwCols; ++e) {
+        const bool open = border[e] || sc[e] < __builtin_inff();
+        const bool near_row = open && (border[e] || sc[e] <= cut);
+        const bool near_col = open && thr[e] >= 0.f && (border[e] || sc[e] <= screen_cutoff(thr[e]));
+        if (near_row || near_col) {
+          const float cost = ward_cost<LIMIT>(nw[e], total, mc[e], rad, rc[e], limit, true);
+          const uint64_t k = pack_cost(cost, ra ^ col[e]);
+          if (near_row) best = k < best ? k : best;
+          if (near_col && cost < __builtin_inff() && k < s.packed[col[e]])
+            atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[col[e]]), static_cast<unsigned long long>(k));
+        }
+      }
+      best = wave_min_key(best);
+      if (l == 0 && best < kInfKey)
+        atomicMin(reinterpret_cast<unsigned long long*>(&s.packed[ra]), static_cast<unsigned long long>(best));
+    }
   }
 }
 
