@@ -181,7 +181,7 @@ int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late,
   b.image_stride = logkv::unified_image_stride(static_cast<int>(M));
   b.image = take(lanes * b.image_stride);
   b.ctl = reinterpret_cast<logkv::LaneCtl*>(take(lanes * static_cast<int64_t>(sizeof(logkv::LaneCtl))));
-  b.live = reinterpret_cast<int16_t*>(take(lanes * M * 4));
+  b.live = reinterpret_cast<int16_t*>(take(lanes * M * 6));
   if (u) *u = b;
   return off;
 }

@@ -580,7 +580,7 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_init_kernel(ReduceArgs a
   const int lane = blockIdx.y, M = a.M;
   const int n = a.count[lane];
   const ReduceLds s = image_of(a, lane);
-  int16_t* lists = a.live + static_cast<int64_t>(lane) * 2 * M;
+  int16_t* lists = a.live + static_cast<int64_t>(lane) * 3 * M;
   for (int i = blockIdx.x * kPhaseThreads + threadIdx.x; i < M; i += gridDim.x * kPhaseThreads) {
     s.mass[i] = i < n ? a.mass[static_cast<int64_t>(lane) * M + i] : 0.f;
     s.radius[i] = 0.f;
@@ -630,32 +630,38 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
   plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok);
   for (int p = t; p < n_ok; p += kReduceThreads) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = kInfKey;
   // The live rows after the merges, ascending (the columns the Lance-Williams
-  // and rescan phases visit: a dead column's key is never a minimum), and the
+  // and rescan phases visit: a dead column's key is never a minimum), the
   // rows to rescan, ascending, their cached minima reset for the rescan's
-  // atomic minima.
-  __shared__ int s_live, s_dirty, part_s[2 * kReduceWaves];
-  int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
+  // atomic minima, and the kept rows, ascending (the Lance-Williams tiles take
+  // neighbouring kept rows, so their mirror writes into a row share lines).
+  __shared__ int s_live, s_dirty, s_kept, part_s[3 * kReduceWaves];
+  int16_t* live = a.live + static_cast<int64_t>(lane) * 3 * M;
   int16_t* dirty = live + M;
+  int16_t* kept = live + 2 * M;
   if (t == 0) {
     s_live = 0;
     s_dirty = 0;
+    s_kept = 0;
   }
   __syncthreads();
   for (int c0 = 0; c0 < n; c0 += kReduceThreads) {
     const int c = c0 + t;
     const bool on = c < n && (s.flags[c] & kAlive);
     const bool re = c < n && is_dirty(s, c);
+    const bool kp = c < n && (s.flags[c] & kKeep);
     const uint64_t below = (1ull << lane_id()) - 1ull;
-    const uint64_t mask = __ballot(on), mask_re = __ballot(re);
+    const uint64_t mask = __ballot(on), mask_re = __ballot(re), mask_kp = __ballot(kp);
     if (lane_id() == 0) {
       part_s[wave_id()] = __popcll(mask);
       part_s[kReduceWaves + wave_id()] = __popcll(mask_re);
+      part_s[2 * kReduceWaves + wave_id()] = __popcll(mask_kp);
     }
     __syncthreads();
-    int base = s_live, base_re = s_dirty;
+    int base = s_live, base_re = s_dirty, base_kp = s_kept;
     for (int q = 0; q < wave_id(); ++q) {
       base += part_s[q];
       base_re += part_s[kReduceWaves + q];
+      base_kp += part_s[2 * kReduceWaves + q];
     }
     if (on) live[base + __popcll(mask & below)] = static_cast<int16_t>(c);
     if (re) {
@@ -663,15 +669,18 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
       s.packed[c] = kInfKey;
       s.flags[c] |= kDirty;
     }
+    if (kp) kept[base_kp + __popcll(mask_kp & below)] = static_cast<int16_t>(c);
     __syncthreads();
     if (t == 0) {
-      int total = 0, total_re = 0;
+      int total = 0, total_re = 0, total_kp = 0;
       for (int q = 0; q < kReduceWaves; ++q) {
         total += part_s[q];
         total_re += part_s[kReduceWaves + q];
+        total_kp += part_s[2 * kReduceWaves + q];
       }
       s_live += total;
       s_dirty += total_re;
+      s_kept += total_kp;
     }
     __syncthreads();
   }
@@ -697,9 +706,10 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
 }
 
 // Round phase 2: the Lance-Williams rows of the round's kept rows
-// (litgpt/log_kv_cache.py:607-626) as wave tiles: up to kLwRows merges x
-// kLwCols * 64 live columns (kLwCols per lane, the columns' state held across
-// the merges). Each element is lw_columns' update: the row and, for a column
+// (litgpt/log_kv_cache.py:607-626) as wave tiles: up to kLwRows kept rows
+// (neighbours in row order) x kLwCols * 64 live columns (kLwCols per lane,
+// the columns' state held across the rows). Each element is lw_columns'
+// update: the row and, for a column
 // that is not kept, its mirror; the screen leaves only the elements that can
 // hold the kept row's minimum key (an atomic minimum per tile) or lower a
 // column's cached minimum to evaluate ward_cost.
@@ -713,7 +723,8 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
   const ReduceLds s = image_of(a, lane);
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * 3 * M;
+  const int16_t* kept = live + 2 * M;
   const int n_live = ctl.n_live, n_ok = ctl.n_ok;
   const int col_chunks = (n_live + kLwTile - 1) / kLwTile, waves = gridDim.x * kPhaseWaves;
   // Merges per item: up to kLwRows, fewer when that would leave waves idle.
@@ -737,8 +748,8 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_lw_kernel(ReduceArgs a) 
       thr[e] = col[e] >= 0 && !(fl[e] & (kKeep | kDirty)) ? key_cost(s.packed[c]) : -1.f;
     }
     const int p1 = min(n_ok, (pg + 1) * rows);
-    for (int p = pg * rows; p < p1; ++p) {
-      const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+    for (int j = pg * rows; j < p1; ++j) {
+      const int ra = kept[j], rb = s.best[ra], p = s.pair_of[ra];
       const float alpha = s.p_alpha[p], beta = s.p_beta[p], shift = s.p_shift[p];
       const float total = s.mass[ra], rad = s.radius[ra];
       float* row_a = dist + static_cast<int64_t>(ra) * M;
@@ -812,7 +823,7 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_rescan_kernel(ReduceArgs
   const ReduceLds s = image_of(a, lane);
   const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
-  const int16_t* live = a.live + static_cast<int64_t>(lane) * 2 * M;
+  const int16_t* live = a.live + static_cast<int64_t>(lane) * 3 * M;
   const int16_t* dirty = live + M;
   const int n_live = ctl.n_live, n_dirty = ctl.n_dirty;
   const int col_chunks = (n_live + kScanChunk - 1) / kScanChunk, waves = gridDim.x * kPhaseWaves;

@@ -40,8 +40,8 @@ struct ReduceArgs {
   uint8_t* image;         // [lanes, image_stride] the reducer state (the LDS layout) between launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
-  int16_t* live;          // [lanes, 2, M] the round's live rows (ctl.n_live) and rows to rescan
-                          // (ctl.n_dirty), each list ascending
+  int16_t* live;          // [lanes, 3, M] the round's live rows (ctl.n_live), rows to rescan
+                          // (ctl.n_dirty) and kept rows (ctl.n_ok), each list ascending
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -75,7 +75,7 @@ struct UnifiedBufs {
   uint8_t* image;         // [lanes, image_stride] reducer state between the round launches
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
-  int16_t* live;          // [lanes, 2, M]
+  int16_t* live;          // [lanes, 3, M]
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,
