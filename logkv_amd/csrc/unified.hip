@@ -383,7 +383,12 @@ int launch_dist(const float* mu, const int32_t* count, float* dist, int M, int D
 constexpr int kPhaseThreads = 256;
 constexpr int kPhaseWaves = kPhaseThreads / kWave;
 constexpr int kPhaseBlocks = 64;      // blocks per lane of the Lance-Williams / rescan phases
-constexpr int kPipelinedRounds = 40;  // rounds enqueued as phase launches before the finish kernel
+// Rounds enqueued as phase launches before the finish kernel: the radius
+// stage of a 4096-row flush of clustered keys ends in about 20 rounds, the
+// budget stage in 40 to 50 (an idle round still costs its three launches; a
+// tail round on the finish kernel's one block costs about what a pipelined
+// round of that size does).
+constexpr int kPipelinedRounds[2] = {40, 24};   // [LIMIT]
 
 __device__ inline ReduceLds image_of(const ReduceArgs& a, int lane) {
   return carve_lds(a.image + static_cast<int64_t>(lane) * a.image_stride, a.M);
@@ -944,7 +949,7 @@ int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
   hipLaunchKernelGGL(reduce_init_kernel, dim3(std::max(1, std::min(16, a.M / kPhaseThreads)), lanes),
                      dim3(kPhaseThreads), 0, stream, a);
   hipLaunchKernelGGL(reduce_rescan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
-  for (int round = 0; round < kPipelinedRounds; ++round) {
+  for (int round = 0; round < kPipelinedRounds[LIMIT]; ++round) {
     hipLaunchKernelGGL(reduce_plan_kernel<LIMIT>, dim3(lanes), dim3(kReduceThreads), lds, stream, a);
     hipLaunchKernelGGL(reduce_lw_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
     hipLaunchKernelGGL(reduce_rescan_kernel<LIMIT>, phase, dim3(kPhaseThreads), 0, stream, a);
