@@ -212,11 +212,11 @@ __global__ __launch_bounds__(256) void load_nodes_kernel(RowsArgs r, int n_group
 // to both (i, j) and (j, i), the diagonal is zero. Tiles wholly below the
 // diagonal or past the node count return at once.
 constexpr int kDistRows = 32, kDistCols = 64, kDistR = 2, kDistC = 4;
+constexpr int kDistThreads = (kDistRows / kDistR) * (kDistCols / kDistC);
 // Feature-major LDS rows padded so a thread's kDistR row values and kDistC
-// column values of one feature are one aligned 8-byte and one aligned 16-byte
-// read.
-constexpr int kDistRowLd = kDistRows + 2, kDistColLd = kDistCols + 4;
-static_assert(kDistR == 2 && kDistC == 4, "the tile reads are float2 / float4");
+// column values of one feature are each one aligned vector read.
+constexpr int kDistRowLd = kDistRows + kDistR, kDistColLd = kDistCols + kDistC;
+static_assert((kDistR == 2 || kDistR == 4) && kDistC == 4, "the tile reads are float2 / float4");
 
 template <int J>
 struct DistTile {
@@ -229,9 +229,15 @@ struct DistTile {
   __device__ __forceinline__ void leaf(const float* xb, const float* yb, int hi, float (&out)[kDistR * kDistC]) const {
 #pragma unroll
     for (int q = 0; q < J; ++q) {
-      const float2 x2 = *reinterpret_cast<const float2*>(xb + (8 * hi + 64 * q) * kDistRowLd);
+      float x[kDistR];
+      if constexpr (kDistR == 4) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xb + (8 * hi + 64 * q) * kDistRowLd);
+        x[0] = x4.x, x[1] = x4.y, x[2] = x4.z, x[3] = x4.w;
+      } else {
+        const float2 x2 = *reinterpret_cast<const float2*>(xb + (8 * hi + 64 * q) * kDistRowLd);
+        x[0] = x2.x, x[1] = x2.y;
+      }
       const float4 y4 = *reinterpret_cast<const float4*>(yb + (8 * hi + 64 * q) * kDistColLd);
-      const float x[kDistR] = {x2.x, x2.y};
       const float y[kDistC] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
       for (int r = 0; r < kDistR; ++r)
@@ -307,7 +313,7 @@ struct DistTile {
 };
 
 template <int J>
-__global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu, const int32_t* __restrict__ count,
+__global__ __launch_bounds__(kDistThreads) void dist_kernel(const float* __restrict__ mu, const int32_t* __restrict__ count,
                                                    float* __restrict__ dist, int M, int D) {
   extern __shared__ __align__(16) float tile_s[];
   const int lane = blockIdx.z, n = count[lane];
@@ -317,11 +323,11 @@ __global__ __launch_bounds__(256) void dist_kernel(const float* __restrict__ mu,
   float* xs = tile_s;
   float* ys = tile_s + 64 * J * kDistRowLd;
   const int t = threadIdx.x;
-  for (int e = t; e < kDistRows * 64 * J; e += 256) {
+  for (int e = t; e < kDistRows * 64 * J; e += kDistThreads) {
     const int r = e / (64 * J), d = e - r * (64 * J);
     xs[d * kDistRowLd + r] = i0 + r < n && d < D ? base[static_cast<int64_t>(i0 + r) * D + d] : 0.f;
   }
-  for (int e = t; e < kDistCols * 64 * J; e += 256) {
+  for (int e = t; e < kDistCols * 64 * J; e += kDistThreads) {
     const int c = e / (64 * J), d = e - c * (64 * J);
     ys[d * kDistColLd + c] = j0 + c < n && d < D ? base[static_cast<int64_t>(j0 + c) * D + d] : 0.f;
   }
@@ -361,10 +367,10 @@ int launch_dist(const float* mu, const int32_t* count, float* dist, int M, int D
                  : J == 3 ? reinterpret_cast<const void*>(&dist_kernel<3>)
                           : reinterpret_cast<const void*>(&dist_kernel<4>);
   if (!allow_dynamic_lds(fn, lds)) return LOGKV_ERUNTIME;
-  if (J == 1) hipLaunchKernelGGL(dist_kernel<1>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
-  else if (J == 2) hipLaunchKernelGGL(dist_kernel<2>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
-  else if (J == 3) hipLaunchKernelGGL(dist_kernel<3>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
-  else hipLaunchKernelGGL(dist_kernel<4>, grid, dim3(256), lds, stream, mu, count, dist, M, D);
+  if (J == 1) hipLaunchKernelGGL(dist_kernel<1>, grid, dim3(kDistThreads), lds, stream, mu, count, dist, M, D);
+  else if (J == 2) hipLaunchKernelGGL(dist_kernel<2>, grid, dim3(kDistThreads), lds, stream, mu, count, dist, M, D);
+  else if (J == 3) hipLaunchKernelGGL(dist_kernel<3>, grid, dim3(kDistThreads), lds, stream, mu, count, dist, M, D);
+  else hipLaunchKernelGGL(dist_kernel<4>, grid, dim3(kDistThreads), lds, stream, mu, count, dist, M, D);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
