@@ -1004,6 +1004,343 @@ __device__ __forceinline__ void ladder_units(const PoolT<KIND>& pool, const Soa&
   }
 }
 
+// ---------------------------------------------------------------------------
+// Beta carries four groups to a wave. A 16-lane row of the wave takes one Beta
+// group; lane l of the row holds features l + 16 k (k < 4 NJ) of the group's
+// rows. That places leaves l, l + 16, l + 32, l + 48 of the 64-leaf canonical
+// order in the lane (leaf a of the lane sums features l + 16 a + 64 j over j in
+// order), so the first two tree levels add inside the lane and the last four
+// (partners 8, 4, 2, 1 lanes away) are row rotations: every lane of the row
+// ends with the canonical sum, and each float operation of beta_group (the
+// cut costs, the side means, the outputs) is evaluated on the same operands
+// in the same order. Row-level scalars (side reciprocals, energies, the 12
+// cost quotients) are computed lane-parallel inside the row and exchanged by
+// lane permutes.
+
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// Value of lane `k` of this lane's 16-lane row.
+__device__ __forceinline__ float row_lane(float x, int k) {
+  return __int_as_float(__shfl(__float_as_int(x), (lane_id() & ~15) + k, kWave));
+}
+__device__ __forceinline__ int row_lane_i(int x, int k) { return __shfl(x, (lane_id() & ~15) + k, kWave); }
+__device__ __forceinline__ double row_lane_d(double x, int k) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __shfl(static_cast<int>(b), (lane_id() & ~15) + k, kWave);
+  const int hi = __shfl(static_cast<int>(b >> 32), (lane_id() & ~15) + k, kWave);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+// Features l16 + 16 k of one bf16 row (0 past D): one base address per row and
+// compile-time offsets; a lane past the row's end loads nothing.
+template <int F, bool FULL>
+__device__ __forceinline__ void load_row16(const LOGKV_G uint16_t* row, int l16, int D, bool valid, float (&x)[F]) {
+  const LOGKV_G uint16_t* at = row + l16;
+#pragma unroll
+  for (int k = 0; k < F; ++k) {
+    float a = 0.f;
+    if (FULL) a = bf16_to_f32(at[16 * k]);   // D == 16 F: every lane's features exist
+    else if (l16 + 16 * k < D) a = bf16_to_f32(at[16 * k]);
+    x[k] = valid ? a : 0.f;
+  }
+}
+
+// beta_component_losses on the row layout. Side sums of the cuts, feature by
+// feature: a side's sum in row order is its member rows' products x w with
+// the other rows' x * 0 between them; those zero-weight terms are +-0 or NaN,
+// and a run of them added to a partial sum gives the same result however the
+// run is grouped (NaN if any is NaN, -0 only if the partial sum and every
+// term are -0, else the partial sum). So the left side of cut c is the prefix
+// p0 + .. + p(c-1) plus the grouped zero-weight terms of rows c..3, and the
+// right side the zero-weight prefix of rows 0..c-1 followed by pc, .., p3 in
+// order: the term-by-term sums' values from shared partial sums. The
+// features are visited leaf by leaf (leaves a and a + 2 of the lane, then
+// a + 1 and a + 3), so only the pending level-32 nodes of the 12 (cut, row)
+// distance sums stay live between the passes.
+template <int NJ>
+__device__ __forceinline__ void row_component_losses(const float (&x)[4][4 * NJ], const float* wr, double rl, float& e,
+                                                     float* loss) {
+  float sq[4];
+  {
+    float n32[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float lf[2][4];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int a = h + 2 * half;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int k = a + 4 * j;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = x[i][k] * x[i][k];
+            lf[half][i] = j == 0 ? v : lf[half][i] + v;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) n32[h][i] = lf[0][i] + lf[1][i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s16 = n32[0][i] + n32[1][i];
+      s16 = s16 + row_ror<8>(s16);
+      s16 = s16 + row_ror<4>(s16);
+      s16 = s16 + row_ror<2>(s16);
+      sq[i] = s16 + row_ror<1>(s16);
+    }
+  }
+  e = sq[0] * wr[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) e = e + sq[i] * wr[i];
+  // The side reciprocals of the cuts (2, 1, 3), left then right, from the
+  // row's lanes 0..5.
+  double rcp[6];
+#pragma unroll
+  for (int q = 0; q < 6; ++q) rcp[q] = row_lane_d(rl, q);
+  float n32[2][3][4];   // [h][opt][row]
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float lf[2][3][4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int a = h + 2 * half;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int k = a + 4 * j;
+        const float p0 = x[0][k] * wr[0], p1 = x[1][k] * wr[1], p2 = x[2][k] * wr[2], p3 = x[3][k] * wr[3];
+        const float z0 = x[0][k] * 0.f, z1 = x[1][k] * 0.f, z2 = x[2][k] * 0.f, z3 = x[3][k] * 0.f;
+        const float l2 = p0 + p1, l3 = l2 + p2;            // left prefixes of cuts 2, 3 (cut 1: p0)
+        const float s2 = z2 + z3, s1 = z1 + s2;            // zero-weight runs of rows c..3 (cut 3: z3)
+        const float zp2 = z0 + z1, zp3 = zp2 + z2;         // zero-weight prefixes of rows 0..c-1
+        float mean[3][2];                                  // [opt][side]
+        mean[1][0] = div_by_rcp(p0 + s1, rcp[2]);
+        mean[0][0] = div_by_rcp(l2 + s2, rcp[0]);
+        mean[2][0] = div_by_rcp(l3 + z3, rcp[4]);
+        mean[1][1] = div_by_rcp(((z0 + p1) + p2) + p3, rcp[3]);
+        mean[0][1] = div_by_rcp((zp2 + p2) + p3, rcp[1]);
+        mean[2][1] = div_by_rcp(zp3 + p3, rcp[5]);
+#pragma unroll
+        for (int opt = 0; opt < 3; ++opt) {
+          const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float d = x[i][k] - mean[opt][i < c ? 0 : 1];
+            const float v = d * d;
+            lf[half][opt][i] = j == 0 ? v : lf[half][opt][i] + v;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int opt = 0; opt < 3; ++opt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) n32[h][opt][i] = lf[0][opt][i] + lf[1][opt][i];
+  }
+#pragma unroll
+  for (int opt = 0; opt < 3; ++opt) {
+    const int c = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s16 = n32[0][opt][i] + n32[1][opt][i];
+      s16 = s16 + row_ror<8>(s16);
+      s16 = s16 + row_ror<4>(s16);
+      s16 = s16 + row_ror<2>(s16);
+      t[i] = s16 + row_ror<1>(s16);
+    }
+    float left = t[0] * (0 < c ? wr[0] : 0.f), right = t[0] * (0 < c ? 0.f : wr[0]);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+      left = left + t[i] * (i < c ? wr[i] : 0.f);
+      right = right + t[i] * (i < c ? 0.f : wr[i]);
+    }
+    loss[2 * opt] = left;
+    loss[2 * opt + 1] = right;
+  }
+}
+
+// Rows of one Beta group as seen by a lane: the pool is per lane (its row's
+// ladder), the staged source by kind.
+struct GroupRows {
+  const LOGKV_G uint16_t* k[4];
+  const LOGKV_G uint16_t* v[4];
+  float w[4];
+};
+
+template <int KIND>
+__device__ __forceinline__ void group_rows(const PoolT<KIND>& pool, int start, int width, GroupRows& g) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = i < width ? start + i : start;
+    g.k[i] = pool.k(p);
+    g.v[i] = pool.v(p);
+    const float wp = pool.w(p);
+    g.w[i] = i < width ? wp : 0.f;
+  }
+}
+
+// One Beta group per 16-lane row: rows [4 gi, 4 gi + width) of the lane's
+// ladder pool at level ell into its carries 2 gi, 2 gi + 1 (beta_group's
+// arithmetic). `live` false: the row only takes part in the row exchanges.
+template <int NJ, bool FULL>
+__device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, int ladder,
+                                               int ell, int gi, bool live) {
+  constexpr int F = 4 * NJ;
+  const int l16 = lane_id() & 15;
+  const LadderPlan* pl = ws.plans + ladder;
+  const int cnt = pl->cnt[ell], m = pl->m[ell];
+  const int n_pair = 2 * carries_of(cnt, m, c.slots, false);
+  const int start = 4 * gi;
+  const int width = max(0, min(4, n_pair - start));
+  const bool flush_src = ell == 0 && pl->kind0 == 0;
+  const Ladder lad = ladder_of(c, ladder);
+  const int64_t base = static_cast<int64_t>(ell) * c.slots;
+  const int dk = c.dk, dv = c.dv;
+  GroupRows g;
+  if (flush_src) group_rows<2>(PoolT<2>{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)}, start, width, g);
+  else group_rows<1>(PoolT<1>{lad, base, cnt, staged_of(ws, ladder, ell, dk, dv)}, start, width, g);
+  float xk[4][F];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) load_row16<F, FULL>(g.k[i], l16, dk, i < width, xk[i]);
+  // Side reciprocals of the cuts (2, 1, 3): lane l16 < 6 of the row divides
+  // (left, right of cut 2, of cut 1, of cut 3).
+  double rl;
+  {
+    float mass = 1.f;
+#pragma unroll
+    for (int opt = 0; opt < 3; ++opt) {
+      const int cc = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+      float wl[4], wrt[4];
+      cut_weights(g.w, cc, wl, wrt);
+      mass = l16 == 2 * opt ? side_mass(wl) : mass;
+      mass = l16 == 2 * opt + 1 ? side_mass(wrt) : mass;
+    }
+    rl = 1.0 / static_cast<double>(fmaxf(mass, 1e-12f));
+  }
+  int cut = 2;
+  {
+    float ek, ev, lk[6], lv[6];
+    row_component_losses<NJ>(xk, g.w, rl, ek, lk);
+    asm volatile("" ::: "memory");   // V's loads after K's costs: one component's rows live at a time
+    float xv[4][F];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_row16<F, FULL>(g.v[i], l16, dv, i < width, xv[i]);
+    row_component_losses<NJ>(xv, g.w, rl, ev, lv);
+    // beta_cut's decision: energies and the 12 quotients lane-parallel in the
+    // row, the costs summed in lane 0 in beta_cut's order.
+    const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
+    const float en = (l16 == 0 ? ek : ev) / total;
+    const float energy_k = fmaxf(row_lane(en, 0), 1e-12f);
+    const float energy_v = fmaxf(row_lane(en, 1), 1e-12f);
+    float num = 0.f;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      num = l16 == k ? lk[k] : num;
+      num = l16 == 6 + k ? lv[k] : num;
+    }
+    const float q = num / (l16 < 6 ? energy_k : energy_v);
+    float costs[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 12; ++k) costs[(k % 6) / 2] = costs[(k % 6) / 2] + row_lane(q, k);
+    int best = 0;
+    if (costs[1] < costs[best]) best = 1;
+    if (costs[2] < costs[best]) best = 2;
+    cut = width == 4 ? (best == 0 ? 2 : (best == 1 ? 1 : 3)) : 2;
+  }
+  // Outputs (beta_group's side means), K then V; the rows are loaded again
+  // (the barrier keeps the compiler from holding the first loads live).
+  asm volatile("" ::: "memory");
+  const int opt = cut == 2 ? 0 : (cut == 1 ? 1 : 2);
+  const int dest = start / 2;
+  const Soa out = carry_of(ws, ladder, ell, dk, dv);
+  const double left_rcp = row_lane_d(rl, 2 * opt), right_rcp = row_lane_d(rl, 2 * opt + 1);
+  const unsigned left_rows = (1u << cut) - 1u;
+#pragma unroll
+  for (int comp = 0; comp < 2; ++comp) {
+    const int D = comp == 0 ? dk : dv;
+    float x[4][F];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_row16<F, FULL>(comp == 0 ? g.k[i] : g.v[i], l16, D, i < width, x[i]);
+    LOGKV_G uint16_t* dst = comp == 0 ? out.k : out.v;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const unsigned member = side == 0 ? left_rows : (0xfu & ~left_rows);
+      const double srcp = side == 0 ? left_rcp : right_rcp;
+      LOGKV_G uint16_t* at = dst + static_cast<int64_t>(dest + side) * D + l16;
+      const bool write = live && (side == 0 || width == 4);
+#pragma unroll
+      for (int k = 0; k < F; ++k) {
+        float acc = (member & 1u) ? x[0][k] * g.w[0] : x[0][k] * 0.f;
+#pragma unroll
+        for (int i = 1; i < 4; ++i) acc = acc + (((member >> i) & 1u) ? x[i][k] * g.w[i] : x[i][k] * 0.f);
+        if (write && (FULL || l16 + 16 * k < D)) at[16 * k] = f32_to_bf16(div_by_rcp(acc, srcp));
+      }
+    }
+  }
+  // Metadata of both outputs: lanes 0-3 of the row hold rows 0-3 for the left
+  // side, lanes 4-7 the same rows for the right side (quads of side_meta).
+  {
+    Meta mine{};
+    const int mi = l16 & 3;
+    if (l16 < 8 && mi < width) {
+      if (flush_src) mine = PoolT<2>{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)}.meta(start + mi);
+      else mine = PoolT<1>{lad, base, cnt, staged_of(ws, ladder, ell, dk, dv)}.meta(start + mi);
+    }
+    const int side = (l16 >> 2) & 1;
+    const unsigned member = side == 0 ? left_rows : (0xfu & ~left_rows);
+    float wt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? g.w[i] : 0.f;
+    const float mass = side_mass(wt);
+    const bool in_side = mi < width && ((member >> mi) & 1u);
+    const Meta res = side_meta(mine, in_side, mass);
+    if (live && l16 < 8 && (l16 & 3) == 0 && (side == 0 || width == 4)) put_soa_meta(out, dest + side, res);
+  }
+}
+
+// Beta carries launch `ell`: the level's units in consecutive quads, one quad
+// per wave step (a wave's quads are contiguous); each lane finds its row's
+// ladder by binary search once, then walks forward.
+template <int NJ, bool FULL>
+__global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderArgs c, RowsArgs r, Workspace ws, int ell) {
+  extern __shared__ __align__(16) int32_t prefix_s[];
+  const int ladders = c.n_batch * c.n_groups * c.k_max;
+  const LOGKV_G int32_t* pre = gp(ws.units + static_cast<int64_t>(ell) * (ladders + 1));
+  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  __syncthreads();
+  const int total = prefix_s[ladders];
+  if (total == 0) return;
+  const int quads = (total + 3) / 4;
+  const int wpb = static_cast<int>(blockDim.x) / kWave;
+  const int n_waves = static_cast<int>(gridDim.x) * wpb;
+  const int per = (quads + n_waves - 1) / n_waves;
+  int qd = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
+  const int qd_end = min(quads, qd + per);
+  if (qd >= qd_end) return;
+  const int row = lane_id() >> 4;
+  int ladder = 0;   // prefix_s[ladder] <= unit < prefix_s[ladder + 1]
+  {
+    const int u0 = min(4 * qd + row, total - 1);
+    for (int len = ladders; len > 1;) {
+      const int half = len >> 1;
+      ladder = prefix_s[ladder + half] <= u0 ? ladder + half : ladder;
+      len -= half;
+    }
+  }
+  for (; qd < qd_end; ++qd) {
+    const int unit = 4 * qd + row;
+    const bool live = unit < total;
+    const int uu = live ? unit : total - 1;
+    while (prefix_s[ladder + 1] <= uu) ++ladder;
+    beta_row_group<NJ, FULL>(c, r, ws, ladder, ell, uu - prefix_s[ladder], live);
+  }
+}
+
 // Carries launch `ell`: the level's work units (numbered ladder after ladder
 // by units_kernel) are split into contiguous ranges, one per wave, so a wave
 // resolves a ladder's plan and sources once for all its units there and reads
@@ -1284,14 +1621,26 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
     hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kUnitsThreads), 0, stream, c, p, ws);
     const size_t carry_shmem = (static_cast<size_t>(ladders) + 1) * 4;
     const bool narrow = c.dk <= 2 * kWave && c.dv <= 2 * kWave;
-    const void* carries = narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
-                                 : reinterpret_cast<const void*>(&carries_kernel<4>);
+    // Beta groups of rows up to 128 features: four groups to a wave.
+    const bool rows16 = narrow && p.beta_merge != 0;
+    const bool full = c.dk == 2 * kWave && c.dv == 2 * kWave;
+    const void* carries = rows16   ? (full ? reinterpret_cast<const void*>(&beta_carries_kernel<2, true>)
+                                           : reinterpret_cast<const void*>(&beta_carries_kernel<2, false>))
+                          : narrow ? reinterpret_cast<const void*>(&carries_kernel<2>)
+                                   : reinterpret_cast<const void*>(&carries_kernel<4>);
     if (!allow_dynamic_lds(carries, carry_shmem)) return LOGKV_ERUNTIME;
+    const int units_per_block = (kCarryThreads / kWave) * (rows16 ? 4 : 1);
     for (int ell = 0; ell + 1 < c.levels; ++ell) {
       // Units at level ell: at most ceil(carries / 2) Beta groups (or carries) per ladder.
       const int64_t bound = static_cast<int64_t>(ladders) * carry_cap(ws.m0_cap, ell);
-      const int64_t blocks = std::min<int64_t>(kCarryBlocks, std::max<int64_t>(1, bound / (kCarryThreads / kWave)));
-      if (narrow)
+      const int64_t blocks = std::min<int64_t>(kCarryBlocks, std::max<int64_t>(1, bound / units_per_block));
+      if (rows16 && full)
+        hipLaunchKernelGGL((beta_carries_kernel<2, true>), dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, ws,
+                           ell);
+      else if (rows16)
+        hipLaunchKernelGGL((beta_carries_kernel<2, false>), dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r,
+                           ws, ell);
+      else if (narrow)
         hipLaunchKernelGGL(carries_kernel<2>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
       else
         hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);

@@ -136,3 +136,36 @@ def test_attach_decisions_with_seeds_and_ragged_rows():
         np.testing.assert_array_equal(to_np(order)[b, :n], want_order[b, :n])
         np.testing.assert_array_equal(to_np(assign)[b, :, :n], want[b, :, :n])
         assert (to_np(assign)[b, :, n:] == -1).all()
+
+
+def test_beta_carries_keep_signed_zero_features():
+    """Beta carries on 128-feature rows (four groups to a wave) whose feature
+    columns are all -0, all +0, or mixed in sign across rows: the output
+    means' zero signs follow the reference's term-by-term row sums, so the
+    stored ladder rows are compared as bf16 bit patterns, not values."""
+    print("case Beta carries, signed-zero columns", flush=True)
+    gpu, ora = make_pair(1, 2, 128, 4, 8, 64, 64, 2048, 16.0, exact=16, span=4, beta_adaptive=True)
+    mix = Mixture(1, 2, 128, clusters=4, seed=41)
+    dev = gpu.level_k.device
+    neg = torch.tensor(-0.0, dtype=torch.bfloat16)
+    for blk in range(12):
+        n = 64
+        k_raw, v, k = mix.rows(n), mix.rows(n), mix.rows(n)
+        for t in (k_raw, v, k):
+            t[..., 0:8] = neg                     # every row -0
+            t[..., 8:16] = 0.0                    # every row +0
+            sign = torch.arange(n) % 3 == 0       # -0 on every third row, +0 elsewhere
+            t[..., :, 16:24] = torch.where(sign[:, None], neg, torch.zeros((), dtype=torch.bfloat16))
+        pos = torch.arange(blk * n, (blk + 1) * n).unsqueeze(0).contiguous()
+        ends = mix.span_ends(blk * n, n)
+        gpu.add_recent(k.to(dev), v.to(dev), k_raw=k_raw.to(dev), input_pos=pos.to(dev), span_ends=ends)
+        ora.add_recent(k.float().numpy(), v.float().numpy(), k_raw.float().numpy(), pos.numpy(), ends)
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"block {blk}: " + "; ".join(bad)
+        for f in ("level_k", "level_v"):
+            bits = getattr(gpu, f).view(torch.int16).cpu().numpy()
+            ref = (np.asarray(getattr(ora, f), np.float32).view(np.uint32) >> 16).astype(np.uint16).view(np.int16)
+            live = np.arange(bits.shape[-2])[None, None, None, None, :] < np.asarray(ora.level_count)[..., None]
+            assert np.array_equal(np.where(live[..., None], bits, 0), np.where(live[..., None], ref, 0)), f"{f} bits"
+    assert int(np.asarray(ora.level_count)[..., 1:].sum()) > 0, "no carry reached level 1"
