@@ -187,6 +187,42 @@ int logkv_replay_commit(const logkv_ladder_view* cache, const logkv_rows_view* r
                         const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
                         const logkv_op_log_view* log, int64_t cursor, int32_t* status, void* stream);
 
+/* Op-log of a unified-routed flush, after logkv_unified_commit on the same
+ * workspace: per lane the WARD_MERGE rows (keep, free, -1) of its old-old
+ * merges in merge order, then the NEW_CLUSTER / JOIN rows logkv_record_ops
+ * writes. Replaces the unified route's recording (litgpt/log_kv_cache.py:
+ * 2597-2598, :3661-3688 with record=True). */
+int logkv_unified_record_ops(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                             const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                             const logkv_op_log_view* log, void* stream);
+
+/* Parses one logged unified flush for replay without routing: per lane from
+ * cursors[lane] (device int64[lanes]), its leading WARD_MERGE rows become the
+ * lane's old-old merges (each between two distinct clusters live at that
+ * point), then one NEW_CLUSTER / JOIN row per valid flush row gives the
+ * decisions, checked as logkv_replay_commit checks them against the clusters
+ * live after the merges. consumed[lane] (device int32) receives the rows the
+ * lane consumed; status (device int32[2]) receives the check bits and the most
+ * merges of any lane. With status[0] == 0, logkv_unified_commit on the same
+ * workspace with merge_steps = status[1] applies the flush. Replaces the
+ * unified branch of _semantic_build_replay_plan and the replay loop
+ * (litgpt/log_kv_cache.py:4856-4926, :5067-5114). */
+int logkv_unified_replay_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                              const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                              const logkv_op_log_view* log, const int64_t* cursors, int32_t* consumed,
+                              int32_t* status, void* stream);
+
+/* Copies a unified plan's decisions between the workspace and caller buffers
+ * (into_workspace = 0: out of the workspace after logkv_unified_plan; 1: back
+ * in before logkv_unified_commit): assign int8[lanes, T], order int32[n_batch,
+ * T], jobs int32[lanes, 32, 2] (old-old merges), n_jobs int32[lanes]. The
+ * update tape's record / replay of a unified flush (litgpt/log_kv_cache.py:
+ * 4946-5031). */
+int logkv_unified_decisions(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                            const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                            int8_t* assign, int32_t* order, int32_t* jobs, int32_t* n_jobs, int32_t into_workspace,
+                            void* stream);
+
 /* Candidate span table over the virtual rows [old exact pool (old_width rows) |
  * flush]: pool_* / flush_* are [n_batch, G, rows, d] bf16 with element strides;
  * span i covers tokens[span_offsets[i] .. span_offsets[i+1]) of batch row

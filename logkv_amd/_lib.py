@@ -155,8 +155,8 @@ OP_NEW_CLUSTER, OP_NEW_SEGMENT, OP_JOIN, OP_WARD_MERGE, OP_PAD_INSERT = 0, 1, 2,
 
 # Replay status bits of logkv_replay_commit -> what failed.
 REPLAY_ERRORS = {
-    1: "a log row is not a NEW_CLUSTER / JOIN of segment 0 of a cluster in range (segment pads and Ward merges "
-       "are not recorded by the attach route)",
+    1: "a log row is not a NEW_CLUSTER / JOIN of segment 0 of a cluster in range (segment pads are not recorded "
+       "on this path; Ward merges only lead a unified-routed flush's rows, between two live clusters)",
     2: "a logged position is not in the current flush positions",
     4: "the current flush positions contain duplicate token ids",
     8: "the log holds fewer rows than the flush has tokens",
@@ -181,6 +181,12 @@ SIGNATURES = {
     "logkv_unified_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p, _i64,
                                     _i32, _p]),
     "logkv_record_ops": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), _p, _i64, C.POINTER(OpLogView), _p]),
+    "logkv_unified_record_ops": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p, _i64,
+                                        C.POINTER(OpLogView), _p]),
+    "logkv_unified_replay_plan": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p,
+                                         _i64, C.POINTER(OpLogView), _p, _p, _p, _p]),
+    "logkv_unified_decisions": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p, _i64,
+                                       _p, _p, _p, _p, _i32, _p]),
     "logkv_replay_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
                                    _p, _i64, C.POINTER(OpLogView), _i64, _p, _p]),
     "logkv_score_spans": (_i32, [C.POINTER(SpanArgs), _p, _p]),

@@ -374,14 +374,18 @@ def alpha_flush(cache, k_raw, v, positions, positions_host, span_ends, record=Fa
         A = bufs["k"].size(2)
         assign = torch.empty(cache.batch_size * cache.n_groups, A, dtype=torch.int8, device=dev)
         order = torch.empty(cache.batch_size, A, dtype=torch.int32, device=dev)
-    cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], assign, order, record=record)
+    merges = cache._route_commit(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], assign, order, record=record)
     if tape is None:
         return None
-    return {"k": tape.save(k_raw), "v": tape.save(v), "pos": tape.save(positions), "ends": tape.save(ends),
-            "keep": tape.save(bufs["keep"]), "archive": tape.save(bufs["archive"]), "count": tape.save(bufs["count"]),
-            "span_len": tape.save(cache.alpha_span_len), "span_closed": tape.save(cache.alpha_span_closed),
-            "span_count": tape.save(cache.alpha_span_count), "alpha_count": tape.save(cache.alpha_count_dev),
-            "assign": tape.save(assign, owned=True), "order": tape.save(order, owned=True)}
+    saved = {"k": tape.save(k_raw), "v": tape.save(v), "pos": tape.save(positions), "ends": tape.save(ends),
+             "keep": tape.save(bufs["keep"]), "archive": tape.save(bufs["archive"]), "count": tape.save(bufs["count"]),
+             "span_len": tape.save(cache.alpha_span_len), "span_closed": tape.save(cache.alpha_span_closed),
+             "span_count": tape.save(cache.alpha_span_count), "alpha_count": tape.save(cache.alpha_count_dev),
+             "assign": tape.save(assign, owned=True), "order": tape.save(order, owned=True)}
+    # The unified route's old-old merges (its decisions are assign / order as the attach route's).
+    for name, t in (merges or {}).items():
+        saved[name] = tape.save(t, owned=True)
+    return saved
 
 
 def _swap_pool(cache):
@@ -414,4 +418,4 @@ def alpha_replay(cache, saved):
     cache.alpha_span_count.copy_(saved["span_count"])
     cache.alpha_count_dev.copy_(saved["alpha_count"])
     cache._alpha_keep_alive = (ends, positions)
-    cache._commit_only(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], saved["assign"], saved["order"])
+    cache._commit_only(bufs["k"], bufs["v"], bufs["pos"], bufs["count"], saved["assign"], saved["order"], saved)

@@ -391,6 +391,85 @@ int logkv_replay_commit(const logkv_ladder_view* cache, const logkv_rows_view* r
   return LOGKV_OK;
 }
 
+namespace {
+
+// Carves the unified workspace as logkv_unified_plan / logkv_unified_commit do.
+int unified_bufs(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
+                 void* workspace, int64_t workspace_bytes, logkv::Workspace& ws, logkv::UnifiedBufs& u) {
+  int rc = carve(cache, rows, params, workspace, workspace_bytes, nullptr, nullptr, ws, 1);
+  if (rc) return rc;
+  if ((rc = check_unified(cache, rows))) return rc;
+  const int late = params->late_joins ? 1 : 0;
+  const int64_t need = unified_layout(cache, rows->tokens, late, nullptr, nullptr);
+  if (workspace_bytes < need)
+    return fail(LOGKV_EINVAL, "workspace of %lld bytes is smaller than the %lld required", (long long)workspace_bytes,
+                (long long)need);
+  unified_layout(cache, rows->tokens, late, static_cast<uint8_t*>(workspace), &u);
+  return LOGKV_OK;
+}
+
+}  // namespace
+
+int logkv_unified_record_ops(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                             const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                             const logkv_op_log_view* log, void* stream) {
+  logkv::Workspace ws{};
+  logkv::UnifiedBufs u{};
+  int rc = unified_bufs(cache, rows, params, workspace, workspace_bytes, ws, u);
+  if (rc) return rc;
+  if ((rc = check_log(cache, log))) return rc;
+  if (!rows->tokens) return LOGKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = logkv::launch_record_wards(*cache, u.jobs, u.n_jobs, *log, s);
+  if (!rc) rc = logkv::launch_record(*cache, *rows, ws, *log, s);
+  if (rc) return fail(rc, "op-log record launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_unified_replay_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                              const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                              const logkv_op_log_view* log, const int64_t* cursors, int32_t* consumed,
+                              int32_t* status, void* stream) {
+  logkv::Workspace ws{};
+  logkv::UnifiedBufs u{};
+  int rc = unified_bufs(cache, rows, params, workspace, workspace_bytes, ws, u);
+  if (rc) return rc;
+  if ((rc = check_log(cache, log))) return rc;
+  if (!cursors || !consumed || !status) return fail(LOGKV_EINVAL, "replay cursors, consumed or status are NULL");
+  if (!rows->tokens) return LOGKV_OK;
+  rc = logkv::launch_unified_replay(*cache, *rows, ws, *log, cursors, consumed, u.jobs, u.n_jobs, status,
+                                    static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "replay launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_unified_decisions(const logkv_ladder_view* cache, const logkv_rows_view* rows,
+                            const logkv_route_params* params, void* workspace, int64_t workspace_bytes,
+                            int8_t* assign, int32_t* order, int32_t* jobs, int32_t* n_jobs, int32_t into_workspace,
+                            void* stream) {
+  logkv::Workspace ws{};
+  logkv::UnifiedBufs u{};
+  int rc = unified_bufs(cache, rows, params, workspace, workspace_bytes, ws, u);
+  if (rc) return rc;
+  if (!assign || !order || !jobs || !n_jobs) return fail(LOGKV_EINVAL, "decision buffers are NULL");
+  const int64_t lanes = int64_t(cache->n_batch) * cache->n_groups;
+  struct Region {
+    void* ws;
+    void* user;
+    int64_t bytes;
+  } const regions[4] = {{ws.assign, assign, lanes * rows->tokens},
+                        {ws.order, order, int64_t(cache->n_batch) * rows->tokens * 4},
+                        {u.jobs, jobs, lanes * logkv::kMaxClusters * 8},
+                        {u.n_jobs, n_jobs, lanes * 4}};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (const Region& g : regions) {
+    const hipError_t e = into_workspace ? hipMemcpyAsync(g.ws, g.user, g.bytes, hipMemcpyDeviceToDevice, s)
+                                        : hipMemcpyAsync(g.user, g.ws, g.bytes, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return fail(LOGKV_ERUNTIME, "decision copy failed: %s", hipGetErrorString(e));
+  }
+  return LOGKV_OK;
+}
+
 int logkv_score_spans(const logkv_span_args* a, float* scores, void* stream) {
   if (!a || !scores) return fail(LOGKV_EINVAL, "span args or output are NULL");
   if (a->n_spans < 0) return fail(LOGKV_EINVAL, "negative span count");

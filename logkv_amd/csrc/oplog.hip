@@ -84,6 +84,23 @@ __global__ __launch_bounds__(kRecordThreads) void record_kernel(LadderArgs c, Ro
   if (threadIdx.x == 0) log.lengths[lane_ix] = static_cast<int32_t>(len0 + total_s);
 }
 
+// WARD_MERGE rows (keep, free, -1) of the unified route's old-old merges, per
+// lane in merge order (litgpt/log_kv_cache.py:2597-2598): appended before the
+// flush's NEW_CLUSTER / JOIN rows, as the reference's merge steps run before
+// its new clusters and joins (:3661-3688). jobs [lanes, kMaxClusters, 2].
+__global__ __launch_bounds__(kWave) void record_ward_kernel(const int32_t* __restrict__ jobs,
+                                                            const int32_t* __restrict__ n_jobs, logkv_op_log_view log) {
+  const int lane_ix = blockIdx.x, l = threadIdx.x;
+  const int n = n_jobs[lane_ix];
+  const int64_t len0 = log.lengths[lane_ix], cap = log.capacity;
+  int32_t* rows = log.rows + static_cast<int64_t>(lane_ix) * cap * 4;
+  const int32_t* jl = jobs + static_cast<int64_t>(lane_ix) * kMaxClusters * 2;
+  for (int j = l; j < n; j += kWave)
+    if (len0 + j < cap) *reinterpret_cast<int4*>(rows + (len0 + j) * 4) = make_int4(LOGKV_OP_WARD_MERGE, jl[2 * j], jl[2 * j + 1], -1);
+  __syncthreads();
+  if (l == 0) log.lengths[lane_ix] = static_cast<int32_t>(len0 + n);
+}
+
 // Replay parse, one wave per lane: the log rows [cursor, cursor + n) name the
 // cluster of every valid flush row by position (litgpt/log_kv_cache.py:
 // 4856-4904, one row per consumed token). Writes the decision array in
@@ -93,12 +110,30 @@ __global__ __launch_bounds__(kRecordThreads) void record_kernel(LadderArgs c, Ro
 // JOIN into a dead one, a cluster's rows out of position order (the commit
 // appends each cluster's rows in position order, and a dead cluster opens
 // with its earliest row, as recorded).
+//
+// With `wards` (the unified route's logs), each lane has its own cursor and
+// the lane's rows may open with WARD_MERGE rows (keep, free): they become the
+// lane's merge list in the unified workspace layout, every merge between two
+// distinct clusters live at that point (the free one dies), and the flush's
+// NEW_CLUSTER / JOIN rows are checked against the clusters live after the
+// merges. The rows a lane consumed and the most merges of any lane are
+// reported for the host.
+struct ReplayWards {
+  const int64_t* cursors;   // [lanes] per-lane cursors
+  int32_t* consumed;        // [lanes] rows consumed (merges + flush rows)
+  int32_t* jobs;            // [lanes, kMaxClusters, 2] (keep, free) in log order
+  int32_t* n_jobs;          // [lanes]
+  int32_t* steps;           // most merges of a lane (atomic max; zeroed by the order launch)
+};
+
 __global__ __launch_bounds__(kWave) void replay_kernel(LadderArgs c, RowsArgs r, Workspace ws, logkv_op_log_view log,
-                                                       int64_t cursor, int32_t* status) {
+                                                       int64_t cursor, int32_t* status, ReplayWards wards) {
   __shared__ int64_t last_pos[kMaxClusters];
   __shared__ int seen[kMaxClusters];
   __shared__ int chunk_c[kWave];
   __shared__ int64_t chunk_p[kWave];
+  __shared__ int n_ward_s, ward_err_s;
+  __shared__ uint32_t alive_s;
   const int lane_ix = blockIdx.x, K = c.k_max, l = threadIdx.x;
   const int b = lane_ix / c.n_groups;
   const int n = valid_rows(r, b), T = r.tokens;
@@ -117,8 +152,39 @@ __global__ __launch_bounds__(kWave) void replay_kernel(LadderArgs c, RowsArgs r,
   for (int s = l + 1; s < n; s += kWave)
     if (posb[ord[s]] == posb[ord[s - 1]]) err |= LOGKV_REPLAY_DUPLICATE_POSITION;
   const int64_t logged = min(static_cast<int64_t>(log.lengths[lane_ix]), log.capacity);
-  if (cursor < 0 || cursor + n > logged) err |= LOGKV_REPLAY_SHORT_LOG;
   const int32_t* rows = log.rows + static_cast<int64_t>(lane_ix) * log.capacity * 4;
+  if (wards.jobs) {
+    cursor = wards.cursors[lane_ix];
+    if (l == 0) {
+      int j = 0, werr = 0;
+      uint32_t live = alive;
+      int32_t* jl = wards.jobs + static_cast<int64_t>(lane_ix) * kMaxClusters * 2;
+      while (cursor >= 0 && cursor + j < logged) {
+        const int4 row = *reinterpret_cast<const int4*>(rows + (cursor + j) * 4);
+        if (row.x != LOGKV_OP_WARD_MERGE) break;
+        const int keep = row.y, fr = row.z;
+        const bool ok = j < K - 1 && keep >= 0 && keep < K && fr >= 0 && fr < K && keep != fr &&
+                        ((live >> keep) & 1u) && ((live >> fr) & 1u);
+        if (!ok) {
+          werr |= LOGKV_REPLAY_BAD_OP;
+          break;
+        }
+        jl[2 * j] = keep;
+        jl[2 * j + 1] = fr;
+        live &= ~(1u << fr);
+        ++j;
+      }
+      wards.n_jobs[lane_ix] = werr ? 0 : j;
+      n_ward_s = j;
+      ward_err_s = werr;
+      alive_s = live;
+    }
+    __syncthreads();
+    err |= ward_err_s;
+    cursor += n_ward_s;
+    alive = alive_s;
+  }
+  if (cursor < 0 || cursor + n > logged) err |= LOGKV_REPLAY_SHORT_LOG;
   __threadfence_block();
   __syncthreads();
   for (int i0 = 0; i0 < n; i0 += kWave) {
@@ -177,6 +243,10 @@ __global__ __launch_bounds__(kWave) void replay_kernel(LadderArgs c, RowsArgs r,
     if (as[s] < 0) err |= LOGKV_REPLAY_UNCONSUMED;
   for (int d = 1; d < kWave; d <<= 1) err |= __shfl_xor(err, d, kWave);
   if (l == 0 && err) atomicOr(status, err);
+  if (wards.jobs && l == 0) {
+    wards.consumed[lane_ix] = n_ward_s + n;
+    atomicMax(wards.steps, n_ward_s);
+  }
 }
 
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
@@ -191,7 +261,26 @@ int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, c
   const int lanes = c.n_batch * c.n_groups;
   int rc = launch_order(r, c.n_batch, ws.order, status, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(replay_kernel, dim3(lanes), dim3(kWave), 0, stream, c, r, ws, log, cursor, status);
+  hipLaunchKernelGGL(replay_kernel, dim3(lanes), dim3(kWave), 0, stream, c, r, ws, log, cursor, status, ReplayWards{});
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+int launch_record_wards(const LadderArgs& c, const int32_t* jobs, const int32_t* n_jobs, const logkv_op_log_view& log,
+                        hipStream_t stream) {
+  hipLaunchKernelGGL(record_ward_kernel, dim3(c.n_batch * c.n_groups), dim3(kWave), 0, stream, jobs, n_jobs, log);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
+// status[0]: the check bits, status[1]: the most merges of a lane (both
+// cleared in stream order by the order launch's first block).
+int launch_unified_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
+                          const int64_t* cursors, int32_t* consumed, int32_t* jobs, int32_t* n_jobs, int32_t* status,
+                          hipStream_t stream) {
+  const int lanes = c.n_batch * c.n_groups;
+  int rc = launch_order(r, c.n_batch, ws.order, status, stream, 2);
+  if (rc) return rc;
+  hipLaunchKernelGGL(replay_kernel, dim3(lanes), dim3(kWave), 0, stream, c, r, ws, log, int64_t(0), status,
+                     ReplayWards{cursors, consumed, jobs, n_jobs, status + 1});
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

@@ -14,11 +14,12 @@ namespace logkv {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void order_kernel(const int64_t* __restrict__ pos, int64_t pos_sb,
                                                      const int32_t* __restrict__ counts, int32_t tokens,
-                                                     int32_t* __restrict__ order, int32_t* __restrict__ clear) {
+                                                     int32_t* __restrict__ order, int32_t* __restrict__ clear,
+                                                     int n_clear) {
   __shared__ uint64_t keys[kMaxOrderRows];
   const int b = blockIdx.x;
-  // An optional status word for the launches that follow, cleared in stream order.
-  if (clear && b == 0 && threadIdx.x == 0) *clear = 0;
+  // Optional status words for the launches that follow, cleared in stream order.
+  if (clear && b == 0 && static_cast<int>(threadIdx.x) < n_clear) clear[threadIdx.x] = 0;
   int n = counts ? counts[b] : tokens;
   n = n < 0 ? 0 : (n > tokens ? tokens : n);
   const int64_t* p = pos + b * pos_sb;
@@ -441,9 +442,9 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
   if (threadIdx.x < n_use) as[picks_s[threadIdx.x]] = static_cast<int8_t>(free_s[threadIdx.x]);
 }
 
-int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream) {
+int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream, int n_clear) {
   hipLaunchKernelGGL(order_kernel, dim3(n_batch), dim3(1024), 0, stream, r.pos, r.pos_sb, r.counts, r.tokens, order,
-                     clear);
+                     clear, n_clear);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
@@ -451,7 +452,7 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
                  hipStream_t stream) {
   const int lanes = c.n_batch * c.n_groups;
   hipLaunchKernelGGL(order_kernel, dim3(c.n_batch), dim3(1024), 0, stream, r.pos, r.pos_sb, r.counts, r.tokens,
-                     ws.order, static_cast<int32_t*>(nullptr));
+                     ws.order, static_cast<int32_t*>(nullptr), 0);
   if (r.tokens > 0) {
     const int nj = (c.dk + kWave - 1) / kWave;
     auto attach = [&](auto kernel, int tile, size_t shmem) {

@@ -73,7 +73,7 @@ int64_t chunk_workspace_floats(const logkv_attention_args& a);
 int launch_combine(const logkv_attention_args& a, const float* part, int n_split, hipStream_t stream);
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream);
-int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream);
+int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream, int n_clear = 1);
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   hipStream_t stream);
 int launch_beta_merge(const logkv_beta_args& a, int32_t* status, hipStream_t stream);
@@ -83,5 +83,10 @@ int launch_chunk_backward(const logkv_attention_args& a, const int32_t* width, c
                           float* stats, hipStream_t stream);
 int launch_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   int64_t cursor, int32_t* status, hipStream_t stream);
+int launch_record_wards(const LadderArgs& c, const int32_t* jobs, const int32_t* n_jobs, const logkv_op_log_view& log,
+                        hipStream_t stream);
+int launch_unified_replay(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
+                          const int64_t* cursors, int32_t* consumed, int32_t* jobs, int32_t* n_jobs, int32_t* status,
+                          hipStream_t stream);
 
 }  // namespace logkv

@@ -220,8 +220,6 @@ class LogStructuredKVCache(nn.Module):
             unsupported.append("semantic_clusters with cluster_k_max > 1")
         if semantic_unified_route and semantic_merge_passes != 1:
             unsupported.append("semantic_merge_passes=1 with the unified route (frozen-center sweeps)")
-        if semantic_unified_route and semantic_replay_updates:
-            unsupported.append("no update tape with the unified route")
         if semantic_legacy_route or semantic_cluster_chunk_size:
             unsupported.append("attach routing (no legacy / chunk-tree route)")
         if semantic_capacity_beta or semantic_capacity_hard_cap_mult:
@@ -443,10 +441,12 @@ class LogStructuredKVCache(nn.Module):
         self._route_commit(k_raw, v, positions, counts, assign_out, order_out, record=record_op_log)
 
     def _route_commit(self, k_raw, v, positions, counts=None, assign_out=None, order_out=None, record=False):
+        """Route and commit one flush; with ``assign_out`` / ``order_out`` the
+        decisions are also written there (for the update tape), and the unified
+        route returns its old-old merges as well (``_unified_route_commit``)."""
         if self.semantic_unified_route:
-            if record:
-                raise NotImplementedError("op-log recording of the unified route is not built")
-            return self._unified_route_commit(k_raw, v, positions, counts)
+            return self._unified_route_commit(k_raw, v, positions, counts, record=record, assign_out=assign_out,
+                                              order_out=order_out)
         view = self._ladder_view()
         rows = self._rows_view(k_raw, v, positions, counts)
         ws = self._workspace_for(view, rows.tokens)
@@ -459,11 +459,7 @@ class LogStructuredKVCache(nn.Module):
             check(lib().logkv_record_ops(C.byref(view), C.byref(rows), ptr(ws), ws.numel(), C.byref(log), stream),
                   "logkv_record_ops")
 
-    def _unified_route_commit(self, k_raw, v, positions, counts=None):
-        """Unified route of one flush (litgpt/log_kv_cache.py:3589-3688): the plan
-        on the device, one read of its two-word summary (the old-old merge
-        rounds to launch and the budget stage's failure flag), then the merges
-        and the commit."""
+    def _unified_workspace(self, k_raw, v, positions, counts):
         view = self._ladder_view()
         rows = self._rows_view(k_raw, v, positions, counts)
         key = ("unified_ws", rows.tokens)
@@ -475,7 +471,17 @@ class LogStructuredKVCache(nn.Module):
             self._views[key] = need
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(need, dtype=torch.uint8, device=self.level_k.device)
-        ws = self._workspace
+        return view, rows, self._workspace
+
+    def _unified_route_commit(self, k_raw, v, positions, counts=None, record=False, assign_out=None, order_out=None):
+        """Unified route of one flush (litgpt/log_kv_cache.py:3589-3688): the plan
+        on the device, one read of its two-word summary (the old-old merge
+        rounds to launch and the budget stage's failure flag), then the merges
+        and the commit. ``record`` appends the flush's op-log rows (its
+        WARD_MERGE rows, then NEW_CLUSTER / JOIN). With ``assign_out`` /
+        ``order_out`` the decisions are copied there and the old-old merges are
+        returned as ``{"jobs", "n_jobs", "steps"}`` (an update-tape record)."""
+        view, rows, ws = self._unified_workspace(k_raw, v, positions, counts)
         summary = self._views.get("unified_summary")
         if summary is None:
             summary = self._views["unified_summary"] = torch.zeros(2, dtype=torch.int32, device=self.level_k.device)
@@ -489,10 +495,36 @@ class LogStructuredKVCache(nn.Module):
         steps, stuck = summary.tolist()
         if stuck:
             raise RuntimeError("unified route: a budget stage found no mutual pair above the cluster budget")
+        merges = None
+        if assign_out is not None:
+            lanes = self.batch_size * self.n_groups
+            jobs = torch.empty(lanes, 32, 2, dtype=torch.int32, device=k_raw.device)
+            n_jobs = torch.empty(lanes, dtype=torch.int32, device=k_raw.device)
+            check(lib().logkv_unified_decisions(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws),
+                                                ws.numel(), ptr(assign_out), ptr(order_out), ptr(jobs), ptr(n_jobs), 0,
+                                                stream), "logkv_unified_decisions")
+            merges = {"jobs": jobs, "n_jobs": n_jobs, "steps": torch.tensor([int(steps)], dtype=torch.int32)}
         check(lib().logkv_unified_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
                                          int(steps), stream), "logkv_unified_commit")
+        if record:
+            check(lib().logkv_unified_record_ops(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws),
+                                                 ws.numel(), C.byref(self._op_log_view()), stream),
+                  "logkv_unified_record_ops")
+        return merges
 
-    def _commit_only(self, k_raw, v, positions, counts, assign, order):
+    def _unified_commit_only(self, k_raw, v, positions, counts, assign, order, merges):
+        """A recorded unified flush applied from its decisions and old-old merges."""
+        view, rows, ws = self._unified_workspace(k_raw, v, positions, counts)
+        stream = stream_of(k_raw.device)
+        check(lib().logkv_unified_decisions(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                            ptr(assign), ptr(order), ptr(merges["jobs"]), ptr(merges["n_jobs"]), 1,
+                                            stream), "logkv_unified_decisions")
+        check(lib().logkv_unified_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                         int(merges["steps"][0]), stream), "logkv_unified_commit")
+
+    def _commit_only(self, k_raw, v, positions, counts, assign, order, merges=None):
+        if self.semantic_unified_route:
+            return self._unified_commit_only(k_raw, v, positions, counts, assign, order, merges)
         view = self._ladder_view()
         rows = self._rows_view(k_raw, v, positions, counts)
         ws = self._workspace_for(view, rows.tokens)
@@ -550,7 +582,7 @@ class LogStructuredKVCache(nn.Module):
                 stream.wait_event(ready)   # device-side wait only
             tensors = {name: None if i is None else updates.tensors[i] for name, i in saved.items()}
             for t in tensors.values():
-                if t is not None:
+                if t is not None and t.is_cuda:   # a unified record's merge-round count stays on the host
                     t.record_stream(stream)
             self._mid_decode_state = None
             if self.alpha_exact_tokens:
@@ -558,7 +590,7 @@ class LogStructuredKVCache(nn.Module):
                 alpha_replay(self, tensors)
             else:
                 self._commit_only(tensors["k"], tensors["v"], tensors["pos"], tensors["counts"], tensors["assign"],
-                                  tensors["order"])
+                                  tensors["order"], tensors)
             self._tape_index += 1
             return
         if replay or key in updates.flushes:
@@ -578,10 +610,12 @@ class LogStructuredKVCache(nn.Module):
             T = k_raw.size(2)
             assign = torch.empty(self.batch_size * self.n_groups, T, dtype=torch.int8, device=dev)
             order = torch.empty(self.batch_size, T, dtype=torch.int32, device=dev)
-            self._route_commit(k_raw, v, positions, counts, assign, order, record=True)
+            merges = self._route_commit(k_raw, v, positions, counts, assign, order, record=True)
             saved = {"k": updates.save(k_raw), "v": updates.save(v), "pos": updates.save(positions),
                      "counts": updates.save(counts), "assign": updates.save(assign, owned=True),
                      "order": updates.save(order, owned=True)}
+            for name, t in (merges or {}).items():
+                saved[name] = updates.save(t, owned=True)
         ready = torch.cuda.Event()
         ready.record(torch.cuda.current_stream(dev))
         updates.flushes[key] = (signature, self._tape_index, saved, ready)
@@ -640,6 +674,8 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError("replay_op_log_len is required with replay_op_log")
         if plans is not None and log_host is not plans.host_log:
             raise RuntimeError("semantic replay plan does not match the CPU op-log")
+        if self.semantic_unified_route:
+            return self._unified_replay_flush(k_raw, v, positions, positions_host, counts, log, lengths, plans)
         B, G, T = k_raw.shape[:3]
         if (log.dim() != 4 or tuple(log.shape[:2]) != (B, G) or log.size(3) != 4 or log.dtype != torch.int32
                 or tuple(lengths.shape) != (B, G) or lengths.dtype != torch.int32):
@@ -676,6 +712,55 @@ class LogStructuredKVCache(nn.Module):
         taken = [T] * B if counts is None else [max(0, min(T, int(c))) for c in counts.tolist()]
         for b in range(B):
             cursors[b][:G] = [cursors[b][g] + taken[b] for g in range(G)]
+
+    def _unified_replay_flush(self, k_raw, v, positions, positions_host, counts, log, lengths, plans):
+        """Re-apply one logged unified flush (litgpt/log_kv_cache.py:5067-5114):
+        per lane from its own cursor, the leading WARD_MERGE rows are the old-old
+        merges and one NEW_CLUSTER / JOIN row per flushed token the decisions.
+        The parse and its checks run on the device; the check bits, the merge
+        rounds and the rows each lane consumed are read back (one
+        synchronisation), and a failed check raises ``RuntimeError`` before
+        anything is written to the cache."""
+        if lengths is None:
+            raise ValueError("replay_op_log_len is required with replay_op_log")
+        B, G, T = k_raw.shape[:3]
+        if (log.dim() != 4 or tuple(log.shape[:2]) != (B, G) or log.size(3) != 4 or log.dtype != torch.int32
+                or tuple(lengths.shape) != (B, G) or lengths.dtype != torch.int32):
+            raise RuntimeError("semantic replay log does not match the current batch/groups")
+        require_device(log, "replay_op_log")
+        require_device(lengths, "replay_op_log_len")
+        log, lengths = log.contiguous(), lengths.contiguous()
+        if getattr(self, "_op_replay_cursor_host", None) is None:
+            self._op_replay_cursor_host = [[0] * G for _ in range(B)]
+        cursors = self._op_replay_cursor_host
+        if plans is not None:
+            current = tuple(tuple(int(x) for x in row) for row in positions_host[:B])
+            key = tuple(tuple(row[:G]) for row in cursors[:B])
+            seen = plans.plans.setdefault(key, current)
+            if seen != current:
+                raise RuntimeError("semantic replay plan does not match the current flush positions")
+        if T == 0:
+            return
+        view, rows, ws = self._unified_workspace(k_raw, v, positions, counts)
+        dev = k_raw.device
+        lanes = B * G
+        out = self._views.get(("unified_replay", lanes))
+        if out is None:
+            out = self._views[("unified_replay", lanes)] = torch.zeros(2 + lanes, dtype=torch.int32, device=dev)
+        cur = torch.tensor([c for row in cursors[:B] for c in row[:G]], dtype=torch.int64).to(dev)
+        stream = stream_of(dev)
+        check(lib().logkv_unified_replay_plan(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                              C.byref(self._op_log_view(log, lengths)), ptr(cur), ptr(out[2:]),
+                                              ptr(out), stream), "logkv_unified_replay_plan")
+        host = out.tolist()
+        bits, steps = host[0], host[1]
+        if bits:
+            why = "; ".join(msg for bit, msg in _lib.REPLAY_ERRORS.items() if bits & bit)
+            raise RuntimeError(f"semantic LogKV replay of a unified flush failed (nothing was written): {why}")
+        check(lib().logkv_unified_commit(C.byref(view), C.byref(rows), C.byref(self._params), ptr(ws), ws.numel(),
+                                         int(steps), stream), "logkv_unified_commit")
+        for b in range(B):
+            cursors[b][:G] = [cursors[b][g] + host[2 + b * G + g] for g in range(G)]
 
     def _semantic_flush_tokens(self, flush_len: int, span_ends=None, **route) -> None:
         pending = int(flush_len)
@@ -950,8 +1035,6 @@ class LogKVStreamTrainingAttention(torch.autograd.Function):
         ctx.span_ends = None if span_ends is None else tuple(tuple(bool(x) for x in row) for row in span_ends)
         if cache.alpha_exact_tokens and (not cache.semantic_replay_updates or second_order_scale != 0.0):
             raise ValueError("AlphaLogKV training requires semantic_replay_updates and second_order_scale=0")
-        if cache.semantic_unified_route:
-            raise NotImplementedError("training replay of the unified route is not built (no op-log recording)")
         T = q.size(2)
         train_block = int(train_block)
         if train_block < 2:

@@ -220,8 +220,13 @@ class OracleCache:
                 rows = np.asarray(offsets, np.int64)
                 self.join(b, g, c, k_raw[b, g, rows], v[b, g, rows], pos[b, rows])
             for b, g, (kind, c, token, offset, _) in specials:
+                if kind == "ward":
+                    # A logged old-old merge of the unified route: cluster `token`
+                    # (the row's arg) merges into c (litgpt/log_kv_cache.py:2597-2598).
+                    unified.ward_merge(self, b, g, c, token)
+                    continue
                 if kind != "new":
-                    raise NotImplementedError("segment pads and Ward merges are not part of the attach route")
+                    raise NotImplementedError("segment pads are not part of this path")
                 self.new_cluster(b, g, c, k_raw[b, g, offset], v[b, g, offset], int(token))
 
     # ---- flush -----------------------------------------------------------

@@ -34,6 +34,7 @@ import math
 import numpy as np
 
 from . import ladder as lad
+from . import oplog
 from .numerics import dsum, f32
 
 INF = np.float32(np.inf)
@@ -324,6 +325,12 @@ def route_unified(cache, ak, av, ap, counts):
     for (b, g), (jobs, _, _, _) in plans.items():
         for keep, free in jobs:
             ward_merge(cache, b, g, keep, free)
+    # With an op-log bound, each lane's WARD_MERGE rows (keep, free, -1) come
+    # first, in merge order (litgpt/log_kv_cache.py:2597-2598, called from the
+    # merge steps at :3661-3664 before the new clusters and joins).
+    if cache.op_log is not None:
+        for (b, g), (jobs, _, _, _) in plans.items():
+            cache.op_log[b][g].extend((oplog.WARD_MERGE, int(keep), int(free), -1) for keep, free in jobs)
     jobs_all = {}
     for (b, g), (_, root, old, surv2) in plans.items():
         n = int(counts[b])
@@ -338,6 +345,7 @@ def route_unified(cache, ak, av, ap, counts):
             c = next(free_slots) if opened else int(old[surv2[r]])
             jobs_all[(b, g, c)] = (opened, sel)
             out[b, g, sel] = c
+    late = set()
     for (b, g, c), (new, rows) in sorted(jobs_all.items()):
         if new:
             t = rows[0]
@@ -347,7 +355,11 @@ def route_unified(cache, ak, av, ap, counts):
             continue
         pos = ap[b, rows].astype(np.int64)
         if cache.P and pos.min() < cache.p_hi_c[b, g, c]:
+            late.add((b, g, c))
             cache.join_late(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
         else:
             cache.join(b, g, c, ak[b, g, rows], av[b, g, rows], pos)
+    if cache.op_log is not None:
+        for (b, g), rows in oplog.flush_rows(jobs_all, ap, late).items():
+            cache.op_log[b][g].extend(rows)
     return out

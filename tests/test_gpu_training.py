@@ -83,18 +83,19 @@ def test_slot_attention_gradients():
     assert int(torch.count_nonzero(dv[:, :, :40][masked])) == 0
 
 
-def _training_cache(alpha):
+def _training_cache(alpha, unified=False):
     cos, sin = rope_tables(1024, 128)
     return LogStructuredKVCache((1, 2, 1024, 128), (1, 2, 1024, 128), B=8, recent_size=64, device="cuda",
                                 dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=6, semantic_s_h=64.0,
                                 semantic_flush_granularity=32, semantic_anchor_mode="mid",
                                 allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=128,
                                 semantic_replay_updates=alpha, alpha_exact_tokens=32 if alpha else 0,
-                                alpha_span_max_tokens=8, beta_novelty=alpha, beta_adaptive_merge=alpha)
+                                alpha_span_max_tokens=8, beta_novelty=alpha, beta_adaptive_merge=alpha,
+                                semantic_unified_route=unified)
 
 
-@pytest.mark.parametrize("alpha", [False, True])
-def test_stream_training_matches_naive_graph_and_replays_the_cache(alpha):
+@pytest.mark.parametrize("alpha,unified", [(False, False), (True, False), (False, True)])
+def test_stream_training_matches_naive_graph_and_replays_the_cache(alpha, unified):
     T, block, heads = 320, 32, 4
     mix = Mixture(1, 2, 128, clusters=6, seed=41)
     k_raw, v = mix.rows(T).cuda(), mix.rows(T).cuda()
@@ -106,7 +107,7 @@ def test_stream_training_matches_naive_graph_and_replays_the_cache(alpha):
     scale = 128 ** -0.5
 
     # Naive graph: per block, attention with a gradient, then the detached commit.
-    cache = _training_cache(alpha)
+    cache = _training_cache(alpha, unified)
     qn, kn, vn = (x.clone().requires_grad_(True) for x in (q, k, v))
     outs = []
     for s in range(0, T, block):
@@ -119,7 +120,7 @@ def test_stream_training_matches_naive_graph_and_replays_the_cache(alpha):
     naive_state = {f: getattr(cache, f).clone() for f in STATE_FIELDS}
     gn = torch.autograd.grad(naive, (qn, kn, vn), dout)
 
-    cache2 = _training_cache(alpha)
+    cache2 = _training_cache(alpha, unified)
     ql, kl, vl = (x.clone().requires_grad_(True) for x in (q, k, v))
     y = LogKVStreamTrainingAttention.apply(ql, kl, vl, cache2, scale, block, 0.0, k_raw, ends)
     assert torch.equal(y, naive)

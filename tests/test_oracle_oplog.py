@@ -105,3 +105,50 @@ def test_replay_parse_errors():
         oplog.replay_plan(log, [[0]], [[14, 15, 16]], 1, 3)
     with pytest.raises(ValueError, match="unknown semantic LogKV op 7"):
         oplog.replay_plan([[[(7, 1, 0, 14)]]], [[0]], [[14]], 1, 1)
+
+
+def test_replay_schedule_leading_ward_rows():
+    """A unified flush's WARD_MERGE rows lead its lane and replay one a round,
+    before any of the flush's opening or join rounds."""
+    log = [[[(3, 2, 0, -1), (3, 1, 3, -1), (0, 0, 0, 11), (2, 1, 0, 10)]]]
+    ends, rounds = oplog.replay_plan(log, [[0]], [[10, 11]], 1, 2)
+    assert ends == ((4,),)
+    assert rounds == [
+        ([], [(0, 0, ("ward", 2, 0, None, None))]),
+        ([], [(0, 0, ("ward", 1, 3, None, None))]),
+        ([], [(0, 0, ("new", 0, 11, 1, None))]),
+        ([(0, 0, 1, 0, False, [0])], []),
+    ]
+
+
+def test_unified_replay_reproduces_recorded_states():
+    """A unified-routed stream's log (old-old Ward merges first in each lane)
+    replays into every recorded state; lanes with Ward rows end at their own
+    cursors."""
+    from workloads import rope_tables
+
+    batch, groups, dim, K, B, T, n, s_h = 2, 2, 16, 4, 8, 24, 8, 4.0
+    cos, sin = rope_tables(T * (n + 2), dim)
+    kw = dict(B=B, recent_size=T, K=K, s_h=s_h, flush=T, exact_tokens=0, span_max=4, beta_novelty=False,
+              beta_adaptive=False, cos=cos.numpy(), sin=sin.numpy(), unified=True)
+    rec = OracleCache(batch, groups, T * (n + 2), dim, dim, **kw)
+    rec.begin_op_log()
+    mix = Mixture(batch, groups, dim, clusters=K + 2, seed=17, drift_every=48)
+    flushes, states = [], []
+    for i in range(n):
+        k, v = mix.rows(T).float().numpy(), mix.rows(T).float().numpy()
+        pos = np.broadcast_to(np.arange(i * T, (i + 1) * T), (batch, T)).copy()
+        rec.flush_rows(k, v, pos)
+        flushes.append((k, v, pos))
+        states.append({f: getattr(rec, f).copy() for f in FIELDS})
+    assert rec.ward_merges > 0
+    wards = [[sum(r[0] == oplog.WARD_MERGE for r in rec.op_log[b][g]) for g in range(groups)] for b in range(batch)]
+    lengths = [[len(rec.op_log[b][g]) for g in range(groups)] for b in range(batch)]
+    assert lengths == [[n * T + w for w in row] for row in wards]
+    assert len({c for row in lengths for c in row}) > 1
+    rep = OracleCache(batch, groups, T * (n + 2), dim, dim, **kw)
+    for i, ((k, v, pos), want) in enumerate(zip(flushes, states)):
+        rep.replay_rows(k, v, pos, rec.op_log)
+        for f in FIELDS:
+            assert np.array_equal(getattr(rep, f), want[f]), (i, f)
+    assert rep.replay_cursor == lengths
