@@ -69,6 +69,11 @@ typedef struct logkv_route_params {
                          * (semantic_centroid_backend="sequential"); 32: in position-ordered tiles of
                          * 32 rows, each tile summed by a halving tree, tiles added in order
                          * ("parallel", litgpt/log_kv_updates_triton.py:236-241, 274-275) */
+  float hard_cap;       /* <= 0: no capacity cap. Else the cap (max_seq / K * semantic_capacity_hard_cap_mult
+                         * as f32, litgpt/log_kv_cache.py:2347-2354): a frozen join needs n_total + 1 <= hard_cap,
+                         * a cluster keeps at most hard_cap_rows - n_total of its direct rows (offset order)
+                         * and orphans fill the nearest cluster with room (attach route only) */
+  int32_t hard_cap_rows; /* int(cap), the truncated cap the rooms count against */
 } logkv_route_params;
 
 const char* logkv_last_error(void);

@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstring>
+#include <cmath>
 
 #include <algorithm>
 #include <mutex>
@@ -97,7 +98,8 @@ Plan plan_for(const logkv_ladder_view* c, int32_t tokens, int32_t late, int32_t 
   p.units = off;
   off += align256(int64_t(c->levels) * (ladders + 1) * 4);
   p.ladder = off;
-  off += ladders * p.stride;
+  // A capped route's orphan distances live in the ladder scratch before the commit uses it.
+  off += std::max(ladders * p.stride, align256(lanes * tokens * c->k_max * 4));
   p.total = off;
   int w = 1;
   while (late && w < m0) w <<= 1;
@@ -113,6 +115,10 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   if (!prm) return fail(LOGKV_EINVAL, "route params are NULL");
   if (prm->center_tile != 0 && prm->center_tile != 1 && prm->center_tile != logkv::kCenterTile)
     return fail(LOGKV_EINVAL, "center_tile must be 0, 1 or %d", logkv::kCenterTile);
+  if (std::isnan(prm->hard_cap) || (prm->hard_cap > 0.f && prm->hard_cap_rows < 0))
+    return fail(LOGKV_EINVAL, "hard_cap must not be NaN and hard_cap_rows must be >= 0");
+  if (ward && prm->hard_cap > 0.f)
+    return fail(LOGKV_EINVAL, "the unified route takes no capacity cap");
   const int late = prm->late_joins ? 1 : 0;
   if (late && int64_t(c->levels) * c->slots + r->tokens > logkv::kMaxOrderRows)
     return fail(LOGKV_EINVAL, "delayed archive sort needs L*B' + T <= %d", logkv::kMaxOrderRows);
@@ -129,6 +135,7 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
   ws.dist = reinterpret_cast<float*>(base + p.dist);
   ws.snap_alive = base + p.snap;
   ws.ladder = base + p.ladder;
+  ws.cap_dist = reinterpret_cast<float*>(base + p.ladder);
   ws.ladder_stride = p.stride;
   ws.s0_rows = p.s0;
   ws.m0_cap = p.m0;

@@ -187,11 +187,15 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
   }
   // The lane's cluster state for the decisions (alive bits, p_hi per cluster).
   __shared__ int64_t phi_s[kMaxClusters];
+  __shared__ int32_t ntot_s[kMaxClusters];
   __shared__ uint32_t alive_s;
   if (tid < kWave) {
     const bool live = tid < K && c.alive[lane_ix * K + tid];
     const uint64_t bits = __ballot(live);
-    if (tid < K) phi_s[tid] = c.p_hi_c[static_cast<int64_t>(lane_ix) * K + tid];
+    if (tid < K) {
+      phi_s[tid] = c.p_hi_c[static_cast<int64_t>(lane_ix) * K + tid];
+      ntot_s[tid] = c.n_total[static_cast<int64_t>(lane_ix) * K + tid];
+    }
     if (tid == 0) alive_s = static_cast<uint32_t>(bits);
   }
   __syncthreads();
@@ -252,13 +256,18 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
         }
       }
     }
-    const bool direct = any_alive && (s_winner <= radius);
+    // With a capacity cap a frozen join also needs room for one more row in
+    // the winner (litgpt/log_kv_cache.py:2677-2680); the per-cluster room and
+    // the orphans are settled by the capped seed launch.
+    const bool capped = prm.hard_cap > 0.f;
+    bool direct = any_alive && (s_winner <= radius);
+    if (capped) direct = direct && static_cast<float>(ntot_s[winner] + 1) <= prm.hard_cap;
     int out;
-    if (!any_free) out = direct ? winner : nearest;
+    if (!any_free && !capped) out = direct ? winner : nearest;
     else out = direct ? winner : -1;
     const int s = tile0 + tid;
     assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = static_cast<int8_t>(out);
-    if (any_free) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
+    if (any_free || capped) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
   }
   // Padding rows of the lane keep -1.
   for (int s = tile0 + tid; s < tile0 + R && s < r.tokens; s += nthr)
@@ -307,40 +316,101 @@ __device__ __forceinline__ void block_argmax(float& v, int& i, float* sv, int* s
   __syncthreads();
 }
 
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, kWave);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------------------
-// Seeds for lanes with free cluster slots (one block per lane).
+// Seeds for lanes with free cluster slots (one block per lane), then the
+// orphans' clusters.
+//
+// CAPPED (a capacity cap, litgpt/log_kv_cache.py:4497-4516, :4734-4822): the
+// lane's decisions are kept in LDS. First every cluster keeps its first
+// max(0, cap - n_total) direct rows in offset order and the rest become
+// orphans; after the seeds, each remaining orphan in position order takes the
+// nearest candidate cluster that still has room (room = cap - n_total - the
+// rows it already took: its kept direct rows, or 1 for a seeded slot), or the
+// nearest candidate when none has room. The distances go to `cap_dist` in
+// orphan order, then one wave walks them in chunks staged through LDS.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, const int32_t* __restrict__ order,
-                                                    int8_t* __restrict__ assign, const float* __restrict__ s_win,
-                                                    float* __restrict__ dist) {
+template <bool CAPPED>
+__global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+                                                    const int32_t* __restrict__ order, int8_t* __restrict__ assign,
+                                                    const float* __restrict__ s_win, float* __restrict__ dist,
+                                                    float* __restrict__ cap_dist) {
   __shared__ float cand_s[kMaxClusters * kMaxDim];
   __shared__ float red_v[16];
   __shared__ int red_i[16];
   __shared__ int picks_s[kMaxClusters];
   __shared__ int free_s[kMaxClusters];
+  __shared__ int kept_s[kMaxClusters];
   __shared__ int n_orphan_s;
+  __shared__ int8_t as_l[CAPPED ? kMaxOrderRows : 1];
+  __shared__ int16_t idx_l[CAPPED ? kMaxOrderRows : 1];
   const int lane_ix = blockIdx.x;
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   const int K = c.k_max, D = c.dk, J = (D + kWave - 1) / kWave;
   const int n = valid_rows(r, b);
+  const int tid = static_cast<int>(threadIdx.x), nthr = static_cast<int>(blockDim.x);
+  const int l = lane_id(), w = wave_id(), nw = nthr / kWave;
   int n_free = 0;
   for (int cc = 0; cc < K; ++cc)
     if (!c.alive[lane_ix * K + cc]) {
-      if (threadIdx.x == 0) free_s[n_free] = cc;
+      if (tid == 0) free_s[n_free] = cc;
       ++n_free;
     }
-  if (n_free == 0 || n == 0) return;
-  int8_t* as = assign + static_cast<int64_t>(lane_ix) * r.tokens;
+  if ((!CAPPED && n_free == 0) || n == 0) return;
+  int8_t* as_g = assign + static_cast<int64_t>(lane_ix) * r.tokens;
+  int8_t* as = CAPPED ? as_l : as_g;
   const float* sw = s_win + static_cast<int64_t>(lane_ix) * r.tokens;
   float* ds = dist + static_cast<int64_t>(lane_ix) * r.tokens;
   const int32_t* ord = order + static_cast<int64_t>(b) * r.tokens;
   const uint16_t* kbase = r.k + b * r.k_sb + g * r.k_sg;
-  if (threadIdx.x == 0) n_orphan_s = 0;
+  const int32_t* ntot = c.n_total + static_cast<int64_t>(lane_ix) * K;
+  if constexpr (CAPPED) {
+    // idx_l: position-order index of each offset (the lane's rows 0..n-1 are
+    // a permutation of the first n offsets).
+    for (int s = tid; s < n; s += nthr) {
+      as_l[s] = as_g[s];
+      idx_l[s] = -1;
+    }
+    __syncthreads();
+    for (int s = tid; s < n; s += nthr) {
+      const int o = ord[s];
+      if (o >= 0 && o < n) idx_l[o] = static_cast<int16_t>(s);
+    }
+    __syncthreads();
+    if (w == 0) {
+      const int room = l < K ? max(0, prm.hard_cap_rows - ntot[l]) : 0;
+      const uint64_t below = (1ull << l) - 1ull;
+      int run = 0;   // lane cc: direct rows of cluster cc met so far, in offset order
+      for (int t0 = 0; t0 < n; t0 += kWave) {
+        const int t = t0 + l;
+        const int s = t < n ? idx_l[t] : -1;
+        const int a = s >= 0 && s < n ? as_l[s] : -1;
+        bool demote = false;
+        for (int cc = 0; cc < K; ++cc) {
+          const uint64_t m = __ballot(a == cc);
+          if (m == 0) continue;
+          const int base = __shfl(run, cc, kWave), room_cc = __shfl(room, cc, kWave);
+          if (a == cc) demote = base + __popcll(m & below) >= room_cc;
+          if (l == cc) run += __popcll(m);
+        }
+        if (demote) as_l[s] = -1;
+      }
+      if (l < K) kept_s[l] = min(run, room);
+    }
+  }
+  if (tid == 0) n_orphan_s = 0;
   __syncthreads();
   int mine = 0;
   float v = -__builtin_inff();
   int vi = 0x7fffffff;
-  for (int s = threadIdx.x; s < n; s += blockDim.x) {
+  for (int s = tid; s < n; s += nthr) {
     if (as[s] < 0) {
       ++mine;
       const float val = sw[s];
@@ -353,15 +423,21 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
   atomicAdd(&n_orphan_s, mine);
   __syncthreads();
   const int n_orphan = n_orphan_s;
-  if (n_orphan == 0) return;
+  if (n_orphan == 0) {
+    if constexpr (CAPPED)
+      for (int s = tid; s < n; s += nthr) as_g[s] = as_l[s];
+    return;
+  }
   int n_use = n_free < n_orphan ? n_free : n_orphan;
   block_argmax(v, vi, red_v, red_i);
   int pick = vi;
   // Every pick is an unpicked orphan with a finite score while n_use <= orphans;
   // a non-finite score (NaN keys) could leave no valid index: seed fewer then.
-  if (pick < 0 || pick >= n) return;
-  if (threadIdx.x == 0) picks_s[0] = pick;
-  const int l = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
+  if (n_use > 0 && (pick < 0 || pick >= n)) {
+    if constexpr (!CAPPED) return;
+    n_use = 0;
+  }
+  if (n_use > 0 && tid == 0) picks_s[0] = pick;
   for (int step = 0; step + 1 < n_use; ++step) {
     // dist = min(dist, d2(., pick)), with the pick itself masked; argmax -> next pick.
     const uint16_t* prow = kbase + static_cast<int64_t>(ord[pick]) * r.k_st;
@@ -392,15 +468,15 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
       break;
     }
     pick = bi;
-    if (threadIdx.x == 0) picks_s[step + 1] = pick;
+    if (tid == 0) picks_s[step + 1] = pick;
     __syncthreads();
   }
   __syncthreads();
   // Candidate centers: live centroids, seed rows at the free slots.
   const float* mu = c.centroid + static_cast<int64_t>(lane_ix) * K * D;
-  for (int i = threadIdx.x; i < K * D; i += blockDim.x) cand_s[i] = mu[i];
+  for (int i = tid; i < K * D; i += nthr) cand_s[i] = mu[i];
   __syncthreads();
-  for (int i = threadIdx.x; i < n_use * D; i += blockDim.x) {
+  for (int i = tid; i < n_use * D; i += nthr) {
     const int k = i / D, d = i % D;
     const uint16_t* row = kbase + static_cast<int64_t>(ord[picks_s[k]]) * r.k_st;
     cand_s[free_s[k] * D + d] = bf16_to_f32(row[d]);
@@ -409,37 +485,109 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, co
   uint32_t cand_bits = 0;
   for (int cc = 0; cc < K; ++cc) cand_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
   for (int k = 0; k < n_use; ++k) cand_bits |= 1u << free_s[k];
-  for (int s = w; s < n; s += nw) {
-    if (as[s] >= 0) continue;
-    float x[kMaxDim / kWave];
-    const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
-#pragma unroll
-    for (int j = 0; j < kMaxDim / kWave; ++j) {
-      const int d = l + j * kWave;
-      x[j] = feat_or_zero(gp(row), d, D);
-    }
-    float best = __builtin_inff();
-    int arg = 0;
-    for (int cc = 0; cc < K; ++cc) {
-      float e = 0.f;
+  if constexpr (!CAPPED) {
+    for (int s = w; s < n; s += nw) {
+      if (as[s] >= 0) continue;
+      float x[kMaxDim / kWave];
+      const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
 #pragma unroll
       for (int j = 0; j < kMaxDim / kWave; ++j) {
-        if (j < J) {
-          const int d = l + j * kWave;
-          const float diff = d < D ? x[j] - cand_s[cc * D + d] : 0.f;
-          e = j == 0 ? diff * diff : e + diff * diff;
+        const int d = l + j * kWave;
+        x[j] = feat_or_zero(gp(row), d, D);
+      }
+      float best = __builtin_inff();
+      int arg = 0;
+      for (int cc = 0; cc < K; ++cc) {
+        float e = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxDim / kWave; ++j) {
+          if (j < J) {
+            const int d = l + j * kWave;
+            const float diff = d < D ? x[j] - cand_s[cc * D + d] : 0.f;
+            e = j == 0 ? diff * diff : e + diff * diff;
+          }
+        }
+        e = wave_sum0(e);
+        if (((cand_bits >> cc) & 1u) && e < best) {
+          best = e;
+          arg = cc;
         }
       }
-      e = wave_sum0(e);
-      if (((cand_bits >> cc) & 1u) && e < best) {
-        best = e;
-        arg = cc;
+      if (l == 0) as[s] = static_cast<int8_t>(arg);
+    }
+    __syncthreads();
+    if (tid < n_use) as[picks_s[tid]] = static_cast<int8_t>(free_s[tid]);
+  } else {
+    // Seeds open their slots; the remaining orphans in position order -> idx_l.
+    if (tid < n_use) as_l[picks_s[tid]] = static_cast<int8_t>(free_s[tid]);
+    __syncthreads();
+    __shared__ int n_rest_s;
+    if (w == 0) {
+      int count = 0;
+      for (int s0 = 0; s0 < n; s0 += kWave) {
+        const bool orphan = s0 + l < n && as_l[s0 + l] < 0;
+        const uint64_t m = __ballot(orphan);
+        if (orphan) idx_l[count + __popcll(m & ((1ull << l) - 1ull))] = static_cast<int16_t>(s0 + l);
+        count += __popcll(m);
+      }
+      if (l == 0) n_rest_s = count;
+    }
+    __syncthreads();
+    const int n_rest = n_rest_s;
+    float* cd = cap_dist + static_cast<int64_t>(lane_ix) * r.tokens * K;
+    for (int i = w; i < n_rest; i += nw) {
+      const int s = idx_l[i];
+      float x[kMaxDim / kWave];
+      const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
+#pragma unroll
+      for (int j = 0; j < kMaxDim / kWave; ++j) {
+        const int d = l + j * kWave;
+        x[j] = feat_or_zero(gp(row), d, D);
+      }
+      for (int cc = 0; cc < K; ++cc) {
+        float e = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxDim / kWave; ++j) {
+          if (j < J) {
+            const int d = l + j * kWave;
+            const float diff = d < D ? x[j] - cand_s[cc * D + d] : 0.f;
+            e = j == 0 ? diff * diff : e + diff * diff;
+          }
+        }
+        e = wave_sum0(e);
+        if (l == 0) cd[static_cast<int64_t>(i) * K + cc] = ((cand_bits >> cc) & 1u) ? e : __builtin_inff();
       }
     }
-    if (l == 0) as[s] = static_cast<int8_t>(arg);
+    __threadfence();
+    __syncthreads();
+    // Rooms, in lane cc of the walking wave.
+    int room = 0;
+    if (l < K && ((cand_bits >> l) & 1u)) {
+      bool seeded = false;
+      for (int k = 0; k < n_use; ++k) seeded |= free_s[k] == l;
+      room = max(0, prm.hard_cap_rows - ntot[l] - (seeded ? 1 : kept_s[l]));
+    }
+    const int chunk = (kMaxClusters * kMaxDim) / K;
+    for (int i0 = 0; i0 < n_rest; i0 += chunk) {
+      const int rows = min(chunk, n_rest - i0);
+      for (int e = tid; e < rows * K; e += nthr) cand_s[e] = cd[static_cast<int64_t>(i0) * K + e];
+      __syncthreads();
+      if (w == 0) {
+        for (int i = 0; i < rows; ++i) {
+          const float e = l < K ? cand_s[i * K + l] : __builtin_inff();
+          const uint64_t key = (static_cast<uint64_t>(__float_as_uint(e)) << 32) | static_cast<uint32_t>(l);
+          uint64_t best = wave_min_u64(l < K && room > 0 ? key : ~0ull);
+          // Every cluster full: the nearest one (litgpt/log_kv_cache.py:4816-4819).
+          if (best == ~0ull) best = wave_min_u64(l < K ? key : ~0ull);
+          const int chosen = static_cast<int>(best & 0xffffffffu);
+          if (l == chosen) --room;
+          if (l == 0) as_l[idx_l[i0 + i]] = static_cast<int8_t>(chosen);
+        }
+      }
+      __syncthreads();
+    }
+    for (int s = tid; s < n; s += nthr) as_g[s] = as_l[s];
   }
-  __syncthreads();
-  if (threadIdx.x < n_use) as[picks_s[threadIdx.x]] = static_cast<int8_t>(free_s[threadIdx.x]);
 }
 
 int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear, hipStream_t stream, int n_clear) {
@@ -469,8 +617,12 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
     else if (nj == 3) ok = attach(attach_kernel<3>, attach_tile<3>(), attach_shmem<3>(c.k_max));
     else ok = attach(attach_kernel<4>, attach_tile<4>(), attach_shmem<4>(c.k_max));
     if (!ok) return LOGKV_ERUNTIME;
-    hipLaunchKernelGGL(seed_kernel, dim3(lanes), dim3(1024), 0, stream, c, r, ws.order, ws.assign, ws.s_win,
-                       ws.dist);
+    if (p.hard_cap > 0.f)
+      hipLaunchKernelGGL(seed_kernel<true>, dim3(lanes), dim3(1024), 0, stream, c, r, p, ws.order, ws.assign,
+                         ws.s_win, ws.dist, ws.cap_dist);
+    else
+      hipLaunchKernelGGL(seed_kernel<false>, dim3(lanes), dim3(1024), 0, stream, c, r, p, ws.order, ws.assign,
+                         ws.s_win, ws.dist, static_cast<float*>(nullptr));
   }
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }

@@ -45,6 +45,8 @@ struct Workspace {
   int8_t* assign;      // [lanes, T]
   float* s_win;        // [lanes, T]
   float* dist;         // [lanes, T]
+  float* cap_dist;     // [lanes, T, K] orphan-to-candidate distances of a capped route (shares the
+                       // ladder scratch, which only the commit launches after the route use)
   uint8_t* snap_alive; // [lanes, K] alive flags before the commit (written by its ladder blocks)
   uint8_t* ladder;     // per-ladder carry / staging rows
   int64_t ladder_stride;  // bytes per ladder

@@ -212,6 +212,9 @@ class LogStructuredKVCache(nn.Module):
             raise ValueError(f"cluster_lambda_rel must be finite and > 0, got {cluster_lambda_rel}")
         if not (math.isfinite(seg_g0) and seg_g0 > 0.0):
             raise ValueError(f"seg_g0 must be finite and > 0, got {seg_g0}")
+        cap_mult = float(semantic_capacity_hard_cap_mult)
+        if not (math.isfinite(cap_mult) and cap_mult >= 0.0):
+            raise ValueError(f"semantic_capacity_hard_cap_mult must be finite >= 0, got {semantic_capacity_hard_cap_mult}")
         if cos_cache is None or sin_cache is None or rope_n_elem is None:
             raise ValueError("semantic LogKV requires cos_cache, sin_cache, and rope_n_elem")
         # The path this library implements; everything else is a different algorithm.
@@ -222,8 +225,10 @@ class LogStructuredKVCache(nn.Module):
             unsupported.append("semantic_merge_passes=1 with the unified route (frozen-center sweeps)")
         if semantic_legacy_route or semantic_cluster_chunk_size:
             unsupported.append("attach routing (no legacy / chunk-tree route)")
-        if semantic_capacity_beta or semantic_capacity_hard_cap_mult:
-            unsupported.append("no capacity penalty or hard cap")
+        if semantic_capacity_beta:
+            unsupported.append("no capacity penalty")
+        if semantic_unified_route and semantic_capacity_hard_cap_mult:
+            unsupported.append("no hard cap with the unified route (its capped full-recompute reducer)")
         if (seg_gap_max is not None and math.isfinite(seg_gap_max)) or seg_block_level:
             unsupported.append("no segment gaps or padding")
         if semantic_anchor_mode != "mid":
@@ -254,6 +259,8 @@ class LogStructuredKVCache(nn.Module):
         self.semantic_replay_updates = bool(semantic_replay_updates)
         self.semantic_unified_route = bool(semantic_unified_route)
         self.semantic_merge_passes = int(semantic_merge_passes)
+        self.semantic_capacity_beta = 0.0
+        self.semantic_capacity_hard_cap_mult = cap_mult
         self.semantic_legacy_route = False
         self.rope_n_elem = int(rope_n_elem)
         self.register_buffer("cos_cache", cos_cache.to(device=device), persistent=False)
@@ -349,9 +356,14 @@ class LogStructuredKVCache(nn.Module):
         # reused (raw pointers: cleared whenever buffers move).
         self._views = {}
         self._alpha_parity = 0   # flips with every swap of the exact pool's two buffer sets
+        # The capacity cap (litgpt/log_kv_cache.py:2347-2354): the direct test
+        # compares float32 counts with it, the rooms count against int(cap).
+        cap = self._semantic_hard_cap()
         self._params = RouteParams(self.seg_eta, self.seg_g0, self.cluster_lambda_rel,
                                    1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0,
-                                   _CENTER_TILES[self._centroid_backend])
+                                   _CENTER_TILES[self._centroid_backend],
+                                   cap if cap != math.inf else 0.0,   # stored as float32
+                                   min(int(cap), 2**31 - 1) if cap != math.inf else 0)
         self.op_log: torch.Tensor | None = None
         self.op_log_len: torch.Tensor | None = None
         self._op_replay_cursor_host = None
@@ -362,6 +374,16 @@ class LogStructuredKVCache(nn.Module):
         self._replaying_updates = False
         self._update_actions = None
         self._tape_index = 0
+
+    def _semantic_capacity_target(self) -> float:
+        """Rows per cluster if the sequence filled every cluster evenly (litgpt/log_kv_cache.py:2347-2348)."""
+        return max(float(self.max_seq_length) / max(self.K_max, 1), 1.0)
+
+    def _semantic_hard_cap(self) -> float:
+        """The attach route's capacity cap, ``inf`` without one (litgpt/log_kv_cache.py:2350-2354)."""
+        if self.semantic_capacity_hard_cap_mult <= 0.0:
+            return math.inf
+        return self._semantic_capacity_target() * self.semantic_capacity_hard_cap_mult
 
     # ------------------------------------------------------------------
     # C-ABI views

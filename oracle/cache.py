@@ -58,7 +58,8 @@ def budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens, element=2):
 class OracleCache:
     def __init__(self, batch, groups, max_seq, dk, dv, *, B=128, recent_size=2048, K=12, lam=1.0, eta=1.0,
                  g0=2048.0, s_h=1.0, flush=2048, exact_tokens=0, span_max=64, beta_novelty=False,
-                 beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False, centroid_tile=1):
+                 beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False, centroid_tile=1,
+                 hard_cap_mult=0.0):
         self.batch, self.groups, self.max_seq, self.dk, self.dv = batch, groups, max_seq, dk, dv
         self.K, self.lam, self.eta, self.g0 = K, lam, eta, g0
         self.B, self.L, *_ = budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens)
@@ -68,6 +69,9 @@ class OracleCache:
         self.beta_novelty, self.beta_adaptive = beta_novelty, beta_adaptive
         self.cos, self.sin, self.table_bf16 = cos, sin, table_bf16
         self.centroid_tile = centroid_tile       # 1: sequential centroid backend, 32: parallel
+        # Capacity cap of the attach route (litgpt/log_kv_cache.py:2347-2354): max_seq / K rows
+        # (at least 1) times the multiplier; none for a multiplier <= 0.
+        self.hard_cap = max(float(max_seq) / max(K, 1), 1.0) * hard_cap_mult if hard_cap_mult > 0 else np.inf
         shp = (batch, groups, K, self.L, self.B)
         self.level_k = np.zeros(shp + (dk,), np.float32)
         self.level_v = np.zeros(shp + (dv,), np.float32)
@@ -178,7 +182,7 @@ class OracleCache:
         if self.unified:
             return unified.route_unified(self, ak, av, ap, counts)
         assign, order = route.attach_assign(ak, ap, counts, self.centroid, self.alive, self.p_hi_c, self.s_h,
-                                            self.eta, self.g0, self.lam)
+                                            self.eta, self.g0, self.lam, self.n_total, self.hard_cap)
         jobs = route.commit_jobs(assign, order, counts, self.alive)
         late = set()
         for (b, g, c), (new, rows) in sorted(jobs.items()):

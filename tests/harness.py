@@ -19,7 +19,8 @@ def to_np(t: torch.Tensor) -> np.ndarray:
 
 
 def make_pair(batch=1, groups=2, dim=128, K=12, B=128, recent=64, flush=64, max_seq=4096, s_h=64.0, exact=0,
-              span=16, beta_novelty=False, beta_adaptive=False, centroid_backend="sequential"):
+              span=16, beta_novelty=False, beta_adaptive=False, centroid_backend="sequential", hard_cap_mult=0.0,
+              lam=1.0):
     from logkv_amd import LogStructuredKVCache
     from oracle import OracleCache
 
@@ -29,10 +30,12 @@ def make_pair(batch=1, groups=2, dim=128, K=12, B=128, recent=64, flush=64, max_
         dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=s_h,
         semantic_flush_granularity=flush, semantic_anchor_mode="mid", allocate_second_order=False,
         cos_cache=cos, sin_cache=sin, rope_n_elem=dim, alpha_exact_tokens=exact, alpha_span_max_tokens=span,
-        beta_novelty=beta_novelty, beta_adaptive_merge=beta_adaptive, semantic_centroid_backend=centroid_backend)
+        beta_novelty=beta_novelty, beta_adaptive_merge=beta_adaptive, semantic_centroid_backend=centroid_backend,
+        semantic_capacity_hard_cap_mult=hard_cap_mult, cluster_lambda_rel=lam)
     ora = OracleCache(batch, groups, max_seq, dim, dim, B=B, recent_size=recent, K=K, s_h=s_h, flush=flush,
                       exact_tokens=exact, span_max=span, beta_novelty=beta_novelty, beta_adaptive=beta_adaptive,
-                      cos=cos.numpy(), sin=sin.numpy(), centroid_tile=32 if centroid_backend == "parallel" else 1)
+                      cos=cos.numpy(), sin=sin.numpy(), centroid_tile=32 if centroid_backend == "parallel" else 1,
+                      hard_cap_mult=hard_cap_mult, lam=lam)
     return gpu, ora
 
 
