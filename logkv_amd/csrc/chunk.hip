@@ -11,8 +11,12 @@
 //   S^T = K Q^T   (keys x queries; each lane holds 16 keys of its own query),
 //   online softmax per lane (its query's max and sum, the other 16 keys of the
 //   32-key block in lane ^ 32),
-//   O^T += V^T P^T (dv x queries), P split into bf16 high and low parts so the
-//   product keeps ~16 significant bits of P (two MFMAs per step).
+//   O^T += V^T P^T (dv x queries) with v_mfma_f32_32x32x16_f16: P in fp16
+//   (11 significant bits, RNE) against an fp16 copy of V made per launch, each
+//   lane's V scaled by 2^-k so its largest magnitude stays below 2^15 and P by
+//   2^k (k = 0 unless |V| >= 2^15; P 2^k <= 2^15; magnitudes of 2^30 and more
+//   overflow). fp16 P rounds P to 2^-11 relative, so an output errs by at most
+//   2^-11 of its values' weighted mean magnitude.
 // Queries live in registers for the whole key range; the K / V tiles are
 // double-buffered in LDS with one barrier per tile.
 // The P^T operand is the lane's own score registers: MFMA B operand element j
@@ -32,6 +36,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWavesPerBlock = 8;                 // waves per block, each owning 32 query rows
 constexpr int kThreads = 64 * kWavesPerBlock;
@@ -42,6 +48,7 @@ constexpr int kMaxSteps = 9;     // 16-wide steps of the packed width (<= 144)
 constexpr int kLdK = 152;        // K tile row stride in LDS (bf16)
 constexpr int kLdV = kKeys + 4;  // V^T row stride in LDS (bf16; 34 dwords: 16 rows' 8-byte reads hit distinct banks)
 constexpr int kMaxDvBlocks = 4;  // dv <= 128
+constexpr int kVSlices = 64;     // row slices of a lane's V in the fp16 copy
 
 __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(x); }
 
@@ -68,7 +75,9 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // shape needs gives the same result.
 template <int NKS, int NDV>
 __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
-                                                       int splits, float* __restrict__ part) {
+                                                       int splits, float* __restrict__ part,
+                                                       const uint16_t* __restrict__ v16,
+                                                       const int32_t* __restrict__ vshift) {
   // Two K / V^T tile buffers: tile i + 1 is written into the other buffer while
   // tile i is read, so one barrier per tile orders both.
   __shared__ __align__(16) uint16_t k_s[2][kKeys * kLdK];
@@ -127,7 +136,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     for (int i = 0; i < 16; ++i) o[blk][i] = 0.f;
   float m = -__builtin_inff(), lsum = 0.f;   // running maximum of s * scale * log2(e), and the sum
   const LOGKV_G uint16_t* kbase = gp(a.k) + static_cast<int64_t>(lane_ix) * a.cap * dim;
-  const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * dim;
+  const LOGKV_G uint16_t* vbase = gp(v16) + static_cast<int64_t>(lane_ix) * a.cap * a.dv;   // fp16 rows of dv
+  const int kv = vshift[lane_ix];
+  const float kvf = static_cast<float>(kv), inv_kv = __builtin_ldexpf(1.f, -kv);
   const int units = dim / 8;
   const int vunits = a.dv / 8;
   // Each thread's staging tasks are the same in every tile: up to kKTasks
@@ -164,8 +175,8 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     for (int q = 0; q < kVTasks; ++q) {
       const int kp = v_pair[q] < 0 ? 0 : v_pair[q];
       const int r0 = min(2 * kp, rows - 1), r1 = min(2 * kp + 1, rows - 1);
-      vx[q][0] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r0) * dim + 8 * v_unit[q]);
-      vx[q][1] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r1) * dim + 8 * v_unit[q]);
+      vx[q][0] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r0) * a.dv + 8 * v_unit[q]);
+      vx[q][1] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r1) * a.dv + 8 * v_unit[q]);
       if (2 * kp >= rows) vx[q][0] = make_uint4(0, 0, 0, 0);
       if (2 * kp + 1 >= rows) vx[q][1] = make_uint4(0, 0, 0, 0);
     }
@@ -248,17 +259,20 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     const float m_new = fmaxf(m, mx * c2);
     const float mb = m_new == -__builtin_inff() ? 0.f : m_new;
     const float corr = __builtin_amdgcn_exp2f(m - mb);
+    // p' = 2^(s c2 - m + k) = P 2^k (the V copy carries 2^-k); the sum is
+    // taken of p' and scaled back by 2^-k (exact).
+    const float arg0 = kvf - mb;
     float sum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], c2, -mb));
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], c2, arg0));
         s[kb][i] = p;
         sum += p;
       }
     }
-    sum = pair_sum32(sum);
+    sum = pair_sum32(sum) * inv_kv;
     lsum = lsum * corr + sum;
     m = m_new;
     if (__ballot(corr != 1.f)) {
@@ -267,34 +281,29 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[blk][i] *= corr;
     }
-    // O^T += V^T P^T, four 16-key steps, P as a truncated high bf16 part plus
-    // the rounded remainder (together ~16 significant bits of P: one bf16 P
-    // misses the 2e-3 bar when values of opposite signs nearly cancel).
+    // O^T += V^T P^T, four 16-key steps, P rounded to fp16.
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      uint32_t hw[4], lw[4];
+      f16x2 pw[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float p0 = s[st / 2][8 * (st % 2) + 2 * j], p1 = s[st / 2][8 * (st % 2) + 2 * j + 1];
-        const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
-        hw[j] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
-        const float r0 = p0 - __uint_as_float(u0 & 0xffff0000u), r1 = p1 - __uint_as_float(u1 & 0xffff0000u);
-        lw[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{r0, r1}, bf16x2));   // one packed RNE
+        pw[j] = __builtin_convertvector(f32x2{p0, p1}, f16x2);   // RNE
       }
-      const bf16x8 ph = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-      const bf16x8 pl = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-      bf16x8 vf[NDV];
+      const f16x8 ph = __builtin_bit_cast(f16x8, make_uint4(__builtin_bit_cast(uint32_t, pw[0]),
+                                                            __builtin_bit_cast(uint32_t, pw[1]),
+                                                            __builtin_bit_cast(uint32_t, pw[2]),
+                                                            __builtin_bit_cast(uint32_t, pw[3])));
+      f16x8 vf[NDV];
 #pragma unroll
       for (int blk = 0; blk < NDV; ++blk) {
         const uint16_t* vr = vt + (32 * blk + col) * kLdV + 16 * st + 4 * h;
         const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
         const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
-        vf[blk] = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+        vf[blk] = __builtin_bit_cast(f16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
       }
 #pragma unroll
-      for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[blk], ph, o[blk], 0, 0, 0);
-#pragma unroll
-      for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[blk], pl, o[blk], 0, 0, 0);
+      for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[blk], ph, o[blk], 0, 0, 0);
     }
     if (it + 1 < ntiles) {
       store_tile(bf ^ 1);
@@ -344,6 +353,76 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
   }
 }
 
+// The fp16 copy of the packed V (rows [0, total) of every lane, dv features):
+// vmax_kernel takes the largest bf16 magnitude (as bits) of each of a lane's
+// kVSlices row slices; vconv_kernel reduces them to the lane's shift k (the
+// largest k in [0, 15] keeping |V| 2^-k below 2^15, 0 when |V| < 2^15 already)
+// and writes V 2^-k as fp16 (exact for normal values; bf16 has 8 significant
+// bits, fp16 11).
+__device__ __forceinline__ int chunk_rows(const logkv_attention_args& a, const int32_t* width_ptr) {
+  return min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
+}
+
+__global__ __launch_bounds__(256) void vmax_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+                                                   int32_t* __restrict__ vmax) {
+  const int slice = blockIdx.x, lane_ix = blockIdx.y;
+  const int total = chunk_rows(a, width_ptr);
+  const int per = (total + kVSlices - 1) / kVSlices, r0 = slice * per, r1 = min(total, r0 + per);
+  const int units = a.dv / 8;
+  const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * a.dim;
+  uint32_t mx = 0;
+  for (int i = threadIdx.x; i < (r1 - r0) * units; i += blockDim.x) {
+    const int row = r0 + i / units, u = i % units;
+    const uint4 x = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * a.dim + 8 * u);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = max(mx, max(w[j] & 0x7fffu, (w[j] >> 16) & 0x7fffu));
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
+  __shared__ uint32_t red[4];
+  if (lane_id() == 0) red[wave_id()] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    vmax[lane_ix * kVSlices + slice] = static_cast<int32_t>(max(max(red[0], red[1]), max(red[2], red[3])));
+}
+
+__global__ __launch_bounds__(256) void vconv_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+                                                    const int32_t* __restrict__ vmax, int32_t* __restrict__ vshift,
+                                                    uint16_t* __restrict__ v16) {
+  const int slice = blockIdx.x, lane_ix = blockIdx.y;
+  __shared__ int shift_s;
+  if (threadIdx.x < kWave) {
+    const int2 pair = *reinterpret_cast<const int2*>(vmax + lane_ix * kVSlices + 2 * threadIdx.x % kVSlices);
+    uint32_t mx = static_cast<uint32_t>(max(pair.x, pair.y));
+    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
+    if (threadIdx.x == 0) {
+      // |V| < 2^(e + 1) with e the exponent of the largest magnitude.
+      const int e = static_cast<int>(mx >> 7) - 127;
+      shift_s = max(0, min(15, e - 14));
+      if (slice == 0) vshift[lane_ix] = shift_s;
+    }
+  }
+  __syncthreads();
+  const float scale = __builtin_ldexpf(1.f, -shift_s);
+  const int total = chunk_rows(a, width_ptr);
+  const int per = (total + kVSlices - 1) / kVSlices, r0 = slice * per, r1 = min(total, r0 + per);
+  const int units = a.dv / 8;
+  const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * a.dim;
+  uint16_t* obase = v16 + static_cast<int64_t>(lane_ix) * a.cap * a.dv;
+  for (int i = threadIdx.x; i < (r1 - r0) * units; i += blockDim.x) {
+    const int row = r0 + i / units, u = i % units;
+    const uint4 x = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * a.dim + 8 * u);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x2 f = {__uint_as_float(w[j] << 16) * scale, __uint_as_float(w[j] & 0xffff0000u) * scale};
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+    }
+    *reinterpret_cast<uint4*>(obase + static_cast<int64_t>(row) * a.dv + 8 * u) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // Partials of the key-range splits combined in split order: two queries per
 // block, one output feature per thread. A partial's maximum m is of s * scale *
 // log2(e), so a split's weight is 2^(m_split - m).
@@ -382,27 +461,58 @@ int chunk_splits(const logkv_attention_args& a) {
   return std::max(1, std::min(splits, 16));
 }
 
-int64_t chunk_workspace_floats(const logkv_attention_args& a) {
+// Workspace: [partials of the key-range splits (splits > 1)] [vmax: lanes x
+// kVSlices] [vshift: lanes] [fp16 V: lanes x cap x dv], regions 256-byte aligned.
+struct ChunkWs {
+  float* part;
+  int32_t* vmax;
+  int32_t* vshift;
+  uint16_t* v16;
+  int64_t bytes;
+};
+
+static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+static ChunkWs chunk_ws(const logkv_attention_args& a, void* base) {
   const int splits = chunk_splits(a);
-  if (splits == 1) return 0;
   const int nq = (a.n_heads / a.n_groups) * a.tq;
-  return static_cast<int64_t>(a.n_batch) * a.n_groups * splits * nq * (a.dv + 2);
+  const int64_t lanes = static_cast<int64_t>(a.n_batch) * a.n_groups;
+  uint8_t* b = static_cast<uint8_t*>(base);
+  int64_t off = 0;
+  ChunkWs w{};
+  w.part = splits > 1 && b ? reinterpret_cast<float*>(b + off) : nullptr;
+  if (splits > 1) off += align256(lanes * splits * nq * (a.dv + 2) * 4);
+  w.vmax = b ? reinterpret_cast<int32_t*>(b + off) : nullptr;
+  off += align256(lanes * kVSlices * 4);
+  w.vshift = b ? reinterpret_cast<int32_t*>(b + off) : nullptr;
+  off += align256(lanes * 4);
+  w.v16 = b ? reinterpret_cast<uint16_t*>(b + off) : nullptr;
+  off += align256(lanes * a.cap * a.dv * 2);
+  w.bytes = off;
+  return w;
 }
 
-int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, float* part, hipStream_t stream) {
+int64_t chunk_workspace_floats(const logkv_attention_args& a) { return chunk_ws(a, nullptr).bytes / 4; }
+
+int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, float* ws, hipStream_t stream) {
   const int nq = (a.n_heads / a.n_groups) * a.tq;
   const int splits = chunk_splits(a);
+  const ChunkWs w = chunk_ws(a, ws);
   const dim3 grid((nq + kQRows - 1) / kQRows, splits, a.n_batch * a.n_groups);
+  const dim3 vgrid(kVSlices, a.n_batch * a.n_groups);
+  hipLaunchKernelGGL(vmax_kernel, vgrid, dim3(256), 0, stream, a, width, w.vmax);
+  hipLaunchKernelGGL(vconv_kernel, vgrid, dim3(256), 0, stream, a, width, w.vmax, w.vshift, w.v16);
   // Shapes with at most 5 steps and 2 dv blocks (head dim 64) take the
   // smaller kernel; every other shape runs the full 9 x 4 one on zero padding.
   if (a.dim <= 80 && a.dv <= 64)
-    hipLaunchKernelGGL((chunk_kernel<5, 2>), grid, dim3(kThreads), 0, stream, a, width, splits, part);
+    hipLaunchKernelGGL((chunk_kernel<5, 2>), grid, dim3(kThreads), 0, stream, a, width, splits, w.part, w.v16,
+                       w.vshift);
   else
     hipLaunchKernelGGL((chunk_kernel<kMaxSteps, kMaxDvBlocks>), grid, dim3(kThreads), 0, stream, a, width, splits,
-                       part);
+                       w.part, w.v16, w.vshift);
   if (splits > 1)
-    hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a, part,
-                       splits);
+    hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a,
+                       w.part, splits);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
