@@ -367,7 +367,6 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, Ro
   int8_t* as_g = assign + static_cast<int64_t>(lane_ix) * r.tokens;
   int8_t* as = CAPPED ? as_l : as_g;
   const float* sw = s_win + static_cast<int64_t>(lane_ix) * r.tokens;
-  float* ds = dist + static_cast<int64_t>(lane_ix) * r.tokens;
   const int32_t* ord = order + static_cast<int64_t>(b) * r.tokens;
   const uint16_t* kbase = r.k + b * r.k_sb + g * r.k_sg;
   const int32_t* ntot = c.n_total + static_cast<int64_t>(lane_ix) * K;
@@ -438,28 +437,49 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, Ro
     n_use = 0;
   }
   if (n_use > 0 && tid == 0) picks_s[0] = pick;
+  // While seeding, the rows' running distances live in LDS (the candidate
+  // centers take the space afterwards); a wave takes kSeedRows rows at a time,
+  // their loads issued together, and holds the pick row in registers.
+  float* ds_l = cand_s;
+  constexpr int kSeedRows = 4, JM = kMaxDim / kWave;
   for (int step = 0; step + 1 < n_use; ++step) {
     // dist = min(dist, d2(., pick)), with the pick itself masked; argmax -> next pick.
     const uint16_t* prow = kbase + static_cast<int64_t>(ord[pick]) * r.k_st;
+    float xp[JM];
+#pragma unroll
+    for (int j = 0; j < JM; ++j) xp[j] = feat_or_zero(gp(prow), l + j * kWave, D);
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
-    for (int s = w; s < n; s += nw) {
-      float x[kMaxDim / kWave];
-      const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
+    for (int s0 = w * kSeedRows; s0 < n; s0 += nw * kSeedRows) {
+      float x[kSeedRows][JM];
 #pragma unroll
-      for (int j = 0; j < kMaxDim / kWave; ++j) {
-        const int d = l + j * kWave;
-        x[j] = feat_or_zero(gp(row), d, D);
+      for (int u = 0; u < kSeedRows; ++u) {
+        const uint16_t* row = kbase + static_cast<int64_t>(ord[min(s0 + u, n - 1)]) * r.k_st;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) x[u][j] = feat_or_zero(gp(row), l + j * kWave, D);
       }
-      const float d2 = row_d2_bf16(x, prow, D, J);
-      float val;
-      if (step == 0) val = as[s] < 0 ? d2 : -__builtin_inff();
-      else val = fminf(ds[s], d2);
-      if (s == pick) val = -__builtin_inff();
-      if (l == 0) ds[s] = val;
-      if (val > bv || (val == bv && s < bi)) {
-        bv = val;
-        bi = s;
+#pragma unroll
+      for (int u = 0; u < kSeedRows; ++u) {
+        const int s = s0 + u;
+        if (s >= n) break;
+        float e = 0.f;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+          if (j < J) {
+            const float diff = l + j * kWave < D ? x[u][j] - xp[j] : 0.f;
+            e = j == 0 ? diff * diff : e + diff * diff;
+          }
+        }
+        const float d2 = wave_sum0(e);
+        float val;
+        if (step == 0) val = as[s] < 0 ? d2 : -__builtin_inff();
+        else val = fminf(ds_l[s], d2);
+        if (s == pick) val = -__builtin_inff();
+        if (l == 0) ds_l[s] = val;
+        if (val > bv || (val == bv && s < bi)) {
+          bv = val;
+          bi = s;
+        }
       }
     }
     block_argmax(bv, bi, red_v, red_i);
@@ -486,34 +506,49 @@ __global__ __launch_bounds__(1024) void seed_kernel(LadderArgs c, RowsArgs r, Ro
   for (int cc = 0; cc < K; ++cc) cand_bits |= (c.alive[lane_ix * K + cc] ? 1u : 0u) << cc;
   for (int k = 0; k < n_use; ++k) cand_bits |= 1u << free_s[k];
   if constexpr (!CAPPED) {
-    for (int s = w; s < n; s += nw) {
-      if (as[s] >= 0) continue;
-      float x[kMaxDim / kWave];
-      const uint16_t* row = kbase + static_cast<int64_t>(ord[s]) * r.k_st;
+    // Every orphan's nearest candidate, kSeedRows rows of a wave at a time.
+    for (int s0 = w * kSeedRows; s0 < n; s0 += nw * kSeedRows) {
+      float x[kSeedRows][JM];
+      bool orphan[kSeedRows];
 #pragma unroll
-      for (int j = 0; j < kMaxDim / kWave; ++j) {
-        const int d = l + j * kWave;
-        x[j] = feat_or_zero(gp(row), d, D);
+      for (int u = 0; u < kSeedRows; ++u) {
+        orphan[u] = s0 + u < n && as[s0 + u] < 0;
+        const uint16_t* row = kbase + static_cast<int64_t>(ord[min(s0 + u, n - 1)]) * r.k_st;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) x[u][j] = orphan[u] ? feat_or_zero(gp(row), l + j * kWave, D) : 0.f;
       }
-      float best = __builtin_inff();
-      int arg = 0;
-      for (int cc = 0; cc < K; ++cc) {
-        float e = 0.f;
+      float best[kSeedRows];
+      int arg[kSeedRows];
 #pragma unroll
-        for (int j = 0; j < kMaxDim / kWave; ++j) {
-          if (j < J) {
-            const int d = l + j * kWave;
-            const float diff = d < D ? x[j] - cand_s[cc * D + d] : 0.f;
-            e = j == 0 ? diff * diff : e + diff * diff;
+      for (int u = 0; u < kSeedRows; ++u) {
+        best[u] = __builtin_inff();
+        arg[u] = 0;
+      }
+      for (int cc = 0; cc < K; ++cc) {
+        float cj[JM];
+#pragma unroll
+        for (int j = 0; j < JM; ++j) cj[j] = j < J && l + j * kWave < D ? cand_s[cc * D + l + j * kWave] : 0.f;
+        const bool cand = (cand_bits >> cc) & 1u;
+#pragma unroll
+        for (int u = 0; u < kSeedRows; ++u) {
+          float e = 0.f;
+#pragma unroll
+          for (int j = 0; j < JM; ++j) {
+            if (j < J) {
+              const float diff = l + j * kWave < D ? x[u][j] - cj[j] : 0.f;
+              e = j == 0 ? diff * diff : e + diff * diff;
+            }
+          }
+          e = wave_sum0(e);
+          if (cand && e < best[u]) {
+            best[u] = e;
+            arg[u] = cc;
           }
         }
-        e = wave_sum0(e);
-        if (((cand_bits >> cc) & 1u) && e < best) {
-          best = e;
-          arg = cc;
-        }
       }
-      if (l == 0) as[s] = static_cast<int8_t>(arg);
+#pragma unroll
+      for (int u = 0; u < kSeedRows; ++u)
+        if (orphan[u] && l == 0) as[s0 + u] = static_cast<int8_t>(arg[u]);
     }
     __syncthreads();
     if (tid < n_use) as[picks_s[tid]] = static_cast<int8_t>(free_s[tid]);
