@@ -473,11 +473,13 @@ int logkv_decode_attention_static(const logkv_attention_args* args, const int32_
                                   void* stream);
 
 /* The same attention for many query rows per KV group (a prefill or training
- * chunk), on the matrix cores (bf16 MFMA, fp32 accumulation, P split into two
- * bf16 parts): packed width <= 144, dv in {32, 64, 96, 128}. The key range is
- * split over several blocks per query tile when that fills the GPU better;
- * their partials go to the workspace (logkv_chunk_workspace_bytes, 0 when
- * not split) and are combined in split order.
+ * chunk), on the matrix cores (QK^T in bf16, PV in fp16 with P rounded to fp16,
+ * fp32 accumulation): packed width <= 144, dv in {32, 64, 96, 128}. The
+ * workspace (logkv_chunk_workspace_bytes, never 0) holds an fp16 copy of each
+ * lane's V scaled by a power of two 2^-k that keeps it below 2^15 (P scaled by
+ * 2^k; magnitudes of 2^30 and more overflow) and, when the key range is split
+ * over several blocks per query tile to fill the GPU, their partials, combined
+ * in split order.
  * Replaces the Flash SDPA call of _packed_flash_attention / _mid_chunk_attention
  * on a chunk (litgpt/log_kv_cache.py:6751-6758, :6802-6836). */
 int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* args);
