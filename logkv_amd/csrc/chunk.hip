@@ -423,31 +423,40 @@ __global__ __launch_bounds__(256) void vconv_kernel(logkv_attention_args a, cons
   }
 }
 
-// Partials of the key-range splits combined in split order: two queries per
-// block, one output feature per thread. A partial's maximum m is of s * scale *
-// log2(e), so a split's weight is 2^(m_split - m).
+// Partials of the key-range splits combined in split order: eight queries per
+// block, 32 threads per query, four output features per thread (dv <= 128). A
+// partial's maximum m is of s * scale * log2(e), so a split's weight is
+// 2^(m_split - m).
+constexpr int kCombineQueries = 8;
 __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args a, const float* __restrict__ part,
                                                             int splits) {
   const int lane_ix = blockIdx.y, G = a.n_groups;
   const int b = lane_ix / G, g = lane_ix % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
-  const int qi = blockIdx.x * 2 + static_cast<int>(threadIdx.x) / 128, d = threadIdx.x % 128;
+  const int qi = blockIdx.x * kCombineQueries + static_cast<int>(threadIdx.x) / 32;
+  const int d = 4 * (static_cast<int>(threadIdx.x) % 32);
   if (qi >= nq || d >= a.dv) return;
   const int stride = a.dv + 2;
   const float* base = part + (static_cast<int64_t>(lane_ix) * splits * nq + qi) * stride;
   const int64_t step = static_cast<int64_t>(nq) * stride;
   float m = -__builtin_inff();
   for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, base[sp * step]);
-  float lsum = 0.f, acc = 0.f;
+  float lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int sp = 0; sp < splits; ++sp) {
     const float* pp = base + sp * step;
     if (pp[0] == -__builtin_inff()) continue;
     const float f = __builtin_amdgcn_exp2f(pp[0] - m);   // maxima are in the base-2 domain
     lsum += pp[1] * f;
-    acc += pp[2 + d] * f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += pp[2 + d + j] * f;
   }
   const int head = g * rep + qi / a.tq, t = qi % a.tq;
-  gp(a.out)[b * a.o_sb + head * a.o_sh + t * a.o_st + d] = f32_to_bf16(acc / lsum);
+  LOGKV_G uint16_t* o = gp(a.out) + b * a.o_sb + head * a.o_sh + t * a.o_st + d;
+  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[0] / lsum)) |
+                      (static_cast<uint32_t>(f32_to_bf16(acc[1] / lsum)) << 16);
+  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[2] / lsum)) |
+                      (static_cast<uint32_t>(f32_to_bf16(acc[3] / lsum)) << 16);
+  *reinterpret_cast<LOGKV_G uint2*>(o) = make_uint2(lo, hi);
 }
 
 // Key-range splits: enough blocks for one resident round (kBlocksPerCu per
@@ -511,8 +520,8 @@ int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, 
     hipLaunchKernelGGL((chunk_kernel<kMaxSteps, kMaxDvBlocks>), grid, dim3(kThreads), 0, stream, a, width, splits,
                        w.part, w.v16, w.vshift);
   if (splits > 1)
-    hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + 1) / 2, a.n_batch * a.n_groups), dim3(256), 0, stream, a,
-                       w.part, splits);
+    hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + kCombineQueries - 1) / kCombineQueries, a.n_batch * a.n_groups),
+                       dim3(256), 0, stream, a, w.part, splits);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
