@@ -712,6 +712,19 @@ def decode_workload(args, torch, np):
 # ----------------------------------------------------------------------
 
 def prefill_workload(args, torch, np):
+    """The streaming prefill on one stream (the line's figures and the attention roofline), then again with
+    every cache's flushes on a side stream (``flush_stream``) beside the later layers' attention."""
+    res = _prefill_pass(args, torch, np, False)
+    if args.prefill_flush_stream:
+        torch.cuda.empty_cache()
+        side = _prefill_pass(args, torch, np, True)
+        res["side_stream"] = {k: side[k] for k in ("ms_per_block", "ms_per_block_by_block", "tokens_per_s")}
+        res["side_stream"]["note"] = ("flushes on a side stream: a layer's next attention waits for its own flush "
+                                      "only; the attention kernels then share the GPU with flush kernels")
+    return res
+
+
+def _prefill_pass(args, torch, np, side_stream):
     """Streaming prefill of a 32,768-token sequence through 28 Qwen3-1.7B-shaped layer caches, one call per
     layer as a model makes them: per 2048-token block and layer, the chunk attention of the block's 16 query
     heads over [compressed cache | block] (causal within the block) and add_recent, which flushes 2048 rows
@@ -733,6 +746,11 @@ def prefill_workload(args, torch, np):
     mix = Mixture(1, G, D, clusters=K, seed=43)
     q = torch.randn(1, HQ, F, D, generator=gen, device=dev).to(torch.bfloat16)
     stream = torch.cuda.current_stream(dev)
+    # Every layer's append + flush runs on a side stream beside the later layers' attention; a layer's
+    # next attention waits for its own flush (the cache orders its readers after it).
+    side = torch.cuda.Stream(dev) if side_stream else None
+    for cache in caches:
+        cache.flush_stream = side
     scale = D ** -0.5
     # Untimed warm-up on a spare cache: two blocks of attention + flush load every kernel of the path.
     spare = LogStructuredKVCache((1, G, 2 * F, D), (1, G, 2 * F, D), B=B, recent_size=F // 2, device=dev,
@@ -767,11 +785,14 @@ def prefill_workload(args, torch, np):
         events = []
         for cache in caches:
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            cache._await_flush(stream)   # the wait for the layer's last flush precedes the timed attention
             ev[0].record(stream)
             log_kv_chunk_attention(cache, q, k_raw, v, scale, second_order_scale=0.0)
             ev[1].record(stream)
             events.append(ev)
             cache.add_recent(k_raw, v, k_raw=k_raw, input_pos=pos, span_ends=ends)
+        for cache in caches:
+            cache._await_flush(stream)
         torch.cuda.synchronize()
         block_ms.append((time.perf_counter() - t0) * 1e3)
         attn_ms.append(float(np.sum([e[0].elapsed_time(e[1]) for e in events])))
@@ -782,7 +803,8 @@ def prefill_workload(args, torch, np):
     return {
         "workload": f"streaming prefill of {blocks * F} tokens through {layers} Qwen3-1.7B-shaped layer caches (16 q / 8 KV "
                     f"heads x 128, bf16), batch 1, {F}-token blocks, recent {F}, K={K}, B={B}, Alpha {EXACT}/{SPAN}, "
-                    "Beta, mid anchor; per block and layer: chunk attention (matrix cores) + add_recent (flush)",
+                    "Beta, mid anchor; per block and layer: chunk attention (matrix cores) + add_recent (flush)"
+                    + (", flushes on a side stream beside the attention" if side is not None else ", one stream"),
         "ms_per_block": float(np.mean(block_ms)), "ms_per_block_by_block": [round(x, 2) for x in block_ms],
         "tokens_per_s": N / (float(np.sum(block_ms)) * 1e-3),
         "attention_ms_per_block": float(np.mean(attn_ms)),
@@ -1071,6 +1093,8 @@ def parse_args(argv=None):
                     help="profiling run: the timed stacked pass of the headline only (no metered pass, no legs)")
     ap.add_argument("--only", choices=("config1", "decode", "prefill", "unified"),
                     help="profiling run: only this measurement, printed as its own JSON line")
+    ap.add_argument("--prefill-flush-stream", type=int, default=1, choices=(0, 1),
+                    help="1: also time the prefill with its flushes on a side stream (cache.flush_stream)")
     ap.add_argument("--prefill-blocks", type=int, default=N // F,
                     help="2048-token blocks of the streaming prefill (16 = the whole 32K-token sequence)")
     ap.add_argument("--step-traffic", type=float, default=None,

@@ -374,6 +374,17 @@ class LogStructuredKVCache(nn.Module):
         self._replaying_updates = False
         self._update_actions = None
         self._tape_index = 0
+        # Side-stream flushes: with `flush_stream` set (a torch.cuda.Stream of
+        # the cache's device), add_recent queues its append and flush there,
+        # after the caller's stream; every reader of the cache's device state
+        # then waits on the last such flush (`_flush_done`).
+        self.flush_stream = None
+        self._flush_done = None
+
+    def _await_flush(self, stream=None) -> None:
+        """Order ``stream`` (default: the current one) after the last flush queued on ``flush_stream``."""
+        if self._flush_done is not None:
+            (torch.cuda.current_stream(self.level_k.device) if stream is None else stream).wait_event(self._flush_done)
 
     def _semantic_capacity_target(self) -> float:
         """Rows per cluster if the sequence filled every cluster evenly (litgpt/log_kv_cache.py:2347-2348)."""
@@ -437,6 +448,7 @@ class LogStructuredKVCache(nn.Module):
         (``begin_op_log``); ``replay_op_log`` / ``replay_op_log_len`` re-apply
         a logged flush without routing (litgpt/log_kv_cache.py:5049-5114).
         """
+        self._await_flush()
         if self._active_updates is not None:
             return self._tape_flush(self._active_updates, k_raw, v, positions, positions_host, span_ends, counts,
                                     record_op_log, replay_op_log is not None or replay_op_log_host is not None)
@@ -653,6 +665,7 @@ class LogStructuredKVCache(nn.Module):
         arg, position) and ``op_log_len`` ``[Bt, G]``, written on the device by
         every flush routed with ``record_op_log=True``.
         """
+        self._await_flush()
         cap = max(1, self.max_seq_length * 3)
         dev = self.level_count.device
         self.op_log = torch.zeros(self.batch_size, self.n_groups, cap, 4, device=dev, dtype=torch.int32)
@@ -674,6 +687,7 @@ class LogStructuredKVCache(nn.Module):
         """
         if getattr(self, "op_log", None) is None or getattr(self, "op_log_len", None) is None:
             return None, None
+        self._await_flush()
         lengths = self.op_log_len.cpu()
         if int(lengths.max()) > self.op_log.size(2):
             raise RuntimeError("semantic LogKV op_log overflow")
@@ -845,7 +859,31 @@ class LogStructuredKVCache(nn.Module):
     def add_recent(self, k, v, *, k_raw=None, input_pos=None, record_op_log=False, replay_op_log=None,
                    replay_op_log_len=None, replay_op_log_host=None, replay_plans=None, span_ends=None):
         """Append a block to the recent window; flush whole granules on overflow
-        (litgpt/log_kv_cache.py:5668-5718, :5847)."""
+        (litgpt/log_kv_cache.py:5668-5718, :5847). With ``flush_stream`` set the
+        append and the flush are queued on that stream after the caller's, and
+        the cache's readers wait for them; the host state advances at once."""
+        side = self.flush_stream
+        if side is not None and side != torch.cuda.current_stream(self.level_k.device):
+            side.wait_stream(torch.cuda.current_stream(self.level_k.device))
+            for t in (k, v, k_raw, input_pos, span_ends):
+                if isinstance(t, torch.Tensor) and t.is_cuda:
+                    t.record_stream(side)
+            with torch.cuda.stream(side):
+                self._add_recent(k, v, k_raw=k_raw, input_pos=input_pos, record_op_log=record_op_log,
+                                 replay_op_log=replay_op_log, replay_op_log_len=replay_op_log_len,
+                                 replay_op_log_host=replay_op_log_host, replay_plans=replay_plans,
+                                 span_ends=span_ends)
+            done = self._flush_done if self._flush_done is not None else torch.cuda.Event()
+            done.record(side)
+            self._flush_done = done
+            return
+        self._add_recent(k, v, k_raw=k_raw, input_pos=input_pos, record_op_log=record_op_log,
+                         replay_op_log=replay_op_log, replay_op_log_len=replay_op_log_len,
+                         replay_op_log_host=replay_op_log_host, replay_plans=replay_plans, span_ends=span_ends)
+
+    def _add_recent(self, k, v, *, k_raw=None, input_pos=None, record_op_log=False, replay_op_log=None,
+                    replay_op_log_len=None, replay_op_log_host=None, replay_plans=None, span_ends=None):
+        self._await_flush()
         if k_raw is None:
             raise ValueError("semantic LogKV add_recent requires pre-RoPE k_raw")
         n = k.size(2)
@@ -880,6 +918,7 @@ class LogStructuredKVCache(nn.Module):
 
     def reset_parameters(self) -> None:
         """Empty cache (litgpt/log_kv_cache.py:6270)."""
+        self._await_flush()
         i64max = torch.iinfo(torch.int64).max
         for name in ("recent_k", "recent_v", "recent_k_raw", "recent_pos", "level_k", "level_v", "level_w",
                      "level_imp", "level_count", "pad_mask", "level_sum_wp", "level_order", "centroid", "n_eff",

@@ -63,6 +63,7 @@ class MidAttentionPlan:
 def readout_view(cache) -> ReadoutView:
     """The cache's readout struct: built once per exact-pool buffer set and
     reused (only the recent row count changes between calls)."""
+    cache._await_flush()
     key = ("readout", cache._alpha_parity)
     view = cache._views.get(key)
     if view is None:
