@@ -228,6 +228,43 @@ int logkv_unified_decisions(const logkv_ladder_view* cache, const logkv_rows_vie
                             int8_t* assign, int32_t* order, int32_t* jobs, int32_t* n_jobs, int32_t into_workspace,
                             void* stream);
 
+/* The recent window's buffers and, for an append, the block's rows:
+ * recent_k [n_batch, G, cap, dk], recent_k_raw [.., dkr], recent_v [.., dv]
+ * (bf16, contiguous), recent_pos int64 [n_batch, cap], recent_ends uint8
+ * [n_batch, cap] or NULL (no Alpha). Sources k / k_raw / v are bf16 with
+ * element strides (batch, group, row; features contiguous), pos int64 with
+ * strides (batch, row), ends uint8 [n_batch, n] rows of stride ends_sb.
+ * Feature counts are multiples of 4; rows and strides 8-byte aligned. */
+typedef struct logkv_recent_args {
+  uint16_t* recent_k;
+  uint16_t* recent_k_raw;
+  uint16_t* recent_v;
+  int64_t* recent_pos;
+  uint8_t* recent_ends;
+  int32_t n_batch, n_groups, cap, dk, dkr, dv;
+  const uint16_t* k;
+  int64_t k_sb, k_sg, k_st;
+  const uint16_t* k_raw;
+  int64_t kr_sb, kr_sg, kr_st;
+  const uint16_t* v;
+  int64_t v_sb, v_sg, v_st;
+  const int64_t* pos;
+  int64_t pos_sb, pos_st;
+  const uint8_t* ends;
+  int64_t ends_sb;
+} logkv_recent_args;
+
+/* Appends rows [0, n) of the sources to recent rows [at, at + n) of every
+ * buffer in one launch. Replaces the recent-window writes of add_recent
+ * (litgpt/log_kv_cache.py:5668-5718). */
+int logkv_recent_append(const logkv_recent_args* args, int32_t at, int32_t n, void* stream);
+
+/* After a flush of the first `take` of `count` recent rows: rows [take, count)
+ * move to the front and rows [count - take, count) are cleared, every buffer
+ * in one launch; needs count - take <= take. Replaces the shift and clear
+ * after a flush (litgpt/log_kv_cache.py:5640-5659). */
+int logkv_recent_shift(const logkv_recent_args* args, int32_t take, int32_t count, void* stream);
+
 /* Candidate span table over the virtual rows [old exact pool (old_width rows) |
  * flush]: pool_* / flush_* are [n_batch, G, rows, d] bf16 with element strides;
  * span i covers tokens[span_offsets[i] .. span_offsets[i+1]) of batch row

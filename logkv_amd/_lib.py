@@ -46,6 +46,15 @@ class RouteParams(C.Structure):
                 ("hard_cap_rows", _i32)]
 
 
+class RecentArgs(C.Structure):
+    _fields_ = [("recent_k", _p), ("recent_k_raw", _p), ("recent_v", _p), ("recent_pos", _p), ("recent_ends", _p),
+                ("n_batch", _i32), ("n_groups", _i32), ("cap", _i32), ("dk", _i32), ("dkr", _i32), ("dv", _i32),
+                ("k", _p), ("k_sb", _i64), ("k_sg", _i64), ("k_st", _i64),
+                ("k_raw", _p), ("kr_sb", _i64), ("kr_sg", _i64), ("kr_st", _i64),
+                ("v", _p), ("v_sb", _i64), ("v_sg", _i64), ("v_st", _i64),
+                ("pos", _p), ("pos_sb", _i64), ("pos_st", _i64), ("ends", _p), ("ends_sb", _i64)]
+
+
 class SpanArgs(C.Structure):
     _fields_ = [
         ("pool_k", _p), ("pk_sb", _i64), ("pk_sg", _i64), ("pk_st", _i64),
@@ -206,6 +215,8 @@ SIGNATURES = {
     "logkv_chunk_attention_backward": (_i32, [C.POINTER(AttentionArgs), _p, _i64, C.POINTER(AttentionGradArgs), _p,
                                               _i64, _p]),
     "logkv_chunk_workspace_bytes": (_i64, [C.POINTER(AttentionArgs)]),
+    "logkv_recent_append": (_i32, [C.POINTER(RecentArgs), _i32, _i32, _p]),
+    "logkv_recent_shift": (_i32, [C.POINTER(RecentArgs), _i32, _i32, _p]),
     "logkv_chunk_attention": (_i32, [C.POINTER(AttentionArgs), _p, _i64, _p, _i64, _p]),
 }
 

@@ -654,6 +654,52 @@ int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, i
   return LOGKV_OK;
 }
 
+namespace {
+int check_recent(const logkv_recent_args* a) {
+  if (!a) return fail(LOGKV_EINVAL, "recent args are NULL");
+  if (a->n_batch < 1 || a->n_groups < 1 || a->cap < 1)
+    return fail(LOGKV_EINVAL, "recent window needs n_batch, n_groups, cap >= 1");
+  for (int d : {a->dk, a->dkr, a->dv})
+    if (d < 4 || d % 4 || d > logkv::kMaxDim)
+      return fail(LOGKV_EINVAL, "recent feature counts must be multiples of 4 in [4, %d]", logkv::kMaxDim);
+  if (!a->recent_k || !a->recent_k_raw || !a->recent_v || !a->recent_pos)
+    return fail(LOGKV_EINVAL, "recent buffer is NULL");
+  if (reinterpret_cast<uintptr_t>(a->recent_k) % 8 || reinterpret_cast<uintptr_t>(a->recent_k_raw) % 8 ||
+      reinterpret_cast<uintptr_t>(a->recent_v) % 8)
+    return fail(LOGKV_EINVAL, "recent buffers must be 8-byte aligned");
+  return LOGKV_OK;
+}
+}  // namespace
+
+int logkv_recent_append(const logkv_recent_args* a, int32_t at, int32_t n, void* stream) {
+  int rc = check_recent(a);
+  if (rc) return rc;
+  if (at < 0 || n < 0 || int64_t(at) + n > a->cap)
+    return fail(LOGKV_EINVAL, "append of %d rows at %d exceeds the recent capacity %d", n, at, a->cap);
+  if (n == 0) return LOGKV_OK;
+  if (!a->k || !a->k_raw || !a->v || !a->pos) return fail(LOGKV_EINVAL, "append source is NULL");
+  if ((a->recent_ends == nullptr) != (a->ends == nullptr))
+    return fail(LOGKV_EINVAL, "span flags must be given exactly when the window keeps them");
+  if (reinterpret_cast<uintptr_t>(a->k) % 8 || reinterpret_cast<uintptr_t>(a->k_raw) % 8 ||
+      reinterpret_cast<uintptr_t>(a->v) % 8 || a->k_sb % 4 || a->k_sg % 4 || a->k_st % 4 || a->kr_sb % 4 ||
+      a->kr_sg % 4 || a->kr_st % 4 || a->v_sb % 4 || a->v_sg % 4 || a->v_st % 4)
+    return fail(LOGKV_EINVAL, "append sources need 8-byte aligned rows (strides multiple of 4 elements)");
+  rc = logkv::launch_recent_append(*a, at, n, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "recent append launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
+int logkv_recent_shift(const logkv_recent_args* a, int32_t take, int32_t count, void* stream) {
+  int rc = check_recent(a);
+  if (rc) return rc;
+  if (take < 1 || take > count || count > a->cap || count - take > take)
+    return fail(LOGKV_EINVAL, "shift of %d of %d rows needs 1 <= take <= count <= cap and count - take <= take",
+                take, count);
+  rc = logkv::launch_recent_shift(*a, take, count, static_cast<hipStream_t>(stream));
+  if (rc) return fail(rc, "recent shift launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return LOGKV_OK;
+}
+
 int logkv_beta_merge(const logkv_beta_args* a, int32_t* status, void* stream) {
   if (!a) return fail(LOGKV_EINVAL, "Beta merge args are NULL");
   if (a->n_rows < 0 || a->n_rows % 2) return fail(LOGKV_EINVAL, "Beta merge needs an even row count, got %lld",

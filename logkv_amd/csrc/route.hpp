@@ -79,6 +79,8 @@ int launch_order(const RowsArgs& r, int n_batch, int32_t* order, int32_t* clear,
 int launch_record(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, const logkv_op_log_view& log,
                   hipStream_t stream);
 int launch_beta_merge(const logkv_beta_args& a, int32_t* status, hipStream_t stream);
+int launch_recent_append(const logkv_recent_args& a, int at, int n, hipStream_t stream);
+int launch_recent_shift(const logkv_recent_args& a, int take, int count, hipStream_t stream);
 int launch_slot_pack(const logkv_slot_pack_args& a, hipStream_t stream);
 int64_t chunk_backward_workspace_floats(const logkv_attention_args& a);
 int launch_chunk_backward(const logkv_attention_args& a, const int32_t* width, const logkv_attention_grad_args& g,

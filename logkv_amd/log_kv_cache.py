@@ -813,6 +813,14 @@ class LogStructuredKVCache(nn.Module):
                 **route,
             )
             remaining = self.recent_count - take
+            if remaining <= take:
+                # One launch moves the remaining rows to the front and clears the rest.
+                args = self._recent_args()
+                check(lib().logkv_recent_shift(C.byref(args), take, self.recent_count,
+                                               stream_of(self.recent_k.device)), "logkv_recent_shift")
+                self.recent_count = remaining
+                pending -= take
+                continue
             if remaining > 0:
                 stage = (lambda x: x) if remaining <= take else torch.Tensor.clone
                 for name in ("recent_k", "recent_k_raw", "recent_v"):
@@ -829,6 +837,40 @@ class LogStructuredKVCache(nn.Module):
                 self.recent_span_ends[:, remaining:self.recent_count].zero_()
             self.recent_count = remaining
             pending -= take
+
+    def _recent_args(self):
+        """The recent window's buffers as the C-ABI struct (built once; the sources are set per append)."""
+        args = self._views.get("recent")
+        if args is None:
+            args = self._views["recent"] = _lib.RecentArgs()
+            args.recent_k, args.recent_k_raw, args.recent_v = ptr(self.recent_k), ptr(self.recent_k_raw), ptr(self.recent_v)
+            args.recent_pos = ptr(self.recent_pos)
+            args.recent_ends = ptr(self.recent_span_ends) if self.alpha_exact_tokens else None
+            args.n_batch, args.n_groups, args.cap = self.batch_size, self.n_groups, self.recent_capacity
+            args.dk, args.dkr, args.dv = self.recent_k.size(-1), self.recent_k_raw.size(-1), self.recent_v.size(-1)
+        return args
+
+    def _recent_append(self, k, k_raw, v, positions, ends, n) -> bool:
+        """Append rows with one launch (litgpt/log_kv_cache.py:5668-5718); False when a source's layout
+        (dtype, feature stride, 8-byte rows) leaves it to tensor copies."""
+        srcs = (k, k_raw, v)
+        if n == 0 or any(t.dtype != torch.bfloat16 or t.stride(-1) != 1 or t.data_ptr() % 8
+                         or any(st % 4 for st in t.stride()[:3]) or t.device != self.recent_k.device for t in srcs):
+            return False
+        if positions.dtype != torch.int64 or (ends is not None and (ends.dtype != torch.uint8 or ends.stride(-1) != 1)):
+            return False
+        if tuple(k.shape) != (self.batch_size, self.n_groups, n, self.recent_k.size(-1)) or \
+                tuple(v.shape) != (self.batch_size, self.n_groups, n, self.recent_v.size(-1)):
+            return False
+        args = self._recent_args()
+        args.k, (args.k_sb, args.k_sg, args.k_st) = ptr(k), k.stride()[:3]
+        args.k_raw, (args.kr_sb, args.kr_sg, args.kr_st) = ptr(k_raw), k_raw.stride()[:3]
+        args.v, (args.v_sb, args.v_sg, args.v_st) = ptr(v), v.stride()[:3]
+        args.pos, (args.pos_sb, args.pos_st) = ptr(positions), positions.stride()
+        args.ends, args.ends_sb = (ptr(ends), ends.stride(0)) if ends is not None else (None, 0)
+        check(lib().logkv_recent_append(C.byref(args), self.recent_count, n, stream_of(self.recent_k.device)),
+              "logkv_recent_append")
+        return True
 
     def _input_positions(self, n, input_pos):
         """Positions of an appended block as a device tensor ``[Bt, n]`` (no host read)."""
@@ -901,13 +943,14 @@ class LogStructuredKVCache(nn.Module):
         if self.recent_count + n > self.recent_capacity:
             raise RuntimeError(f"semantic LogKV recent buffer overflow: recent_count={self.recent_count}, n={n}, "
                                f"capacity={self.recent_capacity}")
-        dst = slice(self.recent_count, self.recent_count + n)
-        self.recent_k[:, :, dst] = k
-        self.recent_k_raw[:, :, dst] = k_raw
-        self.recent_v[:, :, dst] = v
-        self.recent_pos[:, dst] = positions
-        if ends is not None:
-            self.recent_span_ends[:, dst] = ends
+        if not self._recent_append(k, k_raw, v, positions, ends, n):
+            dst = slice(self.recent_count, self.recent_count + n)
+            self.recent_k[:, :, dst] = k
+            self.recent_k_raw[:, :, dst] = k_raw
+            self.recent_v[:, :, dst] = v
+            self.recent_pos[:, dst] = positions
+            if ends is not None:
+                self.recent_span_ends[:, dst] = ends
         self.recent_count += n
         overflow = self.recent_count - self.recent_size
         if overflow > 0:

@@ -60,7 +60,7 @@ STRUCTS = {
     "logkv_pack_args": _lib.PackArgs, "logkv_attention_args": _lib.AttentionArgs,
     "logkv_alpha_select_args": _lib.AlphaSelectArgs, "logkv_op_log_view": _lib.OpLogView,
     "logkv_beta_args": _lib.BetaArgs, "logkv_slot_pack_args": _lib.SlotPackArgs,
-    "logkv_attention_grad_args": _lib.AttentionGradArgs,
+    "logkv_attention_grad_args": _lib.AttentionGradArgs, "logkv_recent_args": _lib.RecentArgs,
 }
 
 
