@@ -89,15 +89,15 @@ class LogKVStreamingAttention:
         pending = self._log_kv_pending
         if pending is not None:
             pk, pv, pk_raw, ppos, pends = pending
-            k0, v0 = k[:, :, :1], v[:, :, :1]
-            outputs.append(log_kv_chunk_attention(cache, q[:, :, :1], torch.cat([pk, k0], dim=2),
-                                                  torch.cat([pv, v0], dim=2), self.scale, 0.0, causal_tail=0,
+            # The pair's keys and values serve the attention and the commit.
+            kk, vv = torch.cat([pk, k[:, :, :1]], dim=2), torch.cat([pv, v[:, :, :1]], dim=2)
+            outputs.append(log_kv_chunk_attention(cache, q[:, :, :1], kk, vv, self.scale, 0.0, causal_tail=0,
                                                   reuse_prefix=True))
             pos0 = pos_slice(0, 1)
             pos = None if ppos is None or pos0 is None else torch.cat([ppos.to(pos0.device), pos0], dim=-1)
             ends = None if pends is None else _join(pends, _cols(span_ends, 0, 1))
-            cache.add_recent(torch.cat([pk, k0], dim=2), torch.cat([pv, v0], dim=2),
-                             k_raw=torch.cat([pk_raw, k_raw[:, :, :1]], dim=2), input_pos=pos, span_ends=ends)
+            cache.add_recent(kk, vv, k_raw=torch.cat([pk_raw, k_raw[:, :, :1]], dim=2), input_pos=pos,
+                             span_ends=ends)
             self._log_kv_pending = None
             start = 1
 
@@ -117,5 +117,5 @@ class LogKVStreamingAttention:
                                         k_raw[:, :, commit_end:end], pos_slice(commit_end, end),
                                         _cols(span_ends, commit_end, end))
             start = end
-        y = torch.cat(outputs, dim=2)   # [B, n_head, T, dv]
+        y = outputs[0] if len(outputs) == 1 else torch.cat(outputs, dim=2)   # [B, n_head, T, dv]
         return y.transpose(1, 2).reshape(B, T, -1)
