@@ -40,6 +40,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import gc
 import json
 import math
 import os
@@ -1059,10 +1060,21 @@ def kernel_counters(counter_dir):
 
 # ----------------------------------------------------------------------
 
+def quiet_gc(fn, *args):
+    """Run a measurement with Python's cycle collector paused (collected before): a collection
+    inside a timed region stalls the host for milliseconds while the GPU waits for launches."""
+    gc.collect()
+    gc.disable()
+    try:
+        return fn(*args)
+    finally:
+        gc.enable()
+
+
 def run_leg(result, key, fn, *args):
     """A secondary measurement: its failure is recorded in the line, never fatal."""
     try:
-        result[key] = fn(*args)
+        result[key] = quiet_gc(fn, *args)
     except Exception as e:
         traceback.print_exc()
         result[key] = {"error": f"{type(e).__name__}: {e}"}
@@ -1150,7 +1162,7 @@ def main():
         return
     if args.profile_flush:
         args.flush_passes = "stacked"
-    fl = flush_workload(args, torch, np)
+    fl = quiet_gc(flush_workload, args, torch, np)
     result = {
         "metric": "flushed tokens/s (route+merge+pack) & decode ms/token at 32K ctx, 1 GPU",
         "value": fl["value"],
