@@ -627,7 +627,9 @@ int logkv_decode_attention_static(const logkv_attention_args* a, const int32_t* 
 }
 
 int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* a) {
-  if (!a || a->n_groups < 1 || a->n_heads % a->n_groups) return -1;
+  if (!a || a->n_groups < 1 || a->n_heads % a->n_groups || a->n_batch < 1 || a->cap < 1 || a->tq < 1 ||
+      a->dv < 1 || a->dv > logkv::kMaxDim)
+    return -1;
   return logkv::chunk_workspace_floats(*a) * 4;
 }
 
@@ -641,6 +643,8 @@ int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, i
   if (a->dv % 32 || a->dv < 32 || a->dv > 128) return fail(LOGKV_EINVAL, "chunk attention takes dv in {32, 64, 96, 128}");
   if (a->causal_tail < 0 || a->causal_tail > a->tail || (a->causal_tail && a->causal_tail != a->tq))
     return fail(LOGKV_EINVAL, "causal_tail must be 0 or the query length");
+  if (a->n_batch < 1 || a->cap < 1 || a->tail < 0 || a->tail > a->cap)
+    return fail(LOGKV_EINVAL, "attention needs n_batch >= 1 and 0 <= tail <= cap (cap >= 1)");
   if (!a->q || !a->k || !a->v || !a->out) return fail(LOGKV_EINVAL, "attention buffer is NULL");
   if (reinterpret_cast<uintptr_t>(a->out) % 8 || a->o_st % 4 || a->o_sh % 4 || a->o_sb % 4)
     return fail(LOGKV_EINVAL, "chunk attention output rows must be 8-byte aligned");
