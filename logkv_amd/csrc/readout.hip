@@ -31,7 +31,8 @@ constexpr int kPlanThreads = 256;
 constexpr int kTile = 64;          // rows per staged K/V tile
 constexpr int kSplitRows = 512;    // rows per attention split (staged decode kernel)
 constexpr int kStreamRows = 512;   // most rows per split of the streaming kernel when the grid is not the limit
-constexpr int kStreamBlocks = 1280;   // streaming blocks resident at once (256 CUs x 5 blocks of 4 waves; 2560 measured slower)
+constexpr int kStreamBlocks = 640;    // streaming blocks per launch at most: 2.5 per CU, so splits are long enough to
+                                      // amortize a block's start and end (1280 / 1024 / 512 / 320 measured slower)
 constexpr int kMaxQ = 16;          // queries per KV group (heads per group x query rows)
 constexpr int kMaxPacked = 264;    // packed row width limit (dk + 1 rounded to 8, dv)
 constexpr int kAccPerThread = kMaxQ * kMaxDim / 256;   // outputs per thread of a 256-thread split block
