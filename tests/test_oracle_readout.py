@@ -114,7 +114,7 @@ def test_masked_softmax_with_causal_tail():
     q = bf16_round(rng.standard_normal((1, 2, tq, dk)).astype(np.float32))
     scale = dk ** -0.5
     got = ro.attention(q, ka, va, scale, tq, dv)
-    inv = float(bf16_round(np.float32(1.0 / scale)))
+    inv = float(bf16_round(np.float32(1.0 / scale)).reshape(-1)[0])
     for h in range(2):
         for i in range(tq):
             logits = scale * (ka[0, 0, :, :dk].astype(np.float64) @ q[0, h, i].astype(np.float64)) \
