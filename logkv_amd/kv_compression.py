@@ -60,6 +60,9 @@ def _count_layer(attn, processed_tokens: int) -> _LayerCount:
     if cache is None:
         raise ValueError("every attention layer needs an initialized KV cache to measure compression")
     if hasattr(cache, "token_count"):
+        await_flush = getattr(cache, "_await_flush", None)
+        if await_flush is not None:
+            await_flush()   # a flush queued on the cache's side stream is counted too
         tail = getattr(attn, "_log_kv_pending", None)
         tail_len = 0 if tail is None else tail[0].size(2)
         lanes = cache.batch_size * cache.n_groups

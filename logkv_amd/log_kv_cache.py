@@ -1049,11 +1049,13 @@ class LogStructuredKVCache(nn.Module):
         """Rows of the exact pool in use (largest kept count); read from the device."""
         if not self.alpha_exact_tokens:
             return self._alpha_count_host
+        self._await_flush()
         return int(self.alpha_count_dev.item())
 
     @alpha_count.setter
     def alpha_count(self, value: int) -> None:
         if self.alpha_exact_tokens:
+            self._await_flush()
             self.alpha_count_dev.fill_(int(value))
         else:
             self._alpha_count_host = int(value)
@@ -1061,6 +1063,7 @@ class LogStructuredKVCache(nn.Module):
     @property
     def _alpha_spans(self):
         """Per batch row, (length, closed) of the exact pool's spans (litgpt/log_kv_cache.py)."""
+        self._await_flush()
         n = self.alpha_span_count.tolist()
         lens, closed = self.alpha_span_len.tolist(), self.alpha_span_closed.tolist()
         return [[(lens[b][i], bool(closed[b][i])) for i in range(n[b])] for b in range(self.batch_size)]
@@ -1074,22 +1077,27 @@ class LogStructuredKVCache(nn.Module):
 
     @property
     def _semantic_counts(self):
+        self._await_flush()
         return self.level_count.long().cpu().tolist()
 
     @property
     def _semantic_alive(self):
+        self._await_flush()
         return self.alive.cpu().tolist()
 
     @property
     def _semantic_p_hi_c(self):
+        self._await_flush()
         return self.p_hi_c.cpu().tolist()
 
     @property
     def _semantic_n_total(self):
+        self._await_flush()
         return self.n_total.long().cpu().tolist()
 
     @property
     def _semantic_level0_phase(self):
+        self._await_flush()
         return self.level0_phase.long().cpu().tolist()
 
     @property
