@@ -45,77 +45,72 @@ class SpanCut:
     length_rows: list
 
 
-def _scan_runs(new_pos, ends, pending, pending_pos, max_span):
-    """Runs of a flush's tokens, scanned once in order: ``(pending_closed, [(start, stop, closed)])``
-    (the run rule of litgpt/alpha_log_kv.py:16-53).
+def _cut_row(spans, old_pos, new_pos, flags, old_width, max_span):
+    """One row's candidates ``[(ranges, old, closed)]`` and its ``[pool | flush]`` positions.
 
-    A run ends after a boundary token, when its hard segment (tokens since the flush start, a
-    boundary or a position jump; the unfinished old span of ``pending`` tokens counts toward the
-    flush's first segment) reaches a multiple of ``max_span`` tokens, or before a position jump;
-    the last run ends with the flush, closed only if its last token closed it. A jump between the
-    old span's last position and the first token closes the old span instead of extending it. An
-    old span of ``max_span`` tokens or more only ends at a boundary or a jump.
+    Closed old spans are candidates as they are. The row's last unfinished old span (the tail) and
+    the flush tokens are then walked as one sequence, in combined coordinates: ``c < t`` is the
+    tail's ``c``-th token (pool row ``t0 + c``), ``c >= t`` the flush's token ``c - t`` (row
+    ``old_width + c - t``). A run of that sequence closes at a boundary token or when its hard
+    segment reaches a multiple of ``max_span`` tokens, and a position jump closes the open run
+    before the jumping token; the run open at the end stays unfinished. The tail's own tokens never
+    close a run (the previous flush left it open), they only count toward the first segment, and a
+    tail of ``max_span`` tokens or more disables the cap until that segment ends. A run is reported
+    as one row range per side of the tail / flush border it covers.
     """
-    n = len(new_pos)
-    if n == 0:
-        return False, []
-    pending_closed = bool(pending) and int(new_pos[0]) != pending_pos + 1
-    depth = 0 if pending_closed else int(pending)   # tokens of the current hard segment so far
-    capped = depth < max_span                        # whether cap closes apply in this segment
-    runs, start = [], 0
-    for i in range(n):
-        if i and int(new_pos[i]) != int(new_pos[i - 1]) + 1:
-            if start < i:
-                runs.append((start, i, True))        # a jump closes the open run
-            start, depth, capped = i, 0, True
+    row, tail, offset = [], None, 0
+    for length, closed in spans:
+        if closed:
+            row.append(([(offset, offset + length)], True, True))
+        else:
+            tail = (offset, length)
+        offset += length
+    positions = np.zeros(old_width + len(new_pos), dtype=np.int64)
+    positions[:len(old_pos)] = old_pos
+    positions[old_width:] = new_pos
+    t0, t = tail if tail is not None else (0, 0)
+
+    def ranges(a, z):
+        out = [(t0 + a, t0 + min(z, t))] if a < t else []
+        if z > t:
+            out.append((old_width + max(a, t) - t, old_width + z - t))
+        return out
+
+    start, depth, capped = 0, t, t < max_span
+    prev = int(positions[t0 + t - 1]) if t else None
+    for i, p in enumerate(int(x) for x in new_pos):
+        c = t + i
+        if prev is not None and p != prev + 1:
+            if start < c:
+                row.append((ranges(start, c), False, True))
+            start, depth, capped = c, 0, True
+        prev = p
         depth += 1
-        if ends[i] or (capped and depth % max_span == 0):
-            runs.append((start, i + 1, True))
-            start = i + 1
-            if ends[i]:
+        if flags[i] or (capped and depth % max_span == 0):
+            row.append((ranges(start, c + 1), False, True))
+            start = c + 1
+            if flags[i]:
                 depth, capped = 0, True
-    if start < n:
-        runs.append((start, n, False))
-    return pending_closed, runs
+    if start < t + len(new_pos):
+        row.append((ranges(start, t + len(new_pos)), False, False))
+    return row, positions
 
 
 def cut_spans(old_spans, old_positions, new_positions, ends, old_width, max_span):
     """Whole candidate spans per row (host only); None when no row has one
     (litgpt/alpha_log_kv.py:84-122).
 
-    Row indices address ``[old exact pool (old_width rows) | current flush]``. A row's candidates:
-    its closed old spans (old), then the old unfinished span when a position jump closes it, then
-    the flush's runs - the first one prefixed by the unfinished old span when that continues - and
-    an unfinished old span the flush leaves untouched. Each candidate is ``(ranges, old, closed)``.
+    Row indices address ``[old exact pool (old_width rows) | current flush]``. A row's candidates
+    are its closed old spans (old), then the runs of its unfinished old span followed by the flush
+    (``_cut_row``): a position jump right after that span closes it alone, otherwise the flush's
+    first run continues it. Each candidate is ``(ranges, old, closed)``.
     """
     candidates, token_rows, length_rows = [], [], []
     for spans, old_pos, new_pos, flags in zip(old_spans, old_positions, new_positions, ends):
-        row = []
-        offset, tail = 0, None
-        for length, closed in spans:
-            if closed:
-                row.append(([(offset, offset + length)], True, True))
-            else:
-                tail = (offset, offset + length)
-            offset += length
-        positions = np.zeros(old_width + len(new_pos), dtype=np.int64)
-        positions[:len(old_pos)] = old_pos
-        positions[old_width:] = new_pos
-        tail_len = 0 if tail is None else tail[1] - tail[0]
-        tail_pos = int(positions[tail[1] - 1]) if tail_len else 0
-        tail_closed, runs = _scan_runs(new_pos, flags, tail_len, tail_pos, max_span)
-        if tail_closed:
-            row.append(([tail], False, True))
-        for i, (a, z, done) in enumerate(runs):
-            joined = i == 0 and tail_len and not tail_closed
-            row.append(([tail, (old_width + a, old_width + z)] if joined else [(old_width + a, old_width + z)],
-                        False, done))
-        if tail_len and not tail_closed and not runs:
-            row.append(([tail], False, False))
-        tokens = [t for ranges, _, _ in row for a, z in ranges for t in range(a, z)]
-        token_rows.append(np.asarray(tokens, dtype=np.int64))
-        length_rows.append([sum(z - a for a, z in ranges) for ranges, _, _ in row])
+        row, positions = _cut_row(spans, old_pos, new_pos, flags, old_width, max_span)
         candidates.append((row, positions))
+        token_rows.append(np.asarray([i for rs, _, _ in row for a, z in rs for i in range(a, z)], dtype=np.int64))
+        length_rows.append([sum(z - a for a, z in rs) for rs, _, _ in row])
     if not any(length_rows):
         return None
     return SpanCut(candidates, token_rows, length_rows)

@@ -8,7 +8,9 @@ from logkv_amd import alpha_log_kv as prod
 from oracle import spans as ora
 
 
-def test_new_runs_match_token_loop():
+def test_one_row_runs_match_token_loop():
+    """One row: an unfinished old span (of up to max_span + 1 tokens, so also one that disables
+    the cap) continued or closed by a position jump, flush rows with jumps and boundaries."""
     rng = np.random.default_rng(11)
     for _ in range(600):
         count = int(rng.integers(0, 30))
@@ -17,10 +19,18 @@ def test_new_runs_match_token_loop():
         steps = 1 + (rng.random(count) < 0.1) * rng.integers(1, 4, count)
         new_pos = (100 + np.cumsum(steps)).tolist()
         ends = (rng.random(count) < 0.2).tolist()
-        pending_pos = new_pos[0] - int(rng.integers(1, 3)) if count else 0
-        got = prod._scan_runs(new_pos, ends, pending, pending_pos, max_span)
-        want = ora.new_runs(new_pos, ends, pending, pending_pos, max_span)
-        assert got == want
+        last = (new_pos[0] if count else 100) - int(rng.integers(1, 3))
+        spans = [[(pending, False)]] if pending else [[]]
+        old_pos = [list(range(last - pending + 1, last + 1))]
+        got = prod.cut_spans(spans, old_pos, [new_pos], [ends], pending, max_span)
+        want = ora.cut_spans(spans, old_pos, [new_pos], [ends], pending, max_span)
+        if want is None:
+            assert got is None
+            continue
+        (cands, all_pos, tokens, lengths), = want
+        assert got.candidates[0][0] == cands
+        assert got.candidates[0][1].tolist() == list(all_pos)
+        assert got.token_rows[0].tolist() == list(tokens) and got.length_rows[0] == list(lengths)
 
 
 def _random_pool(rng, rows, max_span):
