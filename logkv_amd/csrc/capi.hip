@@ -11,6 +11,8 @@
 #include "route.hpp"
 #include "unified.hpp"
 
+thread_local const char* logkv::g_refusal = nullptr;
+
 namespace {
 
 thread_local char g_error[512] = "";
@@ -22,6 +24,13 @@ int fail(int code, const char* fmt, ...) {
   vsnprintf(g_error, sizeof(g_error), fmt, args);
   va_end(args);
   return code;
+}
+
+// A launch function's failure: its refusal reason when it gave one, else the HIP error.
+int launch_failed(int rc, const char* what) {
+  const char* why = logkv::g_refusal;
+  logkv::g_refusal = nullptr;
+  return fail(rc, "%s launch failed: %s", what, why ? why : hipGetErrorString(hipGetLastError()));
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -284,7 +293,7 @@ int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* ro
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = rows->tokens ? logkv::launch_unified_plan(*cache, *rows, u, ws, s) : LOGKV_OK;
   if (!rc) rc = logkv::launch_unified_summary(*cache, u, summary, rows->tokens, s);
-  if (rc) return fail(rc, "unified plan launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "unified plan");
   return LOGKV_OK;
 }
 
@@ -304,7 +313,7 @@ int logkv_unified_commit(const logkv_ladder_view* cache, const logkv_rows_view* 
     if (!rc) rc = logkv::launch_levels(*cache, *rows, *params, ws, s);
   }
   if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
-  if (rc) return fail(rc, "unified commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "unified commit");
   return LOGKV_OK;
 }
 
@@ -321,7 +330,7 @@ int logkv_attach_assign(const logkv_ladder_view* cache, const logkv_rows_view* r
   if (rc) return rc;
   if (!rows->tokens) return LOGKV_OK;
   rc = logkv::launch_route(*cache, *rows, *params, ws, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "attach launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "attach");
   return LOGKV_OK;
 }
 
@@ -335,7 +344,7 @@ int logkv_route_commit(const logkv_ladder_view* cache, const logkv_rows_view* ro
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = logkv::launch_route(*cache, *rows, *params, ws, s);
   if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
-  if (rc) return fail(rc, "route/commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "route/commit");
   return LOGKV_OK;
 }
 
@@ -349,7 +358,7 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
   if (!rows->tokens) return LOGKV_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
-  if (rc) return fail(rc, "commit launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "commit");
   return LOGKV_OK;
 }
 
@@ -376,7 +385,7 @@ int logkv_record_ops(const logkv_ladder_view* cache, const logkv_rows_view* rows
   if ((rc = check_log(cache, log))) return rc;
   if (!rows->tokens) return LOGKV_OK;
   rc = logkv::launch_record(*cache, *rows, ws, *log, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "op-log record launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "op-log record");
   return LOGKV_OK;
 }
 
@@ -394,7 +403,7 @@ int logkv_replay_commit(const logkv_ladder_view* cache, const logkv_rows_view* r
   rc = logkv::launch_replay(*cache, *rows, ws, *log, cursor, status, s);
   ws.abort = status;
   if (!rc) rc = logkv::launch_commit(*cache, *rows, *params, ws, s);
-  if (rc) return fail(rc, "replay launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "replay");
   return LOGKV_OK;
 }
 
@@ -429,7 +438,7 @@ int logkv_unified_record_ops(const logkv_ladder_view* cache, const logkv_rows_vi
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = logkv::launch_record_wards(*cache, u.jobs, u.n_jobs, *log, s);
   if (!rc) rc = logkv::launch_record(*cache, *rows, ws, *log, s);
-  if (rc) return fail(rc, "op-log record launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "op-log record");
   return LOGKV_OK;
 }
 
@@ -446,7 +455,7 @@ int logkv_unified_replay_plan(const logkv_ladder_view* cache, const logkv_rows_v
   if (!rows->tokens) return LOGKV_OK;
   rc = logkv::launch_unified_replay(*cache, *rows, ws, *log, cursors, consumed, u.jobs, u.n_jobs, status,
                                     static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "replay launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "replay");
   return LOGKV_OK;
 }
 
@@ -490,7 +499,7 @@ int logkv_score_spans(const logkv_span_args* a, float* scores, void* stream) {
   if (a->beta_novelty && (!a->centroids || !a->centroid_valid || a->k_max < 1))
     return fail(LOGKV_EINVAL, "Beta novelty needs centroids and their valid flags");
   const int rc = logkv::launch_score(*a, scores, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "score launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "score");
   return LOGKV_OK;
 }
 
@@ -503,7 +512,7 @@ int logkv_alpha_partition(const logkv_partition_args* a, void* stream) {
       (a->A && (!a->arch_k || !a->arch_v || !a->arch_pos || !a->archive)))
     return fail(LOGKV_EINVAL, "partition outputs or index tables are NULL");
   const int rc = logkv::launch_partition(*a, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "partition launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "partition");
   return LOGKV_OK;
 }
 
@@ -540,7 +549,7 @@ int logkv_alpha_select(const logkv_alpha_select_args* a, void* ws, int64_t ws_by
   if (rc) return rc;
   if (!ws || ws_bytes < logkv::select_workspace_bytes(*a)) return fail(LOGKV_EINVAL, "selection workspace too small");
   rc = logkv::launch_select(*a, ws, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "selection launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "selection");
   return LOGKV_OK;
 }
 
@@ -572,7 +581,7 @@ int logkv_mid_plan(const logkv_readout_view* c, int32_t* table, void* stream) {
   if (rc) return rc;
   if (!table) return fail(LOGKV_EINVAL, "plan table is NULL");
   rc = logkv::launch_plan(*c, table, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "plan launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "plan");
   return LOGKV_OK;
 }
 
@@ -589,7 +598,7 @@ int logkv_pack(const logkv_readout_view* c, const logkv_pack_args* p, const int3
                      p->ck_sb % 4 || p->ck_sg % 4 || p->ck_st % 4 || p->cv_sb % 4 || p->cv_sg % 4 || p->cv_st % 4))
     return fail(LOGKV_EINVAL, "current rows must be 8-byte aligned (strides multiples of 4 elements)");
   rc = logkv::launch_pack(*c, *p, table, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "pack launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "pack");
   return LOGKV_OK;
 }
 
@@ -605,7 +614,7 @@ int logkv_decode_attention(const logkv_attention_args* a, const int32_t* table, 
   if (!ws || ws_bytes < logkv::attention_workspace_floats(*a) * 4)
     return fail(LOGKV_EINVAL, "attention workspace too small");
   rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(ws), static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "attention");
   return LOGKV_OK;
 }
 
@@ -622,7 +631,7 @@ int logkv_decode_attention_static(const logkv_attention_args* a, const int32_t* 
   if (rc) return rc;
   rc = logkv::launch_attention(*a, table + table_ints - 1, static_cast<float*>(scratch_ptr),
                                static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "attention");
   return LOGKV_OK;
 }
 
@@ -654,7 +663,7 @@ int logkv_chunk_attention(const logkv_attention_args* a, const int32_t* table, i
     return fail(LOGKV_EINVAL, "chunk attention workspace too small");
   const int rc = logkv::launch_chunk_attention(*a, table + table_ints - 1, static_cast<float*>(ws),
                                                static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "chunk attention launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "chunk attention");
   return LOGKV_OK;
 }
 
@@ -689,7 +698,7 @@ int logkv_recent_append(const logkv_recent_args* a, int32_t at, int32_t n, void*
       a->kr_sg % 4 || a->kr_st % 4 || a->v_sb % 4 || a->v_sg % 4 || a->v_st % 4)
     return fail(LOGKV_EINVAL, "append sources need 8-byte aligned rows (strides multiple of 4 elements)");
   rc = logkv::launch_recent_append(*a, at, n, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "recent append launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "recent append");
   return LOGKV_OK;
 }
 
@@ -700,7 +709,7 @@ int logkv_recent_shift(const logkv_recent_args* a, int32_t take, int32_t count, 
     return fail(LOGKV_EINVAL, "shift of %d of %d rows needs 1 <= take <= count <= cap and count - take <= take",
                 take, count);
   rc = logkv::launch_recent_shift(*a, take, count, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "recent shift launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "recent shift");
   return LOGKV_OK;
 }
 
@@ -720,7 +729,7 @@ int logkv_beta_merge(const logkv_beta_args* a, int32_t* status, void* stream) {
   if (a->out_k && (!a->out_v || !a->out_w)) return fail(LOGKV_EINVAL, "Beta merge outputs K, V and w go together");
   if (a->apply && !a->out_k) return fail(LOGKV_EINVAL, "applying recorded cuts needs the outputs");
   const int rc = logkv::launch_beta_merge(*a, status, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "Beta merge launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "Beta merge");
   return LOGKV_OK;
 }
 
@@ -740,7 +749,7 @@ int logkv_pack_slots(const logkv_slot_pack_args* a, void* stream) {
   if (reinterpret_cast<uintptr_t>(a->out_k) % 8 || reinterpret_cast<uintptr_t>(a->out_v) % 8)
     return fail(LOGKV_EINVAL, "packed rows must be 8-byte aligned");
   const int rc = logkv::launch_slot_pack(*a, static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "slot pack launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "slot pack");
   return LOGKV_OK;
 }
 
@@ -773,7 +782,7 @@ int logkv_chunk_attention_backward(const logkv_attention_args* a, const int32_t*
     return fail(LOGKV_EINVAL, "attention backward workspace too small");
   const int rc = logkv::launch_chunk_backward(*a, table + table_ints - 1, *gr, static_cast<float*>(ws),
                                               static_cast<hipStream_t>(stream));
-  if (rc) return fail(rc, "attention backward launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return launch_failed(rc, "attention backward");
   return LOGKV_OK;
 }
 

@@ -21,13 +21,25 @@
 
 namespace logkv {
 
+// Why a launch function refused before enqueueing anything (a host-side check
+// failed); the C ABI puts it in the text logkv_last_error returns. Defined in
+// capi.hip.
+extern thread_local const char* g_refusal;
+inline int refuse(const char* why) {
+  g_refusal = why;
+  return LOGKV_ERUNTIME;
+}
+
 // Lets kernel `fn` launch with `bytes` of dynamic LDS on the current device.
 // Above the 64 KiB default the limit is raised once per (kernel, device) and
 // remembered, so steady-state launches make no attribute call.
 inline bool allow_dynamic_lds(const void* fn, size_t bytes) {
   if (bytes <= 64 * 1024) return true;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    g_refusal = "no current HIP device";
+    return false;
+  }
   struct Limit {
     const void* fn;
     int dev;
@@ -40,8 +52,10 @@ inline bool allow_dynamic_lds(const void* fn, size_t bytes) {
   for (Limit& e : limits)
     if (e.fn == fn && e.dev == dev) hit = &e;
   if (hit && hit->bytes >= bytes) return true;
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess)
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess) {
+    g_refusal = "the device refused the kernel's dynamic LDS size";
     return false;
+  }
   if (hit) hit->bytes = bytes;
   else limits.push_back(Limit{fn, dev, bytes});
   return true;

@@ -945,8 +945,10 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
 template <bool LIMIT>
 int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
   if (!a.dist || !a.mu || !a.mass || !a.count || !a.image || !a.ctl || !a.live || !a.alive_out || !a.trace ||
-      !a.n_trace || !a.stuck || !a.bound || (LIMIT && !a.limit) || a.image_stride < static_cast<int64_t>(reduce_lds_bytes(a.M)))
-    return LOGKV_ERUNTIME;
+      !a.n_trace || !a.stuck || !a.bound || (LIMIT && !a.limit))
+    return refuse("unified reducer: a workspace buffer of the stage is NULL");
+  if (a.image_stride < static_cast<int64_t>(reduce_lds_bytes(a.M)))
+    return refuse("unified reducer: the per-lane state image is smaller than the reducer's LDS layout");
   const size_t lds = reduce_lds_bytes(a.M);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_plan_kernel<LIMIT>), lds) ||
       !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_finish_kernel<LIMIT>), lds))
