@@ -59,11 +59,9 @@ def _check_block(block):
             raise ValueError("Beta block fields must share one device")
         if f >= 8 and (x.dim() != 1 or x.size(0) != n):
             raise ValueError("Beta block metadata must be [rows]")
-    for x in (k, v):
-        if x.dtype not in (torch.bfloat16, torch.float32) or x.stride(-1) != 1:
-            raise ValueError("Beta payloads must be bfloat16 or float32 with contiguous features")
-    if w.dtype != torch.float32:
-        raise ValueError("Beta masses must be float32")
+    for x in (k, v, w):
+        if not x.dtype.is_floating_point:
+            raise ValueError("Beta payloads and masses must be floating point")
     for f in _META:
         if block[f] is not None and block[f].dtype != torch.int64:
             raise ValueError("Beta anchors and order must be int64")
@@ -75,8 +73,17 @@ def _contig(x):
     return None if x is None else x.contiguous()
 
 
+def _payload(x):
+    """K / V rows as the kernel reads them: bfloat16 or float32 with contiguous features; other
+    floating dtypes are upcast to float32 first, as the reference's ``.float()`` reads them
+    (exact for float16)."""
+    if x.dtype in (torch.bfloat16, torch.float32):
+        return x if x.stride(-1) == 1 else x.contiguous()
+    return x.float().contiguous()
+
+
 def _run(block, layout, cuts, apply, outputs):
-    k, v, w = block[0], block[1], block[2].contiguous()
+    k, v, w = _payload(block[0]), _payload(block[1]), block[2].float().contiguous()
     if layout.dtype != torch.int64 or layout.dim() != 2 or layout.size(1) != 3 or layout.device != k.device:
         raise ValueError("Beta layout must be int64 [groups, 3] on the block's device")
     layout = layout.contiguous()
@@ -90,12 +97,17 @@ def _run(block, layout, cuts, apply, outputs):
         k.size(0), k.size(1), v.size(1), ptr(layout), layout.size(0), ptr(cuts), int(apply))
     if outputs is not None:
         out = outputs
-        args.out_k, args.out_v, args.out_w = ptr(out[0]), ptr(out[1]), ptr(out[2])
+        args.out_k, args.out_v = ptr(out[0]), ptr(out[1])
+        # Side masses are summed in float32; a block of another mass dtype gets them cast below.
+        out_w = out[2] if out[2].dtype == torch.float32 else torch.empty_like(out[2], dtype=torch.float32)
+        args.out_w = ptr(out_w)
         args.out_p_lo, args.out_p_hi, args.out_sum_wp, args.out_order = (ptr(out[f]) for f in _META)
         args.out_pad = None if out[12] is None else out[12].view(torch.uint8).data_ptr()
     _lib.check(_lib.lib().logkv_beta_merge(C.byref(args), ptr(status), _lib.stream_of(k.device)), "logkv_beta_merge")
     if int(status.item()):
         raise ValueError("Beta layout or recorded cuts out of range for this block")
+    if outputs is not None and out_w is not outputs[2]:
+        outputs[2].copy_(out_w)
 
 
 def select_cuts(block, layout):

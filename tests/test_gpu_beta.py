@@ -119,3 +119,20 @@ def test_recorded_cuts_are_validated():
     bad_layout = torch.tensor([[2, 4, 0]], dtype=torch.int64, device=DEV)   # runs past the block
     with pytest.raises(ValueError):
         select_cuts(block, bad_layout)
+
+
+def test_other_float_dtypes_are_upcast():
+    """float16 payloads and bfloat16 masses are read as float32, as the reference's ``.float()``
+    reads them: the merge equals that of the same block upcast beforehand, and the merged masses
+    keep the block's mass dtype."""
+    g = torch.Generator().manual_seed(23)
+    lengths = [6, 4, 10]
+    base = _random_block(g, lengths, 64, 64, torch.float32)
+    half = (base[0].half(), base[1].half(), base[2].bfloat16()) + base[3:]
+    upcast = (half[0].float(), half[1].float(), half[2].float()) + base[3:]
+    out, cuts = merge_blocks(half, lengths)
+    want, want_cuts = merge_blocks(upcast, lengths)
+    assert torch.equal(cuts, want_cuts)
+    assert out[2].dtype == torch.bfloat16 and torch.equal(out[2], want[2].bfloat16())
+    for f in (0, 1, 8, 9, 10, 11, 12):
+        assert torch.equal(out[f], want[f]), f
