@@ -512,11 +512,13 @@ int logkv_decode_attention_static(const logkv_attention_args* args, const int32_
 /* The same attention for many query rows per KV group (a prefill or training
  * chunk), on the matrix cores (QK^T in bf16, PV in fp16 with P rounded to fp16,
  * fp32 accumulation): packed width <= 144, dv in {32, 64, 96, 128}. The
- * workspace (logkv_chunk_workspace_bytes, never 0) holds an fp16 copy of each
- * lane's V scaled by a power of two 2^-k that keeps it below 2^15 (P scaled by
- * 2^k; magnitudes of 2^30 and more overflow) and, when the key range is split
- * over several blocks per query tile to fill the GPU, their partials, combined
- * in split order.
+ * workspace (logkv_chunk_workspace_bytes, never 0) holds an exact fp16 copy of
+ * each lane's V scaled by a power of two 2^-k (any k: the output is scaled
+ * back by 2^k), made when the lane's nonzero magnitudes span at most 29
+ * binades; a lane beyond that, or holding an infinity, NaN or subnormal, reads
+ * its bf16 rows with P split into high and low bf16 parts instead. When the
+ * key range is split over several blocks per query tile to fill the GPU, the
+ * workspace also holds their partials, combined in split order.
  * Replaces the Flash SDPA call of _packed_flash_attention / _mid_chunk_attention
  * on a chunk (litgpt/log_kv_cache.py:6751-6758, :6802-6836). */
 int64_t logkv_chunk_workspace_bytes(const logkv_attention_args* args);

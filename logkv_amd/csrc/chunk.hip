@@ -11,12 +11,17 @@
 //   S^T = K Q^T   (keys x queries; each lane holds 16 keys of its own query),
 //   online softmax per lane (its query's max and sum, the other 16 keys of the
 //   32-key block in lane ^ 32),
-//   O^T += V^T P^T (dv x queries) with v_mfma_f32_32x32x16_f16: P in fp16
-//   (11 significant bits, RNE) against an fp16 copy of V made per launch, each
-//   lane's V scaled by 2^-k so its largest magnitude stays below 2^15 and P by
-//   2^k (k = 0 unless |V| >= 2^15; P 2^k <= 2^15; magnitudes of 2^30 and more
-//   overflow). fp16 P rounds P to 2^-11 relative, so an output errs by at most
-//   2^-11 of its values' weighted mean magnitude.
+//   O^T += V^T P^T (dv x queries) with v_mfma_f32_32x32x16_f16: P 2^15 in
+//   fp16 (11 significant bits, RNE) against an fp16 copy of V 2^-k made per
+//   launch, k chosen per lane so its largest magnitude lands in [2^15, 2^16);
+//   the copy is exact when the lane's nonzero magnitudes span at most 29
+//   binades (all land in fp16's normal range), and the output is scaled back
+//   by 2^(k - 15) after the division by the softmax sum, so any bf16 exponent
+//   works. fp16 P rounds P to 2^-11 relative, so an output errs by at most
+//   2^-11 of its values' weighted mean magnitude. A lane whose V spans more
+//   binades, or holds an infinity, NaN or subnormal, reads its bf16 V rows
+//   instead and splits P 2^15 into high and low bf16 parts (two products per
+//   step, P kept to about 2^-16).
 // Queries live in registers for the whole key range; the K / V tiles are
 // double-buffered in LDS with one barrier per tile.
 // The P^T operand is the lane's own score registers: MFMA B operand element j
@@ -49,6 +54,10 @@ constexpr int kLdK = 152;        // K tile row stride in LDS (bf16)
 constexpr int kLdV = kKeys + 4;  // V^T row stride in LDS (bf16; 34 dwords: 16 rows' 8-byte reads hit distinct banks)
 constexpr int kMaxDvBlocks = 4;  // dv <= 128
 constexpr int kVSlices = 64;     // row slices of a lane's V in the fp16 copy
+// vshift of a lane whose V has no exact fp16 copy (the bf16 path reads its rows).
+constexpr int kBf16Lane = 1 << 20;
+// P is scaled by 2^kPShift before its fp16 rounding (P <= 1, so P 2^15 < 65504).
+constexpr int kPShift = 15;
 
 __device__ __forceinline__ __bf16 to_bf16(float x) { return static_cast<__bf16>(x); }
 
@@ -73,11 +82,11 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // compile time (straight-line tile code); columns past the packed width and
 // V^T rows past dv are zero, so a kernel with more steps or blocks than the
 // shape needs gives the same result.
-template <int NKS, int NDV>
-__global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
-                                                       int splits, float* __restrict__ part,
-                                                       const uint16_t* __restrict__ v16,
-                                                       const int32_t* __restrict__ vshift) {
+// BF16V: the body of a lane without an exact fp16 V copy (vshift kBf16Lane).
+template <int NKS, int NDV, bool BF16V>
+__device__ __forceinline__ void chunk_body(const logkv_attention_args& a, const int32_t* __restrict__ width_ptr,
+                                           int splits, float* __restrict__ part, const uint16_t* __restrict__ v16,
+                                           int kv) {
   // Two K / V^T tile buffers: tile i + 1 is written into the other buffer while
   // tile i is read, so one barrier per tile orders both.
   __shared__ __align__(16) uint16_t k_s[2][kKeys * kLdK];
@@ -136,9 +145,10 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     for (int i = 0; i < 16; ++i) o[blk][i] = 0.f;
   float m = -__builtin_inff(), lsum = 0.f;   // running maximum of s * scale * log2(e), and the sum
   const LOGKV_G uint16_t* kbase = gp(a.k) + static_cast<int64_t>(lane_ix) * a.cap * dim;
-  const LOGKV_G uint16_t* vbase = gp(v16) + static_cast<int64_t>(lane_ix) * a.cap * a.dv;   // fp16 rows of dv
-  const int kv = vshift[lane_ix];
-  const float kvf = static_cast<float>(kv), inv_kv = __builtin_ldexpf(1.f, -kv);
+  // The lane's V source: its fp16 copy (V 2^-k), or its bf16 packed rows.
+  const LOGKV_G uint16_t* vbase = BF16V ? gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * dim
+                                        : gp(v16) + static_cast<int64_t>(lane_ix) * a.cap * a.dv;
+  const int vstride = BF16V ? dim : a.dv;
   const int units = dim / 8;
   const int vunits = a.dv / 8;
   // Each thread's staging tasks are the same in every tile: up to kKTasks
@@ -175,8 +185,8 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     for (int q = 0; q < kVTasks; ++q) {
       const int kp = v_pair[q] < 0 ? 0 : v_pair[q];
       const int r0 = min(2 * kp, rows - 1), r1 = min(2 * kp + 1, rows - 1);
-      vx[q][0] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r0) * a.dv + 8 * v_unit[q]);
-      vx[q][1] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r1) * a.dv + 8 * v_unit[q]);
+      vx[q][0] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r0) * vstride + 8 * v_unit[q]);
+      vx[q][1] = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(t0 + r1) * vstride + 8 * v_unit[q]);
       if (2 * kp >= rows) vx[q][0] = make_uint4(0, 0, 0, 0);
       if (2 * kp + 1 >= rows) vx[q][1] = make_uint4(0, 0, 0, 0);
     }
@@ -259,9 +269,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     const float m_new = fmaxf(m, mx * c2);
     const float mb = m_new == -__builtin_inff() ? 0.f : m_new;
     const float corr = __builtin_amdgcn_exp2f(m - mb);
-    // p' = 2^(s c2 - m + k) = P 2^k (the V copy carries 2^-k); the sum is
-    // taken of p' and scaled back by 2^-k (exact).
-    const float arg0 = kvf - mb;
+    // p' = 2^(s c2 - m + 15) = P 2^15; the sum is taken of p' and scaled
+    // back by 2^-15 (exact).
+    const float arg0 = static_cast<float>(kPShift) - mb;
     float sum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -272,7 +282,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
         sum += p;
       }
     }
-    sum = pair_sum32(sum) * inv_kv;
+    sum = pair_sum32(sum) * __builtin_ldexpf(1.f, -kPShift);
     lsum = lsum * corr + sum;
     m = m_new;
     if (__ballot(corr != 1.f)) {
@@ -281,7 +291,34 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[blk][i] *= corr;
     }
-    // O^T += V^T P^T, four 16-key steps, P rounded to fp16.
+    // O^T += V^T P^T, four 16-key steps, P rounded to fp16 (bf16 lanes: P as
+    // high + low bf16 parts against the bf16 V rows).
+    if constexpr (BF16V) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p0 = s[st / 2][8 * (st % 2) + 2 * j], p1 = s[st / 2][8 * (st % 2) + 2 * j + 1];
+          const uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
+          const float r0 = p0 - __uint_as_float(static_cast<uint32_t>(h0) << 16);
+          const float r1 = p1 - __uint_as_float(static_cast<uint32_t>(h1) << 16);
+          hw[j] = h0 | (static_cast<uint32_t>(h1) << 16);
+          lw[j] = f32_to_bf16(r0) | (static_cast<uint32_t>(f32_to_bf16(r1)) << 16);
+        }
+        const bf16x8 ph = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+        const bf16x8 pl = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+        for (int blk = 0; blk < NDV; ++blk) {
+          const uint16_t* vr = vt + (32 * blk + col) * kLdV + 16 * st + 4 * h;
+          const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
+          const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+          const bf16x8 vb = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+          o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, ph, o[blk], 0, 0, 0);
+          o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pl, o[blk], 0, 0, 0);
+        }
+      }
+    } else {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       f16x2 pw[4];
@@ -304,6 +341,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
       }
 #pragma unroll
       for (int blk = 0; blk < NDV; ++blk) o[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[blk], ph, o[blk], 0, 0, 0);
+    }
     }
     if (it + 1 < ntiles) {
       store_tile(bf ^ 1);
@@ -336,6 +374,8 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
     }
     return;
   }
+  // o holds 2^(15 - k) sum P V: divided by the sum, then scaled by 2^(k - 15) exactly.
+  const int oexp = (BF16V ? 0 : kv) - kPShift;
   LOGKV_G uint16_t* orow = gp(a.out) + b * a.o_sb + head * a.o_sh + t * a.o_st;
 #pragma unroll
   for (int blk = 0; blk < NDV; ++blk) {
@@ -343,22 +383,36 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int d = 32 * blk + 8 * i4 + 4 * h;
-        const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(o[blk][4 * i4] / lsum)) |
-                            (static_cast<uint32_t>(f32_to_bf16(o[blk][4 * i4 + 1] / lsum)) << 16);
-        const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(o[blk][4 * i4 + 2] / lsum)) |
-                            (static_cast<uint32_t>(f32_to_bf16(o[blk][4 * i4 + 3] / lsum)) << 16);
+        float y[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = __builtin_ldexpf(o[blk][4 * i4 + j] / lsum, oexp);
+        const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(y[0])) | (static_cast<uint32_t>(f32_to_bf16(y[1])) << 16);
+        const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(y[2])) | (static_cast<uint32_t>(f32_to_bf16(y[3])) << 16);
         *(LOGKV_G uint2*)(orow + d) = make_uint2(lo, hi);
       }
     }
   }
 }
 
+template <int NKS, int NDV>
+__global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
+                                                       int splits, float* __restrict__ part,
+                                                       const uint16_t* __restrict__ v16,
+                                                       const int32_t* __restrict__ vshift) {
+  const int kv = vshift[blockIdx.z];
+  if (kv == kBf16Lane) chunk_body<NKS, NDV, true>(a, width_ptr, splits, part, v16, kv);
+  else chunk_body<NKS, NDV, false>(a, width_ptr, splits, part, v16, kv);
+}
+
 // The fp16 copy of the packed V (rows [0, total) of every lane, dv features):
-// vmax_kernel takes the largest bf16 magnitude (as bits) of each of a lane's
-// kVSlices row slices; vconv_kernel reduces them to the lane's shift k (the
-// largest k in [0, 15] keeping |V| 2^-k below 2^15, 0 when |V| < 2^15 already)
-// and writes V 2^-k as fp16 (exact for normal values; bf16 has 8 significant
-// bits, fp16 11).
+// vmax_kernel takes the largest and the smallest nonzero bf16 magnitude (as
+// bits) of each of a lane's kVSlices row slices; vconv_kernel reduces them to
+// the lane's shift k = E_max - 15 (E_max the largest value's exponent, so the
+// largest scaled magnitude is in [2^15, 2^16) and at most 65280) and writes V
+// 2^-k as fp16 by moving the exponent field (exact: bf16 has 8 significant
+// bits, fp16 11, and every nonzero value lands in fp16's normal range when
+// E_max - E_min <= 29). Other lanes - wider spans, infinities, NaNs, bf16
+// subnormals - get vshift = kBf16Lane and no copy.
 __device__ __forceinline__ int chunk_rows(const logkv_attention_args& a, const int32_t* width_ptr) {
   return min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
 }
@@ -370,20 +424,33 @@ __global__ __launch_bounds__(256) void vmax_kernel(logkv_attention_args a, const
   const int per = (total + kVSlices - 1) / kVSlices, r0 = slice * per, r1 = min(total, r0 + per);
   const int units = a.dv / 8;
   const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * a.dim;
-  uint32_t mx = 0;
+  uint32_t mx = 0, mn = 0xffffu;   // largest magnitude, smallest nonzero one (0xffff: none)
   for (int i = threadIdx.x; i < (r1 - r0) * units; i += blockDim.x) {
     const int row = r0 + i / units, u = i % units;
     const uint4 x = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * a.dim + 8 * u);
     const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mx = max(mx, max(w[j] & 0x7fffu, (w[j] >> 16) & 0x7fffu));
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t m0 = w[j] & 0x7fffu, m1 = (w[j] >> 16) & 0x7fffu;
+      mx = max(mx, max(m0, m1));
+      mn = min(mn, min(m0 ? m0 : 0xffffu, m1 ? m1 : 0xffffu));
+    }
   }
-  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
-  __shared__ uint32_t red[4];
-  if (lane_id() == 0) red[wave_id()] = mx;
+  for (int off = 32; off >= 1; off >>= 1) {
+    mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
+    mn = min(mn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mn), off, 64)));
+  }
+  __shared__ uint32_t red[2][4];
+  if (lane_id() == 0) {
+    red[0][wave_id()] = mx;
+    red[1][wave_id()] = mn;
+  }
   __syncthreads();
-  if (threadIdx.x == 0)
-    vmax[lane_ix * kVSlices + slice] = static_cast<int32_t>(max(max(red[0], red[1]), max(red[2], red[3])));
+  if (threadIdx.x == 0) {
+    int32_t* out = vmax + 2 * (lane_ix * kVSlices + slice);
+    out[0] = static_cast<int32_t>(max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3])));
+    out[1] = static_cast<int32_t>(min(min(red[1][0], red[1][1]), min(red[1][2], red[1][3])));
+  }
 }
 
 __global__ __launch_bounds__(256) void vconv_kernel(logkv_attention_args a, const int32_t* __restrict__ width_ptr,
@@ -392,33 +459,43 @@ __global__ __launch_bounds__(256) void vconv_kernel(logkv_attention_args a, cons
   const int slice = blockIdx.x, lane_ix = blockIdx.y;
   __shared__ int shift_s;
   if (threadIdx.x < kWave) {
-    const int2 pair = *reinterpret_cast<const int2*>(vmax + lane_ix * kVSlices + 2 * threadIdx.x % kVSlices);
-    uint32_t mx = static_cast<uint32_t>(max(pair.x, pair.y));
-    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
+    const int4 pair = *reinterpret_cast<const int4*>(vmax + 2 * (lane_ix * kVSlices + 2 * threadIdx.x % kVSlices));
+    uint32_t mx = static_cast<uint32_t>(max(pair.x, pair.z)), mn = static_cast<uint32_t>(min(pair.y, pair.w));
+    for (int off = 32; off >= 1; off >>= 1) {
+      mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off, 64)));
+      mn = min(mn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mn), off, 64)));
+    }
     if (threadIdx.x == 0) {
-      // |V| < 2^(e + 1) with e the exponent of the largest magnitude.
-      const int e = static_cast<int>(mx >> 7) - 127;
-      shift_s = max(0, min(15, e - 14));
+      // Exponent fields (biased by 127): 0 is a subnormal, 255 an infinity or NaN.
+      const int emax = static_cast<int>(mx >> 7), emin = static_cast<int>(mn >> 7);
+      const bool exact = mx == 0 || (emax < 255 && emin >= 1 && emax - emin <= 29);
+      shift_s = exact ? (mx == 0 ? 0 : emax - 127 - 15) : kBf16Lane;
       if (slice == 0) vshift[lane_ix] = shift_s;
     }
   }
   __syncthreads();
-  const float scale = __builtin_ldexpf(1.f, -shift_s);
+  const int k = shift_s;
+  if (k == kBf16Lane) return;
   const int total = chunk_rows(a, width_ptr);
   const int per = (total + kVSlices - 1) / kVSlices, r0 = slice * per, r1 = min(total, r0 + per);
   const int units = a.dv / 8;
   const LOGKV_G uint16_t* vbase = gp(a.v) + static_cast<int64_t>(lane_ix) * a.cap * a.dim;
   uint16_t* obase = v16 + static_cast<int64_t>(lane_ix) * a.cap * a.dv;
+  // bf16 exponent field e (value 1.m 2^(e - 127)) -> fp16 field e - 127 - k + 15, in [1, 30] here.
+  const int ebias = 127 + k - 15;
+  auto conv = [&](uint32_t x) -> uint32_t {
+    const uint32_t mag = x & 0x7fffu;
+    const uint32_t h = mag ? ((static_cast<uint32_t>(static_cast<int>(mag >> 7) - ebias) << 10) | ((mag & 0x7fu) << 3))
+                           : 0u;
+    return h | ((x >> 15) << 15);
+  };
   for (int i = threadIdx.x; i < (r1 - r0) * units; i += blockDim.x) {
     const int row = r0 + i / units, u = i % units;
     const uint4 x = *(const LOGKV_G uint4*)(vbase + static_cast<int64_t>(row) * a.dim + 8 * u);
     const uint32_t w[4] = {x.x, x.y, x.z, x.w};
     uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f32x2 f = {__uint_as_float(w[j] << 16) * scale, __uint_as_float(w[j] & 0xffff0000u) * scale};
-      o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
-    }
+    for (int j = 0; j < 4; ++j) o[j] = conv(w[j] & 0xffffu) | (conv(w[j] >> 16) << 16);
     *reinterpret_cast<uint4*>(obase + static_cast<int64_t>(row) * a.dv + 8 * u) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
@@ -429,7 +506,7 @@ __global__ __launch_bounds__(256) void vconv_kernel(logkv_attention_args a, cons
 // 2^(m_split - m).
 constexpr int kCombineQueries = 8;
 __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args a, const float* __restrict__ part,
-                                                            int splits) {
+                                                            int splits, const int32_t* __restrict__ vshift) {
   const int lane_ix = blockIdx.y, G = a.n_groups;
   const int b = lane_ix / G, g = lane_ix % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
@@ -451,11 +528,14 @@ __global__ __launch_bounds__(256) void chunk_combine_kernel(logkv_attention_args
     for (int j = 0; j < 4; ++j) acc[j] += pp[2 + d + j] * f;
   }
   const int head = g * rep + qi / a.tq, t = qi % a.tq;
+  // Partials hold 2^(15 - k) sum P V (see chunk_kernel's output).
+  const int kv = vshift[lane_ix], oexp = (kv == kBf16Lane ? 0 : kv) - kPShift;
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = __builtin_ldexpf(acc[j] / lsum, oexp);
   LOGKV_G uint16_t* o = gp(a.out) + b * a.o_sb + head * a.o_sh + t * a.o_st + d;
-  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[0] / lsum)) |
-                      (static_cast<uint32_t>(f32_to_bf16(acc[1] / lsum)) << 16);
-  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[2] / lsum)) |
-                      (static_cast<uint32_t>(f32_to_bf16(acc[3] / lsum)) << 16);
+  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(y[0])) | (static_cast<uint32_t>(f32_to_bf16(y[1])) << 16);
+  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(y[2])) | (static_cast<uint32_t>(f32_to_bf16(y[3])) << 16);
   *reinterpret_cast<LOGKV_G uint2*>(o) = make_uint2(lo, hi);
 }
 
@@ -471,7 +551,8 @@ int chunk_splits(const logkv_attention_args& a) {
 }
 
 // Workspace: [partials of the key-range splits (splits > 1)] [vmax: lanes x
-// kVSlices] [vshift: lanes] [fp16 V: lanes x cap x dv], regions 256-byte aligned.
+// kVSlices x 2] [vshift: lanes] [fp16 V: lanes x cap x dv], regions 256-byte
+// aligned.
 struct ChunkWs {
   float* part;
   int32_t* vmax;
@@ -492,7 +573,7 @@ static ChunkWs chunk_ws(const logkv_attention_args& a, void* base) {
   w.part = splits > 1 && b ? reinterpret_cast<float*>(b + off) : nullptr;
   if (splits > 1) off += align256(lanes * splits * nq * (a.dv + 2) * 4);
   w.vmax = b ? reinterpret_cast<int32_t*>(b + off) : nullptr;
-  off += align256(lanes * kVSlices * 4);
+  off += align256(lanes * kVSlices * 2 * 4);
   w.vshift = b ? reinterpret_cast<int32_t*>(b + off) : nullptr;
   off += align256(lanes * 4);
   w.v16 = b ? reinterpret_cast<uint16_t*>(b + off) : nullptr;
@@ -521,7 +602,7 @@ int launch_chunk_attention(const logkv_attention_args& a, const int32_t* width, 
                        w.part, w.v16, w.vshift);
   if (splits > 1)
     hipLaunchKernelGGL(chunk_combine_kernel, dim3((nq + kCombineQueries - 1) / kCombineQueries, a.n_batch * a.n_groups),
-                       dim3(256), 0, stream, a, w.part, splits);
+                       dim3(256), 0, stream, a, w.part, splits, w.vshift);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

@@ -258,3 +258,43 @@ def test_matrix_core_chunk_attention_alpha_pool():
     k, v = rand_bf16(g, 2, 2, 96, 64), rand_bf16(g, 2, 2, 96, 64)
     cos, sin = gpu.cos_cache.cpu(), gpu.sin_cache.cpu()
     check_step(gpu, cos, sin, q, k, v, 64 ** -0.5)
+
+
+@pytest.mark.parametrize("max_seq", [4096, 65536])   # one key range per query block, and key-range splits
+def test_chunk_attention_any_value_magnitude(max_seq):
+    """The matrix-core chunk attention over values of any bf16 magnitude: lanes scaled by 1e10,
+    by 1e-30 and by 1, and a lane whose first half of the features is scaled by 1e10 and second
+    half by 1e-30 (a span no single fp16 scale covers, so that lane reads its bf16 rows). Attention
+    is linear in V, so each output feature must be within 2e-3 of the float64 oracle relative to
+    max(its column's scale, |ref|), beyond the output's bf16 rounding."""
+    print(f"case value magnitudes max_seq={max_seq}", flush=True)
+    dk, heads, groups, tq = 128, 8, 4, 200
+    cos, sin = rope_tables(max_seq, dk)
+    cache = LogStructuredKVCache(
+        (1, groups, max_seq, dk), (1, groups, max_seq, dk), B=32, recent_size=256, device="cuda",
+        dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=4, semantic_flush_granularity=256,
+        semantic_anchor_mode="mid", allocate_second_order=False, cos_cache=cos, sin_cache=sin, rope_n_elem=dk)
+    fill_readout_state(cache, seed=21, recent=200)
+    col = torch.ones(groups, dk, dtype=torch.float64)
+    col[0], col[1] = 1e10, 1e-30
+    col[3, : dk // 2], col[3, dk // 2:] = 1e10, 1e-30
+    scale_v = col.to(torch.float32).view(1, groups, 1, 1, 1, dk).to(cache.level_v.device)
+    cache.level_v.copy_((cache.level_v.float() * scale_v).to(torch.bfloat16))
+    rscale = scale_v.view(1, groups, 1, dk)
+    cache.recent_v.copy_((cache.recent_v.float() * rscale).to(torch.bfloat16))
+    g = torch.Generator().manual_seed(8)
+    q = rand_bf16(g, 1, heads, tq, dk)
+    k = rand_bf16(g, 1, groups, tq, dk)
+    v = (torch.randn(1, groups, tq, dk, generator=g) * rscale.cpu()).to(torch.bfloat16)
+    state = state_of(cache)
+    ka_ref, va_ref = ro.pack(state, to_np(k), to_np(v), to_np(cos), to_np(sin))
+    dev = cache.level_k.device
+    with torch.no_grad():
+        out = log_kv_chunk_attention(cache, q.to(dev), k.to(dev), v.to(dev), dk ** -0.5, second_order_scale=0.0)
+    ref = ro.attention(to_np(q), ka_ref, va_ref, dk ** -0.5, tq, dk)
+    got = to_np(out).astype(np.float64)
+    assert np.isfinite(got).all()
+    rep = heads // groups
+    colscale = np.repeat(col.numpy(), rep, axis=0)[None, :, None, :]      # [1, heads, 1, dk]
+    err = (np.abs(got - ref) - half_ulp_bf16(ref)) / np.maximum(colscale, np.abs(ref))
+    assert err.max() <= ATOL, f"error beyond output rounding {err.max():.3e} > {ATOL}"
