@@ -690,7 +690,10 @@ def decode_workload(args, torch, np):
     row_bytes = 2 * (D + 1) + 2 * D
     attn_bytes = lanes * rows * row_bytes + Bt * HQ * D * 2 * 2
     achieved = gbs(attn_bytes, attn_ms)
+    # The packed rows the attention read, for the CPU baseline's slot attention over the same state.
+    cpu_state = (q_s.cpu(), ka[:, :, :rows].float().cpu(), va[:, :, :rows].float().cpu(), scale)
     return {
+        "_cpu_state": cpu_state,
         "workload": "decode, one layer, batch 8, Qwen3-1.7B GQA (16 q / 8 KV heads x 128, bf16), 32K-token cache: "
                     f"recent window ending at {F} rows, exact pool {EXACT}, 12 clusters holding {archived} archived "
                     "tokens per lane, masses ~ U(1,64); ms_per_token = wall time per token through "
@@ -844,6 +847,8 @@ def unified_workload(args, torch, np):
     stream = torch.cuda.current_stream(dev)
     times = []
     t_all = 0.0
+    reducer = np.zeros(4)   # summed over the timed flushes: dist, scan, Lance-Williams bytes; merges
+    rounds = []
     for i in range(flushes):
         k, v = mix.rows(T).to(dev), mix.rows(T).to(dev)
         pos = torch.arange(i * T, (i + 1) * T, device=dev).unsqueeze(0).expand(Bt, -1).contiguous()
@@ -857,17 +862,52 @@ def unified_workload(args, torch, np):
         if i >= warm:
             t_all += time.perf_counter() - t0
             times.append(ev[0].elapsed_time(ev[1]))
+            reducer += unified_reducer_bytes(cache.unified_reduce_stats(T).numpy())
+            rounds.append(int(cache.unified_reduce_stats(T)[:, 0, 1].max()))
     timed = flushes - warm
     ms = t_all / timed * 1e3
+    dev_ms = float(np.mean(times))
+    per_flush = reducer / timed
+    alg = float(per_flush[:3].sum())
+    achieved = gbs(alg, dev_ms)
     progress(f"unified route: {timed} timed flushes, {ms:.1f} ms per flush")
     return {
         "workload": "unified Ward / radius route control, Qwen3-1.7B KV shape (8 x 128 bf16), batch 4, "
                     f"recent = flush = {T}, {stream_tokens}-token stream ({flushes} flush events), 12-Gaussian "
                     f"mixture drifting every 16K tokens, K={K}, B={B}, L={cache.L_alloc}, s_h={s_h}",
         "flushed_tokens_per_s": Bt * T / (ms * 1e-3), "ms_per_flush": ms,
-        "device_ms_per_flush": float(np.mean(times)), "timed_flushes": timed, "warmup_flushes": warm,
+        "device_ms_per_flush": dev_ms, "timed_flushes": timed, "warmup_flushes": warm,
         "live_clusters_per_lane": float(cache.alive.float().sum(-1).mean()),
+        "radius_stage_rounds_max": max(rounds), "merges_per_flush": float(per_flush[3]),
+        "roofline": {"kernel": "whole unified flush: order, load nodes, distances, radius-stage and budget-stage "
+                               "reducer rounds (plan / Lance-Williams / rescan / finish), labels, stage 2, final, "
+                               "old-old merges, commit",
+                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": alg,
+                     "bytes_by_phase": {"distances": float(per_flush[0]), "scans": float(per_flush[1]),
+                                        "lance_williams": float(per_flush[2])},
+                     "avg_launch_ms": dev_ms,
+                     "byte_model": "reducer distance-matrix traffic only (the commit's bytes are not counted): "
+                                   "per lane and stage n^2 x 4 B written by the distance pass, 4 B per rescanned "
+                                   "element (rescanned rows x live columns, the first scan n x n) and 16 B per "
+                                   "Lance-Williams element (kept rows x live columns: both parents' entries read, "
+                                   "the row and its mirror written), from the device reducer's counts",
+                     "timing": "HIP events around each timed flush on its stream"},
     }
+
+
+def unified_reducer_bytes(stats):
+    """Algorithmic bytes of one unified flush's reducer from its per-lane, per-stage counts
+    ``[lanes, 2, 8]`` (nodes, rounds, merges, Lance-Williams elements, rescanned elements): the
+    distance pass writes n^2 f32 per stage, a rescan reads 4 B per element, a Lance-Williams update
+    reads both parents' entries and writes the row and its mirror (16 B per element). Returns
+    (distance, scan, Lance-Williams bytes, merges)."""
+    import numpy as np
+
+    n = stats[..., 0].astype(np.float64)
+    return np.array([float((n * n * 4).sum()), float(stats[..., 4].astype(np.float64).sum() * 4),
+                     float(stats[..., 3].astype(np.float64).sum() * 16), float(stats[..., 2].sum())])
 
 
 # ----------------------------------------------------------------------
@@ -948,7 +988,57 @@ def _cpu_config1(threads, reps=5):
             "clusters_alive_after": int(cache.alive.sum())}
 
 
-def cpu_baseline(seconds: float):
+def _cpu_decode(state, seconds, threads):
+    """Decode attention on the host: the Torch-CPU slot attention (oracle/torch_cpu.py, the reference's
+    SDPA over the Flash encoding, float32) over the packed rows the GPU's step read, one query per
+    head for batch 8 x 16 heads; (ms per token per layer, steps timed)."""
+    import torch
+
+    from oracle.torch_cpu import slot_attention
+
+    torch.set_num_threads(threads)
+    q, ka, va, scale = state
+    slot_attention(q, ka, va, scale, D)
+    n, t = 0, 0.0
+    while t < seconds or n < 3:
+        t0 = time.perf_counter()
+        slot_attention(q, ka, va, scale, D)
+        t += time.perf_counter() - t0
+        n += 1
+    return t / n * 1e3, n
+
+
+def _cpu_unified(threads, lanes, timed, warm):
+    """The unified route's flush on the host for ``lanes`` sampled lanes (the first KV groups of batch
+    row 0 of the GPU leg's stream, same generator and seed): the Torch-CPU reducer with the
+    reference's Gram distances above 32 nodes and the batched commit (oracle/torch_cpu.py); flushes
+    1..warm untimed, the next ``timed`` timed; (seconds per flush of the sampled lanes, flushes)."""
+    import numpy as np
+    import torch
+
+    from oracle.torch_cpu import TorchCpuCache
+    from workloads import Mixture, rope_tables
+
+    torch.set_num_threads(threads)
+    Bt, T, stream_tokens = 4, 4096, 131072
+    cos, sin = (t.numpy() for t in rope_tables(stream_tokens, D))
+    cache = TorchCpuCache(1, lanes, stream_tokens, D, D, B=B, recent_size=T, K=K, s_h=64.0, flush=T, cos=cos,
+                          sin=sin, unified=True)
+    cache.gram_distances = True
+    mix = Mixture(Bt, G, D, clusters=12, seed=31, drift_every=2 * 16384)
+    total = 0.0
+    for i in range(warm + timed):
+        k, v = mix.rows(T), mix.rows(T)
+        k, v = k[:1, :lanes].float().numpy(), v[:1, :lanes].float().numpy()
+        pos = np.arange(i * T, (i + 1) * T)[None]
+        t0 = time.perf_counter()
+        cache.flush_rows(k, v, pos)
+        if i >= warm:
+            total += time.perf_counter() - t0
+    return total / timed, timed
+
+
+def cpu_baseline(seconds: float, decode_state=None, unified=False):
     """The CPU baseline: the batched Torch-CPU port of the flush (oracle/torch_cpu.py, every ladder of
     a flush appended level by level, Beta groups as tensor operations, bit-identical to the oracle) on
     the host cores: the headline flush of one layer (Alpha / Beta, route, commit and the pack of the
@@ -964,8 +1054,34 @@ def cpu_baseline(seconds: float):
     one_rate, one_n, one_t = _cpu_stream_flushes(TorchCpuCache, seconds * 0.3, 1)
     ora_rate, ora_n, ora_t = _cpu_stream_flushes(OracleCache, seconds * 0.2, 1)
     config1 = _cpu_config1(cores)
+    config1["1_thread"] = _cpu_config1(1)
+    legs = {}
+    if decode_state is not None:
+        ms_all, n_all = _cpu_decode(decode_state, seconds * 0.1, cores)
+        ms_one, n_one = _cpu_decode(decode_state, seconds * 0.1, 1)
+        rows = decode_state[1].shape[2]
+        legs["decode"] = {
+            "value": ms_all, "unit": "ms per token per layer", "cores": cores, "kind": "port",
+            "value_1_thread": ms_one, "higher_is_better": False,
+            "sample": f"Torch-CPU slot attention (scaled_dot_product_attention over the packed Flash encoding, "
+                      f"float32) of one decode step: batch 8 x 16 query heads over the GPU step's {rows} packed "
+                      f"rows per lane; {n_all} steps on {cores} threads, {n_one} on 1 thread"}
+    if unified:
+        lanes_all, lanes_one, flush_tokens, all_lanes = 2, 1, 4 * 4096, 4 * G
+        s_all, n_all = _cpu_unified(cores, lanes_all, timed=2, warm=1)
+        s_one, n_one = _cpu_unified(1, lanes_one, timed=1, warm=1)
+        legs["unified"] = {
+            "value": flush_tokens / (s_all * all_lanes / lanes_all), "unit": "flushed tokens/s", "cores": cores,
+            "kind": "port", "value_1_thread": flush_tokens / (s_one * all_lanes / lanes_one),
+            "seconds_per_flush_sampled_lanes": s_all, "seconds_per_flush_sampled_lanes_1_thread": s_one,
+            "sample": f"Torch-CPU unified route (the reducer restated on torch tensors with the reference's Gram "
+                      f"distances, then the batched commit) of {lanes_all} of the {all_lanes} lanes (KV groups of "
+                      f"batch row 0, same stream) for flushes 2..{1 + n_all} on {cores} threads and {lanes_one} lane "
+                      f"for flush 2 on 1 thread; flushed tokens/s = 4 x 4096 / (seconds per flush x "
+                      f"{all_lanes} / sampled lanes), lanes being independent"}
+    torch.set_num_threads(cores)
     threads = torch.get_num_threads()
-    return {"value": all_rate, "unit": "flushed tokens/s", "cores": cores, "kind": "port",
+    return {"legs": legs, "value": all_rate, "unit": "flushed tokens/s", "cores": cores, "kind": "port",
             "value_1_thread": one_rate, "oracle_1_thread": ora_rate, "config1": config1,
             "host_cpu": model, "host_cores_available": cores, "torch_threads": threads,
             "sample": f"batched Torch-CPU port: Alpha/Beta + route + commit + pack of {all_n} flushes of one layer "
@@ -1158,7 +1274,9 @@ def main():
     if args.only:
         legs = {"config1": config1_workload, "decode": decode_workload, "prefill": prefill_workload,
                 "unified": unified_workload}
-        print(json.dumps(legs[args.only](args, torch, np)), flush=True)
+        out = legs[args.only](args, torch, np)
+        out.pop("_cpu_state", None)
+        print(json.dumps(out), flush=True)
         return
     if args.profile_flush:
         args.flush_passes = "stacked"
@@ -1183,18 +1301,53 @@ def main():
     if not args.profile_flush:
         if not args.no_config1:
             run_leg(result, "config1", config1_workload, args, torch, np)
+        decode_state = None
         if not args.no_decode:
             run_leg(result, "decode", decode_workload, args, torch, np)
+            decode_state = result["decode"].pop("_cpu_state", None)
             if "ms_per_token" in result["decode"]:
                 result["decode_ms_per_token"] = result["decode"]["ms_per_token"]
         if not args.no_prefill and args.flush_passes == "all":
             run_leg(result, "prefill", prefill_workload, args, torch, np)
         if not args.no_unified and args.flush_passes == "all":
             run_leg(result, "unified", unified_workload, args, torch, np)
+        run_leg(result, "hbm_copy", copy_peak, torch)
+        if "gbs" in result["hbm_copy"]:
+            result["hbm_copy_peak_gbs"] = result["hbm_copy"]["gbs"]
+            for leg in (result, result.get("decode", {}), result.get("unified", {})):
+                roof = leg.get("roofline") if isinstance(leg, dict) else None
+                if roof and roof.get("unit") == "GB/s":
+                    roof["frac_of_copy_peak"] = roof["achieved"] / result["hbm_copy_peak_gbs"]
         if not args.no_cpu_baseline:
             progress("cpu baseline: oracle flushes on the host")
-            run_leg(result, "cpu_baseline", cpu_baseline, args.cpu_seconds)
+            run_leg(result, "cpu_baseline", cpu_baseline, args.cpu_seconds, decode_state,
+                    "flushed_tokens_per_s" in result.get("unified", {}))
+            for name, leg in result["cpu_baseline"].pop("legs", {}).items():
+                if isinstance(result.get(name), dict):
+                    result[name]["cpu_baseline"] = leg
     print(json.dumps(result), flush=True)
+
+
+def copy_peak(torch, mib=1024, reps=10):
+    """A plain device-to-device copy of ``mib`` MiB timed with HIP events: the measured HBM ceiling
+    (bytes read + bytes written per second) beside the 8 TB/s vendor figure."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    del src, dst
+    return {"gbs": 2 * n / ms * 1e-6, "bytes_per_copy": 2 * n, "ms_per_copy": ms,
+            "how": f"{mib} MiB device-to-device copies (read + write bytes), mean of {reps} after 2 warm-up"}
 
 
 if __name__ == "__main__":

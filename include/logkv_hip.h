@@ -116,6 +116,15 @@ int logkv_commit_only(const logkv_ladder_view* cache, const logkv_rows_view* row
  * At most T + K <= 4608 per flush. */
 int64_t logkv_unified_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins);
 
+/* Byte offset, in that workspace, of the reducer's counts of the last
+ * logkv_unified_plan: int32 [lanes, 2 stages, 8] = nodes, rounds, merges,
+ * Lance-Williams elements (sum of kept rows x live columns over the rounds),
+ * rescanned elements (sum of rescanned rows x live columns, the first scan
+ * n x n), stuck flag, 0, 0; valid once the plan has run on the stream. -1 for
+ * an invalid layout. No counterpart in the reference: the counts are the
+ * roofline's byte model of the reducer (measurement only). */
+int64_t logkv_unified_stats_offset(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins);
+
 /* The decisions of one unified-routed flush, per lane (batch row, KV group):
  * the valid rows merge into candidates by mutual-nearest Ward rounds under
  * the radius limit limits[lane] (f32 [lanes] = sqrt(lambda * s_h)), then old

@@ -186,6 +186,7 @@ SIGNATURES = {
     "logkv_commit_only": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams),
                                  _p, _i64, _p, _p, _p]),
     "logkv_unified_workspace_bytes": (_i64, [C.POINTER(LadderView), _i32, _i32]),
+    "logkv_unified_stats_offset": (_i64, [C.POINTER(LadderView), _i32, _i32]),
     "logkv_unified_plan": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p, _p, _i64,
                                   _p, _p]),
     "logkv_unified_commit": (_i32, [C.POINTER(LadderView), C.POINTER(RowsView), C.POINTER(RouteParams), _p, _i64,

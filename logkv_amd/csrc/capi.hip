@@ -158,7 +158,7 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
 // The unified route's region, after the route workspace sized for old-old
 // merges. With base == NULL only the size is computed.
 int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late, uint8_t* base,
-                       logkv::UnifiedBufs* u) {
+                       logkv::UnifiedBufs* u, int64_t* stats_offset = nullptr) {
   const int64_t lanes = int64_t(c->n_batch) * c->n_groups;
   const int64_t M = int64_t(tokens) + c->k_max, D = c->dk;
   int64_t off = align256(plan_for(c, tokens, late, 1).total);
@@ -198,6 +198,8 @@ int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late,
   b.image = take(lanes * b.image_stride);
   b.ctl = reinterpret_cast<logkv::LaneCtl*>(take(lanes * static_cast<int64_t>(sizeof(logkv::LaneCtl))));
   b.live = reinterpret_cast<int16_t*>(take(lanes * M * 6));
+  if (stats_offset) *stats_offset = off;
+  b.stats = reinterpret_cast<int32_t*>(take(lanes * 2 * logkv::kStatsInts * 4));
   if (u) *u = b;
   return off;
 }
@@ -274,6 +276,13 @@ const char* logkv_last_error(void) { return g_error; }
 int64_t logkv_unified_workspace_bytes(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins) {
   if (check_ladder(cache) || tokens < 0) return -1;
   return unified_layout(cache, tokens, late_joins ? 1 : 0, nullptr, nullptr);
+}
+
+int64_t logkv_unified_stats_offset(const logkv_ladder_view* cache, int32_t tokens, int32_t late_joins) {
+  if (check_ladder(cache) || tokens < 0) return -1;
+  int64_t at = -1;
+  unified_layout(cache, tokens, late_joins ? 1 : 0, nullptr, nullptr, &at);
+  return at;
 }
 
 int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,

@@ -610,6 +610,7 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_init_kernel(ReduceArgs a
     c.work = c.active;
     c.n_live = n;
     c.n_dirty = n;
+    c.scan_elems = c.active ? n * n : 0;   // the first scan runs only for an active stage
     a.ctl[lane] = c;
   }
 }
@@ -711,6 +712,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
     ctl.rounds += 1;
     ctl.n_live = s_live;
     ctl.n_dirty = s_dirty;
+    ctl.lw_elems += n_ok * s_live;
+    ctl.scan_elems += s_dirty * s_live;
     if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
     a.ctl[lane] = ctl;
   }
@@ -889,7 +892,7 @@ __global__ __launch_bounds__(kPhaseThreads) void reduce_rescan_kernel(ReduceArgs
 template <bool LIMIT>
 __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArgs a) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  __shared__ int sh[2], s_nprop, s_nvalid;
+  __shared__ int sh[2], s_nprop, s_nvalid, s_rescans;
   const int lane = blockIdx.x, M = a.M, t = threadIdx.x, l = lane_id(), w = wave_id();
   const int n = a.count[lane];
   LaneCtl ctl = a.ctl[lane];
@@ -908,6 +911,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
   while (ctl.active) {
     int nprop, n_ok;
     plan_phase<LIMIT>(s, a, lane, n, limit, sh, &s_nprop, &s_nvalid, nprop, n_ok);
+    if (t == 0) s_rescans = 0;
     for (int p = w; p < n_ok; p += kReduceWaves) {
       const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, 0, n, limit);
       if (l == 0) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = rmin;
@@ -916,11 +920,16 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
     for (int r = w; r < n; r += kReduceWaves) {
       if (!is_dirty(s, r)) continue;
       const uint64_t k = scan_row<LIMIT>(s, dist, M, n, r, limit);
-      if (l == 0) s.packed[r] = k;
+      if (l == 0) {
+        s.packed[r] = k;
+        atomicAdd(&s_rescans, 1);
+      }
     }
     __syncthreads();
     const int count = ctl.count - n_ok;
     const bool remaining = count > a.target;
+    ctl.lw_elems += n_ok * count;
+    ctl.scan_elems += s_rescans * count;
     ctl.count = count;
     ctl.ntrace += n_ok;
     ctl.stuck = remaining && nprop == 0 ? 1 : 0;
@@ -938,6 +947,15 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
   if (t == 0) {
     a.n_trace[lane] = ctl.ntrace;
     a.stuck[lane] = ctl.stuck;
+    if (a.stats) {
+      int32_t* st = a.stats + static_cast<int64_t>(lane) * a.stats_stride;
+      st[0] = n;
+      st[1] = ctl.rounds;
+      st[2] = ctl.ntrace;
+      st[3] = ctl.lw_elems;
+      st[4] = ctl.scan_elems;
+      st[5] = ctl.stuck;
+    }
   }
 }
 
@@ -1144,7 +1162,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
                      c.n_groups, u);
   if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
-                u.image, u.image_stride, u.ctl, u.live};
+                u.image, u.image_stride, u.ctl, u.live, u.stats, 2 * kStatsInts};
   if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
   const size_t lab_lds = static_cast<size_t>(M) * 8;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
@@ -1154,7 +1172,8 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
   if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
-                u.bound, u.image, u.image_stride, u.ctl, u.live};
+                u.bound, u.image, u.image_stride, u.ctl, u.live, u.stats ? u.stats + kStatsInts : nullptr,
+                2 * kStatsInts};
   if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
                      M, u.label2, u.n_roots2);

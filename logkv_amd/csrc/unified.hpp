@@ -20,8 +20,13 @@ struct LaneCtl {
   int32_t rounds;   // rounds run
   int32_t n_live;   // live rows after the current round's merges
   int32_t n_dirty;  // rows to rescan after the current round's merges
-  int32_t pad[2];
+  int32_t lw_elems;    // sum over rounds of kept rows x live columns (Lance-Williams elements)
+  int32_t scan_elems;  // sum over scans of rescanned rows x live columns (the first scan: n x n)
 };
+
+// Per lane and stage, what the stage's finish writes when ReduceArgs::stats is set:
+// nodes, rounds, merges, Lance-Williams elements, rescanned elements, stuck.
+constexpr int kStatsInts = 8;
 
 // Arguments of one reducer stage over `lanes` lanes of M padded nodes.
 struct ReduceArgs {
@@ -42,6 +47,8 @@ struct ReduceArgs {
   LaneCtl* ctl;           // [lanes]
   int16_t* live;          // [lanes, 3, M] the round's live rows (ctl.n_live), rows to rescan
                           // (ctl.n_dirty) and kept rows (ctl.n_ok), each list ascending
+  int32_t* stats;         // [lanes, stats_stride] the stage's counts (kStatsInts), or NULL
+  int32_t stats_stride;
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -76,6 +83,7 @@ struct UnifiedBufs {
   int64_t image_stride;
   LaneCtl* ctl;           // [lanes]
   int16_t* live;          // [lanes, 3, M]
+  int32_t* stats;         // [lanes, 2, kStatsInts] each stage's counts
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,

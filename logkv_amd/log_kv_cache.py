@@ -546,6 +546,20 @@ class LogStructuredKVCache(nn.Module):
                   "logkv_unified_record_ops")
         return merges
 
+    def unified_reduce_stats(self, tokens: int) -> torch.Tensor:
+        """The reducer's counts of the last unified flush of ``tokens`` rows, int32 ``[Bt * G, 2, 8]`` on
+        the host (one synchronisation): per lane and stage (radius candidates, cluster budget) its
+        nodes, rounds, merges, Lance-Williams elements (kept rows x live columns, summed over the
+        rounds), rescanned elements (rescanned rows x live columns, the first scan n x n) and stuck
+        flag. Measurement only."""
+        self._await_flush()
+        view = self._ladder_view()
+        at = lib().logkv_unified_stats_offset(C.byref(view), int(tokens), self._params.late_joins)
+        lanes = self.batch_size * self.n_groups
+        if at < 0 or self._workspace is None or self._workspace.numel() < at + lanes * 64:
+            raise ValueError("no unified flush of this length has run on this cache")
+        return self._workspace[at:at + lanes * 64].view(torch.int32).reshape(lanes, 2, 8).cpu()
+
     def _unified_commit_only(self, k_raw, v, positions, counts, assign, order, merges):
         """A recorded unified flush applied from its decisions and old-old merges."""
         view, rows, ws = self._unified_workspace(k_raw, v, positions, counts)

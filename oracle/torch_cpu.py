@@ -18,6 +18,13 @@ selection and attach decisions):
 * Beta cut costs and merges as torch float32 tensor operations over all groups at once, in the
   oracle's canonical orders, so every state field stays bit-identical to the oracle's (checked by
   tests/test_torch_cpu.py); torch's intra-op threads parallelise the large operations.
+
+The unified (Ward / radius) route's reducer (litgpt/log_kv_cache.py:448-637, ``_UnifiedReduceTorch``)
+is restated on torch tensors as ``TorchReducer``, element operation for element operation the
+oracle's ``oracle.unified.Reducer``, and its commit takes the same batched level-by-level append.
+``slot_attention`` is the readout's attention over packed rows as the reference evaluates it on the
+CPU (``torch.nn.functional.scaled_dot_product_attention`` over the Flash encoding of the slots,
+litgpt/log_kv_cache.py:6751-6758), in float32.
 """
 
 from __future__ import annotations
@@ -26,7 +33,7 @@ import numpy as np
 import torch
 
 from . import ladder as lad
-from . import readout, route
+from . import readout, route, unified
 from .cache import OracleCache
 from .numerics import WAVE, bf16_round, f32
 
@@ -206,10 +213,218 @@ def _bf16t(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.bfloat16).float()
 
 
+_INF = float("inf")
+_I64_TOP = torch.iinfo(torch.int64).max
+
+
+def _pack_key(cost: torch.Tensor, key: torch.Tensor) -> torch.Tensor:
+    """``oracle.unified.pack`` as int64: (cost bits << 32) | key, -0.0 stored as +0.0 (costs are
+    >= 0 or +inf, so the bits fit in 31)."""
+    cost = torch.where(cost == 0, torch.zeros((), dtype=torch.float32), cost)
+    return (cost.view(torch.int32).to(torch.int64) << 32) | key.to(torch.int64)
+
+
+def _pair_cost(d2, mi, mj, ri, rj, limit, valid):
+    """``oracle.unified.pair_cost`` on tensors (litgpt/log_kv_cache.py:437-445)."""
+    denom = torch.clamp(mi + mj, min=1.0)
+    valid = valid & (mi > 0) & (mj > 0)
+    if limit is not None:
+        distance = torch.sqrt(d2)
+        bound = torch.maximum(ri + (mj / denom) * distance, rj + (mi / denom) * distance)
+        valid = valid & (bound <= limit)
+    cost = torch.where(valid, d2 * (mi * mj / denom), torch.full((), _INF))
+    return cost, valid
+
+
+def pair_distances(mu: torch.Tensor, block: int = 32) -> torch.Tensor:
+    """Squared distances ``[M, M]`` of rows of ``mu``, canonical feature sums of squared
+    differences: the oracle's upper triangle and its mirror (x_i - x_j and x_j - x_i square to the
+    same float), computed in row blocks."""
+    m = mu.shape[0]
+    out = torch.empty(m, m, dtype=torch.float32)
+    for i0 in range(0, m, block):
+        diff = mu[i0:i0 + block, None, :] - mu[None, :, :]
+        out[i0:i0 + block] = _dsum(diff * diff)
+    return out
+
+
+def gram_distances(mu: torch.Tensor) -> torch.Tensor:
+    """Squared distances as the reference forms them above 32 nodes (litgpt/log_kv_cache.py:3028-3047):
+    rows centred on the first one, squared norms plus the Gram matrix (a GEMM), ``|a|^2 + |b|^2 - 2 a.b``
+    clamped at zero. The CPU baseline times this form, the reference's own; its last-ulp values differ
+    from the canonical direct differences (``pair_distances``), so it is not used for parity."""
+    centred = mu - mu[:1]
+    norm = (centred * centred).sum(-1)
+    return torch.clamp(norm[:, None] + norm[None, :] - 2 * (centred @ centred.T), min=0.0)
+
+
+class TorchReducer:
+    """One lane's incremental reducer rounds on torch tensors: ``oracle.unified.Reducer`` with the
+    same element operations in the same order (litgpt/log_kv_cache.py:448-637)."""
+
+    def __init__(self, dist, mu, mass, count, limit, target):
+        self.dist, self.mu, self.mass = dist, mu.clone(), mass.clone()
+        self.limit = None if limit is None else float(np.float32(limit))
+        self.target = int(target)
+        size = self.mass.shape[0]
+        self.ids = torch.arange(size)
+        self.alive = self.ids < count
+        self.radius = torch.zeros(size)
+        self.count = int(count)
+        self.stuck = False
+        self.trace = []
+        self.packed = torch.full((size,), int(unified.INF_KEY), dtype=torch.int64)
+        rows = torch.nonzero(self.alive)[:, 0]
+        if len(rows):
+            self.packed[rows] = self._scan(rows)
+
+    def _scan(self, rows):
+        lim = self.limit is not None
+        cost, _ = _pair_cost(self.dist[rows], self.mass[rows][:, None], self.mass[None, :],
+                             self.radius[rows][:, None] if lim else None, self.radius[None, :] if lim else None,
+                             self.limit, self.ids[None, :] != rows[:, None])
+        return _pack_key(cost, rows[:, None] ^ self.ids[None, :]).min(1).values
+
+    def step(self):
+        size = self.mass.shape[0]
+        ids = self.ids
+        best = torch.clamp((self.packed & 0xFFFFFFFF) ^ ids, 0, size - 1)
+        cost = (self.packed >> 32).to(torch.int32).view(torch.float32)
+        valid = self.alive & (ids < best) & (best[best] == ids) & (cost < _INF)
+        nprop = int(valid.sum())
+        rejected = torch.zeros(size, dtype=torch.bool)
+        bound = None
+        if self.limit is not None:
+            rows = torch.nonzero(valid)[:, 0]
+            other = best[rows]
+            diff = self.mu[rows] - self.mu[other]
+            exact2 = _dsum(diff * diff)
+            exact = torch.sqrt(exact2)
+            ma, mb = self.mass[rows], self.mass[other]
+            denom = torch.clamp(ma + mb, min=1.0)
+            verified = torch.maximum(self.radius[rows] + (mb / denom) * exact,
+                                     self.radius[other] + (ma / denom) * exact)
+            bad = verified > self.limit
+            self.dist[rows[bad], other[bad]] = exact2[bad]
+            self.dist[other[bad], rows[bad]] = exact2[bad]
+            rejected[rows[bad]] = True
+            rejected[other[bad]] = True
+            valid[rows[bad]] = False
+            bound = torch.zeros(size)
+            bound[rows] = verified
+        pair = torch.where(valid, cost, torch.full((), _INF))
+        order = torch.sort(pair, stable=True).indices[:size // 2]
+        ok = pair[order] < _INF
+        ok &= torch.cumsum(ok.to(torch.int64), 0) <= self.count - self.target
+        a = order[ok]
+        b = best[a]
+        keep = torch.zeros(size, dtype=torch.bool)
+        merged = torch.zeros(size, dtype=torch.bool)
+        if len(a):
+            self._merge(a, b, bound, keep, merged)
+        dirty = self.alive & ~keep & (merged[best] | rejected)
+        rows = torch.nonzero(dirty)[:, 0]
+        if len(rows):
+            self.packed[rows] = self._scan(rows)
+        self.count -= int(ok.sum())
+        remaining = self.count > self.target
+        if remaining and nprop == 0:
+            self.stuck = True
+        return remaining and nprop > 0
+
+    def _merge(self, a, b, bound, keep, merged):
+        size = self.mass.shape[0]
+        ids = self.ids
+        ma, mb = self.mass[a], self.mass[b]
+        dab = self.dist[a, b]
+        total = ma + mb
+        alpha, beta = ma / total, mb / total
+        shift = alpha * beta * dab
+        keep[a] = True
+        merged[a] = True
+        merged[b] = True
+        partner = torch.zeros(size, dtype=torch.int64)
+        partner[a] = b
+        pma, pmb, pdab = torch.ones(size), torch.zeros(size), torch.zeros(size)
+        pma[a], pmb[a], pdab[a] = ma, mb, dab
+        self.mass[a] = total
+        self.mass[b] = 0
+        self.alive[b] = False
+        if bound is not None:
+            self.radius[a] = bound[a]
+        self.mu[a] = (ma[:, None] * self.mu[a] + mb[:, None] * self.mu[b]) / torch.clamp(total, min=1.0)[:, None]
+        al, be, sh = alpha[:, None], beta[:, None], shift[:, None]
+        x_aa, x_ba = self.dist[a], self.dist[b]
+        new = al * x_aa + be * x_ba - sh
+        x_ab, x_bb = self.dist[a[:, None], partner[None, :]], self.dist[b[:, None], partner[None, :]]
+        qalpha, qbeta = pma / (pma + pmb), pmb / (pma + pmb)
+        qshift = qalpha * qbeta * pdab
+        own_first = qalpha * new + qbeta * (al * x_ab + be * x_bb - sh) - qshift
+        other_first = al * (qalpha * x_aa + qbeta * x_ab - qshift) + be * (qalpha * x_ba + qbeta * x_bb - qshift) - sh
+        both = torch.where(a[:, None] < ids[None, :], own_first, other_first)
+        new = torch.where(keep[None, :], both, new)
+        new = torch.where(new < 0, torch.zeros(()), new)
+        new[torch.arange(len(a)), a] = 0
+        alive = self.alive
+        cols = torch.nonzero(alive & ~keep)[:, 0]
+        self.dist[cols[:, None], a[None, :]] = new[:, cols].T
+        cols = torch.nonzero(alive)[:, 0]
+        self.dist[a[:, None], cols[None, :]] = new[:, cols]
+        lim = self.limit is not None
+        cost, valid = _pair_cost(new, total[:, None], self.mass[None, :],
+                                 self.radius[a][:, None] if lim else None, self.radius[None, :] if lim else None,
+                                 self.limit, alive[None, :] & (ids[None, :] != a[:, None]))
+        packed = _pack_key(cost, ids[None, :] ^ a[:, None])
+        push = valid & ~keep[None, :]
+        colmin = torch.where(push, packed, torch.full((), _I64_TOP, dtype=torch.int64)).min(0).values
+        self.packed = torch.minimum(self.packed, colmin)
+        self.packed[a] = packed.min(1).values
+        self.trace.extend(zip(a.tolist(), b.tolist()))
+
+
+def reduce(mu, mass, count, limit, target, strict=False, gram=False):
+    """``oracle.unified.reduce`` with ``TorchReducer``: (survivors, trace, centers) as numpy. ``gram``:
+    initial distances in the reference's Gram form above 32 nodes (``gram_distances``), else the
+    canonical differences."""
+    if count <= target:
+        return np.arange(count), [], f32(mu).copy()
+    mu_t = torch.from_numpy(np.ascontiguousarray(f32(mu)))
+    dist = gram_distances(mu_t) if gram and count > 32 else pair_distances(mu_t)
+    r = TorchReducer(dist, mu_t, torch.from_numpy(np.ascontiguousarray(f32(mass))), count, limit, target)
+    size = r.mass.shape[0]
+    for _ in range(2 * size + 7):
+        if not r.step():
+            break
+    if strict and r.stuck:
+        raise RuntimeError("unified route: no mutual pair below the cluster budget")
+    return torch.nonzero(r.alive)[:, 0].numpy(), r.trace, r.mu.numpy()
+
+
+def slot_attention(q: torch.Tensor, ka: torch.Tensor, va: torch.Tensor, scale: float, dv: int) -> torch.Tensor:
+    """Attention of queries ``[Bt, Hq, Tq, Dk]`` over packed rows ``[Bt, G, S, dim]`` (keys with their
+    bias column at Dk, values in the first ``dv`` columns) as the reference's Flash encoding is
+    evaluated (litgpt/log_kv_cache.py:6418-6464, :6751-6758): the query extended by ``1/scale`` in bf16
+    at column Dk, so the bias adds to the scaled scores, then ``scaled_dot_product_attention`` per KV
+    group over its query heads, in float32. No causal mask: one decode query per head."""
+    n_batch, hq, tq, dk = q.shape
+    n_groups, total, dim = ka.shape[1], ka.shape[2], ka.shape[3]
+    rep = hq // n_groups
+    qa = torch.zeros(n_batch, n_groups, rep * tq, dim)
+    qa[..., :dk] = q.float().reshape(n_batch, n_groups, rep * tq, dk)
+    qa[..., dk] = torch.tensor(1.0 / scale, dtype=torch.float32).to(torch.bfloat16).float()
+    out = torch.nn.functional.scaled_dot_product_attention(qa, ka, va[..., :dv], scale=scale)
+    return out.reshape(n_batch, hq, tq, dv)
+
+
 class TorchCpuCache(OracleCache):
-    """``OracleCache`` whose attach-route commit appends every ladder of a flush together, level by
-    level, with the Beta groups of a level batched, and whose pack is batched tensor code (see the
-    module docstring). Unified-route flushes and op-log recording keep the oracle's per-cluster path."""
+    """``OracleCache`` whose commit appends every ladder of a flush together, level by level, with
+    the Beta groups of a level batched, whose unified route reduces on torch tensors, and whose pack
+    is batched tensor code (see the module docstring). Op-log recording keeps the oracle's
+    per-cluster path."""
+
+    # The unified route's initial distances: False, the canonical differences (bit-identical to the
+    # oracle); True, the reference's Gram form (the CPU baseline's timing).
+    gram_distances = False
 
     def pack(self, k_cur=None, v_cur=None):
         """``readout.pack`` (the reference's Torch packer, litgpt/log_kv_pack.py:27-72) as batched
@@ -258,11 +473,22 @@ class TorchCpuCache(OracleCache):
         return ka.numpy(), va.numpy()
 
     def route_and_commit(self, ak, av, ap, counts):
-        if self.unified or self.op_log is not None:
+        if self.op_log is not None:
             return super().route_and_commit(ak, av, ap, counts)
+        if self.unified:
+            fn = (lambda *a, **k: reduce(*a, gram=True, **k)) if self.gram_distances else reduce
+            jobs, out = unified.unified_jobs(self, ak, ap, counts, reduce_fn=fn)
+            self._commit(jobs, f32(ak), f32(av), ap)
+            return out
         assign, order = attach_assign_batched(ak, ap, counts, self.centroid, self.alive, self.p_hi_c, self.s_h,
                                               self.eta, self.g0, self.lam)
         jobs = route.commit_jobs(assign, order, counts, self.alive)
+        self._commit(jobs, ak, av, ap)
+        return assign, order
+
+    def _commit(self, jobs, ak, av, ap):
+        """Stage every job's rows (opened clusters, delayed archives, joins: the oracle's per-cluster
+        rules, centers in position order), then append all of them together level by level."""
         lanes, staged = [], []
         for (b, g, c), (new, rows) in sorted(jobs.items()):
             parts = []
@@ -308,7 +534,6 @@ class TorchCpuCache(OracleCache):
                 lanes.append((b, g, c))
                 staged.append(parts[0] if len(parts) == 1 else lad.concat(parts))
         self._append_many(lanes, staged)
-        return assign, order
 
     def _append_many(self, lanes, staged):
         """``Ladder.append`` of ``staged[i]`` into ladder ``lanes[i]`` for every i, one level at a time

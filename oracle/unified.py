@@ -97,6 +97,9 @@ class Reducer:
         rows = np.flatnonzero(self.alive)
         if len(rows):
             self.packed[rows] = self._scan(rows)
+        # Work counts (the device reports the same): rounds, kept rows x live columns of the
+        # Lance-Williams updates, rescanned rows x live columns (the first scan: every row).
+        self.rounds, self.lw_elems, self.scan_elems = 0, 0, len(rows) * len(rows)
 
     def _scan(self, rows):
         lim = self.limit is not None
@@ -146,6 +149,10 @@ class Reducer:
         rows = np.flatnonzero(dirty)
         if len(rows):
             self.packed[rows] = self._scan(rows)
+        live = int(self.alive.sum())
+        self.rounds += 1
+        self.lw_elems += len(a) * live
+        self.scan_elems += len(rows) * live
         self.count -= int(ok.sum())
         remaining = self.count > self.target
         if remaining and nprop == 0:
@@ -205,10 +212,14 @@ class Reducer:
         self.trace.extend(zip(a.tolist(), b.tolist()))
 
 
-def reduce(mu, mass, count, limit, target, strict=False):
+def reduce(mu, mass, count, limit, target, strict=False, counts=None):
     """Rounds until no mutual pair is left or ``count <= target``
-    (litgpt/log_kv_cache.py:3303-3376). Returns (survivors, trace, centers)."""
+    (litgpt/log_kv_cache.py:3303-3376). Returns (survivors, trace, centers).
+    ``counts``: a list that gets the stage's (nodes, rounds, merges,
+    Lance-Williams elements, rescanned elements)."""
     if count <= target:
+        if counts is not None:
+            counts.append((count, 0, 0, 0, 0))
         return np.arange(count), [], f32(mu).copy()
     r = Reducer(pair_distances(mu), mu, mass, count, limit, target)
     size = r.mass.shape[0]
@@ -217,6 +228,8 @@ def reduce(mu, mass, count, limit, target, strict=False):
             break
     if strict and r.stuck:
         raise RuntimeError("unified route: no mutual pair below the cluster budget")
+    if counts is not None:
+        counts.append((count, r.rounds, len(r.trace), r.lw_elems, r.scan_elems))
     return np.flatnonzero(r.alive), r.trace, r.mu
 
 
@@ -289,30 +302,32 @@ def ward_merge(cache, b, g, keep, free):
         cache._append(b, g, keep, rows)
 
 
-def plan_lane(cache, keys, n, b, g):
+def plan_lane(cache, keys, n, b, g, reduce_fn=reduce):
     """Both stages of one lane: (ward jobs [(keep, free)], target cluster root
-    per row as (root index, n_old, old ids, survivors))."""
+    per row as (root index, n_old, old ids, survivors)). ``reduce_fn`` runs a
+    reducer stage (``reduce``'s signature and results)."""
     limit = np.float32(math.sqrt(float(cache.lam) * float(cache.s_h[b, g])))
     mu = f32(keys[:n])
-    surv1, trace1, mu1 = reduce(mu, np.ones(n, np.float32), n, limit, 1)
+    surv1, trace1, mu1 = reduce_fn(mu, np.ones(n, np.float32), n, limit, 1)
     lab1 = labels(n, surv1, trace1)
     old = np.flatnonzero(cache.alive[b, g])
     weights = np.concatenate((cache.n_total[b, g, old].astype(np.float32),
                               np.bincount(lab1, minlength=len(surv1)).astype(np.float32)))
     centers = np.concatenate((cache.centroid[b, g, old].astype(np.float32), mu1[surv1]))
     m2 = len(weights)
-    surv2, trace2, _ = reduce(centers, weights, m2, None, cache.K, strict=True)
+    surv2, trace2, _ = reduce_fn(centers, weights, m2, None, cache.K, strict=True)
     lab2 = labels(m2, surv2, trace2)
     jobs = [(int(old[a]), int(old[c])) for a, c in trace2 if c < len(old)]
     root = lab2[len(old) + lab1]
     return jobs, root, old, np.asarray(surv2)
 
 
-def route_unified(cache, ak, av, ap, counts):
-    """Unified route + commit of ``counts[b]`` rows of ``ak/av/ap``
-    (litgpt/log_kv_cache.py:3589-3688). Returns per lane the cluster of every
-    row (offset order), -1 past the count."""
-    ak, av = f32(ak), f32(av)
+def unified_jobs(cache, ak, ap, counts, reduce_fn=reduce):
+    """The route half of a unified flush (litgpt/log_kv_cache.py:3589-3664): every lane planned,
+    its old-old merges applied (and logged); returns the commit jobs ``{(b, g, c): (opened, rows
+    in position order)}`` and per lane the cluster of every row (offset order), -1 past the
+    count."""
+    ak = f32(ak)
     n_batch, n_groups, width, _ = ak.shape
     out = np.full((n_batch, n_groups, width), -1, np.int64)
     plans = {}
@@ -321,7 +336,7 @@ def route_unified(cache, ak, av, ap, counts):
         if not n:
             continue
         for g in range(n_groups):
-            plans[(b, g)] = plan_lane(cache, ak[b, g], n, b, g)
+            plans[(b, g)] = plan_lane(cache, ak[b, g], n, b, g, reduce_fn)
     for (b, g), (jobs, _, _, _) in plans.items():
         for keep, free in jobs:
             ward_merge(cache, b, g, keep, free)
@@ -345,6 +360,15 @@ def route_unified(cache, ak, av, ap, counts):
             c = next(free_slots) if opened else int(old[surv2[r]])
             jobs_all[(b, g, c)] = (opened, sel)
             out[b, g, sel] = c
+    return jobs_all, out
+
+
+def route_unified(cache, ak, av, ap, counts):
+    """Unified route + commit of ``counts[b]`` rows of ``ak/av/ap``
+    (litgpt/log_kv_cache.py:3589-3688). Returns per lane the cluster of every
+    row (offset order), -1 past the count."""
+    ak, av = f32(ak), f32(av)
+    jobs_all, out = unified_jobs(cache, ak, ap, counts)
     late = set()
     for (b, g, c), (new, rows) in sorted(jobs_all.items()):
         if new:

@@ -105,3 +105,33 @@ def test_lattice_ties_and_radius_edge(scale):
         torch.cuda.synchronize()
         bad = compare_state(gpu, ora)
         assert not bad, f"flush {i}: " + "; ".join(bad)
+
+
+def test_reducer_counts_match_oracle():
+    """The device reducer's work counts of each flush (``unified_reduce_stats``: per lane and stage the
+    nodes, rounds, merges, Lance-Williams and rescanned elements - the byte model of the unified
+    roofline) equal the oracle reducer's on the same inputs."""
+    from oracle import unified as U
+
+    batch, groups, dim, K, B, T, n, s_h = 1, 2, 128, 12, 16, 256, 4, 64.0
+    print("case reducer counts", flush=True)
+    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h)
+    mix = Mixture(batch, groups, dim, clusters=K + 2, seed=19, drift_every=512)
+    dev = gpu.level_k.device
+    for i in range(n):
+        k, v = mix.rows(T), mix.rows(T)
+        pos = torch.arange(i * T, (i + 1) * T).unsqueeze(0).expand(batch, -1).contiguous()
+        want = []
+        for b in range(batch):
+            for g in range(groups):
+                stages = []
+                U.plan_lane(ora, k[b, g].float().numpy(), T, b, g,
+                            reduce_fn=lambda *a, **kw: U.reduce(*a, counts=stages, **kw))
+                want.append(stages)
+        gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev))
+        ora.flush_rows(k.float().numpy(), v.float().numpy(), pos.numpy())
+        got = gpu.unified_reduce_stats(T)
+        for lane, stages in enumerate(want):
+            for st, counts in enumerate(stages):
+                assert tuple(got[lane, st, :5].tolist()) == counts, f"flush {i} lane {lane} stage {st}"
+        assert want[0][0][2] > 0
