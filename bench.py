@@ -465,6 +465,52 @@ def flush_workload(args, torch, np):
                  f"over {len(segments)} segment(s)")
         return {"elapsed": elapsed, "step_ms": step_ms, "records": records, "B": B_, "L": L_, "width": width}
 
+    def add_recent_pass():
+        """The layers driven as litgpt's model drives them: one cache per layer (batch 1, built as the
+        model builds them, so they form one flush group), and per step, for every layer, the readout
+        (plan + pack of the prefix the next attention reads) then add_recent of the step's 2048-row
+        block. Each step's add_recent leaves the flush of the previous block pending; the first readout
+        of the next step runs the 28 pending flushes as one stacked flush. Steps are blocks 3..15 of
+        32K-token streams (the first three fill the window and the ladders), warm-up steps first."""
+        total, done, elapsed = args.warmup + args.steps, 0, 0.0
+        runs = [0, 0]
+        empty = torch.empty(1, G, 0, D, dtype=torch.bfloat16, device=dev)
+        while done < total:
+            caches = [new_flush_cache(torch, dev, 1, cos, sin) for _ in range(layers)]
+            packs = [tuple(torch.empty(1, G, _decode_capacity(c, 2), dim, dtype=torch.bfloat16, device=dev)
+                           for _ in range(2)) for c in caches]
+            t0 = None
+            for blk in range(STREAM_FLUSHES):
+                steady = blk >= 3
+                if steady and done >= total:
+                    break
+                if steady and done >= args.warmup and t0 is None:
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                k, v = data[blk]
+                for li, cache in enumerate(caches):
+                    view = readout_view(cache)
+                    plan = cache._semantic_attention_plan()
+                    _launch_pack(cache, view, plan, empty, empty, dim, *packs[li], False, 0)
+                    cache.add_recent(k[li:li + 1], v[li:li + 1], k_raw=k[li:li + 1],
+                                     input_pos=positions[blk][li:li + 1], span_ends=ends[blk][li:li + 1])
+                if steady:
+                    done += 1
+            if t0 is not None:
+                torch.cuda.synchronize()
+                elapsed += time.perf_counter() - t0
+            for cache in caches:
+                readout_view(cache)          # the last block's pending flush, outside the timed region
+            group = caches[0]._group
+            if group is not None:
+                runs[0] += group.stacked_runs
+                runs[1] += group.member_runs
+            del caches, packs, group
+        stacked, member = runs
+        progress(f"flush, per-layer add_recent: {args.steps} timed steps in {elapsed:.3f} s "
+                 f"({stacked} stacked group flushes, {member} member flushes)")
+        return elapsed, stacked, member
+
     tokens = F * layers * args.steps
     timed = run_pass(True, 1)
     if args.profile_flush:
@@ -483,6 +529,17 @@ def flush_workload(args, torch, np):
                     r["elapsed"] / args.steps / layers * 1e3
             except Exception as e:   # a secondary pass never loses the headline
                 per_layer[f"per_layer_calls_{n_streams}_stream_error"] = f"{type(e).__name__}: {e}"
+        try:
+            el, stacked_runs, member_runs = add_recent_pass()
+            per_layer["per_layer_add_recent_tokens_per_s"] = tokens / el
+            per_layer["per_layer_add_recent_ms_per_layer_flush"] = el / args.steps / layers * 1e3
+            per_layer["per_layer_add_recent_note"] = (
+                "one cache per layer driven as litgpt/model.py calls them (readout, then add_recent of the "
+                "block); the caches form one flush group, so each step's 28 deferred flushes run as one "
+                f"stacked flush ({stacked_runs} stacked, {member_runs} per-member flushes in the run); "
+                "per_layer_calls_* time direct per-layer route_and_flush_batch calls, which are never deferred")
+        except Exception as e:
+            per_layer["per_layer_add_recent_error"] = f"{type(e).__name__}: {e}"
     recs = metered["records"]
     stage_bytes = {k: float(np.mean([by[k] for by, _ in recs])) for k in ("alpha", "route", "commit", "pack")}
     stage_ms = {k: float(np.mean([ms[k] for _, ms in recs])) for k in ("alpha", "route", "commit", "pack")}

@@ -317,7 +317,10 @@ int logkv_score_spans(const logkv_span_args* args, float* scores, void* stream);
  * [n_batch, P] and archive [n_batch, P + T] source rows (indices into
  * [pool (P rows) | flush], -1 past the end), archive_count [n_batch], the new
  * selection's spans, alpha_count[0] = the largest kept count, and optionally
- * the candidates' scores. At most 4096 candidates per batch row.
+ * the candidates' scores. At most 4096 candidates per batch row. With
+ * count_rows > 0 the batch rows are groups of count_rows consecutive rows
+ * (caches stacked as batch rows, count_rows each) and alpha_count[i] is the
+ * largest kept count of group i; 0 means one group of all rows.
  * Replaces the selection of _alpha_route_flush (litgpt/log_kv_cache.py:
  * 3904-3940): cut_spans, score_spans and choose_spans
  * (litgpt/alpha_log_kv.py:16-226). */
@@ -341,6 +344,7 @@ typedef struct logkv_alpha_select_args {
   int32_t* new_span_count;
   int32_t* alpha_count;
   float* scores;
+  int32_t count_rows;
 } logkv_alpha_select_args;
 
 int64_t logkv_alpha_select_workspace_bytes(const logkv_alpha_select_args* args);

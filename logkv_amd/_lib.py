@@ -74,7 +74,7 @@ class AlphaSelectArgs(C.Structure):
         ("new_pos", _p), ("np_sb", _i64), ("ends", _p), ("ends_sb", _i64), ("tokens", _i32),
         ("n_batch", _i32), ("budget", _i32), ("max_span", _i32), ("rows", SpanArgs),
         ("keep", _p), ("archive", _p), ("archive_count", _p), ("new_span_len", _p), ("new_span_closed", _p),
-        ("new_span_count", _p), ("alpha_count", _p), ("scores", _p),
+        ("new_span_count", _p), ("alpha_count", _p), ("scores", _p), ("count_rows", _i32),
     ]
 
 

@@ -279,7 +279,7 @@ class _AlphaCall:
             slen.data_ptr(), sclosed.data_ptr(), scount.data_ptr(), ppos.data_ptr(), None, 0, None, 0, T,
             n_batch, P, cache.alpha_span_max_tokens, self.rows, keep.data_ptr(), archive.data_ptr(),
             archive_count.data_ptr(), nlen.data_ptr(), nclosed.data_ptr(), ncount.data_ptr(),
-            cache.alpha_count_dev.data_ptr(), None)
+            cache.alpha_count_dev.data_ptr(), None, cache._alpha_count_rows)
         self.sized = False   # the selection workspace is sized on the first call (it checks the row pointers)
         self.part = _lib.PartitionArgs(
             pk.data_ptr(), pk.stride(0), pk.stride(1), pk.stride(2),

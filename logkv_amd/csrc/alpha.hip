@@ -381,7 +381,9 @@ __global__ __launch_bounds__(kSelectThreads) void cut_kernel(logkv_alpha_select_
   uint8_t* oclosed = flags + T;                                              // [P]
   __shared__ int wave_tmp[kSelectThreads / kWave];
   __shared__ int pend_idx_s, pend_off_s, pend_len_s, carry_s, nc_s, nt_s;
-  if (b == 0 && tid == 0) *a.alpha_count = 0;
+  // One count per group of count_rows batch rows (0: one group); its first row's block clears it.
+  const int count_rows = a.count_rows > 0 ? a.count_rows : a.n_batch;
+  if (b % count_rows == 0 && tid == 0) a.alpha_count[b / count_rows] = 0;
   const LOGKV_G int64_t* pos = gp(a.new_pos + b * a.np_sb);
   const LOGKV_G uint8_t* ends = gp(a.ends + b * a.ends_sb);
   const int n_old = min(a.span_count[b], P);
@@ -902,7 +904,7 @@ __global__ __launch_bounds__(kSelectThreads) void choose_kernel(logkv_alpha_sele
   if (tid == 0) {
     a.new_span_count[b] = spans;
     a.archive_count[b] = arch;
-    atomicMax(a.alpha_count, kept);
+    atomicMax(a.alpha_count + b / (a.count_rows > 0 ? a.count_rows : a.n_batch), kept);
   }
   __syncthreads();
   const int A = P + T;

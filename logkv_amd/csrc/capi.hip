@@ -536,6 +536,8 @@ static int check_select(const logkv_alpha_select_args* a) {
       !a->archive_count || !a->new_span_len || !a->new_span_closed || !a->new_span_count || !a->alpha_count)
     return fail(LOGKV_EINVAL, "selection buffer is NULL");
   if (a->tokens && (!a->new_pos || !a->ends)) return fail(LOGKV_EINVAL, "new positions or boundaries are NULL");
+  if (a->count_rows < 0 || (a->count_rows && a->n_batch % a->count_rows))
+    return fail(LOGKV_EINVAL, "count_rows %d must be 0 or divide the %d batch rows", a->count_rows, a->n_batch);
   const logkv_span_args& r = a->rows;
   if (r.n_groups < 1 || r.n_groups > 16 || r.dk < 1 || r.dv < 1 || r.dk > logkv::kMaxDim || r.dv > logkv::kMaxDim)
     return fail(LOGKV_EINVAL, "bad groups or widths");

@@ -25,6 +25,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from . import flush_group as _flush_group
 from ._lib import LadderView, RouteParams, RowsView, check, lib, ptr, require_device, stream_of
 
 # Rows per tile of a center's new-key sum, by semantic_centroid_backend.
@@ -165,6 +166,24 @@ class LogStructuredKVCache(nn.Module):
         beta_adaptive_merge: bool = False,
     ) -> None:
         super().__init__()
+        self._pending = None     # a deferred flush (its token count, the window's rows before it)
+        self._group = None
+        self._init_kwargs = dict(
+            k_shape=tuple(k_shape), v_shape=tuple(v_shape), B=B, recent_size=recent_size, device=device, dtype=dtype,
+            importance_pooling=importance_pooling, importance_pooling_lambda=importance_pooling_lambda,
+            importance_pooling_temperature=importance_pooling_temperature, semantic_clusters=semantic_clusters,
+            cluster_k_max=cluster_k_max, cluster_lambda_rel=cluster_lambda_rel, seg_eta=seg_eta, seg_g0=seg_g0,
+            seg_gap_max=seg_gap_max, seg_block_level=seg_block_level, seg_forget=seg_forget,
+            semantic_s_h=semantic_s_h, semantic_flush_granularity=semantic_flush_granularity,
+            semantic_cluster_chunk_size=semantic_cluster_chunk_size, semantic_capacity_beta=semantic_capacity_beta,
+            semantic_capacity_hard_cap_mult=semantic_capacity_hard_cap_mult,
+            semantic_legacy_route=semantic_legacy_route, semantic_unified_route=semantic_unified_route,
+            semantic_merge_passes=semantic_merge_passes, semantic_anchor_mode=semantic_anchor_mode,
+            semantic_pack_backend=semantic_pack_backend, semantic_centroid_backend=semantic_centroid_backend,
+            semantic_replay_updates=semantic_replay_updates, rope_n_elem=rope_n_elem,
+            allocate_second_order=allocate_second_order, alpha_exact_tokens=alpha_exact_tokens,
+            alpha_span_max_tokens=alpha_span_max_tokens, beta_novelty=beta_novelty,
+            beta_adaptive_merge=beta_adaptive_merge)
         batch_size, n_groups, max_seq_length, k_dim = k_shape
         v_dim = v_shape[-1]
         device = torch.device(device) if device is not None else torch.device("cuda")
@@ -380,9 +399,34 @@ class LogStructuredKVCache(nn.Module):
         # then waits on the last such flush (`_flush_done`).
         self.flush_stream = None
         self._flush_done = None
+        # Rows per count of alpha_count_dev (0: one count for all rows; the owner of a flush group keeps
+        # one count per member).
+        self._alpha_count_rows = 0
+        self._init_kwargs.update(cos_cache=self.cos_cache, sin_cache=self.sin_cache)
+        _flush_group.register(self)
+
+    def _group_key(self):
+        """Caches whose flushes may run stacked share this key (same shapes, budget and route)."""
+        kw = self._init_kwargs
+        return (self.level_k.device, self.level_k.dtype, self.batch_size, self.n_groups, self.max_seq_length,
+                self.k_dim, self.v_dim, self.B_prime, self.L_alloc, self.K_max, self.recent_size,
+                self.semantic_flush_granularity, self.cluster_lambda_rel, self.seg_eta, self.seg_g0,
+                self.semantic_capacity_hard_cap_mult, self.semantic_unified_route, self.semantic_merge_passes,
+                self.alpha_exact_tokens, self.alpha_span_max_tokens, self.beta_novelty, self.beta_adaptive_merge,
+                kw["semantic_centroid_backend"], self.semantic_replay_updates)
+
+    def __getattr__(self, name):
+        # A state buffer read while this cache's flush is deferred runs the flush first.
+        if name in _flush_group.STATE_SET and self.__dict__.get("_pending") is not None:
+            self._group.run()
+        return super().__getattr__(name)
 
     def _await_flush(self, stream=None) -> None:
-        """Order ``stream`` (default: the current one) after the last flush queued on ``flush_stream``."""
+        """Make the device state current for ``stream`` (default: the current one): run a deferred
+        flush of this cache (with the rest of its flush group), then order the stream after the last
+        flush queued on ``flush_stream``."""
+        if self._pending is not None:
+            self._group.run()
         if self._flush_done is not None:
             (torch.cuda.current_stream(self.level_k.device) if stream is None else stream).wait_event(self._flush_done)
 
@@ -969,7 +1013,16 @@ class LogStructuredKVCache(nn.Module):
         overflow = self.recent_count - self.recent_size
         if overflow > 0:
             F = self.semantic_flush_granularity
-            self._semantic_flush_tokens(F * ((overflow + F - 1) // F), record_op_log=record_op_log,
+            take = F * ((overflow + F - 1) // F)
+            plain = not record_op_log and replay_op_log is None and replay_op_log_host is None and replay_plans is None
+            if (plain and self._active_updates is None and self.flush_stream is None and self._group is not None
+                    and self._group.adopt()):
+                # Deferred: the group runs it, stacked with the other layers' flushes, at the first read.
+                self._pending = (take, self.recent_count)
+                self.recent_count -= take
+                self._mid_decode_state = None
+                return
+            self._semantic_flush_tokens(take, record_op_log=record_op_log,
                                         replay_op_log=replay_op_log, replay_op_log_len=replay_op_log_len,
                                         replay_op_log_host=replay_op_log_host, replay_plans=replay_plans)
 
@@ -1001,6 +1054,8 @@ class LogStructuredKVCache(nn.Module):
     def _apply(self, fn, recurse=True):
         # Moving or casting buffers invalidates raw pointers held in workspaces
         # (litgpt/log_kv_cache.py:6226-6232).
+        self._await_flush()
+        before = {name: t.data_ptr() for name, t in self._buffers.items() if t is not None}
         self._mid_decode_state = None
         self._workspace = None
         self._views = {}
@@ -1008,6 +1063,9 @@ class LogStructuredKVCache(nn.Module):
         out = super()._apply(fn, recurse)
         if self.alpha_exact_tokens:
             self._alpha_spare = tuple(fn(t) for t in self._alpha_spare)
+        moved = any(t is not None and t.data_ptr() != before.get(name) for name, t in self._buffers.items())
+        if moved and self._group is not None:
+            self._group.leave(self)      # its buffers no longer view the group's stacked rows
         return out
 
     # ------------------------------------------------------------------
