@@ -12,3 +12,4 @@ from .log_kv_pack import (append_exact_tokens, log_kv_chunk_attention, log_kv_sl
 from . import beta_log_kv  # noqa: F401
 from .kv_compression import cache_compression_snapshot, summarize_compression  # noqa: F401
 from .streaming import LogKVStreamingAttention  # noqa: F401
+from .flush_group import flush_grouping, set_flush_grouping  # noqa: F401
