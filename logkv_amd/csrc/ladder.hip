@@ -1184,6 +1184,142 @@ __device__ __forceinline__ void group_rows(const PoolT<KIND>& pool, int start, i
   }
 }
 
+// Screened cut decision of a full group (rows in the row layout). The loss of a
+// side S is sum_{i<j in S} w_i w_j |x_i - x_j|^2 / m_S (the weighted spread
+// about the side's mean), so the three cuts' costs need only the squared
+// distances d01, d02, d12, d13, d23 and the four squared norms (the energy):
+// 14 operations per feature and component instead of the canonical
+// evaluation's ~76, with every term non-negative, so the costs' relative
+// error stays a few tens of ulps. `screen_sums` leaves in every lane of the
+// row the component's sums [n0, n1, n2, n3, d01, d02, d12, d13, d23], in any
+// order (fused multiply-adds).
+template <int F>
+__device__ __forceinline__ void screen_sums(const float (&x)[4][F], float* s9) {
+#pragma unroll
+  for (int q = 0; q < 9; ++q) s9[q] = 0.f;
+#pragma unroll
+  for (int k = 0; k < F; ++k) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s9[i] = __builtin_fmaf(x[i][k], x[i][k], s9[i]);
+    const float t01 = x[0][k] - x[1][k], t02 = x[0][k] - x[2][k], t12 = x[1][k] - x[2][k];
+    const float t13 = x[1][k] - x[3][k], t23 = x[2][k] - x[3][k];
+    s9[4] = __builtin_fmaf(t01, t01, s9[4]);
+    s9[5] = __builtin_fmaf(t02, t02, s9[5]);
+    s9[6] = __builtin_fmaf(t12, t12, s9[6]);
+    s9[7] = __builtin_fmaf(t13, t13, s9[7]);
+    s9[8] = __builtin_fmaf(t23, t23, s9[8]);
+  }
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+    float v = s9[q];
+    v = v + row_ror<8>(v);
+    v = v + row_ror<4>(v);
+    v = v + row_ror<2>(v);
+    s9[q] = v + row_ror<1>(v);
+  }
+}
+
+// Adds one component's screened costs of the cuts (2, 1, 3) to `cost`.
+__device__ __forceinline__ void screen_costs(const float* s9, const float* w, float total, float* cost) {
+  const float e = ((s9[0] * w[0] + s9[1] * w[1]) + s9[2] * w[2]) + s9[3] * w[3];
+  const float energy = fmaxf(e / total, 1e-12f);
+  const float p01 = (w[0] * w[1]) * s9[4], p02 = (w[0] * w[2]) * s9[5], p12 = (w[1] * w[2]) * s9[6];
+  const float p13 = (w[1] * w[3]) * s9[7], p23 = (w[2] * w[3]) * s9[8];
+  const float c2 = p01 / fmaxf(w[0] + w[1], 1e-12f) + p23 / fmaxf(w[2] + w[3], 1e-12f);
+  const float c1 = ((p12 + p13) + p23) / fmaxf((w[1] + w[2]) + w[3], 1e-12f);
+  const float c3 = ((p01 + p02) + p12) / fmaxf((w[0] + w[1]) + w[2], 1e-12f);
+  cost[0] += c2 / energy;
+  cost[1] += c1 / energy;
+  cost[2] += c3 / energy;
+}
+
+// The cut the canonical evaluation chooses, when the screened costs settle it:
+// its costs and the screen's both err by at most ~90 ulps relative (sums of
+// non-negative terms of depth <= 16, a handful of products and quotients; the
+// canonical side means' rounding adds at most 25 eps^2 of the side's energy
+// per side, covered by the absolute term), so a runner-up more than 2^-13
+// relative above the smallest screened cost (and 2^-36 of the group's mass)
+// cannot be the canonical minimum. Returns 0 when it is not settled: near ties
+// (exact ties, duplicate rows), non-finite costs, masses in (0, 2^-20) whose
+// clamped side means the pairwise form does not model.
+__device__ __forceinline__ int screened_cut(const float* ck, const float* cv, const float* w, float total) {
+  float cost[3] = {0.f, 0.f, 0.f};
+  screen_costs(ck, w, total, cost);
+  screen_costs(cv, w, total, cost);
+  int best = 0;
+  if (cost[1] < cost[best]) best = 1;
+  if (cost[2] < cost[best]) best = 2;
+  const float second = fminf(cost[(best + 1) % 3], cost[(best + 2) % 3]);
+  bool ok = __builtin_isfinite(cost[0]) && __builtin_isfinite(cost[1]) && __builtin_isfinite(cost[2]) &&
+            __builtin_isfinite(total);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ok = ok && (w[i] == 0.f || w[i] >= 0x1p-20f);
+  ok = ok && second - cost[best] > 0x1p-13f * second + 0x1p-36f * total;
+  return ok ? (best == 0 ? 2 : (best == 1 ? 1 : 3)) : 0;
+}
+
+// Raw bf16 rows held 8 contiguous features to a lane (lane l16 of the row:
+// features 8 l16 .. 8 l16 + 7 of a 128-feature row, two 8-byte loads), the
+// layout of the screen and of the outputs, whose sums are order-free.
+struct Rows8 {
+  uint2 k[4][2], v[4][2];
+};
+
+// Rows past the group's width are zeros (their x * 0 terms are +0, as the
+// reference's zero-filled rows give); every load is issued, then selected.
+__device__ __forceinline__ void load_rows8(const GroupRows& g, int l16, int width, Rows8& x) {
+  const uint2 zero = make_uint2(0u, 0u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const LOGKV_G uint2* pk = reinterpret_cast<const LOGKV_G uint2*>(g.k[i] + 8 * l16);
+    const LOGKV_G uint2* pv = reinterpret_cast<const LOGKV_G uint2*>(g.v[i] + 8 * l16);
+    const uint2 k0 = pk[0], k1 = pk[1], v0 = pv[0], v1 = pv[1];
+    x.k[i][0] = i < width ? k0 : zero;
+    x.k[i][1] = i < width ? k1 : zero;
+    x.v[i][0] = i < width ? v0 : zero;
+    x.v[i][1] = i < width ? v1 : zero;
+  }
+}
+
+// Feature f (0..7) of a lane's 8 contiguous bf16 features as float.
+__device__ __forceinline__ float feat8(const uint2 (&u)[2], int f) {
+  const uint32_t w = f < 4 ? (f < 2 ? u[0].x : u[0].y) : (f < 6 ? u[1].x : u[1].y);
+  return (f & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+}
+
+__device__ __forceinline__ void screen_sums8(const uint2 (&x)[4][2], float* s9) {
+  float f[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[i][k] = feat8(x[i], k);
+  screen_sums<8>(f, s9);
+}
+
+// One side's output means of a 128-feature group from the held rows: per
+// feature beta_group's row-order sum (member rows x w, the others x * 0) over
+// the side's double reciprocal, 8 features to a lane, two 8-byte stores.
+__device__ __forceinline__ void side_out8(const uint2 (&x)[4][2], const float* w, unsigned member, double rcp,
+                                          LOGKV_G uint16_t* at) {
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t h[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int f = 2 * q + e;
+      float acc = (member & 1u) ? feat8(x[0], f) * w[0] : feat8(x[0], f) * 0.f;
+#pragma unroll
+      for (int i = 1; i < 4; ++i) acc = acc + (((member >> i) & 1u) ? feat8(x[i], f) * w[i] : feat8(x[i], f) * 0.f);
+      h[e] = f32_to_bf16(div_by_rcp(acc, rcp));
+    }
+    o[q] = h[0] | (h[1] << 16);
+  }
+  LOGKV_G uint2* dst = reinterpret_cast<LOGKV_G uint2*>(at);
+  dst[0] = make_uint2(o[0], o[1]);
+  dst[1] = make_uint2(o[2], o[3]);
+}
+
 // One Beta group per 16-lane row: rows [4 gi, 4 gi + width) of the lane's
 // ladder pool at level ell into its carries 2 gi, 2 gi + 1 (beta_group's
 // arithmetic). `live` false: the row only takes part in the row exchanges.
@@ -1204,6 +1340,25 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
   GroupRows g;
   if (flush_src) group_rows<2>(PoolT<2>{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)}, start, width, g);
   else group_rows<1>(PoolT<1>{lad, base, cnt, staged_of(ws, ladder, ell, dk, dv)}, start, width, g);
+  // The screened decision; the canonical evaluation below runs only when a
+  // group of the wave is not settled by it.
+  int cut = 2;
+  bool settled = true;
+  if constexpr (FULL) {
+    Rows8 held;
+    load_rows8(g, l16, width, held);
+    if (width == 4) {
+      const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
+      float sk[9], sv[9];
+      screen_sums8(held.k, sk);
+      screen_sums8(held.v, sv);
+      cut = screened_cut(sk, sv, g.w, total);
+      settled = cut != 0;
+    }
+  } else {
+    settled = width != 4;
+  }
+  if (__ballot(!settled)) {
   float xk[4][F];
 #pragma unroll
   for (int i = 0; i < 4; ++i) load_row16<F, FULL>(g.k[i], l16, dk, i < width, xk[i]);
@@ -1222,7 +1377,6 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
     }
     rl = 1.0 / static_cast<double>(fmaxf(mass, 1e-12f));
   }
-  int cut = 2;
   {
     float ek, ev, lk[6], lv[6];
     row_component_losses<NJ>(xk, g.w, rl, ek, lk);
@@ -1250,16 +1404,39 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
     int best = 0;
     if (costs[1] < costs[best]) best = 1;
     if (costs[2] < costs[best]) best = 2;
-    cut = width == 4 ? (best == 0 ? 2 : (best == 1 ? 1 : 3)) : 2;
+    if (!settled) cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
+  }
   }
   // Outputs (beta_group's side means), K then V; the rows are loaded again
   // (the barrier keeps the compiler from holding the first loads live).
   asm volatile("" ::: "memory");
-  const int opt = cut == 2 ? 0 : (cut == 1 ? 1 : 2);
+  // The side reciprocals of the chosen cut (lane 0: left, 1: right).
+  double rl;
+  {
+    float wl[4], wrt[4];
+    cut_weights(g.w, cut, wl, wrt);
+    rl = 1.0 / static_cast<double>(fmaxf(l16 == 0 ? side_mass(wl) : side_mass(wrt), 1e-12f));
+  }
   const int dest = start / 2;
   const Soa out = carry_of(ws, ladder, ell, dk, dv);
-  const double left_rcp = row_lane_d(rl, 2 * opt), right_rcp = row_lane_d(rl, 2 * opt + 1);
+  const double left_rcp = row_lane_d(rl, 0), right_rcp = row_lane_d(rl, 1);
   const unsigned left_rows = (1u << cut) - 1u;
+  if constexpr (FULL) {
+    // The rows again (just read, so from the caches): nothing is held across the
+    // canonical evaluation's registers.
+    Rows8 held;
+    load_rows8(g, l16, width, held);
+#pragma unroll
+    for (int comp = 0; comp < 2; ++comp) {
+      LOGKV_G uint16_t* dst = comp == 0 ? out.k : out.v;
+#pragma unroll
+      for (int side = 0; side < 2; ++side) {
+        if (live && (side == 0 || width == 4))
+          side_out8(comp == 0 ? held.k : held.v, g.w, side == 0 ? left_rows : (0xfu & ~left_rows),
+                    side == 0 ? left_rcp : right_rcp, dst + static_cast<int64_t>(dest + side) * 128 + 8 * l16);
+      }
+    }
+  } else
 #pragma unroll
   for (int comp = 0; comp < 2; ++comp) {
     const int D = comp == 0 ? dk : dv;
@@ -1311,14 +1488,16 @@ __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderAr
   extern __shared__ __align__(16) int32_t prefix_s[];
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const LOGKV_G int32_t* pre = gp(ws.units + static_cast<int64_t>(ell) * (ladders + 1));
-  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
-  __syncthreads();
-  const int total = prefix_s[ladders];
+  // The level's unit count first: a block without quads leaves before it stages the table.
+  const int total = pre[ladders];
   if (total == 0) return;
   const int quads = (total + 3) / 4;
   const int wpb = static_cast<int>(blockDim.x) / kWave;
   const int n_waves = static_cast<int>(gridDim.x) * wpb;
   const int per = (quads + n_waves - 1) / n_waves;
+  if (static_cast<int>(blockIdx.x) * wpb * per >= quads) return;
+  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  __syncthreads();
   int qd = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
   const int qd_end = min(quads, qd + per);
   if (qd >= qd_end) return;
@@ -1354,12 +1533,14 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
   extern __shared__ __align__(16) int32_t prefix_s[];
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const LOGKV_G int32_t* pre = gp(ws.units + static_cast<int64_t>(ell) * (ladders + 1));
-  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
-  __syncthreads();
-  const int total = prefix_s[ladders];
+  // The level's unit count first: a block without units leaves before it stages the table.
+  const int total = pre[ladders];
   const int wpb = static_cast<int>(blockDim.x) / kWave;
   const int n_waves = static_cast<int>(gridDim.x) * wpb;
   const int per = (total + n_waves - 1) / n_waves;
+  if (total == 0 || static_cast<int>(blockIdx.x) * wpb * per >= total) return;
+  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  __syncthreads();
   int u = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
   const int u_end = min(total, u + per);
   if (u >= u_end) return;

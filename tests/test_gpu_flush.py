@@ -169,3 +169,37 @@ def test_beta_carries_keep_signed_zero_features():
             live = np.arange(bits.shape[-2])[None, None, None, None, :] < np.asarray(ora.level_count)[..., None]
             assert np.array_equal(np.where(live[..., None], bits, 0), np.where(live[..., None], ref, 0)), f"{f} bits"
     assert int(np.asarray(ora.level_count)[..., 1:].sum()) > 0, "no carry reached level 1"
+
+
+def test_beta_carries_lattice_ties():
+    """Beta carries whose groups tie: every token of a cluster is one of three lattice vectors (exact
+    bf16), so 4-row groups often repeat rows (A A B B, A B A B, A A A A, ...), making cut costs tie
+    exactly or up to the canonical evaluation's rounding (cuts 1 and 3 of A B A B are equal in exact
+    arithmetic, their float costs differ only in rounding). The screened decision must defer every
+    such group to the canonical evaluation: the ladders stay bit-identical to the oracle's."""
+    print("case Beta carries, lattice ties", flush=True)
+    gpu, ora = make_pair(1, 2, 128, 4, 8, 64, 64, 4096, 64.0, exact=16, span=4, beta_adaptive=True)
+    g = torch.Generator().manual_seed(12)
+    centers = (torch.randint(0, 2, (2, 4, 128), generator=g) * 2 - 1).float() * 2.0
+    variants = torch.stack([torch.zeros(2, 128), (torch.randint(0, 2, (2, 128), generator=g) * 2 - 1) * 0.5,
+                            (torch.randint(0, 3, (2, 128), generator=g) - 1) * 0.25], 1)   # [G, 3, D]
+    dev = gpu.level_k.device
+    for blk in range(24):
+        n = 64
+        rows = []
+        for _ in range(3):
+            c = torch.randint(0, 4, (2, n), generator=g)
+            v = torch.randint(0, 3, (2, n), generator=g)
+            x = torch.stack([centers[gi, c[gi]] + variants[gi, v[gi]] for gi in range(2)])
+            rows.append(x.unsqueeze(0).to(torch.bfloat16))
+        k_raw, v, k = rows
+        pos = torch.arange(blk * n, (blk + 1) * n).unsqueeze(0).contiguous()
+        ends = [[(p % 5) == 4 for p in range(blk * n, (blk + 1) * n)]]
+        gpu.add_recent(k.to(dev), v.to(dev), k_raw=k_raw.to(dev), input_pos=pos.to(dev), span_ends=ends)
+        ora.add_recent(k.float().numpy(), v.float().numpy(), k_raw.float().numpy(), pos.numpy(), ends)
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"block {blk}: " + "; ".join(bad)
+    assert int(np.asarray(ora.level_count)[..., 2:].sum()) > 0, "no carry reached level 2"
+    cuts = [int(x) for _, per in ora.beta_cuts for _, lvl in per for x in np.asarray(lvl).reshape(-1)]
+    assert len(set(cuts)) >= 2, "the lattice produced a single cut only"

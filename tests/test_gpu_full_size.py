@@ -113,3 +113,44 @@ def test_unified_flush_4096_rows_two_lanes():
         bad = compare_state(gpu, ora)
         assert not bad, f"flush {i}: " + "; ".join(bad)
     assert ora.ward_merges > 0, "no old-old merge was exercised"
+
+
+@pytest.mark.timeout(300)
+def test_unified_benched_geometry_sampled_lanes():
+    """The unified-route benchmark's geometry on the device - batch 4 x 8 KV groups (32 lanes), 4096-row
+    flushes, B=128, L=9 (131,072-token stream), s_h=64, the benchmark's drifting 12-Gaussian mixture -
+    for five flushes (the centers drift before the fifth), with two lanes
+    (first and last) checked after every flush against the oracle's reducer and commit (the Torch
+    restatement, bit-identical to the numpy oracle) fed the same two lanes' rows: lanes are
+    independent, so the sampled lanes see exactly what the whole batch saw."""
+    from oracle.torch_cpu import TorchCpuCache
+    from test_gpu_unified import _pair
+
+    print("case unified route, benchmark geometry (32 lanes), lanes (0,0) and (3,7)", flush=True)
+    Bt, T, N = 4, 4096, 131072
+    gpu, _ = _pair(Bt, G, D, 12, 128, T, N, 64.0)
+    assert gpu.L_alloc == 9
+    cos, sin = rope_tables(N, D)
+    ora = TorchCpuCache(2, 1, N, D, D, B=128, recent_size=T, K=12, s_h=64.0, flush=T, cos=cos.numpy(),
+                        sin=sin.numpy(), unified=True)
+    lanes = ((0, 0), (3, 7))
+    mix = Mixture(Bt, G, D, clusters=12, seed=31, drift_every=2 * 16384)
+    dev = gpu.level_k.device
+    for i in range(5):
+        print(f"flush {i}", flush=True)
+        k, v = mix.rows(T), mix.rows(T)
+        pos = torch.arange(i * T, (i + 1) * T).unsqueeze(0).expand(Bt, -1).contiguous()
+        gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev))
+        pick = lambda x: torch.stack([x[b, g] for b, g in lanes])[:, None].float().numpy()
+        ora.flush_rows(pick(k), pick(v), pos[:2].numpy(), None)
+        torch.cuda.synchronize()
+        for f in STATE_FIELDS:
+            a = to_np(getattr(gpu, f))
+            got = np.stack([a[b, g] for b, g in lanes])[:, None]
+            want = np.asarray(getattr(ora, f))
+            if got.dtype == np.bool_ or want.dtype == np.bool_:
+                same = got.astype(bool) == want.astype(bool)
+            else:
+                same = got.astype(want.dtype) == want
+            assert same.all(), f"flush {i}: {f}: {int((~same).sum())} mismatches"
+    assert int(ora.level_count[..., 1:].sum()) > 0 and ora.alive.sum() == 24
