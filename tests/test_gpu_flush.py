@@ -203,3 +203,66 @@ def test_beta_carries_lattice_ties():
     assert int(np.asarray(ora.level_count)[..., 2:].sum()) > 0, "no carry reached level 2"
     cuts = [int(x) for _, per in ora.beta_cuts for _, lvl in per for x in np.asarray(lvl).reshape(-1)]
     assert len(set(cuts)) >= 2, "the lattice produced a single cut only"
+
+
+def test_attach_screen_ties_and_radius_edges():
+    """Steady-state attach decisions (every cluster alive: the screened path) on rows built to sit on
+    decision boundaries: midpoints of two lattice centers (equal costs, first cluster wins), rows at
+    exactly the radius from their center and just past it, far rows equidistant from two centers
+    (nearest-cluster ties), mixed with ordinary rows; every decision equals the oracle's."""
+    import ctypes as C
+
+    from logkv_amd._lib import check, lib, ptr, stream_of
+    from oracle import route
+
+    batch, groups, dim, K, T = 1, 2, 128, 8, 256
+    s_h = 4.0
+    gpu, ora = make_pair(batch, groups, dim, K, 16, recent=T, flush=T, max_seq=4096, s_h=s_h)
+    g = torch.Generator().manual_seed(31)
+    centers = (torch.randint(0, 2, (groups, K, dim), generator=g) * 2 - 1).float()       # +-1 lattice
+    for dst in (gpu, ora):
+        cen = centers.unsqueeze(0)
+        if dst is gpu:
+            dst.centroid.copy_(cen.to(dst.centroid.device))
+            dst.alive.fill_(True)
+            dst.p_hi_c.fill_(10)
+            dst.n_total.fill_(5)
+        else:
+            dst.centroid[...] = cen.numpy()
+            dst.alive[...] = True
+            dst.p_hi_c[...] = 10
+            dst.n_total[...] = 5
+    rows = []
+    for gi in range(groups):
+        c = centers[gi]
+        r = []
+        for a in range(K):
+            b = (a + 1 + gi) % K
+            r.append((c[a] + c[b]) / 2)                           # equidistant from a and b
+            e = torch.zeros(dim)
+            e[a] = 2.0
+            r.append(c[a] + e * torch.sign(c[a, a]))              # |x - c_a|^2 = 4 = lambda s_h exactly
+            e[a] = 2.0078125                                      # just past the radius
+            r.append(c[a] + e * torch.sign(c[a, a]))
+            r.append((c[a] + c[b]) / 2 + 6.0 * torch.sign((c[a] + c[b]) / 2 + 0.5))   # far, equidistant
+        while len(r) < T:
+            a = int(torch.randint(0, K, (1,), generator=g))
+            r.append(c[a] + torch.randn(dim, generator=g) * 0.3)
+        rows.append(torch.stack(r[:T]))
+    k = torch.stack(rows).unsqueeze(0).to(torch.bfloat16)
+    pos = (100 + torch.arange(T)).unsqueeze(0).contiguous()
+    dev = gpu.level_k.device
+    view = gpu._ladder_view()
+    k_dev, pos_dev = k.to(dev), pos.to(dev)
+    rv = gpu._rows_view(k_dev, k_dev, pos_dev)
+    ws = gpu._workspace_for(view, T)
+    assign = torch.empty(batch, groups, T, dtype=torch.int8, device=dev)
+    order = torch.empty(batch, T, dtype=torch.int32, device=dev)
+    check(lib().logkv_attach_assign(C.byref(view), C.byref(rv), C.byref(gpu._params), ptr(ws), ws.numel(),
+                                    ptr(assign), ptr(order), stream_of(dev)), "attach")
+    torch.cuda.synchronize()
+    want, _ = route.attach_assign(k.float().numpy(), pos.numpy(), np.array([T]), ora.centroid, ora.alive, ora.p_hi_c,
+                                  ora.s_h, ora.eta, ora.g0, ora.lam)
+    np.testing.assert_array_equal(to_np(assign), want)
+    got = to_np(assign)
+    assert (got[0, :, 0:4 * K:4] != -1).all()                     # midpoints decided (tie: the first)
