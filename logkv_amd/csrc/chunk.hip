@@ -73,6 +73,24 @@ __device__ __forceinline__ float pair_sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The block's logical (query block, split, lane) in a grid of (query blocks,
+// splits, lanes). Workgroups go to the 8 XCDs round robin in dispatch order,
+// and each XCD has its own L2: dispatched block n takes logical block
+// (n % 8) (N / 8) + n / 8 (N blocks, a multiple of 8), so an XCD runs one
+// contiguous range of logical blocks - whole lanes when the lane count is a
+// multiple of 8 - and a lane's K / V tiles, read by all of its query blocks,
+// are fetched into one L2 instead of eight.
+struct ChunkBlock {
+  int qb, split, lane;
+};
+__device__ __forceinline__ ChunkBlock chunk_block() {
+  const int nx = static_cast<int>(gridDim.x), ny = static_cast<int>(gridDim.y);
+  const int n = nx * ny * static_cast<int>(gridDim.z);
+  int lin = static_cast<int>(blockIdx.x) + nx * (static_cast<int>(blockIdx.y) + ny * static_cast<int>(blockIdx.z));
+  if (n % 8 == 0) lin = (lin % 8) * (n / 8) + lin / 8;
+  return ChunkBlock{lin % nx, (lin / nx) % ny, lin / (nx * ny)};
+}
+
 }  // namespace
 
 // splits == 1: the block writes the output. splits > 1: block (x, s) covers the
@@ -86,24 +104,24 @@ __device__ __forceinline__ float pair_sum32(float x) {
 template <int NKS, int NDV, bool BF16V>
 __device__ __forceinline__ void chunk_body(const logkv_attention_args& a, const int32_t* __restrict__ width_ptr,
                                            int splits, float* __restrict__ part, const uint16_t* __restrict__ v16,
-                                           int kv) {
+                                           int kv, const ChunkBlock blk_id) {
   // Two K / V^T tile buffers: tile i + 1 is written into the other buffer while
   // tile i is read, so one barrier per tile orders both.
   __shared__ __align__(16) uint16_t k_s[2][kKeys * kLdK];
   __shared__ __align__(16) uint16_t vt_s[2][kMaxDvBlocks * 32 * kLdV];
-  const int lane_ix = blockIdx.z, split = blockIdx.y, G = a.n_groups;
+  const int lane_ix = blk_id.lane, split = blk_id.split, G = a.n_groups;
   const int b = lane_ix / G, g = lane_ix % G;
   const int rep = a.n_heads / G, nq = rep * a.tq;
   const int w = wave_id(), l = lane_id(), h = l >> 5, col = l & 31;
   const int dim = a.dim, ndv = a.dv / 32;
-  const int qi = blockIdx.x * kQRows + w * 32 + col;
+  const int qi = blk_id.qb * kQRows + w * 32 + col;
   const bool q_ok = qi < nq;
   const int qc = q_ok ? qi : nq - 1;
   const int head = g * rep + qc / a.tq, t = qc % a.tq;
   const int total = min(*width_ptr + a.tail + (a.alpha_count_dev ? *a.alpha_count_dev : 0), a.cap);
   const int tail0 = total - a.causal_tail;
   // Last key row any query of the block can see.
-  const int q_first = blockIdx.x * kQRows, q_last = min(q_first + kQRows, nq) - 1;
+  const int q_first = blk_id.qb * kQRows, q_last = min(q_first + kQRows, nq) - 1;
   const int t_max = q_first / a.tq == q_last / a.tq ? q_last % a.tq : a.tq - 1;
   const int key_end = a.causal_tail ? min(total, tail0 + t_max + 1) : total;
   // This block's part of the key range, in whole tiles.
@@ -399,9 +417,10 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void chunk_kernel(logkv_att
                                                        int splits, float* __restrict__ part,
                                                        const uint16_t* __restrict__ v16,
                                                        const int32_t* __restrict__ vshift) {
-  const int kv = vshift[blockIdx.z];
-  if (kv == kBf16Lane) chunk_body<NKS, NDV, true>(a, width_ptr, splits, part, v16, kv);
-  else chunk_body<NKS, NDV, false>(a, width_ptr, splits, part, v16, kv);
+  const ChunkBlock id = chunk_block();
+  const int kv = vshift[id.lane];
+  if (kv == kBf16Lane) chunk_body<NKS, NDV, true>(a, width_ptr, splits, part, v16, kv, id);
+  else chunk_body<NKS, NDV, false>(a, width_ptr, splits, part, v16, kv, id);
 }
 
 // The fp16 copy of the packed V (rows [0, total) of every lane, dv features):

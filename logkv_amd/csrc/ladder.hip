@@ -1036,14 +1036,13 @@ __device__ __forceinline__ double row_lane_d(double x, int k) {
 
 // Features l16 + 16 k of one bf16 row (0 past D): one base address per row and
 // compile-time offsets; a lane past the row's end loads nothing.
-template <int F, bool FULL>
+template <int F>
 __device__ __forceinline__ void load_row16(const LOGKV_G uint16_t* row, int l16, int D, bool valid, float (&x)[F]) {
   const LOGKV_G uint16_t* at = row + l16;
 #pragma unroll
   for (int k = 0; k < F; ++k) {
     float a = 0.f;
-    if (FULL) a = bf16_to_f32(at[16 * k]);   // D == 16 F: every lane's features exist
-    else if (l16 + 16 * k < D) a = bf16_to_f32(at[16 * k]);
+    if (l16 + 16 * k < D) a = bf16_to_f32(at[16 * k]);
     x[k] = valid ? a : 0.f;
   }
 }
@@ -1322,8 +1321,10 @@ __device__ __forceinline__ void side_out8(const uint2 (&x)[4][2], const float* w
 
 // One Beta group per 16-lane row: rows [4 gi, 4 gi + width) of the lane's
 // ladder pool at level ell into its carries 2 gi, 2 gi + 1 (beta_group's
-// arithmetic). `live` false: the row only takes part in the row exchanges.
-template <int NJ, bool FULL>
+// arithmetic), rows of fewer than 128 features (lane l holding features
+// l + 16 k, masked past the width). `live` false: the row only takes part in
+// the row exchanges.
+template <int NJ>
 __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsArgs& r, const Workspace& ws, int ladder,
                                                int ell, int gi, bool live) {
   constexpr int F = 4 * NJ;
@@ -1340,72 +1341,57 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
   GroupRows g;
   if (flush_src) group_rows<2>(PoolT<2>{lad, base, cnt, flush_rows_global(c, r, ws, pl, ladder)}, start, width, g);
   else group_rows<1>(PoolT<1>{lad, base, cnt, staged_of(ws, ladder, ell, dk, dv)}, start, width, g);
-  // The screened decision; the canonical evaluation below runs only when a
-  // group of the wave is not settled by it.
+  // A full group's cut is evaluated; a partial group is the left side of cut 2.
   int cut = 2;
-  bool settled = true;
-  if constexpr (FULL) {
-    Rows8 held;
-    load_rows8(g, l16, width, held);
-    if (width == 4) {
-      const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
-      float sk[9], sv[9];
-      screen_sums8(held.k, sk);
-      screen_sums8(held.v, sv);
-      cut = screened_cut(sk, sv, g.w, total);
-      settled = cut != 0;
-    }
-  } else {
-    settled = width != 4;
-  }
+  const bool settled = width != 4;
   if (__ballot(!settled)) {
-  float xk[4][F];
+    float xk[4][F];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) load_row16<F, FULL>(g.k[i], l16, dk, i < width, xk[i]);
-  // Side reciprocals of the cuts (2, 1, 3): lane l16 < 6 of the row divides
-  // (left, right of cut 2, of cut 1, of cut 3).
-  double rl;
-  {
-    float mass = 1.f;
+    for (int i = 0; i < 4; ++i) load_row16<F>(g.k[i], l16, dk, i < width, xk[i]);
+    // Side reciprocals of the cuts (2, 1, 3): lane l16 < 6 of the row divides
+    // (left, right of cut 2, of cut 1, of cut 3).
+    double rl;
+    {
+      float mass = 1.f;
 #pragma unroll
-    for (int opt = 0; opt < 3; ++opt) {
-      const int cc = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
-      float wl[4], wrt[4];
-      cut_weights(g.w, cc, wl, wrt);
-      mass = l16 == 2 * opt ? side_mass(wl) : mass;
-      mass = l16 == 2 * opt + 1 ? side_mass(wrt) : mass;
+      for (int opt = 0; opt < 3; ++opt) {
+        const int cc = opt == 0 ? 2 : (opt == 1 ? 1 : 3);
+        float wl[4], wrt[4];
+        cut_weights(g.w, cc, wl, wrt);
+        mass = l16 == 2 * opt ? side_mass(wl) : mass;
+        mass = l16 == 2 * opt + 1 ? side_mass(wrt) : mass;
+      }
+      rl = 1.0 / static_cast<double>(fmaxf(mass, 1e-12f));
     }
-    rl = 1.0 / static_cast<double>(fmaxf(mass, 1e-12f));
-  }
-  {
-    float ek, ev, lk[6], lv[6];
-    row_component_losses<NJ>(xk, g.w, rl, ek, lk);
-    asm volatile("" ::: "memory");   // V's loads after K's costs: one component's rows live at a time
-    float xv[4][F];
+    {
+      float ek, ev, lk[6], lv[6];
+      row_component_losses<NJ>(xk, g.w, rl, ek, lk);
+      asm volatile("" ::: "memory");   // V's loads after K's costs: one component's rows live at a time
+      float xv[4][F];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_row16<F, FULL>(g.v[i], l16, dv, i < width, xv[i]);
-    row_component_losses<NJ>(xv, g.w, rl, ev, lv);
-    // beta_cut's decision: energies and the 12 quotients lane-parallel in the
-    // row, the costs summed in lane 0 in beta_cut's order.
-    const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
-    const float en = (l16 == 0 ? ek : ev) / total;
-    const float energy_k = fmaxf(row_lane(en, 0), 1e-12f);
-    const float energy_v = fmaxf(row_lane(en, 1), 1e-12f);
-    float num = 0.f;
+      for (int i = 0; i < 4; ++i) load_row16<F>(g.v[i], l16, dv, i < width, xv[i]);
+      row_component_losses<NJ>(xv, g.w, rl, ev, lv);
+      // beta_cut's decision: energies and the 12 quotients lane-parallel in the
+      // row, the costs summed in lane 0 in beta_cut's order.
+      const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
+      const float en = (l16 == 0 ? ek : ev) / total;
+      const float energy_k = fmaxf(row_lane(en, 0), 1e-12f);
+      const float energy_v = fmaxf(row_lane(en, 1), 1e-12f);
+      float num = 0.f;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      num = l16 == k ? lk[k] : num;
-      num = l16 == 6 + k ? lv[k] : num;
+      for (int k = 0; k < 6; ++k) {
+        num = l16 == k ? lk[k] : num;
+        num = l16 == 6 + k ? lv[k] : num;
+      }
+      const float q = num / (l16 < 6 ? energy_k : energy_v);
+      float costs[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 12; ++k) costs[(k % 6) / 2] = costs[(k % 6) / 2] + row_lane(q, k);
+      int best = 0;
+      if (costs[1] < costs[best]) best = 1;
+      if (costs[2] < costs[best]) best = 2;
+      if (!settled) cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
     }
-    const float q = num / (l16 < 6 ? energy_k : energy_v);
-    float costs[3] = {0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < 12; ++k) costs[(k % 6) / 2] = costs[(k % 6) / 2] + row_lane(q, k);
-    int best = 0;
-    if (costs[1] < costs[best]) best = 1;
-    if (costs[2] < costs[best]) best = 2;
-    if (!settled) cut = best == 0 ? 2 : (best == 1 ? 1 : 3);
-  }
   }
   // Outputs (beta_group's side means), K then V; the rows are loaded again
   // (the barrier keeps the compiler from holding the first loads live).
@@ -1421,28 +1407,12 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
   const Soa out = carry_of(ws, ladder, ell, dk, dv);
   const double left_rcp = row_lane_d(rl, 0), right_rcp = row_lane_d(rl, 1);
   const unsigned left_rows = (1u << cut) - 1u;
-  if constexpr (FULL) {
-    // The rows again (just read, so from the caches): nothing is held across the
-    // canonical evaluation's registers.
-    Rows8 held;
-    load_rows8(g, l16, width, held);
-#pragma unroll
-    for (int comp = 0; comp < 2; ++comp) {
-      LOGKV_G uint16_t* dst = comp == 0 ? out.k : out.v;
-#pragma unroll
-      for (int side = 0; side < 2; ++side) {
-        if (live && (side == 0 || width == 4))
-          side_out8(comp == 0 ? held.k : held.v, g.w, side == 0 ? left_rows : (0xfu & ~left_rows),
-                    side == 0 ? left_rcp : right_rcp, dst + static_cast<int64_t>(dest + side) * 128 + 8 * l16);
-      }
-    }
-  } else
 #pragma unroll
   for (int comp = 0; comp < 2; ++comp) {
     const int D = comp == 0 ? dk : dv;
     float x[4][F];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_row16<F, FULL>(comp == 0 ? g.k[i] : g.v[i], l16, D, i < width, x[i]);
+    for (int i = 0; i < 4; ++i) load_row16<F>(comp == 0 ? g.k[i] : g.v[i], l16, D, i < width, x[i]);
     LOGKV_G uint16_t* dst = comp == 0 ? out.k : out.v;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
@@ -1455,7 +1425,7 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
         float acc = (member & 1u) ? x[0][k] * g.w[0] : x[0][k] * 0.f;
 #pragma unroll
         for (int i = 1; i < 4; ++i) acc = acc + (((member >> i) & 1u) ? x[i][k] * g.w[i] : x[i][k] * 0.f);
-        if (write && (FULL || l16 + 16 * k < D)) at[16 * k] = f32_to_bf16(div_by_rcp(acc, srcp));
+        if (write && l16 + 16 * k < D) at[16 * k] = f32_to_bf16(div_by_rcp(acc, srcp));
       }
     }
   }
@@ -1480,9 +1450,121 @@ __device__ __forceinline__ void beta_row_group(const LadderArgs& c, const RowsAr
   }
 }
 
+// Plan values of a lane's ladder at one level, kept while the lane's
+// consecutive quads stay on that ladder.
+struct RowPlan {
+  int ladder;
+  int cnt, m;
+  bool flush_src;
+  int first;
+  int64_t order_base;
+};
+
+__device__ __forceinline__ void load_row_plan(const Workspace& ws, int ladder, int ell, RowPlan& pp) {
+  const LadderPlan* pl = ws.plans + ladder;
+  pp.ladder = ladder;
+  pp.cnt = pl->cnt[ell];
+  pp.m = pl->m[ell];
+  pp.flush_src = ell == 0 && pl->kind0 == 0;
+  pp.first = pl->first;
+  pp.order_base = pl->order_base;
+}
+
+// The ladder's flush rows as a level-0 source from a lane's plan values.
+__device__ inline Src flush_rows_planned(const LadderArgs& c, const RowsArgs& r, const Workspace& ws,
+                                         const RowPlan& pp) {
+  const int lane_ix = pp.ladder / c.k_max;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  Src s{};
+  s.kind = 2;
+  s.gtok = gp(ws.tok + static_cast<int64_t>(pp.ladder) * r.tokens + pp.first);
+  s.order_base = pp.order_base;
+  s.kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  s.vb = gp(r.v + b * r.v_sb + g * r.v_sg);
+  s.k_st = r.k_st;
+  s.v_st = r.v_st;
+  s.posb = gp(r.pos + b * r.pos_sb);
+  return s;
+}
+
+// One Beta group of 128-feature rows per 16-lane row, one load batch: the
+// group's rows, weights and metadata are loaded together, the screened cut
+// decides from the held rows and the side means are written from them.
+// Returns false (nothing written) when the screen does not settle the cut.
+__device__ __forceinline__ bool beta_row_group_held(const LadderArgs& c, const RowsArgs& r, const Workspace& ws,
+                                                    const RowPlan& pp, int ell, int gi, bool live) {
+  const int l16 = lane_id() & 15, mi = l16 & 3;
+  const int n_pair = 2 * carries_of(pp.cnt, pp.m, c.slots, false);
+  const int start = 4 * gi;
+  const int width = max(0, min(4, n_pair - start));
+  const Ladder lad = ladder_of(c, pp.ladder);
+  const int64_t base = static_cast<int64_t>(ell) * c.slots;
+  GroupRows g;
+  Meta mine{};
+  if (pp.flush_src) {
+    const PoolT<2> pool{lad, base, pp.cnt, flush_rows_planned(c, r, ws, pp)};
+    group_rows<2>(pool, start, width, g);
+    if (l16 < 8 && mi < width) mine = pool.meta(start + mi);
+  } else {
+    const PoolT<1> pool{lad, base, pp.cnt, staged_of(ws, pp.ladder, ell, c.dk, c.dv)};
+    group_rows<1>(pool, start, width, g);
+    if (l16 < 8 && mi < width) mine = pool.meta(start + mi);
+  }
+  Rows8 held;
+  load_rows8(g, l16, width, held);
+  int cut = 2;
+  if (width == 4) {
+    const float total = fmaxf(((g.w[0] + g.w[1]) + g.w[2]) + g.w[3], 1e-12f);
+    float sk[9], sv[9];
+    screen_sums8(held.k, sk);
+    screen_sums8(held.v, sv);
+    cut = screened_cut(sk, sv, g.w, total);
+  }
+  const bool settled = cut != 0;
+  cut = settled ? cut : 2;
+  const bool emit = live && settled;
+  double rl;
+  {
+    float wl[4], wrt[4];
+    cut_weights(g.w, cut, wl, wrt);
+    rl = 1.0 / static_cast<double>(fmaxf(l16 == 0 ? side_mass(wl) : side_mass(wrt), 1e-12f));
+  }
+  const int dest = start / 2;
+  const Soa out = carry_of(ws, pp.ladder, ell, c.dk, c.dv);
+  const double left_rcp = row_lane_d(rl, 0), right_rcp = row_lane_d(rl, 1);
+  const unsigned left_rows = (1u << cut) - 1u;
+#pragma unroll
+  for (int comp = 0; comp < 2; ++comp) {
+    LOGKV_G uint16_t* dst = comp == 0 ? out.k : out.v;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      if (emit && (side == 0 || width == 4))
+        side_out8(comp == 0 ? held.k : held.v, g.w, side == 0 ? left_rows : (0xfu & ~left_rows),
+                  side == 0 ? left_rcp : right_rcp, dst + static_cast<int64_t>(dest + side) * 128 + 8 * l16);
+    }
+  }
+  {
+    const int side = (l16 >> 2) & 1;
+    const unsigned member = side == 0 ? left_rows : (0xfu & ~left_rows);
+    float wt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wt[i] = ((member >> i) & 1u) ? g.w[i] : 0.f;
+    const float mass = side_mass(wt);
+    const bool in_side = mi < width && ((member >> mi) & 1u);
+    const Meta res = side_meta(mine, in_side, mass);
+    if (emit && l16 < 8 && (l16 & 3) == 0 && (side == 0 || width == 4)) put_soa_meta(out, dest + side, res);
+  }
+  return settled;
+}
+
 // Beta carries launch `ell`: the level's units in consecutive quads, one quad
 // per wave step (a wave's quads are contiguous); each lane finds its row's
-// ladder by binary search once, then walks forward.
+// ladder by binary search once, then walks forward. FULL (128-feature rows):
+// a lane keeps its ladder's plan values while its quads stay on that ladder,
+// a group is one load batch (rows, weights, metadata) decided by the screen
+// and written from the held rows, and the groups the screen leaves open are
+// evaluated canonically by beta_group, one at a time on the whole wave (so
+// the rare path's registers stay out of the screened one's).
 template <int NJ, bool FULL>
 __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderArgs c, RowsArgs r, Workspace ws, int ell) {
   extern __shared__ __align__(16) int32_t prefix_s[];
@@ -1511,12 +1593,50 @@ __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderAr
       len -= half;
     }
   }
-  for (; qd < qd_end; ++qd) {
-    const int unit = 4 * qd + row;
-    const bool live = unit < total;
-    const int uu = live ? unit : total - 1;
-    while (prefix_s[ladder + 1] <= uu) ++ladder;
-    beta_row_group<NJ, FULL>(c, r, ws, ladder, ell, uu - prefix_s[ladder], live);
+  if constexpr (FULL) {
+    RowPlan pp;
+    pp.ladder = -1;
+    for (; qd < qd_end; ++qd) {
+      const int unit = 4 * qd + row;
+      const bool live = unit < total;
+      const int uu = live ? unit : total - 1;
+      while (prefix_s[ladder + 1] <= uu) ++ladder;
+      if (ladder != pp.ladder) load_row_plan(ws, ladder, ell, pp);
+      const int gi = uu - prefix_s[ladder];
+      const bool settled = beta_row_group_held(c, r, ws, pp, ell, gi, live);
+      // Groups the screen leaves open (near ties, non-finite costs, tiny
+      // masses): the canonical evaluation, one group at a time on the whole wave.
+      uint64_t open = __ballot(live && !settled && (lane_id() & 15) == 0);
+      while (open) {
+        const int src = __builtin_ctzll(open);
+        open &= open - 1;
+        RowPlan q;
+        q.ladder = __shfl(pp.ladder, src, kWave);
+        q.cnt = __shfl(pp.cnt, src, kWave);
+        q.m = __shfl(pp.m, src, kWave);
+        q.flush_src = __shfl(static_cast<int>(pp.flush_src), src, kWave) != 0;
+        q.first = __shfl(pp.first, src, kWave);
+        q.order_base = __shfl(pp.order_base, src, kWave);
+        const int qgi = __shfl(gi, src, kWave);
+        const int n_pair = 2 * carries_of(q.cnt, q.m, c.slots, false);
+        const Ladder lad = ladder_of(c, q.ladder);
+        const int64_t base = static_cast<int64_t>(ell) * c.slots;
+        const Soa out = carry_of(ws, q.ladder, ell, c.dk, c.dv);
+        if (q.flush_src)
+          beta_group<NJ, 2>(PoolT<2>{lad, base, q.cnt, flush_rows_planned(c, r, ws, q)}, out, n_pair, qgi, c.dk, c.dv);
+        else
+          beta_group<NJ, 1>(PoolT<1>{lad, base, q.cnt, staged_of(ws, q.ladder, ell, c.dk, c.dv)}, out, n_pair, qgi,
+                            c.dk, c.dv);
+      }
+    }
+  } else {
+    for (; qd < qd_end; ++qd) {
+      const int unit = 4 * qd + row;
+      const bool live = unit < total;
+      const int uu = live ? unit : total - 1;
+      while (prefix_s[ladder + 1] <= uu) ++ladder;
+      beta_row_group<NJ>(c, r, ws, ladder, ell, uu - prefix_s[ladder], live);
+    }
   }
 }
 
