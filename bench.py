@@ -45,6 +45,7 @@ import json
 import math
 import os
 import platform
+import re
 import sys
 import time
 import traceback
@@ -364,6 +365,22 @@ class FlushMeter:
         return out
 
 
+STEP_TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "flush_step_traffic_28layer_stacked_qwen3_1.7b.md"
+
+
+def profiled_step_traffic():
+    """HBM bytes of one headline step as the committed FETCH_SIZE / WRITE_SIZE counter runs of
+    ``--profile-flush`` measured them (the profile's "traffic ... MB per step" line), or (None, None)."""
+    try:
+        text = STEP_TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None, None
+    m = re.search(r"traffic ([0-9.]+) MB per step", text)
+    if not m:
+        return None, None
+    return float(m.group(1)) * 1e6, f"profiles/{STEP_TRAFFIC_PROFILE.name} (rocprofv3 FETCH_SIZE + WRITE_SIZE runs)"
+
+
 def flush_workload(args, torch, np):
     from logkv_amd.log_kv_pack import _decode_capacity, _launch_pack, packed_dim, readout_view
     from workloads import rope_tables
@@ -548,6 +565,9 @@ def flush_workload(args, torch, np):
     achieved = gbs(step_bytes, step_ms)
     stages = {k: {"bytes": stage_bytes[k], "ms": stage_ms[k], "achieved": gbs(stage_bytes[k], stage_ms[k]),
                   "frac": gbs(stage_bytes[k], stage_ms[k]) / HBM_PEAK_GBS} for k in stage_bytes}
+    traffic, traffic_source = args.step_traffic, "--step-traffic" if args.step_traffic else None
+    if traffic is None:
+        traffic, traffic_source = profiled_step_traffic()
     return {
         "value": tokens / timed["elapsed"],
         "ms_per_step": timed["elapsed"] / args.steps * 1e3,
@@ -566,7 +586,7 @@ def flush_workload(args, torch, np):
                                "for all layers)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": args.step_traffic,
+                     "traffic": traffic, "traffic_source": traffic_source,
                      "algorithmic_bytes_per_launch": step_bytes, "avg_launch_ms": step_ms,
                      "launches": len(timed["step_ms"]),
                      "timing": "HIP events around each timed step on its stream",
@@ -716,25 +736,27 @@ def decode_workload(args, torch, np):
     def attention_only():
         return packed_attention(q_s, ka, va, plan, tail, scale, 1, D, G, workspace, cache.alpha_count_dev)[0]
 
-    def replayed_ms(fn, reps=64):
+    def replayed_ms(fn, per_graph=8, replays=8):
+        # per_graph calls captured back to back in one graph (as a model's layers issue them), the
+        # graph replayed `replays` times; ms per call.
         eager = fn()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            out = fn()
+            outs = [fn() for _ in range(per_graph)]
         graph.replay()
         torch.cuda.synchronize()
-        if not torch.equal(out, eager):
+        if not all(torch.equal(o, eager) for o in outs):
             raise RuntimeError("graph replay of the decode step differs from the eager call")
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ev[0].record(stream)
-        for _ in range(reps):
+        for _ in range(replays):
             graph.replay()
         ev[1].record(stream)
         torch.cuda.synchronize()
-        if not torch.equal(out, eager):
+        if not all(torch.equal(o, eager) for o in outs):
             raise RuntimeError("graph replay of the decode step differs from the eager call")
-        return ev[0].elapsed_time(ev[1]) / reps
+        return ev[0].elapsed_time(ev[1]) / (per_graph * replays)
 
     step_ms = replayed_ms(full_step)
     attn_ms = replayed_ms(attention_only)
@@ -758,13 +780,15 @@ def decode_workload(args, torch, np):
                     "of every token pair), launched from Python",
         "ms_per_token": eng_ms, "ms_per_token_28_layers": 28 * eng_ms, "steps": steps,
         "device_ms_per_token": step_ms,
-        "device_ms_per_token_note": "one step's pack + attention replayed from a HIP graph (no host work)",
+        "device_ms_per_token_note": "one step's pack + attention, 8 steps captured back to back in a HIP graph and "
+                                    "replayed 8 times (no host work)",
         "packed_rows_per_lane": rows, "pooled_width": width,
         "roofline": {"kernel": "stream_kernel + combine_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": attn_bytes, "bytes_per_packed_row": row_bytes,
                      "avg_launch_ms": attn_ms,
-                     "timing": "64 back-to-back replays of one step's attention launches (HIP graph)"},
+                     "timing": "HIP events around 8 replays of a HIP graph holding 8 back-to-back attention calls "
+                               "(stream_kernel + combine_kernel each)"},
     }
 
 
