@@ -74,6 +74,9 @@ typedef struct logkv_route_params {
                          * a cluster keeps at most hard_cap_rows - n_total of its direct rows (offset order)
                          * and orphans fill the nearest cluster with room (attach route only) */
   int32_t hard_cap_rows; /* int(cap), the truncated cap the rooms count against */
+  int32_t merge_passes;  /* unified route: matching passes per budget-stage round (semantic_merge_passes); > 1 adds
+                          * frozen-center sweeps (litgpt/log_kv_cache.py:561-588, :3314), 0 or 1 none. The attach
+                          * route ignores it */
 } logkv_route_params;
 
 const char* logkv_last_error(void);

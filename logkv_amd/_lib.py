@@ -43,7 +43,7 @@ class RowsView(C.Structure):
 class RouteParams(C.Structure):
     _fields_ = [("eta", C.c_float), ("g0", C.c_float), ("lam", C.c_float),
                 ("late_joins", _i32), ("beta_merge", _i32), ("center_tile", _i32), ("hard_cap", C.c_float),
-                ("hard_cap_rows", _i32)]
+                ("hard_cap_rows", _i32), ("merge_passes", _i32)]
 
 
 class RecentArgs(C.Structure):

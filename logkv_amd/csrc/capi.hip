@@ -200,6 +200,7 @@ int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late,
   b.live = reinterpret_cast<int16_t*>(take(lanes * M * 6));
   if (stats_offset) *stats_offset = off;
   b.stats = reinterpret_cast<int32_t*>(take(lanes * 2 * logkv::kStatsInts * 4));
+  b.restricted = reinterpret_cast<uint64_t*>(take(lanes * M * 8));
   if (u) *u = b;
   return off;
 }
@@ -296,9 +297,11 @@ int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* ro
   if (workspace_bytes < need)
     return fail(LOGKV_EINVAL, "workspace of %lld bytes is smaller than the %lld required", (long long)workspace_bytes,
                 (long long)need);
+  if (params->merge_passes < 0) return fail(LOGKV_EINVAL, "merge_passes must be >= 0 (0 or 1: one matching pass)");
   logkv::UnifiedBufs u{};
   unified_layout(cache, rows->tokens, params->late_joins ? 1 : 0, static_cast<uint8_t*>(workspace), &u);
   u.limit = limits;
+  u.passes = params->merge_passes > 1 ? params->merge_passes : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = rows->tokens ? logkv::launch_unified_plan(*cache, *rows, u, ws, s) : LOGKV_OK;
   if (!rc) rc = logkv::launch_unified_summary(*cache, u, summary, rows->tokens, s);

@@ -28,6 +28,8 @@ constexpr int kReduceThreads = 1024;
 constexpr int kReduceWaves = kReduceThreads / kWave;
 constexpr uint64_t kInfKey = 0x7F800000ull << 32;
 constexpr uint8_t kAlive = 1, kValid = 2, kKeep = 4, kMerged = 8, kRejected = 16, kDirty = 32;
+// Frozen-center sweeps: in a pair of the round (or its partner), and the lower row of a sweep's pair.
+constexpr uint8_t kMatched = 64, kSweep = 128;
 
 __device__ __forceinline__ uint64_t pack_cost(float cost, int key) {
   const uint32_t bits = cost == 0.f ? 0u : __float_as_uint(cost);
@@ -182,6 +184,28 @@ __device__ uint64_t scan_row(const ReduceLds& s, const float* dist, int M, int n
     best = k < best ? k : best;
   }
   return wave_min_u64(best);
+}
+
+// Packed minimum of row r over the columns not matched this round (a matched
+// column takes mass 0, litgpt/log_kv_cache.py:473-488 with `excluded`), for
+// the budget stage's frozen-center sweeps (no radius limit).
+__device__ uint64_t scan_row_unmatched(const ReduceLds& s, const float* dist, int M, int n, int r) {
+  const float mr = s.mass[r];
+  uint64_t best = kInfKey;
+  const float* row = dist + static_cast<int64_t>(r) * M;
+  for (int c = lane_id(); c < n; c += kWave) {
+    const float mc = (s.flags[c] & kMatched) ? 0.f : s.mass[c];
+    const float cost = ward_cost<false>(row[c], mr, mc, 0.f, 0.f, 0.f, c != r);
+    const uint64_t k = pack_cost(cost, r ^ c);
+    best = k < best ? k : best;
+  }
+  return wave_min_u64(best);
+}
+
+// Partner named by a packed row minimum (the low word is row ^ col).
+__device__ __forceinline__ int key_partner(uint64_t k, int r, int M) {
+  const int p = static_cast<int>(static_cast<uint32_t>(k) ^ static_cast<uint32_t>(r));
+  return p < 0 ? 0 : (p > M - 1 ? M - 1 : p);
 }
 
 }  // namespace
@@ -402,9 +426,82 @@ __device__ inline ReduceLds image_of(const ReduceArgs& a, int lane) {
 
 // Proposals .. merges of one round on state `s` (the block's LDS). Returns the
 // round's merge count; sh[0] = count, sh[1] = ntrace on entry and exit.
+// Frozen-center sweeps of a budget round (litgpt/log_kv_cache.py:561-588),
+// after the round's mutual proposals (kValid): the proposals and their
+// partners are matched; per pass, the unmatched rows whose restricted partner
+// is matched rescan the unmatched columns (restricted minima in
+// a.restricted, starting as the cached ones, which stay untouched), then the
+// unmatched rows whose restricted minima name each other (finite) pair up:
+// the lower row takes kValid | kSweep and its mate in pair_of. Up to
+// passes - 1 passes; a pass that adds no pair ends them (a later pass would
+// rescan nothing). Every row's mate is left in pair_of (its cached partner
+// unless a sweep paired it). Returns the pairs added; *scans gets the rows
+// rescanned.
+__device__ int frozen_sweeps(const ReduceLds& s, const ReduceArgs& a, int lane, int n, int* scans) {
+  __shared__ int s_added, s_scans;
+  const int M = a.M, t = threadIdx.x, l = lane_id(), w = wave_id();
+  const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  uint64_t* restricted = a.restricted + static_cast<int64_t>(lane) * M;
+  for (int r = t; r < n; r += kReduceThreads) {
+    restricted[r] = s.packed[r];
+    s.pair_of[r] = s.best[r];
+    if (s.flags[r] & kValid) {
+      s.flags[r] |= kMatched;
+      s.flags[s.best[r]] |= kMatched;
+    }
+  }
+  if (t == 0) {
+    s_added = 0;
+    s_scans = 0;
+  }
+  __syncthreads();
+  int total = 0;
+  for (int pass = 1; pass < a.passes; ++pass) {
+    for (int r = w; r < n; r += kReduceWaves) {
+      const uint8_t fl = s.flags[r];
+      if (!(fl & kAlive) || (fl & kMatched)) continue;
+      if (!(s.flags[key_partner(restricted[r], r, M)] & kMatched)) continue;
+      const uint64_t k = scan_row_unmatched(s, dist, M, n, r);
+      if (l == 0) {
+        restricted[r] = k;
+        atomicAdd(&s_scans, 1);
+      }
+    }
+    __syncthreads();
+    for (int r = t; r < n; r += kReduceThreads) {
+      const uint8_t fl = s.flags[r];
+      if (!(fl & kAlive) || (fl & kMatched)) continue;
+      const uint64_t k = restricted[r];
+      const int p = key_partner(k, r, M);
+      if (r < p && key_partner(restricted[p], p, M) == r && key_cost(k) < __builtin_inff() &&
+          !(s.flags[p] & kMatched))
+        s.flags[r] = fl | kSweep;
+    }
+    __syncthreads();
+    for (int r = t; r < n; r += kReduceThreads) {
+      const uint8_t fl = s.flags[r];
+      if ((fl & kSweep) && !(fl & kMatched)) {
+        const int p = key_partner(restricted[r], r, M);
+        s.flags[r] = fl | kMatched | kValid;
+        s.flags[p] |= kMatched;
+        s.pair_of[r] = static_cast<int16_t>(p);
+        atomicAdd(&s_added, 1);
+      }
+    }
+    __syncthreads();
+    const int added = s_added - total;
+    total = s_added;
+    __syncthreads();
+    if (added == 0) break;
+  }
+  *scans = s_scans;
+  __syncthreads();
+  return total;
+}
+
 template <bool LIMIT>
 __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, int n, float limit, int* sh,
-                           int* s_nprop, int* s_nvalid, int& nprop_out, int& n_ok_out) {
+                           int* s_nprop, int* s_nvalid, int& nprop_out, int& n_ok_out, int& sweep_scans) {
   const int M = a.M, D = a.D, t = threadIdx.x, l = lane_id(), w = wave_id();
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   float* mu = a.mu + static_cast<int64_t>(lane) * M * D;
@@ -465,11 +562,20 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
     }
     __syncthreads();
   }
-  // Surviving proposals sorted by (cost, row) (a stable argsort by cost).
+  // Frozen-center sweeps (budget stage, passes > 1): more pairs of the round.
+  const bool sweeps = !LIMIT && a.passes > 1;
+  int extra = 0;
+  sweep_scans = 0;
+  if (sweeps) extra = frozen_sweeps(s, a, lane, n, &sweep_scans);
+  const uint64_t* restricted = sweeps ? a.restricted + static_cast<int64_t>(lane) * M : nullptr;
+  // Surviving proposals sorted by (cost, row) (a stable argsort by cost); a
+  // sweep's pair is priced by its restricted minimum.
   for (int r = t; r < n; r += kReduceThreads) {
-    if (s.flags[r] & kValid) {
+    const uint8_t fl = s.flags[r];
+    if (fl & kValid) {
       const int at = atomicAdd(s_nvalid, 1);
-      s.keys[at] = (s.packed[r] & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
+      const uint64_t k = (fl & kSweep) ? restricted[r] : s.packed[r];
+      s.keys[at] = (k & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
     }
   }
   __syncthreads();
@@ -498,7 +604,7 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
   // Merges: centers (one wave per merge, lanes over the features), then pair
   // scalars, masses and radii (litgpt/log_kv_cache.py:589-606).
   for (int p = w; p < n_ok; p += kReduceWaves) {
-    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = sweeps ? s.pair_of[ra] : s.best[ra];
     const float ma = s.mass[ra], mb = s.mass[rb];
     const float total = ma + mb;
     const float scale = total < 1.f ? 1.f : total;
@@ -508,7 +614,10 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
   }
   __syncthreads();
   for (int p = t; p < n_ok; p += kReduceThreads) {
-    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = s.best[ra];
+    const int ra = static_cast<int>(s.keys[p] & 0xFFFFFFFFu), rb = sweeps ? s.pair_of[ra] : s.best[ra];
+    // A kept row's best names its mate from here on (the Lance-Williams phase
+    // reads it); the dirty rule reads the best of rows that are not kept.
+    s.best[ra] = static_cast<int16_t>(rb);
     const float ma = s.mass[ra], mb = s.mass[rb];
     const float dab = dist[static_cast<int64_t>(ra) * M + rb];
     const float total = ma + mb;
@@ -526,7 +635,7 @@ __device__ void plan_phase(const ReduceLds& s, const ReduceArgs& a, int lane, in
     trace[2 * (sh[1] + p) + 1] = rb;
   }
   __syncthreads();
-  nprop_out = nprop;
+  nprop_out = nprop + extra;
   n_ok_out = n_ok;
 }
 
@@ -638,8 +747,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
   }
   __syncthreads();
   const ReduceLds s = carve_lds(dyn, M);
-  int nprop, n_ok;
-  plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok);
+  int nprop, n_ok, sweep_scans;
+  plan_phase<LIMIT>(s, a, lane, n, LIMIT ? a.limit[lane] : 0.f, sh, &s_nprop, &s_nvalid, nprop, n_ok, sweep_scans);
   for (int p = t; p < n_ok; p += kReduceThreads) s.packed[static_cast<int>(s.keys[p] & 0xFFFFFFFFu)] = kInfKey;
   // The live rows after the merges, ascending (the columns the Lance-Williams
   // and rescan phases visit: a dead column's key is never a minimum), the
@@ -713,7 +822,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_plan_kernel(ReduceArgs 
     ctl.n_live = s_live;
     ctl.n_dirty = s_dirty;
     ctl.lw_elems += n_ok * s_live;
-    ctl.scan_elems += s_dirty * s_live;
+    ctl.scan_elems += s_dirty * s_live + sweep_scans * (count + n_ok);   // sweeps scan before the merges
     if (ctl.rounds >= 2 * M + 7) ctl.active = 0;
     a.ctl[lane] = ctl;
   }
@@ -909,8 +1018,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
   float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
   const float limit = LIMIT ? a.limit[lane] : 0.f;
   while (ctl.active) {
-    int nprop, n_ok;
-    plan_phase<LIMIT>(s, a, lane, n, limit, sh, &s_nprop, &s_nvalid, nprop, n_ok);
+    int nprop, n_ok, sweep_scans;
+    plan_phase<LIMIT>(s, a, lane, n, limit, sh, &s_nprop, &s_nvalid, nprop, n_ok, sweep_scans);
     if (t == 0) s_rescans = 0;
     for (int p = w; p < n_ok; p += kReduceWaves) {
       const uint64_t rmin = lw_columns<LIMIT>(s, dist, M, n, p, 0, n, limit);
@@ -926,6 +1035,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_finish_kernel(ReduceArg
       }
     }
     __syncthreads();
+    ctl.scan_elems += sweep_scans * ctl.count;
     const int count = ctl.count - n_ok;
     const bool remaining = count > a.target;
     ctl.lw_elems += n_ok * count;
@@ -967,6 +1077,8 @@ int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
     return refuse("unified reducer: a workspace buffer of the stage is NULL");
   if (a.image_stride < static_cast<int64_t>(reduce_lds_bytes(a.M)))
     return refuse("unified reducer: the per-lane state image is smaller than the reducer's LDS layout");
+  if (!LIMIT && a.passes > 1 && !a.restricted)
+    return refuse("unified reducer: frozen-center sweeps without their restricted-minimum buffer");
   const size_t lds = reduce_lds_bytes(a.M);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_plan_kernel<LIMIT>), lds) ||
       !allow_dynamic_lds(reinterpret_cast<const void*>(&reduce_finish_kernel<LIMIT>), lds))
@@ -1162,7 +1274,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
                      c.n_groups, u);
   if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
-                u.image, u.image_stride, u.ctl, u.live, u.stats, 2 * kStatsInts};
+                u.image, u.image_stride, u.ctl, u.live, u.stats, 2 * kStatsInts, 1, nullptr};
   if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
   const size_t lab_lds = static_cast<size_t>(M) * 8;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
@@ -1173,7 +1285,7 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
   ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
                 u.bound, u.image, u.image_stride, u.ctl, u.live, u.stats ? u.stats + kStatsInts : nullptr,
-                2 * kStatsInts};
+                2 * kStatsInts, u.passes, u.restricted};
   if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
                      M, u.label2, u.n_roots2);

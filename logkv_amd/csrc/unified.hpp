@@ -49,6 +49,8 @@ struct ReduceArgs {
                           // (ctl.n_dirty) and kept rows (ctl.n_ok), each list ascending
   int32_t* stats;         // [lanes, stats_stride] the stage's counts (kStatsInts), or NULL
   int32_t stats_stride;
+  int32_t passes;         // matching passes per round: > 1 adds frozen-center sweeps (no radius limit only)
+  uint64_t* restricted;   // [lanes, M] the sweeps' restricted row minima (passes > 1)
 };
 
 // Device buffers of one unified plan (carved from the caller's workspace).
@@ -84,6 +86,8 @@ struct UnifiedBufs {
   LaneCtl* ctl;           // [lanes]
   int16_t* live;          // [lanes, 3, M]
   int32_t* stats;         // [lanes, 2, kStatsInts] each stage's counts
+  uint64_t* restricted;   // [lanes, M] the budget stage's restricted row minima (frozen-center sweeps)
+  int32_t passes;         // matching passes per budget round (semantic_merge_passes)
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,

@@ -240,8 +240,6 @@ class LogStructuredKVCache(nn.Module):
         unsupported = []
         if not semantic_clusters or cluster_k_max <= 1:
             unsupported.append("semantic_clusters with cluster_k_max > 1")
-        if semantic_unified_route and semantic_merge_passes != 1:
-            unsupported.append("semantic_merge_passes=1 with the unified route (frozen-center sweeps)")
         if semantic_legacy_route or semantic_cluster_chunk_size:
             unsupported.append("attach routing (no legacy / chunk-tree route)")
         if semantic_capacity_beta:
@@ -277,7 +275,7 @@ class LogStructuredKVCache(nn.Module):
         self.semantic_centroid_backend = semantic_centroid_backend
         self.semantic_replay_updates = bool(semantic_replay_updates)
         self.semantic_unified_route = bool(semantic_unified_route)
-        self.semantic_merge_passes = int(semantic_merge_passes)
+        self._merge_passes = int(semantic_merge_passes)
         self.semantic_capacity_beta = 0.0
         self.semantic_capacity_hard_cap_mult = cap_mult
         self.semantic_legacy_route = False
@@ -382,7 +380,8 @@ class LogStructuredKVCache(nn.Module):
                                    1 if self.alpha_exact_tokens else 0, 1 if self.beta_adaptive_merge else 0,
                                    _CENTER_TILES[self._centroid_backend],
                                    cap if cap != math.inf else 0.0,   # stored as float32
-                                   min(int(cap), 2**31 - 1) if cap != math.inf else 0)
+                                   min(int(cap), 2**31 - 1) if cap != math.inf else 0,
+                                   self._merge_passes)
         self.op_log: torch.Tensor | None = None
         self.op_log_len: torch.Tensor | None = None
         self._op_replay_cursor_host = None
@@ -1101,6 +1100,21 @@ class LogStructuredKVCache(nn.Module):
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand
     # ------------------------------------------------------------------
+    @property
+    def semantic_merge_passes(self) -> int:
+        """Matching passes per budget round of the unified route (litgpt/log_kv_cache.py:3314): more than
+        one adds frozen-center sweeps (:561-588). Read by every later unified flush."""
+        return self._merge_passes
+
+    @semantic_merge_passes.setter
+    def semantic_merge_passes(self, value: int) -> None:
+        value = int(value)
+        if value < 1:
+            raise ValueError("semantic_merge_passes must be >= 1")
+        self._merge_passes = value
+        if "_params" in self.__dict__:
+            self._params.merge_passes = value
+
     @property
     def semantic_centroid_backend(self) -> str:
         """Order of a center's new-key sum: "sequential" (one row at a time in position order) or

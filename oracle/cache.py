@@ -59,7 +59,7 @@ class OracleCache:
     def __init__(self, batch, groups, max_seq, dk, dv, *, B=128, recent_size=2048, K=12, lam=1.0, eta=1.0,
                  g0=2048.0, s_h=1.0, flush=2048, exact_tokens=0, span_max=64, beta_novelty=False,
                  beta_adaptive=False, cos=None, sin=None, table_bf16=False, unified=False, centroid_tile=1,
-                 hard_cap_mult=0.0):
+                 hard_cap_mult=0.0, merge_passes=1):
         self.batch, self.groups, self.max_seq, self.dk, self.dv = batch, groups, max_seq, dk, dv
         self.K, self.lam, self.eta, self.g0 = K, lam, eta, g0
         self.B, self.L, *_ = budget(batch, groups, max_seq, dk, dv, B, K, exact_tokens)
@@ -109,6 +109,7 @@ class OracleCache:
         self.late_joins = 0       # delayed-archive re-sorts performed (test coverage evidence)
         self.op_log = None        # per lane lists of (op, cluster, arg, position), see oracle.oplog
         self.unified = unified    # the unified Ward / radius route (oracle.unified) instead of attach
+        self.merge_passes = int(merge_passes)   # frozen-center sweeps per budget round (unified route)
         self.ward_merges = 0      # old-old merges performed by the unified route (test coverage evidence)
         self.replay_cursor = None
 

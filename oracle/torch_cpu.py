@@ -382,10 +382,12 @@ class TorchReducer:
         self.trace.extend(zip(a.tolist(), b.tolist()))
 
 
-def reduce(mu, mass, count, limit, target, strict=False, gram=False):
+def reduce(mu, mass, count, limit, target, strict=False, gram=False, passes=1):
     """``oracle.unified.reduce`` with ``TorchReducer``: (survivors, trace, centers) as numpy. ``gram``:
     initial distances in the reference's Gram form above 32 nodes (``gram_distances``), else the
-    canonical differences."""
+    canonical differences. Frozen-center sweeps (``passes > 1``) are not restated here."""
+    if passes > 1 and limit is None:
+        raise NotImplementedError("the Torch-CPU reducer restates one matching pass per round")
     if count <= target:
         return np.arange(count), [], f32(mu).copy()
     mu_t = torch.from_numpy(np.ascontiguousarray(f32(mu)))

@@ -80,12 +80,17 @@ def clamp0(x):
 
 
 class Reducer:
-    """One lane's incremental rounds (litgpt/log_kv_cache.py:448-637)."""
+    """One lane's incremental rounds (litgpt/log_kv_cache.py:448-637). With
+    ``passes > 1`` (the budget stage only) a round also runs frozen-center
+    sweeps (:561-588): rows whose restricted partner was matched rescan the
+    unmatched columns, unmatched mutual pairs join the round, and every pair
+    of the round is budgeted by cost."""
 
-    def __init__(self, dist, mu, mass, count, limit, target):
+    def __init__(self, dist, mu, mass, count, limit, target, passes=1):
         self.dist, self.mu, self.mass = f32(dist).copy(), f32(mu).copy(), f32(mass).copy()
         self.limit = None if limit is None else np.float32(limit)
         self.target = int(target)
+        self.passes = max(1, int(passes))
         size = self.mass.shape[0]
         self.ids = np.arange(size)
         self.alive = self.ids < count
@@ -101,9 +106,12 @@ class Reducer:
         # Lance-Williams updates, rescanned rows x live columns (the first scan: every row).
         self.rounds, self.lw_elems, self.scan_elems = 0, 0, len(rows) * len(rows)
 
-    def _scan(self, rows):
+    def _scan(self, rows, excluded=None):
+        """Packed row minima (litgpt/log_kv_cache.py:473-488); ``excluded`` columns (matched
+        this round) take no mass."""
         lim = self.limit is not None
-        cost, _ = pair_cost(self.dist[rows], self.mass[rows][:, None], self.mass[None, :],
+        mass = self.mass if excluded is None else np.where(excluded, np.float32(0), self.mass).astype(np.float32)
+        cost, _ = pair_cost(self.dist[rows], self.mass[rows][:, None], mass[None, :],
                             self.radius[rows][:, None] if lim else None, self.radius[None, :] if lim else None,
                             self.limit, self.ids[None, :] != rows[:, None])
         return pack(cost, rows[:, None] ^ self.ids[None, :]).min(1)
@@ -136,11 +144,15 @@ class Reducer:
             bound = np.zeros(size, np.float32)
             bound[rows] = verified
         pair = np.where(valid, cost, INF).astype(np.float32)
+        mate = best
+        if self.passes > 1:
+            mate, pair, extra = self._sweeps(valid, best, pair)
+            nprop += extra
         order = np.argsort(pair, kind="stable")[:size // 2]
         ok = pair[order] < INF
         ok &= np.cumsum(ok) <= self.count - self.target
         a = order[ok]
-        b = best[a]
+        b = mate[a]
         keep = np.zeros(size, bool)
         merged = np.zeros(size, bool)
         if len(a):
@@ -158,6 +170,36 @@ class Reducer:
         if remaining and nprop == 0:
             self.stuck = True
         return remaining and nprop > 0
+
+    def _sweeps(self, valid, best, pair):
+        """Frozen-center sweeps after the round's mutual pairs (litgpt/log_kv_cache.py:561-588):
+        returns each row's mate, the pair costs (at a pair's lower row) and the pairs added."""
+        size = self.mass.shape[0]
+        ids = self.ids
+        matched = np.zeros(size, bool)
+        rows = np.flatnonzero(valid)
+        matched[rows] = True
+        matched[best[rows]] = True
+        restricted = self.packed.copy()
+        mate, extra = best.copy(), 0
+        pair = pair.copy()
+        for _ in range(self.passes - 1):
+            partner = np.clip(((restricted & LOW).astype(np.int64)) ^ ids, 0, size - 1)
+            rows = np.flatnonzero(self.alive & ~matched & matched[partner])
+            if len(rows):
+                restricted[rows] = self._scan(rows, excluded=matched)
+                self.scan_elems += len(rows) * int(self.alive.sum())
+            partner = np.clip(((restricted & LOW).astype(np.int64)) ^ ids, 0, size - 1)
+            cost = (restricted >> np.uint64(32)).astype(np.uint32).view(np.float32)
+            more = (self.alive & ~matched & (ids < partner) & (partner[partner] == ids) & (cost < INF)
+                    & ~matched[partner])
+            extra += int(more.sum())
+            rows = np.flatnonzero(more)
+            matched[rows] = True
+            matched[partner[rows]] = True
+            mate = np.where(more, partner, mate)
+            pair = np.where(more, cost, pair).astype(np.float32)
+        return mate, pair, extra
 
     def _merge(self, a, b, bound, keep, merged):
         size = self.mass.shape[0]
@@ -212,16 +254,17 @@ class Reducer:
         self.trace.extend(zip(a.tolist(), b.tolist()))
 
 
-def reduce(mu, mass, count, limit, target, strict=False, counts=None):
+def reduce(mu, mass, count, limit, target, strict=False, counts=None, passes=1):
     """Rounds until no mutual pair is left or ``count <= target``
     (litgpt/log_kv_cache.py:3303-3376). Returns (survivors, trace, centers).
     ``counts``: a list that gets the stage's (nodes, rounds, merges,
-    Lance-Williams elements, rescanned elements)."""
+    Lance-Williams elements, rescanned elements). ``passes``: frozen-center
+    sweeps per round, used only without a radius limit (:3314)."""
     if count <= target:
         if counts is not None:
             counts.append((count, 0, 0, 0, 0))
         return np.arange(count), [], f32(mu).copy()
-    r = Reducer(pair_distances(mu), mu, mass, count, limit, target)
+    r = Reducer(pair_distances(mu), mu, mass, count, limit, target, passes if limit is None else 1)
     size = r.mass.shape[0]
     for _ in range(2 * size + 7):
         if not r.step():
@@ -315,7 +358,9 @@ def plan_lane(cache, keys, n, b, g, reduce_fn=reduce):
                               np.bincount(lab1, minlength=len(surv1)).astype(np.float32)))
     centers = np.concatenate((cache.centroid[b, g, old].astype(np.float32), mu1[surv1]))
     m2 = len(weights)
-    surv2, trace2, _ = reduce_fn(centers, weights, m2, None, cache.K, strict=True)
+    passes = getattr(cache, "merge_passes", 1)
+    extra = {"passes": passes} if passes > 1 else {}
+    surv2, trace2, _ = reduce_fn(centers, weights, m2, None, cache.K, strict=True, **extra)
     lab2 = labels(m2, surv2, trace2)
     jobs = [(int(old[a]), int(old[c])) for a, c in trace2 if c < len(old)]
     root = lab2[len(old) + lab1]

@@ -13,7 +13,7 @@ from workloads import Mixture, rope_tables
 pytestmark = pytest.mark.gpu
 
 
-def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False):
+def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False, passes=1):
     from logkv_amd import LogStructuredKVCache
     from oracle import OracleCache
 
@@ -22,11 +22,11 @@ def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False
         (batch, groups, max_seq, dim), (batch, groups, max_seq, dim), B=B, recent_size=T, device="cuda",
         dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=s_h,
         semantic_flush_granularity=T, semantic_anchor_mode="mid", allocate_second_order=False,
-        semantic_unified_route=True, semantic_merge_passes=1, cos_cache=cos, sin_cache=sin, rope_n_elem=dim,
+        semantic_unified_route=True, semantic_merge_passes=passes, cos_cache=cos, sin_cache=sin, rope_n_elem=dim,
         alpha_exact_tokens=exact, alpha_span_max_tokens=span, beta_novelty=beta, beta_adaptive_merge=beta)
     ora = OracleCache(batch, groups, max_seq, dim, dim, B=B, recent_size=T, K=K, s_h=s_h, flush=T,
                       exact_tokens=exact, span_max=span, beta_novelty=beta, beta_adaptive=beta,
-                      cos=cos.numpy(), sin=sin.numpy(), unified=True)
+                      cos=cos.numpy(), sin=sin.numpy(), unified=True, merge_passes=passes)
     return gpu, ora
 
 
@@ -38,11 +38,14 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("passes", [1, 4])
 @pytest.mark.parametrize("name", list(CASES))
-def test_unified_route_matches_oracle(name):
+def test_unified_route_matches_oracle(name, passes):
+    """``passes`` 4: the budget stage's frozen-center sweeps (semantic_merge_passes, the reference's
+    evaluation setting for the mid anchor)."""
     batch, groups, dim, K, B, T, n, s_h, exact, beta, drift = CASES[name]
-    print(f"case {name}", flush=True)
-    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h, exact=exact, beta=beta)
+    print(f"case {name}, merge passes {passes}", flush=True)
+    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h, exact=exact, beta=beta, passes=passes)
     mix = Mixture(batch, groups, dim, clusters=K + 2, seed=17, drift_every=drift)
     dev = gpu.level_k.device
     for i in range(n):
@@ -83,15 +86,16 @@ def test_old_old_merge_frees_a_cluster():
     assert ora.n_total[0, 0].tolist() == [4, 4]
 
 
+@pytest.mark.parametrize("passes", [1, 4])
 @pytest.mark.parametrize("scale", [1.0, 2.0])
-def test_lattice_ties_and_radius_edge(scale):
+def test_lattice_ties_and_radius_edge(scale, passes):
     """Rows on a binary lattice: duplicates (zero distances), many exactly
     equal costs, and with s_h = 1 (radius limit 1) singleton pairs at squared
     distance 4 whose radius bound equals the limit exactly, so the rescan
     screen's border and tie cases decide real rows."""
-    print(f"case lattice scale {scale}", flush=True)
+    print(f"case lattice scale {scale}, merge passes {passes}", flush=True)
     dim, T, K = 16, 64, 4
-    gpu, ora = _pair(2, 2, dim, K, 8, T, T * 6, 1.0)
+    gpu, ora = _pair(2, 2, dim, K, 8, T, T * 6, 1.0, passes=passes)
     g = torch.Generator().manual_seed(int(scale * 10))
     dev = gpu.level_k.device
     for i in range(4):
@@ -107,15 +111,17 @@ def test_lattice_ties_and_radius_edge(scale):
         assert not bad, f"flush {i}: " + "; ".join(bad)
 
 
-def test_reducer_counts_match_oracle():
+@pytest.mark.parametrize("passes", [1, 4])
+def test_reducer_counts_match_oracle(passes):
     """The device reducer's work counts of each flush (``unified_reduce_stats``: per lane and stage the
     nodes, rounds, merges, Lance-Williams and rescanned elements - the byte model of the unified
-    roofline) equal the oracle reducer's on the same inputs."""
+    roofline; with sweeps, their restricted rescans too) equal the oracle reducer's on the same
+    inputs."""
     from oracle import unified as U
 
     batch, groups, dim, K, B, T, n, s_h = 1, 2, 128, 12, 16, 256, 4, 64.0
-    print("case reducer counts", flush=True)
-    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h)
+    print(f"case reducer counts, merge passes {passes}", flush=True)
+    gpu, ora = _pair(batch, groups, dim, K, B, T, T * (n + 2), s_h, passes=passes)
     mix = Mixture(batch, groups, dim, clusters=K + 2, seed=19, drift_every=512)
     dev = gpu.level_k.device
     for i in range(n):

@@ -11,6 +11,13 @@
 * the incremental rounds equal a full recompute (centers and distances rebuilt
   from scratch every round) on separated data, as the reference states
   (litgpt/log_kv_cache.py:449-455);
+* frozen-center sweeps (``merge_passes > 1``, the budget stage): a round's
+  pairs equal an independent peeling of the cost matrix (per pass each row's
+  minimum under the ``row ^ col`` tie rule, mutual pairs taken, their rows
+  and columns struck; the reference's own test oracle,
+  tests/test_log_kv_unified.py:503-526) on its integer data, and the
+  incremental rounds equal full-recompute peeling rounds in float64 on
+  distinct random costs (tests/test_log_kv_unified.py:690-706);
 * labels and the Ward entry order on hand-built cases;
 * route invariants: at most K live clusters, every row accounted for once,
   n_total equal to the ladder mass, each candidate's rows within the radius
@@ -84,6 +91,88 @@ def test_incremental_rounds_equal_full_recompute(seed, limit):
         runs.append((np.flatnonzero(r.alive).tolist(), r.trace))
     assert runs[0] == runs[1]
     assert len(runs[0][1]) > 10
+
+
+def _peel_pairs(cost, passes):
+    """Frozen-center matching restated from the reference test's peeling oracle: per pass every row's
+    least cost (ties to the least row ^ col), the mutual pairs taken and their rows and columns
+    struck; the pairs sorted by (cost, lower row)."""
+    n = cost.shape[0]
+    remaining = cost.copy()
+    chosen = []
+    for _ in range(passes):
+        best = np.full(n, -1)
+        for i in range(n):
+            m = remaining[i].min()
+            if np.isfinite(m):
+                cands = np.flatnonzero(remaining[i] == m)
+                best[i] = min(cands, key=lambda j: i ^ j)
+        pairs = [(i, int(best[i])) for i in range(n) if best[i] > i and best[best[i]] == i]
+        chosen.extend(pairs)
+        for i, j in pairs:
+            remaining[[i, j], :] = np.inf
+            remaining[:, [i, j]] = np.inf
+    return sorted(chosen, key=lambda p: (cost[p], p[0]))
+
+
+def _ward_costs(mu, mass):
+    d2 = ((mu[:, None, :] - mu[None, :, :]) ** 2).sum(-1)
+    cost = d2 * (mass[:, None] * mass[None, :] / np.maximum(mass[:, None] + mass[None, :], 1))
+    cost[~((mass > 0)[:, None] & (mass > 0)[None, :])] = np.inf
+    np.fill_diagonal(cost, np.inf)
+    return cost
+
+
+def test_frozen_center_sweeps_match_peeling():
+    rng = np.random.default_rng(98)
+    mu = rng.integers(-4, 5, (3, 65, 8)).astype(np.float32)
+    mu[0] = 0                                   # every cost 0: the tie rule alone pairs the rows
+    mass = np.ones((3, 65), np.float32)
+    mass[1, 51:] = 0                            # massless rows take no pair
+    mass[2] = 0
+    extra = 0
+    for lane in range(3):
+        cost = _ward_costs(mu[lane].astype(np.float64), mass[lane].astype(np.float64))
+        want = _peel_pairs(cost, 4)
+        r = U.Reducer(U.pair_distances(mu[lane]), mu[lane], mass[lane], 65, None, 1, passes=4)
+        r.step()
+        assert r.trace == want, f"lane {lane}"
+        one = U.Reducer(U.pair_distances(mu[lane]), mu[lane], mass[lane], 65, None, 1)
+        one.step()
+        assert one.trace == _peel_pairs(cost, 1), f"lane {lane}, one pass"
+        extra += len(r.trace) - len(one.trace)
+        assert len({x for pair in r.trace for x in pair}) == 2 * len(r.trace)
+    assert extra > 0, "the sweeps added no pair"
+
+
+def _peel_reduce(x, w, target, passes):
+    """Full-recompute rounds in float64: each round the Ward costs of the live clusters' centers,
+    the peeled pairs budgeted by cost (count - target), merged in that order."""
+    mu, mass = x.astype(np.float64).copy(), w.astype(np.float64).copy()
+    trace = []
+    for _ in range(4 * len(w)):
+        count = int((mass > 0).sum())
+        pairs = _peel_pairs(_ward_costs(mu, mass), passes)[:max(count - target, 0)]
+        if not pairs:
+            break
+        for a, b in pairs:
+            total = mass[a] + mass[b]
+            mu[a] = (mass[a] * mu[a] + mass[b] * mu[b]) / max(total, 1)
+            mass[a], mass[b] = total, 0
+            trace.append((a, b))
+    return np.flatnonzero(mass > 0).tolist(), trace
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_frozen_sweep_rounds_equal_full_recompute(seed):
+    rng = np.random.default_rng(223 + seed)
+    for i, n in enumerate((70, 33, 5, 90)):
+        w = rng.integers(1, 4, n).astype(np.float32)
+        x = (rng.standard_normal((n, 8)) * (i + 1)).astype(np.float32)
+        surv, trace, _ = U.reduce(x, w, n, None, 4, passes=4)
+        want_surv, want_trace = _peel_reduce(x, w, 4, 4)
+        assert surv.tolist() == want_surv and trace == want_trace, f"n={n}"
+        assert len(surv) == min(n, 4)
 
 
 def test_labels_and_ward_entry_order():
