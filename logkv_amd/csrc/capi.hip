@@ -126,8 +126,6 @@ int carve(const logkv_ladder_view* c, const logkv_rows_view* r, const logkv_rout
     return fail(LOGKV_EINVAL, "center_tile must be 0, 1 or %d", logkv::kCenterTile);
   if (std::isnan(prm->hard_cap) || (prm->hard_cap > 0.f && prm->hard_cap_rows < 0))
     return fail(LOGKV_EINVAL, "hard_cap must not be NaN and hard_cap_rows must be >= 0");
-  if (ward && prm->hard_cap > 0.f)
-    return fail(LOGKV_EINVAL, "the unified route takes no capacity cap");
   const int late = prm->late_joins ? 1 : 0;
   if (late && int64_t(c->levels) * c->slots + r->tokens > logkv::kMaxOrderRows)
     return fail(LOGKV_EINVAL, "delayed archive sort needs L*B' + T <= %d", logkv::kMaxOrderRows);
@@ -201,6 +199,17 @@ int64_t unified_layout(const logkv_ladder_view* c, int32_t tokens, int32_t late,
   if (stats_offset) *stats_offset = off;
   b.stats = reinterpret_cast<int32_t*>(take(lanes * 2 * logkv::kStatsInts * 4));
   b.restricted = reinterpret_cast<uint64_t*>(take(lanes * M * 8));
+  for (int s = 0; s < 2; ++s) {
+    b.cmu[s] = reinterpret_cast<float*>(take(lanes * M * D * 4));
+    b.cmass[s] = reinterpret_cast<float*>(take(lanes * M * 4));
+    b.crad[s] = reinterpret_cast<float*>(take(lanes * M * 4));
+    b.croot[s] = reinterpret_cast<int32_t*>(take(lanes * M * 4));
+  }
+  b.n_cur = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.cbuf = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.dcount = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.rounds = reinterpret_cast<int32_t*>(take(lanes * 4));
+  b.keys = reinterpret_cast<uint64_t*>(take(lanes * M * 16));
   if (u) *u = b;
   return off;
 }
@@ -302,6 +311,7 @@ int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* ro
   unified_layout(cache, rows->tokens, params->late_joins ? 1 : 0, static_cast<uint8_t*>(workspace), &u);
   u.limit = limits;
   u.passes = params->merge_passes > 1 ? params->merge_passes : 1;
+  u.cap = params->hard_cap > 0.f ? params->hard_cap : 0.f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = rows->tokens ? logkv::launch_unified_plan(*cache, *rows, u, ws, s) : LOGKV_OK;
   if (!rc) rc = logkv::launch_unified_summary(*cache, u, summary, rows->tokens, s);

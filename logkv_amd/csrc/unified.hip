@@ -17,6 +17,8 @@
 // the reference's float32 order (_unified_pair_cost, _merge); the initial
 // squared distances and the radius check's exact distances are canonical
 // wave sums of squared differences (common.hpp).
+#include <vector>
+
 #include "route.hpp"
 #include "unified.hpp"
 
@@ -1096,6 +1098,342 @@ int launch_reduce(const ReduceArgs& a, int lanes, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
+// ---------------------------------------------------------------------------
+// Full-recompute rounds of a capacity-capped unified route
+// (litgpt/log_kv_cache.py:3445-3519; pairs :3067-3117 in the unfused form;
+// merges _semantic_unified_merge_pack :3134-3156). Each round prices the
+// current nodes afresh: their squared distances (dist_kernel, the canonical
+// sums), every row's least cost with the radius bound (candidate stage) and
+// without pairs whose total mass exceeds the cap, mutual minima with the
+// row ^ col tie rule in (cost, row) order; in the budget stage a lane with no
+// capped pair takes its uncapped ones. Candidate pairs are re-checked from
+// their exact distances. The first count - target pairs merge into their lower
+// rows (mass-weighted centers, summed masses, the pair's radius bound) and the
+// survivors are compacted in order, so row indices, and with them the ties,
+// are those of the compacted nodes. The host polls the lanes between batches of
+// rounds (a round with no pair, or at the target, ends a lane).
+constexpr int kRoundPoll = 8;   // rounds enqueued between the host's polls
+
+// Cost of a pair of current nodes (round_pairs' order: Ward cost, radius
+// bound > limit -> +inf); the capped cost is +inf too when the total mass
+// exceeds the cap.
+template <bool LIMIT>
+__device__ __forceinline__ void round_cost(float d2, float mi, float mj, float ri, float rj, float limit, float cap,
+                                           bool valid, float& cost, float& capped) {
+  const float total = mi + mj;
+  const float denom = total < 1.f ? 1.f : total;
+  valid = valid && mi > 0.f && mj > 0.f;
+  cost = valid ? d2 * (mi * mj / denom) : __builtin_inff();
+  if (LIMIT) {
+    const float distance = sqrtf(d2);
+    const float x = ri + (mj / denom) * distance, y = rj + (mi / denom) * distance;
+    if ((x < y ? y : x) > limit) cost = __builtin_inff();
+  }
+  capped = total > cap ? __builtin_inff() : cost;
+}
+
+__global__ __launch_bounds__(kPhaseThreads) void rounds_init_kernel(RoundArgs a) {
+  const int lane = blockIdx.y, M = a.M, D = a.D;
+  const int n = a.count[lane];
+  for (int i = blockIdx.x * kPhaseThreads + threadIdx.x; i < M; i += gridDim.x * kPhaseThreads) {
+    const int64_t at = static_cast<int64_t>(lane) * M + i;
+    a.cmass[0][at] = i < n ? a.mass[at] : 0.f;
+    a.crad[0][at] = 0.f;
+    a.croot[0][at] = i;
+    if (i < n)
+      for (int d = 0; d < D; ++d) a.cmu[0][at * D + d] = a.mu[at * D + d];
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    a.n_cur[lane] = n;
+    a.cbuf[lane] = 0;
+    a.dcount[lane] = n > a.target ? n : 0;
+    a.n_trace[lane] = 0;
+    a.stuck[lane] = 0;
+    a.rounds[lane] = 0;
+  }
+}
+
+// Every current row's least capped and uncapped keys (one wave per row).
+template <bool LIMIT>
+__global__ __launch_bounds__(kPhaseThreads) void rounds_min_kernel(RoundArgs a, int src) {
+  const int lane = blockIdx.y, M = a.M, n = a.dcount[lane];
+  if (n == 0) return;
+  const float limit = LIMIT ? a.limit[lane] : 0.f;
+  const float* mass = a.cmass[src] + static_cast<int64_t>(lane) * M;
+  const float* rad = a.crad[src] + static_cast<int64_t>(lane) * M;
+  const float* dist = a.dist + static_cast<int64_t>(lane) * M * M;
+  for (int r = blockIdx.x * kPhaseWaves + wave_id(); r < n; r += gridDim.x * kPhaseWaves) {
+    const float mr = mass[r], rr = rad[r];
+    uint64_t kc = kInfKey, ka = kInfKey;
+    for (int c = lane_id(); c < n; c += kWave) {
+      float cost, capped;
+      round_cost<LIMIT>(dist[static_cast<int64_t>(r) * M + c], mr, mass[c], rr, rad[c], limit, a.cap, c != r, cost,
+                        capped);
+      const uint64_t k1 = pack_cost(capped, r ^ c), k2 = pack_cost(cost, r ^ c);
+      kc = k1 < kc ? k1 : kc;
+      ka = k2 < ka ? k2 : ka;
+    }
+    kc = wave_min_u64(kc);
+    ka = wave_min_u64(ka);
+    if (lane_id() == 0) {
+      a.keys[(static_cast<int64_t>(lane) * M + r) * 2] = kc;
+      a.keys[(static_cast<int64_t>(lane) * M + r) * 2 + 1] = ka;
+    }
+  }
+}
+
+// One round of a lane on one block: pairs, budget, merges into the other
+// buffer set, compaction, trace.
+template <bool LIMIT>
+__global__ __launch_bounds__(kReduceThreads) void rounds_pair_kernel(RoundArgs a, int src) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  __shared__ int s_nprop, s_nkeep, s_n, part_s[kReduceWaves];
+  const int lane = blockIdx.x, M = a.M, D = a.D, t = threadIdx.x, l = lane_id(), w = wave_id();
+  const int n = a.dcount[lane];
+  if (n == 0) return;
+  const int dst = src ^ 1;
+  const int64_t lm = static_cast<int64_t>(lane) * M;
+  const float* mu = a.cmu[src] + lm * D;
+  const float* mass = a.cmass[src] + lm;
+  const float* rad = a.crad[src] + lm;
+  const int32_t* root = a.croot[src] + lm;
+  const uint64_t* keys = a.keys + lm * 2;
+  // LDS: sort keys [P2], partner [M], new index [M], exact distance of a kept pair [M / 2 + 1].
+  const int P2 = pow2_at_least(half_up(M) > 0 ? half_up(M) : 1);
+  uint64_t* sk = reinterpret_cast<uint64_t*>(dyn);
+  int16_t* partner = reinterpret_cast<int16_t*>(sk + P2);
+  int16_t* nidx = partner + M;
+  float* pdist = reinterpret_cast<float*>(nidx + M);
+  auto key_of = [&](int r, int which) { return keys[2 * r + which]; };
+  auto mate = [&](uint64_t k, int r) { return key_partner(k, r, M); };
+  // Capped proposals (the lower row of each mutual pair); none: the uncapped ones (budget stage).
+  int which = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (t == 0) s_nprop = 0;
+    __syncthreads();
+    for (int r = t; r < n; r += kReduceThreads) {
+      const uint64_t k = key_of(r, which);
+      const int b = mate(k, r);
+      if (r < b && mate(key_of(b, which), b) == r && key_cost(k) < __builtin_inff()) {
+        const int at = atomicAdd(&s_nprop, 1);
+        sk[at] = (k & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(r);
+      }
+    }
+    __syncthreads();
+    if (s_nprop > 0 || !a.strict || which == 1) break;
+    which = 1;
+  }
+  const int nv = s_nprop;
+  const int width = pow2_at_least(nv > 0 ? nv : 1);
+  for (int i = nv + t; i < width; i += kReduceThreads) sk[i] = ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= width; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < width; i += kReduceThreads) {
+        const int p = i ^ stride;
+        if (p > i) {
+          const bool up = (i & size) == 0;
+          const uint64_t x = sk[i], y = sk[p];
+          if ((x > y) == up) {
+            sk[i] = y;
+            sk[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // Candidate stage: each pair's bound from its exact distance (one wave per pair); a pair that
+  // fails is marked (top bit of its key) and skipped in place.
+  for (int p = w; LIMIT && p < nv; p += kReduceWaves) {
+    const int ra = static_cast<int>(sk[p] & 0xFFFFFFFFu), rb = mate(key_of(ra, which), ra);
+    float acc = 0.f;
+    for (int q = 0; q * kWave < D; ++q) {
+      const int d = l + q * kWave;
+      const float diff = (d < D ? mu[static_cast<int64_t>(ra) * D + d] : 0.f) -
+                         (d < D ? mu[static_cast<int64_t>(rb) * D + d] : 0.f);
+      acc = q == 0 ? diff * diff : acc + diff * diff;
+    }
+    const float exact = sqrtf(wave_sum0(acc));
+    if (l == 0) {
+      pdist[p] = exact;
+      const float ma = mass[ra], mb = mass[rb];
+      const float sum = ma + mb;
+      const float den = sum < 1.f ? 1.f : sum;
+      const float x = rad[ra] + mb / den * exact, y = rad[rb] + ma / den * exact;
+      if ((x < y ? y : x) > a.limit[lane]) sk[p] |= 0x8000000000000000ull;   // rejected
+    }
+  }
+  __syncthreads();
+  // Kept pairs in order: the first count - target that passed (a rejected pair keeps its place and
+  // takes no budget).
+  if (t == 0) {
+    const int budget = n - a.target;
+    int kept = 0;
+    for (int p = 0; p < nv; ++p) {
+      const bool ok = !(sk[p] >> 63) && kept < budget;
+      if (ok) ++kept;
+      else sk[p] |= 0x8000000000000000ull;
+    }
+    s_nkeep = kept;
+  }
+  for (int r = t; r < n; r += kReduceThreads) partner[r] = -1;
+  __syncthreads();
+  const int nk = s_nkeep;
+  // Each kept pair marks its rows: the lower row gets the pair's index, the other is retired.
+  for (int p = t; p < nv; p += kReduceThreads) {
+    if (sk[p] >> 63) continue;
+    const int ra = static_cast<int>(sk[p] & 0xFFFFFFFFu), rb = mate(key_of(ra, which), ra);
+    partner[ra] = static_cast<int16_t>(p);      // pair index of a kept lower row
+    partner[rb] = static_cast<int16_t>(-2);     // retired
+  }
+  __syncthreads();
+  // Trace in kept order (input ids), by one thread (nk is at most n / 2).
+  if (t == 0) {
+    int32_t* tr = a.trace + lm * 2;
+    int at = a.n_trace[lane];
+    for (int p = 0; p < nv; ++p) {
+      if (sk[p] >> 63) continue;
+      const int ra = static_cast<int>(sk[p] & 0xFFFFFFFFu), rb = mate(key_of(ra, which), ra);
+      tr[2 * at] = root[ra];
+      tr[2 * at + 1] = root[rb];
+      ++at;
+    }
+    a.n_trace[lane] = at;
+  }
+  // New indices of the survivors (ballot prefix sums, row order).
+  if (t == 0) s_n = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < n; c0 += kReduceThreads) {
+    const int r = c0 + t;
+    const bool on = r < n && partner[r] != -2;
+    const uint64_t mask = __ballot(on);
+    if (l == 0) part_s[w] = __popcll(mask);
+    __syncthreads();
+    int base = s_n;
+    for (int q = 0; q < w; ++q) base += part_s[q];
+    if (on) nidx[r] = static_cast<int16_t>(base + __popcll(mask & ((1ull << l) - 1ull)));
+    __syncthreads();
+    if (t == 0) {
+      int total = 0;
+      for (int q = 0; q < kReduceWaves; ++q) total += part_s[q];
+      s_n += total;
+    }
+    __syncthreads();
+  }
+  const int n_new = s_n;
+  // Survivors into the other buffer set: a kept lower row merges (one wave per row).
+  float* omu = a.cmu[dst] + lm * D;
+  for (int r = w; r < n; r += kReduceWaves) {
+    const int pr = partner[r];
+    if (pr == -2) continue;
+    const int i = nidx[r];
+    const int64_t o = lm + i;
+    if (pr < 0) {
+      for (int d = l; d < D; d += kWave) omu[static_cast<int64_t>(i) * D + d] = mu[static_cast<int64_t>(r) * D + d];
+      if (l == 0) {
+        a.cmass[dst][o] = mass[r];
+        a.crad[dst][o] = LIMIT ? rad[r] : 0.f;
+        a.croot[dst][o] = root[r];
+      }
+      continue;
+    }
+    const int rb = mate(key_of(r, which), r);
+    const float ma = mass[r], mb = mass[rb];
+    const float comb = ma + mb;
+    const float scale = comb < 1.f ? 1.f : comb;
+    for (int d = l; d < D; d += kWave)
+      omu[static_cast<int64_t>(i) * D + d] =
+          (ma * mu[static_cast<int64_t>(r) * D + d] + mb * mu[static_cast<int64_t>(rb) * D + d]) / scale;
+    if (l == 0) {
+      a.cmass[dst][o] = comb;
+      if (LIMIT) {
+        const float dd = pdist[pr];
+        const float x = rad[r] + mb / scale * dd, y = rad[rb] + ma / scale * dd;
+        a.crad[dst][o] = x < y ? y : x;
+      } else {
+        a.crad[dst][o] = 0.f;
+      }
+      a.croot[dst][o] = root[r];
+    }
+  }
+  for (int i = n_new + t; i < M; i += kReduceThreads) a.cmass[dst][lm + i] = 0.f;
+  if (t == 0) {
+    a.n_cur[lane] = n_new;
+    a.cbuf[lane] = dst;
+    const bool more = nk > 0 && n_new > a.target;
+    a.dcount[lane] = more ? n_new : 0;
+    a.rounds[lane] += 1;
+    if (nk == 0 && a.strict && n > a.target) a.stuck[lane] = 1;
+  }
+}
+
+// The stage's outputs in the incremental reducer's form: survivors by input
+// id, their final centers at their input rows, merge count, stuck flag.
+__global__ __launch_bounds__(kPhaseThreads) void rounds_finish_kernel(RoundArgs a) {
+  const int lane = blockIdx.x, M = a.M, D = a.D, t = threadIdx.x;
+  const int64_t lm = static_cast<int64_t>(lane) * M;
+  const int n = a.n_cur[lane];
+  const int src = a.cbuf[lane];   // the buffer set of the lane's last round
+  for (int i = t; i < M; i += kPhaseThreads) a.alive_out[lm + i] = 0;
+  __syncthreads();
+  for (int i = t; i < n; i += kPhaseThreads) {
+    const int r = a.croot[src][lm + i];
+    a.alive_out[lm + r] = 1;
+    for (int d = 0; d < D; ++d) a.mu[(lm + r) * D + d] = a.cmu[src][(lm + i) * D + d];
+  }
+  if (t == 0 && a.stats) {
+    int32_t* st = a.stats + lane * static_cast<int64_t>(a.stats_stride);
+    st[0] = a.count[lane];
+    st[1] = a.rounds[lane];
+    st[2] = a.n_trace[lane];
+    st[3] = 0;
+    st[4] = 0;
+    st[5] = a.stuck[lane];
+  }
+}
+
+size_t rounds_pair_lds(int M) {
+  const int P2 = pow2_at_least(half_up(M) > 0 ? half_up(M) : 1);
+  return static_cast<size_t>(P2) * 8 + static_cast<size_t>(M) * 4 + static_cast<size_t>(half_up(M) + 1) * 4 + 16;
+}
+
+// One stage of full-recompute rounds; the host reads the lanes' round flags
+// after every kRoundPoll rounds (the stream is synchronized there).
+template <bool LIMIT>
+int launch_rounds(const RoundArgs& a, int lanes, hipStream_t stream) {
+  if (!a.mu || !a.mass || !a.count || (LIMIT && !a.limit) || !a.n_cur || !a.dcount || !a.cbuf || !a.keys || !a.dist ||
+      !a.alive_out || !a.trace || !a.n_trace || !a.stuck || !a.rounds)
+    return refuse("unified rounds: a workspace buffer of the stage is NULL");
+  for (int s = 0; s < 2; ++s)
+    if (!a.cmu[s] || !a.cmass[s] || !a.crad[s] || !a.croot[s])
+      return refuse("unified rounds: a node buffer of the stage is NULL");
+  const size_t lds = rounds_pair_lds(a.M);
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&rounds_pair_kernel<LIMIT>), lds)) return LOGKV_ERUNTIME;
+  hipLaunchKernelGGL(rounds_init_kernel, dim3(std::max(1, std::min(16, a.M / kPhaseThreads)), lanes),
+                     dim3(kPhaseThreads), 0, stream, a);
+  std::vector<int32_t> host(lanes);
+  int src = 0;
+  for (int round = 0; round < 2 * a.M + 8; ++round) {
+    if (round > 0 && round % kRoundPoll == 0) {
+      if (hipMemcpyAsync(host.data(), a.dcount, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, stream) !=
+              hipSuccess ||
+          hipStreamSynchronize(stream) != hipSuccess)
+        return LOGKV_ERUNTIME;
+      bool any = false;
+      for (int32_t v : host) any = any || v > 0;
+      if (!any) break;
+    }
+    int rc = launch_dist(a.cmu[src], a.dcount, a.dist, a.M, a.D, lanes, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(rounds_min_kernel<LIMIT>, dim3(kPhaseBlocks, lanes), dim3(kPhaseThreads), 0, stream, a, src);
+    hipLaunchKernelGGL(rounds_pair_kernel<LIMIT>, dim3(lanes), dim3(kReduceThreads), lds, stream, a, src);
+    src ^= 1;
+  }
+  hipLaunchKernelGGL(rounds_finish_kernel, dim3(lanes), dim3(kPhaseThreads), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
+}
+
 // Leaf -> compact surviving row (litgpt/log_kv_cache.py:3553-3568): parents
 // from the trace, pointer jumping to the roots, roots numbered in order.
 __global__ __launch_bounds__(1024) void labels_kernel(const uint8_t* __restrict__ alive, const int32_t* __restrict__ trace,
@@ -1272,21 +1610,46 @@ int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBuf
   if (rc) return rc;
   hipLaunchKernelGGL(load_nodes_kernel, dim3(std::max(1, std::min(64, M * D / 4096)), lanes), dim3(256), 0, stream, r,
                      c.n_groups, u);
-  if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
-  ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1, u.bound,
-                u.image, u.image_stride, u.ctl, u.live, u.stats, 2 * kStatsInts, 1, nullptr};
-  if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
+  // A capacity cap runs the full-recompute rounds (litgpt/log_kv_cache.py:3283-3288), else the
+  // incremental reducer.
+  const bool capped = u.cap > 0.f;
+  auto rounds_args = [&](float* mu, const float* mass, const int32_t* count, const float* limit, int target,
+                         int strict, uint8_t* alive, int32_t* trace, int32_t* n_trace, int32_t* stuck,
+                         int32_t* stats) {
+    return RoundArgs{mu, mass, count, limit, target, M, D, strict, u.cap,
+                     {u.cmu[0], u.cmu[1]}, {u.cmass[0], u.cmass[1]}, {u.crad[0], u.crad[1]},
+                     {u.croot[0], u.croot[1]}, u.n_cur, u.cbuf, u.dcount, u.keys, u.dist, alive, trace, n_trace,
+                     stuck, u.rounds, stats, 2 * kStatsInts};
+  };
+  if (capped) {
+    if ((rc = launch_rounds<true>(rounds_args(u.mu1, u.mass1, u.count1, u.limit, 1, 0, u.alive1, u.trace1,
+                                              u.n_trace1, u.stuck1, u.stats),
+                                  lanes, stream)))
+      return rc;
+  } else {
+    if ((rc = launch_dist(u.mu1, u.count1, u.dist, M, D, lanes, stream))) return rc;
+    ReduceArgs a1{u.dist, u.mu1, u.mass1, u.count1, u.limit, 1, M, D, u.alive1, u.trace1, u.n_trace1, u.stuck1,
+                  u.bound, u.image, u.image_stride, u.ctl, u.live, u.stats, 2 * kStatsInts, 1, nullptr};
+    if ((rc = launch_reduce<true>(a1, lanes, stream))) return rc;
+  }
   const size_t lab_lds = static_cast<size_t>(M) * 8;
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&labels_kernel), lab_lds)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive1, u.trace1, u.n_trace1, u.count1,
                      M, u.label1, u.n_roots1);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&stage2_kernel), lab_lds)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(stage2_kernel, dim3(lanes), dim3(256), lab_lds, stream, c, u);
-  if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
-  ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2, u.stuck2,
-                u.bound, u.image, u.image_stride, u.ctl, u.live, u.stats ? u.stats + kStatsInts : nullptr,
-                2 * kStatsInts, u.passes, u.restricted};
-  if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
+  if (capped) {
+    if ((rc = launch_rounds<false>(rounds_args(u.mu2, u.mass2, u.count2, nullptr, c.k_max, 1, u.alive2, u.trace2,
+                                               u.n_trace2, u.stuck2, u.stats ? u.stats + kStatsInts : nullptr),
+                                   lanes, stream)))
+      return rc;
+  } else {
+    if ((rc = launch_dist(u.mu2, u.count2, u.dist, M, D, lanes, stream))) return rc;
+    ReduceArgs a2{u.dist, u.mu2, u.mass2, u.count2, nullptr, c.k_max, M, D, u.alive2, u.trace2, u.n_trace2,
+                  u.stuck2, u.bound, u.image, u.image_stride, u.ctl, u.live, u.stats ? u.stats + kStatsInts : nullptr,
+                  2 * kStatsInts, u.passes, u.restricted};
+    if ((rc = launch_reduce<false>(a2, lanes, stream))) return rc;
+  }
   hipLaunchKernelGGL(labels_kernel, dim3(lanes), dim3(1024), lab_lds, stream, u.alive2, u.trace2, u.n_trace2, u.count2,
                      M, u.label2, u.n_roots2);
   hipLaunchKernelGGL(final_kernel, dim3(lanes), dim3(256), 0, stream, c, r, u, ws.order, ws.assign);

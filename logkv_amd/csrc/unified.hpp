@@ -53,6 +53,36 @@ struct ReduceArgs {
   uint64_t* restricted;   // [lanes, M] the sweeps' restricted row minima (passes > 1)
 };
 
+// Full-recompute rounds of one reducer stage (a capacity-capped route): the
+// stage's input and outputs as ReduceArgs names them, the cap, and the
+// compacted node state, which alternates between two buffer sets round by
+// round.
+struct RoundArgs {
+  float* mu;              // [lanes, M, D] the stage's nodes; the survivors' rows get their final centers
+  const float* mass;      // [lanes, M]
+  const int32_t* count;   // [lanes]
+  const float* limit;     // [lanes] radius limit (the candidate stage), or NULL
+  int32_t target, M, D, strict;   // strict: a lane with no pair above the target may take uncapped pairs,
+                                  // and ends stuck (an error) if none is left either
+  float cap;              // total-mass cap of a pair (> 0)
+  float* cmu[2];          // [lanes, M, D] compacted centers
+  float* cmass[2];        // [lanes, M]
+  float* crad[2];         // [lanes, M] radius bounds (candidate stage)
+  int32_t* croot[2];      // [lanes, M] the compacted rows' input ids
+  int32_t* n_cur;         // [lanes] compacted nodes now
+  int32_t* cbuf;          // [lanes] the buffer set holding the lane's nodes (its last round's output)
+  int32_t* dcount;        // [lanes] n_cur of a lane with rounds to go, else 0 (the distance launch's count)
+  uint64_t* keys;         // [lanes, M, 2] each row's least capped and uncapped packed cost
+  float* dist;            // [lanes, M, M]
+  uint8_t* alive_out;     // [lanes, M] survivors by input id
+  int32_t* trace;         // [lanes, M, 2] merges in input ids, round by round, each round in cost order
+  int32_t* n_trace;       // [lanes]
+  int32_t* stuck;         // [lanes]
+  int32_t* rounds;        // [lanes] rounds run
+  int32_t* stats;         // [lanes, stats_stride] the stage's counts (kStatsInts), or NULL
+  int32_t stats_stride;
+};
+
 // Device buffers of one unified plan (carved from the caller's workspace).
 struct UnifiedBufs {
   int32_t M, D;
@@ -88,6 +118,16 @@ struct UnifiedBufs {
   int32_t* stats;         // [lanes, 2, kStatsInts] each stage's counts
   uint64_t* restricted;   // [lanes, M] the budget stage's restricted row minima (frozen-center sweeps)
   int32_t passes;         // matching passes per budget round (semantic_merge_passes)
+  float cap;              // > 0: the capacity cap of a merged pair's mass (full-recompute rounds)
+  float* cmu[2];          // full-recompute rounds' compacted node state (see RoundArgs)
+  float* cmass[2];
+  float* crad[2];
+  int32_t* croot[2];
+  int32_t* n_cur;
+  int32_t* cbuf;
+  int32_t* dcount;
+  uint64_t* keys;         // [lanes, M, 2]
+  int32_t* rounds;        // [lanes]
 };
 
 int launch_unified_plan(const LadderArgs& c, const RowsArgs& r, const UnifiedBufs& u, const Workspace& ws,

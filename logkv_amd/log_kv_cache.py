@@ -244,8 +244,6 @@ class LogStructuredKVCache(nn.Module):
             unsupported.append("attach routing (no legacy / chunk-tree route)")
         if semantic_capacity_beta:
             unsupported.append("no capacity penalty")
-        if semantic_unified_route and semantic_capacity_hard_cap_mult:
-            unsupported.append("no hard cap with the unified route (its capped full-recompute reducer)")
         if (seg_gap_max is not None and math.isfinite(seg_gap_max)) or seg_block_level:
             unsupported.append("no segment gaps or padding")
         if semantic_anchor_mode != "mid":

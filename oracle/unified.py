@@ -29,6 +29,7 @@ radius check's squared distance likewise.
 
 from __future__ import annotations
 
+import functools
 import math
 
 import numpy as np
@@ -276,6 +277,114 @@ def reduce(mu, mass, count, limit, target, strict=False, counts=None, passes=1):
     return np.flatnonzero(r.alive), r.trace, r.mu
 
 
+def mutual_pairs(cost):
+    """Disjoint mutual-minimum pairs of a cost matrix (litgpt/log_kv_cache.py:2988-3016): each row's
+    least cost, ties to the least ``row ^ col``; a pair is named by its lower row, the pairs in
+    (cost, row) order. Returns [(left, right, cost)]."""
+    n = cost.shape[0]
+    ids = np.arange(n)
+    best_cost = cost.min(1) if n else np.zeros(0, np.float32)
+    tie = ids[:, None] ^ ids[None, :]
+    best = np.where(cost == best_cost[:, None], tie, 2 * n).argmin(1) if n else ids
+    valid = (ids < best) & (best[best] == ids) & np.isfinite(best_cost)
+    rows = np.flatnonzero(valid)
+    order = rows[np.argsort(best_cost[rows], kind="stable")]
+    return [(int(r), int(best[r]), best_cost[r]) for r in order]
+
+
+def round_pairs(mu, mass, radius, limit, cap, overflow):
+    """One full-recompute round's pairs over the current nodes (litgpt/log_kv_cache.py:3067-3117, the
+    unfused form): Ward costs, with a limit the radius bound, with a finite cap no pair whose total
+    mass exceeds it (``overflow``: a lane left with no capped pair takes the uncapped ones); mutual
+    minima in (cost, row) order; with a limit each pair's bound re-checked from its exact distance
+    and the pairs that fail dropped."""
+    n = len(mass)
+    d2 = pair_distances(mu)
+    mi, mj = mass[:, None], mass[None, :]
+    total = (mi + mj).astype(np.float32)
+    denom = np.maximum(total, np.float32(1))
+    cost = (d2 * (mi * mj / denom)).astype(np.float32)
+    live = mass > 0
+    cost = np.where(live[:, None] & live[None, :], cost, INF).astype(np.float32)
+    np.fill_diagonal(cost, INF)
+    if limit is not None:
+        distance = np.sqrt(d2)
+        bound = np.maximum(radius[:, None] + (mj / denom) * distance, radius[None, :] + (mi / denom) * distance)
+        cost = np.where(bound > limit, INF, cost).astype(np.float32)
+    capped = np.isfinite(cap)
+    pairs = mutual_pairs(np.where(total > cap, INF, cost).astype(np.float32) if capped else cost)
+    if overflow and capped and not pairs:
+        pairs = mutual_pairs(cost)
+    if limit is not None:
+        kept = []
+        for l, r, c in pairs:
+            diff = mu[l] - mu[r]
+            exact = np.sqrt(dsum((diff * diff)[None])[0])
+            ml, mr = mass[l], mass[r]
+            den = np.maximum(ml + mr, np.float32(1))
+            bound = max(radius[l] + mr / den * exact, radius[r] + ml / den * exact)
+            if not bound > limit:
+                kept.append((l, r, c))
+        pairs = kept
+    return pairs
+
+
+def reduce_rounds(mu, mass, count, limit, target, cap=INF, strict=False, counts=None, passes=1):
+    """Full-recompute rounds (litgpt/log_kv_cache.py:3445-3519), the reducer of a capacity-capped
+    unified route: each round prices the current nodes afresh (``round_pairs``), takes its first
+    ``count - target`` pairs, merges each pair into its lower row (``_semantic_unified_merge_pack``,
+    :3134-3156: the mass-weighted center, summed mass, with a limit the pair's radius bound from
+    their exact distance) and compacts the survivors in order, until no pair is left or ``count <=
+    target``. Returns ``reduce``'s (survivors, trace, centers) in input row ids; ``strict``: a round
+    with no pair above the target raises. ``counts`` gets (nodes, rounds, merges, 0, 0)."""
+    if passes > 1 and limit is None and not np.isfinite(cap):
+        raise NotImplementedError("frozen-center sweeps of the full-recompute rounds are not restated")
+    out = f32(mu).copy()
+    if count <= target:
+        if counts is not None:
+            counts.append((count, 0, 0, 0, 0))
+        return np.arange(count), [], out
+    cur, m, rad = f32(mu[:count]).copy(), f32(mass[:count]).copy(), np.zeros(count, np.float32)
+    roots = np.arange(count)
+    trace, rounds = [], 0
+    cap = np.float32(cap)
+    while len(roots) > target:
+        pairs = round_pairs(cur, m, rad, limit, cap, strict)[:len(roots) - target]
+        rounds += 1
+        if not pairs:
+            if strict:
+                raise RuntimeError("unified route: no mutual pair below the cluster budget")
+            break
+        trace.extend((int(roots[l]), int(roots[r])) for l, r, _ in pairs)
+        partner = np.full(len(roots), -1)
+        keep = np.ones(len(roots), bool)
+        for l, r, _ in pairs:
+            partner[l] = r
+            keep[r] = False
+        surv = np.flatnonzero(keep)
+        new_mu, new_m, new_r = cur[surv].copy(), m[surv].copy(), np.zeros(len(surv), np.float32)
+        for i, s_ in enumerate(surv):
+            b = partner[s_]
+            if limit is not None:
+                new_r[i] = rad[s_]
+            if b < 0:
+                continue
+            ma, mb = m[s_], m[b]
+            comb = ma + mb
+            scale = np.maximum(comb, np.float32(1))
+            new_mu[i] = ((ma * cur[s_] + mb * cur[b]) / scale).astype(np.float32)
+            new_m[i] = comb
+            if limit is not None:
+                diff = cur[s_] - cur[b]
+                dist = np.sqrt(dsum((diff * diff)[None])[0])
+                new_r[i] = max(rad[s_] + mb / scale * dist, rad[b] + ma / scale * dist)
+        cur, m, rad, roots = new_mu, new_m, new_r, roots[surv]
+    out[roots] = cur
+    if counts is not None:
+        counts.append((count, rounds, len(trace), 0, 0))
+    return roots, trace, out
+
+
 def labels(size, survivors, trace):
     """Leaf -> compact surviving row (litgpt/log_kv_cache.py:3544-3568)."""
     parent = np.arange(size)
@@ -351,6 +460,10 @@ def plan_lane(cache, keys, n, b, g, reduce_fn=reduce):
     reducer stage (``reduce``'s signature and results)."""
     limit = np.float32(math.sqrt(float(cache.lam) * float(cache.s_h[b, g])))
     mu = f32(keys[:n])
+    cap = float(getattr(cache, "hard_cap", np.inf))
+    if np.isfinite(cap):
+        # A capacity cap runs the full-recompute rounds (litgpt/log_kv_cache.py:3283-3288).
+        reduce_fn = functools.partial(reduce_rounds, cap=cap)
     surv1, trace1, mu1 = reduce_fn(mu, np.ones(n, np.float32), n, limit, 1)
     lab1 = labels(n, surv1, trace1)
     old = np.flatnonzero(cache.alive[b, g])

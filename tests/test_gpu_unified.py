@@ -13,7 +13,7 @@ from workloads import Mixture, rope_tables
 pytestmark = pytest.mark.gpu
 
 
-def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False, passes=1):
+def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False, passes=1, cap=0.0):
     from logkv_amd import LogStructuredKVCache
     from oracle import OracleCache
 
@@ -23,10 +23,11 @@ def _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=0, span=4, beta=False
         dtype=torch.bfloat16, semantic_clusters=True, cluster_k_max=K, semantic_s_h=s_h,
         semantic_flush_granularity=T, semantic_anchor_mode="mid", allocate_second_order=False,
         semantic_unified_route=True, semantic_merge_passes=passes, cos_cache=cos, sin_cache=sin, rope_n_elem=dim,
-        alpha_exact_tokens=exact, alpha_span_max_tokens=span, beta_novelty=beta, beta_adaptive_merge=beta)
+        alpha_exact_tokens=exact, alpha_span_max_tokens=span, beta_novelty=beta, beta_adaptive_merge=beta,
+        semantic_capacity_hard_cap_mult=cap)
     ora = OracleCache(batch, groups, max_seq, dim, dim, B=B, recent_size=T, K=K, s_h=s_h, flush=T,
                       exact_tokens=exact, span_max=span, beta_novelty=beta, beta_adaptive=beta,
-                      cos=cos.numpy(), sin=sin.numpy(), unified=True, merge_passes=passes)
+                      cos=cos.numpy(), sin=sin.numpy(), unified=True, merge_passes=passes, hard_cap_mult=cap)
     return gpu, ora
 
 
@@ -59,6 +60,32 @@ def test_unified_route_matches_oracle(name, passes):
         assert not bad, f"flush {i}: " + "; ".join(bad)
         assert (ora.alive.sum(-1) <= K).all()
     assert ora.ward_merges > 0, "no old-old merge was exercised"
+
+
+@pytest.mark.parametrize("name", ["small", "alpha_beta", "wide"])
+def test_capped_unified_route_matches_oracle(name):
+    """A capacity cap (semantic_capacity_hard_cap_mult) runs the full-recompute rounds: each round
+    prices the compacted nodes afresh, no pair above the cap merges, and the budget stage takes
+    uncapped pairs when no capped one is left; the cluster state after every flush equals the
+    oracle's bit for bit."""
+    batch, groups, dim, K, B, T, n, s_h, exact, beta, drift = CASES[name]
+    print(f"case capped {name}", flush=True)
+    max_seq = T * (n + 2)
+    # A cap of a few flushes' worth of rows per cluster: binding within the run.
+    mult = 0.5 if name != "wide" else 0.75
+    gpu, ora = _pair(batch, groups, dim, K, B, T, max_seq, s_h, exact=exact, beta=beta, cap=mult)
+    mix = Mixture(batch, groups, dim, clusters=K + 2, seed=23, drift_every=drift)
+    dev = gpu.level_k.device
+    for i in range(n):
+        k, v = mix.rows(T), mix.rows(T)
+        pos = torch.arange(i * T, (i + 1) * T).unsqueeze(0).expand(batch, -1).contiguous()
+        ends = [[(p + 3 * b) % 5 == 0 for p in range(i * T, (i + 1) * T)] for b in range(batch)] if exact else None
+        gpu.route_and_flush_batch(k.to(dev), v.to(dev), pos.to(dev), span_ends=ends)
+        ora.flush_rows(k.float().numpy(), v.float().numpy(), pos.numpy(), ends)
+        torch.cuda.synchronize()
+        bad = compare_state(gpu, ora)
+        assert not bad, f"flush {i}: " + "; ".join(bad)
+        assert (ora.alive.sum(-1) <= K).all()
 
 
 def test_old_old_merge_frees_a_cluster():

@@ -18,6 +18,12 @@
   tests/test_log_kv_unified.py:503-526) on its integer data, and the
   incremental rounds equal full-recompute peeling rounds in float64 on
   distinct random costs (tests/test_log_kv_unified.py:690-706);
+* the full-recompute rounds of a capacity-capped route (``reduce_rounds``)
+  equal the incremental rounds without a cap on separated data (the
+  reference's own check, tests/test_log_kv_unified.py:560-580), and with a
+  cap give hand-worked answers: the nearest pair over the cap leaves the
+  second-cheapest pair to merge, the budget stage overflows the cap when no
+  capped pair is left, the candidate stage stops there instead;
 * labels and the Ward entry order on hand-built cases;
 * route invariants: at most K live clusters, every row accounted for once,
   n_total equal to the ladder mass, each candidate's rows within the radius
@@ -173,6 +179,39 @@ def test_frozen_sweep_rounds_equal_full_recompute(seed):
         want_surv, want_trace = _peel_reduce(x, w, 4, 4)
         assert surv.tolist() == want_surv and trace == want_trace, f"n={n}"
         assert len(surv) == min(n, 4)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("limit", [None, 6.0])
+def test_full_recompute_rounds_equal_incremental_without_cap(seed, limit):
+    rng = np.random.default_rng(seed)
+    centers = rng.standard_normal((6, 16)).astype(np.float32) * 8
+    x = (centers[rng.integers(0, 6, 40)] + rng.standard_normal((40, 16)) * 0.7).astype(np.float32)
+    mass = rng.integers(1, 4, 40).astype(np.float32)
+    target = 4 if limit is None else 1
+    s1, t1, m1 = U.reduce(x, mass, 40, limit, target)
+    s2, t2, m2 = U.reduce_rounds(x, mass, 40, limit, target)
+    assert s1.tolist() == s2.tolist() and t1 == t2 and len(t1) > 10
+    assert np.allclose(m1[s1], m2[s2], rtol=1e-5, atol=1e-5)
+
+
+def test_full_recompute_rounds_with_a_cap():
+    # Masses 2, 2, 1 at 0, 1, 5, cap 3.5: the nearest pair (0, 1) (cost 1 * 4/4 = 1) would
+    # hold mass 4, so row 0's least capped cost is row 2 (25 * 2/3) and rows 1 and 2 pick
+    # each other (16 * 2/3): (1, 2) merges, center (2 * 1 + 1 * 5) / 3.
+    x, w = line(0, 1, 5), np.asarray([2, 2, 1], np.float32)
+    s, t, mu = U.reduce_rounds(x, w, 3, None, 2, cap=3.5)
+    assert s.tolist() == [0, 1] and t == [(1, 2)]
+    assert mu[1, 0] == np.float32(np.float32(2 + 5) / np.float32(3))
+    s, t, _ = U.reduce_rounds(x, w, 3, None, 2)
+    assert t == [(0, 1)]
+    # 0, 1, 10, 11 with mass 1 and cap 2.5: both close pairs merge (mass 2 each); the last
+    # pair would hold 4. The budget stage (strict) takes it anyway, the candidate stage stops.
+    x, w = line(0, 1, 10, 11), ONES(4)
+    s, t, _ = U.reduce_rounds(x, w, 4, None, 1, cap=2.5, strict=True)
+    assert s.tolist() == [0] and t == [(0, 1), (2, 3), (0, 2)]
+    s, t, _ = U.reduce_rounds(x, w, 4, 100.0, 1, cap=2.5)
+    assert s.tolist() == [0, 2] and t == [(0, 1), (2, 3)]
 
 
 def test_labels_and_ward_entry_order():
