@@ -139,7 +139,10 @@ int64_t logkv_unified_stats_offset(const logkv_ladder_view* cache, int32_t token
  * 3589-3660) with _semantic_unified_reduce_device / _incremental and
  * _UnifiedReduceTorch / UnifiedReduce (litgpt/log_kv_cache.py:3225-3376,
  * :448-637; litgpt/log_kv_route_triton.py:197-838) and the labels
- * (litgpt/log_kv_cache.py:3544-3568). */
+ * (litgpt/log_kv_cache.py:3544-3568). With params->hard_cap > 0 the stages run
+ * the full-recompute rounds of a capacity-capped route (_semantic_unified_reduce_rounds,
+ * :3445-3519), and the call synchronizes `stream` every 8 rounds to read the lanes'
+ * round flags (the reference polls every 4 rounds). */
 int logkv_unified_plan(const logkv_ladder_view* cache, const logkv_rows_view* rows, const logkv_route_params* params,
                        const float* limits, void* workspace, int64_t workspace_bytes, int32_t* summary, void* stream);
 
