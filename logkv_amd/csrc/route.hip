@@ -274,6 +274,323 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
     if (s >= n) assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = -1;
 }
 
+// ---------------------------------------------------------------------------
+// Frozen-center decisions for 128-feature rows with a matrix-core screen (the
+// decisions of attach_kernel, bit for bit).
+//
+// A wave takes 32 rows at a time. Lane r + 32 h holds features 16 j + 8 h + e
+// (j, e < 8) of row r: the A operand of v_mfma_f32_32x32x16_bf16 for k step j,
+// and whole leaves of the canonical tree (leaf L's features L and L + 64 sit
+// in the same lane; only the fold of leaves L and L + 8 and the last fold of
+// the two half sums cross to the partner lane).
+//
+// Screen: each center is split into three bf16 parts whose sum is the f32
+// center (exactly, barring subnormal parts), so 24 products give every
+// (row, cluster) dot product d~ = x.m up to the matrix core's accumulation
+// error, about 384 u sum|x m| <= 2^-15.4 sqrt(xx mm) if it rounds like a
+// chain of f32 adds. From d~ and the canonical norms each live cluster gets
+// its cost c~ and squared difference v~ = (xx + mm) - 2 d~, with the bounds
+// D = 2^-11 (sqrt(xx mm) + |v~| + |c~| + |t~|) + 2^-80 on |c~ - cost| and
+// D' = 2^-11 (xx + mm + |v~|) + 2^-80 on |v~ - canonical squared difference|
+// (generous for every rounding on either side, the temporal term t~ taken
+// with a hardware reciprocal). A cluster can win only if c~ - D <= min(c~ + D)
+// and be the nearest only if v~ - D' <= min(v~ + D'): the canonical trees run
+// for those candidates only, the winner's dot always (its semantic distance
+// is compared with the radius and stored). A lane with a center whose sum of
+// squares is above 2^60 or not finite, and a row with such a sum or any
+// non-finite screened value, evaluate every cluster canonically.
+// ---------------------------------------------------------------------------
+typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float att_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kAttachMfmaWaves = 4;
+constexpr int kAttachTilesPerWave = 2;   // 32-row tiles per wave (the block's centers are staged once)
+constexpr int kCenterPitchF = 132;   // floats per staged f32 center (16 B of padding)
+constexpr int kCenterPitchB = 136;   // bf16 per staged center part (16 B of padding)
+
+__host__ __device__ inline size_t attach_mfma_shmem(int K) {
+  return static_cast<size_t>(K) * kCenterPitchF * 4 + static_cast<size_t>(3 * K) * kCenterPitchB * 2 +
+         static_cast<size_t>(kAttachMfmaWaves) * 2 * 32 * (K + 1) * 4;
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4 q, float (&f)[8]) {
+  f[0] = __uint_as_float(q.x << 16);
+  f[1] = __uint_as_float(q.x & 0xffff0000u);
+  f[2] = __uint_as_float(q.y << 16);
+  f[3] = __uint_as_float(q.y & 0xffff0000u);
+  f[4] = __uint_as_float(q.z << 16);
+  f[5] = __uint_as_float(q.z & 0xffff0000u);
+  f[6] = __uint_as_float(q.w << 16);
+  f[7] = __uint_as_float(q.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ void load_f32x8(const float* p, float (&f)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x;
+  f[1] = a.y;
+  f[2] = a.z;
+  f[3] = a.w;
+  f[4] = b.x;
+  f[5] = b.y;
+  f[6] = b.z;
+  f[7] = b.w;
+}
+
+// The canonical tree of canon_tree / canon_sq for a row held as above, against
+// center m (f32, natural feature order): KIND 0 the row's sum of squares, 1 the
+// dot product, 2 the squared difference. Both lanes of the row must be active;
+// both return the same value.
+template <int KIND>
+__device__ __forceinline__ float pair_tree(const uint4 (&xq)[8], const float* m, int h) {
+  float p2[8];
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp) {
+    float lf[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int j = jp + 2 * q;     // leaves 16 j + 8 h + e: features j and j + 4 of the lane
+      float xa[8], xb[8], ma[8], mb[8];
+      unpack_bf16x8(xq[j], xa);
+      unpack_bf16x8(xq[j + 4], xb);
+      if constexpr (KIND != 0) {
+        load_f32x8(m + 16 * j + 8 * h, ma);
+        load_f32x8(m + 16 * (j + 4) + 8 * h, mb);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (KIND == 0) {
+          lf[q][e] = xa[e] * xa[e] + xb[e] * xb[e];
+        } else if constexpr (KIND == 1) {
+          lf[q][e] = xa[e] * ma[e] + xb[e] * mb[e];
+        } else {
+          const float da = xa[e] - ma[e], db = xb[e] - mb[e];
+          lf[q][e] = da * da + db * db;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p1 = lf[0][e] + lf[1][e];   // leaves L and L + 32
+      p2[e] = jp == 0 ? p1 : p2[e] + p1;      // then L and L + 16
+    }
+  }
+  // Leaves L and L + 8 sit in the two lanes of the row: the low lane folds the
+  // even e, the high lane the odd e (one permlane32 swap per pair).
+  float q4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(p2[2 * k]), __float_as_uint(p2[2 * k + 1]),
+                                                     false, false);
+    q4[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  const float s = (q4[0] + q4[2]) + (q4[1] + q4[3]);   // + 4, + 2
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);   // + 1
+}
+
+// Wave-local LDS exchange point: the wave's earlier LDS writes are seen by its
+// later reads from any lane.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
+    LadderArgs c, RowsArgs r, RouteParams prm, const int32_t* __restrict__ order, int8_t* __restrict__ assign,
+    float* __restrict__ s_win, int tiles_per_wave) {
+  extern __shared__ __align__(16) float att[];
+  const int K = c.k_max, tp = K + 1;
+  float* mf = att;                                                              // [K][132] f32 centers
+  uint16_t* bs = reinterpret_cast<uint16_t*>(mf + K * kCenterPitchF);          // [3][K][136] bf16 parts
+  float* tw = reinterpret_cast<float*>(bs + 3 * K * kCenterPitchB);            // [waves][2][32][K + 1]
+  __shared__ float mm_s[kMaxClusters];
+  __shared__ int64_t phi_s[kMaxClusters];
+  __shared__ int32_t ntot_s[kMaxClusters];
+  __shared__ uint32_t alive_s;
+  const int lane_ix = blockIdx.y;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const int n = valid_rows(r, b);
+  const int tid = static_cast<int>(threadIdx.x), l = lane_id(), w = wave_id();
+  // Centers: f32 copies for the canonical trees and the three bf16 parts.
+  const LOGKV_G float* mu = gp(c.centroid) + static_cast<int64_t>(lane_ix) * K * 128;
+  for (int i = tid; i < K * 32; i += static_cast<int>(blockDim.x)) {
+    const int cc = i >> 5, q = i & 31;
+    const float4 v = *reinterpret_cast<const LOGKV_G float4*>(mu + cc * 128 + 4 * q);
+    *reinterpret_cast<float4*>(mf + cc * kCenterPitchF + 4 * q) = v;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    uint16_t part[3][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      part[0][k] = f32_to_bf16(e[k]);
+      const float r1 = e[k] - bf16_to_f32(part[0][k]);
+      part[1][k] = f32_to_bf16(r1);
+      const float r2 = r1 - bf16_to_f32(part[1][k]);
+      part[2][k] = f32_to_bf16(r2);
+    }
+#pragma unroll
+    for (int pt = 0; pt < 3; ++pt)
+      *reinterpret_cast<uint2*>(bs + (pt * K + cc) * kCenterPitchB + 4 * q) =
+          make_uint2(part[pt][0] | (static_cast<uint32_t>(part[pt][1]) << 16),
+                     part[pt][2] | (static_cast<uint32_t>(part[pt][3]) << 16));
+  }
+  if (tid < kWave) {
+    const bool live = tid < K && c.alive[lane_ix * K + tid];
+    const uint64_t bits = __ballot(live);
+    if (tid < K) {
+      phi_s[tid] = c.p_hi_c[static_cast<int64_t>(lane_ix) * K + tid];
+      ntot_s[tid] = c.n_total[static_cast<int64_t>(lane_ix) * K + tid];
+    }
+    if (tid == 0) alive_s = static_cast<uint32_t>(bits);
+  }
+  __syncthreads();
+  // Canonical squared norms of the centers (leaf l: features l and l + 64).
+  for (int cc = w; cc < K; cc += kAttachMfmaWaves) {
+    const float a = mf[cc * kCenterPitchF + l], a2 = mf[cc * kCenterPitchF + l + 64];
+    const float s = wave_tree(a * a + a2 * a2);
+    if (l == 0) mm_s[cc] = s;
+  }
+  __syncthreads();
+  bool lane_ok = true;
+  for (int cc = 0; cc < K; ++cc) lane_ok = lane_ok && mm_s[cc] <= 0x1p60f;
+  const uint32_t alive_bits = alive_s;
+  const uint32_t all_bits = K >= 32 ? 0xffffffffu : ((1u << K) - 1u);
+  const bool any_alive = alive_bits != 0;
+  const bool any_free = alive_bits != all_bits;
+  const bool capped = prm.hard_cap > 0.f;
+  const float radius = prm.lam * c.s_h[lane_ix];
+  const float inf = __builtin_inff();
+  float* t0 = tw + w * 2 * 32 * tp;   // d~, then the winner screen's lower bounds
+  float* t1 = t0 + 32 * tp;           // the nearest screen's lower bounds
+  const int rr = l & 31, h = l >> 5;
+  const int colc = rr < K ? rr : K - 1;
+  const LOGKV_G uint16_t* kbase = gp(r.k + b * r.k_sb + g * r.k_sg) + 8 * h;
+  const int tiles = (r.tokens + 31) / 32;
+  for (int it = 0; it < tiles_per_wave; ++it) {
+    const int tile = (static_cast<int>(blockIdx.x) * tiles_per_wave + it) * kAttachMfmaWaves + w;
+    if (tile >= tiles) break;
+    const int s = tile * 32 + rr;
+    const bool valid = s < n;
+    int64_t pos = 0;
+    uint4 xq[8];
+    if (valid) {
+      const int t = order[static_cast<int64_t>(b) * r.tokens + s];
+      pos = r.pos[b * r.pos_sb + t];
+      const LOGKV_G uint16_t* row = kbase + static_cast<int64_t>(t) * r.k_st;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xq[j] = *reinterpret_cast<const LOGKV_G uint4*>(row + 16 * j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xq[j] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    // Screened dot products (parts accumulated smallest first).
+    att_f32x16 acc = {};
+#pragma unroll
+    for (int pt = 2; pt >= 0; --pt) {
+      const uint16_t* bp = bs + (pt * K + colc) * kCenterPitchB + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        uint4 bq = *reinterpret_cast<const uint4*>(bp + 16 * ks);
+        if (rr >= K) bq = make_uint4(0u, 0u, 0u, 0u);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(att_bf16x8, xq[ks]),
+                                                      __builtin_bit_cast(att_bf16x8, bq), acc, 0, 0, 0);
+      }
+    }
+    if (rr < K) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t0[(8 * (i >> 2) + 4 * h + (i & 3)) * tp + rr] = acc[i];
+    }
+    const float xx = pair_tree<0>(xq, nullptr, h);
+    wave_lds_sync();
+    if (valid) {
+      float* d0 = t0 + rr * tp;
+      float* d1 = t1 + rr * tp;
+      bool ok = lane_ok && xx <= 0x1p60f;
+      float U = inf, Un = inf;
+      for (int cc = 0; cc < K; ++cc) {
+        if (!((alive_bits >> cc) & 1u)) continue;
+        const float mmc = mm_s[cc];
+        const float v = (xx + mmc) - 2.0f * d0[cc];
+        const int64_t gi = pos - phi_s[cc];
+        const float gap = static_cast<float>(gi > 0 ? gi : 0);
+        const float tq = prm.eta * (gap * __builtin_amdgcn_rcpf(gap + prm.g0));
+        const float cost = fmaxf(v, 0.f) + tq;
+        const float dw = 0x1p-11f * (((__builtin_amdgcn_sqrtf(xx * mmc) + fabsf(v)) + fabsf(cost)) + fabsf(tq)) +
+                         0x1p-80f;
+        const float dn = 0x1p-11f * ((xx + mmc) + fabsf(v)) + 0x1p-80f;
+        ok = ok && fabsf(cost) <= 0x1p100f && dw <= 0x1p100f;
+        U = fminf(U, cost + dw);
+        Un = fminf(Un, v + dn);
+        d0[cc] = cost - dw;
+        d1[cc] = v - dn;
+      }
+      uint32_t sw = all_bits, sn = alive_bits;
+      if (ok) {
+        sw = 0u;
+        sn = 0u;
+        for (int cc = 0; cc < K; ++cc) {
+          if (!((alive_bits >> cc) & 1u)) continue;
+          if (d0[cc] <= U) sw |= 1u << cc;
+          if (d1[cc] <= Un) sn |= 1u << cc;
+        }
+        if (sw == 0u) sw = 1u;   // no live cluster: the winner stays cluster 0
+      }
+      // Canonical costs of the candidates, in cluster order as attach_kernel.
+      float best = inf, s_winner = 0.f;
+      int winner = 0;
+      for (uint32_t m = sw; m; m &= m - 1u) {
+        const int cc = __builtin_ctz(m);
+        const float dot = pair_tree<1>(xq, mf + cc * kCenterPitchF, h);
+        const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot, 0.0f);
+        if (cc == 0) s_winner = semantic;
+        if ((alive_bits >> cc) & 1u) {
+          const int64_t gi = pos - phi_s[cc];
+          const float gap = static_cast<float>(gi > 0 ? gi : 0);
+          const float cost = semantic + prm.eta * (gap / (gap + prm.g0));
+          if (cost < best) {
+            best = cost;
+            winner = cc;
+            s_winner = semantic;
+          }
+        }
+      }
+      bool direct = any_alive && (s_winner <= radius);
+      if (capped) direct = direct && static_cast<float>(ntot_s[winner] + 1) <= prm.hard_cap;
+      int out;
+      if (!any_free && !capped) {
+        out = winner;
+        if (!direct) {
+          int nearest = 0;
+          if (ok && __popc(sn) == 1) {
+            nearest = __builtin_ctz(sn);
+          } else {
+            float best_e = inf;
+            for (uint32_t m = sn; m; m &= m - 1u) {
+              const int cc = __builtin_ctz(m);
+              const float ex = pair_tree<2>(xq, mf + cc * kCenterPitchF, h);
+              if (ex < best_e) {
+                best_e = ex;
+                nearest = cc;
+              }
+            }
+          }
+          out = nearest;
+        }
+      } else {
+        out = direct ? winner : -1;
+      }
+      if (h == 0) {
+        assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = static_cast<int8_t>(out);
+        if (any_free || capped) s_win[static_cast<int64_t>(lane_ix) * r.tokens + s] = s_winner;
+      }
+    } else if (h == 0 && s < r.tokens) {
+      assign[static_cast<int64_t>(lane_ix) * r.tokens + s] = -1;   // padding rows of the lane
+    }
+    wave_lds_sync();
+  }
+}
+
 // Canonical squared distance between a row (held in x[]) and another bf16 row.
 __device__ __forceinline__ float row_d2_bf16(const float* x, const uint16_t* other, int D, int J) {
   const int l = lane_id();
@@ -646,8 +963,21 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
                          ws.order, ws.assign, ws.s_win);
       return true;
     };
+    // 128-feature rows that allow 16-byte loads take the matrix-core screen.
+    const bool aligned16 = (reinterpret_cast<uintptr_t>(r.k) & 15u) == 0 && r.k_sb % 8 == 0 && r.k_sg % 8 == 0 &&
+                           r.k_st % 8 == 0;
     bool ok;
-    if (nj == 1) ok = attach(attach_kernel<1>, attach_tile<1>(), attach_shmem<1>(c.k_max));
+    if (c.dk == 128 && c.k_max >= 1 && aligned16) {
+      const size_t shmem = attach_mfma_shmem(c.k_max);
+      ok = allow_dynamic_lds(reinterpret_cast<const void*>(attach_mfma_kernel), shmem);
+      if (ok) {
+        const int tiles = (r.tokens + 31) / 32;
+        const int per_block = kAttachMfmaWaves * kAttachTilesPerWave;
+        hipLaunchKernelGGL(attach_mfma_kernel, dim3((tiles + per_block - 1) / per_block, lanes),
+                           dim3(kAttachMfmaWaves * kWave), shmem, stream, c, r, p, ws.order, ws.assign, ws.s_win,
+                           kAttachTilesPerWave);
+      }
+    } else if (nj == 1) ok = attach(attach_kernel<1>, attach_tile<1>(), attach_shmem<1>(c.k_max));
     else if (nj == 2) ok = attach(attach_kernel<2>, attach_tile<2>(), attach_shmem<2>(c.k_max));
     else if (nj == 3) ok = attach(attach_kernel<3>, attach_tile<3>(), attach_shmem<3>(c.k_max));
     else ok = attach(attach_kernel<4>, attach_tile<4>(), attach_shmem<4>(c.k_max));

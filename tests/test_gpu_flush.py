@@ -266,3 +266,55 @@ def test_attach_screen_ties_and_radius_edges():
     np.testing.assert_array_equal(to_np(assign), want)
     got = to_np(assign)
     assert (got[0, :, 0:4 * K:4] != -1).all()                     # midpoints decided (tie: the first)
+
+
+def test_attach_screen_extreme_magnitudes():
+    """Attach decisions on 128-feature rows where the matrix-core screen cannot decide: rows scaled
+    by 2^31 (sums of squares far above 2^60), rows of magnitude 1e-30 (sums of squares underflow, so
+    every cluster stays a candidate), and a lane with one center scaled by 2^40 (the whole lane takes
+    the canonical trees); ordinary rows between them. Every decision equals the oracle's."""
+    import ctypes as C
+
+    from logkv_amd._lib import check, lib, ptr, stream_of
+    from oracle import route
+
+    print("case attach screen, extreme magnitudes", flush=True)
+    batch, groups, dim, K, T = 1, 2, 128, 8, 192
+    gpu, ora = make_pair(batch, groups, dim, K, 16, recent=T, flush=T, max_seq=4096, s_h=8.0)
+    g = torch.Generator().manual_seed(53)
+    centers = (torch.randint(0, 2, (groups, K, dim), generator=g) * 2 - 1).float()
+    centers = centers + torch.randn(groups, K, dim, generator=g) * 0.25
+    centers[1, 3] *= 2.0 ** 40
+    for dst in (gpu, ora):
+        if dst is gpu:
+            dst.centroid.copy_(centers.unsqueeze(0).to(dst.centroid.device))
+            dst.alive.fill_(True)
+            dst.p_hi_c.fill_(10)
+            dst.n_total.fill_(5)
+        else:
+            dst.centroid[...] = centers.unsqueeze(0).numpy()
+            dst.alive[...] = True
+            dst.p_hi_c[...] = 10
+            dst.n_total[...] = 5
+    a = torch.randint(0, K, (groups, T), generator=g)
+    x = torch.stack([centers[gi, a[gi]] for gi in range(groups)]) + torch.randn(groups, T, dim, generator=g) * 0.4
+    x[1, a[1] == 3] = torch.randn(int((a[1] == 3).sum()), dim, generator=g)
+    kind = torch.arange(T) % 4
+    x[:, kind == 1] *= 2.0 ** 31
+    x[:, kind == 2] *= 1e-30
+    k = x.unsqueeze(0).to(torch.bfloat16)
+    pos = (100 + torch.arange(T)).unsqueeze(0).contiguous()
+    dev = gpu.level_k.device
+    view = gpu._ladder_view()
+    k_dev, pos_dev = k.to(dev), pos.to(dev)
+    rv = gpu._rows_view(k_dev, k_dev, pos_dev)
+    ws = gpu._workspace_for(view, T)
+    assign = torch.empty(batch, groups, T, dtype=torch.int8, device=dev)
+    order = torch.empty(batch, T, dtype=torch.int32, device=dev)
+    check(lib().logkv_attach_assign(C.byref(view), C.byref(rv), C.byref(gpu._params), ptr(ws), ws.numel(),
+                                    ptr(assign), ptr(order), stream_of(dev)), "attach")
+    torch.cuda.synchronize()
+    want, _ = route.attach_assign(k.float().numpy(), pos.numpy(), np.array([T]), ora.centroid, ora.alive, ora.p_hi_c,
+                                  ora.s_h, ora.eta, ora.g0, ora.lam)
+    np.testing.assert_array_equal(to_np(assign), want)
+    assert len(set(to_np(assign)[0, 0].tolist())) > 2
