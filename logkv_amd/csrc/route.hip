@@ -284,21 +284,22 @@ __global__ __launch_bounds__(kAttachMaxThreads) void attach_kernel(LadderArgs c,
 // in the same lane; only the fold of leaves L and L + 8 and the last fold of
 // the two half sums cross to the partner lane).
 //
-// Screen: each center is split into three bf16 parts whose sum is the f32
-// center (exactly, barring subnormal parts), so 24 products give every
-// (row, cluster) dot product d~ = x.m up to the matrix core's accumulation
-// error, about 384 u sum|x m| <= 2^-15.4 sqrt(xx mm) if it rounds like a
-// chain of f32 adds. From d~ and the canonical norms each live cluster gets
-// its cost c~ and squared difference v~ = (xx + mm) - 2 d~, with the bounds
-// D = 2^-11 (sqrt(xx mm) + |v~| + |c~| + |t~|) + 2^-80 on |c~ - cost| and
+// Screen: each center is split into two bf16 parts, hi + mid, within 2^-16
+// (relative) of the f32 center, so 16 products give every (row, cluster) dot
+// product d~ = x.m within about 2^-15 sum|x m| <= 2^-15 sqrt(xx mm) (the
+// residual plus the matrix core's accumulation, if it rounds like a chain of
+// f32 adds). From d~ and the canonical norms each live cluster gets its cost
+// c~ and squared difference v~ = (xx + mm) - 2 d~, with the bounds
+// D = 2^-11 (sqrt(xx) sqrt(mm) + |v~| + |t~|) + 2^-80 on |c~ - cost| and
 // D' = 2^-11 (xx + mm + |v~|) + 2^-80 on |v~ - canonical squared difference|
 // (generous for every rounding on either side, the temporal term t~ taken
 // with a hardware reciprocal). A cluster can win only if c~ - D <= min(c~ + D)
 // and be the nearest only if v~ - D' <= min(v~ + D'): the canonical trees run
 // for those candidates only, the winner's dot always (its semantic distance
-// is compared with the radius and stored). A lane with a center whose sum of
-// squares is above 2^60 or not finite, and a row with such a sum or any
-// non-finite screened value, evaluate every cluster canonically.
+// is compared with the radius and stored). The two lanes of a row screen
+// alternate clusters and merge their minima and candidate masks. A lane with a
+// center whose sum of squares is above 2^60 or not finite, and a row with such
+// a sum or a non-finite screened value, evaluate every cluster canonically.
 // ---------------------------------------------------------------------------
 typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float att_f32x16 __attribute__((ext_vector_type(16)));
@@ -307,10 +308,21 @@ constexpr int kAttachMfmaWaves = 4;
 constexpr int kAttachTilesPerWave = 2;   // 32-row tiles per wave (the block's centers are staged once)
 constexpr int kCenterPitchF = 132;   // floats per staged f32 center (16 B of padding)
 constexpr int kCenterPitchB = 136;   // bf16 per staged center part (16 B of padding)
+constexpr int kCenterParts = 2;      // bf16 parts per center (hi, mid)
 
 __host__ __device__ inline size_t attach_mfma_shmem(int K) {
-  return static_cast<size_t>(K) * kCenterPitchF * 4 + static_cast<size_t>(3 * K) * kCenterPitchB * 2 +
+  return static_cast<size_t>(K) * kCenterPitchF * 4 + static_cast<size_t>(kCenterParts * K) * kCenterPitchB * 2 +
          static_cast<size_t>(kAttachMfmaWaves) * 2 * 32 * (K + 1) * 4;
+}
+
+// min / or of a value over the two lanes of a row (lanes r and r + 32).
+__device__ __forceinline__ float pair_min(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fminf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ uint32_t pair_or(uint32_t v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return p[0] | p[1];
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4 q, float (&f)[8]) {
@@ -346,6 +358,7 @@ __device__ __forceinline__ float pair_tree(const uint4 (&xq)[8], const float* m,
   float p2[8];
 #pragma unroll
   for (int jp = 0; jp < 2; ++jp) {
+    if (jp == 1) __builtin_amdgcn_sched_barrier(0);   // one half of the center's loads in flight at a time
     float lf[2][8];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -389,6 +402,13 @@ __device__ __forceinline__ float pair_tree(const uint4 (&xq)[8], const float* m,
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);   // + 1
 }
 
+// Marks the packed row as rewritten, so the loops over candidate clusters
+// unpack it per evaluation instead of hoisting all 64 unpacked features.
+__device__ __forceinline__ void keep_packed(uint4 (&xq)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(xq[j].x), "+v"(xq[j].y), "+v"(xq[j].z), "+v"(xq[j].w));
+}
+
 // Wave-local LDS exchange point: the wave's earlier LDS writes are seen by its
 // later reads from any lane.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -403,9 +423,9 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
   extern __shared__ __align__(16) float att[];
   const int K = c.k_max, tp = K + 1;
   float* mf = att;                                                              // [K][132] f32 centers
-  uint16_t* bs = reinterpret_cast<uint16_t*>(mf + K * kCenterPitchF);          // [3][K][136] bf16 parts
-  float* tw = reinterpret_cast<float*>(bs + 3 * K * kCenterPitchB);            // [waves][2][32][K + 1]
-  __shared__ float mm_s[kMaxClusters];
+  uint16_t* bs = reinterpret_cast<uint16_t*>(mf + K * kCenterPitchF);          // [2][K][136] bf16 parts
+  float* tw = reinterpret_cast<float*>(bs + kCenterParts * K * kCenterPitchB); // [waves][2][32][K + 1]
+  __shared__ float mm_s[kMaxClusters], sm_s[kMaxClusters];
   __shared__ int64_t phi_s[kMaxClusters];
   __shared__ int32_t ntot_s[kMaxClusters];
   __shared__ uint32_t alive_s;
@@ -420,17 +440,14 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
     const float4 v = *reinterpret_cast<const LOGKV_G float4*>(mu + cc * 128 + 4 * q);
     *reinterpret_cast<float4*>(mf + cc * kCenterPitchF + 4 * q) = v;
     const float e[4] = {v.x, v.y, v.z, v.w};
-    uint16_t part[3][4];
+    uint16_t part[kCenterParts][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       part[0][k] = f32_to_bf16(e[k]);
-      const float r1 = e[k] - bf16_to_f32(part[0][k]);
-      part[1][k] = f32_to_bf16(r1);
-      const float r2 = r1 - bf16_to_f32(part[1][k]);
-      part[2][k] = f32_to_bf16(r2);
+      part[1][k] = f32_to_bf16(e[k] - bf16_to_f32(part[0][k]));
     }
 #pragma unroll
-    for (int pt = 0; pt < 3; ++pt)
+    for (int pt = 0; pt < kCenterParts; ++pt)
       *reinterpret_cast<uint2*>(bs + (pt * K + cc) * kCenterPitchB + 4 * q) =
           make_uint2(part[pt][0] | (static_cast<uint32_t>(part[pt][1]) << 16),
                      part[pt][2] | (static_cast<uint32_t>(part[pt][3]) << 16));
@@ -449,7 +466,10 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
   for (int cc = w; cc < K; cc += kAttachMfmaWaves) {
     const float a = mf[cc * kCenterPitchF + l], a2 = mf[cc * kCenterPitchF + l + 64];
     const float s = wave_tree(a * a + a2 * a2);
-    if (l == 0) mm_s[cc] = s;
+    if (l == 0) {
+      mm_s[cc] = s;
+      sm_s[cc] = __builtin_amdgcn_sqrtf(s);
+    }
   }
   __syncthreads();
   bool lane_ok = true;
@@ -487,7 +507,7 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
     // Screened dot products (parts accumulated smallest first).
     att_f32x16 acc = {};
 #pragma unroll
-    for (int pt = 2; pt >= 0; --pt) {
+    for (int pt = kCenterParts - 1; pt >= 0; --pt) {
       const uint16_t* bp = bs + (pt * K + colc) * kCenterPitchB + 8 * h;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
@@ -507,8 +527,9 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
       float* d0 = t0 + rr * tp;
       float* d1 = t1 + rr * tp;
       bool ok = lane_ok && xx <= 0x1p60f;
+      const float sx = __builtin_amdgcn_sqrtf(xx);
       float U = inf, Un = inf;
-      for (int cc = 0; cc < K; ++cc) {
+      for (int cc = h; cc < K; cc += 2) {
         if (!((alive_bits >> cc) & 1u)) continue;
         const float mmc = mm_s[cc];
         const float v = (xx + mmc) - 2.0f * d0[cc];
@@ -516,8 +537,7 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
         const float gap = static_cast<float>(gi > 0 ? gi : 0);
         const float tq = prm.eta * (gap * __builtin_amdgcn_rcpf(gap + prm.g0));
         const float cost = fmaxf(v, 0.f) + tq;
-        const float dw = 0x1p-11f * (((__builtin_amdgcn_sqrtf(xx * mmc) + fabsf(v)) + fabsf(cost)) + fabsf(tq)) +
-                         0x1p-80f;
+        const float dw = 0x1p-11f * ((sx * sm_s[cc] + fabsf(v)) + fabsf(tq)) + 0x1p-80f;
         const float dn = 0x1p-11f * ((xx + mmc) + fabsf(v)) + 0x1p-80f;
         ok = ok && fabsf(cost) <= 0x1p100f && dw <= 0x1p100f;
         U = fminf(U, cost + dw);
@@ -525,15 +545,20 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
         d0[cc] = cost - dw;
         d1[cc] = v - dn;
       }
+      U = pair_min(U);
+      Un = pair_min(Un);
+      ok = pair_or(ok ? 0u : 1u) == 0u;
       uint32_t sw = all_bits, sn = alive_bits;
       if (ok) {
         sw = 0u;
         sn = 0u;
-        for (int cc = 0; cc < K; ++cc) {
+        for (int cc = h; cc < K; cc += 2) {
           if (!((alive_bits >> cc) & 1u)) continue;
           if (d0[cc] <= U) sw |= 1u << cc;
           if (d1[cc] <= Un) sn |= 1u << cc;
         }
+        sw = pair_or(sw);
+        sn = pair_or(sn);
         if (sw == 0u) sw = 1u;   // no live cluster: the winner stays cluster 0
       }
       // Canonical costs of the candidates, in cluster order as attach_kernel.
@@ -541,6 +566,7 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
       int winner = 0;
       for (uint32_t m = sw; m; m &= m - 1u) {
         const int cc = __builtin_ctz(m);
+        keep_packed(xq);
         const float dot = pair_tree<1>(xq, mf + cc * kCenterPitchF, h);
         const float semantic = fmaxf((xx + mm_s[cc]) - 2.0f * dot, 0.0f);
         if (cc == 0) s_winner = semantic;
@@ -568,6 +594,7 @@ __global__ __launch_bounds__(kAttachMfmaWaves* kWave) void attach_mfma_kernel(
             float best_e = inf;
             for (uint32_t m = sn; m; m &= m - 1u) {
               const int cc = __builtin_ctz(m);
+              keep_packed(xq);
               const float ex = pair_tree<2>(xq, mf + cc * kCenterPitchF, h);
               if (ex < best_e) {
                 best_e = ex;
