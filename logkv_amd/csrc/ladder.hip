@@ -1218,22 +1218,34 @@ __device__ __forceinline__ void screen_sums(const float (&x)[4][F], float* s9) {
   }
 }
 
-// Adds one component's screened costs of the cuts (2, 1, 3) to `cost`.
-__device__ __forceinline__ void screen_costs(const float* s9, const float* w, float total, float* cost) {
+// Reciprocals a group's screened costs divide by: the total mass and the
+// masses of the four sides the cuts (2, 1, 3) form (shared by K and V).
+struct ScreenRcp {
+  float total, s01, s23, s123, s012;
+};
+
+__device__ __forceinline__ ScreenRcp screen_rcp(const float* w, float total) {
+  return ScreenRcp{1.0f / total, 1.0f / fmaxf(w[0] + w[1], 1e-12f), 1.0f / fmaxf(w[2] + w[3], 1e-12f),
+                   1.0f / fmaxf((w[1] + w[2]) + w[3], 1e-12f), 1.0f / fmaxf((w[0] + w[1]) + w[2], 1e-12f)};
+}
+
+// Adds one component's screened costs of the cuts (2, 1, 3) to `cost`; each
+// quotient is a product with a rounded reciprocal (one more half ulp).
+__device__ __forceinline__ void screen_costs(const float* s9, const float* w, const ScreenRcp& rc, float* cost) {
   const float e = ((s9[0] * w[0] + s9[1] * w[1]) + s9[2] * w[2]) + s9[3] * w[3];
-  const float energy = fmaxf(e / total, 1e-12f);
+  const float re = 1.0f / fmaxf(e * rc.total, 1e-12f);
   const float p01 = (w[0] * w[1]) * s9[4], p02 = (w[0] * w[2]) * s9[5], p12 = (w[1] * w[2]) * s9[6];
   const float p13 = (w[1] * w[3]) * s9[7], p23 = (w[2] * w[3]) * s9[8];
-  const float c2 = p01 / fmaxf(w[0] + w[1], 1e-12f) + p23 / fmaxf(w[2] + w[3], 1e-12f);
-  const float c1 = ((p12 + p13) + p23) / fmaxf((w[1] + w[2]) + w[3], 1e-12f);
-  const float c3 = ((p01 + p02) + p12) / fmaxf((w[0] + w[1]) + w[2], 1e-12f);
-  cost[0] += c2 / energy;
-  cost[1] += c1 / energy;
-  cost[2] += c3 / energy;
+  const float c2 = p01 * rc.s01 + p23 * rc.s23;
+  const float c1 = ((p12 + p13) + p23) * rc.s123;
+  const float c3 = ((p01 + p02) + p12) * rc.s012;
+  cost[0] += c2 * re;
+  cost[1] += c1 * re;
+  cost[2] += c3 * re;
 }
 
 // The cut the canonical evaluation chooses, when the screened costs settle it:
-// its costs and the screen's both err by at most ~90 ulps relative (sums of
+// its costs and the screen's both err by at most ~95 ulps relative (sums of
 // non-negative terms of depth <= 16, a handful of products and quotients; the
 // canonical side means' rounding adds at most 25 eps^2 of the side's energy
 // per side, covered by the absolute term), so a runner-up more than 2^-13
@@ -1243,8 +1255,9 @@ __device__ __forceinline__ void screen_costs(const float* s9, const float* w, fl
 // clamped side means the pairwise form does not model.
 __device__ __forceinline__ int screened_cut(const float* ck, const float* cv, const float* w, float total) {
   float cost[3] = {0.f, 0.f, 0.f};
-  screen_costs(ck, w, total, cost);
-  screen_costs(cv, w, total, cost);
+  const ScreenRcp rc = screen_rcp(w, total);
+  screen_costs(ck, w, rc, cost);
+  screen_costs(cv, w, rc, cost);
   int best = 0;
   if (cost[1] < cost[best]) best = 1;
   if (cost[2] < cost[best]) best = 2;
@@ -1295,6 +1308,16 @@ __device__ __forceinline__ void screen_sums8(const uint2 (&x)[4][2], float* s9) 
   screen_sums<8>(f, s9);
 }
 
+// Two floats to packed bf16, round to nearest even (the hardware conversion;
+// f32_to_bf16 agrees on every non-NaN float, and a settled group's means are
+// never NaN: its costs are finite, so are its rows and their weighted sums).
+__device__ __forceinline__ uint32_t pack_bf16_finite(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 // One side's output means of a 128-feature group from the held rows: per
 // feature beta_group's row-order sum (member rows x w, the others x * 0) over
 // the side's double reciprocal, 8 features to a lane, two 8-byte stores.
@@ -1303,16 +1326,16 @@ __device__ __forceinline__ void side_out8(const uint2 (&x)[4][2], const float* w
   uint32_t o[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    uint32_t h[2];
+    float h[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int f = 2 * q + e;
       float acc = (member & 1u) ? feat8(x[0], f) * w[0] : feat8(x[0], f) * 0.f;
 #pragma unroll
       for (int i = 1; i < 4; ++i) acc = acc + (((member >> i) & 1u) ? feat8(x[i], f) * w[i] : feat8(x[i], f) * 0.f);
-      h[e] = f32_to_bf16(div_by_rcp(acc, rcp));
+      h[e] = div_by_rcp(acc, rcp);
     }
-    o[q] = h[0] | (h[1] << 16);
+    o[q] = pack_bf16_finite(h[0], h[1]);
   }
   LOGKV_G uint2* dst = reinterpret_cast<LOGKV_G uint2*>(at);
   dst[0] = make_uint2(o[0], o[1]);
@@ -1523,6 +1546,13 @@ __device__ __forceinline__ bool beta_row_group_held(const LadderArgs& c, const R
   const bool settled = cut != 0;
   cut = settled ? cut : 2;
   const bool emit = live && settled;
+  // The held rows count as rewritten here, so the output means unpack them
+  // again instead of keeping the screen's 64 unpacked features live.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      asm volatile("" : "+v"(held.k[i][h2].x), "+v"(held.k[i][h2].y), "+v"(held.v[i][h2].x), "+v"(held.v[i][h2].y));
   double rl;
   {
     float wl[4], wrt[4];
