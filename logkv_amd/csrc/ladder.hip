@@ -24,7 +24,6 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kMoveUnits = 8;    // 8-byte units per thread staged in registers per move chunk
-constexpr int kCenterRows = 128;  // key rows staged in LDS per center-update chunk
 
 struct Soa {
   LOGKV_G uint16_t* k;
@@ -618,7 +617,133 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(LadderArgs c, Ro
     }
     __syncthreads();
   }
-  if (tid < K) ws.plans[static_cast<int64_t>(lane_ix) * K + tid].m_tok = base_s[tid];
+  if (tid < K) {
+    const int64_t cl = static_cast<int64_t>(lane_ix) * K + tid;
+    ws.plans[cl].m_tok = base_s[tid];
+    // The alive flags as they were before the flush (the commit launches read
+    // this snapshot; the op-log record keeps it).
+    ws.snap_alive[cl] = c.alive[cl] ? 1 : 0;
+  }
+}
+
+// Center updates of the commit: mu <- (pre*mu + sum k) / (pre + n), pre =
+// n_eff, the new rows' keys summed in position order
+// (litgpt/log_kv_cache.py:4344-4359), one at a time (a left fold) or in tiles
+// of kCenterTile rows from the first new row, each tile summed by a halving
+// tree with zeros past the last row and the tiles folded in order
+// (prm.center_tile, the centroid backend); a new cluster starts from its first
+// row's key with n_eff = 1 (litgpt/log_kv_cache.py:2276-2278).
+//
+// Every feature is its own fold, so a ladder takes two waves and a lane folds
+// features 64 w + l + 128 j. The ladder's row list is staged in LDS; rows come
+// in batches of kCenterTile whose loads are issued a batch ahead of the fold
+// (two register sets), since one cluster can hold most of a flush's rows. Runs
+// on a side stream beside the commit and level launches, which neither read
+// the centers nor write what this launch reads (the row lists, m_tok and the
+// alive snapshot are bucket_kernel's); the caller's stream waits for it.
+constexpr int kCenterWaves = 2;
+
+template <int NJ>
+__device__ __forceinline__ void center_batch_load(const LOGKV_G uint16_t* kb, const uint16_t* tok, int64_t k_st,
+                                                  int r0, int m, int f0, int dk, float (&x)[kCenterTile][NJ]) {
+#pragma unroll
+  for (int q = 0; q < kCenterTile; ++q) {
+    const int64_t base = static_cast<int64_t>(tok[min(r0 + q, m - 1)]) * k_st;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int f = f0 + 2 * kWave * j;
+      x[q][j] = bf16_to_f32(kb[base + (f < dk ? f : 0)]);
+    }
+  }
+}
+
+// Folds one batch (rows r0 .. r0 + rows - 1) into acc: a left fold, or a tile's
+// halving tree (zeros past the last row) added to acc. `start`: the batch
+// begins the sum.
+template <int NJ>
+__device__ __forceinline__ void center_batch_fold(float (&x)[kCenterTile][NJ], int rows, bool start, bool tiles,
+                                                  float (&acc)[NJ]) {
+  if (tiles) {
+#pragma unroll
+    for (int q = 0; q < kCenterTile; ++q)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) x[q][j] = q < rows ? x[q][j] : 0.f;
+#pragma unroll
+    for (int h = kCenterTile / 2; h >= 1; h /= 2)
+#pragma unroll
+      for (int q = 0; q < h; ++q)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) x[q][j] = x[q][j] + x[q + h][j];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] = start ? x[0][j] : acc[j] + x[0][j];
+  } else {
+#pragma unroll
+    for (int q = 0; q < kCenterTile; ++q)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (q < rows) acc[j] = (start && q == 0) ? x[q][j] : acc[j] + x[q][j];
+  }
+}
+
+template <int NJ>
+__global__ __launch_bounds__(kCenterWaves* kWave) void center_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+                                                                    Workspace ws) {
+  extern __shared__ __align__(16) uint16_t ctok[];
+  const int ladder = static_cast<int>(blockIdx.x);
+  if (ws.abort && *ws.abort) return;   // a failed replay check: nothing written
+  const int m = ws.plans[ladder].m_tok;
+  if (m == 0) return;
+  const int K = c.k_max, dk = c.dk;
+  const int lane_ix = ladder / K;
+  const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
+  const int64_t cl = ladder;
+  const bool was_alive = ws.snap_alive[cl] != 0;   // the top-level finish may rewrite `alive` meanwhile
+  const int first = was_alive ? 0 : 1;            // a dead cluster opens with its earliest row
+  const int nn = m - first;
+  {
+    const LOGKV_G uint16_t* list = gp(ws.tok + cl * r.tokens);
+    for (int i = threadIdx.x; i < m; i += kCenterWaves * kWave) ctok[i] = list[i];
+  }
+  __syncthreads();
+  const LOGKV_G uint16_t* kb = gp(r.k + b * r.k_sb + g * r.k_sg);
+  LOGKV_G float* mu = gp(c.centroid + cl * dk);
+  const int f0 = wave_id() * kWave + lane_id();
+  float n_eff = was_alive ? c.n_eff[cl] : 1.0f;
+  float mu_d[NJ];
+  {
+    const int64_t t0 = static_cast<int64_t>(ctok[0]) * r.k_st;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int f = f0 + 2 * kWave * j;
+      mu_d[j] = 0.f;
+      if (f < dk) mu_d[j] = was_alive ? mu[f] : bf16_to_f32(kb[t0 + f]);
+    }
+  }
+  if (nn > 0) {
+    const bool tiles = prm.center_tile == kCenterTile;
+    float acc[NJ], xa[kCenterTile][NJ], xb[kCenterTile][NJ];
+    center_batch_load<NJ>(kb, ctok, r.k_st, first, m, f0, dk, xa);
+    for (int r0 = first; r0 < m; r0 += 2 * kCenterTile) {
+      const int r1 = r0 + kCenterTile;
+      if (r1 < m) center_batch_load<NJ>(kb, ctok, r.k_st, r1, m, f0, dk, xb);
+      center_batch_fold<NJ>(xa, min(kCenterTile, m - r0), r0 == first, tiles, acc);
+      if (r1 >= m) break;
+      const int r2 = r1 + kCenterTile;
+      if (r2 < m) center_batch_load<NJ>(kb, ctok, r.k_st, r2, m, f0, dk, xa);
+      center_batch_fold<NJ>(xb, min(kCenterTile, m - r1), false, tiles, acc);
+    }
+    const float pre = n_eff;
+    const float den = pre + static_cast<float>(nn);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mu_d[j] = pre > 0.f ? (pre * mu_d[j] + acc[j]) / den : acc[j] / static_cast<float>(nn);
+    n_eff = den;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = f0 + 2 * kWave * j;
+    if (f < dk) mu[f] = mu_d[j];
+  }
+  if (threadIdx.x == 0) c.n_eff[cl] = n_eff;
 }
 
 __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws) {
@@ -630,12 +755,11 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const int lane_ix = ladder / K;
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
-  const int c_stage_off = (2 * r.tokens + 15) & ~15;
-  const int keys_off = c_stage_off + kCenterRows * dk * 2;
+  const int keys_off = (2 * r.tokens + 15) & ~15;
 
   if (ws.abort && *ws.abort) {
     // A failed replay check: no rows, nothing written (the later launches read the plan).
-    if (blockIdx.y == 0 && threadIdx.x == 0) {
+    if (threadIdx.x == 0) {
       ws.plans[ladder].active = 0;
       ws.plans[ladder].m_tok = 0;
     }
@@ -650,10 +774,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   }
   __syncthreads();
   if (m == 0) {
-    if (blockIdx.y == 0 && threadIdx.x == 0) {
-      ws.plans[ladder].active = 0;
-      ws.plans[ladder].m_tok = 0;
-    }
+    if (threadIdx.x == 0) ws.plans[ladder].active = 0;   // m_tok is already 0
     return;
   }
 
@@ -665,97 +786,12 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const LOGKV_G uint16_t* kb = gp(r.k + b * r.k_sb + g * r.k_sg);
   const LOGKV_G uint16_t* vb = gp(r.v + b * r.v_sb + g * r.v_sg);
   const LOGKV_G int64_t* posb = gp(r.pos + b * r.pos_sb);
-  LOGKV_G float* mu = gp(c.centroid + cl * dk);
   const LOGKV_S uint16_t* tok_s = (const LOGKV_S uint16_t*)tok;
   const Soa S0 = s0_of(ws, ladder, dk, dv);
 
-  // No launch of the commit writes `alive` before the top-level finish, so both
-  // roles read the flags as they were before the flush; the ladder role keeps
-  // a copy for the op-log record.
-  const bool was_alive = c.alive[cl] != 0;
-  if (blockIdx.y == 0 && threadIdx.x == 0) ws.snap_alive[cl] = was_alive ? 1 : 0;
+  const bool was_alive = ws.snap_alive[cl] != 0;   // written by bucket_kernel
   const int first = was_alive ? 0 : 1;   // a dead cluster opens with its earliest row
   const int nn = m - first;
-
-  if (blockIdx.y == 1) {
-    // Center role: mu <- (pre*mu + sum k) / (pre + n), pre = n_eff, the new
-    // rows' keys summed in position order (litgpt/log_kv_cache.py:4344-4359),
-    // one at a time or in tiles (prm.center_tile, the centroid backend);
-    // a new cluster starts from its first row's key with n_eff = 1
-    // (litgpt/log_kv_cache.py:2276-2278). Key rows are staged in LDS by all
-    // threads; one thread per feature adds them in order.
-    float n_eff = was_alive ? c.n_eff[cl] : 1.0f;
-    const int d = threadIdx.x;
-    float mu_d = 0.f;
-    if (d < dk) mu_d = was_alive ? mu[d] : bf16_to_f32(kb[static_cast<int64_t>(tok[0]) * r.k_st + d]);
-    if (nn > 0) {
-      uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + c_stage_off);
-      const int ku = dk / 4;
-      float acc = 0.f;
-      for (int c0 = first; c0 < m; c0 += kCenterRows) {
-        const int rows = min(kCenterRows, m - c0);
-        // kBatch units per thread loaded (clamped, unconditionally) before any store.
-        for (int i0 = threadIdx.x; i0 < rows * ku; i0 += kBatch * kThreads) {
-          uint2 x[kBatch];
-#pragma unroll
-          for (int q = 0; q < kBatch; ++q) {
-            const int i = min(i0 + q * kThreads, rows * ku - 1);
-            const int rr = i / ku, u = i - rr * ku;
-            x[q] = *(const LOGKV_G uint2*)(kb + static_cast<int64_t>(tok[c0 + rr]) * r.k_st + 4 * u);
-          }
-#pragma unroll
-          for (int q = 0; q < kBatch; ++q) {
-            const int i = i0 + q * kThreads;
-            if (i < rows * ku) {
-              const int rr = i / ku, u = i - rr * ku;
-              *reinterpret_cast<uint2*>(stage + rr * dk + 4 * u) = x[q];
-            }
-          }
-        }
-        __syncthreads();
-        if (d < dk && prm.center_tile == kCenterTile) {
-          // Tiles of kCenterTile rows from the first new row (kCenterRows is a
-          // multiple, so chunks start on tile boundaries), each summed by a
-          // halving tree with zeros past the last row, then added in order.
-          static_assert(kCenterRows % kCenterTile == 0, "center chunks hold whole tiles");
-          for (int t0 = 0; t0 < rows; t0 += kCenterTile) {
-            float x[kCenterTile];
-#pragma unroll
-            for (int q = 0; q < kCenterTile; ++q)
-              x[q] = t0 + q < rows ? bf16_to_f32(stage[(t0 + q) * dk + d]) : 0.f;
-#pragma unroll
-            for (int h = kCenterTile / 2; h >= 1; h /= 2) {
-#pragma unroll
-              for (int q = 0; q < h; ++q) x[q] = x[q] + x[q + h];
-            }
-            acc = (c0 == first && t0 == 0) ? x[0] : acc + x[0];
-          }
-        } else if (d < dk) {
-          int rr = 0;
-          if (c0 == first) {
-            acc = bf16_to_f32(stage[d]);
-            rr = 1;
-          }
-          for (; rr + 8 <= rows; rr += 8) {
-            float x[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) x[q] = bf16_to_f32(stage[(rr + q) * dk + d]);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc = acc + x[q];
-          }
-          for (; rr < rows; ++rr) acc = acc + bf16_to_f32(stage[rr * dk + d]);
-        }
-        __syncthreads();
-      }
-      const float pre = n_eff;
-      const float den = pre + static_cast<float>(nn);
-      if (d < dk) mu_d = pre > 0.f ? (pre * mu_d + acc) / den : acc / static_cast<float>(nn);
-      n_eff = den;
-    }
-    if (d < dk) mu[d] = mu_d;
-    if (threadIdx.x == 0) c.n_eff[cl] = n_eff;
-    return;
-  }
 
   // Ladder role.
   for (int e = threadIdx.x; e < L; e += kThreads) counts_s[e] = c.level_count[cl * L + e];
@@ -909,7 +945,6 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
     LadderPlan pl;
     pl.active = nn > 0 ? 1 : 0;
     pl.kind0 = kind0;
-    pl.m_tok = m;
     pl.first = first;
     pl.order_base = order_base;
     int mm = m0;
@@ -919,7 +954,17 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
       pl.m[e] = used ? mm : 0;
       mm = used ? carries_of(counts_s[e], mm, B, e == L - 1) : 0;
     }
-    ws.plans[ladder] = pl;
+    // Every field but m_tok (bucket_kernel's count, which the center launch
+    // may be reading concurrently).
+    LadderPlan* dst = ws.plans + ladder;
+    dst->active = pl.active;
+    dst->kind0 = pl.kind0;
+    dst->first = pl.first;
+    dst->order_base = pl.order_base;
+    for (int e = 0; e < kMaxLevels; ++e) {
+      dst->cnt[e] = pl.cnt[e];
+      dst->m[e] = pl.m[e];
+    }
     c.n_total[cl] = n_total;
     c.p_hi_c[cl] = p_hi;
     c.level0_phase[cl] = phase;
@@ -1928,18 +1973,84 @@ int launch_ward_step(const LadderArgs& c, const Workspace& ws, const int32_t* jo
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
+// A side stream and its fork / join events per (device, caller stream),
+// created on first use and kept for the process (default priority,
+// non-blocking). Returned locked: the caller unlocks once its join is
+// enqueued, so two host threads on one stream never share the events
+// mid-sequence. Null when none can be made (the work then stays on the
+// caller's stream).
+struct SideStream {
+  int dev = -1;
+  hipStream_t main = nullptr, side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex mu;
+};
+
+static SideStream* side_stream_for(hipStream_t main) {
+  constexpr int kSlots = 64;
+  static SideStream slots[kSlots];
+  static std::mutex table_mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  SideStream* hit = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(table_mu);
+    for (SideStream& e : slots)
+      if (e.side && e.dev == dev && e.main == main) hit = &e;
+    if (!hit) {
+      for (SideStream& e : slots)
+        if (!e.side) {
+          hipStream_t s = nullptr;
+          hipEvent_t f = nullptr, j = nullptr;
+          if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+          if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+              hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess)
+            return nullptr;
+          e.dev = dev;
+          e.main = main;
+          e.fork = f;
+          e.join = j;
+          e.side = s;
+          hit = &e;
+          break;
+        }
+    }
+  }
+  if (hit) hit->mu.lock();
+  return hit;
+}
+
 int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
                   hipStream_t stream) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
-  size_t region = static_cast<size_t>(kCenterRows) * c.dk * 2;
-  if (p.late_joins) region += static_cast<size_t>(ws.sort_width) * 8;
-  const size_t shmem = tok_bytes + region;
+  const size_t shmem = tok_bytes + (p.late_joins ? static_cast<size_t>(ws.sort_width) * 8 : 0);
   if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel), shmem)) return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(bucket_kernel, dim3(c.n_batch * c.n_groups), dim3(kBucketThreads), 0, stream, c, r, ws);
-  // y = 0: ladder blocks; y = 1: center blocks (independent outputs, same rows).
-  hipLaunchKernelGGL(commit_kernel, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
-  return launch_levels(c, r, p, ws, stream);
+  // The center updates run beside the ladder launches (a few clusters can hold
+  // most of a flush's rows, and each center is a fold over its rows in order).
+  SideStream* side = side_stream_for(stream);
+  hipStream_t cs = stream;
+  if (side && hipEventRecord(side->fork, stream) == hipSuccess && hipStreamWaitEvent(side->side, side->fork, 0) == hipSuccess)
+    cs = side->side;
+  const int nj = (c.dk + kCenterWaves * kWave - 1) / (kCenterWaves * kWave);
+  const size_t ctok_bytes = 2 * static_cast<size_t>(r.tokens);
+  if (nj == 1) hipLaunchKernelGGL(center_kernel<1>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p,
+                                  ws);
+  else hipLaunchKernelGGL(center_kernel<2>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p, ws);
+  const bool forked = cs != stream;
+  if (forked && hipEventRecord(side->join, cs) != hipSuccess) {
+    if (side) side->mu.unlock();
+    return LOGKV_ERUNTIME;
+  }
+  hipLaunchKernelGGL(commit_kernel, dim3(ladders), dim3(kThreads), shmem, stream, c, r, p, ws);
+  const int rc = launch_levels(c, r, p, ws, stream);
+  if (forked && hipStreamWaitEvent(stream, side->join, 0) != hipSuccess) {
+    side->mu.unlock();
+    return LOGKV_ERUNTIME;
+  }
+  if (side) side->mu.unlock();
+  return rc;
 }
 
 // The level launches that follow a prepare step (commit_kernel or ward_kernel):
