@@ -1775,9 +1775,9 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
 // (grid y = 1), whose saturated fold keeps its registers out of the other
 // levels' launch.
 template <bool TOP>
-__global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs r, Workspace ws) {
+__global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs r, Workspace ws, int ell0) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  const int ladder = blockIdx.x, ell = TOP ? c.levels - 1 : static_cast<int>(blockIdx.y);
+  const int ladder = blockIdx.x, ell = TOP ? c.levels - 1 : ell0 + static_cast<int>(blockIdx.y);
   const LadderPlan* pl = ws.plans + ladder;
   // The last launch of a commit marks every cluster that took rows as live.
   if (TOP && threadIdx.x == 0 && pl->m_tok > 0) c.alive[ladder] = 1;
@@ -1983,6 +1983,7 @@ struct SideStream {
   int dev = -1;
   hipStream_t main = nullptr, side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  hipEvent_t level[kMaxLevels] = {};   // level ell's carries enqueued on the caller's stream
   std::mutex mu;
 };
 
@@ -2006,6 +2007,8 @@ static SideStream* side_stream_for(hipStream_t main) {
           if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
               hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess)
             return nullptr;
+          for (hipEvent_t& ev : e.level)
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return nullptr;
           e.dev = dev;
           e.main = main;
           e.fork = f;
@@ -2039,12 +2042,12 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
                                   ws);
   else hipLaunchKernelGGL(center_kernel<2>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p, ws);
   const bool forked = cs != stream;
-  if (forked && hipEventRecord(side->join, cs) != hipSuccess) {
-    if (side) side->mu.unlock();
+  hipLaunchKernelGGL(commit_kernel, dim3(ladders), dim3(kThreads), shmem, stream, c, r, p, ws);
+  const int rc = launch_levels(c, r, p, ws, stream, forked ? side : nullptr);
+  if (forked && hipEventRecord(side->join, side->side) != hipSuccess) {
+    side->mu.unlock();
     return LOGKV_ERUNTIME;
   }
-  hipLaunchKernelGGL(commit_kernel, dim3(ladders), dim3(kThreads), shmem, stream, c, r, p, ws);
-  const int rc = launch_levels(c, r, p, ws, stream);
   if (forked && hipStreamWaitEvent(stream, side->join, 0) != hipSuccess) {
     side->mu.unlock();
     return LOGKV_ERUNTIME;
@@ -2056,7 +2059,7 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
 // The level launches that follow a prepare step (commit_kernel or ward_kernel):
 // carry work units, carries per level, then the slot writes of every level.
 int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
-                  hipStream_t stream) {
+                  hipStream_t stream, SideStream* side) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
   if (c.levels > 1) {
@@ -2086,11 +2089,22 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
         hipLaunchKernelGGL(carries_kernel<2>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
       else
         hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
+      // With a side stream, level ell's finish (its slots: staged rows in, survivors moved) runs
+      // there once this launch is done: the later carries launches read only higher levels' slots
+      // and the carry buffers, which no finish writes.
+      if (side) {
+        if (hipEventRecord(side->level[ell], stream) != hipSuccess ||
+            hipStreamWaitEvent(side->side, side->level[ell], 0) != hipSuccess)
+          return LOGKV_ERUNTIME;
+        hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, 1), dim3(kThreads), tok_bytes, side->side, c, r, ws,
+                           ell);
+      }
     }
   }
-  if (c.levels > 1)
-    hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, c.levels - 1), dim3(kThreads), tok_bytes, stream, c, r, ws);
-  hipLaunchKernelGGL(finish_kernel<true>, dim3(ladders, 1), dim3(kThreads), tok_bytes, stream, c, r, ws);
+  if (c.levels > 1 && !side)
+    hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, c.levels - 1), dim3(kThreads), tok_bytes, stream, c, r, ws,
+                       0);
+  hipLaunchKernelGGL(finish_kernel<true>, dim3(ladders, 1), dim3(kThreads), tok_bytes, stream, c, r, ws, 0);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 

@@ -140,6 +140,6 @@ int launch_unified_summary(const LadderArgs& c, const UnifiedBufs& u, int32_t* s
 int launch_ward_step(const LadderArgs& c, const Workspace& ws, const int32_t* jobs, const int32_t* n_jobs, int step,
                      hipStream_t stream);
 int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, const Workspace& ws,
-                  hipStream_t stream);
+                  hipStream_t stream, struct SideStream* side = nullptr);
 
 }  // namespace logkv
