@@ -46,64 +46,109 @@ __device__ __forceinline__ float canon_sum(const float* t) {
 
 constexpr int kTokBatch = 8;   // span rows whose loads are issued together
 
-// Token statistics of one component over a span: means (per lane features),
-// energy E and mean square of the means; returns R = residual / energy. Rows
-// are loaded kTokBatch at a time and then added in span order.
+// x / d rounded as the division: a product with the reciprocal when d is a
+// power of two (the reciprocal is exact, so the product's one rounding is the
+// quotient's).
+struct DimDiv {
+  float d, inv;
+  bool pow2;
+  __device__ __forceinline__ explicit DimDiv(int D)
+      : d(static_cast<float>(D)), inv(1.0f / static_cast<float>(D)), pow2(D > 0 && (D & (D - 1)) == 0) {}
+  __device__ __forceinline__ float operator()(float x) const { return pow2 ? x * inv : x / d; }
+};
+
+// Running token statistics of one component over a span.
 template <int NJ>
-__device__ __forceinline__ float span_component(const Rows2& src, int b, int g, const LOGKV_G int32_t* tok, int n,
-                                                int D, float* mean, float& energy, float& msq) {
+struct SpanAcc {
+  float acc[NJ];
+  float e;
+};
+
+// Folds kTokBatch held rows (those of them before `rows`) into a component's
+// statistics: token sums and the rows' mean squares (canonical sums of
+// squares, four rows per fold, divided by D lane-parallel), in span order.
+template <int NJ>
+__device__ __forceinline__ void span_fold(const float (&x)[kTokBatch][NJ], int i0, int rows, const DimDiv& dd,
+                                          SpanAcc<NJ>& s) {
   const int l = lane_id();
-  float acc[NJ], e = 0.f;
+  float ss[kTokBatch];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = 0.f;
-  const float d_f = static_cast<float>(D);
-  for (int i0 = 0; i0 < n; i0 += kTokBatch) {
-    float xb[kTokBatch][NJ];
+  for (int t = 0; t < kTokBatch; t += 4) {
+    float part[4];
 #pragma unroll
-    for (int t = 0; t < kTokBatch; ++t) {
-      const int i = i0 + t < n ? i0 + t : n - 1;
-      const LOGKV_G uint16_t* row = src.row(b, g, tok[i]);
+    for (int k = 0; k < 4; ++k) {
+      part[k] = x[t + k][0] * x[t + k][0];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) xb[t][j] = feat_or_zero(row, l + j * kWave, D);
+      for (int j = 1; j < NJ; ++j) part[k] = part[k] + x[t + k][j] * x[t + k][j];
     }
-    // Per-row canonical sums of squares, four rows per fold; the rows' mean
-    // squares (sum / D) as one lane-parallel division, added in span order.
-    float ss[kTokBatch];
-#pragma unroll
-    for (int t = 0; t < kTokBatch; t += 4) {
-      float part[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        part[k] = xb[t + k][0] * xb[t + k][0];
-#pragma unroll
-        for (int j = 1; j < NJ; ++j) part[k] = part[k] + xb[t + k][j] * xb[t + k][j];
-      }
-      wave_sum4(part[0], part[1], part[2], part[3], ss[t], ss[t + 1], ss[t + 2], ss[t + 3]);
-    }
-    float num = 0.f;
-#pragma unroll
-    for (int t = 0; t < kTokBatch; ++t) num = l == t ? ss[t] : num;
-    const float msl = num / d_f;
-#pragma unroll
-    for (int t = 0; t < kTokBatch; ++t) {
-      const int i = i0 + t;
-      if (i >= n) break;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[j] = i == 0 ? xb[t][j] : acc[j] + xb[t][j];
-      const float ms = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(msl), t));
-      e = i == 0 ? ms : e + ms;
-    }
+    wave_sum4(part[0], part[1], part[2], part[3], ss[t], ss[t + 1], ss[t + 2], ss[t + 3]);
   }
+  float num = 0.f;
+#pragma unroll
+  for (int t = 0; t < kTokBatch; ++t) num = l == t ? ss[t] : num;
+  const float msl = dd(num);
+#pragma unroll
+  for (int t = 0; t < kTokBatch; ++t) {
+    if (t >= rows) break;
+    const int i = i0 + t;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) s.acc[j] = i == 0 ? x[t][j] : s.acc[j] + x[t][j];
+    const float ms = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(msl), t));
+    s.e = i == 0 ? ms : s.e + ms;
+  }
+}
+
+// A component's means (per lane features), energy E and mean square of the
+// means; returns R = residual / energy.
+template <int NJ>
+__device__ __forceinline__ float span_finish(const SpanAcc<NJ>& s, int n, int D, const DimDiv& dd, float* mean,
+                                             float& energy, float& msq) {
+  const int l = lane_id();
   const float cnt = static_cast<float>(n);
   float m2[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    mean[j] = acc[j] / cnt;
+    mean[j] = s.acc[j] / cnt;
     m2[j] = (l + j * kWave < D) ? mean[j] * mean[j] : 0.f;
   }
-  energy = e / cnt;
-  msq = canon_sum<NJ>(m2) / d_f;
+  energy = s.e / cnt;
+  msq = dd(canon_sum<NJ>(m2));
   return fmaxf(energy - msq, 0.f) / fmaxf(energy, 1e-12f);
+}
+
+// Token statistics of both components over a span in one pass: the span's row
+// indices are read a lane each, 64 at a time, and kTokBatch K and V rows are
+// loaded together per step.
+template <int NJ>
+__device__ __forceinline__ void span_components(const Rows2& ks, const Rows2& vs, int b, int g,
+                                                const LOGKV_G int32_t* tok, int n, int dk, int dv, float* mean_k,
+                                                float& e_k, float& msq_k, float& rk, float& rv) {
+  const int l = lane_id();
+  const DimDiv dk_div(dk), dv_div(dv);
+  SpanAcc<NJ> sk{}, sv{};
+  for (int c0 = 0; c0 < n; c0 += kWave) {
+    const int cn = min(kWave, n - c0);
+    const int tl = l < cn ? tok[c0 + l] : 0;
+    for (int i0 = 0; i0 < cn; i0 += kTokBatch) {
+      float xk[kTokBatch][NJ], xv[kTokBatch][NJ];
+#pragma unroll
+      for (int t = 0; t < kTokBatch; ++t) {
+        const int tt = __builtin_amdgcn_readlane(tl, min(i0 + t, cn - 1));
+        const LOGKV_G uint16_t* rowk = ks.row(b, g, tt);
+        const LOGKV_G uint16_t* rowv = vs.row(b, g, tt);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          xk[t][j] = feat_or_zero(rowk, l + j * kWave, dk);
+          xv[t][j] = feat_or_zero(rowv, l + j * kWave, dv);
+        }
+      }
+      span_fold<NJ>(xk, c0 + i0, cn - i0, dk_div, sk);
+      span_fold<NJ>(xv, c0 + i0, cn - i0, dv_div, sv);
+    }
+  }
+  float mean_v[NJ], e_v, msq_v;
+  rk = span_finish<NJ>(sk, n, dk, dk_div, mean_k, e_k, msq_k);
+  rv = span_finish<NJ>(sv, n, dv, dv_div, mean_v, e_v, msq_v);
 }
 
 // Candidate slots of the select path: row b owns slots [b * slots, (b + 1) *
@@ -130,30 +175,45 @@ __device__ __forceinline__ void score_span(const logkv_span_args& a, int s, floa
   if (g < G && n > 0) {
     Rows2 ks{gp(a.pool_k), a.pk_sb, a.pk_sg, a.pk_st, gp(a.flush_k), a.fk_sb, a.fk_sg, a.fk_st, a.old_width};
     Rows2 vs{gp(a.pool_v), a.pv_sb, a.pv_sg, a.pv_st, gp(a.flush_v), a.fv_sb, a.fv_sg, a.fv_st, a.old_width};
-    float mean_k[NJ], mean_v[NJ], e_k, e_v, msq_k, msq_v;
-    const float rk = span_component<NJ>(ks, b, g, tok, n, a.dk, mean_k, e_k, msq_k);
-    const float rv = span_component<NJ>(vs, b, g, tok, n, a.dv, mean_v, e_v, msq_v);
+    float mean_k[NJ], e_k, msq_k, rk, rv;
+    span_components<NJ>(ks, vs, b, g, tok, n, a.dk, a.dv, mean_k, e_k, msq_k, rk, rv);
     float q = 0.f;
     if (a.beta_novelty) {
       const int l = lane_id();
       const LOGKV_G float* mu = gp(a.centroids) + (static_cast<int64_t>(b) * G + g) * a.k_max * a.dk;
       const LOGKV_G uint8_t* valid = gp(a.centroid_valid) + (static_cast<int64_t>(b) * G + g) * a.k_max;
+      const DimDiv dk_div(a.dk);
       float nearest = __builtin_inff();
       bool any = false;
-      for (int c = 0; c < a.k_max; ++c) {
-        float dt[NJ], cc[NJ];
+      // Four centers at a time: their dot and square sums, each one canonical sum (wave_sum4).
+      for (int c0 = 0; c0 < a.k_max; c0 += 4) {
+        float pd[4], pc[4];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float m = feat_or_zero(mu + c * a.dk, l + j * kWave, a.dk);
-          dt[j] = mean_k[j] * m;
-          cc[j] = m * m;
+        for (int k = 0; k < 4; ++k) {
+          const int c = min(c0 + k, a.k_max - 1);
+          float m[NJ];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) m[j] = feat_or_zero(mu + c * a.dk, l + j * kWave, a.dk);
+          pd[k] = mean_k[0] * m[0];
+          pc[k] = m[0] * m[0];
+#pragma unroll
+          for (int j = 1; j < NJ; ++j) {
+            pd[k] = pd[k] + mean_k[j] * m[j];
+            pc[k] = pc[k] + m[j] * m[j];
+          }
         }
-        const float dot = canon_sum<NJ>(dt) / static_cast<float>(a.dk);
-        const float cms = canon_sum<NJ>(cc) / static_cast<float>(a.dk);
-        const float dist = fmaxf((msq_k + cms) - 2.0f * dot, 0.f);
-        if (valid[c]) {
-          any = true;
-          nearest = fminf(nearest, dist);
+        float sd[4], sc[4];
+        wave_sum4(pd[0], pd[1], pd[2], pd[3], sd[0], sd[1], sd[2], sd[3]);
+        wave_sum4(pc[0], pc[1], pc[2], pc[3], sc[0], sc[1], sc[2], sc[3]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int c = c0 + k;
+          if (c >= a.k_max) break;
+          const float dist = fmaxf((msq_k + dk_div(sc[k])) - 2.0f * dk_div(sd[k]), 0.f);
+          if (valid[c]) {
+            any = true;
+            nearest = fminf(nearest, dist);
+          }
         }
       }
       if (!any) nearest = 0.f;
