@@ -27,7 +27,7 @@ namespace logkv {
 
 namespace {
 
-constexpr int kPlanThreads = 256;
+constexpr int kPlanThreads = 1024;
 constexpr int kTile = 64;          // rows per staged K/V tile
 constexpr int kSplitRows = 512;    // rows per attention split (staged decode kernel)
 constexpr int kStreamRows = 512;   // most rows per split of the streaming kernel when the grid is not the limit
@@ -44,29 +44,44 @@ struct PlanCtx {
 
 // Lane pooled-row prefix over (cluster, level top-down) blocks -> plan table
 // [lanes, K*L + 1] (offsets), plus the maximum lane count at table[lanes*(K*L+1)].
+// One thread per lane; a lane's counts are loaded kPlanChunk at a time, all
+// before the chunk's prefix stores.
+constexpr int kPlanChunk = 32;
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(logkv_readout_view c, int32_t* __restrict__ table) {
-  __shared__ int lane_max[kPlanThreads];
+  __shared__ int wave_max[kPlanThreads / kWave];
   const int lanes = c.n_batch * c.n_groups;
-  const int KL = c.k_max * c.levels;
+  const int L = c.levels, KL = c.k_max * L;
   int best = 0;
   for (int lane = threadIdx.x; lane < lanes; lane += kPlanThreads) {
     const LOGKV_G int16_t* cnt = gp(c.level_count) + static_cast<int64_t>(lane) * KL;
     LOGKV_G int32_t* row = gp(table) + static_cast<int64_t>(lane) * (KL + 1);
     int acc = 0;
-    for (int cc = 0; cc < c.k_max; ++cc) {
-      for (int e = c.levels - 1; e >= 0; --e) {
-        row[cc * c.levels + (c.levels - 1 - e)] = acc;
-        acc += cnt[cc * c.levels + e];
+    for (int j0 = 0; j0 < KL; j0 += kPlanChunk) {
+      int v[kPlanChunk];
+#pragma unroll
+      for (int q = 0; q < kPlanChunk; ++q) {
+        // Table entry j = cc * L + k is cluster cc's level L - 1 - k (top level first).
+        const int j = min(j0 + q, KL - 1), cc = j / L, k = j - cc * L;
+        v[q] = cnt[cc * L + (L - 1 - k)];
+      }
+#pragma unroll
+      for (int q = 0; q < kPlanChunk; ++q) {
+        if (j0 + q < KL) {
+          row[j0 + q] = acc;
+          acc += v[q];
+        }
       }
     }
     row[KL] = acc;
     best = acc > best ? acc : best;
   }
-  lane_max[threadIdx.x] = best;
+  for (int off = kWave / 2; off >= 1; off >>= 1) best = max(best, __shfl_xor(best, off, kWave));
+  if (lane_id() == 0) wave_max[wave_id()] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
     int m = 0;
-    for (int i = 0; i < kPlanThreads; ++i) m = lane_max[i] > m ? lane_max[i] : m;
+    for (int i = 0; i < kPlanThreads / kWave; ++i) m = wave_max[i] > m ? wave_max[i] : m;
     table[static_cast<int64_t>(lanes) * (KL + 1)] = m;
   }
 }
