@@ -40,6 +40,9 @@ STATE = (
     "alive", "s_h", "_unified_limits", "alpha_count_dev",
 )
 STATE_SET = frozenset(STATE)
+# The exact pool's buffer set, which the owner swaps with its spare set at every Alpha flush.
+ALPHA_SET = ("alpha_k_raw", "alpha_v", "alpha_pos", "alpha_valid", "alpha_span_len", "alpha_span_closed",
+             "alpha_span_count")
 
 _enabled = True
 _open: dict = {}          # configuration key -> the group new caches join (not yet adopted)
@@ -168,6 +171,23 @@ class FlushGroup:
             m._views = {}
         m._mid_decode_state = None
 
+    def _swap_alpha(self, m):
+        """After a stacked Alpha flush only the exact-pool set changed (the owner swapped its two
+        sets): member ``m`` takes its views of the owner's current set, built once per set."""
+        owner, i, bt = self.owner, m._group_index, self.rows
+        cur = owner._buffers["alpha_k_raw"]
+        cache = m.__dict__.setdefault("_alpha_view_sets", {})
+        hit = cache.get(owner._alpha_parity)
+        if hit is None or hit[0] is not cur:
+            views = {name: owner._buffers[name][i * bt:(i + 1) * bt] for name in ALPHA_SET if name in m._buffers}
+            spare = tuple(t[i * bt:(i + 1) * bt] for t in owner._alpha_spare)
+            hit = cache[owner._alpha_parity] = (cur, views, spare)
+        m._buffers.update(hit[1])
+        d = m.__dict__
+        d["_alpha_spare"] = hit[2]
+        d["_alpha_parity"] = owner._alpha_parity
+        d["_mid_decode_state"] = None
+
     def _realign(self, m):
         """After a member's own Alpha flushes left its exact pool in the other buffer set, copy it back
         into the owner's current set, so the member's rows and the owner's current set agree again."""
@@ -223,7 +243,7 @@ class FlushGroup:
             self.stacked_runs += 1
             if owner.alpha_exact_tokens:
                 for m in members:
-                    self._point(m, m._group_index, fresh=False)
+                    self._swap_alpha(m)
             return
         for m, (take, count) in jobs:
             m.recent_count = count
