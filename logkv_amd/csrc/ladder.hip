@@ -685,11 +685,11 @@ __device__ __forceinline__ void center_batch_fold(float (&x)[kCenterTile][NJ], i
   }
 }
 
+// One ladder's center update by a block of at least kCenterWaves waves (the
+// others leave once the row list is staged in `ctok`, 2 * T bytes of LDS).
 template <int NJ>
-__global__ __launch_bounds__(kCenterWaves* kWave) void center_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
-                                                                    Workspace ws) {
-  extern __shared__ __align__(16) uint16_t ctok[];
-  const int ladder = static_cast<int>(blockIdx.x);
+__device__ __forceinline__ void center_block(const LadderArgs& c, const RowsArgs& r, const RouteParams& prm,
+                                             const Workspace& ws, int ladder, uint16_t* ctok) {
   if (ws.abort && *ws.abort) return;   // a failed replay check: nothing written
   const int m = ws.plans[ladder].m_tok;
   if (m == 0) return;
@@ -702,9 +702,10 @@ __global__ __launch_bounds__(kCenterWaves* kWave) void center_kernel(LadderArgs 
   const int nn = m - first;
   {
     const LOGKV_G uint16_t* list = gp(ws.tok + cl * r.tokens);
-    for (int i = threadIdx.x; i < m; i += kCenterWaves * kWave) ctok[i] = list[i];
+    for (int i = threadIdx.x; i < m; i += blockDim.x) ctok[i] = list[i];
   }
   __syncthreads();
+  if (wave_id() >= kCenterWaves) return;
   const LOGKV_G uint16_t* kb = gp(r.k + b * r.k_sb + g * r.k_sg);
   LOGKV_G float* mu = gp(c.centroid + cl * dk);
   const int f0 = wave_id() * kWave + lane_id();
@@ -746,6 +747,17 @@ __global__ __launch_bounds__(kCenterWaves* kWave) void center_kernel(LadderArgs 
   if (threadIdx.x == 0) c.n_eff[cl] = n_eff;
 }
 
+template <int NJ>
+__global__ __launch_bounds__(kCenterWaves* kWave) void center_kernel(LadderArgs c, RowsArgs r, RouteParams prm,
+                                                                    Workspace ws) {
+  extern __shared__ __align__(16) uint16_t ctok[];
+  center_block<NJ>(c, r, prm, ws, static_cast<int>(blockIdx.x), ctok);
+}
+
+// The ladder plans of the commit (y = 0) and, when the call has no side stream
+// for center_kernel and keys of at most 128 features, the center updates
+// beside them (y = 1, CENTERS).
+template <bool CENTERS>
 __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs r, RouteParams prm, Workspace ws) {
   extern __shared__ __align__(16) uint8_t dyn[];
   __shared__ int16_t counts_s[64];
@@ -756,6 +768,12 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   uint16_t* tok = reinterpret_cast<uint16_t*>(dyn);
   const int keys_off = (2 * r.tokens + 15) & ~15;
+  if constexpr (CENTERS) {
+    if (blockIdx.y == 1) {   // keys of at most 128 features
+      center_block<1>(c, r, prm, ws, ladder, tok);
+      return;
+    }
+  }
 
   if (ws.abort && *ws.abort) {
     // A failed replay check: no rows, nothing written (the later launches read the plan).
@@ -1987,6 +2005,8 @@ struct SideStream {
   std::mutex mu;
 };
 
+constexpr int kSideLadders = 1024;
+
 static SideStream* side_stream_for(hipStream_t main) {
   constexpr int kSlots = 64;
   static SideStream slots[kSlots];
@@ -2028,21 +2048,33 @@ int launch_commit(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
   const size_t shmem = tok_bytes + (p.late_joins ? static_cast<size_t>(ws.sort_width) * 8 : 0);
-  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel), shmem)) return LOGKV_ERUNTIME;
+  if (!allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel<false>), shmem) ||
+      !allow_dynamic_lds(reinterpret_cast<const void*>(&commit_kernel<true>), shmem))
+    return LOGKV_ERUNTIME;
   hipLaunchKernelGGL(bucket_kernel, dim3(c.n_batch * c.n_groups), dim3(kBucketThreads), 0, stream, c, r, ws);
   // The center updates run beside the ladder launches (a few clusters can hold
-  // most of a flush's rows, and each center is a fold over its rows in order).
-  SideStream* side = side_stream_for(stream);
+  // most of a flush's rows, and each center is a fold over its rows in order),
+  // for calls of at least kSideLadders ladders: every cross-queue event costs
+  // the queue a few microseconds, and small calls from several streams would
+  // share the device's few hardware queues with their side streams.
+  SideStream* side = ladders >= kSideLadders ? side_stream_for(stream) : nullptr;
   hipStream_t cs = stream;
   if (side && hipEventRecord(side->fork, stream) == hipSuccess && hipStreamWaitEvent(side->side, side->fork, 0) == hipSuccess)
     cs = side->side;
-  const int nj = (c.dk + kCenterWaves * kWave - 1) / (kCenterWaves * kWave);
-  const size_t ctok_bytes = 2 * static_cast<size_t>(r.tokens);
-  if (nj == 1) hipLaunchKernelGGL(center_kernel<1>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p,
-                                  ws);
-  else hipLaunchKernelGGL(center_kernel<2>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p, ws);
   const bool forked = cs != stream;
-  hipLaunchKernelGGL(commit_kernel, dim3(ladders), dim3(kThreads), shmem, stream, c, r, p, ws);
+  const int nj = (c.dk + kCenterWaves * kWave - 1) / (kCenterWaves * kWave);
+  const bool inline_centers = !forked && nj == 1;   // commit_kernel's y = 1 blocks
+  if (!inline_centers) {
+    const size_t ctok_bytes = 2 * static_cast<size_t>(r.tokens);
+    if (nj == 1)
+      hipLaunchKernelGGL(center_kernel<1>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p, ws);
+    else
+      hipLaunchKernelGGL(center_kernel<2>, dim3(ladders), dim3(kCenterWaves * kWave), ctok_bytes, cs, c, r, p, ws);
+  }
+  if (inline_centers)
+    hipLaunchKernelGGL(commit_kernel<true>, dim3(ladders, 2), dim3(kThreads), shmem, stream, c, r, p, ws);
+  else
+    hipLaunchKernelGGL(commit_kernel<false>, dim3(ladders, 1), dim3(kThreads), shmem, stream, c, r, p, ws);
   const int rc = launch_levels(c, r, p, ws, stream, forked ? side : nullptr);
   if (forked && hipEventRecord(side->join, side->side) != hipSuccess) {
     side->mu.unlock();
