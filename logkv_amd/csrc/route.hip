@@ -999,10 +999,11 @@ int launch_route(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, c
       ok = allow_dynamic_lds(reinterpret_cast<const void*>(attach_mfma_kernel), shmem);
       if (ok) {
         const int tiles = (r.tokens + 31) / 32;
-        const int per_block = kAttachMfmaWaves * kAttachTilesPerWave;
+        // Two tiles per wave share a block's staged centers; a small launch takes one, for more blocks.
+        const int tpw = static_cast<int64_t>(tiles) * lanes >= 4096 ? kAttachTilesPerWave : 1;
+        const int per_block = kAttachMfmaWaves * tpw;
         hipLaunchKernelGGL(attach_mfma_kernel, dim3((tiles + per_block - 1) / per_block, lanes),
-                           dim3(kAttachMfmaWaves * kWave), shmem, stream, c, r, p, ws.order, ws.assign, ws.s_win,
-                           kAttachTilesPerWave);
+                           dim3(kAttachMfmaWaves * kWave), shmem, stream, c, r, p, ws.order, ws.assign, ws.s_win, tpw);
       }
     } else if (nj == 1) ok = attach(attach_kernel<1>, attach_tile<1>(), attach_shmem<1>(c.k_max));
     else if (nj == 2) ok = attach(attach_kernel<2>, attach_tile<2>(), attach_shmem<2>(c.k_max));
