@@ -170,6 +170,20 @@ struct PoolT {
     const LOGKV_G float* wp = st ? L.w + base + p : src.buf.w + (p - cnt);
     return *wp;
   }
+  // Row pointers and metadata of pool row p whose staged row index t is
+  // already known (KIND 2: a flush row list read ahead).
+  __device__ __forceinline__ const LOGKV_G uint16_t* k_at(int p, int64_t t) const {
+    return p < cnt ? L.k + (base + p) * L.dk : src.kb + t * src.k_st;
+  }
+  __device__ __forceinline__ const LOGKV_G uint16_t* v_at(int p, int64_t t) const {
+    return p < cnt ? L.v + (base + p) * L.dv : src.vb + t * src.v_st;
+  }
+  __device__ __forceinline__ Meta meta_at(int p, int64_t t) const {
+    const bool st = p < cnt;
+    const int64_t pos = src.posb[t];
+    const Meta stored = slot_meta(L, st ? base + p : base);
+    return st ? stored : Meta{1.0f, pos, pos, pos, src.order_base + (p - cnt), 0};
+  }
   __device__ __forceinline__ Meta meta(int p) const {
     const bool st = p < cnt;
     const int64_t i = st ? base + p : 0;
@@ -1234,6 +1248,21 @@ struct GroupRows {
   float w[4];
 };
 
+// Group rows of a flush-sourced pool whose four staged row indices (for rows
+// start .. start + 3) were read ahead.
+__device__ __forceinline__ void group_rows_at(const PoolT<2>& pool, int start, int width, const uint32_t (&t)[4],
+                                              GroupRows& g) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = i < width ? start + i : start;
+    const int64_t ti = i < width ? t[i] : t[0];
+    g.k[i] = pool.k_at(p, ti);
+    g.v[i] = pool.v_at(p, ti);
+    const float wp = pool.w(p);
+    g.w[i] = i < width ? wp : 0.f;
+  }
+}
+
 template <int KIND>
 __device__ __forceinline__ void group_rows(const PoolT<KIND>& pool, int start, int width, GroupRows& g) {
 #pragma unroll
@@ -1578,7 +1607,8 @@ __device__ inline Src flush_rows_planned(const LadderArgs& c, const RowsArgs& r,
 // decides from the held rows and the side means are written from them.
 // Returns false (nothing written) when the screen does not settle the cut.
 __device__ __forceinline__ bool beta_row_group_held(const LadderArgs& c, const RowsArgs& r, const Workspace& ws,
-                                                    const RowPlan& pp, int ell, int gi, bool live) {
+                                                    const RowPlan& pp, int ell, int gi, bool live,
+                                                    const uint32_t (&pre)[4], bool have_pre) {
   const int l16 = lane_id() & 15, mi = l16 & 3;
   const int n_pair = 2 * carries_of(pp.cnt, pp.m, c.slots, false);
   const int start = 4 * gi;
@@ -1589,8 +1619,13 @@ __device__ __forceinline__ bool beta_row_group_held(const LadderArgs& c, const R
   Meta mine{};
   if (pp.flush_src) {
     const PoolT<2> pool{lad, base, pp.cnt, flush_rows_planned(c, r, ws, pp)};
-    group_rows<2>(pool, start, width, g);
-    if (l16 < 8 && mi < width) mine = pool.meta(start + mi);
+    if (have_pre) {
+      group_rows_at(pool, start, width, pre, g);
+      if (l16 < 8 && mi < width) mine = pool.meta_at(start + mi, pre[mi]);
+    } else {
+      group_rows<2>(pool, start, width, g);
+      if (l16 < 8 && mi < width) mine = pool.meta(start + mi);
+    }
   } else {
     const PoolT<1> pool{lad, base, pp.cnt, staged_of(ws, pp.ladder, ell, c.dk, c.dv)};
     group_rows<1>(pool, start, width, g);
@@ -1689,6 +1724,10 @@ __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderAr
   if constexpr (FULL) {
     RowPlan pp;
     pp.ladder = -1;
+    // The next group's flush row indices, read a group ahead when it is on the
+    // same flush-sourced ladder (its loads precede this group's row loads).
+    uint32_t pre[4] = {0u, 0u, 0u, 0u};
+    int pre_ladder = -1, pre_gi = -1;
     for (; qd < qd_end; ++qd) {
       const int unit = 4 * qd + row;
       const bool live = unit < total;
@@ -1696,7 +1735,25 @@ __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderAr
       while (prefix_s[ladder + 1] <= uu) ++ladder;
       if (ladder != pp.ladder) load_row_plan(ws, ladder, ell, pp);
       const int gi = uu - prefix_s[ladder];
-      const bool settled = beta_row_group_held(c, r, ws, pp, ell, gi, live);
+      const bool have_pre = pre_ladder == ladder && pre_gi == gi;
+      uint32_t cur[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cur[i] = pre[i];
+      const int nx = uu + 4;
+      if (pp.flush_src && qd + 1 < qd_end && nx < total && nx < prefix_s[ladder + 1]) {
+        const LOGKV_G uint16_t* gtok = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens + pp.first);
+        const int n_rows = pp.cnt + pp.m;   // pool rows: stored, then staged
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = 4 * (gi + 4) + i;
+          pre[i] = (p >= pp.cnt && p < n_rows) ? gtok[p - pp.cnt] : 0u;
+        }
+        pre_ladder = ladder;
+        pre_gi = gi + 4;
+      } else {
+        pre_ladder = -1;
+      }
+      const bool settled = beta_row_group_held(c, r, ws, pp, ell, gi, live, cur, have_pre);
       // Groups the screen leaves open (near ties, non-finite costs, tiny
       // masses): the canonical evaluation, one group at a time on the whole wave.
       uint64_t open = __ballot(live && !settled && (lane_id() & 15) == 0);
