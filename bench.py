@@ -582,8 +582,8 @@ def flush_workload(args, torch, np):
                    "mode": "the layers' caches stacked as the batch rows of one cache, one flush call per step",
                    **per_layer},
         "roofline": {"kernel": "whole flush step: cut/score/choose + partition, order/attach/seed, "
-                               "bucket/commit/units/carries x6/top finish with centers and the level "
-                               "finishes on a side stream, plan + pack (one launch sequence for all layers)",
+                               "bucket/commit/units/carries x6/finishes (centers and the finishes of levels 0..2 "
+                               "on a side stream), plan + pack (one launch sequence for all layers)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic, "traffic_source": traffic_source,

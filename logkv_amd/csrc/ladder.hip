@@ -1849,22 +1849,31 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
 // TOP = false: levels 0..L-2 (grid y = L - 1); TOP = true: the top level
 // (grid y = 1), whose saturated fold keeps its registers out of the other
 // levels' launch.
+// Slot writes of levels ell0 .. ell0 + gridDim.y - 1 (blockIdx.y), one block per
+// (ladder, level). TOP launches end at the top level and put it at y = 0, so the
+// top folds (sequential in their rows, the slowest blocks) are dispatched first.
 template <bool TOP>
 __global__ __launch_bounds__(kThreads) void finish_kernel(LadderArgs c, RowsArgs r, Workspace ws, int ell0) {
   extern __shared__ __align__(16) uint8_t dyn[];
-  const int ladder = blockIdx.x, ell = TOP ? c.levels - 1 : ell0 + static_cast<int>(blockIdx.y);
+  const int y = static_cast<int>(blockIdx.y);
+  const bool top = TOP && y == 0;
+  const int ladder = blockIdx.x, ell = top ? c.levels - 1 : ell0 + y - (TOP ? 1 : 0);
   const LadderPlan* pl = ws.plans + ladder;
   // The last launch of a commit marks every cluster that took rows as live.
-  if (TOP && threadIdx.x == 0 && pl->m_tok > 0) c.alive[ladder] = 1;
+  if (top && threadIdx.x == 0 && pl->m_tok > 0) c.alive[ladder] = 1;
   if (!pl->active) return;
   const int cnt = pl->cnt[ell], m = pl->m[ell];
   if (m == 0) return;
   const Ladder lad = ladder_of(c, ladder);
   int n;
-  if (ell == 0 && pl->kind0 == 0)
-    n = level_finish<0, TOP>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m);
+  if (top)
+    n = ell == 0 && pl->kind0 == 0
+            ? level_finish<0, true>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m)
+            : level_finish<1, true>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m);
+  else if (ell == 0 && pl->kind0 == 0)
+    n = level_finish<0, false>(lad, ell, cnt, flush_rows_of(c, r, ws, pl, ladder, reinterpret_cast<uint16_t*>(dyn)), m);
   else
-    n = level_finish<1, TOP>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m);
+    n = level_finish<1, false>(lad, ell, cnt, staged_of(ws, ladder, ell, c.dk, c.dv), m);
   if (threadIdx.x == 0) c.level_count[static_cast<int64_t>(ladder) * c.levels + ell] = static_cast<int16_t>(n);
 }
 
@@ -2063,6 +2072,7 @@ struct SideStream {
 };
 
 constexpr int kSideLadders = 1024;
+constexpr int kSideFinishLevels = 3;   // lowest levels whose finishes run on the side stream
 
 static SideStream* side_stream_for(hipStream_t main) {
   constexpr int kSlots = 64;
@@ -2151,6 +2161,7 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
                   hipStream_t stream, SideStream* side) {
   const int ladders = c.n_batch * c.n_groups * c.k_max;
   const size_t tok_bytes = (2 * static_cast<size_t>(r.tokens) + 15) & ~size_t(15);
+  const int side_levels = side ? std::min(kSideFinishLevels, c.levels - 1) : 0;
   if (c.levels > 1) {
     hipLaunchKernelGGL(units_kernel, dim3(c.levels - 1), dim3(kUnitsThreads), 0, stream, c, p, ws);
     const size_t carry_shmem = (static_cast<size_t>(ladders) + 1) * 4;
@@ -2178,10 +2189,12 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
         hipLaunchKernelGGL(carries_kernel<2>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
       else
         hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
-      // With a side stream, level ell's finish (its slots: staged rows in, survivors moved) runs
-      // there once this launch is done: the later carries launches read only higher levels' slots
-      // and the carry buffers, which no finish writes.
-      if (side) {
+      // With a side stream, the finish of each of the lowest kSideFinishLevels levels (its
+      // slots: staged rows in, survivors moved) runs there once this launch is done: the later
+      // carries launches read only higher levels' slots and the carry buffers, which no finish
+      // writes. Every event costs each queue a few microseconds, so the smaller finishes of the
+      // levels above wait for the last carries launch and run with the top level's.
+      if (side && ell < side_levels) {
         if (hipEventRecord(side->level[ell], stream) != hipSuccess ||
             hipStreamWaitEvent(side->side, side->level[ell], 0) != hipSuccess)
           return LOGKV_ERUNTIME;
@@ -2190,10 +2203,9 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
       }
     }
   }
-  if (c.levels > 1 && !side)
-    hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, c.levels - 1), dim3(kThreads), tok_bytes, stream, c, r, ws,
-                       0);
-  hipLaunchKernelGGL(finish_kernel<true>, dim3(ladders, 1), dim3(kThreads), tok_bytes, stream, c, r, ws, 0);
+  // Levels side_levels .. levels - 2, then the top level (y = 0).
+  hipLaunchKernelGGL(finish_kernel<true>, dim3(ladders, c.levels - side_levels), dim3(kThreads), tok_bytes, stream, c,
+                     r, ws, side_levels);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
