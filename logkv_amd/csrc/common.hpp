@@ -83,6 +83,32 @@ __device__ __forceinline__ const LOGKV_G T* gp(const T* p) {
 
 constexpr int kWave = 64;
 
+// dst[i] = src[i] for i < n by the threads of a block (thread tid of nthr): each
+// thread issues up to kStageLoads loads before its first store, so staging a
+// table into LDS waits on one load latency per kStageLoads * nthr elements
+// instead of one per nthr (a plain strided loop waits on every load).
+constexpr int kStageLoads = 16;
+template <typename T, typename Dst, typename Src>
+__device__ __forceinline__ void stage_copy(Dst dst, Src src, int n, int tid, int nthr) {
+  if (n <= nthr) {   // one element per thread at most
+    if (tid < n) dst[tid] = src[tid];
+    return;
+  }
+  for (int i0 = tid; i0 < n; i0 += kStageLoads * nthr) {
+    T v[kStageLoads];
+#pragma unroll
+    for (int q = 0; q < kStageLoads; ++q) {
+      const int i = i0 + q * nthr;
+      v[q] = i < n ? src[i] : T{};
+    }
+#pragma unroll
+    for (int q = 0; q < kStageLoads; ++q) {
+      const int i = i0 + q * nthr;
+      if (i < n) dst[i] = v[q];
+    }
+  }
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }

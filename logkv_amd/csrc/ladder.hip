@@ -564,7 +564,7 @@ __device__ inline Src flush_rows_of(const LadderArgs& c, const RowsArgs& r, cons
   const int lane_ix = ladder / c.k_max;
   const int b = lane_ix / c.n_groups, g = lane_ix % c.n_groups;
   const LOGKV_G uint16_t* src = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
-  for (int i = threadIdx.x; i < pl->m_tok; i += blockDim.x) tok[i] = src[i];
+  stage_copy<uint16_t>(tok, src, pl->m_tok, threadIdx.x, blockDim.x);
   __syncthreads();
   Src s{};
   s.kind = 0;
@@ -716,7 +716,7 @@ __device__ __forceinline__ void center_block(const LadderArgs& c, const RowsArgs
   const int nn = m - first;
   {
     const LOGKV_G uint16_t* list = gp(ws.tok + cl * r.tokens);
-    for (int i = threadIdx.x; i < m; i += blockDim.x) ctok[i] = list[i];
+    stage_copy<uint16_t>(ctok, list, m, threadIdx.x, blockDim.x);
   }
   __syncthreads();
   if (wave_id() >= kCenterWaves) return;
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(kThreads) void commit_kernel(LadderArgs c, RowsArgs
   const int m = ws.plans[ladder].m_tok;
   {
     const LOGKV_G uint16_t* list = gp(ws.tok + static_cast<int64_t>(ladder) * r.tokens);
-    for (int i = threadIdx.x; i < m; i += kThreads) tok[i] = list[i];
+    stage_copy<uint16_t>(tok, list, m, threadIdx.x, kThreads);
   }
   __syncthreads();
   if (m == 0) {
@@ -1706,7 +1706,7 @@ __global__ __launch_bounds__(kCarryThreads, 3) void beta_carries_kernel(LadderAr
   const int n_waves = static_cast<int>(gridDim.x) * wpb;
   const int per = (quads + n_waves - 1) / n_waves;
   if (static_cast<int>(blockIdx.x) * wpb * per >= quads) return;
-  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  stage_copy<int32_t>(prefix_s, pre, ladders + 1, threadIdx.x, blockDim.x);
   __syncthreads();
   int qd = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
   const int qd_end = min(quads, qd + per);
@@ -1809,7 +1809,7 @@ __global__ __launch_bounds__(kCarryThreads) void carries_kernel(LadderArgs c, Ro
   const int n_waves = static_cast<int>(gridDim.x) * wpb;
   const int per = (total + n_waves - 1) / n_waves;
   if (total == 0 || static_cast<int>(blockIdx.x) * wpb * per >= total) return;
-  for (int i = threadIdx.x; i <= ladders; i += blockDim.x) prefix_s[i] = pre[i];
+  stage_copy<int32_t>(prefix_s, pre, ladders + 1, threadIdx.x, blockDim.x);
   __syncthreads();
   int u = (static_cast<int>(blockIdx.x) * wpb + wave_id()) * per;
   const int u_end = min(total, u + per);
