@@ -100,7 +100,7 @@ __device__ __forceinline__ void span_fold(const float (&x)[kTokBatch][NJ], int i
 
 // A component's means (per lane features), energy E and mean square of the
 // means; returns R = residual / energy.
-template <int NJ>
+template <int NJ, bool FULL>
 __device__ __forceinline__ float span_finish(const SpanAcc<NJ>& s, int n, int D, const DimDiv& dd, float* mean,
                                              float& energy, float& msq) {
   const int l = lane_id();
@@ -109,7 +109,7 @@ __device__ __forceinline__ float span_finish(const SpanAcc<NJ>& s, int n, int D,
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     mean[j] = s.acc[j] / cnt;
-    m2[j] = (l + j * kWave < D) ? mean[j] * mean[j] : 0.f;
+    m2[j] = (FULL || l + j * kWave < D) ? mean[j] * mean[j] : 0.f;
   }
   energy = s.e / cnt;
   msq = dd(canon_sum<NJ>(m2));
@@ -119,12 +119,13 @@ __device__ __forceinline__ float span_finish(const SpanAcc<NJ>& s, int n, int D,
 // Token statistics of both components over a span in one pass: the span's row
 // indices are read a lane each, 64 at a time, and kTokBatch K and V rows are
 // loaded together per step.
-template <int NJ>
+// FULL: dk = dv = 64 NJ, every lane's features are in the row (no masking).
+template <int NJ, bool FULL>
 __device__ __forceinline__ void span_components(const Rows2& ks, const Rows2& vs, int b, int g,
                                                 const LOGKV_G int32_t* tok, int n, int dk, int dv, float* mean_k,
                                                 float& e_k, float& msq_k, float& rk, float& rv) {
   const int l = lane_id();
-  const DimDiv dk_div(dk), dv_div(dv);
+  const DimDiv dk_div(FULL ? kWave * NJ : dk), dv_div(FULL ? kWave * NJ : dv);
   SpanAcc<NJ> sk{}, sv{};
   for (int c0 = 0; c0 < n; c0 += kWave) {
     const int cn = min(kWave, n - c0);
@@ -138,8 +139,8 @@ __device__ __forceinline__ void span_components(const Rows2& ks, const Rows2& vs
         const LOGKV_G uint16_t* rowv = vs.row(b, g, tt);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          xk[t][j] = feat_or_zero(rowk, l + j * kWave, dk);
-          xv[t][j] = feat_or_zero(rowv, l + j * kWave, dv);
+          xk[t][j] = FULL ? bf16_to_f32(rowk[l + j * kWave]) : feat_or_zero(rowk, l + j * kWave, dk);
+          xv[t][j] = FULL ? bf16_to_f32(rowv[l + j * kWave]) : feat_or_zero(rowv, l + j * kWave, dv);
         }
       }
       span_fold<NJ>(xk, c0 + i0, cn - i0, dk_div, sk);
@@ -147,8 +148,8 @@ __device__ __forceinline__ void span_components(const Rows2& ks, const Rows2& vs
     }
   }
   float mean_v[NJ], e_v, msq_v;
-  rk = span_finish<NJ>(sk, n, dk, dk_div, mean_k, e_k, msq_k);
-  rv = span_finish<NJ>(sv, n, dv, dv_div, mean_v, e_v, msq_v);
+  rk = span_finish<NJ, FULL>(sk, n, dk, dk_div, mean_k, e_k, msq_k);
+  rv = span_finish<NJ, FULL>(sv, n, dv, dv_div, mean_v, e_v, msq_v);
 }
 
 // Candidate slots of the select path: row b owns slots [b * slots, (b + 1) *
@@ -163,7 +164,7 @@ __device__ __forceinline__ bool span_live(const logkv_span_args& a, const SpanSl
   return !a.n_spans_dev || s < *a.n_spans_dev;
 }
 
-template <int NJ>
+template <int NJ, bool FULL>
 __device__ __forceinline__ void score_span(const logkv_span_args& a, int s, float* part_k, float* part_v, float* q_s,
                                            float* __restrict__ out) {
   const int g = wave_id();
@@ -176,13 +177,13 @@ __device__ __forceinline__ void score_span(const logkv_span_args& a, int s, floa
     Rows2 ks{gp(a.pool_k), a.pk_sb, a.pk_sg, a.pk_st, gp(a.flush_k), a.fk_sb, a.fk_sg, a.fk_st, a.old_width};
     Rows2 vs{gp(a.pool_v), a.pv_sb, a.pv_sg, a.pv_st, gp(a.flush_v), a.fv_sb, a.fv_sg, a.fv_st, a.old_width};
     float mean_k[NJ], e_k, msq_k, rk, rv;
-    span_components<NJ>(ks, vs, b, g, tok, n, a.dk, a.dv, mean_k, e_k, msq_k, rk, rv);
+    span_components<NJ, FULL>(ks, vs, b, g, tok, n, a.dk, a.dv, mean_k, e_k, msq_k, rk, rv);
     float q = 0.f;
     if (a.beta_novelty) {
       const int l = lane_id();
       const LOGKV_G float* mu = gp(a.centroids) + (static_cast<int64_t>(b) * G + g) * a.k_max * a.dk;
       const LOGKV_G uint8_t* valid = gp(a.centroid_valid) + (static_cast<int64_t>(b) * G + g) * a.k_max;
-      const DimDiv dk_div(a.dk);
+      const DimDiv dk_div(FULL ? kWave * NJ : a.dk);
       float nearest = __builtin_inff();
       bool any = false;
       // Four centers at a time: their dot and square sums, each one canonical sum (wave_sum4).
@@ -193,7 +194,8 @@ __device__ __forceinline__ void score_span(const logkv_span_args& a, int s, floa
           const int c = min(c0 + k, a.k_max - 1);
           float m[NJ];
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) m[j] = feat_or_zero(mu + c * a.dk, l + j * kWave, a.dk);
+          for (int j = 0; j < NJ; ++j)
+            m[j] = FULL ? mu[c * a.dk + l + j * kWave] : feat_or_zero(mu + c * a.dk, l + j * kWave, a.dk);
           pd[k] = mean_k[0] * m[0];
           pc[k] = m[0] * m[0];
 #pragma unroll
@@ -258,19 +260,19 @@ __device__ __forceinline__ void score_span(const logkv_span_args& a, int s, floa
 
 // One span per block iteration (grid-stride over the span slots), one wave
 // per KV group.
-template <int NJ>
+template <int NJ, bool FULL>
 __global__ __launch_bounds__(kMaxGroups * kWave) void score_kernel(logkv_span_args a, SpanSlots sl,
                                                                    float* __restrict__ out) {
   __shared__ float part_k[kMaxGroups], part_v[kMaxGroups], q_s[kMaxGroups];
   if (sl.row_count) {   // grid (x, batch row): row b's candidates x, x + gridDim.x, ...
     const int b = blockIdx.y, n = sl.row_count[b];
     for (int i = blockIdx.x; i < n; i += gridDim.x)
-      score_span<NJ>(a, b * sl.slots + i, part_k, part_v, q_s, out);
+      score_span<NJ, FULL>(a, b * sl.slots + i, part_k, part_v, q_s, out);
     return;
   }
   for (int s = blockIdx.x; s < a.n_spans; s += gridDim.x) {
     if (!span_live(a, sl, s)) continue;
-    score_span<NJ>(a, s, part_k, part_v, q_s, out);
+    score_span<NJ, FULL>(a, s, part_k, part_v, q_s, out);
   }
 }
 
@@ -1023,10 +1025,12 @@ int launch_score_slots(const logkv_span_args& a, const SpanSlots& sl, float* out
                         ? dim3(static_cast<unsigned>(std::min(sl.slots, std::max(32, kScoreBlocks / n_rows))),
                                static_cast<unsigned>(n_rows))
                         : dim3(static_cast<unsigned>(std::min(a.n_spans, kScoreBlocks)));
-  if (a.dk <= 2 * kWave && a.dv <= 2 * kWave)
-    hipLaunchKernelGGL(score_kernel<2>, grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
+  if (a.dk == 2 * kWave && a.dv == 2 * kWave)
+    hipLaunchKernelGGL((score_kernel<2, true>), grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
+  else if (a.dk <= 2 * kWave && a.dv <= 2 * kWave)
+    hipLaunchKernelGGL((score_kernel<2, false>), grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
   else
-    hipLaunchKernelGGL(score_kernel<4>, grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
+    hipLaunchKernelGGL((score_kernel<4, false>), grid, dim3(a.n_groups * kWave), 0, stream, a, sl, out);
   return hipGetLastError() == hipSuccess ? LOGKV_OK : LOGKV_ERUNTIME;
 }
 
