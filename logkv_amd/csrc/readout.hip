@@ -594,14 +594,22 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
         const int t = (q < nq ? q : nq - 1) % a.tq;
         if (q >= nq || (a.causal_tail && row >= tail0 && row - tail0 > t)) sc = -__builtin_inff();
         const float m_new = fmaxf(m[q], sc);
-        const float corr = m_new == -__builtin_inff() ? 1.f : __expf(m[q] - m_new);
         const float p = sc == -__builtin_inff() ? 0.f : __expf(sc - m_new);
-        l[q] = l[q] * corr + p;
+        // A new maximum rescales the sums; otherwise the factor is exactly 1
+        // (2^0) and the products by it change nothing, so a wave whose lanes
+        // all kept their maximum skips them.
+        if (__ballot(m_new != m[q])) {
+          const float corr = m_new == -__builtin_inff() ? 1.f : __expf(m[q] - m_new);
+          l[q] = l[q] * corr;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[q][e] = acc[q][e] * corr;
+        }
+        l[q] = l[q] + p;
         m[q] = m_new;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[q][2 * e] = __builtin_fmaf(p, __uint_as_float(v4[e] << 16), acc[q][2 * e] * corr);
-          acc[q][2 * e + 1] = __builtin_fmaf(p, __uint_as_float(v4[e] & 0xffff0000u), acc[q][2 * e + 1] * corr);
+          acc[q][2 * e] = __builtin_fmaf(p, __uint_as_float(v4[e] << 16), acc[q][2 * e]);
+          acc[q][2 * e + 1] = __builtin_fmaf(p, __uint_as_float(v4[e] & 0xffff0000u), acc[q][2 * e + 1]);
         }
       }
     }
