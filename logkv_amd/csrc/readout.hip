@@ -27,6 +27,7 @@ namespace logkv {
 
 namespace {
 
+typedef __bf16 rd_bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kPlanThreads = 1024;
 constexpr int kTile = 64;          // rows per staged K/V tile
 constexpr int kSplitRows = 512;    // rows per attention split (staged decode kernel)
@@ -519,8 +520,9 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
   const int share = max(64, (total + 64 * static_cast<int>(gridDim.x) - 1) / (64 * static_cast<int>(gridDim.x)) * 64);
   const int r_begin = blockIdx.x * share, r_end = min(r_begin + share, total);
   float* out = part + (static_cast<int64_t>(lane) * gridDim.x + blockIdx.x) * nq * (a.dv + 2);
-  // This lane's slices of the queries [q, 1/scale (bf16), 0...]: units gl + 16 j.
-  float qv[NQ][UJ][8];
+  // This lane's slices of the queries [q, 1/scale (bf16), 0...]: units gl + 16 j,
+  // as bf16 pairs (features 2e, 2e + 1 of a unit) for the packed dot products.
+  uint32_t qp[NQ][UJ][4];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int qq = q < nq ? q : nq - 1;
@@ -528,12 +530,17 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
 #pragma unroll
     for (int j = 0; j < UJ; ++j) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * (gl + kGl * j) + e;
-        float x = 0.f;
-        if (d < a.dk) x = bf16_to_f32(gp(a.q)[b * a.q_sb + h * a.q_sh + t * a.q_st + d]);
-        else if (!SPLIT && d == a.dk) x = a.inv_scale_bf16;
-        qv[q][j][e] = q < nq ? x : 0.f;
+      for (int e = 0; e < 8; e += 2) {
+        uint32_t pair = 0u;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int d = 8 * (gl + kGl * j) + e + hf;
+          uint32_t x = 0u;
+          if (d < a.dk) x = gp(a.q)[b * a.q_sb + h * a.q_sh + t * a.q_st + d];
+          else if (!SPLIT && d == a.dk) x = f32_to_bf16(a.inv_scale_bf16);
+          pair |= (q < nq ? x : 0u) << (16 * hf);
+        }
+        qp[q][j][e / 2] = pair;
       }
     }
   }
@@ -575,12 +582,10 @@ __global__ __launch_bounds__(256) void stream_kernel(logkv_attention_args a, con
           const uint32_t w4[4] = {kx[i][j].x, kx[i][j].y, kx[i][j].z, kx[i][j].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float k0 = __uint_as_float(w4[e] << 16), k1 = __uint_as_float(w4[e] & 0xffff0000u);
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-              dot[q] = __builtin_fmaf(qv[q][j][2 * e], k0, dot[q]);
-              dot[q] = __builtin_fmaf(qv[q][j][2 * e + 1], k1, dot[q]);
-            }
+            for (int q = 0; q < NQ; ++q)
+              dot[q] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(rd_bf16x2, w4[e]),
+                                                       __builtin_bit_cast(rd_bf16x2, qp[q][j][e]), dot[q], false);
           }
         }
       }
