@@ -1,8 +1,8 @@
 """The oracle: a CPU (numpy) restatement of SemanticLogKV's flush and readout path.
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or
-the timed CPU baseline - the product package ``logkv_amd`` never imports it and
+``cpu_baseline`` leg of ``bench.py`` may import it, and only to check results or
+as the timed CPU baseline - the product package ``logkv_amd`` never imports it and
 has no CPU fallback.
 
 Modules and what pins them (the tests named in brackets):

@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY: ``bench.py``'s ``cpu_baseline`` leg times it and tests
 checks it; the product package never imports it.
 
 The oracle (``oracle.cache.OracleCache``) walks ladders and Beta groups one at a time, which is
-what makes it a readable checker and a slow baseline. The reference's CPU path instead schedules
+what makes it a readable restatement and a slow baseline. The reference's CPU path instead schedules
 every ladder of a flush together, level by level, and evaluates the Beta groups of a level as
 tensor operations (litgpt/log_kv_cache.py:1756-1929, ``_semantic_append_entries_batched``;
 litgpt/beta_log_kv.py:29-105, ``select_cuts`` / ``apply_cuts`` over all groups). ``TorchCpuCache``

@@ -1,7 +1,7 @@
 """Write the golden fixtures of tests/golden from the reference's own CPU Torch path.
 
-Run in the build container only (the reference tree is read from /root/reference; nothing on a
-GPU box reads it): ``python tests/golden/make_fixtures.py``. It imports the reference's hot-path
+Run only where the reference tree is present (it is read from /root/reference; the tests read
+the fixtures, never the reference): ``python tests/golden/make_fixtures.py``. It imports the reference's hot-path
 modules through a bare namespace package, as the reference's own tools do
 (unused/semantic_logkv_microbench.py:22-25), so neither ``litgpt/__init__.py`` nor anything
 outside the LogKV modules is imported, and runs them on the CPU with seeded inputs:

@@ -1,6 +1,6 @@
 """Loading and comparison helpers for the golden fixtures written by tests/golden/make_fixtures.py
-from the reference's CPU Torch path. The bar (north star of this path): integer fields, decisions and
-indices bit for bit; merged keys / values and masses within 1e-5 relative or one bf16 ulp."""
+from the reference's CPU Torch path. The bar: integer fields, decisions and indices bit for bit;
+merged keys / values and masses within 1e-5 relative or one bf16 ulp."""
 
 from __future__ import annotations
 

@@ -4,8 +4,8 @@ before anything is launched. Every case here fails a check that precedes the fir
 HIP call of its entry point; the pointers are never dereferenced.
 
 The fake device addresses are only safe while no kernel can launch, so the module
-runs only where no HIP device is visible (the CPU suite); on a GPU box the same
-checks are exercised through real tensors by the GPU tests."""
+runs only where no HIP device is visible (the CPU suite); where a device is
+visible the same checks are exercised through real tensors by the GPU tests."""
 
 import ctypes as C
 

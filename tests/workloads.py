@@ -3,7 +3,7 @@
 Keys and values are a Gaussian mixture around K frozen centers ``N(0,1)*4``:
 90% of rows are a center plus ``N(0, 0.5^2)`` noise, 10% are far outliers
 ``N(0,1)*12``. Everything is drawn on the CPU from a ``torch.Generator`` so the
-same bytes can be fed to the device and to any CPU checker.
+same bytes can be fed to the device and to the oracle.
 """
 
 from __future__ import annotations
