@@ -2189,17 +2189,20 @@ int launch_levels(const LadderArgs& c, const RowsArgs& r, const RouteParams& p, 
         hipLaunchKernelGGL(carries_kernel<2>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
       else
         hipLaunchKernelGGL(carries_kernel<4>, dim3(blocks), dim3(kCarryThreads), carry_shmem, stream, c, r, p, ws, ell);
-      // With a side stream, the finish of each of the lowest kSideFinishLevels levels (its
-      // slots: staged rows in, survivors moved) runs there once this launch is done: the later
-      // carries launches read only higher levels' slots and the carry buffers, which no finish
-      // writes. Every event costs each queue a few microseconds, so the smaller finishes of the
-      // levels above wait for the last carries launch and run with the top level's.
-      if (side && ell < side_levels) {
+      // With a side stream, the finishes of the lowest kSideFinishLevels levels (their slots:
+      // staged rows in, survivors moved) run there once their carries launches are done: the
+      // later carries launches read only higher levels' slots and the carry buffers, which no
+      // finish writes. Every event costs each queue a few microseconds, so level 0's finish (the
+      // largest) follows its own carries, levels 1 .. kSideFinishLevels - 1 share one launch after
+      // the last of theirs, and the smaller finishes of the levels above wait for the last carries
+      // launch and run with the top level's.
+      if (side && ell < side_levels && (ell == 0 || ell == side_levels - 1)) {
         if (hipEventRecord(side->level[ell], stream) != hipSuccess ||
             hipStreamWaitEvent(side->side, side->level[ell], 0) != hipSuccess)
           return LOGKV_ERUNTIME;
-        hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, 1), dim3(kThreads), tok_bytes, side->side, c, r, ws,
-                           ell);
+        const int e0 = ell == 0 ? 0 : 1;
+        hipLaunchKernelGGL(finish_kernel<false>, dim3(ladders, ell - e0 + 1), dim3(kThreads), tok_bytes, side->side, c,
+                           r, ws, e0);
       }
     }
   }
