@@ -257,3 +257,23 @@ def stream_of(device: torch.device) -> int:
 def require_device(t: torch.Tensor, what: str) -> None:
     if t.device.type != "cuda":
         raise ValueError(f"{what} must live on a ROCm device (got {t.device}); the LogKV HIP library has no CPU path")
+
+
+# Activation dtypes the cache accepts. Its entries are always stored as bfloat16 (the kernels read and
+# write bf16 rows with fp32 arithmetic); rows of another activation dtype are rounded to bf16 (nearest
+# even) where they enter, and readouts are returned in the caller's dtype.
+ACTIVATION_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def check_activation_dtype(dtype: torch.dtype) -> None:
+    if dtype not in ACTIVATION_DTYPES:
+        raise NotImplementedError(f"logkv_amd takes bfloat16, float16 or float32 activations, not {dtype}")
+
+
+def as_storage(t):
+    """``t`` at the cache's storage precision: bf16 tensors (and None) pass through, float16 / float32
+    rows are rounded to bf16 by a differentiable cast."""
+    if t is None or not isinstance(t, torch.Tensor) or t.dtype == torch.bfloat16:
+        return t
+    check_activation_dtype(t.dtype)
+    return t.to(torch.bfloat16)

@@ -252,8 +252,8 @@ class LogStructuredKVCache(nn.Module):
             unsupported.append("allocate_second_order=False")
         if importance_pooling:
             unsupported.append("importance_pooling=False")
-        if dtype != torch.bfloat16:
-            unsupported.append("bfloat16 storage")
+        if dtype not in _lib.ACTIVATION_DTYPES:
+            unsupported.append("a bfloat16, float16 or float32 dtype")
         if cluster_k_max > 32:
             unsupported.append("cluster_k_max <= 32")
         if unsupported:
@@ -281,7 +281,11 @@ class LogStructuredKVCache(nn.Module):
         self.register_buffer("cos_cache", cos_cache.to(device=device), persistent=False)
         self.register_buffer("sin_cache", sin_cache.to(device=device), persistent=False)
         self.slot_k_dim = int(cos_cache.size(1)) + k_dim - self.rope_n_elem
+        # The Alpha budget is priced at the constructor's dtype, as the reference prices it before any
+        # later _convert_dtype; the entries themselves are stored as bfloat16 whatever the dtype.
         element = torch.empty((), dtype=dtype).element_size()
+        self.activation_dtype = dtype
+        dtype = torch.bfloat16
         B_eff, L, budget = ladder_budget(batch_size, n_groups, max_seq_length, k_dim, v_dim, B, self.K_max,
                                          self.alpha_exact_tokens, element)
         if budget is not None:
@@ -489,6 +493,7 @@ class LogStructuredKVCache(nn.Module):
         (``begin_op_log``); ``replay_op_log`` / ``replay_op_log_len`` re-apply
         a logged flush without routing (litgpt/log_kv_cache.py:5049-5114).
         """
+        k_raw, v = _lib.as_storage(k_raw), _lib.as_storage(v)
         self._await_flush()
         if self._active_updates is not None:
             return self._tape_flush(self._active_updates, k_raw, v, positions, positions_host, span_ends, counts,
@@ -959,6 +964,7 @@ class LogStructuredKVCache(nn.Module):
         (litgpt/log_kv_cache.py:5668-5718, :5847). With ``flush_stream`` set the
         append and the flush are queued on that stream after the caller's, and
         the cache's readers wait for them; the host state advances at once."""
+        k, v, k_raw = _lib.as_storage(k), _lib.as_storage(v), _lib.as_storage(k_raw)
         side = self.flush_stream
         if side is not None and side != torch.cuda.current_stream(self.level_k.device):
             side.wait_stream(torch.cuda.current_stream(self.level_k.device))
@@ -1088,12 +1094,17 @@ class LogStructuredKVCache(nn.Module):
         return self.get_attention_state(with_stats, plan=plan)
 
     def _convert_dtype(self, dtype: torch.dtype) -> None:
-        """Reconcile the data buffers with the activation dtype (litgpt/log_kv_cache.py:6236-6268): a
-        no-op when they match. The HIP kernels store and read bfloat16 entries only, so another
-        activation dtype raises instead of converting the buffers."""
-        if self.recent_k.dtype == dtype:
+        """Reconcile the cache with the activation dtype (litgpt/log_kv_cache.py:6236-6268); a no-op
+        once it matches. The reference converts its buffers to ``dtype``; here the entries stay
+        bfloat16 (the kernels' storage type) and ``dtype`` becomes the activation dtype: float16 /
+        float32 rows are rounded to bf16 where they enter (``add_recent``, ``route_and_flush_batch``,
+        the attention entry points) and readouts come back in ``dtype``. As in the reference, the
+        decode prefix kept for reuse is dropped when the dtype changes."""
+        _lib.check_activation_dtype(dtype)
+        if self.activation_dtype == dtype:
             return
-        raise NotImplementedError(f"logkv_amd caches hold bfloat16 entries; activations are {dtype}")
+        self._mid_decode_state = None
+        self.activation_dtype = dtype
 
     # ------------------------------------------------------------------
     # Host mirrors of the reference, read from the device on demand

@@ -26,7 +26,7 @@ import math
 
 import torch
 
-from ._lib import (AttentionArgs, AttentionGradArgs, PackArgs, ReadoutView, SlotPackArgs, check, lib, ptr,
+from ._lib import (AttentionArgs, AttentionGradArgs, PackArgs, ReadoutView, SlotPackArgs, as_storage, check, lib, ptr,
                    require_device, stream_of)
 
 _BACKENDS = ("auto", "triton", "hip")
@@ -139,6 +139,11 @@ def pack_mid_kv(cache, plan, k, v, dim, *, backend=None, buffers=None, skip_pool
     pooled width plus the exact, recent and current rows (reading the width
     back once per plan).
     """
+    if (k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16) and buffers is None:
+        # float16 / float32 rows: packed at the cache's bf16 precision, returned in k's dtype.
+        ka, va = pack_mid_kv(cache, plan, as_storage(k), as_storage(v), dim, backend=backend,
+                             skip_pooled=skip_pooled, recent_start=recent_start)
+        return ka.to(k.dtype), va.to(v.dtype)
     backend = cache.semantic_pack_backend if backend is None else backend
     _check_backend(backend)
     if cache.semantic_anchor_mode != "mid":
@@ -303,6 +308,13 @@ def log_kv_chunk_attention(cache, q_b, k_b, v_b, scale, second_order_scale=1.0, 
     rows) the packed prefix is kept on the cache and later steps re-pack only
     their new rows, as in litgpt/log_kv_cache.py:6772-6799.
     """
+    if q_b.dtype != torch.bfloat16 or k_b.dtype != torch.bfloat16 or v_b.dtype != torch.bfloat16:
+        # float16 / float32 activations: the rows are rounded to the cache's bf16 storage and the output
+        # is returned in the queries' dtype (both casts differentiable).
+        out = log_kv_chunk_attention(cache, as_storage(q_b), as_storage(k_b), as_storage(v_b), scale,
+                                     second_order_scale, attention_plan, causal_tail=causal_tail,
+                                     reuse_prefix=reuse_prefix)
+        return out.to(q_b.dtype)
     causal_tail = q_b.size(2) if causal_tail is None else causal_tail
     if causal_tail and causal_tail != q_b.size(2):
         raise ValueError("causal_tail must equal query length or be zero")
@@ -380,7 +392,9 @@ def attention_state(cache, plan):
     if rows:
         _launch_pack(cache, readout_view(cache), plan, empty, empty, dim, ka, va, False, 0, w, valid)
     slot_valid = valid[:, :, :width + exact].bool()
-    return CacheAttentionState(ka[:, :, :rows, :dk], va[:, :, :rows, :dv], w[:, :, :rows], slot_valid=slot_valid,
+    act = cache.activation_dtype
+    return CacheAttentionState(ka[:, :, :rows, :dk].to(act), va[:, :, :rows, :dv].to(act), w[:, :, :rows],
+                               slot_valid=slot_valid,
                                M_s=torch.ones(B, G, width + exact, dtype=torch.int64, device=dev))
 
 
@@ -450,7 +464,10 @@ def log_kv_slot_attention(q, slot_k, slot_v, slot_w, scale, mask=None, lam=1.0, 
     if mask is not None:
         raise NotImplementedError("logkv_amd masks through causal_tail and slot_valid, not a (T_q, S) mask")
     if q.dtype != torch.bfloat16 or slot_k.dtype != torch.bfloat16 or slot_v.dtype != torch.bfloat16:
-        raise NotImplementedError("logkv_amd slot attention takes bfloat16 queries and slots")
+        # float16 / float32 activations: queries and slots rounded to bf16, the output in q's dtype.
+        return log_kv_slot_attention(as_storage(q), as_storage(slot_k), as_storage(slot_v), slot_w, scale, mask,
+                                     lam, causal_tail, slot_M, slot_valid, check_valid, slot_sigma_u, slot_sigma2,
+                                     slot_gamma_a, slot_gamma_b, slot_gamma, second_order_scale).to(q.dtype)
     if not math.isfinite(scale) or not 1e-3 <= scale <= 1.0:
         raise NotImplementedError("attention scale must lie in [1e-3, 1]")
     G = slot_k.size(1)

@@ -10,6 +10,7 @@ from __future__ import annotations
 import inspect
 
 import pytest
+import torch
 
 
 def params(fn):
@@ -103,3 +104,24 @@ def test_compression_accounting(name):
     import logkv_amd
 
     assert callable(getattr(logkv_amd, name))
+
+
+def test_activation_rows_round_to_bf16_storage():
+    """float16 / float32 activations enter the cache rounded to bf16 (nearest even, differentiably);
+    other dtypes are refused as the options this library does not implement."""
+    from logkv_amd._lib import as_storage, check_activation_dtype
+
+    x = torch.tensor([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -3.0e38, 65504.0], dtype=torch.float32)
+    y = as_storage(x)
+    assert y.dtype == torch.bfloat16
+    # ties to even: 1+2^-8 -> 1, 1+3*2^-8 -> 1+2^-6; 65504 -> 65536 (bf16 spacing 256 there)
+    assert [y[i].item() for i in (0, 1, 3)] == [1.0, 1.0 + 2.0 ** -6, 65536.0]
+    assert torch.isfinite(y[2]) and y[2].item() < -2.99e38
+    h = as_storage(torch.tensor([2050.0], dtype=torch.float16, requires_grad=True))
+    assert h.dtype == torch.bfloat16 and h.requires_grad and h.item() == 2048.0
+    b = torch.ones(2, dtype=torch.bfloat16)
+    assert as_storage(b) is b and as_storage(None) is None
+    with pytest.raises(NotImplementedError):
+        check_activation_dtype(torch.float64)
+    with pytest.raises(NotImplementedError):
+        as_storage(torch.zeros(1, dtype=torch.float64))

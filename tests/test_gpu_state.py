@@ -124,5 +124,7 @@ def test_append_exact_tokens_and_dtype_contract():
     assert grown.slot_k.size(2) == S + 3 and torch.equal(grown.slot_v[:, :, S:], 2 * k)
     assert bool((grown.slot_w[:, :, S:] == 1).all()) and grown.slot_valid is st.slot_valid
     cache._convert_dtype(torch.bfloat16)           # no-op when the activations match
+    cache._convert_dtype(torch.float32)            # entries stay bf16, readouts come back in float32
+    assert cache.level_k.dtype == torch.bfloat16 and cache.get_attention_state().slot_k.dtype == torch.float32
     with pytest.raises(NotImplementedError):
-        cache._convert_dtype(torch.float32)
+        cache._convert_dtype(torch.float64)
