@@ -1063,9 +1063,21 @@ class LogStructuredKVCache(nn.Module):
         self._workspace = None
         self._views = {}
         self._alpha_keep_alive = None
-        out = super()._apply(fn, recurse)
+        # A cast of the module (``.float()``, ``.to(dtype)``) keeps every buffer's dtype - the kernels'
+        # storage contract - and moves devices only; a floating cast (fn maps float32 and bf16 to one
+        # dtype) sets the activation dtype instead, as ``_convert_dtype`` does.
+        probes = [fn(torch.empty(0, dtype=dt, device=self.level_k.device)) for dt in (torch.float32, torch.bfloat16)]
+        cast = probes[0].dtype if probes[0].dtype == probes[1].dtype else None
+
+        def keep_dtype(t):
+            target = fn(t.new_empty(0))
+            return t if target.device == t.device else t.to(target.device)
+
+        out = super()._apply(keep_dtype, recurse)
         if self.alpha_exact_tokens:
-            self._alpha_spare = tuple(fn(t) for t in self._alpha_spare)
+            self._alpha_spare = tuple(keep_dtype(t) for t in self._alpha_spare)
+        if cast in _lib.ACTIVATION_DTYPES:
+            self.activation_dtype = cast
         moved = any(t is not None and t.data_ptr() != before.get(name) for name, t in self._buffers.items())
         if moved and self._group is not None:
             self._group.leave(self)      # its buffers no longer view the group's stacked rows

@@ -48,10 +48,10 @@ def test_activation_dtype_matches_bf16_cache(act, exact):
         assert out_w.dtype == act and torch.equal(out_w, out_r.to(act)), f"block {blk}: attention"
         wide.add_recent(k, v, k_raw=kr, input_pos=pos, span_ends=ends)
         ref.add_recent(k.bfloat16(), v.bfloat16(), k_raw=kr.bfloat16(), input_pos=pos, span_ends=ends)
-    torch.cuda.synchronize()
+    assert wide._semantic_counts == ref._semantic_counts      # host reads run any pending (grouped) flush
     diff = [n for (n, a), (_, b) in zip(wide.named_buffers(), ref.named_buffers()) if not torch.equal(a, b)]
     assert not diff, diff
-    assert wide.level_k.dtype == torch.bfloat16 and wide._semantic_counts == ref._semantic_counts
+    assert wide.level_k.dtype == torch.bfloat16
 
     # Unpacked state and slot attention in the activation dtype.
     q = torch.randn(2, 4, 16, 128, generator=g).to(act).to(dev)
@@ -118,3 +118,35 @@ def test_float32_constructor_prices_the_budget_at_four_bytes(max_seq, exact):
         assert caches[torch.float32].B_prime == caches[torch.bfloat16].B_prime - 1
     with pytest.raises(NotImplementedError):
         caches[torch.bfloat16]._convert_dtype(torch.float64)
+
+
+def test_module_casts_keep_bf16_entries():
+    """``.float()`` / ``.to(dtype)`` on a module holding the cache (litgpt casts whole models) leave
+    every buffer's dtype and contents alone and set the activation dtype; the cache then runs as after
+    ``_convert_dtype``."""
+    print("case module casts", flush=True)
+    kw = dict(batch=1, groups=2, dim=128, K=6, B=8, recent=64, flush=64, max_seq=64 * 8, s_h=16.0)
+    cache, _ = make_pair(**kw)
+    ref, _ = make_pair(**kw)
+    mix = Mixture(1, 2, 128, clusters=5, seed=3)
+    dev = cache.level_k.device
+    for blk in range(3):
+        k, v = mix.rows(64).to(dev), mix.rows(64).to(dev)
+        pos = torch.arange(blk * 64, blk * 64 + 64).unsqueeze(0).to(dev)
+        for c in (cache, ref):
+            c.add_recent(k, v, k_raw=k, input_pos=pos)
+    assert cache._semantic_counts == ref._semantic_counts      # host reads run any pending (grouped) flush
+    dtypes = {n: t.dtype for n, t in cache.named_buffers()}
+    holder = torch.nn.Module()
+    holder.kv_cache = cache
+    holder.float()
+    assert {n: t.dtype for n, t in cache.named_buffers()} == dtypes and cache.activation_dtype == torch.float32
+    assert all(torch.equal(a, b) for (_, a), (_, b) in zip(cache.named_buffers(), ref.named_buffers()))
+    q = torch.randn(1, 4, 16, 128, device=dev)
+    k, v = mix.rows(16).to(dev), mix.rows(16).to(dev)
+    with torch.no_grad():
+        out = log_kv_chunk_attention(cache, q, k.float(), v.float(), 128 ** -0.5, second_order_scale=0.0)
+        out_r = log_kv_chunk_attention(ref, q.bfloat16(), k, v, 128 ** -0.5, second_order_scale=0.0)
+    assert out.dtype == torch.float32 and torch.equal(out, out_r.float())
+    holder.to(torch.bfloat16)
+    assert cache.activation_dtype == torch.bfloat16 and cache.level_k.dtype == torch.bfloat16
